@@ -1,0 +1,259 @@
+// ref_driver.cpp -- C API over the reference's own CPUBackend, TransformerBlock and CausalLM.
+//
+// TEST INFRASTRUCTURE ONLY. Compiled by oracle/Makefile together with the reference's path
+// sources, read where they lie under /root/reference (nothing is copied), into
+// oracle/_ref/libpxref.so. The entry points mirror oracle/pxo.h with a pxr_ prefix, so the tests
+// can run the oracle restatement and the real reference on identical inputs.
+
+#include <algorithm>
+#include <cstdint>
+#include <map>
+#include <memory>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "pulsatrix/causal_lm.hpp"
+#include "pulsatrix/cpu_backend.hpp"
+#include "pulsatrix/hf_model.hpp"
+#include "pulsatrix/linear_module.hpp"
+#include "pulsatrix/lrp_rule_config.hpp"
+#include "pulsatrix/transformer_block.hpp"
+
+#include "pxo.h"
+
+using namespace pulsatrix;
+
+namespace {
+
+thread_local std::string g_error;
+
+template <typename F>
+int guarded(F&& f) {
+    try {
+        f();
+        return 0;
+    } catch (const std::exception& e) {
+        g_error = e.what();
+        return -1;
+    }
+}
+
+int64_t kv_heads(const px_model_config& c) { return c.num_kv_heads > 0 ? c.num_kv_heads : c.num_heads; }
+int64_t head_dim(const px_model_config& c) { return c.head_dim > 0 ? c.head_dim : c.hidden_size / c.num_heads; }
+
+AttentionConfig attention_config(const px_model_config& c) {
+    AttentionConfig a;
+    a.d_model = c.hidden_size;
+    a.num_heads = c.num_heads;
+    a.num_kv_heads = kv_heads(c);
+    a.head_dim = head_dim(c);
+    a.use_rope = c.use_rope != 0;
+    a.rope_layout = c.rope_rotate_half ? RoPELayout::RotateHalf : RoPELayout::AdjacentPairs;
+    a.rope_base = c.rope_theta;
+    a.qkv_bias = c.qkv_bias != 0;
+    a.out_bias = c.out_bias != 0;
+    a.causal = c.causal != 0;
+    return a;
+}
+
+// Names and sizes of one block's parameters in the flat blob's order.
+std::vector<std::pair<std::string, int64_t>> block_layout(const px_model_config& c) {
+    const int64_t d = c.hidden_size, q = c.num_heads * head_dim(c), kv = kv_heads(c) * head_dim(c),
+                  f = c.intermediate_size;
+    std::vector<std::pair<std::string, int64_t>> out{{"norm1.weight", d}};
+    auto lin = [&](const std::string& name, int64_t in, int64_t o, bool bias) {
+        out.push_back({name + ".weight", in * o});
+        if (bias) out.push_back({name + ".bias", o});
+    };
+    lin("mha.q_proj", d, q, c.qkv_bias);
+    lin("mha.k_proj", d, kv, c.qkv_bias);
+    lin("mha.v_proj", d, kv, c.qkv_bias);
+    lin("mha.out_proj", q, d, c.out_bias);
+    out.push_back({"norm2.weight", d});
+    lin("swiglu.gate_proj", d, f, c.mlp_bias);
+    lin("swiglu.up_proj", d, f, c.mlp_bias);
+    lin("swiglu.down_proj", f, d, c.mlp_bias);
+    return out;
+}
+
+void load(Module& m, const std::vector<std::pair<std::string, int64_t>>& layout, const float* params,
+          DeviceBackend* be) {
+    std::map<std::string, Tensor*> targets;
+    for (NamedParamRef& p : m.named_parameters()) targets.emplace(p.name, p.ref.value);
+    const float* p = params;
+    for (const auto& [name, size] : layout) {
+        auto it = targets.find(name);
+        if (it == targets.end()) throw std::invalid_argument("ref_driver: the model has no parameter " + name);
+        if (it->second->numel() != size) throw std::invalid_argument("ref_driver: size mismatch for " + name);
+        *it->second = Tensor(it->second->shape(), be, std::vector<float>(p, p + size));
+        p += size;
+    }
+}
+
+struct RefBlock {
+    CPUBackend be;
+    std::unique_ptr<TransformerBlock> block;
+    int64_t n = 0, l = 0, d = 0;
+};
+
+struct RefLM {
+    CPUBackend be;
+    std::unique_ptr<CausalLM> lm;
+    px_model_config c{};
+    int64_t n = 0, l = 0;
+};
+
+LRPRuleConfig rule(float eps, int bias_in_denominator) {
+    LRPRuleConfig r{eps};
+    r.epsilon_bias_in_denominator = bias_in_denominator != 0;
+    return r;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* pxr_last_error(void) { return g_error.c_str(); }
+
+void* pxr_block_create(const px_model_config* cfg, const float* params) {
+    RefBlock* out = nullptr;
+    guarded([&] {
+        auto b = std::make_unique<RefBlock>();
+        TransformerBlockOptions opt;
+        opt.norm_eps = cfg->rms_norm_eps;
+        opt.mlp_bias = cfg->mlp_bias != 0;
+        b->block = std::make_unique<TransformerBlock>(attention_config(*cfg), cfg->intermediate_size, &b->be, opt);
+        load(*b->block, block_layout(*cfg), params, &b->be);
+        b->d = cfg->hidden_size;
+        out = b.release();
+    });
+    return out;
+}
+
+int pxr_block_forward(void* h, const float* x, int64_t n, int64_t l, float* y) {
+    return guarded([&] {
+        auto* b = static_cast<RefBlock*>(h);
+        b->n = n;
+        b->l = l;
+        Tensor in(Shape({n, l, b->d}), &b->be, std::vector<float>(x, x + n * l * b->d));
+        const std::vector<float> out = b->block->forward(in).to_host_vector();
+        std::copy(out.begin(), out.end(), y);
+    });
+}
+
+int pxr_block_relevance(void* h, const float* r_out, float eps, int bias_in_denominator, float* r_in) {
+    return guarded([&] {
+        auto* b = static_cast<RefBlock*>(h);
+        Tensor r(Shape({b->n, b->l, b->d}), &b->be, std::vector<float>(r_out, r_out + b->n * b->l * b->d));
+        const std::vector<float> out = b->block->propagate_relevance(r, rule(eps, bias_in_denominator)).to_host_vector();
+        std::copy(out.begin(), out.end(), r_in);
+    });
+}
+
+void pxr_block_destroy(void* h) { delete static_cast<RefBlock*>(h); }
+
+void* pxr_lm_create(const px_model_config* cfg, const float* params) {
+    RefLM* out = nullptr;
+    guarded([&] {
+        auto m = std::make_unique<RefLM>();
+        HfModelConfig hc;
+        hc.model_type = "llama";
+        hc.hidden_size = cfg->hidden_size;
+        hc.intermediate_size = cfg->intermediate_size;
+        hc.num_hidden_layers = cfg->num_layers;
+        hc.num_attention_heads = cfg->num_heads;
+        hc.num_key_value_heads = kv_heads(*cfg);
+        hc.head_dim = head_dim(*cfg);
+        hc.vocab_size = cfg->vocab_size;
+        hc.rms_norm_eps = cfg->rms_norm_eps;
+        hc.rope_theta = cfg->rope_theta;
+        hc.tie_word_embeddings = cfg->tie_word_embeddings != 0;
+        hc.qkv_bias = cfg->qkv_bias != 0;
+        hc.out_bias = cfg->out_bias != 0;
+        hc.mlp_bias = cfg->mlp_bias != 0;
+        hc.causal = cfg->causal != 0;
+        m->lm = std::make_unique<CausalLM>(hc, &m->be);
+        std::vector<std::pair<std::string, int64_t>> layout{{"embed_tokens.weight", cfg->vocab_size * cfg->hidden_size}};
+        for (int64_t i = 0; i < cfg->num_layers; ++i)
+            for (const auto& [name, size] : block_layout(*cfg)) layout.push_back({"layers." + std::to_string(i) + "." + name, size});
+        layout.push_back({"norm.weight", cfg->hidden_size});
+        if (!cfg->tie_word_embeddings) layout.push_back({"lm_head.weight", cfg->hidden_size * cfg->vocab_size});
+        load(*m->lm, layout, params, &m->be);
+        m->c = *cfg;
+        out = m.release();
+    });
+    return out;
+}
+
+int pxr_lm_forward(void* h, const int64_t* ids, int64_t n, int64_t l, float* logits) {
+    return guarded([&] {
+        auto* m = static_cast<RefLM*>(h);
+        m->n = n;
+        m->l = l;
+        std::vector<float> x(static_cast<size_t>(n * l));
+        for (size_t i = 0; i < x.size(); ++i) x[i] = static_cast<float>(ids[i]);
+        const std::vector<float> out = m->lm->forward(Tensor(Shape({n, l}), &m->be, x)).to_host_vector();
+        if (logits) std::copy(out.begin(), out.end(), logits);
+    });
+}
+
+int pxr_lm_relevance(void* h, const float* seed, float eps, int bias_in_denominator, float* r_embed, float* r_tokens,
+                     float* key_rel, float* value_rel) {
+    return guarded([&] {
+        auto* m = static_cast<RefLM*>(h);
+        const int64_t V = m->c.vocab_size;
+        Tensor s(Shape({m->n, m->l, V}), &m->be, std::vector<float>(seed, seed + m->n * m->l * V));
+        const LRPRuleConfig cfg = rule(eps, bias_in_denominator);
+        const std::vector<Tensor> bounds = m->lm->propagate_relevance_by_layer(s, cfg);
+        if (r_embed) {
+            const std::vector<float> e = bounds.front().to_host_vector();
+            std::copy(e.begin(), e.end(), r_embed);
+        }
+        if (r_tokens) {
+            const std::vector<float> t = m->lm->embed_tokens().propagate_relevance(bounds.front(), cfg).to_host_vector();
+            std::copy(t.begin(), t.end(), r_tokens);
+        }
+        const size_t kv = static_cast<size_t>(m->n * m->l * kv_heads(m->c) * head_dim(m->c));
+        for (int64_t i = 0; i < m->lm->num_layers(); ++i) {
+            MultiHeadAttentionModule& mha = m->lm->layer(i).mha();
+            if (key_rel) {
+                const std::vector<float> k = mha.key_relevance().to_host_vector();
+                std::copy(k.begin(), k.end(), key_rel + i * kv);
+            }
+            if (value_rel) {
+                const std::vector<float> v = mha.value_relevance().to_host_vector();
+                std::copy(v.begin(), v.end(), value_rel + i * kv);
+            }
+        }
+    });
+}
+
+void pxr_lm_destroy(void* h) { delete static_cast<RefLM*>(h); }
+
+int pxr_linear_relevance(const float* x, const float* w, const float* bias, const float* r, int64_t n, int64_t in,
+                         int64_t out, float eps, int bias_in_denominator, float* r_in) {
+    return guarded([&] {
+        CPUBackend be;
+        LinearModule lin(in, out, &be, bias != nullptr);
+        lin.set_weight(std::vector<float>(w, w + in * out));
+        if (bias) lin.set_bias(std::vector<float>(bias, bias + out));
+        (void)lin.forward(Tensor(Shape({n, in}), &be, std::vector<float>(x, x + n * in)));
+        Tensor rr(Shape({n, out}), &be, std::vector<float>(r, r + n * out));
+        const std::vector<float> res = lin.propagate_relevance(rr, rule(eps, bias_in_denominator)).to_host_vector();
+        std::copy(res.begin(), res.end(), r_in);
+    });
+}
+
+void pxr_lrp_bilinear_matmul(const float* a, const float* b, const float* o, const float* r_o, float* r_a, float* r_b,
+                             size_t slices, size_t m, size_t p, size_t q, float eps, int bt) {
+    CPUBackend be;
+    be.lrp_bilinear_matmul(a, b, o, r_o, r_a, r_b, slices, m, p, q, eps, bt != 0);
+}
+
+void pxr_gemm_ex(const float* a, int ta, const float* b, int tb, float* out, size_t m, size_t k, size_t n, float beta) {
+    CPUBackend be;
+    be.gemm_ex(a, ta != 0, b, tb != 0, out, m, k, n, beta);
+}
+
+}  // extern "C"

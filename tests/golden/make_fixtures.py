@@ -1,0 +1,52 @@
+"""Writes the committed golden fixtures under tests/golden/ from the reference's own test data.
+
+Run in a container that has the reference at /root/reference (it never runs on the GPU box):
+
+    python tests/golden/make_fixtures.py
+
+What it takes, all data (no source text):
+  * hf_tiny/<model>/: the tiny HF checkpoints with their golden logits (transformers) and AttnLRP
+    relevance (LXT 2.1) -- copied byte for byte from tests/fixtures/hf_tiny/.
+  * lxt_values.json: the float vectors pasted into tests/lrp_reference_test.cpp (kMhaLogits,
+    kMhaRelevance, kBlockLogits, kBlockRelevance), parsed out of the file's array literals.
+"""
+import json
+import os
+import re
+import shutil
+
+REF = os.environ.get("PULSATRIX_REF", "/root/reference")
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+MODELS = ("llama", "qwen2")
+FILES = ("config.json", "golden.safetensors", "attnlrp.safetensors", "model.safetensors",
+         "model.safetensors.index.json", "model-00001-of-00002.safetensors", "model-00002-of-00002.safetensors")
+
+
+def copy_hf_tiny():
+    for m in MODELS:
+        src = os.path.join(REF, "tests", "fixtures", "hf_tiny", m)
+        dst = os.path.join(HERE, "hf_tiny", m)
+        os.makedirs(dst, exist_ok=True)
+        for f in FILES:
+            p = os.path.join(src, f)
+            if os.path.exists(p):
+                shutil.copyfile(p, os.path.join(dst, f))
+
+
+def extract_lxt_values():
+    text = open(os.path.join(REF, "tests", "lrp_reference_test.cpp")).read()
+    out = {}
+    for name in ("kMhaLogits", "kMhaRelevance", "kBlockLogits", "kBlockRelevance"):
+        m = re.search(r"const std::vector<float> %s = \{([^}]*)\};" % name, text)
+        if m is None:
+            raise RuntimeError("missing " + name)
+        out[name] = [float(v.strip().rstrip("f")) for v in m.group(1).split(",") if v.strip()]
+    with open(os.path.join(HERE, "lxt_values.json"), "w") as f:
+        json.dump(out, f, indent=1)
+
+
+if __name__ == "__main__":
+    copy_hf_tiny()
+    extract_lxt_values()
+    print("fixtures written under", HERE)

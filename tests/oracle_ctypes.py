@@ -1,0 +1,274 @@
+"""ctypes bindings for the CPU oracle (oracle/liboracle.so) and, where it was built, the compiled
+reference (oracle/_ref/libpxref.so).
+
+Test infrastructure: the oracle is the checker for the MI355X path, never part of it.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+ORACLE_SO = os.path.join(ROOT, "oracle", "liboracle.so")
+REF_SO = os.path.join(ROOT, "oracle", "_ref", "libpxref.so")
+
+_f32p = ctypes.POINTER(ctypes.c_float)
+_i64p = ctypes.POINTER(ctypes.c_int64)
+
+
+class ModelConfig(ctypes.Structure):
+    """px_model_config (oracle/pxo.h, include/pulsatrix_amd.h)."""
+
+    _fields_ = [
+        ("vocab_size", ctypes.c_int64),
+        ("hidden_size", ctypes.c_int64),
+        ("num_layers", ctypes.c_int64),
+        ("num_heads", ctypes.c_int64),
+        ("num_kv_heads", ctypes.c_int64),
+        ("head_dim", ctypes.c_int64),
+        ("intermediate_size", ctypes.c_int64),
+        ("rms_norm_eps", ctypes.c_float),
+        ("rope_theta", ctypes.c_float),
+        ("use_rope", ctypes.c_int32),
+        ("rope_rotate_half", ctypes.c_int32),
+        ("causal", ctypes.c_int32),
+        ("qkv_bias", ctypes.c_int32),
+        ("out_bias", ctypes.c_int32),
+        ("mlp_bias", ctypes.c_int32),
+        ("tie_word_embeddings", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
+    ]
+
+    def kv_heads(self):
+        return self.num_kv_heads if self.num_kv_heads > 0 else self.num_heads
+
+    def hd(self):
+        return self.head_dim if self.head_dim > 0 else self.hidden_size // self.num_heads
+
+
+def model_config(**kw):
+    base = dict(vocab_size=0, hidden_size=0, num_layers=1, num_heads=1, num_kv_heads=0, head_dim=0,
+                intermediate_size=0, rms_norm_eps=1e-5, rope_theta=10000.0, use_rope=1, rope_rotate_half=1,
+                causal=1, qkv_bias=0, out_bias=0, mlp_bias=0, tie_word_embeddings=1, reserved=0)
+    base.update(kw)
+    return ModelConfig(**base)
+
+
+def fptr(a):
+    return a.ctypes.data_as(_f32p) if a is not None else None
+
+
+def block_layout(cfg):
+    """(name, shape) of one block's parameters in the flat blob order."""
+    d, q, kv, f = cfg.hidden_size, cfg.num_heads * cfg.hd(), cfg.kv_heads() * cfg.hd(), cfg.intermediate_size
+    out = [("norm1.weight", (d,))]
+
+    def lin(name, i, o, bias):
+        out.append((name + ".weight", (i, o)))
+        if bias:
+            out.append((name + ".bias", (o,)))
+
+    lin("mha.q_proj", d, q, cfg.qkv_bias)
+    lin("mha.k_proj", d, kv, cfg.qkv_bias)
+    lin("mha.v_proj", d, kv, cfg.qkv_bias)
+    lin("mha.out_proj", q, d, cfg.out_bias)
+    out.append(("norm2.weight", (d,)))
+    lin("swiglu.gate_proj", d, f, cfg.mlp_bias)
+    lin("swiglu.up_proj", d, f, cfg.mlp_bias)
+    lin("swiglu.down_proj", f, d, cfg.mlp_bias)
+    return out
+
+
+def lm_layout(cfg):
+    out = [("embed_tokens.weight", (cfg.vocab_size, cfg.hidden_size))]
+    for i in range(cfg.num_layers):
+        out += [("layers.%d.%s" % (i, n), s) for n, s in block_layout(cfg)]
+    out.append(("norm.weight", (cfg.hidden_size,)))
+    if not cfg.tie_word_embeddings:
+        out.append(("lm_head.weight", (cfg.hidden_size, cfg.vocab_size)))
+    return out
+
+
+def pack(layout, tensors):
+    parts = [np.ascontiguousarray(tensors[name], dtype=np.float32).reshape(shape) for name, shape in layout]
+    return np.concatenate([p.ravel() for p in parts]).astype(np.float32)
+
+
+class _Lib:
+    def __init__(self, path, prefix):
+        self.lib = ctypes.CDLL(path)
+        self.p = prefix
+        L = self.lib
+        cfgp = ctypes.POINTER(ModelConfig)
+        for name, res, args in [
+            ("block_create", ctypes.c_void_p, [cfgp, _f32p]),
+            ("block_forward", ctypes.c_int, [ctypes.c_void_p, _f32p, ctypes.c_int64, ctypes.c_int64, _f32p]),
+            ("block_relevance", ctypes.c_int, [ctypes.c_void_p, _f32p, ctypes.c_float, ctypes.c_int, _f32p]),
+            ("block_destroy", None, [ctypes.c_void_p]),
+            ("lm_create", ctypes.c_void_p, [cfgp, _f32p]),
+            ("lm_forward", ctypes.c_int, [ctypes.c_void_p, _i64p, ctypes.c_int64, ctypes.c_int64, _f32p]),
+            ("lm_relevance", ctypes.c_int, [ctypes.c_void_p, _f32p, ctypes.c_float, ctypes.c_int, _f32p, _f32p, _f32p,
+                                            _f32p]),
+            ("lm_destroy", None, [ctypes.c_void_p]),
+            ("last_error", ctypes.c_char_p, []),
+        ]:
+            fn = getattr(L, prefix + name)
+            fn.restype = res
+            fn.argtypes = args
+
+    def fn(self, name):
+        return getattr(self.lib, self.p + name)
+
+    def check(self, rc):
+        if rc != 0:
+            raise RuntimeError(self.fn("last_error")().decode())
+
+    # ---- block ----
+    def block(self, cfg, params):
+        return _Block(self, cfg, params)
+
+    def lm(self, cfg, params):
+        return _LM(self, cfg, params)
+
+
+class _Block:
+    def __init__(self, lib, cfg, params):
+        self.lib, self.cfg = lib, cfg
+        self.params = np.ascontiguousarray(params, dtype=np.float32)
+        self.h = lib.fn("block_create")(ctypes.byref(cfg), fptr(self.params))
+        if not self.h:
+            raise RuntimeError(lib.fn("last_error")().decode())
+
+    def forward(self, x):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        n, l, _ = x.shape
+        y = np.empty_like(x)
+        self.lib.check(self.lib.fn("block_forward")(self.h, fptr(x), n, l, fptr(y)))
+        return y
+
+    def relevance(self, r, eps, bias_in_denominator):
+        r = np.ascontiguousarray(r, dtype=np.float32)
+        out = np.empty_like(r)
+        self.lib.check(self.lib.fn("block_relevance")(self.h, fptr(r), eps, int(bias_in_denominator), fptr(out)))
+        return out
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            self.lib.fn("block_destroy")(self.h)
+            self.h = None
+
+
+class _LM:
+    def __init__(self, lib, cfg, params):
+        self.lib, self.cfg = lib, cfg
+        self.params = np.ascontiguousarray(params, dtype=np.float32)
+        self.h = lib.fn("lm_create")(ctypes.byref(cfg), fptr(self.params))
+        if not self.h:
+            raise RuntimeError(lib.fn("last_error")().decode())
+        self.shape = None
+
+    def forward(self, ids):
+        ids = np.ascontiguousarray(ids, dtype=np.int64)
+        n, l = ids.shape
+        logits = np.empty((n, l, self.cfg.vocab_size), dtype=np.float32)
+        self.lib.check(self.lib.fn("lm_forward")(self.h, ids.ctypes.data_as(_i64p), n, l, fptr(logits)))
+        self.shape = (n, l)
+        return logits
+
+    def relevance(self, seed, eps, bias_in_denominator, want_kv=False):
+        n, l = self.shape
+        c = self.cfg
+        seed = np.ascontiguousarray(seed, dtype=np.float32)
+        r_embed = np.empty((n, l, c.hidden_size), dtype=np.float32)
+        r_tok = np.empty((n, l), dtype=np.float32)
+        kv = (c.num_layers, n * l, c.kv_heads() * c.hd())
+        k = np.empty(kv, dtype=np.float32) if want_kv else None
+        v = np.empty(kv, dtype=np.float32) if want_kv else None
+        self.lib.check(self.lib.fn("lm_relevance")(self.h, fptr(seed), eps, int(bias_in_denominator), fptr(r_embed),
+                                                    fptr(r_tok), fptr(k), fptr(v)))
+        return (r_embed, r_tok, k, v) if want_kv else (r_embed, r_tok)
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            self.lib.fn("lm_destroy")(self.h)
+            self.h = None
+
+
+_oracle = None
+_ref = None
+
+
+def oracle():
+    global _oracle
+    if _oracle is None:
+        if not os.path.exists(ORACLE_SO):
+            raise RuntimeError("oracle/liboracle.so is not built (run __graft_entry__.build())")
+        _oracle = _Lib(ORACLE_SO, "pxo_")
+        L = _oracle.lib
+        L.pxo_fill_normal.argtypes = [_f32p, ctypes.c_size_t, ctypes.c_uint64, ctypes.c_double]
+        L.pxo_fill_normal.restype = None
+        L.pxo_param_count.argtypes = [ctypes.POINTER(ModelConfig)]
+        L.pxo_param_count.restype = ctypes.c_int64
+        L.pxo_block_param_count.argtypes = [ctypes.POINTER(ModelConfig)]
+        L.pxo_block_param_count.restype = ctypes.c_int64
+        L.pxo_set_threads.argtypes = [ctypes.c_int]
+        L.pxo_get_threads.restype = ctypes.c_int
+        L.pxo_rope_tables.argtypes = [ctypes.c_int64, ctypes.c_float, ctypes.c_int64, ctypes.c_int64, _f32p, _f32p]
+    return _oracle
+
+
+def ref():
+    """The compiled reference, or None where oracle/_ref was not built."""
+    global _ref
+    if _ref is None and os.path.exists(REF_SO):
+        _ref = _Lib(REF_SO, "pxr_")
+    return _ref
+
+
+def fill_normal(n, seed, std):
+    out = np.empty(n, dtype=np.float32)
+    oracle().lib.pxo_fill_normal(fptr(out), n, seed, std)
+    return out
+
+
+def synthetic_params(cfg, seed, std=0.02, block=False):
+    """The flat blob of a random-init model: N(0, std) from seed, every RMSNorm gamma = 1."""
+    layout = block_layout(cfg) if block else lm_layout(cfg)
+    total = sum(int(np.prod(s)) for _, s in layout)
+    blob = fill_normal(total, seed, std)
+    off = 0
+    for name, shape in layout:
+        size = int(np.prod(shape))
+        if name.endswith("norm1.weight") or name.endswith("norm2.weight") or name == "norm.weight":
+            blob[off:off + size] = 1.0
+        off += size
+    return blob
+
+
+def linear_forward(x, w, b):
+    """Oracle LinearModule::forward: returns (pre_bias, y)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    n, i = x.shape
+    o = w.shape[1]
+    pre, y = np.empty((n, o), np.float32), np.empty((n, o), np.float32)
+    bb = None if b is None else np.ascontiguousarray(b, dtype=np.float32)
+    L = oracle()
+    L.lib.pxo_linear_forward.argtypes = [_f32p, _f32p, _f32p, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, _f32p,
+                                         _f32p]
+    L.check(L.lib.pxo_linear_forward(fptr(x), fptr(w), fptr(bb), n, i, o, fptr(pre), fptr(y)))
+    return pre, y
+
+
+def linear_relevance(x, w, b, pre, r, eps, bias_in_denominator):
+    x, w, pre, r = (np.ascontiguousarray(a, dtype=np.float32) for a in (x, w, pre, r))
+    n, i = x.shape
+    o = w.shape[1]
+    out = np.empty((n, i), np.float32)
+    bb = None if b is None else np.ascontiguousarray(b, dtype=np.float32)
+    L = oracle()
+    L.lib.pxo_linear_relevance.argtypes = [_f32p, _f32p, _f32p, _f32p, _f32p, ctypes.c_int64, ctypes.c_int64,
+                                           ctypes.c_int64, ctypes.c_float, ctypes.c_int, _f32p]
+    L.check(L.lib.pxo_linear_relevance(fptr(x), fptr(w), fptr(bb), fptr(pre), fptr(r), n, i, o, eps,
+                                       int(bias_in_denominator), fptr(out)))
+    return out
