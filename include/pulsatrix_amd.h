@@ -1,0 +1,104 @@
+/*
+ * pulsatrix_amd.h -- C ABI of the MI355X host framework (libpulsatrix_amd.so).
+ *
+ * The C++17 surface (MI355XBackend, TransformerBlock, CausalLM, ... in
+ * pulsatrix_amd/csrc/host/include/pulsatrix/) is what a C++ caller of Pulsatrix uses directly. This
+ * header is the flat binding a foreign-language caller (ctypes, cgo, JNI) uses for the same path:
+ * plain pointers and sizes, no C++ types. Entry points return 0 on success and -1 on failure;
+ * pxa_last_error() then holds the message of the C++ exception (std::invalid_argument,
+ * std::logic_error, std::runtime_error -- the reference's error behaviour).
+ *
+ * Weights travel as one flat float blob in the reference's parameter order and layout
+ * (CausalLM::named_parameters(), causal_lm.cpp:115-125; Linear weights (in, out)):
+ *   embed_tokens.weight (V, d)
+ *   per layer: norm1.weight (d), mha.{q,k,v}_proj.weight (d, H*D | Hkv*D) [+ .bias when qkv_bias],
+ *              mha.out_proj.weight (H*D, d) [+ .bias when out_bias], norm2.weight (d),
+ *              swiglu.{gate,up}_proj.weight (d, F) [+ .bias], swiglu.down_proj.weight (F, d) [+ .bias]
+ *   norm.weight (d), lm_head.weight (d, V) when not tied.
+ * A bare block uses the per-layer part alone.
+ */
+#ifndef PULSATRIX_AMD_H
+#define PULSATRIX_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* HfModelConfig (include/pulsatrix/hf_model.hpp:33-101) + AttentionConfig/TransformerBlockOptions
+ * fields the path reads; vocab_size == 0 describes a bare TransformerBlock. */
+typedef struct px_model_config {
+    int64_t vocab_size;
+    int64_t hidden_size;
+    int64_t num_layers;
+    int64_t num_heads;
+    int64_t num_kv_heads;
+    int64_t head_dim;
+    int64_t intermediate_size;
+    float rms_norm_eps;
+    float rope_theta;
+    int32_t use_rope;
+    int32_t rope_rotate_half;
+    int32_t causal;
+    int32_t qkv_bias;
+    int32_t out_bias;
+    int32_t mlp_bias;
+    int32_t tie_word_embeddings;
+    int32_t reserved;
+} px_model_config;
+
+const char* pxa_last_error(void);
+int pxa_device_count(void);
+
+/* The process-wide MI355XBackend on device 0 (created on first use) that the block / LM handles
+ * below run on; its HIP stream, and a wait for it. */
+void* pxa_backend(void);
+void* pxa_backend_stream(void);
+int pxa_backend_synchronize(void);
+/* Bytes the backend's caching allocator holds (in use, cached). */
+int pxa_backend_memory(size_t* in_use, size_t* cached);
+
+/* Seeded N(0, stddev) on the host: SplitMix64 bits, Box-Muller in double (src/portable_random.hpp:11-29). */
+void pxa_fill_normal(float* dst, size_t n, uint64_t seed, double stddev);
+int64_t pxa_param_count(const px_model_config* cfg);
+int64_t pxa_block_param_count(const px_model_config* cfg);
+/* The flat blob of a random-init model: N(0, stddev) from seed, every RMSNorm gamma = 1. */
+int pxa_synthetic_params(const px_model_config* cfg, int block, uint64_t seed, double stddev, float* dst);
+
+/* ---- TransformerBlock (transformer_block.hpp) ; host tensors ---- */
+void* pxa_block_create(const px_model_config* cfg, const float* params);
+int pxa_block_forward(void* block, const float* x, int64_t n, int64_t l, float* y);
+int pxa_block_relevance(void* block, const float* r_out, float eps, int bias_in_denominator, float* r_in);
+void pxa_block_destroy(void* block);
+
+/* ---- CausalLM (causal_lm.hpp) ---- */
+void* pxa_lm_create(const px_model_config* cfg, const float* params);
+void* pxa_lm_create_random(const px_model_config* cfg, uint64_t seed, double stddev);
+/* Host ids (n, l) -> host logits (n, l, vocab) (nullable). CausalLM::forward. */
+int pxa_lm_forward(void* lm, const int64_t* ids, int64_t n, int64_t l, float* logits);
+/* Host seed (n, l, vocab) -> host outputs (each nullable): r_embed (n, l, d) =
+ * propagate_relevance_by_layer()[0]; r_tokens (n, l); key_rel / value_rel per layer
+ * (layers, n*l, Hkv*D) = MultiHeadAttentionModule::key_relevance() / value_relevance(). */
+int pxa_lm_relevance(void* lm, const float* seed, float eps, int bias_in_denominator, float* r_embed,
+                     float* r_tokens, float* key_rel, float* value_rel);
+/* The device hot path (CausalLM::explain_device): ids (n*l floats) in HBM -> forward, argmax (or
+ * targets_in, host, n entries, nullable) seed at each sequence's last position, relevance, per-token
+ * sums into token_rel (n*l, HBM) and targets (n int64, HBM). Asynchronous on pxa_backend_stream(). */
+int pxa_lm_explain_device(void* lm, const float* ids, int64_t n, int64_t l, float eps, int bias_in_denominator,
+                          float* token_rel, int64_t* targets, const int64_t* targets_in, int unit_seed);
+/* Captures one pxa_lm_explain_device call into a HIP graph (no launch); pxa_lm_replay runs it. */
+int pxa_lm_capture_explain(void* lm, const float* ids, int64_t n, int64_t l, float eps, int bias_in_denominator,
+                           float* token_rel, int64_t* targets);
+int pxa_lm_replay(void* lm);
+/* Device pointers of the last pass: logits (n*l*vocab), embedding-level relevance (n*l*d). */
+const float* pxa_lm_last_logits(void* lm);
+const float* pxa_lm_last_embedding_relevance(void* lm);
+void pxa_lm_destroy(void* lm);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PULSATRIX_AMD_H */

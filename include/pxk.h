@@ -1,0 +1,220 @@
+/*
+ * pxk.h -- C ABI of the gfx950 kernel library (libpxk_gfx950.so).
+ *
+ * Hand-written HIP kernels for MI355X (CDNA4, wave64, fp32 MFMA) behind plain C entry points:
+ * device pointers, sizes, scalars and a hipStream_t passed as void*. No C++ types cross this
+ * boundary. Every entry point is asynchronous on `stream` (NULL = the default stream), returns
+ * PXK_OK or an error code, and leaves a message for pxk_last_error(). Sizes are validated on the
+ * host before any launch; n == 0 is a no-op (src/hip_backend.hip:142-147 contract).
+ *
+ * Each entry point names the reference interface it replaces: the DeviceBackend virtual in
+ * include/pulsatrix/device_backend.hpp (file:line) and, where Pulsatrix's HIP backend ran it
+ * through hipBLAS or a one-thread-per-output kernel, that implementation. Aliasing follows the
+ * virtual's contract.
+ */
+#ifndef PXK_H
+#define PXK_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    PXK_OK = 0,
+    PXK_ERR_INVALID = 1,  /* bad size, layout or mode: nothing was launched */
+    PXK_ERR_LAUNCH = 2,   /* the HIP runtime refused the launch */
+    PXK_ERR_WORKSPACE = 3 /* a split-K GEMM was given too small a workspace */
+};
+
+const char* pxk_last_error(void);
+/* Library and device identification, for the test that the library loads on the GPU box. */
+const char* pxk_version(void);
+
+/* ---- the fused fp32 MFMA GEMM ------------------------------------------------------------------
+ * C[b] = op(Aeff[b]) * op(B[b]) over a batch of independent products, fp32 in, fp32 MFMA
+ * (v_mfma_f32_16x16x4_f32) with fp32 accumulation, LDS-staged double-buffered 64x64 or 128x128
+ * tiles, optional deterministic split-K (fixed-order reduction, no atomics in the sum).
+ *
+ * Batch addressing, per operand: batch index b = outer * inner + i (inner = desc.inner), and
+ *   base(b, s) = ptr + outer * batch_stride + (i / inner_div) * inner_stride + s * group_stride
+ * where s runs over desc.kgroups sub-products accumulated into the same output (a GQA key/value
+ * head summing its query heads). inner_div maps a query head to its KV head.
+ *
+ * Replaces: DeviceBackend::gemm (device_backend.hpp:303), gemm_ex (:361), gemm_strided_batched
+ * (:372-383) -- HIPBackend's hipblasSgemm / hipblasSgemmStridedBatched (hip_backend.hip:122-139,
+ * 170-190, 277-295) -- and, through the prologue/epilogue modes, the op sequences of
+ * lrp_rules::linear (lrp_rules.cpp:197-220), DeviceBackend::lrp_linear (:627), lrp_bilinear_matmul
+ * (:643) and the tied head's epsilon rule (tied_lm_head_module.cpp:76-111).
+ */
+typedef struct pxk_operand {
+    const float* ptr;
+    int64_t ld;           /* row stride (elements) of the stored matrix */
+    int64_t batch_stride; /* per outer batch index */
+    int64_t inner_stride; /* per (inner index / inner_div) */
+    int64_t inner_div;    /* <= 1: none */
+    int64_t group_stride; /* per k-group sub-product */
+} pxk_operand;
+
+enum {
+    PXK_CAUSAL_NONE = 0,
+    PXK_CAUSAL_TRI = 1,    /* only output tiles touching n <= m are computed; the rest are not written */
+    PXK_CAUSAL_K_LE_M = 2, /* the sum runs over k <= m (P @ V, S @ K) */
+    PXK_CAUSAL_K_GE_M = 3  /* the sum runs over k >= m (P^T @ S, S^T @ Q) */
+};
+
+enum {
+    PXK_PRO_NONE = 0,
+    PXK_PRO_DIV_STAB = 1 /* A / (Z + bias[k] + eps * sign(Z + bias[k])), sign(0) = +1 (lrp_math.hpp:17) */
+};
+
+enum {
+    PXK_EPI_STORE = 0,       /* C = acc, or acc + beta * C when beta != 0 */
+    PXK_EPI_STORE_BIAS = 1,  /* C = acc (pre-bias z); C2 = acc + bias[n] when bias given */
+    PXK_EPI_ADD_RESID = 2,   /* C = acc; C2 = acc + bias[n] (bias optional, else C2 = C); C3 = X + C2 */
+    PXK_EPI_MUL_X = 3,       /* C = X * acc, or Y + X * acc when Y is given */
+    PXK_EPI_SPV = 4,         /* r = X * acc; C = r / (2 X + eps * sign X) */
+    PXK_EPI_ROPE_REL = 5,    /* r = Y * acc; RoPE epsilon rule with x = X, y = Y over the head's pairs;
+                                C = r_in (may be NULL); C2 = r_in / stab(Z + bias[n]) */
+    PXK_EPI_VALUE_REL = 6,   /* r = Y * acc; C = r (may be NULL); C2 = r / stab(Z + bias[n]) */
+    PXK_EPI_SWIGLU_REL = 7   /* SwiGLU relevance: rh = X * acc (X = hidden); c = Y * W (gate_post * up);
+                                rg = (c / (2c + eps sign c)) * rh; C = rg / stab(Z2 + bias[n]) (gate);
+                                C2 = rg / stab(Z3 + bias2[n]) (up). Z stays the prologue's. */
+};
+
+typedef struct pxk_gemm_desc {
+    int64_t m, n, k;
+    int64_t batch;   /* >= 1 */
+    int64_t inner;   /* >= 1 */
+    int64_t kgroups; /* >= 1 */
+    int32_t trans_a; /* A stored (K x M) instead of (M x K) */
+    int32_t trans_b; /* B stored (N x K) instead of (K x N) */
+    int32_t causal;
+    int32_t prologue;
+    int32_t epilogue;
+    int32_t splits; /* split-K factor; 0 = chosen by the library */
+    float beta;
+    float eps;
+    pxk_operand a, b, c;
+    pxk_operand z;        /* prologue denominators, laid out like A */
+    pxk_operand z_bias;   /* prologue bias over k (ld 0; batch strides as for A), ptr nullable */
+    pxk_operand c2, c3;   /* extra outputs, laid out like C */
+    pxk_operand x, y, w;  /* epilogue inputs, laid out like C */
+    pxk_operand z2, z3;   /* SWIGLU_REL's gate / up denominators */
+    pxk_operand e_bias;   /* epilogue bias over n (ld 0; batch strides as for C), ptr nullable */
+    pxk_operand e_bias2;
+    const float* cos_t;   /* RoPE tables (positions x head_dim/2), position = m */
+    const float* sin_t;
+    int64_t head_dim;     /* ROPE_REL: pairs live inside each head_dim-wide column block */
+    int32_t rope_half;    /* 1: pair (i, i + D/2); 0: pair (2i, 2i+1) */
+    int32_t reserved;
+    float* workspace;     /* split-K partials */
+    size_t workspace_bytes;
+} pxk_gemm_desc;
+
+/* Bytes of workspace pxk_gemm needs for this descriptor (0 when it runs without split-K). */
+size_t pxk_gemm_workspace(const pxk_gemm_desc* d);
+int pxk_gemm(const pxk_gemm_desc* d, void* stream);
+
+/* The (trans_a, trans_b, prologue, epilogue) combinations built into the library; pxk_gemm
+ * rejects others with PXK_ERR_INVALID. */
+int pxk_gemm_supported(int trans_a, int trans_b, int prologue, int epilogue);
+
+/* Plain gemm_ex: out = op(a) op(b) + beta out, row-major, contiguous (device_backend.hpp:361). */
+int pxk_gemm_ex(const float* a, int transpose_a, const float* b, int transpose_b, float* out, int64_t m, int64_t k,
+                int64_t n, float beta, float* workspace, size_t workspace_bytes, void* stream);
+
+/* ---- elementwise (memory-bound, 128-bit accesses where aligned) --------------------------------- */
+/* DeviceBackend::fill (:291) */
+int pxk_fill(float* ptr, float value, int64_t n, void* stream);
+/* DeviceBackend::elementwise (:313); op = ElementwiseOp order: Relu, Neg, Tanh, Sigmoid, Silu, Exp,
+ * GeluTanh, Gelu (device_backend.hpp:39-48). */
+int pxk_elementwise(int op, const float* in, float* out, int64_t n, void* stream);
+/* DeviceBackend::add (:328), mul (:344), axpby (:436) */
+int pxk_add(const float* a, const float* b, float* out, int64_t n, void* stream);
+int pxk_mul(const float* a, const float* b, float* out, int64_t n, void* stream);
+int pxk_axpby(float alpha, const float* x, float beta, const float* y, float* out, int64_t n, void* stream);
+/* DeviceBackend::add_row_vector (:405) */
+int pxk_add_row_vector(const float* in, const float* row, float* out, int64_t rows, int64_t cols, void* stream);
+/* DeviceBackend::lrp_residual_split (:631), lrp_bilinear_elementwise (:635), lrp_stabilized_divide (:712) */
+int pxk_lrp_residual_split(const float* a, const float* b, const float* r, float* r_a, float* r_b, int64_t n,
+                           float eps, void* stream);
+int pxk_lrp_bilinear_elementwise(const float* a, const float* b, const float* r, float* r_out, int64_t n, float eps,
+                                 void* stream);
+int pxk_lrp_stabilized_divide(const float* r, const float* denom, const float* gate, float* out, int64_t n, float eps,
+                              int gate_mode, void* stream);
+/* The Eq. 15 scaled relevance of a product O = A B: s = r / (2 o + eps sign o) (lrp_math.hpp:57-61),
+ * the shared factor of DeviceBackend::lrp_bilinear_matmul's two shares (:643). */
+int pxk_lrp_bilinear_scale(const float* r, const float* o, float* s, int64_t n, float eps, void* stream);
+/* SwiGLU gate (swiglu_module.cpp:80-88): gate_post = silu(gate), hidden = gate_post * up, over an
+ * (rows x 2F) [gate | up] buffer with row stride ld. */
+int pxk_swiglu_forward(const float* gu, int64_t ld, float* gate_post, float* hidden, int64_t rows, int64_t f,
+                       void* stream);
+/* DeviceBackend::copy_2d (:783), accumulate_rows (:792), gather_rows (:596) */
+int pxk_copy_2d(float* dst, int64_t dst_stride, const float* src, int64_t src_stride, int64_t rows, int64_t cols,
+                void* stream);
+int pxk_accumulate_rows(const float* in, float* out, int64_t rows, int64_t cols, void* stream);
+int pxk_gather_rows(const float* table, const float* indices, float* out, int64_t count, int64_t dim, void* stream);
+/* DeviceBackend::column_sums (:399) */
+int pxk_column_sums(const float* in, float* out, int64_t rows, int64_t cols, float beta, void* stream);
+
+/* ---- row kernels (one wave64 per row, shuffle reductions) ------------------------------------- */
+/* DeviceBackend::rms_norm_forward (:550); row_rms may be NULL. */
+int pxk_rms_norm_forward(const float* in, const float* gamma, float* out, float* row_rms, int64_t rows, int64_t cols,
+                         float eps, void* stream);
+/* DeviceBackend::softmax_rows (:456) */
+int pxk_softmax_rows(const float* in, float* out, int64_t rows, int64_t cols, void* stream);
+/* DeviceBackend::lrp_softmax_rows (:648) */
+int pxk_lrp_softmax_rows(const float* x, const float* y, const float* r, float* r_in, int64_t rows, int64_t cols,
+                         void* stream);
+/* Per-row sums (EmbeddingModule::propagate_relevance's ones-gemm, embedding_module.cpp:116-123). */
+int pxk_row_sums(const float* in, float* out, int64_t rows, int64_t cols, void* stream);
+/* DeviceBackend::sum (:504) / dot (:443): deterministic two-pass reduction into out[0]. */
+int pxk_sum(const float* in, int64_t n, float* out, float* partials, void* stream);
+int pxk_dot(const float* a, const float* b, int64_t n, float* out, float* partials, void* stream);
+size_t pxk_reduce_partials(int64_t n);
+
+/* ---- attention ------------------------------------------------------------------------------- */
+/* Causal/plain softmax of scaled scores (the module's axpby + attention_mask_fill(lowest) +
+ * softmax_rows, multihead_attention_module.cpp:280-285): P = softmax(scale * raw) over the keys
+ * each query sees; masked entries of P are written 0. raw (slices, L, L); only its visible
+ * entries are read. */
+int pxk_attention_softmax(const float* raw, float* p, int64_t slices, int64_t l, float scale, int causal,
+                          void* stream);
+/* The AttnLRP score step, fused: r_sc = x * (r_attn - P * sum(r_attn)) with x = scale * raw
+ * (SoftmaxModule rule, lrp_math.hpp:89-98), masked entries 0 (fill_masked(0), :441), then the
+ * Q K^T bilinear denominator s = r_sc / (2 raw + eps sign raw) (lrp_math.hpp:57-61). Writes s
+ * over whole rows (0 where masked). s may alias r_attn. */
+int pxk_attention_lrp_scores(const float* r_attn, const float* p, const float* raw, float* s, int64_t slices,
+                             int64_t l, float scale, float eps, int causal, void* stream);
+/* RoPE of the packed projections (rope_module.cpp:104-121 + permute-free layout): q_out (rows x H*D),
+ * k_out (rows x Hkv*D) from q/k columns of `in` (row stride ld_in), positions = row % seq_len. */
+int pxk_rope_qk(const float* q_in, const float* k_in, int64_t ld_in, float* q_out, float* k_out, const float* cos_t,
+                const float* sin_t, int64_t rows, int64_t seq_len, int64_t heads, int64_t kv_heads, int64_t head_dim,
+                int rotate_half, void* stream);
+/* DeviceBackend::rope_rotate (:568) and lrp_rope (:652) over (slices, seq_len, head_dim). */
+int pxk_rope_rotate(const float* in, const float* cos_t, const float* sin_t, float* out, int64_t slices,
+                    int64_t seq_len, int64_t head_dim, int inverse, int rotate_half, void* stream);
+int pxk_lrp_rope(const float* x, const float* y, const float* r, const float* cos_t, const float* sin_t, float* r_in,
+                 int64_t slices, int64_t seq_len, int64_t head_dim, float eps, int rotate_half, void* stream);
+/* DeviceBackend::permute_0213 (:576) */
+int pxk_permute_0213(const float* in, float* out, int64_t d0, int64_t d1, int64_t d2, int64_t d3, void* stream);
+/* DeviceBackend::attention_mask_fill (:592) */
+int pxk_attention_mask_fill(float* scores, const float* key_keep, int64_t batch, int64_t heads, int64_t q_len,
+                            int64_t k_len, int causal, int64_t q_offset, int64_t window, float value, void* stream);
+
+/* ---- seeding ------------------------------------------------------------------------------------
+ * On-device LRP seed for a causal LM (src/attnlrp_parity.cpp:104-109 moved to the device): for
+ * each sequence n, target[n] = argmax of logits[n, L-1, :] (lowest index on ties) unless targets
+ * are given (targets_in != NULL), and seed = one-hot(target) * logit (OutputValue) or one-hot
+ * (unit). seed (N, L, V) is fully written; targets_out (N) as int64. */
+int pxk_lm_seed(const float* logits, int64_t n, int64_t l, int64_t vocab, const int64_t* targets_in,
+                int64_t* targets_out, float* seed, int unit, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PXK_H */

@@ -1,0 +1,73 @@
+/** @file causal_lm.hpp
+ *  @brief Llama-family decoder LM (the surface of include/pulsatrix/causal_lm.hpp:82-167):
+ *         embedding -> blocks -> RMSNorm -> tied or untied head, with AttnLRP relevance back to
+ *         the embeddings.
+ *
+ *  explain_device() is the MI355X hot path: ids already in HBM, forward, on-device argmax seed
+ *  (or given targets), relevance and per-token sums, all queued on the backend's stream with no
+ *  host round trip, on buffers whose addresses stay fixed for a given (N, L) -- so one call can
+ *  be captured into a HIP graph and replayed.
+ */
+#pragma once
+
+#include <memory>
+#include <vector>
+
+#include "pulsatrix/embedding_module.hpp"
+#include "pulsatrix/hf_model.hpp"
+#include "pulsatrix/linear_module.hpp"
+#include "pulsatrix/rms_norm_module.hpp"
+#include "pulsatrix/tied_lm_head_module.hpp"
+#include "pulsatrix/transformer_block.hpp"
+
+namespace pulsatrix {
+
+class CausalLM : public Module {
+public:
+    CausalLM(const HfModelConfig& config, DeviceBackend* backend);
+
+    /** @brief Relevance at the embeddings' input: per-token sums, (N, L). */
+    [[nodiscard]] Tensor propagate_relevance(const Tensor& relevance_out, const LRPRuleConfig& config) override;
+    /** @brief Relevance at every layer boundary, embeddings first: layers + 1 tensors (N, L, d). */
+    [[nodiscard]] std::vector<Tensor> propagate_relevance_by_layer(const Tensor& relevance_out,
+                                                                   const LRPRuleConfig& config);
+
+    [[nodiscard]] const HfModelConfig& config() const noexcept { return config_; }
+    [[nodiscard]] EmbeddingModule& embed_tokens() { return embed_; }
+    [[nodiscard]] TransformerBlock& layer(int64_t i) { return *layers_.at(static_cast<size_t>(i)); }
+    [[nodiscard]] int64_t num_layers() const noexcept { return static_cast<int64_t>(layers_.size()); }
+    [[nodiscard]] RMSNormModule& norm() { return norm_; }
+    [[nodiscard]] LinearModule* lm_head() { return lm_head_.get(); }
+
+    /** @brief Forward + seed + relevance + per-token sums on device. ids (N*L floats) in HBM;
+     *         token_relevance (N*L) and targets (N int64) written in HBM. targets_in (host, N
+     *         entries, nullable): explain those ids at each sequence's last position instead of the
+     *         argmax. unit_seed: one-hot seed (LRPSeed::OneHot) instead of the logit value. */
+    void explain_device(const float* ids, int64_t n, int64_t l, const LRPRuleConfig& config, float* token_relevance,
+                        int64_t* targets, const int64_t* targets_in = nullptr, bool unit_seed = false);
+    /** @brief Device pointers of the last pass: logits (N*L*V), embedding-level relevance (N*L*d). */
+    [[nodiscard]] const float* last_logits() const noexcept;
+    [[nodiscard]] const float* last_embedding_relevance() const noexcept { return r_embed_; }
+
+    /** @brief Fused-path forward from device ids; returns the logits pointer. */
+    const float* run_forward(const float* ids, int64_t n, int64_t l);
+    /** @brief Fused-path relevance from a device seed (N*L*V); returns the embedding-level relevance. */
+    const float* run_relevance(const float* seed, const LRPRuleConfig& config);
+
+protected:
+    Tensor forward_impl(const Tensor& input) override;
+
+private:
+    HfModelConfig config_;
+    MI355XBackend* be_;
+    EmbeddingModule embed_;
+    std::vector<std::unique_ptr<TransformerBlock>> layers_;
+    RMSNormModule norm_;
+    std::unique_ptr<TiedLMHeadModule> tied_head_;
+    std::unique_ptr<LinearModule> lm_head_;
+    int64_t N_ = 0, L_ = 0;
+    const float* r_embed_ = nullptr;
+    detail::DevBuf ids_, seed_;
+};
+
+}  // namespace pulsatrix

@@ -1,0 +1,66 @@
+/** @file fused.hpp
+ *  @brief Internals shared by the MI355X modules: module-owned device buffers and GEMM
+ *         descriptor helpers.
+ */
+#pragma once
+
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+
+#include "pulsatrix/mi355x_backend.hpp"
+#include "pulsatrix/tensor.hpp"
+
+namespace pulsatrix::detail {
+
+/** @brief A module-owned device buffer. Its storage (and address) is kept while its size is
+ *         unchanged, so repeated passes at one shape launch on the same addresses (and can be
+ *         captured into a HIP graph once). */
+class DevBuf {
+public:
+    float* ensure(DeviceBackend* be, int64_t n) {
+        if (t_.numel() != n || t_.backend() != be) t_ = Tensor::uninitialized(Shape({n}), be);
+        return t_.data();
+    }
+    [[nodiscard]] float* data() noexcept { return t_.data(); }
+    [[nodiscard]] const float* data() const noexcept { return t_.data(); }
+    [[nodiscard]] int64_t size() const noexcept { return t_.numel(); }
+    void release() { t_ = Tensor(); }
+
+private:
+    Tensor t_;
+};
+
+/** @brief The MI355X modules compute through MI355XBackend's fused kernels. */
+inline MI355XBackend* require_mi355x(DeviceBackend* be, const char* module) {
+    auto* m = dynamic_cast<MI355XBackend*>(be);
+    if (m == nullptr) throw std::invalid_argument(std::string(module) + ": needs an MI355XBackend");
+    return m;
+}
+
+/** @brief A fresh tensor holding a copy of device data (the reference's modules return new tensors). */
+Tensor copy_out(MI355XBackend* be, const float* src, Shape shape);
+/** @brief Copies a caller's tensor into a module buffer (a module keeps its input for relevance). */
+const float* keep_input(MI355XBackend* be, DevBuf& buf, const Tensor& t);
+
+inline pxk_operand mat(const float* p, int64_t ld, int64_t batch_stride = 0, int64_t inner_stride = 0,
+                       int64_t inner_div = 0, int64_t group_stride = 0) {
+    return pxk_operand{p, ld, batch_stride, inner_stride, inner_div, group_stride};
+}
+
+inline pxk_gemm_desc gemm_desc(int64_t m, int64_t n, int64_t k) {
+    pxk_gemm_desc d{};
+    d.m = m;
+    d.n = n;
+    d.k = k;
+    d.batch = d.inner = d.kgroups = 1;
+    return d;
+}
+
+/** @brief The stabilizer bias a rule puts in a Linear's denominator: the layer's bias under the
+ *         bias-in-denominator epsilon rule, none under the pre-bias rule (lrp_rules.cpp:197-220). */
+inline const float* rule_bias(const float* bias, bool use_bias, bool bias_in_denominator) {
+    return (use_bias && bias_in_denominator) ? bias : nullptr;
+}
+
+}  // namespace pulsatrix::detail

@@ -1,0 +1,45 @@
+/** @file embedding_module.hpp
+ *  @brief Token embedding (V, d) (the surface of include/pulsatrix/embedding_module.hpp).
+ *         forward() validates ids on the host as the reference does (embedding_module.cpp:48-59);
+ *         run_forward_device() takes ids already validated and resident in HBM.
+ */
+#pragma once
+
+#include <vector>
+
+#include "pulsatrix/detail/fused.hpp"
+#include "pulsatrix/module.hpp"
+
+namespace pulsatrix {
+
+class EmbeddingModule : public Module {
+public:
+    EmbeddingModule(int64_t num_embeddings, int64_t embedding_dim, DeviceBackend* backend);
+
+    /** @brief Each token's relevance: the sum of its embedding row's relevance, (N, L). */
+    [[nodiscard]] Tensor propagate_relevance(const Tensor& relevance_out, const LRPRuleConfig& config) override;
+
+    void set_weight(const std::vector<float>& values);
+    [[nodiscard]] Tensor& weight() noexcept { return weight_; }
+    [[nodiscard]] const Tensor& weight() const noexcept { return weight_; }
+    [[nodiscard]] int64_t num_embeddings() const noexcept { return V_; }
+    [[nodiscard]] int64_t embedding_dim() const noexcept { return d_; }
+
+    /** @brief Gathers rows for n x l ids (floats holding whole numbers in [0, V)) into a
+     *         module-owned (n*l, d) buffer. */
+    const float* run_forward_device(const float* ids, int64_t n, int64_t l);
+    /** @brief Per-token sums of a (count, d) relevance into out (count). */
+    void token_relevance(const float* relevance, int64_t count, float* out);
+
+protected:
+    Tensor forward_impl(const Tensor& input) override;
+
+private:
+    int64_t V_, d_;
+    MI355XBackend* be_;
+    Tensor weight_;
+    Shape last_shape_;
+    detail::DevBuf ids_, out_;
+};
+
+}  // namespace pulsatrix

@@ -1,0 +1,215 @@
+/** @file mi355x_backend.hpp
+ *  @brief MI355XBackend: the DeviceBackend of one MI355X (gfx950), over libpxk_gfx950's C ABI.
+ *
+ *  Replaces Pulsatrix's HIPBackend (src/hip_backend.hip, include/pulsatrix/hip_backend.hpp) for the
+ *  causal-LM forward + AttnLRP path. Every path op is a hand-written gfx950 kernel (include/pxk.h);
+ *  no hipBLAS. One in-order HIP stream per backend; the host waits only on host copies, dot() and
+ *  sum() (hip_backend.hpp:64-71). Device memory comes from a size-class caching allocator with
+ *  Pulsatrix's contract (bad_alloc -> release the cache -> retry once; hip_backend.hip:36-54).
+ *  DeviceBackend virtuals outside that path (convolution, pooling, batch/group norm, recurrent
+ *  and state-space cells, RL, optimizer steps, dropout, losses, backward passes) throw
+ *  std::logic_error naming the op.
+ */
+#pragma once
+
+#include <cstddef>
+#include <cstdint>
+#include <mutex>
+#include <unordered_map>
+#include <vector>
+
+#include "pulsatrix/device_backend.hpp"
+#include "pxk.h"
+
+namespace pulsatrix {
+
+/** @brief Size-class cache of device blocks (the role of Pulsatrix's CachingAllocator). */
+class CachingAllocator {
+public:
+    using RawAlloc = void* (*)(size_t bytes, void* ctx);  // returns nullptr on out-of-memory
+    using RawFree = void (*)(void* ptr, void* ctx);
+    CachingAllocator(RawAlloc alloc, RawFree free, void* ctx, size_t budget_bytes);
+    ~CachingAllocator();
+    CachingAllocator(const CachingAllocator&) = delete;
+    CachingAllocator& operator=(const CachingAllocator&) = delete;
+
+    /** @brief nullptr for 0 bytes; throws std::bad_alloc when the device (or budget) is exhausted. */
+    void* allocate(size_t bytes);
+    void free(void* ptr) noexcept;
+    /** @brief Returns every cached block to the device. */
+    void release_cache() noexcept;
+    size_t bytes_in_use() const;
+    size_t bytes_cached() const;
+    static size_t round_size(size_t bytes);
+
+private:
+    RawAlloc raw_alloc_;
+    RawFree raw_free_;
+    void* ctx_;
+    size_t budget_;
+    mutable std::mutex mu_;
+    std::unordered_map<void*, size_t> live_;
+    std::unordered_map<size_t, std::vector<void*>> cache_;
+    size_t in_use_ = 0, cached_ = 0;
+};
+
+class MI355XBackend : public DeviceBackend {
+public:
+    /** @brief Binds device `device_index`, creates the backend's stream (default priority). */
+    explicit MI355XBackend(int device_index = 0);
+    ~MI355XBackend() override;
+    MI355XBackend(const MI355XBackend&) = delete;
+    MI355XBackend& operator=(const MI355XBackend&) = delete;
+
+    [[nodiscard]] DeviceType device() const noexcept override { return DeviceType::Hip; }
+    [[nodiscard]] void* allocate(size_t bytes) override;
+    void free(void* ptr) noexcept override;
+    void copy(void* dst, const void* src, size_t bytes, CopyDirection dir) override;
+    void fill(void* ptr, float value, size_t n) override;
+    void gemm(const float* a, const float* b, float* out, size_t m, size_t k, size_t n) override;
+    void elementwise(ElementwiseOp op, const float* in, float* out, size_t n) override;
+    void add(const float* a, const float* b, float* out, size_t n) override;
+    void mul(const float* a, const float* b, float* out, size_t n) override;
+    void gemm_ex(const float* a, bool transpose_a, const float* b, bool transpose_b, float* out, size_t m, size_t k,
+                 size_t n, float beta) override;
+    void gemm_strided_batched(const float* a, bool transpose_a, size_t stride_a, const float* b, bool transpose_b,
+                              size_t stride_b, float* out, size_t stride_out, size_t m, size_t k, size_t n,
+                              size_t batch, float beta = 0.0f) override;
+    void column_sums(const float* in, float* out, size_t rows, size_t cols, float beta) override;
+    void add_row_vector(const float* in, const float* row, float* out, size_t rows, size_t cols) override;
+    void elementwise_backward(ElementwiseOp op, const float* x, const float* grad_out, float* grad_in,
+                              size_t n) override;
+    void axpby(float alpha, const float* x, float beta, const float* y, float* out, size_t n) override;
+    [[nodiscard]] float dot(const float* a, const float* b, size_t n) override;
+    void dot_into(const float* a, const float* b, size_t n, float* out) override;
+    void softmax_rows(const float* in, float* out, size_t rows, size_t cols) override;
+    void softmax_rows_backward(const float* y, const float* dy, float* dx, size_t rows, size_t cols) override;
+    void logsumexp_rows(const float* in, float* out, size_t rows, size_t cols) override;
+    void adam_step(float* param, const float* grad, float* m, float* v, size_t n, float lr, float beta1, float beta2,
+                   float eps, float bias_correction1, float bias_correction2) override;
+    [[nodiscard]] float sum(const float* in, size_t n) override;
+    void dropout_forward(const float* in, float* out, float* mask, size_t n, float p, float scale, uint64_t seed,
+                         uint64_t offset) override;
+    void bce_with_logits(const float* logits, const float* target, float* out, size_t n) override;
+    void bce_with_logits_grad(const float* logits, const float* target, float* grad, size_t n, float scale) override;
+    void layer_norm_forward(const float* in, const float* gamma, const float* beta, float* xhat, float* out,
+                            float* row_std, size_t rows, size_t cols, float eps) override;
+    void layer_norm_backward(const float* grad_out, const float* gamma, const float* xhat, const float* row_std,
+                             float* grad_in, size_t rows, size_t cols) override;
+    void rms_norm_forward(const float* in, const float* gamma, float* out, float* row_rms, size_t rows, size_t cols,
+                          float eps) override;
+    void rms_norm_backward(const float* grad_out, const float* gamma, const float* in, const float* row_rms,
+                           float* grad_in, float* gamma_terms, size_t rows, size_t cols) override;
+    void rope_rotate(const float* in, const float* cos_table, const float* sin_table, float* out, size_t num_slices,
+                     size_t seq_len, size_t head_dim, bool inverse, bool rotate_half) override;
+    void permute_0213(const float* in, float* out, size_t d0, size_t d1, size_t d2, size_t d3) override;
+    void attention_mask_fill(float* scores, const float* key_keep, size_t batch, size_t heads, size_t q_len,
+                             size_t k_len, bool causal, size_t q_offset, size_t window, float value) override;
+    void gather_rows(const float* table, const float* indices, float* out, size_t count, size_t dim) override;
+    void scatter_add_rows(const float* src, const float* indices, float* table, size_t count, size_t dim) override;
+    void tanh_gaussian_forward(const float* mean, const float* log_std, const float* eps, float* action,
+                               float* std_cache, float* log_prob, size_t rows, size_t cols, float stabilizer,
+                               double half_log_two_pi) override;
+    void tanh_gaussian_backward(const float* action, const float* std_cache, const float* eps,
+                                const float* grad_action, const float* grad_log_prob, float* grad_mean,
+                                float* grad_log_std, size_t n, float stabilizer) override;
+    void lrp_linear(const float* x, const float* w, const float* z, const float* r, float* r_in, size_t rows,
+                    size_t in_features, size_t out_features, float eps) override;
+    void lrp_residual_split(const float* a, const float* b, const float* r, float* r_a, float* r_b, size_t n,
+                            float eps) override;
+    void lrp_bilinear_elementwise(const float* a, const float* b, const float* r, float* r_out, size_t n,
+                                  float eps) override;
+    void lrp_bilinear_matmul(const float* a, const float* b, const float* o, const float* r_o, float* r_a, float* r_b,
+                             size_t slices, size_t m, size_t p, size_t q, float eps, bool b_transposed) override;
+    void lrp_softmax_rows(const float* x, const float* y, const float* r, float* r_in, size_t rows,
+                          size_t cols) override;
+    void lrp_rope(const float* x, const float* y, const float* r, const float* cos_table, const float* sin_table,
+                  float* r_in, size_t slices, size_t seq_len, size_t head_dim, float eps, bool rotate_half) override;
+    void logic_pointwise(LogicOp op, int norm, const float* a, const float* b, const float* g_or_r, const float* y,
+                         float* out_a, float* out_b, size_t n, float eps) override;
+    void aggregator_forward(const float* x, float* mean_pow, float* out, size_t n, size_t cols, float p) override;
+    void aggregator_backward(const float* x, const float* mean_pow, const float* grad_out, float* grad_in, size_t n,
+                             size_t cols, float p) override;
+    void aggregator_lrp(const float* x, const float* mean_pow, const float* r_out, float* r_in, size_t n, size_t cols,
+                        float p, float eps) override;
+    void im2col(const float* in, float* col, size_t n, size_t c, size_t h, size_t w,
+                const ConvGeometry& geometry) override;
+    void col2im_add(const float* col, float* out, size_t n, size_t c, size_t h, size_t w,
+                    const ConvGeometry& geometry) override;
+    void add_channel_vector(const float* in, const float* vec, float* out, size_t n, size_t c, size_t inner) override;
+    void lrp_conv(const float* col, const float* kernel, const float* pre_bias, const float* r, float* r_col,
+                  size_t n, size_t out_channels, size_t p, size_t q, float eps) override;
+    void lrp_stabilized_divide(const float* r, const float* denom, const float* gate, float* out, size_t n, float eps,
+                               LrpGate gate_mode) override;
+    void max_pool_forward(const float* in, float* out, float* argmax, size_t planes, size_t h, size_t w, size_t kh,
+                          size_t kw, size_t sh, size_t sw, size_t ph, size_t pw) override;
+    void max_unpool(const float* src, const float* argmax, float* dst, size_t planes, size_t h, size_t w, size_t kh,
+                    size_t kw, size_t sh, size_t sw, size_t ph, size_t pw) override;
+    void avg_pool_forward(const float* in, float* out, size_t planes, size_t h, size_t w, size_t kh,
+                          size_t kw) override;
+    void avg_pool_backward(const float* grad_out, float* grad_in, size_t planes, size_t h, size_t w, size_t kh,
+                           size_t kw) override;
+    void lrp_avg_pool(const float* x, const float* r, float* r_in, size_t planes, size_t h, size_t w, size_t kh,
+                      size_t kw, float eps) override;
+    void batch_norm_forward(const float* in, const float* gamma, const float* beta, float* xhat, float* out,
+                            float* channel_std, size_t n, size_t c, size_t spatial, float eps) override;
+    void batch_norm_backward(const float* grad_out, const float* gamma, const float* xhat, const float* channel_std,
+                             float* grad_in, float* gamma_grad, float* beta_grad, size_t n, size_t c,
+                             size_t spatial) override;
+    void batch_norm_update_running(const float* in, float* running_mean, float* running_var, size_t n, size_t c,
+                                   size_t spatial, float momentum) override;
+    void batch_norm_eval_forward(const float* in, const float* gamma, const float* beta, const float* running_mean,
+                                 const float* running_var, float* xhat, float* out, float* channel_std, size_t n,
+                                 size_t c, size_t spatial, float eps) override;
+    void batch_norm_eval_backward(const float* grad_out, const float* gamma, const float* xhat,
+                                  const float* channel_std, float* grad_in, float* gamma_grad, float* beta_grad,
+                                  size_t n, size_t c, size_t spatial) override;
+    void group_norm_forward(const float* in, const float* gamma, const float* beta, float* xhat, float* out,
+                            float* group_std, size_t n, size_t c, size_t spatial, size_t num_groups,
+                            float eps) override;
+    void group_norm_backward(const float* grad_out, const float* gamma, const float* xhat, const float* group_std,
+                             float* grad_in, float* gamma_grad, float* beta_grad, size_t n, size_t c, size_t spatial,
+                             size_t num_groups) override;
+    void copy_2d(float* dst, size_t dst_stride, const float* src, size_t src_stride, size_t rows,
+                 size_t cols) override;
+    void accumulate_rows(const float* in, float* out, size_t rows, size_t cols) override;
+    void recurrent_cell(RecurrentCellOp op, const RecurrentCellArgs& args, size_t n) override;
+    void gru_lrp_hprev(const float* h_prev, const float* w_hn, const float* hn, const float* r_term_b,
+                       const float* direct, float* r_hprev, size_t rows, size_t hidden, float eps) override;
+    void ssm_pass(SsmPassOp op, const SsmPassArgs& args) override;
+    void rl_rows(RlRowOp op, const RlRowArgs& args) override;
+    void top_k_rows(const float* in, float* values, float* indices, size_t rows, size_t cols, size_t k,
+                    bool largest) override;
+
+    // ---- MI355X extensions used by the fused module path ----------------------------------
+    /** @brief The backend's HIP stream (hipStream_t as void*). */
+    [[nodiscard]] void* stream() const noexcept { return stream_; }
+    /** @brief Waits for everything queued on the stream. */
+    void synchronize();
+    /** @brief Runs one fused GEMM, supplying the split-K workspace from the backend's own pool. */
+    void run_gemm(pxk_gemm_desc& d);
+    /** @brief Throws (std::invalid_argument / std::runtime_error) unless rc == PXK_OK. */
+    static void check(int rc, const char* what);
+    /** @brief Capture everything queued between begin_capture() and end_capture() into a HIP
+     *         graph; replay() relaunches it with one call. Buffers used inside must not move. */
+    void begin_capture();
+    void end_capture();
+    void replay();
+    [[nodiscard]] bool has_graph() const noexcept { return graph_exec_ != nullptr; }
+    CachingAllocator& allocator() { return *allocator_; }
+
+private:
+    float* workspace(size_t bytes);
+
+    int device_ = 0;
+    void* stream_ = nullptr;
+    CachingAllocator* allocator_ = nullptr;
+    float* ws_ = nullptr;
+    size_t ws_bytes_ = 0;
+    float* reduce_ = nullptr;  // dot/sum partials + result slot
+    void* graph_ = nullptr;
+    void* graph_exec_ = nullptr;
+    bool sync_debug_ = false;
+};
+
+}  // namespace pulsatrix

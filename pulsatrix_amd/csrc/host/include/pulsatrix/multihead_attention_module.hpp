@@ -1,0 +1,98 @@
+/** @file multihead_attention_module.hpp
+ *  @brief Causal GQA multi-head attention with RoPE and its AttnLRP relevance
+ *         (the surface of include/pulsatrix/multihead_attention_module.hpp).
+ *
+ *  MI355X layout: Q, K, V stay head-packed in the projections' (N*L, heads*D) row layout (no
+ *  permutes, no repeat_kv copies: a query head reads its KV head through the GEMM's batch map);
+ *  scores and P are (N, H, L, L). The forward is a fused QKV GEMM, one RoPE kernel, a causal
+ *  scores GEMM (tiles above the diagonal skipped), the row softmax and a causal P V GEMM. The
+ *  relevance is the reference's Eq. 15 / softmax rule sequence (multihead_attention_module.cpp:
+ *  404-485) in GEMM form with the divides, RoPE rule and projection denominators fused into the
+ *  GEMM epilogues.
+ */
+#pragma once
+
+#include <cstdint>
+#include <vector>
+
+#include "pulsatrix/detail/fused.hpp"
+#include "pulsatrix/linear_module.hpp"
+#include "pulsatrix/module.hpp"
+
+namespace pulsatrix {
+
+/** @brief Pair layout of the rotary embedding: (2i, 2i+1) or Hugging Face's (i, i + D/2). */
+enum class RoPELayout { AdjacentPairs, RotateHalf };
+
+/** @brief AttentionConfig of include/pulsatrix/multihead_attention_module.hpp:31-63. */
+struct AttentionConfig {
+    int64_t d_model = 0;
+    int64_t num_heads = 0;
+    int64_t num_kv_heads = 0;
+    int64_t head_dim = 0;
+    bool use_rope = true;
+    RoPELayout rope_layout = RoPELayout::AdjacentPairs;
+    float rope_base = 10000.0f;
+    std::vector<double> rope_inverse_frequencies;
+    bool use_qk_norm = false;
+    float qk_norm_eps = 1e-6f;
+    bool qkv_bias = true;
+    bool out_bias = true;
+    bool causal = false;
+    int64_t sliding_window = 0;
+    float score_scale = 0.0f;
+    float qk_norm_weight_offset = 0.0f;
+};
+
+class MultiHeadAttentionModule : public Module {
+public:
+    MultiHeadAttentionModule(const AttentionConfig& config, DeviceBackend* backend);
+    MultiHeadAttentionModule(int64_t d_model, int64_t num_heads, DeviceBackend* backend, bool use_rope = true,
+                             bool use_qk_norm = false);
+
+    [[nodiscard]] Tensor propagate_relevance(const Tensor& relevance_out, const LRPRuleConfig& config) override;
+
+    [[nodiscard]] LinearModule& q_proj() { return q_proj_; }
+    [[nodiscard]] LinearModule& k_proj() { return k_proj_; }
+    [[nodiscard]] LinearModule& v_proj() { return v_proj_; }
+    [[nodiscard]] LinearModule& out_proj() { return out_proj_; }
+    [[nodiscard]] const AttentionConfig& config() const noexcept { return config_; }
+    /** @brief Relevance at the key / value projections' outputs, (N*L, Hkv*D), from the last
+     *         propagate_relevance() (multihead_attention_module.cpp:488-496). */
+    [[nodiscard]] const Tensor& key_relevance() const;
+    [[nodiscard]] const Tensor& value_relevance() const;
+    [[nodiscard]] float score_scale() const;
+
+    /** @brief Fused-path forward. With `resid`, the output projection's epilogue also writes
+     *         resid + attention output into `resid_out` (the block's first residual add). */
+    const float* run_forward(const float* x, int64_t n, int64_t l, const float* resid = nullptr,
+                             float* resid_out = nullptr);
+    /** @brief Fused-path relevance; `add` (nullable) is summed into the input relevance. */
+    const float* run_relevance(const float* relevance_out, const LRPRuleConfig& config, const float* add = nullptr);
+    /** @brief The attention output (after the output projection's bias) of the last forward. */
+    [[nodiscard]] const float* output() const noexcept;
+
+protected:
+    Tensor forward_impl(const Tensor& input) override;
+
+private:
+    void pack_weights();
+    void ensure_tables(int64_t l);
+
+    AttentionConfig config_;
+    int64_t d_, H_, Hkv_, D_;
+    MI355XBackend* be_;
+    LinearModule q_proj_, k_proj_, v_proj_, out_proj_;
+    uint64_t packed_version_ = ~uint64_t{0};
+    detail::DevBuf wqkv_, bqkv_;
+    int64_t table_len_ = -1;
+    detail::DevBuf cos_, sin_;
+    int64_t N_ = 0, L_ = 0;
+    const float* x_ = nullptr;
+    detail::DevBuf x_copy_, qkv_z_, qkv_y_, q_rot_, k_rot_, raw_, p_, ctx_, out_z_, out_y_;
+    detail::DevBuf spv_, ra_, g_, r_in_;
+    Tensor key_rel_, value_rel_;
+    bool has_relevance_ = false;
+};
+
+}  // namespace pulsatrix

@@ -1,0 +1,43 @@
+/** @file rms_norm_module.hpp
+ *  @brief RMSNorm over the last axis (the surface of include/pulsatrix/rms_norm_module.hpp).
+ *         gamma starts at zero, as the reference's does; relevance is the identity
+ *         (rms_norm_module.cpp:101-111).
+ */
+#pragma once
+
+#include <vector>
+
+#include "pulsatrix/detail/fused.hpp"
+#include "pulsatrix/module.hpp"
+
+namespace pulsatrix {
+
+class RMSNormModule : public Module {
+public:
+    RMSNormModule(int64_t num_features, DeviceBackend* backend, DeviceType device = DeviceType::Hip, float eps = 1e-6f);
+
+    [[nodiscard]] Tensor propagate_relevance(const Tensor& relevance_out, const LRPRuleConfig& config) override;
+
+    void set_gamma(const std::vector<float>& values);
+    [[nodiscard]] const Tensor& gamma() const noexcept { return gamma_; }
+    [[nodiscard]] Tensor& gamma() noexcept { return gamma_; }
+    [[nodiscard]] float eps() const noexcept { return eps_; }
+    [[nodiscard]] int64_t num_features() const noexcept { return d_; }
+
+    /** @brief Fused-path forward into a module-owned buffer. */
+    const float* run_forward(const float* x, int64_t rows);
+    [[nodiscard]] const float* output() const noexcept { return out_.data(); }
+
+protected:
+    Tensor forward_impl(const Tensor& input) override;
+
+private:
+    int64_t d_;
+    float eps_;
+    MI355XBackend* be_;
+    Tensor gamma_;
+    int64_t rows_ = 0;
+    detail::DevBuf out_, rms_;
+};
+
+}  // namespace pulsatrix

@@ -1,0 +1,50 @@
+/** @file swiglu_module.hpp
+ *  @brief Gated MLP down(act(gate(x)) * up(x)) (the surface of include/pulsatrix/swiglu_module.hpp).
+ *         Fused path: one [gate | up] GEMM, the gate kernel, the down GEMM; relevance is the down
+ *         projection's epsilon rule with Eq. 15's split of gate * up and both projection
+ *         denominators fused into its epilogue, then one GEMM over [gate | up] (swiglu_module.cpp:139-170).
+ */
+#pragma once
+
+#include "pulsatrix/detail/fused.hpp"
+#include "pulsatrix/linear_module.hpp"
+#include "pulsatrix/module.hpp"
+
+namespace pulsatrix {
+
+enum class GatedActivation { Silu, GeluTanh };
+
+class SwiGLUModule : public Module {
+public:
+    SwiGLUModule(int64_t d_model, int64_t d_ff, DeviceBackend* backend, bool use_bias = true,
+                 GatedActivation activation = GatedActivation::Silu);
+
+    [[nodiscard]] Tensor propagate_relevance(const Tensor& relevance_out, const LRPRuleConfig& config) override;
+
+    [[nodiscard]] LinearModule& gate_proj() { return gate_proj_; }
+    [[nodiscard]] LinearModule& up_proj() { return up_proj_; }
+    [[nodiscard]] LinearModule& down_proj() { return down_proj_; }
+
+    const float* run_forward(const float* x, int64_t rows, const float* resid = nullptr, float* resid_out = nullptr);
+    const float* run_relevance(const float* relevance_out, const LRPRuleConfig& config, const float* add = nullptr);
+    [[nodiscard]] const float* output() const noexcept;
+
+protected:
+    Tensor forward_impl(const Tensor& input) override;
+
+private:
+    void pack_weights();
+
+    int64_t d_, F_;
+    bool use_bias_;
+    MI355XBackend* be_;
+    LinearModule gate_proj_, up_proj_, down_proj_;
+    uint64_t packed_version_ = ~uint64_t{0};
+    detail::DevBuf wgu_, bgu_;
+    int64_t rows_ = 0;
+    const float* x_ = nullptr;
+    Shape last_shape_;
+    detail::DevBuf x_copy_, gu_z_, gu_y_, gate_post_, hidden_, down_z_, down_y_, g_, r_in_;
+};
+
+}  // namespace pulsatrix

@@ -1,0 +1,57 @@
+/** @file transformer_block.hpp
+ *  @brief Pre-norm decoder block x + attn(norm1(x)), then + mlp(norm2(.)) (the surface of
+ *         include/pulsatrix/transformer_block.hpp); relevance per transformer_block.cpp:189-227
+ *         with both residual adds fused into the sublayers' last GEMM epilogues.
+ */
+#pragma once
+
+#include "pulsatrix/multihead_attention_module.hpp"
+#include "pulsatrix/rms_norm_module.hpp"
+#include "pulsatrix/swiglu_module.hpp"
+
+namespace pulsatrix {
+
+/** @brief TransformerBlockOptions of include/pulsatrix/transformer_block.hpp:20-32. */
+struct TransformerBlockOptions {
+    float norm_eps = 1e-6f;
+    bool mlp_bias = true;
+    GatedActivation mlp_activation = GatedActivation::Silu;
+    bool post_norms = false;
+    float norm_weight_offset = 0.0f;
+};
+
+class TransformerBlock : public Module {
+public:
+    TransformerBlock(const AttentionConfig& attention, int64_t d_ff, DeviceBackend* backend,
+                     const TransformerBlockOptions& options = {});
+    TransformerBlock(int64_t d_model, int64_t num_heads, int64_t d_ff, DeviceBackend* backend, bool use_rope = true,
+                     bool use_qk_norm = false);
+
+    [[nodiscard]] Tensor propagate_relevance(const Tensor& relevance_out, const LRPRuleConfig& config) override;
+
+    [[nodiscard]] RMSNormModule& norm1() { return norm1_; }
+    [[nodiscard]] RMSNormModule& norm2() { return norm2_; }
+    [[nodiscard]] MultiHeadAttentionModule& mha() { return mha_; }
+    [[nodiscard]] SwiGLUModule& swiglu() { return swiglu_; }
+
+    /** @brief Fused-path forward; x must stay valid until the relevance pass. Returns y2. */
+    const float* run_forward(const float* x, int64_t n, int64_t l);
+    const float* run_relevance(const float* relevance_out, const LRPRuleConfig& config);
+
+protected:
+    Tensor forward_impl(const Tensor& input) override;
+
+private:
+    int64_t d_;
+    MI355XBackend* be_;
+    RMSNormModule norm1_;
+    MultiHeadAttentionModule mha_;
+    RMSNormModule norm2_;
+    SwiGLUModule swiglu_;
+    int64_t N_ = 0, L_ = 0;
+    const float* x_ = nullptr;
+    Shape last_shape_;
+    detail::DevBuf x_copy_, y1_, y2_, r_y1d_, r_ffn_, r_y1_, r_xd_, r_attn_;
+};
+
+}  // namespace pulsatrix

@@ -1,0 +1,386 @@
+// MultiHeadAttentionModule on MI355XBackend: fused GQA attention forward and its AttnLRP pass.
+#include <cmath>
+#include <stdexcept>
+
+#include "pulsatrix/multihead_attention_module.hpp"
+
+namespace pulsatrix {
+
+using detail::gemm_desc;
+using detail::mat;
+
+namespace {
+
+AttentionConfig resolve(AttentionConfig c) {  // multihead_attention_module.cpp:20-51
+    if (c.d_model <= 0) throw std::invalid_argument("MultiHeadAttentionModule: d_model must be positive");
+    if (c.num_heads <= 0) throw std::invalid_argument("MultiHeadAttentionModule: num_heads must be positive");
+    if (c.num_kv_heads < 0 || c.head_dim < 0)
+        throw std::invalid_argument("MultiHeadAttentionModule: num_kv_heads and head_dim must not be negative");
+    if (c.num_kv_heads == 0) c.num_kv_heads = c.num_heads;
+    if (c.num_heads % c.num_kv_heads != 0)
+        throw std::invalid_argument("MultiHeadAttentionModule: num_heads must be a multiple of num_kv_heads");
+    if (c.head_dim == 0) {
+        if (c.d_model % c.num_heads != 0)
+            throw std::invalid_argument("MultiHeadAttentionModule: d_model must be divisible by num_heads");
+        c.head_dim = c.d_model / c.num_heads;
+    }
+    if (c.use_rope && c.head_dim % 2 != 0)
+        throw std::invalid_argument("MultiHeadAttentionModule: use_rope requires an even head_dim (d_model / num_heads)");
+    if (c.use_qk_norm) throw std::invalid_argument("MultiHeadAttentionModule: QK-Norm is not on the MI355X path");
+    if (c.sliding_window != 0)
+        throw std::invalid_argument("MultiHeadAttentionModule: sliding-window attention is not on the MI355X path");
+    if (c.use_rope && c.head_dim > 64 && c.head_dim % 64 != 0)
+        throw std::invalid_argument("MultiHeadAttentionModule: head_dim above 64 must be a multiple of 64");
+    return c;
+}
+
+AttentionConfig legacy(int64_t d_model, int64_t num_heads, bool use_rope, bool use_qk_norm) {
+    AttentionConfig c;
+    c.d_model = d_model;
+    c.num_heads = num_heads;
+    c.use_rope = use_rope;
+    c.use_qk_norm = use_qk_norm;
+    return c;
+}
+
+}  // namespace
+
+MultiHeadAttentionModule::MultiHeadAttentionModule(int64_t d_model, int64_t num_heads, DeviceBackend* backend,
+                                                   bool use_rope, bool use_qk_norm)
+    : MultiHeadAttentionModule(legacy(d_model, num_heads, use_rope, use_qk_norm), backend) {}
+
+MultiHeadAttentionModule::MultiHeadAttentionModule(const AttentionConfig& config, DeviceBackend* backend)
+    : config_(resolve(config)),
+      d_(config_.d_model),
+      H_(config_.num_heads),
+      Hkv_(config_.num_kv_heads),
+      D_(config_.head_dim),
+      be_(detail::require_mi355x(backend, "MultiHeadAttentionModule")),
+      q_proj_(d_, H_ * D_, backend, config_.qkv_bias),
+      k_proj_(d_, Hkv_ * D_, backend, config_.qkv_bias),
+      v_proj_(d_, Hkv_ * D_, backend, config_.qkv_bias),
+      out_proj_(H_ * D_, d_, backend, config_.out_bias) {}
+
+float MultiHeadAttentionModule::score_scale() const {
+    return config_.score_scale > 0.0f ? config_.score_scale : 1.0f / std::sqrt(static_cast<float>(D_));
+}
+
+void MultiHeadAttentionModule::pack_weights() {
+    const uint64_t v = q_proj_.version() + k_proj_.version() + v_proj_.version();
+    if (v == packed_version_ && wqkv_.size() > 0) return;
+    const int64_t qd = H_ * D_, kvd = Hkv_ * D_, w3 = qd + 2 * kvd;
+    float* w = wqkv_.ensure(be_, d_ * w3);  // [Wq | Wk | Wv], (d, w3)
+    be_->copy_2d(w, w3, q_proj_.weight_data(), qd, d_, qd);
+    be_->copy_2d(w + qd, w3, k_proj_.weight_data(), kvd, d_, kvd);
+    be_->copy_2d(w + qd + kvd, w3, v_proj_.weight_data(), kvd, d_, kvd);
+    if (config_.qkv_bias) {
+        float* b = bqkv_.ensure(be_, w3);
+        be_->copy_2d(b, w3, q_proj_.bias_data(), qd, 1, qd);
+        be_->copy_2d(b + qd, w3, k_proj_.bias_data(), kvd, 1, kvd);
+        be_->copy_2d(b + qd + kvd, w3, v_proj_.bias_data(), kvd, 1, kvd);
+    }
+    packed_version_ = v;
+}
+
+void MultiHeadAttentionModule::ensure_tables(int64_t l) {
+    if (!config_.use_rope || l == table_len_) return;
+    // RoPEModule::ensure_tables (rope_module.cpp:67-69, 83-101): tables in double, rounded to float.
+    const int64_t half = D_ / 2;
+    std::vector<double> inv(static_cast<size_t>(half));
+    for (int64_t i = 0; i < half; ++i)
+        inv[static_cast<size_t>(i)] =
+            config_.rope_inverse_frequencies.empty()
+                ? std::pow(static_cast<double>(config_.rope_base), -2.0 * static_cast<double>(i) / static_cast<double>(D_))
+                : config_.rope_inverse_frequencies.at(static_cast<size_t>(i));
+    std::vector<float> c(static_cast<size_t>(l * half)), s(c.size());
+    for (int64_t pos = 0; pos < l; ++pos)
+        for (int64_t i = 0; i < half; ++i) {
+            const double theta = static_cast<double>(pos) * inv[static_cast<size_t>(i)];
+            c[static_cast<size_t>(pos * half + i)] = static_cast<float>(std::cos(theta));
+            s[static_cast<size_t>(pos * half + i)] = static_cast<float>(std::sin(theta));
+        }
+    be_->copy(cos_.ensure(be_, l * half), c.data(), c.size() * sizeof(float), CopyDirection::HostToDevice);
+    be_->copy(sin_.ensure(be_, l * half), s.data(), s.size() * sizeof(float), CopyDirection::HostToDevice);
+    table_len_ = l;
+}
+
+const float* MultiHeadAttentionModule::output() const noexcept {
+    return config_.out_bias ? out_y_.data() : out_z_.data();
+}
+
+const float* MultiHeadAttentionModule::run_forward(const float* x, int64_t n, int64_t l, const float* resid,
+                                                   float* resid_out) {
+    pack_weights();
+    ensure_tables(l);
+    N_ = n;
+    L_ = l;
+    x_ = x;
+    const int64_t M = n * l, qd = H_ * D_, kvd = Hkv_ * D_, w3 = qd + 2 * kvd, grp = H_ / Hkv_, LL = l * l;
+    const bool causal = config_.causal;
+    void* st = be_->stream();
+
+    // 1. q, k, v in one GEMM against [Wq | Wk | Wv]; z (pre-bias) kept for the relevance pass.
+    float* z = qkv_z_.ensure(be_, M * w3);
+    float* y = z;
+    {
+        pxk_gemm_desc d = gemm_desc(M, w3, d_);
+        d.a = mat(x, d_);
+        d.b = mat(wqkv_.data(), w3);
+        d.c = mat(z, w3);
+        if (config_.qkv_bias) {
+            y = qkv_y_.ensure(be_, M * w3);
+            d.epilogue = PXK_EPI_STORE_BIAS;
+            d.c2 = mat(y, w3);
+            d.e_bias = mat(bqkv_.data(), 0);
+        }
+        be_->run_gemm(d);
+    }
+    // 2. RoPE on q and k (positions from 0: no KV cache here).
+    const float *q = y, *k = y + qd, *v = y + qd + kvd;
+    int64_t ldq = w3, ldk = w3;
+    if (config_.use_rope) {
+        float* qr = q_rot_.ensure(be_, M * qd);
+        float* kr = k_rot_.ensure(be_, M * kvd);
+        MI355XBackend::check(pxk_rope_qk(y, y + qd, w3, qr, kr, cos_.data(), sin_.data(), M, l, H_, Hkv_, D_,
+                                         config_.rope_layout == RoPELayout::RotateHalf, st),
+                             "MultiHeadAttentionModule::forward (rope)");
+        q = qr;
+        k = kr;
+        ldq = qd;
+        ldk = kvd;
+    }
+    // 3. raw scores = Q K^T per query head; K read through the KV-head map.
+    float* raw = raw_.ensure(be_, n * H_ * LL);
+    {
+        pxk_gemm_desc d = gemm_desc(l, l, D_);
+        d.batch = n * H_;
+        d.inner = H_;
+        d.trans_b = 1;
+        d.causal = causal ? PXK_CAUSAL_TRI : PXK_CAUSAL_NONE;
+        d.a = mat(q, ldq, l * ldq, D_);
+        d.b = mat(k, ldk, l * ldk, D_, grp);
+        d.c = mat(raw, l, H_ * LL, LL);
+        be_->run_gemm(d);
+    }
+    // 4. P = softmax(scale * raw) over the visible keys.
+    float* p = p_.ensure(be_, n * H_ * LL);
+    MI355XBackend::check(pxk_attention_softmax(raw, p, n * H_, l, score_scale(), causal, st),
+                         "MultiHeadAttentionModule::forward (softmax)");
+    // 5. context = P V, written head-packed (N*L, H*D): the merge permute is the store layout.
+    float* ctx = ctx_.ensure(be_, M * qd);
+    {
+        pxk_gemm_desc d = gemm_desc(l, D_, l);
+        d.batch = n * H_;
+        d.inner = H_;
+        d.causal = causal ? PXK_CAUSAL_K_LE_M : PXK_CAUSAL_NONE;
+        d.a = mat(p, l, H_ * LL, LL);
+        d.b = mat(v, w3, l * w3, D_, grp);
+        d.c = mat(ctx, qd, l * qd, D_);
+        be_->run_gemm(d);
+    }
+    // 6. output projection, with the block's residual add fused into the epilogue when asked.
+    float* oz = out_z_.ensure(be_, M * d_);
+    float* oy = config_.out_bias ? out_y_.ensure(be_, M * d_) : oz;
+    {
+        pxk_gemm_desc d = gemm_desc(M, d_, qd);
+        d.a = mat(ctx, qd);
+        d.b = mat(out_proj_.weight_data(), d_);
+        d.c = mat(oz, d_);
+        if (config_.out_bias) {
+            d.c2 = mat(oy, d_);
+            d.e_bias = mat(out_proj_.bias_data(), 0);
+        }
+        if (resid) {
+            d.epilogue = PXK_EPI_ADD_RESID;
+            d.x = mat(resid, d_);
+            d.c3 = mat(resid_out, d_);
+        } else {
+            d.epilogue = config_.out_bias ? PXK_EPI_STORE_BIAS : PXK_EPI_STORE;
+        }
+        be_->run_gemm(d);
+    }
+    return oy;
+}
+
+const float* MultiHeadAttentionModule::run_relevance(const float* relevance_out, const LRPRuleConfig& config,
+                                                     const float* add) {
+    require_epsilon_rule(config, "MultiHeadAttentionModule");
+    if (x_ == nullptr)
+        throw std::logic_error("MultiHeadAttentionModule::propagate_relevance: called before any forward()");
+    const int64_t n = N_, l = L_, M = n * l, qd = H_ * D_, kvd = Hkv_ * D_, w3 = qd + 2 * kvd, grp = H_ / Hkv_;
+    const int64_t LL = l * l;
+    const bool causal = config_.causal, bid = config.epsilon_bias_in_denominator;
+    const float eps = config.epsilon;
+    const float* z = qkv_z_.data();
+    const float* y = config_.qkv_bias ? qkv_y_.data() : z;
+    const float* q = config_.use_rope ? q_rot_.data() : y;
+    const float* k = config_.use_rope ? k_rot_.data() : y + qd;
+    const float* v = y + qd + kvd;
+    const int64_t ldq = config_.use_rope ? qd : w3, ldk = config_.use_rope ? kvd : w3;
+    const float* bq = detail::rule_bias(bqkv_.data(), config_.qkv_bias, bid);
+    void* st = be_->stream();
+
+    // 1. out_proj epsilon rule; its epilogue forms the P V bilinear factor
+    //    s_pv = r_ctx / (2 ctx + eps sign ctx) with r_ctx = ctx * (g W_o^T).
+    float* spv = spv_.ensure(be_, M * qd);
+    {
+        pxk_gemm_desc d = gemm_desc(M, qd, d_);
+        d.trans_b = 1;
+        d.prologue = PXK_PRO_DIV_STAB;
+        d.epilogue = PXK_EPI_SPV;
+        d.eps = eps;
+        d.a = mat(relevance_out, d_);
+        d.z = mat(out_z_.data(), d_);
+        if (const float* bo = detail::rule_bias(out_proj_.bias_data(), config_.out_bias, bid)) d.z_bias = mat(bo, 0);
+        d.b = mat(out_proj_.weight_data(), d_);
+        d.c = mat(spv, qd);
+        d.x = mat(ctx_.data(), qd);
+        be_->run_gemm(d);
+    }
+    // 2. r_attn = P * (s_pv V^T) per query head (Eq. 15, A-share of P V).
+    float* ra = ra_.ensure(be_, n * H_ * LL);
+    const float* p = p_.data();
+    {
+        pxk_gemm_desc d = gemm_desc(l, l, D_);
+        d.batch = n * H_;
+        d.inner = H_;
+        d.trans_b = 1;
+        d.causal = causal ? PXK_CAUSAL_TRI : PXK_CAUSAL_NONE;
+        d.epilogue = PXK_EPI_MUL_X;
+        d.a = mat(spv, qd, l * qd, D_);
+        d.b = mat(v, w3, l * w3, D_, grp);
+        d.c = mat(ra, l, H_ * LL, LL);
+        d.x = mat(p, l, H_ * LL, LL);
+        be_->run_gemm(d);
+    }
+    // 3. softmax rule on the scaled scores, mask, then the Q K^T factor s_qk (in place).
+    MI355XBackend::check(pxk_attention_lrp_scores(ra, p, raw_.data(), ra, n * H_, l, score_scale(), eps, causal, st),
+                         "MultiHeadAttentionModule::propagate_relevance (scores)");
+    float* g = g_.ensure(be_, M * w3);  // [g_q | g_k | g_v]: relevance / stab(z) per projection
+    if (!key_rel_.data() || key_rel_.numel() != M * kvd) {
+        key_rel_ = Tensor::uninitialized(Shape({M, kvd}), be_);
+        value_rel_ = Tensor::uninitialized(Shape({M, kvd}), be_);
+    }
+    // 4. query share: r_q = Q * (s_qk K), then the RoPE rule and q_proj's denominator.
+    {
+        pxk_gemm_desc d = gemm_desc(l, D_, l);
+        d.batch = n * H_;
+        d.inner = H_;
+        d.causal = causal ? PXK_CAUSAL_K_LE_M : PXK_CAUSAL_NONE;
+        d.eps = eps;
+        d.a = mat(ra, l, H_ * LL, LL);
+        d.b = mat(k, ldk, l * ldk, D_, grp);
+        d.c2 = mat(g, w3, l * w3, D_);
+        d.z = mat(z, w3, l * w3, D_);
+        if (bq) d.e_bias = mat(bq, 0, 0, D_);
+        if (config_.use_rope) {
+            d.epilogue = PXK_EPI_ROPE_REL;
+            d.x = mat(y, w3, l * w3, D_);
+            d.y = mat(q, ldq, l * ldq, D_);
+            d.cos_t = cos_.data();
+            d.sin_t = sin_.data();
+            d.head_dim = D_;
+            d.rope_half = config_.rope_layout == RoPELayout::RotateHalf;
+        } else {
+            d.epilogue = PXK_EPI_VALUE_REL;
+            d.y = mat(q, ldq, l * ldq, D_);
+        }
+        be_->run_gemm(d);
+    }
+    // 5. key share per KV head, summed over its query heads: r_k = K * sum_h s_qk_h^T Q_h.
+    {
+        pxk_gemm_desc d = gemm_desc(l, D_, l);
+        d.batch = n * Hkv_;
+        d.inner = Hkv_;
+        d.kgroups = grp;
+        d.trans_a = 1;
+        d.causal = causal ? PXK_CAUSAL_K_GE_M : PXK_CAUSAL_NONE;
+        d.eps = eps;
+        d.a = mat(ra, l, H_ * LL, grp * LL, 0, LL);
+        d.b = mat(q, ldq, l * ldq, grp * D_, 0, D_);
+        d.c = mat(key_rel_.data(), kvd, l * kvd, D_);
+        d.c2 = mat(g + qd, w3, l * w3, D_);
+        d.z = mat(z + qd, w3, l * w3, D_);
+        if (bq) d.e_bias = mat(bq + qd, 0, 0, D_);
+        if (config_.use_rope) {
+            d.epilogue = PXK_EPI_ROPE_REL;
+            d.x = mat(y + qd, w3, l * w3, D_);
+            d.y = mat(k, ldk, l * ldk, D_);
+            d.cos_t = cos_.data();
+            d.sin_t = sin_.data();
+            d.head_dim = D_;
+            d.rope_half = config_.rope_layout == RoPELayout::RotateHalf;
+        } else {
+            d.epilogue = PXK_EPI_VALUE_REL;
+            d.y = mat(k, ldk, l * ldk, D_);
+        }
+        be_->run_gemm(d);
+    }
+    // 6. value share per KV head: r_v = V * sum_h P_h^T s_pv_h.
+    {
+        pxk_gemm_desc d = gemm_desc(l, D_, l);
+        d.batch = n * Hkv_;
+        d.inner = Hkv_;
+        d.kgroups = grp;
+        d.trans_a = 1;
+        d.causal = causal ? PXK_CAUSAL_K_GE_M : PXK_CAUSAL_NONE;
+        d.epilogue = PXK_EPI_VALUE_REL;
+        d.eps = eps;
+        d.a = mat(p, l, H_ * LL, grp * LL, 0, LL);
+        d.b = mat(spv, qd, l * qd, grp * D_, 0, D_);
+        d.c = mat(value_rel_.data(), kvd, l * kvd, D_);
+        d.c2 = mat(g + qd + kvd, w3, l * w3, D_);
+        d.z = mat(z + qd + kvd, w3, l * w3, D_);
+        d.y = mat(v, w3, l * w3, D_);
+        if (bq) d.e_bias = mat(bq + qd + kvd, 0, 0, D_);
+        be_->run_gemm(d);
+    }
+    // 7. the three projections' input relevance in one GEMM: x * ([g_q | g_k | g_v] [Wq | Wk | Wv]^T).
+    float* r_in = r_in_.ensure(be_, M * d_);
+    {
+        pxk_gemm_desc d = gemm_desc(M, d_, w3);
+        d.trans_b = 1;
+        d.epilogue = PXK_EPI_MUL_X;
+        d.a = mat(g, w3);
+        d.b = mat(wqkv_.data(), w3);
+        d.c = mat(r_in, d_);
+        d.x = mat(x_, d_);
+        if (add) d.y = mat(add, d_);
+        be_->run_gemm(d);
+    }
+    has_relevance_ = true;
+    return r_in;
+}
+
+Tensor MultiHeadAttentionModule::forward_impl(const Tensor& input) {
+    if (input.rank() != 3 || input.shape().dim(2) != d_)
+        throw std::invalid_argument("MultiHeadAttentionModule::forward: input must be rank-3 (N, L, d_model)");
+    const int64_t n = input.shape().dim(0), l = input.shape().dim(1);
+    const float* out = run_forward(detail::keep_input(be_, x_copy_, input), n, l);
+    return detail::copy_out(be_, out, Shape({n, l, d_}));
+}
+
+Tensor MultiHeadAttentionModule::propagate_relevance(const Tensor& relevance_out, const LRPRuleConfig& config) {
+    if (x_ == nullptr)
+        throw std::logic_error("MultiHeadAttentionModule::propagate_relevance: called before any forward()");
+    if (relevance_out.rank() != 3 || relevance_out.shape().dim(0) != N_ || relevance_out.shape().dim(1) != L_ ||
+        relevance_out.shape().dim(2) != d_)
+        throw std::invalid_argument(
+            "MultiHeadAttentionModule::propagate_relevance: relevance_out must be rank-3 (N, L, d_model) matching the "
+            "cached forward shape");
+    return detail::copy_out(be_, run_relevance(relevance_out.data(), config), Shape({N_, L_, d_}));
+}
+
+const Tensor& MultiHeadAttentionModule::key_relevance() const {
+    if (!has_relevance_)
+        throw std::logic_error("MultiHeadAttentionModule::key_relevance: no propagate_relevance() yet");
+    return key_rel_;
+}
+
+const Tensor& MultiHeadAttentionModule::value_relevance() const {
+    if (!has_relevance_)
+        throw std::logic_error("MultiHeadAttentionModule::value_relevance: no propagate_relevance() yet");
+    return value_rel_;
+}
+
+}  // namespace pulsatrix

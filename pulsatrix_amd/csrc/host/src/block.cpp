@@ -1,0 +1,221 @@
+// SwiGLUModule and TransformerBlock on MI355XBackend.
+#include <stdexcept>
+
+#include "pulsatrix/swiglu_module.hpp"
+#include "pulsatrix/transformer_block.hpp"
+
+namespace pulsatrix {
+
+using detail::gemm_desc;
+using detail::mat;
+
+// ---- SwiGLUModule (src/swiglu_module.cpp) ----------------------------------------------------------
+
+SwiGLUModule::SwiGLUModule(int64_t d_model, int64_t d_ff, DeviceBackend* backend, bool use_bias,
+                           GatedActivation activation)
+    : d_(d_model),
+      F_(d_ff),
+      use_bias_(use_bias),
+      be_(detail::require_mi355x(backend, "SwiGLUModule")),
+      gate_proj_(d_model, d_ff, backend, use_bias),
+      up_proj_(d_model, d_ff, backend, use_bias),
+      down_proj_(d_ff, d_model, backend, use_bias) {
+    if (activation != GatedActivation::Silu)
+        throw std::invalid_argument("SwiGLUModule: the MI355X path implements the SiLU gate");
+}
+
+void SwiGLUModule::pack_weights() {
+    const uint64_t v = gate_proj_.version() + up_proj_.version();
+    if (v == packed_version_ && wgu_.size() > 0) return;
+    float* w = wgu_.ensure(be_, d_ * 2 * F_);  // [W_gate | W_up], (d, 2F)
+    be_->copy_2d(w, 2 * F_, gate_proj_.weight_data(), F_, d_, F_);
+    be_->copy_2d(w + F_, 2 * F_, up_proj_.weight_data(), F_, d_, F_);
+    if (use_bias_) {
+        float* b = bgu_.ensure(be_, 2 * F_);
+        be_->copy_2d(b, 2 * F_, gate_proj_.bias_data(), F_, 1, F_);
+        be_->copy_2d(b + F_, 2 * F_, up_proj_.bias_data(), F_, 1, F_);
+    }
+    packed_version_ = v;
+}
+
+const float* SwiGLUModule::output() const noexcept { return use_bias_ ? down_y_.data() : down_z_.data(); }
+
+const float* SwiGLUModule::run_forward(const float* x, int64_t rows, const float* resid, float* resid_out) {
+    pack_weights();
+    x_ = x;
+    rows_ = rows;
+    const int64_t f2 = 2 * F_;
+    float* gz = gu_z_.ensure(be_, rows * f2);
+    float* gy = gz;
+    {  // gate and up projections in one GEMM
+        pxk_gemm_desc d = gemm_desc(rows, f2, d_);
+        d.a = mat(x, d_);
+        d.b = mat(wgu_.data(), f2);
+        d.c = mat(gz, f2);
+        if (use_bias_) {
+            gy = gu_y_.ensure(be_, rows * f2);
+            d.epilogue = PXK_EPI_STORE_BIAS;
+            d.c2 = mat(gy, f2);
+            d.e_bias = mat(bgu_.data(), 0);
+        }
+        be_->run_gemm(d);
+    }
+    float* gp = gate_post_.ensure(be_, rows * F_);
+    float* h = hidden_.ensure(be_, rows * F_);
+    MI355XBackend::check(pxk_swiglu_forward(gy, f2, gp, h, rows, F_, be_->stream()), "SwiGLUModule::forward");
+    float* dz = down_z_.ensure(be_, rows * d_);
+    float* dy = use_bias_ ? down_y_.ensure(be_, rows * d_) : dz;
+    {
+        pxk_gemm_desc d = gemm_desc(rows, d_, F_);
+        d.a = mat(h, F_);
+        d.b = mat(down_proj_.weight_data(), d_);
+        d.c = mat(dz, d_);
+        if (use_bias_) {
+            d.c2 = mat(dy, d_);
+            d.e_bias = mat(down_proj_.bias_data(), 0);
+        }
+        if (resid) {
+            d.epilogue = PXK_EPI_ADD_RESID;
+            d.x = mat(resid, d_);
+            d.c3 = mat(resid_out, d_);
+        } else {
+            d.epilogue = use_bias_ ? PXK_EPI_STORE_BIAS : PXK_EPI_STORE;
+        }
+        be_->run_gemm(d);
+    }
+    return dy;
+}
+
+const float* SwiGLUModule::run_relevance(const float* relevance_out, const LRPRuleConfig& config, const float* add) {
+    require_epsilon_rule(config, "SwiGLUModule");
+    if (x_ == nullptr) throw std::logic_error("SwiGLUModule::propagate_relevance: called before any forward()");
+    const bool bid = config.epsilon_bias_in_denominator;
+    const int64_t rows = rows_, f2 = 2 * F_;
+    const float* gz = gu_z_.data();
+    const float* gy = use_bias_ ? gu_y_.data() : gz;
+    float* g = g_.ensure(be_, rows * f2);
+    {  // down projection's rule, Eq. 15's gate * up split and both projections' denominators
+        pxk_gemm_desc d = gemm_desc(rows, F_, d_);
+        d.trans_b = 1;
+        d.prologue = PXK_PRO_DIV_STAB;
+        d.epilogue = PXK_EPI_SWIGLU_REL;
+        d.eps = config.epsilon;
+        d.a = mat(relevance_out, d_);
+        d.z = mat(down_z_.data(), d_);
+        if (const float* bd = detail::rule_bias(down_proj_.bias_data(), use_bias_, bid)) d.z_bias = mat(bd, 0);
+        d.b = mat(down_proj_.weight_data(), d_);
+        d.c = mat(g, f2);
+        d.c2 = mat(g + F_, f2);
+        d.x = mat(hidden_.data(), F_);
+        d.y = mat(gate_post_.data(), F_);
+        d.w = mat(gy + F_, f2);
+        d.z2 = mat(gz, f2);
+        d.z3 = mat(gz + F_, f2);
+        if (use_bias_ && bid) {
+            d.e_bias = mat(gate_proj_.bias_data(), 0);
+            d.e_bias2 = mat(up_proj_.bias_data(), 0);
+        }
+        be_->run_gemm(d);
+    }
+    float* r_in = r_in_.ensure(be_, rows * d_);
+    {  // gate and up projections' input relevance in one GEMM: x * ([g_gate | g_up] [W_gate | W_up]^T)
+        pxk_gemm_desc d = gemm_desc(rows, d_, f2);
+        d.trans_b = 1;
+        d.epilogue = PXK_EPI_MUL_X;
+        d.a = mat(g, f2);
+        d.b = mat(wgu_.data(), f2);
+        d.c = mat(r_in, d_);
+        d.x = mat(x_, d_);
+        if (add) d.y = mat(add, d_);
+        be_->run_gemm(d);
+    }
+    return r_in;
+}
+
+Tensor SwiGLUModule::forward_impl(const Tensor& input) {
+    if (input.rank() < 2 || input.shape().dim(static_cast<size_t>(input.rank() - 1)) != d_)
+        throw std::invalid_argument("SwiGLUModule::forward: input must be rank >= 2 with final dimension d_model");
+    last_shape_ = input.shape();
+    const float* out = run_forward(detail::keep_input(be_, x_copy_, input), input.numel() / d_);
+    return detail::copy_out(be_, out, last_shape_);
+}
+
+Tensor SwiGLUModule::propagate_relevance(const Tensor& relevance_out, const LRPRuleConfig& config) {
+    if (x_ == nullptr) throw std::logic_error("SwiGLUModule::propagate_relevance: called before any forward()");
+    if (relevance_out.shape() != last_shape_)
+        throw std::invalid_argument("SwiGLUModule::propagate_relevance: relevance_out must match the cached forward shape");
+    return detail::copy_out(be_, run_relevance(relevance_out.data(), config), last_shape_);
+}
+
+// ---- TransformerBlock (src/transformer_block.cpp) ------------------------------------------------
+
+TransformerBlock::TransformerBlock(const AttentionConfig& attention, int64_t d_ff, DeviceBackend* backend,
+                                   const TransformerBlockOptions& options)
+    : d_(attention.d_model),
+      be_(detail::require_mi355x(backend, "TransformerBlock")),
+      norm1_(attention.d_model > 0 ? attention.d_model : 1, backend, DeviceType::Hip, options.norm_eps),
+      mha_(attention, backend),
+      norm2_(attention.d_model > 0 ? attention.d_model : 1, backend, DeviceType::Hip, options.norm_eps),
+      swiglu_(attention.d_model, d_ff, backend, options.mlp_bias, options.mlp_activation) {
+    if (options.post_norms || options.norm_weight_offset != 0.0f)
+        throw std::invalid_argument("TransformerBlock: Gemma sandwich norms are not on the MI355X path");
+}
+
+TransformerBlock::TransformerBlock(int64_t d_model, int64_t num_heads, int64_t d_ff, DeviceBackend* backend,
+                                   bool use_rope, bool use_qk_norm)
+    : d_(d_model),
+      be_(detail::require_mi355x(backend, "TransformerBlock")),
+      norm1_(d_model, backend),
+      mha_(d_model, num_heads, backend, use_rope, use_qk_norm),
+      norm2_(d_model, backend),
+      swiglu_(d_model, d_ff, backend) {}
+
+const float* TransformerBlock::run_forward(const float* x, int64_t n, int64_t l) {
+    N_ = n;
+    L_ = l;
+    x_ = x;
+    const int64_t M = n * l;
+    float* y1 = y1_.ensure(be_, M * d_);
+    float* y2 = y2_.ensure(be_, M * d_);
+    mha_.run_forward(norm1_.run_forward(x, M), n, l, x, y1);        // y1 = x + attn(norm1(x))
+    swiglu_.run_forward(norm2_.run_forward(y1, M), M, y1, y2);       // y2 = y1 + mlp(norm2(y1))
+    return y2;
+}
+
+const float* TransformerBlock::run_relevance(const float* relevance_out, const LRPRuleConfig& config) {
+    if (x_ == nullptr) throw std::logic_error("TransformerBlock::propagate_relevance: called before any forward()");
+    const int64_t M = N_ * L_, n = M * d_;
+    void* st = be_->stream();
+    // y2 = y1 + ffn: epsilon split, the MLP's relevance (RMSNorm's rule is the identity), then
+    // r_y1 = r_y1_direct + r_from_norm2 fused into the MLP's last GEMM.
+    float* ry1d = r_y1d_.ensure(be_, n);
+    float* rffn = r_ffn_.ensure(be_, n);
+    MI355XBackend::check(pxk_lrp_residual_split(y1_.data(), swiglu_.output(), relevance_out, ry1d, rffn, n,
+                                                config.epsilon, st),
+                         "TransformerBlock::propagate_relevance");
+    const float* ry1 = swiglu_.run_relevance(rffn, config, ry1d);
+    // y1 = x + attn: the same one level up.
+    float* rxd = r_xd_.ensure(be_, n);
+    float* rattn = r_attn_.ensure(be_, n);
+    MI355XBackend::check(pxk_lrp_residual_split(x_, mha_.output(), ry1, rxd, rattn, n, config.epsilon, st),
+                         "TransformerBlock::propagate_relevance");
+    return mha_.run_relevance(rattn, config, rxd);
+}
+
+Tensor TransformerBlock::forward_impl(const Tensor& input) {
+    if (input.rank() != 3 || input.shape().dim(2) != d_)
+        throw std::invalid_argument("TransformerBlock::forward: input must be rank-3 (N, L, d_model)");
+    last_shape_ = input.shape();
+    const float* out = run_forward(detail::keep_input(be_, x_copy_, input), input.shape().dim(0), input.shape().dim(1));
+    return detail::copy_out(be_, out, last_shape_);
+}
+
+Tensor TransformerBlock::propagate_relevance(const Tensor& relevance_out, const LRPRuleConfig& config) {
+    if (x_ == nullptr) throw std::logic_error("TransformerBlock::propagate_relevance: called before any forward()");
+    if (relevance_out.shape() != last_shape_)
+        throw std::invalid_argument(
+            "TransformerBlock::propagate_relevance: relevance_out must match the cached forward shape");
+    return detail::copy_out(be_, run_relevance(relevance_out.data(), config), last_shape_);
+}
+
+}  // namespace pulsatrix

@@ -1,0 +1,371 @@
+// C ABI of the MI355X host framework (include/pulsatrix_amd.h).
+#include "pulsatrix_amd.h"
+
+#include <hip/hip_runtime_api.h>
+
+#include <cmath>
+#include <memory>
+#include <mutex>
+#include <stdexcept>
+#include <string>
+#include <utility>
+#include <vector>
+
+#include "pulsatrix/causal_lm.hpp"
+#include "pulsatrix/mi355x_backend.hpp"
+#include "pulsatrix/transformer_block.hpp"
+
+using namespace pulsatrix;
+
+namespace {
+
+thread_local std::string g_error;
+
+template <typename F>
+int guarded(F&& f) {
+    try {
+        f();
+        return 0;
+    } catch (const std::exception& e) {
+        g_error = e.what();
+        return -1;
+    }
+}
+
+std::once_flag g_once;
+std::unique_ptr<MI355XBackend> g_backend;
+
+MI355XBackend* backend() {
+    std::call_once(g_once, [] { g_backend = std::make_unique<MI355XBackend>(0); });
+    return g_backend.get();
+}
+
+int64_t kv_heads(const px_model_config& c) { return c.num_kv_heads > 0 ? c.num_kv_heads : c.num_heads; }
+int64_t head_dim(const px_model_config& c) { return c.head_dim > 0 ? c.head_dim : c.hidden_size / c.num_heads; }
+
+// (size, is_norm_gamma) of each parameter of one block, in the flat blob's order.
+std::vector<std::pair<int64_t, bool>> block_layout(const px_model_config& c) {
+    const int64_t d = c.hidden_size, q = c.num_heads * head_dim(c), kv = kv_heads(c) * head_dim(c),
+                  f = c.intermediate_size;
+    std::vector<std::pair<int64_t, bool>> out{{d, true}};
+    auto lin = [&](int64_t in, int64_t o, bool bias) {
+        out.push_back({in * o, false});
+        if (bias) out.push_back({o, false});
+    };
+    lin(d, q, c.qkv_bias);
+    lin(d, kv, c.qkv_bias);
+    lin(d, kv, c.qkv_bias);
+    lin(q, d, c.out_bias);
+    out.push_back({d, true});
+    lin(d, f, c.mlp_bias);
+    lin(d, f, c.mlp_bias);
+    lin(f, d, c.mlp_bias);
+    return out;
+}
+
+std::vector<std::pair<int64_t, bool>> lm_layout(const px_model_config& c) {
+    std::vector<std::pair<int64_t, bool>> out{{c.vocab_size * c.hidden_size, false}};
+    for (int64_t i = 0; i < c.num_layers; ++i) {
+        auto b = block_layout(c);
+        out.insert(out.end(), b.begin(), b.end());
+    }
+    out.push_back({c.hidden_size, true});
+    if (!c.tie_word_embeddings) out.push_back({c.hidden_size * c.vocab_size, false});
+    return out;
+}
+
+int64_t total(const std::vector<std::pair<int64_t, bool>>& layout) {
+    int64_t n = 0;
+    for (const auto& e : layout) n += e.first;
+    return n;
+}
+
+AttentionConfig attention_config(const px_model_config& c) {
+    AttentionConfig a;
+    a.d_model = c.hidden_size;
+    a.num_heads = c.num_heads;
+    a.num_kv_heads = kv_heads(c);
+    a.head_dim = head_dim(c);
+    a.use_rope = c.use_rope != 0;
+    a.rope_layout = c.rope_rotate_half ? RoPELayout::RotateHalf : RoPELayout::AdjacentPairs;
+    a.rope_base = c.rope_theta;
+    a.qkv_bias = c.qkv_bias != 0;
+    a.out_bias = c.out_bias != 0;
+    a.causal = c.causal != 0;
+    return a;
+}
+
+std::vector<float> take(const float*& p, int64_t n) {
+    std::vector<float> v(p, p + n);
+    p += n;
+    return v;
+}
+
+void load_linear(LinearModule& m, const float*& p) {
+    m.set_weight(take(p, m.in_features() * m.out_features()));
+    if (m.use_bias()) m.set_bias(take(p, m.out_features()));
+}
+
+void load_block(TransformerBlock& b, const float*& p) {
+    b.norm1().set_gamma(take(p, b.norm1().num_features()));
+    load_linear(b.mha().q_proj(), p);
+    load_linear(b.mha().k_proj(), p);
+    load_linear(b.mha().v_proj(), p);
+    load_linear(b.mha().out_proj(), p);
+    b.norm2().set_gamma(take(p, b.norm2().num_features()));
+    load_linear(b.swiglu().gate_proj(), p);
+    load_linear(b.swiglu().up_proj(), p);
+    load_linear(b.swiglu().down_proj(), p);
+}
+
+struct BlockHandle {
+    std::unique_ptr<TransformerBlock> block;
+    int64_t d = 0, n = 0, l = 0;
+};
+
+struct LmHandle {
+    std::unique_ptr<CausalLM> lm;
+    px_model_config cfg{};
+    int64_t n = 0, l = 0;
+};
+
+LmHandle* make_lm(const px_model_config& c, const float* params) {
+    if (c.vocab_size <= 0 || c.num_layers <= 0) throw std::invalid_argument("model config: vocab_size and num_layers must be positive");
+    HfModelConfig hc;
+    hc.hidden_size = c.hidden_size;
+    hc.intermediate_size = c.intermediate_size;
+    hc.num_hidden_layers = c.num_layers;
+    hc.num_attention_heads = c.num_heads;
+    hc.num_key_value_heads = kv_heads(c);
+    hc.head_dim = head_dim(c);
+    hc.vocab_size = c.vocab_size;
+    hc.rms_norm_eps = c.rms_norm_eps;
+    hc.rope_theta = c.rope_theta;
+    hc.tie_word_embeddings = c.tie_word_embeddings != 0;
+    hc.qkv_bias = c.qkv_bias != 0;
+    hc.out_bias = c.out_bias != 0;
+    hc.mlp_bias = c.mlp_bias != 0;
+    hc.causal = c.causal != 0;
+    if (!c.use_rope || !c.rope_rotate_half)
+        throw std::invalid_argument("model config: the causal LM uses rotate-half RoPE (ToAttentionConfig)");
+    auto h = std::make_unique<LmHandle>();
+    h->cfg = c;
+    h->lm = std::make_unique<CausalLM>(hc, backend());
+    const float* p = params;
+    h->lm->embed_tokens().set_weight(take(p, c.vocab_size * c.hidden_size));
+    for (int64_t i = 0; i < c.num_layers; ++i) load_block(h->lm->layer(i), p);
+    h->lm->norm().set_gamma(take(p, c.hidden_size));
+    if (!c.tie_word_embeddings) h->lm->lm_head()->set_weight(take(p, c.hidden_size * c.vocab_size));
+    return h.release();
+}
+
+LRPRuleConfig rule(float eps, int bias_in_denominator) {
+    LRPRuleConfig r{eps};
+    r.epsilon_bias_in_denominator = bias_in_denominator != 0;
+    return r;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* pxa_last_error(void) { return g_error.c_str(); }
+
+int pxa_device_count(void) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) return 0;
+    return n;
+}
+
+void* pxa_backend(void) {
+    void* out = nullptr;
+    guarded([&] { out = backend(); });
+    return out;
+}
+
+void* pxa_backend_stream(void) {
+    void* out = nullptr;
+    guarded([&] { out = backend()->stream(); });
+    return out;
+}
+
+int pxa_backend_synchronize(void) {
+    return guarded([&] { backend()->synchronize(); });
+}
+
+int pxa_backend_memory(size_t* in_use, size_t* cached) {
+    return guarded([&] {
+        if (in_use) *in_use = backend()->allocator().bytes_in_use();
+        if (cached) *cached = backend()->allocator().bytes_cached();
+    });
+}
+
+void pxa_fill_normal(float* dst, size_t n, uint64_t seed, double stddev) {
+    uint64_t state = seed;
+    auto next = [&state]() {  // SplitMix64
+        state += 0x9E3779B97F4A7C15ULL;
+        uint64_t z = state;
+        z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ULL;
+        z = (z ^ (z >> 27)) * 0x94D049BB133111EBULL;
+        return z ^ (z >> 31);
+    };
+    auto uniform = [&]() { return (static_cast<double>(next() >> 11) + 0.5) / static_cast<double>(1ULL << 53); };
+    constexpr double kTwoPi = 6.28318530717958647692;
+    for (size_t i = 0; i < n; ++i) {
+        const double u1 = uniform();
+        const double u2 = uniform();
+        dst[i] = static_cast<float>(stddev * (std::sqrt(-2.0 * std::log(u1)) * std::cos(kTwoPi * u2)));
+    }
+}
+
+int64_t pxa_param_count(const px_model_config* cfg) { return total(lm_layout(*cfg)); }
+int64_t pxa_block_param_count(const px_model_config* cfg) { return total(block_layout(*cfg)); }
+
+int pxa_synthetic_params(const px_model_config* cfg, int block, uint64_t seed, double stddev, float* dst) {
+    return guarded([&] {
+        const auto layout = block ? block_layout(*cfg) : lm_layout(*cfg);
+        pxa_fill_normal(dst, static_cast<size_t>(total(layout)), seed, stddev);
+        int64_t off = 0;
+        for (const auto& [size, gamma] : layout) {
+            if (gamma)
+                for (int64_t i = 0; i < size; ++i) dst[off + i] = 1.0f;
+            off += size;
+        }
+    });
+}
+
+void* pxa_block_create(const px_model_config* cfg, const float* params) {
+    BlockHandle* out = nullptr;
+    guarded([&] {
+        auto h = std::make_unique<BlockHandle>();
+        TransformerBlockOptions opt;
+        opt.norm_eps = cfg->rms_norm_eps;
+        opt.mlp_bias = cfg->mlp_bias != 0;
+        h->block = std::make_unique<TransformerBlock>(attention_config(*cfg), cfg->intermediate_size, backend(), opt);
+        const float* p = params;
+        load_block(*h->block, p);
+        h->d = cfg->hidden_size;
+        out = h.release();
+    });
+    return out;
+}
+
+int pxa_block_forward(void* handle, const float* x, int64_t n, int64_t l, float* y) {
+    return guarded([&] {
+        auto* h = static_cast<BlockHandle*>(handle);
+        Tensor in(Shape({n, l, h->d}), backend(), std::vector<float>(x, x + n * l * h->d));
+        const std::vector<float> out = h->block->forward(in).to_host_vector();
+        std::copy(out.begin(), out.end(), y);
+        h->n = n;
+        h->l = l;
+    });
+}
+
+int pxa_block_relevance(void* handle, const float* r_out, float eps, int bias_in_denominator, float* r_in) {
+    return guarded([&] {
+        auto* h = static_cast<BlockHandle*>(handle);
+        if (h->n == 0) throw std::logic_error("TransformerBlock::propagate_relevance: called before any forward()");
+        const int64_t count = h->n * h->l * h->d;
+        Tensor r(Shape({h->n, h->l, h->d}), backend(), std::vector<float>(r_out, r_out + count));
+        const std::vector<float> out = h->block->propagate_relevance(r, rule(eps, bias_in_denominator)).to_host_vector();
+        std::copy(out.begin(), out.end(), r_in);
+    });
+}
+
+void pxa_block_destroy(void* handle) { delete static_cast<BlockHandle*>(handle); }
+
+void* pxa_lm_create(const px_model_config* cfg, const float* params) {
+    LmHandle* out = nullptr;
+    guarded([&] { out = make_lm(*cfg, params); });
+    return out;
+}
+
+void* pxa_lm_create_random(const px_model_config* cfg, uint64_t seed, double stddev) {
+    LmHandle* out = nullptr;
+    guarded([&] {
+        std::vector<float> params(static_cast<size_t>(total(lm_layout(*cfg))));
+        if (pxa_synthetic_params(cfg, 0, seed, stddev, params.data()) != 0) throw std::runtime_error(g_error);
+        out = make_lm(*cfg, params.data());
+    });
+    return out;
+}
+
+int pxa_lm_forward(void* handle, const int64_t* ids, int64_t n, int64_t l, float* logits) {
+    return guarded([&] {
+        auto* h = static_cast<LmHandle*>(handle);
+        std::vector<float> f(static_cast<size_t>(n * l));
+        for (size_t i = 0; i < f.size(); ++i) f[i] = static_cast<float>(ids[i]);
+        Tensor out = h->lm->forward(Tensor(Shape({n, l}), backend(), f));
+        h->n = n;
+        h->l = l;
+        if (logits) {
+            const std::vector<float> v = out.to_host_vector();
+            std::copy(v.begin(), v.end(), logits);
+        }
+    });
+}
+
+int pxa_lm_relevance(void* handle, const float* seed, float eps, int bias_in_denominator, float* r_embed,
+                     float* r_tokens, float* key_rel, float* value_rel) {
+    return guarded([&] {
+        auto* h = static_cast<LmHandle*>(handle);
+        if (h->n == 0) throw std::logic_error("CausalLM::propagate_relevance_by_layer: called before any forward()");
+        CausalLM& lm = *h->lm;
+        const px_model_config& c = h->cfg;
+        const int64_t count = h->n * h->l * c.vocab_size;
+        Tensor s(Shape({h->n, h->l, c.vocab_size}), backend(), std::vector<float>(seed, seed + count));
+        const LRPRuleConfig cfg = rule(eps, bias_in_denominator);
+        const std::vector<Tensor> bounds = lm.propagate_relevance_by_layer(s, cfg);
+        auto to_host = [](const Tensor& t, float* dst) {
+            const std::vector<float> v = t.to_host_vector();
+            std::copy(v.begin(), v.end(), dst);
+        };
+        if (r_embed) to_host(bounds.front(), r_embed);
+        if (r_tokens) to_host(lm.embed_tokens().propagate_relevance(bounds.front(), cfg), r_tokens);
+        const int64_t kv = h->n * h->l * kv_heads(c) * head_dim(c);
+        for (int64_t i = 0; i < lm.num_layers(); ++i) {
+            if (key_rel) to_host(lm.layer(i).mha().key_relevance(), key_rel + i * kv);
+            if (value_rel) to_host(lm.layer(i).mha().value_relevance(), value_rel + i * kv);
+        }
+    });
+}
+
+int pxa_lm_explain_device(void* handle, const float* ids, int64_t n, int64_t l, float eps, int bias_in_denominator,
+                          float* token_rel, int64_t* targets, const int64_t* targets_in, int unit_seed) {
+    return guarded([&] {
+        auto* h = static_cast<LmHandle*>(handle);
+        h->lm->explain_device(ids, n, l, rule(eps, bias_in_denominator), token_rel, targets, targets_in, unit_seed != 0);
+    });
+}
+
+int pxa_lm_capture_explain(void* handle, const float* ids, int64_t n, int64_t l, float eps, int bias_in_denominator,
+                           float* token_rel, int64_t* targets) {
+    return guarded([&] {
+        auto* h = static_cast<LmHandle*>(handle);
+        MI355XBackend* be = backend();
+        be->begin_capture();
+        try {
+            h->lm->explain_device(ids, n, l, rule(eps, bias_in_denominator), token_rel, targets, nullptr, false);
+        } catch (...) {
+            try {
+                be->end_capture();
+            } catch (...) {
+            }
+            throw;
+        }
+        be->end_capture();
+    });
+}
+
+int pxa_lm_replay(void*) {
+    return guarded([&] { backend()->replay(); });
+}
+
+const float* pxa_lm_last_logits(void* handle) { return static_cast<LmHandle*>(handle)->lm->last_logits(); }
+const float* pxa_lm_last_embedding_relevance(void* handle) {
+    return static_cast<LmHandle*>(handle)->lm->last_embedding_relevance();
+}
+
+void pxa_lm_destroy(void* handle) { delete static_cast<LmHandle*>(handle); }
+
+}  // extern "C"

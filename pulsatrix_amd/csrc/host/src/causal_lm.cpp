@@ -1,0 +1,135 @@
+// CausalLM on MI355XBackend (src/causal_lm.cpp, src/hf_model.cpp:282-313).
+#include "pulsatrix/causal_lm.hpp"
+
+#include <cmath>
+#include <stdexcept>
+
+namespace pulsatrix {
+
+AttentionConfig ToAttentionConfig(const HfModelConfig& config) {
+    AttentionConfig a;
+    a.d_model = config.hidden_size;
+    a.num_heads = config.num_attention_heads;
+    a.num_kv_heads = config.num_key_value_heads;
+    a.head_dim = config.head_dim;
+    a.use_rope = true;
+    a.rope_layout = RoPELayout::RotateHalf;
+    a.rope_base = config.rope_theta;
+    a.use_qk_norm = config.qk_norm;
+    a.qk_norm_eps = config.rms_norm_eps;
+    a.qkv_bias = config.qkv_bias;
+    a.out_bias = config.out_bias;
+    a.causal = config.causal;
+    return a;
+}
+
+namespace {
+
+const HfModelConfig& checked(const HfModelConfig& c) {
+    if (c.hidden_size <= 0 || c.num_hidden_layers <= 0 || c.vocab_size <= 0 || c.intermediate_size <= 0)
+        throw std::invalid_argument("CausalLM: hidden_size, num_hidden_layers, vocab_size and intermediate_size "
+                                    "must be positive");
+    if (c.hidden_act != "silu") throw std::invalid_argument("CausalLM: the MI355X path runs SiLU-gated MLPs");
+    if (c.embed_scale != 1.0f) throw std::invalid_argument("CausalLM: embedding scaling is not on the MI355X path");
+    return c;
+}
+
+TransformerBlockOptions block_options(const HfModelConfig& c) {
+    TransformerBlockOptions o;
+    o.norm_eps = c.rms_norm_eps;
+    o.mlp_bias = c.mlp_bias;
+    o.mlp_activation = GatedActivation::Silu;
+    return o;
+}
+
+}  // namespace
+
+CausalLM::CausalLM(const HfModelConfig& config, DeviceBackend* backend)
+    : config_(checked(config)),
+      be_(detail::require_mi355x(backend, "CausalLM")),
+      embed_(config.vocab_size, config.hidden_size, backend),
+      norm_(config.hidden_size, backend, DeviceType::Hip, config.rms_norm_eps) {
+    for (int64_t i = 0; i < config.num_hidden_layers; ++i)
+        layers_.push_back(std::make_unique<TransformerBlock>(ToAttentionConfig(config), config.intermediate_size,
+                                                             backend, block_options(config)));
+    if (config.tie_word_embeddings)
+        tied_head_ = std::make_unique<TiedLMHeadModule>(embed_, backend);
+    else
+        lm_head_ = std::make_unique<LinearModule>(config.hidden_size, config.vocab_size, backend, false);
+}
+
+const float* CausalLM::last_logits() const noexcept { return tied_head_ ? tied_head_->logits() : nullptr; }
+
+const float* CausalLM::run_forward(const float* ids, int64_t n, int64_t l) {
+    N_ = n;
+    L_ = l;
+    const int64_t M = n * l;
+    const float* x = embed_.run_forward_device(ids, n, l);
+    for (auto& layer : layers_) x = layer->run_forward(x, n, l);
+    const float* xn = norm_.run_forward(x, M);
+    return tied_head_ ? tied_head_->run_forward(xn, M) : lm_head_->run_forward(xn, M);
+}
+
+const float* CausalLM::run_relevance(const float* seed, const LRPRuleConfig& config) {
+    if (N_ == 0) throw std::logic_error("CausalLM::propagate_relevance_by_layer: called before any forward()");
+    const float* r = tied_head_ ? tied_head_->run_relevance(seed, config) : lm_head_->run_relevance(seed, config);
+    // The final RMSNorm passes relevance through unchanged (rms_norm_module.cpp:101-111).
+    for (size_t i = layers_.size(); i-- > 0;) r = layers_[i]->run_relevance(r, config);
+    r_embed_ = r;
+    return r;
+}
+
+void CausalLM::explain_device(const float* ids, int64_t n, int64_t l, const LRPRuleConfig& config,
+                              float* token_relevance, int64_t* targets, const int64_t* targets_in, bool unit_seed) {
+    const int64_t V = config_.vocab_size, M = n * l;
+    const float* logits = run_forward(ids, n, l);
+    float* seed = seed_.ensure(be_, M * V);
+    MI355XBackend::check(pxk_lm_seed(logits, n, l, V, targets_in, targets, seed, unit_seed, be_->stream()),
+                         "CausalLM::explain_device (seed)");
+    embed_.token_relevance(run_relevance(seed, config), M, token_relevance);
+}
+
+Tensor CausalLM::forward_impl(const Tensor& input) {
+    if (input.rank() != 2) throw std::invalid_argument("CausalLM::forward: input must be (N, L) token ids");
+    const int64_t n = input.shape().dim(0), l = input.shape().dim(1), V = config_.vocab_size;
+    std::vector<float> raw = input.to_host_vector();
+    for (float& v : raw) {  // EmbeddingModule::forward_impl's validation (embedding_module.cpp:48-59)
+        const auto idx = static_cast<int64_t>(std::llround(static_cast<double>(v)));
+        if (idx < 0 || idx >= V)
+            throw std::invalid_argument("EmbeddingModule::forward: index out of range [0, num_embeddings)");
+        v = static_cast<float>(idx);
+    }
+    float* ids = ids_.ensure(be_, n * l);
+    be_->copy(ids, raw.data(), raw.size() * sizeof(float), CopyDirection::HostToDevice);
+    return detail::copy_out(be_, run_forward(ids, n, l), Shape({n, l, V}));
+}
+
+std::vector<Tensor> CausalLM::propagate_relevance_by_layer(const Tensor& relevance_out, const LRPRuleConfig& config) {
+    if (N_ == 0) throw std::logic_error("CausalLM::propagate_relevance_by_layer: called before any forward()");
+    const int64_t V = config_.vocab_size, d = config_.hidden_size;
+    if (relevance_out.numel() != N_ * L_ * V)
+        throw std::invalid_argument("CausalLM::propagate_relevance_by_layer: relevance_out must be (N, L, vocab)");
+    const Shape shape({N_, L_, d});
+    std::vector<Tensor> bounds(layers_.size() + 1);
+    const float* r = tied_head_ ? tied_head_->run_relevance(relevance_out.data(), config)
+                                : lm_head_->run_relevance(relevance_out.data(), config);
+    for (size_t i = layers_.size(); i-- > 0;) {
+        bounds[i + 1] = detail::copy_out(be_, r, shape);
+        r = layers_[i]->run_relevance(r, config);
+    }
+    bounds[0] = detail::copy_out(be_, r, shape);
+    r_embed_ = r;
+    return bounds;
+}
+
+Tensor CausalLM::propagate_relevance(const Tensor& relevance_out, const LRPRuleConfig& config) {
+    if (N_ == 0) throw std::logic_error("CausalLM::propagate_relevance: called before any forward()");
+    if (relevance_out.numel() != N_ * L_ * config_.vocab_size)
+        throw std::invalid_argument("CausalLM::propagate_relevance: relevance_out must be (N, L, vocab)");
+    const float* r = run_relevance(relevance_out.data(), config);
+    Tensor out = Tensor::uninitialized(Shape({N_, L_}), be_);
+    embed_.token_relevance(r, N_ * L_, out.data());
+    return out;
+}
+
+}  // namespace pulsatrix

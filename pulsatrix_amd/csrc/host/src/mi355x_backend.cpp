@@ -1,0 +1,615 @@
+// MI355XBackend: DeviceBackend over libpxk_gfx950 (include/pxk.h).
+#include "pulsatrix/mi355x_backend.hpp"
+
+#include <hip/hip_runtime_api.h>
+
+#include <algorithm>
+#include <cstdlib>
+#include <cstring>
+#include <new>
+#include <stdexcept>
+#include <string>
+
+namespace pulsatrix {
+
+namespace {
+
+void hip_check(hipError_t e, const char* what) {
+    if (e != hipSuccess) throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
+}
+
+[[noreturn]] void off_path(const char* op) {
+    throw std::logic_error(std::string("MI355XBackend::") + op +
+                           ": outside the causal-LM forward + AttnLRP path this backend implements");
+}
+
+hipStream_t S(void* s) { return static_cast<hipStream_t>(s); }
+
+void* raw_alloc(size_t bytes, void*) {
+    void* p = nullptr;
+    if (hipMalloc(&p, bytes) != hipSuccess) {
+        (void)hipGetLastError();  // clear the sticky out-of-memory status before a retry
+        return nullptr;
+    }
+    return p;
+}
+
+void raw_free(void* p, void*) { (void)hipFree(p); }
+
+pxk_operand op(const float* p, int64_t ld) { return pxk_operand{p, ld, 0, 0, 0, 0}; }
+
+constexpr size_t kReduceFloats = 1024 + 64;
+
+}  // namespace
+
+// ---- CachingAllocator --------------------------------------------------------------------------
+
+CachingAllocator::CachingAllocator(RawAlloc alloc, RawFree free, void* ctx, size_t budget_bytes)
+    : raw_alloc_(alloc), raw_free_(free), ctx_(ctx), budget_(budget_bytes) {}
+
+CachingAllocator::~CachingAllocator() {
+    release_cache();
+    std::lock_guard<std::mutex> lock(mu_);
+    for (auto& [p, size] : live_) raw_free_(p, ctx_);
+    live_.clear();
+}
+
+size_t CachingAllocator::round_size(size_t bytes) {
+    // 512 B granules below 1 MiB, then 1 MiB granules: a reused activation of the same shape hits.
+    const size_t small = 512, big = size_t{1} << 20;
+    return bytes < big ? (bytes + small - 1) / small * small : (bytes + big - 1) / big * big;
+}
+
+void* CachingAllocator::allocate(size_t bytes) {
+    if (bytes == 0) return nullptr;
+    const size_t size = round_size(bytes);
+    std::lock_guard<std::mutex> lock(mu_);
+    auto it = cache_.find(size);
+    if (it != cache_.end() && !it->second.empty()) {
+        void* p = it->second.back();
+        it->second.pop_back();
+        cached_ -= size;
+        live_.emplace(p, size);
+        in_use_ += size;
+        return p;
+    }
+    auto attempt = [&]() -> void* {
+        if (budget_ > 0 && in_use_ + cached_ + size > budget_) return nullptr;
+        return raw_alloc_(size, ctx_);
+    };
+    void* p = attempt();
+    if (p == nullptr) {  // out of memory: give the cache back and retry once
+        for (auto& [sz, blocks] : cache_)
+            for (void* b : blocks) raw_free_(b, ctx_);
+        cache_.clear();
+        cached_ = 0;
+        p = attempt();
+    }
+    if (p == nullptr) throw std::bad_alloc();
+    live_.emplace(p, size);
+    in_use_ += size;
+    return p;
+}
+
+void CachingAllocator::free(void* ptr) noexcept {
+    if (ptr == nullptr) return;
+    std::lock_guard<std::mutex> lock(mu_);
+    auto it = live_.find(ptr);
+    if (it == live_.end()) return;
+    const size_t size = it->second;
+    live_.erase(it);
+    in_use_ -= size;
+    cache_[size].push_back(ptr);
+    cached_ += size;
+}
+
+void CachingAllocator::release_cache() noexcept {
+    std::lock_guard<std::mutex> lock(mu_);
+    for (auto& [sz, blocks] : cache_)
+        for (void* b : blocks) raw_free_(b, ctx_);
+    cache_.clear();
+    cached_ = 0;
+}
+
+size_t CachingAllocator::bytes_in_use() const {
+    std::lock_guard<std::mutex> lock(mu_);
+    return in_use_;
+}
+
+size_t CachingAllocator::bytes_cached() const {
+    std::lock_guard<std::mutex> lock(mu_);
+    return cached_;
+}
+
+// ---- MI355XBackend -------------------------------------------------------------------------------
+
+MI355XBackend::MI355XBackend(int device_index) : device_(device_index) {
+    int count = 0;
+    hip_check(hipGetDeviceCount(&count), "MI355XBackend: hipGetDeviceCount");
+    if (device_index < 0 || device_index >= count)
+        throw std::runtime_error("MI355XBackend: no HIP device " + std::to_string(device_index));
+    hip_check(hipSetDevice(device_index), "MI355XBackend: hipSetDevice");
+    hipStream_t s = nullptr;
+    hip_check(hipStreamCreateWithFlags(&s, hipStreamNonBlocking), "MI355XBackend: hipStreamCreate");
+    stream_ = s;
+    size_t budget = 0;
+    if (const char* mb = std::getenv("PULSATRIX_HIP_MEMORY_BUDGET_MB")) budget = std::strtoull(mb, nullptr, 10) << 20;
+    sync_debug_ = std::getenv("PULSATRIX_HIP_SYNC_DEBUG") != nullptr;
+    allocator_ = new CachingAllocator(raw_alloc, raw_free, nullptr, budget);
+    reduce_ = static_cast<float*>(allocator_->allocate(kReduceFloats * sizeof(float)));
+}
+
+MI355XBackend::~MI355XBackend() {
+    if (stream_) (void)hipStreamSynchronize(S(stream_));
+    if (graph_exec_) (void)hipGraphExecDestroy(static_cast<hipGraphExec_t>(graph_exec_));
+    if (graph_) (void)hipGraphDestroy(static_cast<hipGraph_t>(graph_));
+    delete allocator_;
+    if (stream_) (void)hipStreamDestroy(S(stream_));
+}
+
+void MI355XBackend::check(int rc, const char* what) {
+    if (rc == PXK_OK) return;
+    const std::string msg = std::string(what) + ": " + pxk_last_error();
+    if (rc == PXK_ERR_INVALID) throw std::invalid_argument(msg);
+    throw std::runtime_error(msg);
+}
+
+void MI355XBackend::synchronize() { hip_check(hipStreamSynchronize(S(stream_)), "MI355XBackend::synchronize"); }
+
+void* MI355XBackend::allocate(size_t bytes) {
+    if (bytes == 0) return nullptr;
+    try {
+        return allocator_->allocate(bytes);
+    } catch (const std::bad_alloc&) {
+        throw std::runtime_error("MI355XBackend::allocate: failed to allocate " + std::to_string(bytes) + " bytes");
+    }
+}
+
+void MI355XBackend::free(void* ptr) noexcept {
+    // Kernels queued on the stream may still read the block; the allocator only recycles it to
+    // later work on the same in-order stream, so no wait is needed.
+    allocator_->free(ptr);
+}
+
+void MI355XBackend::copy(void* dst, const void* src, size_t bytes, CopyDirection dir) {
+    if (bytes == 0) return;
+    hipMemcpyKind kind = hipMemcpyDeviceToDevice;
+    switch (dir) {
+        case CopyDirection::HostToDevice: kind = hipMemcpyHostToDevice; break;
+        case CopyDirection::DeviceToHost: kind = hipMemcpyDeviceToHost; break;
+        case CopyDirection::DeviceToDevice: kind = hipMemcpyDeviceToDevice; break;
+        case CopyDirection::HostToHost: std::memcpy(dst, src, bytes); return;
+    }
+    if (kind == hipMemcpyDeviceToDevice && bytes % sizeof(float) == 0) {
+        // A copy kernel rather than an SDMA copy: it stays inside a captured graph.
+        check(pxk_copy_2d(static_cast<float*>(dst), 0, static_cast<const float*>(src), 0, 1,
+                          static_cast<int64_t>(bytes / sizeof(float)), stream_),
+              "MI355XBackend::copy");
+        return;
+    }
+    hip_check(hipMemcpyAsync(dst, src, bytes, kind, S(stream_)), "MI355XBackend::copy");
+    if (kind != hipMemcpyDeviceToDevice) synchronize();  // host copies synchronize (hip_backend.hip:102-110)
+}
+
+void MI355XBackend::fill(void* ptr, float value, size_t n) {
+    check(pxk_fill(static_cast<float*>(ptr), value, static_cast<int64_t>(n), stream_), "MI355XBackend::fill");
+}
+
+float* MI355XBackend::workspace(size_t bytes) {
+    if (bytes > ws_bytes_) {
+        if (ws_) allocator_->free(ws_);
+        ws_bytes_ = std::max(bytes, ws_bytes_ * 2);
+        ws_ = static_cast<float*>(allocator_->allocate(ws_bytes_));
+    }
+    return ws_;
+}
+
+void MI355XBackend::run_gemm(pxk_gemm_desc& d) {
+    const size_t need = pxk_gemm_workspace(&d);
+    if (need > 0) {
+        d.workspace = workspace(need);
+        d.workspace_bytes = ws_bytes_;
+    }
+    check(pxk_gemm(&d, stream_), "MI355XBackend gemm");
+    if (sync_debug_) synchronize();
+}
+
+void MI355XBackend::gemm(const float* a, const float* b, float* out, size_t m, size_t k, size_t n) {
+    gemm_ex(a, false, b, false, out, m, k, n, 0.0f);
+}
+
+void MI355XBackend::gemm_ex(const float* a, bool ta, const float* b, bool tb, float* out, size_t m, size_t k,
+                            size_t n, float beta) {
+    if (m == 0 || n == 0) return;
+    pxk_gemm_desc d{};
+    d.m = static_cast<int64_t>(m);
+    d.n = static_cast<int64_t>(n);
+    d.k = static_cast<int64_t>(k);
+    d.batch = d.inner = d.kgroups = 1;
+    d.trans_a = ta;
+    d.trans_b = tb;
+    d.epilogue = PXK_EPI_STORE;
+    d.beta = beta;
+    d.a = op(a, ta ? d.m : d.k);
+    d.b = op(b, tb ? d.k : d.n);
+    d.c = op(out, d.n);
+    run_gemm(d);
+}
+
+void MI355XBackend::gemm_strided_batched(const float* a, bool ta, size_t stride_a, const float* b, bool tb,
+                                         size_t stride_b, float* out, size_t stride_out, size_t m, size_t k, size_t n,
+                                         size_t batch, float beta) {
+    if (m == 0 || n == 0 || batch == 0) return;
+    pxk_gemm_desc d{};
+    d.m = static_cast<int64_t>(m);
+    d.n = static_cast<int64_t>(n);
+    d.k = static_cast<int64_t>(k);
+    d.batch = static_cast<int64_t>(batch);
+    d.inner = d.kgroups = 1;
+    d.trans_a = ta;
+    d.trans_b = tb;
+    d.epilogue = PXK_EPI_STORE;
+    d.beta = beta;
+    d.a = pxk_operand{a, ta ? d.m : d.k, static_cast<int64_t>(stride_a), 0, 0, 0};
+    d.b = pxk_operand{b, tb ? d.k : d.n, static_cast<int64_t>(stride_b), 0, 0, 0};
+    d.c = pxk_operand{out, d.n, static_cast<int64_t>(stride_out), 0, 0, 0};
+    run_gemm(d);
+}
+
+void MI355XBackend::elementwise(ElementwiseOp o, const float* in, float* out, size_t n) {
+    check(pxk_elementwise(static_cast<int>(o), in, out, static_cast<int64_t>(n), stream_), "MI355XBackend::elementwise");
+}
+
+void MI355XBackend::add(const float* a, const float* b, float* out, size_t n) {
+    check(pxk_add(a, b, out, static_cast<int64_t>(n), stream_), "MI355XBackend::add");
+}
+
+void MI355XBackend::mul(const float* a, const float* b, float* out, size_t n) {
+    check(pxk_mul(a, b, out, static_cast<int64_t>(n), stream_), "MI355XBackend::mul");
+}
+
+void MI355XBackend::column_sums(const float* in, float* out, size_t rows, size_t cols, float beta) {
+    check(pxk_column_sums(in, out, static_cast<int64_t>(rows), static_cast<int64_t>(cols), beta, stream_),
+          "MI355XBackend::column_sums");
+}
+
+void MI355XBackend::add_row_vector(const float* in, const float* row, float* out, size_t rows, size_t cols) {
+    check(pxk_add_row_vector(in, row, out, static_cast<int64_t>(rows), static_cast<int64_t>(cols), stream_),
+          "MI355XBackend::add_row_vector");
+}
+
+void MI355XBackend::axpby(float alpha, const float* x, float beta, const float* y, float* out, size_t n) {
+    check(pxk_axpby(alpha, x, beta, y, out, static_cast<int64_t>(n), stream_), "MI355XBackend::axpby");
+}
+
+float MI355XBackend::dot(const float* a, const float* b, size_t n) {
+    check(pxk_dot(a, b, static_cast<int64_t>(n), reduce_ + 1024, reduce_, stream_), "MI355XBackend::dot");
+    float out = 0.0f;
+    hip_check(hipMemcpyAsync(&out, reduce_ + 1024, sizeof(float), hipMemcpyDeviceToHost, S(stream_)),
+              "MI355XBackend::dot");
+    synchronize();
+    return out;
+}
+
+void MI355XBackend::dot_into(const float* a, const float* b, size_t n, float* out) {
+    float* partials = static_cast<float*>(allocator_->allocate(pxk_reduce_partials(static_cast<int64_t>(n))));
+    check(pxk_dot(a, b, static_cast<int64_t>(n), out, partials, stream_), "MI355XBackend::dot_into");
+    allocator_->free(partials);
+}
+
+float MI355XBackend::sum(const float* in, size_t n) {
+    check(pxk_sum(in, static_cast<int64_t>(n), reduce_ + 1024, reduce_, stream_), "MI355XBackend::sum");
+    float out = 0.0f;
+    hip_check(hipMemcpyAsync(&out, reduce_ + 1024, sizeof(float), hipMemcpyDeviceToHost, S(stream_)),
+              "MI355XBackend::sum");
+    synchronize();
+    return out;
+}
+
+void MI355XBackend::softmax_rows(const float* in, float* out, size_t rows, size_t cols) {
+    check(pxk_softmax_rows(in, out, static_cast<int64_t>(rows), static_cast<int64_t>(cols), stream_),
+          "MI355XBackend::softmax_rows");
+}
+
+void MI355XBackend::rms_norm_forward(const float* in, const float* gamma, float* out, float* row_rms, size_t rows,
+                                     size_t cols, float eps) {
+    check(pxk_rms_norm_forward(in, gamma, out, row_rms, static_cast<int64_t>(rows), static_cast<int64_t>(cols), eps,
+                               stream_),
+          "MI355XBackend::rms_norm_forward");
+}
+
+void MI355XBackend::rope_rotate(const float* in, const float* cos_table, const float* sin_table, float* out,
+                                size_t num_slices, size_t seq_len, size_t head_dim, bool inverse, bool rotate_half) {
+    check(pxk_rope_rotate(in, cos_table, sin_table, out, static_cast<int64_t>(num_slices),
+                          static_cast<int64_t>(seq_len), static_cast<int64_t>(head_dim), inverse, rotate_half,
+                          stream_),
+          "MI355XBackend::rope_rotate");
+}
+
+void MI355XBackend::permute_0213(const float* in, float* out, size_t d0, size_t d1, size_t d2, size_t d3) {
+    check(pxk_permute_0213(in, out, static_cast<int64_t>(d0), static_cast<int64_t>(d1), static_cast<int64_t>(d2),
+                           static_cast<int64_t>(d3), stream_),
+          "MI355XBackend::permute_0213");
+}
+
+void MI355XBackend::attention_mask_fill(float* scores, const float* key_keep, size_t batch, size_t heads,
+                                        size_t q_len, size_t k_len, bool causal, size_t q_offset, size_t window,
+                                        float value) {
+    check(pxk_attention_mask_fill(scores, key_keep, static_cast<int64_t>(batch), static_cast<int64_t>(heads),
+                                  static_cast<int64_t>(q_len), static_cast<int64_t>(k_len), causal,
+                                  static_cast<int64_t>(q_offset), static_cast<int64_t>(window), value, stream_),
+          "MI355XBackend::attention_mask_fill");
+}
+
+void MI355XBackend::gather_rows(const float* table, const float* indices, float* out, size_t count, size_t dim) {
+    check(pxk_gather_rows(table, indices, out, static_cast<int64_t>(count), static_cast<int64_t>(dim), stream_),
+          "MI355XBackend::gather_rows");
+}
+
+void MI355XBackend::lrp_linear(const float* x, const float* w, const float* z, const float* r, float* r_in,
+                               size_t rows, size_t in_features, size_t out_features, float eps) {
+    // r_in = x * ((r / stab(z)) W^T): the per-term divide of lrp_math.hpp:21-30 factored out of
+    // the sum, one fused MFMA GEMM (DIV_STAB prologue, MUL_X epilogue).
+    if (rows == 0 || in_features == 0) return;
+    pxk_gemm_desc d{};
+    d.m = static_cast<int64_t>(rows);
+    d.n = static_cast<int64_t>(in_features);
+    d.k = static_cast<int64_t>(out_features);
+    d.batch = d.inner = d.kgroups = 1;
+    d.trans_b = 1;
+    d.prologue = PXK_PRO_DIV_STAB;
+    d.epilogue = PXK_EPI_MUL_X;
+    d.eps = eps;
+    d.a = op(r, d.k);
+    d.z = op(z, d.k);
+    d.b = op(w, d.k);
+    d.c = op(r_in, d.n);
+    d.x = op(x, d.n);
+    run_gemm(d);
+}
+
+void MI355XBackend::lrp_residual_split(const float* a, const float* b, const float* r, float* r_a, float* r_b,
+                                       size_t n, float eps) {
+    check(pxk_lrp_residual_split(a, b, r, r_a, r_b, static_cast<int64_t>(n), eps, stream_),
+          "MI355XBackend::lrp_residual_split");
+}
+
+void MI355XBackend::lrp_bilinear_elementwise(const float* a, const float* b, const float* r, float* r_out, size_t n,
+                                             float eps) {
+    check(pxk_lrp_bilinear_elementwise(a, b, r, r_out, static_cast<int64_t>(n), eps, stream_),
+          "MI355XBackend::lrp_bilinear_elementwise");
+}
+
+void MI355XBackend::lrp_bilinear_matmul(const float* a, const float* b, const float* o, const float* r_o, float* r_a,
+                                        float* r_b, size_t slices, size_t m, size_t p, size_t q, float eps,
+                                        bool b_transposed) {
+    // GEMM form of Eq. 15 (lrp_math.hpp:57-86): s = R / (2 O + eps sign O);
+    // r_a = A * (s B^T); r_b = B * (A^T s) (or B^T * (s^T A) when B is stored transposed).
+    if (slices == 0 || m == 0 || p == 0 || q == 0) return;
+    const int64_t M = static_cast<int64_t>(m), P = static_cast<int64_t>(p), Q = static_cast<int64_t>(q);
+    const int64_t B = static_cast<int64_t>(slices);
+    float* s = static_cast<float*>(allocate(static_cast<size_t>(B * M * Q) * sizeof(float)));
+    check(pxk_lrp_bilinear_scale(r_o, o, s, B * M * Q, eps, stream_), "MI355XBackend::lrp_bilinear_matmul");
+    pxk_gemm_desc d{};
+    d.batch = B;
+    d.inner = d.kgroups = 1;
+    d.epilogue = PXK_EPI_MUL_X;
+    // r_a (M x P) = A (M x P) * [s (M x Q) @ B^T (Q x P)]
+    d.m = M;
+    d.n = P;
+    d.k = Q;
+    d.trans_b = b_transposed ? 0 : 1;
+    d.a = pxk_operand{s, Q, M * Q, 0, 0, 0};
+    d.b = pxk_operand{b, P, P * Q, 0, 0, 0};  // stored (P x Q) read as N x K, or (Q x P) as K x N
+    if (!b_transposed) d.b.ld = Q;
+    d.c = pxk_operand{r_a, P, M * P, 0, 0, 0};
+    d.x = pxk_operand{a, P, M * P, 0, 0, 0};
+    run_gemm(d);
+    // r_b, in B's stored layout
+    pxk_gemm_desc e{};
+    e.batch = B;
+    e.inner = e.kgroups = 1;
+    e.epilogue = PXK_EPI_MUL_X;
+    e.trans_a = 1;
+    e.k = M;
+    if (!b_transposed) {  // (P x Q) = B * (A^T s)
+        e.m = P;
+        e.n = Q;
+        e.a = pxk_operand{a, P, M * P, 0, 0, 0};
+        e.b = pxk_operand{s, Q, M * Q, 0, 0, 0};
+        e.c = pxk_operand{r_b, Q, P * Q, 0, 0, 0};
+        e.x = pxk_operand{b, Q, P * Q, 0, 0, 0};
+    } else {  // (Q x P) = B^T * (s^T A)
+        e.m = Q;
+        e.n = P;
+        e.a = pxk_operand{s, Q, M * Q, 0, 0, 0};
+        e.b = pxk_operand{a, P, M * P, 0, 0, 0};
+        e.c = pxk_operand{r_b, P, P * Q, 0, 0, 0};
+        e.x = pxk_operand{b, P, P * Q, 0, 0, 0};
+    }
+    run_gemm(e);
+    free(s);
+}
+
+void MI355XBackend::lrp_softmax_rows(const float* x, const float* y, const float* r, float* r_in, size_t rows,
+                                     size_t cols) {
+    check(pxk_lrp_softmax_rows(x, y, r, r_in, static_cast<int64_t>(rows), static_cast<int64_t>(cols), stream_),
+          "MI355XBackend::lrp_softmax_rows");
+}
+
+void MI355XBackend::lrp_rope(const float* x, const float* y, const float* r, const float* cos_table,
+                             const float* sin_table, float* r_in, size_t slices, size_t seq_len, size_t head_dim,
+                             float eps, bool rotate_half) {
+    check(pxk_lrp_rope(x, y, r, cos_table, sin_table, r_in, static_cast<int64_t>(slices), static_cast<int64_t>(seq_len),
+                       static_cast<int64_t>(head_dim), eps, rotate_half, stream_),
+          "MI355XBackend::lrp_rope");
+}
+
+void MI355XBackend::lrp_stabilized_divide(const float* r, const float* denom, const float* gate, float* out, size_t n,
+                                          float eps, LrpGate gate_mode) {
+    check(pxk_lrp_stabilized_divide(r, denom, gate, out, static_cast<int64_t>(n), eps, static_cast<int>(gate_mode),
+                                    stream_),
+          "MI355XBackend::lrp_stabilized_divide");
+}
+
+void MI355XBackend::copy_2d(float* dst, size_t dst_stride, const float* src, size_t src_stride, size_t rows,
+                            size_t cols) {
+    check(pxk_copy_2d(dst, static_cast<int64_t>(dst_stride), src, static_cast<int64_t>(src_stride),
+                      static_cast<int64_t>(rows), static_cast<int64_t>(cols), stream_),
+          "MI355XBackend::copy_2d");
+}
+
+void MI355XBackend::accumulate_rows(const float* in, float* out, size_t rows, size_t cols) {
+    check(pxk_accumulate_rows(in, out, static_cast<int64_t>(rows), static_cast<int64_t>(cols), stream_),
+          "MI355XBackend::accumulate_rows");
+}
+
+// ---- graphs ------------------------------------------------------------------------------------
+
+void MI355XBackend::begin_capture() {
+    if (graph_exec_) {
+        (void)hipGraphExecDestroy(static_cast<hipGraphExec_t>(graph_exec_));
+        graph_exec_ = nullptr;
+    }
+    if (graph_) {
+        (void)hipGraphDestroy(static_cast<hipGraph_t>(graph_));
+        graph_ = nullptr;
+    }
+    hip_check(hipStreamBeginCapture(S(stream_), hipStreamCaptureModeThreadLocal), "MI355XBackend::begin_capture");
+}
+
+void MI355XBackend::end_capture() {
+    hipGraph_t g = nullptr;
+    hip_check(hipStreamEndCapture(S(stream_), &g), "MI355XBackend::end_capture");
+    graph_ = g;
+    hipGraphExec_t e = nullptr;
+    hip_check(hipGraphInstantiate(&e, g, nullptr, nullptr, 0), "MI355XBackend::end_capture (instantiate)");
+    graph_exec_ = e;
+}
+
+void MI355XBackend::replay() {
+    if (!graph_exec_) throw std::logic_error("MI355XBackend::replay: nothing was captured");
+    hip_check(hipGraphLaunch(static_cast<hipGraphExec_t>(graph_exec_), S(stream_)), "MI355XBackend::replay");
+}
+
+// ---- outside the path ---------------------------------------------------------------------------
+
+void MI355XBackend::elementwise_backward(ElementwiseOp, const float*, const float*, float*, size_t) {
+    off_path("elementwise_backward");
+}
+void MI355XBackend::softmax_rows_backward(const float*, const float*, float*, size_t, size_t) {
+    off_path("softmax_rows_backward");
+}
+void MI355XBackend::logsumexp_rows(const float*, float*, size_t, size_t) { off_path("logsumexp_rows"); }
+void MI355XBackend::adam_step(float*, const float*, float*, float*, size_t, float, float, float, float, float, float) {
+    off_path("adam_step");
+}
+void MI355XBackend::dropout_forward(const float*, float*, float*, size_t, float, float, uint64_t, uint64_t) {
+    off_path("dropout_forward");
+}
+void MI355XBackend::bce_with_logits(const float*, const float*, float*, size_t) { off_path("bce_with_logits"); }
+void MI355XBackend::bce_with_logits_grad(const float*, const float*, float*, size_t, float) {
+    off_path("bce_with_logits_grad");
+}
+void MI355XBackend::layer_norm_forward(const float*, const float*, const float*, float*, float*, float*, size_t, size_t,
+                                       float) {
+    off_path("layer_norm_forward");
+}
+void MI355XBackend::layer_norm_backward(const float*, const float*, const float*, const float*, float*, size_t, size_t) {
+    off_path("layer_norm_backward");
+}
+void MI355XBackend::rms_norm_backward(const float*, const float*, const float*, const float*, float*, float*, size_t,
+                                      size_t) {
+    off_path("rms_norm_backward");
+}
+void MI355XBackend::scatter_add_rows(const float*, const float*, float*, size_t, size_t) {
+    off_path("scatter_add_rows");
+}
+void MI355XBackend::tanh_gaussian_forward(const float*, const float*, const float*, float*, float*, float*, size_t,
+                                          size_t, float, double) {
+    off_path("tanh_gaussian_forward");
+}
+void MI355XBackend::tanh_gaussian_backward(const float*, const float*, const float*, const float*, const float*,
+                                           float*, float*, size_t, float) {
+    off_path("tanh_gaussian_backward");
+}
+void MI355XBackend::logic_pointwise(LogicOp, int, const float*, const float*, const float*, const float*, float*,
+                                    float*, size_t, float) {
+    off_path("logic_pointwise");
+}
+void MI355XBackend::aggregator_forward(const float*, float*, float*, size_t, size_t, float) {
+    off_path("aggregator_forward");
+}
+void MI355XBackend::aggregator_backward(const float*, const float*, const float*, float*, size_t, size_t, float) {
+    off_path("aggregator_backward");
+}
+void MI355XBackend::aggregator_lrp(const float*, const float*, const float*, float*, size_t, size_t, float, float) {
+    off_path("aggregator_lrp");
+}
+void MI355XBackend::im2col(const float*, float*, size_t, size_t, size_t, size_t, const ConvGeometry&) {
+    off_path("im2col");
+}
+void MI355XBackend::col2im_add(const float*, float*, size_t, size_t, size_t, size_t, const ConvGeometry&) {
+    off_path("col2im_add");
+}
+void MI355XBackend::add_channel_vector(const float*, const float*, float*, size_t, size_t, size_t) {
+    off_path("add_channel_vector");
+}
+void MI355XBackend::lrp_conv(const float*, const float*, const float*, const float*, float*, size_t, size_t, size_t,
+                             size_t, float) {
+    off_path("lrp_conv");
+}
+void MI355XBackend::max_pool_forward(const float*, float*, float*, size_t, size_t, size_t, size_t, size_t, size_t,
+                                     size_t, size_t, size_t) {
+    off_path("max_pool_forward");
+}
+void MI355XBackend::max_unpool(const float*, const float*, float*, size_t, size_t, size_t, size_t, size_t, size_t,
+                               size_t, size_t, size_t) {
+    off_path("max_unpool");
+}
+void MI355XBackend::avg_pool_forward(const float*, float*, size_t, size_t, size_t, size_t, size_t) {
+    off_path("avg_pool_forward");
+}
+void MI355XBackend::avg_pool_backward(const float*, float*, size_t, size_t, size_t, size_t, size_t) {
+    off_path("avg_pool_backward");
+}
+void MI355XBackend::lrp_avg_pool(const float*, const float*, float*, size_t, size_t, size_t, size_t, size_t, float) {
+    off_path("lrp_avg_pool");
+}
+void MI355XBackend::batch_norm_forward(const float*, const float*, const float*, float*, float*, float*, size_t, size_t,
+                                       size_t, float) {
+    off_path("batch_norm_forward");
+}
+void MI355XBackend::batch_norm_backward(const float*, const float*, const float*, const float*, float*, float*, float*,
+                                        size_t, size_t, size_t) {
+    off_path("batch_norm_backward");
+}
+void MI355XBackend::batch_norm_update_running(const float*, float*, float*, size_t, size_t, size_t, float) {
+    off_path("batch_norm_update_running");
+}
+void MI355XBackend::batch_norm_eval_forward(const float*, const float*, const float*, const float*, const float*,
+                                            float*, float*, float*, size_t, size_t, size_t, float) {
+    off_path("batch_norm_eval_forward");
+}
+void MI355XBackend::batch_norm_eval_backward(const float*, const float*, const float*, const float*, float*, float*,
+                                             float*, size_t, size_t, size_t) {
+    off_path("batch_norm_eval_backward");
+}
+void MI355XBackend::group_norm_forward(const float*, const float*, const float*, float*, float*, float*, size_t, size_t,
+                                       size_t, size_t, float) {
+    off_path("group_norm_forward");
+}
+void MI355XBackend::group_norm_backward(const float*, const float*, const float*, const float*, float*, float*, float*,
+                                        size_t, size_t, size_t, size_t) {
+    off_path("group_norm_backward");
+}
+void MI355XBackend::recurrent_cell(RecurrentCellOp, const RecurrentCellArgs&, size_t) { off_path("recurrent_cell"); }
+void MI355XBackend::gru_lrp_hprev(const float*, const float*, const float*, const float*, const float*, float*, size_t,
+                                  size_t, float) {
+    off_path("gru_lrp_hprev");
+}
+void MI355XBackend::ssm_pass(SsmPassOp, const SsmPassArgs&) { off_path("ssm_pass"); }
+void MI355XBackend::rl_rows(RlRowOp, const RlRowArgs&) { off_path("rl_rows"); }
+void MI355XBackend::top_k_rows(const float*, float*, float*, size_t, size_t, size_t, bool) { off_path("top_k_rows"); }
+
+}  // namespace pulsatrix

@@ -1,0 +1,270 @@
+// LinearModule, RMSNormModule, EmbeddingModule and TiedLMHeadModule on MI355XBackend.
+#include <cmath>
+#include <stdexcept>
+#include <string>
+
+#include "pulsatrix/embedding_module.hpp"
+#include "pulsatrix/linear_module.hpp"
+#include "pulsatrix/rms_norm_module.hpp"
+#include "pulsatrix/tied_lm_head_module.hpp"
+
+namespace pulsatrix {
+
+using detail::gemm_desc;
+using detail::mat;
+
+void require_epsilon_rule(const LRPRuleConfig& config, const char* module_name) {
+    if (config.rule != LRPRule::Epsilon)
+        throw std::invalid_argument(std::string(module_name) +
+                                    "::propagate_relevance: the MI355X path implements the epsilon rule only");
+}
+
+namespace detail {
+
+/** @brief A fresh tensor holding a copy of n device floats (the reference returns new tensors). */
+Tensor copy_out(MI355XBackend* be, const float* src, Shape shape) {
+    Tensor t = Tensor::uninitialized(std::move(shape), be);
+    if (t.numel() > 0) be->copy(t.data(), src, static_cast<size_t>(t.numel()) * sizeof(float), CopyDirection::DeviceToDevice);
+    return t;
+}
+
+/** @brief Copies a caller's tensor into a module buffer (the module keeps its input for relevance). */
+const float* keep_input(MI355XBackend* be, DevBuf& buf, const Tensor& t) {
+    float* p = buf.ensure(be, t.numel());
+    be->copy(p, t.data(), static_cast<size_t>(t.numel()) * sizeof(float), CopyDirection::DeviceToDevice);
+    return p;
+}
+
+}  // namespace detail
+
+// ---- LinearModule (src/linear_module.cpp) ----------------------------------------------------------
+
+LinearModule::LinearModule(int64_t in_features, int64_t out_features, DeviceBackend* backend, bool use_bias)
+    : in_(in_features),
+      out_(out_features),
+      use_bias_(use_bias),
+      be_(detail::require_mi355x(backend, "LinearModule")),
+      weight_(Shape({in_features, out_features}), backend),
+      bias_(Shape({out_features}), backend) {
+    if (in_features <= 0 || out_features <= 0)
+        throw std::invalid_argument("LinearModule: in_features and out_features must be positive");
+}
+
+void LinearModule::set_weight(const std::vector<float>& values) {
+    weight_ = Tensor(weight_.shape(), be_, values);
+    ++version_;
+}
+
+void LinearModule::set_bias(const std::vector<float>& values) {
+    if (!use_bias_) throw std::logic_error("LinearModule::set_bias: this layer was built without a bias");
+    bias_ = Tensor(bias_.shape(), be_, values);
+    ++version_;
+}
+
+const float* LinearModule::run_forward(const float* x, int64_t rows) {
+    x_ = x;
+    rows_ = rows;
+    float* z = z_.ensure(be_, rows * out_);
+    pxk_gemm_desc d = gemm_desc(rows, out_, in_);
+    d.a = mat(x, in_);
+    d.b = mat(weight_.data(), out_);
+    d.c = mat(z, out_);
+    d.epilogue = PXK_EPI_STORE;
+    float* y = z;
+    if (use_bias_) {
+        y = y_.ensure(be_, rows * out_);
+        d.epilogue = PXK_EPI_STORE_BIAS;
+        d.c2 = mat(y, out_);
+        d.e_bias = mat(bias_.data(), 0);
+    }
+    be_->run_gemm(d);
+    return y;
+}
+
+const float* LinearModule::run_relevance(const float* r, const LRPRuleConfig& config, const float* add) {
+    require_epsilon_rule(config, "LinearModule");
+    if (x_ == nullptr) throw std::logic_error("LinearModule::propagate_relevance: called before any forward()");
+    float* out = r_in_.ensure(be_, rows_ * in_);
+    pxk_gemm_desc d = gemm_desc(rows_, in_, out_);
+    d.trans_b = 1;
+    d.prologue = PXK_PRO_DIV_STAB;
+    d.epilogue = PXK_EPI_MUL_X;
+    d.eps = config.epsilon;
+    d.a = mat(r, out_);
+    d.z = mat(z_.data(), out_);
+    if (const float* b = detail::rule_bias(bias_.data(), use_bias_, config.epsilon_bias_in_denominator))
+        d.z_bias = mat(b, 0);
+    d.b = mat(weight_.data(), out_);
+    d.c = mat(out, in_);
+    d.x = mat(x_, in_);
+    if (add) d.y = mat(add, in_);
+    be_->run_gemm(d);
+    return out;
+}
+
+Tensor LinearModule::forward_impl(const Tensor& input) {
+    if (input.rank() != 2 || input.shape().dim(1) != in_)
+        throw std::invalid_argument("LinearModule::forward: input must be rank-2 (N, in_features)");
+    const int64_t n = input.shape().dim(0);
+    const float* y = run_forward(detail::keep_input(be_, x_copy_, input), n);
+    return detail::copy_out(be_, y, Shape({n, out_}));
+}
+
+Tensor LinearModule::propagate_relevance(const Tensor& relevance_out, const LRPRuleConfig& config) {
+    require_device(relevance_out, DeviceType::Hip, "LinearModule::propagate_relevance");
+    if (x_ == nullptr) throw std::logic_error("LinearModule::propagate_relevance: called before any forward()");
+    if (relevance_out.rank() != 2 || relevance_out.shape().dim(0) != rows_ || relevance_out.shape().dim(1) != out_)
+        throw std::invalid_argument(
+            "LinearModule::propagate_relevance: relevance_out must be rank-2 (N, out_features) matching the cached "
+            "batch size");
+    return detail::copy_out(be_, run_relevance(relevance_out.data(), config), Shape({rows_, in_}));
+}
+
+// ---- RMSNormModule (src/rms_norm_module.cpp) -----------------------------------------------------
+
+RMSNormModule::RMSNormModule(int64_t num_features, DeviceBackend* backend, DeviceType, float eps)
+    : d_(num_features),
+      eps_(eps),
+      be_(detail::require_mi355x(backend, "RMSNormModule")),
+      gamma_(Shape({num_features > 0 ? num_features : 1}), backend) {
+    if (num_features <= 0) throw std::invalid_argument("RMSNormModule: num_features must be positive");
+}
+
+void RMSNormModule::set_gamma(const std::vector<float>& values) { gamma_ = Tensor(gamma_.shape(), be_, values); }
+
+const float* RMSNormModule::run_forward(const float* x, int64_t rows) {
+    rows_ = rows;
+    float* out = out_.ensure(be_, rows * d_);
+    float* rms = rms_.ensure(be_, rows);
+    MI355XBackend::check(pxk_rms_norm_forward(x, gamma_.data(), out, rms, rows, d_, eps_, be_->stream()),
+                         "RMSNormModule::forward");
+    return out;
+}
+
+Tensor RMSNormModule::forward_impl(const Tensor& input) {
+    if (input.rank() != 2 || input.shape().dim(1) != d_)
+        throw std::invalid_argument("RMSNormModule::forward: input must be rank-2 (N, num_features)");
+    const int64_t n = input.shape().dim(0);
+    return detail::copy_out(be_, run_forward(input.data(), n), Shape({n, d_}));
+}
+
+Tensor RMSNormModule::propagate_relevance(const Tensor& relevance_out, const LRPRuleConfig&) {
+    if (rows_ == 0) throw std::logic_error("RMSNormModule::propagate_relevance: called before any forward()");
+    if (relevance_out.numel() != rows_ * d_)
+        throw std::invalid_argument(
+            "RMSNormModule::propagate_relevance: relevance_out size must match the cached forward shape");
+    return Tensor(relevance_out);  // the identity rule
+}
+
+// ---- EmbeddingModule (src/embedding_module.cpp) ----------------------------------------------------
+
+EmbeddingModule::EmbeddingModule(int64_t num_embeddings, int64_t embedding_dim, DeviceBackend* backend)
+    : V_(num_embeddings),
+      d_(embedding_dim),
+      be_(detail::require_mi355x(backend, "EmbeddingModule")),
+      weight_(Shape({num_embeddings, embedding_dim}), backend) {
+    if (num_embeddings <= 0 || embedding_dim <= 0)
+        throw std::invalid_argument("EmbeddingModule: num_embeddings and embedding_dim must be positive");
+}
+
+void EmbeddingModule::set_weight(const std::vector<float>& values) { weight_ = Tensor(weight_.shape(), be_, values); }
+
+const float* EmbeddingModule::run_forward_device(const float* ids, int64_t n, int64_t l) {
+    const int64_t count = n * l;
+    last_shape_ = Shape({n, l});
+    float* out = out_.ensure(be_, count * d_);
+    MI355XBackend::check(pxk_gather_rows(weight_.data(), ids, out, count, d_, be_->stream()), "EmbeddingModule::forward");
+    return out;
+}
+
+Tensor EmbeddingModule::forward_impl(const Tensor& input) {
+    if (input.rank() != 2) throw std::invalid_argument("EmbeddingModule::forward: input must be rank-2 (N, L)");
+    const int64_t n = input.shape().dim(0), l = input.shape().dim(1), count = n * l;
+    // Host-side validation, as the reference does it (embedding_module.cpp:48-59).
+    std::vector<float> raw = input.to_host_vector();
+    for (float& v : raw) {
+        const auto idx = static_cast<int64_t>(std::llround(static_cast<double>(v)));
+        if (idx < 0 || idx >= V_)
+            throw std::invalid_argument("EmbeddingModule::forward: index out of range [0, num_embeddings)");
+        v = static_cast<float>(idx);
+    }
+    float* ids = ids_.ensure(be_, count);
+    be_->copy(ids, raw.data(), raw.size() * sizeof(float), CopyDirection::HostToDevice);
+    return detail::copy_out(be_, run_forward_device(ids, n, l), Shape({n, l, d_}));
+}
+
+void EmbeddingModule::token_relevance(const float* relevance, int64_t count, float* out) {
+    MI355XBackend::check(pxk_row_sums(relevance, out, count, d_, be_->stream()),
+                         "EmbeddingModule::propagate_relevance");
+}
+
+Tensor EmbeddingModule::propagate_relevance(const Tensor& relevance_out, const LRPRuleConfig&) {
+    if (last_shape_.rank() != 2) throw std::logic_error("EmbeddingModule::propagate_relevance: called before any forward()");
+    const int64_t n = last_shape_.dim(0), l = last_shape_.dim(1);
+    if (relevance_out.numel() != n * l * d_)
+        throw std::invalid_argument(
+            "EmbeddingModule::propagate_relevance: relevance_out must be (N, L, embedding_dim) matching the cached "
+            "forward shape");
+    Tensor out = Tensor::uninitialized(last_shape_, be_);
+    token_relevance(relevance_out.data(), n * l, out.data());
+    return out;
+}
+
+// ---- TiedLMHeadModule (src/tied_lm_head_module.cpp) -------------------------------------------------
+
+TiedLMHeadModule::TiedLMHeadModule(EmbeddingModule& embedding, DeviceBackend* backend)
+    : embedding_(embedding), be_(detail::require_mi355x(backend, "TiedLMHeadModule")) {}
+
+const float* TiedLMHeadModule::run_forward(const float* x, int64_t rows) {
+    const int64_t V = embedding_.num_embeddings(), D = embedding_.embedding_dim();
+    x_ = x;
+    rows_ = rows;
+    float* logits = logits_.ensure(be_, rows * V);
+    pxk_gemm_desc d = gemm_desc(rows, V, D);
+    d.trans_b = 1;  // E (V, D) read transposed in place
+    d.a = mat(x, D);
+    d.b = mat(embedding_.weight().data(), D);
+    d.c = mat(logits, V);
+    be_->run_gemm(d);
+    return logits;
+}
+
+const float* TiedLMHeadModule::run_relevance(const float* relevance_out, const LRPRuleConfig& config) {
+    require_epsilon_rule(config, "TiedLMHeadModule");
+    if (x_ == nullptr) throw std::logic_error("TiedLMHeadModule::propagate_relevance: called before any forward()");
+    const int64_t V = embedding_.num_embeddings(), D = embedding_.embedding_dim();
+    float* out = r_in_.ensure(be_, rows_ * D);
+    // z = logits + 0 bias; g = R / stab(z); r_in = x * (g E): K = V, split-K across the chip.
+    pxk_gemm_desc d = gemm_desc(rows_, D, V);
+    d.prologue = PXK_PRO_DIV_STAB;
+    d.epilogue = PXK_EPI_MUL_X;
+    d.eps = config.epsilon;
+    d.a = mat(relevance_out, V);
+    d.z = mat(logits_.data(), V);
+    d.b = mat(embedding_.weight().data(), D);
+    d.c = mat(out, D);
+    d.x = mat(x_, D);
+    be_->run_gemm(d);
+    return out;
+}
+
+Tensor TiedLMHeadModule::forward_impl(const Tensor& input) {
+    const int64_t D = embedding_.embedding_dim(), V = embedding_.num_embeddings();
+    if (input.rank() < 2 || input.shape().dim(static_cast<size_t>(input.rank() - 1)) != D)
+        throw std::invalid_argument("TiedLMHeadModule::forward: input must be rank >= 2 with shape (..., d_model)");
+    const int64_t m = input.numel() / D;
+    std::vector<int64_t> dims = input.shape().dims();
+    dims.back() = V;
+    last_in_shape_ = input.shape();
+    last_out_shape_ = Shape(dims);
+    return detail::copy_out(be_, run_forward(detail::keep_input(be_, x_copy_, input), m), last_out_shape_);
+}
+
+Tensor TiedLMHeadModule::propagate_relevance(const Tensor& relevance_out, const LRPRuleConfig& config) {
+    if (x_ == nullptr) throw std::logic_error("TiedLMHeadModule::propagate_relevance: called before any forward()");
+    if (relevance_out.shape() != last_out_shape_)
+        throw std::invalid_argument("TiedLMHeadModule::propagate_relevance: relevance_out must match the cached output shape");
+    return detail::copy_out(be_, run_relevance(relevance_out.data(), config), last_in_shape_);
+}
+
+}  // namespace pulsatrix

@@ -1,0 +1,351 @@
+// elementwise.hip -- memory-bound elementwise kernels (include/pxk.h). Grid-stride loops over
+// 128-bit (float4) accesses when every operand is 16-byte aligned, scalar otherwise; each element's
+// arithmetic is the reference's expression for that element (src/cpu_backend.cpp, lrp_math.hpp).
+#include <cstdarg>
+#include <cstring>
+#include <string>
+
+#include "common.hpp"
+
+namespace pxk {
+
+namespace {
+thread_local std::string g_error;
+}
+
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_error = buf;
+    return code;
+}
+
+int launched(const char* what) {
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(PXK_ERR_LAUNCH, "%s: %s", what, hipGetErrorString(e));
+    return PXK_OK;
+}
+
+namespace {
+
+constexpr int kThreads = 256;
+
+__device__ __forceinline__ float sigmoidf_(float z) { return 1.0f / (1.0f + expf(-z)); }  // cpu_backend.cpp:29
+
+__device__ __forceinline__ float apply_op(int op, float x) {
+    switch (op) {
+        case 0: return fmaxf(x, 0.0f);
+        case 1: return -x;
+        case 2: return tanhf(x);
+        case 3: return sigmoidf_(x);
+        case 4: return x * sigmoidf_(x);
+        case 5: return expf(x);
+        case 6: {  // pointwise_math.hpp:32-36
+            const float kBeta = 0.7978845608028654f, kKappa = 0.044715f;
+            return 0.5f * x * (1.0f + tanhf(kBeta * (x + kKappa * x * x * x)));
+        }
+        default: {  // 7: exact GELU, pointwise_math.hpp:50-53
+            const float kInvSqrt2 = 0.7071067811865476f;
+            return 0.5f * x * (1.0f + erff(x * kInvSqrt2));
+        }
+    }
+}
+
+// Pointer arrays travel by value inside a small struct (kernel arguments, no device allocation).
+template <int NIN, int NOUT>
+struct Ptrs {
+    const float* in[NIN > 0 ? NIN : 1];
+    float* out[NOUT];
+};
+
+template <typename F, int NIN, int NOUT, bool VEC>
+__global__ void __launch_bounds__(kThreads) map_kernel_p(F f, Ptrs<NIN, NOUT> p, int64_t n) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
+    if constexpr (VEC) {
+        typedef float f4 __attribute__((ext_vector_type(4)));
+        const int64_t n4 = n / 4;
+        for (int64_t i = blockIdx.x * kThreads + threadIdx.x; i < n4; i += stride) {
+            f4 a[NIN > 0 ? NIN : 1];
+#pragma unroll
+            for (int j = 0; j < NIN; ++j) a[j] = reinterpret_cast<const f4*>(p.in[j])[i];
+            f4 o[NOUT];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                float x[NIN > 0 ? NIN : 1], y[NOUT];
+#pragma unroll
+                for (int j = 0; j < NIN; ++j) x[j] = a[j][e];
+                f(x, y);
+#pragma unroll
+                for (int j = 0; j < NOUT; ++j) o[j][e] = y[j];
+            }
+#pragma unroll
+            for (int j = 0; j < NOUT; ++j) reinterpret_cast<f4*>(p.out[j])[i] = o[j];
+        }
+        for (int64_t i = n4 * 4 + blockIdx.x * kThreads + threadIdx.x; i < n; i += stride) {
+            float x[NIN > 0 ? NIN : 1], y[NOUT];
+#pragma unroll
+            for (int j = 0; j < NIN; ++j) x[j] = p.in[j][i];
+            f(x, y);
+#pragma unroll
+            for (int j = 0; j < NOUT; ++j) p.out[j][i] = y[j];
+        }
+    } else {
+        for (int64_t i = blockIdx.x * kThreads + threadIdx.x; i < n; i += stride) {
+            float x[NIN > 0 ? NIN : 1], y[NOUT];
+#pragma unroll
+            for (int j = 0; j < NIN; ++j) x[j] = p.in[j][i];
+            f(x, y);
+#pragma unroll
+            for (int j = 0; j < NOUT; ++j) p.out[j][i] = y[j];
+        }
+    }
+}
+
+template <int NIN, int NOUT, typename F>
+int run_map(const char* what, F f, Ptrs<NIN, NOUT> p, int64_t n, void* stream) {
+    if (n < 0) return fail(PXK_ERR_INVALID, "%s: negative size", what);
+    if (n == 0) return PXK_OK;
+    bool vec = true;
+    for (int j = 0; j < NIN; ++j) {
+        if (p.in[j] == nullptr) return fail(PXK_ERR_INVALID, "%s: null input", what);
+        vec = vec && aligned16(p.in[j]);
+    }
+    for (int j = 0; j < NOUT; ++j) {
+        if (p.out[j] == nullptr) return fail(PXK_ERR_INVALID, "%s: null output", what);
+        vec = vec && aligned16(p.out[j]);
+    }
+    const unsigned grid = grid_for(vec ? cdiv(n, 4) : n, kThreads);
+    if (vec)
+        hipLaunchKernelGGL((map_kernel_p<F, NIN, NOUT, true>), dim3(grid), dim3(kThreads), 0, S(stream), f, p, n);
+    else
+        hipLaunchKernelGGL((map_kernel_p<F, NIN, NOUT, false>), dim3(grid), dim3(kThreads), 0, S(stream), f, p, n);
+    return launched(what);
+}
+
+struct FillF {
+    float v;
+    __device__ void operator()(const float*, float* y) const { y[0] = v; }
+};
+struct OpF {
+    int op;
+    __device__ void operator()(const float* x, float* y) const { y[0] = apply_op(op, x[0]); }
+};
+struct AddF {
+    __device__ void operator()(const float* x, float* y) const { y[0] = x[0] + x[1]; }
+};
+struct MulF {
+    __device__ void operator()(const float* x, float* y) const { y[0] = x[0] * x[1]; }
+};
+struct ScaleF {
+    float a;
+    __device__ void operator()(const float* x, float* y) const { y[0] = a * x[0]; }
+};
+struct AxpbyF {
+    float a, b;
+    __device__ void operator()(const float* x, float* y) const { y[0] = a * x[0] + b * x[1]; }
+};
+struct ResidualSplitF {  // lrp_math.hpp:33-38
+    float eps;
+    __device__ void operator()(const float* x, float* y) const {
+        const float s = x[0] + x[1];
+        const float denom = stab(s, eps);
+        y[0] = (x[0] / denom) * x[2];
+        y[1] = (x[1] / denom) * x[2];
+    }
+};
+struct BilinearF {  // lrp_math.hpp:41-45
+    float eps;
+    __device__ void operator()(const float* x, float* y) const {
+        const float c = x[0] * x[1];
+        const float denom = 2.0f * c + eps * ((c >= 0.0f) ? 1.0f : -1.0f);
+        y[0] = (x[0] * x[1] / denom) * x[2];
+    }
+};
+struct BilinearScaleF {  // lrp_math.hpp:57-61
+    float eps;
+    __device__ void operator()(const float* x, float* y) const {
+        const float o = x[1];
+        y[0] = x[0] / (2.0f * o + eps * ((o >= 0.0f) ? 1.0f : -1.0f));
+    }
+};
+struct DivideF {  // lrp_math.hpp:312-315, gate mode None
+    float eps;
+    __device__ void operator()(const float* x, float* y) const { y[0] = x[0] / stab(x[1], eps); }
+};
+struct DivideGatedF {
+    float eps;
+    int mode;
+    __device__ void operator()(const float* x, float* y) const {
+        const bool pass = (mode == 1 && x[2] > 0.0f) || (mode == 2 && x[2] < 0.0f);
+        y[0] = pass ? x[0] / stab(x[1], eps) : 0.0f;
+    }
+};
+
+// add_row_vector: out[i][j] = in[i][j] + row[j].
+__global__ void __launch_bounds__(kThreads) add_row_kernel(const float* in, const float* row, float* out, int64_t rows,
+                                                           int64_t cols) {
+    const int64_t n = rows * cols, stride = static_cast<int64_t>(gridDim.x) * kThreads;
+    for (int64_t i = blockIdx.x * kThreads + threadIdx.x; i < n; i += stride) out[i] = in[i] + row[i % cols];
+}
+
+// SwiGLU gate over a [gate | up] row block (swiglu_module.cpp:80-88).
+__global__ void __launch_bounds__(kThreads) swiglu_kernel(const float* gu, int64_t ld, float* gate_post, float* hidden,
+                                                          int64_t rows, int64_t f) {
+    const int64_t n = rows * f, stride = static_cast<int64_t>(gridDim.x) * kThreads;
+    for (int64_t i = blockIdx.x * kThreads + threadIdx.x; i < n; i += stride) {
+        const int64_t r = i / f, c = i % f;
+        const float x = gu[r * ld + c];
+        const float gp = x * sigmoidf_(x);
+        gate_post[i] = gp;
+        hidden[i] = gp * gu[r * ld + f + c];
+    }
+}
+
+__global__ void __launch_bounds__(kThreads) copy2d_kernel(float* dst, int64_t ds, const float* src, int64_t ss,
+                                                          int64_t rows, int64_t cols) {
+    const int64_t n = rows * cols, stride = static_cast<int64_t>(gridDim.x) * kThreads;
+    for (int64_t i = blockIdx.x * kThreads + threadIdx.x; i < n; i += stride) {
+        const int64_t r = i / cols, c = i % cols;
+        dst[r * ds + c] = src[r * ss + c];
+    }
+}
+
+// out[j] += in[i][j] for i in order: one thread per column keeps the reference's order.
+__global__ void __launch_bounds__(kThreads) accumulate_rows_kernel(const float* in, float* out, int64_t rows,
+                                                                   int64_t cols) {
+    const int64_t j = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+    if (j >= cols) return;
+    float acc = out[j];
+    for (int64_t r = 0; r < rows; ++r) acc += in[r * cols + j];
+    out[j] = acc;
+}
+
+__global__ void __launch_bounds__(kThreads) column_sums_kernel(const float* in, float* out, int64_t rows, int64_t cols,
+                                                               float beta) {
+    const int64_t j = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+    if (j >= cols) return;
+    float acc = 0.0f;
+    for (int64_t r = 0; r < rows; ++r) acc += in[r * cols + j];
+    out[j] = (beta == 0.0f) ? acc : beta * out[j] + acc;
+}
+
+__global__ void __launch_bounds__(kThreads) gather_kernel(const float* table, const float* idx, float* out,
+                                                          int64_t count, int64_t dim) {
+    const int64_t n = count * dim, stride = static_cast<int64_t>(gridDim.x) * kThreads;
+    for (int64_t i = blockIdx.x * kThreads + threadIdx.x; i < n; i += stride) {
+        const int64_t r = i / dim, c = i % dim;
+        out[i] = table[static_cast<int64_t>(idx[r]) * dim + c];
+    }
+}
+
+}  // namespace
+}  // namespace pxk
+
+using namespace pxk;
+
+extern "C" {
+
+const char* pxk_last_error(void) { return g_error.c_str(); }
+
+const char* pxk_version(void) { return "pxk_gfx950 1.0 (fp32 MFMA 16x16x4, wave64)"; }
+
+int pxk_fill(float* ptr, float value, int64_t n, void* stream) {
+    Ptrs<0, 1> p{{nullptr}, {ptr}};
+    return run_map<0, 1>("pxk_fill", FillF{value}, p, n, stream);
+}
+
+int pxk_elementwise(int op, const float* in, float* out, int64_t n, void* stream) {
+    if (op < 0 || op > 7) return fail(PXK_ERR_INVALID, "pxk_elementwise: unknown op %d", op);
+    return run_map<1, 1>("pxk_elementwise", OpF{op}, Ptrs<1, 1>{{in}, {out}}, n, stream);
+}
+
+int pxk_add(const float* a, const float* b, float* out, int64_t n, void* stream) {
+    return run_map<2, 1>("pxk_add", AddF{}, Ptrs<2, 1>{{a, b}, {out}}, n, stream);
+}
+
+int pxk_mul(const float* a, const float* b, float* out, int64_t n, void* stream) {
+    return run_map<2, 1>("pxk_mul", MulF{}, Ptrs<2, 1>{{a, b}, {out}}, n, stream);
+}
+
+int pxk_axpby(float alpha, const float* x, float beta, const float* y, float* out, int64_t n, void* stream) {
+    if (beta == 0.0f)  // y is not read (device_backend.hpp:433-435)
+        return run_map<1, 1>("pxk_axpby", ScaleF{alpha}, Ptrs<1, 1>{{x}, {out}}, n, stream);
+    return run_map<2, 1>("pxk_axpby", AxpbyF{alpha, beta}, Ptrs<2, 1>{{x, y}, {out}}, n, stream);
+}
+
+int pxk_add_row_vector(const float* in, const float* row, float* out, int64_t rows, int64_t cols, void* stream) {
+    if (rows < 0 || cols < 0) return fail(PXK_ERR_INVALID, "pxk_add_row_vector: negative size");
+    if (rows * cols == 0) return PXK_OK;
+    hipLaunchKernelGGL(add_row_kernel, dim3(grid_for(rows * cols, kThreads)), dim3(kThreads), 0, S(stream), in, row,
+                       out, rows, cols);
+    return launched("pxk_add_row_vector");
+}
+
+int pxk_lrp_residual_split(const float* a, const float* b, const float* r, float* r_a, float* r_b, int64_t n,
+                           float eps, void* stream) {
+    return run_map<3, 2>("pxk_lrp_residual_split", ResidualSplitF{eps}, Ptrs<3, 2>{{a, b, r}, {r_a, r_b}}, n, stream);
+}
+
+int pxk_lrp_bilinear_elementwise(const float* a, const float* b, const float* r, float* r_out, int64_t n, float eps,
+                                 void* stream) {
+    return run_map<3, 1>("pxk_lrp_bilinear_elementwise", BilinearF{eps}, Ptrs<3, 1>{{a, b, r}, {r_out}}, n, stream);
+}
+
+int pxk_lrp_bilinear_scale(const float* r, const float* o, float* s, int64_t n, float eps, void* stream) {
+    return run_map<2, 1>("pxk_lrp_bilinear_scale", BilinearScaleF{eps}, Ptrs<2, 1>{{r, o}, {s}}, n, stream);
+}
+
+int pxk_lrp_stabilized_divide(const float* r, const float* denom, const float* gate, float* out, int64_t n, float eps,
+                              int gate_mode, void* stream) {
+    if (gate_mode < 0 || gate_mode > 2) return fail(PXK_ERR_INVALID, "pxk_lrp_stabilized_divide: bad gate mode");
+    if (gate_mode == 0)
+        return run_map<2, 1>("pxk_lrp_stabilized_divide", DivideF{eps}, Ptrs<2, 1>{{r, denom}, {out}}, n, stream);
+    return run_map<3, 1>("pxk_lrp_stabilized_divide", DivideGatedF{eps, gate_mode}, Ptrs<3, 1>{{r, denom, gate}, {out}},
+                         n, stream);
+}
+
+int pxk_swiglu_forward(const float* gu, int64_t ld, float* gate_post, float* hidden, int64_t rows, int64_t f,
+                       void* stream) {
+    if (rows < 0 || f < 0 || ld < 2 * f) return fail(PXK_ERR_INVALID, "pxk_swiglu_forward: bad sizes");
+    if (rows * f == 0) return PXK_OK;
+    hipLaunchKernelGGL(swiglu_kernel, dim3(grid_for(rows * f, kThreads)), dim3(kThreads), 0, S(stream), gu, ld,
+                       gate_post, hidden, rows, f);
+    return launched("pxk_swiglu_forward");
+}
+
+int pxk_copy_2d(float* dst, int64_t ds, const float* src, int64_t ss, int64_t rows, int64_t cols, void* stream) {
+    if (rows < 0 || cols < 0) return fail(PXK_ERR_INVALID, "pxk_copy_2d: negative size");
+    if (rows * cols == 0) return PXK_OK;
+    hipLaunchKernelGGL(copy2d_kernel, dim3(grid_for(rows * cols, kThreads)), dim3(kThreads), 0, S(stream), dst, ds, src,
+                       ss, rows, cols);
+    return launched("pxk_copy_2d");
+}
+
+int pxk_accumulate_rows(const float* in, float* out, int64_t rows, int64_t cols, void* stream) {
+    if (rows < 0 || cols < 0) return fail(PXK_ERR_INVALID, "pxk_accumulate_rows: negative size");
+    if (cols == 0) return PXK_OK;
+    hipLaunchKernelGGL(accumulate_rows_kernel, dim3(static_cast<unsigned>(cdiv(cols, kThreads))), dim3(kThreads), 0,
+                       S(stream), in, out, rows, cols);
+    return launched("pxk_accumulate_rows");
+}
+
+int pxk_column_sums(const float* in, float* out, int64_t rows, int64_t cols, float beta, void* stream) {
+    if (rows < 0 || cols < 0) return fail(PXK_ERR_INVALID, "pxk_column_sums: negative size");
+    if (cols == 0) return PXK_OK;
+    hipLaunchKernelGGL(column_sums_kernel, dim3(static_cast<unsigned>(cdiv(cols, kThreads))), dim3(kThreads), 0,
+                       S(stream), in, out, rows, cols, beta);
+    return launched("pxk_column_sums");
+}
+
+int pxk_gather_rows(const float* table, const float* indices, float* out, int64_t count, int64_t dim, void* stream) {
+    if (count < 0 || dim < 0) return fail(PXK_ERR_INVALID, "pxk_gather_rows: negative size");
+    if (count * dim == 0) return PXK_OK;
+    hipLaunchKernelGGL(gather_kernel, dim3(grid_for(count * dim, kThreads)), dim3(kThreads), 0, S(stream), table,
+                       indices, out, count, dim);
+    return launched("pxk_gather_rows");
+}
+
+}  // extern "C"

@@ -1,0 +1,459 @@
+// rows.hip -- row-wise and attention kernels for gfx950 (include/pxk.h).
+//
+// Row reductions run one wave64 per row (four rows per 256-thread workgroup) with lane-strided
+// loads and a cross-lane shuffle tree, so each row's sum or max is a fixed-order reduction (the
+// same every run). The reference's HIP backend ran these one thread per row (gpu_kernels.cuh:
+// 315-334, 609-615), leaving almost all of a 256-CU device idle.
+#include <algorithm>
+#include <cstring>
+
+#include "common.hpp"
+
+namespace pxk {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kRowsPerBlock = kThreads / kWave;
+
+__device__ __forceinline__ int64_t row_id() {
+    return static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + (threadIdx.x >> 6);
+}
+__device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
+
+// ---- RMSNorm (row_math.hpp:59-71) -------------------------------------------------------------
+__global__ void __launch_bounds__(kThreads) rms_norm_kernel(const float* in, const float* gamma, float* out,
+                                                            float* row_rms, int64_t rows, int64_t cols, float eps) {
+    const int64_t r = row_id();
+    if (r >= rows) return;
+    const int lane = lane_id();
+    const float* x = in + r * cols;
+    float ss = 0.0f;
+    for (int64_t i = lane; i < cols; i += kWave) ss += x[i] * x[i];
+    ss = wave_sum(ss);
+    const float rms = sqrtf(ss / static_cast<float>(cols) + eps);
+    if (row_rms && lane == 0) row_rms[r] = rms;
+    float* o = out + r * cols;
+    for (int64_t i = lane; i < cols; i += kWave) o[i] = gamma[i] * x[i] / rms;
+}
+
+// ---- softmax_rows (cpu_backend.cpp:292-310) ---------------------------------------------------
+__global__ void __launch_bounds__(kThreads) softmax_kernel(const float* in, float* out, int64_t rows, int64_t cols) {
+    const int64_t r = row_id();
+    if (r >= rows) return;
+    const int lane = lane_id();
+    const float* x = in + r * cols;
+    float* y = out + r * cols;
+    float mx = -INFINITY;
+    for (int64_t j = lane; j < cols; j += kWave) mx = fmaxf(mx, x[j]);
+    mx = wave_max(mx);
+    float s = 0.0f;
+    for (int64_t j = lane; j < cols; j += kWave) s += expf(x[j] - mx);
+    s = wave_sum(s);
+    for (int64_t j = lane; j < cols; j += kWave) y[j] = expf(x[j] - mx) / s;
+}
+
+// ---- lrp_softmax_rows (lrp_math.hpp:89-98) ----------------------------------------------------
+__global__ void __launch_bounds__(kThreads) lrp_softmax_kernel(const float* x, const float* y, const float* r,
+                                                               float* r_in, int64_t rows, int64_t cols) {
+    const int64_t row = row_id();
+    if (row >= rows) return;
+    const int lane = lane_id();
+    const int64_t off = row * cols;
+    float s = 0.0f;
+    for (int64_t j = lane; j < cols; j += kWave) s += r[off + j];
+    s = wave_sum(s);
+    for (int64_t j = lane; j < cols; j += kWave) r_in[off + j] = x[off + j] * (r[off + j] - y[off + j] * s);
+}
+
+__global__ void __launch_bounds__(kThreads) row_sums_kernel(const float* in, float* out, int64_t rows, int64_t cols) {
+    const int64_t r = row_id();
+    if (r >= rows) return;
+    const int lane = lane_id();
+    float s = 0.0f;
+    for (int64_t j = lane; j < cols; j += kWave) s += in[r * cols + j];
+    s = wave_sum(s);
+    if (lane == 0) out[r] = s;
+}
+
+// ---- deterministic two-pass sum / dot ---------------------------------------------------------
+constexpr int kReduceBlocks = 1024;
+
+__device__ float block_sum(float v) {
+    __shared__ float part[kThreads / kWave];
+    v = wave_sum(v);
+    if (lane_id() == 0) part[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float t = 0.0f;
+    if (threadIdx.x == 0)
+        for (int w = 0; w < kThreads / kWave; ++w) t += part[w];
+    return t;
+}
+
+__global__ void __launch_bounds__(kThreads) reduce_pass1(const float* a, const float* b, int64_t n, float* partials) {
+    float s = 0.0f;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < n; i += stride)
+        s += b ? a[i] * b[i] : a[i];
+    const float t = block_sum(s);
+    if (threadIdx.x == 0) partials[blockIdx.x] = t;
+}
+
+__global__ void __launch_bounds__(kThreads) reduce_pass2(const float* partials, int count, float* out) {
+    float s = 0.0f;
+    for (int i = threadIdx.x; i < count; i += kThreads) s += partials[i];
+    const float t = block_sum(s);
+    if (threadIdx.x == 0) out[0] = t;
+}
+
+// ---- attention -----------------------------------------------------------------------------------
+// P = softmax(scale * raw) over visible keys; masked entries of P written 0.
+__global__ void __launch_bounds__(kThreads) attention_softmax_kernel(const float* raw, float* p, int64_t rows,
+                                                                     int64_t L, float scale, int causal) {
+    const int64_t r = row_id();
+    if (r >= rows) return;
+    const int lane = lane_id();
+    const int64_t i = r % L;
+    const int64_t vis = causal ? i + 1 : L;
+    const float* x = raw + r * L;
+    float* y = p + r * L;
+    float mx = -INFINITY;
+    for (int64_t j = lane; j < vis; j += kWave) mx = fmaxf(mx, scale * x[j]);
+    mx = wave_max(mx);
+    float s = 0.0f;
+    for (int64_t j = lane; j < vis; j += kWave) s += expf(scale * x[j] - mx);
+    s = wave_sum(s);
+    for (int64_t j = lane; j < L; j += kWave) y[j] = j < vis ? expf(scale * x[j] - mx) / s : 0.0f;
+}
+
+// s = [x * (r - P * sum r)] / (2 raw + eps sign raw), x = scale * raw; 0 where masked.
+__global__ void __launch_bounds__(kThreads) attention_lrp_scores_kernel(const float* r_attn, const float* p,
+                                                                        const float* raw, float* s_out, int64_t rows,
+                                                                        int64_t L, float scale, float eps, int causal) {
+    const int64_t r = row_id();
+    if (r >= rows) return;
+    const int lane = lane_id();
+    const int64_t i = r % L;
+    const int64_t vis = causal ? i + 1 : L;
+    const int64_t off = r * L;
+    float sum = 0.0f;
+    for (int64_t j = lane; j < vis; j += kWave) sum += r_attn[off + j];
+    sum = wave_sum(sum);
+    for (int64_t j = lane; j < L; j += kWave) {
+        float v = 0.0f;
+        if (j < vis) {
+            const float o = raw[off + j];
+            const float rs = (scale * o) * (r_attn[off + j] - p[off + j] * sum);
+            v = rs / (2.0f * o + eps * ((o >= 0.0f) ? 1.0f : -1.0f));
+        }
+        s_out[off + j] = v;
+    }
+}
+
+// RoPE of q and k from the packed projection buffer into head-packed (rows, heads*D) outputs.
+__global__ void __launch_bounds__(kThreads) rope_qk_kernel(const float* q_in, const float* k_in, int64_t ld,
+                                                           float* q_out, float* k_out, const float* cos_t,
+                                                           const float* sin_t, int64_t rows, int64_t L, int64_t H,
+                                                           int64_t Hkv, int64_t D, int rotate_half) {
+    const int64_t half = D / 2;
+    const int64_t nq = rows * H * half, nk = rows * Hkv * half;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
+    for (int64_t t = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; t < nq + nk; t += stride) {
+        const bool is_q = t < nq;
+        const int64_t u = is_q ? t : t - nq;
+        const int64_t heads = is_q ? H : Hkv;
+        const int64_t i = u % half, h = (u / half) % heads, row = u / (half * heads);
+        const int64_t pos = row % L;
+        const int64_t lo = rotate_half ? i : 2 * i, hi = rotate_half ? i + half : 2 * i + 1;
+        const float* src = (is_q ? q_in : k_in) + row * ld + h * D;
+        float* dst = (is_q ? q_out : k_out) + row * heads * D + h * D;
+        const float c = cos_t[pos * half + i], s = sin_t[pos * half + i];
+        const float x0 = src[lo], x1 = src[hi];
+        dst[lo] = x0 * c - x1 * s;
+        dst[hi] = x0 * s + x1 * c;
+    }
+}
+
+__global__ void __launch_bounds__(kThreads) rope_rotate_kernel(const float* in, const float* cos_t, const float* sin_t,
+                                                               float* out, int64_t slices, int64_t L, int64_t D,
+                                                               int inverse, int rotate_half) {
+    const int64_t half = D / 2, n = slices * L * half;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
+    for (int64_t t = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; t < n; t += stride) {
+        const int64_t i = t % half, row = t / half, pos = row % L;
+        const int64_t lo = row * D + (rotate_half ? i : 2 * i), hi = row * D + (rotate_half ? i + half : 2 * i + 1);
+        const float c = cos_t[pos * half + i], s = sin_t[pos * half + i];
+        const float x0 = in[lo], x1 = in[hi];
+        if (inverse) {
+            out[lo] = x0 * c + x1 * s;
+            out[hi] = -x0 * s + x1 * c;
+        } else {
+            out[lo] = x0 * c - x1 * s;
+            out[hi] = x0 * s + x1 * c;
+        }
+    }
+}
+
+// lrp_math.hpp:104-123, one thread per pair.
+__global__ void __launch_bounds__(kThreads) lrp_rope_kernel(const float* x, const float* y, const float* r,
+                                                            const float* cos_t, const float* sin_t, float* r_in,
+                                                            int64_t slices, int64_t L, int64_t D, float eps,
+                                                            int rotate_half) {
+    const int64_t half = D / 2, n = slices * L * half;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
+    for (int64_t t = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; t < n; t += stride) {
+        const int64_t i = t % half, row = t / half, pos = row % L;
+        const int64_t lo = row * D + (rotate_half ? i : 2 * i), hi = row * D + (rotate_half ? i + half : 2 * i + 1);
+        const float c = cos_t[pos * half + i], s = sin_t[pos * half + i];
+        const float d0 = stab(y[lo], eps), d1 = stab(y[hi], eps);
+        float rl = 0.0f, rh = 0.0f;
+        rl += (x[lo] * c / d0) * r[lo];
+        rh += (x[hi] * -s / d0) * r[lo];
+        rl += (x[lo] * s / d1) * r[hi];
+        rh += (x[hi] * c / d1) * r[hi];
+        r_in[lo] = rl;
+        r_in[hi] = rh;
+    }
+}
+
+__global__ void __launch_bounds__(kThreads) permute_kernel(const float* in, float* out, int64_t d0, int64_t d1,
+                                                           int64_t d2, int64_t d3) {
+    const int64_t n = d0 * d1 * d2 * d3, stride = static_cast<int64_t>(gridDim.x) * kThreads;
+    for (int64_t t = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; t < n; t += stride) {
+        // t indexes the output (a, c, b, e)
+        const int64_t e = t % d3, b = (t / d3) % d1, c = (t / (d3 * d1)) % d2, a = t / (d3 * d1 * d2);
+        out[t] = in[((a * d1 + b) * d2 + c) * d3 + e];
+    }
+}
+
+__global__ void __launch_bounds__(kThreads) mask_fill_kernel(float* scores, const float* keep, int64_t batch,
+                                                             int64_t heads, int64_t q_len, int64_t k_len, int causal,
+                                                             int64_t q_offset, int64_t window, float value) {
+    const int64_t n = batch * heads * q_len * k_len, stride = static_cast<int64_t>(gridDim.x) * kThreads;
+    for (int64_t t = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; t < n; t += stride) {
+        const int64_t j = t % k_len, i = (t / k_len) % q_len, b = t / (k_len * q_len * heads);
+        bool masked = causal && j > i + q_offset;  // row_math.hpp:117-126
+        masked = masked || (causal && window > 0 && j + window <= i + q_offset);
+        masked = masked || (keep != nullptr && keep[b * k_len + j] == 0.0f);
+        if (masked) scores[t] = value;
+    }
+}
+
+// ---- LM seeding --------------------------------------------------------------------------------
+struct Targets {
+    int64_t t[64];
+};
+
+__global__ void __launch_bounds__(kThreads) lm_seed_kernel(const float* logits, int64_t L, int64_t V, int use_given,
+                                                           Targets given, int64_t* targets_out, float* seed,
+                                                           int unit) {
+    const int64_t n = blockIdx.x;
+    const float* row = logits + (n * L + (L - 1)) * V;
+    __shared__ float bv[kThreads];
+    __shared__ int64_t bi[kThreads];
+    float best = -INFINITY;
+    int64_t idx = V;  // "none yet"
+    if (use_given) {
+        if (threadIdx.x == 0) {
+            best = row[given.t[n]];
+            idx = given.t[n];
+        }
+    } else {
+        for (int64_t j = threadIdx.x; j < V; j += kThreads) {  // j ascends: ties keep the first index
+            const float v = row[j];
+            if (idx == V || v > best) {
+                best = v;
+                idx = j;
+            }
+        }
+    }
+    bv[threadIdx.x] = best;
+    bi[threadIdx.x] = idx;
+    __syncthreads();
+    for (int s = kThreads / 2; s > 0; s >>= 1) {
+        if (threadIdx.x < s) {
+            const float ov = bv[threadIdx.x + s];
+            const int64_t oi = bi[threadIdx.x + s];
+            const float cv = bv[threadIdx.x];
+            const int64_t ci = bi[threadIdx.x];
+            // larger value wins; equal values keep the lower index; "none" (index V) always loses
+            const bool take = (ci == V) || (oi != V && (ov > cv || (ov == cv && oi < ci)));
+            if (take) {
+                bv[threadIdx.x] = ov;
+                bi[threadIdx.x] = oi;
+            }
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        const int64_t t = bi[0];
+        targets_out[n] = t;
+        seed[(n * L + (L - 1)) * V + t] = unit ? 1.0f : row[t];
+    }
+}
+
+unsigned rows_grid(int64_t rows) { return static_cast<unsigned>(cdiv(rows, kRowsPerBlock)); }
+
+bool sizes_ok(const char* what, int64_t a, int64_t b, int* rc) {
+    if (a < 0 || b < 0) {
+        *rc = fail(PXK_ERR_INVALID, "%s: negative size", what);
+        return false;
+    }
+    *rc = PXK_OK;
+    return a > 0 && b > 0;
+}
+
+}  // namespace
+}  // namespace pxk
+
+using namespace pxk;
+
+extern "C" {
+
+int pxk_rms_norm_forward(const float* in, const float* gamma, float* out, float* row_rms, int64_t rows, int64_t cols,
+                         float eps, void* stream) {
+    int rc;
+    if (!sizes_ok("pxk_rms_norm_forward", rows, cols, &rc)) return rc;
+    hipLaunchKernelGGL(rms_norm_kernel, dim3(rows_grid(rows)), dim3(kThreads), 0, S(stream), in, gamma, out, row_rms,
+                       rows, cols, eps);
+    return launched("pxk_rms_norm_forward");
+}
+
+int pxk_softmax_rows(const float* in, float* out, int64_t rows, int64_t cols, void* stream) {
+    int rc;
+    if (!sizes_ok("pxk_softmax_rows", rows, cols, &rc)) return rc;
+    hipLaunchKernelGGL(softmax_kernel, dim3(rows_grid(rows)), dim3(kThreads), 0, S(stream), in, out, rows, cols);
+    return launched("pxk_softmax_rows");
+}
+
+int pxk_lrp_softmax_rows(const float* x, const float* y, const float* r, float* r_in, int64_t rows, int64_t cols,
+                         void* stream) {
+    int rc;
+    if (!sizes_ok("pxk_lrp_softmax_rows", rows, cols, &rc)) return rc;
+    hipLaunchKernelGGL(lrp_softmax_kernel, dim3(rows_grid(rows)), dim3(kThreads), 0, S(stream), x, y, r, r_in, rows,
+                       cols);
+    return launched("pxk_lrp_softmax_rows");
+}
+
+int pxk_row_sums(const float* in, float* out, int64_t rows, int64_t cols, void* stream) {
+    int rc;
+    if (!sizes_ok("pxk_row_sums", rows, cols, &rc)) {
+        if (rc == PXK_OK && rows > 0) return pxk_fill(out, 0.0f, rows, stream);
+        return rc;
+    }
+    hipLaunchKernelGGL(row_sums_kernel, dim3(rows_grid(rows)), dim3(kThreads), 0, S(stream), in, out, rows, cols);
+    return launched("pxk_row_sums");
+}
+
+size_t pxk_reduce_partials(int64_t) { return kReduceBlocks * sizeof(float); }
+
+static int reduce(const char* what, const float* a, const float* b, int64_t n, float* out, float* partials,
+                  void* stream) {
+    if (n < 0) return fail(PXK_ERR_INVALID, "%s: negative size", what);
+    if (n == 0) return pxk_fill(out, 0.0f, 1, stream);
+    const unsigned blocks = static_cast<unsigned>(std::min<int64_t>(kReduceBlocks, cdiv(n, kThreads)));
+    hipLaunchKernelGGL(reduce_pass1, dim3(blocks), dim3(kThreads), 0, S(stream), a, b, n, partials);
+    if (const int rc = launched(what)) return rc;
+    hipLaunchKernelGGL(reduce_pass2, dim3(1), dim3(kThreads), 0, S(stream), partials, static_cast<int>(blocks), out);
+    return launched(what);
+}
+
+int pxk_sum(const float* in, int64_t n, float* out, float* partials, void* stream) {
+    return reduce("pxk_sum", in, nullptr, n, out, partials, stream);
+}
+
+int pxk_dot(const float* a, const float* b, int64_t n, float* out, float* partials, void* stream) {
+    return reduce("pxk_dot", a, b, n, out, partials, stream);
+}
+
+int pxk_attention_softmax(const float* raw, float* p, int64_t slices, int64_t l, float scale, int causal,
+                          void* stream) {
+    int rc;
+    if (!sizes_ok("pxk_attention_softmax", slices, l, &rc)) return rc;
+    hipLaunchKernelGGL(attention_softmax_kernel, dim3(rows_grid(slices * l)), dim3(kThreads), 0, S(stream), raw, p,
+                       slices * l, l, scale, causal);
+    return launched("pxk_attention_softmax");
+}
+
+int pxk_attention_lrp_scores(const float* r_attn, const float* p, const float* raw, float* s, int64_t slices,
+                             int64_t l, float scale, float eps, int causal, void* stream) {
+    int rc;
+    if (!sizes_ok("pxk_attention_lrp_scores", slices, l, &rc)) return rc;
+    hipLaunchKernelGGL(attention_lrp_scores_kernel, dim3(rows_grid(slices * l)), dim3(kThreads), 0, S(stream), r_attn,
+                       p, raw, s, slices * l, l, scale, eps, causal);
+    return launched("pxk_attention_lrp_scores");
+}
+
+int pxk_rope_qk(const float* q_in, const float* k_in, int64_t ld_in, float* q_out, float* k_out, const float* cos_t,
+                const float* sin_t, int64_t rows, int64_t seq_len, int64_t heads, int64_t kv_heads, int64_t head_dim,
+                int rotate_half, void* stream) {
+    if (rows < 0 || seq_len <= 0 || heads <= 0 || kv_heads <= 0 || head_dim <= 0 || head_dim % 2 != 0)
+        return fail(PXK_ERR_INVALID, "pxk_rope_qk: bad sizes");
+    if (rows == 0) return PXK_OK;
+    const int64_t work = rows * (heads + kv_heads) * (head_dim / 2);
+    hipLaunchKernelGGL(rope_qk_kernel, dim3(grid_for(work, kThreads)), dim3(kThreads), 0, S(stream), q_in, k_in, ld_in,
+                       q_out, k_out, cos_t, sin_t, rows, seq_len, heads, kv_heads, head_dim, rotate_half);
+    return launched("pxk_rope_qk");
+}
+
+int pxk_rope_rotate(const float* in, const float* cos_t, const float* sin_t, float* out, int64_t slices,
+                    int64_t seq_len, int64_t head_dim, int inverse, int rotate_half, void* stream) {
+    if (slices < 0 || seq_len < 0 || head_dim <= 0 || head_dim % 2 != 0)
+        return fail(PXK_ERR_INVALID, "pxk_rope_rotate: bad sizes");
+    const int64_t work = slices * seq_len * (head_dim / 2);
+    if (work == 0) return PXK_OK;
+    hipLaunchKernelGGL(rope_rotate_kernel, dim3(grid_for(work, kThreads)), dim3(kThreads), 0, S(stream), in, cos_t,
+                       sin_t, out, slices, seq_len, head_dim, inverse, rotate_half);
+    return launched("pxk_rope_rotate");
+}
+
+int pxk_lrp_rope(const float* x, const float* y, const float* r, const float* cos_t, const float* sin_t, float* r_in,
+                 int64_t slices, int64_t seq_len, int64_t head_dim, float eps, int rotate_half, void* stream) {
+    if (slices < 0 || seq_len < 0 || head_dim <= 0 || head_dim % 2 != 0)
+        return fail(PXK_ERR_INVALID, "pxk_lrp_rope: bad sizes");
+    const int64_t work = slices * seq_len * (head_dim / 2);
+    if (work == 0) return PXK_OK;
+    hipLaunchKernelGGL(lrp_rope_kernel, dim3(grid_for(work, kThreads)), dim3(kThreads), 0, S(stream), x, y, r, cos_t,
+                       sin_t, r_in, slices, seq_len, head_dim, eps, rotate_half);
+    return launched("pxk_lrp_rope");
+}
+
+int pxk_permute_0213(const float* in, float* out, int64_t d0, int64_t d1, int64_t d2, int64_t d3, void* stream) {
+    if (d0 < 0 || d1 < 0 || d2 < 0 || d3 < 0) return fail(PXK_ERR_INVALID, "pxk_permute_0213: negative size");
+    const int64_t n = d0 * d1 * d2 * d3;
+    if (n == 0) return PXK_OK;
+    hipLaunchKernelGGL(permute_kernel, dim3(grid_for(n, kThreads)), dim3(kThreads), 0, S(stream), in, out, d0, d1, d2,
+                       d3);
+    return launched("pxk_permute_0213");
+}
+
+int pxk_attention_mask_fill(float* scores, const float* key_keep, int64_t batch, int64_t heads, int64_t q_len,
+                            int64_t k_len, int causal, int64_t q_offset, int64_t window, float value, void* stream) {
+    if (batch < 0 || heads < 0 || q_len < 0 || k_len < 0 || q_offset < 0 || window < 0)
+        return fail(PXK_ERR_INVALID, "pxk_attention_mask_fill: negative size");
+    const int64_t n = batch * heads * q_len * k_len;
+    if (n == 0 || (!causal && key_keep == nullptr)) return PXK_OK;
+    hipLaunchKernelGGL(mask_fill_kernel, dim3(grid_for(n, kThreads)), dim3(kThreads), 0, S(stream), scores, key_keep,
+                       batch, heads, q_len, k_len, causal, q_offset, window, value);
+    return launched("pxk_attention_mask_fill");
+}
+
+int pxk_lm_seed(const float* logits, int64_t n, int64_t l, int64_t vocab, const int64_t* targets_in,
+                int64_t* targets_out, float* seed, int unit, void* stream) {
+    if (n <= 0 || l <= 0 || vocab <= 0) return fail(PXK_ERR_INVALID, "pxk_lm_seed: sizes must be positive");
+    Targets given{};
+    if (targets_in) {
+        if (n > 64) return fail(PXK_ERR_INVALID, "pxk_lm_seed: at most 64 sequences with explicit targets");
+        for (int64_t i = 0; i < n; ++i) {
+            if (targets_in[i] < 0 || targets_in[i] >= vocab)
+                return fail(PXK_ERR_INVALID, "pxk_lm_seed: target %lld outside the vocabulary",
+                            static_cast<long long>(targets_in[i]));
+            given.t[i] = targets_in[i];
+        }
+    }
+    if (const int rc = pxk_fill(seed, 0.0f, n * l * vocab, stream)) return rc;
+    hipLaunchKernelGGL(lm_seed_kernel, dim3(static_cast<unsigned>(n)), dim3(kThreads), 0, S(stream), logits, l, vocab,
+                       targets_in ? 1 : 0, given, targets_out, seed, unit);
+    return launched("pxk_lm_seed");
+}
+
+}  // extern "C"

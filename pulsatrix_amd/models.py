@@ -1,0 +1,128 @@
+"""Python handles over the host framework's C ABI (include/pulsatrix_amd.h).
+
+Block and CausalLM take host numpy arrays (the parity-test interface, same calls as the oracle's
+ctypes wrapper); CausalLM.explain_device runs the device hot path on buffers already in HBM.
+"""
+import ctypes
+
+import numpy as np
+
+from . import native as N
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+def param_count(cfg, block=False):
+    h = N.host()
+    return (h.pxa_block_param_count if block else h.pxa_param_count)(ctypes.byref(cfg))
+
+
+def synthetic_params(cfg, seed, std=0.02, block=False):
+    """Random-init blob: N(0, std) from seed, every RMSNorm gamma 1 (SplitMix64 + Box-Muller)."""
+    out = np.empty(param_count(cfg, block), np.float32)
+    N.host_check(N.host().pxa_synthetic_params(ctypes.byref(cfg), int(block), seed, std, _p(out)))
+    return out
+
+
+class Block:
+    """TransformerBlock on the process-wide MI355XBackend."""
+
+    def __init__(self, cfg, params):
+        self.cfg = cfg
+        params = np.ascontiguousarray(params, dtype=np.float32)
+        self.h = N.host().pxa_block_create(ctypes.byref(cfg), _p(params))
+        if not self.h:
+            raise N.PxkError(N.host().pxa_last_error().decode())
+
+    def forward(self, x):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        n, l, _ = x.shape
+        y = np.empty_like(x)
+        N.host_check(N.host().pxa_block_forward(self.h, _p(x), n, l, _p(y)))
+        return y
+
+    def relevance(self, r, eps, bias_in_denominator):
+        r = np.ascontiguousarray(r, dtype=np.float32)
+        out = np.empty_like(r)
+        N.host_check(N.host().pxa_block_relevance(self.h, _p(r), eps, int(bias_in_denominator), _p(out)))
+        return out
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            N.host().pxa_block_destroy(self.h)
+            self.h = None
+
+
+class CausalLM:
+    """CausalLM on the process-wide MI355XBackend."""
+
+    def __init__(self, cfg, params=None, seed=None, std=0.02):
+        self.cfg = cfg
+        h = N.host()
+        if params is None:
+            self.h = h.pxa_lm_create_random(ctypes.byref(cfg), seed, std)
+        else:
+            params = np.ascontiguousarray(params, dtype=np.float32)
+            self.h = h.pxa_lm_create(ctypes.byref(cfg), _p(params))
+        if not self.h:
+            raise N.PxkError(h.pxa_last_error().decode())
+        self.shape = None
+
+    def forward(self, ids):
+        ids = np.ascontiguousarray(ids, dtype=np.int64)
+        n, l = ids.shape
+        logits = np.empty((n, l, self.cfg.vocab_size), np.float32)
+        N.host_check(N.host().pxa_lm_forward(self.h, ids.ctypes.data_as(ctypes.POINTER(ctypes.c_int64)), n, l,
+                                             _p(logits)))
+        self.shape = (n, l)
+        return logits
+
+    def relevance(self, seed, eps, bias_in_denominator, want_kv=False):
+        n, l = self.shape
+        c = self.cfg
+        seed = np.ascontiguousarray(seed, dtype=np.float32)
+        r_embed = np.empty((n, l, c.hidden_size), np.float32)
+        r_tok = np.empty((n, l), np.float32)
+        kvh = c.num_kv_heads if c.num_kv_heads > 0 else c.num_heads
+        hd = c.head_dim if c.head_dim > 0 else c.hidden_size // c.num_heads
+        kv = (c.num_layers, n * l, kvh * hd)
+        k = np.empty(kv, np.float32) if want_kv else None
+        v = np.empty(kv, np.float32) if want_kv else None
+        N.host_check(N.host().pxa_lm_relevance(self.h, _p(seed), eps, int(bias_in_denominator), _p(r_embed),
+                                               _p(r_tok), _p(k), _p(v)))
+        return (r_embed, r_tok, k, v) if want_kv else (r_embed, r_tok)
+
+    def explain_device(self, ids_ptr, n, l, eps, bias_in_denominator, token_rel_ptr, targets_ptr, targets=None,
+                       unit_seed=False):
+        """Device hot path; pointers are device addresses (ints or c_void_p)."""
+        t = None
+        if targets is not None:
+            t = np.ascontiguousarray(targets, dtype=np.int64)
+        N.host_check(N.host().pxa_lm_explain_device(
+            self.h, ids_ptr, n, l, eps, int(bias_in_denominator), token_rel_ptr, targets_ptr,
+            t.ctypes.data_as(ctypes.POINTER(ctypes.c_int64)) if t is not None else None, int(unit_seed)))
+
+    def capture_explain(self, ids_ptr, n, l, eps, bias_in_denominator, token_rel_ptr, targets_ptr):
+        N.host_check(N.host().pxa_lm_capture_explain(self.h, ids_ptr, n, l, eps, int(bias_in_denominator),
+                                                     token_rel_ptr, targets_ptr))
+
+    def replay(self):
+        N.host_check(N.host().pxa_lm_replay(self.h))
+
+    def last_logits_ptr(self):
+        return N.host().pxa_lm_last_logits(self.h)
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            N.host().pxa_lm_destroy(self.h)
+            self.h = None
+
+
+def stream():
+    return N.host().pxa_backend_stream()
+
+
+def synchronize():
+    N.host_check(N.host().pxa_backend_synchronize())

@@ -1,0 +1,218 @@
+"""ctypes bindings of the MI355X libraries' C ABI (include/pxk.h, include/pulsatrix_amd.h).
+
+This is the binding a Python caller of the library uses. It loads the in-tree libraries built by
+pulsatrix_amd/build.py and raises if they are missing: there is no fallback path.
+"""
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_DIR = os.path.join(HERE, "lib")
+PXK_SO = os.path.join(LIB_DIR, "libpxk_gfx950.so")
+HOST_SO = os.path.join(LIB_DIR, "libpulsatrix_amd.so")
+
+c_f32p = ctypes.POINTER(ctypes.c_float)
+c_i64 = ctypes.c_int64
+c_vp = ctypes.c_void_p
+
+
+class PxkError(RuntimeError):
+    pass
+
+
+class Operand(ctypes.Structure):
+    _fields_ = [("ptr", c_vp), ("ld", c_i64), ("batch_stride", c_i64), ("inner_stride", c_i64),
+                ("inner_div", c_i64), ("group_stride", c_i64)]
+
+
+class GemmDesc(ctypes.Structure):
+    _fields_ = [("m", c_i64), ("n", c_i64), ("k", c_i64), ("batch", c_i64), ("inner", c_i64), ("kgroups", c_i64),
+                ("trans_a", ctypes.c_int32), ("trans_b", ctypes.c_int32), ("causal", ctypes.c_int32),
+                ("prologue", ctypes.c_int32), ("epilogue", ctypes.c_int32), ("splits", ctypes.c_int32),
+                ("beta", ctypes.c_float), ("eps", ctypes.c_float),
+                ("a", Operand), ("b", Operand), ("c", Operand), ("z", Operand), ("z_bias", Operand),
+                ("c2", Operand), ("c3", Operand), ("x", Operand), ("y", Operand), ("w", Operand), ("z2", Operand), ("z3", Operand),
+                ("e_bias", Operand), ("e_bias2", Operand),
+                ("cos_t", c_vp), ("sin_t", c_vp), ("head_dim", c_i64), ("rope_half", ctypes.c_int32),
+                ("reserved", ctypes.c_int32), ("workspace", c_vp), ("workspace_bytes", ctypes.c_size_t)]
+
+
+CAUSAL_NONE, CAUSAL_TRI, CAUSAL_K_LE_M, CAUSAL_K_GE_M = 0, 1, 2, 3
+PRO_NONE, PRO_DIV_STAB = 0, 1
+(EPI_STORE, EPI_STORE_BIAS, EPI_ADD_RESID, EPI_MUL_X, EPI_SPV, EPI_ROPE_REL, EPI_VALUE_REL,
+ EPI_SWIGLU_REL) = range(8)
+
+# (name, restype, argtypes) of every pxk entry point; `p` = device pointer (void*), `i` = int64,
+# `f` = float, `n` = int, `s` = size_t.
+_T = {"p": c_vp, "i": c_i64, "f": ctypes.c_float, "n": ctypes.c_int, "s": ctypes.c_size_t}
+PXK_SIGNATURES = {
+    "pxk_gemm_ex": "pnpnpiiifps" + "p",
+    "pxk_fill": "pfip",
+    "pxk_elementwise": "nppip",
+    "pxk_add": "pppip",
+    "pxk_mul": "pppip",
+    "pxk_axpby": "fpfppip",
+    "pxk_add_row_vector": "pppiip",
+    "pxk_lrp_residual_split": "pppppifp",
+    "pxk_lrp_bilinear_elementwise": "ppppifp",
+    "pxk_lrp_stabilized_divide": "ppppifnp",
+    "pxk_lrp_bilinear_scale": "pppifp",
+    "pxk_swiglu_forward": "pippiip",
+    "pxk_copy_2d": "pipiiip",
+    "pxk_accumulate_rows": "ppiip",
+    "pxk_gather_rows": "pppiip",
+    "pxk_column_sums": "ppiifp",
+    "pxk_rms_norm_forward": "ppppiifp",
+    "pxk_softmax_rows": "ppiip",
+    "pxk_lrp_softmax_rows": "ppppiip",
+    "pxk_row_sums": "ppiip",
+    "pxk_sum": "pippp",
+    "pxk_dot": "ppippp",
+    "pxk_attention_softmax": "ppiifnp",
+    "pxk_attention_lrp_scores": "ppppiiffnp",
+    "pxk_rope_qk": "ppippppiiiiinp",
+    "pxk_rope_rotate": "ppppiiinnp",
+    "pxk_lrp_rope": "ppppppiiifnp",
+    "pxk_permute_0213": "ppiiiip",
+    "pxk_attention_mask_fill": "ppiiiiniifp",
+    "pxk_lm_seed": "piiipppnp",
+}
+
+
+def _bind(lib, sigs):
+    for name, sig in sigs.items():
+        fn = getattr(lib, name)
+        fn.restype = ctypes.c_int
+        fn.argtypes = [_T[c] for c in sig]
+
+
+_pxk = None
+
+
+def _share_hip_runtime():
+    """Load PyTorch's HIP runtime first when PyTorch is installed, so the native libraries bind to
+    that same libamdhip64.so.7 (by soname) and the process holds one HIP runtime. Loaded the other
+    way round, PyTorch brings a second copy of the runtime that cannot see the device."""
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
+
+
+def pxk():
+    """The kernel library, loaded once; raises PxkError if it was not built."""
+    global _pxk
+    if _pxk is None:
+        _share_hip_runtime()
+        if not os.path.exists(PXK_SO):
+            raise PxkError("%s is missing: build it with __graft_entry__.build()" % PXK_SO)
+        lib = ctypes.CDLL(PXK_SO)
+        _bind(lib, PXK_SIGNATURES)
+        lib.pxk_last_error.restype = ctypes.c_char_p
+        lib.pxk_version.restype = ctypes.c_char_p
+        lib.pxk_gemm.restype = ctypes.c_int
+        lib.pxk_gemm.argtypes = [ctypes.POINTER(GemmDesc), c_vp]
+        lib.pxk_gemm_workspace.restype = ctypes.c_size_t
+        lib.pxk_gemm_workspace.argtypes = [ctypes.POINTER(GemmDesc)]
+        lib.pxk_gemm_supported.restype = ctypes.c_int
+        lib.pxk_gemm_supported.argtypes = [ctypes.c_int] * 4
+        lib.pxk_reduce_partials.restype = ctypes.c_size_t
+        lib.pxk_reduce_partials.argtypes = [c_i64]
+        _pxk = lib
+    return _pxk
+
+
+def check(rc):
+    if rc != 0:
+        raise PxkError(pxk().pxk_last_error().decode())
+
+
+def call(name, *args):
+    check(getattr(pxk(), name)(*args))
+
+
+def operand(ptr, ld, batch_stride=0, inner_stride=0, inner_div=0, group_stride=0):
+    return Operand(ptr, ld, batch_stride, inner_stride, inner_div, group_stride)
+
+
+def gemm(desc, stream=None):
+    check(pxk().pxk_gemm(ctypes.byref(desc), stream))
+
+
+def gemm_workspace(desc):
+    return pxk().pxk_gemm_workspace(ctypes.byref(desc))
+
+
+# ---- the host framework (include/pulsatrix_amd.h) ----------------------------------------------
+
+class ModelConfig(ctypes.Structure):
+    """px_model_config."""
+
+    _fields_ = [("vocab_size", c_i64), ("hidden_size", c_i64), ("num_layers", c_i64), ("num_heads", c_i64),
+                ("num_kv_heads", c_i64), ("head_dim", c_i64), ("intermediate_size", c_i64),
+                ("rms_norm_eps", ctypes.c_float), ("rope_theta", ctypes.c_float), ("use_rope", ctypes.c_int32),
+                ("rope_rotate_half", ctypes.c_int32), ("causal", ctypes.c_int32), ("qkv_bias", ctypes.c_int32),
+                ("out_bias", ctypes.c_int32), ("mlp_bias", ctypes.c_int32), ("tie_word_embeddings", ctypes.c_int32),
+                ("reserved", ctypes.c_int32)]
+
+
+_host = None
+
+
+def host():
+    """libpulsatrix_amd.so, loaded once; raises PxkError if it was not built."""
+    global _host
+    if _host is None:
+        if not os.path.exists(HOST_SO):
+            raise PxkError("%s is missing: build it with __graft_entry__.build()" % HOST_SO)
+        pxk()  # its dependency, from the same directory
+        lib = ctypes.CDLL(HOST_SO)
+        cfgp = ctypes.POINTER(ModelConfig)
+        i64p = ctypes.POINTER(ctypes.c_int64)
+        sigs = {
+            "pxa_last_error": (ctypes.c_char_p, []),
+            "pxa_device_count": (ctypes.c_int, []),
+            "pxa_backend": (c_vp, []),
+            "pxa_backend_stream": (c_vp, []),
+            "pxa_backend_synchronize": (ctypes.c_int, []),
+            "pxa_backend_memory": (ctypes.c_int, [ctypes.POINTER(ctypes.c_size_t), ctypes.POINTER(ctypes.c_size_t)]),
+            "pxa_fill_normal": (None, [c_vp, ctypes.c_size_t, ctypes.c_uint64, ctypes.c_double]),
+            "pxa_param_count": (c_i64, [cfgp]),
+            "pxa_block_param_count": (c_i64, [cfgp]),
+            "pxa_synthetic_params": (ctypes.c_int, [cfgp, ctypes.c_int, ctypes.c_uint64, ctypes.c_double, c_vp]),
+            "pxa_block_create": (c_vp, [cfgp, c_vp]),
+            "pxa_block_forward": (ctypes.c_int, [c_vp, c_vp, c_i64, c_i64, c_vp]),
+            "pxa_block_relevance": (ctypes.c_int, [c_vp, c_vp, ctypes.c_float, ctypes.c_int, c_vp]),
+            "pxa_block_destroy": (None, [c_vp]),
+            "pxa_lm_create": (c_vp, [cfgp, c_vp]),
+            "pxa_lm_create_random": (c_vp, [cfgp, ctypes.c_uint64, ctypes.c_double]),
+            "pxa_lm_forward": (ctypes.c_int, [c_vp, i64p, c_i64, c_i64, c_vp]),
+            "pxa_lm_relevance": (ctypes.c_int, [c_vp, c_vp, ctypes.c_float, ctypes.c_int, c_vp, c_vp, c_vp, c_vp]),
+            "pxa_lm_explain_device": (ctypes.c_int, [c_vp, c_vp, c_i64, c_i64, ctypes.c_float, ctypes.c_int, c_vp,
+                                                     c_vp, i64p, ctypes.c_int]),
+            "pxa_lm_capture_explain": (ctypes.c_int, [c_vp, c_vp, c_i64, c_i64, ctypes.c_float, ctypes.c_int, c_vp,
+                                                      c_vp]),
+            "pxa_lm_replay": (ctypes.c_int, [c_vp]),
+            "pxa_lm_last_logits": (c_vp, [c_vp]),
+            "pxa_lm_last_embedding_relevance": (c_vp, [c_vp]),
+            "pxa_lm_destroy": (None, [c_vp]),
+        }
+        for name, (res, args) in sigs.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _host = lib
+    return _host
+
+
+def host_check(rc):
+    if rc != 0:
+        raise PxkError(host().pxa_last_error().decode())
+
+
+def model_config(**kw):
+    base = dict(vocab_size=0, hidden_size=0, num_layers=1, num_heads=1, num_kv_heads=0, head_dim=0,
+                intermediate_size=0, rms_norm_eps=1e-5, rope_theta=10000.0, use_rope=1, rope_rotate_half=1,
+                causal=1, qkv_bias=0, out_bias=0, mlp_bias=0, tie_word_embeddings=1, reserved=0)
+    base.update(kw)
+    return ModelConfig(**base)

@@ -8,3 +8,11 @@ sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (runs the HIP path)")
+
+
+@pytest.fixture(autouse=True)
+def _release_device_buffers():
+    yield
+    import gpu_util
+
+    gpu_util.release_all()
