@@ -1,0 +1,284 @@
+"""Throughput of the causal-LM forward + AttnLRP path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--mode graph|eager] [--no-cpu-baseline]
+
+Workload: the SmolLM2-135M-shaped causal LM (30 layers, hidden 576, 9 query / 3 KV heads of 64,
+SwiGLU FFN 1536, vocab 49152, tied embeddings, RMSNorm eps 1e-5, RoPE theta 100000), fp32,
+random init N(0, 0.02) from a seed with every RMSNorm gamma 1, batch 1 x 512 uniform-random token
+ids. One step: forward logits, the argmax of the last position's logits seeded with its value
+(on device), the AttnLRP relevance pass (LXT settings: epsilon 1e-9, bias in the denominator) back
+to the embeddings, and per-token relevance sums. The ids are resident in HBM before the timed
+region; every step launches the whole path (a HIP graph of it in graph mode).
+
+Prints one JSON line. `roofline` is the dominant GEMM kernel's algorithmic fp32 FLOP rate (timed
+with HIP events on the backend's stream) against MI355X's 157.3 TFLOP/s dense fp32 matrix peak.
+`cpu_baseline` times the reference CPUBackend (oracle/_ref where built, else the oracle
+restatement) on the host cores: the same model at 1 and 3 layers, extrapolated linearly to 30.
+"""
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+FP32_MFMA_PEAK_TFLOPS = 157.3
+HBM_PEAK_GBS = 8000.0
+LXT_EPS = 1e-9
+
+S_CONFIG = dict(vocab_size=49152, hidden_size=576, num_layers=30, num_heads=9, num_kv_heads=3, head_dim=64,
+                intermediate_size=1536, rms_norm_eps=1e-5, rope_theta=100000.0, use_rope=1, rope_rotate_half=1,
+                causal=1, qkv_bias=0, out_bias=0, mlp_bias=0, tie_word_embeddings=1, reserved=0)
+BATCH, SEQ, SEED = 1, 512, 1234
+
+
+def gemm_flops_per_sequence(c, L, causal_effective):
+    """Algorithmic GEMM FLOPs of one forward + AttnLRP pass (dense L^2 attention squares, as the
+    reference computes them; causal_effective counts only the lower triangle)."""
+    d, H, Hkv, D, F, V, layers = (c["hidden_size"], c["num_heads"], c["num_kv_heads"], c["head_dim"],
+                                  c["intermediate_size"], c["vocab_size"], c["num_layers"])
+    qd, kvd = H * D, Hkv * D
+    proj = 2 * L * d * (qd + 2 * kvd) + 2 * L * qd * d
+    mlp = 2 * L * d * 2 * F + 2 * L * F * d
+    att = 2 * (2 * H * L * L * D)  # Q K^T and P V
+    if causal_effective:
+        att = att * (L + 1) / (2 * L)
+    head = 2 * L * d * V
+    fwd = layers * (proj + mlp + att) + head
+    rel = layers * (proj + mlp + 2 * att) + head  # Linear-transposed GEMMs; both bilinear shares of each product
+    return fwd + rel
+
+
+def time_cpu_baseline(cfg_fields, seq):
+    """Reference CPUBackend on the host cores, 1 and 3 layers, extrapolated to the full depth."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle_ctypes as oc
+
+    lib, kind = oc.ref(), "reference"
+    if lib is None:
+        lib, kind = oc.oracle(), "port"
+    ids = np.random.RandomState(SEED).randint(0, cfg_fields["vocab_size"], size=(1, seq))
+    times = {}
+    for layers in (1, 3):
+        f = dict(cfg_fields, num_layers=layers)
+        cfg = oc.model_config(**f)
+        params = oc.synthetic_params(cfg, SEED)
+        lm = lib.lm(cfg, params)
+        t0 = time.perf_counter()
+        logits = lm.forward(ids)
+        seed = np.zeros_like(logits)
+        t = int(np.argmax(logits[0, -1]))
+        seed[0, -1, t] = logits[0, -1, t]
+        lm.relevance(seed, LXT_EPS, True)
+        times[layers] = time.perf_counter() - t0
+        del lm
+    per_layer = (times[3] - times[1]) / 2.0
+    full = times[1] + (cfg_fields["num_layers"] - 1) * per_layer
+    cores = oc.oracle().lib.pxo_get_threads()
+    return {
+        "value": round(seq / full, 3),
+        "unit": "tokens/s",
+        "cores": int(cores),
+        "kind": kind,
+        "sample": "1 sequence x %d tokens at the full shape with 1 and 3 of %d layers (%.1f s, %.1f s); "
+                  "time extrapolated per layer to %d layers = %.1f s; GEMMs on %d std::threads "
+                  "(cpu_backend.cpp:38-59), everything else single-threaded"
+                  % (seq, cfg_fields["num_layers"], times[1], times[3], cfg_fields["num_layers"], full, cores),
+        "cpu_model": cpu_model(),
+        "nproc": os.cpu_count(),
+    }
+
+
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def time_kernel(torch, stream, launch, reps):
+    """Average duration of `launch()` over reps, HIP events recorded on `stream`."""
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    launch()
+    e0.record(stream)
+    for _ in range(reps):
+        launch()
+    e1.record(stream)
+    e1.synchronize()
+    return e0.elapsed_time(e1) / reps * 1e-3  # seconds
+
+
+def head_relevance_gemm(torch, N, c, L):
+    """The LM head's relevance GEMM exactly as TiedLMHeadModule::run_relevance launches it:
+    r_in (L x d) = x * ((R / stab(logits)) E), K = vocab, split-K."""
+    V, d = c["vocab_size"], c["hidden_size"]
+    g = torch.Generator(device="cuda").manual_seed(1)
+    R = torch.zeros(L, V, device="cuda")
+    R[-1, 7] = 3.0
+    Z = torch.randn(L, V, device="cuda", generator=g)
+    E = torch.randn(V, d, device="cuda", generator=g) * 0.02
+    X = torch.randn(L, d, device="cuda", generator=g)
+    out = torch.empty(L, d, device="cuda")
+    desc = N.GemmDesc()
+    desc.m, desc.n, desc.k, desc.batch, desc.inner, desc.kgroups = L, d, V, 1, 1, 1
+    desc.prologue, desc.epilogue, desc.eps = N.PRO_DIV_STAB, N.EPI_MUL_X, LXT_EPS
+    desc.a = N.operand(R.data_ptr(), V)
+    desc.z = N.operand(Z.data_ptr(), V)
+    desc.b = N.operand(E.data_ptr(), d)
+    desc.c = N.operand(out.data_ptr(), d)
+    desc.x = N.operand(X.data_ptr(), d)
+    ws_bytes = N.gemm_workspace(desc)
+    ws = torch.empty(max(ws_bytes // 4, 1), device="cuda")
+    desc.workspace, desc.workspace_bytes = ws.data_ptr(), ws_bytes
+    keep = (R, Z, E, X, out, ws)
+    return desc, 2.0 * L * V * d, keep
+
+
+def mlp_gate_up_gemm(torch, N, c, L):
+    """The MLP's [gate | up] forward GEMM as SwiGLUModule::run_forward launches it (L x d x 2F)."""
+    d, F = c["hidden_size"], c["intermediate_size"]
+    g = torch.Generator(device="cuda").manual_seed(2)
+    A = torch.randn(L, d, device="cuda", generator=g)
+    B = torch.randn(d, 2 * F, device="cuda", generator=g) * 0.02
+    C = torch.empty(L, 2 * F, device="cuda")
+    desc = N.GemmDesc()
+    desc.m, desc.n, desc.k, desc.batch, desc.inner, desc.kgroups = L, 2 * F, d, 1, 1, 1
+    desc.a = N.operand(A.data_ptr(), d)
+    desc.b = N.operand(B.data_ptr(), 2 * F)
+    desc.c = N.operand(C.data_ptr(), 2 * F)
+    return desc, 2.0 * L * d * 2 * F, (A, B, C)
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--mode", choices=("graph", "eager"), default="graph")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--layers", type=int, default=S_CONFIG["num_layers"], help=argparse.SUPPRESS)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py: this build measures one MI355X (the path runs on one GPU; --gpus %d is not supported)"
+              % args.gpus, file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from pulsatrix_amd import models
+    from pulsatrix_amd import native as N
+
+    fields = dict(S_CONFIG, num_layers=args.layers)
+    cfg = N.model_config(**fields)
+    t_setup = time.perf_counter()
+    lm = models.CausalLM(cfg, seed=SEED, std=0.02)
+    ids_host = np.random.RandomState(SEED).randint(0, cfg.vocab_size, size=(BATCH, SEQ)).astype(np.float32)
+    ids = torch.from_numpy(ids_host).cuda()
+    tok = torch.empty(BATCH * SEQ, device="cuda")
+    tgt = torch.empty(BATCH, dtype=torch.int64, device="cuda")
+    torch.cuda.synchronize()
+    stream = torch.cuda.ExternalStream(models.stream())
+
+    def eager_step():
+        lm.explain_device(ids.data_ptr(), BATCH, SEQ, LXT_EPS, 1, tok.data_ptr(), tgt.data_ptr())
+
+    for _ in range(max(1, args.warmup)):
+        eager_step()
+    models.synchronize()
+    step = eager_step
+    if args.mode == "graph":
+        lm.capture_explain(ids.data_ptr(), BATCH, SEQ, LXT_EPS, 1, tok.data_ptr(), tgt.data_ptr())
+        step = lm.replay
+        for _ in range(max(1, args.warmup)):
+            step()
+        models.synchronize()
+    setup_s = time.perf_counter() - t_setup
+
+    # ---- timed region: K steps, synchronized on both sides -------------------------------------
+    torch.cuda.synchronize()
+    models.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for _ in range(args.steps):
+        step()
+    e1.record(stream)
+    models.synchronize()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    gpu_s = e0.elapsed_time(e1) * 1e-3
+    relevance = tok.cpu().numpy()
+    if not np.all(np.isfinite(relevance)):
+        print("bench.py: non-finite relevance", file=sys.stderr)
+        sys.exit(1)
+
+    tokens = BATCH * SEQ * args.steps
+    value = tokens / wall
+    flops_dense = gemm_flops_per_sequence(fields, SEQ, False) * BATCH
+    flops_causal = gemm_flops_per_sequence(fields, SEQ, True) * BATCH
+
+    # ---- roofline of the dominant GEMM kernel, HIP events on the backend's stream ---------------
+    desc, flops, keep = head_relevance_gemm(torch, N, fields, SEQ)
+    ker_s = time_kernel(torch, stream, lambda: N.gemm(desc, models.stream()), 20)
+    desc2, flops2, keep2 = mlp_gate_up_gemm(torch, N, fields, SEQ)
+    ker2_s = time_kernel(torch, stream, lambda: N.gemm(desc2, models.stream()), 50)
+    achieved = flops / ker_s / 1e12
+
+    out = {
+        "metric": "forward+AttnLRP tokens/s, 135M-shape LM seq 512; GEMM % fp32 MFMA peak",
+        "value": round(value, 2),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall / args.steps * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic: random-init N(0,0.02) weights from seed %d, uniform-random token ids" % SEED,
+        "config": {
+            "workload": "SmolLM2-135M-shaped causal LM forward + AttnLRP (LxtAttnLrpConfig: eps 1e-9, bias in "
+                        "denominator), argmax seed at the last position, batch 1 x seq 512",
+            "layers": fields["num_layers"], "hidden": 576, "heads": "9/3", "head_dim": 64, "ffn": 1536,
+            "vocab": 49152, "tied": True, "rope_theta": 100000.0, "global_batch": BATCH, "seq_len": SEQ,
+            "parallelism": "single GPU", "mode": args.mode,
+        },
+        "gpu_time_ms_per_step": round(gpu_s / args.steps * 1e3, 4),
+        "path_gemm_gflop_per_step": {"dense": round(flops_dense / 1e9, 2), "causal": round(flops_causal / 1e9, 2)},
+        "path_tflops_dense": round(flops_dense * args.steps / wall / 1e12, 2),
+        "roofline": {
+            "kernel": "pxk gemm_kernel<64,64,NN,DIV_STAB,MUL_X> + split-K reduce: LM-head relevance "
+                      "512 x 576 x 49152",
+            "bound": "mfma",
+            "achieved": round(achieved, 2),
+            "peak": FP32_MFMA_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / FP32_MFMA_PEAK_TFLOPS, 4),
+            "traffic": None,
+            "avg_launch_us": round(ker_s * 1e6, 2),
+            "algorithmic_gflop_per_launch": round(flops / 1e9, 3),
+        },
+        "kernels": {
+            "mlp_gate_up_512x576x3072": {"avg_us": round(ker2_s * 1e6, 2),
+                                         "tflops": round(flops2 / ker2_s / 1e12, 2)},
+        },
+        "setup_s": round(setup_s, 1),
+    }
+    del keep, keep2
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = time_cpu_baseline(fields, SEQ)
+        out["gpu_vs_cpu"] = round(value / out["cpu_baseline"]["value"], 1)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()
