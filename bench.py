@@ -231,6 +231,8 @@ def main():
     desc2, flops2, keep2 = mlp_gate_up_gemm(torch, N, fields, SEQ)
     ker2_s = time_kernel(torch, stream, lambda: N.gemm(desc2, models.stream()), 50)
     achieved = flops / ker_s / 1e12
+    tile, splits = N.gemm_plan(desc)
+    tile_name = {N.TILE_128x128: "128x128", N.TILE_64x64: "64x64", N.TILE_32x64: "32x64", N.TILE_32x32: "32x32"}[tile]
 
     out = {
         "metric": "forward+AttnLRP tokens/s, 135M-shape LM seq 512; GEMM % fp32 MFMA peak",
@@ -256,8 +258,9 @@ def main():
         "path_gemm_gflop_per_step": {"dense": round(flops_dense / 1e9, 2), "causal": round(flops_causal / 1e9, 2)},
         "path_tflops_dense": round(flops_dense * args.steps / wall / 1e12, 2),
         "roofline": {
-            "kernel": "pxk gemm_kernel<64,64,NN,DIV_STAB,MUL_X> + split-K reduce: LM-head relevance "
-                      "512 x 576 x 49152",
+            "kernel": "pxk_gemm NN, DIV_STAB prologue, MUL_X epilogue (LM-head relevance 512 x 576 x 49152): "
+                      "gemm_kernel %s tiles with split-K %d%s" % (tile_name, splits,
+                                                                 " + splitk_reduce_kernel" if splits > 1 else ""),
             "bound": "mfma",
             "achieved": round(achieved, 2),
             "peak": FP32_MFMA_PEAK_TFLOPS,

@@ -35,8 +35,9 @@ const char* pxk_version(void);
 
 /* ---- the fused fp32 MFMA GEMM ------------------------------------------------------------------
  * C[b] = op(Aeff[b]) * op(B[b]) over a batch of independent products, fp32 in, fp32 MFMA
- * (v_mfma_f32_16x16x4_f32) with fp32 accumulation, LDS-staged double-buffered 64x64 or 128x128
- * tiles, optional deterministic split-K (fixed-order reduction, no atomics in the sum).
+ * (v_mfma_f32_16x16x4_f32) with fp32 accumulation, LDS-staged double-buffered tiles of 128x128,
+ * 64x64, 32x64 or 32x32 (the small ones split each K stage over their four waves), optional
+ * deterministic split-K (fixed-order reduction, no atomics in the sum).
  *
  * Batch addressing, per operand: batch index b = outer * inner + i (inner = desc.inner), and
  *   base(b, s) = ptr + outer * batch_stride + (i / inner_div) * inner_stride + s * group_stride
@@ -84,6 +85,14 @@ enum {
                                 C2 = rg / stab(Z3 + bias2[n]) (up). Z stays the prologue's. */
 };
 
+enum {
+    PXK_TILE_AUTO = 0,
+    PXK_TILE_128x128 = 1, /* 4 waves of 64x64, K stage 32 */
+    PXK_TILE_64x64 = 2,   /* 4 waves of 32x32, K stage 32 */
+    PXK_TILE_32x64 = 3,   /* 4 waves each on a quarter of a 64-wide K stage, summed in LDS */
+    PXK_TILE_32x32 = 4    /* as 32x64 */
+};
+
 typedef struct pxk_gemm_desc {
     int64_t m, n, k;
     int64_t batch;   /* >= 1 */
@@ -109,7 +118,7 @@ typedef struct pxk_gemm_desc {
     const float* sin_t;
     int64_t head_dim;     /* ROPE_REL: pairs live inside each head_dim-wide column block */
     int32_t rope_half;    /* 1: pair (i, i + D/2); 0: pair (2i, 2i+1) */
-    int32_t reserved;
+    int32_t tile;         /* 0 = chosen by the library; else PXK_TILE_* (a tuning override) */
     float* workspace;     /* split-K partials */
     size_t workspace_bytes;
 } pxk_gemm_desc;
@@ -117,6 +126,10 @@ typedef struct pxk_gemm_desc {
 /* Bytes of workspace pxk_gemm needs for this descriptor (0 when it runs without split-K). */
 size_t pxk_gemm_workspace(const pxk_gemm_desc* d);
 int pxk_gemm(const pxk_gemm_desc* d, void* stream);
+
+/* The tile shape (PXK_TILE_*) and split-K count pxk_gemm would launch for this descriptor, after
+ * the same validation. Introspection for tuning and tests; no reference counterpart. */
+int pxk_gemm_plan(const pxk_gemm_desc* d, int32_t* tile, int32_t* splits);
 
 /* The (trans_a, trans_b, prologue, epilogue) combinations built into the library; pxk_gemm
  * rejects others with PXK_ERR_INVALID. */

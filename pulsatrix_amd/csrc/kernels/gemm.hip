@@ -1,21 +1,38 @@
 // gemm.hip -- the fused fp32 MFMA GEMM for gfx950 (pxk_gemm, include/pxk.h).
 //
-// Tiling. A workgroup of 256 threads (4 wave64s in a 2x2 grid) owns a BM x BN output tile
-// (64x64 or 128x128). K advances in blocks of 16 staged through LDS, double-buffered: the next
-// block's global loads are in flight while the MFMA pipe works on the current one. LDS holds A as
-// [BM][16+4] and B as [BN][16+4], both K-contiguous, so each lane fetches its MFMA operands for a
-// whole K block with one 128-bit ds_read per 16x16 sub-tile.
+// Tiling. A workgroup of 256 threads (four wave64s) owns a BM x BN output tile. K advances in
+// stages of BK staged through LDS, double-buffered: the next stage's global loads are in flight
+// while the MFMA pipe works on the current one, and one barrier per stage separates them.
+//   128x128 and 64x64: the waves form a 2x2 grid of 64x64 / 32x32 wave tiles, BK = 32.
+//   32x64 and 32x32: every wave owns the whole tile and a quarter of a BK = 64 stage; the four
+//   partial tiles are summed in LDS in wave order at the end. This keeps four waves busy on tiles
+//   small enough that a 512-token GEMM still spreads over all 256 CUs without split-K.
+//
+// LDS layout. Each operand is kept in the contiguity it has in HBM, so every global->LDS move is
+// a 128-bit load and a 128-bit ds_write. A K-contiguous operand sits as [rows][BK + 4] and a lane
+// fetches its fragment for a 16-wide K chunk with one ds_read_b128; an M- or N-contiguous operand
+// sits as [BK][cols + 4] and a lane fetches its four K values with four ds_read_b32 that the
+// 4-float row padding keeps free of bank conflicts.
 //
 // MFMA mapping. v_mfma_f32_16x16x4_f32 multiplies a 16x4 by a 4x16 fragment; lane l supplies
 // A[l%16][kk] and B[kk][l%16] with kk = l/16, and holds D[4*(l/16)+r][l%16] in its r-th result
-// register. Lane group g = l/16 is given K indices 4g..4g+3 of the block, one per MFMA step, so
-// four steps cover the 16-wide block with operands read as float4 from LDS.
+// register. Lane group g = l/16 is given K indices 16c + 4g + s (chunk c, MFMA step s), so a
+// K-contiguous fragment for all four steps is one float4.
 //
-// Epilogue. The accumulator tile is staged through LDS and then walked row-major by the whole
-// workgroup, so global writes (and the reads of epilogue operands) are coalesced and an element
-// can see its RoPE pair partner. Split-K writes raw partials to a workspace instead; a second
-// kernel sums them in split order (deterministic, no atomics) and runs the same tile epilogue.
+// Grid. One-dimensional, M-tile fastest, then N-tile, then (batch, split). When the tile count is
+// a multiple of 8 the block index is regrouped so that each of the 8 XCDs receives one contiguous
+// run of tiles: the M-tiles sharing one B panel then run together on the XCD whose L2 holds it.
+//
+// Epilogue. The accumulator tile is staged through LDS and walked row-major in float4 columns by
+// the whole workgroup, so global writes (and the reads of epilogue operands) are 128-bit and
+// coalesced, and an element can see its RoPE pair partner. Split-K writes raw partials to a
+// workspace instead; a second kernel sums them in split order (deterministic, no atomics) over
+// row slabs and runs the same epilogue.
+#include <algorithm>
+#include <cmath>
 #include <cstring>
+#include <type_traits>
+#include <utility>
 
 #include "common.hpp"
 
@@ -38,35 +55,98 @@ struct Args {
     const float* sin_t;
     int64_t head_dim;
     int rope_half;
-    int vec_a, vec_b;
+    int vec_a, vec_b, vec_e;  // 128-bit global access allowed: A (and Z), B, epilogue operands
+    int tiles_m, tiles_n, bm;
+    int remap;  // XCD-grouped block order
     float* ws;
 };
 
+// Batch and group counts fit 32 bits (the host checks the grid), so the index splits use 32-bit
+// division; batch 0 of group 0 (every unbatched GEMM) needs none.
 __device__ __forceinline__ const float* obase(const Op& o, int64_t b, int64_t inner, int64_t s) {
-    const int64_t bo = b / inner, bi = b % inner;
-    const int64_t d = o.div > 1 ? o.div : 1;
-    return o.p + bo * o.so + (bi / d) * o.si + s * o.sg;
+    if (b == 0) return o.p + s * o.sg;
+    const uint32_t bb = static_cast<uint32_t>(b), in = static_cast<uint32_t>(inner);
+    const uint32_t bo = bb / in, bi = bb - bo * in;
+    const uint32_t d = o.div > 1 ? static_cast<uint32_t>(o.div) : 1u;
+    return o.p + static_cast<int64_t>(bo) * o.so + static_cast<int64_t>(bi / d) * o.si + s * o.sg;
 }
 __device__ __forceinline__ float* obase_w(const Op& o, int64_t b, int64_t inner) {
     return const_cast<float*>(obase(o, b, inner, 0));
 }
 
-constexpr int BK = 16;
-constexpr int LDK = BK + 4;
 constexpr int NT = 256;
+// Kernel-side prologue variants: PXK_PRO_NONE, PXK_PRO_DIV_STAB without a bias over k, and with one.
+constexpr int kProStabBias = 2;
 
-template <int BM, int BN>
-struct Smem {
-    static constexpr int AB = 2 * (BM + BN) * LDK;
+// NS_: register sets of prefetched stages. Stage t + 1 .. t + NS are in flight while stage t is
+// on the MFMA pipe, so the short stages of the small tiles still cover a global load's latency.
+template <int BM_, int BN_, int WM_, int WN_, int KS_, int NS_>
+struct Cfg {
+    static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, KS = KS_, NS = NS_;
+    static_assert(WM * WN * KS == 4, "four waves per workgroup");
+    static constexpr int TM = BM / WM / 16, TN = BN / WN / 16;  // 16x16 MFMA tiles per wave
+    static constexpr int CH = KS == 1 ? 2 : 1;                   // 16-wide K chunks per wave per stage
+    static constexpr int BK = 16 * KS * CH;
     static constexpr int LDC = BN + 4;
-    static constexpr int C = BM * LDC;
-    static constexpr int SIZE = AB > C ? AB : C;
 };
 
-// ---- tile epilogue: acc tile in LDS (Cs[BM][LDC]) -> outputs --------------------------------------
-template <int BM, int BN, int EPI>
-__device__ void epilogue_tile(const float* Cs, int64_t m0, int64_t n0, int64_t b, const Args& g) {
-    constexpr int LDC = Smem<BM, BN>::LDC;
+using C128 = Cfg<128, 128, 2, 2, 1, 1>;
+using C64 = Cfg<64, 64, 2, 2, 1, 3>;
+using C32x64 = Cfg<32, 64, 1, 1, 4, 2>;
+using C32 = Cfg<32, 32, 1, 1, 4, 3>;
+
+template <class F, int... Is>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, Is...>) {
+    (f(std::integral_constant<int, Is>{}), ...);
+}
+// f(integral_constant<int, 0>), ..., f(integral_constant<int, N - 1>): register arrays indexed by
+// the constant stay in registers.
+template <int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+    static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+// LDS footprint of one operand panel: R rows of M (or N) by BK of K.
+template <int R, int BK, bool KC>
+struct Panel {
+    static constexpr int LD = KC ? BK + 4 : R + 4;
+    static constexpr int SIZE = KC ? R * LD : BK * LD;
+    static constexpr int NV = R * BK / 4 / NT;  // float4 moved per thread per stage
+    static_assert(NV >= 1 && R * BK % (4 * NT) == 0, "panel must split evenly over the workgroup");
+};
+
+template <class C, bool TA, bool TB>
+struct Layout {
+    using PA = Panel<C::BM, C::BK, !TA>;
+    using PB = Panel<C::BN, C::BK, TB>;
+    static constexpr int STAGE = PA::SIZE + PB::SIZE;
+    static constexpr int PART = C::BM * C::LDC;
+    static constexpr int SIZE = 2 * STAGE > C::KS * PART ? 2 * STAGE : C::KS * PART;
+};
+
+// ---- 128-bit epilogue access with a scalar tail ------------------------------------------------------
+__device__ __forceinline__ f4 ld4(const float* p, bool vec, int cnt) {
+    if (vec) return *reinterpret_cast<const f4*>(p);
+    f4 v = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        if (j < cnt) v[j] = p[j];
+    return v;
+}
+__device__ __forceinline__ void st4(float* p, f4 v, bool vec, int cnt) {
+    if (vec) {
+        *reinterpret_cast<f4*>(p) = v;
+        return;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        if (j < cnt) p[j] = v[j];
+}
+
+// ---- tile epilogue: ROWS x BN accumulator rows in LDS (Cs[ROWS][ldc]) -> outputs -----------------------
+template <int ROWS, int BN, int EPI>
+__device__ void epilogue_rows(const float* Cs, int ldc, int64_t m0, int64_t n0, int64_t b, const Args& g) {
+    constexpr int CPR = BN / 4;  // float4 columns per row
     const int tid = threadIdx.x;
     const int64_t inner = g.inner;
     float* C = g.c.p ? obase_w(g.c, b, inner) : nullptr;
@@ -81,206 +161,268 @@ __device__ void epilogue_tile(const float* Cs, int64_t m0, int64_t n0, int64_t b
     const float* EB = g.eb.p ? obase(g.eb, b, inner, 0) : nullptr;
     const float* EB2 = g.eb2.p ? obase(g.eb2, b, inner, 0) : nullptr;
     const float eps = g.eps;
-#pragma unroll 4
-    for (int e = tid; e < BM * BN; e += NT) {
-        const int row = e / BN, col = e % BN;
+#pragma unroll 2
+    for (int it = tid; it < ROWS * CPR; it += NT) {
+        const int row = it / CPR, col = 4 * (it % CPR);
         const int64_t m = m0 + row, n = n0 + col;
         if (m >= g.M || n >= g.N) continue;
-        const float acc = Cs[row * LDC + col];
+        const int cnt = g.N - n < 4 ? static_cast<int>(g.N - n) : 4;
+        const bool vec = g.vec_e && cnt == 4;
+        const f4 acc = *reinterpret_cast<const f4*>(Cs + row * ldc + col);
         if constexpr (EPI == PXK_EPI_STORE) {
             float* dst = C + m * g.c.ld + n;
-            *dst = (g.beta == 0.0f) ? acc : g.beta * *dst + acc;
-        } else if constexpr (EPI == PXK_EPI_STORE_BIAS) {
-            C[m * g.c.ld + n] = acc;
-            if (EB) C2[m * g.c2.ld + n] = acc + EB[n];
-        } else if constexpr (EPI == PXK_EPI_ADD_RESID) {
-            C[m * g.c.ld + n] = acc;
-            float y = acc;
-            if (EB) {
-                y = acc + EB[n];
-                C2[m * g.c2.ld + n] = y;
+            f4 v = acc;
+            if (g.beta != 0.0f) {
+                const f4 old = ld4(dst, vec, cnt);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) v[j] = g.beta * old[j] + acc[j];
             }
-            C3[m * g.c3.ld + n] = X[m * g.x.ld + n] + y;
+            st4(dst, v, vec, cnt);
+        } else if constexpr (EPI == PXK_EPI_STORE_BIAS) {
+            st4(C + m * g.c.ld + n, acc, vec, cnt);
+            if (EB) st4(C2 + m * g.c2.ld + n, acc + ld4(EB + n, vec, cnt), vec, cnt);
+        } else if constexpr (EPI == PXK_EPI_ADD_RESID) {
+            st4(C + m * g.c.ld + n, acc, vec, cnt);
+            f4 y = acc;
+            if (EB) {
+                y = acc + ld4(EB + n, vec, cnt);
+                st4(C2 + m * g.c2.ld + n, y, vec, cnt);
+            }
+            st4(C3 + m * g.c3.ld + n, ld4(X + m * g.x.ld + n, vec, cnt) + y, vec, cnt);
         } else if constexpr (EPI == PXK_EPI_MUL_X) {
-            float v = X[m * g.x.ld + n] * acc;
-            if (Y) v = Y[m * g.y.ld + n] + v;
-            C[m * g.c.ld + n] = v;
+            f4 v = ld4(X + m * g.x.ld + n, vec, cnt) * acc;
+            if (Y) v = ld4(Y + m * g.y.ld + n, vec, cnt) + v;
+            st4(C + m * g.c.ld + n, v, vec, cnt);
         } else if constexpr (EPI == PXK_EPI_SPV) {
-            const float o = X[m * g.x.ld + n];
-            const float r = o * acc;
-            C[m * g.c.ld + n] = r / (2.0f * o + eps * ((o >= 0.0f) ? 1.0f : -1.0f));
+            const f4 o = ld4(X + m * g.x.ld + n, vec, cnt);
+            f4 v;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float r = o[j] * acc[j];
+                v[j] = r / (2.0f * o[j] + eps * ((o[j] >= 0.0f) ? 1.0f : -1.0f));
+            }
+            st4(C + m * g.c.ld + n, v, vec, cnt);
         } else if constexpr (EPI == PXK_EPI_ROPE_REL) {
             // Pair (lo, hi) inside the head block holding n; the tile spans whole heads.
             const int64_t D = g.head_dim, half = D / 2;
-            const int64_t d = n % D, hb = n - d;
-            const int64_t i = g.rope_half ? (d < half ? d : d - half) : d / 2;
-            const int64_t lo = hb + (g.rope_half ? i : 2 * i), hi = hb + (g.rope_half ? i + half : 2 * i + 1);
-            const bool is_lo = (n == lo);
-            const float acc_lo = Cs[row * LDC + (int)(lo - n0)], acc_hi = Cs[row * LDC + (int)(hi - n0)];
-            const float y_lo = Y[m * g.y.ld + lo], y_hi = Y[m * g.y.ld + hi];
-            const float r_lo = y_lo * acc_lo, r_hi = y_hi * acc_hi;  // bilinear share: Q (or K) * (S @ K)
-            const float c = g.cos_t[m * half + i], s = g.sin_t[m * half + i];
-            const float d0 = stab(y_lo, eps), d1 = stab(y_hi, eps);
-            const float xv = X[m * g.x.ld + n];
-            float r_in = 0.0f;
-            if (is_lo) {
-                r_in += (xv * c / d0) * r_lo;
-                r_in += (xv * s / d1) * r_hi;
-            } else {
-                r_in += (xv * -s / d0) * r_lo;
-                r_in += (xv * c / d1) * r_hi;
+            const f4 xv = ld4(X + m * g.x.ld + n, vec, cnt);
+            const f4 zv = ld4(Z + m * g.z.ld + n, vec, cnt);
+            const f4 bv = EB ? ld4(EB + n, vec, cnt) : f4{0.f, 0.f, 0.f, 0.f};
+            f4 rin, rz;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                if (j >= cnt) {  // past the last column: nothing stored
+                    rin[j] = rz[j] = 0.0f;
+                    continue;
+                }
+                const int64_t nj = n + j;
+                const int64_t d = nj % D, hb = nj - d;
+                const int64_t i = g.rope_half ? (d < half ? d : d - half) : d / 2;
+                const int64_t lo = hb + (g.rope_half ? i : 2 * i), hi = hb + (g.rope_half ? i + half : 2 * i + 1);
+                const float acc_lo = Cs[row * ldc + static_cast<int>(lo - n0)];
+                const float acc_hi = Cs[row * ldc + static_cast<int>(hi - n0)];
+                const float y_lo = Y[m * g.y.ld + lo], y_hi = Y[m * g.y.ld + hi];
+                const float r_lo = y_lo * acc_lo, r_hi = y_hi * acc_hi;  // bilinear share: Q (or K) * (S @ K)
+                const float c = g.cos_t[m * half + i], s = g.sin_t[m * half + i];
+                const float d0 = stab(y_lo, eps), d1 = stab(y_hi, eps);
+                float r_in = 0.0f;
+                if (nj == lo) {
+                    r_in += (xv[j] * c / d0) * r_lo;
+                    r_in += (xv[j] * s / d1) * r_hi;
+                } else {
+                    r_in += (xv[j] * -s / d0) * r_lo;
+                    r_in += (xv[j] * c / d1) * r_hi;
+                }
+                rin[j] = r_in;
+                const float zb = EB ? zv[j] + bv[j] : zv[j];
+                rz[j] = r_in / stab(zb, eps);
             }
-            if (C) C[m * g.c.ld + n] = r_in;
-            const float zb = EB ? Z[m * g.z.ld + n] + EB[n] : Z[m * g.z.ld + n];
-            C2[m * g.c2.ld + n] = r_in / stab(zb, eps);
+            if (C) st4(C + m * g.c.ld + n, rin, vec, cnt);
+            st4(C2 + m * g.c2.ld + n, rz, vec, cnt);
         } else if constexpr (EPI == PXK_EPI_VALUE_REL) {
-            const float r = Y[m * g.y.ld + n] * acc;
-            if (C) C[m * g.c.ld + n] = r;
-            const float zb = EB ? Z[m * g.z.ld + n] + EB[n] : Z[m * g.z.ld + n];
-            C2[m * g.c2.ld + n] = r / stab(zb, eps);
+            const f4 r = ld4(Y + m * g.y.ld + n, vec, cnt) * acc;
+            if (C) st4(C + m * g.c.ld + n, r, vec, cnt);
+            const f4 zv = ld4(Z + m * g.z.ld + n, vec, cnt);
+            const f4 bv = EB ? ld4(EB + n, vec, cnt) : f4{0.f, 0.f, 0.f, 0.f};
+            f4 v;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) v[j] = r[j] / stab(EB ? zv[j] + bv[j] : zv[j], eps);
+            st4(C2 + m * g.c2.ld + n, v, vec, cnt);
         } else if constexpr (EPI == PXK_EPI_SWIGLU_REL) {
-            const float rh = X[m * g.x.ld + n] * acc;  // hidden * (g_down @ W_down^T)
-            const float a = Y[m * g.y.ld + n], bb = W[m * g.w.ld + n];
-            const float cc = a * bb;
-            const float denom = 2.0f * cc + eps * ((cc >= 0.0f) ? 1.0f : -1.0f);
-            const float rg = (a * bb / denom) * rh;  // lrp_math.hpp:41-45
-            const float zg = EB ? Z2[m * g.z2.ld + n] + EB[n] : Z2[m * g.z2.ld + n];
-            const float zu = EB2 ? Z3[m * g.z3.ld + n] + EB2[n] : Z3[m * g.z3.ld + n];
-            C[m * g.c.ld + n] = rg / stab(zg, eps);
-            C2[m * g.c2.ld + n] = rg / stab(zu, eps);
+            const f4 rh = ld4(X + m * g.x.ld + n, vec, cnt) * acc;  // hidden * (g_down @ W_down^T)
+            const f4 a = ld4(Y + m * g.y.ld + n, vec, cnt), bb = ld4(W + m * g.w.ld + n, vec, cnt);
+            const f4 zg = ld4(Z2 + m * g.z2.ld + n, vec, cnt), zu = ld4(Z3 + m * g.z3.ld + n, vec, cnt);
+            const f4 bg = EB ? ld4(EB + n, vec, cnt) : f4{0.f, 0.f, 0.f, 0.f};
+            const f4 bu = EB2 ? ld4(EB2 + n, vec, cnt) : f4{0.f, 0.f, 0.f, 0.f};
+            f4 o1, o2;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float cc = a[j] * bb[j];
+                const float denom = 2.0f * cc + eps * ((cc >= 0.0f) ? 1.0f : -1.0f);
+                const float rg = (a[j] * bb[j] / denom) * rh[j];  // lrp_math.hpp:41-45
+                o1[j] = rg / stab(EB ? zg[j] + bg[j] : zg[j], eps);
+                o2[j] = rg / stab(EB2 ? zu[j] + bu[j] : zu[j], eps);
+            }
+            st4(C + m * g.c.ld + n, o1, vec, cnt);
+            st4(C2 + m * g.c2.ld + n, o2, vec, cnt);
         }
     }
 }
 
-// ---- global -> register loads of one K block --------------------------------------------------------
-template <int BM, int BN, bool TA, bool TB, int PRO>
-struct Loader {
-    static constexpr int AF = BM * BK / 4 / NT;  // float4 slots per thread (A)
-    static constexpr int BF = BN * BK / 4 / NT;
-    f4 ra[AF];
-    f4 rb[BF];
+// ---- global -> registers -> LDS for one operand panel ------------------------------------------------
+// KC: the operand is stored K-contiguous ((rows of M or N) x K); else (K x (M or N)). `mn` is the
+// stored extent along M (or N). issue() only starts the global loads; commit() waits for them,
+// applies the DIV_STAB prologue (operand A only) and writes LDS, so the loads of a stage overlap
+// the MFMAs of the stages before it.
+template <int R, int BK, bool KC, int PRO>
+struct PanelLoader {
+    using P = Panel<R, BK, KC>;
+    static constexpr bool DS = PRO != PXK_PRO_NONE;
+    static constexpr bool HB = PRO == kProStabBias;
+    f4 v[P::NV];
+    f4 z[DS ? P::NV : 1];   // prologue denominators
+    f4 zb[HB ? P::NV : 1];  // prologue bias over k
 
-    __device__ __forceinline__ void load(const Args& g, const float* A, const float* Z, const float* ZB,
-                                         const float* B, int64_t m0, int64_t n0, int64_t k0) {
-        const int tid = threadIdx.x;
-#pragma unroll
-        for (int i = 0; i < AF; ++i) {
-            const int idx = tid + i * NT;
-            int64_t r, c;  // stored coordinates: (row, first of 4 contiguous)
-            if constexpr (!TA) {
-                r = m0 + idx / (BK / 4);
-                c = k0 + 4 * (idx % (BK / 4));
-            } else {
-                r = k0 + idx / (BM / 4);
-                c = m0 + 4 * (idx % (BM / 4));
-            }
-            const int64_t rows = TA ? g.K : g.M, cols = TA ? g.M : g.K;
-            f4 v = {0.f, 0.f, 0.f, 0.f};
-            f4 zv = {0.f, 0.f, 0.f, 0.f};
-            if (r < rows) {
-                if (g.vec_a && c + 3 < cols) {
-                    v = *reinterpret_cast<const f4*>(A + r * g.a.ld + c);
-                    if constexpr (PRO == PXK_PRO_DIV_STAB) zv = *reinterpret_cast<const f4*>(Z + r * g.z.ld + c);
-                } else {
-#pragma unroll
-                    for (int j = 0; j < 4; ++j)
-                        if (c + j < cols) {
-                            v[j] = A[r * g.a.ld + c + j];
-                            if constexpr (PRO == PXK_PRO_DIV_STAB) zv[j] = Z[r * g.z.ld + c + j];
-                        }
-                }
-                if constexpr (PRO == PXK_PRO_DIV_STAB) {
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        const int64_t kk = TA ? r : c + j;  // K index of this element
-                        const bool in = TA ? true : (c + j < cols);
-                        if (in) {
-                            const float zz = ZB ? zv[j] + ZB[kk] : zv[j];
-                            v[j] = v[j] / stab(zz, g.eps);
-                        }
-                    }
-                }
-            }
-            ra[i] = v;
-        }
-#pragma unroll
-        for (int i = 0; i < BF; ++i) {
-            const int idx = tid + i * NT;
-            int64_t r, c;
-            if constexpr (TB) {
-                r = n0 + idx / (BK / 4);
-                c = k0 + 4 * (idx % (BK / 4));
-            } else {
-                r = k0 + idx / (BN / 4);
-                c = n0 + 4 * (idx % (BN / 4));
-            }
-            const int64_t rows = TB ? g.N : g.K, cols = TB ? g.K : g.N;
-            f4 v = {0.f, 0.f, 0.f, 0.f};
-            if (r < rows) {
-                if (g.vec_b && c + 3 < cols) {
-                    v = *reinterpret_cast<const f4*>(B + r * g.b.ld + c);
-                } else {
-#pragma unroll
-                    for (int j = 0; j < 4; ++j)
-                        if (c + j < cols) v[j] = B[r * g.b.ld + c + j];
-                }
-            }
-            rb[i] = v;
+    __device__ __forceinline__ static void coords(int idx, int64_t r0, int64_t k0, int64_t& r, int64_t& c) {
+        if constexpr (KC) {
+            r = r0 + idx / (BK / 4);
+            c = k0 + 4 * (idx % (BK / 4));
+        } else {
+            r = k0 + idx / (R / 4);
+            c = r0 + 4 * (idx % (R / 4));
         }
     }
 
-    // Registers -> LDS buffer (As [BM][LDK], Bs [BN][LDK], K contiguous).
-    __device__ __forceinline__ void store(float* As, float* Bs) const {
+    // The panel lies inside the matrix and every access is 16-byte aligned: straight-line 128-bit
+    // loads, so the compiler can wait for exactly the oldest register set at commit().
+    __device__ __forceinline__ void issue_fast(const float* A, int64_t lda, const float* Z, int64_t ldz,
+                                               const float* ZB, int64_t r0, int64_t k0) {
         const int tid = threadIdx.x;
 #pragma unroll
-        for (int i = 0; i < AF; ++i) {
-            const int idx = tid + i * NT;
-            if constexpr (!TA) {
-                *reinterpret_cast<f4*>(As + (idx / (BK / 4)) * LDK + 4 * (idx % (BK / 4))) = ra[i];
-            } else {
-                const int kr = idx / (BM / 4), mc = 4 * (idx % (BM / 4));
-#pragma unroll
-                for (int j = 0; j < 4; ++j) As[(mc + j) * LDK + kr] = ra[i][j];
+        for (int i = 0; i < P::NV; ++i) {
+            int64_t r, c;
+            coords(tid + i * NT, r0, k0, r, c);
+            v[i] = *reinterpret_cast<const f4*>(A + r * lda + c);
+            if constexpr (DS) z[i] = *reinterpret_cast<const f4*>(Z + r * ldz + c);
+            if constexpr (HB) {
+                if constexpr (KC)
+                    zb[i] = *reinterpret_cast<const f4*>(ZB + c);
+                else
+                    zb[i] = f4{ZB[r], ZB[r], ZB[r], ZB[r]};
             }
         }
+    }
+
+    // Any panel: element-wise bounds checks, zeros outside the matrix.
+    __device__ __forceinline__ void issue(const Args& g, const float* A, int64_t lda, const float* Z, int64_t ldz,
+                                          const float* ZB, int64_t mn, int64_t r0, int64_t k0) {
+        const int tid = threadIdx.x;
+        const int64_t rows = KC ? mn : g.K, cols = KC ? g.K : mn;
 #pragma unroll
-        for (int i = 0; i < BF; ++i) {
-            const int idx = tid + i * NT;
-            if constexpr (TB) {
-                *reinterpret_cast<f4*>(Bs + (idx / (BK / 4)) * LDK + 4 * (idx % (BK / 4))) = rb[i];
-            } else {
-                const int kr = idx / (BN / 4), nc = 4 * (idx % (BN / 4));
+        for (int i = 0; i < P::NV; ++i) {
+            int64_t r, c;
+            coords(tid + i * NT, r0, k0, r, c);
+            f4 a = {0.f, 0.f, 0.f, 0.f};
+            f4 zz = {1.f, 1.f, 1.f, 1.f};
+            f4 bb = {0.f, 0.f, 0.f, 0.f};
+            if (r < rows) {
 #pragma unroll
-                for (int j = 0; j < 4; ++j) Bs[(nc + j) * LDK + kr] = rb[i][j];
+                for (int j = 0; j < 4; ++j)
+                    if (c + j < cols) {
+                        a[j] = A[r * lda + c + j];
+                        if constexpr (DS) zz[j] = Z[r * ldz + c + j];
+                        if constexpr (HB) bb[j] = ZB[KC ? c + j : r];
+                    }
             }
+            v[i] = a;
+            if constexpr (DS) z[i] = zz;
+            if constexpr (HB) zb[i] = bb;
+        }
+    }
+
+    __device__ __forceinline__ void commit(float* lds, float eps) {
+        const int tid = threadIdx.x;
+#pragma unroll
+        for (int i = 0; i < P::NV; ++i) {
+            const int idx = tid + i * NT;
+            f4 a = v[i];
+            // A element a is divided once per N tile that reads it, so the prologue multiplies by
+            // v_rcp_f32 (within 1 ulp of 1/x) instead of the IEEE division sequence; |stab(z)| >= eps
+            // keeps the operand normal.
+            if constexpr (HB) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) a[j] = a[j] * __builtin_amdgcn_rcpf(stab(z[i][j] + zb[i][j], eps));
+            } else if constexpr (DS) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) a[j] = a[j] * __builtin_amdgcn_rcpf(stab(z[i][j], eps));
+            }
+            if constexpr (KC)
+                *reinterpret_cast<f4*>(lds + (idx / (BK / 4)) * P::LD + 4 * (idx % (BK / 4))) = a;
+            else
+                *reinterpret_cast<f4*>(lds + (idx / (R / 4)) * P::LD + 4 * (idx % (R / 4))) = a;
         }
     }
 };
 
-__device__ __forceinline__ void tile_range(const Args& g, int64_t m0, int64_t bm, int64_t& k_lo, int64_t& k_hi) {
-    k_lo = 0;
-    k_hi = g.K;
-    if (g.causal == PXK_CAUSAL_K_LE_M) k_hi = (m0 + bm < g.K) ? m0 + bm : g.K;
-    if (g.causal == PXK_CAUSAL_K_GE_M) k_lo = (m0 / BK) * BK;
+// MFMA operand fragment of a 16-row (or 16-column) block at `off` for K chunk `c`: element s is
+// the value at K index 16c + 4g + s, g = lane / 16.
+template <int BK, bool KC, int LD>
+__device__ __forceinline__ f4 fragment(const float* lds, int off, int c, int lane) {
+    if constexpr (KC) {
+        return *reinterpret_cast<const f4*>(lds + (off + (lane & 15)) * LD + 16 * c + 4 * (lane >> 4));
+    } else {
+        const float* p = lds + (16 * c + 4 * (lane >> 4)) * LD + off + (lane & 15);
+        return f4{p[0], p[LD], p[2 * LD], p[3 * LD]};
+    }
 }
 
-template <int BM, int BN, bool TA, bool TB, int PRO, int EPI>
+// K range a tile sums over: K_LE_M stops after the tile's last row, K_GE_M starts at its first.
+__device__ __forceinline__ int64_t k_first(const Args& g, int64_t m0) {
+    return g.causal == PXK_CAUSAL_K_GE_M ? (m0 < g.K ? m0 : g.K) : 0;
+}
+__device__ __forceinline__ int64_t k_end(const Args& g, int64_t m0, int64_t bm) {
+    return g.causal == PXK_CAUSAL_K_LE_M ? (m0 + bm < g.K ? m0 + bm : g.K) : g.K;
+}
+
+// Block index -> (M tile, N tile, batch * splits + split).
+__device__ __forceinline__ void tile_of(const Args& g, int& tm, int& tn, int& tz) {
+    int id = static_cast<int>(blockIdx.x);
+    if (g.remap) {
+        const int per = static_cast<int>(gridDim.x) / 8;
+        id = (id % 8) * per + id / 8;
+    }
+    tm = id % g.tiles_m;
+    id /= g.tiles_m;
+    tn = id % g.tiles_n;
+    tz = id / g.tiles_n;
+}
+
+template <class C, bool TA, bool TB, int PRO, int EPI>
 __global__ void __launch_bounds__(NT) gemm_kernel(const Args g) {
-    constexpr int TM = BM / 32, TN = BN / 32;  // 16x16 MFMA tiles per wave along M, N
-    __shared__ __attribute__((aligned(16))) float smem[Smem<BM, BN>::SIZE];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = (wave >> 1) * (BM / 2), wn = (wave & 1) * (BN / 2);
-    const int64_t n0 = static_cast<int64_t>(blockIdx.x) * BN, m0 = static_cast<int64_t>(blockIdx.y) * BM;
-    const int64_t split = blockIdx.z % g.splits, b = blockIdx.z / g.splits;
+    constexpr int BM = C::BM, BN = C::BN, BK = C::BK, TM = C::TM, TN = C::TN, LDC = C::LDC;
+    using L = Layout<C, TA, TB>;
+    using PA = typename L::PA;
+    using PB = typename L::PB;
+    __shared__ __attribute__((aligned(16))) float smem[L::SIZE];
+
+    int tm, tn, tz;
+    tile_of(g, tm, tn, tz);
+    const int64_t m0 = static_cast<int64_t>(tm) * BM, n0 = static_cast<int64_t>(tn) * BN;
+    const int64_t split = tz % g.splits, b = tz / g.splits;  // 32-bit operands
     if (g.causal == PXK_CAUSAL_TRI && n0 > m0 + BM - 1) return;  // tile strictly above the diagonal
 
-    int64_t k_lo, k_hi;
-    tile_range(g, m0, BM, k_lo, k_hi);
-    const int64_t nkb = k_hi > k_lo ? (k_hi - k_lo + BK - 1) / BK : 0;
-    const int64_t per = (nkb + g.splits - 1) / g.splits;
-    const int64_t kb0 = split * per, kb1 = (kb0 + per < nkb) ? kb0 + per : nkb;
-    const int64_t nk = kb1 > kb0 ? kb1 - kb0 : 0;
-    const int64_t total = nk * g.kgroups;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int ks = wave / (C::WM * C::WN), wmn = wave % (C::WM * C::WN);
+    const int wm = (wmn / C::WN) * (BM / C::WM), wn = (wmn % C::WN) * (BN / C::WN);
+
+    const int64_t k_lo = k_first(g, m0), k_hi = k_end(g, m0, BM);
+    // Stage counts fit 32 bits (K / BK * kgroups < 2^31, checked on the host).
+    const int nkb = k_hi > k_lo ? static_cast<int>((k_hi - k_lo + BK - 1) / BK) : 0;
+    const int total = nkb * static_cast<int>(g.kgroups);
+    const int per = (total + g.splits - 1) / g.splits;
+    const int t0 = static_cast<int>(split) * per < total ? static_cast<int>(split) * per : total;
+    const int t1 = t0 + per < total ? t0 + per : total;
+    const int64_t nt = t1 - t0;
 
     f4 acc[TM][TN];
 #pragma unroll
@@ -288,113 +430,205 @@ __global__ void __launch_bounds__(NT) gemm_kernel(const Args g) {
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
 
-    Loader<BM, BN, TA, TB, PRO> ld;
-    auto issue = [&](int64_t t) {
-        const int64_t s = t / nk, kb = kb0 + t % nk;
-        const float* A = obase(g.a, b, g.inner, s);
-        const float* B = obase(g.b, b, g.inner, s);
-        const float* Z = PRO ? obase(g.z, b, g.inner, s) : nullptr;
-        const float* ZB = (PRO && g.zb.p) ? obase(g.zb, b, g.inner, s) : nullptr;
-        ld.load(g, A, Z, ZB, B, m0, n0, k_lo + kb * BK);
+    constexpr int NS = C::NS;
+    PanelLoader<BM, BK, !TA, PRO> la[NS];
+    PanelLoader<BN, BK, TB, PXK_PRO_NONE> lb[NS];
+    // Load cursor: stage `lt` of the flattened (k-group, K stage) range, at (grp, kb).
+    int64_t lt = 0, grp = nkb > 0 ? t0 / nkb : 0, kb = nkb > 0 ? t0 % nkb : 0;  // 32-bit division
+    const float* A = obase(g.a, b, g.inner, grp);
+    const float* B = obase(g.b, b, g.inner, grp);
+    const float* Z = PRO != PXK_PRO_NONE ? obase(g.z, b, g.inner, grp) : nullptr;
+    const float* ZB = PRO == kProStabBias ? obase(g.zb, b, g.inner, grp) : nullptr;
+    auto advance = [&]() {
+        ++lt;
+        if (++kb == nkb) {  // next k-group: rebase the operands
+            kb = 0;
+            ++grp;
+            A = obase(g.a, b, g.inner, grp);
+            B = obase(g.b, b, g.inner, grp);
+            if constexpr (PRO != PXK_PRO_NONE) Z = obase(g.z, b, g.inner, grp);
+            if constexpr (PRO == kProStabBias) ZB = obase(g.zb, b, g.inner, grp);
+        }
+    };
+    auto commit = [&](auto S, int64_t t) {  // register set S holds stage t -> LDS buffer t % 2
+        float* dst = smem + (t & 1) * L::STAGE;
+        la[S.value].commit(dst, g.eps);
+        lb[S.value].commit(dst + PA::SIZE, g.eps);
+    };
+    auto compute = [&](int64_t t) {
+        const float* As = smem + (t & 1) * L::STAGE;
+        const float* Bs = As + PA::SIZE;
+#pragma unroll
+        for (int cc = 0; cc < C::CH; ++cc) {
+            const int c = ks * C::CH + cc;
+            f4 af[TM], bf[TN];
+#pragma unroll
+            for (int i = 0; i < TM; ++i) af[i] = fragment<BK, !TA, PA::LD>(As, wm + 16 * i, c, lane);
+#pragma unroll
+            for (int j = 0; j < TN; ++j) bf[j] = fragment<BK, TB, PB::LD>(Bs, wn + 16 * j, c, lane);
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int j = 0; j < TN; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i][s], bf[j][s], acc[i][j], 0, 0, 0);
+        }
     };
 
-    float* As0 = smem;
-    float* Bs0 = smem + BM * LDK;
-    float* As1 = smem + (BM + BN) * LDK;
-    float* Bs1 = As1 + BM * LDK;
-
-    if (total > 0) {
-        issue(0);
-        ld.store(As0, Bs0);
+    // Fast path: every stage of this tile lies inside both matrices and is 16-byte aligned, and
+    // there are more stages than register sets. Stage s lives in register set s % NS; before
+    // iteration t, stages t + 1 .. t + NS are in flight. Loads are issued unconditionally (past the
+    // last stage the cursor stays put and the last stage is loaded again, into a set nobody
+    // commits), so the loop body has no branches around vector loads.
+    const bool k_inside = k_lo + nkb * BK <= g.K;
+    const bool fast = nt >= NS + 1 && k_inside && g.vec_a && g.vec_b && m0 + BM <= g.M && n0 + BN <= g.N;
+    if (fast) {
+        auto issue = [&](auto S) {
+            const int64_t k0 = k_lo + kb * BK;
+            la[S.value].issue_fast(A, g.a.ld, Z, g.z.ld, ZB, m0, k0);
+            lb[S.value].issue_fast(B, g.b.ld, nullptr, 0, nullptr, n0, k0);
+            if (lt + 1 < nt) advance();
+        };
+        issue(std::integral_constant<int, 0>{});
+        commit(std::integral_constant<int, 0>{}, 0);
+        static_for<NS>([&](auto U) { issue(std::integral_constant<int, (U.value + 1) % NS>{}); });
         __syncthreads();
-    }
-    for (int64_t t = 0; t < total; ++t) {
-        const bool cur0 = (t & 1) == 0;
-        const float* As = cur0 ? As0 : As1;
-        const float* Bs = cur0 ? Bs0 : Bs1;
-        if (t + 1 < total) issue(t + 1);
-        f4 af[TM], bf[TN];
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
-            af[i] = *reinterpret_cast<const f4*>(As + (wm + i * 16 + (lane & 15)) * LDK + 4 * (lane >> 4));
-#pragma unroll
-        for (int j = 0; j < TN; ++j)
-            bf[j] = *reinterpret_cast<const f4*>(Bs + (wn + j * 16 + (lane & 15)) * LDK + 4 * (lane >> 4));
-#pragma unroll
-        for (int s = 0; s < 4; ++s)
-#pragma unroll
-            for (int i = 0; i < TM; ++i)
-#pragma unroll
-                for (int j = 0; j < TN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i][s], bf[j][s], acc[i][j], 0, 0, 0);
-        if (t + 1 < total) {
-            ld.store(cur0 ? As1 : As0, cur0 ? Bs1 : Bs0);
+        const int64_t main_iters = (nt - 2) / NS * NS;  // a multiple of NS, >= nt - NS - 1
+        for (int64_t tb = 0; tb < main_iters; tb += NS) {
+            static_for<NS>([&](auto U) {
+                constexpr int nxt = (U.value + 1) % NS;
+                const int64_t t = tb + U.value;
+                // Buffer (t + 1) % 2 was last read by stage t - 1, before the previous barrier, so
+                // stage t + 1 goes to LDS first and its writes overlap this stage's MFMAs.
+                commit(std::integral_constant<int, nxt>{}, t + 1);
+                compute(t);
+                __syncthreads();
+                issue(std::integral_constant<int, nxt>{});  // stage t + 1 + NS (or the last one again)
+            });
         }
+        static_for<NS + 1>([&](auto U) {  // the last 2 .. NS + 1 stages: already in flight
+            constexpr int nxt = (U.value + 1) % NS;
+            const int64_t t = main_iters + U.value;
+            if (t < nt) {
+                if (t + 1 < nt) commit(std::integral_constant<int, nxt>{}, t + 1);
+                compute(t);
+                __syncthreads();
+            }
+        });
+    } else if (nt > 0) {
+        // Edge tiles and short K ranges: bounds-checked loads, one stage ahead.
+        auto issue = [&]() {
+            const int64_t k0 = k_lo + kb * BK;
+            la[0].issue(g, A, g.a.ld, Z, g.z.ld, ZB, g.M, m0, k0);
+            lb[0].issue(g, B, g.b.ld, nullptr, 0, nullptr, g.N, n0, k0);
+            advance();
+        };
+        issue();
+        commit(std::integral_constant<int, 0>{}, 0);
         __syncthreads();
+        for (int64_t t = 0; t < nt; ++t) {
+            const bool more = t + 1 < nt;
+            if (more) issue();
+            compute(t);
+            if (more) commit(std::integral_constant<int, 0>{}, t + 1);
+            __syncthreads();
+        }
     }
 
-    if (g.splits > 1) {  // raw partial tile -> workspace [split][batch][M][N]
-        float* P = g.ws + ((split * g.batch + b) * g.M) * g.N;
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
-#pragma unroll
-            for (int j = 0; j < TN; ++j)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int64_t m = m0 + wm + i * 16 + 4 * (lane >> 4) + r, n = n0 + wn + j * 16 + (lane & 15);
-                    if (m < g.M && n < g.N) P[m * g.N + n] = acc[i][j][r];
-                }
-        return;
-    }
-    constexpr int LDC = Smem<BM, BN>::LDC;
-    float* Cs = smem;  // the loop ended on a barrier: LDS is free
+    // Accumulators -> LDS (one partial tile per K slice); the loop ended on a barrier.
+    float* Cp = smem + ks * L::PART;
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j)
 #pragma unroll
             for (int r = 0; r < 4; ++r)
-                Cs[(wm + i * 16 + 4 * (lane >> 4) + r) * LDC + wn + j * 16 + (lane & 15)] = acc[i][j][r];
+                Cp[(wm + 16 * i + 4 * (lane >> 4) + r) * LDC + wn + 16 * j + (lane & 15)] = acc[i][j][r];
     __syncthreads();
-    epilogue_tile<BM, BN, EPI>(Cs, m0, n0, b, g);
+    if constexpr (C::KS > 1) {  // sum the K-slice partials in slice order
+        for (int it = tid; it < BM * (BN / 4); it += NT) {
+            const int off = (it / (BN / 4)) * LDC + 4 * (it % (BN / 4));
+            f4 v = *reinterpret_cast<const f4*>(smem + off);
+#pragma unroll
+            for (int q = 1; q < C::KS; ++q) v += *reinterpret_cast<const f4*>(smem + q * L::PART + off);
+            *reinterpret_cast<f4*>(smem + off) = v;
+        }
+        __syncthreads();
+    }
+    if (g.splits > 1) {  // raw partial tile -> workspace [split][batch][M][N]
+        float* P = g.ws + ((split * g.batch + b) * g.M) * g.N;
+        const bool vec = (g.N % 4) == 0;
+        for (int it = tid; it < BM * (BN / 4); it += NT) {
+            const int row = it / (BN / 4), col = 4 * (it % (BN / 4));
+            const int64_t m = m0 + row, n = n0 + col;
+            if (m >= g.M || n >= g.N) continue;
+            const int cnt = g.N - n < 4 ? static_cast<int>(g.N - n) : 4;
+            st4(P + m * g.N + n, *reinterpret_cast<const f4*>(smem + row * LDC + col), vec && cnt == 4, cnt);
+        }
+        return;
+    }
+    epilogue_rows<BM, BN, EPI>(smem, LDC, m0, n0, b, g);
 }
 
-// Sums the split partials of one tile in split order and runs the tile epilogue.
-template <int BM, int BN, int EPI>
+// Sums the split partials of a slab of rows in split order and runs the tile epilogue. One
+// workgroup per RS x BN slab, one float4 column per thread.
+template <int BN, int EPI>
 __global__ void __launch_bounds__(NT) splitk_reduce_kernel(const Args g) {
-    constexpr int LDC = Smem<BM, BN>::LDC;
-    __shared__ float Cs[BM * LDC];
-    const int64_t n0 = static_cast<int64_t>(blockIdx.x) * BN, m0 = static_cast<int64_t>(blockIdx.y) * BM;
+    constexpr int RS = 4 * NT / BN, LDC = BN + 4;
+    __shared__ __attribute__((aligned(16))) float Cs[RS * LDC];
+    const int64_t n0 = static_cast<int64_t>(blockIdx.x) * BN, m0 = static_cast<int64_t>(blockIdx.y) * RS;
     const int64_t b = blockIdx.z;
-    if (g.causal == PXK_CAUSAL_TRI && n0 > m0 + BM - 1) return;
-    const int64_t plane = g.batch * g.M * g.N;
-    for (int e = threadIdx.x; e < BM * BN; e += NT) {
-        const int row = e / BN, col = e % BN;
-        const int64_t m = m0 + row, n = n0 + col;
-        float s = 0.0f;
-        if (m < g.M && n < g.N) {
-            const float* P = g.ws + (b * g.M + m) * g.N + n;
-            for (int k = 0; k < g.splits; ++k) s += P[k * plane];
+    if (g.causal == PXK_CAUSAL_TRI && n0 > (m0 / g.bm) * g.bm + g.bm - 1) return;  // tile never computed
+    const int row = threadIdx.x / (BN / 4), col = 4 * (threadIdx.x % (BN / 4));
+    const int64_t m = m0 + row, n = n0 + col;
+    f4 v = {0.f, 0.f, 0.f, 0.f};
+    if (m < g.M && n < g.N) {
+        const int cnt = g.N - n < 4 ? static_cast<int>(g.N - n) : 4;
+        const bool vec = (g.N % 4) == 0 && cnt == 4;
+        const int64_t plane = g.batch * g.M * g.N;
+        const float* P = g.ws + (b * g.M + m) * g.N + n;
+        int k = 0;
+        for (; k + 8 <= g.splits; k += 8) {
+            f4 t[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) t[u] = ld4(P + (k + u) * plane, vec, cnt);
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v += t[u];
         }
-        Cs[row * LDC + col] = s;
+        for (; k < g.splits; ++k) v += ld4(P + k * plane, vec, cnt);
     }
+    *reinterpret_cast<f4*>(Cs + row * LDC + col) = v;
     __syncthreads();
-    epilogue_tile<BM, BN, EPI>(Cs, m0, n0, b, g);
+    epilogue_rows<RS, BN, EPI>(Cs, LDC, m0, n0, b, g);
 }
 
 // ---- host side --------------------------------------------------------------------------------
 
 using KernelFn = void (*)(const Args);
 
-struct Entry {
-    int ta, tb, pro, epi;
-    KernelFn k64, k128, r64, r128;
+constexpr int kTiles = 4;  // PXK_TILE_128x128 .. PXK_TILE_32x32
+
+struct TileInfo {
+    int bm, bn, bk, smem_bytes;
+    double floor_us;  // a K stage of a workgroup alone on its CU (load latency bound), measured
+    double util;      // MFMA utilisation when several waves share a SIMD, measured
 };
 
-#define PXK_GEMM_ENTRY(TA, TB, PRO, EPI)                                                                     \
-    Entry {                                                                                                  \
-        TA, TB, PRO, EPI, gemm_kernel<64, 64, TA, TB, PRO, EPI>, gemm_kernel<128, 128, TA, TB, PRO, EPI>,    \
-            splitk_reduce_kernel<64, 64, EPI>, splitk_reduce_kernel<128, 128, EPI>                           \
+struct Entry {
+    int ta, tb, pro, epi;
+    KernelFn k[2][kTiles];  // [prologue bias over k present][tile]
+    KernelFn r[kTiles];
+};
+
+#define PXK_KSET(TA, TB, P, EPI)                                                                    \
+    {gemm_kernel<C128, TA, TB, P, EPI>, gemm_kernel<C64, TA, TB, P, EPI>, gemm_kernel<C32x64, TA, TB, P, EPI>, \
+     gemm_kernel<C32, TA, TB, P, EPI>}
+#define PXK_GEMM_ENTRY(TA, TB, PRO, EPI)                                                                   \
+    Entry {                                                                                                \
+        TA, TB, PRO, EPI, {PXK_KSET(TA, TB, PRO, EPI), PXK_KSET(TA, TB, (PRO ? kProStabBias : PRO), EPI)}, \
+            {splitk_reduce_kernel<128, EPI>, splitk_reduce_kernel<64, EPI>, splitk_reduce_kernel<64, EPI>, \
+             splitk_reduce_kernel<32, EPI>},                                                               \
     }
 
 const Entry kTable[] = {
@@ -417,6 +651,23 @@ const Entry kTable[] = {
     PXK_GEMM_ENTRY(0, 1, PXK_PRO_DIV_STAB, PXK_EPI_SWIGLU_REL),
 };
 
+template <class C>
+constexpr int smem_of() {
+    // The largest of the four (TA, TB) layouts: what a CU must hold for one workgroup.
+    int s = Layout<C, false, false>::SIZE;
+    if (Layout<C, false, true>::SIZE > s) s = Layout<C, false, true>::SIZE;
+    if (Layout<C, true, false>::SIZE > s) s = Layout<C, true, false>::SIZE;
+    if (Layout<C, true, true>::SIZE > s) s = Layout<C, true, true>::SIZE;
+    return 4 * s;
+}
+
+const TileInfo kTileInfo[kTiles] = {
+    {128, 128, 32, smem_of<C128>(), 1.0, 0.75},
+    {64, 64, 32, smem_of<C64>(), 0.8, 0.65},
+    {32, 64, 64, smem_of<C32x64>(), 0.8, 0.55},
+    {32, 32, 64, smem_of<C32>(), 0.8, 0.5},
+};
+
 const Entry* find_entry(int ta, int tb, int pro, int epi) {
     for (const Entry& e : kTable)
         if (e.ta == ta && e.tb == tb && e.pro == pro && e.epi == epi) return &e;
@@ -435,15 +686,64 @@ bool vec_ok(const pxk_operand& o, int64_t contiguous_extent) {
 
 struct Plan {
     const Entry* e;
-    int bm, bn, splits;
+    int tile, splits;
     int64_t tiles_m, tiles_n;
 };
+
+bool rope_fits(const pxk_gemm_desc* d, int bn) {
+    return d->n <= bn || bn % d->head_dim == 0;
+}
+
+// Output tiles a launch computes (TRI skips those strictly above the diagonal).
+int64_t live_tiles(const pxk_gemm_desc* d, int bm, int bn) {
+    const int64_t tm = cdiv(d->m, bm), tn = cdiv(d->n, bn);
+    if (d->causal != PXK_CAUSAL_TRI) return tm * tn * d->batch;
+    int64_t t = 0;
+    for (int64_t i = 0; i < tm; ++i) {
+        const int64_t lim = (i * bm + bm - 1) / bn + 1;
+        t += lim < tn ? lim : tn;
+    }
+    return t * d->batch;
+}
+
+// K stages of the longest tile (K_LE_M / K_GE_M tiles see a triangular share of K; the slowest
+// one bounds the launch).
+double max_stages(const pxk_gemm_desc* d, int bm, int bk) {
+    const int64_t tm = cdiv(d->m, bm);
+    if (d->causal == PXK_CAUSAL_NONE || d->causal == PXK_CAUSAL_TRI)
+        return static_cast<double>(cdiv(d->k, bk)) * static_cast<double>(d->kgroups);
+    int64_t most = 0;
+    for (int64_t i = 0; i < tm; ++i) {
+        int64_t lo = 0, hi = d->k;
+        if (d->causal == PXK_CAUSAL_K_LE_M) hi = i * bm + bm < d->k ? i * bm + bm : d->k;
+        if (d->causal == PXK_CAUSAL_K_GE_M) lo = i * bm < d->k ? i * bm : d->k;
+        const int64_t st = hi > lo ? cdiv(hi - lo, bk) : 0;
+        if (st > most) most = st;
+    }
+    return static_cast<double>(most) * static_cast<double>(d->kgroups);
+}
+
+// Estimated microseconds of one launch on 256 CUs (4 SIMDs each, ~2.4 GHz), calibrated on the
+// 512-token GEMMs of a 576-wide model and its 49152-entry LM head: a fixed launch/prologue/epilogue
+// cost, then per K stage the larger of the tile's latency floor and the MFMA time of the waves that
+// share a SIMD; split-K adds the reduction launch and the partials' round trip through HBM.
+double estimate(const pxk_gemm_desc* d, const TileInfo& t, double tiles, double stages, int splits) {
+    const double per = std::ceil(stages / splits);
+    const double waves_per_simd = std::ceil(tiles * splits / 256.0);
+    const double mfma_us = static_cast<double>(t.bm) * t.bn * t.bk / 128.0 / 2400.0;
+    const double stage_us = std::max(t.floor_us, waves_per_simd * mfma_us / t.util);
+    double us = 4.0 + per * stage_us;
+    if (splits > 1) us += 6.0 + 2.0 * splits * d->batch * d->m * d->n * 4.0 / 5.0e6;
+    return us;
+}
 
 int plan(const pxk_gemm_desc* d, Plan* p) {
     if (d->m <= 0 || d->n <= 0 || d->batch <= 0) return fail(PXK_ERR_INVALID, "pxk_gemm: m, n and batch must be positive");
     if (d->k < 0 || d->inner <= 0 || d->kgroups <= 0 || d->batch % d->inner != 0)
         return fail(PXK_ERR_INVALID, "pxk_gemm: bad k, inner or kgroups (batch must be a multiple of inner)");
     if (d->causal < 0 || d->causal > 3) return fail(PXK_ERR_INVALID, "pxk_gemm: unknown causal mode %d", d->causal);
+    if (d->tile < 0 || d->tile > kTiles) return fail(PXK_ERR_INVALID, "pxk_gemm: unknown tile %d", d->tile);
+    if (d->splits < 0 || d->splits > 4096) return fail(PXK_ERR_INVALID, "pxk_gemm: bad split count %d", d->splits);
     p->e = find_entry(d->trans_a != 0, d->trans_b != 0, d->prologue, d->epilogue);
     if (!p->e)
         return fail(PXK_ERR_INVALID, "pxk_gemm: combination trans_a=%d trans_b=%d prologue=%d epilogue=%d is not built",
@@ -475,27 +775,53 @@ int plan(const pxk_gemm_desc* d, Plan* p) {
         const int64_t D = d->head_dim;
         if (D <= 0 || D % 2 != 0 || d->cos_t == nullptr || d->sin_t == nullptr)
             return fail(PXK_ERR_INVALID, "pxk_gemm: ROPE_REL needs an even head_dim and cos/sin tables");
-        if (!(d->n <= 64 || (64 % D == 0 && d->n % D == 0)))
-            return fail(PXK_ERR_INVALID, "pxk_gemm: ROPE_REL needs whole heads inside a 64-wide tile");
+        if (d->n % D != 0)
+            return fail(PXK_ERR_INVALID, "pxk_gemm: ROPE_REL needs n to be a whole number of heads");
+        if (!rope_fits(d, 128))
+            return fail(PXK_ERR_INVALID, "pxk_gemm: ROPE_REL needs whole heads inside a 128-wide tile");
+        if (d->tile > 0 && !rope_fits(d, kTileInfo[d->tile - 1].bn))
+            return fail(PXK_ERR_INVALID, "pxk_gemm: ROPE_REL heads do not fit tile %d", d->tile);
     }
-    // Tile size: big tiles when they still give the chip a few waves of workgroups.
-    const double tri = d->causal == PXK_CAUSAL_TRI ? 0.5 : 1.0;
-    const int64_t t128 = cdiv(d->m, 128) * cdiv(d->n, 128) * d->batch;
-    const bool big = (epi != PXK_EPI_ROPE_REL) && t128 * tri >= 512 && d->m >= 128 && d->n >= 128;
-    p->bm = p->bn = big ? 128 : 64;
-    p->tiles_m = cdiv(d->m, p->bm);
-    p->tiles_n = cdiv(d->n, p->bn);
-    // Split-K when the tiles alone leave most CUs idle and K is long.
-    int splits = d->splits;
-    if (splits <= 0) {
-        const double tiles = static_cast<double>(p->tiles_m * p->tiles_n * d->batch) * tri;
-        const int64_t kwork = d->k * d->kgroups;
-        splits = 1;
-        while (tiles * splits < 384 && kwork / (splits * 2) >= 256 && splits < 64) splits *= 2;
+    if (d->k > (int64_t{1} << 40) || static_cast<double>(d->k) * d->kgroups / 32.0 > 2.0e9 || d->batch > (int64_t{1} << 31))
+        return fail(PXK_ERR_INVALID, "pxk_gemm: k * kgroups or batch too large");
+
+    // Tile shape and split count: the forced ones, else the cheapest by estimate().
+    int best_t = -1, best_s = 1;
+    double best = 0.0;
+    for (int t = 0; t < kTiles; ++t) {
+        if (d->tile > 0 && t != d->tile - 1) continue;
+        const TileInfo& ti = kTileInfo[t];
+        if (epi == PXK_EPI_ROPE_REL && !rope_fits(d, ti.bn)) continue;
+        const double stages = max_stages(d, ti.bm, ti.bk);
+        const double tiles = static_cast<double>(live_tiles(d, ti.bm, ti.bn));
+        // The 128x128 tile only pays off when its tiles alone fill the chip.
+        const bool big_only = d->tile == 0 && t == 0;
+        if (big_only && tiles < 256.0) continue;
+        for (int s = 1; s <= 64; s *= 2) {
+            if (d->splits > 0 && s != 1) break;
+            const int splits = d->splits > 0 ? d->splits : s;
+            if (d->splits == 0 && s > 1 && (big_only || stages / s < 2.0)) break;
+            const double us = estimate(d, ti, tiles, stages, splits);
+            if (best_t < 0 || us < best) {
+                best = us;
+                best_t = t;
+                best_s = splits;
+            }
+        }
     }
-    if (splits > 1 && d->beta != 0.0f) splits = 1;  // beta reads C: keep it single-pass
-    p->splits = splits;
+    if (best_t < 0) return fail(PXK_ERR_INVALID, "pxk_gemm: no tile shape fits this descriptor");
+    const TileInfo& ti = kTileInfo[best_t];
+    p->tile = best_t;
+    p->splits = best_s;
+    p->tiles_m = cdiv(d->m, ti.bm);
+    p->tiles_n = cdiv(d->n, ti.bn);
+    const int64_t blocks = p->tiles_m * p->tiles_n * d->batch * p->splits;
+    if (blocks > (int64_t{1} << 31) - 1) return fail(PXK_ERR_INVALID, "pxk_gemm: grid too large");
     return PXK_OK;
+}
+
+size_t workspace_bytes(const pxk_gemm_desc* d, const Plan& p) {
+    return p.splits > 1 ? static_cast<size_t>(p.splits) * d->batch * d->m * d->n * sizeof(float) : 0;
 }
 
 }  // namespace
@@ -505,10 +831,18 @@ using namespace pxk;
 
 extern "C" int pxk_gemm_supported(int ta, int tb, int pro, int epi) { return find_entry(ta != 0, tb != 0, pro, epi) != nullptr; }
 
+extern "C" int pxk_gemm_plan(const pxk_gemm_desc* d, int32_t* tile, int32_t* splits) {
+    Plan p;
+    if (const int rc = plan(d, &p)) return rc;
+    if (tile) *tile = p.tile + 1;
+    if (splits) *splits = p.splits;
+    return PXK_OK;
+}
+
 extern "C" size_t pxk_gemm_workspace(const pxk_gemm_desc* d) {
     Plan p;
-    if (plan(d, &p) != PXK_OK || p.splits <= 1) return 0;
-    return static_cast<size_t>(p.splits) * d->batch * d->m * d->n * sizeof(float);
+    if (plan(d, &p) != PXK_OK) return 0;
+    return workspace_bytes(d, p);
 }
 
 extern "C" int pxk_gemm(const pxk_gemm_desc* d, void* stream) {
@@ -516,11 +850,15 @@ extern "C" int pxk_gemm(const pxk_gemm_desc* d, void* stream) {
     Plan p;
     if (const int rc = plan(d, &p)) return rc;
     if (p.splits > 1) {
-        const size_t need = static_cast<size_t>(p.splits) * d->batch * d->m * d->n * sizeof(float);
-        if (d->workspace == nullptr || d->workspace_bytes < need) {
+        const size_t need = workspace_bytes(d, p);
+        if (d->workspace == nullptr || d->workspace_bytes < need || !aligned16(d->workspace)) {
             if (d->splits > 1)
-                return fail(PXK_ERR_WORKSPACE, "pxk_gemm: split-K %d needs %zu workspace bytes", p.splits, need);
-            p.splits = 1;  // library-chosen split without a workspace: run single-pass
+                return fail(PXK_ERR_WORKSPACE, "pxk_gemm: split-K %d needs %zu workspace bytes (16-byte aligned)",
+                            p.splits, need);
+            // Library-chosen split without a workspace: the best single-pass plan instead.
+            pxk_gemm_desc one = *d;
+            one.splits = 1;
+            if (const int rc = plan(&one, &p)) return rc;
         }
     }
     Args g{};
@@ -553,21 +891,30 @@ extern "C" int pxk_gemm(const pxk_gemm_desc* d, void* stream) {
     g.head_dim = d->head_dim;
     g.rope_half = d->rope_half;
     g.ws = d->workspace;
-    // 128-bit loads when every base, stride and the contiguous extent allow them.
+    // 128-bit loads when every base, stride and the contiguous extent allow them; the causal
+    // K ranges start at multiples of the tile height, so they keep the alignment.
     const int64_t a_ext = d->trans_a ? d->m : d->k, b_ext = d->trans_b ? d->k : d->n;
-    g.vec_a = vec_ok(d->a, a_ext) && (d->prologue == PXK_PRO_NONE || vec_ok(d->z, a_ext));
+    g.vec_a = vec_ok(d->a, a_ext) && (d->prologue == PXK_PRO_NONE || (vec_ok(d->z, a_ext) && vec_ok(d->z_bias, a_ext)));
     g.vec_b = vec_ok(d->b, b_ext);
-    const dim3 grid(static_cast<unsigned>(p.tiles_n), static_cast<unsigned>(p.tiles_m),
-                    static_cast<unsigned>(d->batch * p.splits));
-    if (grid.y > 65535 || grid.z > 65535) return fail(PXK_ERR_INVALID, "pxk_gemm: grid too large");
-    KernelFn k = p.bm == 128 ? p.e->k128 : p.e->k64;
-    hipLaunchKernelGGL(k, grid, dim3(NT), 0, S(stream), g);
+    g.vec_e = d->n % 4 == 0 && vec_ok(d->c, d->n) && vec_ok(d->c2, d->n) && vec_ok(d->c3, d->n) &&
+              vec_ok(d->x, d->n) && vec_ok(d->y, d->n) && vec_ok(d->w, d->n) && vec_ok(d->z2, d->n) &&
+              vec_ok(d->z3, d->n) && vec_ok(d->e_bias, d->n) && vec_ok(d->e_bias2, d->n) &&
+              (d->epilogue == PXK_EPI_ROPE_REL || d->epilogue == PXK_EPI_VALUE_REL ? vec_ok(d->z, d->n) : true);
+    g.tiles_m = static_cast<int>(p.tiles_m);
+    g.tiles_n = static_cast<int>(p.tiles_n);
+    g.bm = kTileInfo[p.tile].bm;
+    const int64_t blocks = p.tiles_m * p.tiles_n * d->batch * p.splits;
+    g.remap = blocks % 8 == 0;
+    const int has_bias = d->prologue == PXK_PRO_DIV_STAB && d->z_bias.ptr != nullptr;
+    hipLaunchKernelGGL(p.e->k[has_bias][p.tile], dim3(static_cast<unsigned>(blocks)), dim3(NT), 0, S(stream), g);
     if (const int rc = launched("pxk_gemm")) return rc;
     if (p.splits > 1) {
-        const dim3 rgrid(static_cast<unsigned>(p.tiles_n), static_cast<unsigned>(p.tiles_m),
+        const int bn = kTileInfo[p.tile].bn;
+        const int rs = 4 * NT / bn;
+        const dim3 rgrid(static_cast<unsigned>(p.tiles_n), static_cast<unsigned>(cdiv(d->m, rs)),
                          static_cast<unsigned>(d->batch));
-        KernelFn r = p.bm == 128 ? p.e->r128 : p.e->r64;
-        hipLaunchKernelGGL(r, rgrid, dim3(NT), 0, S(stream), g);
+        if (rgrid.y > 65535 || rgrid.z > 65535) return fail(PXK_ERR_INVALID, "pxk_gemm: reduce grid too large");
+        hipLaunchKernelGGL(p.e->r[p.tile], rgrid, dim3(NT), 0, S(stream), g);
         return launched("pxk_gemm split-K reduce");
     }
     return PXK_OK;

@@ -34,13 +34,14 @@ class GemmDesc(ctypes.Structure):
                 ("c2", Operand), ("c3", Operand), ("x", Operand), ("y", Operand), ("w", Operand), ("z2", Operand), ("z3", Operand),
                 ("e_bias", Operand), ("e_bias2", Operand),
                 ("cos_t", c_vp), ("sin_t", c_vp), ("head_dim", c_i64), ("rope_half", ctypes.c_int32),
-                ("reserved", ctypes.c_int32), ("workspace", c_vp), ("workspace_bytes", ctypes.c_size_t)]
+                ("tile", ctypes.c_int32), ("workspace", c_vp), ("workspace_bytes", ctypes.c_size_t)]
 
 
 CAUSAL_NONE, CAUSAL_TRI, CAUSAL_K_LE_M, CAUSAL_K_GE_M = 0, 1, 2, 3
 PRO_NONE, PRO_DIV_STAB = 0, 1
 (EPI_STORE, EPI_STORE_BIAS, EPI_ADD_RESID, EPI_MUL_X, EPI_SPV, EPI_ROPE_REL, EPI_VALUE_REL,
  EPI_SWIGLU_REL) = range(8)
+TILE_AUTO, TILE_128x128, TILE_64x64, TILE_32x64, TILE_32x32 = range(5)
 
 # (name, restype, argtypes) of every pxk entry point; `p` = device pointer (void*), `i` = int64,
 # `f` = float, `n` = int, `s` = size_t.
@@ -114,6 +115,9 @@ def pxk():
         lib.pxk_gemm.argtypes = [ctypes.POINTER(GemmDesc), c_vp]
         lib.pxk_gemm_workspace.restype = ctypes.c_size_t
         lib.pxk_gemm_workspace.argtypes = [ctypes.POINTER(GemmDesc)]
+        lib.pxk_gemm_plan.restype = ctypes.c_int
+        lib.pxk_gemm_plan.argtypes = [ctypes.POINTER(GemmDesc), ctypes.POINTER(ctypes.c_int32),
+                                      ctypes.POINTER(ctypes.c_int32)]
         lib.pxk_gemm_supported.restype = ctypes.c_int
         lib.pxk_gemm_supported.argtypes = [ctypes.c_int] * 4
         lib.pxk_reduce_partials.restype = ctypes.c_size_t
@@ -141,6 +145,13 @@ def gemm(desc, stream=None):
 
 def gemm_workspace(desc):
     return pxk().pxk_gemm_workspace(ctypes.byref(desc))
+
+
+def gemm_plan(desc):
+    """(tile, splits) pxk_gemm would launch for `desc`."""
+    tile, splits = ctypes.c_int32(), ctypes.c_int32()
+    check(pxk().pxk_gemm_plan(ctypes.byref(desc), ctypes.byref(tile), ctypes.byref(splits)))
+    return tile.value, splits.value
 
 
 # ---- the host framework (include/pulsatrix_amd.h) ----------------------------------------------

@@ -1,0 +1,193 @@
+"""Every (transpose, prologue, epilogue) combination of pxk_gemm on every tile shape and with
+split-K, against float64 numpy.
+
+The library picks a tile shape and split count per descriptor; the tuning override
+(pxk_gemm_desc.tile, .splits) pins each one here so that every kernel instance the library can
+launch is exercised, including ragged M/N/K edges and an odd split count that leaves uneven K
+ranges. The fused prologue/epilogue semantics are the ones include/pxk.h states; the model
+tests pin them end to end against the oracle (lrp_rules.cpp, multihead_attention_module.cpp).
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+import gpu_util as G
+from pulsatrix_amd import native as N
+
+gpu = pytest.mark.gpu
+
+COMBOS = [
+    (0, 0, N.PRO_NONE, N.EPI_STORE), (0, 1, N.PRO_NONE, N.EPI_STORE), (1, 0, N.PRO_NONE, N.EPI_STORE),
+    (1, 1, N.PRO_NONE, N.EPI_STORE), (0, 0, N.PRO_NONE, N.EPI_STORE_BIAS), (0, 0, N.PRO_NONE, N.EPI_ADD_RESID),
+    (0, 0, N.PRO_NONE, N.EPI_MUL_X), (0, 1, N.PRO_NONE, N.EPI_MUL_X), (1, 0, N.PRO_NONE, N.EPI_MUL_X),
+    (0, 0, N.PRO_DIV_STAB, N.EPI_MUL_X), (0, 1, N.PRO_DIV_STAB, N.EPI_MUL_X), (0, 1, N.PRO_DIV_STAB, N.EPI_SPV),
+    (0, 0, N.PRO_NONE, N.EPI_ROPE_REL), (1, 0, N.PRO_NONE, N.EPI_ROPE_REL), (0, 0, N.PRO_NONE, N.EPI_VALUE_REL),
+    (1, 0, N.PRO_NONE, N.EPI_VALUE_REL), (0, 1, N.PRO_DIV_STAB, N.EPI_SWIGLU_REL),
+]
+TILES = [N.TILE_128x128, N.TILE_64x64, N.TILE_32x64, N.TILE_32x32]
+TILE_BN = {N.TILE_128x128: 128, N.TILE_64x64: 64, N.TILE_32x64: 64, N.TILE_32x32: 32}
+EPS = 1e-6
+
+
+def away(shape, seed):
+    """Uniform magnitudes in [0.5, 1.5) with random signs: denominators stay clear of zero."""
+    r = np.random.RandomState(seed)
+    return (r.uniform(0.5, 1.5, size=shape) * r.choice([-1.0, 1.0], size=shape)).astype(np.float32)
+
+
+def stab(z):
+    return z + EPS * np.where(z >= 0, 1.0, -1.0)
+
+
+def rope_tables(m, d, theta=10000.0):
+    half = d // 2
+    inv = theta ** (-np.arange(half, dtype=np.float64) * 2.0 / d)
+    ang = np.arange(m, dtype=np.float64)[:, None] * inv[None, :]
+    return np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+
+
+def expected(epi, acc, t, D, half_layout):
+    """The epilogue of include/pxk.h on a float64 accumulator tile."""
+    X, Y, W, Z, Z2, Z3, C0 = (t.get(k) for k in ("x", "y", "w", "z", "z2", "z3", "c0"))
+    eb, eb2 = t.get("eb"), t.get("eb2")
+    if epi == N.EPI_STORE:
+        return {"c": acc + 0.5 * C0}
+    if epi == N.EPI_STORE_BIAS:
+        return {"c": acc, "c2": acc + eb}
+    if epi == N.EPI_ADD_RESID:
+        return {"c": acc, "c2": acc + eb, "c3": X + acc + eb}
+    if epi == N.EPI_MUL_X:
+        return {"c": Y + X * acc}
+    if epi == N.EPI_SPV:
+        return {"c": X * acc / (2 * X + EPS * np.where(X >= 0, 1.0, -1.0))}
+    if epi == N.EPI_VALUE_REL:
+        r = Y * acc
+        return {"c": r, "c2": r / stab(Z + eb)}
+    if epi == N.EPI_SWIGLU_REL:
+        c = Y * W
+        rg = (c / (2 * c + EPS * np.where(c >= 0, 1.0, -1.0))) * (X * acc)
+        return {"c": rg / stab(Z2 + eb), "c2": rg / stab(Z3 + eb2)}
+    assert epi == N.EPI_ROPE_REL
+    m, n = acc.shape
+    cos, sin = t["cos"].astype(np.float64), t["sin"].astype(np.float64)
+    half = D // 2
+    col = np.arange(n)
+    d = col % D
+    hb = col - d
+    if half_layout:
+        i = np.where(d < half, d, d - half)
+        lo, hi = hb + i, hb + i + half
+    else:
+        i = d // 2
+        lo, hi = hb + 2 * i, hb + 2 * i + 1
+    r_lo, r_hi = Y[:, lo] * acc[:, lo], Y[:, hi] * acc[:, hi]
+    c, s = cos[:, i], sin[:, i]
+    d0, d1 = stab(Y[:, lo]), stab(Y[:, hi])
+    is_lo = (col == lo)[None, :]
+    r_in = np.where(is_lo, X * c / d0 * r_lo + X * s / d1 * r_hi, X * -s / d0 * r_lo + X * c / d1 * r_hi)
+    return {"c": r_in, "c2": r_in / stab(Z + eb)}
+
+
+def run(d, splits):
+    d.splits = splits
+    if splits > 1:
+        nbytes = N.gemm_workspace(d)
+        assert nbytes >= splits * d.m * d.n * 4
+        ws = G.empty((nbytes // 4,), 0.0)
+        d.workspace, d.workspace_bytes = G.ptr(ws).value, nbytes
+    return N.pxk().pxk_gemm(ctypes.byref(d), G.stream())
+
+
+@gpu
+@pytest.mark.parametrize("splits", [1, 3])
+@pytest.mark.parametrize("tile", TILES)
+@pytest.mark.parametrize("combo", COMBOS, ids=lambda c: "ta%d_tb%d_pro%d_epi%d" % c)
+def test_fused_gemm_on_every_tile(combo, tile, splits):
+    ta, tb, pro, epi = combo
+    rope = epi == N.EPI_ROPE_REL
+    D = 64 if rope and tile != N.TILE_32x32 else 16
+    m, n, k = 77, 128, 150  # ragged M and K; N = whole heads for the RoPE rule
+    a, b = G.uniform((k, m) if ta else (m, k), 1), G.uniform((n, k) if tb else (k, n), 2)
+    t = {"x": G.uniform((m, n), 3), "y": away((m, n), 4), "w": away((m, n), 5), "z": away((m, n), 6),
+         "z2": away((m, n), 7), "z3": away((m, n), 8), "c0": G.uniform((m, n), 9),
+         "eb": G.uniform((n,), 10), "eb2": G.uniform((n,), 11)}
+    t["cos"], t["sin"] = rope_tables(m, D)
+    zp, zb = away((m, k), 12), G.uniform((k,), 13)  # prologue denominators over A's layout, bias over k
+    a64 = (a.T if ta else a).astype(np.float64)
+    b64 = (b.T if tb else b).astype(np.float64)
+    if pro == N.PRO_DIV_STAB:
+        a64 = a64 / stab(zp.astype(np.float64) + zb)
+    acc = a64 @ b64
+    t64 = {key: v.astype(np.float64) for key, v in t.items()}
+    want = expected(epi, acc, t64, D, True)
+
+    dv = {key: G.dev(v) for key, v in t.items()}
+    outs = {key: G.empty((m, n)) for key in ("c", "c2", "c3")}
+    if epi == N.EPI_STORE:
+        outs["c"] = G.dev(t["c0"])
+    d = N.GemmDesc()
+    d.m, d.n, d.k, d.batch, d.inner, d.kgroups = m, n, k, 1, 1, 1
+    d.trans_a, d.trans_b, d.prologue, d.epilogue, d.eps, d.tile = ta, tb, pro, epi, EPS, tile
+    d.beta = 0.5 if epi == N.EPI_STORE else 0.0
+    d.a = N.operand(G.ptr(G.dev(a)).value, m if ta else k)
+    d.b = N.operand(G.ptr(G.dev(b)).value, k if tb else n)
+    for key in ("c", "c2", "c3"):
+        setattr(d, key, N.operand(G.ptr(outs[key]).value, n))
+    for key in ("x", "y", "w", "z2", "z3"):
+        setattr(d, key, N.operand(G.ptr(dv[key]).value, n))
+    if pro == N.PRO_DIV_STAB:
+        d.z = N.operand(G.ptr(G.dev(zp)).value, k)
+        d.z_bias = N.operand(G.ptr(G.dev(zb)).value, 0)
+    else:
+        d.z = N.operand(G.ptr(dv["z"]).value, n)
+    d.e_bias = N.operand(G.ptr(dv["eb"]).value, 0)
+    d.e_bias2 = N.operand(G.ptr(dv["eb2"]).value, 0)
+    d.cos_t, d.sin_t = G.ptr(dv["cos"]).value, G.ptr(dv["sin"]).value
+    d.head_dim, d.rope_half = D, 1
+    if epi == N.EPI_MUL_X and pro == N.PRO_NONE and ta == 0 and tb == 0:
+        d.y = N.operand(None, 0)  # the Y-less form: C = X * acc
+        want = {"c": t64["x"] * acc}
+    rc = run(d, splits)
+    assert rc == 0, N.pxk().pxk_last_error()
+    for key, ref in want.items():
+        G.assert_close(G.host(outs[key]), ref, 2e-5, "tile %d splits %d output %s" % (tile, splits, key))
+
+
+@gpu
+@pytest.mark.parametrize("half", [0, 1])
+@pytest.mark.parametrize("tile", [N.TILE_64x64, N.TILE_32x64])
+def test_rope_rule_epilogue_interleaved_and_half_pairs(half, tile):
+    """ROPE_REL for both pair layouts (rotate-half and interleaved)."""
+    m, n, k, D = 45, 128, 40, 64
+    a, b = G.uniform((m, k), 21), G.uniform((k, n), 22)
+    t = {"x": G.uniform((m, n), 23), "y": away((m, n), 24), "z": away((m, n), 25), "eb": G.uniform((n,), 26)}
+    t["cos"], t["sin"] = rope_tables(m, D)
+    acc = a.astype(np.float64) @ b.astype(np.float64)
+    want = expected(N.EPI_ROPE_REL, acc, {key: v.astype(np.float64) for key, v in t.items()}, D, half == 1)
+    dv = {key: G.dev(v) for key, v in t.items()}
+    c, c2 = G.empty((m, n)), G.empty((m, n))
+    d = N.GemmDesc()
+    d.m, d.n, d.k, d.batch, d.inner, d.kgroups = m, n, k, 1, 1, 1
+    d.epilogue, d.eps, d.tile = N.EPI_ROPE_REL, EPS, tile
+    d.a, d.b = N.operand(G.ptr(G.dev(a)).value, k), N.operand(G.ptr(G.dev(b)).value, n)
+    d.c, d.c2 = N.operand(G.ptr(c).value, n), N.operand(G.ptr(c2).value, n)
+    d.x, d.y, d.z = (N.operand(G.ptr(dv[key]).value, n) for key in ("x", "y", "z"))
+    d.e_bias = N.operand(G.ptr(dv["eb"]).value, 0)
+    d.cos_t, d.sin_t = G.ptr(dv["cos"]).value, G.ptr(dv["sin"]).value
+    d.head_dim, d.rope_half = D, half
+    assert run(d, 1) == 0, N.pxk().pxk_last_error()
+    G.assert_close(G.host(c), want["c"], 2e-5, "r_in")
+    G.assert_close(G.host(c2), want["c2"], 2e-5, "r_in / z")
+
+
+def test_rope_rule_rejects_heads_wider_than_the_tile():
+    """CPU-side: a 64-wide head cannot be split across 32-wide tiles; nothing is launched."""
+    d = N.GemmDesc()
+    d.m, d.n, d.k, d.batch, d.inner, d.kgroups = 8, 128, 8, 1, 1, 1
+    d.epilogue, d.tile, d.head_dim = N.EPI_ROPE_REL, N.TILE_32x32, 64
+    for key in ("a", "b", "c2", "x", "y", "z"):
+        setattr(d, key, N.operand(16, 8))  # never dereferenced: validation fails first
+    d.cos_t = d.sin_t = 16
+    assert N.pxk().pxk_gemm(ctypes.byref(d), None) == 1
+    assert b"do not fit" in N.pxk().pxk_last_error()

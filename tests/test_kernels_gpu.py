@@ -108,9 +108,21 @@ def test_split_k_requires_workspace():
     assert N.pxk().pxk_gemm(ctypes.byref(d), None) == 3
 
 
+def launch(d, tile, splits):
+    """pxk_gemm with a pinned tile shape / split count (0 = the library's choice)."""
+    d.tile, d.splits = tile, splits
+    nbytes = N.gemm_workspace(d)
+    if nbytes:
+        ws = G.empty((nbytes // 4,), 0.0)
+        d.workspace, d.workspace_bytes = G.ptr(ws).value, nbytes
+    N.gemm(d, G.stream())
+
+
 @gpu
+@pytest.mark.parametrize("tile,splits", [(0, 0), (N.TILE_128x128, 1), (N.TILE_64x64, 2), (N.TILE_32x64, 1),
+                                         (N.TILE_32x32, 3)])
 @pytest.mark.parametrize("L,H,Hkv,D", [(37, 4, 2, 16), (128, 9, 3, 64)])
-def test_gqa_attention_gemms_match_numpy(L, H, Hkv, D):
+def test_gqa_attention_gemms_match_numpy(L, H, Hkv, D, tile, splits):
     """Scores (TRI), P @ V (K <= M) and the GQA key sum (kgroups, K >= M) with head-packed layouts."""
     torch = G.torch_cuda()
     grp = H // Hkv
@@ -125,7 +137,7 @@ def test_gqa_attention_gemms_match_numpy(L, H, Hkv, D):
     d.a = N.operand(G.ptr(qd).value, H * D, 0, D)
     d.b = N.operand(G.ptr(kd).value, Hkv * D, 0, D, grp)
     d.c = N.operand(G.ptr(raw).value, L, 0, L * L)
-    N.gemm(d, G.stream())
+    launch(d, tile, splits)
     qh = q.reshape(L, H, D).transpose(1, 0, 2).astype(np.float64)
     kh = kk.reshape(L, Hkv, D).transpose(1, 0, 2).astype(np.float64)
     ref = np.einsum("hid,hjd->hij", qh, np.repeat(kh, grp, axis=0))
@@ -140,7 +152,7 @@ def test_gqa_attention_gemms_match_numpy(L, H, Hkv, D):
     d.a = N.operand(G.ptr(pd).value, L, 0, L * L)
     d.b = N.operand(G.ptr(kd).value, Hkv * D, 0, D, grp)
     d.c = N.operand(G.ptr(ctx).value, H * D, 0, D)
-    N.gemm(d, G.stream())
+    launch(d, tile, splits)
     ref = np.einsum("hij,hjd->ihd", p.astype(np.float64), np.repeat(kh, grp, axis=0)).reshape(L, H * D)
     G.assert_close(G.host(ctx), ref, 1e-4, "context")
     # per KV head: sum over its query heads of P_h^T @ Q_h, i >= j
@@ -151,7 +163,7 @@ def test_gqa_attention_gemms_match_numpy(L, H, Hkv, D):
     d.a = N.operand(G.ptr(pd).value, L, 0, grp * L * L, 0, L * L)
     d.b = N.operand(G.ptr(qd).value, H * D, 0, grp * D, 0, D)
     d.c = N.operand(G.ptr(out).value, Hkv * D, 0, D)
-    N.gemm(d, G.stream())
+    launch(d, tile, splits)
     per_head = np.einsum("hij,hid->hjd", p.astype(np.float64), qh)
     ref = per_head.reshape(Hkv, grp, L, D).sum(axis=1).transpose(1, 0, 2).reshape(L, Hkv * D)
     G.assert_close(G.host(out), ref, 1e-4, "kv sum")

@@ -94,8 +94,30 @@ def test_transformer_block_matches_lxt_reference_values():
     assert np.all(np.abs(r_in.ravel() - expected) <= 1e-4 * np.maximum(1, np.abs(expected)))
 
 
+def oracle_sensitivity(cfg, params, x, seed, eps, bid, trials=3):
+    """Largest relative change of the oracle's own block relevance when params and x move by
+    ~2e-7 relative (float32 rounding). The epsilon rule divides by pre-activations; where one sits
+    near zero, any fp32 evaluation order lands further apart than the 1e-3 gate, so a parity case
+    must first show that the oracle itself is stable there."""
+    ref = oc.oracle().block(cfg, params)
+    ref.forward(x)
+    r0 = ref.relevance(seed, eps, bid)
+    worst = 0.0
+    for t in range(trials):
+        rs = np.random.RandomState(100 + t)
+        p2 = (params * (1 + 2e-7 * rs.standard_normal(params.shape))).astype(np.float32)
+        x2 = (x * (1 + 2e-7 * rs.standard_normal(x.shape))).astype(np.float32)
+        other = oc.oracle().block(cfg, p2)
+        other.forward(x2)
+        worst = max(worst, float(np.abs(other.relevance(seed, eps, bid) - r0).max() / np.abs(r0).max()))
+    return worst
+
+
 @pytest.mark.parametrize("rope_half,causal", [(0, 0), (1, 1)])
 def test_block_with_biases_matches_oracle(rope_half, causal):
+    """Biases on every projection under both rules (bias in the denominator, and the legacy
+    pre-bias rule). With seeded N(0, 1) relevance and eps 1e-6 this block is ill-conditioned (the
+    oracle moves by up to 3e-3 under rounding-level input changes); eps 0.1 keeps it below 1e-4."""
     cfg = b_config(hidden_size=48, num_heads=4, num_kv_heads=2, head_dim=12, intermediate_size=40, qkv_bias=1,
                    out_bias=1, mlp_bias=1, causal=causal, rope_rotate_half=rope_half)
     params = oc.synthetic_params(cfg, 3, std=0.2, block=True)
@@ -103,7 +125,8 @@ def test_block_with_biases_matches_oracle(rope_half, causal):
     ref, gpu = oc.oracle().block(cfg, params), models.Block(to_px(cfg), params)
     G.assert_close(gpu.forward(x), ref.forward(x), 1e-4, "forward")
     seed = oc.fill_normal(2 * 7 * 48, 8, 1.0).reshape(2, 7, 48)
-    for eps, bid in ((1e-6, False), (1e-6, True)):
+    for eps, bid in ((0.1, False), (0.1, True)):
+        assert oracle_sensitivity(cfg, params, x, seed, eps, bid) < 1e-4
         expect_relevance_agrees(gpu.relevance(seed, eps, bid), ref.relevance(seed, eps, bid), "bid=%s" % bid)
 
 
