@@ -190,6 +190,20 @@ int pxk_dot(const float* a, const float* b, int64_t n, float* out, float* partia
 size_t pxk_reduce_partials(int64_t n);
 
 /* ---- attention ------------------------------------------------------------------------------- */
+/* Fused causal (or full) GQA attention forward over (n, l) tokens: raw = Q K^T per query head,
+ * P = softmax(scale * raw) over the visible keys, ctx = P V, in one launch. q, k, v are token-major
+ * head-packed rows (row b*l + i, head h at column h*head_dim; query head h reads KV head
+ * h / (heads / kv_heads)); raw and P are (n, heads, l, l), P with zeros past the visible keys and
+ * raw defined on the visible keys only; ctx is written head-packed like q. Replaces the sequence of
+ * MultiHeadAttentionModule::forward (multihead_attention_module.cpp:268-291): per-head gemm_ex,
+ * axpby scale, attention_mask_fill, softmax_rows, gemm. pxk_attention_supported() tells whether
+ * a shape is handled: head_dim a multiple of 4 up to 128, q/k row strides a multiple of 4, and a
+ * workgroup's 16 score rows (16 x seq_len floats) within LDS, about 2000 tokens. */
+int pxk_attention_supported(int64_t head_dim, int64_t seq_len, int64_t ldq, int64_t ldk, int64_t ldv);
+int pxk_attention_forward(const float* q, int64_t ldq, const float* k, int64_t ldk, const float* v, int64_t ldv,
+                          float* raw, float* p, float* ctx, int64_t ldctx, int64_t n, int64_t l, int64_t heads,
+                          int64_t kv_heads, int64_t head_dim, float scale, int causal, void* stream);
+
 /* Causal/plain softmax of scaled scores (the module's axpby + attention_mask_fill(lowest) +
  * softmax_rows, multihead_attention_module.cpp:280-285): P = softmax(scale * raw) over the keys
  * each query sees; masked entries of P are written 0. raw (slices, L, L); only its visible

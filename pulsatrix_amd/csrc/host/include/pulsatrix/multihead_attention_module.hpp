@@ -78,6 +78,8 @@ protected:
 private:
     void pack_weights();
     void ensure_tables(int64_t l);
+    void run_attention_unfused(const float* q, int64_t ldq, const float* k, int64_t ldk, const float* v, int64_t n,
+                               int64_t l);
 
     AttentionConfig config_;
     int64_t d_, H_, Hkv_, D_;

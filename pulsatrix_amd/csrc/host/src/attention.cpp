@@ -115,7 +115,7 @@ const float* MultiHeadAttentionModule::run_forward(const float* x, int64_t n, in
     N_ = n;
     L_ = l;
     x_ = x;
-    const int64_t M = n * l, qd = H_ * D_, kvd = Hkv_ * D_, w3 = qd + 2 * kvd, grp = H_ / Hkv_, LL = l * l;
+    const int64_t M = n * l, qd = H_ * D_, kvd = Hkv_ * D_, w3 = qd + 2 * kvd, LL = l * l;
     const bool causal = config_.causal;
     void* st = be_->stream();
 
@@ -149,34 +149,16 @@ const float* MultiHeadAttentionModule::run_forward(const float* x, int64_t n, in
         ldq = qd;
         ldk = kvd;
     }
-    // 3. raw scores = Q K^T per query head; K read through the KV-head map.
     float* raw = raw_.ensure(be_, n * H_ * LL);
-    {
-        pxk_gemm_desc d = gemm_desc(l, l, D_);
-        d.batch = n * H_;
-        d.inner = H_;
-        d.trans_b = 1;
-        d.causal = causal ? PXK_CAUSAL_TRI : PXK_CAUSAL_NONE;
-        d.a = mat(q, ldq, l * ldq, D_);
-        d.b = mat(k, ldk, l * ldk, D_, grp);
-        d.c = mat(raw, l, H_ * LL, LL);
-        be_->run_gemm(d);
-    }
-    // 4. P = softmax(scale * raw) over the visible keys.
     float* p = p_.ensure(be_, n * H_ * LL);
-    MI355XBackend::check(pxk_attention_softmax(raw, p, n * H_, l, score_scale(), causal, st),
-                         "MultiHeadAttentionModule::forward (softmax)");
-    // 5. context = P V, written head-packed (N*L, H*D): the merge permute is the store layout.
     float* ctx = ctx_.ensure(be_, M * qd);
-    {
-        pxk_gemm_desc d = gemm_desc(l, D_, l);
-        d.batch = n * H_;
-        d.inner = H_;
-        d.causal = causal ? PXK_CAUSAL_K_LE_M : PXK_CAUSAL_NONE;
-        d.a = mat(p, l, H_ * LL, LL);
-        d.b = mat(v, w3, l * w3, D_, grp);
-        d.c = mat(ctx, qd, l * qd, D_);
-        be_->run_gemm(d);
+    if (pxk_attention_supported(D_, l, ldq, ldk, w3)) {
+        // 3-5 fused: scores, mask, softmax and P V in one launch, P and raw kept for relevance.
+        MI355XBackend::check(pxk_attention_forward(q, ldq, k, ldk, v, w3, raw, p, ctx, qd, n, l, H_, Hkv_, D_,
+                                                   score_scale(), causal, st),
+                             "MultiHeadAttentionModule::forward (attention)");
+    } else {
+        run_attention_unfused(q, ldq, k, ldk, v, n, l);
     }
     // 6. output projection, with the block's residual add fused into the epilogue when asked.
     float* oz = out_z_.ensure(be_, M * d_);
@@ -200,6 +182,43 @@ const float* MultiHeadAttentionModule::run_forward(const float* x, int64_t n, in
         be_->run_gemm(d);
     }
     return oy;
+}
+
+// Scores GEMM, softmax and P V as three launches: head_dim outside pxk_attention_supported().
+void MultiHeadAttentionModule::run_attention_unfused(const float* q, int64_t ldq, const float* k, int64_t ldk,
+                                                     const float* v, int64_t n, int64_t l) {
+    const int64_t qd = H_ * D_, kvd = Hkv_ * D_, w3 = qd + 2 * kvd, grp = H_ / Hkv_, LL = l * l;
+    const bool causal = config_.causal;
+    void* st = be_->stream();
+    float* raw = raw_.data();
+    float* p = p_.data();
+    float* ctx = ctx_.data();
+    // 3. raw scores = Q K^T per query head; K read through the KV-head map.
+    {
+        pxk_gemm_desc d = gemm_desc(l, l, D_);
+        d.batch = n * H_;
+        d.inner = H_;
+        d.trans_b = 1;
+        d.causal = causal ? PXK_CAUSAL_TRI : PXK_CAUSAL_NONE;
+        d.a = mat(q, ldq, l * ldq, D_);
+        d.b = mat(k, ldk, l * ldk, D_, grp);
+        d.c = mat(raw, l, H_ * LL, LL);
+        be_->run_gemm(d);
+    }
+    // 4. P = softmax(scale * raw) over the visible keys.
+    MI355XBackend::check(pxk_attention_softmax(raw, p, n * H_, l, score_scale(), causal, st),
+                         "MultiHeadAttentionModule::forward (softmax)");
+    // 5. context = P V, written head-packed (N*L, H*D): the merge permute is the store layout.
+    {
+        pxk_gemm_desc d = gemm_desc(l, D_, l);
+        d.batch = n * H_;
+        d.inner = H_;
+        d.causal = causal ? PXK_CAUSAL_K_LE_M : PXK_CAUSAL_NONE;
+        d.a = mat(p, l, H_ * LL, LL);
+        d.b = mat(v, w3, l * w3, D_, grp);
+        d.c = mat(ctx, qd, l * qd, D_);
+        be_->run_gemm(d);
+    }
 }
 
 const float* MultiHeadAttentionModule::run_relevance(const float* relevance_out, const LRPRuleConfig& config,

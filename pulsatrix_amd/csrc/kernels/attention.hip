@@ -1,0 +1,329 @@
+// attention.hip -- fused causal GQA attention for gfx950 (include/pxk.h): scores, mask, softmax
+// and P V in one launch, keeping what the AttnLRP pass reads (raw scores and P).
+//
+// Tiling. One workgroup owns 16 query rows of one query head; its four wave64s take the visible
+// keys in 16-key tiles, round-robin. Scores are formed transposed, S^T = K Q^T, on
+// v_mfma_f32_16x16x4_f32: lane l then holds S[row = l % 16][key = 4 (l / 16) + r] in its r-th
+// result register, which is exactly the B-operand layout of ctx^T = V^T P^T. P therefore never
+// leaves registers between the two products; a row's max and sum are in-lane reductions plus two
+// wavefront shuffles (lanes l, l ^ 16, l ^ 32, l ^ 48 share a row). K and V are streamed from L2
+// (the 16-row workgroups of one KV head re-read the same 2 x L x D floats) two tiles ahead, with
+// no LDS staging and no barrier in the key loop.
+//
+// Softmax. Each wave runs an online softmax over its tiles (running max, rescaled sum and
+// context); the four waves are merged in LDS in wave order at the end (deterministic). The raw
+// scores of the workgroup's 16 rows wait in LDS meanwhile (16 x L floats), so the last pass
+// writes raw and the normalized P = exp(scale * raw - max) / sum (DeviceBackend::softmax_rows,
+// cpu_backend.cpp:292-310; the hardware exponential __expf on arguments <= 0, and one reciprocal
+// per row) as whole contiguous row segments, 16 threads per row, reading nothing back from HBM. P is written over whole rows, zeros past the
+// visible keys: the relevance pass reads it as a dense operand.
+#include <cmath>
+
+#include "common.hpp"
+
+namespace pxk {
+namespace {
+
+typedef float f4 __attribute__((ext_vector_type(4)));
+constexpr int kThreads = 256;
+constexpr int kWaves = 4;
+
+struct FwdArgs {
+    const float* q;
+    const float* k;
+    const float* v;
+    float* raw;
+    float* p;
+    float* ctx;
+    int64_t ldq, ldk, ldv, ldctx;
+    int n, l, heads, kv_heads, D;
+    float scale;
+    int causal;
+    int lds_ld;  // row stride of the LDS score block
+};
+
+__device__ __forceinline__ float row_max4(float v) {
+    v = fmaxf(v, __shfl_xor(v, 16, kWave));
+    return fmaxf(v, __shfl_xor(v, 32, kWave));
+}
+__device__ __forceinline__ float row_sum4(float v) {
+    v += __shfl_xor(v, 16, kWave);
+    return v + __shfl_xor(v, 32, kWave);
+}
+
+// DT: head_dim in 16-wide tiles (D <= 16 DT, D % 4 == 0). VEC: l % 4 == 0 (128-bit row stores).
+template <int DT, bool VEC>
+__global__ void __launch_bounds__(kThreads) attn_fwd_kernel(const FwdArgs a) {
+    extern __shared__ __attribute__((aligned(16))) float sc[];  // [16][lds_ld] raw scores of the block's rows
+    __shared__ float s_m[kWaves][16], s_s[kWaves][16];
+    __shared__ __attribute__((aligned(16))) float s_ctx[kWaves][16][16 * DT + 4];
+    __shared__ float f_m[16], f_s[16];
+
+    const int lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: the tile loop is scalar
+    const int l = a.l, D = a.D, ld = a.lds_ld;
+    const int nrb = (l + 15) / 16;
+    const int rb = blockIdx.x % nrb, bh = blockIdx.x / nrb;
+    const int h = bh % a.heads, b = bh / a.heads;
+    const int hk = h / (a.heads / a.kv_heads);
+    const int i0 = rb * 16, row = i0 + c;
+    const bool row_ok = row < l;
+
+    // Q^T fragments: qf[t][s] = Q[row][16 t + 4 g + s].
+    f4 qf[DT];
+    {
+        const float* qp = a.q + (static_cast<int64_t>(b) * l + (row_ok ? row : l - 1)) * a.ldq + h * D;
+#pragma unroll
+        for (int t = 0; t < DT; ++t) {
+            const int d0 = 16 * t + 4 * g;
+            qf[t] = (row_ok && d0 < D) ? *reinterpret_cast<const f4*>(qp + d0) : f4{0.f, 0.f, 0.f, 0.f};
+        }
+    }
+    const float* kbase = a.k + static_cast<int64_t>(b) * l * a.ldk + hk * D;
+    const float* vbase = a.v + static_cast<int64_t>(b) * l * a.ldv + hk * D;
+    const int vis_end = a.causal ? min(i0 + 16, l) : l;
+    const int ntile = (vis_end + 15) / 16;
+
+    float m = -INFINITY, ssum = 0.0f;
+    f4 acc[DT];
+#pragma unroll
+    for (int t = 0; t < DT; ++t) acc[t] = f4{0.f, 0.f, 0.f, 0.f};
+
+    // Operands of one 16-key tile: kf[t][s] = K[key0 + c][16 t + 4 g + s] (A of S^T) and
+    // vf[t][s] = V[key0 + 4 g + s][16 t + c] (A of ctx^T). Two register sets per wave: while one
+    // tile is on the MFMA pipe the next one's K and V are in flight. A set is reloaded right after
+    // its last read (K after the score MFMAs, V after the context MFMAs), so old and new values
+    // never live at once and the loop needs no register copies (a copy of a register with a load
+    // pending would wait for that load). Addresses are clamped into the matrix and no value is
+    // masked: a K column past head_dim meets a zero Q fragment, a V row past the last key meets a
+    // zero probability, and ctx rows past head_dim are never stored. Every lane issues the same
+    // loads, with no branch around them.
+    f4 kf[2][DT], vf[2][DT];
+    // 32-bit element offsets from the head's base (l * ld < 2^31 is checked on the host).
+    const int ldk = static_cast<int>(a.ldk), ldv = static_cast<int>(a.ldv);
+    auto load_k = [&](int set, int kt) {
+        const int key0 = 16 * min(kt, ntile - 1);  // past the last tile: the last one again, unused
+        const float* kp = kbase + min(key0 + c, l - 1) * ldk;
+#pragma unroll
+        for (int t = 0; t < DT; ++t) kf[set][t] = *reinterpret_cast<const f4*>(kp + min(16 * t + 4 * g, D - 4));
+    };
+    auto load_v = [&](int set, int kt) {
+        const int key0 = 16 * min(kt, ntile - 1);
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+            const float* vp = vbase + min(key0 + 4 * g + st, l - 1) * ldv;
+#pragma unroll
+            for (int t = 0; t < DT; ++t) vf[set][t][st] = vp[min(16 * t + c, D - 1)];
+        }
+    };
+    auto tile = [&](int set, int kt) {
+        const int key0 = 16 * kt;
+        // S^T tile = K[key0 .. key0 + 15] Q^T over the head dimension.
+        f4 s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int t = 0; t < DT; ++t)
+#pragma unroll
+            for (int st = 0; st < 4; ++st) s = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[set][t][st], qf[t][st], s, 0, 0, 0);
+        // The reloads stay where they are written: the scheduler would otherwise sink them to the
+        // end of the loop body and the next tile would wait for them.
+        __builtin_amdgcn_sched_barrier(0);
+        load_k(set, kt + 2 * kWaves);
+        __builtin_amdgcn_sched_barrier(0);
+        // s[r] = raw score of (row, key0 + 4 g + r), kept in LDS for the last pass.
+        const int kk0 = key0 + 4 * g;
+        if (kt < ntile) *reinterpret_cast<f4*>(sc + c * ld + kk0) = s;
+        float x[4];
+        bool valid[4];
+        float mt = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int kk = kk0 + r;
+            valid[r] = (kk < l) & ((!a.causal) | (kk <= row));
+            x[r] = a.scale * s[r];
+            mt = fmaxf(mt, valid[r] ? x[r] : -INFINITY);
+        }
+        mt = row_max4(mt);
+        const float m_new = fmaxf(m, mt);
+        const float alpha = m_new == -INFINITY ? 1.0f : __expf(m - m_new);
+        float e[4];
+        float part = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            e[r] = valid[r] ? __expf(x[r] - m_new) : 0.0f;
+            part += e[r];
+        }
+        ssum = ssum * alpha + part;
+        m = m_new;
+        // ctx^T (D x rows) += V^T (D x keys) P^T (keys x rows); the rescale is per row = per lane.
+#pragma unroll
+        for (int t = 0; t < DT; ++t) {
+            acc[t] *= alpha;
+#pragma unroll
+            for (int st = 0; st < 4; ++st)
+                acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf[set][t][st], e[st], acc[t], 0, 0, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        load_v(set, kt + 2 * kWaves);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    // Tiles go in pairs, the second one unconditionally: past the last tile every key of it is
+    // masked (keys >= 16 ntile are past the diagonal, or past l), so it leaves m, the sum and the
+    // context unchanged. No branch splits the load stream.
+    load_k(0, wave);
+    load_v(0, wave);
+    load_k(1, wave + kWaves);
+    load_v(1, wave + kWaves);
+    for (int kt = wave; kt < ntile; kt += 2 * kWaves) {
+        tile(0, kt);
+        tile(1, kt + kWaves);
+    }
+
+    // Merge the four waves: acc[t][r] = ctx^T[16 t + 4 g + r][row c] of this wave.
+    ssum = row_sum4(ssum);
+    if (g == 0) {
+        s_m[wave][c] = m;
+        s_s[wave][c] = ssum;
+    }
+#pragma unroll
+    for (int t = 0; t < DT; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) s_ctx[wave][c][16 * t + 4 * g + r] = acc[t][r];
+    __syncthreads();
+    const int rr = threadIdx.x >> 4, cc = threadIdx.x & 15;  // 16 rows x 16 threads
+    const int orow = i0 + rr;
+    {
+        float mx = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) mx = fmaxf(mx, s_m[w][rr]);
+        float wsc[kWaves];
+        float tot = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+            wsc[w] = s_m[w][rr] == -INFINITY ? 0.0f : __expf(s_m[w][rr] - mx);
+            tot += s_s[w][rr] * wsc[w];
+        }
+        if (cc == 0) {
+            f_m[rr] = mx;
+            f_s[rr] = tot;
+        }
+        if (orow < l) {
+            float* cp = a.ctx + (static_cast<int64_t>(b) * l + orow) * a.ldctx + h * D;
+            for (int d = cc; d < D; d += 16) {
+                float v = 0.0f;
+#pragma unroll
+                for (int w = 0; w < kWaves; ++w) v += s_ctx[w][rr][d] * wsc[w];
+                cp[d] = v / tot;
+            }
+        }
+    }
+    __syncthreads();
+
+    // raw (visible keys) and P (every key, zeros past the visible ones) as contiguous row segments.
+    if (orow < l) {
+        const float mx = f_m[rr], inv = 1.0f / f_s[rr];
+        const int vis = a.causal ? orow + 1 : l;
+        const int64_t off = ((static_cast<int64_t>(b) * a.heads + h) * l + orow) * l;
+        float* prow = a.p + off;
+        float* rrow = a.raw + off;
+        const float* srow = sc + rr * ld;
+        if constexpr (VEC) {
+            for (int k0 = 4 * cc; k0 < l; k0 += 64) {
+                f4 out = {0.f, 0.f, 0.f, 0.f};
+                if (k0 < vis) {
+                    const f4 x = *reinterpret_cast<const f4*>(srow + k0);
+                    if (k0 + 3 < vis) {
+                        *reinterpret_cast<f4*>(rrow + k0) = x;
+                    } else {
+#pragma unroll
+                        for (int r = 0; r < 4; ++r)
+                            if (k0 + r < vis) rrow[k0 + r] = x[r];
+                    }
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) out[r] = k0 + r < vis ? __expf(a.scale * x[r] - mx) * inv : 0.0f;
+                }
+                *reinterpret_cast<f4*>(prow + k0) = out;
+            }
+        } else {
+            for (int k = cc; k < l; k += 16) {
+                float out = 0.0f;
+                if (k < vis) {
+                    const float x = srow[k];
+                    rrow[k] = x;
+                    out = __expf(a.scale * x - mx) * inv;
+                }
+                prow[k] = out;
+            }
+        }
+    }
+}
+
+}  // namespace
+}  // namespace pxk
+
+using namespace pxk;
+
+namespace {
+
+constexpr int kMaxLds = 160 * 1024;  // gfx950 LDS per workgroup
+
+// Row stride of the LDS score block: a multiple of 64 floats plus 16, so a wave's 16-byte
+// accesses to 4 consecutive rows (the score-tile writes, the last pass's row reads) fall in
+// distinct banks.
+int score_lds_ld(int64_t l) { return static_cast<int>((l + 63) / 64 * 64 + 16); }
+
+template <int DT>
+int static_lds() {
+    return static_cast<int>(sizeof(float) * (2 * kWaves * 16 + kWaves * 16 * (16 * DT + 4) + 2 * 16));
+}
+
+int dt_of(int64_t head_dim) { return head_dim <= 16 ? 1 : head_dim <= 32 ? 2 : head_dim <= 64 ? 4 : 8; }
+
+int lds_bytes_needed(int64_t head_dim, int64_t l) {
+    const int stat = dt_of(head_dim) == 8 ? static_lds<8>() : static_lds<4>();
+    return stat + 16 * score_lds_ld(l) * static_cast<int>(sizeof(float));
+}
+
+}  // namespace
+
+extern "C" int pxk_attention_supported(int64_t head_dim, int64_t seq_len, int64_t ldq, int64_t ldk, int64_t ldv) {
+    return head_dim > 0 && head_dim <= 128 && head_dim % 4 == 0 && ldq % 4 == 0 && ldk % 4 == 0 && ldv >= head_dim &&
+           seq_len >= 0 && seq_len <= 8192 && lds_bytes_needed(head_dim, seq_len) <= kMaxLds;
+}
+
+extern "C" int pxk_attention_forward(const float* q, int64_t ldq, const float* k, int64_t ldk, const float* v,
+                                     int64_t ldv, float* raw, float* p, float* ctx, int64_t ldctx, int64_t n,
+                                     int64_t l, int64_t heads, int64_t kv_heads, int64_t head_dim, float scale,
+                                     int causal, void* stream) {
+    if (n < 0 || l < 0 || heads <= 0 || kv_heads <= 0 || heads % kv_heads != 0)
+        return fail(PXK_ERR_INVALID, "pxk_attention_forward: bad sizes (heads must be a multiple of kv_heads)");
+    if (!pxk_attention_supported(head_dim, l, ldq, ldk, ldv) || ldq < heads * head_dim ||
+        ldk < kv_heads * head_dim || ldv < kv_heads * head_dim || ldctx < heads * head_dim)
+        return fail(PXK_ERR_INVALID, "pxk_attention_forward: head_dim must be a multiple of 4 up to 128, the "
+                                     "sequence's score rows must fit LDS (about 2000 tokens), and the row strides "
+                                     "must hold every head (q and k strides a multiple of 4)");
+    if (!aligned16(q) || !aligned16(k))
+        return fail(PXK_ERR_INVALID, "pxk_attention_forward: q and k must be 16-byte aligned");
+    if (n == 0 || l == 0) return PXK_OK;
+    const int64_t blocks = n * heads * ((l + 15) / 16);
+    if (blocks > (int64_t{1} << 31) - 1 || n * heads * l * l > (int64_t{1} << 40) || l * ldk >= (int64_t{1} << 31) ||
+        l * ldv >= (int64_t{1} << 31))
+        return fail(PXK_ERR_INVALID, "pxk_attention_forward: problem too large");
+    const int lds_ld = score_lds_ld(l);
+    FwdArgs a{q, k, v, raw, p, ctx, ldq, ldk, ldv, ldctx, static_cast<int>(n), static_cast<int>(l),
+              static_cast<int>(heads), static_cast<int>(kv_heads), static_cast<int>(head_dim), scale, causal != 0,
+              lds_ld};
+    const bool vec = l % 4 == 0 && aligned16(raw) && aligned16(p);
+    using K = void (*)(const FwdArgs);
+    static const K table[2][4] = {
+        {attn_fwd_kernel<1, false>, attn_fwd_kernel<2, false>, attn_fwd_kernel<4, false>, attn_fwd_kernel<8, false>},
+        {attn_fwd_kernel<1, true>, attn_fwd_kernel<2, true>, attn_fwd_kernel<4, true>, attn_fwd_kernel<8, true>}};
+    const int dt = dt_of(head_dim);
+    const K fn = table[vec ? 1 : 0][dt == 1 ? 0 : dt == 2 ? 1 : dt == 4 ? 2 : 3];
+    const size_t dyn = static_cast<size_t>(16) * lds_ld * sizeof(float);
+    if (dyn > 64 * 1024 &&
+        hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            static_cast<int>(dyn)) != hipSuccess)
+        return fail(PXK_ERR_LAUNCH, "pxk_attention_forward: %zu bytes of LDS refused", dyn);
+    hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), dyn, S(stream), a);
+    return launched("pxk_attention_forward");
+}

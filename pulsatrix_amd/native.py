@@ -69,6 +69,8 @@ PXK_SIGNATURES = {
     "pxk_row_sums": "ppiip",
     "pxk_sum": "pippp",
     "pxk_dot": "ppippp",
+    "pxk_attention_supported": "iiiii",
+    "pxk_attention_forward": "pipipipppiiiiiifnp",
     "pxk_attention_softmax": "ppiifnp",
     "pxk_attention_lrp_scores": "ppppiiffnp",
     "pxk_rope_qk": "ppippppiiiiinp",
