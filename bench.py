@@ -232,7 +232,8 @@ def main():
     ker2_s = time_kernel(torch, stream, lambda: N.gemm(desc2, models.stream()), 50)
     achieved = flops / ker_s / 1e12
     tile, splits = N.gemm_plan(desc)
-    tile_name = {N.TILE_128x128: "128x128", N.TILE_64x64: "64x64", N.TILE_32x64: "32x64", N.TILE_32x32: "32x32"}[tile]
+    tile_name = {N.TILE_128x128: "128x128", N.TILE_64x64: "64x64", N.TILE_32x64: "32x64", N.TILE_32x32: "32x32",
+                 N.TILE_32x64_DIRECT: "32x64 direct", N.TILE_32x32_DIRECT: "32x32 direct"}[tile]
 
     out = {
         "metric": "forward+AttnLRP tokens/s, 135M-shape LM seq 512; GEMM % fp32 MFMA peak",

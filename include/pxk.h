@@ -90,7 +90,9 @@ enum {
     PXK_TILE_128x128 = 1, /* 4 waves of 64x64, K stage 32 */
     PXK_TILE_64x64 = 2,   /* 4 waves of 32x32, K stage 32 */
     PXK_TILE_32x64 = 3,   /* 4 waves each on a quarter of a 64-wide K stage, summed in LDS */
-    PXK_TILE_32x32 = 4    /* as 32x64 */
+    PXK_TILE_32x32 = 4,   /* as 32x64 */
+    PXK_TILE_32x64_DIRECT = 5, /* as 32x64, each wave streaming its operands from L2 into registers */
+    PXK_TILE_32x32_DIRECT = 6
 };
 
 typedef struct pxk_gemm_desc {
@@ -203,6 +205,44 @@ int pxk_attention_supported(int64_t head_dim, int64_t seq_len, int64_t ldq, int6
 int pxk_attention_forward(const float* q, int64_t ldq, const float* k, int64_t ldk, const float* v, int64_t ldv,
                           float* raw, float* p, float* ctx, int64_t ldctx, int64_t n, int64_t l, int64_t heads,
                           int64_t kv_heads, int64_t head_dim, float scale, int causal, void* stream);
+
+/* The AttnLRP pass of one attention layer through the steps that need whole score rows, fused per
+ * query head and 16-row block (MultiHeadAttentionModule::propagate_relevance,
+ * multihead_attention_module.cpp:404-485, with lrp_bilinear_matmul lrp_math.hpp:57-86,
+ * lrp_softmax_rows :89-98 and lrp_rope :104-123):
+ *   r_attn = P * (s_pv V^T)                  P V bilinear share (s_pv = r_ctx / (2 ctx + eps sign ctx))
+ *   s      = (scale raw)(r_attn - P sum_row r_attn) / (2 raw + eps sign raw), 0 where masked
+ *   r_q    = Q * (s K)                        Q K^T bilinear share (Q, K after RoPE)
+ *   g_q    = RoPE rule(x = Q before RoPE, y = Q, r_q) / stab(z_q + bias)   (no RoPE: r_q / stab(...))
+ * s is written over whole rows (zeros past the visible keys) for the key share. Layouts as for
+ * pxk_attention_forward; z, q_pre and g are head-packed rows with their own strides, bias (heads *
+ * head_dim) is NULL under the pre-bias rule or without a q_proj bias. */
+typedef struct pxk_attn_rel_desc {
+    int64_t n, l, heads, kv_heads, head_dim;
+    float scale, eps;
+    int32_t causal, rope, rope_half, reserved;
+    const float* spv;
+    int64_t ld_spv;
+    const float* v;
+    int64_t ld_v;
+    const float* k;
+    int64_t ld_k;
+    const float* p;
+    const float* raw;
+    float* s;
+    const float* q;
+    int64_t ld_q;
+    const float* q_pre;
+    int64_t ld_q_pre;
+    const float* z;
+    int64_t ld_z;
+    const float* bias;
+    const float* cos_t; /* (l x head_dim/2), position = row within the sequence */
+    const float* sin_t;
+    float* g;
+    int64_t ld_g;
+} pxk_attn_rel_desc;
+int pxk_attention_relevance_q(const pxk_attn_rel_desc* d, void* stream);
 
 /* Causal/plain softmax of scaled scores (the module's axpby + attention_mask_fill(lowest) +
  * softmax_rows, multihead_attention_module.cpp:280-285): P = softmax(scale * raw) over the keys

@@ -80,6 +80,7 @@ private:
     void ensure_tables(int64_t l);
     void run_attention_unfused(const float* q, int64_t ldq, const float* k, int64_t ldk, const float* v, int64_t n,
                                int64_t l);
+    void relevance_scores_unfused(const float* spv, float eps, bool bid);
 
     AttentionConfig config_;
     int64_t d_, H_, Hkv_, D_;

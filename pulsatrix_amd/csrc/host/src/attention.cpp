@@ -256,55 +256,50 @@ const float* MultiHeadAttentionModule::run_relevance(const float* relevance_out,
         d.x = mat(ctx_.data(), qd);
         be_->run_gemm(d);
     }
-    // 2. r_attn = P * (s_pv V^T) per query head (Eq. 15, A-share of P V).
-    float* ra = ra_.ensure(be_, n * H_ * LL);
+    float* ra = ra_.ensure(be_, n * H_ * LL);  // r_attn, then the Q K^T factor s
     const float* p = p_.data();
-    {
-        pxk_gemm_desc d = gemm_desc(l, l, D_);
-        d.batch = n * H_;
-        d.inner = H_;
-        d.trans_b = 1;
-        d.causal = causal ? PXK_CAUSAL_TRI : PXK_CAUSAL_NONE;
-        d.epilogue = PXK_EPI_MUL_X;
-        d.a = mat(spv, qd, l * qd, D_);
-        d.b = mat(v, w3, l * w3, D_, grp);
-        d.c = mat(ra, l, H_ * LL, LL);
-        d.x = mat(p, l, H_ * LL, LL);
-        be_->run_gemm(d);
-    }
-    // 3. softmax rule on the scaled scores, mask, then the Q K^T factor s_qk (in place).
-    MI355XBackend::check(pxk_attention_lrp_scores(ra, p, raw_.data(), ra, n * H_, l, score_scale(), eps, causal, st),
-                         "MultiHeadAttentionModule::propagate_relevance (scores)");
     float* g = g_.ensure(be_, M * w3);  // [g_q | g_k | g_v]: relevance / stab(z) per projection
     if (!key_rel_.data() || key_rel_.numel() != M * kvd) {
         key_rel_ = Tensor::uninitialized(Shape({M, kvd}), be_);
         value_rel_ = Tensor::uninitialized(Shape({M, kvd}), be_);
     }
-    // 4. query share: r_q = Q * (s_qk K), then the RoPE rule and q_proj's denominator.
-    {
-        pxk_gemm_desc d = gemm_desc(l, D_, l);
-        d.batch = n * H_;
-        d.inner = H_;
-        d.causal = causal ? PXK_CAUSAL_K_LE_M : PXK_CAUSAL_NONE;
-        d.eps = eps;
-        d.a = mat(ra, l, H_ * LL, LL);
-        d.b = mat(k, ldk, l * ldk, D_, grp);
-        d.c2 = mat(g, w3, l * w3, D_);
-        d.z = mat(z, w3, l * w3, D_);
-        if (bq) d.e_bias = mat(bq, 0, 0, D_);
-        if (config_.use_rope) {
-            d.epilogue = PXK_EPI_ROPE_REL;
-            d.x = mat(y, w3, l * w3, D_);
-            d.y = mat(q, ldq, l * ldq, D_);
-            d.cos_t = cos_.data();
-            d.sin_t = sin_.data();
-            d.head_dim = D_;
-            d.rope_half = config_.rope_layout == RoPELayout::RotateHalf;
-        } else {
-            d.epilogue = PXK_EPI_VALUE_REL;
-            d.y = mat(q, ldq, l * ldq, D_);
-        }
-        be_->run_gemm(d);
+    if (pxk_attention_supported(D_, l, ldq, ldk, w3)) {
+        // 2-4 fused: r_attn, the softmax rule with the Q K^T denominator (s), and the query share
+        // with the RoPE rule and q_proj's denominator, one launch per layer.
+        pxk_attn_rel_desc rd{};
+        rd.n = n;
+        rd.l = l;
+        rd.heads = H_;
+        rd.kv_heads = Hkv_;
+        rd.head_dim = D_;
+        rd.scale = score_scale();
+        rd.eps = eps;
+        rd.causal = causal;
+        rd.rope = config_.use_rope;
+        rd.rope_half = config_.rope_layout == RoPELayout::RotateHalf;
+        rd.spv = spv;
+        rd.ld_spv = qd;
+        rd.v = v;
+        rd.ld_v = w3;
+        rd.k = k;
+        rd.ld_k = ldk;
+        rd.p = p;
+        rd.raw = raw_.data();
+        rd.s = ra;
+        rd.q = q;
+        rd.ld_q = ldq;
+        rd.q_pre = y;
+        rd.ld_q_pre = w3;
+        rd.z = z;
+        rd.ld_z = w3;
+        rd.bias = bq;
+        rd.cos_t = cos_.data();
+        rd.sin_t = sin_.data();
+        rd.g = g;
+        rd.ld_g = w3;
+        MI355XBackend::check(pxk_attention_relevance_q(&rd, st), "MultiHeadAttentionModule::propagate_relevance");
+    } else {
+        relevance_scores_unfused(spv, eps, bid);
     }
     // 5. key share per KV head, summed over its query heads: r_k = K * sum_h s_qk_h^T Q_h.
     {
@@ -369,6 +364,67 @@ const float* MultiHeadAttentionModule::run_relevance(const float* relevance_out,
     }
     has_relevance_ = true;
     return r_in;
+}
+
+// Steps 2-4 of run_relevance as GEMM and row-kernel launches: head_dim outside
+// pxk_attention_supported().
+void MultiHeadAttentionModule::relevance_scores_unfused(const float* spv, float eps, bool bid) {
+    const int64_t n = N_, l = L_, qd = H_ * D_, kvd = Hkv_ * D_, w3 = qd + 2 * kvd, grp = H_ / Hkv_, LL = l * l;
+    const bool causal = config_.causal;
+    const float* z = qkv_z_.data();
+    const float* y = config_.qkv_bias ? qkv_y_.data() : z;
+    const float* q = config_.use_rope ? q_rot_.data() : y;
+    const float* k = config_.use_rope ? k_rot_.data() : y + qd;
+    const float* v = y + qd + kvd;
+    const int64_t ldq = config_.use_rope ? qd : w3, ldk = config_.use_rope ? kvd : w3;
+    const float* bq = detail::rule_bias(bqkv_.data(), config_.qkv_bias, bid);
+    void* st = be_->stream();
+    float* ra = ra_.data();
+    const float* p = p_.data();
+    float* g = g_.data();
+    // 2. r_attn = P * (s_pv V^T) per query head (Eq. 15, A-share of P V).
+    {
+        pxk_gemm_desc d = gemm_desc(l, l, D_);
+        d.batch = n * H_;
+        d.inner = H_;
+        d.trans_b = 1;
+        d.causal = causal ? PXK_CAUSAL_TRI : PXK_CAUSAL_NONE;
+        d.epilogue = PXK_EPI_MUL_X;
+        d.a = mat(spv, qd, l * qd, D_);
+        d.b = mat(v, w3, l * w3, D_, grp);
+        d.c = mat(ra, l, H_ * LL, LL);
+        d.x = mat(p, l, H_ * LL, LL);
+        be_->run_gemm(d);
+    }
+    // 3. softmax rule on the scaled scores, mask, then the Q K^T factor s_qk (in place).
+    MI355XBackend::check(pxk_attention_lrp_scores(ra, p, raw_.data(), ra, n * H_, l, score_scale(), eps, causal, st),
+                         "MultiHeadAttentionModule::propagate_relevance (scores)");
+    // 4. query share: r_q = Q * (s_qk K), then the RoPE rule and q_proj's denominator.
+    {
+        pxk_gemm_desc d = gemm_desc(l, D_, l);
+        d.batch = n * H_;
+        d.inner = H_;
+        d.causal = causal ? PXK_CAUSAL_K_LE_M : PXK_CAUSAL_NONE;
+        d.eps = eps;
+        d.a = mat(ra, l, H_ * LL, LL);
+        d.b = mat(k, ldk, l * ldk, D_, grp);
+        d.c2 = mat(g, w3, l * w3, D_);
+        d.z = mat(z, w3, l * w3, D_);
+        if (bq) d.e_bias = mat(bq, 0, 0, D_);
+        if (config_.use_rope) {
+            d.epilogue = PXK_EPI_ROPE_REL;
+            d.x = mat(y, w3, l * w3, D_);
+            d.y = mat(q, ldq, l * ldq, D_);
+            d.cos_t = cos_.data();
+            d.sin_t = sin_.data();
+            d.head_dim = D_;
+            d.rope_half = config_.rope_layout == RoPELayout::RotateHalf;
+        } else {
+            d.epilogue = PXK_EPI_VALUE_REL;
+            d.y = mat(q, ldq, l * ldq, D_);
+        }
+        be_->run_gemm(d);
+    }
 }
 
 Tensor MultiHeadAttentionModule::forward_impl(const Tensor& input) {

@@ -17,6 +17,15 @@
 // cpu_backend.cpp:292-310; the hardware exponential __expf on arguments <= 0, and one reciprocal
 // per row) as whole contiguous row segments, 16 threads per row, reading nothing back from HBM. P is written over whole rows, zeros past the
 // visible keys: the relevance pass reads it as a dense operand.
+//
+// Relevance (pxk_attention_relevance_q). The same workgroup tiling runs the AttnLRP steps of one
+// query head that need whole score rows: the P V bilinear share r_attn = P * (s_pv V^T), formed
+// as (V s_pv^T)^T so it lands in the score layout; the softmax rule and the Q K^T bilinear
+// denominator, s = (scale raw)(r_attn - P sum r_attn) / (2 raw + eps sign raw); and the query
+// share (s K), whose transposed product takes s straight from registers as its B operand, with
+// the RoPE epsilon rule and q_proj's denominator applied per pair at the end. r_attn, then s, wait
+// in LDS for the row sums and for the contiguous store of s (the key share reads it).
+#include <algorithm>
 #include <cmath>
 
 #include "common.hpp"
@@ -257,6 +266,248 @@ __global__ void __launch_bounds__(kThreads) attn_fwd_kernel(const FwdArgs a) {
     }
 }
 
+struct RelArgs {
+    const float* spv;
+    const float* v;
+    const float* k;
+    const float* p;
+    const float* raw;
+    float* s;
+    const float* q;
+    const float* q_pre;
+    const float* z;
+    const float* bias;
+    const float* cos_t;
+    const float* sin_t;
+    float* g;
+    int ld_spv, ld_v, ld_k, ld_q, ld_q_pre, ld_z, ld_g;
+    int n, l, heads, kv_heads, D;
+    float scale, eps;
+    int causal, rope, rope_half;
+    int lds_ld;
+};
+
+template <int DT, bool VEC>
+__global__ void __launch_bounds__(kThreads) attn_rel_q_kernel(const RelArgs a) {
+    extern __shared__ __attribute__((aligned(16))) float ra[];  // [16][lds_ld]: r_attn, then s
+    __shared__ float s_sum[kWaves][16], f_sum[16];
+    __shared__ __attribute__((aligned(16))) float s_acc[kWaves][16][16 * DT + 4];
+    __shared__ __attribute__((aligned(16))) float m_acc[16][16 * DT + 4];
+
+    const int lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: the tile loops are scalar
+    const int l = a.l, D = a.D, ld = a.lds_ld;
+    const int nrb = (l + 15) / 16;
+    const int rb = blockIdx.x % nrb, bh = blockIdx.x / nrb;
+    const int h = bh % a.heads, b = bh / a.heads;
+    const int hk = h / (a.heads / a.kv_heads);
+    const int i0 = rb * 16, row = i0 + c;
+    const bool row_ok = row < l;
+    const int64_t slab = (static_cast<int64_t>(b) * a.heads + h) * l * l;  // P, raw, s (N, H, L, L)
+    const float* prow = a.p + slab + static_cast<int64_t>(row_ok ? row : l - 1) * l;
+    const float* rrow = a.raw + slab + static_cast<int64_t>(row_ok ? row : l - 1) * l;
+
+    // s_pv^T fragments (B operand): bf[t][s] = s_pv[row][16 t + 4 g + s].
+    f4 bf[DT];
+    {
+        const float* sp = a.spv + (static_cast<int64_t>(b) * l + (row_ok ? row : l - 1)) * a.ld_spv + h * D;
+#pragma unroll
+        for (int t = 0; t < DT; ++t) {
+            const int d0 = 16 * t + 4 * g;
+            bf[t] = (row_ok && d0 < D) ? *reinterpret_cast<const f4*>(sp + d0) : f4{0.f, 0.f, 0.f, 0.f};
+        }
+    }
+    const float* vbase = a.v + static_cast<int64_t>(b) * l * a.ld_v + hk * D;
+    const float* kbase = a.k + static_cast<int64_t>(b) * l * a.ld_k + hk * D;
+    const int vis_end = a.causal ? min(i0 + 16, l) : l;
+    const int ntile = (vis_end + 15) / 16;
+
+    // Both passes walk this wave's tiles two at a time with two register sets: a set is reloaded
+    // with the tile after next right after its last read, the second tile of a pair runs even
+    // past the last tile (all its keys masked: it adds nothing and stores nothing to LDS), and
+    // loads clamp their addresses, so no branch surrounds a load.
+    const int ldv = a.ld_v, ldk = a.ld_k;
+    auto p4 = [&](const float* rowp, int kt) -> f4 {  // 4 entries of a score row at tile kt, clamped
+        const int kk0 = 16 * min(kt, ntile - 1) + 4 * g;
+        if constexpr (VEC) return *reinterpret_cast<const f4*>(rowp + min(kk0, l - 4));
+        f4 v;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = rowp[min(kk0 + j, l - 1)];
+        return v;
+    };
+    auto valid_mask = [&](int kk0, bool (&valid)[4]) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int kk = kk0 + r;
+            valid[r] = (kk < l) & ((!a.causal) | (kk <= row));
+        }
+    };
+
+    // Pass 1: r_attn = P * (s_pv V^T), row sums. A operand: va[t][s] = V[key0 + c][16 t + 4 g + s].
+    f4 va[2][DT], pa[2];
+    auto load1 = [&](int set, int kt) {
+        const float* vp = vbase + min(16 * min(kt, ntile - 1) + c, l - 1) * ldv;
+#pragma unroll
+        for (int t = 0; t < DT; ++t) va[set][t] = *reinterpret_cast<const f4*>(vp + min(16 * t + 4 * g, D - 4));
+        pa[set] = p4(prow, kt);
+    };
+    float rs = 0.0f;
+    auto tile1 = [&](int set, int kt) {
+        const int kk0 = 16 * kt + 4 * g;
+        f4 u = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int t = 0; t < DT; ++t)
+#pragma unroll
+            for (int st = 0; st < 4; ++st) u = __builtin_amdgcn_mfma_f32_16x16x4f32(va[set][t][st], bf[t][st], u, 0, 0, 0);
+        const f4 pv = pa[set];
+        __builtin_amdgcn_sched_barrier(0);
+        load1(set, kt + 2 * kWaves);
+        __builtin_amdgcn_sched_barrier(0);
+        bool valid[4];
+        valid_mask(kk0, valid);
+        f4 r4;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            r4[r] = valid[r] ? pv[r] * u[r] : 0.0f;
+            rs += r4[r];
+        }
+        if (kt < ntile) *reinterpret_cast<f4*>(ra + c * ld + kk0) = r4;
+    };
+    load1(0, wave);
+    load1(1, wave + kWaves);
+    for (int kt = wave; kt < ntile; kt += 2 * kWaves) {
+        tile1(0, kt);
+        tile1(1, kt + kWaves);
+    }
+    rs = row_sum4(rs);
+    if (g == 0) s_sum[wave][c] = rs;
+    __syncthreads();
+    if (threadIdx.x < 16) {
+        float t = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) t += s_sum[w][threadIdx.x];
+        f_sum[threadIdx.x] = t;
+    }
+    __syncthreads();
+
+    // Pass 2: s = (scale raw)(r_attn - P sum) / (2 raw + eps sign raw); (s K)^T += K^T s^T with
+    // A operand kb[t][s] = K[key0 + 4 g + s][16 t + c] and B = this lane's s values.
+    const float sum = f_sum[c];
+    f4 acc[DT];
+#pragma unroll
+    for (int t = 0; t < DT; ++t) acc[t] = f4{0.f, 0.f, 0.f, 0.f};
+    f4 kb[2][DT], pb[2], rb2[2];
+    auto load2 = [&](int set, int kt) {
+        const int key0 = 16 * min(kt, ntile - 1);
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+            const float* kp = kbase + min(key0 + 4 * g + st, l - 1) * ldk;
+#pragma unroll
+            for (int t = 0; t < DT; ++t) kb[set][t][st] = kp[min(16 * t + c, D - 1)];
+        }
+        pb[set] = p4(prow, kt);
+        rb2[set] = p4(rrow, kt);
+    };
+    auto tile2 = [&](int set, int kt) {
+        const int kk0 = 16 * kt + 4 * g;
+        const f4 pv = pb[set], rw = rb2[set];
+        const f4 r4 = kt < ntile ? *reinterpret_cast<const f4*>(ra + c * ld + kk0) : f4{0.f, 0.f, 0.f, 0.f};
+        bool valid[4];
+        valid_mask(kk0, valid);
+        f4 s4;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float o = rw[r];
+            const float rsc = (a.scale * o) * (r4[r] - pv[r] * sum);
+            s4[r] = valid[r] ? rsc / (2.0f * o + a.eps * ((o >= 0.0f) ? 1.0f : -1.0f)) : 0.0f;
+        }
+        if (kt < ntile) *reinterpret_cast<f4*>(ra + c * ld + kk0) = s4;
+#pragma unroll
+        for (int t = 0; t < DT; ++t)
+#pragma unroll
+            for (int st = 0; st < 4; ++st)
+                acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(kb[set][t][st], s4[st], acc[t], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        load2(set, kt + 2 * kWaves);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    load2(0, wave);
+    load2(1, wave + kWaves);
+    for (int kt = wave; kt < ntile; kt += 2 * kWaves) {
+        tile2(0, kt);
+        tile2(1, kt + kWaves);
+    }
+    // Merge: acc[t][r] = (s K)^T[16 t + 4 g + r][row c] of this wave.
+#pragma unroll
+    for (int t = 0; t < DT; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) s_acc[wave][c][16 * t + 4 * g + r] = acc[t][r];
+    __syncthreads();
+    const int rr = threadIdx.x >> 4, cc = threadIdx.x & 15;
+    for (int d = cc; d < D; d += 16) {
+        float v = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) v += s_acc[w][rr][d];
+        m_acc[rr][d] = v;
+    }
+    __syncthreads();
+
+    const int orow = i0 + rr;
+    if (orow < l) {
+        // s over the whole row (zeros past the visible keys), contiguous.
+        const int vis = a.causal ? orow + 1 : l;
+        float* srow = a.s + slab + static_cast<int64_t>(orow) * l;
+        const float* lrow = ra + rr * ld;
+        if constexpr (VEC) {
+            for (int k0 = 4 * cc; k0 < l; k0 += 64) {
+                f4 out = {0.f, 0.f, 0.f, 0.f};
+                if (k0 < vis) {
+                    const f4 x = *reinterpret_cast<const f4*>(lrow + k0);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) out[r] = k0 + r < vis ? x[r] : 0.0f;
+                }
+                *reinterpret_cast<f4*>(srow + k0) = out;
+            }
+        } else {
+            for (int k = cc; k < l; k += 16) srow[k] = k < vis ? lrow[k] : 0.0f;
+        }
+        // Query share: r = Q_rot * (s K), the RoPE epsilon rule (lrp_math.hpp:104-123), then q_proj's
+        // denominator: g = r_in / stab(z + bias).
+        const int64_t tok = static_cast<int64_t>(b) * l + orow;
+        const float* qr = a.q + tok * a.ld_q + h * D;
+        const float* qx = a.q_pre + tok * a.ld_q_pre + h * D;
+        const float* zr = a.z + tok * a.ld_z + h * D;
+        const float* br = a.bias ? a.bias + h * D : nullptr;
+        float* gr = a.g + tok * a.ld_g + h * D;
+        const int half = D / 2;
+        for (int d = cc; d < D; d += 16) {
+            float r_in;
+            if (a.rope) {
+                const int i = a.rope_half ? (d < half ? d : d - half) : d / 2;
+                const int lo = a.rope_half ? i : 2 * i, hi = a.rope_half ? i + half : 2 * i + 1;
+                const float y_lo = qr[lo], y_hi = qr[hi];
+                const float r_lo = y_lo * m_acc[rr][lo], r_hi = y_hi * m_acc[rr][hi];
+                const float cs = a.cos_t[static_cast<int64_t>(orow) * half + i];
+                const float sn = a.sin_t[static_cast<int64_t>(orow) * half + i];
+                const float d0 = stab(y_lo, a.eps), d1 = stab(y_hi, a.eps);
+                const float xv = qx[d];
+                r_in = 0.0f;
+                if (d == lo) {
+                    r_in += (xv * cs / d0) * r_lo;
+                    r_in += (xv * sn / d1) * r_hi;
+                } else {
+                    r_in += (xv * -sn / d0) * r_lo;
+                    r_in += (xv * cs / d1) * r_hi;
+                }
+            } else {
+                r_in = qr[d] * m_acc[rr][d];
+            }
+            const float zz = br ? zr[d] + br[d] : zr[d];
+            gr[d] = r_in / stab(zz, a.eps);
+        }
+    }
+}
+
 }  // namespace
 }  // namespace pxk
 
@@ -326,4 +577,59 @@ extern "C" int pxk_attention_forward(const float* q, int64_t ldq, const float* k
         return fail(PXK_ERR_LAUNCH, "pxk_attention_forward: %zu bytes of LDS refused", dyn);
     hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), dyn, S(stream), a);
     return launched("pxk_attention_forward");
+}
+
+namespace {
+
+template <int DT>
+int rel_static_lds() {
+    return static_cast<int>(sizeof(float) * (kWaves * 16 + 16 + (kWaves + 1) * 16 * (16 * DT + 4)));
+}
+
+}  // namespace
+
+extern "C" int pxk_attention_relevance_q(const pxk_attn_rel_desc* d, void* stream) {
+    const int64_t n = d->n, l = d->l, H = d->heads, Hkv = d->kv_heads, D = d->head_dim;
+    if (n < 0 || l < 0 || H <= 0 || Hkv <= 0 || H % Hkv != 0)
+        return fail(PXK_ERR_INVALID, "pxk_attention_relevance_q: bad sizes (heads must be a multiple of kv_heads)");
+    if (D <= 0 || D > 128 || D % 4 != 0 || (d->rope && D % 2 != 0))
+        return fail(PXK_ERR_INVALID, "pxk_attention_relevance_q: head_dim must be a multiple of 4 up to 128");
+    if (!d->spv || !d->v || !d->k || !d->p || !d->raw || !d->s || !d->q || !d->z || !d->g ||
+        (d->rope && (!d->q_pre || !d->cos_t || !d->sin_t)))
+        return fail(PXK_ERR_INVALID, "pxk_attention_relevance_q: a required operand is NULL");
+    if (d->ld_spv % 4 || d->ld_v % 4 || !aligned16(d->spv) || !aligned16(d->v) || d->ld_spv < H * D ||
+        d->ld_v < Hkv * D || d->ld_k < Hkv * D || d->ld_q < H * D || d->ld_z < H * D || d->ld_g < H * D ||
+        (d->rope && d->ld_q_pre < H * D))
+        return fail(PXK_ERR_INVALID, "pxk_attention_relevance_q: row strides must hold every head (s_pv and v "
+                                     "16-byte aligned with strides a multiple of 4)");
+    const int lds_ld = score_lds_ld(l);
+    const int dt = dt_of(D);
+    const int stat = dt == 8 ? rel_static_lds<8>() : rel_static_lds<4>();
+    const size_t dyn = static_cast<size_t>(16) * lds_ld * sizeof(float);
+    if (l > 8192 || stat + static_cast<int64_t>(dyn) > kMaxLds)
+        return fail(PXK_ERR_INVALID, "pxk_attention_relevance_q: the sequence's score rows must fit LDS");
+    if (n == 0 || l == 0) return PXK_OK;
+    const int64_t blocks = n * H * ((l + 15) / 16);
+    const int64_t lds_max = std::max({d->ld_spv, d->ld_v, d->ld_k, d->ld_q, d->ld_q_pre, d->ld_z, d->ld_g});
+    if (blocks > (int64_t{1} << 31) - 1 || n * l * lds_max >= (int64_t{1} << 31))
+        return fail(PXK_ERR_INVALID, "pxk_attention_relevance_q: problem too large");
+    RelArgs a{d->spv, d->v, d->k, d->p, d->raw, d->s, d->q, d->q_pre, d->z, d->bias, d->cos_t, d->sin_t, d->g,
+              static_cast<int>(d->ld_spv), static_cast<int>(d->ld_v), static_cast<int>(d->ld_k),
+              static_cast<int>(d->ld_q), static_cast<int>(d->ld_q_pre), static_cast<int>(d->ld_z),
+              static_cast<int>(d->ld_g), static_cast<int>(n), static_cast<int>(l), static_cast<int>(H),
+              static_cast<int>(Hkv), static_cast<int>(D), d->scale, d->eps, d->causal != 0, d->rope != 0,
+              d->rope_half != 0, lds_ld};
+    const bool vec = l % 4 == 0 && aligned16(d->p) && aligned16(d->raw) && aligned16(d->s);
+    using K = void (*)(const RelArgs);
+    static const K table[2][4] = {
+        {attn_rel_q_kernel<1, false>, attn_rel_q_kernel<2, false>, attn_rel_q_kernel<4, false>,
+         attn_rel_q_kernel<8, false>},
+        {attn_rel_q_kernel<1, true>, attn_rel_q_kernel<2, true>, attn_rel_q_kernel<4, true>, attn_rel_q_kernel<8, true>}};
+    const K fn = table[vec ? 1 : 0][dt == 1 ? 0 : dt == 2 ? 1 : dt == 4 ? 2 : 3];
+    if (dyn > 64 * 1024 &&
+        hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            static_cast<int>(dyn)) != hipSuccess)
+        return fail(PXK_ERR_LAUNCH, "pxk_attention_relevance_q: %zu bytes of LDS refused", dyn);
+    hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), dyn, S(stream), a);
+    return launched("pxk_attention_relevance_q");
 }

@@ -83,7 +83,8 @@ constexpr int kProStabBias = 2;
 template <int BM_, int BN_, int WM_, int WN_, int KS_, int NS_>
 struct Cfg {
     static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, KS = KS_, NS = NS_;
-    static_assert(WM * WN * KS == 4, "four waves per workgroup");
+    static constexpr int NT = 64 * WM * WN * KS;  // threads: four or eight wave64s
+    static_assert(NT == 256 || NT == 512, "four or eight waves per workgroup");
     static constexpr int TM = BM / WM / 16, TN = BN / WN / 16;  // 16x16 MFMA tiles per wave
     static constexpr int CH = KS == 1 ? 2 : 1;                   // 16-wide K chunks per wave per stage
     static constexpr int BK = 16 * KS * CH;
@@ -106,19 +107,19 @@ __device__ __forceinline__ void static_for(F&& f) {
     static_for_impl(f, std::make_integer_sequence<int, N>{});
 }
 
-// LDS footprint of one operand panel: R rows of M (or N) by BK of K.
-template <int R, int BK, bool KC>
+// LDS footprint of one operand panel: R rows of M (or N) by BK of K, moved by T threads.
+template <int R, int BK, bool KC, int T>
 struct Panel {
     static constexpr int LD = KC ? BK + 4 : R + 4;
     static constexpr int SIZE = KC ? R * LD : BK * LD;
-    static constexpr int NV = R * BK / 4 / NT;  // float4 moved per thread per stage
-    static_assert(NV >= 1 && R * BK % (4 * NT) == 0, "panel must split evenly over the workgroup");
+    static constexpr int NV = R * BK / 4 / T;  // float4 moved per thread per stage
+    static_assert(NV >= 1 && R * BK % (4 * T) == 0, "panel must split evenly over the workgroup");
 };
 
 template <class C, bool TA, bool TB>
 struct Layout {
-    using PA = Panel<C::BM, C::BK, !TA>;
-    using PB = Panel<C::BN, C::BK, TB>;
+    using PA = Panel<C::BM, C::BK, !TA, C::NT>;
+    using PB = Panel<C::BN, C::BK, TB, C::NT>;
     static constexpr int STAGE = PA::SIZE + PB::SIZE;
     static constexpr int PART = C::BM * C::LDC;
     static constexpr int SIZE = 2 * STAGE > C::KS * PART ? 2 * STAGE : C::KS * PART;
@@ -144,7 +145,7 @@ __device__ __forceinline__ void st4(float* p, f4 v, bool vec, int cnt) {
 }
 
 // ---- tile epilogue: ROWS x BN accumulator rows in LDS (Cs[ROWS][ldc]) -> outputs -----------------------
-template <int ROWS, int BN, int EPI>
+template <int ROWS, int BN, int EPI, int T>
 __device__ void epilogue_rows(const float* Cs, int ldc, int64_t m0, int64_t n0, int64_t b, const Args& g) {
     constexpr int CPR = BN / 4;  // float4 columns per row
     const int tid = threadIdx.x;
@@ -162,7 +163,7 @@ __device__ void epilogue_rows(const float* Cs, int ldc, int64_t m0, int64_t n0, 
     const float* EB2 = g.eb2.p ? obase(g.eb2, b, inner, 0) : nullptr;
     const float eps = g.eps;
 #pragma unroll 2
-    for (int it = tid; it < ROWS * CPR; it += NT) {
+    for (int it = tid; it < ROWS * CPR; it += T) {
         const int row = it / CPR, col = 4 * (it % CPR);
         const int64_t m = m0 + row, n = n0 + col;
         if (m >= g.M || n >= g.N) continue;
@@ -274,9 +275,9 @@ __device__ void epilogue_rows(const float* Cs, int ldc, int64_t m0, int64_t n0, 
 // stored extent along M (or N). issue() only starts the global loads; commit() waits for them,
 // applies the DIV_STAB prologue (operand A only) and writes LDS, so the loads of a stage overlap
 // the MFMAs of the stages before it.
-template <int R, int BK, bool KC, int PRO>
+template <int R, int BK, bool KC, int PRO, int T>
 struct PanelLoader {
-    using P = Panel<R, BK, KC>;
+    using P = Panel<R, BK, KC, T>;
     static constexpr bool DS = PRO != PXK_PRO_NONE;
     static constexpr bool HB = PRO == kProStabBias;
     f4 v[P::NV];
@@ -301,7 +302,7 @@ struct PanelLoader {
 #pragma unroll
         for (int i = 0; i < P::NV; ++i) {
             int64_t r, c;
-            coords(tid + i * NT, r0, k0, r, c);
+            coords(tid + i * T, r0, k0, r, c);
             v[i] = *reinterpret_cast<const f4*>(A + r * lda + c);
             if constexpr (DS) z[i] = *reinterpret_cast<const f4*>(Z + r * ldz + c);
             if constexpr (HB) {
@@ -321,7 +322,7 @@ struct PanelLoader {
 #pragma unroll
         for (int i = 0; i < P::NV; ++i) {
             int64_t r, c;
-            coords(tid + i * NT, r0, k0, r, c);
+            coords(tid + i * T, r0, k0, r, c);
             f4 a = {0.f, 0.f, 0.f, 0.f};
             f4 zz = {1.f, 1.f, 1.f, 1.f};
             f4 bb = {0.f, 0.f, 0.f, 0.f};
@@ -344,7 +345,7 @@ struct PanelLoader {
         const int tid = threadIdx.x;
 #pragma unroll
         for (int i = 0; i < P::NV; ++i) {
-            const int idx = tid + i * NT;
+            const int idx = tid + i * T;
             f4 a = v[i];
             // A element a is divided once per N tile that reads it, so the prologue multiplies by
             // v_rcp_f32 (within 1 ulp of 1/x) instead of the IEEE division sequence; |stab(z)| >= eps
@@ -397,8 +398,49 @@ __device__ __forceinline__ void tile_of(const Args& g, int& tm, int& tn, int& tz
     tz = id / g.tiles_n;
 }
 
+// Each wave's accumulators (one partial tile per K slice) -> LDS, summed in slice order; then the
+// split-K partial store or the tile epilogue. smem holds KS * BM * (BN + 4) floats and no wave
+// still reads it.
+template <class C, int EPI>
+__device__ __forceinline__ void finish_tile(f4 (&acc)[C::TM][C::TN], float* smem, int ks, int wm, int wn, int lane,
+                                            int tid, int64_t m0, int64_t n0, int64_t split, int64_t b, const Args& g) {
+    constexpr int BM = C::BM, BN = C::BN, TM = C::TM, TN = C::TN, LDC = C::LDC, PART = BM * LDC;
+    float* Cp = smem + ks * PART;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                Cp[(wm + 16 * i + 4 * (lane >> 4) + r) * LDC + wn + 16 * j + (lane & 15)] = acc[i][j][r];
+    __syncthreads();
+    if constexpr (C::KS > 1) {  // sum the K-slice partials in slice order
+        for (int it = tid; it < BM * (BN / 4); it += C::NT) {
+            const int off = (it / (BN / 4)) * LDC + 4 * (it % (BN / 4));
+            f4 v = *reinterpret_cast<const f4*>(smem + off);
+#pragma unroll
+            for (int q = 1; q < C::KS; ++q) v += *reinterpret_cast<const f4*>(smem + q * PART + off);
+            *reinterpret_cast<f4*>(smem + off) = v;
+        }
+        __syncthreads();
+    }
+    if (g.splits > 1) {  // raw partial tile -> workspace [split][batch][M][N]
+        float* P = g.ws + ((split * g.batch + b) * g.M) * g.N;
+        const bool vec = (g.N % 4) == 0;
+        for (int it = tid; it < BM * (BN / 4); it += C::NT) {
+            const int row = it / (BN / 4), col = 4 * (it % (BN / 4));
+            const int64_t m = m0 + row, n = n0 + col;
+            if (m >= g.M || n >= g.N) continue;
+            const int cnt = g.N - n < 4 ? static_cast<int>(g.N - n) : 4;
+            st4(P + m * g.N + n, *reinterpret_cast<const f4*>(smem + row * LDC + col), vec && cnt == 4, cnt);
+        }
+        return;
+    }
+    epilogue_rows<BM, BN, EPI, C::NT>(smem, LDC, m0, n0, b, g);
+}
+
 template <class C, bool TA, bool TB, int PRO, int EPI>
-__global__ void __launch_bounds__(NT) gemm_kernel(const Args g) {
+__global__ void __launch_bounds__(C::NT) gemm_kernel(const Args g) {
     constexpr int BM = C::BM, BN = C::BN, BK = C::BK, TM = C::TM, TN = C::TN, LDC = C::LDC;
     using L = Layout<C, TA, TB>;
     using PA = typename L::PA;
@@ -431,8 +473,8 @@ __global__ void __launch_bounds__(NT) gemm_kernel(const Args g) {
         for (int j = 0; j < TN; ++j) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
 
     constexpr int NS = C::NS;
-    PanelLoader<BM, BK, !TA, PRO> la[NS];
-    PanelLoader<BN, BK, TB, PXK_PRO_NONE> lb[NS];
+    PanelLoader<BM, BK, !TA, PRO, C::NT> la[NS];
+    PanelLoader<BN, BK, TB, PXK_PRO_NONE, C::NT> lb[NS];
     // Load cursor: stage `lt` of the flattened (k-group, K stage) range, at (grp, kb).
     int64_t lt = 0, grp = nkb > 0 ? t0 / nkb : 0, kb = nkb > 0 ? t0 % nkb : 0;  // 32-bit division
     const float* A = obase(g.a, b, g.inner, grp);
@@ -536,39 +578,183 @@ __global__ void __launch_bounds__(NT) gemm_kernel(const Args g) {
         }
     }
 
-    // Accumulators -> LDS (one partial tile per K slice); the loop ended on a barrier.
-    float* Cp = smem + ks * L::PART;
+    // The loop ended on a barrier: LDS is free for the partial tiles.
+    finish_tile<C, EPI>(acc, smem, ks, wm, wn, lane, tid, m0, n0, split, b, g);
+}
+
+// ---- direct-load variant of the K-sliced tiles ---------------------------------------------------
+// In the 32x64 and 32x32 tiles the four waves own disjoint K slices and share no operand data, so
+// LDS staging is only a layout step costing a write, a read and a barrier per stage. Here every
+// wave streams its own 16-deep K chunks straight from L2 into MFMA operand registers: a
+// K-contiguous operand is one float4 per 16x16 fragment, an M- or N-contiguous one four dwords.
+// PF register sets keep that many chunks in flight; past the wave's last chunk the last one is
+// reloaded (unused), so no branch surrounds a load. LDS is used once, to merge the four slices.
+template <class C, bool TA, bool TB, int PRO>
+struct DirectChunk {
+    static constexpr bool DS = PRO != PXK_PRO_NONE, HB = PRO == kProStabBias;
+    f4 a[C::TM], b[C::TN];
+    f4 z[DS ? C::TM : 1];
+    f4 zb;  // bias over k, the same for every A row
+
+    // An interior chunk (the whole 16-deep chunk of the tile lies inside both matrices) at K offset
+    // kc: unconditional loads.
+    __device__ __forceinline__ void load(const Args& g, const float* A, const float* Z, const float* ZB, const float* B,
+                                         int64_t m0, int64_t n0, int64_t kc, int lane) {
+        const int c = lane & 15, g4 = 4 * (lane >> 4);
+#pragma unroll
+        for (int i = 0; i < C::TM; ++i) {
+            const int64_t m = m0 + 16 * i + c;
+            if constexpr (!TA) {
+                a[i] = *reinterpret_cast<const f4*>(A + m * g.a.ld + kc + g4);
+                if constexpr (DS) z[i] = *reinterpret_cast<const f4*>(Z + m * g.z.ld + kc + g4);
+            } else {
+#pragma unroll
+                for (int s = 0; s < 4; ++s) {
+                    a[i][s] = A[(kc + g4 + s) * g.a.ld + m];
+                    if constexpr (DS) z[i][s] = Z[(kc + g4 + s) * g.z.ld + m];
+                }
+            }
+        }
+        if constexpr (HB) zb = *reinterpret_cast<const f4*>(ZB + kc + g4);
+#pragma unroll
+        for (int j = 0; j < C::TN; ++j) {
+            const int64_t n = n0 + 16 * j + c;
+            if constexpr (TB) {
+                b[j] = *reinterpret_cast<const f4*>(B + n * g.b.ld + kc + g4);
+            } else {
+#pragma unroll
+                for (int s = 0; s < 4; ++s) b[j][s] = B[(kc + g4 + s) * g.b.ld + n];
+            }
+        }
+    }
+
+    // Any chunk: element-wise bounds checks on M, N and K, zeros outside the matrix.
+    __device__ __forceinline__ void load_guarded(const Args& g, const float* A, const float* Z, const float* ZB,
+                                                 const float* B, int64_t m0, int64_t n0, int64_t kc, int lane) {
+        const int c = lane & 15, g4 = 4 * (lane >> 4);
+#pragma unroll
+        for (int i = 0; i < C::TM; ++i) {
+            const int64_t m = m0 + 16 * i + c;
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                const int64_t k = kc + g4 + s;
+                const bool in = m < g.M && k < g.K;
+                a[i][s] = in ? (TA ? A[k * g.a.ld + m] : A[m * g.a.ld + k]) : 0.0f;
+                if constexpr (DS) z[i][s] = in ? (TA ? Z[k * g.z.ld + m] : Z[m * g.z.ld + k]) : 1.0f;
+            }
+        }
+        if constexpr (HB) {
+#pragma unroll
+            for (int s = 0; s < 4; ++s) zb[s] = kc + g4 + s < g.K ? ZB[kc + g4 + s] : 0.0f;
+        }
+#pragma unroll
+        for (int j = 0; j < C::TN; ++j) {
+            const int64_t n = n0 + 16 * j + c;
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                const int64_t k = kc + g4 + s;
+                b[j][s] = (n < g.N && k < g.K) ? (TB ? B[n * g.b.ld + k] : B[k * g.b.ld + n]) : 0.0f;
+            }
+        }
+    }
+
+    __device__ __forceinline__ void mma(f4 (&acc)[C::TM][C::TN], float eps) {
+        if constexpr (DS) {
+#pragma unroll
+            for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+                for (int s = 0; s < 4; ++s) {
+                    const float zz = HB ? z[i][s] + zb[s] : z[i][s];
+                    a[i][s] = a[i][s] * __builtin_amdgcn_rcpf(stab(zz, eps));
+                }
+        }
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+                for (int j = 0; j < C::TN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i][s], b[j][s], acc[i][j], 0, 0, 0);
+    }
+};
+
+template <class C, bool TA, bool TB, int PRO, int EPI>
+__global__ void __launch_bounds__(C::NT) gemm_direct_kernel(const Args g) {
+    static_assert(C::WM == 1 && C::WN == 1, "direct loads: every wave owns the whole tile");
+    constexpr int BM = C::BM, BN = C::BN, TM = C::TM, TN = C::TN, KS = C::KS, PF = 3;
+    __shared__ __attribute__((aligned(16))) float smem[KS * BM * C::LDC];
+
+    int tm, tn, tz;
+    tile_of(g, tm, tn, tz);
+    const int64_t m0 = static_cast<int64_t>(tm) * BM, n0 = static_cast<int64_t>(tn) * BN;
+    const int64_t split = tz % g.splits, b = tz / g.splits;
+    if (g.causal == PXK_CAUSAL_TRI && n0 > m0 + BM - 1) return;
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int ks = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int64_t k_lo = k_first(g, m0), k_hi = k_end(g, m0, BM);
+    const int nch = k_hi > k_lo ? static_cast<int>((k_hi - k_lo + 15) / 16) : 0;  // 16-deep chunks
+    const int total = nch * static_cast<int>(g.kgroups);
+    const int per = (total + g.splits - 1) / g.splits;
+    const int t0 = static_cast<int>(split) * per < total ? static_cast<int>(split) * per : total;
+    const int t1 = t0 + per < total ? t0 + per : total;
+    const int first = t0 + ks;                                       // this wave: t0 + ks, + KS, ...
+    const int nw = first < t1 ? (t1 - first + KS - 1) / KS : 0;
+
+    f4 acc[TM][TN];
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < TN; ++j)
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-                Cp[(wm + 16 * i + 4 * (lane >> 4) + r) * LDC + wn + 16 * j + (lane & 15)] = acc[i][j][r];
-    __syncthreads();
-    if constexpr (C::KS > 1) {  // sum the K-slice partials in slice order
-        for (int it = tid; it < BM * (BN / 4); it += NT) {
-            const int off = (it / (BN / 4)) * LDC + 4 * (it % (BN / 4));
-            f4 v = *reinterpret_cast<const f4*>(smem + off);
-#pragma unroll
-            for (int q = 1; q < C::KS; ++q) v += *reinterpret_cast<const f4*>(smem + q * L::PART + off);
-            *reinterpret_cast<f4*>(smem + off) = v;
+        for (int j = 0; j < TN; ++j) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
+
+    // Cursor over this wave's chunks: (grp, kk) of flattened chunk `first + KS * u`.
+    int grp = nch > 0 ? first / nch : 0, kk = nch > 0 ? first % nch : 0, lu = 0;
+    const float* A = obase(g.a, b, g.inner, grp);
+    const float* B = obase(g.b, b, g.inner, grp);
+    const float* Z = PRO != PXK_PRO_NONE ? obase(g.z, b, g.inner, grp) : nullptr;
+    const float* ZB = PRO == kProStabBias ? obase(g.zb, b, g.inner, grp) : nullptr;
+    auto advance = [&]() {  // to this wave's next chunk
+        ++lu;
+        kk += KS;
+        bool moved = false;
+        while (kk >= nch) {
+            kk -= nch;
+            ++grp;
+            moved = true;
         }
-        __syncthreads();
-    }
-    if (g.splits > 1) {  // raw partial tile -> workspace [split][batch][M][N]
-        float* P = g.ws + ((split * g.batch + b) * g.M) * g.N;
-        const bool vec = (g.N % 4) == 0;
-        for (int it = tid; it < BM * (BN / 4); it += NT) {
-            const int row = it / (BN / 4), col = 4 * (it % (BN / 4));
-            const int64_t m = m0 + row, n = n0 + col;
-            if (m >= g.M || n >= g.N) continue;
-            const int cnt = g.N - n < 4 ? static_cast<int>(g.N - n) : 4;
-            st4(P + m * g.N + n, *reinterpret_cast<const f4*>(smem + row * LDC + col), vec && cnt == 4, cnt);
+        if (moved) {
+            A = obase(g.a, b, g.inner, grp);
+            B = obase(g.b, b, g.inner, grp);
+            if constexpr (PRO != PXK_PRO_NONE) Z = obase(g.z, b, g.inner, grp);
+            if constexpr (PRO == kProStabBias) ZB = obase(g.zb, b, g.inner, grp);
         }
-        return;
+    };
+    const bool interior = m0 + BM <= g.M && n0 + BN <= g.N && k_lo + 16 * static_cast<int64_t>(nch) <= g.K &&
+                          g.vec_a && g.vec_b;
+    if (nw > 0) {
+        if (interior) {
+            DirectChunk<C, TA, TB, PRO> ch[PF];
+            auto load = [&](auto S) {  // the cursor's chunk -> set S; the cursor stops at the last one
+                ch[S.value].load(g, A, Z, ZB, B, m0, n0, k_lo + 16 * kk, lane);
+                if (lu + 1 < nw) advance();
+            };
+            static_for<PF>([&](auto U) { load(U); });
+            for (int u0 = 0; u0 < nw; u0 += PF) {
+                static_for<PF>([&](auto U) {
+                    if (u0 + U.value < nw) ch[U.value].mma(acc, g.eps);
+                    load(U);  // chunk u0 + U + PF (or the last one again)
+                });
+            }
+        } else {
+            DirectChunk<C, TA, TB, PRO> ch;
+            for (int u = 0; u < nw; ++u) {
+                ch.load_guarded(g, A, Z, ZB, B, m0, n0, k_lo + 16 * kk, lane);
+                ch.mma(acc, g.eps);
+                if (u + 1 < nw) advance();
+            }
+        }
     }
-    epilogue_rows<BM, BN, EPI>(smem, LDC, m0, n0, b, g);
+    finish_tile<C, EPI>(acc, smem, ks, 0, 0, lane, tid, m0, n0, split, b, g);
 }
 
 // Sums the split partials of a slab of rows in split order and runs the tile epilogue. One
@@ -600,17 +786,17 @@ __global__ void __launch_bounds__(NT) splitk_reduce_kernel(const Args g) {
     }
     *reinterpret_cast<f4*>(Cs + row * LDC + col) = v;
     __syncthreads();
-    epilogue_rows<RS, BN, EPI>(Cs, LDC, m0, n0, b, g);
+    epilogue_rows<RS, BN, EPI, NT>(Cs, LDC, m0, n0, b, g);
 }
 
 // ---- host side --------------------------------------------------------------------------------
 
 using KernelFn = void (*)(const Args);
 
-constexpr int kTiles = 4;  // PXK_TILE_128x128 .. PXK_TILE_32x32
+constexpr int kTiles = 6;  // PXK_TILE_128x128 .. PXK_TILE_32x32_DIRECT
 
 struct TileInfo {
-    int bm, bn, bk, smem_bytes;
+    int bm, bn, bk, threads, smem_bytes;
     double floor_us;  // a K stage of a workgroup alone on its CU (load latency bound), measured
     double util;      // MFMA utilisation when several waves share a SIMD, measured
 };
@@ -623,12 +809,13 @@ struct Entry {
 
 #define PXK_KSET(TA, TB, P, EPI)                                                                    \
     {gemm_kernel<C128, TA, TB, P, EPI>, gemm_kernel<C64, TA, TB, P, EPI>, gemm_kernel<C32x64, TA, TB, P, EPI>, \
-     gemm_kernel<C32, TA, TB, P, EPI>}
+     gemm_kernel<C32, TA, TB, P, EPI>, gemm_direct_kernel<C32x64, TA, TB, P, EPI>,                         \
+     gemm_direct_kernel<C32, TA, TB, P, EPI>}
 #define PXK_GEMM_ENTRY(TA, TB, PRO, EPI)                                                                   \
     Entry {                                                                                                \
         TA, TB, PRO, EPI, {PXK_KSET(TA, TB, PRO, EPI), PXK_KSET(TA, TB, (PRO ? kProStabBias : PRO), EPI)}, \
             {splitk_reduce_kernel<128, EPI>, splitk_reduce_kernel<64, EPI>, splitk_reduce_kernel<64, EPI>, \
-             splitk_reduce_kernel<32, EPI>},                                                               \
+             splitk_reduce_kernel<32, EPI>, splitk_reduce_kernel<64, EPI>, splitk_reduce_kernel<32, EPI>},  \
     }
 
 const Entry kTable[] = {
@@ -662,10 +849,12 @@ constexpr int smem_of() {
 }
 
 const TileInfo kTileInfo[kTiles] = {
-    {128, 128, 32, smem_of<C128>(), 1.0, 0.75},
-    {64, 64, 32, smem_of<C64>(), 0.8, 0.65},
-    {32, 64, 64, smem_of<C32x64>(), 0.8, 0.55},
-    {32, 32, 64, smem_of<C32>(), 0.8, 0.5},
+    {128, 128, 32, C128::NT, smem_of<C128>(), 1.0, 0.75},
+    {64, 64, 32, C64::NT, smem_of<C64>(), 0.8, 0.65},
+    {32, 64, 64, C32x64::NT, smem_of<C32x64>(), 0.8, 0.55},
+    {32, 32, 64, C32::NT, smem_of<C32>(), 0.8, 0.5},
+    {32, 64, 64, C32x64::NT, 4 * C32x64::KS * 32 * C32x64::LDC, 0.65, 0.55},  // direct loads
+    {32, 32, 64, C32::NT, 4 * C32::KS * 32 * C32::LDC, 0.65, 0.5},
 };
 
 const Entry* find_entry(int ta, int tb, int pro, int epi) {
@@ -906,7 +1095,8 @@ extern "C" int pxk_gemm(const pxk_gemm_desc* d, void* stream) {
     const int64_t blocks = p.tiles_m * p.tiles_n * d->batch * p.splits;
     g.remap = blocks % 8 == 0;
     const int has_bias = d->prologue == PXK_PRO_DIV_STAB && d->z_bias.ptr != nullptr;
-    hipLaunchKernelGGL(p.e->k[has_bias][p.tile], dim3(static_cast<unsigned>(blocks)), dim3(NT), 0, S(stream), g);
+    hipLaunchKernelGGL(p.e->k[has_bias][p.tile], dim3(static_cast<unsigned>(blocks)),
+                       dim3(static_cast<unsigned>(kTileInfo[p.tile].threads)), 0, S(stream), g);
     if (const int rc = launched("pxk_gemm")) return rc;
     if (p.splits > 1) {
         const int bn = kTileInfo[p.tile].bn;

@@ -41,7 +41,7 @@ CAUSAL_NONE, CAUSAL_TRI, CAUSAL_K_LE_M, CAUSAL_K_GE_M = 0, 1, 2, 3
 PRO_NONE, PRO_DIV_STAB = 0, 1
 (EPI_STORE, EPI_STORE_BIAS, EPI_ADD_RESID, EPI_MUL_X, EPI_SPV, EPI_ROPE_REL, EPI_VALUE_REL,
  EPI_SWIGLU_REL) = range(8)
-TILE_AUTO, TILE_128x128, TILE_64x64, TILE_32x64, TILE_32x32 = range(5)
+TILE_AUTO, TILE_128x128, TILE_64x64, TILE_32x64, TILE_32x32, TILE_32x64_DIRECT, TILE_32x32_DIRECT = range(7)
 
 # (name, restype, argtypes) of every pxk entry point; `p` = device pointer (void*), `i` = int64,
 # `f` = float, `n` = int, `s` = size_t.
@@ -120,6 +120,8 @@ def pxk():
         lib.pxk_gemm_plan.restype = ctypes.c_int
         lib.pxk_gemm_plan.argtypes = [ctypes.POINTER(GemmDesc), ctypes.POINTER(ctypes.c_int32),
                                       ctypes.POINTER(ctypes.c_int32)]
+        lib.pxk_attention_relevance_q.restype = ctypes.c_int
+        lib.pxk_attention_relevance_q.argtypes = [ctypes.POINTER(AttnRelDesc), c_vp]
         lib.pxk_gemm_supported.restype = ctypes.c_int
         lib.pxk_gemm_supported.argtypes = [ctypes.c_int] * 4
         lib.pxk_reduce_partials.restype = ctypes.c_size_t
@@ -139,6 +141,18 @@ def call(name, *args):
 
 def operand(ptr, ld, batch_stride=0, inner_stride=0, inner_div=0, group_stride=0):
     return Operand(ptr, ld, batch_stride, inner_stride, inner_div, group_stride)
+
+
+class AttnRelDesc(ctypes.Structure):
+    """pxk_attn_rel_desc."""
+
+    _fields_ = [("n", c_i64), ("l", c_i64), ("heads", c_i64), ("kv_heads", c_i64), ("head_dim", c_i64),
+                ("scale", ctypes.c_float), ("eps", ctypes.c_float), ("causal", ctypes.c_int32),
+                ("rope", ctypes.c_int32), ("rope_half", ctypes.c_int32), ("reserved", ctypes.c_int32),
+                ("spv", c_vp), ("ld_spv", c_i64), ("v", c_vp), ("ld_v", c_i64), ("k", c_vp), ("ld_k", c_i64),
+                ("p", c_vp), ("raw", c_vp), ("s", c_vp), ("q", c_vp), ("ld_q", c_i64), ("q_pre", c_vp),
+                ("ld_q_pre", c_i64), ("z", c_vp), ("ld_z", c_i64), ("bias", c_vp), ("cos_t", c_vp), ("sin_t", c_vp),
+                ("g", c_vp), ("ld_g", c_i64)]
 
 
 def gemm(desc, stream=None):

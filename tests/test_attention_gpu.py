@@ -6,6 +6,8 @@ the primitive contract's 1e-4 scaled by max(1, |ref|), applied to every output t
 pass later reads: raw scores on the visible keys, P on every key (zeros past the visible ones),
 and the head-packed context.
 """
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -88,3 +90,84 @@ def test_fused_attention_support_and_rejection():
     assert lib.pxk_attention_supported(64, 4096, 960, 960, 960) == 0  # score rows beyond LDS
     rc = lib.pxk_attention_forward(16, 64, 16, 64, 16, 64, 16, 16, 16, 64, 1, 8, 3, 2, 16, 0.25, 1, None)
     assert rc == 1  # 3 query heads over 2 KV heads
+
+
+def stab(z, eps):
+    return z + eps * np.where(z >= 0, 1.0, -1.0)
+
+
+def relevance_q_reference(spv, q, q_pre, k, v, z, bias, p, raw, cos, sin, n, L, H, Hkv, D, scale, eps, causal, rope,
+                          half):
+    """s (n, H, L, L) and g_q (n*L, H*D) in float64: the module's steps 2-4 (multihead_attention_module.cpp
+    :435-447 with lrp_bilinear_matmul, lrp_softmax_rows and lrp_rope)."""
+    grp = H // Hkv
+    f = lambda a, heads: a.reshape(n, L, heads, D).transpose(0, 2, 1, 3).astype(np.float64)
+    spv_h, q_h, qx_h, z_h = f(spv, H), f(q, H), f(q_pre, H), f(z, H)
+    k_h = np.repeat(f(k, Hkv), grp, axis=1)
+    v_h = np.repeat(f(v, Hkv), grp, axis=1)
+    vis = np.tril(np.ones((L, L), bool)) if causal else np.ones((L, L), bool)
+    r_attn = np.where(vis, p * (spv_h @ v_h.transpose(0, 1, 3, 2)), 0.0)
+    tot = r_attn.sum(axis=-1, keepdims=True)
+    s = np.where(vis, (scale * raw) * (r_attn - p * tot) / (2.0 * raw + eps * np.where(raw >= 0, 1.0, -1.0)), 0.0)
+    sk = s @ k_h
+    r = q_h * sk
+    if rope:
+        d = np.arange(D)
+        hf = D // 2
+        i = np.where(d < hf, d, d - hf) if half else d // 2
+        lo = i if half else 2 * i
+        hi = i + hf if half else 2 * i + 1
+        c, sn = cos[:, i][None, None], sin[:, i][None, None]
+        y_lo, y_hi = q_h[..., lo], q_h[..., hi]
+        d0, d1 = stab(y_lo, eps), stab(y_hi, eps)
+        r_lo, r_hi = r[..., lo], r[..., hi]
+        is_lo = (d == lo)
+        r_in = np.where(is_lo, qx_h * c / d0 * r_lo + qx_h * sn / d1 * r_hi, qx_h * -sn / d0 * r_lo + qx_h * c / d1 * r_hi)
+    else:
+        r_in = r
+    zz = z_h + (bias.reshape(1, H, 1, D) if bias is not None else 0.0)
+    g = (r_in / stab(zz, eps)).transpose(0, 2, 1, 3).reshape(n * L, H * D)
+    return s, g
+
+
+@gpu
+@pytest.mark.parametrize("rope,half,bias", [(1, 1, 0), (1, 0, 1), (0, 0, 1)])
+@pytest.mark.parametrize("causal", [1, 0])
+@pytest.mark.parametrize("n,L,H,Hkv,D", [(1, 37, 4, 2, 16), (2, 64, 3, 1, 12), (1, 128, 9, 3, 64), (1, 40, 2, 2, 128)])
+def test_fused_attention_relevance_matches_numpy(n, L, H, Hkv, D, causal, rope, half, bias):
+    qd, kvd = H * D, Hkv * D
+    scale, eps = 1.0 / np.sqrt(D), 1e-6
+    rs = np.random.RandomState(L + D)
+    away = lambda *shape: (rs.uniform(0.5, 1.5, shape) * rs.choice([-1.0, 1.0], shape)).astype(np.float32)
+    spv, q, q_pre, z = G.uniform((n * L, qd), 1), away(n * L, qd), G.uniform((n * L, qd), 3), away(n * L, qd)
+    k, v = G.uniform((n * L, kvd), 4), G.uniform((n * L, kvd), 5)
+    b = (G.uniform((qd,), 6) * 0.1) if bias else None
+    raw = away(n, H, L, L)  # denominators 2 raw + eps sign raw stay clear of 0
+    vis = np.tril(np.ones((L, L), bool)) if causal else np.ones((L, L), bool)
+    x = np.where(vis, scale * raw.astype(np.float64), -np.inf)
+    e = np.exp(x - x.max(-1, keepdims=True))
+    p = (e / e.sum(-1, keepdims=True)).astype(np.float32)
+    ang = np.arange(L)[:, None] * (10000.0 ** (-np.arange(D // 2) * 2.0 / D))[None, :]
+    cos, sin = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+    want_s, want_g = relevance_q_reference(spv, q, q_pre, k, v, z, b, p.astype(np.float64), raw.astype(np.float64),
+                                           cos.astype(np.float64), sin.astype(np.float64), n, L, H, Hkv, D, scale,
+                                           eps, causal, rope, half)
+    dv = {key: G.dev(a) for key, a in dict(spv=spv, q=q, q_pre=q_pre, z=z, k=k, v=v, p=p, raw=raw, cos=cos,
+                                            sin=sin).items()}
+    s_out, g_out = G.empty((n, H, L, L)), G.empty((n * L, qd))
+    d = N.AttnRelDesc()
+    d.n, d.l, d.heads, d.kv_heads, d.head_dim = n, L, H, Hkv, D
+    d.scale, d.eps, d.causal, d.rope, d.rope_half = scale, eps, causal, rope, half
+    d.spv, d.ld_spv = G.ptr(dv["spv"]).value, qd
+    d.v, d.ld_v, d.k, d.ld_k = G.ptr(dv["v"]).value, kvd, G.ptr(dv["k"]).value, kvd
+    d.p, d.raw, d.s = G.ptr(dv["p"]).value, G.ptr(dv["raw"]).value, G.ptr(s_out).value
+    d.q, d.ld_q, d.q_pre, d.ld_q_pre = G.ptr(dv["q"]).value, qd, G.ptr(dv["q_pre"]).value, qd
+    d.z, d.ld_z = G.ptr(dv["z"]).value, qd
+    d.bias = G.ptr(G.dev(b)).value if bias else None
+    d.cos_t, d.sin_t = G.ptr(dv["cos"]).value, G.ptr(dv["sin"]).value
+    d.g, d.ld_g = G.ptr(g_out).value, qd
+    assert N.pxk().pxk_attention_relevance_q(ctypes.byref(d), G.stream()) == 0, N.pxk().pxk_last_error()
+    got_s = G.host(s_out)
+    G.assert_close(got_s, want_s, 1e-4, "s")
+    assert np.all(got_s[..., ~vis] == 0.0)
+    G.assert_close(G.host(g_out), want_g, 1e-4, "g_q")

@@ -25,8 +25,9 @@ COMBOS = [
     (0, 0, N.PRO_NONE, N.EPI_ROPE_REL), (1, 0, N.PRO_NONE, N.EPI_ROPE_REL), (0, 0, N.PRO_NONE, N.EPI_VALUE_REL),
     (1, 0, N.PRO_NONE, N.EPI_VALUE_REL), (0, 1, N.PRO_DIV_STAB, N.EPI_SWIGLU_REL),
 ]
-TILES = [N.TILE_128x128, N.TILE_64x64, N.TILE_32x64, N.TILE_32x32]
-TILE_BN = {N.TILE_128x128: 128, N.TILE_64x64: 64, N.TILE_32x64: 64, N.TILE_32x32: 32}
+TILES = [N.TILE_128x128, N.TILE_64x64, N.TILE_32x64, N.TILE_32x32, N.TILE_32x64_DIRECT, N.TILE_32x32_DIRECT]
+TILE_BN = {N.TILE_128x128: 128, N.TILE_64x64: 64, N.TILE_32x64: 64, N.TILE_32x32: 32, N.TILE_32x64_DIRECT: 64,
+           N.TILE_32x32_DIRECT: 32}
 EPS = 1e-6
 
 
@@ -106,7 +107,7 @@ def run(d, splits):
 def test_fused_gemm_on_every_tile(combo, tile, splits):
     ta, tb, pro, epi = combo
     rope = epi == N.EPI_ROPE_REL
-    D = 64 if rope and tile != N.TILE_32x32 else 16
+    D = 64 if rope and TILE_BN[tile] >= 64 else 16
     m, n, k = 77, 128, 150  # ragged M and K; N = whole heads for the RoPE rule
     a, b = G.uniform((k, m) if ta else (m, k), 1), G.uniform((n, k) if tb else (k, n), 2)
     t = {"x": G.uniform((m, n), 3), "y": away((m, n), 4), "w": away((m, n), 5), "z": away((m, n), 6),
