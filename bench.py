@@ -31,6 +31,13 @@ FP32_MFMA_PEAK_TFLOPS = 157.3
 HBM_PEAK_GBS = 8000.0
 LXT_EPS = 1e-9
 
+# HBM bytes of one launch of the LM-head relevance GEMM (main kernel + split-K reduce), from two
+# rocprofv3 --pmc runs of `bench.py --kernel-probe` (FETCH_SIZE, then WRITE_SIZE; see
+# profiles/head_relevance_gemm_traffic.md), each scaled by what the counter reads for the probe's
+# 256 MiB copy (FETCH_SIZE x 2.0, WRITE_SIZE x 1.0); median dispatch of five. Valid for the plan
+# it was measured on.
+HEAD_REL_TRAFFIC = {"plan": (2, 32), "bytes": (341338 * 2.0 + 36864 + 19056 * 2.0 + 1152) * 1024}
+
 S_CONFIG = dict(vocab_size=49152, hidden_size=576, num_layers=30, num_heads=9, num_kv_heads=3, head_dim=64,
                 intermediate_size=1536, rms_norm_eps=1e-5, rope_theta=100000.0, use_rope=1, rope_rotate_half=1,
                 causal=1, qkv_bias=0, out_bias=0, mlp_bias=0, tie_word_embeddings=1, reserved=0)
@@ -157,6 +164,23 @@ def mlp_gate_up_gemm(torch, N, c, L):
     return desc, 2.0 * L * d * 2 * F, (A, B, C)
 
 
+def kernel_probe(torch, N, models):
+    """Counter-collection workload: 5 copies of 256 MiB (the counters' calibration) and 5 launches of
+    the LM-head relevance GEMM, on the backend's stream."""
+    st = models.stream()
+    n = 64 * 1024 * 1024
+    src, dst = torch.rand(n, device="cuda"), torch.empty(n, device="cuda")
+    torch.cuda.synchronize()
+    for _ in range(5):
+        N.call("pxk_copy_2d", dst.data_ptr(), 1 << 20, src.data_ptr(), 1 << 20, 64, 1 << 20, st)
+    desc, _, keep = head_relevance_gemm(torch, N, S_CONFIG, SEQ)
+    for _ in range(5):
+        N.gemm(desc, st)
+    models.synchronize()
+    print("kernel probe: copy 256 MiB x5, LM-head relevance GEMM x5 (plan tile %d, split-K %d)" % N.gemm_plan(desc))
+    del keep
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -165,6 +189,8 @@ def main():
     ap.add_argument("--mode", choices=("graph", "eager"), default="graph")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--layers", type=int, default=S_CONFIG["num_layers"], help=argparse.SUPPRESS)
+    ap.add_argument("--kernel-probe", action="store_true",
+                    help="only launch a 256 MiB copy and the LM-head relevance GEMM, 5 times each (for rocprofv3 --pmc)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one MI355X (the path runs on one GPU; --gpus %d is not supported)"
@@ -175,6 +201,10 @@ def main():
 
     from pulsatrix_amd import models
     from pulsatrix_amd import native as N
+
+    if args.kernel_probe:
+        kernel_probe(torch, N, models)
+        return
 
     fields = dict(S_CONFIG, num_layers=args.layers)
     cfg = N.model_config(**fields)
@@ -267,9 +297,12 @@ def main():
             "peak": FP32_MFMA_PEAK_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / FP32_MFMA_PEAK_TFLOPS, 4),
-            "traffic": None,
+            "traffic": HEAD_REL_TRAFFIC["bytes"] if (tile, splits) == HEAD_REL_TRAFFIC["plan"] else None,
+            "traffic_unit": "bytes per launch (main kernel + split-K reduce)",
             "avg_launch_us": round(ker_s * 1e6, 2),
             "algorithmic_gflop_per_launch": round(flops / 1e9, 3),
+            "algorithmic_bytes_per_launch": 4 * SEQ * S_CONFIG["vocab_size"] * 2 + 4 * S_CONFIG["vocab_size"] * 576 +
+                                            4 * SEQ * 576 * 2,
         },
         "kernels": {
             "mlp_gate_up_512x576x3072": {"avg_us": round(ker2_s * 1e6, 2),
