@@ -1,6 +1,8 @@
 """Throughput of the causal-LM forward + AttnLRP path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--mode graph|eager] [--no-cpu-baseline]
+    python bench.py --op-sweep        # raw op sweep: GEMM shapes, elementwise 2^26, RMSNorm 32768 x 2048
+    python bench.py --kernel-probe    # 256 MiB copy + LM-head relevance GEMM, for rocprofv3 --pmc runs
 
 Workload: the SmolLM2-135M-shaped causal LM (30 layers, hidden 576, 9 query / 3 KV heads of 64,
 SwiGLU FFN 1536, vocab 49152, tied embeddings, RMSNorm eps 1e-5, RoPE theta 100000), fp32,
@@ -181,6 +183,101 @@ def kernel_probe(torch, N, models):
     del keep
 
 
+# The raw DeviceBackend op sweep: GEMM shapes M x K x N (forward), seeded uniform(-1, 1) data.
+SWEEP_GEMMS = [(512, 576, 1536), (512, 1536, 576), (4096, 2048, 8192), (512, 576, 49152)]
+SWEEP_ELEMENTS = 1 << 26
+SWEEP_RMS_ROWS, SWEEP_RMS_COLS = 32768, 2048
+
+
+def sweep_gemm(torch, N, M, K, Nn, orient):
+    """One sweep GEMM: "NN" C = A B (forward, M x K x N); "NT" the Linear relevance form
+    r_in (M x K) = x * ((R / stab(z)) W^T) against the stored (K x N) W (lrp_rules.cpp:197-215,
+    device_backend.hpp:627-628); "TN" C (K x N) = A^T S, the weight-side share of a bilinear
+    product (lrp_math.hpp:57-86). All three do 2 M K N FLOPs."""
+    g = torch.Generator(device="cuda").manual_seed(M + 3 * K + 7 * Nn)
+    u = lambda *s: torch.rand(*s, device="cuda", generator=g) * 2 - 1
+    desc = N.GemmDesc()
+    desc.batch, desc.inner, desc.kgroups = 1, 1, 1
+    if orient == "NN":
+        A, B, C = u(M, K), u(K, Nn), torch.empty(M, Nn, device="cuda")
+        desc.m, desc.n, desc.k = M, Nn, K
+        desc.a, desc.b, desc.c = N.operand(A.data_ptr(), K), N.operand(B.data_ptr(), Nn), N.operand(C.data_ptr(), Nn)
+        keep = (A, B, C)
+    elif orient == "NT":
+        R, Z, W, X, C = u(M, Nn), u(M, Nn), u(K, Nn), u(M, K), torch.empty(M, K, device="cuda")
+        desc.m, desc.n, desc.k, desc.trans_b = M, K, Nn, 1
+        desc.prologue, desc.epilogue, desc.eps = N.PRO_DIV_STAB, N.EPI_MUL_X, 1e-6
+        desc.a, desc.z = N.operand(R.data_ptr(), Nn), N.operand(Z.data_ptr(), Nn)
+        desc.b, desc.c, desc.x = N.operand(W.data_ptr(), Nn), N.operand(C.data_ptr(), K), N.operand(X.data_ptr(), K)
+        keep = (R, Z, W, X, C)
+    else:
+        A, S, C = u(M, K), u(M, Nn), torch.empty(K, Nn, device="cuda")
+        desc.m, desc.n, desc.k, desc.trans_a = K, Nn, M, 1
+        desc.a, desc.b, desc.c = N.operand(A.data_ptr(), K), N.operand(S.data_ptr(), Nn), N.operand(C.data_ptr(), Nn)
+        keep = (A, S, C)
+    ws_bytes = N.gemm_workspace(desc)
+    ws = torch.empty(max(ws_bytes // 4, 1), device="cuda")
+    desc.workspace, desc.workspace_bytes = ws.data_ptr(), ws_bytes
+    return desc, keep + (ws,)
+
+
+def timed_reps(torch, stream, launch, target_s=0.02):
+    """Average launch duration over enough repetitions for about target_s of GPU time."""
+    once = time_kernel(torch, stream, launch, 1)
+    return time_kernel(torch, stream, launch, int(min(500, max(5, target_s / max(once, 1e-6)))))
+
+
+def op_sweep(torch, N, models):
+    """The op sweep: GEMM TFLOP/s against the fp32 MFMA peak, elementwise and RMSNorm GB/s
+    against HBM, each kernel timed with HIP events on the backend's stream."""
+    raw_st = models.stream()
+    stream = torch.cuda.ExternalStream(raw_st)
+    rows = []
+    tile_name = {N.TILE_128x128: "128x128", N.TILE_64x64: "64x64", N.TILE_32x64: "32x64", N.TILE_32x32: "32x32",
+                 N.TILE_32x64_DIRECT: "32x64d", N.TILE_32x32_DIRECT: "32x32d"}
+    for (M, K, Nn) in SWEEP_GEMMS:
+        for orient in ("NN", "NT", "TN"):
+            desc, keep = sweep_gemm(torch, N, M, K, Nn, orient)
+            t = timed_reps(torch, stream, lambda: N.gemm(desc, raw_st))
+            tile, splits = N.gemm_plan(desc)
+            tf = 2.0 * M * K * Nn / t / 1e12
+            rows.append({"op": "gemm %s" % orient, "shape": "%dx%dx%d" % (M, K, Nn), "plan": "%s/%d" % (tile_name[tile],
+                         splits), "avg_us": round(t * 1e6, 2), "tflops": round(tf, 2),
+                         "frac": round(tf / FP32_MFMA_PEAK_TFLOPS, 4)})
+            del keep
+    n = SWEEP_ELEMENTS
+    g = torch.Generator(device="cuda").manual_seed(5)
+    a, b, r = [torch.rand(n, device="cuda", generator=g) * 2 - 1 for _ in range(3)]
+    o1, o2 = torch.empty(n, device="cuda"), torch.empty(n, device="cuda")
+    P = lambda x: x.data_ptr()
+    ew = [
+        ("add", 12, lambda: N.call("pxk_add", P(a), P(b), P(o1), n, raw_st)),
+        ("mul", 12, lambda: N.call("pxk_mul", P(a), P(b), P(o1), n, raw_st)),
+        ("relu", 8, lambda: N.call("pxk_elementwise", 0, P(a), P(o1), n, raw_st)),
+        ("epsilon-divide", 12, lambda: N.call("pxk_lrp_stabilized_divide", P(a), P(b), None, P(o1), n, 1e-6, 0, raw_st)),
+        ("epsilon-divide gated", 16,
+         lambda: N.call("pxk_lrp_stabilized_divide", P(a), P(b), P(r), P(o1), n, 1e-6, 1, raw_st)),
+        ("residual split", 20, lambda: N.call("pxk_lrp_residual_split", P(a), P(b), P(r), P(o1), P(o2), n, 1e-6, raw_st)),
+        ("bilinear elementwise", 16,
+         lambda: N.call("pxk_lrp_bilinear_elementwise", P(a), P(b), P(r), P(o1), n, 1e-6, raw_st)),
+    ]
+    for name, bpe, launch in ew:
+        t = timed_reps(torch, stream, launch)
+        gbs = bpe * n / t / 1e9
+        rows.append({"op": name, "shape": "2^26", "bytes_per_element": bpe, "avg_us": round(t * 1e6, 2),
+                     "gbs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)})
+    del a, b, r, o1, o2
+    R, C = SWEEP_RMS_ROWS, SWEEP_RMS_COLS
+    x = torch.rand(R, C, device="cuda", generator=g) * 2 - 1
+    gamma, y, rms = torch.rand(C, device="cuda", generator=g), torch.empty(R, C, device="cuda"), torch.empty(R, device="cuda")
+    t = timed_reps(torch, stream, lambda: N.call("pxk_rms_norm_forward", P(x), P(gamma), P(y), P(rms), R, C, 1e-5, raw_st))
+    nbytes = 8 * R * C + 4 * R + 4 * C
+    rows.append({"op": "rms_norm", "shape": "%dx%d" % (R, C), "bytes_per_element": 8, "avg_us": round(t * 1e6, 2),
+                 "gbs": round(nbytes / t / 1e9, 1), "frac": round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4)})
+    print(json.dumps({"sweep": "raw DeviceBackend op sweep, fp32, seeded uniform(-1,1) data", "peak_tflops":
+                      FP32_MFMA_PEAK_TFLOPS, "peak_gbs": HBM_PEAK_GBS, "ops": rows}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -191,6 +288,8 @@ def main():
     ap.add_argument("--layers", type=int, default=S_CONFIG["num_layers"], help=argparse.SUPPRESS)
     ap.add_argument("--kernel-probe", action="store_true",
                     help="only launch a 256 MiB copy and the LM-head relevance GEMM, 5 times each (for rocprofv3 --pmc)")
+    ap.add_argument("--op-sweep", action="store_true",
+                    help="time the raw op sweep (GEMM shapes, elementwise over 2^26, RMSNorm 32768 x 2048) instead")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one MI355X (the path runs on one GPU; --gpus %d is not supported)"
@@ -204,6 +303,9 @@ def main():
 
     if args.kernel_probe:
         kernel_probe(torch, N, models)
+        return
+    if args.op_sweep:
+        op_sweep(torch, N, models)
         return
 
     fields = dict(S_CONFIG, num_layers=args.layers)

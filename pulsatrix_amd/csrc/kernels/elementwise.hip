@@ -1,6 +1,7 @@
 // elementwise.hip -- memory-bound elementwise kernels (include/pxk.h). Grid-stride loops over
 // 128-bit (float4) accesses when every operand is 16-byte aligned, scalar otherwise; each element's
 // arithmetic is the reference's expression for that element (src/cpu_backend.cpp, lrp_math.hpp).
+#include <algorithm>
 #include <cstdarg>
 #include <cstring>
 #include <string>
@@ -61,30 +62,62 @@ struct Ptrs {
     float* out[NOUT];
 };
 
-template <typename F, int NIN, int NOUT, bool VEC>
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+// Streaming loads and stores (the `nt` cache policy) for operands far larger than the caches, so a
+// pass over them does not evict what the next kernel re-reads; plain accesses otherwise.
+template <bool NT>
+__device__ __forceinline__ f4 ld4(const f4* p) {
+    if constexpr (NT) return __builtin_nontemporal_load(p);
+    else return *p;
+}
+template <bool NT>
+__device__ __forceinline__ void st4(f4* p, f4 v) {
+    if constexpr (NT) __builtin_nontemporal_store(v, p);
+    else *p = v;
+}
+
+// Float4 elements per thread per grid-stride iteration of the vector path: all of a thread's
+// loads are issued before the first use, which keeps enough bytes in flight to saturate HBM.
+constexpr int kUnroll = 4;
+
+template <typename F, int NIN, int NOUT, bool VEC, bool NT>
 __global__ void __launch_bounds__(kThreads) map_kernel_p(F f, Ptrs<NIN, NOUT> p, int64_t n) {
-    const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
     if constexpr (VEC) {
-        typedef float f4 __attribute__((ext_vector_type(4)));
         const int64_t n4 = n / 4;
-        for (int64_t i = blockIdx.x * kThreads + threadIdx.x; i < n4; i += stride) {
-            f4 a[NIN > 0 ? NIN : 1];
+        const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads * kUnroll;
+        for (int64_t base = static_cast<int64_t>(blockIdx.x) * kThreads * kUnroll + threadIdx.x; base < n4;
+             base += stride) {
+            f4 a[kUnroll][NIN > 0 ? NIN : 1];
 #pragma unroll
-            for (int j = 0; j < NIN; ++j) a[j] = reinterpret_cast<const f4*>(p.in[j])[i];
-            f4 o[NOUT];
+            for (int u = 0; u < kUnroll; ++u) {
+                const int64_t i = base + u * kThreads;
+                if (i < n4) {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                float x[NIN > 0 ? NIN : 1], y[NOUT];
-#pragma unroll
-                for (int j = 0; j < NIN; ++j) x[j] = a[j][e];
-                f(x, y);
-#pragma unroll
-                for (int j = 0; j < NOUT; ++j) o[j][e] = y[j];
+                    for (int j = 0; j < NIN; ++j) a[u][j] = ld4<NT>(reinterpret_cast<const f4*>(p.in[j]) + i);
+                }
             }
 #pragma unroll
-            for (int j = 0; j < NOUT; ++j) reinterpret_cast<f4*>(p.out[j])[i] = o[j];
+            for (int u = 0; u < kUnroll; ++u) {
+                const int64_t i = base + u * kThreads;
+                if (i < n4) {
+                    f4 o[NOUT];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        float x[NIN > 0 ? NIN : 1], y[NOUT];
+#pragma unroll
+                        for (int j = 0; j < NIN; ++j) x[j] = a[u][j][e];
+                        f(x, y);
+#pragma unroll
+                        for (int j = 0; j < NOUT; ++j) o[j][e] = y[j];
+                    }
+#pragma unroll
+                    for (int j = 0; j < NOUT; ++j) st4<NT>(reinterpret_cast<f4*>(p.out[j]) + i, o[j]);
+                }
+            }
         }
-        for (int64_t i = n4 * 4 + blockIdx.x * kThreads + threadIdx.x; i < n; i += stride) {
+        const int64_t tstride = static_cast<int64_t>(gridDim.x) * kThreads;
+        for (int64_t i = n4 * 4 + blockIdx.x * kThreads + threadIdx.x; i < n; i += tstride) {
             float x[NIN > 0 ? NIN : 1], y[NOUT];
 #pragma unroll
             for (int j = 0; j < NIN; ++j) x[j] = p.in[j][i];
@@ -93,6 +126,7 @@ __global__ void __launch_bounds__(kThreads) map_kernel_p(F f, Ptrs<NIN, NOUT> p,
             for (int j = 0; j < NOUT; ++j) p.out[j][i] = y[j];
         }
     } else {
+        const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
         for (int64_t i = blockIdx.x * kThreads + threadIdx.x; i < n; i += stride) {
             float x[NIN > 0 ? NIN : 1], y[NOUT];
 #pragma unroll
@@ -117,11 +151,20 @@ int run_map(const char* what, F f, Ptrs<NIN, NOUT> p, int64_t n, void* stream) {
         if (p.out[j] == nullptr) return fail(PXK_ERR_INVALID, "%s: null output", what);
         vec = vec && aligned16(p.out[j]);
     }
-    const unsigned grid = grid_for(vec ? cdiv(n, 4) : n, kThreads);
-    if (vec)
-        hipLaunchKernelGGL((map_kernel_p<F, NIN, NOUT, true>), dim3(grid), dim3(kThreads), 0, S(stream), f, p, n);
-    else
-        hipLaunchKernelGGL((map_kernel_p<F, NIN, NOUT, false>), dim3(grid), dim3(kThreads), 0, S(stream), f, p, n);
+    if (vec) {
+        // One unrolled iteration per thread up to 32768 workgroups; streaming cache policy once an
+        // operand reaches 16 MiB (beyond what the L2s hold).
+        const int64_t g = std::max<int64_t>(1, std::min<int64_t>(cdiv(cdiv(n, 4), kThreads * kUnroll), 32768));
+        if (n >= (int64_t{1} << 22))
+            hipLaunchKernelGGL((map_kernel_p<F, NIN, NOUT, true, true>), dim3(static_cast<unsigned>(g)), dim3(kThreads),
+                               0, S(stream), f, p, n);
+        else
+            hipLaunchKernelGGL((map_kernel_p<F, NIN, NOUT, true, false>), dim3(static_cast<unsigned>(g)),
+                               dim3(kThreads), 0, S(stream), f, p, n);
+    } else {
+        hipLaunchKernelGGL((map_kernel_p<F, NIN, NOUT, false, false>), dim3(grid_for(n, kThreads)), dim3(kThreads), 0,
+                           S(stream), f, p, n);
+    }
     return launched(what);
 }
 

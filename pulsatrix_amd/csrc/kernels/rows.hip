@@ -36,6 +36,53 @@ __global__ void __launch_bounds__(kThreads) rms_norm_kernel(const float* in, con
     for (int64_t i = lane; i < cols; i += kWave) o[i] = gamma[i] * x[i] / rms;
 }
 
+// The same row with 128-bit accesses and the row held in registers between the two passes: lane l
+// owns float4 columns l, l + 64, ..., so x is read from HBM once. Needs cols % 4 == 0, 16-byte
+// aligned rows, and cols <= 256 * NV. NT: streaming (non-temporal) cache policy for x and out, for
+// tensors far larger than the caches.
+template <int NV, bool NT>
+__global__ void __launch_bounds__(kThreads) rms_norm_vec_kernel(const float* in, const float* gamma, float* out,
+                                                                float* row_rms, int64_t rows, int cols4, float eps) {
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    const int64_t r = row_id();
+    if (r >= rows) return;
+    const int lane = lane_id();
+    const f4* x = reinterpret_cast<const f4*>(in) + r * cols4;
+    f4 v[NV];
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int c = lane + j * kWave;
+        if (c < cols4) {
+            if constexpr (NT) v[j] = __builtin_nontemporal_load(x + c);
+            else v[j] = x[c];
+        } else {
+            v[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) ss += v[j].x * v[j].x + v[j].y * v[j].y + v[j].z * v[j].z + v[j].w * v[j].w;
+    ss = wave_sum(ss);
+    const float rms = sqrtf(ss / static_cast<float>(4 * cols4) + eps);
+    if (row_rms && lane == 0) row_rms[r] = rms;
+    f4* o = reinterpret_cast<f4*>(out) + r * cols4;
+    const f4* g = reinterpret_cast<const f4*>(gamma);
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int c = lane + j * kWave;
+        if (c < cols4) {
+            const f4 gv = g[c];
+            f4 y;
+            y.x = gv.x * v[j].x / rms;
+            y.y = gv.y * v[j].y / rms;
+            y.z = gv.z * v[j].z / rms;
+            y.w = gv.w * v[j].w / rms;
+            if constexpr (NT) __builtin_nontemporal_store(y, o + c);
+            else o[c] = y;
+        }
+    }
+}
+
 // ---- softmax_rows (cpu_backend.cpp:292-310) ---------------------------------------------------
 __global__ void __launch_bounds__(kThreads) softmax_kernel(const float* in, float* out, int64_t rows, int64_t cols) {
     const int64_t r = row_id();
@@ -291,6 +338,21 @@ __global__ void __launch_bounds__(kThreads) lm_seed_kernel(const float* logits, 
     }
 }
 
+template <bool NT>
+void launch_rms_vec(int64_t nv, dim3 grid, dim3 block, hipStream_t st, const float* in, const float* gamma, float* out,
+                    float* row_rms, int64_t rows, int cols4, float eps) {
+    if (nv <= 2)
+        hipLaunchKernelGGL((rms_norm_vec_kernel<2, NT>), grid, block, 0, st, in, gamma, out, row_rms, rows, cols4, eps);
+    else if (nv <= 3)
+        hipLaunchKernelGGL((rms_norm_vec_kernel<3, NT>), grid, block, 0, st, in, gamma, out, row_rms, rows, cols4, eps);
+    else if (nv <= 4)
+        hipLaunchKernelGGL((rms_norm_vec_kernel<4, NT>), grid, block, 0, st, in, gamma, out, row_rms, rows, cols4, eps);
+    else if (nv <= 8)
+        hipLaunchKernelGGL((rms_norm_vec_kernel<8, NT>), grid, block, 0, st, in, gamma, out, row_rms, rows, cols4, eps);
+    else
+        hipLaunchKernelGGL((rms_norm_vec_kernel<16, NT>), grid, block, 0, st, in, gamma, out, row_rms, rows, cols4, eps);
+}
+
 unsigned rows_grid(int64_t rows) { return static_cast<unsigned>(cdiv(rows, kRowsPerBlock)); }
 
 bool sizes_ok(const char* what, int64_t a, int64_t b, int* rc) {
@@ -313,8 +375,17 @@ int pxk_rms_norm_forward(const float* in, const float* gamma, float* out, float*
                          float eps, void* stream) {
     int rc;
     if (!sizes_ok("pxk_rms_norm_forward", rows, cols, &rc)) return rc;
-    hipLaunchKernelGGL(rms_norm_kernel, dim3(rows_grid(rows)), dim3(kThreads), 0, S(stream), in, gamma, out, row_rms,
-                       rows, cols, eps);
+    const dim3 grid(rows_grid(rows)), block(kThreads);
+    const int64_t c4 = cols / 4, nv = cdiv(c4, kWave);
+    if (cols % 4 == 0 && nv <= 16 && aligned16(in) && aligned16(gamma) && aligned16(out)) {
+        const int cols4 = static_cast<int>(c4);
+        if (rows * cols >= (int64_t{1} << 22))
+            launch_rms_vec<true>(nv, grid, block, S(stream), in, gamma, out, row_rms, rows, cols4, eps);
+        else
+            launch_rms_vec<false>(nv, grid, block, S(stream), in, gamma, out, row_rms, rows, cols4, eps);
+    } else {
+        hipLaunchKernelGGL(rms_norm_kernel, grid, block, 0, S(stream), in, gamma, out, row_rms, rows, cols, eps);
+    }
     return launched("pxk_rms_norm_forward");
 }
 

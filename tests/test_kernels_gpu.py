@@ -241,6 +241,23 @@ def test_elementwise_ops_match_oracle():
 
 
 @gpu
+@pytest.mark.parametrize("rows,cols,offset", [(7, 100, 0), (513, 576, 0), (64, 1024, 0), (130, 2048, 0),
+                                              (33, 4096, 0), (9, 4100, 0), (17, 6, 0), (40, 576, 1)])
+def test_rms_norm_widths_match_oracle(rows, cols, offset):
+    """Every register-resident width class (2, 3, 4, 8, 16 float4 per lane), the scalar fallback for
+    wide, odd and misaligned rows, and rows_rms, against the oracle (row_math.hpp:59-71)."""
+    x, g = G.uniform((rows, cols), 4 + cols), G.uniform((cols,), 5)
+    ref, rms = np.empty_like(x), np.empty((rows,), np.float32)
+    G.oracle_call("pxo_rms_norm_forward", x, g, ref, rms, rows, cols, 1e-5)
+    xd = G.dev(np.concatenate([np.zeros(offset, np.float32), x.ravel()]))
+    out, orms = G.empty((rows * cols + offset,)), G.empty((rows,))
+    N.call("pxk_rms_norm_forward", xd.data_ptr() + 4 * offset, G.ptr(G.dev(g)), out.data_ptr() + 4 * offset,
+           G.ptr(orms), rows, cols, 1e-5, G.stream())
+    G.assert_close(G.host(out)[offset:].reshape(rows, cols), ref, 1e-5, "rmsnorm")
+    G.assert_close(G.host(orms), rms, 1e-5, "rms")
+
+
+@gpu
 def test_row_kernels_match_oracle():
     rows, cols = 333, 2048
     x, g = G.uniform((rows, cols), 1), G.uniform((cols,), 2)
