@@ -244,6 +244,52 @@ typedef struct pxk_attn_rel_desc {
 } pxk_attn_rel_desc;
 int pxk_attention_relevance_q(const pxk_attn_rel_desc* d, void* stream);
 
+/* The key and value shares of one attention layer's AttnLRP pass, fused per KV head, 16-key
+ * block and 16-wide group of head dimensions (MultiHeadAttentionModule::propagate_relevance,
+ * multihead_attention_module.cpp:446-475: the b-shares of lrp_bilinear_matmul, lrp_math.hpp:57-86,
+ * summed over the query heads of each KV head as sum_kv_groups does, :173-188; lrp_rope
+ * lrp_math.hpp:104-123 for the keys; then the k/v projections' stabilised denominators):
+ *   r_k = K * sum_h s_h^T Q_h      -> key_rel = RoPE rule(x = k_pre, y = K, r_k),  g_k = key_rel / stab(z_k + bias_k)
+ *   r_v = V * sum_h P_h^T s_pv_h   -> value_rel = r_v,                          g_v = r_v / stab(z_v + bias_v)
+ * s and P are (n, heads, l, l) with zeros at masked entries (as pxk_attention_relevance_q and
+ * pxk_attention_forward write them); under `causal` only queries at or after each key are read.
+ * q (post-RoPE), s_pv, k (post-RoPE), k_pre, v, z_k, z_v, key_rel, value_rel, g_k and g_v are
+ * token-major head-packed rows with the given strides (query head h at column h*head_dim, KV
+ * head j at column j*head_dim). Without RoPE, key_rel = r_k and k_pre is unused. key_rel and
+ * value_rel may be NULL; bias_k / bias_v are NULL under the pre-bias rule or without a bias.
+ * Replaces the two transposed k/v-share GEMMs and their split-K reductions. */
+typedef struct pxk_attn_rel_kv_desc {
+    int64_t n, l, heads, kv_heads, head_dim;
+    float eps;
+    int32_t causal, rope, rope_half;
+    const float* s;
+    const float* p;
+    const float* q;
+    int64_t ld_q;
+    const float* spv;
+    int64_t ld_spv;
+    const float* k;
+    int64_t ld_k;
+    const float* k_pre;
+    int64_t ld_k_pre;
+    const float* v;
+    int64_t ld_v;
+    const float* z_k;
+    const float* z_v;
+    int64_t ld_z;
+    const float* bias_k;
+    const float* bias_v;
+    const float* cos_t; /* (l x head_dim/2), position = row within the sequence */
+    const float* sin_t;
+    float* key_rel;
+    float* value_rel;
+    int64_t ld_rel;
+    float* g_k;
+    float* g_v;
+    int64_t ld_g;
+} pxk_attn_rel_kv_desc;
+int pxk_attention_relevance_kv(const pxk_attn_rel_kv_desc* d, void* stream);
+
 /* Causal/plain softmax of scaled scores (the module's axpby + attention_mask_fill(lowest) +
  * softmax_rows, multihead_attention_module.cpp:280-285): P = softmax(scale * raw) over the keys
  * each query sees; masked entries of P are written 0. raw (slices, L, L); only its visible

@@ -301,53 +301,46 @@ const float* MultiHeadAttentionModule::run_relevance(const float* relevance_out,
     } else {
         relevance_scores_unfused(spv, eps, bid);
     }
-    // 5. key share per KV head, summed over its query heads: r_k = K * sum_h s_qk_h^T Q_h.
+    // 5-6. key and value shares per KV head, summed over its query heads, fused:
+    //      r_k = K * sum_h s_qk_h^T Q_h with the RoPE rule, r_v = V * sum_h P_h^T s_pv_h, and the
+    //      k/v projections' denominators into g.
     {
-        pxk_gemm_desc d = gemm_desc(l, D_, l);
-        d.batch = n * Hkv_;
-        d.inner = Hkv_;
-        d.kgroups = grp;
-        d.trans_a = 1;
-        d.causal = causal ? PXK_CAUSAL_K_GE_M : PXK_CAUSAL_NONE;
-        d.eps = eps;
-        d.a = mat(ra, l, H_ * LL, grp * LL, 0, LL);
-        d.b = mat(q, ldq, l * ldq, grp * D_, 0, D_);
-        d.c = mat(key_rel_.data(), kvd, l * kvd, D_);
-        d.c2 = mat(g + qd, w3, l * w3, D_);
-        d.z = mat(z + qd, w3, l * w3, D_);
-        if (bq) d.e_bias = mat(bq + qd, 0, 0, D_);
-        if (config_.use_rope) {
-            d.epilogue = PXK_EPI_ROPE_REL;
-            d.x = mat(y + qd, w3, l * w3, D_);
-            d.y = mat(k, ldk, l * ldk, D_);
-            d.cos_t = cos_.data();
-            d.sin_t = sin_.data();
-            d.head_dim = D_;
-            d.rope_half = config_.rope_layout == RoPELayout::RotateHalf;
-        } else {
-            d.epilogue = PXK_EPI_VALUE_REL;
-            d.y = mat(k, ldk, l * ldk, D_);
-        }
-        be_->run_gemm(d);
-    }
-    // 6. value share per KV head: r_v = V * sum_h P_h^T s_pv_h.
-    {
-        pxk_gemm_desc d = gemm_desc(l, D_, l);
-        d.batch = n * Hkv_;
-        d.inner = Hkv_;
-        d.kgroups = grp;
-        d.trans_a = 1;
-        d.causal = causal ? PXK_CAUSAL_K_GE_M : PXK_CAUSAL_NONE;
-        d.epilogue = PXK_EPI_VALUE_REL;
-        d.eps = eps;
-        d.a = mat(p, l, H_ * LL, grp * LL, 0, LL);
-        d.b = mat(spv, qd, l * qd, grp * D_, 0, D_);
-        d.c = mat(value_rel_.data(), kvd, l * kvd, D_);
-        d.c2 = mat(g + qd + kvd, w3, l * w3, D_);
-        d.z = mat(z + qd + kvd, w3, l * w3, D_);
-        d.y = mat(v, w3, l * w3, D_);
-        if (bq) d.e_bias = mat(bq + qd + kvd, 0, 0, D_);
-        be_->run_gemm(d);
+        pxk_attn_rel_kv_desc kd{};
+        kd.n = n;
+        kd.l = l;
+        kd.heads = H_;
+        kd.kv_heads = Hkv_;
+        kd.head_dim = D_;
+        kd.eps = eps;
+        kd.causal = causal;
+        kd.rope = config_.use_rope;
+        kd.rope_half = config_.rope_layout == RoPELayout::RotateHalf;
+        kd.s = ra;
+        kd.p = p;
+        kd.q = q;
+        kd.ld_q = ldq;
+        kd.spv = spv;
+        kd.ld_spv = qd;
+        kd.k = k;
+        kd.ld_k = ldk;
+        kd.k_pre = y + qd;
+        kd.ld_k_pre = w3;
+        kd.v = v;
+        kd.ld_v = w3;
+        kd.z_k = z + qd;
+        kd.z_v = z + qd + kvd;
+        kd.ld_z = w3;
+        kd.bias_k = bq ? bq + qd : nullptr;
+        kd.bias_v = bq ? bq + qd + kvd : nullptr;
+        kd.cos_t = cos_.data();
+        kd.sin_t = sin_.data();
+        kd.key_rel = key_rel_.data();
+        kd.value_rel = value_rel_.data();
+        kd.ld_rel = kvd;
+        kd.g_k = g + qd;
+        kd.g_v = g + qd + kvd;
+        kd.ld_g = w3;
+        MI355XBackend::check(pxk_attention_relevance_kv(&kd, st), "MultiHeadAttentionModule::propagate_relevance (k/v)");
     }
     // 7. the three projections' input relevance in one GEMM: x * ([g_q | g_k | g_v] [Wq | Wk | Wv]^T).
     float* r_in = r_in_.ensure(be_, M * d_);

@@ -633,3 +633,213 @@ extern "C" int pxk_attention_relevance_q(const pxk_attn_rel_desc* d, void* strea
     hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), dyn, S(stream), a);
     return launched("pxk_attention_relevance_q");
 }
+
+// ---- key and value shares (pxk_attention_relevance_kv) ------------------------------------------------
+//
+// One workgroup owns 16 keys of one KV head and one group of 16 head dimensions, closed under the
+// RoPE pairing: dims 8j..8j+7 with their partners 8j+half.. under rotate-half, 16j..16j+15 for
+// adjacent pairs or no RoPE. Its products are D[key][dim] = sum over (query head of the group,
+// query row) of s[row][key] * Q[row][dim] and P[row][key] * s_pv[row][dim]: v_mfma_f32_16x16x4_f32
+// with A = one 16-key segment of 4 score rows and B = the matching 4 query rows' dims, so every
+// operand is a single coalesced float per lane. The (head, 4-row) items go round-robin over the
+// four waves, each with two accumulator pairs; the waves merge in LDS in wave order
+// (deterministic). Loads run two item groups ahead in two register sets, with addresses clamped
+// in range and rows past the end masked to 0 in the A operand, so the loop has no branch around a
+// load. Causal: rows before the block's first key hold only masked (zero) entries and are skipped.
+// Workgroups are ordered so each group of eight pairs a long causal key block with a short one,
+// and (with a multiple of 8 workgroups) a group shares one XCD and its L2.
+namespace {
+
+constexpr int kKvUnroll = 4;  // items per register set
+
+struct RelKvArgs {
+    const float* s;
+    const float* p;
+    const float* q;
+    const float* spv;
+    const float* k;
+    const float* k_pre;
+    const float* v;
+    const float* z_k;
+    const float* z_v;
+    const float* bias_k;
+    const float* bias_v;
+    const float* cos_t;
+    const float* sin_t;
+    float* key_rel;
+    float* value_rel;
+    float* g_k;
+    float* g_v;
+    int ld_q, ld_spv, ld_k, ld_k_pre, ld_v, ld_z, ld_rel, ld_g;
+    int n, l, heads, kv_heads, D, ngroups, nkb;
+    float eps;
+    int causal, rope, rope_half, remap;
+};
+
+// Head dimension held by MFMA column c of dim group dq, or -1.
+__device__ __forceinline__ int kv_dim(const RelKvArgs& a, int dq, int c) {
+    if (a.rope && a.rope_half) {
+        const int half = a.D / 2, i = 8 * dq + (c & 7);
+        return i < half ? (c < 8 ? i : i + half) : -1;
+    }
+    const int d = 16 * dq + c;
+    return d < a.D ? d : -1;
+}
+
+struct KvSet {
+    float s[kKvUnroll], p[kKvUnroll], q[kKvUnroll], v[kKvUnroll];
+    unsigned ok;  // bit u: the lane's row of item u is a real row
+};
+
+__device__ __forceinline__ void kv_load(KvSet& r, const RelKvArgs& a, int b, int hk, int grp, int wave, int step,
+                                        int total, int nq, int i_start, int key_c, int dim_c, int g4) {
+    r.ok = 0;
+#pragma unroll
+    for (int u = 0; u < kKvUnroll; ++u) {
+        const int item = wave + kWaves * (step * kKvUnroll + u);  // uniform across the wave
+        const bool it_ok = item < total;
+        const int itc = it_ok ? item : total - 1;
+        const int j = itc / nq, qi = itc - j * nq;
+        const int h = hk * grp + j;
+        const int i = i_start + 4 * qi + g4;
+        const int ic = i < a.l ? i : a.l - 1;
+        if (it_ok && i < a.l) r.ok |= 1u << u;
+        const int srow = ((b * a.heads + h) * a.l + ic) * a.l;
+        const int trow = b * a.l + ic;
+        r.s[u] = a.s[srow + key_c];
+        r.p[u] = a.p[srow + key_c];
+        r.q[u] = a.q[trow * a.ld_q + h * a.D + dim_c];
+        r.v[u] = a.spv[trow * a.ld_spv + h * a.D + dim_c];
+    }
+}
+
+__device__ __forceinline__ void kv_compute(const KvSet& r, f4* acck, f4* accv) {
+#pragma unroll
+    for (int u = 0; u < kKvUnroll; ++u) {
+        const bool ok = (r.ok >> u) & 1u;
+        const float as = ok ? r.s[u] : 0.0f, ap = ok ? r.p[u] : 0.0f;
+        acck[u & 1] = __builtin_amdgcn_mfma_f32_16x16x4f32(as, r.q[u], acck[u & 1], 0, 0, 0);
+        accv[u & 1] = __builtin_amdgcn_mfma_f32_16x16x4f32(ap, r.v[u], accv[u & 1], 0, 0, 0);
+    }
+}
+
+__global__ void __launch_bounds__(kThreads) attn_rel_kv_kernel(const RelKvArgs a) {
+    __shared__ float red[2][kWaves][16][17];  // per-wave k / v partial blocks [key][dim column]
+
+    const int lane = threadIdx.x & 63, g4 = lane >> 4, c = lane & 15;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    int id = blockIdx.x;
+    if (a.remap) id = (id % 8) * (gridDim.x / 8) + id / 8;
+    const int dq = id % a.ngroups;
+    const int t = id / a.ngroups;
+    const int tkb = t % a.nkb, bg = t / a.nkb;
+    const int kb = (tkb & 1) ? a.nkb - 1 - (tkb >> 1) : (tkb >> 1);  // long and short causal blocks alternate
+    const int hk = bg % a.kv_heads, b = bg / a.kv_heads;
+    const int grp = a.heads / a.kv_heads;
+    const int m0 = kb * 16;
+
+    const int key_c = min(m0 + c, a.l - 1);
+    const int dim = kv_dim(a, dq, c);
+    const int dim_c = dim < 0 ? 0 : dim;
+    const int i_start = a.causal ? m0 : 0;
+    const int nq = (a.l - i_start + 3) / 4;
+    const int total = grp * nq;
+    const int mine = total > wave ? (total - wave + kWaves - 1) / kWaves : 0;
+    const int steps = (mine + kKvUnroll - 1) / kKvUnroll;
+
+    f4 acck[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+    f4 accv[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+    KvSet s0, s1;
+    kv_load(s0, a, b, hk, grp, wave, 0, total, nq, i_start, key_c, dim_c, g4);
+    kv_load(s1, a, b, hk, grp, wave, 1, total, nq, i_start, key_c, dim_c, g4);
+    __builtin_amdgcn_sched_barrier(0);
+    for (int st = 0; st < steps; st += 2) {
+        kv_compute(s0, acck, accv);
+        kv_load(s0, a, b, hk, grp, wave, st + 2, total, nq, i_start, key_c, dim_c, g4);
+        __builtin_amdgcn_sched_barrier(0);
+        kv_compute(s1, acck, accv);
+        kv_load(s1, a, b, hk, grp, wave, st + 3, total, nq, i_start, key_c, dim_c, g4);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    const f4 kk = acck[0] + acck[1], vv = accv[0] + accv[1];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        red[0][wave][4 * g4 + r][c] = kk[r];
+        red[1][wave][4 * g4 + r][c] = vv[r];
+    }
+    __syncthreads();
+
+    // Epilogue: thread -> (key row kl, dim column nn) of the 16 x 16 block.
+    const int kl = threadIdx.x >> 4, nn = threadIdx.x & 15;
+    const int m = m0 + kl, d = kv_dim(a, dq, nn);
+    if (m >= a.l || d < 0) return;
+    auto sum4 = [&](int which, int col) {
+        return ((red[which][0][kl][col] + red[which][1][kl][col]) + red[which][2][kl][col]) + red[which][3][kl][col];
+    };
+    const int row = b * a.l + m, col = hk * a.D + d;
+    const float eps = a.eps;
+    float rk;
+    if (a.rope) {
+        const int D = a.D, half = D / 2;
+        const int i = a.rope_half ? (d < half ? d : d - half) : d / 2;
+        const int lo = a.rope_half ? i : 2 * i, hi = a.rope_half ? i + half : 2 * i + 1;
+        const int n_lo = a.rope_half ? (nn & 7) : (nn & ~1), n_hi = a.rope_half ? (nn | 8) : (nn | 1);
+        const float acc_lo = sum4(0, n_lo), acc_hi = sum4(0, n_hi);
+        const float* K = a.k + row * a.ld_k + hk * D;
+        const float y_lo = K[lo], y_hi = K[hi];
+        const float r_lo = y_lo * acc_lo, r_hi = y_hi * acc_hi;
+        const float cs = a.cos_t[m * half + i], sn = a.sin_t[m * half + i];
+        const float d0 = stab(y_lo, eps), d1 = stab(y_hi, eps);
+        const float xv = a.k_pre[row * a.ld_k_pre + col];
+        rk = 0.0f;
+        if (d == lo) {
+            rk += (xv * cs / d0) * r_lo;
+            rk += (xv * sn / d1) * r_hi;
+        } else {
+            rk += (xv * -sn / d0) * r_lo;
+            rk += (xv * cs / d1) * r_hi;
+        }
+    } else {
+        rk = a.k[row * a.ld_k + col] * sum4(0, nn);
+    }
+    if (a.key_rel) a.key_rel[row * a.ld_rel + col] = rk;
+    const float zk = a.bias_k ? a.z_k[row * a.ld_z + col] + a.bias_k[col] : a.z_k[row * a.ld_z + col];
+    a.g_k[row * a.ld_g + col] = rk / stab(zk, eps);
+    const float rv = a.v[row * a.ld_v + col] * sum4(1, nn);
+    if (a.value_rel) a.value_rel[row * a.ld_rel + col] = rv;
+    const float zv = a.bias_v ? a.z_v[row * a.ld_z + col] + a.bias_v[col] : a.z_v[row * a.ld_z + col];
+    a.g_v[row * a.ld_g + col] = rv / stab(zv, eps);
+}
+
+}  // namespace
+
+extern "C" int pxk_attention_relevance_kv(const pxk_attn_rel_kv_desc* d, void* stream) {
+    const int64_t n = d->n, l = d->l, H = d->heads, Hkv = d->kv_heads, D = d->head_dim;
+    if (n < 0 || l < 0 || H <= 0 || Hkv <= 0 || H % Hkv != 0 || D <= 0 || D > 1024 || (d->rope && D % 2 != 0))
+        return fail(PXK_ERR_INVALID, "pxk_attention_relevance_kv: bad sizes (heads a multiple of kv_heads, head_dim "
+                                     "up to 1024 and even with RoPE)");
+    if (!d->s || !d->p || !d->q || !d->spv || !d->k || !d->v || !d->z_k || !d->z_v || !d->g_k || !d->g_v ||
+        (d->rope && (!d->k_pre || !d->cos_t || !d->sin_t)))
+        return fail(PXK_ERR_INVALID, "pxk_attention_relevance_kv: a required operand is NULL");
+    if (d->ld_q < H * D || d->ld_spv < H * D || d->ld_k < Hkv * D || d->ld_v < Hkv * D || d->ld_z < Hkv * D ||
+        d->ld_g < Hkv * D || (d->rope && d->ld_k_pre < Hkv * D) ||
+        ((d->key_rel || d->value_rel) && d->ld_rel < Hkv * D))
+        return fail(PXK_ERR_INVALID, "pxk_attention_relevance_kv: row strides must hold every head");
+    if (n == 0 || l == 0) return PXK_OK;
+    const int64_t ngroups = (d->rope && d->rope_half) ? (D / 2 + 7) / 8 : (D + 15) / 16;
+    const int64_t nkb = (l + 15) / 16;
+    const int64_t blocks = n * Hkv * nkb * ngroups;
+    const int64_t lds_max = std::max({d->ld_q, d->ld_spv, d->ld_k, d->rope ? d->ld_k_pre : 0, d->ld_v, d->ld_z,
+                                      d->ld_rel, d->ld_g});
+    if (blocks > (int64_t{1} << 31) - 1 || n * H * l * l >= (int64_t{1} << 31) || n * l * lds_max >= (int64_t{1} << 31))
+        return fail(PXK_ERR_INVALID, "pxk_attention_relevance_kv: problem too large");
+    RelKvArgs a{d->s, d->p, d->q, d->spv, d->k, d->k_pre, d->v, d->z_k, d->z_v, d->bias_k, d->bias_v, d->cos_t,
+                d->sin_t, d->key_rel, d->value_rel, d->g_k, d->g_v, static_cast<int>(d->ld_q),
+                static_cast<int>(d->ld_spv), static_cast<int>(d->ld_k), static_cast<int>(d->rope ? d->ld_k_pre : 0),
+                static_cast<int>(d->ld_v), static_cast<int>(d->ld_z), static_cast<int>(d->ld_rel),
+                static_cast<int>(d->ld_g), static_cast<int>(n), static_cast<int>(l), static_cast<int>(H),
+                static_cast<int>(Hkv), static_cast<int>(D), static_cast<int>(ngroups), static_cast<int>(nkb), d->eps,
+                d->causal != 0, d->rope != 0, d->rope_half != 0, blocks % 8 == 0};
+    hipLaunchKernelGGL(attn_rel_kv_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0, S(stream), a);
+    return launched("pxk_attention_relevance_kv");
+}

@@ -122,6 +122,8 @@ def pxk():
                                       ctypes.POINTER(ctypes.c_int32)]
         lib.pxk_attention_relevance_q.restype = ctypes.c_int
         lib.pxk_attention_relevance_q.argtypes = [ctypes.POINTER(AttnRelDesc), c_vp]
+        lib.pxk_attention_relevance_kv.restype = ctypes.c_int
+        lib.pxk_attention_relevance_kv.argtypes = [ctypes.POINTER(AttnRelKvDesc), c_vp]
         lib.pxk_gemm_supported.restype = ctypes.c_int
         lib.pxk_gemm_supported.argtypes = [ctypes.c_int] * 4
         lib.pxk_reduce_partials.restype = ctypes.c_size_t
@@ -153,6 +155,18 @@ class AttnRelDesc(ctypes.Structure):
                 ("p", c_vp), ("raw", c_vp), ("s", c_vp), ("q", c_vp), ("ld_q", c_i64), ("q_pre", c_vp),
                 ("ld_q_pre", c_i64), ("z", c_vp), ("ld_z", c_i64), ("bias", c_vp), ("cos_t", c_vp), ("sin_t", c_vp),
                 ("g", c_vp), ("ld_g", c_i64)]
+
+
+class AttnRelKvDesc(ctypes.Structure):
+    """pxk_attn_rel_kv_desc."""
+
+    _fields_ = [("n", c_i64), ("l", c_i64), ("heads", c_i64), ("kv_heads", c_i64), ("head_dim", c_i64),
+                ("eps", ctypes.c_float), ("causal", ctypes.c_int32), ("rope", ctypes.c_int32),
+                ("rope_half", ctypes.c_int32), ("s", c_vp), ("p", c_vp), ("q", c_vp), ("ld_q", c_i64),
+                ("spv", c_vp), ("ld_spv", c_i64), ("k", c_vp), ("ld_k", c_i64), ("k_pre", c_vp),
+                ("ld_k_pre", c_i64), ("v", c_vp), ("ld_v", c_i64), ("z_k", c_vp), ("z_v", c_vp), ("ld_z", c_i64),
+                ("bias_k", c_vp), ("bias_v", c_vp), ("cos_t", c_vp), ("sin_t", c_vp), ("key_rel", c_vp),
+                ("value_rel", c_vp), ("ld_rel", c_i64), ("g_k", c_vp), ("g_v", c_vp), ("ld_g", c_i64)]
 
 
 def gemm(desc, stream=None):

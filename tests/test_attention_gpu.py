@@ -171,3 +171,90 @@ def test_fused_attention_relevance_matches_numpy(n, L, H, Hkv, D, causal, rope, 
     G.assert_close(got_s, want_s, 1e-4, "s")
     assert np.all(got_s[..., ~vis] == 0.0)
     G.assert_close(G.host(g_out), want_g, 1e-4, "g_q")
+
+
+def relevance_kv_reference(s, p, q, spv, k, k_pre, v, z_k, z_v, bk, bv, cos, sin, n, L, H, Hkv, D, eps, causal, rope,
+                           half):
+    """key_rel, value_rel, g_k, g_v (n*L, Hkv*D) in float64: the module's b-shares of the two
+    bilinear products (multihead_attention_module.cpp:446-447 and :435-436), sum_kv_groups
+    (:173-188), lrp_rope on the keys and the k/v projections' denominators."""
+    grp = H // Hkv
+    f = lambda a, heads: a.reshape(n, L, heads, D).transpose(0, 2, 1, 3).astype(np.float64)
+    q_h, spv_h = f(q, H), f(spv, H)
+    k_h, kp_h, v_h, zk_h, zv_h = f(k, Hkv), f(k_pre, Hkv), f(v, Hkv), f(z_k, Hkv), f(z_v, Hkv)
+    vis = np.tril(np.ones((L, L), bool)) if causal else np.ones((L, L), bool)
+    sm, pm = np.where(vis, s, 0.0), np.where(vis, p, 0.0)
+    sk = np.einsum("nhij,nhid->nhjd", sm, q_h).reshape(n, Hkv, grp, L, D).sum(axis=2)
+    pv = np.einsum("nhij,nhid->nhjd", pm, spv_h).reshape(n, Hkv, grp, L, D).sum(axis=2)
+    r = k_h * sk
+    if rope:
+        d = np.arange(D)
+        hf = D // 2
+        i = np.where(d < hf, d, d - hf) if half else d // 2
+        lo = i if half else 2 * i
+        hi = i + hf if half else 2 * i + 1
+        c, sn = cos[:, i][None, None], sin[:, i][None, None]
+        d0, d1 = stab(k_h[..., lo], eps), stab(k_h[..., hi], eps)
+        r_lo, r_hi = r[..., lo], r[..., hi]
+        r = np.where(d == lo, kp_h * c / d0 * r_lo + kp_h * sn / d1 * r_hi,
+                     kp_h * -sn / d0 * r_lo + kp_h * c / d1 * r_hi)
+    rv = v_h * pv
+    gk = r / stab(zk_h + (bk.reshape(1, Hkv, 1, D) if bk is not None else 0.0), eps)
+    gv = rv / stab(zv_h + (bv.reshape(1, Hkv, 1, D) if bv is not None else 0.0), eps)
+    t = lambda a: a.transpose(0, 2, 1, 3).reshape(n * L, Hkv * D)
+    return t(r), t(rv), t(gk), t(gv)
+
+
+@gpu
+@pytest.mark.parametrize("rope,half,bias", [(1, 1, 0), (1, 0, 1), (0, 0, 1)])
+@pytest.mark.parametrize("causal", [1, 0])
+@pytest.mark.parametrize("n,L,H,Hkv,D", [(1, 37, 4, 2, 16), (2, 64, 3, 1, 12), (1, 128, 9, 3, 64), (1, 40, 2, 2, 128),
+                                         (1, 512, 9, 3, 64), (2, 70, 4, 4, 20)])
+def test_fused_attention_kv_relevance_matches_numpy(n, L, H, Hkv, D, causal, rope, half, bias):
+    print("kv relevance n=%d L=%d H=%d Hkv=%d D=%d causal=%d rope=%d half=%d" % (n, L, H, Hkv, D, causal, rope, half),
+          flush=True)
+    qd, kvd = H * D, Hkv * D
+    eps = 1e-6
+    rs = np.random.RandomState(3 * L + D)
+    away = lambda *shape: (rs.uniform(0.5, 1.5, shape) * rs.choice([-1.0, 1.0], shape)).astype(np.float32)
+    vis = np.tril(np.ones((L, L), bool)) if causal else np.ones((L, L), bool)
+    s = np.where(vis, G.uniform((n, H, L, L), 1), 0.0).astype(np.float32)  # zeros where masked, as written upstream
+    p = np.where(vis, G.uniform((n, H, L, L), 2, 0.0, 1.0), 0.0).astype(np.float32)
+    q, spv = G.uniform((n * L, qd), 3), G.uniform((n * L, qd), 4)
+    k, k_pre, v = away(n * L, kvd), G.uniform((n * L, kvd), 6), G.uniform((n * L, kvd), 7)
+    z_k, z_v = away(n * L, kvd), away(n * L, kvd)
+    bk, bv = ((G.uniform((kvd,), 8) * 0.1, G.uniform((kvd,), 9) * 0.1) if bias else (None, None))
+    ang = np.arange(L)[:, None] * (10000.0 ** (-np.arange(D // 2) * 2.0 / D))[None, :]
+    cos, sin = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+    want = relevance_kv_reference(s.astype(np.float64), p.astype(np.float64), q, spv, k, k_pre, v, z_k, z_v,
+                                  bk, bv, cos.astype(np.float64), sin.astype(np.float64), n, L, H, Hkv, D, eps,
+                                  causal, rope, half)
+    dv = {key: G.dev(a) for key, a in dict(s=s, p=p, q=q, spv=spv, k=k, k_pre=k_pre, v=v, z_k=z_k, z_v=z_v, cos=cos,
+                                            sin=sin).items()}
+    outs = [G.empty((n * L, kvd)) for _ in range(4)]
+    d = N.AttnRelKvDesc()
+    d.n, d.l, d.heads, d.kv_heads, d.head_dim = n, L, H, Hkv, D
+    d.eps, d.causal, d.rope, d.rope_half = eps, causal, rope, half
+    d.s, d.p = G.ptr(dv["s"]).value, G.ptr(dv["p"]).value
+    d.q, d.ld_q, d.spv, d.ld_spv = G.ptr(dv["q"]).value, qd, G.ptr(dv["spv"]).value, qd
+    d.k, d.ld_k, d.k_pre, d.ld_k_pre = G.ptr(dv["k"]).value, kvd, G.ptr(dv["k_pre"]).value, kvd
+    d.v, d.ld_v = G.ptr(dv["v"]).value, kvd
+    d.z_k, d.z_v, d.ld_z = G.ptr(dv["z_k"]).value, G.ptr(dv["z_v"]).value, kvd
+    d.bias_k = G.ptr(G.dev(bk)).value if bias else None
+    d.bias_v = G.ptr(G.dev(bv)).value if bias else None
+    d.cos_t, d.sin_t = G.ptr(dv["cos"]).value, G.ptr(dv["sin"]).value
+    d.key_rel, d.value_rel, d.ld_rel = G.ptr(outs[0]).value, G.ptr(outs[1]).value, kvd
+    d.g_k, d.g_v, d.ld_g = G.ptr(outs[2]).value, G.ptr(outs[3]).value, kvd
+    assert N.pxk().pxk_attention_relevance_kv(ctypes.byref(d), G.stream()) == 0, N.pxk().pxk_last_error()
+    for got, ref, name in zip(outs, want, ("key_rel", "value_rel", "g_k", "g_v")):
+        G.assert_close(G.host(got), ref, 1e-4, name)
+
+
+def test_fused_attention_kv_relevance_rejects_bad_descs():
+    """CPU-side validation: nothing is launched for a bad descriptor."""
+    d = N.AttnRelKvDesc()
+    d.n, d.l, d.heads, d.kv_heads, d.head_dim = 1, 8, 3, 2, 16
+    assert N.pxk().pxk_attention_relevance_kv(ctypes.byref(d), None) == 1  # heads not a multiple of kv_heads
+    d.heads = 4
+    assert N.pxk().pxk_attention_relevance_kv(ctypes.byref(d), None) == 1  # NULL operands
+    assert b"NULL" in N.pxk().pxk_last_error()
