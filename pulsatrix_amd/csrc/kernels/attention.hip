@@ -27,6 +27,7 @@
 // in LDS for the row sums and for the contiguous store of s (the key share reads it).
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 
 #include "common.hpp"
 
@@ -650,7 +651,6 @@ extern "C" int pxk_attention_relevance_q(const pxk_attn_rel_desc* d, void* strea
 // and (with a multiple of 8 workgroups) a group shares one XCD and its L2.
 namespace {
 
-constexpr int kKvUnroll = 4;  // items per register set
 
 struct RelKvArgs {
     const float* s;
@@ -686,17 +686,19 @@ __device__ __forceinline__ int kv_dim(const RelKvArgs& a, int dq, int c) {
     return d < a.D ? d : -1;
 }
 
+template <int U>
 struct KvSet {
-    float s[kKvUnroll], p[kKvUnroll], q[kKvUnroll], v[kKvUnroll];
+    float s[U], p[U], q[U], v[U];
     unsigned ok;  // bit u: the lane's row of item u is a real row
 };
 
-__device__ __forceinline__ void kv_load(KvSet& r, const RelKvArgs& a, int b, int hk, int grp, int wave, int step,
+template <int NW, int U>
+__device__ __forceinline__ void kv_load(KvSet<U>& r, const RelKvArgs& a, int b, int hk, int grp, int wave, int step,
                                         int total, int nq, int i_start, int key_c, int dim_c, int g4) {
     r.ok = 0;
 #pragma unroll
-    for (int u = 0; u < kKvUnroll; ++u) {
-        const int item = wave + kWaves * (step * kKvUnroll + u);  // uniform across the wave
+    for (int u = 0; u < U; ++u) {
+        const int item = wave + NW * (step * U + u);  // uniform across the wave
         const bool it_ok = item < total;
         const int itc = it_ok ? item : total - 1;
         const int j = itc / nq, qi = itc - j * nq;
@@ -713,9 +715,10 @@ __device__ __forceinline__ void kv_load(KvSet& r, const RelKvArgs& a, int b, int
     }
 }
 
-__device__ __forceinline__ void kv_compute(const KvSet& r, f4* acck, f4* accv) {
+template <int U>
+__device__ __forceinline__ void kv_compute(const KvSet<U>& r, f4* acck, f4* accv) {
 #pragma unroll
-    for (int u = 0; u < kKvUnroll; ++u) {
+    for (int u = 0; u < U; ++u) {
         const bool ok = (r.ok >> u) & 1u;
         const float as = ok ? r.s[u] : 0.0f, ap = ok ? r.p[u] : 0.0f;
         acck[u & 1] = __builtin_amdgcn_mfma_f32_16x16x4f32(as, r.q[u], acck[u & 1], 0, 0, 0);
@@ -723,8 +726,10 @@ __device__ __forceinline__ void kv_compute(const KvSet& r, f4* acck, f4* accv) {
     }
 }
 
-__global__ void __launch_bounds__(kThreads) attn_rel_kv_kernel(const RelKvArgs a) {
-    __shared__ float red[2][kWaves][16][17];  // per-wave k / v partial blocks [key][dim column]
+// NW waves per workgroup, U items per register set.
+template <int NW, int U>
+__global__ void __launch_bounds__(NW * kWave) attn_rel_kv_kernel(const RelKvArgs a) {
+    __shared__ float red[2][NW][16][17];  // per-wave k / v partial blocks [key][dim column]
 
     const int lane = threadIdx.x & 63, g4 = lane >> 4, c = lane & 15;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -744,21 +749,21 @@ __global__ void __launch_bounds__(kThreads) attn_rel_kv_kernel(const RelKvArgs a
     const int i_start = a.causal ? m0 : 0;
     const int nq = (a.l - i_start + 3) / 4;
     const int total = grp * nq;
-    const int mine = total > wave ? (total - wave + kWaves - 1) / kWaves : 0;
-    const int steps = (mine + kKvUnroll - 1) / kKvUnroll;
+    const int mine = total > wave ? (total - wave + NW - 1) / NW : 0;
+    const int steps = (mine + U - 1) / U;
 
     f4 acck[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
     f4 accv[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
-    KvSet s0, s1;
-    kv_load(s0, a, b, hk, grp, wave, 0, total, nq, i_start, key_c, dim_c, g4);
-    kv_load(s1, a, b, hk, grp, wave, 1, total, nq, i_start, key_c, dim_c, g4);
+    KvSet<U> s0, s1;
+    kv_load<NW, U>(s0, a, b, hk, grp, wave, 0, total, nq, i_start, key_c, dim_c, g4);
+    kv_load<NW, U>(s1, a, b, hk, grp, wave, 1, total, nq, i_start, key_c, dim_c, g4);
     __builtin_amdgcn_sched_barrier(0);
     for (int st = 0; st < steps; st += 2) {
         kv_compute(s0, acck, accv);
-        kv_load(s0, a, b, hk, grp, wave, st + 2, total, nq, i_start, key_c, dim_c, g4);
+        kv_load<NW, U>(s0, a, b, hk, grp, wave, st + 2, total, nq, i_start, key_c, dim_c, g4);
         __builtin_amdgcn_sched_barrier(0);
         kv_compute(s1, acck, accv);
-        kv_load(s1, a, b, hk, grp, wave, st + 3, total, nq, i_start, key_c, dim_c, g4);
+        kv_load<NW, U>(s1, a, b, hk, grp, wave, st + 3, total, nq, i_start, key_c, dim_c, g4);
         __builtin_amdgcn_sched_barrier(0);
     }
     const f4 kk = acck[0] + acck[1], vv = accv[0] + accv[1];
@@ -770,11 +775,15 @@ __global__ void __launch_bounds__(kThreads) attn_rel_kv_kernel(const RelKvArgs a
     __syncthreads();
 
     // Epilogue: thread -> (key row kl, dim column nn) of the 16 x 16 block.
+    if (threadIdx.x >= 256) return;
     const int kl = threadIdx.x >> 4, nn = threadIdx.x & 15;
     const int m = m0 + kl, d = kv_dim(a, dq, nn);
     if (m >= a.l || d < 0) return;
     auto sum4 = [&](int which, int col) {
-        return ((red[which][0][kl][col] + red[which][1][kl][col]) + red[which][2][kl][col]) + red[which][3][kl][col];
+        float v = red[which][0][kl][col];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) v += red[which][w][kl][col];
+        return v;
     };
     const int row = b * a.l + m, col = hk * a.D + d;
     const float eps = a.eps;
@@ -840,6 +849,15 @@ extern "C" int pxk_attention_relevance_kv(const pxk_attn_rel_kv_desc* d, void* s
                 static_cast<int>(d->ld_g), static_cast<int>(n), static_cast<int>(l), static_cast<int>(H),
                 static_cast<int>(Hkv), static_cast<int>(D), static_cast<int>(ngroups), static_cast<int>(nkb), d->eps,
                 d->causal != 0, d->rope != 0, d->rope_half != 0, blocks % 8 == 0};
-    hipLaunchKernelGGL(attn_rel_kv_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0, S(stream), a);
+    static const int variant = getenv("PXK_KV_VARIANT") ? atoi(getenv("PXK_KV_VARIANT")) : 0;
+    const dim3 grid(static_cast<unsigned>(blocks));
+    switch (variant) {
+        case 1: hipLaunchKernelGGL((attn_rel_kv_kernel<4, 8>), grid, dim3(256), 0, S(stream), a); break;
+        case 2: hipLaunchKernelGGL((attn_rel_kv_kernel<8, 4>), grid, dim3(512), 0, S(stream), a); break;
+        case 3: hipLaunchKernelGGL((attn_rel_kv_kernel<8, 8>), grid, dim3(512), 0, S(stream), a); break;
+        case 4: hipLaunchKernelGGL((attn_rel_kv_kernel<16, 4>), grid, dim3(1024), 0, S(stream), a); break;
+        case 5: hipLaunchKernelGGL((attn_rel_kv_kernel<16, 2>), grid, dim3(1024), 0, S(stream), a); break;
+        default: hipLaunchKernelGGL((attn_rel_kv_kernel<4, 4>), grid, dim3(256), 0, S(stream), a); break;
+    }
     return launched("pxk_attention_relevance_kv");
 }
