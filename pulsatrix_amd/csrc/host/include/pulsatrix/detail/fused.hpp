@@ -63,4 +63,29 @@ inline const float* rule_bias(const float* bias, bool use_bias, bool bias_in_den
     return (use_bias && bias_in_denominator) ? bias : nullptr;
 }
 
+/** @brief The epsilon split of a residual sum s = a + b (lrp_residual_split, lrp_math.hpp:33-38)
+ *         requested from the GEMM that produces the relevance of s: with a request, that GEMM
+ *         writes r_a = (a / stab(s)) r and r_b = (b / stab(s)) r (PXK_EPI_MUL_X_SPLIT) instead of r.
+ *         s must be the forward's stored a + b. */
+struct ResidualSplit {
+    const float* a = nullptr;
+    const float* b = nullptr;
+    const float* s = nullptr;
+    float* r_a = nullptr;
+    float* r_b = nullptr;
+    [[nodiscard]] bool requested() const noexcept { return r_a != nullptr; }
+};
+
+/** @brief Turns a MUL_X relevance GEMM (C = X * acc [+ Y], row stride ld) into its split form. */
+inline void apply_split(pxk_gemm_desc& d, const ResidualSplit& sp, int64_t ld, float eps) {
+    if (!sp.requested()) return;
+    d.epilogue = PXK_EPI_MUL_X_SPLIT;
+    d.eps = eps;
+    d.c = mat(sp.r_a, ld);
+    d.c2 = mat(sp.r_b, ld);
+    d.z2 = mat(sp.a, ld);
+    d.z3 = mat(sp.b, ld);
+    d.w = mat(sp.s, ld);
+}
+
 }  // namespace pulsatrix::detail

@@ -42,7 +42,8 @@ public:
     /** @brief Fused-path forward over `rows` rows of x (kept by pointer until the next call). */
     const float* run_forward(const float* x, int64_t rows);
     /** @brief Fused-path relevance; `add` (nullable) is summed into the result. */
-    const float* run_relevance(const float* r, const LRPRuleConfig& config, const float* add = nullptr);
+    const float* run_relevance(const float* r, const LRPRuleConfig& config, const float* add = nullptr,
+                               const detail::ResidualSplit& split = {});
 
 protected:
     Tensor forward_impl(const Tensor& input) override;

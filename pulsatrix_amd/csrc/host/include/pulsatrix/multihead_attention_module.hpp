@@ -68,7 +68,8 @@ public:
     const float* run_forward(const float* x, int64_t n, int64_t l, const float* resid = nullptr,
                              float* resid_out = nullptr);
     /** @brief Fused-path relevance; `add` (nullable) is summed into the input relevance. */
-    const float* run_relevance(const float* relevance_out, const LRPRuleConfig& config, const float* add = nullptr);
+    const float* run_relevance(const float* relevance_out, const LRPRuleConfig& config, const float* add = nullptr,
+                               const detail::ResidualSplit& split = {});
     /** @brief The attention output (after the output projection's bias) of the last forward. */
     [[nodiscard]] const float* output() const noexcept;
 

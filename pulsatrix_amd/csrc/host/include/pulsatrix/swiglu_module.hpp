@@ -26,7 +26,8 @@ public:
     [[nodiscard]] LinearModule& down_proj() { return down_proj_; }
 
     const float* run_forward(const float* x, int64_t rows, const float* resid = nullptr, float* resid_out = nullptr);
-    const float* run_relevance(const float* relevance_out, const LRPRuleConfig& config, const float* add = nullptr);
+    const float* run_relevance(const float* relevance_out, const LRPRuleConfig& config, const float* add = nullptr,
+                               const detail::ResidualSplit& split = {});
     [[nodiscard]] const float* output() const noexcept;
 
 protected:

@@ -17,7 +17,8 @@ public:
     [[nodiscard]] Tensor propagate_relevance(const Tensor& relevance_out, const LRPRuleConfig& config) override;
 
     const float* run_forward(const float* x, int64_t rows);
-    const float* run_relevance(const float* relevance_out, const LRPRuleConfig& config);
+    const float* run_relevance(const float* relevance_out, const LRPRuleConfig& config,
+                               const detail::ResidualSplit& split = {});
     [[nodiscard]] const float* logits() const noexcept { return logits_.data(); }
 
 protected:

@@ -37,6 +37,13 @@ public:
     /** @brief Fused-path forward; x must stay valid until the relevance pass. Returns y2. */
     const float* run_forward(const float* x, int64_t n, int64_t l);
     const float* run_relevance(const float* relevance_out, const LRPRuleConfig& config);
+    /** @brief The epsilon split of this block's output y2 = y1 + mlp, for the GEMM that produces the
+     *         block's output relevance to perform into this block's buffers. Valid after run_forward. */
+    detail::ResidualSplit output_split();
+    /** @brief Relevance pass once the producer applied output_split(); `below` is the split the block
+     *         underneath asks for (its output is this block's input), or none. Returns the input
+     *         relevance when `below` is empty, else nullptr. */
+    const float* run_relevance_split(const LRPRuleConfig& config, const detail::ResidualSplit& below);
 
 protected:
     Tensor forward_impl(const Tensor& input) override;

@@ -222,7 +222,7 @@ void MultiHeadAttentionModule::run_attention_unfused(const float* q, int64_t ldq
 }
 
 const float* MultiHeadAttentionModule::run_relevance(const float* relevance_out, const LRPRuleConfig& config,
-                                                     const float* add) {
+                                                     const float* add, const detail::ResidualSplit& split) {
     require_epsilon_rule(config, "MultiHeadAttentionModule");
     if (x_ == nullptr)
         throw std::logic_error("MultiHeadAttentionModule::propagate_relevance: called before any forward()");
@@ -353,10 +353,11 @@ const float* MultiHeadAttentionModule::run_relevance(const float* relevance_out,
         d.c = mat(r_in, d_);
         d.x = mat(x_, d_);
         if (add) d.y = mat(add, d_);
+        detail::apply_split(d, split, d_, eps);
         be_->run_gemm(d);
     }
     has_relevance_ = true;
-    return r_in;
+    return split.requested() ? nullptr : r_in;
 }
 
 // Steps 2-4 of run_relevance as GEMM and row-kernel launches: head_dim outside

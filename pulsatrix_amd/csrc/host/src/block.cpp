@@ -86,7 +86,8 @@ const float* SwiGLUModule::run_forward(const float* x, int64_t rows, const float
     return dy;
 }
 
-const float* SwiGLUModule::run_relevance(const float* relevance_out, const LRPRuleConfig& config, const float* add) {
+const float* SwiGLUModule::run_relevance(const float* relevance_out, const LRPRuleConfig& config, const float* add,
+                                         const detail::ResidualSplit& split) {
     require_epsilon_rule(config, "SwiGLUModule");
     if (x_ == nullptr) throw std::logic_error("SwiGLUModule::propagate_relevance: called before any forward()");
     const bool bid = config.epsilon_bias_in_denominator;
@@ -127,9 +128,10 @@ const float* SwiGLUModule::run_relevance(const float* relevance_out, const LRPRu
         d.c = mat(r_in, d_);
         d.x = mat(x_, d_);
         if (add) d.y = mat(add, d_);
+        detail::apply_split(d, split, d_, config.epsilon);
         be_->run_gemm(d);
     }
-    return r_in;
+    return split.requested() ? nullptr : r_in;
 }
 
 Tensor SwiGLUModule::forward_impl(const Tensor& input) {
@@ -180,6 +182,22 @@ const float* TransformerBlock::run_forward(const float* x, int64_t n, int64_t l)
     mha_.run_forward(norm1_.run_forward(x, M), n, l, x, y1);        // y1 = x + attn(norm1(x))
     swiglu_.run_forward(norm2_.run_forward(y1, M), M, y1, y2);       // y2 = y1 + mlp(norm2(y1))
     return y2;
+}
+
+detail::ResidualSplit TransformerBlock::output_split() {
+    const int64_t n = N_ * L_ * d_;
+    return {y1_.data(), swiglu_.output(), y2_.data(), r_y1d_.ensure(be_, n), r_ffn_.ensure(be_, n)};
+}
+
+const float* TransformerBlock::run_relevance_split(const LRPRuleConfig& config, const detail::ResidualSplit& below) {
+    if (x_ == nullptr) throw std::logic_error("TransformerBlock::propagate_relevance: called before any forward()");
+    const int64_t n = N_ * L_ * d_;
+    // The producer of this block's output relevance wrote its two shares (output_split). The MLP's
+    // last GEMM writes the split one level up (y1 = x + attn) the same way.
+    float* rxd = r_xd_.ensure(be_, n);
+    float* rattn = r_attn_.ensure(be_, n);
+    swiglu_.run_relevance(r_ffn_.data(), config, r_y1d_.data(), {x_, mha_.output(), y1_.data(), rxd, rattn});
+    return mha_.run_relevance(rattn, config, rxd, below);
 }
 
 const float* TransformerBlock::run_relevance(const float* relevance_out, const LRPRuleConfig& config) {

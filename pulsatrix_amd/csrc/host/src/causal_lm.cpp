@@ -72,9 +72,16 @@ const float* CausalLM::run_forward(const float* ids, int64_t n, int64_t l) {
 
 const float* CausalLM::run_relevance(const float* seed, const LRPRuleConfig& config) {
     if (N_ == 0) throw std::logic_error("CausalLM::propagate_relevance_by_layer: called before any forward()");
-    const float* r = tied_head_ ? tied_head_->run_relevance(seed, config) : lm_head_->run_relevance(seed, config);
-    // The final RMSNorm passes relevance through unchanged (rms_norm_module.cpp:101-111).
-    for (size_t i = layers_.size(); i-- > 0;) r = layers_[i]->run_relevance(r, config);
+    // The final RMSNorm passes relevance through unchanged (rms_norm_module.cpp:101-111). Each
+    // residual sum's epsilon split (lrp_residual_split) runs inside the GEMM that produces the
+    // sum's relevance: the head's for the top block's output, each block's q/k/v GEMM for the
+    // output of the block below.
+    const size_t nl = layers_.size();
+    const detail::ResidualSplit top = nl > 0 ? layers_.back()->output_split() : detail::ResidualSplit{};
+    const float* r = tied_head_ ? tied_head_->run_relevance(seed, config, top)
+                                : lm_head_->run_relevance(seed, config, nullptr, top);
+    for (size_t i = nl; i-- > 0;)
+        r = layers_[i]->run_relevance_split(config, i > 0 ? layers_[i - 1]->output_split() : detail::ResidualSplit{});
     r_embed_ = r;
     return r;
 }

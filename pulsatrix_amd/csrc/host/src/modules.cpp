@@ -81,7 +81,8 @@ const float* LinearModule::run_forward(const float* x, int64_t rows) {
     return y;
 }
 
-const float* LinearModule::run_relevance(const float* r, const LRPRuleConfig& config, const float* add) {
+const float* LinearModule::run_relevance(const float* r, const LRPRuleConfig& config, const float* add,
+                                         const detail::ResidualSplit& split) {
     require_epsilon_rule(config, "LinearModule");
     if (x_ == nullptr) throw std::logic_error("LinearModule::propagate_relevance: called before any forward()");
     float* out = r_in_.ensure(be_, rows_ * in_);
@@ -98,8 +99,9 @@ const float* LinearModule::run_relevance(const float* r, const LRPRuleConfig& co
     d.c = mat(out, in_);
     d.x = mat(x_, in_);
     if (add) d.y = mat(add, in_);
+    detail::apply_split(d, split, in_, config.epsilon);
     be_->run_gemm(d);
-    return out;
+    return split.requested() ? nullptr : out;
 }
 
 Tensor LinearModule::forward_impl(const Tensor& input) {
@@ -229,7 +231,8 @@ const float* TiedLMHeadModule::run_forward(const float* x, int64_t rows) {
     return logits;
 }
 
-const float* TiedLMHeadModule::run_relevance(const float* relevance_out, const LRPRuleConfig& config) {
+const float* TiedLMHeadModule::run_relevance(const float* relevance_out, const LRPRuleConfig& config,
+                                             const detail::ResidualSplit& split) {
     require_epsilon_rule(config, "TiedLMHeadModule");
     if (x_ == nullptr) throw std::logic_error("TiedLMHeadModule::propagate_relevance: called before any forward()");
     const int64_t V = embedding_.num_embeddings(), D = embedding_.embedding_dim();
@@ -244,8 +247,9 @@ const float* TiedLMHeadModule::run_relevance(const float* relevance_out, const L
     d.b = mat(embedding_.weight().data(), D);
     d.c = mat(out, D);
     d.x = mat(x_, D);
+    detail::apply_split(d, split, D, config.epsilon);
     be_->run_gemm(d);
-    return out;
+    return split.requested() ? nullptr : out;
 }
 
 Tensor TiedLMHeadModule::forward_impl(const Tensor& input) {

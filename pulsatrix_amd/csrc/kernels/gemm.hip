@@ -194,6 +194,20 @@ __device__ void epilogue_rows(const float* Cs, int ldc, int64_t m0, int64_t n0, 
             f4 v = ld4(X + m * g.x.ld + n, vec, cnt) * acc;
             if (Y) v = ld4(Y + m * g.y.ld + n, vec, cnt) + v;
             st4(C + m * g.c.ld + n, v, vec, cnt);
+        } else if constexpr (EPI == PXK_EPI_MUL_X_SPLIT) {
+            f4 v = ld4(X + m * g.x.ld + n, vec, cnt) * acc;
+            if (Y) v = ld4(Y + m * g.y.ld + n, vec, cnt) + v;
+            const f4 sa = ld4(Z2 + m * g.z2.ld + n, vec, cnt), sb = ld4(Z3 + m * g.z3.ld + n, vec, cnt);
+            const f4 sum = ld4(W + m * g.w.ld + n, vec, cnt);
+            f4 ra, rb;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {  // ResidualSplitF's expression, with the stored sum
+                const float denom = stab(sum[j], eps);
+                ra[j] = (sa[j] / denom) * v[j];
+                rb[j] = (sb[j] / denom) * v[j];
+            }
+            st4(C + m * g.c.ld + n, ra, vec, cnt);
+            st4(C2 + m * g.c2.ld + n, rb, vec, cnt);
         } else if constexpr (EPI == PXK_EPI_SPV) {
             const f4 o = ld4(X + m * g.x.ld + n, vec, cnt);
             f4 v;
@@ -836,6 +850,9 @@ const Entry kTable[] = {
     PXK_GEMM_ENTRY(0, 0, PXK_PRO_NONE, PXK_EPI_VALUE_REL),
     PXK_GEMM_ENTRY(1, 0, PXK_PRO_NONE, PXK_EPI_VALUE_REL),
     PXK_GEMM_ENTRY(0, 1, PXK_PRO_DIV_STAB, PXK_EPI_SWIGLU_REL),
+    PXK_GEMM_ENTRY(0, 1, PXK_PRO_NONE, PXK_EPI_MUL_X_SPLIT),
+    PXK_GEMM_ENTRY(0, 0, PXK_PRO_DIV_STAB, PXK_EPI_MUL_X_SPLIT),
+    PXK_GEMM_ENTRY(0, 1, PXK_PRO_DIV_STAB, PXK_EPI_MUL_X_SPLIT),
 };
 
 template <class C>
@@ -956,6 +973,9 @@ int plan(const pxk_gemm_desc* d, Plan* p) {
         return fail(PXK_ERR_INVALID, "pxk_gemm: SWIGLU_REL needs Y and C2");
     if (epi == PXK_EPI_SWIGLU_REL && (d->w.ptr == nullptr || d->z2.ptr == nullptr || d->z3.ptr == nullptr))
         return fail(PXK_ERR_INVALID, "pxk_gemm: SWIGLU_REL needs W, Z2 and Z3");
+    if (epi == PXK_EPI_MUL_X_SPLIT && (d->x.ptr == nullptr || d->c2.ptr == nullptr || d->w.ptr == nullptr ||
+                                       d->z2.ptr == nullptr || d->z3.ptr == nullptr))
+        return fail(PXK_ERR_INVALID, "pxk_gemm: MUL_X_SPLIT needs X, C2, W, Z2 and Z3");
     if (d->prologue == PXK_PRO_DIV_STAB && d->z.ptr == nullptr)
         return fail(PXK_ERR_INVALID, "pxk_gemm: the DIV_STAB prologue needs Z");
     if (d->prologue == PXK_PRO_DIV_STAB && (epi == PXK_EPI_ROPE_REL || epi == PXK_EPI_VALUE_REL))

@@ -24,6 +24,8 @@ COMBOS = [
     (0, 0, N.PRO_DIV_STAB, N.EPI_MUL_X), (0, 1, N.PRO_DIV_STAB, N.EPI_MUL_X), (0, 1, N.PRO_DIV_STAB, N.EPI_SPV),
     (0, 0, N.PRO_NONE, N.EPI_ROPE_REL), (1, 0, N.PRO_NONE, N.EPI_ROPE_REL), (0, 0, N.PRO_NONE, N.EPI_VALUE_REL),
     (1, 0, N.PRO_NONE, N.EPI_VALUE_REL), (0, 1, N.PRO_DIV_STAB, N.EPI_SWIGLU_REL),
+    (0, 1, N.PRO_NONE, N.EPI_MUL_X_SPLIT), (0, 0, N.PRO_DIV_STAB, N.EPI_MUL_X_SPLIT),
+    (0, 1, N.PRO_DIV_STAB, N.EPI_MUL_X_SPLIT),
 ]
 TILES = [N.TILE_128x128, N.TILE_64x64, N.TILE_32x64, N.TILE_32x32, N.TILE_32x64_DIRECT, N.TILE_32x32_DIRECT]
 TILE_BN = {N.TILE_128x128: 128, N.TILE_64x64: 64, N.TILE_32x64: 64, N.TILE_32x32: 32, N.TILE_32x64_DIRECT: 64,
@@ -65,6 +67,10 @@ def expected(epi, acc, t, D, half_layout):
     if epi == N.EPI_VALUE_REL:
         r = Y * acc
         return {"c": r, "c2": r / stab(Z + eb)}
+    if epi == N.EPI_MUL_X_SPLIT:
+        r = Y + X * acc
+        den = stab(W)
+        return {"c": (Z2 / den) * r, "c2": (Z3 / den) * r}
     if epi == N.EPI_SWIGLU_REL:
         c = Y * W
         rg = (c / (2 * c + EPS * np.where(c >= 0, 1.0, -1.0))) * (X * acc)
