@@ -27,7 +27,6 @@
 // in LDS for the row sums and for the contiguous store of s (the key share reads it).
 #include <algorithm>
 #include <cmath>
-#include <cstdlib>
 
 #include "common.hpp"
 
@@ -73,7 +72,9 @@ __global__ void __launch_bounds__(kThreads) attn_fwd_kernel(const FwdArgs a) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: the tile loop is scalar
     const int l = a.l, D = a.D, ld = a.lds_ld;
     const int nrb = (l + 15) / 16;
-    const int rb = blockIdx.x % nrb, bh = blockIdx.x / nrb;
+    // Long causal rows first, heads fastest: the heaviest blocks start first and spread over the CUs.
+    const int nbh = a.n * a.heads;
+    const int rb = nrb - 1 - static_cast<int>(blockIdx.x) / nbh, bh = static_cast<int>(blockIdx.x) % nbh;
     const int h = bh % a.heads, b = bh / a.heads;
     const int hk = h / (a.heads / a.kv_heads);
     const int i0 = rb * 16, row = i0 + c;
@@ -85,8 +86,10 @@ __global__ void __launch_bounds__(kThreads) attn_fwd_kernel(const FwdArgs a) {
         const float* qp = a.q + (static_cast<int64_t>(b) * l + (row_ok ? row : l - 1)) * a.ldq + h * D;
 #pragma unroll
         for (int t = 0; t < DT; ++t) {
+            // Unconditional loads (clamped column), then a zero factor for columns past head_dim:
+            // no branch around the loads, so the key loop inherits no pending-load state.
             const int d0 = 16 * t + 4 * g;
-            qf[t] = (row_ok && d0 < D) ? *reinterpret_cast<const f4*>(qp + d0) : f4{0.f, 0.f, 0.f, 0.f};
+            qf[t] = *reinterpret_cast<const f4*>(qp + min(d0, D - 4)) * (d0 < D ? 1.0f : 0.0f);
         }
     }
     const float* kbase = a.k + static_cast<int64_t>(b) * l * a.ldk + hk * D;
@@ -141,7 +144,9 @@ __global__ void __launch_bounds__(kThreads) attn_fwd_kernel(const FwdArgs a) {
         __builtin_amdgcn_sched_barrier(0);
         // s[r] = raw score of (row, key0 + 4 g + r), kept in LDS for the last pass.
         const int kk0 = key0 + 4 * g;
-        if (kt < ntile) *reinterpret_cast<f4*>(sc + c * ld + kk0) = s;
+        // A tile past the last one (the second of a pair) lands on column block ntile, inside the
+        // LDS row and past every visible key of this block: written, never read. No branch.
+        *reinterpret_cast<f4*>(sc + c * ld + 16 * min(kt, ntile) + 4 * g) = s;
         float x[4];
         bool valid[4];
         float mt = -INFINITY;
@@ -183,6 +188,9 @@ __global__ void __launch_bounds__(kThreads) attn_fwd_kernel(const FwdArgs a) {
     load_v(0, wave);
     load_k(1, wave + kWaves);
     load_v(1, wave + kWaves);
+    // Enter the loop with nothing in flight: the loop head's wait then covers only the loop's own
+    // reloads (two tiles ahead) instead of draining every load at each iteration.
+    __builtin_amdgcn_s_waitcnt(0);
     for (int kt = wave; kt < ntile; kt += 2 * kWaves) {
         tile(0, kt);
         tile(1, kt + kWaves);
@@ -299,7 +307,9 @@ __global__ void __launch_bounds__(kThreads) attn_rel_q_kernel(const RelArgs a) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: the tile loops are scalar
     const int l = a.l, D = a.D, ld = a.lds_ld;
     const int nrb = (l + 15) / 16;
-    const int rb = blockIdx.x % nrb, bh = blockIdx.x / nrb;
+    // Long causal rows first, heads fastest: the heaviest blocks start first and spread over the CUs.
+    const int nbh = a.n * a.heads;
+    const int rb = nrb - 1 - static_cast<int>(blockIdx.x) / nbh, bh = static_cast<int>(blockIdx.x) % nbh;
     const int h = bh % a.heads, b = bh / a.heads;
     const int hk = h / (a.heads / a.kv_heads);
     const int i0 = rb * 16, row = i0 + c;
@@ -315,7 +325,7 @@ __global__ void __launch_bounds__(kThreads) attn_rel_q_kernel(const RelArgs a) {
 #pragma unroll
         for (int t = 0; t < DT; ++t) {
             const int d0 = 16 * t + 4 * g;
-            bf[t] = (row_ok && d0 < D) ? *reinterpret_cast<const f4*>(sp + d0) : f4{0.f, 0.f, 0.f, 0.f};
+            bf[t] = *reinterpret_cast<const f4*>(sp + min(d0, D - 4)) * (d0 < D ? 1.0f : 0.0f);
         }
     }
     const float* vbase = a.v + static_cast<int64_t>(b) * l * a.ld_v + hk * D;
@@ -360,22 +370,24 @@ __global__ void __launch_bounds__(kThreads) attn_rel_q_kernel(const RelArgs a) {
         for (int t = 0; t < DT; ++t)
 #pragma unroll
             for (int st = 0; st < 4; ++st) u = __builtin_amdgcn_mfma_f32_16x16x4f32(va[set][t][st], bf[t][st], u, 0, 0, 0);
-        const f4 pv = pa[set];
-        __builtin_amdgcn_sched_barrier(0);
-        load1(set, kt + 2 * kWaves);
-        __builtin_amdgcn_sched_barrier(0);
         bool valid[4];
         valid_mask(kk0, valid);
         f4 r4;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            r4[r] = valid[r] ? pv[r] * u[r] : 0.0f;
+            r4[r] = valid[r] ? pa[set][r] * u[r] : 0.0f;
             rs += r4[r];
         }
-        if (kt < ntile) *reinterpret_cast<f4*>(ra + c * ld + kk0) = r4;
+        *reinterpret_cast<f4*>(ra + c * ld + 16 * min(kt, ntile) + 4 * g) = r4;  // past the end: never read
+        // The set is reloaded only after its last read: a copy of a register whose reload is in
+        // flight would make the wave wait for that reload.
+        __builtin_amdgcn_sched_barrier(0);
+        load1(set, kt + 2 * kWaves);
+        __builtin_amdgcn_sched_barrier(0);
     };
     load1(0, wave);
     load1(1, wave + kWaves);
+    __builtin_amdgcn_s_waitcnt(0);  // enter the loop with nothing in flight (as in attn_fwd_kernel)
     for (int kt = wave; kt < ntile; kt += 2 * kWaves) {
         tile1(0, kt);
         tile1(1, kt + kWaves);
@@ -412,7 +424,8 @@ __global__ void __launch_bounds__(kThreads) attn_rel_q_kernel(const RelArgs a) {
     auto tile2 = [&](int set, int kt) {
         const int kk0 = 16 * kt + 4 * g;
         const f4 pv = pb[set], rw = rb2[set];
-        const f4 r4 = kt < ntile ? *reinterpret_cast<const f4*>(ra + c * ld + kk0) : f4{0.f, 0.f, 0.f, 0.f};
+        const int lcol = 16 * min(kt, ntile) + 4 * g;  // past the end: a masked, never-stored column
+        const f4 r4 = *reinterpret_cast<const f4*>(ra + c * ld + lcol);
         bool valid[4];
         valid_mask(kk0, valid);
         f4 s4;
@@ -422,7 +435,7 @@ __global__ void __launch_bounds__(kThreads) attn_rel_q_kernel(const RelArgs a) {
             const float rsc = (a.scale * o) * (r4[r] - pv[r] * sum);
             s4[r] = valid[r] ? rsc / (2.0f * o + a.eps * ((o >= 0.0f) ? 1.0f : -1.0f)) : 0.0f;
         }
-        if (kt < ntile) *reinterpret_cast<f4*>(ra + c * ld + kk0) = s4;
+        *reinterpret_cast<f4*>(ra + c * ld + lcol) = s4;
 #pragma unroll
         for (int t = 0; t < DT; ++t)
 #pragma unroll
@@ -434,6 +447,7 @@ __global__ void __launch_bounds__(kThreads) attn_rel_q_kernel(const RelArgs a) {
     };
     load2(0, wave);
     load2(1, wave + kWaves);
+    __builtin_amdgcn_s_waitcnt(0);
     for (int kt = wave; kt < ntile; kt += 2 * kWaves) {
         tile2(0, kt);
         tile2(1, kt + kWaves);
@@ -849,15 +863,9 @@ extern "C" int pxk_attention_relevance_kv(const pxk_attn_rel_kv_desc* d, void* s
                 static_cast<int>(d->ld_g), static_cast<int>(n), static_cast<int>(l), static_cast<int>(H),
                 static_cast<int>(Hkv), static_cast<int>(D), static_cast<int>(ngroups), static_cast<int>(nkb), d->eps,
                 d->causal != 0, d->rope != 0, d->rope_half != 0, blocks % 8 == 0};
-    static const int variant = getenv("PXK_KV_VARIANT") ? atoi(getenv("PXK_KV_VARIANT")) : 0;
-    const dim3 grid(static_cast<unsigned>(blocks));
-    switch (variant) {
-        case 1: hipLaunchKernelGGL((attn_rel_kv_kernel<4, 8>), grid, dim3(256), 0, S(stream), a); break;
-        case 2: hipLaunchKernelGGL((attn_rel_kv_kernel<8, 4>), grid, dim3(512), 0, S(stream), a); break;
-        case 3: hipLaunchKernelGGL((attn_rel_kv_kernel<8, 8>), grid, dim3(512), 0, S(stream), a); break;
-        case 4: hipLaunchKernelGGL((attn_rel_kv_kernel<16, 4>), grid, dim3(1024), 0, S(stream), a); break;
-        case 5: hipLaunchKernelGGL((attn_rel_kv_kernel<16, 2>), grid, dim3(1024), 0, S(stream), a); break;
-        default: hipLaunchKernelGGL((attn_rel_kv_kernel<4, 4>), grid, dim3(256), 0, S(stream), a); break;
-    }
+    // Sixteen waves per workgroup, two items per register set: the widest spread of a long key
+    // block's rows measured fastest at 512 tokens (against 4 or 8 waves and 4 or 8 items).
+    hipLaunchKernelGGL((attn_rel_kv_kernel<16, 2>), dim3(static_cast<unsigned>(blocks)), dim3(16 * kWave), 0,
+                       S(stream), a);
     return launched("pxk_attention_relevance_kv");
 }
