@@ -107,27 +107,39 @@ __global__ void __launch_bounds__(kThreads) attn_fwd_kernel(const FwdArgs a) {
     // tile is on the MFMA pipe the next one's K and V are in flight. A set is reloaded right after
     // its last read (K after the score MFMAs, V after the context MFMAs), so old and new values
     // never live at once and the loop needs no register copies (a copy of a register with a load
-    // pending would wait for that load). Addresses are clamped into the matrix and no value is
-    // masked: a K column past head_dim meets a zero Q fragment, a V row past the last key meets a
-    // zero probability, and ctx rows past head_dim are never stored. Every lane issues the same
-    // loads, with no branch around them.
+    // pending would wait for that load).
+    //
+    // The loads are buffer loads: a tile's rows start at a scalar base (the buffer resource, built
+    // per tile with scalar instructions) and each lane's offsets are fixed for the whole loop, with
+    // the head-dimension step in the instruction's immediate offset, so a tile costs no vector
+    // address arithmetic. Rows past the sequence fall outside the resource's range and read 0 (a
+    // V row there meets a zero probability anyway); columns past head_dim read finite neighbouring
+    // data (a K column there meets a zero Q fragment, a ctx row there is never stored). The range
+    // ends with the head's last row, so no load leaves the caller's rows.
     f4 kf[2][DT], vf[2][DT];
-    // 32-bit element offsets from the head's base (l * ld < 2^31 is checked on the host).
     const int ldk = static_cast<int>(a.ldk), ldv = static_cast<int>(a.ldv);
+    const int kvcol = hk * D;
+    const int koff = (c * ldk + 4 * g) * 4, voff = ((4 * g) * ldv + c) * 4;
+    auto rsrc = [&](const float* base, int key0, int ldr) {
+        return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base + key0 * ldr), 0,
+                                                 ((l - key0) * ldr - kvcol) * 4, 0x00020000);
+    };
     auto load_k = [&](int set, int kt) {
         const int key0 = 16 * min(kt, ntile - 1);  // past the last tile: the last one again, unused
-        const float* kp = kbase + min(key0 + c, l - 1) * ldk;
+        const __amdgpu_buffer_rsrc_t r = rsrc(kbase, key0, ldk);
 #pragma unroll
-        for (int t = 0; t < DT; ++t) kf[set][t] = *reinterpret_cast<const f4*>(kp + min(16 * t + 4 * g, D - 4));
+        for (int t = 0; t < DT; ++t)
+            kf[set][t] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(r, koff + 64 * t, 0, 0));
     };
     auto load_v = [&](int set, int kt) {
         const int key0 = 16 * min(kt, ntile - 1);
+        const __amdgpu_buffer_rsrc_t r = rsrc(vbase, key0, ldv);
 #pragma unroll
-        for (int st = 0; st < 4; ++st) {
-            const float* vp = vbase + min(key0 + 4 * g + st, l - 1) * ldv;
+        for (int st = 0; st < 4; ++st)
 #pragma unroll
-            for (int t = 0; t < DT; ++t) vf[set][t][st] = vp[min(16 * t + c, D - 1)];
-        }
+            for (int t = 0; t < DT; ++t)
+                vf[set][t][st] =
+                    __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff + st * ldv * 4 + 64 * t, 0, 0));
     };
     auto tile = [&](int set, int kt) {
         const int key0 = 16 * kt;
@@ -170,9 +182,14 @@ __global__ void __launch_bounds__(kThreads) attn_fwd_kernel(const FwdArgs a) {
         ssum = ssum * alpha + part;
         m = m_new;
         // ctx^T (D x rows) += V^T (D x keys) P^T (keys x rows); the rescale is per row = per lane.
+        // The rescale is skipped (wave-uniformly) once no row's running max moved, which is most
+        // tiles after the first few; it multiplies by exactly 1 otherwise.
+        if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {
+#pragma unroll
+            for (int t = 0; t < DT; ++t) acc[t] *= alpha;
+        }
 #pragma unroll
         for (int t = 0; t < DT; ++t) {
-            acc[t] *= alpha;
 #pragma unroll
             for (int st = 0; st < 4; ++st)
                 acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf[set][t][st], e[st], acc[t], 0, 0, 0);
