@@ -83,10 +83,13 @@ enum {
     PXK_EPI_SWIGLU_REL = 7,  /* SwiGLU relevance: rh = X * acc (X = hidden); c = Y * W (gate_post * up);
                                 rg = (c / (2c + eps sign c)) * rh; C = rg / stab(Z2 + bias[n]) (gate);
                                 C2 = rg / stab(Z3 + bias2[n]) (up). Z stays the prologue's. */
-    PXK_EPI_MUL_X_SPLIT = 8  /* r = X * acc, or Y + X * acc; then the epsilon split of the residual sum
+    PXK_EPI_MUL_X_SPLIT = 8, /* r = X * acc, or Y + X * acc; then the epsilon split of the residual sum
                                 W = Z2 + Z3 whose relevance r is (lrp_residual_split, lrp_math.hpp:33-38):
                                 C = (Z2 / stab(W)) * r, C2 = (Z3 / stab(W)) * r. W must hold Z2 + Z3 as the
                                 forward computed it. Z stays the prologue's. */
+    PXK_EPI_ROPE_FWD = 9     /* C = acc; C2 = y = acc + bias[n] when a bias is given (else y = acc); and
+                                for columns n < rope_cols, C3 = y rotated pairwise at position m
+                                (rope_rotate, row_math.hpp:93-110; pairs inside each head_dim block) */
 };
 
 enum {
@@ -127,6 +130,7 @@ typedef struct pxk_gemm_desc {
     int32_t tile;         /* 0 = chosen by the library; else PXK_TILE_* (a tuning override) */
     float* workspace;     /* split-K partials */
     size_t workspace_bytes;
+    int64_t rope_cols;    /* ROPE_FWD: the leading columns (whole heads) that are rotated into C3 */
 } pxk_gemm_desc;
 
 /* Bytes of workspace pxk_gemm needs for this descriptor (0 when it runs without split-K). */

@@ -93,7 +93,7 @@ private:
     detail::DevBuf cos_, sin_;
     int64_t N_ = 0, L_ = 0;
     const float* x_ = nullptr;
-    detail::DevBuf x_copy_, qkv_z_, qkv_y_, q_rot_, k_rot_, raw_, p_, ctx_, out_z_, out_y_;
+    detail::DevBuf x_copy_, qkv_z_, qkv_y_, qk_rot_, raw_, p_, ctx_, out_z_, out_y_;
     detail::DevBuf spv_, ra_, g_, r_in_;
     Tensor key_rel_, value_rel_;
     bool has_relevance_ = false;

@@ -119,36 +119,39 @@ const float* MultiHeadAttentionModule::run_forward(const float* x, int64_t n, in
     const bool causal = config_.causal;
     void* st = be_->stream();
 
-    // 1. q, k, v in one GEMM against [Wq | Wk | Wv]; z (pre-bias) kept for the relevance pass.
+    // 1-2. q, k, v in one GEMM against [Wq | Wk | Wv], z (pre-bias) kept for the relevance pass;
+    //      with RoPE the epilogue also writes the rotated q | k heads (positions from 0: no KV
+    //      cache here), one batch entry per sequence so that a row's position is its row.
     float* z = qkv_z_.ensure(be_, M * w3);
-    float* y = z;
+    float* y = config_.qkv_bias ? qkv_y_.ensure(be_, M * w3) : z;
+    const int64_t rw = qd + kvd;  // row length of the rotated q | k block
+    float* rot = config_.use_rope ? qk_rot_.ensure(be_, M * rw) : nullptr;
     {
-        pxk_gemm_desc d = gemm_desc(M, w3, d_);
-        d.a = mat(x, d_);
+        pxk_gemm_desc d = gemm_desc(l, w3, d_);
+        d.batch = n;
+        d.a = mat(x, d_, l * d_);
         d.b = mat(wqkv_.data(), w3);
-        d.c = mat(z, w3);
+        d.c = mat(z, w3, l * w3);
         if (config_.qkv_bias) {
-            y = qkv_y_.ensure(be_, M * w3);
             d.epilogue = PXK_EPI_STORE_BIAS;
-            d.c2 = mat(y, w3);
+            d.c2 = mat(y, w3, l * w3);
             d.e_bias = mat(bqkv_.data(), 0);
+        }
+        if (config_.use_rope) {
+            d.epilogue = PXK_EPI_ROPE_FWD;
+            d.c3 = mat(rot, rw, l * rw);
+            d.cos_t = cos_.data();
+            d.sin_t = sin_.data();
+            d.head_dim = D_;
+            d.rope_half = config_.rope_layout == RoPELayout::RotateHalf;
+            d.rope_cols = rw;
         }
         be_->run_gemm(d);
     }
-    // 2. RoPE on q and k (positions from 0: no KV cache here).
-    const float *q = y, *k = y + qd, *v = y + qd + kvd;
-    int64_t ldq = w3, ldk = w3;
-    if (config_.use_rope) {
-        float* qr = q_rot_.ensure(be_, M * qd);
-        float* kr = k_rot_.ensure(be_, M * kvd);
-        MI355XBackend::check(pxk_rope_qk(y, y + qd, w3, qr, kr, cos_.data(), sin_.data(), M, l, H_, Hkv_, D_,
-                                         config_.rope_layout == RoPELayout::RotateHalf, st),
-                             "MultiHeadAttentionModule::forward (rope)");
-        q = qr;
-        k = kr;
-        ldq = qd;
-        ldk = kvd;
-    }
+    const float* q = config_.use_rope ? rot : y;
+    const float* k = config_.use_rope ? rot + qd : y + qd;
+    const float* v = y + qd + kvd;
+    const int64_t ldq = config_.use_rope ? rw : w3, ldk = ldq;
     float* raw = raw_.ensure(be_, n * H_ * LL);
     float* p = p_.ensure(be_, n * H_ * LL);
     float* ctx = ctx_.ensure(be_, M * qd);
@@ -232,10 +235,10 @@ const float* MultiHeadAttentionModule::run_relevance(const float* relevance_out,
     const float eps = config.epsilon;
     const float* z = qkv_z_.data();
     const float* y = config_.qkv_bias ? qkv_y_.data() : z;
-    const float* q = config_.use_rope ? q_rot_.data() : y;
-    const float* k = config_.use_rope ? k_rot_.data() : y + qd;
+    const float* q = config_.use_rope ? qk_rot_.data() : y;
+    const float* k = config_.use_rope ? qk_rot_.data() + qd : y + qd;
     const float* v = y + qd + kvd;
-    const int64_t ldq = config_.use_rope ? qd : w3, ldk = config_.use_rope ? kvd : w3;
+    const int64_t ldq = config_.use_rope ? qd + kvd : w3, ldk = ldq;  // q | k rotated rows, or the packed rows
     const float* bq = detail::rule_bias(bqkv_.data(), config_.qkv_bias, bid);
     void* st = be_->stream();
 
@@ -367,10 +370,10 @@ void MultiHeadAttentionModule::relevance_scores_unfused(const float* spv, float 
     const bool causal = config_.causal;
     const float* z = qkv_z_.data();
     const float* y = config_.qkv_bias ? qkv_y_.data() : z;
-    const float* q = config_.use_rope ? q_rot_.data() : y;
-    const float* k = config_.use_rope ? k_rot_.data() : y + qd;
+    const float* q = config_.use_rope ? qk_rot_.data() : y;
+    const float* k = config_.use_rope ? qk_rot_.data() + qd : y + qd;
     const float* v = y + qd + kvd;
-    const int64_t ldq = config_.use_rope ? qd : w3, ldk = config_.use_rope ? kvd : w3;
+    const int64_t ldq = config_.use_rope ? qd + kvd : w3, ldk = ldq;  // q | k rotated rows, or the packed rows
     const float* bq = detail::rule_bias(bqkv_.data(), config_.qkv_bias, bid);
     void* st = be_->stream();
     float* ra = ra_.data();

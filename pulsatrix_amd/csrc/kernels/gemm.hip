@@ -53,7 +53,7 @@ struct Args {
     Op a, b, c, z, zb, c2, c3, x, y, w, z2, z3, eb, eb2;
     const float* cos_t;
     const float* sin_t;
-    int64_t head_dim;
+    int64_t head_dim, rope_cols;
     int rope_half;
     int vec_a, vec_b, vec_e;  // 128-bit global access allowed: A (and Z), B, epilogue operands
     int tiles_m, tiles_n, bm;
@@ -194,6 +194,32 @@ __device__ void epilogue_rows(const float* Cs, int ldc, int64_t m0, int64_t n0, 
             f4 v = ld4(X + m * g.x.ld + n, vec, cnt) * acc;
             if (Y) v = ld4(Y + m * g.y.ld + n, vec, cnt) + v;
             st4(C + m * g.c.ld + n, v, vec, cnt);
+        } else if constexpr (EPI == PXK_EPI_ROPE_FWD) {
+            // z, y = z + bias, and the rotated y of the q / k heads; a head's pair partner is in
+            // this tile (whole heads per tile).
+            st4(C + m * g.c.ld + n, acc, vec, cnt);
+            if (EB) st4(C2 + m * g.c2.ld + n, acc + ld4(EB + n, vec, cnt), vec, cnt);
+            if (n < g.rope_cols) {
+                const int64_t D = g.head_dim, half = D / 2;
+                f4 out = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    if (j >= cnt) continue;
+                    const int64_t nj = n + j;
+                    const int64_t d = nj % D, hb = nj - d;
+                    const int64_t i = g.rope_half ? (d < half ? d : d - half) : d / 2;
+                    const int64_t lo = hb + (g.rope_half ? i : 2 * i), hi = hb + (g.rope_half ? i + half : 2 * i + 1);
+                    float x0 = Cs[row * ldc + static_cast<int>(lo - n0)];
+                    float x1 = Cs[row * ldc + static_cast<int>(hi - n0)];
+                    if (EB) {
+                        x0 = x0 + EB[lo];
+                        x1 = x1 + EB[hi];
+                    }
+                    const float c = g.cos_t[m * half + i], sn = g.sin_t[m * half + i];
+                    out[j] = nj == lo ? x0 * c - x1 * sn : x0 * sn + x1 * c;  // row_math.hpp:93-110
+                }
+                st4(C3 + m * g.c3.ld + n, out, vec, cnt);
+            }
         } else if constexpr (EPI == PXK_EPI_MUL_X_SPLIT) {
             f4 v = ld4(X + m * g.x.ld + n, vec, cnt) * acc;
             if (Y) v = ld4(Y + m * g.y.ld + n, vec, cnt) + v;
@@ -851,6 +877,7 @@ const Entry kTable[] = {
     PXK_GEMM_ENTRY(1, 0, PXK_PRO_NONE, PXK_EPI_VALUE_REL),
     PXK_GEMM_ENTRY(0, 1, PXK_PRO_DIV_STAB, PXK_EPI_SWIGLU_REL),
     PXK_GEMM_ENTRY(0, 1, PXK_PRO_NONE, PXK_EPI_MUL_X_SPLIT),
+    PXK_GEMM_ENTRY(0, 0, PXK_PRO_NONE, PXK_EPI_ROPE_FWD),
     PXK_GEMM_ENTRY(0, 0, PXK_PRO_DIV_STAB, PXK_EPI_MUL_X_SPLIT),
     PXK_GEMM_ENTRY(0, 1, PXK_PRO_DIV_STAB, PXK_EPI_MUL_X_SPLIT),
 };
@@ -980,6 +1007,17 @@ int plan(const pxk_gemm_desc* d, Plan* p) {
         return fail(PXK_ERR_INVALID, "pxk_gemm: the DIV_STAB prologue needs Z");
     if (d->prologue == PXK_PRO_DIV_STAB && (epi == PXK_EPI_ROPE_REL || epi == PXK_EPI_VALUE_REL))
         return fail(PXK_ERR_INVALID, "pxk_gemm: epilogue %d reads Z, which the DIV_STAB prologue owns", epi);
+    if (epi == PXK_EPI_ROPE_FWD) {
+        const int64_t D = d->head_dim;
+        if (D <= 0 || D % 2 != 0 || d->cos_t == nullptr || d->sin_t == nullptr || d->c3.ptr == nullptr)
+            return fail(PXK_ERR_INVALID, "pxk_gemm: ROPE_FWD needs an even head_dim, cos/sin tables and C3");
+        if (d->rope_cols < 0 || d->rope_cols > d->n || d->rope_cols % D != 0 || d->n % D != 0)
+            return fail(PXK_ERR_INVALID, "pxk_gemm: ROPE_FWD rotates whole heads: rope_cols and n multiples of head_dim");
+        if (!rope_fits(d, 128))
+            return fail(PXK_ERR_INVALID, "pxk_gemm: ROPE_FWD needs whole heads inside a 128-wide tile");
+        if (d->tile > 0 && !rope_fits(d, kTileInfo[d->tile - 1].bn))
+            return fail(PXK_ERR_INVALID, "pxk_gemm: ROPE_FWD heads do not fit tile %d", d->tile);
+    }
     if (epi == PXK_EPI_ROPE_REL) {
         const int64_t D = d->head_dim;
         if (D <= 0 || D % 2 != 0 || d->cos_t == nullptr || d->sin_t == nullptr)
@@ -1000,11 +1038,13 @@ int plan(const pxk_gemm_desc* d, Plan* p) {
     for (int t = 0; t < kTiles; ++t) {
         if (d->tile > 0 && t != d->tile - 1) continue;
         const TileInfo& ti = kTileInfo[t];
-        if (epi == PXK_EPI_ROPE_REL && !rope_fits(d, ti.bn)) continue;
+        if ((epi == PXK_EPI_ROPE_REL || epi == PXK_EPI_ROPE_FWD) && !rope_fits(d, ti.bn)) continue;
         const double stages = max_stages(d, ti.bm, ti.bk);
         const double tiles = static_cast<double>(live_tiles(d, ti.bm, ti.bn));
-        // The 128x128 tile only pays off when its tiles alone fill the chip.
-        const bool big_only = d->tile == 0 && t == 0;
+        // The 128x128 tile only pays off when its tiles alone fill the chip, unless it is the only
+        // one that holds whole heads for a RoPE epilogue.
+        const bool rope_epi = epi == PXK_EPI_ROPE_REL || epi == PXK_EPI_ROPE_FWD;
+        const bool big_only = d->tile == 0 && t == 0 && !(rope_epi && !rope_fits(d, 64));
         if (big_only && tiles < 256.0) continue;
         for (int s = 1; s <= 64; s *= 2) {
             if (d->splits > 0 && s != 1) break;
@@ -1099,6 +1139,7 @@ extern "C" int pxk_gemm(const pxk_gemm_desc* d, void* stream) {
     g.sin_t = d->sin_t;
     g.head_dim = d->head_dim;
     g.rope_half = d->rope_half;
+    g.rope_cols = d->rope_cols;
     g.ws = d->workspace;
     // 128-bit loads when every base, stride and the contiguous extent allow them; the causal
     // K ranges start at multiples of the tile height, so they keep the alignment.

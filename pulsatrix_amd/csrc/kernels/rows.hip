@@ -290,13 +290,19 @@ struct Targets {
     int64_t t[64];
 };
 
-__global__ void __launch_bounds__(kThreads) lm_seed_kernel(const float* logits, int64_t L, int64_t V, int use_given,
-                                                           Targets given, int64_t* targets_out, float* seed,
-                                                           int unit) {
+constexpr int kSeedThreads = 1024;
+
+// One workgroup per sequence scans the last position's logits: each thread keeps the first
+// maximum of its strided share (indices ascending), loading eight values ahead of the compares so
+// the scan is not one memory round trip per element; the shares then merge in LDS, larger value
+// first and the lower index on ties.
+__global__ void __launch_bounds__(kSeedThreads) lm_seed_kernel(const float* logits, int64_t L, int64_t V,
+                                                               int use_given, Targets given, int64_t* targets_out,
+                                                               float* seed, int unit) {
     const int64_t n = blockIdx.x;
     const float* row = logits + (n * L + (L - 1)) * V;
-    __shared__ float bv[kThreads];
-    __shared__ int64_t bi[kThreads];
+    __shared__ float bv[kSeedThreads];
+    __shared__ int64_t bi[kSeedThreads];
     float best = -INFINITY;
     int64_t idx = V;  // "none yet"
     if (use_given) {
@@ -305,18 +311,28 @@ __global__ void __launch_bounds__(kThreads) lm_seed_kernel(const float* logits, 
             idx = given.t[n];
         }
     } else {
-        for (int64_t j = threadIdx.x; j < V; j += kThreads) {  // j ascends: ties keep the first index
-            const float v = row[j];
-            if (idx == V || v > best) {
-                best = v;
-                idx = j;
+        constexpr int kAhead = 8;
+        for (int64_t j0 = threadIdx.x; j0 < V; j0 += static_cast<int64_t>(kAhead) * kSeedThreads) {
+            float v[kAhead];
+#pragma unroll
+            for (int u = 0; u < kAhead; ++u) {
+                const int64_t j = j0 + static_cast<int64_t>(u) * kSeedThreads;
+                v[u] = row[j < V ? j : V - 1];
+            }
+#pragma unroll
+            for (int u = 0; u < kAhead; ++u) {  // j ascends: ties keep the first index
+                const int64_t j = j0 + static_cast<int64_t>(u) * kSeedThreads;
+                if (j < V && (idx == V || v[u] > best)) {
+                    best = v[u];
+                    idx = j;
+                }
             }
         }
     }
     bv[threadIdx.x] = best;
     bi[threadIdx.x] = idx;
     __syncthreads();
-    for (int s = kThreads / 2; s > 0; s >>= 1) {
+    for (int s = kSeedThreads / 2; s > 0; s >>= 1) {
         if (threadIdx.x < s) {
             const float ov = bv[threadIdx.x + s];
             const int64_t oi = bi[threadIdx.x + s];
@@ -522,7 +538,7 @@ int pxk_lm_seed(const float* logits, int64_t n, int64_t l, int64_t vocab, const 
         }
     }
     if (const int rc = pxk_fill(seed, 0.0f, n * l * vocab, stream)) return rc;
-    hipLaunchKernelGGL(lm_seed_kernel, dim3(static_cast<unsigned>(n)), dim3(kThreads), 0, S(stream), logits, l, vocab,
+    hipLaunchKernelGGL(lm_seed_kernel, dim3(static_cast<unsigned>(n)), dim3(kSeedThreads), 0, S(stream), logits, l, vocab,
                        targets_in ? 1 : 0, given, targets_out, seed, unit);
     return launched("pxk_lm_seed");
 }

@@ -34,13 +34,14 @@ class GemmDesc(ctypes.Structure):
                 ("c2", Operand), ("c3", Operand), ("x", Operand), ("y", Operand), ("w", Operand), ("z2", Operand), ("z3", Operand),
                 ("e_bias", Operand), ("e_bias2", Operand),
                 ("cos_t", c_vp), ("sin_t", c_vp), ("head_dim", c_i64), ("rope_half", ctypes.c_int32),
-                ("tile", ctypes.c_int32), ("workspace", c_vp), ("workspace_bytes", ctypes.c_size_t)]
+                ("tile", ctypes.c_int32), ("workspace", c_vp), ("workspace_bytes", ctypes.c_size_t),
+                ("rope_cols", c_i64)]
 
 
 CAUSAL_NONE, CAUSAL_TRI, CAUSAL_K_LE_M, CAUSAL_K_GE_M = 0, 1, 2, 3
 PRO_NONE, PRO_DIV_STAB = 0, 1
 (EPI_STORE, EPI_STORE_BIAS, EPI_ADD_RESID, EPI_MUL_X, EPI_SPV, EPI_ROPE_REL, EPI_VALUE_REL,
- EPI_SWIGLU_REL, EPI_MUL_X_SPLIT) = range(9)
+ EPI_SWIGLU_REL, EPI_MUL_X_SPLIT, EPI_ROPE_FWD) = range(10)
 TILE_AUTO, TILE_128x128, TILE_64x64, TILE_32x64, TILE_32x32, TILE_32x64_DIRECT, TILE_32x32_DIRECT = range(7)
 
 # (name, restype, argtypes) of every pxk entry point; `p` = device pointer (void*), `i` = int64,

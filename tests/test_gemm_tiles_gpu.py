@@ -25,7 +25,7 @@ COMBOS = [
     (0, 0, N.PRO_NONE, N.EPI_ROPE_REL), (1, 0, N.PRO_NONE, N.EPI_ROPE_REL), (0, 0, N.PRO_NONE, N.EPI_VALUE_REL),
     (1, 0, N.PRO_NONE, N.EPI_VALUE_REL), (0, 1, N.PRO_DIV_STAB, N.EPI_SWIGLU_REL),
     (0, 1, N.PRO_NONE, N.EPI_MUL_X_SPLIT), (0, 0, N.PRO_DIV_STAB, N.EPI_MUL_X_SPLIT),
-    (0, 1, N.PRO_DIV_STAB, N.EPI_MUL_X_SPLIT),
+    (0, 1, N.PRO_DIV_STAB, N.EPI_MUL_X_SPLIT), (0, 0, N.PRO_NONE, N.EPI_ROPE_FWD),
 ]
 TILES = [N.TILE_128x128, N.TILE_64x64, N.TILE_32x64, N.TILE_32x32, N.TILE_32x64_DIRECT, N.TILE_32x32_DIRECT]
 TILE_BN = {N.TILE_128x128: 128, N.TILE_64x64: 64, N.TILE_32x64: 64, N.TILE_32x32: 32, N.TILE_32x64_DIRECT: 64,
@@ -50,6 +50,24 @@ def rope_tables(m, d, theta=10000.0):
     return np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
 
 
+def rotate(y, cos, sin, D, half_layout):
+    """rope_rotate (row_math.hpp:93-110) of every head_dim block of y's columns, position = row."""
+    m, n = y.shape
+    half = D // 2
+    col = np.arange(n)
+    d = col % D
+    hb = col - d
+    if half_layout:
+        i = np.where(d < half, d, d - half)
+        lo, hi = hb + i, hb + i + half
+    else:
+        i = d // 2
+        lo, hi = hb + 2 * i, hb + 2 * i + 1
+    c, s = cos[:, i], sin[:, i]
+    x0, x1 = y[:, lo], y[:, hi]
+    return np.where((col == lo)[None, :], x0 * c - x1 * s, x0 * s + x1 * c)
+
+
 def expected(epi, acc, t, D, half_layout):
     """The epilogue of include/pxk.h on a float64 accumulator tile."""
     X, Y, W, Z, Z2, Z3, C0 = (t.get(k) for k in ("x", "y", "w", "z", "z2", "z3", "c0"))
@@ -67,6 +85,9 @@ def expected(epi, acc, t, D, half_layout):
     if epi == N.EPI_VALUE_REL:
         r = Y * acc
         return {"c": r, "c2": r / stab(Z + eb)}
+    if epi == N.EPI_ROPE_FWD:
+        y = acc + eb
+        return {"c": acc, "c2": y, "c3": rotate(y, t["cos"], t["sin"], D, half_layout)}
     if epi == N.EPI_MUL_X_SPLIT:
         r = Y + X * acc
         den = stab(W)
@@ -112,7 +133,7 @@ def run(d, splits):
 @pytest.mark.parametrize("combo", COMBOS, ids=lambda c: "ta%d_tb%d_pro%d_epi%d" % c)
 def test_fused_gemm_on_every_tile(combo, tile, splits):
     ta, tb, pro, epi = combo
-    rope = epi == N.EPI_ROPE_REL
+    rope = epi in (N.EPI_ROPE_REL, N.EPI_ROPE_FWD)
     D = 64 if rope and TILE_BN[tile] >= 64 else 16
     m, n, k = 77, 128, 150  # ragged M and K; N = whole heads for the RoPE rule
     a, b = G.uniform((k, m) if ta else (m, k), 1), G.uniform((n, k) if tb else (k, n), 2)
@@ -152,13 +173,17 @@ def test_fused_gemm_on_every_tile(combo, tile, splits):
     d.e_bias2 = N.operand(G.ptr(dv["eb2"]).value, 0)
     d.cos_t, d.sin_t = G.ptr(dv["cos"]).value, G.ptr(dv["sin"]).value
     d.head_dim, d.rope_half = D, 1
+    d.rope_cols = n - D  # every head but the last is rotated
     if epi == N.EPI_MUL_X and pro == N.PRO_NONE and ta == 0 and tb == 0:
         d.y = N.operand(None, 0)  # the Y-less form: C = X * acc
         want = {"c": t64["x"] * acc}
     rc = run(d, splits)
     assert rc == 0, N.pxk().pxk_last_error()
     for key, ref in want.items():
-        G.assert_close(G.host(outs[key]), ref, 2e-5, "tile %d splits %d output %s" % (tile, splits, key))
+        got = G.host(outs[key])
+        if epi == N.EPI_ROPE_FWD and key == "c3":
+            got, ref = got[:, :n - D], ref[:, :n - D]
+        G.assert_close(got, ref, 2e-5, "tile %d splits %d output %s" % (tile, splits, key))
 
 
 @gpu
