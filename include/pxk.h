@@ -87,9 +87,14 @@ enum {
                                 W = Z2 + Z3 whose relevance r is (lrp_residual_split, lrp_math.hpp:33-38):
                                 C = (Z2 / stab(W)) * r, C2 = (Z3 / stab(W)) * r. W must hold Z2 + Z3 as the
                                 forward computed it. Z stays the prologue's. */
-    PXK_EPI_ROPE_FWD = 9     /* C = acc; C2 = y = acc + bias[n] when a bias is given (else y = acc); and
+    PXK_EPI_ROPE_FWD = 9,    /* C = acc; C2 = y = acc + bias[n] when a bias is given (else y = acc); and
                                 for columns n < rope_cols, C3 = y rotated pairwise at position m
                                 (rope_rotate, row_math.hpp:93-110; pairs inside each head_dim block) */
+    PXK_EPI_SWIGLU_FWD = 10  /* SwiGLU gate (swiglu_module.cpp:80-88) on a gate/up GEMM whose B columns
+                                alternate 32-wide gate and up blocks (block 2b: gate features 32b..32b+31,
+                                block 2b+1: the same up features); N = 2F, F a multiple of 32, no bias.
+                                C (ld >= 2F) = z as [gate | up] halves; C3 = gate_post = silu(z_gate)
+                                (x / (1 + e^-x), cpu_backend.cpp:29); C2 = hidden = gate_post * z_up. */
 };
 
 enum {

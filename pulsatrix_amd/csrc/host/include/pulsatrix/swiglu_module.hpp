@@ -35,13 +35,15 @@ protected:
 
 private:
     void pack_weights();
+    /** @brief The forward applies the gate in the gate/up GEMM's epilogue (no bias, F a multiple of 32). */
+    [[nodiscard]] bool fused_gate() const noexcept { return !use_bias_ && F_ % 32 == 0; }
 
     int64_t d_, F_;
     bool use_bias_;
     MI355XBackend* be_;
     LinearModule gate_proj_, up_proj_, down_proj_;
     uint64_t packed_version_ = ~uint64_t{0};
-    detail::DevBuf wgu_, bgu_;
+    detail::DevBuf wgu_, wgu_il_, bgu_;
     int64_t rows_ = 0;
     const float* x_ = nullptr;
     Shape last_shape_;

@@ -35,6 +35,16 @@ void SwiGLUModule::pack_weights() {
         be_->copy_2d(b, 2 * F_, gate_proj_.bias_data(), F_, 1, F_);
         be_->copy_2d(b + F_, 2 * F_, up_proj_.bias_data(), F_, 1, F_);
     }
+    if (fused_gate()) {
+        // The forward's copy: 32-column blocks alternate gate and up (block 2b = gate features
+        // 32b..32b+31, block 2b+1 = the same up features), so one GEMM tile holds both factors of
+        // its hidden features and applies the gate in its epilogue (PXK_EPI_SWIGLU_FWD).
+        float* wi = wgu_il_.ensure(be_, d_ * 2 * F_);
+        for (int64_t b = 0; b < F_ / 32; ++b) {
+            be_->copy_2d(wi + 64 * b, 2 * F_, gate_proj_.weight_data() + 32 * b, F_, d_, 32);
+            be_->copy_2d(wi + 64 * b + 32, 2 * F_, up_proj_.weight_data() + 32 * b, F_, d_, 32);
+        }
+    }
     packed_version_ = v;
 }
 
@@ -47,7 +57,18 @@ const float* SwiGLUModule::run_forward(const float* x, int64_t rows, const float
     const int64_t f2 = 2 * F_;
     float* gz = gu_z_.ensure(be_, rows * f2);
     float* gy = gz;
-    {  // gate and up projections in one GEMM
+    float* gp = gate_post_.ensure(be_, rows * F_);
+    float* h = hidden_.ensure(be_, rows * F_);
+    if (fused_gate()) {  // gate and up projections and the gate itself in one GEMM
+        pxk_gemm_desc d = gemm_desc(rows, f2, d_);
+        d.a = mat(x, d_);
+        d.b = mat(wgu_il_.data(), f2);
+        d.c = mat(gz, f2);
+        d.c2 = mat(h, F_);
+        d.c3 = mat(gp, F_);
+        d.epilogue = PXK_EPI_SWIGLU_FWD;
+        be_->run_gemm(d);
+    } else {  // gate and up projections in one GEMM, then the gate
         pxk_gemm_desc d = gemm_desc(rows, f2, d_);
         d.a = mat(x, d_);
         d.b = mat(wgu_.data(), f2);
@@ -59,10 +80,8 @@ const float* SwiGLUModule::run_forward(const float* x, int64_t rows, const float
             d.e_bias = mat(bgu_.data(), 0);
         }
         be_->run_gemm(d);
+        MI355XBackend::check(pxk_swiglu_forward(gy, f2, gp, h, rows, F_, be_->stream()), "SwiGLUModule::forward");
     }
-    float* gp = gate_post_.ensure(be_, rows * F_);
-    float* h = hidden_.ensure(be_, rows * F_);
-    MI355XBackend::check(pxk_swiglu_forward(gy, f2, gp, h, rows, F_, be_->stream()), "SwiGLUModule::forward");
     float* dz = down_z_.ensure(be_, rows * d_);
     float* dy = use_bias_ ? down_y_.ensure(be_, rows * d_) : dz;
     {

@@ -194,6 +194,21 @@ __device__ void epilogue_rows(const float* Cs, int ldc, int64_t m0, int64_t n0, 
             f4 v = ld4(X + m * g.x.ld + n, vec, cnt) * acc;
             if (Y) v = ld4(Y + m * g.y.ld + n, vec, cnt) + v;
             st4(C + m * g.c.ld + n, v, vec, cnt);
+        } else if constexpr (EPI == PXK_EPI_SWIGLU_FWD) {
+            // Columns alternate 32-wide gate and up blocks; the gate block's threads do both.
+            if ((n & 63) >= 32) continue;
+            const int64_t F = g.N / 2, j = (n >> 6) * 32 + (n & 63);
+            const f4 up = *reinterpret_cast<const f4*>(Cs + row * ldc + col + 32);
+            st4(C + m * g.c.ld + j, acc, vec, cnt);
+            st4(C + m * g.c.ld + F + j, up, vec, cnt);
+            f4 gp, hid;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                gp[r] = acc[r] * (1.0f / (1.0f + expf(-acc[r])));  // x * sigmoid(x), cpu_backend.cpp:29
+                hid[r] = gp[r] * up[r];
+            }
+            st4(C3 + m * g.c3.ld + j, gp, vec, cnt);
+            st4(C2 + m * g.c2.ld + j, hid, vec, cnt);
         } else if constexpr (EPI == PXK_EPI_ROPE_FWD) {
             // z, y = z + bias, and the rotated y of the q / k heads; a head's pair partner is in
             // this tile (whole heads per tile).
@@ -878,6 +893,7 @@ const Entry kTable[] = {
     PXK_GEMM_ENTRY(0, 1, PXK_PRO_DIV_STAB, PXK_EPI_SWIGLU_REL),
     PXK_GEMM_ENTRY(0, 1, PXK_PRO_NONE, PXK_EPI_MUL_X_SPLIT),
     PXK_GEMM_ENTRY(0, 0, PXK_PRO_NONE, PXK_EPI_ROPE_FWD),
+    PXK_GEMM_ENTRY(0, 0, PXK_PRO_NONE, PXK_EPI_SWIGLU_FWD),
     PXK_GEMM_ENTRY(0, 0, PXK_PRO_DIV_STAB, PXK_EPI_MUL_X_SPLIT),
     PXK_GEMM_ENTRY(0, 1, PXK_PRO_DIV_STAB, PXK_EPI_MUL_X_SPLIT),
 };
@@ -1007,6 +1023,12 @@ int plan(const pxk_gemm_desc* d, Plan* p) {
         return fail(PXK_ERR_INVALID, "pxk_gemm: the DIV_STAB prologue needs Z");
     if (d->prologue == PXK_PRO_DIV_STAB && (epi == PXK_EPI_ROPE_REL || epi == PXK_EPI_VALUE_REL))
         return fail(PXK_ERR_INVALID, "pxk_gemm: epilogue %d reads Z, which the DIV_STAB prologue owns", epi);
+    if (epi == PXK_EPI_SWIGLU_FWD) {
+        if (d->n % 64 != 0 || d->c2.ptr == nullptr || d->c3.ptr == nullptr || d->e_bias.ptr != nullptr)
+            return fail(PXK_ERR_INVALID, "pxk_gemm: SWIGLU_FWD needs n a multiple of 64, C2 and C3, and no bias");
+        if (d->tile > 0 && kTileInfo[d->tile - 1].bn % 64 != 0)
+            return fail(PXK_ERR_INVALID, "pxk_gemm: SWIGLU_FWD needs 64-wide tile multiples (tile %d)", d->tile);
+    }
     if (epi == PXK_EPI_ROPE_FWD) {
         const int64_t D = d->head_dim;
         if (D <= 0 || D % 2 != 0 || d->cos_t == nullptr || d->sin_t == nullptr || d->c3.ptr == nullptr)
@@ -1039,6 +1061,7 @@ int plan(const pxk_gemm_desc* d, Plan* p) {
         if (d->tile > 0 && t != d->tile - 1) continue;
         const TileInfo& ti = kTileInfo[t];
         if ((epi == PXK_EPI_ROPE_REL || epi == PXK_EPI_ROPE_FWD) && !rope_fits(d, ti.bn)) continue;
+        if (epi == PXK_EPI_SWIGLU_FWD && ti.bn % 64 != 0) continue;
         const double stages = max_stages(d, ti.bm, ti.bk);
         const double tiles = static_cast<double>(live_tiles(d, ti.bm, ti.bn));
         // The 128x128 tile only pays off when its tiles alone fill the chip, unless it is the only

@@ -187,6 +187,33 @@ def test_fused_gemm_on_every_tile(combo, tile, splits):
 
 
 @gpu
+@pytest.mark.parametrize("splits", [1, 3])
+@pytest.mark.parametrize("tile", [t for t in TILES if TILE_BN[t] % 64 == 0])
+def test_swiglu_gate_epilogue(tile, splits):
+    """SWIGLU_FWD: B's columns alternate 32-wide gate and up blocks; C gets z as [gate | up] halves,
+    C3 = silu(gate), C2 = silu(gate) * up (swiglu_module.cpp:80-88)."""
+    m, k, F = 77, 150, 96
+    a, wg, wu = G.uniform((m, k), 31), G.uniform((k, F), 32), G.uniform((k, F), 33)
+    b = np.empty((k, 2 * F), np.float32)
+    for blk in range(F // 32):
+        b[:, 64 * blk:64 * blk + 32] = wg[:, 32 * blk:32 * blk + 32]
+        b[:, 64 * blk + 32:64 * blk + 64] = wu[:, 32 * blk:32 * blk + 32]
+    zg = a.astype(np.float64) @ wg.astype(np.float64)
+    zu = a.astype(np.float64) @ wu.astype(np.float64)
+    gp = zg / (1.0 + np.exp(-zg))
+    c, hid, gpo = G.empty((m, 2 * F)), G.empty((m, F)), G.empty((m, F))
+    d = N.GemmDesc()
+    d.m, d.n, d.k, d.batch, d.inner, d.kgroups = m, 2 * F, k, 1, 1, 1
+    d.epilogue, d.tile = N.EPI_SWIGLU_FWD, tile
+    d.a, d.b = N.operand(G.ptr(G.dev(a)).value, k), N.operand(G.ptr(G.dev(b)).value, 2 * F)
+    d.c, d.c2, d.c3 = N.operand(G.ptr(c).value, 2 * F), N.operand(G.ptr(hid).value, F), N.operand(G.ptr(gpo).value, F)
+    assert run(d, splits) == 0, N.pxk().pxk_last_error()
+    G.assert_close(G.host(c), np.concatenate([zg, zu], axis=1), 2e-5, "z")
+    G.assert_close(G.host(gpo), gp, 2e-5, "gate_post")
+    G.assert_close(G.host(hid), gp * zu, 2e-5, "hidden")
+
+
+@gpu
 @pytest.mark.parametrize("half", [0, 1])
 @pytest.mark.parametrize("tile", [N.TILE_64x64, N.TILE_32x64])
 def test_rope_rule_epilogue_interleaved_and_half_pairs(half, tile):
