@@ -92,6 +92,11 @@ int pxa_lm_explain_device(void* lm, const float* ids, int64_t n, int64_t l, floa
 int pxa_lm_capture_explain(void* lm, const float* ids, int64_t n, int64_t l, float eps, int bias_in_denominator,
                            float* token_rel, int64_t* targets);
 int pxa_lm_replay(void* lm);
+/* After a device-side pass (explain or replay): 0 when every id was in [0, vocab), else -1 with
+ * the reference's message ("EmbeddingModule::forward: index out of range [0, num_embeddings)") in
+ * pxa_last_error(); an out-of-range id is gathered as id 0 so the pass itself completes. Waits for
+ * the backend's stream. */
+int pxa_lm_check_device_ids(void* lm);
 /* Device pointers of the last pass: logits (n*l*vocab), embedding-level relevance (n*l*d). */
 const float* pxa_lm_last_logits(void* lm);
 const float* pxa_lm_last_embedding_relevance(void* lm);

@@ -331,6 +331,13 @@ int pxk_permute_0213(const float* in, float* out, int64_t d0, int64_t d1, int64_
 int pxk_attention_mask_fill(float* scores, const float* key_keep, int64_t batch, int64_t heads, int64_t q_len,
                             int64_t k_len, int causal, int64_t q_offset, int64_t window, float value, void* stream);
 
+/* Device-side token id validation for EmbeddingModule::forward (embedding_module.cpp:48-59, which
+ * reads the ids back to the host): ids_out[i] = llround(ids[i]) (halves away from zero) when that
+ * lies in [0, vocab); otherwise ids_out[i] = 0, so the gather that follows stays inside the table,
+ * and the id is reported. *status (device memory) is set to 0 when every id is valid, else to 1;
+ * it is written on every call (one workgroup, no atomics), so it needs no clearing. */
+int pxk_embedding_ids(const float* ids, int64_t count, int64_t vocab, float* ids_out, int32_t* status, void* stream);
+
 /* ---- seeding ------------------------------------------------------------------------------------
  * On-device LRP seed for a causal LM (src/attnlrp_parity.cpp:104-109 moved to the device): for
  * each sequence n, target[n] = argmax of logits[n, L-1, :] (lowest index on ties) unless targets

@@ -45,6 +45,10 @@ public:
      *         argmax. unit_seed: one-hot seed (LRPSeed::OneHot) instead of the logit value. */
     void explain_device(const float* ids, int64_t n, int64_t l, const LRPRuleConfig& config, float* token_relevance,
                         int64_t* targets, const int64_t* targets_in = nullptr, bool unit_seed = false);
+    /** @brief Whether every id of the last device-side pass was in [0, vocab) (waits for the
+     *         stream). An out-of-range id is gathered as id 0, so its pass completes; the reference
+     *         would have thrown "EmbeddingModule::forward: index out of range [0, num_embeddings)". */
+    [[nodiscard]] bool device_ids_valid() { return embed_.device_ids_valid(); }
     /** @brief Device pointers of the last pass: logits (N*L*V), embedding-level relevance (N*L*d). */
     [[nodiscard]] const float* last_logits() const noexcept;
     [[nodiscard]] const float* last_embedding_relevance() const noexcept { return r_embed_; }

@@ -1,7 +1,7 @@
 /** @file embedding_module.hpp
  *  @brief Token embedding (V, d) (the surface of include/pulsatrix/embedding_module.hpp).
  *         forward() validates ids on the host as the reference does (embedding_module.cpp:48-59);
- *         run_forward_device() takes ids already validated and resident in HBM.
+ *         run_forward_device() takes ids resident in HBM and validates them there.
  */
 #pragma once
 
@@ -25,9 +25,12 @@ public:
     [[nodiscard]] int64_t num_embeddings() const noexcept { return V_; }
     [[nodiscard]] int64_t embedding_dim() const noexcept { return d_; }
 
-    /** @brief Gathers rows for n x l ids (floats holding whole numbers in [0, V)) into a
-     *         module-owned (n*l, d) buffer. */
+    /** @brief Gathers rows for n x l ids (floats, rounded as llround does) into a module-owned
+     *         (n*l, d) buffer. The ids are validated on the device: an id outside [0, V) gathers
+     *         row 0 instead and is reported by device_ids_valid(). */
     const float* run_forward_device(const float* ids, int64_t n, int64_t l);
+    /** @brief Whether every id of the last run_forward_device() was in range (waits for the stream). */
+    [[nodiscard]] bool device_ids_valid();
     /** @brief Per-token sums of a (count, d) relevance into out (count). */
     void token_relevance(const float* relevance, int64_t count, float* out);
 
@@ -39,7 +42,7 @@ private:
     MI355XBackend* be_;
     Tensor weight_;
     Shape last_shape_;
-    detail::DevBuf ids_, out_;
+    detail::DevBuf ids_, out_, ids_checked_, ids_status_;
 };
 
 }  // namespace pulsatrix

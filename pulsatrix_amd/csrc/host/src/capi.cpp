@@ -361,6 +361,13 @@ int pxa_lm_replay(void*) {
     return guarded([&] { backend()->replay(); });
 }
 
+int pxa_lm_check_device_ids(void* handle) {
+    return guarded([&] {
+        if (!static_cast<LmHandle*>(handle)->lm->device_ids_valid())
+            throw std::invalid_argument("EmbeddingModule::forward: index out of range [0, num_embeddings)");
+    });
+}
+
 const float* pxa_lm_last_logits(void* handle) { return static_cast<LmHandle*>(handle)->lm->last_logits(); }
 const float* pxa_lm_last_embedding_relevance(void* handle) {
     return static_cast<LmHandle*>(handle)->lm->last_embedding_relevance();

@@ -175,8 +175,22 @@ const float* EmbeddingModule::run_forward_device(const float* ids, int64_t n, in
     const int64_t count = n * l;
     last_shape_ = Shape({n, l});
     float* out = out_.ensure(be_, count * d_);
-    MI355XBackend::check(pxk_gather_rows(weight_.data(), ids, out, count, d_, be_->stream()), "EmbeddingModule::forward");
+    // The ids are validated on the device (rounded, range-checked, out-of-range ones replaced by 0
+    // and reported through ids_status()); the host never waits for them.
+    float* checked = ids_checked_.ensure(be_, count);
+    auto* status = reinterpret_cast<int32_t*>(ids_status_.ensure(be_, 1));
+    MI355XBackend::check(pxk_embedding_ids(ids, count, num_embeddings(), checked, status, be_->stream()),
+                         "EmbeddingModule::forward");
+    MI355XBackend::check(pxk_gather_rows(weight_.data(), checked, out, count, d_, be_->stream()),
+                         "EmbeddingModule::forward");
     return out;
+}
+
+bool EmbeddingModule::device_ids_valid() {
+    if (ids_status_.size() == 0) return true;
+    int32_t status = 0;
+    be_->copy(&status, ids_status_.data(), sizeof(status), CopyDirection::DeviceToHost);
+    return status == 0;
 }
 
 Tensor EmbeddingModule::forward_impl(const Tensor& input) {

@@ -284,6 +284,21 @@ __global__ void __launch_bounds__(kThreads) gather_kernel(const float* table, co
     }
 }
 
+constexpr int kIdThreads = 1024;
+
+__global__ void __launch_bounds__(kIdThreads) embedding_ids_kernel(const float* ids, int64_t count, int64_t vocab,
+                                                                   float* ids_out, int32_t* status) {
+    int bad = 0;
+    for (int64_t i = threadIdx.x; i < count; i += kIdThreads) {
+        const float r = roundf(ids[i]);  // llround's rounding: halves away from zero
+        const bool ok = r >= 0.0f && r < static_cast<float>(vocab);  // NaN and infinities fail
+        ids_out[i] = ok ? r : 0.0f;
+        bad |= !ok;
+    }
+    bad = __syncthreads_or(bad);
+    if (threadIdx.x == 0) *status = bad ? 1 : 0;
+}
+
 }  // namespace
 }  // namespace pxk
 
@@ -381,6 +396,15 @@ int pxk_column_sums(const float* in, float* out, int64_t rows, int64_t cols, flo
     hipLaunchKernelGGL(column_sums_kernel, dim3(static_cast<unsigned>(cdiv(cols, kThreads))), dim3(kThreads), 0,
                        S(stream), in, out, rows, cols, beta);
     return launched("pxk_column_sums");
+}
+
+int pxk_embedding_ids(const float* ids, int64_t count, int64_t vocab, float* ids_out, int32_t* status, void* stream) {
+    if (count < 0 || vocab <= 0 || vocab > (int64_t{1} << 24))
+        return fail(PXK_ERR_INVALID, "pxk_embedding_ids: count must be >= 0 and vocab in [1, 2^24]");
+    if (!status || (count > 0 && (!ids || !ids_out))) return fail(PXK_ERR_INVALID, "pxk_embedding_ids: NULL operand");
+    hipLaunchKernelGGL(embedding_ids_kernel, dim3(1), dim3(kIdThreads), 0, S(stream), ids, count, vocab, ids_out,
+                       status);
+    return launched("pxk_embedding_ids");
 }
 
 int pxk_gather_rows(const float* table, const float* indices, float* out, int64_t count, int64_t dim, void* stream) {

@@ -111,6 +111,11 @@ class CausalLM:
     def replay(self):
         N.host_check(N.host().pxa_lm_replay(self.h))
 
+    def check_device_ids(self):
+        """Raises PxkError (the reference's out-of-range message) if the last device-side pass saw
+        an id outside [0, vocab)."""
+        N.host_check(N.host().pxa_lm_check_device_ids(self.h))
+
     def last_logits_ptr(self):
         return N.host().pxa_lm_last_logits(self.h)
 

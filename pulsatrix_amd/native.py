@@ -63,6 +63,7 @@ PXK_SIGNATURES = {
     "pxk_copy_2d": "pipiiip",
     "pxk_accumulate_rows": "ppiip",
     "pxk_gather_rows": "pppiip",
+    "pxk_embedding_ids": "piippp",
     "pxk_column_sums": "ppiifp",
     "pxk_rms_norm_forward": "ppppiifp",
     "pxk_softmax_rows": "ppiip",
@@ -235,6 +236,7 @@ def host():
             "pxa_lm_capture_explain": (ctypes.c_int, [c_vp, c_vp, c_i64, c_i64, ctypes.c_float, ctypes.c_int, c_vp,
                                                       c_vp]),
             "pxa_lm_replay": (ctypes.c_int, [c_vp]),
+            "pxa_lm_check_device_ids": (ctypes.c_int, [c_vp]),
             "pxa_lm_last_logits": (c_vp, [c_vp]),
             "pxa_lm_last_embedding_relevance": (c_vp, [c_vp]),
             "pxa_lm_destroy": (None, [c_vp]),

@@ -408,3 +408,23 @@ def test_lm_seed_picks_argmax_and_writes_one_hot():
     for i in range(n):
         ref[i, -1, expect[i]] = logits[i, -1, expect[i]]
     assert np.array_equal(got, ref)
+
+
+@gpu
+def test_embedding_ids_validated_on_device():
+    """pxk_embedding_ids: llround (halves away from zero) and the [0, vocab) range check of
+    embedding_module.cpp:48-59; out-of-range ids become 0 and set the status."""
+    torch = G.torch_cuda()
+    vocab = 50
+    good = np.array([0, 49, 2.5, -0.4, 48.6, 7], np.float32)
+    out, status = G.empty((good.size,)), G.keep(torch.full((1,), 7, dtype=torch.int32, device="cuda"))
+    N.call("pxk_embedding_ids", G.ptr(G.dev(good)), good.size, vocab, G.ptr(out), G.ptr(status), G.stream())
+    assert list(G.host(out)) == [0, 49, 3, 0, 49, 7] and int(status.cpu()[0]) == 0
+    bad = np.array([3, -1, 50, np.nan, np.inf, 49.5, 1e9], np.float32)
+    out = G.empty((bad.size,))
+    N.call("pxk_embedding_ids", G.ptr(G.dev(bad)), bad.size, vocab, G.ptr(out), G.ptr(status), G.stream())
+    assert list(G.host(out)) == [3, 0, 0, 0, 0, 0, 0] and int(status.cpu()[0]) == 1
+    many = np.random.RandomState(3).randint(0, vocab, size=5000).astype(np.float32)
+    out = G.empty((many.size,))
+    N.call("pxk_embedding_ids", G.ptr(G.dev(many)), many.size, vocab, G.ptr(out), G.ptr(status), G.stream())
+    assert np.array_equal(G.host(out), many) and int(status.cpu()[0]) == 0

@@ -214,6 +214,22 @@ def test_explain_device_and_graph_replay_match_host_path():
         assert np.array_equal(G.host(tok), eager)
 
 
+def test_explain_device_reports_out_of_range_ids():
+    """Device-side id validation: a pass with an id outside [0, vocab) completes (the id reads row
+    0) and check_device_ids() raises the reference's message; valid ids pass the check."""
+    torch = G.torch_cuda()
+    cfg = small_lm_config(num_layers=1)
+    lm = models.CausalLM(to_px(cfg), oc.synthetic_params(cfg, 8))
+    ids = np.random.RandomState(6).randint(0, cfg.vocab_size, size=(1, 12)).astype(np.float32)
+    tok, tgt = G.empty((1, 12)), G.keep(torch.empty(1, dtype=torch.int64, device="cuda"))
+    lm.explain_device(G.dev(ids).data_ptr(), 1, 12, LXT_EPS, 1, tok.data_ptr(), tgt.data_ptr())
+    lm.check_device_ids()
+    ids[0, 5] = cfg.vocab_size
+    lm.explain_device(G.dev(ids).data_ptr(), 1, 12, LXT_EPS, 1, tok.data_ptr(), tgt.data_ptr())
+    with pytest.raises(N.PxkError, match="index out of range"):
+        lm.check_device_ids()
+
+
 def test_explain_device_with_given_targets_and_unit_seed():
     torch = G.torch_cuda()
     cfg = small_lm_config(num_layers=1)
