@@ -76,6 +76,11 @@ void pxa_block_destroy(void* block);
 /* ---- CausalLM (causal_lm.hpp) ---- */
 void* pxa_lm_create(const px_model_config* cfg, const float* params);
 void* pxa_lm_create_random(const px_model_config* cfg, uint64_t seed, double stddev);
+/* LoadCausalLM (src/causal_lm.cpp:293-301): config.json and model.safetensors (or the shards of
+ * model.safetensors.index.json) from `directory`, Llama / Qwen2 family; tensor bytes are copied
+ * to HBM as stored and widened (BF16, F16, F8, F64) and transposed there. The model's settings
+ * are written to cfg_out (nullable). NULL on failure, with the message in pxa_last_error(). */
+void* pxa_lm_load(const char* directory, px_model_config* cfg_out);
 /* Host ids (n, l) -> host logits (n, l, vocab) (nullable). CausalLM::forward. */
 int pxa_lm_forward(void* lm, const int64_t* ids, int64_t n, int64_t l, float* logits);
 /* Host seed (n, l, vocab) -> host outputs (each nullable): r_embed (n, l, d) =

@@ -331,6 +331,23 @@ int pxk_permute_0213(const float* in, float* out, int64_t d0, int64_t d1, int64_
 int pxk_attention_mask_fill(float* scores, const float* key_keep, int64_t batch, int64_t heads, int64_t q_len,
                             int64_t k_len, int causal, int64_t q_offset, int64_t window, float value, void* stream);
 
+/* ---- checkpoint loading ----------------------------------------------------------------------
+ * A checkpoint tensor's raw little-endian bytes (already copied to the device) widened to fp32 as
+ * SafetensorsFile::tensor does on the host (src/safetensors.cpp:676-740): BF16 and F16 and both
+ * F8 kinds exactly (subnormals, infinities, NaN), F64 rounded to nearest. With `transpose`, the
+ * (rows x cols) source lands as (cols x rows): the (out, in) -> (in, out) Linear weight transform
+ * of the Hugging Face mapping (src/causal_lm.cpp:257-291, WeightTransform::Transpose). */
+enum {
+    PXK_DTYPE_F32 = 0,
+    PXK_DTYPE_F16 = 1,
+    PXK_DTYPE_BF16 = 2,
+    PXK_DTYPE_F64 = 3,
+    PXK_DTYPE_F8_E4M3 = 4,
+    PXK_DTYPE_F8_E5M2 = 5
+};
+int pxk_convert_weight(const void* src, int dtype, int64_t rows, int64_t cols, int transpose, float* dst,
+                       void* stream);
+
 /* Device-side token id validation for EmbeddingModule::forward (embedding_module.cpp:48-59, which
  * reads the ids back to the host): ids_out[i] = llround(ids[i]) (halves away from zero) when that
  * lies in [0, vocab); otherwise ids_out[i] = 0, so the gather that follows stays inside the table,

@@ -12,6 +12,7 @@
 #include <vector>
 
 #include "pulsatrix/causal_lm.hpp"
+#include "pulsatrix/checkpoint.hpp"
 #include "pulsatrix/mi355x_backend.hpp"
 #include "pulsatrix/transformer_block.hpp"
 
@@ -286,6 +287,36 @@ void* pxa_lm_create_random(const px_model_config* cfg, uint64_t seed, double std
         std::vector<float> params(static_cast<size_t>(total(lm_layout(*cfg))));
         if (pxa_synthetic_params(cfg, 0, seed, stddev, params.data()) != 0) throw std::runtime_error(g_error);
         out = make_lm(*cfg, params.data());
+    });
+    return out;
+}
+
+void* pxa_lm_load(const char* directory, px_model_config* cfg_out) {
+    LmHandle* out = nullptr;
+    guarded([&] {
+        if (directory == nullptr) throw std::invalid_argument("pxa_lm_load: directory is NULL");
+        auto h = std::make_unique<LmHandle>();
+        h->lm = LoadCausalLM(directory, backend());
+        const HfModelConfig& hc = h->lm->config();
+        px_model_config& c = h->cfg;
+        c.vocab_size = hc.vocab_size;
+        c.hidden_size = hc.hidden_size;
+        c.num_layers = hc.num_hidden_layers;
+        c.num_heads = hc.num_attention_heads;
+        c.num_kv_heads = hc.num_key_value_heads;
+        c.head_dim = hc.head_dim;
+        c.intermediate_size = hc.intermediate_size;
+        c.rms_norm_eps = hc.rms_norm_eps;
+        c.rope_theta = hc.rope_theta;
+        c.use_rope = 1;
+        c.rope_rotate_half = 1;
+        c.causal = hc.causal ? 1 : 0;
+        c.qkv_bias = hc.qkv_bias ? 1 : 0;
+        c.out_bias = hc.out_bias ? 1 : 0;
+        c.mlp_bias = hc.mlp_bias ? 1 : 0;
+        c.tie_word_embeddings = hc.tie_word_embeddings ? 1 : 0;
+        if (cfg_out) *cfg_out = c;
+        out = h.release();
     });
     return out;
 }

@@ -70,6 +70,17 @@ class CausalLM:
             raise N.PxkError(h.pxa_last_error().decode())
         self.shape = None
 
+    @classmethod
+    def load(cls, directory):
+        """LoadCausalLM: a Hugging Face checkpoint directory, weights converted on the device."""
+        self = cls.__new__(cls)
+        cfg = N.ModelConfig()
+        self.h = N.host().pxa_lm_load(str(directory).encode(), ctypes.byref(cfg))
+        if not self.h:
+            raise N.PxkError(N.host().pxa_last_error().decode())
+        self.cfg, self.shape = cfg, None
+        return self
+
     def forward(self, ids):
         ids = np.ascontiguousarray(ids, dtype=np.int64)
         n, l = ids.shape

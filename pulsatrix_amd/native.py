@@ -64,6 +64,7 @@ PXK_SIGNATURES = {
     "pxk_accumulate_rows": "ppiip",
     "pxk_gather_rows": "pppiip",
     "pxk_embedding_ids": "piippp",
+    "pxk_convert_weight": "pniinpp",
     "pxk_column_sums": "ppiifp",
     "pxk_rms_norm_forward": "ppppiifp",
     "pxk_softmax_rows": "ppiip",
@@ -229,6 +230,7 @@ def host():
             "pxa_block_destroy": (None, [c_vp]),
             "pxa_lm_create": (c_vp, [cfgp, c_vp]),
             "pxa_lm_create_random": (c_vp, [cfgp, ctypes.c_uint64, ctypes.c_double]),
+            "pxa_lm_load": (c_vp, [ctypes.c_char_p, cfgp]),
             "pxa_lm_forward": (ctypes.c_int, [c_vp, i64p, c_i64, c_i64, c_vp]),
             "pxa_lm_relevance": (ctypes.c_int, [c_vp, c_vp, ctypes.c_float, ctypes.c_int, c_vp, c_vp, c_vp, c_vp]),
             "pxa_lm_explain_device": (ctypes.c_int, [c_vp, c_vp, c_i64, c_i64, ctypes.c_float, ctypes.c_int, c_vp,
