@@ -38,12 +38,12 @@ void SwiGLUModule::pack_weights() {
     if (fused_gate()) {
         // The forward's copy: 32-column blocks alternate gate and up (block 2b = gate features
         // 32b..32b+31, block 2b+1 = the same up features), so one GEMM tile holds both factors of
-        // its hidden features and applies the gate in its epilogue (PXK_EPI_SWIGLU_FWD).
+        // its hidden features and applies the gate in its epilogue (PXK_EPI_SWIGLU_FWD). Seen as
+        // d * F / 32 rows of 32 floats, the source blocks are 32 apart and their places 64 apart,
+        // so each projection is one strided copy.
         float* wi = wgu_il_.ensure(be_, d_ * 2 * F_);
-        for (int64_t b = 0; b < F_ / 32; ++b) {
-            be_->copy_2d(wi + 64 * b, 2 * F_, gate_proj_.weight_data() + 32 * b, F_, d_, 32);
-            be_->copy_2d(wi + 64 * b + 32, 2 * F_, up_proj_.weight_data() + 32 * b, F_, d_, 32);
-        }
+        be_->copy_2d(wi, 64, gate_proj_.weight_data(), 32, d_ * F_ / 32, 32);
+        be_->copy_2d(wi + 32, 64, up_proj_.weight_data(), 32, d_ * F_ / 32, 32);
     }
     packed_version_ = v;
 }
