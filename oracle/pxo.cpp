@@ -16,6 +16,7 @@
 #include <cmath>
 #include <cstdint>
 #include <cstring>
+#include <functional>
 #include <limits>
 #include <memory>
 #include <stdexcept>
@@ -377,10 +378,159 @@ void rope_tables(int64_t hd, float base, int64_t seq, int64_t offset, float* cs,
 
 // ---- modules -------------------------------------------------------------------------------
 
+// LRPRuleConfig (include/pulsatrix/lrp_rule_config.hpp:72-115); rule in LRPRule order.
+enum Rule { kEpsilon = 0, kGamma = 1, kAlphaBeta = 2, kZBox = 3 };
+
 struct RuleConfig {
     float eps;
     bool bias_in_denominator;
+    int rule = kEpsilon;
+    float gamma = 0.25f, alpha = 1.0f, beta = 0.0f, low = 0.0f, high = 1.0f;
 };
+
+// ---- Zennit-compatible affine rules (src/lrp_rules.cpp:13-160) ----------------------------------
+// An affine layer seen abstractly (lrp_rules.hpp:35-52): forward(x, w) -> output-shaped,
+// backward(g, w) -> input-shaped, add_bias(y, b) -> y + b. Each rule is composed from the
+// primitives above in the order lrp_rules.cpp issues them, each step into a fresh zero-filled
+// buffer as the reference's Tensor scratch is.
+struct Affine {
+    size_t n_in = 0, n_out = 0, n_w = 0, n_b = 0;
+    std::function<void(const float*, const float*, float*)> forward, backward, add_bias;
+};
+
+Buf rule_pos(const float* v, size_t n) {  // lrp_rules.cpp:18-22, max(v, 0)
+    Buf out(n, 0.0f);
+    elementwise(0, v, out.data(), n);
+    return out;
+}
+
+Buf rule_neg(const float* v, size_t n) {  // :24-29, v - max(v, 0)
+    Buf out = rule_pos(v, n);
+    axpby(1.0f, v, -1.0f, out.data(), out.data(), n);
+    return out;
+}
+
+Buf rule_plus_scaled(const float* a, float scale, const Buf& b) {  // :31-36, a + scale b
+    Buf out(b.size(), 0.0f);
+    axpby(1.0f, a, scale, b.data(), out.data(), b.size());
+    return out;
+}
+
+Buf rule_affine(const Affine& op, const float* x, const float* w, const float* bias) {  // :38-46
+    Buf out(op.n_out, 0.0f);
+    op.forward(x, w, out.data());
+    if (bias) op.add_bias(out.data(), bias, out.data());
+    return out;
+}
+
+Buf rule_divide(const Affine& op, const float* r, const float* den, const float* gate, int mode, float eps) {  // :48-53
+    Buf out(op.n_out, 0.0f);
+    lrp_stabilized_divide(r, den, gate, out.data(), op.n_out, eps, mode);
+    return out;
+}
+
+// acc = (first ? 0 : acc) + scale * (x_mod * backward(g, w))  (:55-62)
+void rule_term(const Affine& op, const float* x_mod, const float* g, const float* w, float scale, float* acc,
+               bool first) {
+    Buf t(op.n_in, 0.0f);
+    op.backward(g, w, t.data());
+    mul(x_mod, t.data(), t.data(), op.n_in);
+    axpby(scale, t.data(), first ? 0.0f : 1.0f, acc, acc, op.n_in);
+}
+
+void rule_epsilon(const Affine& op, const float* x, const float* w, const float* b, const float* pre, const float* r,
+                  float* r_in, float eps) {  // :64-70
+    Buf z(op.n_out, 0.0f);
+    op.add_bias(pre, b, z.data());
+    const Buf g = rule_divide(op, r, z.data(), nullptr, 0, eps);
+    rule_term(op, x, g.data(), w, 1.0f, r_in, true);
+}
+
+void rule_alpha_beta(const Affine& op, const float* x, const float* w, const float* b, const float* r, float* r_in,
+                     const RuleConfig& c) {  // :72-111
+    const Buf xp = rule_pos(x, op.n_in), xn = rule_neg(x, op.n_in);
+    const Buf wp = rule_pos(w, op.n_w), wn = rule_neg(w, op.n_w);
+    const Buf bp = rule_pos(b, op.n_b), bn = rule_neg(b, op.n_b);
+    Buf zp = rule_affine(op, xp.data(), wp.data(), bp.data());
+    const Buf zp_rest = rule_affine(op, xn.data(), wn.data(), nullptr);
+    add(zp.data(), zp_rest.data(), zp.data(), op.n_out);
+    const Buf gp = rule_divide(op, r, zp.data(), nullptr, 0, c.eps);
+    Buf positive(op.n_in, 0.0f);
+    rule_term(op, xp.data(), gp.data(), wp.data(), 1.0f, positive.data(), true);
+    rule_term(op, xn.data(), gp.data(), wn.data(), 1.0f, positive.data(), false);
+    if (c.beta == 0.0f) {
+        axpby(c.alpha, positive.data(), 0.0f, positive.data(), r_in, op.n_in);
+        return;
+    }
+    Buf zn = rule_affine(op, xp.data(), wn.data(), bn.data());
+    const Buf zn_rest = rule_affine(op, xn.data(), wp.data(), nullptr);
+    add(zn.data(), zn_rest.data(), zn.data(), op.n_out);
+    const Buf gn = rule_divide(op, r, zn.data(), nullptr, 0, c.eps);
+    Buf negative(op.n_in, 0.0f);
+    rule_term(op, xp.data(), gn.data(), wn.data(), 1.0f, negative.data(), true);
+    rule_term(op, xn.data(), gn.data(), wp.data(), 1.0f, negative.data(), false);
+    axpby(c.alpha, positive.data(), -c.beta, negative.data(), r_in, op.n_in);
+}
+
+void rule_gamma(const Affine& op, const float* x, const float* w, const float* b, const float* pre, const float* r,
+                float* r_in, const RuleConfig& c) {  // :113-140
+    const float g = c.gamma;
+    const Buf xp = rule_pos(x, op.n_in), xn = rule_neg(x, op.n_in);
+    const Buf wa = rule_plus_scaled(w, g, rule_pos(w, op.n_w)), wb = rule_plus_scaled(w, g, rule_neg(w, op.n_w));
+    const Buf ba = rule_plus_scaled(b, g, rule_pos(b, op.n_b)), bb = rule_plus_scaled(b, g, rule_neg(b, op.n_b));
+    Buf z(op.n_out, 0.0f);  // the original output selects the pair that explains each unit
+    op.add_bias(pre, b, z.data());
+    Buf den_pos = rule_affine(op, xp.data(), wa.data(), ba.data());
+    const Buf o1 = rule_affine(op, xn.data(), wb.data(), nullptr);
+    add(den_pos.data(), o1.data(), den_pos.data(), op.n_out);
+    Buf den_neg = rule_affine(op, xp.data(), wb.data(), bb.data());
+    const Buf o3 = rule_affine(op, xn.data(), wa.data(), nullptr);
+    add(den_neg.data(), o3.data(), den_neg.data(), op.n_out);
+    const Buf gp = rule_divide(op, r, den_pos.data(), z.data(), 1, c.eps);
+    const Buf gn = rule_divide(op, r, den_neg.data(), z.data(), 2, c.eps);
+    rule_term(op, xp.data(), gp.data(), wa.data(), 1.0f, r_in, true);
+    rule_term(op, xn.data(), gp.data(), wb.data(), 1.0f, r_in, false);
+    rule_term(op, xp.data(), gn.data(), wb.data(), 1.0f, r_in, false);
+    rule_term(op, xn.data(), gn.data(), wa.data(), 1.0f, r_in, false);
+}
+
+void rule_zbox(const Affine& op, const float* x, const float* w, const float* pre, const float* r, float* r_in,
+               const RuleConfig& c) {  // :142-160, constant bounds (no fill_bound for dense layers)
+    const Buf wp = rule_pos(w, op.n_w), wn = rule_neg(w, op.n_w);
+    const Buf lo(op.n_in, c.low), hi(op.n_in, c.high);
+    Buf den(op.n_out, 0.0f);
+    const Buf lo_out = rule_affine(op, lo.data(), wp.data(), nullptr);
+    const Buf hi_out = rule_affine(op, hi.data(), wn.data(), nullptr);
+    axpby(1.0f, pre, -1.0f, lo_out.data(), den.data(), op.n_out);
+    axpby(1.0f, den.data(), -1.0f, hi_out.data(), den.data(), op.n_out);
+    const Buf g = rule_divide(op, r, den.data(), nullptr, 0, c.eps);
+    rule_term(op, x, g.data(), w, 1.0f, r_in, true);
+    rule_term(op, lo.data(), g.data(), wp.data(), -1.0f, r_in, false);
+    rule_term(op, hi.data(), g.data(), wn.data(), -1.0f, r_in, false);
+}
+
+// lrp_rules::validate (:164-176)
+void rule_validate(const RuleConfig& c, const char* module) {
+    if (c.rule < kEpsilon || c.rule > kZBox) throw std::invalid_argument("lrp_rules::apply: unknown LRPRule");
+    if (c.rule != kAlphaBeta) return;
+    if (!(c.alpha >= 0.0f) || !(c.beta >= 0.0f))
+        throw std::invalid_argument(std::string(module) +
+                                    "::propagate_relevance: AlphaBeta rule needs alpha >= 0 and beta >= 0");
+    if (c.alpha - c.beta != 1.0f)
+        throw std::invalid_argument(std::string(module) + "::propagate_relevance: AlphaBeta rule needs alpha - beta == 1");
+}
+
+// lrp_rules::apply (:178-195)
+void rule_apply(const Affine& op, const float* x, const float* w, const float* b, const float* pre, const float* r,
+                float* r_in, const RuleConfig& c) {
+    switch (c.rule) {
+        case kEpsilon: rule_epsilon(op, x, w, b, pre, r, r_in, c.eps); return;
+        case kAlphaBeta: rule_alpha_beta(op, x, w, b, r, r_in, c); return;
+        case kGamma: rule_gamma(op, x, w, b, pre, r, r_in, c); return;
+        case kZBox: rule_zbox(op, x, w, pre, r, r_in, c); return;
+        default: throw std::invalid_argument("lrp_rules::apply: unknown LRPRule");
+    }
+}
 
 // LinearModule (linear_module.cpp:189-228 forward; 333-341 relevance -> lrp_rules::linear,
 // lrp_rules.cpp:197-220). The bias tensor always exists; it is zero when the layer has none
@@ -417,19 +567,23 @@ struct Linear {
     }
 
     Buf relevance(const Buf& r, const RuleConfig& cfg) const {
+        rule_validate(cfg, "LinearModule");
         Buf r_in(static_cast<size_t>(n * in), 0.0f);
         const size_t N = n, I = in, O = out;
-        if (!cfg.bias_in_denominator) {  // legacy pre-bias epsilon rule: the fused lrp_linear
+        if (cfg.rule == kEpsilon && !cfg.bias_in_denominator) {  // legacy pre-bias epsilon rule: lrp_linear
             lrp_linear(x.data(), w.data(), z.data(), r.data(), r_in.data(), N, I, O, cfg.eps);
             return r_in;
         }
-        // epsilon_with_bias (lrp_rules.cpp:64-70): z' = z + b; g = r / stab(z'); r_in = x * (g W^T).
-        Buf zb(N * O), g(N * O), term(N * I);
-        add_row_vector(z.data(), b.data(), zb.data(), N, O);
-        lrp_stabilized_divide(r.data(), zb.data(), nullptr, g.data(), N * O, cfg.eps, 0);
-        gemm_ex(g.data(), false, w.data(), true, term.data(), N, O, I, 0.0f);
-        mul(x.data(), term.data(), term.data(), N * I);
-        axpby(1.0f, term.data(), 0.0f, r_in.data(), r_in.data(), N * I);
+        // lrp_rules::linear (lrp_rules.cpp:197-215): x (N, in) through w (in, out).
+        Affine op;
+        op.n_in = N * I;
+        op.n_out = N * O;
+        op.n_w = I * O;
+        op.n_b = O;
+        op.forward = [=](const float* xs, const float* ws, float* y) { gemm(xs, ws, y, N, I, O); };
+        op.backward = [=](const float* g, const float* ws, float* gx) { gemm_ex(g, false, ws, true, gx, N, O, I, 0.0f); };
+        op.add_bias = [=](const float* y, const float* bb, float* o) { add_row_vector(y, bb, o, N, O); };
+        rule_apply(op, x.data(), w.data(), b.data(), z.data(), r.data(), r_in.data(), cfg);
         return r_in;
     }
 };
@@ -753,17 +907,26 @@ struct LM {
         return logits;
     }
 
-    // TiedLMHeadModule::propagate_relevance (tied_lm_head_module.cpp:76-111): always the
-    // bias-in-denominator epsilon rule against a zero bias.
+    // TiedLMHeadModule::propagate_relevance (tied_lm_head_module.cpp:76-111): the table E (V, d)
+    // as an affine layer x E^T with a zero bias; the pre-bias epsilon rule becomes the
+    // bias-in-denominator one.
     Buf head_relevance(const Buf& r, const RuleConfig& cfg) const {
         const size_t M = N * L, V = c.vocab_size, D = s.d;
         if (!c.tie_word_embeddings) return head.relevance(r, cfg);
-        Buf zero(V, 0.0f), z(M * V), g(M * V), term(M * D), r_in(M * D, 0.0f);
-        add_row_vector(logits.data(), zero.data(), z.data(), M, V);
-        lrp_stabilized_divide(r.data(), z.data(), nullptr, g.data(), M * V, cfg.eps, 0);
-        gemm(g.data(), embed.data(), term.data(), M, V, D);
-        mul(head_x.data(), term.data(), term.data(), M * D);
-        axpby(1.0f, term.data(), 0.0f, r_in.data(), r_in.data(), M * D);
+        rule_validate(cfg, "TiedLMHeadModule");
+        Affine op;
+        op.n_in = M * D;
+        op.n_out = M * V;
+        op.n_w = V * D;
+        op.n_b = V;
+        op.forward = [=](const float* xs, const float* w, float* y) { gemm_ex(xs, false, w, true, y, M, D, V, 0.0f); };
+        op.backward = [=](const float* g, const float* w, float* gx) { gemm(g, w, gx, M, V, D); };
+        op.add_bias = [=](const float* y, const float* bb, float* o) { add_row_vector(y, bb, o, M, V); };
+        RuleConfig rule = cfg;
+        if (rule.rule == kEpsilon) rule.bias_in_denominator = true;
+        const Buf zero(V, 0.0f);
+        Buf r_in(M * D, 0.0f);
+        rule_apply(op, head_x.data(), embed.data(), zero.data(), logits.data(), r.data(), r_in.data(), rule);
         return r_in;
     }
 
@@ -785,6 +948,17 @@ struct LM {
 void token_sums(const float* r, float* out, size_t count, size_t dim) {
     Buf ones(dim, 1.0f);
     gemm_ex(r, false, ones.data(), false, out, count, dim, 1, 0.0f);
+}
+
+RuleConfig rule_config(const px_lrp_rule& r) {
+    RuleConfig c{r.epsilon, r.bias_in_denominator != 0};
+    c.rule = r.rule;
+    c.gamma = r.gamma;
+    c.alpha = r.alpha;
+    c.beta = r.beta;
+    c.low = r.low;
+    c.high = r.high;
+    return c;
 }
 
 template <typename F>
@@ -865,6 +1039,16 @@ int pxo_block_relevance(void* h, const float* r_out, float eps, int bias_in_deno
     });
 }
 
+int pxo_block_relevance_rule(void* h, const float* r_out, const px_lrp_rule* rule, float* r_in) {
+    return guarded([&] {
+        auto* b = static_cast<Block*>(h);
+        if (b->N == 0) throw std::logic_error("TransformerBlock::propagate_relevance: called before any forward()");
+        Buf r(r_out, r_out + b->N * b->L * b->s.d);
+        Buf out = b->relevance(r, rule_config(*rule));
+        std::copy(out.begin(), out.end(), r_in);
+    });
+}
+
 void pxo_block_destroy(void* h) { delete static_cast<Block*>(h); }
 
 void* pxo_lm_create(const px_model_config* cfg, const float* params) {
@@ -900,6 +1084,19 @@ int pxo_lm_relevance(void* h, const float* seed, float eps, int bias_in_denomina
     });
 }
 
+int pxo_lm_relevance_rule(void* h, const float* seed, const px_lrp_rule* rule, float* r_embed, float* r_tokens,
+                          float* key_rel, float* value_rel) {
+    return guarded([&] {
+        LM* m = static_cast<LM*>(h);
+        if (m->N == 0) throw std::logic_error("CausalLM::propagate_relevance_by_layer: called before any forward()");
+        const size_t rows = static_cast<size_t>(m->N * m->L);
+        Buf s(seed, seed + rows * m->c.vocab_size);
+        Buf r = m->relevance(s, rule_config(*rule), key_rel, value_rel);
+        if (r_embed) std::copy(r.begin(), r.end(), r_embed);
+        if (r_tokens) token_sums(r.data(), r_tokens, rows, m->s.d);
+    });
+}
+
 void pxo_lm_destroy(void* h) { delete static_cast<LM*>(h); }
 
 int pxo_linear_forward(const float* x, const float* w, const float* bias, int64_t n, int64_t in, int64_t out,
@@ -926,6 +1123,26 @@ int pxo_linear_relevance(const float* x, const float* w, const float* bias, cons
         lin.z.assign(pre_bias, pre_bias + n * out);
         Buf rr(r, r + n * out);
         Buf res = lin.relevance(rr, RuleConfig{eps, bias_in_denominator != 0});
+        std::copy(res.begin(), res.end(), r_in);
+    });
+}
+
+int pxo_linear_relevance_rule(const float* x, const float* w, const float* bias, const float* pre_bias,
+                              const float* r, int64_t n, int64_t in, int64_t out, const px_lrp_rule* rule,
+                              float* r_in) {
+    return guarded([&] {
+        Linear lin;
+        lin.in = in;
+        lin.out = out;
+        lin.n = n;
+        lin.has_bias = bias != nullptr;
+        lin.w.assign(w, w + in * out);
+        lin.b.assign(static_cast<size_t>(out), 0.0f);
+        if (bias) lin.b.assign(bias, bias + out);
+        lin.x.assign(x, x + n * in);
+        lin.z.assign(pre_bias, pre_bias + n * out);
+        Buf rr(r, r + n * out);
+        Buf res = lin.relevance(rr, rule_config(*rule));
         std::copy(res.begin(), res.end(), r_in);
     });
 }

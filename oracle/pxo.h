@@ -43,6 +43,19 @@ typedef struct px_model_config {
     int32_t reserved;
 } px_model_config;
 
+/* LRPRuleConfig (include/pulsatrix/lrp_rule_config.hpp:72-115): rule in LRPRule order
+ * (0 Epsilon, 1 Gamma, 2 AlphaBeta, 3 ZBox); epsilon is every rule's stabilizer. */
+typedef struct px_lrp_rule {
+    float epsilon;
+    int32_t rule;
+    float gamma;
+    float alpha;
+    float beta;
+    float low;
+    float high;
+    int32_t bias_in_denominator;
+} px_lrp_rule;
+
 const char* pxo_last_error(void);
 void pxo_set_threads(int threads); /* GEMM worker threads; <= 0 restores hardware_concurrency() */
 int pxo_get_threads(void);
@@ -58,6 +71,7 @@ int64_t pxo_block_param_count(const px_model_config* cfg);
 void* pxo_block_create(const px_model_config* cfg, const float* params);
 int pxo_block_forward(void* h, const float* x, int64_t n, int64_t l, float* y);
 int pxo_block_relevance(void* h, const float* r_out, float eps, int bias_in_denominator, float* r_in);
+int pxo_block_relevance_rule(void* h, const float* r_out, const px_lrp_rule* rule, float* r_in);
 void pxo_block_destroy(void* h);
 
 /* ---- CausalLM (src/causal_lm.cpp) ---- */
@@ -69,6 +83,10 @@ int pxo_lm_forward(void* h, const int64_t* ids, int64_t n, int64_t l, float* log
  * (layers, n*l, kv_heads*head_dim). */
 int pxo_lm_relevance(void* h, const float* seed, float eps, int bias_in_denominator, float* r_embed,
                      float* r_tokens, float* key_rel, float* value_rel);
+/* The same under any rule: the config reaches every Linear and the head, as the reference's modules
+ * pass it down (the attention, SwiGLU and residual rules read only its epsilon). */
+int pxo_lm_relevance_rule(void* h, const float* seed, const px_lrp_rule* rule, float* r_embed, float* r_tokens,
+                          float* key_rel, float* value_rel);
 void pxo_lm_destroy(void* h);
 
 /* ---- Single Linear layer (src/linear_module.cpp + src/lrp_rules.cpp) ---- */
@@ -76,6 +94,11 @@ int pxo_linear_forward(const float* x, const float* w, const float* bias, int64_
                        float* pre_bias, float* y);
 int pxo_linear_relevance(const float* x, const float* w, const float* bias, const float* pre_bias, const float* r,
                          int64_t n, int64_t in, int64_t out, float eps, int bias_in_denominator, float* r_in);
+/* LinearModule::propagate_relevance under any rule (lrp_rules::linear, lrp_rules.cpp:197-215); bias may
+ * be NULL (a zero bias, as a bias-free layer holds). */
+int pxo_linear_relevance_rule(const float* x, const float* w, const float* bias, const float* pre_bias,
+                              const float* r, int64_t n, int64_t in, int64_t out, const px_lrp_rule* rule,
+                              float* r_in);
 
 /* ---- CPUBackend primitives (src/cpu_backend.cpp) ---- */
 void pxo_gemm(const float* a, const float* b, float* out, size_t m, size_t k, size_t n);

@@ -110,6 +110,18 @@ LRPRuleConfig rule(float eps, int bias_in_denominator) {
     return r;
 }
 
+LRPRuleConfig rule_of(const px_lrp_rule& p) {
+    LRPRuleConfig r{p.epsilon};
+    r.rule = static_cast<LRPRule>(p.rule);
+    r.gamma = p.gamma;
+    r.alpha = p.alpha;
+    r.beta = p.beta;
+    r.low = p.low;
+    r.high = p.high;
+    r.epsilon_bias_in_denominator = p.bias_in_denominator != 0;
+    return r;
+}
+
 }  // namespace
 
 extern "C" {
@@ -142,13 +154,21 @@ int pxr_block_forward(void* h, const float* x, int64_t n, int64_t l, float* y) {
     });
 }
 
-int pxr_block_relevance(void* h, const float* r_out, float eps, int bias_in_denominator, float* r_in) {
+static int block_relevance(void* h, const float* r_out, const LRPRuleConfig& cfg, float* r_in) {
     return guarded([&] {
         auto* b = static_cast<RefBlock*>(h);
         Tensor r(Shape({b->n, b->l, b->d}), &b->be, std::vector<float>(r_out, r_out + b->n * b->l * b->d));
-        const std::vector<float> out = b->block->propagate_relevance(r, rule(eps, bias_in_denominator)).to_host_vector();
+        const std::vector<float> out = b->block->propagate_relevance(r, cfg).to_host_vector();
         std::copy(out.begin(), out.end(), r_in);
     });
+}
+
+int pxr_block_relevance(void* h, const float* r_out, float eps, int bias_in_denominator, float* r_in) {
+    return block_relevance(h, r_out, rule(eps, bias_in_denominator), r_in);
+}
+
+int pxr_block_relevance_rule(void* h, const float* r_out, const px_lrp_rule* r, float* r_in) {
+    return block_relevance(h, r_out, rule_of(*r), r_in);
 }
 
 void pxr_block_destroy(void* h) { delete static_cast<RefBlock*>(h); }
@@ -198,13 +218,12 @@ int pxr_lm_forward(void* h, const int64_t* ids, int64_t n, int64_t l, float* log
     });
 }
 
-int pxr_lm_relevance(void* h, const float* seed, float eps, int bias_in_denominator, float* r_embed, float* r_tokens,
-                     float* key_rel, float* value_rel) {
+static int lm_relevance(void* h, const float* seed, const LRPRuleConfig& cfg, float* r_embed, float* r_tokens, float* key_rel,
+                 float* value_rel) {
     return guarded([&] {
         auto* m = static_cast<RefLM*>(h);
         const int64_t V = m->c.vocab_size;
         Tensor s(Shape({m->n, m->l, V}), &m->be, std::vector<float>(seed, seed + m->n * m->l * V));
-        const LRPRuleConfig cfg = rule(eps, bias_in_denominator);
         const std::vector<Tensor> bounds = m->lm->propagate_relevance_by_layer(s, cfg);
         if (r_embed) {
             const std::vector<float> e = bounds.front().to_host_vector();
@@ -229,6 +248,16 @@ int pxr_lm_relevance(void* h, const float* seed, float eps, int bias_in_denomina
     });
 }
 
+int pxr_lm_relevance(void* h, const float* seed, float eps, int bias_in_denominator, float* r_embed, float* r_tokens,
+                     float* key_rel, float* value_rel) {
+    return lm_relevance(h, seed, rule(eps, bias_in_denominator), r_embed, r_tokens, key_rel, value_rel);
+}
+
+int pxr_lm_relevance_rule(void* h, const float* seed, const px_lrp_rule* r, float* r_embed, float* r_tokens,
+                          float* key_rel, float* value_rel) {
+    return lm_relevance(h, seed, rule_of(*r), r_embed, r_tokens, key_rel, value_rel);
+}
+
 void pxr_lm_destroy(void* h) { delete static_cast<RefLM*>(h); }
 
 int pxr_linear_relevance(const float* x, const float* w, const float* bias, const float* r, int64_t n, int64_t in,
@@ -241,6 +270,20 @@ int pxr_linear_relevance(const float* x, const float* w, const float* bias, cons
         (void)lin.forward(Tensor(Shape({n, in}), &be, std::vector<float>(x, x + n * in)));
         Tensor rr(Shape({n, out}), &be, std::vector<float>(r, r + n * out));
         const std::vector<float> res = lin.propagate_relevance(rr, rule(eps, bias_in_denominator)).to_host_vector();
+        std::copy(res.begin(), res.end(), r_in);
+    });
+}
+
+int pxr_linear_relevance_rule(const float* x, const float* w, const float* bias, const float* r, int64_t n, int64_t in,
+                              int64_t out, const px_lrp_rule* rl, float* r_in) {
+    return guarded([&] {
+        CPUBackend be;
+        LinearModule lin(in, out, &be, bias != nullptr);
+        lin.set_weight(std::vector<float>(w, w + in * out));
+        if (bias) lin.set_bias(std::vector<float>(bias, bias + out));
+        (void)lin.forward(Tensor(Shape({n, in}), &be, std::vector<float>(x, x + n * in)));
+        Tensor rr(Shape({n, out}), &be, std::vector<float>(r, r + n * out));
+        const std::vector<float> res = lin.propagate_relevance(rr, rule_of(*rl)).to_host_vector();
         std::copy(res.begin(), res.end(), r_in);
     });
 }

@@ -9,6 +9,9 @@ What it takes, all data (no source text):
     relevance (LXT 2.1) -- copied byte for byte from tests/fixtures/hf_tiny/.
   * lxt_values.json: the float vectors pasted into tests/lrp_reference_test.cpp (kMhaLogits,
     kMhaRelevance, kBlockLogits, kBlockRelevance), parsed out of the file's array literals.
+  * zennit_values.json: the same file's Zennit 1.0.0 MLP input relevance (kMlpEpsilon1e6,
+    kMlpEpsilon025, kMlpZPlus, kMlpAlphaBeta21, kMlpGamma025, kMlpEpsilonPlus,
+    kMlpEpsilonAlpha2Beta1, kMlpEpsilonGammaBox).
 """
 import json
 import os
@@ -34,19 +37,29 @@ def copy_hf_tiny():
                 shutil.copyfile(p, os.path.join(dst, f))
 
 
-def extract_lxt_values():
+def extract_vectors(names, filename):
     text = open(os.path.join(REF, "tests", "lrp_reference_test.cpp")).read()
     out = {}
-    for name in ("kMhaLogits", "kMhaRelevance", "kBlockLogits", "kBlockRelevance"):
+    for name in names:
         m = re.search(r"const std::vector<float> %s = \{([^}]*)\};" % name, text)
         if m is None:
             raise RuntimeError("missing " + name)
         out[name] = [float(v.strip().rstrip("f")) for v in m.group(1).split(",") if v.strip()]
-    with open(os.path.join(HERE, "lxt_values.json"), "w") as f:
+    with open(os.path.join(HERE, filename), "w") as f:
         json.dump(out, f, indent=1)
+
+
+def extract_lxt_values():
+    extract_vectors(("kMhaLogits", "kMhaRelevance", "kBlockLogits", "kBlockRelevance"), "lxt_values.json")
+
+
+def extract_zennit_values():
+    extract_vectors(("kMlpEpsilon1e6", "kMlpEpsilon025", "kMlpZPlus", "kMlpAlphaBeta21", "kMlpGamma025",
+                     "kMlpEpsilonPlus", "kMlpEpsilonAlpha2Beta1", "kMlpEpsilonGammaBox"), "zennit_values.json")
 
 
 if __name__ == "__main__":
     copy_hf_tiny()
     extract_lxt_values()
+    extract_zennit_values()
     print("fixtures written under", HERE)

@@ -46,6 +46,29 @@ class ModelConfig(ctypes.Structure):
         return self.head_dim if self.head_dim > 0 else self.hidden_size // self.num_heads
 
 
+EPSILON, GAMMA, ALPHA_BETA, ZBOX = 0, 1, 2, 3  # LRPRule order (include/pulsatrix/lrp_rule_config.hpp)
+
+
+class LrpRule(ctypes.Structure):
+    """px_lrp_rule (oracle/pxo.h, include/pulsatrix_amd.h): LRPRuleConfig's fields."""
+
+    _fields_ = [
+        ("epsilon", ctypes.c_float),
+        ("rule", ctypes.c_int32),
+        ("gamma", ctypes.c_float),
+        ("alpha", ctypes.c_float),
+        ("beta", ctypes.c_float),
+        ("low", ctypes.c_float),
+        ("high", ctypes.c_float),
+        ("bias_in_denominator", ctypes.c_int32),
+    ]
+
+
+def lrp_rule(rule=EPSILON, epsilon=1e-6, gamma=0.25, alpha=1.0, beta=0.0, low=0.0, high=1.0,
+             bias_in_denominator=False):
+    return LrpRule(epsilon, rule, gamma, alpha, beta, low, high, int(bias_in_denominator))
+
+
 def model_config(**kw):
     base = dict(vocab_size=0, hidden_size=0, num_layers=1, num_heads=1, num_kv_heads=0, head_dim=0,
                 intermediate_size=0, rms_norm_eps=1e-5, rope_theta=10000.0, use_rope=1, rope_rotate_half=1,
@@ -110,6 +133,9 @@ class _Lib:
             ("lm_relevance", ctypes.c_int, [ctypes.c_void_p, _f32p, ctypes.c_float, ctypes.c_int, _f32p, _f32p, _f32p,
                                             _f32p]),
             ("lm_destroy", None, [ctypes.c_void_p]),
+            ("block_relevance_rule", ctypes.c_int, [ctypes.c_void_p, _f32p, ctypes.POINTER(LrpRule), _f32p]),
+            ("lm_relevance_rule", ctypes.c_int, [ctypes.c_void_p, _f32p, ctypes.POINTER(LrpRule), _f32p, _f32p,
+                                                 _f32p, _f32p]),
             ("last_error", ctypes.c_char_p, []),
         ]:
             fn = getattr(L, prefix + name)
@@ -152,6 +178,12 @@ class _Block:
         self.lib.check(self.lib.fn("block_relevance")(self.h, fptr(r), eps, int(bias_in_denominator), fptr(out)))
         return out
 
+    def relevance_rule(self, r, rule):
+        r = np.ascontiguousarray(r, dtype=np.float32)
+        out = np.empty_like(r)
+        self.lib.check(self.lib.fn("block_relevance_rule")(self.h, fptr(r), ctypes.byref(rule), fptr(out)))
+        return out
+
     def __del__(self):
         if getattr(self, "h", None):
             self.lib.fn("block_destroy")(self.h)
@@ -186,6 +218,19 @@ class _LM:
         v = np.empty(kv, dtype=np.float32) if want_kv else None
         self.lib.check(self.lib.fn("lm_relevance")(self.h, fptr(seed), eps, int(bias_in_denominator), fptr(r_embed),
                                                     fptr(r_tok), fptr(k), fptr(v)))
+        return (r_embed, r_tok, k, v) if want_kv else (r_embed, r_tok)
+
+    def relevance_rule(self, seed, rule, want_kv=False):
+        n, l = self.shape
+        c = self.cfg
+        seed = np.ascontiguousarray(seed, dtype=np.float32)
+        r_embed = np.empty((n, l, c.hidden_size), dtype=np.float32)
+        r_tok = np.empty((n, l), dtype=np.float32)
+        kv = (c.num_layers, n * l, c.kv_heads() * c.hd())
+        k = np.empty(kv, dtype=np.float32) if want_kv else None
+        v = np.empty(kv, dtype=np.float32) if want_kv else None
+        self.lib.check(self.lib.fn("lm_relevance_rule")(self.h, fptr(seed), ctypes.byref(rule), fptr(r_embed),
+                                                         fptr(r_tok), fptr(k), fptr(v)))
         return (r_embed, r_tok, k, v) if want_kv else (r_embed, r_tok)
 
     def __del__(self):
@@ -271,4 +316,34 @@ def linear_relevance(x, w, b, pre, r, eps, bias_in_denominator):
                                            ctypes.c_int64, ctypes.c_float, ctypes.c_int, _f32p]
     L.check(L.lib.pxo_linear_relevance(fptr(x), fptr(w), fptr(bb), fptr(pre), fptr(r), n, i, o, eps,
                                        int(bias_in_denominator), fptr(out)))
+    return out
+
+
+def linear_relevance_rule(x, w, b, pre, r, rule):
+    """Oracle LinearModule::propagate_relevance under `rule` (an LrpRule)."""
+    x, w, pre, r = (np.ascontiguousarray(a, dtype=np.float32) for a in (x, w, pre, r))
+    n, i = x.shape
+    o = w.shape[1]
+    out = np.empty((n, i), np.float32)
+    bb = None if b is None else np.ascontiguousarray(b, dtype=np.float32)
+    L = oracle()
+    L.lib.pxo_linear_relevance_rule.argtypes = [_f32p, _f32p, _f32p, _f32p, _f32p, ctypes.c_int64, ctypes.c_int64,
+                                                ctypes.c_int64, ctypes.POINTER(LrpRule), _f32p]
+    L.check(L.lib.pxo_linear_relevance_rule(fptr(x), fptr(w), fptr(bb), fptr(pre), fptr(r), n, i, o,
+                                            ctypes.byref(rule), fptr(out)))
+    return out
+
+
+def ref_linear_relevance_rule(x, w, b, r, rule):
+    """The compiled reference's LinearModule (forward, then propagate_relevance under `rule`)."""
+    R = ref()
+    x, w, r = (np.ascontiguousarray(a, dtype=np.float32) for a in (x, w, r))
+    n, i = x.shape
+    o = w.shape[1]
+    out = np.empty((n, i), np.float32)
+    bb = None if b is None else np.ascontiguousarray(b, dtype=np.float32)
+    R.lib.pxr_linear_relevance_rule.argtypes = [_f32p, _f32p, _f32p, _f32p, ctypes.c_int64, ctypes.c_int64,
+                                                ctypes.c_int64, ctypes.POINTER(LrpRule), _f32p]
+    R.check(R.lib.pxr_linear_relevance_rule(fptr(x), fptr(w), fptr(bb), fptr(r), n, i, o, ctypes.byref(rule),
+                                            fptr(out)))
     return out
