@@ -3,6 +3,7 @@
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--mode graph|eager] [--no-cpu-baseline]
     python bench.py --op-sweep        # raw op sweep: GEMM shapes, elementwise 2^26, RMSNorm 32768 x 2048
     python bench.py --kernel-probe    # 256 MiB copy + LM-head relevance GEMM, for rocprofv3 --pmc runs
+    python bench.py --rule gamma      # the same step under Zennit's Gamma(0.25) (or zplus, alpha2beta1, zbox)
 
 Workload: the SmolLM2-135M-shaped causal LM (30 layers, hidden 576, 9 query / 3 KV heads of 64,
 SwiGLU FFN 1536, vocab 49152, tied embeddings, RMSNorm eps 1e-5, RoPE theta 100000), fp32,
@@ -45,10 +46,27 @@ S_CONFIG = dict(vocab_size=49152, hidden_size=576, num_layers=30, num_heads=9, n
                 causal=1, qkv_bias=0, out_bias=0, mlp_bias=0, tie_word_embeddings=1, reserved=0)
 BATCH, SEQ, SEED = 1, 512, 1234
 
+# The rules --rule selects (LRPRuleConfig fields; LRPRule order 0 Epsilon, 1 Gamma, 2 AlphaBeta, 3 ZBox):
+# LXT's AttnLRP (the default, and the headline metric) and Zennit's affine rules at their usual settings.
+RULES = {
+    "lxt": dict(rule=0, epsilon=LXT_EPS, bias_in_denominator=True),
+    "gamma": dict(rule=1, epsilon=1e-6, gamma=0.25),
+    "zplus": dict(rule=2, epsilon=1e-6, alpha=1.0, beta=0.0),
+    "alpha2beta1": dict(rule=2, epsilon=1e-6, alpha=2.0, beta=1.0),
+    "zbox": dict(rule=3, epsilon=1e-6, low=-3.0, high=3.0),
+}
 
-def gemm_flops_per_sequence(c, L, causal_effective):
+
+# GEMM work of one Linear's relevance relative to its forward GEMM, per rule: epsilon one transposed
+# GEMM; Gamma and AlphaBeta the reference's eight (four denominators, four backward products: here a
+# 2in x 2out stacked GEMM each way); ZBox two backward products (its denominator reuses x W).
+LINEAR_RELEVANCE_GEMMS = {"lxt": 1, "gamma": 8, "zplus": 8, "alpha2beta1": 8, "zbox": 2}
+
+
+def gemm_flops_per_sequence(c, L, causal_effective, linear_factor=1):
     """Algorithmic GEMM FLOPs of one forward + AttnLRP pass (dense L^2 attention squares, as the
-    reference computes them; causal_effective counts only the lower triangle)."""
+    reference computes them; causal_effective counts only the lower triangle); linear_factor scales
+    each Linear's and the head's relevance GEMMs (LINEAR_RELEVANCE_GEMMS)."""
     d, H, Hkv, D, F, V, layers = (c["hidden_size"], c["num_heads"], c["num_kv_heads"], c["head_dim"],
                                   c["intermediate_size"], c["vocab_size"], c["num_layers"])
     qd, kvd = H * D, Hkv * D
@@ -59,14 +77,17 @@ def gemm_flops_per_sequence(c, L, causal_effective):
         att = att * (L + 1) / (2 * L)
     head = 2 * L * d * V
     fwd = layers * (proj + mlp + att) + head
-    rel = layers * (proj + mlp + 2 * att) + head  # Linear-transposed GEMMs; both bilinear shares of each product
+    # Linear-relevance GEMMs; both bilinear shares of each attention product
+    rel = layers * (linear_factor * (proj + mlp) + 2 * att) + linear_factor * head
     return fwd + rel
 
 
-def time_cpu_baseline(cfg_fields, seq):
+def time_cpu_baseline(cfg_fields, seq, rule_name="lxt"):
     """Reference CPUBackend on the host cores, 1 and 3 layers, extrapolated to the full depth."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import oracle_ctypes as oc
+
+    rule = oc.lrp_rule(**RULES[rule_name])
 
     lib, kind = oc.ref(), "reference"
     if lib is None:
@@ -83,7 +104,7 @@ def time_cpu_baseline(cfg_fields, seq):
         seed = np.zeros_like(logits)
         t = int(np.argmax(logits[0, -1]))
         seed[0, -1, t] = logits[0, -1, t]
-        lm.relevance(seed, LXT_EPS, True)
+        lm.relevance_rule(seed, rule)
         times[layers] = time.perf_counter() - t0
         del lm
     per_layer = (times[3] - times[1]) / 2.0
@@ -290,6 +311,8 @@ def main():
                     help="only launch a 256 MiB copy and the LM-head relevance GEMM, 5 times each (for rocprofv3 --pmc)")
     ap.add_argument("--op-sweep", action="store_true",
                     help="time the raw op sweep (GEMM shapes, elementwise over 2^26, RMSNorm 32768 x 2048) instead")
+    ap.add_argument("--rule", choices=sorted(RULES), default="lxt",
+                    help="the LRP rule of the relevance pass (default: LXT's AttnLRP epsilon rule, the headline)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one MI355X (the path runs on one GPU; --gpus %d is not supported)"
@@ -319,15 +342,17 @@ def main():
     torch.cuda.synchronize()
     stream = torch.cuda.ExternalStream(models.stream())
 
+    rule = N.lrp_rule(**RULES[args.rule])
+
     def eager_step():
-        lm.explain_device(ids.data_ptr(), BATCH, SEQ, LXT_EPS, 1, tok.data_ptr(), tgt.data_ptr())
+        lm.explain_device_rule(ids.data_ptr(), BATCH, SEQ, rule, tok.data_ptr(), tgt.data_ptr())
 
     for _ in range(max(1, args.warmup)):
         eager_step()
     models.synchronize()
     step = eager_step
     if args.mode == "graph":
-        lm.capture_explain(ids.data_ptr(), BATCH, SEQ, LXT_EPS, 1, tok.data_ptr(), tgt.data_ptr())
+        lm.capture_explain_rule(ids.data_ptr(), BATCH, SEQ, rule, tok.data_ptr(), tgt.data_ptr())
         step = lm.replay
         for _ in range(max(1, args.warmup)):
             step()
@@ -354,8 +379,9 @@ def main():
 
     tokens = BATCH * SEQ * args.steps
     value = tokens / wall
-    flops_dense = gemm_flops_per_sequence(fields, SEQ, False) * BATCH
-    flops_causal = gemm_flops_per_sequence(fields, SEQ, True) * BATCH
+    lf = LINEAR_RELEVANCE_GEMMS[args.rule]
+    flops_dense = gemm_flops_per_sequence(fields, SEQ, False, lf) * BATCH
+    flops_causal = gemm_flops_per_sequence(fields, SEQ, True, lf) * BATCH
 
     # ---- roofline of the dominant GEMM kernel, HIP events on the backend's stream ---------------
     desc, flops, keep = head_relevance_gemm(torch, N, fields, SEQ)
@@ -367,6 +393,11 @@ def main():
     tile_name = {N.TILE_128x128: "128x128", N.TILE_64x64: "64x64", N.TILE_32x64: "32x64", N.TILE_32x32: "32x32",
                  N.TILE_32x64_DIRECT: "32x64 direct", N.TILE_32x32_DIRECT: "32x32 direct"}[tile]
 
+    rule_text = {"lxt": "LxtAttnLrpConfig: eps 1e-9, bias in denominator",
+                 "gamma": "Gamma(0.25) on every Linear and the head, eps 1e-6 elsewhere",
+                 "zplus": "ZPlus (AlphaBeta 1, 0) on every Linear and the head, eps 1e-6 elsewhere",
+                 "alpha2beta1": "AlphaBeta(2, 1) on every Linear and the head, eps 1e-6 elsewhere",
+                 "zbox": "ZBox(-3, 3) on every Linear and the head, eps 1e-6 elsewhere"}[args.rule]
     out = {
         "metric": "forward+AttnLRP tokens/s, 135M-shape LM seq 512; GEMM % fp32 MFMA peak",
         "value": round(value, 2),
@@ -381,8 +412,8 @@ def main():
         "dtype": "fp32",
         "data": "synthetic: random-init N(0,0.02) weights from seed %d, uniform-random token ids" % SEED,
         "config": {
-            "workload": "SmolLM2-135M-shaped causal LM forward + AttnLRP (LxtAttnLrpConfig: eps 1e-9, bias in "
-                        "denominator), argmax seed at the last position, batch 1 x seq 512",
+            "workload": "SmolLM2-135M-shaped causal LM forward + AttnLRP (%s), argmax seed at the last "
+                        "position, batch 1 x seq 512" % rule_text,
             "layers": fields["num_layers"], "hidden": 576, "heads": "9/3", "head_dim": 64, "ffn": 1536,
             "vocab": 49152, "tied": True, "rope_theta": 100000.0, "global_batch": BATCH, "seq_len": SEQ,
             "parallelism": "single GPU", "mode": args.mode,
@@ -414,7 +445,7 @@ def main():
     }
     del keep, keep2
     if not args.no_cpu_baseline:
-        out["cpu_baseline"] = time_cpu_baseline(fields, SEQ)
+        out["cpu_baseline"] = time_cpu_baseline(fields, SEQ, args.rule)
         out["gpu_vs_cpu"] = round(value / out["cpu_baseline"]["value"], 1)
     print(json.dumps(out), flush=True)
 

@@ -49,6 +49,21 @@ typedef struct px_model_config {
     int32_t reserved;
 } px_model_config;
 
+/* LRPRuleConfig (include/pulsatrix/lrp_rule_config.hpp:72-115): rule in LRPRule order (0 Epsilon,
+ * 1 Gamma, 2 AlphaBeta, 3 ZBox); epsilon is every rule's stabilizer. The config reaches every
+ * Linear and the head, as the reference's modules pass it down; the attention, SwiGLU and residual
+ * rules read only its epsilon. */
+typedef struct px_lrp_rule {
+    float epsilon;
+    int32_t rule;
+    float gamma;
+    float alpha;
+    float beta;
+    float low;
+    float high;
+    int32_t bias_in_denominator;
+} px_lrp_rule;
+
 const char* pxa_last_error(void);
 int pxa_device_count(void);
 
@@ -71,7 +86,15 @@ int pxa_synthetic_params(const px_model_config* cfg, int block, uint64_t seed, d
 void* pxa_block_create(const px_model_config* cfg, const float* params);
 int pxa_block_forward(void* block, const float* x, int64_t n, int64_t l, float* y);
 int pxa_block_relevance(void* block, const float* r_out, float eps, int bias_in_denominator, float* r_in);
+int pxa_block_relevance_rule(void* block, const float* r_out, const px_lrp_rule* rule, float* r_in);
 void pxa_block_destroy(void* block);
+
+/* ---- LinearModule (linear_module.hpp) ; host tensors ----
+ * x (n, in) through w (in, out) and bias (out, nullable: a layer without a bias) on the device,
+ * then LinearModule::propagate_relevance of r (n, out) under `rule` into r_in (n, in); y (n, out,
+ * nullable) receives the forward output. */
+int pxa_linear_relevance_rule(const float* x, const float* w, const float* bias, int64_t n, int64_t in, int64_t out,
+                              const float* r, const px_lrp_rule* rule, float* y, float* r_in);
 
 /* ---- CausalLM (causal_lm.hpp) ---- */
 void* pxa_lm_create(const px_model_config* cfg, const float* params);
@@ -88,6 +111,8 @@ int pxa_lm_forward(void* lm, const int64_t* ids, int64_t n, int64_t l, float* lo
  * (layers, n*l, Hkv*D) = MultiHeadAttentionModule::key_relevance() / value_relevance(). */
 int pxa_lm_relevance(void* lm, const float* seed, float eps, int bias_in_denominator, float* r_embed,
                      float* r_tokens, float* key_rel, float* value_rel);
+int pxa_lm_relevance_rule(void* lm, const float* seed, const px_lrp_rule* rule, float* r_embed, float* r_tokens,
+                          float* key_rel, float* value_rel);
 /* The device hot path (CausalLM::explain_device): ids (n*l floats) in HBM -> forward, argmax (or
  * targets_in, host, n entries, nullable) seed at each sequence's last position, relevance, per-token
  * sums into token_rel (n*l, HBM) and targets (n int64, HBM). Asynchronous on pxa_backend_stream(). */
@@ -96,6 +121,11 @@ int pxa_lm_explain_device(void* lm, const float* ids, int64_t n, int64_t l, floa
 /* Captures one pxa_lm_explain_device call into a HIP graph (no launch); pxa_lm_replay runs it. */
 int pxa_lm_capture_explain(void* lm, const float* ids, int64_t n, int64_t l, float eps, int bias_in_denominator,
                            float* token_rel, int64_t* targets);
+/* The same two under any rule. */
+int pxa_lm_explain_device_rule(void* lm, const float* ids, int64_t n, int64_t l, const px_lrp_rule* rule,
+                               float* token_rel, int64_t* targets, const int64_t* targets_in, int unit_seed);
+int pxa_lm_capture_explain_rule(void* lm, const float* ids, int64_t n, int64_t l, const px_lrp_rule* rule,
+                                float* token_rel, int64_t* targets);
 int pxa_lm_replay(void* lm);
 /* After a device-side pass (explain or replay): 0 when every id was in [0, vocab), else -1 with
  * the reference's message ("EmbeddingModule::forward: index out of range [0, num_embeddings)") in

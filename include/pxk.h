@@ -233,7 +233,8 @@ int pxk_attention_forward(const float* q, int64_t ldq, const float* k, int64_t l
 typedef struct pxk_attn_rel_desc {
     int64_t n, l, heads, kv_heads, head_dim;
     float scale, eps;
-    int32_t causal, rope, rope_half, reserved;
+    int32_t causal, rope, rope_half;
+    int32_t relevance_only; /* 1: g = the RoPE rule's r_q itself, no q_proj denominator (z may be NULL) */
     const float* spv;
     int64_t ld_spv;
     const float* v;
@@ -300,6 +301,7 @@ typedef struct pxk_attn_rel_kv_desc {
     float* g_k;
     float* g_v;
     int64_t ld_g;
+    int32_t relevance_only; /* 1: g_k = key_rel and g_v = value_rel themselves (z_k, z_v may be NULL) */
 } pxk_attn_rel_kv_desc;
 int pxk_attention_relevance_kv(const pxk_attn_rel_kv_desc* d, void* stream);
 
@@ -315,11 +317,13 @@ int pxk_attention_softmax(const float* raw, float* p, int64_t slices, int64_t l,
  * over whole rows (0 where masked). s may alias r_attn. */
 int pxk_attention_lrp_scores(const float* r_attn, const float* p, const float* raw, float* s, int64_t slices,
                              int64_t l, float scale, float eps, int causal, void* stream);
-/* RoPE of the packed projections (rope_module.cpp:104-121 + permute-free layout): q_out (rows x H*D),
- * k_out (rows x Hkv*D) from q/k columns of `in` (row stride ld_in), positions = row % seq_len. */
-int pxk_rope_qk(const float* q_in, const float* k_in, int64_t ld_in, float* q_out, float* k_out, const float* cos_t,
-                const float* sin_t, int64_t rows, int64_t seq_len, int64_t heads, int64_t kv_heads, int64_t head_dim,
-                int rotate_half, void* stream);
+/* RoPE of the packed projections (rope_module.cpp:104-121 + permute-free layout): q_out (rows x H*D)
+ * and k_out (rows x Hkv*D), both with row stride ld_out, from the q/k columns of `in` (row stride
+ * ld_in), positions = row % seq_len. The attention forward's rotation where head_dim does not tile
+ * the projection GEMM's epilogue. */
+int pxk_rope_qk(const float* q_in, const float* k_in, int64_t ld_in, float* q_out, float* k_out, int64_t ld_out,
+                const float* cos_t, const float* sin_t, int64_t rows, int64_t seq_len, int64_t heads, int64_t kv_heads,
+                int64_t head_dim, int rotate_half, void* stream);
 /* DeviceBackend::rope_rotate (:568) and lrp_rope (:652) over (slices, seq_len, head_dim). */
 int pxk_rope_rotate(const float* in, const float* cos_t, const float* sin_t, float* out, int64_t slices,
                     int64_t seq_len, int64_t head_dim, int inverse, int rotate_half, void* stream);
@@ -330,6 +334,67 @@ int pxk_permute_0213(const float* in, float* out, int64_t d0, int64_t d1, int64_
 /* DeviceBackend::attention_mask_fill (:592) */
 int pxk_attention_mask_fill(float* scores, const float* key_keep, int64_t batch, int64_t heads, int64_t q_len,
                             int64_t k_len, int causal, int64_t q_offset, int64_t window, float value, void* stream);
+
+/* ---- Zennit-compatible affine rules ------------------------------------------------------------
+ * Gamma, AlphaBeta and ZBox for a dense layer y = x W + b with W (in x out), as lrp_rules::apply
+ * defines them (lrp_rules.cpp:72-160; stab(z) = z + eps sign z, x+ = max(x, 0), x- = x - x+):
+ *   Gamma:     Wa = W + g W+, Wb = W + g W-, ba = b + g b+, bb = b + g b-, z = x W + b;
+ *              gp = [z > 0] R / stab(x+ Wa + x- Wb + ba), gn = [z < 0] R / stab(x+ Wb + x- Wa + bb);
+ *              R_in = x+ (gp Wa^T + gn Wb^T) + x- (gp Wb^T + gn Wa^T)
+ *   AlphaBeta: as Gamma with Wa = W+, Wb = W-, ba = b+, bb = b-, no gate, gp scaled by alpha and gn
+ *              by -beta (R_in = alpha * positive - beta * negative)
+ *   ZBox:      den = x W - low 1 W+ - high 1 W-; g = R / stab(den);
+ *              R_in = x (g W^T) - g (low W+ + high W-)^T
+ * Each becomes two MFMA GEMMs over weights stacked once per layer (pxk_lrp_rule_weights):
+ *   Gamma / AlphaBeta: W2 (2in x 2out) = [[Wa, Wb], [Wb, Wa]], b2 = [ba | bb];
+ *                      den = [x+ | x-] W2 (pxk_lrp_sign_split, then pxk_gemm), g from den
+ *                      (pxk_lrp_rule_divide), C = g W2^T (2in wide), R_in from C (pxk_lrp_rule_combine)
+ *   ZBox:              W2 (2in x out) = [W ; low W+ + high W-], b2 = [low 1 W+ | high 1 W-] (column
+ *                      sums in the reference's order); den from the cached x W and b2, C = g W2^T
+ * Every rule is independent per output column, so one call covers column-packed layers (q | k | v,
+ * gate | up) and gives the sum of their input relevances. Replaces lrp_rules::apply's composition
+ * of relu / axpby / gemm / add_row_vector / lrp_stabilized_divide / mul calls for LinearModule
+ * (lrp_rules.cpp:197-215) and TiedLMHeadModule (tied_lm_head_module.cpp:76-111). */
+enum { PXK_RULE_GAMMA = 1, PXK_RULE_ALPHA_BETA = 2, PXK_RULE_ZBOX = 3 }; /* LRPRule order */
+
+typedef struct pxk_rule_params {
+    int32_t rule;
+    float eps, gamma, alpha, beta, low, high;
+} pxk_rule_params;
+
+/* One column block of a layer's W (in x cols): W[i][j] = w[i * ld + j], or w[j * ld + i] when
+ * trans (the tied head reads the embedding table, vocab x hidden, in place). bias (cols) may be
+ * NULL (a zero bias). */
+typedef struct pxk_rule_block {
+    const float* w;
+    int64_t ld;
+    int64_t cols;
+    int32_t trans;
+    const float* bias;
+} pxk_rule_block;
+
+/* W2 and b2 for the layer whose columns are the blocks in order (out = the sum of their cols):
+ * W2 holds 2in x 2out floats (Gamma, AlphaBeta) or 2in x out (ZBox), b2 2 * out. */
+int pxk_lrp_rule_weights(const pxk_rule_params* p, const pxk_rule_block* blocks, int nblocks, int64_t in,
+                         float* w2, float* b2, void* stream);
+/* out (rows x 2in, row stride 2in) = [x+ | x-] of x (rows x in, row stride ldx). */
+int pxk_lrp_sign_split(const float* x, int64_t ldx, int64_t rows, int64_t in, float* out, void* stream);
+/* The rule's gated quotients over rows x out outputs. r[m][j % r_cols] (row stride ldr) is the
+ * output relevance, so r_cols < out repeats one relevance over several column blocks (the gate and
+ * up projections of a SwiGLU both receive the product's share). Gamma / AlphaBeta: den (rows x 2out,
+ * stride ld_den) from the den GEMM, g (rows x 2out, may alias den); z (pre-bias x W, stride ldz) and
+ * bias (nullable) give Gamma's gate. ZBox: den is not read, g is rows x out from z and b2. */
+int pxk_lrp_rule_divide(const pxk_rule_params* p, const float* r, int64_t ldr, int64_t r_cols, const float* den,
+                        int64_t ld_den, const float* z, int64_t ldz, const float* bias, const float* b2, int64_t rows,
+                        int64_t out, float* g, int64_t ldg, void* stream);
+/* R_in from C (rows x 2in, stride ldc) and x: Gamma / AlphaBeta x+ C[:, :in] + x- C[:, in:],
+ * ZBox x C[:, :in] - C[:, in:]; then + add (nullable). Without a split, r_in receives it. With
+ * split_sum given, it is the relevance of the residual sum s = a + b (lrp_residual_split,
+ * lrp_math.hpp:33-38): r_in = (a / stab(s)) R, r_b = (b / stab(s)) R. Every operand has row
+ * stride ld. */
+int pxk_lrp_rule_combine(int rule, const float* x, int64_t ldx, const float* c, int64_t ldc, const float* add,
+                         int64_t rows, int64_t in, float* r_in, int64_t ld, const float* split_a,
+                         const float* split_b, const float* split_sum, float* r_b, float eps, void* stream);
 
 /* ---- checkpoint loading ----------------------------------------------------------------------
  * A checkpoint tensor's raw little-endian bytes (already copied to the device) widened to fp32 as

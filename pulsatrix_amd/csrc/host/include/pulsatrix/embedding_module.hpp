@@ -20,8 +20,14 @@ public:
     [[nodiscard]] Tensor propagate_relevance(const Tensor& relevance_out, const LRPRuleConfig& config) override;
 
     void set_weight(const std::vector<float>& values);
-    [[nodiscard]] Tensor& weight() noexcept { return weight_; }
+    /** @brief Mutable access counts as a change (the tied head's rule weights are rebuilt). */
+    [[nodiscard]] Tensor& weight() noexcept {
+        ++version_;
+        return weight_;
+    }
     [[nodiscard]] const Tensor& weight() const noexcept { return weight_; }
+    [[nodiscard]] const float* weight_data() const noexcept { return weight_.data(); }
+    [[nodiscard]] uint64_t version() const noexcept { return version_; }
     [[nodiscard]] int64_t num_embeddings() const noexcept { return V_; }
     [[nodiscard]] int64_t embedding_dim() const noexcept { return d_; }
 
@@ -41,6 +47,7 @@ private:
     int64_t V_, d_;
     MI355XBackend* be_;
     Tensor weight_;
+    uint64_t version_ = 0;
     Shape last_shape_;
     detail::DevBuf ids_, out_, ids_checked_, ids_status_;
 };

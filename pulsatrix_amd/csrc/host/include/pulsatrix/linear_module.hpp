@@ -7,6 +7,7 @@
 #include <vector>
 
 #include "pulsatrix/detail/fused.hpp"
+#include "pulsatrix/detail/rules.hpp"
 #include "pulsatrix/module.hpp"
 
 namespace pulsatrix {
@@ -16,7 +17,8 @@ public:
     LinearModule(int64_t in_features, int64_t out_features, DeviceBackend* backend, bool use_bias = true);
 
     /** @brief Epsilon rule, pre-bias or bias-in-denominator (linear_module.cpp:333-341,
-     *         lrp_rules.cpp:197-220), as one fused MFMA GEMM: x * ((r / stab(z [+ b])) W^T). */
+     *         lrp_rules.cpp:197-220), as one fused MFMA GEMM: x * ((r / stab(z [+ b])) W^T);
+     *         Gamma, AlphaBeta and ZBox (lrp_rules.cpp:72-160) over stacked-weight GEMMs. */
     [[nodiscard]] Tensor propagate_relevance(const Tensor& relevance_out, const LRPRuleConfig& config) override;
 
     void set_weight(const std::vector<float>& values);
@@ -57,6 +59,7 @@ private:
     const float* x_ = nullptr;
     int64_t rows_ = 0;
     detail::DevBuf x_copy_, z_, y_, r_in_;
+    detail::AffineRule rule_;
 };
 
 }  // namespace pulsatrix

@@ -1,8 +1,11 @@
 /** @file lrp_rule_config.hpp
- *  @brief LRP rule configuration (the surface of include/pulsatrix/lrp_rule_config.hpp:72-115).
+ *  @brief LRP rule configuration (the surface of include/pulsatrix/lrp_rule_config.hpp:15-115).
  *
- *  The MI355X path implements the epsilon rule in both of Pulsatrix's forms: the pre-bias rule
- *  (the default) and the bias-in-denominator rule LXT and Zennit use. Other rules throw.
+ *  The MI355X path runs every rule the reference defines for the causal LM's affine layers:
+ *  epsilon in both of Pulsatrix's forms (pre-bias, the default, and bias-in-denominator as LXT and
+ *  Zennit use it) on the fused GEMMs, and Zennit's Gamma, AlphaBeta and ZBox (lrp_rules.cpp:72-160)
+ *  over stacked-weight GEMMs. The attention, SwiGLU and residual rules read only `epsilon`, as in
+ *  the reference.
  */
 #pragma once
 
@@ -10,7 +13,19 @@
 
 namespace pulsatrix {
 
-enum class LRPRule { Epsilon, AlphaBeta, Gamma, ZBox };
+/** @brief The reference's LRPRule, in its declaration order (lrp_rule_config.hpp:21-35). */
+enum class LRPRule { Epsilon, Gamma, AlphaBeta, ZBox };
+
+/** @brief Lower-case rule name (lrp_rule_config.hpp:52-64). */
+inline std::string lrp_rule_name(LRPRule rule) {
+    switch (rule) {
+        case LRPRule::Epsilon: return "epsilon";
+        case LRPRule::Gamma: return "gamma";
+        case LRPRule::AlphaBeta: return "alpha_beta";
+        case LRPRule::ZBox: return "zbox";
+    }
+    return "unknown";
+}
 
 struct LRPRuleConfig {
     float epsilon = 1e-6f;
@@ -31,8 +46,5 @@ inline LRPRuleConfig LxtAttnLrpConfig() {
     config.layer_norm_detach_std = true;
     return config;
 }
-
-/** @brief Throws std::invalid_argument unless the config is an epsilon rule (the one this path runs). */
-void require_epsilon_rule(const LRPRuleConfig& config, const char* module_name);
 
 }  // namespace pulsatrix

@@ -81,7 +81,7 @@ private:
     void ensure_tables(int64_t l);
     void run_attention_unfused(const float* q, int64_t ldq, const float* k, int64_t ldk, const float* v, int64_t n,
                                int64_t l);
-    void relevance_scores_unfused(const float* spv, float eps, bool bid);
+    void relevance_scores_unfused(const float* spv, float eps, bool bid, bool rel_only);
 
     AttentionConfig config_;
     int64_t d_, H_, Hkv_, D_;
@@ -94,7 +94,8 @@ private:
     int64_t N_ = 0, L_ = 0;
     const float* x_ = nullptr;
     detail::DevBuf x_copy_, qkv_z_, qkv_y_, qk_rot_, raw_, p_, ctx_, out_z_, out_y_;
-    detail::DevBuf spv_, ra_, g_, r_in_;
+    detail::DevBuf spv_, ra_, g_, r_in_, rctx_;
+    detail::AffineRule out_rule_, qkv_rule_;
     Tensor key_rel_, value_rel_;
     bool has_relevance_ = false;
 };

@@ -35,6 +35,8 @@ protected:
 
 private:
     void pack_weights();
+    const float* run_relevance_rule(const float* relevance_out, const LRPRuleConfig& config, const float* add,
+                                    const detail::ResidualSplit& split);
     /** @brief The forward applies the gate in the gate/up GEMM's epilogue (no bias, F a multiple of 32). */
     [[nodiscard]] bool fused_gate() const noexcept { return !use_bias_ && F_ % 32 == 0; }
 
@@ -48,6 +50,7 @@ private:
     const float* x_ = nullptr;
     Shape last_shape_;
     detail::DevBuf x_copy_, gu_z_, gu_y_, gate_post_, hidden_, down_z_, down_y_, g_, r_in_;
+    detail::AffineRule down_rule_, gate_up_rule_;
 };
 
 }  // namespace pulsatrix

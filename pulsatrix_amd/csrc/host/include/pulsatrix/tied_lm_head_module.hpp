@@ -3,9 +3,11 @@
  *         include/pulsatrix/tied_lm_head_module.hpp). Relevance is the bias-in-denominator
  *         epsilon rule against a zero bias (tied_lm_head_module.cpp:76-111): one split-K MFMA
  *         GEMM with the divide by stab(logits) in its prologue and the multiply by x in its epilogue.
+ *         Gamma, AlphaBeta and ZBox run on W = E^T over stacked-weight GEMMs.
  */
 #pragma once
 
+#include "pulsatrix/detail/rules.hpp"
 #include "pulsatrix/embedding_module.hpp"
 
 namespace pulsatrix {
@@ -31,6 +33,7 @@ private:
     const float* x_ = nullptr;
     Shape last_in_shape_, last_out_shape_;
     detail::DevBuf x_copy_, logits_, r_in_;
+    detail::AffineRule rule_;
 };
 
 }  // namespace pulsatrix

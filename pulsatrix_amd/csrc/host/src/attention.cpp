@@ -126,6 +126,9 @@ const float* MultiHeadAttentionModule::run_forward(const float* x, int64_t n, in
     float* y = config_.qkv_bias ? qkv_y_.ensure(be_, M * w3) : z;
     const int64_t rw = qd + kvd;  // row length of the rotated q | k block
     float* rot = config_.use_rope ? qk_rot_.ensure(be_, M * rw) : nullptr;
+    // The ROPE_FWD epilogue needs whole heads inside the GEMM's 128-wide tiles; other head_dims
+    // rotate in a second launch.
+    const bool rope_in_gemm = config_.use_rope && (w3 <= 128 || 128 % D_ == 0);
     {
         pxk_gemm_desc d = gemm_desc(l, w3, d_);
         d.batch = n;
@@ -137,7 +140,7 @@ const float* MultiHeadAttentionModule::run_forward(const float* x, int64_t n, in
             d.c2 = mat(y, w3, l * w3);
             d.e_bias = mat(bqkv_.data(), 0);
         }
-        if (config_.use_rope) {
+        if (rope_in_gemm) {
             d.epilogue = PXK_EPI_ROPE_FWD;
             d.c3 = mat(rot, rw, l * rw);
             d.cos_t = cos_.data();
@@ -148,6 +151,10 @@ const float* MultiHeadAttentionModule::run_forward(const float* x, int64_t n, in
         }
         be_->run_gemm(d);
     }
+    if (config_.use_rope && !rope_in_gemm)
+        MI355XBackend::check(pxk_rope_qk(y, y + qd, w3, rot, rot + qd, rw, cos_.data(), sin_.data(), M, l, H_, Hkv_, D_,
+                                         config_.rope_layout == RoPELayout::RotateHalf, st),
+                             "MultiHeadAttentionModule::forward (RoPE)");
     const float* q = config_.use_rope ? rot : y;
     const float* k = config_.use_rope ? rot + qd : y + qd;
     const float* v = y + qd + kvd;
@@ -226,9 +233,12 @@ void MultiHeadAttentionModule::run_attention_unfused(const float* q, int64_t ldq
 
 const float* MultiHeadAttentionModule::run_relevance(const float* relevance_out, const LRPRuleConfig& config,
                                                      const float* add, const detail::ResidualSplit& split) {
-    require_epsilon_rule(config, "MultiHeadAttentionModule");
     if (x_ == nullptr)
         throw std::logic_error("MultiHeadAttentionModule::propagate_relevance: called before any forward()");
+    detail::validate_rule(config, "LinearModule");  // the projections validate it (linear_module.cpp:342)
+    // Gamma / AlphaBeta / ZBox reach the four projections; the bilinear, softmax and RoPE rules
+    // read only epsilon (multihead_attention_module.cpp:404-485).
+    const bool affine = detail::is_affine_rule(config);
     const int64_t n = N_, l = L_, M = n * l, qd = H_ * D_, kvd = Hkv_ * D_, w3 = qd + 2 * kvd, grp = H_ / Hkv_;
     const int64_t LL = l * l;
     const bool causal = config_.causal, bid = config.epsilon_bias_in_denominator;
@@ -245,7 +255,15 @@ const float* MultiHeadAttentionModule::run_relevance(const float* relevance_out,
     // 1. out_proj epsilon rule; its epilogue forms the P V bilinear factor
     //    s_pv = r_ctx / (2 ctx + eps sign ctx) with r_ctx = ctx * (g W_o^T).
     float* spv = spv_.ensure(be_, M * qd);
-    {
+    if (affine) {
+        // r_ctx under the rule, then the P V bilinear factor s_pv = r_ctx / (2 ctx + eps sign ctx).
+        float* rctx = rctx_.ensure(be_, M * qd);
+        const float* bo = config_.out_bias ? out_proj_.bias_data() : nullptr;
+        out_rule_.run(be_, config, out_proj_.version(), {{out_proj_.weight_data(), d_, d_, false, bo}},
+                      {ctx_.data(), qd, M, qd, out_z_.data(), d_, bo, relevance_out, d_, d_, rctx, nullptr});
+        MI355XBackend::check(pxk_lrp_bilinear_scale(rctx, ctx_.data(), spv, M * qd, eps, st),
+                             "MultiHeadAttentionModule::propagate_relevance");
+    } else {
         pxk_gemm_desc d = gemm_desc(M, qd, d_);
         d.trans_b = 1;
         d.prologue = PXK_PRO_DIV_STAB;
@@ -261,7 +279,8 @@ const float* MultiHeadAttentionModule::run_relevance(const float* relevance_out,
     }
     float* ra = ra_.ensure(be_, n * H_ * LL);  // r_attn, then the Q K^T factor s
     const float* p = p_.data();
-    float* g = g_.ensure(be_, M * w3);  // [g_q | g_k | g_v]: relevance / stab(z) per projection
+    // [g_q | g_k | g_v]: relevance / stab(z) per projection, or the relevances themselves under a rule
+    float* g = g_.ensure(be_, M * w3);
     if (!key_rel_.data() || key_rel_.numel() != M * kvd) {
         key_rel_ = Tensor::uninitialized(Shape({M, kvd}), be_);
         value_rel_ = Tensor::uninitialized(Shape({M, kvd}), be_);
@@ -300,9 +319,10 @@ const float* MultiHeadAttentionModule::run_relevance(const float* relevance_out,
         rd.sin_t = sin_.data();
         rd.g = g;
         rd.ld_g = w3;
+        rd.relevance_only = affine;
         MI355XBackend::check(pxk_attention_relevance_q(&rd, st), "MultiHeadAttentionModule::propagate_relevance");
     } else {
-        relevance_scores_unfused(spv, eps, bid);
+        relevance_scores_unfused(spv, eps, bid, affine);
     }
     // 5-6. key and value shares per KV head, summed over its query heads, fused:
     //      r_k = K * sum_h s_qk_h^T Q_h with the RoPE rule, r_v = V * sum_h P_h^T s_pv_h, and the
@@ -343,11 +363,19 @@ const float* MultiHeadAttentionModule::run_relevance(const float* relevance_out,
         kd.g_k = g + qd;
         kd.g_v = g + qd + kvd;
         kd.ld_g = w3;
+        kd.relevance_only = affine;
         MI355XBackend::check(pxk_attention_relevance_kv(&kd, st), "MultiHeadAttentionModule::propagate_relevance (k/v)");
     }
     // 7. the three projections' input relevance in one GEMM: x * ([g_q | g_k | g_v] [Wq | Wk | Wv]^T).
     float* r_in = r_in_.ensure(be_, M * d_);
-    {
+    if (affine) {  // the rule over the packed q | k | v projections: the sum of their input relevances
+        const bool qb = config_.qkv_bias;
+        qkv_rule_.run(be_, config, packed_version_,
+                      {{q_proj_.weight_data(), qd, qd, false, qb ? q_proj_.bias_data() : nullptr},
+                       {k_proj_.weight_data(), kvd, kvd, false, qb ? k_proj_.bias_data() : nullptr},
+                       {v_proj_.weight_data(), kvd, kvd, false, qb ? v_proj_.bias_data() : nullptr}},
+                      {x_, d_, M, d_, z, w3, qb ? bqkv_.data() : nullptr, g, w3, w3, r_in, add}, split);
+    } else {
         pxk_gemm_desc d = gemm_desc(M, d_, w3);
         d.trans_b = 1;
         d.epilogue = PXK_EPI_MUL_X;
@@ -365,7 +393,7 @@ const float* MultiHeadAttentionModule::run_relevance(const float* relevance_out,
 
 // Steps 2-4 of run_relevance as GEMM and row-kernel launches: head_dim outside
 // pxk_attention_supported().
-void MultiHeadAttentionModule::relevance_scores_unfused(const float* spv, float eps, bool bid) {
+void MultiHeadAttentionModule::relevance_scores_unfused(const float* spv, float eps, bool bid, bool rel_only) {
     const int64_t n = N_, l = L_, qd = H_ * D_, kvd = Hkv_ * D_, w3 = qd + 2 * kvd, grp = H_ / Hkv_, LL = l * l;
     const bool causal = config_.causal;
     const float* z = qkv_z_.data();
@@ -406,6 +434,10 @@ void MultiHeadAttentionModule::relevance_scores_unfused(const float* spv, float 
         d.a = mat(ra, l, H_ * LL, LL);
         d.b = mat(k, ldk, l * ldk, D_, grp);
         d.c2 = mat(g, w3, l * w3, D_);
+        if (rel_only) {  // the relevance itself into g; the divided copy lands in scratch
+            d.c = mat(g, w3, l * w3, D_);
+            d.c2 = mat(rctx_.ensure(be_, n * l * qd), qd, l * qd, D_);
+        }
         d.z = mat(z, w3, l * w3, D_);
         if (bq) d.e_bias = mat(bq, 0, 0, D_);
         if (config_.use_rope) {

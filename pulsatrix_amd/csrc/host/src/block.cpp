@@ -107,12 +107,13 @@ const float* SwiGLUModule::run_forward(const float* x, int64_t rows, const float
 
 const float* SwiGLUModule::run_relevance(const float* relevance_out, const LRPRuleConfig& config, const float* add,
                                          const detail::ResidualSplit& split) {
-    require_epsilon_rule(config, "SwiGLUModule");
     if (x_ == nullptr) throw std::logic_error("SwiGLUModule::propagate_relevance: called before any forward()");
+    detail::validate_rule(config, "LinearModule");  // the projections validate it (linear_module.cpp:342)
     const bool bid = config.epsilon_bias_in_denominator;
     const int64_t rows = rows_, f2 = 2 * F_;
     const float* gz = gu_z_.data();
     const float* gy = use_bias_ ? gu_y_.data() : gz;
+    if (detail::is_affine_rule(config)) return run_relevance_rule(relevance_out, config, add, split);
     float* g = g_.ensure(be_, rows * f2);
     {  // down projection's rule, Eq. 15's gate * up split and both projections' denominators
         pxk_gemm_desc d = gemm_desc(rows, F_, d_);
@@ -150,6 +151,32 @@ const float* SwiGLUModule::run_relevance(const float* relevance_out, const LRPRu
         detail::apply_split(d, split, d_, config.epsilon);
         be_->run_gemm(d);
     }
+    return split.requested() ? nullptr : r_in;
+}
+
+// Gamma / AlphaBeta / ZBox (swiglu_module.cpp:139-170): the down projection's rule, Eq. 15's
+// share of gate * up for both factors, then the rule over the packed gate | up projections with
+// that one share as the relevance of both halves.
+const float* SwiGLUModule::run_relevance_rule(const float* relevance_out, const LRPRuleConfig& config,
+                                              const float* add, const detail::ResidualSplit& split) {
+    const int64_t rows = rows_, f2 = 2 * F_;
+    const float* gz = gu_z_.data();
+    const float* gy = use_bias_ ? gu_y_.data() : gz;
+    void* st = be_->stream();
+    float* rh = g_.ensure(be_, rows * f2);  // r_hidden, then the product's share
+    float* up = rh + rows * F_;             // the up projection's output, contiguous
+    const float* bd = use_bias_ ? down_proj_.bias_data() : nullptr;
+    down_rule_.run(be_, config, down_proj_.version(), {{down_proj_.weight_data(), d_, d_, false, bd}},
+                   {hidden_.data(), F_, rows, F_, down_z_.data(), d_, bd, relevance_out, d_, d_, rh, nullptr});
+    be_->copy_2d(up, F_, gy + F_, f2, static_cast<size_t>(rows), static_cast<size_t>(F_));
+    MI355XBackend::check(pxk_lrp_bilinear_elementwise(gate_post_.data(), up, rh, rh, rows * F_, config.epsilon, st),
+                         "SwiGLUModule::propagate_relevance");
+    float* r_in = r_in_.ensure(be_, rows * d_);
+    const float* bg = use_bias_ ? gate_proj_.bias_data() : nullptr;
+    const float* bu = use_bias_ ? up_proj_.bias_data() : nullptr;
+    gate_up_rule_.run(be_, config, gate_proj_.version() + up_proj_.version(),
+                      {{gate_proj_.weight_data(), F_, F_, false, bg}, {up_proj_.weight_data(), F_, F_, false, bu}},
+                      {x_, d_, rows, d_, gz, f2, use_bias_ ? bgu_.data() : nullptr, rh, F_, F_, r_in, add}, split);
     return split.requested() ? nullptr : r_in;
 }
 

@@ -4,6 +4,7 @@
 #include <hip/hip_runtime_api.h>
 
 #include <cmath>
+#include <functional>
 #include <memory>
 #include <mutex>
 #include <stdexcept>
@@ -166,6 +167,66 @@ LRPRuleConfig rule(float eps, int bias_in_denominator) {
     return r;
 }
 
+LRPRuleConfig rule(const px_lrp_rule* p) {
+    if (p == nullptr) throw std::invalid_argument("LRP rule config is NULL");
+    if (p->rule < 0 || p->rule > 3) throw std::invalid_argument("unknown LRPRule " + std::to_string(p->rule));
+    LRPRuleConfig r{p->epsilon};
+    r.rule = static_cast<LRPRule>(p->rule);
+    r.gamma = p->gamma;
+    r.alpha = p->alpha;
+    r.beta = p->beta;
+    r.low = p->low;
+    r.high = p->high;
+    r.epsilon_bias_in_denominator = p->bias_in_denominator != 0;
+    return r;
+}
+
+void capture(const std::function<void()>& work) {
+    MI355XBackend* be = backend();
+    be->begin_capture();
+    try {
+        work();
+    } catch (...) {
+        try {
+            be->end_capture();
+        } catch (...) {
+        }
+        throw;
+    }
+    be->end_capture();
+}
+
+void block_relevance(void* handle, const float* r_out, const LRPRuleConfig& cfg, float* r_in) {
+    auto* h = static_cast<BlockHandle*>(handle);
+    if (h->n == 0) throw std::logic_error("TransformerBlock::propagate_relevance: called before any forward()");
+    const int64_t count = h->n * h->l * h->d;
+    Tensor r(Shape({h->n, h->l, h->d}), backend(), std::vector<float>(r_out, r_out + count));
+    const std::vector<float> out = h->block->propagate_relevance(r, cfg).to_host_vector();
+    std::copy(out.begin(), out.end(), r_in);
+}
+
+void lm_relevance(void* handle, const float* seed, const LRPRuleConfig& cfg, float* r_embed, float* r_tokens,
+                  float* key_rel, float* value_rel) {
+    auto* h = static_cast<LmHandle*>(handle);
+    if (h->n == 0) throw std::logic_error("CausalLM::propagate_relevance_by_layer: called before any forward()");
+    CausalLM& lm = *h->lm;
+    const px_model_config& c = h->cfg;
+    const int64_t count = h->n * h->l * c.vocab_size;
+    Tensor s(Shape({h->n, h->l, c.vocab_size}), backend(), std::vector<float>(seed, seed + count));
+    const std::vector<Tensor> bounds = lm.propagate_relevance_by_layer(s, cfg);
+    auto to_host = [](const Tensor& t, float* dst) {
+        const std::vector<float> v = t.to_host_vector();
+        std::copy(v.begin(), v.end(), dst);
+    };
+    if (r_embed) to_host(bounds.front(), r_embed);
+    if (r_tokens) to_host(lm.embed_tokens().propagate_relevance(bounds.front(), cfg), r_tokens);
+    const int64_t kv = h->n * h->l * kv_heads(c) * head_dim(c);
+    for (int64_t i = 0; i < lm.num_layers(); ++i) {
+        if (key_rel) to_host(lm.layer(i).mha().key_relevance(), key_rel + i * kv);
+        if (value_rel) to_host(lm.layer(i).mha().value_relevance(), value_rel + i * kv);
+    }
+}
+
 }  // namespace
 
 extern "C" {
@@ -263,13 +324,29 @@ int pxa_block_forward(void* handle, const float* x, int64_t n, int64_t l, float*
 }
 
 int pxa_block_relevance(void* handle, const float* r_out, float eps, int bias_in_denominator, float* r_in) {
+    return guarded([&] { block_relevance(handle, r_out, rule(eps, bias_in_denominator), r_in); });
+}
+
+int pxa_block_relevance_rule(void* handle, const float* r_out, const px_lrp_rule* p, float* r_in) {
+    return guarded([&] { block_relevance(handle, r_out, rule(p), r_in); });
+}
+
+int pxa_linear_relevance_rule(const float* x, const float* w, const float* bias, int64_t n, int64_t in, int64_t out,
+                              const float* r, const px_lrp_rule* p, float* y, float* r_in) {
     return guarded([&] {
-        auto* h = static_cast<BlockHandle*>(handle);
-        if (h->n == 0) throw std::logic_error("TransformerBlock::propagate_relevance: called before any forward()");
-        const int64_t count = h->n * h->l * h->d;
-        Tensor r(Shape({h->n, h->l, h->d}), backend(), std::vector<float>(r_out, r_out + count));
-        const std::vector<float> out = h->block->propagate_relevance(r, rule(eps, bias_in_denominator)).to_host_vector();
-        std::copy(out.begin(), out.end(), r_in);
+        const LRPRuleConfig cfg = rule(p);
+        LinearModule layer(in, out, backend(), bias != nullptr);
+        layer.set_weight(std::vector<float>(w, w + in * out));
+        if (bias) layer.set_bias(std::vector<float>(bias, bias + out));
+        const std::vector<float> xs(x, x + n * in);
+        const Tensor fy = layer.forward(Tensor(Shape({n, in}), backend(), xs));
+        if (y) {
+            const std::vector<float> v = fy.to_host_vector();
+            std::copy(v.begin(), v.end(), y);
+        }
+        const Tensor rr(Shape({n, out}), backend(), std::vector<float>(r, r + n * out));
+        const std::vector<float> v = layer.propagate_relevance(rr, cfg).to_host_vector();
+        std::copy(v.begin(), v.end(), r_in);
     });
 }
 
@@ -338,27 +415,13 @@ int pxa_lm_forward(void* handle, const int64_t* ids, int64_t n, int64_t l, float
 
 int pxa_lm_relevance(void* handle, const float* seed, float eps, int bias_in_denominator, float* r_embed,
                      float* r_tokens, float* key_rel, float* value_rel) {
-    return guarded([&] {
-        auto* h = static_cast<LmHandle*>(handle);
-        if (h->n == 0) throw std::logic_error("CausalLM::propagate_relevance_by_layer: called before any forward()");
-        CausalLM& lm = *h->lm;
-        const px_model_config& c = h->cfg;
-        const int64_t count = h->n * h->l * c.vocab_size;
-        Tensor s(Shape({h->n, h->l, c.vocab_size}), backend(), std::vector<float>(seed, seed + count));
-        const LRPRuleConfig cfg = rule(eps, bias_in_denominator);
-        const std::vector<Tensor> bounds = lm.propagate_relevance_by_layer(s, cfg);
-        auto to_host = [](const Tensor& t, float* dst) {
-            const std::vector<float> v = t.to_host_vector();
-            std::copy(v.begin(), v.end(), dst);
-        };
-        if (r_embed) to_host(bounds.front(), r_embed);
-        if (r_tokens) to_host(lm.embed_tokens().propagate_relevance(bounds.front(), cfg), r_tokens);
-        const int64_t kv = h->n * h->l * kv_heads(c) * head_dim(c);
-        for (int64_t i = 0; i < lm.num_layers(); ++i) {
-            if (key_rel) to_host(lm.layer(i).mha().key_relevance(), key_rel + i * kv);
-            if (value_rel) to_host(lm.layer(i).mha().value_relevance(), value_rel + i * kv);
-        }
-    });
+    return guarded(
+        [&] { lm_relevance(handle, seed, rule(eps, bias_in_denominator), r_embed, r_tokens, key_rel, value_rel); });
+}
+
+int pxa_lm_relevance_rule(void* handle, const float* seed, const px_lrp_rule* p, float* r_embed, float* r_tokens,
+                          float* key_rel, float* value_rel) {
+    return guarded([&] { lm_relevance(handle, seed, rule(p), r_embed, r_tokens, key_rel, value_rel); });
 }
 
 int pxa_lm_explain_device(void* handle, const float* ids, int64_t n, int64_t l, float eps, int bias_in_denominator,
@@ -373,18 +436,25 @@ int pxa_lm_capture_explain(void* handle, const float* ids, int64_t n, int64_t l,
                            float* token_rel, int64_t* targets) {
     return guarded([&] {
         auto* h = static_cast<LmHandle*>(handle);
-        MI355XBackend* be = backend();
-        be->begin_capture();
-        try {
-            h->lm->explain_device(ids, n, l, rule(eps, bias_in_denominator), token_rel, targets, nullptr, false);
-        } catch (...) {
-            try {
-                be->end_capture();
-            } catch (...) {
-            }
-            throw;
-        }
-        be->end_capture();
+        const LRPRuleConfig cfg = rule(eps, bias_in_denominator);
+        capture([&] { h->lm->explain_device(ids, n, l, cfg, token_rel, targets, nullptr, false); });
+    });
+}
+
+int pxa_lm_explain_device_rule(void* handle, const float* ids, int64_t n, int64_t l, const px_lrp_rule* p,
+                               float* token_rel, int64_t* targets, const int64_t* targets_in, int unit_seed) {
+    return guarded([&] {
+        auto* h = static_cast<LmHandle*>(handle);
+        h->lm->explain_device(ids, n, l, rule(p), token_rel, targets, targets_in, unit_seed != 0);
+    });
+}
+
+int pxa_lm_capture_explain_rule(void* handle, const float* ids, int64_t n, int64_t l, const px_lrp_rule* p,
+                                float* token_rel, int64_t* targets) {
+    return guarded([&] {
+        auto* h = static_cast<LmHandle*>(handle);
+        const LRPRuleConfig cfg = rule(p);
+        capture([&] { h->lm->explain_device(ids, n, l, cfg, token_rel, targets, nullptr, false); });
     });
 }
 

@@ -13,12 +13,6 @@ namespace pulsatrix {
 using detail::gemm_desc;
 using detail::mat;
 
-void require_epsilon_rule(const LRPRuleConfig& config, const char* module_name) {
-    if (config.rule != LRPRule::Epsilon)
-        throw std::invalid_argument(std::string(module_name) +
-                                    "::propagate_relevance: the MI355X path implements the epsilon rule only");
-}
-
 namespace detail {
 
 /** @brief A fresh tensor holding a copy of n device floats (the reference returns new tensors). */
@@ -83,9 +77,15 @@ const float* LinearModule::run_forward(const float* x, int64_t rows) {
 
 const float* LinearModule::run_relevance(const float* r, const LRPRuleConfig& config, const float* add,
                                          const detail::ResidualSplit& split) {
-    require_epsilon_rule(config, "LinearModule");
     if (x_ == nullptr) throw std::logic_error("LinearModule::propagate_relevance: called before any forward()");
+    detail::validate_rule(config, "LinearModule");
     float* out = r_in_.ensure(be_, rows_ * in_);
+    if (detail::is_affine_rule(config)) {  // lrp_rules::apply (lrp_rules.cpp:177-195)
+        const float* b = use_bias_ ? bias_.data() : nullptr;
+        rule_.run(be_, config, version_, {{weight_.data(), out_, out_, false, b}},
+                  {x_, in_, rows_, in_, z_.data(), out_, b, r, out_, out_, out, add}, split);
+        return split.requested() ? nullptr : out;
+    }
     pxk_gemm_desc d = gemm_desc(rows_, in_, out_);
     d.trans_b = 1;
     d.prologue = PXK_PRO_DIV_STAB;
@@ -169,7 +169,10 @@ EmbeddingModule::EmbeddingModule(int64_t num_embeddings, int64_t embedding_dim, 
         throw std::invalid_argument("EmbeddingModule: num_embeddings and embedding_dim must be positive");
 }
 
-void EmbeddingModule::set_weight(const std::vector<float>& values) { weight_ = Tensor(weight_.shape(), be_, values); }
+void EmbeddingModule::set_weight(const std::vector<float>& values) {
+    weight_ = Tensor(weight_.shape(), be_, values);
+    ++version_;
+}
 
 const float* EmbeddingModule::run_forward_device(const float* ids, int64_t n, int64_t l) {
     const int64_t count = n * l;
@@ -239,7 +242,7 @@ const float* TiedLMHeadModule::run_forward(const float* x, int64_t rows) {
     pxk_gemm_desc d = gemm_desc(rows, V, D);
     d.trans_b = 1;  // E (V, D) read transposed in place
     d.a = mat(x, D);
-    d.b = mat(embedding_.weight().data(), D);
+    d.b = mat(embedding_.weight_data(), D);
     d.c = mat(logits, V);
     be_->run_gemm(d);
     return logits;
@@ -247,10 +250,17 @@ const float* TiedLMHeadModule::run_forward(const float* x, int64_t rows) {
 
 const float* TiedLMHeadModule::run_relevance(const float* relevance_out, const LRPRuleConfig& config,
                                              const detail::ResidualSplit& split) {
-    require_epsilon_rule(config, "TiedLMHeadModule");
     if (x_ == nullptr) throw std::logic_error("TiedLMHeadModule::propagate_relevance: called before any forward()");
+    detail::validate_rule(config, "TiedLMHeadModule");
     const int64_t V = embedding_.num_embeddings(), D = embedding_.embedding_dim();
     float* out = r_in_.ensure(be_, rows_ * D);
+    if (detail::is_affine_rule(config)) {
+        // The rules on W = E^T (read transposed in place) against a zero bias
+        // (tied_lm_head_module.cpp:85-111).
+        rule_.run(be_, config, embedding_.version(), {{embedding_.weight_data(), D, V, true, nullptr}},
+                  {x_, D, rows_, D, logits_.data(), V, nullptr, relevance_out, V, V, out, nullptr}, split);
+        return split.requested() ? nullptr : out;
+    }
     // z = logits + 0 bias; g = R / stab(z); r_in = x * (g E): K = V, split-K across the chip.
     pxk_gemm_desc d = gemm_desc(rows_, D, V);
     d.prologue = PXK_PRO_DIV_STAB;
@@ -258,7 +268,7 @@ const float* TiedLMHeadModule::run_relevance(const float* relevance_out, const L
     d.eps = config.epsilon;
     d.a = mat(relevance_out, V);
     d.z = mat(logits_.data(), V);
-    d.b = mat(embedding_.weight().data(), D);
+    d.b = mat(embedding_.weight_data(), D);
     d.c = mat(out, D);
     d.x = mat(x_, D);
     detail::apply_split(d, split, D, config.epsilon);

@@ -311,6 +311,7 @@ struct RelArgs {
     float scale, eps;
     int causal, rope, rope_half;
     int lds_ld;
+    int rel_only;  // g receives the relevance itself (no projection denominator)
 };
 
 template <int DT, bool VEC>
@@ -508,7 +509,7 @@ __global__ void __launch_bounds__(kThreads) attn_rel_q_kernel(const RelArgs a) {
         const int64_t tok = static_cast<int64_t>(b) * l + orow;
         const float* qr = a.q + tok * a.ld_q + h * D;
         const float* qx = a.q_pre + tok * a.ld_q_pre + h * D;
-        const float* zr = a.z + tok * a.ld_z + h * D;
+        const float* zr = a.rel_only ? nullptr : a.z + tok * a.ld_z + h * D;
         const float* br = a.bias ? a.bias + h * D : nullptr;
         float* gr = a.g + tok * a.ld_g + h * D;
         const int half = D / 2;
@@ -534,8 +535,12 @@ __global__ void __launch_bounds__(kThreads) attn_rel_q_kernel(const RelArgs a) {
             } else {
                 r_in = qr[d] * m_acc[rr][d];
             }
-            const float zz = br ? zr[d] + br[d] : zr[d];
-            gr[d] = r_in / stab(zz, a.eps);
+            if (a.rel_only) {
+                gr[d] = r_in;
+            } else {
+                const float zz = br ? zr[d] + br[d] : zr[d];
+                gr[d] = r_in / stab(zz, a.eps);
+            }
         }
     }
 }
@@ -626,7 +631,7 @@ extern "C" int pxk_attention_relevance_q(const pxk_attn_rel_desc* d, void* strea
         return fail(PXK_ERR_INVALID, "pxk_attention_relevance_q: bad sizes (heads must be a multiple of kv_heads)");
     if (D <= 0 || D > 128 || D % 4 != 0 || (d->rope && D % 2 != 0))
         return fail(PXK_ERR_INVALID, "pxk_attention_relevance_q: head_dim must be a multiple of 4 up to 128");
-    if (!d->spv || !d->v || !d->k || !d->p || !d->raw || !d->s || !d->q || !d->z || !d->g ||
+    if (!d->spv || !d->v || !d->k || !d->p || !d->raw || !d->s || !d->q || (!d->z && !d->relevance_only) || !d->g ||
         (d->rope && (!d->q_pre || !d->cos_t || !d->sin_t)))
         return fail(PXK_ERR_INVALID, "pxk_attention_relevance_q: a required operand is NULL");
     if (d->ld_spv % 4 || d->ld_v % 4 || !aligned16(d->spv) || !aligned16(d->v) || d->ld_spv < H * D ||
@@ -650,7 +655,7 @@ extern "C" int pxk_attention_relevance_q(const pxk_attn_rel_desc* d, void* strea
               static_cast<int>(d->ld_q), static_cast<int>(d->ld_q_pre), static_cast<int>(d->ld_z),
               static_cast<int>(d->ld_g), static_cast<int>(n), static_cast<int>(l), static_cast<int>(H),
               static_cast<int>(Hkv), static_cast<int>(D), d->scale, d->eps, d->causal != 0, d->rope != 0,
-              d->rope_half != 0, lds_ld};
+              d->rope_half != 0, lds_ld, d->relevance_only != 0};
     const bool vec = l % 4 == 0 && aligned16(d->p) && aligned16(d->raw) && aligned16(d->s);
     using K = void (*)(const RelArgs);
     static const K table[2][4] = {
@@ -705,6 +710,7 @@ struct RelKvArgs {
     int n, l, heads, kv_heads, D, ngroups, nkb;
     float eps;
     int causal, rope, rope_half, remap;
+    int rel_only;  // g_k / g_v receive the relevances themselves (no projection denominators)
 };
 
 // Head dimension held by MFMA column c of dim group dq, or -1.
@@ -843,10 +849,15 @@ __global__ void __launch_bounds__(NW * kWave) attn_rel_kv_kernel(const RelKvArgs
         rk = a.k[row * a.ld_k + col] * sum4(0, nn);
     }
     if (a.key_rel) a.key_rel[row * a.ld_rel + col] = rk;
-    const float zk = a.bias_k ? a.z_k[row * a.ld_z + col] + a.bias_k[col] : a.z_k[row * a.ld_z + col];
-    a.g_k[row * a.ld_g + col] = rk / stab(zk, eps);
     const float rv = a.v[row * a.ld_v + col] * sum4(1, nn);
     if (a.value_rel) a.value_rel[row * a.ld_rel + col] = rv;
+    if (a.rel_only) {
+        a.g_k[row * a.ld_g + col] = rk;
+        a.g_v[row * a.ld_g + col] = rv;
+        return;
+    }
+    const float zk = a.bias_k ? a.z_k[row * a.ld_z + col] + a.bias_k[col] : a.z_k[row * a.ld_z + col];
+    a.g_k[row * a.ld_g + col] = rk / stab(zk, eps);
     const float zv = a.bias_v ? a.z_v[row * a.ld_z + col] + a.bias_v[col] : a.z_v[row * a.ld_z + col];
     a.g_v[row * a.ld_g + col] = rv / stab(zv, eps);
 }
@@ -858,7 +869,8 @@ extern "C" int pxk_attention_relevance_kv(const pxk_attn_rel_kv_desc* d, void* s
     if (n < 0 || l < 0 || H <= 0 || Hkv <= 0 || H % Hkv != 0 || D <= 0 || D > 1024 || (d->rope && D % 2 != 0))
         return fail(PXK_ERR_INVALID, "pxk_attention_relevance_kv: bad sizes (heads a multiple of kv_heads, head_dim "
                                      "up to 1024 and even with RoPE)");
-    if (!d->s || !d->p || !d->q || !d->spv || !d->k || !d->v || !d->z_k || !d->z_v || !d->g_k || !d->g_v ||
+    if (!d->s || !d->p || !d->q || !d->spv || !d->k || !d->v || ((!d->z_k || !d->z_v) && !d->relevance_only) ||
+        !d->g_k || !d->g_v ||
         (d->rope && (!d->k_pre || !d->cos_t || !d->sin_t)))
         return fail(PXK_ERR_INVALID, "pxk_attention_relevance_kv: a required operand is NULL");
     if (d->ld_q < H * D || d->ld_spv < H * D || d->ld_k < Hkv * D || d->ld_v < Hkv * D || d->ld_z < Hkv * D ||
@@ -879,7 +891,7 @@ extern "C" int pxk_attention_relevance_kv(const pxk_attn_rel_kv_desc* d, void* s
                 static_cast<int>(d->ld_v), static_cast<int>(d->ld_z), static_cast<int>(d->ld_rel),
                 static_cast<int>(d->ld_g), static_cast<int>(n), static_cast<int>(l), static_cast<int>(H),
                 static_cast<int>(Hkv), static_cast<int>(D), static_cast<int>(ngroups), static_cast<int>(nkb), d->eps,
-                d->causal != 0, d->rope != 0, d->rope_half != 0, blocks % 8 == 0};
+                d->causal != 0, d->rope != 0, d->rope_half != 0, blocks % 8 == 0, d->relevance_only != 0};
     // Sixteen waves per workgroup, two items per register set: the widest spread of a long key
     // block's rows measured fastest at 512 tokens (against 4 or 8 waves and 4 or 8 items).
     hipLaunchKernelGGL((attn_rel_kv_kernel<16, 2>), dim3(static_cast<unsigned>(blocks)), dim3(16 * kWave), 0,

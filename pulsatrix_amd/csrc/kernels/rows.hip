@@ -198,7 +198,8 @@ __global__ void __launch_bounds__(kThreads) attention_lrp_scores_kernel(const fl
 
 // RoPE of q and k from the packed projection buffer into head-packed (rows, heads*D) outputs.
 __global__ void __launch_bounds__(kThreads) rope_qk_kernel(const float* q_in, const float* k_in, int64_t ld,
-                                                           float* q_out, float* k_out, const float* cos_t,
+                                                           float* q_out, float* k_out, int64_t ld_out,
+                                                           const float* cos_t,
                                                            const float* sin_t, int64_t rows, int64_t L, int64_t H,
                                                            int64_t Hkv, int64_t D, int rotate_half) {
     const int64_t half = D / 2;
@@ -212,7 +213,7 @@ __global__ void __launch_bounds__(kThreads) rope_qk_kernel(const float* q_in, co
         const int64_t pos = row % L;
         const int64_t lo = rotate_half ? i : 2 * i, hi = rotate_half ? i + half : 2 * i + 1;
         const float* src = (is_q ? q_in : k_in) + row * ld + h * D;
-        float* dst = (is_q ? q_out : k_out) + row * heads * D + h * D;
+        float* dst = (is_q ? q_out : k_out) + row * ld_out + h * D;
         const float c = cos_t[pos * half + i], s = sin_t[pos * half + i];
         const float x0 = src[lo], x1 = src[hi];
         dst[lo] = x0 * c - x1 * s;
@@ -470,15 +471,17 @@ int pxk_attention_lrp_scores(const float* r_attn, const float* p, const float* r
     return launched("pxk_attention_lrp_scores");
 }
 
-int pxk_rope_qk(const float* q_in, const float* k_in, int64_t ld_in, float* q_out, float* k_out, const float* cos_t,
-                const float* sin_t, int64_t rows, int64_t seq_len, int64_t heads, int64_t kv_heads, int64_t head_dim,
-                int rotate_half, void* stream) {
+int pxk_rope_qk(const float* q_in, const float* k_in, int64_t ld_in, float* q_out, float* k_out, int64_t ld_out,
+                const float* cos_t, const float* sin_t, int64_t rows, int64_t seq_len, int64_t heads, int64_t kv_heads,
+                int64_t head_dim, int rotate_half, void* stream) {
     if (rows < 0 || seq_len <= 0 || heads <= 0 || kv_heads <= 0 || head_dim <= 0 || head_dim % 2 != 0)
         return fail(PXK_ERR_INVALID, "pxk_rope_qk: bad sizes");
+    if (ld_in < heads * head_dim || ld_in < kv_heads * head_dim || ld_out < heads * head_dim)
+        return fail(PXK_ERR_INVALID, "pxk_rope_qk: row strides must hold every head");
     if (rows == 0) return PXK_OK;
     const int64_t work = rows * (heads + kv_heads) * (head_dim / 2);
     hipLaunchKernelGGL(rope_qk_kernel, dim3(grid_for(work, kThreads)), dim3(kThreads), 0, S(stream), q_in, k_in, ld_in,
-                       q_out, k_out, cos_t, sin_t, rows, seq_len, heads, kv_heads, head_dim, rotate_half);
+                       q_out, k_out, ld_out, cos_t, sin_t, rows, seq_len, heads, kv_heads, head_dim, rotate_half);
     return launched("pxk_rope_qk");
 }
 

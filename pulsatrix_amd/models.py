@@ -26,6 +26,20 @@ def synthetic_params(cfg, seed, std=0.02, block=False):
     return out
 
 
+def linear_relevance_rule(x, w, b, r, rule):
+    """A LinearModule on the device: forward of x (n, in) through w (in, out) and bias b (nullable),
+    then propagate_relevance of r (n, out) under `rule`. Returns (y, r_in)."""
+    x, w, r = (np.ascontiguousarray(a, dtype=np.float32) for a in (x, w, r))
+    b = None if b is None else np.ascontiguousarray(b, dtype=np.float32)
+    n, i = x.shape
+    o = w.shape[1]
+    y = np.empty((n, o), np.float32)
+    r_in = np.empty((n, i), np.float32)
+    N.host_check(N.host().pxa_linear_relevance_rule(_p(x), _p(w), _p(b), n, i, o, _p(r), ctypes.byref(N.as_rule(rule)),
+                                                    _p(y), _p(r_in)))
+    return y, r_in
+
+
 class Block:
     """TransformerBlock on the process-wide MI355XBackend."""
 
@@ -47,6 +61,12 @@ class Block:
         r = np.ascontiguousarray(r, dtype=np.float32)
         out = np.empty_like(r)
         N.host_check(N.host().pxa_block_relevance(self.h, _p(r), eps, int(bias_in_denominator), _p(out)))
+        return out
+
+    def relevance_rule(self, r, rule):
+        r = np.ascontiguousarray(r, dtype=np.float32)
+        out = np.empty_like(r)
+        N.host_check(N.host().pxa_block_relevance_rule(self.h, _p(r), ctypes.byref(N.as_rule(rule)), _p(out)))
         return out
 
     def __del__(self):
@@ -90,19 +110,28 @@ class CausalLM:
         self.shape = (n, l)
         return logits
 
-    def relevance(self, seed, eps, bias_in_denominator, want_kv=False):
+    def _relevance_outputs(self, want_kv):
         n, l = self.shape
         c = self.cfg
-        seed = np.ascontiguousarray(seed, dtype=np.float32)
-        r_embed = np.empty((n, l, c.hidden_size), np.float32)
-        r_tok = np.empty((n, l), np.float32)
         kvh = c.num_kv_heads if c.num_kv_heads > 0 else c.num_heads
         hd = c.head_dim if c.head_dim > 0 else c.hidden_size // c.num_heads
         kv = (c.num_layers, n * l, kvh * hd)
-        k = np.empty(kv, np.float32) if want_kv else None
-        v = np.empty(kv, np.float32) if want_kv else None
+        return (np.empty((n, l, c.hidden_size), np.float32), np.empty((n, l), np.float32),
+                np.empty(kv, np.float32) if want_kv else None, np.empty(kv, np.float32) if want_kv else None)
+
+    def relevance(self, seed, eps, bias_in_denominator, want_kv=False):
+        seed = np.ascontiguousarray(seed, dtype=np.float32)
+        r_embed, r_tok, k, v = self._relevance_outputs(want_kv)
         N.host_check(N.host().pxa_lm_relevance(self.h, _p(seed), eps, int(bias_in_denominator), _p(r_embed),
                                                _p(r_tok), _p(k), _p(v)))
+        return (r_embed, r_tok, k, v) if want_kv else (r_embed, r_tok)
+
+    def relevance_rule(self, seed, rule, want_kv=False):
+        """propagate_relevance_by_layer under any LRPRuleConfig (an LrpRule, or the oracle's)."""
+        seed = np.ascontiguousarray(seed, dtype=np.float32)
+        r_embed, r_tok, k, v = self._relevance_outputs(want_kv)
+        N.host_check(N.host().pxa_lm_relevance_rule(self.h, _p(seed), ctypes.byref(N.as_rule(rule)), _p(r_embed),
+                                                    _p(r_tok), _p(k), _p(v)))
         return (r_embed, r_tok, k, v) if want_kv else (r_embed, r_tok)
 
     def explain_device(self, ids_ptr, n, l, eps, bias_in_denominator, token_rel_ptr, targets_ptr, targets=None,
@@ -118,6 +147,16 @@ class CausalLM:
     def capture_explain(self, ids_ptr, n, l, eps, bias_in_denominator, token_rel_ptr, targets_ptr):
         N.host_check(N.host().pxa_lm_capture_explain(self.h, ids_ptr, n, l, eps, int(bias_in_denominator),
                                                      token_rel_ptr, targets_ptr))
+
+    def explain_device_rule(self, ids_ptr, n, l, rule, token_rel_ptr, targets_ptr, targets=None, unit_seed=False):
+        t = None if targets is None else np.ascontiguousarray(targets, dtype=np.int64)
+        N.host_check(N.host().pxa_lm_explain_device_rule(
+            self.h, ids_ptr, n, l, ctypes.byref(N.as_rule(rule)), token_rel_ptr, targets_ptr,
+            t.ctypes.data_as(ctypes.POINTER(ctypes.c_int64)) if t is not None else None, int(unit_seed)))
+
+    def capture_explain_rule(self, ids_ptr, n, l, rule, token_rel_ptr, targets_ptr):
+        N.host_check(N.host().pxa_lm_capture_explain_rule(self.h, ids_ptr, n, l, ctypes.byref(N.as_rule(rule)),
+                                                          token_rel_ptr, targets_ptr))
 
     def replay(self):
         N.host_check(N.host().pxa_lm_replay(self.h))

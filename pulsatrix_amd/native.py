@@ -76,7 +76,7 @@ PXK_SIGNATURES = {
     "pxk_attention_forward": "pipipipppiiiiiifnp",
     "pxk_attention_softmax": "ppiifnp",
     "pxk_attention_lrp_scores": "ppppiiffnp",
-    "pxk_rope_qk": "ppippppiiiiinp",
+    "pxk_rope_qk": "ppippipppiiiiinp",
     "pxk_rope_rotate": "ppppiiinnp",
     "pxk_lrp_rope": "ppppppiiifnp",
     "pxk_permute_0213": "ppiiiip",
@@ -129,6 +129,17 @@ def pxk():
         lib.pxk_attention_relevance_kv.argtypes = [ctypes.POINTER(AttnRelKvDesc), c_vp]
         lib.pxk_gemm_supported.restype = ctypes.c_int
         lib.pxk_gemm_supported.argtypes = [ctypes.c_int] * 4
+        lib.pxk_lrp_rule_weights.restype = ctypes.c_int
+        lib.pxk_lrp_rule_weights.argtypes = [ctypes.POINTER(RuleParams), ctypes.POINTER(RuleBlock), ctypes.c_int,
+                                             c_i64, c_vp, c_vp, c_vp]
+        lib.pxk_lrp_sign_split.restype = ctypes.c_int
+        lib.pxk_lrp_sign_split.argtypes = [c_vp, c_i64, c_i64, c_i64, c_vp, c_vp]
+        lib.pxk_lrp_rule_divide.restype = ctypes.c_int
+        lib.pxk_lrp_rule_divide.argtypes = [ctypes.POINTER(RuleParams), c_vp, c_i64, c_i64, c_vp, c_i64, c_vp, c_i64,
+                                            c_vp, c_vp, c_i64, c_i64, c_vp, c_i64, c_vp]
+        lib.pxk_lrp_rule_combine.restype = ctypes.c_int
+        lib.pxk_lrp_rule_combine.argtypes = [ctypes.c_int, c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_i64, c_vp, c_i64,
+                                             c_vp, c_vp, c_vp, c_vp, ctypes.c_float, c_vp]
         lib.pxk_reduce_partials.restype = ctypes.c_size_t
         lib.pxk_reduce_partials.argtypes = [c_i64]
         _pxk = lib
@@ -153,7 +164,7 @@ class AttnRelDesc(ctypes.Structure):
 
     _fields_ = [("n", c_i64), ("l", c_i64), ("heads", c_i64), ("kv_heads", c_i64), ("head_dim", c_i64),
                 ("scale", ctypes.c_float), ("eps", ctypes.c_float), ("causal", ctypes.c_int32),
-                ("rope", ctypes.c_int32), ("rope_half", ctypes.c_int32), ("reserved", ctypes.c_int32),
+                ("rope", ctypes.c_int32), ("rope_half", ctypes.c_int32), ("relevance_only", ctypes.c_int32),
                 ("spv", c_vp), ("ld_spv", c_i64), ("v", c_vp), ("ld_v", c_i64), ("k", c_vp), ("ld_k", c_i64),
                 ("p", c_vp), ("raw", c_vp), ("s", c_vp), ("q", c_vp), ("ld_q", c_i64), ("q_pre", c_vp),
                 ("ld_q_pre", c_i64), ("z", c_vp), ("ld_z", c_i64), ("bias", c_vp), ("cos_t", c_vp), ("sin_t", c_vp),
@@ -169,7 +180,22 @@ class AttnRelKvDesc(ctypes.Structure):
                 ("spv", c_vp), ("ld_spv", c_i64), ("k", c_vp), ("ld_k", c_i64), ("k_pre", c_vp),
                 ("ld_k_pre", c_i64), ("v", c_vp), ("ld_v", c_i64), ("z_k", c_vp), ("z_v", c_vp), ("ld_z", c_i64),
                 ("bias_k", c_vp), ("bias_v", c_vp), ("cos_t", c_vp), ("sin_t", c_vp), ("key_rel", c_vp),
-                ("value_rel", c_vp), ("ld_rel", c_i64), ("g_k", c_vp), ("g_v", c_vp), ("ld_g", c_i64)]
+                ("value_rel", c_vp), ("ld_rel", c_i64), ("g_k", c_vp), ("g_v", c_vp), ("ld_g", c_i64),
+                ("relevance_only", ctypes.c_int32)]
+
+
+class RuleParams(ctypes.Structure):
+    """pxk_rule_params."""
+
+    _fields_ = [("rule", ctypes.c_int32), ("eps", ctypes.c_float), ("gamma", ctypes.c_float),
+                ("alpha", ctypes.c_float), ("beta", ctypes.c_float), ("low", ctypes.c_float),
+                ("high", ctypes.c_float)]
+
+
+class RuleBlock(ctypes.Structure):
+    """pxk_rule_block."""
+
+    _fields_ = [("w", c_vp), ("ld", c_i64), ("cols", c_i64), ("trans", ctypes.c_int32), ("bias", c_vp)]
 
 
 def gemm(desc, stream=None):
@@ -200,6 +226,27 @@ class ModelConfig(ctypes.Structure):
                 ("reserved", ctypes.c_int32)]
 
 
+EPSILON, GAMMA, ALPHA_BETA, ZBOX = 0, 1, 2, 3  # LRPRule order
+
+
+class LrpRule(ctypes.Structure):
+    """px_lrp_rule: LRPRuleConfig's fields (rule in LRPRule order)."""
+
+    _fields_ = [("epsilon", ctypes.c_float), ("rule", ctypes.c_int32), ("gamma", ctypes.c_float),
+                ("alpha", ctypes.c_float), ("beta", ctypes.c_float), ("low", ctypes.c_float),
+                ("high", ctypes.c_float), ("bias_in_denominator", ctypes.c_int32)]
+
+
+def lrp_rule(rule=EPSILON, epsilon=1e-6, gamma=0.25, alpha=1.0, beta=0.0, low=0.0, high=1.0,
+             bias_in_denominator=False):
+    return LrpRule(epsilon, rule, gamma, alpha, beta, low, high, int(bias_in_denominator))
+
+
+def as_rule(r):
+    """An LrpRule from any object with LRPRuleConfig's field names (the oracle's struct included)."""
+    return LrpRule(*[getattr(r, f) for f, _ in LrpRule._fields_])
+
+
 _host = None
 
 
@@ -213,6 +260,7 @@ def host():
         lib = ctypes.CDLL(HOST_SO)
         cfgp = ctypes.POINTER(ModelConfig)
         i64p = ctypes.POINTER(ctypes.c_int64)
+        rulep = ctypes.POINTER(LrpRule)
         sigs = {
             "pxa_last_error": (ctypes.c_char_p, []),
             "pxa_device_count": (ctypes.c_int, []),
@@ -238,6 +286,13 @@ def host():
             "pxa_lm_capture_explain": (ctypes.c_int, [c_vp, c_vp, c_i64, c_i64, ctypes.c_float, ctypes.c_int, c_vp,
                                                       c_vp]),
             "pxa_lm_replay": (ctypes.c_int, [c_vp]),
+            "pxa_block_relevance_rule": (ctypes.c_int, [c_vp, c_vp, rulep, c_vp]),
+            "pxa_linear_relevance_rule": (ctypes.c_int, [c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_vp, rulep, c_vp,
+                                                         c_vp]),
+            "pxa_lm_relevance_rule": (ctypes.c_int, [c_vp, c_vp, rulep, c_vp, c_vp, c_vp, c_vp]),
+            "pxa_lm_explain_device_rule": (ctypes.c_int, [c_vp, c_vp, c_i64, c_i64, rulep, c_vp, c_vp, i64p,
+                                                          ctypes.c_int]),
+            "pxa_lm_capture_explain_rule": (ctypes.c_int, [c_vp, c_vp, c_i64, c_i64, rulep, c_vp, c_vp]),
             "pxa_lm_check_device_ids": (ctypes.c_int, [c_vp]),
             "pxa_lm_last_logits": (c_vp, [c_vp]),
             "pxa_lm_last_embedding_relevance": (c_vp, [c_vp]),
