@@ -376,6 +376,45 @@ void rope_tables(int64_t hd, float base, int64_t seq, int64_t offset, float* cs,
         }
 }
 
+// RoPEModule built from an inverse-frequency list (rope_module.cpp:36-51): the same tables.
+void rope_tables_inv(const std::vector<double>& inv, int64_t hd, int64_t seq, int64_t offset, float* cs, float* sn) {
+    const int64_t half = hd / 2;
+    for (int64_t pos = 0; pos < seq; ++pos)
+        for (int64_t i = 0; i < half; ++i) {
+            const double theta = static_cast<double>(offset + pos) * inv[static_cast<size_t>(i)];
+            cs[pos * half + i] = static_cast<float>(std::cos(theta));
+            sn[pos * half + i] = static_cast<float>(std::sin(theta));
+        }
+}
+
+// RopeInverseFrequencies (hf_model.cpp:258-287): 1 / theta^(2i/D), then linear or llama3 scaling.
+std::vector<double> rope_inverse_frequencies(const px_model_config& c, int64_t hd) {
+    const int64_t half = hd / 2;
+    std::vector<double> inv(static_cast<size_t>(half));
+    for (int64_t i = 0; i < half; ++i)
+        inv[static_cast<size_t>(i)] =
+            1.0 / std::pow(static_cast<double>(c.rope_theta), 2.0 * static_cast<double>(i) / static_cast<double>(hd));
+    if (c.rope_scaling == 1) {
+        for (double& f : inv) f /= c.rope_factor;
+        return inv;
+    }
+    const double old_len = static_cast<double>(c.rope_original_max_position);
+    const double low_wavelen = old_len / c.rope_low_freq_factor;
+    const double high_wavelen = old_len / c.rope_high_freq_factor;
+    constexpr double kPi = 3.14159265358979323846;
+    for (double& f : inv) {
+        const double wavelen = 2.0 * kPi / f;
+        if (wavelen > low_wavelen) {
+            f /= c.rope_factor;
+        } else if (wavelen >= high_wavelen) {
+            const double smooth =
+                (old_len / wavelen - c.rope_low_freq_factor) / (c.rope_high_freq_factor - c.rope_low_freq_factor);
+            f = (1.0 - smooth) * f / c.rope_factor + smooth * f;
+        }
+    }
+    return inv;
+}
+
 // ---- modules -------------------------------------------------------------------------------
 
 // LRPRuleConfig (include/pulsatrix/lrp_rule_config.hpp:72-115); rule in LRPRule order.
@@ -592,10 +631,21 @@ struct Linear {
 struct RMSNorm {
     int64_t d = 0;
     float eps = 1e-6f;
+    float offset = 0.0f;  // EffectiveGamma (rms_norm_module.cpp:40-49): fill(offset), then add gamma
     Buf gamma;
+    void init(int64_t d_, float eps_, float offset_, const float*& p) {
+        d = d_;
+        eps = eps_;
+        offset = offset_;
+        gamma.assign(p, p + d);
+        p += d;
+    }
     Buf forward(const Buf& x, int64_t rows) const {
         Buf out(x.size()), rms(static_cast<size_t>(rows));
-        rms_norm_forward(x.data(), gamma.data(), out.data(), rms.data(), rows, d, eps);
+        Buf g = gamma;
+        if (offset != 0.0f)
+            for (size_t i = 0; i < g.size(); ++i) g[i] = offset + gamma[i];
+        rms_norm_forward(x.data(), g.data(), out.data(), rms.data(), rows, d, eps);
         return out;
     }
 };
@@ -604,12 +654,20 @@ struct ModelShape {
     int64_t d, H, Hkv, D, F;
     float norm_eps, theta;
     bool rope, half_layout, causal, qkv_bias, out_bias, mlp_bias;
+    // Variants (ToAttentionConfig(config, layer), hf_model.cpp:289-313; TransformerBlockOptions)
+    int act = 0;                 // 0 SiLU, 1 GeLU tanh
+    bool qk_norm = false, post_norms = false;
+    float norm_offset = 0.0f;
+    float score_scale = 0.0f;    // 0: 1/sqrt(D)
+    size_t window = 0;           // this layer's sliding window (0: none)
+    std::vector<double> inv_freq;  // non-empty: the RoPE inverse frequencies (else theta's schedule)
 };
 
 // MultiHeadAttentionModule (multihead_attention_module.cpp:204-310 forward, 404-485 relevance).
 struct MHA {
     ModelShape s;
     Linear q, k, v, o;
+    RMSNorm q_norm, k_norm;
     int64_t N = 0, L = 0;
     Buf q_in, q_out, k_in, k_out;  // RoPE caches (RoPEModule last_input_/last_output_)
     Buf cos_t, sin_t;
@@ -622,6 +680,10 @@ struct MHA {
         k.init(s.d, s.Hkv * s.D, s.qkv_bias, p);
         v.init(s.d, s.Hkv * s.D, s.qkv_bias, p);
         o.init(s.H * s.D, s.d, s.out_bias, p);
+        if (s.qk_norm) {  // qk_norm_eps = rms_norm_eps, offset = norm_weight_offset (hf_model.cpp:299-311)
+            q_norm.init(s.D, s.norm_eps, s.norm_offset, p);
+            k_norm.init(s.D, s.norm_eps, s.norm_offset, p);
+        }
     }
 
     // repeat_kv (:154-171): head h reads KV head h / group.
@@ -648,7 +710,7 @@ struct MHA {
 
     void fill_masked(Buf& scores, float value) const {  // :194-202
         if (!s.causal) return;
-        attention_mask_fill(scores.data(), nullptr, N, s.H, L, L, true, 0, 0, value);
+        attention_mask_fill(scores.data(), nullptr, N, s.H, L, L, true, 0, s.window, value);
     }
 
     Buf forward(const Buf& input, int64_t n_, int64_t l_) {
@@ -660,10 +722,17 @@ struct MHA {
         permute_0213(qf.data(), qh.data(), N, L, H, D);
         permute_0213(kf.data(), kh.data(), N, L, Hkv, D);
         permute_0213(vf.data(), vh.data(), N, L, Hkv, D);
+        if (s.qk_norm) {  // step 3, QK-Norm over each (head, position) row of D
+            qh = q_norm.forward(qh, N * H * L);
+            kh = k_norm.forward(kh, N * Hkv * L);
+        }
         if (s.rope) {
             cos_t.assign(static_cast<size_t>(L * D / 2), 0.0f);
             sin_t.assign(cos_t.size(), 0.0f);
-            rope_tables(D, s.theta, L, 0, cos_t.data(), sin_t.data());
+            if (s.inv_freq.empty())
+                rope_tables(D, s.theta, L, 0, cos_t.data(), sin_t.data());
+            else
+                rope_tables_inv(s.inv_freq, D, L, 0, cos_t.data(), sin_t.data());
             q_in = qh;
             k_in = kh;
             q_out.assign(qh.size(), 0.0f);
@@ -679,10 +748,11 @@ struct MHA {
         const size_t LL = static_cast<size_t>(L * L), LD = static_cast<size_t>(L * D);
         raw.assign(static_cast<size_t>(N * H) * LL, 0.0f);
         scaled.assign(raw.size(), 0.0f);
-        const float inv_sqrt_d = 1.0f / std::sqrt(static_cast<float>(D));  // score_scale(), :190-192
+        // score_scale(), :190-192
+        const float scale = s.score_scale > 0.0f ? s.score_scale : 1.0f / std::sqrt(static_cast<float>(D));
         for (int64_t nh = 0; nh < N * H; ++nh)
             gemm_ex(Q.data() + nh * LD, false, K.data() + nh * LD, true, raw.data() + nh * LL, L, D, L, 0.0f);
-        axpby(inv_sqrt_d, raw.data(), 0.0f, nullptr, scaled.data(), raw.size());
+        axpby(scale, raw.data(), 0.0f, nullptr, scaled.data(), raw.size());
         fill_masked(scaled, std::numeric_limits<float>::lowest());
         attn.assign(raw.size(), 0.0f);
         softmax_rows(scaled.data(), attn.data(), N * H * L, L);  // SoftmaxModule (softmax_module.cpp:39-51)
@@ -738,8 +808,10 @@ struct SwiGLU {
     Linear gate, up, down;
     Buf gate_post, up_out;
     int64_t rows = 0;
+    int act = 0;
 
     void init(const ModelShape& s, const float*& p) {
+        act = s.act;
         gate.init(s.d, s.F, s.mlp_bias, p);
         up.init(s.d, s.F, s.mlp_bias, p);
         down.init(s.F, s.d, s.mlp_bias, p);
@@ -749,7 +821,7 @@ struct SwiGLU {
         rows = n_flat;
         Buf gp = gate.forward(x, rows);
         gate_post.assign(gp.size(), 0.0f);
-        elementwise(4, gp.data(), gate_post.data(), gp.size());
+        elementwise(act == 1 ? 6 : 4, gp.data(), gate_post.data(), gp.size());  // GeluTanh or Silu
         up_out = up.forward(x, rows);
         Buf hidden(gp.size());
         mul(gate_post.data(), up_out.data(), hidden.data(), hidden.size());
@@ -771,22 +843,22 @@ struct SwiGLU {
 // TransformerBlock (transformer_block.cpp:99-133 forward, 189-227 relevance), pre-norm.
 struct Block {
     ModelShape s;
-    RMSNorm norm1, norm2;
+    RMSNorm norm1, norm2, post_attn_norm, post_mlp_norm;
     MHA mha;
     SwiGLU mlp;
     Buf last_x, last_attn, last_y1, last_ffn;
     int64_t N = 0, L = 0;
 
-    void init(const ModelShape& sh, const float*& p) {
+    void init(const ModelShape& sh, const float*& p) {  // named_parameters order (transformer_block.cpp:240-249)
         s = sh;
-        norm1.d = norm2.d = s.d;
-        norm1.eps = norm2.eps = s.norm_eps;
-        norm1.gamma.assign(p, p + s.d);
-        p += s.d;
+        norm1.init(s.d, s.norm_eps, s.norm_offset, p);
         mha.init(s, p);
-        norm2.gamma.assign(p, p + s.d);
-        p += s.d;
+        norm2.init(s.d, s.norm_eps, s.norm_offset, p);
         mlp.init(s, p);
+        if (s.post_norms) {
+            post_attn_norm.init(s.d, s.norm_eps, s.norm_offset, p);
+            post_mlp_norm.init(s.d, s.norm_eps, s.norm_offset, p);
+        }
     }
 
     Buf forward(const Buf& x, int64_t n_, int64_t l_) {
@@ -794,9 +866,11 @@ struct Block {
         L = l_;
         const int64_t rows = N * L;
         Buf attn_out = mha.forward(norm1.forward(x, rows), N, L);
+        if (s.post_norms) attn_out = post_attn_norm.forward(attn_out, rows);  // PostNorm (:99-133)
         Buf y1(x.size());
         add(x.data(), attn_out.data(), y1.data(), y1.size());
         Buf ffn = mlp.forward(norm2.forward(y1, rows), rows);
+        if (s.post_norms) ffn = post_mlp_norm.forward(ffn, rows);
         Buf y2(x.size());
         add(y1.data(), ffn.data(), y2.data(), y2.size());
         last_x = x;
@@ -837,6 +911,31 @@ ModelShape shape_of(const px_model_config& c) {
     s.qkv_bias = c.qkv_bias != 0;
     s.out_bias = c.out_bias != 0;
     s.mlp_bias = c.mlp_bias != 0;
+    s.act = c.hidden_act;
+    s.qk_norm = c.qk_norm != 0;
+    s.post_norms = c.post_norms != 0;
+    s.norm_offset = c.norm_weight_offset;
+    if (c.query_pre_attn_scalar > 0.0f)
+        s.score_scale = static_cast<float>(1.0 / std::sqrt(static_cast<double>(c.query_pre_attn_scalar)));
+    if (c.rope_scaling != 0) s.inv_freq = rope_inverse_frequencies(c, s.D);
+    return s;
+}
+
+// is_sliding_layer (hf_model.cpp:249-253) and ToAttentionConfig(config, layer) (:305-313): a
+// sliding layer gets the window and, when given, its own unscaled RoPE base.
+bool sliding_layer(const px_model_config& c, int64_t i) {
+    if (c.sliding_window <= 0) return false;
+    return c.sliding_layers == 0 || (i < 64 && ((c.sliding_layers >> i) & 1u) != 0);
+}
+
+ModelShape shape_of_layer(const px_model_config& c, int64_t i) {
+    ModelShape s = shape_of(c);
+    if (!sliding_layer(c, i)) return s;
+    s.window = static_cast<size_t>(c.sliding_window);
+    if (c.rope_local_base > 0.0f) {
+        s.theta = c.rope_local_base;
+        s.inv_freq.clear();
+    }
     return s;
 }
 
@@ -848,6 +947,10 @@ void validate(const px_model_config& c, bool lm) {
     if (s.rope && s.D % 2 != 0) throw std::invalid_argument("model config: RoPE needs an even head_dim");
     if (lm && (c.vocab_size <= 0 || c.num_layers <= 0))
         throw std::invalid_argument("model config: vocab_size and num_layers must be positive");
+    if (c.hidden_act < 0 || c.hidden_act > 1) throw std::invalid_argument("model config: unknown hidden_act");
+    if (c.rope_scaling < 0 || c.rope_scaling > 2) throw std::invalid_argument("model config: unknown rope_scaling");
+    if (c.sliding_layers != 0 && c.num_layers > 64)
+        throw std::invalid_argument("model config: sliding_layers names at most 64 layers");
 }
 
 int64_t block_params(const ModelShape& s) {
@@ -856,6 +959,8 @@ int64_t block_params(const ModelShape& s) {
     if (s.qkv_bias) n += q + 2 * kv;
     if (s.out_bias) n += s.d;
     if (s.mlp_bias) n += 2 * s.F + s.d;
+    if (s.qk_norm) n += 2 * s.D;
+    if (s.post_norms) n += 2 * s.d;
     return n;
 }
 
@@ -878,12 +983,9 @@ struct LM {
         p += c.vocab_size * s.d;
         for (int64_t i = 0; i < c.num_layers; ++i) {
             layers.push_back(std::make_unique<Block>());
-            layers.back()->init(s, p);
+            layers.back()->init(shape_of_layer(c, i), p);
         }
-        norm.d = s.d;
-        norm.eps = s.norm_eps;
-        norm.gamma.assign(p, p + s.d);
-        p += s.d;
+        norm.init(s.d, s.norm_eps, s.norm_offset, p);
         if (!c.tie_word_embeddings) head.init(s.d, c.vocab_size, false, p);
     }
 
@@ -899,6 +1001,8 @@ struct LM {
         }
         Buf x(static_cast<size_t>(rows * s.d));
         gather_rows(embed.data(), ids_f.data(), x.data(), rows, s.d);
+        if (c.embed_scale != 0.0f && c.embed_scale != 1.0f)  // ScaleEmbeddings (causal_lm.cpp:56-61)
+            axpby(c.embed_scale, x.data(), 0.0f, nullptr, x.data(), x.size());
         for (auto& layer : layers) x = layer->forward(x, N, L);
         head_x = norm.forward(x, rows);
         if (!c.tie_word_embeddings) return head.forward(head_x, rows);
@@ -1013,7 +1117,7 @@ void* pxo_block_create(const px_model_config* cfg, const float* params) {
             validate(*cfg, false);
             auto blk = std::make_unique<Block>();
             const float* p = params;
-            blk->init(shape_of(*cfg), p);
+            blk->init(shape_of_layer(*cfg, 0), p);
             b = blk.release();
         }) != 0)
         return nullptr;

@@ -41,6 +41,23 @@ typedef struct px_model_config {
     int32_t mlp_bias;
     int32_t tie_word_embeddings;
     int32_t reserved;
+    /* The architecture variants ToAttentionConfig and TransformerBlockOptions carry
+     * (hf_model.cpp:282-313, causal_lm.cpp:30-54); all zero is the Llama family. */
+    int32_t hidden_act;          /* 0 SiLU, 1 GeLU with the tanh approximation (gelu_pytorch_tanh) */
+    int32_t qk_norm;             /* RMSNorm over each head's queries and keys, eps rms_norm_eps */
+    int32_t post_norms;          /* Gemma 3 sandwich norms after the attention and after the MLP */
+    int32_t rope_scaling;        /* full-attention layers: 0 none, 1 linear, 2 llama3 */
+    float norm_weight_offset;    /* every RMSNorm scales by offset + gamma (Gemma 3: 1) */
+    float embed_scale;           /* embeddings multiplied by this; 0 means 1 (Gemma 3: sqrt(hidden)) */
+    float query_pre_attn_scalar; /* > 0: scores scaled by 1/sqrt(this), else by 1/sqrt(head_dim) */
+    float rope_local_base;       /* > 0: the sliding layers' own RoPE base, without scaling */
+    float rope_factor;           /* rope_scaling's factor, low_freq_factor, high_freq_factor */
+    float rope_low_freq_factor;
+    float rope_high_freq_factor;
+    int32_t reserved2;
+    int64_t rope_original_max_position; /* rope_scaling's original_max_position_embeddings */
+    int64_t sliding_window;      /* > 0: a sliding layer's query i sees only keys j > i - window */
+    uint64_t sliding_layers;     /* bit i: layer i slides (layer_types); 0 with a window: every layer */
 } px_model_config;
 
 /* LRPRuleConfig (include/pulsatrix/lrp_rule_config.hpp:72-115): rule in LRPRule order

@@ -42,8 +42,53 @@ int guarded(F&& f) {
 int64_t kv_heads(const px_model_config& c) { return c.num_kv_heads > 0 ? c.num_kv_heads : c.num_heads; }
 int64_t head_dim(const px_model_config& c) { return c.head_dim > 0 ? c.head_dim : c.hidden_size / c.num_heads; }
 
+// The reference's HfModelConfig for a px_model_config: its own ToAttentionConfig(config, layer)
+// then builds each layer's attention.
+HfModelConfig hf_config(const px_model_config& c) {
+    HfModelConfig hc;
+    hc.model_type = "llama";
+    hc.hidden_size = c.hidden_size;
+    hc.intermediate_size = c.intermediate_size;
+    hc.num_hidden_layers = c.num_layers;
+    hc.num_attention_heads = c.num_heads;
+    hc.num_key_value_heads = kv_heads(c);
+    hc.head_dim = head_dim(c);
+    hc.vocab_size = c.vocab_size;
+    hc.rms_norm_eps = c.rms_norm_eps;
+    hc.rope_theta = c.rope_theta;
+    hc.tie_word_embeddings = c.tie_word_embeddings != 0;
+    hc.qkv_bias = c.qkv_bias != 0;
+    hc.out_bias = c.out_bias != 0;
+    hc.mlp_bias = c.mlp_bias != 0;
+    hc.causal = c.causal != 0;
+    hc.hidden_act = c.hidden_act == 1 ? "gelu_pytorch_tanh" : "silu";
+    hc.qk_norm = c.qk_norm != 0;
+    hc.post_norms = c.post_norms != 0;
+    hc.norm_weight_offset = c.norm_weight_offset;
+    if (c.embed_scale != 0.0f) hc.embed_scale = c.embed_scale;
+    if (c.query_pre_attn_scalar > 0.0f) hc.query_pre_attn_scalar = c.query_pre_attn_scalar;
+    if (c.rope_local_base > 0.0f) hc.rope_local_base_freq = c.rope_local_base;
+    if (c.rope_scaling != 0) {
+        HfRopeScaling r;
+        r.type = c.rope_scaling == 1 ? "linear" : "llama3";
+        r.factor = c.rope_factor;
+        r.low_freq_factor = c.rope_low_freq_factor;
+        r.high_freq_factor = c.rope_high_freq_factor;
+        r.original_max_position_embeddings = c.rope_original_max_position;
+        hc.rope_scaling = r;
+    }
+    if (c.sliding_window > 0) {
+        hc.sliding_window = c.sliding_window;
+        if (c.sliding_layers != 0)
+            for (int64_t i = 0; i < c.num_layers; ++i)
+                hc.layer_types.push_back(((c.sliding_layers >> i) & 1u) ? "sliding_attention" : "full_attention");
+    }
+    return hc;
+}
+
 AttentionConfig attention_config(const px_model_config& c) {
-    AttentionConfig a;
+    if (c.use_rope && c.rope_rotate_half) return ToAttentionConfig(hf_config(c), 0);
+    AttentionConfig a;  // the layouts ToAttentionConfig does not produce (no RoPE, adjacent pairs)
     a.d_model = c.hidden_size;
     a.num_heads = c.num_heads;
     a.num_kv_heads = kv_heads(c);
@@ -55,6 +100,16 @@ AttentionConfig attention_config(const px_model_config& c) {
     a.out_bias = c.out_bias != 0;
     a.causal = c.causal != 0;
     return a;
+}
+
+TransformerBlockOptions block_options(const px_model_config& c) {
+    TransformerBlockOptions opt;
+    opt.norm_eps = c.rms_norm_eps;
+    opt.mlp_bias = c.mlp_bias != 0;
+    opt.mlp_activation = c.hidden_act == 1 ? GatedActivation::GeluTanh : GatedActivation::Silu;
+    opt.post_norms = c.post_norms != 0;
+    opt.norm_weight_offset = c.norm_weight_offset;
+    return opt;
 }
 
 // Names and sizes of one block's parameters in the flat blob's order.
@@ -70,10 +125,18 @@ std::vector<std::pair<std::string, int64_t>> block_layout(const px_model_config&
     lin("mha.k_proj", d, kv, c.qkv_bias);
     lin("mha.v_proj", d, kv, c.qkv_bias);
     lin("mha.out_proj", q, d, c.out_bias);
+    if (c.qk_norm) {
+        out.push_back({"mha.q_norm.weight", head_dim(c)});
+        out.push_back({"mha.k_norm.weight", head_dim(c)});
+    }
     out.push_back({"norm2.weight", d});
     lin("swiglu.gate_proj", d, f, c.mlp_bias);
     lin("swiglu.up_proj", d, f, c.mlp_bias);
     lin("swiglu.down_proj", f, d, c.mlp_bias);
+    if (c.post_norms) {
+        out.push_back({"post_attn_norm.weight", d});
+        out.push_back({"post_mlp_norm.weight", d});
+    }
     return out;
 }
 
@@ -132,10 +195,8 @@ void* pxr_block_create(const px_model_config* cfg, const float* params) {
     RefBlock* out = nullptr;
     guarded([&] {
         auto b = std::make_unique<RefBlock>();
-        TransformerBlockOptions opt;
-        opt.norm_eps = cfg->rms_norm_eps;
-        opt.mlp_bias = cfg->mlp_bias != 0;
-        b->block = std::make_unique<TransformerBlock>(attention_config(*cfg), cfg->intermediate_size, &b->be, opt);
+        b->block = std::make_unique<TransformerBlock>(attention_config(*cfg), cfg->intermediate_size, &b->be,
+                                                      block_options(*cfg));
         load(*b->block, block_layout(*cfg), params, &b->be);
         b->d = cfg->hidden_size;
         out = b.release();
@@ -177,23 +238,7 @@ void* pxr_lm_create(const px_model_config* cfg, const float* params) {
     RefLM* out = nullptr;
     guarded([&] {
         auto m = std::make_unique<RefLM>();
-        HfModelConfig hc;
-        hc.model_type = "llama";
-        hc.hidden_size = cfg->hidden_size;
-        hc.intermediate_size = cfg->intermediate_size;
-        hc.num_hidden_layers = cfg->num_layers;
-        hc.num_attention_heads = cfg->num_heads;
-        hc.num_key_value_heads = kv_heads(*cfg);
-        hc.head_dim = head_dim(*cfg);
-        hc.vocab_size = cfg->vocab_size;
-        hc.rms_norm_eps = cfg->rms_norm_eps;
-        hc.rope_theta = cfg->rope_theta;
-        hc.tie_word_embeddings = cfg->tie_word_embeddings != 0;
-        hc.qkv_bias = cfg->qkv_bias != 0;
-        hc.out_bias = cfg->out_bias != 0;
-        hc.mlp_bias = cfg->mlp_bias != 0;
-        hc.causal = cfg->causal != 0;
-        m->lm = std::make_unique<CausalLM>(hc, &m->be);
+        m->lm = std::make_unique<CausalLM>(hf_config(*cfg), &m->be);
         std::vector<std::pair<std::string, int64_t>> layout{{"embed_tokens.weight", cfg->vocab_size * cfg->hidden_size}};
         for (int64_t i = 0; i < cfg->num_layers; ++i)
             for (const auto& [name, size] : block_layout(*cfg)) layout.push_back({"layers." + std::to_string(i) + "." + name, size});

@@ -223,7 +223,14 @@ class ModelConfig(ctypes.Structure):
                 ("rms_norm_eps", ctypes.c_float), ("rope_theta", ctypes.c_float), ("use_rope", ctypes.c_int32),
                 ("rope_rotate_half", ctypes.c_int32), ("causal", ctypes.c_int32), ("qkv_bias", ctypes.c_int32),
                 ("out_bias", ctypes.c_int32), ("mlp_bias", ctypes.c_int32), ("tie_word_embeddings", ctypes.c_int32),
-                ("reserved", ctypes.c_int32)]
+                ("reserved", ctypes.c_int32), ("hidden_act", ctypes.c_int32), ("qk_norm", ctypes.c_int32),
+                ("post_norms", ctypes.c_int32), ("rope_scaling", ctypes.c_int32),
+                ("norm_weight_offset", ctypes.c_float), ("embed_scale", ctypes.c_float),
+                ("query_pre_attn_scalar", ctypes.c_float), ("rope_local_base", ctypes.c_float),
+                ("rope_factor", ctypes.c_float), ("rope_low_freq_factor", ctypes.c_float),
+                ("rope_high_freq_factor", ctypes.c_float), ("reserved2", ctypes.c_int32),
+                ("rope_original_max_position", c_i64), ("sliding_window", c_i64),
+                ("sliding_layers", ctypes.c_uint64)]
 
 
 EPSILON, GAMMA, ALPHA_BETA, ZBOX = 0, 1, 2, 3  # LRPRule order

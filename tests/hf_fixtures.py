@@ -27,27 +27,26 @@ def hf_tiny(name):
     for f in sorted(os.listdir(d)):
         if f.startswith("model") and f.endswith(".safetensors"):
             tensors.update(_load_st(os.path.join(d, f)))
-    heads = hc["num_attention_heads"]
-    rope = hc.get("rope_parameters", {}).get("rope_theta", hc.get("rope_theta", 10000.0))
-    qkv_bias = bool(hc.get("attention_bias", hc["model_type"] == "qwen2"))
-    cfg = model_config(vocab_size=hc["vocab_size"], hidden_size=hc["hidden_size"],
-                       num_layers=hc["num_hidden_layers"], num_heads=heads,
-                       num_kv_heads=hc.get("num_key_value_heads", heads),
-                       head_dim=hc.get("head_dim", hc["hidden_size"] // heads),
-                       intermediate_size=hc["intermediate_size"], rms_norm_eps=hc["rms_norm_eps"],
-                       rope_theta=float(rope), use_rope=1, rope_rotate_half=1, causal=1, qkv_bias=int(qkv_bias),
-                       out_bias=0, mlp_bias=int(hc.get("mlp_bias", False)),
-                       tie_word_embeddings=int(hc.get("tie_word_embeddings", True)))
+    cfg = config_of(hc)
+    gemma = hc["model_type"] in ("gemma3", "gemma3_text")
     named = {"embed_tokens.weight": tensors["model.embed_tokens.weight"], "norm.weight": tensors["model.norm.weight"]}
     for i in range(cfg.num_layers):
         hf, px = "model.layers.%d." % i, "layers.%d." % i
         named[px + "norm1.weight"] = tensors[hf + "input_layernorm.weight"]
-        named[px + "norm2.weight"] = tensors[hf + "post_attention_layernorm.weight"]
+        if gemma:  # sandwich norms (HuggingFaceMapping, src/causal_lm.cpp:257-291)
+            named[px + "norm2.weight"] = tensors[hf + "pre_feedforward_layernorm.weight"]
+            named[px + "post_attn_norm.weight"] = tensors[hf + "post_attention_layernorm.weight"]
+            named[px + "post_mlp_norm.weight"] = tensors[hf + "post_feedforward_layernorm.weight"]
+        else:
+            named[px + "norm2.weight"] = tensors[hf + "post_attention_layernorm.weight"]
         for p in ("q_proj", "k_proj", "v_proj"):
             named[px + "mha.%s.weight" % p] = tensors[hf + "self_attn.%s.weight" % p].T
             if cfg.qkv_bias:
                 named[px + "mha.%s.bias" % p] = tensors[hf + "self_attn.%s.bias" % p]
         named[px + "mha.out_proj.weight"] = tensors[hf + "self_attn.o_proj.weight"].T
+        if cfg.qk_norm:
+            named[px + "mha.q_norm.weight"] = tensors[hf + "self_attn.q_norm.weight"]
+            named[px + "mha.k_norm.weight"] = tensors[hf + "self_attn.k_norm.weight"]
         for p in ("gate_proj", "up_proj", "down_proj"):
             named[px + "swiglu.%s.weight" % p] = tensors[hf + "mlp.%s.weight" % p].T
     if not cfg.tie_word_embeddings:
@@ -56,6 +55,48 @@ def hf_tiny(name):
     golden = _load_st(os.path.join(d, "golden.safetensors"))
     attnlrp = _load_st(os.path.join(d, "attnlrp.safetensors"))
     return cfg, params, golden, attnlrp
+
+
+def config_of(hc):
+    """px_model_config of a Hugging Face config.json, as ParseHfConfig + ToAttentionConfig read it
+    (src/hf_model.cpp:99-313) for the Llama, Qwen2, Qwen3 and Gemma 3 fields."""
+    heads = hc["num_attention_heads"]
+    mt = hc["model_type"]
+    gemma = mt in ("gemma3", "gemma3_text")
+    rp = hc.get("rope_parameters") or {}
+    full, sliding = rp.get("full_attention"), rp.get("sliding_attention")
+    if "rope_theta" in hc:
+        rope = hc["rope_theta"]
+    elif isinstance(full, dict):
+        rope = full.get("rope_theta", 10000.0)
+    else:
+        rope = rp.get("rope_theta", 10000.0)
+    scaling = full if isinstance(full, dict) else (rp or hc.get("rope_scaling") or {})
+    stype = scaling.get("rope_type", scaling.get("type", "default"))
+    local = hc.get("rope_local_base_freq", sliding.get("rope_theta") if isinstance(sliding, dict) else None)
+    window = hc.get("sliding_window") if hc.get("use_sliding_window", True) else None
+    if window is not None and 0 < hc.get("max_position_embeddings", 0) <= window:
+        window = None
+    types = hc.get("layer_types") or []
+    mask = sum(1 << i for i, t in enumerate(types) if t == "sliding_attention") if window else 0
+    act = hc.get("hidden_act", hc.get("hidden_activation", "silu"))
+    qkv_bias = bool(hc.get("attention_bias", mt == "qwen2"))
+    return model_config(
+        vocab_size=hc["vocab_size"], hidden_size=hc["hidden_size"], num_layers=hc["num_hidden_layers"],
+        num_heads=heads, num_kv_heads=hc.get("num_key_value_heads", heads),
+        head_dim=hc.get("head_dim", hc["hidden_size"] // heads), intermediate_size=hc["intermediate_size"],
+        rms_norm_eps=hc.get("rms_norm_eps", 1e-6), rope_theta=float(rope), use_rope=1, rope_rotate_half=1, causal=1,
+        qkv_bias=int(qkv_bias), out_bias=0, mlp_bias=int(hc.get("mlp_bias", False)),
+        tie_word_embeddings=int(hc.get("tie_word_embeddings", True)),
+        hidden_act=0 if act == "silu" else 1, qk_norm=int(mt in ("qwen3", "qwen3_moe", "gemma3", "gemma3_text")),
+        post_norms=int(gemma), norm_weight_offset=1.0 if gemma else 0.0,
+        embed_scale=float(np.float32(np.sqrt(np.float64(hc["hidden_size"])))) if gemma else 0.0,
+        query_pre_attn_scalar=float(hc.get("query_pre_attn_scalar") or 0.0),
+        rope_local_base=float(local or 0.0), rope_scaling={"default": 0, "linear": 1, "llama3": 2}[stype],
+        rope_factor=float(scaling.get("factor", 1.0)), rope_low_freq_factor=float(scaling.get("low_freq_factor", 1.0)),
+        rope_high_freq_factor=float(scaling.get("high_freq_factor", 1.0)),
+        rope_original_max_position=int(scaling.get("original_max_position_embeddings", 0)),
+        sliding_window=int(window or 0), sliding_layers=mask)
 
 
 def sequences(fixture, prefix="ids"):

@@ -37,6 +37,21 @@ class ModelConfig(ctypes.Structure):
         ("mlp_bias", ctypes.c_int32),
         ("tie_word_embeddings", ctypes.c_int32),
         ("reserved", ctypes.c_int32),
+        ("hidden_act", ctypes.c_int32),
+        ("qk_norm", ctypes.c_int32),
+        ("post_norms", ctypes.c_int32),
+        ("rope_scaling", ctypes.c_int32),
+        ("norm_weight_offset", ctypes.c_float),
+        ("embed_scale", ctypes.c_float),
+        ("query_pre_attn_scalar", ctypes.c_float),
+        ("rope_local_base", ctypes.c_float),
+        ("rope_factor", ctypes.c_float),
+        ("rope_low_freq_factor", ctypes.c_float),
+        ("rope_high_freq_factor", ctypes.c_float),
+        ("reserved2", ctypes.c_int32),
+        ("rope_original_max_position", ctypes.c_int64),
+        ("sliding_window", ctypes.c_int64),
+        ("sliding_layers", ctypes.c_uint64),
     ]
 
     def kv_heads(self):
@@ -95,10 +110,14 @@ def block_layout(cfg):
     lin("mha.k_proj", d, kv, cfg.qkv_bias)
     lin("mha.v_proj", d, kv, cfg.qkv_bias)
     lin("mha.out_proj", q, d, cfg.out_bias)
+    if cfg.qk_norm:
+        out += [("mha.q_norm.weight", (cfg.hd(),)), ("mha.k_norm.weight", (cfg.hd(),))]
     out.append(("norm2.weight", (d,)))
     lin("swiglu.gate_proj", d, f, cfg.mlp_bias)
     lin("swiglu.up_proj", d, f, cfg.mlp_bias)
     lin("swiglu.down_proj", f, d, cfg.mlp_bias)
+    if cfg.post_norms:
+        out += [("post_attn_norm.weight", (d,)), ("post_mlp_norm.weight", (d,))]
     return out
 
 
@@ -276,16 +295,21 @@ def fill_normal(n, seed, std):
     return out
 
 
+def is_norm_weight(name):
+    return name.endswith("norm.weight") or name.endswith("norm1.weight") or name.endswith("norm2.weight")
+
+
 def synthetic_params(cfg, seed, std=0.02, block=False):
-    """The flat blob of a random-init model: N(0, std) from seed, every RMSNorm gamma = 1."""
+    """The flat blob of a random-init model: N(0, std) from seed, every RMSNorm's effective scale
+    (norm_weight_offset + gamma) 1."""
     layout = block_layout(cfg) if block else lm_layout(cfg)
     total = sum(int(np.prod(s)) for _, s in layout)
     blob = fill_normal(total, seed, std)
     off = 0
     for name, shape in layout:
         size = int(np.prod(shape))
-        if name.endswith("norm1.weight") or name.endswith("norm2.weight") or name == "norm.weight":
-            blob[off:off + size] = 1.0
+        if is_norm_weight(name):
+            blob[off:off + size] = np.float32(1.0) - np.float32(cfg.norm_weight_offset)
         off += size
     return blob
 

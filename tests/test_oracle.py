@@ -23,7 +23,7 @@ def close(actual, expected, rel=1e-4):
     return np.all(np.abs(np.asarray(actual) - expected) <= tol)
 
 
-@pytest.mark.parametrize("name", ["llama", "qwen2"])
+@pytest.mark.parametrize("name", ["llama", "qwen2", "gemma3"])
 def test_oracle_logits_match_transformers(name):
     cfg, params, golden, _ = hf_tiny(name)
     lm = oc.oracle().lm(cfg, params)
@@ -33,7 +33,7 @@ def test_oracle_logits_match_transformers(name):
         assert close(logits, golden["logits.%d" % k]), (name, k, np.abs(logits - golden["logits.%d" % k]).max())
 
 
-@pytest.mark.parametrize("name", ["llama", "qwen2"])
+@pytest.mark.parametrize("name", ["llama", "qwen2", "gemma3"])
 def test_oracle_attnlrp_matches_lxt(name):
     """The checks of tests/attnlrp_parity_test.cpp:28-51 (via CompareToAttnLrp)."""
     cfg, params, _, ref = hf_tiny(name)
@@ -195,3 +195,70 @@ def test_oracle_zero_weight_block_is_identity():
 def test_fill_normal_moments():
     v = oc.fill_normal(200000, 42, 0.02).astype(np.float64)
     assert abs(v.mean()) < 3e-4 and abs(v.std() - 0.02) < 3e-4
+
+
+def gemma_config(**kw):
+    """A Gemma-3-style config: GeLU-tanh gates, QK-norm, sandwich norms, (1 + w) norms, scaled
+    embeddings, query_pre_attn_scalar, sliding layers with their own RoPE base, linear RoPE scaling
+    on the full layers (the hf_tiny gemma3 fixture's settings at other sizes)."""
+    base = dict(vocab_size=211, hidden_size=48, num_layers=3, num_heads=4, num_kv_heads=1, head_dim=24,
+                intermediate_size=56, rms_norm_eps=1e-6, rope_theta=10000.0, hidden_act=1, qk_norm=1, post_norms=1,
+                norm_weight_offset=1.0, embed_scale=float(np.float32(np.sqrt(48.0))), query_pre_attn_scalar=20.0,
+                rope_local_base=100.0, rope_scaling=1, rope_factor=2.0, sliding_window=5, sliding_layers=0b101)
+    base.update(kw)
+    return oc.model_config(**base)
+
+
+@needs_ref
+@pytest.mark.parametrize("tied", [1, 0])
+def test_oracle_gemma_lm_bit_identical_to_reference(tied):
+    """Every Gemma 3 variant at once, LXT and pre-bias epsilon rules and Gamma, against the compiled
+    reference built through its own ToAttentionConfig(config, layer)."""
+    cfg = gemma_config(tie_word_embeddings=tied)
+    params = oc.synthetic_params(cfg, 23, std=0.1)
+    ids = np.random.RandomState(2).randint(0, 211, size=(2, 13))
+    o, r = oc.oracle().lm(cfg, params), oc.ref().lm(cfg, params)
+    lo = o.forward(ids)
+    assert np.array_equal(lo, r.forward(ids))
+    seed = np.zeros_like(lo)
+    for n in range(2):
+        t = int(np.argmax(lo[n, -1]))
+        seed[n, -1, t] = lo[n, -1, t]
+    for a, b in zip(o.relevance(seed, LXT_EPS, True, want_kv=True), r.relevance(seed, LXT_EPS, True, want_kv=True)):
+        assert np.array_equal(a, b)
+    for a, b in zip(o.relevance(seed, 1e-6, False), r.relevance(seed, 1e-6, False)):
+        assert np.array_equal(a, b)
+    g = oc.lrp_rule(oc.GAMMA, gamma=0.25)
+    for a, b in zip(o.relevance_rule(seed, g), r.relevance_rule(seed, g)):
+        assert np.array_equal(a, b)
+
+
+@needs_ref
+@pytest.mark.parametrize("kw", [dict(sliding_layers=0), dict(rope_scaling=2, rope_factor=8.0, rope_low_freq_factor=1.0,
+                                                              rope_high_freq_factor=4.0,
+                                                              rope_original_max_position=8, sliding_window=0)])
+def test_oracle_variant_lm_bit_identical_to_reference(kw):
+    """A window on every layer (Mistral's form), and llama3 RoPE scaling without windows."""
+    cfg = gemma_config(**kw)
+    params = oc.synthetic_params(cfg, 29, std=0.1)
+    ids = np.random.RandomState(3).randint(0, 211, size=(1, 17))
+    o, r = oc.oracle().lm(cfg, params), oc.ref().lm(cfg, params)
+    lo = o.forward(ids)
+    assert np.array_equal(lo, r.forward(ids))
+    seed = np.zeros_like(lo)
+    t = int(np.argmax(lo[0, -1]))
+    seed[0, -1, t] = lo[0, -1, t]
+    for a, b in zip(o.relevance(seed, LXT_EPS, True), r.relevance(seed, LXT_EPS, True)):
+        assert np.array_equal(a, b)
+
+
+@needs_ref
+def test_oracle_gemma_block_bit_identical_to_reference():
+    cfg = gemma_config(num_layers=1, sliding_layers=1)
+    params = oc.synthetic_params(cfg, 5, std=0.2, block=True)
+    x = oc.fill_normal(2 * 9 * 48, 6, 1.0).reshape(2, 9, 48)
+    o, r = oc.oracle().block(cfg, params), oc.ref().block(cfg, params)
+    yo = o.forward(x)
+    assert np.array_equal(yo, r.forward(x))
+    seed = oc.fill_normal(yo.size, 8, 1.0).reshape(yo.shape)
+    assert np.array_equal(o.relevance(seed, 0.1, True), r.relevance(seed, 0.1, True))
