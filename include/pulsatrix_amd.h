@@ -12,8 +12,10 @@
  * (CausalLM::named_parameters(), causal_lm.cpp:115-125; Linear weights (in, out)):
  *   embed_tokens.weight (V, d)
  *   per layer: norm1.weight (d), mha.{q,k,v}_proj.weight (d, H*D | Hkv*D) [+ .bias when qkv_bias],
- *              mha.out_proj.weight (H*D, d) [+ .bias when out_bias], norm2.weight (d),
- *              swiglu.{gate,up}_proj.weight (d, F) [+ .bias], swiglu.down_proj.weight (F, d) [+ .bias]
+ *              mha.out_proj.weight (H*D, d) [+ .bias when out_bias], [mha.{q,k}_norm.weight (D) with
+ *              qk_norm], norm2.weight (d), swiglu.{gate,up}_proj.weight (d, F) [+ .bias],
+ *              swiglu.down_proj.weight (F, d) [+ .bias], [post_attn_norm.weight, post_mlp_norm.weight
+ *              (d) with post_norms]
  *   norm.weight (d), lm_head.weight (d, V) when not tied.
  * A bare block uses the per-layer part alone.
  */
@@ -96,7 +98,8 @@ int pxa_backend_memory(size_t* in_use, size_t* cached);
 void pxa_fill_normal(float* dst, size_t n, uint64_t seed, double stddev);
 int64_t pxa_param_count(const px_model_config* cfg);
 int64_t pxa_block_param_count(const px_model_config* cfg);
-/* The flat blob of a random-init model: N(0, stddev) from seed, every RMSNorm gamma = 1. */
+/* The flat blob of a random-init model: N(0, stddev) from seed, every RMSNorm's effective scale
+ * (norm_weight_offset + gamma) 1. */
 int pxa_synthetic_params(const px_model_config* cfg, int block, uint64_t seed, double stddev, float* dst);
 
 /* ---- TransformerBlock (transformer_block.hpp) ; host tensors ---- */

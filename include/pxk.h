@@ -94,7 +94,8 @@ enum {
                                 alternate 32-wide gate and up blocks (block 2b: gate features 32b..32b+31,
                                 block 2b+1: the same up features); N = 2F, F a multiple of 32, no bias.
                                 C (ld >= 2F) = z as [gate | up] halves; C3 = gate_post = silu(z_gate)
-                                (x / (1 + e^-x), cpu_backend.cpp:29); C2 = hidden = gate_post * z_up. */
+                                (x / (1 + e^-x), cpu_backend.cpp:29; GeLU tanh with gate_act 1);
+                                C2 = hidden = gate_post * z_up. */
 };
 
 enum {
@@ -136,6 +137,8 @@ typedef struct pxk_gemm_desc {
     float* workspace;     /* split-K partials */
     size_t workspace_bytes;
     int64_t rope_cols;    /* ROPE_FWD: the leading columns (whole heads) that are rotated into C3 */
+    int32_t gate_act;     /* SWIGLU_FWD's gate: 0 SiLU, 1 GeLU tanh (pointwise_math.hpp:32-36) */
+    int32_t reserved;
 } pxk_gemm_desc;
 
 /* Bytes of workspace pxk_gemm needs for this descriptor (0 when it runs without split-K). */
@@ -176,9 +179,9 @@ int pxk_lrp_stabilized_divide(const float* r, const float* denom, const float* g
 /* The Eq. 15 scaled relevance of a product O = A B: s = r / (2 o + eps sign o) (lrp_math.hpp:57-61),
  * the shared factor of DeviceBackend::lrp_bilinear_matmul's two shares (:643). */
 int pxk_lrp_bilinear_scale(const float* r, const float* o, float* s, int64_t n, float eps, void* stream);
-/* SwiGLU gate (swiglu_module.cpp:80-88): gate_post = silu(gate), hidden = gate_post * up, over an
- * (rows x 2F) [gate | up] buffer with row stride ld. */
-int pxk_swiglu_forward(const float* gu, int64_t ld, float* gate_post, float* hidden, int64_t rows, int64_t f,
+/* SwiGLU gate (swiglu_module.cpp:80-88): gate_post = act(gate), hidden = gate_post * up, over an
+ * (rows x 2F) [gate | up] buffer with row stride ld; act 0 SiLU, 1 GeLU tanh (Gemma's GeGLU). */
+int pxk_swiglu_forward(const float* gu, int64_t ld, float* gate_post, float* hidden, int64_t rows, int64_t f, int act,
                        void* stream);
 /* DeviceBackend::copy_2d (:783), accumulate_rows (:792), gather_rows (:596) */
 int pxk_copy_2d(float* dst, int64_t dst_stride, const float* src, int64_t src_stride, int64_t rows, int64_t cols,
@@ -310,13 +313,26 @@ int pxk_attention_relevance_kv(const pxk_attn_rel_kv_desc* d, void* stream);
  * each query sees; masked entries of P are written 0. raw (slices, L, L); only its visible
  * entries are read. */
 int pxk_attention_softmax(const float* raw, float* p, int64_t slices, int64_t l, float scale, int causal,
-                          void* stream);
+                          int64_t window, void* stream);
 /* The AttnLRP score step, fused: r_sc = x * (r_attn - P * sum(r_attn)) with x = scale * raw
  * (SoftmaxModule rule, lrp_math.hpp:89-98), masked entries 0 (fill_masked(0), :441), then the
  * Q K^T bilinear denominator s = r_sc / (2 raw + eps sign raw) (lrp_math.hpp:57-61). Writes s
  * over whole rows (0 where masked). s may alias r_attn. */
 int pxk_attention_lrp_scores(const float* r_attn, const float* p, const float* raw, float* s, int64_t slices,
-                             int64_t l, float scale, float eps, int causal, void* stream);
+                             int64_t l, float scale, float eps, int causal, int64_t window, void* stream);
+/* QK-Norm (multihead_attention_module.cpp step 3): RMSNorm (row_math.hpp:59-71) over each head's
+ * head_dim values of head-packed rows, in (rows x heads*head_dim, row stride ld_in) -> out (row
+ * stride ld_out); gamma (head_dim) is the effective scale (weight offset already added). */
+int pxk_rms_norm_heads(const float* in, int64_t ld_in, float* out, int64_t ld_out, const float* gamma, int64_t rows,
+                       int64_t heads, int64_t head_dim, float eps, void* stream);
+/* The query share's RoPE epsilon rule (lrp_math.hpp:104-123) on token-major head-packed rows, for
+ * head_dims the ROPE_REL epilogue cannot take: r = y * acc (acc = s K, y the rotated queries),
+ * r_in from x (the queries before rotation) per pair, then g = r_in / stab(z + bias), or g = r_in
+ * when rel_only. Positions are row % seq_len. */
+int pxk_lrp_rope_rows(const float* acc, int64_t ld_acc, const float* x, int64_t ldx, const float* y, int64_t ldy,
+                      const float* z, int64_t ldz, const float* bias, const float* cos_t, const float* sin_t, float* g,
+                      int64_t ldg, int64_t rows, int64_t seq_len, int64_t heads, int64_t head_dim, float eps,
+                      int rotate_half, int rel_only, void* stream);
 /* RoPE of the packed projections (rope_module.cpp:104-121 + permute-free layout): q_out (rows x H*D)
  * and k_out (rows x Hkv*D), both with row stride ld_out, from the q/k columns of `in` (row stride
  * ld_in), positions = row % seq_len. The attention forward's rotation where head_dim does not tile

@@ -13,11 +13,13 @@
 #pragma once
 
 #include <cstdint>
+#include <memory>
 #include <vector>
 
 #include "pulsatrix/detail/fused.hpp"
 #include "pulsatrix/linear_module.hpp"
 #include "pulsatrix/module.hpp"
+#include "pulsatrix/rms_norm_module.hpp"
 
 namespace pulsatrix {
 
@@ -56,6 +58,10 @@ public:
     [[nodiscard]] LinearModule& k_proj() { return k_proj_; }
     [[nodiscard]] LinearModule& v_proj() { return v_proj_; }
     [[nodiscard]] LinearModule& out_proj() { return out_proj_; }
+    /** @brief QK-Norm's query and key RMSNorms (multihead_attention_module.cpp:116-121); throws
+     *         std::logic_error when the module has none. */
+    [[nodiscard]] RMSNormModule& q_norm();
+    [[nodiscard]] RMSNormModule& k_norm();
     [[nodiscard]] const AttentionConfig& config() const noexcept { return config_; }
     /** @brief Relevance at the key / value projections' outputs, (N*L, Hkv*D), from the last
      *         propagate_relevance() (multihead_attention_module.cpp:488-496). */
@@ -82,18 +88,24 @@ private:
     void run_attention_unfused(const float* q, int64_t ldq, const float* k, int64_t ldk, const float* v, int64_t n,
                                int64_t l);
     void relevance_scores_unfused(const float* spv, float eps, bool bid, bool rel_only);
+    /** @brief The sliding window that masks something at length l (0: none). */
+    [[nodiscard]] int64_t window_for(int64_t l) const;
+    /** @brief Whether the fused attention kernels take this layer at length l (head_dim up to 128,
+     *         score rows within LDS, no active sliding window). */
+    [[nodiscard]] bool fused_attention(int64_t l) const;
 
     AttentionConfig config_;
     int64_t d_, H_, Hkv_, D_;
     MI355XBackend* be_;
     LinearModule q_proj_, k_proj_, v_proj_, out_proj_;
+    std::unique_ptr<RMSNormModule> q_norm_, k_norm_;
     uint64_t packed_version_ = ~uint64_t{0};
     detail::DevBuf wqkv_, bqkv_;
     int64_t table_len_ = -1;
     detail::DevBuf cos_, sin_;
     int64_t N_ = 0, L_ = 0;
     const float* x_ = nullptr;
-    detail::DevBuf x_copy_, qkv_z_, qkv_y_, qk_rot_, raw_, p_, ctx_, out_z_, out_y_;
+    detail::DevBuf x_copy_, qkv_z_, qkv_y_, qk_norm_out_, qk_rot_, raw_, p_, ctx_, out_z_, out_y_;
     detail::DevBuf spv_, ra_, g_, r_in_, rctx_;
     detail::AffineRule out_rule_, qkv_rule_;
     Tensor key_rel_, value_rel_;

@@ -20,7 +20,19 @@ public:
 
     void set_gamma(const std::vector<float>& values);
     [[nodiscard]] const Tensor& gamma() const noexcept { return gamma_; }
-    [[nodiscard]] Tensor& gamma() noexcept { return gamma_; }
+    /** @brief Mutable access counts as a change (the effective scale is rebuilt). */
+    [[nodiscard]] Tensor& gamma() noexcept {
+        ++version_;
+        return gamma_;
+    }
+    /** @brief Scale by offset + gamma (Gemma's 1 + w; rms_norm_module.cpp:40-49). */
+    void set_weight_offset(float offset) noexcept {
+        offset_ = offset;
+        ++version_;
+    }
+    [[nodiscard]] float weight_offset() const noexcept { return offset_; }
+    /** @brief The scale the forward applies: gamma, or offset + gamma computed on the device. */
+    const float* effective_gamma();
     [[nodiscard]] float eps() const noexcept { return eps_; }
     [[nodiscard]] int64_t num_features() const noexcept { return d_; }
 
@@ -36,8 +48,10 @@ private:
     float eps_;
     MI355XBackend* be_;
     Tensor gamma_;
+    float offset_ = 0.0f;
+    uint64_t version_ = 0, eff_version_ = ~uint64_t{0};
     int64_t rows_ = 0;
-    detail::DevBuf out_, rms_;
+    detail::DevBuf out_, rms_, eff_;
 };
 
 }  // namespace pulsatrix

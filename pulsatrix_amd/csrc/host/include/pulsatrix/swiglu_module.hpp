@@ -44,6 +44,7 @@ private:
     bool use_bias_;
     MI355XBackend* be_;
     LinearModule gate_proj_, up_proj_, down_proj_;
+    int act_;  // the gate: 0 SiLU, 1 GeLU tanh
     uint64_t packed_version_ = ~uint64_t{0};
     detail::DevBuf wgu_, wgu_il_, bgu_;
     int64_t rows_ = 0;

@@ -1,9 +1,13 @@
 /** @file transformer_block.hpp
  *  @brief Pre-norm decoder block x + attn(norm1(x)), then + mlp(norm2(.)) (the surface of
  *         include/pulsatrix/transformer_block.hpp); relevance per transformer_block.cpp:189-227
- *         with both residual adds fused into the sublayers' last GEMM epilogues.
+ *         with both residual adds fused into the sublayers' last GEMM epilogues. With Gemma's
+ *         sandwich norms each sublayer output is normalised again before its residual add (the
+ *         adds then run after the norms), and relevance passes those norms unchanged.
  */
 #pragma once
+
+#include <memory>
 
 #include "pulsatrix/multihead_attention_module.hpp"
 #include "pulsatrix/rms_norm_module.hpp"
@@ -33,6 +37,11 @@ public:
     [[nodiscard]] RMSNormModule& norm2() { return norm2_; }
     [[nodiscard]] MultiHeadAttentionModule& mha() { return mha_; }
     [[nodiscard]] SwiGLUModule& swiglu() { return swiglu_; }
+    /** @brief Gemma's sandwich norms (TransformerBlockOptions::post_norms); throw std::logic_error
+     *         when the block has none. */
+    [[nodiscard]] RMSNormModule& post_attn_norm();
+    [[nodiscard]] RMSNormModule& post_mlp_norm();
+    [[nodiscard]] bool has_post_norms() const noexcept { return post_attn_norm_ != nullptr; }
 
     /** @brief Fused-path forward; x must stay valid until the relevance pass. Returns y2. */
     const float* run_forward(const float* x, int64_t n, int64_t l);
@@ -55,6 +64,9 @@ private:
     MultiHeadAttentionModule mha_;
     RMSNormModule norm2_;
     SwiGLUModule swiglu_;
+    std::unique_ptr<RMSNormModule> post_attn_norm_, post_mlp_norm_;
+    const float* attn_out_ = nullptr;  // the sublayer outputs the residual sums add (after any post norm)
+    const float* ffn_out_ = nullptr;
     int64_t N_ = 0, L_ = 0;
     const float* x_ = nullptr;
     Shape last_shape_;

@@ -26,11 +26,7 @@ AttentionConfig resolve(AttentionConfig c) {  // multihead_attention_module.cpp:
     }
     if (c.use_rope && c.head_dim % 2 != 0)
         throw std::invalid_argument("MultiHeadAttentionModule: use_rope requires an even head_dim (d_model / num_heads)");
-    if (c.use_qk_norm) throw std::invalid_argument("MultiHeadAttentionModule: QK-Norm is not on the MI355X path");
-    if (c.sliding_window != 0)
-        throw std::invalid_argument("MultiHeadAttentionModule: sliding-window attention is not on the MI355X path");
-    if (c.use_rope && c.head_dim > 64 && c.head_dim % 64 != 0)
-        throw std::invalid_argument("MultiHeadAttentionModule: head_dim above 64 must be a multiple of 64");
+    if (c.sliding_window < 0) throw std::invalid_argument("MultiHeadAttentionModule: sliding_window must not be negative");
     return c;
 }
 
@@ -59,7 +55,35 @@ MultiHeadAttentionModule::MultiHeadAttentionModule(const AttentionConfig& config
       q_proj_(d_, H_ * D_, backend, config_.qkv_bias),
       k_proj_(d_, Hkv_ * D_, backend, config_.qkv_bias),
       v_proj_(d_, Hkv_ * D_, backend, config_.qkv_bias),
-      out_proj_(H_ * D_, d_, backend, config_.out_bias) {}
+      out_proj_(H_ * D_, d_, backend, config_.out_bias) {
+    if (config_.use_qk_norm) {  // multihead_attention_module.cpp:116-121
+        q_norm_ = std::make_unique<RMSNormModule>(D_, backend, DeviceType::Hip, config_.qk_norm_eps);
+        k_norm_ = std::make_unique<RMSNormModule>(D_, backend, DeviceType::Hip, config_.qk_norm_eps);
+        q_norm_->set_weight_offset(config_.qk_norm_weight_offset);
+        k_norm_->set_weight_offset(config_.qk_norm_weight_offset);
+    }
+}
+
+RMSNormModule& MultiHeadAttentionModule::q_norm() {
+    if (!q_norm_) throw std::logic_error("MultiHeadAttentionModule::q_norm: the module has no QK-Norm");
+    return *q_norm_;
+}
+
+RMSNormModule& MultiHeadAttentionModule::k_norm() {
+    if (!k_norm_) throw std::logic_error("MultiHeadAttentionModule::k_norm: the module has no QK-Norm");
+    return *k_norm_;
+}
+
+int64_t MultiHeadAttentionModule::window_for(int64_t l) const {
+    // A window no query of this length reaches back past masks nothing.
+    return (config_.causal && config_.sliding_window > 0 && config_.sliding_window < l) ? config_.sliding_window : 0;
+}
+
+bool MultiHeadAttentionModule::fused_attention(int64_t l) const {
+    const int64_t qd = H_ * D_, kvd = Hkv_ * D_, w3 = qd + 2 * kvd;
+    const int64_t ldq = (config_.use_rope || config_.use_qk_norm) ? qd + kvd : w3;
+    return window_for(l) == 0 && pxk_attention_supported(D_, l, ldq, ldq, w3);
+}
 
 float MultiHeadAttentionModule::score_scale() const {
     return config_.score_scale > 0.0f ? config_.score_scale : 1.0f / std::sqrt(static_cast<float>(D_));
@@ -83,7 +107,9 @@ void MultiHeadAttentionModule::pack_weights() {
 }
 
 void MultiHeadAttentionModule::ensure_tables(int64_t l) {
-    if (!config_.use_rope || l == table_len_) return;
+    // Position-major tables: the first l rows of a longer table are this length's table, so the
+    // tables only grow (no host work when the length shrinks, as it does along a decode).
+    if (!config_.use_rope || l <= table_len_) return;
     // RoPEModule::ensure_tables (rope_module.cpp:67-69, 83-101): tables in double, rounded to float.
     const int64_t half = D_ / 2;
     std::vector<double> inv(static_cast<size_t>(half));
@@ -126,9 +152,10 @@ const float* MultiHeadAttentionModule::run_forward(const float* x, int64_t n, in
     float* y = config_.qkv_bias ? qkv_y_.ensure(be_, M * w3) : z;
     const int64_t rw = qd + kvd;  // row length of the rotated q | k block
     float* rot = config_.use_rope ? qk_rot_.ensure(be_, M * rw) : nullptr;
-    // The ROPE_FWD epilogue needs whole heads inside the GEMM's 128-wide tiles; other head_dims
-    // rotate in a second launch.
-    const bool rope_in_gemm = config_.use_rope && (w3 <= 128 || 128 % D_ == 0);
+    // The ROPE_FWD epilogue needs whole heads inside the GEMM's 128-wide tiles and no QK-Norm in
+    // between; otherwise the norm and the rotation run as their own launches.
+    const bool qkn = config_.use_qk_norm;
+    const bool rope_in_gemm = config_.use_rope && !qkn && (w3 <= 128 || 128 % D_ == 0);
     {
         pxk_gemm_desc d = gemm_desc(l, w3, d_);
         d.batch = n;
@@ -151,18 +178,31 @@ const float* MultiHeadAttentionModule::run_forward(const float* x, int64_t n, in
         }
         be_->run_gemm(d);
     }
+    const float* pre = y;  // q | k before the rotation (the RoPE rule's x), row stride ld_pre
+    int64_t ld_pre = w3;
+    if (qkn) {  // step 3: QK-Norm over each head's queries and keys
+        float* nq = qk_norm_out_.ensure(be_, M * rw);
+        MI355XBackend::check(pxk_rms_norm_heads(y, w3, nq, rw, q_norm_->effective_gamma(), M, H_, D_,
+                                                q_norm_->eps(), st),
+                             "MultiHeadAttentionModule::forward (QK-Norm)");
+        MI355XBackend::check(pxk_rms_norm_heads(y + qd, w3, nq + qd, rw, k_norm_->effective_gamma(), M, Hkv_, D_,
+                                                k_norm_->eps(), st),
+                             "MultiHeadAttentionModule::forward (QK-Norm)");
+        pre = nq;
+        ld_pre = rw;
+    }
     if (config_.use_rope && !rope_in_gemm)
-        MI355XBackend::check(pxk_rope_qk(y, y + qd, w3, rot, rot + qd, rw, cos_.data(), sin_.data(), M, l, H_, Hkv_, D_,
-                                         config_.rope_layout == RoPELayout::RotateHalf, st),
+        MI355XBackend::check(pxk_rope_qk(pre, pre + qd, ld_pre, rot, rot + qd, rw, cos_.data(), sin_.data(), M, l, H_,
+                                         Hkv_, D_, config_.rope_layout == RoPELayout::RotateHalf, st),
                              "MultiHeadAttentionModule::forward (RoPE)");
-    const float* q = config_.use_rope ? rot : y;
-    const float* k = config_.use_rope ? rot + qd : y + qd;
+    const float* q = config_.use_rope ? rot : pre;
+    const float* k = config_.use_rope ? rot + qd : pre + qd;
     const float* v = y + qd + kvd;
-    const int64_t ldq = config_.use_rope ? rw : w3, ldk = ldq;
+    const int64_t ldq = config_.use_rope ? rw : ld_pre, ldk = ldq;
     float* raw = raw_.ensure(be_, n * H_ * LL);
     float* p = p_.ensure(be_, n * H_ * LL);
     float* ctx = ctx_.ensure(be_, M * qd);
-    if (pxk_attention_supported(D_, l, ldq, ldk, w3)) {
+    if (fused_attention(l)) {
         // 3-5 fused: scores, mask, softmax and P V in one launch, P and raw kept for relevance.
         MI355XBackend::check(pxk_attention_forward(q, ldq, k, ldk, v, w3, raw, p, ctx, qd, n, l, H_, Hkv_, D_,
                                                    score_scale(), causal, st),
@@ -216,7 +256,7 @@ void MultiHeadAttentionModule::run_attention_unfused(const float* q, int64_t ldq
         be_->run_gemm(d);
     }
     // 4. P = softmax(scale * raw) over the visible keys.
-    MI355XBackend::check(pxk_attention_softmax(raw, p, n * H_, l, score_scale(), causal, st),
+    MI355XBackend::check(pxk_attention_softmax(raw, p, n * H_, l, score_scale(), causal, window_for(l), st),
                          "MultiHeadAttentionModule::forward (softmax)");
     // 5. context = P V, written head-packed (N*L, H*D): the merge permute is the store layout.
     {
@@ -245,10 +285,13 @@ const float* MultiHeadAttentionModule::run_relevance(const float* relevance_out,
     const float eps = config.epsilon;
     const float* z = qkv_z_.data();
     const float* y = config_.qkv_bias ? qkv_y_.data() : z;
-    const float* q = config_.use_rope ? qk_rot_.data() : y;
-    const float* k = config_.use_rope ? qk_rot_.data() + qd : y + qd;
+    // q | k before the rotation (after QK-Norm when there is one): the RoPE rule's x
+    const float* pre = config_.use_qk_norm ? qk_norm_out_.data() : y;
+    const int64_t ld_pre = config_.use_qk_norm ? qd + kvd : w3;
+    const float* q = config_.use_rope ? qk_rot_.data() : pre;
+    const float* k = config_.use_rope ? qk_rot_.data() + qd : pre + qd;
     const float* v = y + qd + kvd;
-    const int64_t ldq = config_.use_rope ? qd + kvd : w3, ldk = ldq;  // q | k rotated rows, or the packed rows
+    const int64_t ldq = config_.use_rope ? qd + kvd : ld_pre, ldk = ldq;  // q | k rotated rows, or the packed rows
     const float* bq = detail::rule_bias(bqkv_.data(), config_.qkv_bias, bid);
     void* st = be_->stream();
 
@@ -285,7 +328,7 @@ const float* MultiHeadAttentionModule::run_relevance(const float* relevance_out,
         key_rel_ = Tensor::uninitialized(Shape({M, kvd}), be_);
         value_rel_ = Tensor::uninitialized(Shape({M, kvd}), be_);
     }
-    if (pxk_attention_supported(D_, l, ldq, ldk, w3)) {
+    if (fused_attention(l)) {
         // 2-4 fused: r_attn, the softmax rule with the Q K^T denominator (s), and the query share
         // with the RoPE rule and q_proj's denominator, one launch per layer.
         pxk_attn_rel_desc rd{};
@@ -310,8 +353,8 @@ const float* MultiHeadAttentionModule::run_relevance(const float* relevance_out,
         rd.s = ra;
         rd.q = q;
         rd.ld_q = ldq;
-        rd.q_pre = y;
-        rd.ld_q_pre = w3;
+        rd.q_pre = pre;
+        rd.ld_q_pre = ld_pre;
         rd.z = z;
         rd.ld_z = w3;
         rd.bias = bq;
@@ -346,8 +389,8 @@ const float* MultiHeadAttentionModule::run_relevance(const float* relevance_out,
         kd.ld_spv = qd;
         kd.k = k;
         kd.ld_k = ldk;
-        kd.k_pre = y + qd;
-        kd.ld_k_pre = w3;
+        kd.k_pre = pre + qd;
+        kd.ld_k_pre = ld_pre;
         kd.v = v;
         kd.ld_v = w3;
         kd.z_k = z + qd;
@@ -398,10 +441,12 @@ void MultiHeadAttentionModule::relevance_scores_unfused(const float* spv, float 
     const bool causal = config_.causal;
     const float* z = qkv_z_.data();
     const float* y = config_.qkv_bias ? qkv_y_.data() : z;
-    const float* q = config_.use_rope ? qk_rot_.data() : y;
-    const float* k = config_.use_rope ? qk_rot_.data() + qd : y + qd;
+    const float* pre = config_.use_qk_norm ? qk_norm_out_.data() : y;
+    const int64_t ld_pre = config_.use_qk_norm ? qd + kvd : w3;
+    const float* q = config_.use_rope ? qk_rot_.data() : pre;
+    const float* k = config_.use_rope ? qk_rot_.data() + qd : pre + qd;
     const float* v = y + qd + kvd;
-    const int64_t ldq = config_.use_rope ? qd + kvd : w3, ldk = ldq;  // q | k rotated rows, or the packed rows
+    const int64_t ldq = config_.use_rope ? qd + kvd : ld_pre, ldk = ldq;  // q | k rotated rows, or the packed rows
     const float* bq = detail::rule_bias(bqkv_.data(), config_.qkv_bias, bid);
     void* st = be_->stream();
     float* ra = ra_.data();
@@ -422,8 +467,27 @@ void MultiHeadAttentionModule::relevance_scores_unfused(const float* spv, float 
         be_->run_gemm(d);
     }
     // 3. softmax rule on the scaled scores, mask, then the Q K^T factor s_qk (in place).
-    MI355XBackend::check(pxk_attention_lrp_scores(ra, p, raw_.data(), ra, n * H_, l, score_scale(), eps, causal, st),
+    MI355XBackend::check(pxk_attention_lrp_scores(ra, p, raw_.data(), ra, n * H_, l, score_scale(), eps, causal,
+                                                  window_for(l), st),
                          "MultiHeadAttentionModule::propagate_relevance (scores)");
+    if (config_.use_rope && D_ > 128) {
+        // 4 with head_dims the ROPE_REL epilogue cannot hold in one tile: acc = s K per query head,
+        // then the RoPE rule and q_proj's denominator on the head-packed rows.
+        float* acc = rctx_.ensure(be_, n * l * qd);
+        pxk_gemm_desc d = gemm_desc(l, D_, l);
+        d.batch = n * H_;
+        d.inner = H_;
+        d.causal = causal ? PXK_CAUSAL_K_LE_M : PXK_CAUSAL_NONE;
+        d.a = mat(ra, l, H_ * LL, LL);
+        d.b = mat(k, ldk, l * ldk, D_, grp);
+        d.c = mat(acc, qd, l * qd, D_);
+        be_->run_gemm(d);
+        MI355XBackend::check(pxk_lrp_rope_rows(acc, qd, pre, ld_pre, q, ldq, z, w3, bq, cos_.data(), sin_.data(), g, w3,
+                                               n * l, l, H_, D_, eps, config_.rope_layout == RoPELayout::RotateHalf,
+                                               rel_only, st),
+                             "MultiHeadAttentionModule::propagate_relevance (RoPE rule)");
+        return;
+    }
     // 4. query share: r_q = Q * (s_qk K), then the RoPE rule and q_proj's denominator.
     {
         pxk_gemm_desc d = gemm_desc(l, D_, l);
@@ -442,7 +506,7 @@ void MultiHeadAttentionModule::relevance_scores_unfused(const float* spv, float 
         if (bq) d.e_bias = mat(bq, 0, 0, D_);
         if (config_.use_rope) {
             d.epilogue = PXK_EPI_ROPE_REL;
-            d.x = mat(y, w3, l * w3, D_);
+            d.x = mat(pre, ld_pre, l * ld_pre, D_);
             d.y = mat(q, ldq, l * ldq, D_);
             d.cos_t = cos_.data();
             d.sin_t = sin_.data();

@@ -19,10 +19,8 @@ SwiGLUModule::SwiGLUModule(int64_t d_model, int64_t d_ff, DeviceBackend* backend
       be_(detail::require_mi355x(backend, "SwiGLUModule")),
       gate_proj_(d_model, d_ff, backend, use_bias),
       up_proj_(d_model, d_ff, backend, use_bias),
-      down_proj_(d_ff, d_model, backend, use_bias) {
-    if (activation != GatedActivation::Silu)
-        throw std::invalid_argument("SwiGLUModule: the MI355X path implements the SiLU gate");
-}
+      down_proj_(d_ff, d_model, backend, use_bias),
+      act_(activation == GatedActivation::GeluTanh ? 1 : 0) {}
 
 void SwiGLUModule::pack_weights() {
     const uint64_t v = gate_proj_.version() + up_proj_.version();
@@ -67,6 +65,7 @@ const float* SwiGLUModule::run_forward(const float* x, int64_t rows, const float
         d.c2 = mat(h, F_);
         d.c3 = mat(gp, F_);
         d.epilogue = PXK_EPI_SWIGLU_FWD;
+        d.gate_act = act_;
         be_->run_gemm(d);
     } else {  // gate and up projections in one GEMM, then the gate
         pxk_gemm_desc d = gemm_desc(rows, f2, d_);
@@ -80,7 +79,7 @@ const float* SwiGLUModule::run_forward(const float* x, int64_t rows, const float
             d.e_bias = mat(bgu_.data(), 0);
         }
         be_->run_gemm(d);
-        MI355XBackend::check(pxk_swiglu_forward(gy, f2, gp, h, rows, F_, be_->stream()), "SwiGLUModule::forward");
+        MI355XBackend::check(pxk_swiglu_forward(gy, f2, gp, h, rows, F_, act_, be_->stream()), "SwiGLUModule::forward");
     }
     float* dz = down_z_.ensure(be_, rows * d_);
     float* dy = use_bias_ ? down_y_.ensure(be_, rows * d_) : dz;
@@ -205,8 +204,24 @@ TransformerBlock::TransformerBlock(const AttentionConfig& attention, int64_t d_f
       mha_(attention, backend),
       norm2_(attention.d_model > 0 ? attention.d_model : 1, backend, DeviceType::Hip, options.norm_eps),
       swiglu_(attention.d_model, d_ff, backend, options.mlp_bias, options.mlp_activation) {
-    if (options.post_norms || options.norm_weight_offset != 0.0f)
-        throw std::invalid_argument("TransformerBlock: Gemma sandwich norms are not on the MI355X path");
+    norm1_.set_weight_offset(options.norm_weight_offset);
+    norm2_.set_weight_offset(options.norm_weight_offset);
+    if (options.post_norms) {  // transformer_block.cpp:60-80
+        post_attn_norm_ = std::make_unique<RMSNormModule>(d_, backend, DeviceType::Hip, options.norm_eps);
+        post_mlp_norm_ = std::make_unique<RMSNormModule>(d_, backend, DeviceType::Hip, options.norm_eps);
+        post_attn_norm_->set_weight_offset(options.norm_weight_offset);
+        post_mlp_norm_->set_weight_offset(options.norm_weight_offset);
+    }
+}
+
+RMSNormModule& TransformerBlock::post_attn_norm() {
+    if (!post_attn_norm_) throw std::logic_error("TransformerBlock::post_attn_norm: the block has no sandwich norms");
+    return *post_attn_norm_;
+}
+
+RMSNormModule& TransformerBlock::post_mlp_norm() {
+    if (!post_mlp_norm_) throw std::logic_error("TransformerBlock::post_mlp_norm: the block has no sandwich norms");
+    return *post_mlp_norm_;
 }
 
 TransformerBlock::TransformerBlock(int64_t d_model, int64_t num_heads, int64_t d_ff, DeviceBackend* backend,
@@ -225,14 +240,25 @@ const float* TransformerBlock::run_forward(const float* x, int64_t n, int64_t l)
     const int64_t M = n * l;
     float* y1 = y1_.ensure(be_, M * d_);
     float* y2 = y2_.ensure(be_, M * d_);
-    mha_.run_forward(norm1_.run_forward(x, M), n, l, x, y1);        // y1 = x + attn(norm1(x))
-    swiglu_.run_forward(norm2_.run_forward(y1, M), M, y1, y2);       // y2 = y1 + mlp(norm2(y1))
+    if (!post_attn_norm_) {
+        mha_.run_forward(norm1_.run_forward(x, M), n, l, x, y1);     // y1 = x + attn(norm1(x))
+        swiglu_.run_forward(norm2_.run_forward(y1, M), M, y1, y2);    // y2 = y1 + mlp(norm2(y1))
+        attn_out_ = mha_.output();
+        ffn_out_ = swiglu_.output();
+        return y2;
+    }
+    // Sandwich norms: y1 = x + post_attn_norm(attn(norm1(x))), y2 = y1 + post_mlp_norm(mlp(norm2(y1))).
+    void* st = be_->stream();
+    attn_out_ = post_attn_norm_->run_forward(mha_.run_forward(norm1_.run_forward(x, M), n, l), M);
+    MI355XBackend::check(pxk_add(x, attn_out_, y1, M * d_, st), "TransformerBlock::forward");
+    ffn_out_ = post_mlp_norm_->run_forward(swiglu_.run_forward(norm2_.run_forward(y1, M), M), M);
+    MI355XBackend::check(pxk_add(y1, ffn_out_, y2, M * d_, st), "TransformerBlock::forward");
     return y2;
 }
 
 detail::ResidualSplit TransformerBlock::output_split() {
     const int64_t n = N_ * L_ * d_;
-    return {y1_.data(), swiglu_.output(), y2_.data(), r_y1d_.ensure(be_, n), r_ffn_.ensure(be_, n)};
+    return {y1_.data(), ffn_out_, y2_.data(), r_y1d_.ensure(be_, n), r_ffn_.ensure(be_, n)};
 }
 
 const float* TransformerBlock::run_relevance_split(const LRPRuleConfig& config, const detail::ResidualSplit& below) {
@@ -242,7 +268,8 @@ const float* TransformerBlock::run_relevance_split(const LRPRuleConfig& config, 
     // last GEMM writes the split one level up (y1 = x + attn) the same way.
     float* rxd = r_xd_.ensure(be_, n);
     float* rattn = r_attn_.ensure(be_, n);
-    swiglu_.run_relevance(r_ffn_.data(), config, r_y1d_.data(), {x_, mha_.output(), y1_.data(), rxd, rattn});
+    // The sandwich norms pass relevance unchanged (PostNormRelevance, transformer_block.cpp:92-95).
+    swiglu_.run_relevance(r_ffn_.data(), config, r_y1d_.data(), {x_, attn_out_, y1_.data(), rxd, rattn});
     return mha_.run_relevance(rattn, config, rxd, below);
 }
 
@@ -254,14 +281,14 @@ const float* TransformerBlock::run_relevance(const float* relevance_out, const L
     // r_y1 = r_y1_direct + r_from_norm2 fused into the MLP's last GEMM.
     float* ry1d = r_y1d_.ensure(be_, n);
     float* rffn = r_ffn_.ensure(be_, n);
-    MI355XBackend::check(pxk_lrp_residual_split(y1_.data(), swiglu_.output(), relevance_out, ry1d, rffn, n,
+    MI355XBackend::check(pxk_lrp_residual_split(y1_.data(), ffn_out_, relevance_out, ry1d, rffn, n,
                                                 config.epsilon, st),
                          "TransformerBlock::propagate_relevance");
     const float* ry1 = swiglu_.run_relevance(rffn, config, ry1d);
     // y1 = x + attn: the same one level up.
     float* rxd = r_xd_.ensure(be_, n);
     float* rattn = r_attn_.ensure(be_, n);
-    MI355XBackend::check(pxk_lrp_residual_split(x_, mha_.output(), ry1, rxd, rattn, n, config.epsilon, st),
+    MI355XBackend::check(pxk_lrp_residual_split(x_, attn_out_, ry1, rxd, rattn, n, config.epsilon, st),
                          "TransformerBlock::propagate_relevance");
     return mha_.run_relevance(rattn, config, rxd);
 }

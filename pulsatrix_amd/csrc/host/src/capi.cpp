@@ -58,10 +58,18 @@ std::vector<std::pair<int64_t, bool>> block_layout(const px_model_config& c) {
     lin(d, kv, c.qkv_bias);
     lin(d, kv, c.qkv_bias);
     lin(q, d, c.out_bias);
+    if (c.qk_norm) {
+        out.push_back({head_dim(c), true});
+        out.push_back({head_dim(c), true});
+    }
     out.push_back({d, true});
     lin(d, f, c.mlp_bias);
     lin(d, f, c.mlp_bias);
     lin(f, d, c.mlp_bias);
+    if (c.post_norms) {
+        out.push_back({d, true});
+        out.push_back({d, true});
+    }
     return out;
 }
 
@@ -82,8 +90,55 @@ int64_t total(const std::vector<std::pair<int64_t, bool>>& layout) {
     return n;
 }
 
+// The reference's HfModelConfig for a px_model_config (the fields ParseHfConfig fills).
+HfModelConfig hf_config(const px_model_config& c) {
+    if (c.hidden_act < 0 || c.hidden_act > 1) throw std::invalid_argument("model config: unknown hidden_act");
+    if (c.rope_scaling < 0 || c.rope_scaling > 2) throw std::invalid_argument("model config: unknown rope_scaling");
+    if (c.sliding_layers != 0 && c.num_layers > 64)
+        throw std::invalid_argument("model config: sliding_layers names at most 64 layers");
+    HfModelConfig hc;
+    hc.hidden_size = c.hidden_size;
+    hc.intermediate_size = c.intermediate_size;
+    hc.num_hidden_layers = c.num_layers;
+    hc.num_attention_heads = c.num_heads;
+    hc.num_key_value_heads = kv_heads(c);
+    hc.head_dim = head_dim(c);
+    hc.vocab_size = c.vocab_size;
+    hc.rms_norm_eps = c.rms_norm_eps;
+    hc.rope_theta = c.rope_theta;
+    hc.tie_word_embeddings = c.tie_word_embeddings != 0;
+    hc.qkv_bias = c.qkv_bias != 0;
+    hc.out_bias = c.out_bias != 0;
+    hc.mlp_bias = c.mlp_bias != 0;
+    hc.causal = c.causal != 0;
+    hc.hidden_act = c.hidden_act == 1 ? "gelu_pytorch_tanh" : "silu";
+    hc.qk_norm = c.qk_norm != 0;
+    hc.post_norms = c.post_norms != 0;
+    hc.norm_weight_offset = c.norm_weight_offset;
+    if (c.embed_scale != 0.0f) hc.embed_scale = c.embed_scale;
+    if (c.query_pre_attn_scalar > 0.0f) hc.query_pre_attn_scalar = c.query_pre_attn_scalar;
+    if (c.rope_local_base > 0.0f) hc.rope_local_base_freq = c.rope_local_base;
+    if (c.rope_scaling != 0) {
+        HfRopeScaling r;
+        r.type = c.rope_scaling == 1 ? "linear" : "llama3";
+        r.factor = c.rope_factor;
+        r.low_freq_factor = c.rope_low_freq_factor;
+        r.high_freq_factor = c.rope_high_freq_factor;
+        r.original_max_position_embeddings = c.rope_original_max_position;
+        hc.rope_scaling = r;
+    }
+    if (c.sliding_window > 0) {
+        hc.sliding_window = c.sliding_window;
+        if (c.sliding_layers != 0)
+            for (int64_t i = 0; i < c.num_layers; ++i)
+                hc.layer_types.push_back(((c.sliding_layers >> i) & 1u) ? "sliding_attention" : "full_attention");
+    }
+    return hc;
+}
+
 AttentionConfig attention_config(const px_model_config& c) {
-    AttentionConfig a;
+    if (c.use_rope && c.rope_rotate_half) return ToAttentionConfig(hf_config(c), 0);
+    AttentionConfig a;  // the layouts ToAttentionConfig does not produce (no RoPE, adjacent pairs)
     a.d_model = c.hidden_size;
     a.num_heads = c.num_heads;
     a.num_kv_heads = kv_heads(c);
@@ -94,7 +149,22 @@ AttentionConfig attention_config(const px_model_config& c) {
     a.qkv_bias = c.qkv_bias != 0;
     a.out_bias = c.out_bias != 0;
     a.causal = c.causal != 0;
+    a.use_qk_norm = c.qk_norm != 0;
+    a.qk_norm_eps = c.rms_norm_eps;
+    a.qk_norm_weight_offset = c.norm_weight_offset;
+    if (c.query_pre_attn_scalar > 0.0f)
+        a.score_scale = static_cast<float>(1.0 / std::sqrt(static_cast<double>(c.query_pre_attn_scalar)));
     return a;
+}
+
+TransformerBlockOptions block_options(const px_model_config& c) {
+    TransformerBlockOptions opt;
+    opt.norm_eps = c.rms_norm_eps;
+    opt.mlp_bias = c.mlp_bias != 0;
+    opt.mlp_activation = c.hidden_act == 1 ? GatedActivation::GeluTanh : GatedActivation::Silu;
+    opt.post_norms = c.post_norms != 0;
+    opt.norm_weight_offset = c.norm_weight_offset;
+    return opt;
 }
 
 std::vector<float> take(const float*& p, int64_t n) {
@@ -114,10 +184,18 @@ void load_block(TransformerBlock& b, const float*& p) {
     load_linear(b.mha().k_proj(), p);
     load_linear(b.mha().v_proj(), p);
     load_linear(b.mha().out_proj(), p);
+    if (b.mha().config().use_qk_norm) {
+        b.mha().q_norm().set_gamma(take(p, b.mha().q_norm().num_features()));
+        b.mha().k_norm().set_gamma(take(p, b.mha().k_norm().num_features()));
+    }
     b.norm2().set_gamma(take(p, b.norm2().num_features()));
     load_linear(b.swiglu().gate_proj(), p);
     load_linear(b.swiglu().up_proj(), p);
     load_linear(b.swiglu().down_proj(), p);
+    if (b.has_post_norms()) {
+        b.post_attn_norm().set_gamma(take(p, b.post_attn_norm().num_features()));
+        b.post_mlp_norm().set_gamma(take(p, b.post_mlp_norm().num_features()));
+    }
 }
 
 struct BlockHandle {
@@ -133,21 +211,7 @@ struct LmHandle {
 
 LmHandle* make_lm(const px_model_config& c, const float* params) {
     if (c.vocab_size <= 0 || c.num_layers <= 0) throw std::invalid_argument("model config: vocab_size and num_layers must be positive");
-    HfModelConfig hc;
-    hc.hidden_size = c.hidden_size;
-    hc.intermediate_size = c.intermediate_size;
-    hc.num_hidden_layers = c.num_layers;
-    hc.num_attention_heads = c.num_heads;
-    hc.num_key_value_heads = kv_heads(c);
-    hc.head_dim = head_dim(c);
-    hc.vocab_size = c.vocab_size;
-    hc.rms_norm_eps = c.rms_norm_eps;
-    hc.rope_theta = c.rope_theta;
-    hc.tie_word_embeddings = c.tie_word_embeddings != 0;
-    hc.qkv_bias = c.qkv_bias != 0;
-    hc.out_bias = c.out_bias != 0;
-    hc.mlp_bias = c.mlp_bias != 0;
-    hc.causal = c.causal != 0;
+    const HfModelConfig hc = hf_config(c);
     if (!c.use_rope || !c.rope_rotate_half)
         throw std::invalid_argument("model config: the causal LM uses rotate-half RoPE (ToAttentionConfig)");
     auto h = std::make_unique<LmHandle>();
@@ -288,9 +352,10 @@ int pxa_synthetic_params(const px_model_config* cfg, int block, uint64_t seed, d
         const auto layout = block ? block_layout(*cfg) : lm_layout(*cfg);
         pxa_fill_normal(dst, static_cast<size_t>(total(layout)), seed, stddev);
         int64_t off = 0;
+        const float g = 1.0f - cfg->norm_weight_offset;  // every RMSNorm's effective scale 1
         for (const auto& [size, gamma] : layout) {
             if (gamma)
-                for (int64_t i = 0; i < size; ++i) dst[off + i] = 1.0f;
+                for (int64_t i = 0; i < size; ++i) dst[off + i] = g;
             off += size;
         }
     });
@@ -300,10 +365,8 @@ void* pxa_block_create(const px_model_config* cfg, const float* params) {
     BlockHandle* out = nullptr;
     guarded([&] {
         auto h = std::make_unique<BlockHandle>();
-        TransformerBlockOptions opt;
-        opt.norm_eps = cfg->rms_norm_eps;
-        opt.mlp_bias = cfg->mlp_bias != 0;
-        h->block = std::make_unique<TransformerBlock>(attention_config(*cfg), cfg->intermediate_size, backend(), opt);
+        h->block = std::make_unique<TransformerBlock>(attention_config(*cfg), cfg->intermediate_size, backend(),
+                                                      block_options(*cfg));
         const float* p = params;
         load_block(*h->block, p);
         h->d = cfg->hidden_size;
@@ -392,6 +455,23 @@ void* pxa_lm_load(const char* directory, px_model_config* cfg_out) {
         c.out_bias = hc.out_bias ? 1 : 0;
         c.mlp_bias = hc.mlp_bias ? 1 : 0;
         c.tie_word_embeddings = hc.tie_word_embeddings ? 1 : 0;
+        c.hidden_act = hc.hidden_act == "silu" ? 0 : 1;
+        c.qk_norm = hc.qk_norm ? 1 : 0;
+        c.post_norms = hc.post_norms ? 1 : 0;
+        c.norm_weight_offset = hc.norm_weight_offset;
+        c.embed_scale = hc.embed_scale;
+        c.query_pre_attn_scalar = hc.query_pre_attn_scalar.value_or(0.0f);
+        c.rope_local_base = hc.rope_local_base_freq.value_or(0.0f);
+        if (hc.rope_scaling) {
+            c.rope_scaling = hc.rope_scaling->type == "linear" ? 1 : 2;
+            c.rope_factor = hc.rope_scaling->factor;
+            c.rope_low_freq_factor = hc.rope_scaling->low_freq_factor;
+            c.rope_high_freq_factor = hc.rope_scaling->high_freq_factor;
+            c.rope_original_max_position = hc.rope_scaling->original_max_position_embeddings;
+        }
+        c.sliding_window = hc.sliding_window.value_or(0);
+        for (size_t i = 0; i < hc.layer_types.size() && i < 64; ++i)
+            if (hc.layer_types[i] == "sliding_attention") c.sliding_layers |= uint64_t{1} << i;
         if (cfg_out) *cfg_out = c;
         out = h.release();
     });

@@ -6,6 +6,44 @@
 
 namespace pulsatrix {
 
+bool HfModelConfig::is_sliding_layer(int64_t i) const {
+    if (!sliding_window) return false;
+    if (layer_types.empty()) return true;
+    return i >= 0 && static_cast<size_t>(i) < layer_types.size() &&
+           layer_types[static_cast<size_t>(i)] == "sliding_attention";
+}
+
+std::vector<double> RopeInverseFrequencies(const HfModelConfig& config) {
+    const int64_t half = config.head_dim / 2;
+    std::vector<double> inv(static_cast<size_t>(half));
+    for (int64_t i = 0; i < half; ++i)
+        inv[static_cast<size_t>(i)] = 1.0 / std::pow(static_cast<double>(config.rope_theta),
+                                                     2.0 * static_cast<double>(i) / static_cast<double>(config.head_dim));
+    if (!config.rope_scaling) return inv;
+    const HfRopeScaling& s = *config.rope_scaling;
+    if (s.type == "linear") {
+        for (double& f : inv) f /= s.factor;
+        return inv;
+    }
+    if (s.type != "llama3")
+        throw std::invalid_argument("RopeInverseFrequencies: rope_scaling \"" + s.type + "\" is not supported");
+    // Hugging Face's _compute_llama3_parameters: stretch low frequencies, keep high ones,
+    // interpolate in between (wavelen == high_wavelen counts as in between).
+    const double old_len = static_cast<double>(s.original_max_position_embeddings);
+    const double low_wavelen = old_len / s.low_freq_factor, high_wavelen = old_len / s.high_freq_factor;
+    constexpr double kPi = 3.14159265358979323846;
+    for (double& f : inv) {
+        const double wavelen = 2.0 * kPi / f;
+        if (wavelen > low_wavelen) {
+            f /= s.factor;
+        } else if (wavelen >= high_wavelen) {
+            const double smooth = (old_len / wavelen - s.low_freq_factor) / (s.high_freq_factor - s.low_freq_factor);
+            f = (1.0 - smooth) * f / s.factor + smooth * f;
+        }
+    }
+    return inv;
+}
+
 AttentionConfig ToAttentionConfig(const HfModelConfig& config) {
     AttentionConfig a;
     a.d_model = config.hidden_size;
@@ -15,11 +53,26 @@ AttentionConfig ToAttentionConfig(const HfModelConfig& config) {
     a.use_rope = true;
     a.rope_layout = RoPELayout::RotateHalf;
     a.rope_base = config.rope_theta;
+    if (config.rope_scaling) a.rope_inverse_frequencies = RopeInverseFrequencies(config);
     a.use_qk_norm = config.qk_norm;
     a.qk_norm_eps = config.rms_norm_eps;
     a.qkv_bias = config.qkv_bias;
     a.out_bias = config.out_bias;
     a.causal = config.causal;
+    if (config.query_pre_attn_scalar)
+        a.score_scale = static_cast<float>(1.0 / std::sqrt(static_cast<double>(*config.query_pre_attn_scalar)));
+    a.qk_norm_weight_offset = config.norm_weight_offset;
+    return a;
+}
+
+AttentionConfig ToAttentionConfig(const HfModelConfig& config, int64_t layer) {
+    AttentionConfig a = ToAttentionConfig(config);
+    if (!config.is_sliding_layer(layer)) return a;
+    a.sliding_window = *config.sliding_window;
+    if (config.rope_local_base_freq) {
+        a.rope_base = *config.rope_local_base_freq;
+        a.rope_inverse_frequencies.clear();
+    }
     return a;
 }
 
@@ -29,16 +82,19 @@ const HfModelConfig& checked(const HfModelConfig& c) {
     if (c.hidden_size <= 0 || c.num_hidden_layers <= 0 || c.vocab_size <= 0 || c.intermediate_size <= 0)
         throw std::invalid_argument("CausalLM: hidden_size, num_hidden_layers, vocab_size and intermediate_size "
                                     "must be positive");
-    if (c.hidden_act != "silu") throw std::invalid_argument("CausalLM: the MI355X path runs SiLU-gated MLPs");
-    if (c.embed_scale != 1.0f) throw std::invalid_argument("CausalLM: embedding scaling is not on the MI355X path");
+    if (c.hidden_act != "silu" && c.hidden_act != "gelu_pytorch_tanh" && c.hidden_act != "gelu_new")
+        throw std::invalid_argument("CausalLM: the config needs features pulsatrix can't run yet: activation \"" +
+                                    c.hidden_act + "\" in the MLP");
     return c;
 }
 
-TransformerBlockOptions block_options(const HfModelConfig& c) {
+TransformerBlockOptions block_options(const HfModelConfig& c) {  // causal_lm.cpp:36-41
     TransformerBlockOptions o;
     o.norm_eps = c.rms_norm_eps;
     o.mlp_bias = c.mlp_bias;
-    o.mlp_activation = GatedActivation::Silu;
+    o.mlp_activation = c.hidden_act == "silu" ? GatedActivation::Silu : GatedActivation::GeluTanh;
+    o.post_norms = c.post_norms;
+    o.norm_weight_offset = c.norm_weight_offset;
     return o;
 }
 
@@ -49,8 +105,11 @@ CausalLM::CausalLM(const HfModelConfig& config, DeviceBackend* backend)
       be_(detail::require_mi355x(backend, "CausalLM")),
       embed_(config.vocab_size, config.hidden_size, backend),
       norm_(config.hidden_size, backend, DeviceType::Hip, config.rms_norm_eps) {
+    norm_.set_weight_offset(config.norm_weight_offset);
+    // Each layer's own attention: Gemma 3 alternates sliding-window and full layers, each with its
+    // own RoPE base (causal_lm.cpp:42-47).
     for (int64_t i = 0; i < config.num_hidden_layers; ++i)
-        layers_.push_back(std::make_unique<TransformerBlock>(ToAttentionConfig(config), config.intermediate_size,
+        layers_.push_back(std::make_unique<TransformerBlock>(ToAttentionConfig(config, i), config.intermediate_size,
                                                              backend, block_options(config)));
     if (config.tie_word_embeddings)
         tied_head_ = std::make_unique<TiedLMHeadModule>(embed_, backend);
@@ -65,6 +124,12 @@ const float* CausalLM::run_forward(const float* ids, int64_t n, int64_t l) {
     L_ = l;
     const int64_t M = n * l;
     const float* x = embed_.run_forward_device(ids, n, l);
+    if (config_.embed_scale != 1.0f) {  // ScaleEmbeddings (causal_lm.cpp:56-61), in the gather's own buffer
+        float* xs = const_cast<float*>(x);
+        MI355XBackend::check(pxk_axpby(config_.embed_scale, xs, 0.0f, nullptr, xs, M * config_.hidden_size,
+                                       be_->stream()),
+                             "CausalLM::forward");
+    }
     for (auto& layer : layers_) x = layer->run_forward(x, n, l);
     const float* xn = norm_.run_forward(x, M);
     return tied_head_ ? tied_head_->run_forward(xn, M) : lm_head_->run_forward(xn, M);

@@ -307,27 +307,76 @@ HfModelConfig ParseHfConfig(std::string_view json) {
     } else if (rp != nullptr) {
         c.rope_theta = static_cast<float>(opt_number(*rp, "rope_theta").value_or(10000.0));
     }
-    // RoPE frequency scaling (rope_scaling or a rope_type other than "default") is not on this path.
-    if (const Json* rs = t.find("rope_scaling"); rs != nullptr && rs->t != Json::T::Null)
-        bad_config("rope_scaling is not on the MI355X path");
-    if (rp != nullptr) {
-        const Json* kind = rp->find("rope_type");
-        if (kind != nullptr && kind->t == Json::T::String && kind->str != "default")
-            bad_config("rope_type \"" + kind->str + "\" is not on the MI355X path");
+    if (const auto local = opt_number(t, "rope_local_base_freq")) {
+        c.rope_local_base_freq = static_cast<float>(*local);
+    } else if (const Json* rs = rp != nullptr ? rp->find("sliding_attention") : nullptr;
+               rs != nullptr && rs->t == Json::T::Object) {
+        if (const auto theta = opt_number(*rs, "rope_theta")) c.rope_local_base_freq = static_cast<float>(*theta);
+    }
+    // RoPE scaling (RopeScaling, hf_model.cpp:67-87): rope_scaling, or rope_parameters (the
+    // full-attention layers' entry when it is per layer type); "default" means none.
+    const Json* scaling = t.find("rope_scaling");
+    if (scaling == nullptr || scaling->t == Json::T::Null) scaling = rp;
+    if (scaling != nullptr && scaling->t == Json::T::Object) {
+        if (const Json* full = scaling->find("full_attention"); full != nullptr && full->t == Json::T::Object)
+            scaling = full;
+        HfRopeScaling r;
+        r.type = opt_string(*scaling, "rope_type").value_or(opt_string(*scaling, "type").value_or("default"));
+        if (r.type != "default") {
+            r.factor = static_cast<float>(opt_number(*scaling, "factor").value_or(1.0));
+            r.low_freq_factor = static_cast<float>(opt_number(*scaling, "low_freq_factor").value_or(1.0));
+            r.high_freq_factor = static_cast<float>(opt_number(*scaling, "high_freq_factor").value_or(1.0));
+            r.original_max_position_embeddings = opt_integer(*scaling, "original_max_position_embeddings").value_or(0);
+            if (r.type != "linear" && r.type != "llama3")
+                bad_config("rope_scaling \"" + r.type + "\" is not on the MI355X path");
+            c.rope_scaling = r;
+        }
+    } else if (scaling != nullptr && scaling->t != Json::T::Null) {
+        bad_config("rope_scaling must be an object");
     }
     c.tie_word_embeddings = opt_bool(t, "tie_word_embeddings").value_or(opt_bool(root, "tie_word_embeddings").value_or(true));
     const std::string& type = c.model_type;
     const bool qwen2 = type == "qwen2" || type == "qwen2_moe";
+    const bool gemma3 = type == "gemma3" || type == "gemma3_text";
     const std::optional<bool> attention_bias = opt_bool(t, "attention_bias");
     c.qkv_bias = attention_bias.value_or(qwen2);
     c.out_bias = qwen2 ? false : attention_bias.value_or(false);
     c.mlp_bias = opt_bool(t, "mlp_bias").value_or(false);
-    c.qk_norm = type == "qwen3" || type == "qwen3_moe" || type == "gemma3" || type == "gemma3_text" || type == "olmo2";
+    c.qk_norm = type == "qwen3" || type == "qwen3_moe" || gemma3 || type == "olmo2";
     c.hidden_act = opt_string(t, "hidden_act").value_or(opt_string(t, "hidden_activation").value_or("silu"));
-    if (c.qk_norm) bad_config("QK-norm models (" + type + ") are not on the MI355X path");
-    if (c.hidden_act != "silu") bad_config("hidden_act \"" + c.hidden_act + "\" is not on the MI355X path");
-    if (opt_bool(t, "use_sliding_window").value_or(true) && opt_integer(t, "sliding_window").has_value())
-        bad_config("sliding-window attention is not on the MI355X path");
+    c.max_position_embeddings = opt_integer(t, "max_position_embeddings").value_or(0);
+    if (c.hidden_act != "silu" && c.hidden_act != "gelu_pytorch_tanh" && c.hidden_act != "gelu_new")
+        bad_config("hidden_act \"" + c.hidden_act + "\" is not on the MI355X path");
+    if (opt_bool(t, "use_sliding_window").value_or(true)) c.sliding_window = opt_integer(t, "sliding_window");
+    if (const auto qs = opt_number(t, "query_pre_attn_scalar")) c.query_pre_attn_scalar = static_cast<float>(*qs);
+    if (const Json* lt = t.find("layer_types"); lt != nullptr && lt->t != Json::T::Null) {
+        if (lt->t != Json::T::Array) bad_config("layer_types must be a list");
+        for (const Json& v : lt->arr) {
+            if (v.t != Json::T::String) bad_config("layer_types must hold strings");
+            if (v.str != "full_attention" && v.str != "sliding_attention")
+                bad_config("layer type \"" + v.str + "\" is not on the MI355X path");
+            c.layer_types.push_back(v.str);
+        }
+        if (static_cast<int64_t>(c.layer_types.size()) != c.num_hidden_layers)
+            bad_config("layer_types must name one type per layer");
+    }
+    // A window no sequence can exceed changes nothing (hf_model.cpp:206-213).
+    if (c.sliding_window && c.max_position_embeddings > 0 && *c.sliding_window >= c.max_position_embeddings)
+        c.sliding_window.reset();
+    if (c.sliding_window && c.layer_types.empty() && type == "qwen2")
+        bad_config("Qwen2's sliding window without layer_types (max_window_layers) is not on the MI355X path");
+    if (gemma3) {  // (1 + w) RMSNorms, embeddings scaled by sqrt(hidden_size), sandwich norms (hf_model.cpp:221-228)
+        c.norm_weight_offset = 1.0f;
+        c.embed_scale = static_cast<float>(std::sqrt(static_cast<double>(c.hidden_size)));
+        c.post_norms = true;
+    } else if (type.rfind("gemma", 0) == 0) {
+        bad_config("Gemma 1 and 2 (" + type + ") are not on the MI355X path");
+    }
+    for (const char* softcap : {"attn_logit_softcapping", "final_logit_softcapping"}) {
+        const Json* v = t.find(softcap);
+        if (v != nullptr && v->t != Json::T::Null)
+            bad_config(std::string("logit softcapping (") + softcap + ") is not on the MI355X path");
+    }
     return c;
 }
 
@@ -488,8 +537,18 @@ std::unique_ptr<CausalLM> LoadCausalLM(const std::string& directory, DeviceBacke
         const std::string hf = "model.layers." + std::to_string(i) + ".";
         TransformerBlock& blk = model->layer(i);
         targets.push_back({hf + "input_layernorm.weight", &blk.norm1().gamma(), false});
-        targets.push_back({hf + "post_attention_layernorm.weight", &blk.norm2().gamma(), false});
+        if (config.post_norms) {  // Gemma 3: the sandwich norms and the MLP's pre-norm
+            targets.push_back({hf + "post_attention_layernorm.weight", &blk.post_attn_norm().gamma(), false});
+            targets.push_back({hf + "pre_feedforward_layernorm.weight", &blk.norm2().gamma(), false});
+            targets.push_back({hf + "post_feedforward_layernorm.weight", &blk.post_mlp_norm().gamma(), false});
+        } else {
+            targets.push_back({hf + "post_attention_layernorm.weight", &blk.norm2().gamma(), false});
+        }
         MultiHeadAttentionModule& mha = blk.mha();
+        if (config.qk_norm) {
+            targets.push_back({hf + "self_attn.q_norm.weight", &mha.q_norm().gamma(), false});
+            targets.push_back({hf + "self_attn.k_norm.weight", &mha.k_norm().gamma(), false});
+        }
         LinearModule* proj[] = {&mha.q_proj(), &mha.k_proj(), &mha.v_proj()};
         const char* names[] = {"q_proj", "k_proj", "v_proj"};
         for (int p = 0; p < 3; ++p) {

@@ -132,13 +132,28 @@ RMSNormModule::RMSNormModule(int64_t num_features, DeviceBackend* backend, Devic
     if (num_features <= 0) throw std::invalid_argument("RMSNormModule: num_features must be positive");
 }
 
-void RMSNormModule::set_gamma(const std::vector<float>& values) { gamma_ = Tensor(gamma_.shape(), be_, values); }
+void RMSNormModule::set_gamma(const std::vector<float>& values) {
+    gamma_ = Tensor(gamma_.shape(), be_, values);
+    ++version_;
+}
+
+const float* RMSNormModule::effective_gamma() {
+    if (offset_ == 0.0f) return gamma_.data();
+    if (eff_version_ != version_ || eff_.size() != d_) {
+        // EffectiveGamma (rms_norm_module.cpp:40-49): fill(offset), then add gamma, in float.
+        float* e = eff_.ensure(be_, d_);
+        MI355XBackend::check(pxk_fill(e, offset_, d_, be_->stream()), "RMSNormModule::forward");
+        MI355XBackend::check(pxk_add(e, gamma_.data(), e, d_, be_->stream()), "RMSNormModule::forward");
+        eff_version_ = version_;
+    }
+    return eff_.data();
+}
 
 const float* RMSNormModule::run_forward(const float* x, int64_t rows) {
     rows_ = rows;
     float* out = out_.ensure(be_, rows * d_);
     float* rms = rms_.ensure(be_, rows);
-    MI355XBackend::check(pxk_rms_norm_forward(x, gamma_.data(), out, rms, rows, d_, eps_, be_->stream()),
+    MI355XBackend::check(pxk_rms_norm_forward(x, effective_gamma(), out, rms, rows, d_, eps_, be_->stream()),
                          "RMSNormModule::forward");
     return out;
 }

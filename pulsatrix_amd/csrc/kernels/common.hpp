@@ -34,6 +34,16 @@ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 // z + eps * sign(z), sign(0) = +1: the stabilizer of every epsilon rule (src/lrp_math.hpp:17).
 __device__ __forceinline__ float stab(float z, float eps) { return z + eps * ((z >= 0.0f) ? 1.0f : -1.0f); }
 
+// SwiGLU gate activations: SiLU x / (1 + e^-x) (cpu_backend.cpp:29) and GeLU with the tanh
+// approximation (pointwise_math.hpp:32-36), selected by act (0 SiLU, 1 GeLU tanh).
+__device__ __forceinline__ float gate_activation(float x, int act) {
+    if (act == 1) {
+        const float kBeta = 0.7978845608028654f, kKappa = 0.044715f;
+        return 0.5f * x * (1.0f + tanhf(kBeta * (x + kKappa * x * x * x)));
+    }
+    return x * (1.0f / (1.0f + expf(-x)));
+}
+
 // Sum / max over a full wave64 with cross-lane shuffles.
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

@@ -236,12 +236,12 @@ __global__ void __launch_bounds__(kThreads) add_row_kernel(const float* in, cons
 
 // SwiGLU gate over a [gate | up] row block (swiglu_module.cpp:80-88).
 __global__ void __launch_bounds__(kThreads) swiglu_kernel(const float* gu, int64_t ld, float* gate_post, float* hidden,
-                                                          int64_t rows, int64_t f) {
+                                                          int64_t rows, int64_t f, int act) {
     const int64_t n = rows * f, stride = static_cast<int64_t>(gridDim.x) * kThreads;
     for (int64_t i = blockIdx.x * kThreads + threadIdx.x; i < n; i += stride) {
         const int64_t r = i / f, c = i % f;
         const float x = gu[r * ld + c];
-        const float gp = x * sigmoidf_(x);
+        const float gp = gate_activation(x, act);
         gate_post[i] = gp;
         hidden[i] = gp * gu[r * ld + f + c];
     }
@@ -365,12 +365,13 @@ int pxk_lrp_stabilized_divide(const float* r, const float* denom, const float* g
                          n, stream);
 }
 
-int pxk_swiglu_forward(const float* gu, int64_t ld, float* gate_post, float* hidden, int64_t rows, int64_t f,
+int pxk_swiglu_forward(const float* gu, int64_t ld, float* gate_post, float* hidden, int64_t rows, int64_t f, int act,
                        void* stream) {
     if (rows < 0 || f < 0 || ld < 2 * f) return fail(PXK_ERR_INVALID, "pxk_swiglu_forward: bad sizes");
+    if (act < 0 || act > 1) return fail(PXK_ERR_INVALID, "pxk_swiglu_forward: unknown gate activation %d", act);
     if (rows * f == 0) return PXK_OK;
     hipLaunchKernelGGL(swiglu_kernel, dim3(grid_for(rows * f, kThreads)), dim3(kThreads), 0, S(stream), gu, ld,
-                       gate_post, hidden, rows, f);
+                       gate_post, hidden, rows, f, act);
     return launched("pxk_swiglu_forward");
 }
 

@@ -54,7 +54,7 @@ struct Args {
     const float* cos_t;
     const float* sin_t;
     int64_t head_dim, rope_cols;
-    int rope_half;
+    int rope_half, gate_act;
     int vec_a, vec_b, vec_e;  // 128-bit global access allowed: A (and Z), B, epilogue operands
     int tiles_m, tiles_n, bm;
     int remap;  // XCD-grouped block order
@@ -204,7 +204,7 @@ __device__ void epilogue_rows(const float* Cs, int ldc, int64_t m0, int64_t n0, 
             f4 gp, hid;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                gp[r] = acc[r] * (1.0f / (1.0f + expf(-acc[r])));  // x * sigmoid(x), cpu_backend.cpp:29
+                gp[r] = gate_activation(acc[r], g.gate_act);
                 hid[r] = gp[r] * up[r];
             }
             st4(C3 + m * g.c3.ld + j, gp, vec, cnt);
@@ -1163,6 +1163,7 @@ extern "C" int pxk_gemm(const pxk_gemm_desc* d, void* stream) {
     g.head_dim = d->head_dim;
     g.rope_half = d->rope_half;
     g.rope_cols = d->rope_cols;
+    g.gate_act = d->gate_act;
     g.ws = d->workspace;
     // 128-bit loads when every base, stride and the contiguous extent allow them; the causal
     // K ranges start at multiples of the tile height, so they keep the alignment.

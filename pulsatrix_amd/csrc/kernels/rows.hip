@@ -153,46 +153,126 @@ __global__ void __launch_bounds__(kThreads) reduce_pass2(const float* partials, 
 }
 
 // ---- attention -----------------------------------------------------------------------------------
+// Keys [lo, vis) a query row i sees: all of them, the causal prefix, or its last `window` keys
+// (attention_masked, row_math.hpp:117-126: j masked when j > i or j + window <= i).
+__device__ __forceinline__ void visible_keys(int64_t i, int64_t L, int causal, int64_t window, int64_t& lo,
+                                             int64_t& vis) {
+    vis = causal ? i + 1 : L;
+    lo = (causal && window > 0 && i + 1 > window) ? i + 1 - window : 0;
+}
+
 // P = softmax(scale * raw) over visible keys; masked entries of P written 0.
 __global__ void __launch_bounds__(kThreads) attention_softmax_kernel(const float* raw, float* p, int64_t rows,
-                                                                     int64_t L, float scale, int causal) {
+                                                                     int64_t L, float scale, int causal,
+                                                                     int64_t window) {
     const int64_t r = row_id();
     if (r >= rows) return;
     const int lane = lane_id();
-    const int64_t i = r % L;
-    const int64_t vis = causal ? i + 1 : L;
+    int64_t lo, vis;
+    visible_keys(r % L, L, causal, window, lo, vis);
     const float* x = raw + r * L;
     float* y = p + r * L;
     float mx = -INFINITY;
-    for (int64_t j = lane; j < vis; j += kWave) mx = fmaxf(mx, scale * x[j]);
+    for (int64_t j = lo + lane; j < vis; j += kWave) mx = fmaxf(mx, scale * x[j]);
     mx = wave_max(mx);
     float s = 0.0f;
-    for (int64_t j = lane; j < vis; j += kWave) s += expf(scale * x[j] - mx);
+    for (int64_t j = lo + lane; j < vis; j += kWave) s += expf(scale * x[j] - mx);
     s = wave_sum(s);
-    for (int64_t j = lane; j < L; j += kWave) y[j] = j < vis ? expf(scale * x[j] - mx) / s : 0.0f;
+    for (int64_t j = lane; j < L; j += kWave) y[j] = (j >= lo && j < vis) ? expf(scale * x[j] - mx) / s : 0.0f;
 }
 
 // s = [x * (r - P * sum r)] / (2 raw + eps sign raw), x = scale * raw; 0 where masked.
 __global__ void __launch_bounds__(kThreads) attention_lrp_scores_kernel(const float* r_attn, const float* p,
                                                                         const float* raw, float* s_out, int64_t rows,
-                                                                        int64_t L, float scale, float eps, int causal) {
+                                                                        int64_t L, float scale, float eps, int causal,
+                                                                        int64_t window) {
     const int64_t r = row_id();
     if (r >= rows) return;
     const int lane = lane_id();
-    const int64_t i = r % L;
-    const int64_t vis = causal ? i + 1 : L;
+    int64_t lo, vis;
+    visible_keys(r % L, L, causal, window, lo, vis);
     const int64_t off = r * L;
     float sum = 0.0f;
-    for (int64_t j = lane; j < vis; j += kWave) sum += r_attn[off + j];
+    for (int64_t j = lo + lane; j < vis; j += kWave) sum += r_attn[off + j];
     sum = wave_sum(sum);
     for (int64_t j = lane; j < L; j += kWave) {
         float v = 0.0f;
-        if (j < vis) {
+        if (j >= lo && j < vis) {
             const float o = raw[off + j];
             const float rs = (scale * o) * (r_attn[off + j] - p[off + j] * sum);
             v = rs / (2.0f * o + eps * ((o >= 0.0f) ? 1.0f : -1.0f));
         }
         s_out[off + j] = v;
+    }
+}
+
+// RMSNorm over each head's D values of head-packed rows (QK-Norm, multihead_attention_module.cpp
+// step 3): wave per (row, head); in row m, head h at in + m * ld_in + h * D.
+__global__ void __launch_bounds__(kThreads) rms_norm_heads_kernel(const float* in, int64_t ld_in, float* out,
+                                                                  int64_t ld_out, const float* gamma, int64_t rows,
+                                                                  int64_t heads, int64_t D, float eps) {
+    const int64_t r = row_id();
+    if (r >= rows * heads) return;
+    const int lane = lane_id();
+    const int64_t m = r / heads, h = r - m * heads;
+    const float* x = in + m * ld_in + h * D;
+    float ss = 0.0f;
+    for (int64_t i = lane; i < D; i += kWave) ss += x[i] * x[i];
+    ss = wave_sum(ss);
+    const float rms = sqrtf(ss / static_cast<float>(D) + eps);
+    float* o = out + m * ld_out + h * D;
+    for (int64_t i = lane; i < D; i += kWave) o[i] = gamma[i] * x[i] / rms;
+}
+
+// The RoPE epsilon rule (lrp_math.hpp:104-123) on token-major head-packed rows, then the
+// projection's stabilised divide: r = y * s_acc (the bilinear share, y the rotated values),
+// r_in per pair from x (before rotation), and g = r_in / stab(z + bias) -- or g = r_in under
+// rel_only. One thread per (row, head, pair).
+struct RopeRelArgs {
+    const float* acc;  // (rows, heads*D) sums s @ K for the queries
+    int64_t ld_acc;
+    const float* x;
+    int64_t ldx;
+    const float* y;
+    int64_t ldy;
+    const float* z;
+    int64_t ldz;
+    const float* bias;
+    const float* cos_t;
+    const float* sin_t;
+    float* g;
+    int64_t ldg;
+    int64_t rows, L, heads, D;
+    float eps;
+    int rotate_half, rel_only;
+};
+
+__global__ void __launch_bounds__(kThreads) rope_rel_rows_kernel(const RopeRelArgs a) {
+    const int64_t half = a.D / 2, n = a.rows * a.heads * half;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
+    for (int64_t t = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; t < n; t += stride) {
+        const int64_t i = t % half, h = (t / half) % a.heads, m = t / (half * a.heads);
+        const int64_t pos = m % a.L;
+        const int64_t lo = h * a.D + (a.rotate_half ? i : 2 * i), hi = h * a.D + (a.rotate_half ? i + half : 2 * i + 1);
+        const float y_lo = a.y[m * a.ldy + lo], y_hi = a.y[m * a.ldy + hi];
+        const float r_lo = y_lo * a.acc[m * a.ld_acc + lo], r_hi = y_hi * a.acc[m * a.ld_acc + hi];
+        const float c = a.cos_t[pos * half + i], sn = a.sin_t[pos * half + i];
+        const float d0 = stab(y_lo, a.eps), d1 = stab(y_hi, a.eps);
+        const float x_lo = a.x[m * a.ldx + lo], x_hi = a.x[m * a.ldx + hi];
+        float in_lo = 0.0f, in_hi = 0.0f;
+        in_lo += (x_lo * c / d0) * r_lo;
+        in_lo += (x_lo * sn / d1) * r_hi;
+        in_hi += (x_hi * -sn / d0) * r_lo;
+        in_hi += (x_hi * c / d1) * r_hi;
+        if (a.rel_only) {
+            a.g[m * a.ldg + lo] = in_lo;
+            a.g[m * a.ldg + hi] = in_hi;
+        } else {
+            const float zl = a.bias ? a.z[m * a.ldz + lo] + a.bias[lo] : a.z[m * a.ldz + lo];
+            const float zh = a.bias ? a.z[m * a.ldz + hi] + a.bias[hi] : a.z[m * a.ldz + hi];
+            a.g[m * a.ldg + lo] = in_lo / stab(zl, a.eps);
+            a.g[m * a.ldg + hi] = in_hi / stab(zh, a.eps);
+        }
     }
 }
 
@@ -454,21 +534,52 @@ int pxk_dot(const float* a, const float* b, int64_t n, float* out, float* partia
 }
 
 int pxk_attention_softmax(const float* raw, float* p, int64_t slices, int64_t l, float scale, int causal,
-                          void* stream) {
+                          int64_t window, void* stream) {
     int rc;
     if (!sizes_ok("pxk_attention_softmax", slices, l, &rc)) return rc;
+    if (window < 0) return fail(PXK_ERR_INVALID, "pxk_attention_softmax: negative window");
     hipLaunchKernelGGL(attention_softmax_kernel, dim3(rows_grid(slices * l)), dim3(kThreads), 0, S(stream), raw, p,
-                       slices * l, l, scale, causal);
+                       slices * l, l, scale, causal, window);
     return launched("pxk_attention_softmax");
 }
 
 int pxk_attention_lrp_scores(const float* r_attn, const float* p, const float* raw, float* s, int64_t slices,
-                             int64_t l, float scale, float eps, int causal, void* stream) {
+                             int64_t l, float scale, float eps, int causal, int64_t window, void* stream) {
     int rc;
     if (!sizes_ok("pxk_attention_lrp_scores", slices, l, &rc)) return rc;
+    if (window < 0) return fail(PXK_ERR_INVALID, "pxk_attention_lrp_scores: negative window");
     hipLaunchKernelGGL(attention_lrp_scores_kernel, dim3(rows_grid(slices * l)), dim3(kThreads), 0, S(stream), r_attn,
-                       p, raw, s, slices * l, l, scale, eps, causal);
+                       p, raw, s, slices * l, l, scale, eps, causal, window);
     return launched("pxk_attention_lrp_scores");
+}
+
+int pxk_rms_norm_heads(const float* in, int64_t ld_in, float* out, int64_t ld_out, const float* gamma, int64_t rows,
+                       int64_t heads, int64_t head_dim, float eps, void* stream) {
+    if (rows < 0 || heads <= 0 || head_dim <= 0 || ld_in < heads * head_dim || ld_out < heads * head_dim)
+        return fail(PXK_ERR_INVALID, "pxk_rms_norm_heads: bad sizes or row strides");
+    if (rows == 0) return PXK_OK;
+    if (!in || !out || !gamma) return fail(PXK_ERR_INVALID, "pxk_rms_norm_heads: NULL operand");
+    hipLaunchKernelGGL(rms_norm_heads_kernel, dim3(rows_grid(rows * heads)), dim3(kThreads), 0, S(stream), in, ld_in,
+                       out, ld_out, gamma, rows, heads, head_dim, eps);
+    return launched("pxk_rms_norm_heads");
+}
+
+int pxk_lrp_rope_rows(const float* acc, int64_t ld_acc, const float* x, int64_t ldx, const float* y, int64_t ldy,
+                      const float* z, int64_t ldz, const float* bias, const float* cos_t, const float* sin_t, float* g,
+                      int64_t ldg, int64_t rows, int64_t seq_len, int64_t heads, int64_t head_dim, float eps,
+                      int rotate_half, int rel_only, void* stream) {
+    const int64_t w = heads * head_dim;
+    if (rows < 0 || seq_len <= 0 || heads <= 0 || head_dim <= 0 || head_dim % 2 != 0 || ld_acc < w || ldx < w ||
+        ldy < w || ldg < w || (!rel_only && ldz < w))
+        return fail(PXK_ERR_INVALID, "pxk_lrp_rope_rows: bad sizes or row strides");
+    if (rows == 0) return PXK_OK;
+    if (!acc || !x || !y || !cos_t || !sin_t || !g || (!rel_only && !z))
+        return fail(PXK_ERR_INVALID, "pxk_lrp_rope_rows: a required operand is NULL");
+    const RopeRelArgs a{acc, ld_acc, x, ldx, y, ldy, z, ldz, bias, cos_t, sin_t, g, ldg, rows, seq_len, heads,
+                        head_dim, eps, rotate_half, rel_only};
+    hipLaunchKernelGGL(rope_rel_rows_kernel, dim3(grid_for(rows * heads * (head_dim / 2), kThreads)), dim3(kThreads), 0,
+                       S(stream), a);
+    return launched("pxk_lrp_rope_rows");
 }
 
 int pxk_rope_qk(const float* q_in, const float* k_in, int64_t ld_in, float* q_out, float* k_out, int64_t ld_out,

@@ -35,7 +35,7 @@ class GemmDesc(ctypes.Structure):
                 ("e_bias", Operand), ("e_bias2", Operand),
                 ("cos_t", c_vp), ("sin_t", c_vp), ("head_dim", c_i64), ("rope_half", ctypes.c_int32),
                 ("tile", ctypes.c_int32), ("workspace", c_vp), ("workspace_bytes", ctypes.c_size_t),
-                ("rope_cols", c_i64)]
+                ("rope_cols", c_i64), ("gate_act", ctypes.c_int32), ("reserved", ctypes.c_int32)]
 
 
 CAUSAL_NONE, CAUSAL_TRI, CAUSAL_K_LE_M, CAUSAL_K_GE_M = 0, 1, 2, 3
@@ -59,7 +59,7 @@ PXK_SIGNATURES = {
     "pxk_lrp_bilinear_elementwise": "ppppifp",
     "pxk_lrp_stabilized_divide": "ppppifnp",
     "pxk_lrp_bilinear_scale": "pppifp",
-    "pxk_swiglu_forward": "pippiip",
+    "pxk_swiglu_forward": "pippiinp",
     "pxk_copy_2d": "pipiiip",
     "pxk_accumulate_rows": "ppiip",
     "pxk_gather_rows": "pppiip",
@@ -74,8 +74,10 @@ PXK_SIGNATURES = {
     "pxk_dot": "ppippp",
     "pxk_attention_supported": "iiiii",
     "pxk_attention_forward": "pipipipppiiiiiifnp",
-    "pxk_attention_softmax": "ppiifnp",
-    "pxk_attention_lrp_scores": "ppppiiffnp",
+    "pxk_attention_softmax": "ppiifnip",
+    "pxk_attention_lrp_scores": "ppppiiffnip",
+    "pxk_rms_norm_heads": "pipipiiifp",
+    "pxk_lrp_rope_rows": "pipipipippppiiiiifnnp",
     "pxk_rope_qk": "ppippipppiiiiinp",
     "pxk_rope_rotate": "ppppiiinnp",
     "pxk_lrp_rope": "ppppppiiifnp",

@@ -365,31 +365,33 @@ def test_data_movement_kernels_match_oracle():
 
 
 @gpu
-@pytest.mark.parametrize("causal", [1, 0])
-def test_attention_row_kernels_match_oracle(causal):
-    """pxk_attention_softmax / pxk_attention_lrp_scores = the module's op sequences on the oracle."""
+@pytest.mark.parametrize("causal,window", [(1, 0), (0, 0), (1, 7), (1, 1)])
+def test_attention_row_kernels_match_oracle(causal, window):
+    """pxk_attention_softmax / pxk_attention_lrp_scores = the module's op sequences on the oracle,
+    causal, full, and causal with a sliding window (attention_mask_fill's window, row_math.hpp:117-126)."""
     H, L, scale, eps = 3, 45, 0.125, 1e-9
     raw = G.uniform((H, L, L), 1, -4, 4)
     scaled = np.empty_like(raw)
     G.oracle_call("pxo_axpby", scale, raw, 0.0, raw, scaled, raw.size)
     if causal:
-        G.oracle_call("pxo_attention_mask_fill", scaled, None, 1, H, L, L, 1, 0, 0, float(np.finfo(np.float32).min))
+        G.oracle_call("pxo_attention_mask_fill", scaled, None, 1, H, L, L, 1, 0, window,
+                      float(np.finfo(np.float32).min))
     p_ref = np.empty_like(raw)
     G.oracle_call("pxo_softmax_rows", scaled, p_ref, H * L, L)
     s = G.stream()
     p = G.empty(raw.shape)
     rawd = G.dev(raw)
-    N.call("pxk_attention_softmax", G.ptr(rawd), G.ptr(p), H, L, scale, causal, s)
+    N.call("pxk_attention_softmax", G.ptr(rawd), G.ptr(p), H, L, scale, causal, window, s)
     G.assert_close(G.host(p), p_ref, 1e-6, "softmax")
     r_attn = G.uniform((H, L, L), 2) * (p_ref > 0)
     r_sc = np.empty_like(raw)
     G.oracle_call("pxo_lrp_softmax_rows", scaled, p_ref, r_attn, r_sc, H * L, L)
     if causal:
-        G.oracle_call("pxo_attention_mask_fill", r_sc, None, 1, H, L, L, 1, 0, 0, 0.0)
+        G.oracle_call("pxo_attention_mask_fill", r_sc, None, 1, H, L, L, 1, 0, window, 0.0)
     ref = r_sc / (2 * raw + eps * np.where(raw >= 0, 1, -1).astype(np.float32))
     out = G.empty(raw.shape)
     N.call("pxk_attention_lrp_scores", G.ptr(G.dev(r_attn)), G.ptr(G.dev(p_ref)), G.ptr(rawd), G.ptr(out), H, L,
-           scale, eps, causal, s)
+           scale, eps, causal, window, s)
     G.assert_close(G.host(out), ref.astype(np.float32), 1e-5, "lrp scores")
 
 
