@@ -4,6 +4,7 @@
     python bench.py --op-sweep        # raw op sweep: GEMM shapes, elementwise 2^26, RMSNorm 32768 x 2048
     python bench.py --kernel-probe    # 256 MiB copy + LM-head relevance GEMM, for rocprofv3 --pmc runs
     python bench.py --rule gamma      # the same step under Zennit's Gamma(0.25) (or zplus, alpha2beta1, zbox)
+    python bench.py --decode          # Gemma-3-270m shape: batched KV-cached greedy decode + AttnLRP per token
 
 Workload: the SmolLM2-135M-shaped causal LM (30 layers, hidden 576, 9 query / 3 KV heads of 64,
 SwiGLU FFN 1536, vocab 49152, tied embeddings, RMSNorm eps 1e-5, RoPE theta 100000), fp32,
@@ -56,6 +57,18 @@ RULES = {
     "zbox": dict(rule=3, epsilon=1e-6, low=-3.0, high=3.0),
 }
 
+
+# Gemma-3-270m's shape (random init): 18 layers, hidden 640, 4 query / 1 KV heads of 256, GeGLU FFN
+# 2048, vocab 262144, tied; Gemma 3's (1 + w) and sandwich norms, QK-Norm, embeddings x sqrt(640),
+# query_pre_attn_scalar 256, RoPE 1e6 on the full layers (every sixth) and 1e4 on the sliding ones
+# (window 512).
+GEMMA_270M = dict(vocab_size=262144, hidden_size=640, num_layers=18, num_heads=4, num_kv_heads=1, head_dim=256,
+                  intermediate_size=2048, rms_norm_eps=1e-6, rope_theta=1e6, use_rope=1, rope_rotate_half=1, causal=1,
+                  qkv_bias=0, out_bias=0, mlp_bias=0, tie_word_embeddings=1, reserved=0, hidden_act=1, qk_norm=1,
+                  post_norms=1, norm_weight_offset=1.0, embed_scale=float(np.float32(np.sqrt(640.0))),
+                  query_pre_attn_scalar=256.0, rope_local_base=10000.0, sliding_window=512,
+                  sliding_layers=sum(1 << i for i in range(18) if i % 6 != 5))
+DECODE_BATCH, DECODE_PROMPT, DECODE_NEW = 4, 64, 256
 
 # GEMM work of one Linear's relevance relative to its forward GEMM, per rule: epsilon one transposed
 # GEMM; Gamma and AlphaBeta the reference's eight (four denominators, four backward products: here a
@@ -299,6 +312,88 @@ def op_sweep(torch, N, models):
                       FP32_MFMA_PEAK_TFLOPS, "peak_gbs": HBM_PEAK_GBS, "ops": rows}), flush=True)
 
 
+def decode_bench(args, torch, N, models):
+    """The Gemma-3-270m-shaped decode workload: batch 4, 64-token uniform-random prompts, 256 greedy
+    tokens through the KV caches (one HIP graph replay per token), then every generated token
+    explained by AttnLRP (LXT settings) over its prefix. A step is the whole job."""
+    cfg = N.model_config(**GEMMA_270M)
+    t_setup = time.perf_counter()
+    lm = models.CausalLM(cfg, seed=SEED, std=0.02)
+    n, p, T = DECODE_BATCH, DECODE_PROMPT, DECODE_NEW
+    ld = p + T
+    prompts = np.random.RandomState(SEED).randint(0, cfg.vocab_size, size=(n, p)).astype(np.float32)
+    ids = torch.full((n, ld), -1.0, device="cuda")
+    ids[:, :p] = torch.from_numpy(prompts).cuda()
+    picked = torch.zeros(n, ld, device="cuda")
+    W = p + T - 1
+    rel = torch.empty(T, n, W, device="cuda")
+    rule = N.lrp_rule(**RULES["lxt"])
+    stream = torch.cuda.ExternalStream(models.stream())
+    torch.cuda.synchronize()
+
+    def job():
+        e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+        e[0].record(stream)
+        lm.generate_device(ids.data_ptr(), n, p, T, ld, picked.data_ptr())
+        e[1].record(stream)
+        lm.explain_generated_device(ids.data_ptr(), n, p, T, ld, rule, rel.data_ptr())
+        e[2].record(stream)
+        return e
+
+    for _ in range(max(1, args.warmup)):
+        job()
+    models.synchronize()
+    setup_s = time.perf_counter() - t_setup
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    events = [job() for _ in range(args.steps)]
+    models.synchronize()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    dec_s = sum(e[0].elapsed_time(e[1]) for e in events) * 1e-3 / args.steps
+    exp_s = sum(e[1].elapsed_time(e[2]) for e in events) * 1e-3 / args.steps
+    out_ids = ids.cpu().numpy()
+    r = rel.cpu().numpy()
+    if not (np.all(np.isfinite(r)) and np.all(out_ids[:, p:] >= 0)):
+        print("bench.py: decode produced non-finite relevance or missing ids", file=sys.stderr)
+        sys.exit(1)
+    tokens = n * T * args.steps
+    out = {
+        "metric": "KV-cached greedy decode + per-token AttnLRP tokens/s, Gemma-3-270m shape, batch 4, 64 -> 256",
+        "value": round(tokens / wall, 2),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall / args.steps * 1e3, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic: random-init N(0,0.02) weights from seed %d, uniform-random prompt ids" % SEED,
+        "config": {"workload": "Gemma-3-270m-shaped causal LM (18 layers, hidden 640, 4/1 heads of 256, GeGLU FFN "
+                               "2048, vocab 262144, sliding window 512 on 5 of every 6 layers): batch 4, 64-token "
+                               "prompts, 256 greedy tokens through KV caches, each generated token explained by "
+                               "AttnLRP (LxtAttnLrpConfig) over its prefix",
+                   "global_batch": n, "prompt": p, "new_tokens": T, "parallelism": "single GPU"},
+        "decode_ms": round(dec_s * 1e3, 3),
+        "decode_tokens_per_s": round(n * T / dec_s, 1),
+        "decode_ms_per_step": round(dec_s * 1e3 / T, 4),
+        "explain_ms": round(exp_s * 1e3, 3),
+        "explained_tokens_per_s": round(n * T / exp_s, 1),
+        "setup_s": round(setup_s, 1),
+    }
+    if not args.no_cpu_baseline:
+        # One explanation at the generation's mean prefix length (the bulk of the job), 1 sequence.
+        mean_prefix = p + T // 2
+        cb = time_cpu_baseline(GEMMA_270M, mean_prefix, "lxt")
+        cb["sample"] = "one generated token explained at the mean prefix length (%d): %s" % (mean_prefix, cb["sample"])
+        cb["unit"] = "explained tokens/s (1 sequence; decode itself excluded)"
+        cb["value"] = round(cb["value"] / mean_prefix, 5)
+        out["cpu_baseline"] = cb
+    print(json.dumps(out), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -311,6 +406,8 @@ def main():
                     help="only launch a 256 MiB copy and the LM-head relevance GEMM, 5 times each (for rocprofv3 --pmc)")
     ap.add_argument("--op-sweep", action="store_true",
                     help="time the raw op sweep (GEMM shapes, elementwise over 2^26, RMSNorm 32768 x 2048) instead")
+    ap.add_argument("--decode", action="store_true",
+                    help="the Gemma-3-270m decode workload (batch 4, 64 -> 256 tokens, AttnLRP per generated token)")
     ap.add_argument("--rule", choices=sorted(RULES), default="lxt",
                     help="the LRP rule of the relevance pass (default: LXT's AttnLRP epsilon rule, the headline)")
     args = ap.parse_args()
@@ -329,6 +426,9 @@ def main():
         return
     if args.op_sweep:
         op_sweep(torch, N, models)
+        return
+    if args.decode:
+        decode_bench(args, torch, N, models)
         return
 
     fields = dict(S_CONFIG, num_layers=args.layers)

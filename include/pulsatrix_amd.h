@@ -147,6 +147,22 @@ int pxa_lm_explain_device_rule(void* lm, const float* ids, int64_t n, int64_t l,
 int pxa_lm_capture_explain_rule(void* lm, const float* ids, int64_t n, int64_t l, const px_lrp_rule* rule,
                                 float* token_rel, int64_t* targets);
 int pxa_lm_replay(void* lm);
+/* Forward over ids (n*l floats, HBM) and the LRP pass seeded at each sequence's last row only: the
+ * target id targets[b * target_stride] (floats in HBM) with its logit (or 1 with unit_seed). The head
+ * runs on those rows alone. token_rel (n*l) and targets_out (n int64, nullable) in HBM. */
+int pxa_lm_explain_rows_device(void* lm, const float* ids, int64_t n, int64_t l, const float* targets,
+                               int64_t target_stride, const px_lrp_rule* rule, float* token_rel, int64_t* targets_out,
+                               int unit_seed);
+/* Batched KV-cached greedy decode (MakeCachedNextTokenLogits + greedy Generate,
+ * src/generation.cpp:189-258, for a batch): ids (n rows of ld_ids floats, HBM) hold each prompt in
+ * the first `prompt` columns; columns prompt .. prompt + new_tokens - 1 receive the generated ids and
+ * picked_logit (same layout, nullable) their logits. One HIP graph replay per token; returns when done. */
+int pxa_lm_generate_device(void* lm, float* ids, int64_t n, int64_t prompt, int64_t new_tokens, int64_t ld_ids,
+                           float* picked_logit);
+/* AttnLRP of every generated token through a forward over its prefix (the reference's way to explain a
+ * cached generation): token_rel (new_tokens, n, prompt + new_tokens - 1) in HBM, zero past each prefix. */
+int pxa_lm_explain_generated_device(void* lm, const float* ids, int64_t n, int64_t prompt, int64_t new_tokens,
+                                    int64_t ld_ids, const px_lrp_rule* rule, float* token_rel, int unit_seed);
 /* After a device-side pass (explain or replay): 0 when every id was in [0, vocab), else -1 with
  * the reference's message ("EmbeddingModule::forward: index out of range [0, num_embeddings)") in
  * pxa_last_error(); an out-of-range id is gathered as id 0 so the pass itself completes. Waits for

@@ -412,6 +412,39 @@ int pxk_lrp_rule_combine(int rule, const float* x, int64_t ldx, const float* c, 
                          int64_t rows, int64_t in, float* r_in, int64_t ld, const float* split_a,
                          const float* split_b, const float* split_sum, float* r_b, float eps, void* stream);
 
+/* ---- KV-cached decode ----------------------------------------------------------------------------
+ * The position-dependent steps of a batched greedy decode step. The position is an int32 in device
+ * memory shared by the batch, so a step launches with the same arguments at every position (a HIP
+ * graph of one step is replayed per token) and pxk_decode_advance() moves it after the step.
+ * Replaces MakeCachedNextTokenLogits's per-step work (generation.cpp:189-258): KVCache::append
+ * (kv_cache.cpp:18-39), MultiHeadAttentionModule::forward_cached (multihead_attention_module.cpp:
+ * 501-587) and the host round trip of the last hidden row; batch 1 there, any batch here.
+ * Cache layout: sequence b at cache + b * seq_stride, position p at + p * kv_heads * head_dim. */
+/* q (rotated, at *pos) -> q_out (n x heads*head_dim); k (rotated) and v -> the caches at *pos, for
+ * *pos < positions (the caches' length, also the RoPE tables' (positions x head_dim/2)). */
+int pxk_decode_rope_append(const float* q, int64_t ldq, const float* k, int64_t ldk, const float* v, int64_t ldv,
+                           float* q_out, float* k_cache, float* v_cache, int64_t seq_stride, int64_t positions,
+                           const float* cos_t, const float* sin_t, const int32_t* pos, int64_t n, int64_t heads,
+                           int64_t kv_heads, int64_t head_dim, int rope, int rotate_half, void* stream);
+/* ctx (n x heads*head_dim) = softmax(scale q K^T) V over the cached keys 0..*pos (the last `window`
+ * of them when window > 0), one workgroup per (sequence, query head); max_keys bounds *pos + 1. */
+int pxk_decode_attention(const float* q, const float* k_cache, const float* v_cache, int64_t seq_stride, float* ctx,
+                         const int32_t* pos, int64_t n, int64_t heads, int64_t kv_heads, int64_t head_dim,
+                         int64_t window, int64_t max_keys, float scale, void* stream);
+/* Greedy pick (the first maximum of each sequence's logits row, rows ld_logits apart): ids[b * ld_ids +
+ * *pos + 1] and cur[b] get the id, picked_logit[b * ld_logit + *pos + 1] (nullable) its logit. */
+int pxk_decode_pick(const float* logits, int64_t ld_logits, int64_t n, int64_t vocab, float* ids, int64_t ld_ids,
+                    float* cur, float* picked_logit, int64_t ld_logit, const int32_t* pos, void* stream);
+/* *pos += 1 (one thread). */
+int pxk_decode_advance(int32_t* pos, void* stream);
+/* The LRP seed of one row per sequence (n x vocab, every other entry 0; the explained rows' logits
+ * are rows ld_logits apart): one-hot at the id targets[b * stride] (a float, rounded; an id outside
+ * the vocabulary seeds id 0) with that logit as its value (LRPSeed::OutputValue) or 1 (unit,
+ * OneHot); targets_out (n int64, nullable) receives the ids. The device-resident-targets form of
+ * pxk_lm_seed, for explaining tokens a decode generated. */
+int pxk_seed_rows(const float* logits, int64_t ld_logits, const float* targets, int64_t stride, int64_t n,
+                  int64_t vocab, float* seed, int64_t* targets_out, int unit, void* stream);
+
 /* ---- checkpoint loading ----------------------------------------------------------------------
  * A checkpoint tensor's raw little-endian bytes (already copied to the device) widened to fp32 as
  * SafetensorsFile::tensor does on the host (src/safetensors.cpp:676-740): BF16 and F16 and both

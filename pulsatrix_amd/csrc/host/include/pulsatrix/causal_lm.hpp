@@ -45,6 +45,30 @@ public:
      *         argmax. unit_seed: one-hot seed (LRPSeed::OneHot) instead of the logit value. */
     void explain_device(const float* ids, int64_t n, int64_t l, const LRPRuleConfig& config, float* token_relevance,
                         int64_t* targets, const int64_t* targets_in = nullptr, bool unit_seed = false);
+    /** @brief Forward over n x l ids in HBM, then the LRP pass seeded at each sequence's last row
+     *         only: target id targets[b * target_stride] (a float id in HBM) with its logit as the
+     *         value (or 1 with unit_seed). The head runs on the last rows alone (every other row's
+     *         relevance is exactly zero: its seed row is zero), so no (n*l, vocab) logits or seed exist.
+     *         token_relevance (n*l) and targets_out (n int64, nullable) in HBM. */
+    void explain_rows_device(const float* ids, int64_t n, int64_t l, const float* targets, int64_t target_stride,
+                             const LRPRuleConfig& config, float* token_relevance, int64_t* targets_out = nullptr,
+                             bool unit_seed = false);
+    /** @brief Batched KV-cached greedy decode on the device (MakeCachedNextTokenLogits and greedy
+     *         Generate, generation.cpp:189-258, with a batch): ids (n rows of ld_ids floats in HBM)
+     *         hold each prompt in its first `prompt` columns; columns prompt .. prompt + new_tokens - 1
+     *         receive the generated ids and picked_logit (same layout, nullable) the logits that picked
+     *         them. One forward over the prompts fills the KV caches; then each decode step is one HIP
+     *         graph replay (the position lives on the device, so no host work between steps). Returns
+     *         once the replays have run (the graph is then released). */
+    void generate_greedy_device(float* ids, int64_t n, int64_t prompt, int64_t new_tokens, int64_t ld_ids,
+                                float* picked_logit = nullptr);
+    /** @brief AttnLRP of each generated token: token t (at column prompt + t) explained through a
+     *         forward over its prefix (columns 0 .. prompt + t - 1), seeded with its id at the
+     *         prefix's last row (explain_rows_device), as the reference explains a cached generation
+     *         (forward_cached keeps no relevance state). token_relevance (new_tokens, n, W) in HBM with
+     *         W = prompt + new_tokens - 1, zero past each prefix. */
+    void explain_generated_device(const float* ids, int64_t n, int64_t prompt, int64_t new_tokens, int64_t ld_ids,
+                                  const LRPRuleConfig& config, float* token_relevance, bool unit_seed = false);
     /** @brief Whether every id of the last device-side pass was in [0, vocab) (waits for the
      *         stream). An out-of-range id is gathered as id 0, so its pass completes; the reference
      *         would have thrown "EmbeddingModule::forward: index out of range [0, num_embeddings)". */
@@ -69,9 +93,14 @@ private:
     RMSNormModule norm_;
     std::unique_ptr<TiedLMHeadModule> tied_head_;
     std::unique_ptr<LinearModule> lm_head_;
+    /** @brief Layers, final norm and the head on the last row of each sequence: (n, vocab) logits. */
+    const float* forward_last_rows(const float* ids, int64_t n, int64_t l);
+    const float* run_forward_hidden(const float* ids, int64_t n, int64_t l);
+
     int64_t N_ = 0, L_ = 0;
     const float* r_embed_ = nullptr;
-    detail::DevBuf ids_, seed_;
+    detail::DevBuf ids_, seed_, last_x_, r_top_, prompt_ids_, dec_x_, cur_ids_, pos_, tok_tmp_;
+    std::vector<KVCacheState> caches_;
 };
 
 }  // namespace pulsatrix

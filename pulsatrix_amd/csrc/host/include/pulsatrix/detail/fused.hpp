@@ -13,22 +13,30 @@
 
 namespace pulsatrix::detail {
 
-/** @brief A module-owned device buffer. Its storage (and address) is kept while its size is
- *         unchanged, so repeated passes at one shape launch on the same addresses (and can be
- *         captured into a HIP graph once). */
+/** @brief A module-owned device buffer with capacity semantics: its storage (and address) is kept
+ *         while the requested size fits, so repeated passes at one shape launch on the same
+ *         addresses (and can be captured into a HIP graph once), and passes at shorter lengths
+ *         (a generation's growing prefixes, explained longest first) reuse the longest one's
+ *         storage instead of allocating per length. */
 class DevBuf {
 public:
     float* ensure(DeviceBackend* be, int64_t n) {
-        if (t_.numel() != n || t_.backend() != be) t_ = Tensor::uninitialized(Shape({n}), be);
+        if (t_.numel() < n || t_.backend() != be || (n == 0 && t_.numel() != 0)) t_ = Tensor::uninitialized(Shape({n}), be);
+        n_ = n;
         return t_.data();
     }
     [[nodiscard]] float* data() noexcept { return t_.data(); }
     [[nodiscard]] const float* data() const noexcept { return t_.data(); }
-    [[nodiscard]] int64_t size() const noexcept { return t_.numel(); }
-    void release() { t_ = Tensor(); }
+    /** @brief The size of the last ensure() (the storage may be larger). */
+    [[nodiscard]] int64_t size() const noexcept { return n_; }
+    void release() {
+        t_ = Tensor();
+        n_ = 0;
+    }
 
 private:
     Tensor t_;
+    int64_t n_ = 0;
 };
 
 /** @brief The MI355X modules compute through MI355XBackend's fused kernels. */

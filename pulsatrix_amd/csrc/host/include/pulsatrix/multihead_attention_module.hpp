@@ -46,6 +46,14 @@ struct AttentionConfig {
     float qk_norm_weight_offset = 0.0f;
 };
 
+/** @brief One layer's KV cache for a batched decode (the KVCache of kv_cache.cpp:18-39, for a
+ *         batch): keys after QK-Norm and RoPE and values, sequence b's position p at row
+ *         b * positions + p of (n * positions, kv_heads * head_dim). */
+struct KVCacheState {
+    detail::DevBuf k, v;
+    int64_t n = 0, positions = 0;
+};
+
 class MultiHeadAttentionModule : public Module {
 public:
     MultiHeadAttentionModule(const AttentionConfig& config, DeviceBackend* backend);
@@ -79,6 +87,16 @@ public:
     /** @brief The attention output (after the output projection's bias) of the last forward. */
     [[nodiscard]] const float* output() const noexcept;
 
+    /** @brief Fills `cache` (n sequences, `positions` each) with the last forward's keys and values:
+     *         the prompt rows of a decode. Also sizes the RoPE tables for every cached position. */
+    void export_kv(KVCacheState& cache, int64_t positions);
+    /** @brief One decode step of n sequences (forward_cached, multihead_attention_module.cpp:501-587):
+     *         x (n, d_model) at the device position *pos; the step's key and value join the cache.
+     *         With `resid`, resid_out = resid + output. Returns the output (n, d_model). Launches the
+     *         same kernels with the same arguments at every position (HIP-graph capturable). */
+    const float* decode_step(const float* x, int64_t n, KVCacheState& cache, const int32_t* pos,
+                             const float* resid = nullptr, float* resid_out = nullptr);
+
 protected:
     Tensor forward_impl(const Tensor& input) override;
 
@@ -107,6 +125,7 @@ private:
     const float* x_ = nullptr;
     detail::DevBuf x_copy_, qkv_z_, qkv_y_, qk_norm_out_, qk_rot_, raw_, p_, ctx_, out_z_, out_y_;
     detail::DevBuf spv_, ra_, g_, r_in_, rctx_;
+    detail::DevBuf dec_z_, dec_y_, dec_qkn_, dec_q_, dec_ctx_, dec_oz_, dec_oy_;
     detail::AffineRule out_rule_, qkv_rule_;
     Tensor key_rel_, value_rel_;
     bool has_relevance_ = false;

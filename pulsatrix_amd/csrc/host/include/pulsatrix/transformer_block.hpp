@@ -53,6 +53,9 @@ public:
      *         underneath asks for (its output is this block's input), or none. Returns the input
      *         relevance when `below` is empty, else nullptr. */
     const float* run_relevance_split(const LRPRuleConfig& config, const detail::ResidualSplit& below);
+    /** @brief One KV-cached decode step of n sequences at the device position *pos
+     *         (forward_cached, transformer_block.cpp:135-153). Returns y2 (n, d_model). */
+    const float* decode_step(const float* x, int64_t n, KVCacheState& cache, const int32_t* pos);
 
 protected:
     Tensor forward_impl(const Tensor& input) override;
@@ -70,7 +73,7 @@ private:
     int64_t N_ = 0, L_ = 0;
     const float* x_ = nullptr;
     Shape last_shape_;
-    detail::DevBuf x_copy_, y1_, y2_, r_y1d_, r_ffn_, r_y1_, r_xd_, r_attn_;
+    detail::DevBuf x_copy_, y1_, y2_, r_y1d_, r_ffn_, r_y1_, r_xd_, r_attn_, dec_y1_, dec_y2_;
 };
 
 }  // namespace pulsatrix

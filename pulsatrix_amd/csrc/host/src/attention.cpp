@@ -234,6 +234,94 @@ const float* MultiHeadAttentionModule::run_forward(const float* x, int64_t n, in
     return oy;
 }
 
+void MultiHeadAttentionModule::export_kv(KVCacheState& cache, int64_t positions) {
+    if (x_ == nullptr) throw std::logic_error("MultiHeadAttentionModule::export_kv: called before any forward()");
+    if (positions < L_) throw std::invalid_argument("MultiHeadAttentionModule::export_kv: the cache is shorter than the prompt");
+    const int64_t qd = H_ * D_, kvd = Hkv_ * D_, w3 = qd + 2 * kvd, rw = qd + kvd;
+    ensure_tables(positions);
+    cache.n = N_;
+    cache.positions = positions;
+    float* kc = cache.k.ensure(be_, N_ * positions * kvd);
+    float* vc = cache.v.ensure(be_, N_ * positions * kvd);
+    const float* z = qkv_z_.data();
+    const float* y = config_.qkv_bias ? qkv_y_.data() : z;
+    // The keys the attention read: rotated, or after QK-Norm alone, or the projection itself.
+    const float* k = config_.use_rope ? qk_rot_.data() + qd : (config_.use_qk_norm ? qk_norm_out_.data() + qd : y + qd);
+    const int64_t ldk = (config_.use_rope || config_.use_qk_norm) ? rw : w3;
+    for (int64_t b = 0; b < N_; ++b) {
+        be_->copy_2d(kc + b * positions * kvd, static_cast<size_t>(kvd), k + b * L_ * ldk, static_cast<size_t>(ldk),
+                     static_cast<size_t>(L_), static_cast<size_t>(kvd));
+        be_->copy_2d(vc + b * positions * kvd, static_cast<size_t>(kvd), y + qd + kvd + b * L_ * w3,
+                     static_cast<size_t>(w3), static_cast<size_t>(L_), static_cast<size_t>(kvd));
+    }
+}
+
+const float* MultiHeadAttentionModule::decode_step(const float* x, int64_t n, KVCacheState& cache, const int32_t* pos,
+                                                   const float* resid, float* resid_out) {
+    if (cache.positions <= 0 || cache.n != n)
+        throw std::logic_error("MultiHeadAttentionModule::decode_step: the cache holds no prompt for this batch");
+    pack_weights();
+    const int64_t qd = H_ * D_, kvd = Hkv_ * D_, w3 = qd + 2 * kvd, rw = qd + kvd;
+    void* st = be_->stream();
+    float* z = dec_z_.ensure(be_, n * w3);
+    float* y = config_.qkv_bias ? dec_y_.ensure(be_, n * w3) : z;
+    {
+        pxk_gemm_desc d = gemm_desc(n, w3, d_);
+        d.a = mat(x, d_);
+        d.b = mat(wqkv_.data(), w3);
+        d.c = mat(z, w3);
+        if (config_.qkv_bias) {
+            d.epilogue = PXK_EPI_STORE_BIAS;
+            d.c2 = mat(y, w3);
+            d.e_bias = mat(bqkv_.data(), 0);
+        }
+        be_->run_gemm(d);
+    }
+    const float* pre = y;
+    int64_t ld_pre = w3;
+    if (config_.use_qk_norm) {
+        float* nq = dec_qkn_.ensure(be_, n * rw);
+        MI355XBackend::check(pxk_rms_norm_heads(y, w3, nq, rw, q_norm_->effective_gamma(), n, H_, D_, q_norm_->eps(), st),
+                             "MultiHeadAttentionModule::decode_step (QK-Norm)");
+        MI355XBackend::check(pxk_rms_norm_heads(y + qd, w3, nq + qd, rw, k_norm_->effective_gamma(), n, Hkv_, D_,
+                                                k_norm_->eps(), st),
+                             "MultiHeadAttentionModule::decode_step (QK-Norm)");
+        pre = nq;
+        ld_pre = rw;
+    }
+    const int64_t stride = cache.positions * kvd;
+    float* q = dec_q_.ensure(be_, n * qd);
+    MI355XBackend::check(pxk_decode_rope_append(pre, ld_pre, pre + qd, ld_pre, y + qd + kvd, w3, q, cache.k.data(),
+                                                cache.v.data(), stride, cache.positions, cos_.data(), sin_.data(), pos, n,
+                                                H_, Hkv_, D_, config_.use_rope,
+                                                config_.rope_layout == RoPELayout::RotateHalf, st),
+                         "MultiHeadAttentionModule::decode_step (RoPE, cache)");
+    float* ctx = dec_ctx_.ensure(be_, n * qd);
+    const int64_t window = config_.causal ? config_.sliding_window : 0;
+    MI355XBackend::check(pxk_decode_attention(q, cache.k.data(), cache.v.data(), stride, ctx, pos, n, H_, Hkv_, D_,
+                                              window, cache.positions, score_scale(), st),
+                         "MultiHeadAttentionModule::decode_step (attention)");
+    float* oz = dec_oz_.ensure(be_, n * d_);
+    float* oy = config_.out_bias ? dec_oy_.ensure(be_, n * d_) : oz;
+    pxk_gemm_desc d = gemm_desc(n, d_, qd);
+    d.a = mat(ctx, qd);
+    d.b = mat(out_proj_.weight_data(), d_);
+    d.c = mat(oz, d_);
+    if (config_.out_bias) {
+        d.c2 = mat(oy, d_);
+        d.e_bias = mat(out_proj_.bias_data(), 0);
+    }
+    if (resid) {
+        d.epilogue = PXK_EPI_ADD_RESID;
+        d.x = mat(resid, d_);
+        d.c3 = mat(resid_out, d_);
+    } else {
+        d.epilogue = config_.out_bias ? PXK_EPI_STORE_BIAS : PXK_EPI_STORE;
+    }
+    be_->run_gemm(d);
+    return oy;
+}
+
 // Scores GEMM, softmax and P V as three launches: head_dim outside pxk_attention_supported().
 void MultiHeadAttentionModule::run_attention_unfused(const float* q, int64_t ldq, const float* k, int64_t ldk,
                                                      const float* v, int64_t n, int64_t l) {

@@ -256,6 +256,22 @@ const float* TransformerBlock::run_forward(const float* x, int64_t n, int64_t l)
     return y2;
 }
 
+const float* TransformerBlock::decode_step(const float* x, int64_t n, KVCacheState& cache, const int32_t* pos) {
+    float* y1 = dec_y1_.ensure(be_, n * d_);
+    float* y2 = dec_y2_.ensure(be_, n * d_);
+    if (!post_attn_norm_) {
+        mha_.decode_step(norm1_.run_forward(x, n), n, cache, pos, x, y1);
+        swiglu_.run_forward(norm2_.run_forward(y1, n), n, y1, y2);
+        return y2;
+    }
+    void* st = be_->stream();
+    const float* a = post_attn_norm_->run_forward(mha_.decode_step(norm1_.run_forward(x, n), n, cache, pos), n);
+    MI355XBackend::check(pxk_add(x, a, y1, n * d_, st), "TransformerBlock::decode_step");
+    const float* f = post_mlp_norm_->run_forward(swiglu_.run_forward(norm2_.run_forward(y1, n), n), n);
+    MI355XBackend::check(pxk_add(y1, f, y2, n * d_, st), "TransformerBlock::decode_step");
+    return y2;
+}
+
 detail::ResidualSplit TransformerBlock::output_split() {
     const int64_t n = N_ * L_ * d_;
     return {y1_.data(), ffn_out_, y2_.data(), r_y1d_.ensure(be_, n), r_ffn_.ensure(be_, n)};

@@ -538,6 +538,30 @@ int pxa_lm_capture_explain_rule(void* handle, const float* ids, int64_t n, int64
     });
 }
 
+int pxa_lm_explain_rows_device(void* handle, const float* ids, int64_t n, int64_t l, const float* targets,
+                               int64_t target_stride, const px_lrp_rule* p, float* token_rel, int64_t* targets_out,
+                               int unit_seed) {
+    return guarded([&] {
+        static_cast<LmHandle*>(handle)->lm->explain_rows_device(ids, n, l, targets, target_stride, rule(p), token_rel,
+                                                                targets_out, unit_seed != 0);
+    });
+}
+
+int pxa_lm_generate_device(void* handle, float* ids, int64_t n, int64_t prompt, int64_t new_tokens, int64_t ld_ids,
+                           float* picked_logit) {
+    return guarded([&] {
+        static_cast<LmHandle*>(handle)->lm->generate_greedy_device(ids, n, prompt, new_tokens, ld_ids, picked_logit);
+    });
+}
+
+int pxa_lm_explain_generated_device(void* handle, const float* ids, int64_t n, int64_t prompt, int64_t new_tokens,
+                                    int64_t ld_ids, const px_lrp_rule* p, float* token_rel, int unit_seed) {
+    return guarded([&] {
+        static_cast<LmHandle*>(handle)->lm->explain_generated_device(ids, n, prompt, new_tokens, ld_ids, rule(p),
+                                                                     token_rel, unit_seed != 0);
+    });
+}
+
 int pxa_lm_replay(void*) {
     return guarded([&] { backend()->replay(); });
 }

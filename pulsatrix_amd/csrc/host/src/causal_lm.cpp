@@ -1,8 +1,11 @@
 // CausalLM on MI355XBackend (src/causal_lm.cpp, src/hf_model.cpp:282-313).
 #include "pulsatrix/causal_lm.hpp"
 
+#include <hip/hip_runtime_api.h>
+
 #include <cmath>
 #include <stdexcept>
+#include <string>
 
 namespace pulsatrix {
 
@@ -119,7 +122,7 @@ CausalLM::CausalLM(const HfModelConfig& config, DeviceBackend* backend)
 
 const float* CausalLM::last_logits() const noexcept { return tied_head_ ? tied_head_->logits() : nullptr; }
 
-const float* CausalLM::run_forward(const float* ids, int64_t n, int64_t l) {
+const float* CausalLM::run_forward_hidden(const float* ids, int64_t n, int64_t l) {
     N_ = n;
     L_ = l;
     const int64_t M = n * l;
@@ -131,8 +134,22 @@ const float* CausalLM::run_forward(const float* ids, int64_t n, int64_t l) {
                              "CausalLM::forward");
     }
     for (auto& layer : layers_) x = layer->run_forward(x, n, l);
-    const float* xn = norm_.run_forward(x, M);
+    return norm_.run_forward(x, M);
+}
+
+const float* CausalLM::run_forward(const float* ids, int64_t n, int64_t l) {
+    const int64_t M = n * l;
+    const float* xn = run_forward_hidden(ids, n, l);
     return tied_head_ ? tied_head_->run_forward(xn, M) : lm_head_->run_forward(xn, M);
+}
+
+const float* CausalLM::forward_last_rows(const float* ids, int64_t n, int64_t l) {
+    const int64_t d = config_.hidden_size;
+    const float* xn = run_forward_hidden(ids, n, l);
+    float* xl = last_x_.ensure(be_, n * d);
+    be_->copy_2d(xl, static_cast<size_t>(d), xn + (l - 1) * d, static_cast<size_t>(l * d), static_cast<size_t>(n),
+                 static_cast<size_t>(d));
+    return tied_head_ ? tied_head_->run_forward(xl, n) : lm_head_->run_forward(xl, n);
 }
 
 const float* CausalLM::run_relevance(const float* seed, const LRPRuleConfig& config) {
@@ -159,6 +176,129 @@ void CausalLM::explain_device(const float* ids, int64_t n, int64_t l, const LRPR
     MI355XBackend::check(pxk_lm_seed(logits, n, l, V, targets_in, targets, seed, unit_seed, be_->stream()),
                          "CausalLM::explain_device (seed)");
     embed_.token_relevance(run_relevance(seed, config), M, token_relevance);
+}
+
+void CausalLM::explain_rows_device(const float* ids, int64_t n, int64_t l, const float* targets, int64_t target_stride,
+                                   const LRPRuleConfig& config, float* token_relevance, int64_t* targets_out,
+                                   bool unit_seed) {
+    if (n <= 0 || l <= 0) throw std::invalid_argument("CausalLM::explain_rows_device: n and l must be positive");
+    const int64_t V = config_.vocab_size, d = config_.hidden_size, M = n * l;
+    void* st = be_->stream();
+    const float* logits = forward_last_rows(ids, n, l);
+    float* seed = seed_.ensure(be_, n * V);
+    MI355XBackend::check(pxk_seed_rows(logits, V, targets, target_stride, n, V, seed, targets_out, unit_seed, st),
+                         "CausalLM::explain_rows_device (seed)");
+    // The head's rule on the n seeded rows, then those rows' relevance placed at each sequence's last
+    // row of the stack's output (every other row's is zero, as the dense pass computes it).
+    const float* rl = tied_head_ ? tied_head_->run_relevance(seed, config) : lm_head_->run_relevance(seed, config);
+    float* rtop = r_top_.ensure(be_, M * d);
+    MI355XBackend::check(pxk_fill(rtop, 0.0f, M * d, st), "CausalLM::explain_rows_device");
+    be_->copy_2d(rtop + (l - 1) * d, static_cast<size_t>(l * d), rl, static_cast<size_t>(d), static_cast<size_t>(n),
+                 static_cast<size_t>(d));
+    const float* r = rtop;
+    if (!layers_.empty()) {  // the final RMSNorm passes relevance unchanged
+        const detail::ResidualSplit top = layers_.back()->output_split();
+        MI355XBackend::check(pxk_lrp_residual_split(top.a, top.b, rtop, top.r_a, top.r_b, M * d, config.epsilon, st),
+                             "CausalLM::explain_rows_device");
+        for (size_t i = layers_.size(); i-- > 0;)
+            r = layers_[i]->run_relevance_split(config, i > 0 ? layers_[i - 1]->output_split() : detail::ResidualSplit{});
+    }
+    r_embed_ = r;
+    embed_.token_relevance(r, M, token_relevance);
+}
+
+void CausalLM::generate_greedy_device(float* ids, int64_t n, int64_t prompt, int64_t new_tokens, int64_t ld_ids,
+                                      float* picked_logit) {
+    if (!config_.causal)
+        throw std::logic_error("CausalLM::next_token_logits: the model attends bidirectionally (a diffusion LM), so it "
+                               "has no next-token cache");
+    if (n <= 0 || prompt <= 0 || new_tokens <= 0)
+        throw std::invalid_argument("CausalLM::generate: n, the prompt length and new_tokens must be positive");
+    if (ld_ids < prompt + new_tokens)
+        throw std::invalid_argument("CausalLM::generate: the id rows must hold the prompt and every new token");
+    const int64_t V = config_.vocab_size, d = config_.hidden_size;
+    const int64_t positions = prompt + new_tokens - 1;  // the last generated token is never fed back
+    void* st = be_->stream();
+    // 1. the prompts: one forward fills every layer's cache; its last rows pick the first token.
+    float* pid = prompt_ids_.ensure(be_, n * prompt);
+    be_->copy_2d(pid, static_cast<size_t>(prompt), ids, static_cast<size_t>(ld_ids), static_cast<size_t>(n),
+                 static_cast<size_t>(prompt));
+    const float* logits = forward_last_rows(pid, n, prompt);
+    caches_.resize(layers_.size());
+    for (size_t i = 0; i < layers_.size(); ++i) layers_[i]->mha().export_kv(caches_[i], positions);
+    auto* pos = reinterpret_cast<int32_t*>(pos_.ensure(be_, 1));
+    const int32_t start = static_cast<int32_t>(prompt - 1);
+    be_->copy(pos, &start, sizeof(start), CopyDirection::HostToDevice);
+    float* cur = cur_ids_.ensure(be_, n);
+    auto pick = [&](const float* lg) {
+        MI355XBackend::check(pxk_decode_pick(lg, V, n, V, ids, ld_ids, cur, picked_logit, ld_ids, pos, st),
+                             "CausalLM::generate (pick)");
+        MI355XBackend::check(pxk_decode_advance(pos, st), "CausalLM::generate (advance)");
+    };
+    pick(logits);
+    // 2. decode steps: the step's own token in, the next one out, at the device position.
+    auto step = [&] {
+        float* x = dec_x_.ensure(be_, n * d);
+        MI355XBackend::check(pxk_gather_rows(embed_.weight_data(), cur, x, n, d, st), "CausalLM::generate");
+        if (config_.embed_scale != 1.0f)
+            MI355XBackend::check(pxk_axpby(config_.embed_scale, x, 0.0f, nullptr, x, n * d, st), "CausalLM::generate");
+        const float* h = x;
+        for (size_t i = 0; i < layers_.size(); ++i) h = layers_[i]->decode_step(h, n, caches_[i], pos);
+        const float* hn = norm_.run_forward(h, n);
+        pick(tied_head_ ? tied_head_->run_forward(hn, n) : lm_head_->run_forward(hn, n));
+    };
+    if (new_tokens < 2) return;
+    step();  // eagerly once: every buffer and workspace the step uses exists before the capture
+    if (new_tokens < 3) return;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    auto hip = [](hipError_t e, const char* what) {
+        if (e != hipSuccess) throw std::runtime_error(std::string("CausalLM::generate: ") + what + ": " + hipGetErrorString(e));
+    };
+    hip(hipStreamBeginCapture(static_cast<hipStream_t>(st), hipStreamCaptureModeThreadLocal), "begin capture");
+    try {
+        step();
+    } catch (...) {
+        hipGraph_t g = nullptr;
+        (void)hipStreamEndCapture(static_cast<hipStream_t>(st), &g);
+        if (g) (void)hipGraphDestroy(g);
+        throw;
+    }
+    hip(hipStreamEndCapture(static_cast<hipStream_t>(st), &graph), "end capture");
+    const hipError_t inst = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    if (inst != hipSuccess) {
+        (void)hipGraphDestroy(graph);
+        hip(inst, "instantiate");
+    }
+    hipError_t rc = hipSuccess;
+    for (int64_t t = 2; t < new_tokens && rc == hipSuccess; ++t) rc = hipGraphLaunch(exec, static_cast<hipStream_t>(st));
+    // The graph is released only once its replays have run.
+    const hipError_t done = hipStreamSynchronize(static_cast<hipStream_t>(st));
+    (void)hipGraphExecDestroy(exec);
+    (void)hipGraphDestroy(graph);
+    hip(rc, "replay");
+    hip(done, "synchronize");
+}
+
+void CausalLM::explain_generated_device(const float* ids, int64_t n, int64_t prompt, int64_t new_tokens, int64_t ld_ids,
+                                        const LRPRuleConfig& config, float* token_relevance, bool unit_seed) {
+    if (n <= 0 || prompt <= 0 || new_tokens <= 0 || ld_ids < prompt + new_tokens)
+        throw std::invalid_argument("CausalLM::explain_generated_device: bad sizes");
+    const int64_t W = prompt + new_tokens - 1;
+    void* st = be_->stream();
+    // Longest prefix first: its buffers then serve every shorter one at the same addresses.
+    for (int64_t t = new_tokens - 1; t >= 0; --t) {
+        const int64_t l = prompt + t;
+        float* pid = prompt_ids_.ensure(be_, n * l);
+        be_->copy_2d(pid, static_cast<size_t>(l), ids, static_cast<size_t>(ld_ids), static_cast<size_t>(n),
+                     static_cast<size_t>(l));
+        float* tmp = tok_tmp_.ensure(be_, n * l);
+        explain_rows_device(pid, n, l, ids + l, ld_ids, config, tmp, nullptr, unit_seed);
+        float* out = token_relevance + t * n * W;
+        MI355XBackend::check(pxk_fill(out, 0.0f, n * W, st), "CausalLM::explain_generated_device");
+        be_->copy_2d(out, static_cast<size_t>(W), tmp, static_cast<size_t>(l), static_cast<size_t>(n),
+                     static_cast<size_t>(l));
+    }
 }
 
 Tensor CausalLM::forward_impl(const Tensor& input) {

@@ -158,6 +158,21 @@ class CausalLM:
         N.host_check(N.host().pxa_lm_capture_explain_rule(self.h, ids_ptr, n, l, ctypes.byref(N.as_rule(rule)),
                                                           token_rel_ptr, targets_ptr))
 
+    def explain_rows_device(self, ids_ptr, n, l, targets_ptr, target_stride, rule, token_rel_ptr, targets_out_ptr=None,
+                            unit_seed=False):
+        N.host_check(N.host().pxa_lm_explain_rows_device(self.h, ids_ptr, n, l, targets_ptr, target_stride,
+                                                         ctypes.byref(N.as_rule(rule)), token_rel_ptr, targets_out_ptr,
+                                                         int(unit_seed)))
+
+    def generate_device(self, ids_ptr, n, prompt, new_tokens, ld_ids, picked_logit_ptr=None):
+        """Batched KV-cached greedy decode into the id rows (device pointers)."""
+        N.host_check(N.host().pxa_lm_generate_device(self.h, ids_ptr, n, prompt, new_tokens, ld_ids, picked_logit_ptr))
+
+    def explain_generated_device(self, ids_ptr, n, prompt, new_tokens, ld_ids, rule, token_rel_ptr, unit_seed=False):
+        N.host_check(N.host().pxa_lm_explain_generated_device(self.h, ids_ptr, n, prompt, new_tokens, ld_ids,
+                                                              ctypes.byref(N.as_rule(rule)), token_rel_ptr,
+                                                              int(unit_seed)))
+
     def replay(self):
         N.host_check(N.host().pxa_lm_replay(self.h))
 

@@ -84,6 +84,11 @@ PXK_SIGNATURES = {
     "pxk_permute_0213": "ppiiiip",
     "pxk_attention_mask_fill": "ppiiiiniifp",
     "pxk_lm_seed": "piiipppnp",
+    "pxk_decode_advance": "pp",
+    "pxk_seed_rows": "pipiiippnp",
+    "pxk_decode_pick": "piiipippipp",
+    "pxk_decode_attention": "pppippiiiiiifp",
+    "pxk_decode_rope_append": "pipipipppiipppiiiinnp",
 }
 
 
@@ -302,6 +307,11 @@ def host():
             "pxa_lm_explain_device_rule": (ctypes.c_int, [c_vp, c_vp, c_i64, c_i64, rulep, c_vp, c_vp, i64p,
                                                           ctypes.c_int]),
             "pxa_lm_capture_explain_rule": (ctypes.c_int, [c_vp, c_vp, c_i64, c_i64, rulep, c_vp, c_vp]),
+            "pxa_lm_explain_rows_device": (ctypes.c_int, [c_vp, c_vp, c_i64, c_i64, c_vp, c_i64, rulep, c_vp, c_vp,
+                                                          ctypes.c_int]),
+            "pxa_lm_generate_device": (ctypes.c_int, [c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_vp]),
+            "pxa_lm_explain_generated_device": (ctypes.c_int, [c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, rulep, c_vp,
+                                                               ctypes.c_int]),
             "pxa_lm_check_device_ids": (ctypes.c_int, [c_vp]),
             "pxa_lm_last_logits": (c_vp, [c_vp]),
             "pxa_lm_last_embedding_relevance": (c_vp, [c_vp]),

@@ -129,10 +129,12 @@ def test_load_rejects_bad_checkpoints(tmp_path):
     assert "cannot open" in load(tmp_path) and "config.json" in load(tmp_path)
     (tmp_path / "config.json").write_text(json.dumps(cfg))
     assert "no model.safetensors" in load(tmp_path)
-    bad = dict(cfg, rope_scaling={"rope_type": "llama3", "factor": 8.0})
+    bad = dict(cfg, rope_scaling={"rope_type": "yarn", "factor": 8.0})  # linear and llama3 are supported
     (tmp_path / "config.json").write_text(json.dumps(bad))
     write_safetensors(tmp_path / "model.safetensors", {"x": ("F32", np.zeros(2, np.float32))})
-    assert "rope_scaling" in load(tmp_path)
+    assert "rope_scaling \"yarn\"" in load(tmp_path)
+    (tmp_path / "config.json").write_text(json.dumps(dict(cfg, hidden_act="relu")))
+    assert "hidden_act \"relu\"" in load(tmp_path)
     (tmp_path / "config.json").write_text(json.dumps(cfg))
     assert "has no tensor \"model.embed_tokens.weight\"" in load(tmp_path)
     (tmp_path / "model.safetensors").write_bytes(struct.pack("<Q", 1 << 40))
