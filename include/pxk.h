@@ -105,7 +105,11 @@ enum {
     PXK_TILE_32x64 = 3,   /* 4 waves each on a quarter of a 64-wide K stage, summed in LDS */
     PXK_TILE_32x32 = 4,   /* as 32x64 */
     PXK_TILE_32x64_DIRECT = 5, /* as 32x64, each wave streaming its operands from L2 into registers */
-    PXK_TILE_32x32_DIRECT = 6
+    PXK_TILE_32x32_DIRECT = 6,
+    PXK_TILE_SKINNY = 7   /* m <= 16, unbatched, A untransposed, no prologue or causal range: B streamed
+                             with 128-bit vector loads, A in LDS, 64-column tiles; NN split over K
+                             (STORE, STORE_BIAS, ADD_RESID, SWIGLU_FWD), NT in one pass (STORE, K up
+                             to about 4000 rows at m <= 4). PXK_TILE_AUTO picks it whenever it applies */
 };
 
 typedef struct pxk_gemm_desc {
@@ -427,14 +431,23 @@ int pxk_decode_rope_append(const float* q, int64_t ldq, const float* k, int64_t 
                            const float* cos_t, const float* sin_t, const int32_t* pos, int64_t n, int64_t heads,
                            int64_t kv_heads, int64_t head_dim, int rope, int rotate_half, void* stream);
 /* ctx (n x heads*head_dim) = softmax(scale q K^T) V over the cached keys 0..*pos (the last `window`
- * of them when window > 0), one workgroup per (sequence, query head); max_keys bounds *pos + 1. */
+ * of them when window > 0); max_keys bounds *pos + 1. Two launches: every (sequence, query head,
+ * 64-key chunk) scores its keys and keeps a max / exp-sum / exp-weighted context partial in the
+ * workspace (pxk_decode_attention_workspace() bytes), then one workgroup per (sequence, head)
+ * merges the partials. */
+size_t pxk_decode_attention_workspace(int64_t n, int64_t heads, int64_t head_dim, int64_t max_keys);
 int pxk_decode_attention(const float* q, const float* k_cache, const float* v_cache, int64_t seq_stride, float* ctx,
                          const int32_t* pos, int64_t n, int64_t heads, int64_t kv_heads, int64_t head_dim,
-                         int64_t window, int64_t max_keys, float scale, void* stream);
+                         int64_t window, int64_t max_keys, float scale, float* workspace, size_t workspace_bytes,
+                         void* stream);
 /* Greedy pick (the first maximum of each sequence's logits row, rows ld_logits apart): ids[b * ld_ids +
- * *pos + 1] and cur[b] get the id, picked_logit[b * ld_logit + *pos + 1] (nullable) its logit. */
+ * *pos + 1] and cur[b] get the id, picked_logit[b * ld_logit + *pos + 1] (nullable) its logit. Two
+ * launches: 64 slices of each row reduced to their first maxima in a 16-byte aligned workspace of
+ * pxk_decode_pick_workspace() bytes, then merged in index order. */
+size_t pxk_decode_pick_workspace(int64_t n);
 int pxk_decode_pick(const float* logits, int64_t ld_logits, int64_t n, int64_t vocab, float* ids, int64_t ld_ids,
-                    float* cur, float* picked_logit, int64_t ld_logit, const int32_t* pos, void* stream);
+                    float* cur, float* picked_logit, int64_t ld_logit, const int32_t* pos, void* workspace,
+                    size_t workspace_bytes, void* stream);
 /* *pos += 1 (one thread). */
 int pxk_decode_advance(int32_t* pos, void* stream);
 /* The LRP seed of one row per sequence (n x vocab, every other entry 0; the explained rows' logits

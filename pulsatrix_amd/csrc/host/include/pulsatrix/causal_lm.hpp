@@ -99,7 +99,7 @@ private:
 
     int64_t N_ = 0, L_ = 0;
     const float* r_embed_ = nullptr;
-    detail::DevBuf ids_, seed_, last_x_, r_top_, prompt_ids_, dec_x_, cur_ids_, pos_, tok_tmp_;
+    detail::DevBuf ids_, seed_, last_x_, r_top_, prompt_ids_, dec_x_, cur_ids_, pos_, tok_tmp_, pick_ws_;
     std::vector<KVCacheState> caches_;
 };
 

@@ -125,7 +125,7 @@ private:
     const float* x_ = nullptr;
     detail::DevBuf x_copy_, qkv_z_, qkv_y_, qk_norm_out_, qk_rot_, raw_, p_, ctx_, out_z_, out_y_;
     detail::DevBuf spv_, ra_, g_, r_in_, rctx_;
-    detail::DevBuf dec_z_, dec_y_, dec_qkn_, dec_q_, dec_ctx_, dec_oz_, dec_oy_;
+    detail::DevBuf dec_z_, dec_y_, dec_qkn_, dec_q_, dec_ctx_, dec_oz_, dec_oy_, dec_ws_;
     detail::AffineRule out_rule_, qkv_rule_;
     Tensor key_rel_, value_rel_;
     bool has_relevance_ = false;

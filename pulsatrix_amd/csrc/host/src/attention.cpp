@@ -298,8 +298,10 @@ const float* MultiHeadAttentionModule::decode_step(const float* x, int64_t n, KV
                          "MultiHeadAttentionModule::decode_step (RoPE, cache)");
     float* ctx = dec_ctx_.ensure(be_, n * qd);
     const int64_t window = config_.causal ? config_.sliding_window : 0;
+    const size_t ws_bytes = pxk_decode_attention_workspace(n, H_, D_, cache.positions);
+    float* ws = dec_ws_.ensure(be_, static_cast<int64_t>(ws_bytes / sizeof(float)));
     MI355XBackend::check(pxk_decode_attention(q, cache.k.data(), cache.v.data(), stride, ctx, pos, n, H_, Hkv_, D_,
-                                              window, cache.positions, score_scale(), st),
+                                              window, cache.positions, score_scale(), ws, ws_bytes, st),
                          "MultiHeadAttentionModule::decode_step (attention)");
     float* oz = dec_oz_.ensure(be_, n * d_);
     float* oy = config_.out_bias ? dec_oy_.ensure(be_, n * d_) : oz;

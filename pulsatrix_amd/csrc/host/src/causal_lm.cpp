@@ -230,8 +230,11 @@ void CausalLM::generate_greedy_device(float* ids, int64_t n, int64_t prompt, int
     const int32_t start = static_cast<int32_t>(prompt - 1);
     be_->copy(pos, &start, sizeof(start), CopyDirection::HostToDevice);
     float* cur = cur_ids_.ensure(be_, n);
+    const size_t pick_bytes = pxk_decode_pick_workspace(n);
+    void* pick_ws = pick_ws_.ensure(be_, static_cast<int64_t>(pick_bytes / sizeof(float)));
     auto pick = [&](const float* lg) {
-        MI355XBackend::check(pxk_decode_pick(lg, V, n, V, ids, ld_ids, cur, picked_logit, ld_ids, pos, st),
+        MI355XBackend::check(pxk_decode_pick(lg, V, n, V, ids, ld_ids, cur, picked_logit, ld_ids, pos, pick_ws,
+                                             pick_bytes, st),
                              "CausalLM::generate (pick)");
         MI355XBackend::check(pxk_decode_advance(pos, st), "CausalLM::generate (advance)");
     };

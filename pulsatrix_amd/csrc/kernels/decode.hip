@@ -71,85 +71,128 @@ struct DecodeAttnArgs {
     const float* v_cache;
     int64_t seq_stride;
     float* ctx;      // (n, H*D) contiguous
+    float* part;     // per (sequence, head, chunk): running max, sum and D partial context values
     const int32_t* pos;
-    int64_t H, Hkv, D, window, max_keys;
+    int64_t H, Hkv, D, window, max_keys, chunks;
     float scale;
+    int vec;  // 128-bit key loads (head_dim, the strides and the bases multiples of 4 floats)
 };
 
-// One workgroup per (sequence, query head): the single query's scores against keys
-// [lo, pos] of the cache (a sliding layer's window, attention_masked row_math.hpp:117-126), the
-// softmax over them (max-subtract, exp, sum, divide: softmax_rows cpu_backend.cpp:292-310) and
-// ctx = P V. Scores live in LDS (max_keys floats, dynamic).
-__global__ void __launch_bounds__(kThreads) decode_attention_kernel(const DecodeAttnArgs a) {
-    extern __shared__ float sm[];
-    float* qs = sm;              // D
-    float* sc = sm + a.D;        // max_keys
-    __shared__ float red[kThreads / kWave];
-    const int64_t b = blockIdx.x / a.H, h = blockIdx.x % a.H, hk = h / (a.H / a.Hkv);
+constexpr int kKeyChunk = 64;  // keys per workgroup of the first pass
+static_assert(kKeyChunk == kWave && kThreads == 4 * kKeyChunk, "a lane per key in the softmax, four threads per key");
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+// First pass, one workgroup per (sequence, query head, 64-key chunk): the chunk's visible keys
+// (within [lo, pos], a sliding layer's window per attention_masked, row_math.hpp:117-126) scored
+// against the query by four threads per key (each on every fourth float4 of head_dim, summed with
+// two shuffles), their max, exp-sum and exp-weighted values. Chunks past the position write an
+// empty partial; the grid is the same at every position, so a step stays capturable.
+__global__ void __launch_bounds__(kThreads) decode_attention_part_kernel(const DecodeAttnArgs a) {
+    extern __shared__ __attribute__((aligned(16))) float sm[];
+    float* qs = sm;        // D
+    float* sc = sm + a.D;  // kKeyChunk
+    const int64_t bh = blockIdx.x / a.chunks, chunk = blockIdx.x - bh * a.chunks;
+    const int64_t b = bh / a.H, h = bh - b * a.H, hk = h / (a.H / a.Hkv);
     const int64_t kvd = a.Hkv * a.D;
-    const int64_t p = min(max(static_cast<int64_t>(*a.pos), int64_t{0}), a.max_keys - 1);  // stays inside the cache
+    const int64_t p = min(max(static_cast<int64_t>(*a.pos), int64_t{0}), a.max_keys - 1);
     const int64_t lo = (a.window > 0 && p + 1 > a.window) ? p + 1 - a.window : 0;
-    const int64_t nkeys = p + 1 - lo;
-    const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+    const int64_t j0 = max(chunk * kKeyChunk, lo), j1 = min(chunk * kKeyChunk + kKeyChunk, p + 1);
+    const int nk = j1 > j0 ? static_cast<int>(j1 - j0) : 0;
+    float* out = a.part + (bh * a.chunks + chunk) * (a.D + 2);
+    const int tid = threadIdx.x;
+    if (nk == 0) {  // nothing visible here
+        for (int64_t d = tid; d < a.D + 2; d += kThreads) out[d] = d == 0 ? -INFINITY : 0.0f;
+        return;
+    }
     for (int64_t d = tid; d < a.D; d += kThreads) qs[d] = a.q[b * a.H * a.D + h * a.D + d];
     __syncthreads();
-    const float* kb = a.k_cache + b * a.seq_stride + hk * a.D;
-    for (int64_t j = wave; j < nkeys; j += kThreads / kWave) {
-        const float* kr = kb + (lo + j) * kvd;
-        float s = 0.0f;
-        for (int64_t d = lane; d < a.D; d += kWave) s += qs[d] * kr[d];
-        s = wave_sum(s);
-        if (lane == 0) sc[j] = a.scale * s;
+    const int key = tid >> 2, quarter = tid & 3;
+    float s = 0.0f;
+    if (key < nk) {
+        const float* kr = a.k_cache + b * a.seq_stride + (j0 + key) * kvd + hk * a.D;
+        if (a.vec) {
+            const int64_t nv = a.D / 4;
+            for (int64_t f = quarter; f < nv; f += 4) {
+                const f4 kv = *reinterpret_cast<const f4*>(kr + 4 * f);
+                const f4 qv = *reinterpret_cast<const f4*>(qs + 4 * f);
+                s += qv[0] * kv[0] + qv[1] * kv[1] + qv[2] * kv[2] + qv[3] * kv[3];
+            }
+        } else {
+            for (int64_t d = quarter; d < a.D; d += 4) s += qs[d] * kr[d];
+        }
+    }
+    s += __shfl_xor(s, 1, kWave);
+    s += __shfl_xor(s, 2, kWave);
+    if (key < nk && quarter == 0) sc[key] = a.scale * s;
+    __syncthreads();
+    if (tid < kWave) {  // kKeyChunk == kWave: one key per lane of the first wave
+        const float v = tid < nk ? sc[tid] : -INFINITY;
+        const float mx = wave_max(v);
+        const float e = tid < nk ? expf(v - mx) : 0.0f;
+        const float sum = wave_sum(e);
+        if (tid < nk) sc[tid] = e;
+        if (tid == 0) {
+            out[0] = mx;
+            out[1] = sum;
+        }
     }
     __syncthreads();
-    float mx = -INFINITY;
-    for (int64_t j = tid; j < nkeys; j += kThreads) mx = fmaxf(mx, sc[j]);
-    mx = wave_max(mx);
-    if (lane == 0) red[wave] = mx;
-    __syncthreads();
-    mx = red[0];
-    for (int w = 1; w < kThreads / kWave; ++w) mx = fmaxf(mx, red[w]);
-    __syncthreads();
-    float sum = 0.0f;
-    for (int64_t j = tid; j < nkeys; j += kThreads) {
-        const float e = expf(sc[j] - mx);
-        sc[j] = e;
-        sum += e;
-    }
-    sum = wave_sum(sum);
-    if (lane == 0) red[wave] = sum;
-    __syncthreads();
-    sum = 0.0f;
-    for (int w = 0; w < kThreads / kWave; ++w) sum += red[w];
-    const float* vb = a.v_cache + b * a.seq_stride + hk * a.D;
+    const float* vb = a.v_cache + b * a.seq_stride + j0 * kvd + hk * a.D;
     for (int64_t d = tid; d < a.D; d += kThreads) {
         float acc = 0.0f;
-        for (int64_t j = 0; j < nkeys; ++j) acc += (sc[j] / sum) * vb[(lo + j) * kvd + d];
-        a.ctx[b * a.H * a.D + h * a.D + d] = acc;
+#pragma unroll 8
+        for (int j = 0; j < nk; ++j) acc += sc[j] * vb[j * kvd + d];
+        out[2 + d] = acc;
     }
 }
 
-constexpr int kPickThreads = 1024;
+// Second pass, one workgroup per (sequence, query head): the chunks' partials merged with their
+// maxima, ctx = sum_c e^(m_c - M) acc_c / sum_c e^(m_c - M) l_c.
+__global__ void __launch_bounds__(kThreads) decode_attention_merge_kernel(const DecodeAttnArgs a) {
+    const int64_t bh = blockIdx.x;
+    const float* part = a.part + bh * a.chunks * (a.D + 2);
+    float M = -INFINITY;
+    for (int64_t c = 0; c < a.chunks; ++c) M = fmaxf(M, part[c * (a.D + 2)]);
+    float l = 0.0f;
+    for (int64_t c = 0; c < a.chunks; ++c) {
+        const float m = part[c * (a.D + 2)];
+        if (m != -INFINITY) l += expf(m - M) * part[c * (a.D + 2) + 1];
+    }
+    for (int64_t d = threadIdx.x; d < a.D; d += kThreads) {
+        float acc = 0.0f;
+        for (int64_t c = 0; c < a.chunks; ++c) {
+            const float m = part[c * (a.D + 2)];
+            if (m != -INFINITY) acc += expf(m - M) * part[c * (a.D + 2) + 2 + d];
+        }
+        a.ctx[bh * a.D + d] = acc / l;
+    }
+}
 
-// Greedy pick per sequence (Generate's greedy step: the first maximum of the logits): one
-// workgroup scans a row, shares merged larger value first and lower index on ties. The pick is
-// written as the sequence's next id (ids[b, pos + 1]), as this step's token (cur[b]) and its logit
-// (picked_logit[b * ld_logit + pos + 1], the OutputValue seed an explanation of it uses).
-__global__ void __launch_bounds__(kPickThreads) decode_pick_kernel(const float* logits, int64_t ld_logits, int64_t V,
-                                                                  float* ids, int64_t ld_ids, float* cur,
-                                                                  float* picked_logit, int64_t ld_logit,
-                                                                  const int32_t* pos) {
-    const int64_t b = blockIdx.x;
-    const float* row = logits + b * ld_logits;
+constexpr int kPickThreads = 256;
+constexpr int kPickSlices = 64;  // workgroups per sequence in the first pass
+
+// The first maximum of a range of a row (ties to the lower index), 8 loads in flight per thread,
+// merged across the workgroup in LDS; `none` is index V.
+__device__ void argmax_range(const float* row, int64_t j0, int64_t j1, int64_t V, float& best, int64_t& idx) {
     __shared__ float bv[kPickThreads];
     __shared__ int64_t bi[kPickThreads];
-    float best = -INFINITY;
-    int64_t idx = V;
-    for (int64_t j = threadIdx.x; j < V; j += kPickThreads) {
-        const float x = row[j];
-        if (idx == V || x > best) {
-            best = x;
-            idx = j;
+    best = -INFINITY;
+    idx = V;
+    constexpr int kAhead = 8;
+    for (int64_t base = j0 + threadIdx.x; base < j1; base += static_cast<int64_t>(kAhead) * kPickThreads) {
+        float v[kAhead];
+#pragma unroll
+        for (int u = 0; u < kAhead; ++u) {
+            const int64_t j = base + static_cast<int64_t>(u) * kPickThreads;
+            v[u] = row[j < j1 ? j : j1 - 1];
+        }
+#pragma unroll
+        for (int u = 0; u < kAhead; ++u) {  // j ascends within a thread: ties keep the first
+            const int64_t j = base + static_cast<int64_t>(u) * kPickThreads;
+            if (j < j1 && (idx == V || v[u] > best)) {
+                best = v[u];
+                idx = j;
+            }
         }
     }
     bv[threadIdx.x] = best;
@@ -166,13 +209,59 @@ __global__ void __launch_bounds__(kPickThreads) decode_pick_kernel(const float* 
         }
         __syncthreads();
     }
+    best = bv[0];
+    idx = bi[0];
+}
+
+struct PickArgs {
+    const float* logits;
+    int64_t ld_logits, V;
+    float* ids;
+    int64_t ld_ids;
+    float* cur;
+    float* picked_logit;
+    int64_t ld_logit;
+    const int32_t* pos;
+    float* part_v;  // (n, kPickSlices) slice maxima and their indices
+    int64_t* part_i;
+};
+
+// Greedy pick (Generate's greedy step: the first maximum of the logits), first pass: one slice of
+// a row per workgroup.
+__global__ void __launch_bounds__(kPickThreads) decode_pick_part_kernel(const PickArgs a) {
+    const int64_t b = blockIdx.y, slice = blockIdx.x;
+    const int64_t len = (a.V + kPickSlices - 1) / kPickSlices;
+    const int64_t j0 = slice * len, j1 = min(a.V, j0 + len);
+    float best;
+    int64_t idx;
+    argmax_range(a.logits + b * a.ld_logits, j0, j1 > j0 ? j1 : j0, a.V, best, idx);
     if (threadIdx.x == 0) {
-        const int64_t next = static_cast<int64_t>(*pos) + 1;
-        const int64_t t = bi[0] < V ? bi[0] : 0;  // a row of NaNs picks id 0 rather than leave the table
-        cur[b] = static_cast<float>(t);
-        if (next >= 0 && next < ld_ids) ids[b * ld_ids + next] = static_cast<float>(t);
-        if (picked_logit && next >= 0 && next < ld_logit) picked_logit[b * ld_logit + next] = bv[0];
+        a.part_v[b * kPickSlices + slice] = best;
+        a.part_i[b * kPickSlices + slice] = idx;
     }
+}
+
+// Second pass: the slices merged in index order (larger value first, the lower index on ties); the
+// pick is written as the sequence's next id (ids[b, pos + 1]), as the next step's token (cur[b]) and
+// with its logit (picked_logit[b, pos + 1], the OutputValue seed an explanation of it uses).
+__global__ void __launch_bounds__(kWave) decode_pick_merge_kernel(const PickArgs a) {
+    const int64_t b = blockIdx.x;
+    if (threadIdx.x != 0) return;
+    float best = -INFINITY;
+    int64_t idx = a.V;
+    for (int s = 0; s < kPickSlices; ++s) {
+        const float v = a.part_v[b * kPickSlices + s];
+        const int64_t i = a.part_i[b * kPickSlices + s];
+        if (i != a.V && (idx == a.V || v > best)) {
+            best = v;
+            idx = i;
+        }
+    }
+    const int64_t next = static_cast<int64_t>(*a.pos) + 1;
+    const int64_t t = idx < a.V ? idx : 0;  // a row of NaNs picks id 0 rather than leave the table
+    a.cur[b] = static_cast<float>(t);
+    if (next >= 0 && next < a.ld_ids) a.ids[b * a.ld_ids + next] = static_cast<float>(t);
+    if (a.picked_logit && next >= 0 && next < a.ld_logit) a.picked_logit[b * a.ld_logit + next] = best;
 }
 
 __global__ void decode_advance_kernel(int32_t* pos) {
@@ -219,33 +308,60 @@ extern "C" int pxk_decode_rope_append(const float* q, int64_t ldq, const float* 
     return launched("pxk_decode_rope_append");
 }
 
+extern "C" size_t pxk_decode_attention_workspace(int64_t n, int64_t heads, int64_t head_dim, int64_t max_keys) {
+    if (n <= 0 || heads <= 0 || head_dim <= 0 || max_keys <= 0) return 0;
+    return static_cast<size_t>(n * heads * cdiv(max_keys, kKeyChunk) * (head_dim + 2)) * sizeof(float);
+}
+
 extern "C" int pxk_decode_attention(const float* q, const float* k_cache, const float* v_cache, int64_t seq_stride,
                                     float* ctx, const int32_t* pos, int64_t n, int64_t heads, int64_t kv_heads,
-                                    int64_t head_dim, int64_t window, int64_t max_keys, float scale, void* stream) {
+                                    int64_t head_dim, int64_t window, int64_t max_keys, float scale, float* workspace,
+                                    size_t workspace_bytes, void* stream) {
     if (n < 0 || heads <= 0 || kv_heads <= 0 || heads % kv_heads != 0 || head_dim <= 0 || window < 0 ||
         max_keys <= 0 || seq_stride < max_keys * kv_heads * head_dim)
         return fail(PXK_ERR_INVALID, "pxk_decode_attention: bad sizes (the cache must hold max_keys positions)");
-    const size_t lds = static_cast<size_t>(head_dim + max_keys) * sizeof(float);
-    if (lds > 60 * 1024)
-        return fail(PXK_ERR_INVALID, "pxk_decode_attention: head_dim + max_keys must fit 60 KiB of LDS");
+    const size_t lds = static_cast<size_t>(head_dim + kKeyChunk) * sizeof(float);
+    if (lds > 60 * 1024) return fail(PXK_ERR_INVALID, "pxk_decode_attention: head_dim must fit LDS");
     if (n == 0) return PXK_OK;
     if (!q || !k_cache || !v_cache || !ctx || !pos) return fail(PXK_ERR_INVALID, "pxk_decode_attention: NULL operand");
-    const DecodeAttnArgs a{q, k_cache, v_cache, seq_stride, ctx, pos, heads, kv_heads, head_dim, window, max_keys, scale};
-    hipLaunchKernelGGL(decode_attention_kernel, dim3(static_cast<unsigned>(n * heads)), dim3(kThreads), lds, S(stream),
-                       a);
-    return launched("pxk_decode_attention");
+    const size_t need = pxk_decode_attention_workspace(n, heads, head_dim, max_keys);
+    if (!workspace || workspace_bytes < need)
+        return fail(PXK_ERR_WORKSPACE, "pxk_decode_attention: needs %zu workspace bytes", need);
+    const int64_t chunks = cdiv(max_keys, kKeyChunk);
+    if (n * heads * chunks > (int64_t{1} << 31) - 1) return fail(PXK_ERR_INVALID, "pxk_decode_attention: too large");
+    const int vec = head_dim % 4 == 0 && seq_stride % 4 == 0 && (reinterpret_cast<uintptr_t>(k_cache) & 15u) == 0;
+    const DecodeAttnArgs a{q,        k_cache, v_cache,  seq_stride, ctx,   workspace, pos, heads,
+                           kv_heads, head_dim, window, max_keys, chunks, scale, vec};
+    hipLaunchKernelGGL(decode_attention_part_kernel, dim3(static_cast<unsigned>(n * heads * chunks)), dim3(kThreads),
+                       lds, S(stream), a);
+    if (const int rc = launched("pxk_decode_attention")) return rc;
+    hipLaunchKernelGGL(decode_attention_merge_kernel, dim3(static_cast<unsigned>(n * heads)), dim3(kThreads), 0,
+                       S(stream), a);
+    return launched("pxk_decode_attention (merge)");
+}
+
+extern "C" size_t pxk_decode_pick_workspace(int64_t n) {
+    return n > 0 ? static_cast<size_t>(n * kPickSlices) * (sizeof(float) + sizeof(int64_t)) : 0;
 }
 
 extern "C" int pxk_decode_pick(const float* logits, int64_t ld_logits, int64_t n, int64_t vocab, float* ids,
                                int64_t ld_ids, float* cur, float* picked_logit, int64_t ld_logit, const int32_t* pos,
-                               void* stream) {
-    if (n < 0 || vocab <= 0 || ld_logits < vocab || ld_ids < 1 || (picked_logit && ld_logit < 1))
+                               void* workspace, size_t workspace_bytes, void* stream) {
+    if (n < 0 || vocab <= 0 || ld_logits < vocab || ld_ids < 1 || (picked_logit && ld_logit < 1) || n > 65535)
         return fail(PXK_ERR_INVALID, "pxk_decode_pick: bad sizes");
     if (n == 0) return PXK_OK;
     if (!logits || !ids || !cur || !pos) return fail(PXK_ERR_INVALID, "pxk_decode_pick: NULL operand");
-    hipLaunchKernelGGL(decode_pick_kernel, dim3(static_cast<unsigned>(n)), dim3(kPickThreads), 0, S(stream), logits,
-                       ld_logits, vocab, ids, ld_ids, cur, picked_logit, ld_logit, pos);
-    return launched("pxk_decode_pick");
+    if (!workspace || workspace_bytes < pxk_decode_pick_workspace(n) || !aligned16(workspace))
+        return fail(PXK_ERR_WORKSPACE, "pxk_decode_pick: needs %zu workspace bytes (16-byte aligned)",
+                    pxk_decode_pick_workspace(n));
+    auto* pi = static_cast<int64_t*>(workspace);
+    auto* pv = reinterpret_cast<float*>(pi + n * kPickSlices);
+    const PickArgs a{logits, ld_logits, vocab, ids, ld_ids, cur, picked_logit, ld_logit, pos, pv, pi};
+    hipLaunchKernelGGL(decode_pick_part_kernel, dim3(kPickSlices, static_cast<unsigned>(n)), dim3(kPickThreads), 0,
+                       S(stream), a);
+    if (const int rc = launched("pxk_decode_pick")) return rc;
+    hipLaunchKernelGGL(decode_pick_merge_kernel, dim3(static_cast<unsigned>(n)), dim3(kWave), 0, S(stream), a);
+    return launched("pxk_decode_pick (merge)");
 }
 
 extern "C" int pxk_decode_advance(int32_t* pos, void* stream) {

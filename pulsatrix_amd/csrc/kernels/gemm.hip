@@ -59,6 +59,7 @@ struct Args {
     int tiles_m, tiles_n, bm;
     int remap;  // XCD-grouped block order
     float* ws;
+    int64_t kc;  // skinny path: K rows per split
 };
 
 // Batch and group counts fit 32 bits (the host checks the grid), so the index splits use 32-bit
@@ -844,6 +845,171 @@ __global__ void __launch_bounds__(NT) splitk_reduce_kernel(const Args g) {
     epilogue_rows<RS, BN, EPI, NT>(Cs, LDC, m0, n0, b, g);
 }
 
+// ---- skinny M: up to 16 rows against a wide weight (decode steps, last-row heads) --------------------
+// MFMA tiles of 32 or more rows waste most of their work on a handful of rows, and the launch is
+// bound by streaming B from HBM anyway, so these kernels stream B with 128-bit loads on the vector
+// ALUs and keep the few A rows in LDS. Both end in the tile epilogue.
+constexpr int kSkinnyBN = 64;  // NT column tile
+constexpr int kSkinnyLDC = kSkinnyBN + 4;
+constexpr int kSkinnyRows = 8;  // B rows per thread per chunk (NN)
+
+// NN (B is K x N, N-contiguous): a workgroup owns W = 4 TX columns and the K range of one split,
+// walked in chunks of CH = TY * 8 rows. Thread (ty, tx) = (tid / TX, tid % TX) accumulates columns
+// 4 tx .. 4 tx + 3 over rows kb + ty + TY i of each chunk from the chunk's A columns in LDS; the
+// next chunk's B and A loads are in flight while the current one is multiplied. The TY partial sums
+// of a column are added in ty order. One split runs the epilogue; several write their partials to
+// the workspace for splitk_reduce_kernel<W, EPI>.
+template <int MB, int TX, int EPI>
+__global__ void __launch_bounds__(NT) skinny_nn_kernel(const Args g) {
+    constexpr int TY = NT / TX, W = 4 * TX, CH = TY * kSkinnyRows, LDC = W + 4;
+    constexpr int AU = MB * CH / NT;  // A values each thread stages per chunk
+    __shared__ __attribute__((aligned(16))) float As[MB * CH];
+    __shared__ __attribute__((aligned(16))) float Ps[TY * 4 * W];
+    __shared__ __attribute__((aligned(16))) float Cs[MB * LDC];
+    const int tid = threadIdx.x, tx = tid % TX, ty = tid / TX;
+    const int64_t tile = blockIdx.x % g.tiles_n, split = blockIdx.x / g.tiles_n;
+    const int64_t n0 = tile * W, n = n0 + 4 * tx;
+    const int64_t k0 = split * g.kc, k1 = min(g.K, k0 + g.kc);
+    const int cnt = n < g.N ? (g.N - n < 4 ? static_cast<int>(g.N - n) : 4) : 0;
+    const bool vec = g.vec_b && cnt == 4;
+    const float* B = g.b.p;
+    const float* A = g.a.p;
+    auto load = [&](f4* bv, float* av, int64_t kb) {
+#pragma unroll
+        for (int r = 0; r < kSkinnyRows; ++r) {
+            const int64_t k = kb + ty + TY * r;
+            bv[r] = (k < k1 && cnt > 0) ? ld4(B + k * g.b.ld + n, vec, cnt) : f4{0.f, 0.f, 0.f, 0.f};
+        }
+#pragma unroll
+        for (int u = 0; u < AU; ++u) {
+            const int i = tid + NT * u, m = i / CH;
+            const int64_t k = kb + (i - m * CH);
+            av[u] = (m < g.M && k < k1) ? A[m * g.a.ld + k] : 0.0f;
+        }
+    };
+    f4 cur[kSkinnyRows], nxt[kSkinnyRows];
+    float acur[AU], anxt[AU];
+    load(cur, acur, k0);
+    float acc[MB][4];
+#pragma unroll
+    for (int m = 0; m < MB; ++m)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[m][j] = 0.0f;
+    for (int64_t kb = k0; kb < k1; kb += CH) {
+        const bool more = kb + CH < k1;
+        if (more) load(nxt, anxt, kb + CH);
+        __syncthreads();  // the previous chunk's A is consumed
+#pragma unroll
+        for (int u = 0; u < AU; ++u) As[tid + NT * u] = acur[u];
+        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < kSkinnyRows; ++r) {
+#pragma unroll
+            for (int m = 0; m < MB; ++m) {
+                const float a = As[m * CH + ty + TY * r];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[m][j] += a * cur[r][j];
+            }
+        }
+        if (more) {
+#pragma unroll
+            for (int r = 0; r < kSkinnyRows; ++r) cur[r] = nxt[r];
+#pragma unroll
+            for (int u = 0; u < AU; ++u) acur[u] = anxt[u];
+        }
+    }
+    // Sum the TY row-lane partials of each column in ty order, four rows of M at a time.
+    for (int mg = 0; mg < MB; mg += 4) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            *reinterpret_cast<f4*>(Ps + (ty * 4 + r) * W + 4 * tx) =
+                f4{acc[mg + r][0], acc[mg + r][1], acc[mg + r][2], acc[mg + r][3]};
+        __syncthreads();
+        for (int o = tid; o < 4 * W; o += NT) {
+            const int rr = o / W, cc = o - rr * W;
+            float v = 0.0f;
+#pragma unroll 8
+            for (int t = 0; t < TY; ++t) v += Ps[(t * 4 + rr) * W + cc];
+            Cs[(mg + rr) * LDC + cc] = v;
+        }
+        __syncthreads();
+    }
+    if (g.splits == 1) {
+        epilogue_rows<MB, W, EPI, NT>(Cs, LDC, 0, n0, 0, g);
+        return;
+    }
+    const int64_t plane = g.M * g.N;
+    for (int i = tid; i < MB * W; i += NT) {
+        const int m = i / W, c = i - m * W;
+        if (m < g.M && n0 + c < g.N) g.ws[split * plane + m * g.N + n0 + c] = Cs[m * LDC + c];
+    }
+}
+
+// NT (B is N x K, K-contiguous: a tied head's table): a workgroup owns 64 columns; each 16-lane
+// group takes four of them (group + 16 c) and walks K in float4 steps, lane l at 4 l + 64 i, so a
+// group streams 256 contiguous bytes of each column's row per step. A (MB x K) sits in LDS.
+// The 16 lane sums are combined with xor shuffles inside the group.
+template <int MB, int EPI>
+__global__ void __launch_bounds__(NT) skinny_nt_kernel(const Args g) {
+    extern __shared__ __attribute__((aligned(16))) float smem[];
+    float* As = smem;                         // MB x kpad
+    float* Cs = smem + MB * g.kc;             // MB x kSkinnyLDC (kc = K rounded up to 64 here)
+    const int tid = threadIdx.x, lane = tid & 15, grp = tid >> 4;
+    const int64_t n0 = static_cast<int64_t>(blockIdx.x) * kSkinnyBN;
+    const int64_t kp = g.kc;
+    const int kpi = static_cast<int>(kp);  // at most 16K floats of LDS
+    for (int i = tid; i < MB * kpi; i += NT) {
+        const int m = i / kpi, k = i - m * kpi;
+        As[i] = (m < g.M && k < g.K) ? g.a.p[m * g.a.ld + k] : 0.0f;
+    }
+    __syncthreads();
+    const float* B = g.b.p;
+    float acc[4][MB];
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int m = 0; m < MB; ++m) acc[c][m] = 0.0f;
+    const float* rows[4];
+    bool live[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const int64_t n = n0 + grp + 16 * c;
+        live[c] = n < g.N;
+        rows[c] = B + (live[c] ? n : 0) * g.b.ld;
+    }
+    for (int64_t k = 4 * lane; k < kp; k += 64) {
+        const int cnt = g.K - k >= 4 ? 4 : (g.K > k ? static_cast<int>(g.K - k) : 0);
+        const bool vec = g.vec_b && cnt == 4;
+        f4 bv[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) bv[c] = (live[c] && cnt > 0) ? ld4(rows[c] + k, vec, cnt) : f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int m = 0; m < MB; ++m) {
+            const f4 av = *reinterpret_cast<const f4*>(As + m * kp + k);
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+                acc[c][m] += av[0] * bv[c][0] + av[1] * bv[c][1] + av[2] * bv[c][2] + av[3] * bv[c][3];
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int m = 0; m < MB; ++m) {
+            float v = acc[c][m];
+#pragma unroll
+            for (int o = 8; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+            acc[c][m] = v;
+        }
+    if (lane == 0) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+            for (int m = 0; m < MB; ++m) Cs[m * kSkinnyLDC + grp + 16 * c] = acc[c][m];
+    }
+    __syncthreads();
+    epilogue_rows<MB, kSkinnyBN, EPI, NT>(Cs, kSkinnyLDC, 0, n0, 0, g);
+}
+
 // ---- host side --------------------------------------------------------------------------------
 
 using KernelFn = void (*)(const Args);
@@ -917,6 +1083,57 @@ const TileInfo kTileInfo[kTiles] = {
     {32, 32, 64, C32::NT, 4 * C32::KS * 32 * C32::LDC, 0.65, 0.5},
 };
 
+// The skinny kernels built: B layout, epilogue, kernels for up to 4, 8 and 16 rows (NN: with 64-,
+// 32- and 16-column tiles), and the split reductions of the NN ones.
+struct SkinnyEntry {
+    int tb, epi;
+    KernelFn k[3][3];  // [rows 4, 8, 16][NN: 64, 32, 16 columns; NT: 64]
+    KernelFn r[3];
+};
+
+#define PXK_SKINNY_NN_W(MB, EPI) {skinny_nn_kernel<MB, 16, EPI>, skinny_nn_kernel<MB, 8, EPI>, skinny_nn_kernel<MB, 4, EPI>}
+#define PXK_SKINNY_NN(EPI)                                                                                        \
+    SkinnyEntry {                                                                                                 \
+        0, EPI, {PXK_SKINNY_NN_W(4, EPI), PXK_SKINNY_NN_W(8, EPI), PXK_SKINNY_NN_W(16, EPI)},                    \
+            {splitk_reduce_kernel<64, EPI>, splitk_reduce_kernel<32, EPI>, splitk_reduce_kernel<16, EPI>}         \
+    }
+
+const SkinnyEntry kSkinny[] = {
+    PXK_SKINNY_NN(PXK_EPI_STORE),
+    PXK_SKINNY_NN(PXK_EPI_STORE_BIAS),
+    PXK_SKINNY_NN(PXK_EPI_ADD_RESID),
+    PXK_SKINNY_NN(PXK_EPI_SWIGLU_FWD),
+    SkinnyEntry{1,
+                PXK_EPI_STORE,
+                {{skinny_nt_kernel<4, PXK_EPI_STORE>}, {skinny_nt_kernel<8, PXK_EPI_STORE>}, {skinny_nt_kernel<16, PXK_EPI_STORE>}},
+                {nullptr, nullptr, nullptr}},
+};
+
+constexpr int kSkinnyTile = kTiles;  // plan index of PXK_TILE_SKINNY
+constexpr int kSkinnyMaxLds = 64 * 1024;
+
+int skinny_mb(int64_t m) { return m <= 4 ? 4 : (m <= 8 ? 8 : 16); }
+
+// The NT kernel's LDS: A (MB x K rounded up to 64) and the MB x 68 output tile.
+size_t skinny_nt_lds(const pxk_gemm_desc* d) {
+    const int64_t mb = skinny_mb(d->m), kp = cdiv(d->k, 64) * 64;
+    return static_cast<size_t>(mb * kp + mb * kSkinnyLDC) * sizeof(float);
+}
+
+// Whether the descriptor is one the skinny kernels compute: up to 16 rows of an unbatched,
+// untransposed A, no prologue or causal range, one of the built (layout, epilogue) pairs.
+const SkinnyEntry* skinny_entry(const pxk_gemm_desc* d) {
+    if (d->m > 16 || d->k <= 0 || d->batch != 1 || d->kgroups != 1 || d->causal != PXK_CAUSAL_NONE ||
+        d->prologue != PXK_PRO_NONE || d->trans_a != 0)
+        return nullptr;
+    for (const SkinnyEntry& e : kSkinny)
+        if (e.tb == (d->trans_b != 0) && e.epi == d->epilogue) {
+            if (e.tb && (d->splits > 1 || skinny_nt_lds(d) > kSkinnyMaxLds)) return nullptr;
+            return &e;
+        }
+    return nullptr;
+}
+
 const Entry* find_entry(int ta, int tb, int pro, int epi) {
     for (const Entry& e : kTable)
         if (e.ta == ta && e.tb == tb && e.pro == pro && e.epi == epi) return &e;
@@ -935,8 +1152,11 @@ bool vec_ok(const pxk_operand& o, int64_t contiguous_extent) {
 
 struct Plan {
     const Entry* e;
+    const SkinnyEntry* skinny;  // set when tile == kSkinnyTile
     int tile, splits;
     int64_t tiles_m, tiles_n;
+    int64_t kc;  // skinny NN: K rows per split; skinny NT: K rounded up to 64
+    int width;   // skinny: columns per workgroup
 };
 
 bool rope_fits(const pxk_gemm_desc* d, int bn) {
@@ -991,7 +1211,8 @@ int plan(const pxk_gemm_desc* d, Plan* p) {
     if (d->k < 0 || d->inner <= 0 || d->kgroups <= 0 || d->batch % d->inner != 0)
         return fail(PXK_ERR_INVALID, "pxk_gemm: bad k, inner or kgroups (batch must be a multiple of inner)");
     if (d->causal < 0 || d->causal > 3) return fail(PXK_ERR_INVALID, "pxk_gemm: unknown causal mode %d", d->causal);
-    if (d->tile < 0 || d->tile > kTiles) return fail(PXK_ERR_INVALID, "pxk_gemm: unknown tile %d", d->tile);
+    if (d->tile < 0 || d->tile > kTiles + 1) return fail(PXK_ERR_INVALID, "pxk_gemm: unknown tile %d", d->tile);
+    const TileInfo* forced = d->tile > 0 && d->tile <= kTiles ? &kTileInfo[d->tile - 1] : nullptr;
     if (d->splits < 0 || d->splits > 4096) return fail(PXK_ERR_INVALID, "pxk_gemm: bad split count %d", d->splits);
     p->e = find_entry(d->trans_a != 0, d->trans_b != 0, d->prologue, d->epilogue);
     if (!p->e)
@@ -1026,7 +1247,7 @@ int plan(const pxk_gemm_desc* d, Plan* p) {
     if (epi == PXK_EPI_SWIGLU_FWD) {
         if (d->n % 64 != 0 || d->c2.ptr == nullptr || d->c3.ptr == nullptr || d->e_bias.ptr != nullptr)
             return fail(PXK_ERR_INVALID, "pxk_gemm: SWIGLU_FWD needs n a multiple of 64, C2 and C3, and no bias");
-        if (d->tile > 0 && kTileInfo[d->tile - 1].bn % 64 != 0)
+        if (forced && forced->bn % 64 != 0)
             return fail(PXK_ERR_INVALID, "pxk_gemm: SWIGLU_FWD needs 64-wide tile multiples (tile %d)", d->tile);
     }
     if (epi == PXK_EPI_ROPE_FWD) {
@@ -1037,7 +1258,7 @@ int plan(const pxk_gemm_desc* d, Plan* p) {
             return fail(PXK_ERR_INVALID, "pxk_gemm: ROPE_FWD rotates whole heads: rope_cols and n multiples of head_dim");
         if (!rope_fits(d, 128))
             return fail(PXK_ERR_INVALID, "pxk_gemm: ROPE_FWD needs whole heads inside a 128-wide tile");
-        if (d->tile > 0 && !rope_fits(d, kTileInfo[d->tile - 1].bn))
+        if (forced && !rope_fits(d, forced->bn))
             return fail(PXK_ERR_INVALID, "pxk_gemm: ROPE_FWD heads do not fit tile %d", d->tile);
     }
     if (epi == PXK_EPI_ROPE_REL) {
@@ -1048,11 +1269,43 @@ int plan(const pxk_gemm_desc* d, Plan* p) {
             return fail(PXK_ERR_INVALID, "pxk_gemm: ROPE_REL needs n to be a whole number of heads");
         if (!rope_fits(d, 128))
             return fail(PXK_ERR_INVALID, "pxk_gemm: ROPE_REL needs whole heads inside a 128-wide tile");
-        if (d->tile > 0 && !rope_fits(d, kTileInfo[d->tile - 1].bn))
+        if (forced && !rope_fits(d, forced->bn))
             return fail(PXK_ERR_INVALID, "pxk_gemm: ROPE_REL heads do not fit tile %d", d->tile);
     }
     if (d->k > (int64_t{1} << 40) || static_cast<double>(d->k) * d->kgroups / 32.0 > 2.0e9 || d->batch > (int64_t{1} << 31))
         return fail(PXK_ERR_INVALID, "pxk_gemm: k * kgroups or batch too large");
+
+    // Up to 16 rows: the skinny kernels. NN: the widest column tile that still gives 160 workgroups
+    // (64 columns for the SwiGLU gate, whose gate and up blocks interleave in 64s), and no split over
+    // K unless a workgroup would stream more than 1 MiB of B.
+    p->skinny = nullptr;
+    if (d->tile == 0 || d->tile == kSkinnyTile + 1) {
+        if (const SkinnyEntry* se = skinny_entry(d)) {
+            p->skinny = se;
+            p->tile = kSkinnyTile;
+            p->tiles_m = 1;
+            if (se->tb) {
+                p->width = kSkinnyBN;
+                p->splits = 1;
+                p->kc = cdiv(d->k, 64) * 64;
+            } else {
+                p->width = 64;
+                if (epi != PXK_EPI_SWIGLU_FWD)
+                    while (p->width > 16 && cdiv(d->n, p->width) < 160) p->width /= 2;
+                const int64_t s = d->splits > 0 ? d->splits : cdiv(d->k * p->width * 4, int64_t{1} << 20);
+                p->kc = cdiv(cdiv(d->k, s), 16) * 16;
+                p->splits = static_cast<int>(cdiv(d->k, p->kc));
+            }
+            p->tiles_n = cdiv(d->n, p->width);
+            if (p->tiles_n * p->splits > (int64_t{1} << 31) - 1) return fail(PXK_ERR_INVALID, "pxk_gemm: grid too large");
+            return PXK_OK;
+        }
+        if (d->tile == kSkinnyTile + 1)
+            return fail(PXK_ERR_INVALID,
+                        "pxk_gemm: the skinny tile needs m <= 16, batch 1, no prologue or causal range, A untransposed "
+                        "and a built epilogue (STORE, STORE_BIAS, ADD_RESID, SWIGLU_FWD; NT: STORE, K up to the LDS)");
+    }
+    p->kc = 0;
 
     // Tile shape and split count: the forced ones, else the cheapest by estimate().
     int best_t = -1, best_s = 1;
@@ -1176,6 +1429,22 @@ extern "C" int pxk_gemm(const pxk_gemm_desc* d, void* stream) {
               (d->epilogue == PXK_EPI_ROPE_REL || d->epilogue == PXK_EPI_VALUE_REL ? vec_ok(d->z, d->n) : true);
     g.tiles_m = static_cast<int>(p.tiles_m);
     g.tiles_n = static_cast<int>(p.tiles_n);
+    g.kc = p.kc;
+    if (p.skinny) {
+        const int mi = d->m <= 4 ? 0 : (d->m <= 8 ? 1 : 2);
+        const int wi = p.width == 64 ? 0 : (p.width == 32 ? 1 : 2);
+        g.bm = 16;
+        const size_t lds = p.skinny->tb ? skinny_nt_lds(d) : 0;
+        hipLaunchKernelGGL(p.skinny->k[mi][p.skinny->tb ? 0 : wi], dim3(static_cast<unsigned>(p.tiles_n * p.splits)),
+                           dim3(NT), lds, S(stream), g);
+        if (const int rc = launched("pxk_gemm (skinny)")) return rc;
+        if (p.splits > 1) {
+            const dim3 rgrid(static_cast<unsigned>(p.tiles_n), 1, 1);  // at least 16 rows per reduce workgroup
+            hipLaunchKernelGGL(p.skinny->r[wi], rgrid, dim3(NT), 0, S(stream), g);
+            return launched("pxk_gemm (skinny split-K reduce)");
+        }
+        return PXK_OK;
+    }
     g.bm = kTileInfo[p.tile].bm;
     const int64_t blocks = p.tiles_m * p.tiles_n * d->batch * p.splits;
     g.remap = blocks % 8 == 0;
