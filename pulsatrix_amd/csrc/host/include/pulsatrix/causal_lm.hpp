@@ -65,8 +65,10 @@ public:
     /** @brief AttnLRP of each generated token: token t (at column prompt + t) explained through a
      *         forward over its prefix (columns 0 .. prompt + t - 1), seeded with its id at the
      *         prefix's last row (explain_rows_device), as the reference explains a cached generation
-     *         (forward_cached keeps no relevance state). token_relevance (new_tokens, n, W) in HBM with
-     *         W = prompt + new_tokens - 1, zero past each prefix. */
+     *         (forward_cached keeps no relevance state). Consecutive tokens share one pass over the
+     *         longest of their prefixes, each seeded at its own row (a causal model's row sees no
+     *         later row). token_relevance (new_tokens, n, W) in HBM with W = prompt + new_tokens - 1,
+     *         zero past each prefix. */
     void explain_generated_device(const float* ids, int64_t n, int64_t prompt, int64_t new_tokens, int64_t ld_ids,
                                   const LRPRuleConfig& config, float* token_relevance, bool unit_seed = false);
     /** @brief Whether every id of the last device-side pass was in [0, vocab) (waits for the
@@ -95,6 +97,11 @@ private:
     std::unique_ptr<LinearModule> lm_head_;
     /** @brief Layers, final norm and the head on the last row of each sequence: (n, vocab) logits. */
     const float* forward_last_rows(const float* ids, int64_t n, int64_t l);
+    /** @brief explain_rows_device over groups * n sequences of length l (sequence g * n + b),
+     *         seeded at row l - groups + g with the id targets[g + b * target_stride]. */
+    void explain_staggered_rows(const float* ids, int64_t n, int64_t groups, int64_t l, const float* targets,
+                                int64_t target_stride, const LRPRuleConfig& config, float* token_relevance,
+                                int64_t* targets_out, bool unit_seed);
     const float* run_forward_hidden(const float* ids, int64_t n, int64_t l);
 
     int64_t N_ = 0, L_ = 0;

@@ -3,6 +3,7 @@
 
 #include <hip/hip_runtime_api.h>
 
+#include <algorithm>
 #include <cmath>
 #include <stdexcept>
 #include <string>
@@ -182,19 +183,34 @@ void CausalLM::explain_rows_device(const float* ids, int64_t n, int64_t l, const
                                    const LRPRuleConfig& config, float* token_relevance, int64_t* targets_out,
                                    bool unit_seed) {
     if (n <= 0 || l <= 0) throw std::invalid_argument("CausalLM::explain_rows_device: n and l must be positive");
-    const int64_t V = config_.vocab_size, d = config_.hidden_size, M = n * l;
+    explain_staggered_rows(ids, n, 1, l, targets, target_stride, config, token_relevance, targets_out, unit_seed);
+}
+
+void CausalLM::explain_staggered_rows(const float* ids, int64_t n, int64_t groups, int64_t l, const float* targets,
+                                      int64_t target_stride, const LRPRuleConfig& config, float* token_relevance,
+                                      int64_t* targets_out, bool unit_seed) {
+    const int64_t V = config_.vocab_size, d = config_.hidden_size, S = groups * n, M = S * l;
     void* st = be_->stream();
-    const float* logits = forward_last_rows(ids, n, l);
-    float* seed = seed_.ensure(be_, n * V);
-    MI355XBackend::check(pxk_seed_rows(logits, V, targets, target_stride, n, V, seed, targets_out, unit_seed, st),
-                         "CausalLM::explain_rows_device (seed)");
-    // The head's rule on the n seeded rows, then those rows' relevance placed at each sequence's last
-    // row of the stack's output (every other row's is zero, as the dense pass computes it).
+    // Layers and final norm over every row; the head on the seeded row of each sequence only.
+    const float* xn = run_forward_hidden(ids, S, l);
+    float* xl = last_x_.ensure(be_, S * d);
+    for (int64_t g = 0; g < groups; ++g)
+        be_->copy_2d(xl + g * n * d, static_cast<size_t>(d), xn + (g * n * l + l - groups + g) * d,
+                     static_cast<size_t>(l * d), static_cast<size_t>(n), static_cast<size_t>(d));
+    const float* logits = tied_head_ ? tied_head_->run_forward(xl, S) : lm_head_->run_forward(xl, S);
+    float* seed = seed_.ensure(be_, S * V);
+    for (int64_t g = 0; g < groups; ++g)
+        MI355XBackend::check(pxk_seed_rows(logits + g * n * V, V, targets + g, target_stride, n, V, seed + g * n * V,
+                                           targets_out ? targets_out + g * n : nullptr, unit_seed, st),
+                             "CausalLM::explain_rows_device (seed)");
+    // The head's rule on the seeded rows, then those rows' relevance placed at their rows of the
+    // stack's output (every other row's is zero, as the dense pass computes it).
     const float* rl = tied_head_ ? tied_head_->run_relevance(seed, config) : lm_head_->run_relevance(seed, config);
     float* rtop = r_top_.ensure(be_, M * d);
     MI355XBackend::check(pxk_fill(rtop, 0.0f, M * d, st), "CausalLM::explain_rows_device");
-    be_->copy_2d(rtop + (l - 1) * d, static_cast<size_t>(l * d), rl, static_cast<size_t>(d), static_cast<size_t>(n),
-                 static_cast<size_t>(d));
+    for (int64_t g = 0; g < groups; ++g)
+        be_->copy_2d(rtop + (g * n * l + l - groups + g) * d, static_cast<size_t>(l * d), rl + g * n * d,
+                     static_cast<size_t>(d), static_cast<size_t>(n), static_cast<size_t>(d));
     const float* r = rtop;
     if (!layers_.empty()) {  // the final RMSNorm passes relevance unchanged
         const detail::ResidualSplit top = layers_.back()->output_split();
@@ -289,18 +305,31 @@ void CausalLM::explain_generated_device(const float* ids, int64_t n, int64_t pro
         throw std::invalid_argument("CausalLM::explain_generated_device: bad sizes");
     const int64_t W = prompt + new_tokens - 1;
     void* st = be_->stream();
-    // Longest prefix first: its buffers then serve every shorter one at the same addresses.
-    for (int64_t t = new_tokens - 1; t >= 0; --t) {
-        const int64_t l = prompt + t;
-        float* pid = prompt_ids_.ensure(be_, n * l);
-        be_->copy_2d(pid, static_cast<size_t>(l), ids, static_cast<size_t>(ld_ids), static_cast<size_t>(n),
-                     static_cast<size_t>(l));
-        float* tmp = tok_tmp_.ensure(be_, n * l);
-        explain_rows_device(pid, n, l, ids + l, ld_ids, config, tmp, nullptr, unit_seed);
-        float* out = token_relevance + t * n * W;
-        MI355XBackend::check(pxk_fill(out, 0.0f, n * W, st), "CausalLM::explain_generated_device");
-        be_->copy_2d(out, static_cast<size_t>(W), tmp, static_cast<size_t>(l), static_cast<size_t>(n),
-                     static_cast<size_t>(l));
+    // Tokens t0 .. t1 go through one pass as G = t1 - t0 + 1 copies of the longest prefix (columns
+    // 0 .. prompt + t1 - 1), copy g seeded at row prompt + t0 + g - 1 with the id that followed it.
+    // The model is causal, so a row sees nothing after it and the relevance of a row seeded there
+    // reaches no later row: copy g's relevance over its own prefix is that of the pass over the
+    // prefix alone (the later rows carry zero). Groups hold about kExplainRows rows; the longest
+    // comes first, so its buffers serve every later group at the same addresses.
+    constexpr int64_t kExplainRows = 8192, kMaxGroup = 16;
+    for (int64_t t1 = new_tokens - 1; t1 >= 0;) {
+        const int64_t l = prompt + t1;
+        const int64_t G = std::max<int64_t>(1, std::min<int64_t>({t1 + 1, kMaxGroup, kExplainRows / (n * l)}));
+        const int64_t t0 = t1 - G + 1;
+        float* pid = prompt_ids_.ensure(be_, G * n * l);
+        for (int64_t g = 0; g < G; ++g)
+            be_->copy_2d(pid + g * n * l, static_cast<size_t>(l), ids, static_cast<size_t>(ld_ids),
+                         static_cast<size_t>(n), static_cast<size_t>(l));
+        float* tmp = tok_tmp_.ensure(be_, G * n * l);
+        explain_staggered_rows(pid, n, G, l, ids + (l - G + 1), ld_ids, config, tmp, nullptr, unit_seed);
+        for (int64_t g = 0; g < G; ++g) {
+            const int64_t t = t0 + g, lt = prompt + t;
+            float* out = token_relevance + t * n * W;
+            MI355XBackend::check(pxk_fill(out, 0.0f, n * W, st), "CausalLM::explain_generated_device");
+            be_->copy_2d(out, static_cast<size_t>(W), tmp + g * n * l, static_cast<size_t>(l), static_cast<size_t>(n),
+                         static_cast<size_t>(lt));
+        }
+        t1 = t0 - 1;
     }
 }
 
