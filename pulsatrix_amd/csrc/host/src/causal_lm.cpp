@@ -309,12 +309,14 @@ void CausalLM::explain_generated_device(const float* ids, int64_t n, int64_t pro
     // 0 .. prompt + t1 - 1), copy g seeded at row prompt + t0 + g - 1 with the id that followed it.
     // The model is causal, so a row sees nothing after it and the relevance of a row seeded there
     // reaches no later row: copy g's relevance over its own prefix is that of the pass over the
-    // prefix alone (the later rows carry zero). Groups hold about kExplainRows rows; the longest
-    // comes first, so its buffers serve every later group at the same addresses.
-    constexpr int64_t kExplainRows = 8192, kMaxGroup = 16;
+    // prefix alone (the later rows carry zero). Groups hold up to 16384 rows (fewer for models wider
+    // than 1024, so the pass's activations stay a few GiB); the longest comes first, so its buffers
+    // serve every later group at the same addresses.
+    constexpr int64_t kMaxGroup = 32;
+    const int64_t rows = std::clamp<int64_t>(16384 * 1024 / std::max<int64_t>(1, config_.hidden_size), 1024, 16384);
     for (int64_t t1 = new_tokens - 1; t1 >= 0;) {
         const int64_t l = prompt + t1;
-        const int64_t G = std::max<int64_t>(1, std::min<int64_t>({t1 + 1, kMaxGroup, kExplainRows / (n * l)}));
+        const int64_t G = std::max<int64_t>(1, std::min<int64_t>({t1 + 1, kMaxGroup, rows / (n * l)}));
         const int64_t t0 = t1 - G + 1;
         float* pid = prompt_ids_.ensure(be_, G * n * l);
         for (int64_t g = 0; g < G; ++g)
