@@ -185,6 +185,23 @@ def head_relevance_gemm(torch, N, c, L):
     return desc, 2.0 * L * V * d, keep
 
 
+def decode_head_gemm(torch, N, c, n):
+    """The tied head of a decode step as TiedLMHeadModule::run_forward launches it: logits (n x V) =
+    h (n x d) E^T with E stored (V, d), the skinny NT kernel."""
+    V, d = c["vocab_size"], c["hidden_size"]
+    g = torch.Generator(device="cuda").manual_seed(3)
+    H = torch.randn(n, d, device="cuda", generator=g)
+    E = torch.randn(V, d, device="cuda", generator=g) * 0.02
+    out = torch.empty(n, V, device="cuda")
+    desc = N.GemmDesc()
+    desc.m, desc.n, desc.k, desc.batch, desc.inner, desc.kgroups = n, V, d, 1, 1, 1
+    desc.trans_b = 1
+    desc.a = N.operand(H.data_ptr(), d)
+    desc.b = N.operand(E.data_ptr(), d)
+    desc.c = N.operand(out.data_ptr(), V)
+    return desc, 4.0 * (V * d + n * d + n * V), (H, E, out)
+
+
 def mlp_gate_up_gemm(torch, N, c, L):
     """The MLP's [gate | up] forward GEMM as SwiGLUModule::run_forward launches it (L x d x 2F)."""
     d, F = c["hidden_size"], c["intermediate_size"]
@@ -383,6 +400,24 @@ def decode_bench(args, torch, N, models):
         "explained_tokens_per_s": round(n * T / exp_s, 1),
         "setup_s": round(setup_s, 1),
     }
+    # ---- roofline: the decode step's largest launch, the tied head over the vocabulary ------------
+    desc, nbytes, keep = decode_head_gemm(torch, N, GEMMA_270M, n)
+    ker_s = time_kernel(torch, stream, lambda: N.gemm(desc, models.stream()), 20)
+    assert N.gemm_plan(desc) == (N.TILE_SKINNY, 1)
+    achieved = nbytes / ker_s / 1e9
+    out["roofline"] = {
+        "kernel": "pxk_gemm NT skinny (decode-step tied head %d x %d x %d: skinny_nt_kernel)" %
+                  (n, GEMMA_270M["hidden_size"], GEMMA_270M["vocab_size"]),
+        "bound": "hbm",
+        "achieved": round(achieved, 1),
+        "peak": HBM_PEAK_GBS,
+        "unit": "GB/s",
+        "frac": round(achieved / HBM_PEAK_GBS, 4),
+        "traffic": None,
+        "avg_launch_us": round(ker_s * 1e6, 2),
+        "algorithmic_bytes_per_launch": int(nbytes),
+    }
+    del keep
     if not args.no_cpu_baseline:
         # One explanation at the generation's mean prefix length (the bulk of the job), 1 sequence.
         mean_prefix = p + T // 2
@@ -491,7 +526,7 @@ def main():
     achieved = flops / ker_s / 1e12
     tile, splits = N.gemm_plan(desc)
     tile_name = {N.TILE_128x128: "128x128", N.TILE_64x64: "64x64", N.TILE_32x64: "32x64", N.TILE_32x32: "32x32",
-                 N.TILE_32x64_DIRECT: "32x64 direct", N.TILE_32x32_DIRECT: "32x32 direct"}[tile]
+                 N.TILE_32x64_DIRECT: "32x64 direct", N.TILE_32x32_DIRECT: "32x32 direct", N.TILE_SKINNY: "skinny"}[tile]
 
     rule_text = {"lxt": "LxtAttnLrpConfig: eps 1e-9, bias in denominator",
                  "gamma": "Gamma(0.25) on every Linear and the head, eps 1e-6 elsewhere",

@@ -851,44 +851,49 @@ __global__ void __launch_bounds__(NT) splitk_reduce_kernel(const Args g) {
 // ALUs and keep the few A rows in LDS. Both end in the tile epilogue.
 constexpr int kSkinnyBN = 64;  // NT column tile
 constexpr int kSkinnyLDC = kSkinnyBN + 4;
-constexpr int kSkinnyRows = 8;  // B rows per thread per chunk (NN)
 
 // NN (B is K x N, N-contiguous): a workgroup owns W = 4 TX columns and the K range of one split,
-// walked in chunks of CH = TY * 8 rows. Thread (ty, tx) = (tid / TX, tid % TX) accumulates columns
-// 4 tx .. 4 tx + 3 over rows kb + ty + TY i of each chunk from the chunk's A columns in LDS; the
-// next chunk's B and A loads are in flight while the current one is multiplied. The TY partial sums
-// of a column are added in ty order. One split runs the epilogue; several write their partials to
-// the workspace for splitk_reduce_kernel<W, EPI>.
-template <int MB, int TX, int EPI>
+// walked in chunks of CH = TY * R rows (TY = 256 / TX). Thread (ty, tx) = (tid / TX, tid % TX)
+// accumulates columns 4 tx .. 4 tx + 3 over rows kb + ty + TY i of each chunk from the chunk's A
+// columns in LDS. R is 16 rows for up to eight rows of A (a workgroup then has 64 KiB of B loads in
+// flight and one chunk covers K up to 1024 at 16 columns) and 8 for sixteen, where the next
+// chunk's loads are in flight while the current one is multiplied. A column's partial
+// sums are added first across the lanes of each wave (xor shuffles over the ty bits), then over the
+// waves in wave order. One split runs the epilogue; several write their partials to the workspace
+// for splitk_reduce_kernel<W, EPI>.
+template <int MB, int TX, int EPI, int R>
 __global__ void __launch_bounds__(NT) skinny_nn_kernel(const Args g) {
-    constexpr int TY = NT / TX, W = 4 * TX, CH = TY * kSkinnyRows, LDC = W + 4;
-    constexpr int AU = MB * CH / NT;  // A values each thread stages per chunk
+    constexpr int T = NT, TY = T / TX, W = 4 * TX, CH = TY * R, LDC = W + 4, NW = T / kWave;
+    constexpr int AU = MB * CH / T;  // A values each thread stages per chunk
+    constexpr bool DB = R <= 8;      // register double-buffering of the chunks
+    static_assert(AU * T == MB * CH && kWave % TX == 0, "chunk must split evenly");
     __shared__ __attribute__((aligned(16))) float As[MB * CH];
-    __shared__ __attribute__((aligned(16))) float Ps[TY * 4 * W];
+    __shared__ __attribute__((aligned(16))) float Ps[NW * MB * W];
     __shared__ __attribute__((aligned(16))) float Cs[MB * LDC];
-    const int tid = threadIdx.x, tx = tid % TX, ty = tid / TX;
+    const int tid = threadIdx.x, tx = tid % TX, ty = tid / TX, lane = tid & (kWave - 1), wave = tid / kWave;
     const int64_t tile = blockIdx.x % g.tiles_n, split = blockIdx.x / g.tiles_n;
     const int64_t n0 = tile * W, n = n0 + 4 * tx;
     const int64_t k0 = split * g.kc, k1 = min(g.K, k0 + g.kc);
     const int cnt = n < g.N ? (g.N - n < 4 ? static_cast<int>(g.N - n) : 4) : 0;
     const bool vec = g.vec_b && cnt == 4;
-    const float* B = g.b.p;
     const float* A = g.a.p;
+    const int64_t row_step = TY * g.b.ld;
     auto load = [&](f4* bv, float* av, int64_t kb) {
+        const float* bp = g.b.p + (kb + ty) * g.b.ld + n;
 #pragma unroll
-        for (int r = 0; r < kSkinnyRows; ++r) {
+        for (int r = 0; r < R; ++r) {
             const int64_t k = kb + ty + TY * r;
-            bv[r] = (k < k1 && cnt > 0) ? ld4(B + k * g.b.ld + n, vec, cnt) : f4{0.f, 0.f, 0.f, 0.f};
+            bv[r] = (k < k1 && cnt > 0) ? ld4(bp + r * row_step, vec, cnt) : f4{0.f, 0.f, 0.f, 0.f};
         }
 #pragma unroll
         for (int u = 0; u < AU; ++u) {
-            const int i = tid + NT * u, m = i / CH;
+            const int i = tid + T * u, m = i / CH;
             const int64_t k = kb + (i - m * CH);
             av[u] = (m < g.M && k < k1) ? A[m * g.a.ld + k] : 0.0f;
         }
     };
-    f4 cur[kSkinnyRows], nxt[kSkinnyRows];
-    float acur[AU], anxt[AU];
+    f4 cur[R], nxt[DB ? R : 1];
+    float acur[AU], anxt[DB ? AU : 1];
     load(cur, acur, k0);
     float acc[MB][4];
 #pragma unroll
@@ -897,13 +902,15 @@ __global__ void __launch_bounds__(NT) skinny_nn_kernel(const Args g) {
         for (int j = 0; j < 4; ++j) acc[m][j] = 0.0f;
     for (int64_t kb = k0; kb < k1; kb += CH) {
         const bool more = kb + CH < k1;
-        if (more) load(nxt, anxt, kb + CH);
+        if constexpr (DB) {
+            if (more) load(nxt, anxt, kb + CH);
+        }
         __syncthreads();  // the previous chunk's A is consumed
 #pragma unroll
-        for (int u = 0; u < AU; ++u) As[tid + NT * u] = acur[u];
+        for (int u = 0; u < AU; ++u) As[tid + T * u] = acur[u];
         __syncthreads();
 #pragma unroll
-        for (int r = 0; r < kSkinnyRows; ++r) {
+        for (int r = 0; r < R; ++r) {
 #pragma unroll
             for (int m = 0; m < MB; ++m) {
                 const float a = As[m * CH + ty + TY * r];
@@ -912,34 +919,46 @@ __global__ void __launch_bounds__(NT) skinny_nn_kernel(const Args g) {
             }
         }
         if (more) {
+            if constexpr (DB) {
 #pragma unroll
-            for (int r = 0; r < kSkinnyRows; ++r) cur[r] = nxt[r];
+                for (int r = 0; r < R; ++r) cur[r] = nxt[r];
 #pragma unroll
-            for (int u = 0; u < AU; ++u) acur[u] = anxt[u];
+                for (int u = 0; u < AU; ++u) acur[u] = anxt[u];
+            } else {
+                load(cur, acur, kb + CH);
+            }
         }
     }
-    // Sum the TY row-lane partials of each column in ty order, four rows of M at a time.
-    for (int mg = 0; mg < MB; mg += 4) {
+    // Across the lanes of a wave that share tx, then over the waves in order.
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-            *reinterpret_cast<f4*>(Ps + (ty * 4 + r) * W + 4 * tx) =
-                f4{acc[mg + r][0], acc[mg + r][1], acc[mg + r][2], acc[mg + r][3]};
-        __syncthreads();
-        for (int o = tid; o < 4 * W; o += NT) {
-            const int rr = o / W, cc = o - rr * W;
-            float v = 0.0f;
-#pragma unroll 8
-            for (int t = 0; t < TY; ++t) v += Ps[(t * 4 + rr) * W + cc];
-            Cs[(mg + rr) * LDC + cc] = v;
+    for (int m = 0; m < MB; ++m)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            float v = acc[m][j];
+#pragma unroll
+            for (int o = TX; o < kWave; o <<= 1) v += __shfl_xor(v, o, kWave);
+            acc[m][j] = v;
         }
-        __syncthreads();
+    if (lane < TX) {
+#pragma unroll
+        for (int m = 0; m < MB; ++m)
+            *reinterpret_cast<f4*>(Ps + (wave * MB + m) * W + 4 * tx) = f4{acc[m][0], acc[m][1], acc[m][2], acc[m][3]};
     }
+    __syncthreads();
+    for (int o = tid; o < MB * W; o += T) {
+        const int m = o / W, c = o - m * W;
+        float v = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) v += Ps[(w * MB + m) * W + c];
+        Cs[m * LDC + c] = v;
+    }
+    __syncthreads();
     if (g.splits == 1) {
-        epilogue_rows<MB, W, EPI, NT>(Cs, LDC, 0, n0, 0, g);
+        epilogue_rows<MB, W, EPI, T>(Cs, LDC, 0, n0, 0, g);
         return;
     }
     const int64_t plane = g.M * g.N;
-    for (int i = tid; i < MB * W; i += NT) {
+    for (int i = tid; i < MB * W; i += T) {
         const int m = i / W, c = i - m * W;
         if (m < g.M && n0 + c < g.N) g.ws[split * plane + m * g.N + n0 + c] = Cs[m * LDC + c];
     }
@@ -1091,7 +1110,10 @@ struct SkinnyEntry {
     KernelFn r[3];
 };
 
-#define PXK_SKINNY_NN_W(MB, EPI) {skinny_nn_kernel<MB, 16, EPI>, skinny_nn_kernel<MB, 8, EPI>, skinny_nn_kernel<MB, 4, EPI>}
+constexpr int skinny_rows(int mb) { return mb == 4 ? 16 : (mb == 8 ? 16 : 8); }
+#define PXK_SKINNY_NN_W(MB, EPI)                                                                        \
+    {skinny_nn_kernel<MB, 16, EPI, skinny_rows(MB)>, skinny_nn_kernel<MB, 8, EPI, skinny_rows(MB)>, \
+     skinny_nn_kernel<MB, 4, EPI, skinny_rows(MB)>}
 #define PXK_SKINNY_NN(EPI)                                                                                        \
     SkinnyEntry {                                                                                                 \
         0, EPI, {PXK_SKINNY_NN_W(4, EPI), PXK_SKINNY_NN_W(8, EPI), PXK_SKINNY_NN_W(16, EPI)},                    \
