@@ -88,6 +88,28 @@ def test_explain_generated_matches_oracle(name):
         assert np.all(rel[t][:, l:] == 0.0)
 
 
+@pytest.mark.parametrize("name", sorted(dc.CASES))
+def test_grouped_explanation_matches_single_prefix_passes(name):
+    """explain_generated_device runs consecutive tokens as seeded copies of their longest prefix; each
+    token's relevance against explain_rows_device over its own prefix alone, for every token."""
+    cfg, params, prompts, new = dc.case(name)
+    lm = models.CausalLM(to_px(cfg), params)
+    ids_d, ids, _ = generate(lm, prompts, new)
+    n, p = prompts.shape
+    ld, W = ids.shape[1], p + new - 1
+    out = G.empty((new, n, W))
+    lm.explain_generated_device(G.ptr(ids_d), n, p, new, ld, LXT, G.ptr(out))
+    grouped = G.host(out)
+    for t in range(new):
+        l = p + t
+        pid = G.dev(np.ascontiguousarray(ids[:, :l]))
+        tg = G.dev(np.ascontiguousarray(ids[:, l]))
+        rows = G.empty((n * l,))
+        lm.explain_rows_device(G.ptr(pid), n, l, G.ptr(tg), 1, LXT, G.ptr(rows))
+        expect_relevance_agrees(grouped[t][:, :l], G.host(rows).reshape(n, l), "token %d" % t)
+        assert np.all(grouped[t][:, l:] == 0.0)
+
+
 def test_explain_rows_matches_the_dense_explain():
     """Seeding the last rows only (the head on n rows) against the dense explain_device (the head on
     every row) for the same targets, under LXT and Gamma."""
