@@ -416,6 +416,14 @@ int pxk_lrp_rule_combine(int rule, const float* x, int64_t ldx, const float* c, 
                          int64_t rows, int64_t in, float* r_in, int64_t ld, const float* split_a,
                          const float* split_b, const float* split_sum, float* r_b, float eps, void* stream);
 
+/* A sandwich block's sublayer output a, its post-norm and the residual add, then the norm that reads
+ * the sum (Gemma 3, transformer_block.cpp's post_attention / post_feedforward norms followed by the
+ * next pre-norm): y = x + gamma_a * a / rms(a), rms(a) = sqrt(mean(a^2) + eps_a), and, when y_norm is
+ * given, y_norm = gamma_y * y / rms(y). Row-major rows x cols; replaces rms_norm_forward + add +
+ * rms_norm_forward in one pass. */
+int pxk_rms_norm_add(const float* x, const float* a, const float* gamma_a, float eps_a, float* y,
+                     const float* gamma_y, float eps_y, float* y_norm, int64_t rows, int64_t cols, void* stream);
+
 /* ---- KV-cached decode ----------------------------------------------------------------------------
  * The position-dependent steps of a batched greedy decode step. The position is an int32 in device
  * memory shared by the batch, so a step launches with the same arguments at every position (a HIP
@@ -425,11 +433,14 @@ int pxk_lrp_rule_combine(int rule, const float* x, int64_t ldx, const float* c, 
  * 501-587) and the host round trip of the last hidden row; batch 1 there, any batch here.
  * Cache layout: sequence b at cache + b * seq_stride, position p at + p * kv_heads * head_dim. */
 /* q (rotated, at *pos) -> q_out (n x heads*head_dim); k (rotated) and v -> the caches at *pos, for
- * *pos < positions (the caches' length, also the RoPE tables' (positions x head_dim/2)). */
+ * *pos < positions (the caches' length, also the RoPE tables' (positions x head_dim/2)). With q_gamma
+ * and k_gamma (QK-Norm, Qwen3 / Gemma 3: both or neither), each q and k head is first normalised as
+ * pxk_rms_norm_heads does (eps norm_eps), in the same launch. */
 int pxk_decode_rope_append(const float* q, int64_t ldq, const float* k, int64_t ldk, const float* v, int64_t ldv,
                            float* q_out, float* k_cache, float* v_cache, int64_t seq_stride, int64_t positions,
                            const float* cos_t, const float* sin_t, const int32_t* pos, int64_t n, int64_t heads,
-                           int64_t kv_heads, int64_t head_dim, int rope, int rotate_half, void* stream);
+                           int64_t kv_heads, int64_t head_dim, int rope, int rotate_half, const float* q_gamma,
+                           const float* k_gamma, float norm_eps, void* stream);
 /* ctx (n x heads*head_dim) = softmax(scale q K^T) V over the cached keys 0..*pos (the last `window`
  * of them when window > 0); max_keys bounds *pos + 1. Two launches: every (sequence, query head,
  * 64-key chunk) scores its keys and keeps a max / exp-sum / exp-weighted context partial in the

@@ -54,8 +54,13 @@ public:
      *         relevance when `below` is empty, else nullptr. */
     const float* run_relevance_split(const LRPRuleConfig& config, const detail::ResidualSplit& below);
     /** @brief One KV-cached decode step of n sequences at the device position *pos
-     *         (forward_cached, transformer_block.cpp:135-153). Returns y2 (n, d_model). */
-    const float* decode_step(const float* x, int64_t n, KVCacheState& cache, const int32_t* pos);
+     *         (forward_cached, transformer_block.cpp:135-153). Returns y2 (n, d_model). x_normed
+     *         (nullable) is norm1(x) when the caller has it. With next_norm and next_normed, a block
+     *         with sandwich norms also writes next_norm(y2) and points *next_normed at it (else
+     *         nullptr). */
+    const float* decode_step(const float* x, const float* x_normed, int64_t n, KVCacheState& cache,
+                             const int32_t* pos, RMSNormModule* next_norm = nullptr,
+                             const float** next_normed = nullptr);
 
 protected:
     Tensor forward_impl(const Tensor& input) override;
@@ -73,7 +78,7 @@ private:
     int64_t N_ = 0, L_ = 0;
     const float* x_ = nullptr;
     Shape last_shape_;
-    detail::DevBuf x_copy_, y1_, y2_, r_y1d_, r_ffn_, r_y1_, r_xd_, r_attn_, dec_y1_, dec_y2_;
+    detail::DevBuf x_copy_, y1_, y2_, r_y1d_, r_ffn_, r_y1_, r_xd_, r_attn_, dec_y1_, dec_y2_, dec_n2_, dec_next_;
 };
 
 }  // namespace pulsatrix

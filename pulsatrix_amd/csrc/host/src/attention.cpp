@@ -279,7 +279,10 @@ const float* MultiHeadAttentionModule::decode_step(const float* x, int64_t n, KV
     }
     const float* pre = y;
     int64_t ld_pre = w3;
-    if (config_.use_qk_norm) {
+    // QK-Norm inside the RoPE / cache kernel when both norms share their eps (they do for every
+    // checkpoint the loader reads); otherwise its own two launches first.
+    const bool fused_norm = config_.use_qk_norm && q_norm_->eps() == k_norm_->eps();
+    if (config_.use_qk_norm && !fused_norm) {
         float* nq = dec_qkn_.ensure(be_, n * rw);
         MI355XBackend::check(pxk_rms_norm_heads(y, w3, nq, rw, q_norm_->effective_gamma(), n, H_, D_, q_norm_->eps(), st),
                              "MultiHeadAttentionModule::decode_step (QK-Norm)");
@@ -294,7 +297,10 @@ const float* MultiHeadAttentionModule::decode_step(const float* x, int64_t n, KV
     MI355XBackend::check(pxk_decode_rope_append(pre, ld_pre, pre + qd, ld_pre, y + qd + kvd, w3, q, cache.k.data(),
                                                 cache.v.data(), stride, cache.positions, cos_.data(), sin_.data(), pos, n,
                                                 H_, Hkv_, D_, config_.use_rope,
-                                                config_.rope_layout == RoPELayout::RotateHalf, st),
+                                                config_.rope_layout == RoPELayout::RotateHalf,
+                                                fused_norm ? q_norm_->effective_gamma() : nullptr,
+                                                fused_norm ? k_norm_->effective_gamma() : nullptr,
+                                                fused_norm ? q_norm_->eps() : 0.0f, st),
                          "MultiHeadAttentionModule::decode_step (RoPE, cache)");
     float* ctx = dec_ctx_.ensure(be_, n * qd);
     const int64_t window = config_.causal ? config_.sliding_window : 0;

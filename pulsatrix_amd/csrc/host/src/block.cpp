@@ -256,19 +256,33 @@ const float* TransformerBlock::run_forward(const float* x, int64_t n, int64_t l)
     return y2;
 }
 
-const float* TransformerBlock::decode_step(const float* x, int64_t n, KVCacheState& cache, const int32_t* pos) {
+const float* TransformerBlock::decode_step(const float* x, const float* x_normed, int64_t n, KVCacheState& cache,
+                                          const int32_t* pos, RMSNormModule* next_norm, const float** next_normed) {
     float* y1 = dec_y1_.ensure(be_, n * d_);
     float* y2 = dec_y2_.ensure(be_, n * d_);
+    const float* xn = x_normed ? x_normed : norm1_.run_forward(x, n);
+    if (next_normed) *next_normed = nullptr;
     if (!post_attn_norm_) {
-        mha_.decode_step(norm1_.run_forward(x, n), n, cache, pos, x, y1);
+        mha_.decode_step(xn, n, cache, pos, x, y1);
         swiglu_.run_forward(norm2_.run_forward(y1, n), n, y1, y2);
         return y2;
     }
+    // Each sublayer's post-norm, its residual add and the norm that reads the sum next run as one
+    // row kernel: y1 = x + post_attn_norm(attn) with norm2(y1), then y2 = y1 + post_mlp_norm(mlp)
+    // with the caller's next norm (the next block's norm1 or the final norm) of y2.
     void* st = be_->stream();
-    const float* a = post_attn_norm_->run_forward(mha_.decode_step(norm1_.run_forward(x, n), n, cache, pos), n);
-    MI355XBackend::check(pxk_add(x, a, y1, n * d_, st), "TransformerBlock::decode_step");
-    const float* f = post_mlp_norm_->run_forward(swiglu_.run_forward(norm2_.run_forward(y1, n), n), n);
-    MI355XBackend::check(pxk_add(y1, f, y2, n * d_, st), "TransformerBlock::decode_step");
+    const float* a = mha_.decode_step(xn, n, cache, pos);
+    float* n2 = dec_n2_.ensure(be_, n * d_);
+    MI355XBackend::check(pxk_rms_norm_add(x, a, post_attn_norm_->effective_gamma(), post_attn_norm_->eps(), y1,
+                                          norm2_.effective_gamma(), norm2_.eps(), n2, n, d_, st),
+                         "TransformerBlock::decode_step");
+    const float* f = swiglu_.run_forward(n2, n);
+    float* nn = next_norm && next_normed ? dec_next_.ensure(be_, n * d_) : nullptr;
+    MI355XBackend::check(pxk_rms_norm_add(y1, f, post_mlp_norm_->effective_gamma(), post_mlp_norm_->eps(), y2,
+                                          nn ? next_norm->effective_gamma() : nullptr, nn ? next_norm->eps() : 0.0f, nn,
+                                          n, d_, st),
+                         "TransformerBlock::decode_step");
+    if (nn) *next_normed = nn;
     return y2;
 }
 

@@ -262,8 +262,12 @@ void CausalLM::generate_greedy_device(float* ids, int64_t n, int64_t prompt, int
         if (config_.embed_scale != 1.0f)
             MI355XBackend::check(pxk_axpby(config_.embed_scale, x, 0.0f, nullptr, x, n * d, st), "CausalLM::generate");
         const float* h = x;
-        for (size_t i = 0; i < layers_.size(); ++i) h = layers_[i]->decode_step(h, n, caches_[i], pos);
-        const float* hn = norm_.run_forward(h, n);
+        const float* hn = nullptr;  // norm1(h) of the next layer (or the final norm) when a block wrote it
+        for (size_t i = 0; i < layers_.size(); ++i) {
+            RMSNormModule* next = i + 1 < layers_.size() ? &layers_[i + 1]->norm1() : &norm_;
+            h = layers_[i]->decode_step(h, hn, n, caches_[i], pos, next, &hn);
+        }
+        if (!hn) hn = norm_.run_forward(h, n);
         pick(tied_head_ ? tied_head_->run_forward(hn, n) : lm_head_->run_forward(hn, n));
     };
     if (new_tokens < 2) return;

@@ -33,6 +33,9 @@ struct RopeAppendArgs {
     const int32_t* pos;
     int64_t n, H, Hkv, D, positions;  // positions: what the cache and the tables hold
     int rope, rotate_half;
+    const float* q_gamma;  // QK-Norm's scales (both or neither)
+    const float* k_gamma;
+    float norm_eps;
 };
 
 // One thread per (row, head, pair) of q and of k, and per (row, element) of v.
@@ -62,6 +65,56 @@ __global__ void __launch_bounds__(kThreads) rope_append_kernel(const RopeAppendA
             dst[lo] = x0;
             dst[hi] = x1;
         }
+    }
+}
+
+// With QK-Norm: one workgroup per (sequence, query or key head). The head's D values are staged in
+// LDS, normalised (RMSNorm over the head, as pxk_rms_norm_heads computes it: the wave sums of squares
+// added in wave order), rotated at the position and written; a key head's workgroup also copies its
+// value head into the cache.
+__global__ void __launch_bounds__(kThreads) rope_append_norm_kernel(const RopeAppendArgs a) {
+    extern __shared__ float row[];  // D
+    __shared__ float part[kThreads / kWave];
+    const int64_t p = *a.pos, half = a.D / 2, kvd = a.Hkv * a.D;
+    if (p < 0 || p >= a.positions) return;  // past the cache: nothing is written (the host bounds the steps)
+    const int64_t blk = blockIdx.x, hs = a.H + a.Hkv, b = blk / hs, hh = blk - b * hs;
+    const bool is_q = hh < a.H;
+    const int64_t h = is_q ? hh : hh - a.H;
+    const float* src = is_q ? a.q + b * a.ldq + h * a.D : a.k + b * a.ldk + h * a.D;
+    const float* gamma = is_q ? a.q_gamma : a.k_gamma;
+    const int tid = threadIdx.x;
+    float ss = 0.0f;
+    for (int64_t d = tid; d < a.D; d += kThreads) {
+        const float x = src[d];
+        row[d] = x;
+        ss += x * x;
+    }
+    ss = wave_sum(ss);
+    if ((tid & (kWave - 1)) == 0) part[tid / kWave] = ss;
+    __syncthreads();
+    float tot = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kThreads / kWave; ++w) tot += part[w];
+    const float rms = sqrtf(tot / static_cast<float>(a.D) + a.norm_eps);
+    for (int64_t d = tid; d < a.D; d += kThreads) row[d] = gamma[d] * row[d] / rms;
+    __syncthreads();
+    float* dst = is_q ? a.q_out + b * a.H * a.D + h * a.D : a.k_cache + b * a.seq_stride + p * kvd + h * a.D;
+    for (int64_t i = tid; i < half; i += kThreads) {
+        const int64_t lo = a.rotate_half ? i : 2 * i, hi = a.rotate_half ? i + half : 2 * i + 1;
+        const float x0 = row[lo], x1 = row[hi];
+        if (a.rope) {  // rope_rotate (row_math.hpp:93-110) at position p
+            const float c = a.cos_t[p * half + i], s = a.sin_t[p * half + i];
+            dst[lo] = x0 * c - x1 * s;
+            dst[hi] = x0 * s + x1 * c;
+        } else {
+            dst[lo] = x0;
+            dst[hi] = x1;
+        }
+    }
+    if (!is_q) {
+        const float* vs = a.v + b * a.ldv + h * a.D;
+        float* vd = a.v_cache + b * a.seq_stride + p * kvd + h * a.D;
+        for (int64_t d = tid; d < a.D; d += kThreads) vd[d] = vs[d];
     }
 }
 
@@ -293,7 +346,8 @@ extern "C" int pxk_decode_rope_append(const float* q, int64_t ldq, const float* 
                                       int64_t ldv, float* q_out, float* k_cache, float* v_cache, int64_t seq_stride,
                                       int64_t positions, const float* cos_t, const float* sin_t, const int32_t* pos,
                                       int64_t n, int64_t heads, int64_t kv_heads, int64_t head_dim, int rope,
-                                      int rotate_half, void* stream) {
+                                      int rotate_half, const float* q_gamma, const float* k_gamma, float norm_eps,
+                                      void* stream) {
     const int64_t qd = heads * head_dim, kvd = kv_heads * head_dim;
     if (n < 0 || heads <= 0 || kv_heads <= 0 || heads % kv_heads != 0 || head_dim <= 0 || head_dim % 2 != 0 ||
         ldq < qd || ldk < kvd || ldv < kvd || positions <= 0 || seq_stride < positions * kvd)
@@ -301,8 +355,19 @@ extern "C" int pxk_decode_rope_append(const float* q, int64_t ldq, const float* 
     if (n == 0) return PXK_OK;
     if (!q || !k || !v || !q_out || !k_cache || !v_cache || !pos || (rope && (!cos_t || !sin_t)))
         return fail(PXK_ERR_INVALID, "pxk_decode_rope_append: a required operand is NULL");
-    const RopeAppendArgs a{q, ldq, k, ldk, v, ldv, q_out, k_cache, v_cache, seq_stride, cos_t, sin_t, pos,
-                           n, heads, kv_heads, head_dim, positions, rope, rotate_half};
+    if ((q_gamma == nullptr) != (k_gamma == nullptr))
+        return fail(PXK_ERR_INVALID, "pxk_decode_rope_append: QK-Norm needs both q_gamma and k_gamma");
+    const RopeAppendArgs a{q,        ldq,     k,       ldk,   v,       ldv,       q_out,    k_cache,
+                           v_cache,  seq_stride, cos_t, sin_t, pos,   n,         heads,    kv_heads,
+                           head_dim, positions,  rope,  rotate_half, q_gamma, k_gamma, norm_eps};
+    if (q_gamma) {
+        const size_t lds = static_cast<size_t>(head_dim) * sizeof(float);
+        if (lds > 60 * 1024 || n * (heads + kv_heads) > (int64_t{1} << 31) - 1)
+            return fail(PXK_ERR_INVALID, "pxk_decode_rope_append: head_dim must fit LDS");
+        hipLaunchKernelGGL(rope_append_norm_kernel, dim3(static_cast<unsigned>(n * (heads + kv_heads))), dim3(kThreads),
+                           lds, S(stream), a);
+        return launched("pxk_decode_rope_append (QK-Norm)");
+    }
     const int64_t work = n * (heads + kv_heads) * (head_dim / 2) + n * kvd;
     hipLaunchKernelGGL(rope_append_kernel, dim3(grid_for(work, kThreads)), dim3(kThreads), 0, S(stream), a);
     return launched("pxk_decode_rope_append");

@@ -83,6 +83,105 @@ __global__ void __launch_bounds__(kThreads) rms_norm_vec_kernel(const float* in,
     }
 }
 
+// ---- a sublayer's post-norm and residual add, then the next norm (Gemma 3 sandwich blocks) --------
+// y = x + g_a * a / rms(a), and yn = g_y * y / rms(y) when g_y is given: the post-attention (or
+// post-MLP) RMSNorm, the residual sum and the norm that reads the sum next, each with RMSNorm's and
+// the add's own expressions. One wave per row; a row of a and of y stays in registers (lane l owns
+// float4 columns l, l + 64, ...).
+struct NormAddArgs {
+    const float* x;
+    const float* a;
+    const float* ga;
+    float* y;
+    const float* gy;
+    float* yn;
+    int64_t rows;
+    int cols4;
+    float ea, ey;
+};
+
+template <int NV>
+__global__ void __launch_bounds__(kThreads) rms_norm_add_vec_kernel(const NormAddArgs g) {
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    const int64_t r = row_id();
+    if (r >= g.rows) return;
+    const int lane = lane_id();
+    const int64_t base = r * g.cols4;
+    const f4* a = reinterpret_cast<const f4*>(g.a) + base;
+    const f4* x = reinterpret_cast<const f4*>(g.x) + base;
+    const f4* ga = reinterpret_cast<const f4*>(g.ga);
+    f4 v[NV];
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int c = lane + j * kWave;
+        v[j] = c < g.cols4 ? a[c] : f4{0.0f, 0.0f, 0.0f, 0.0f};
+        ss += v[j].x * v[j].x + v[j].y * v[j].y + v[j].z * v[j].z + v[j].w * v[j].w;
+    }
+    ss = wave_sum(ss);
+    const float rms_a = sqrtf(ss / static_cast<float>(4 * g.cols4) + g.ea);
+    f4* y = reinterpret_cast<f4*>(g.y) + base;
+    float sy = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int c = lane + j * kWave;
+        if (c < g.cols4) {
+            const f4 gv = ga[c], xv = x[c];
+            f4 t;
+            t.x = xv.x + gv.x * v[j].x / rms_a;
+            t.y = xv.y + gv.y * v[j].y / rms_a;
+            t.z = xv.z + gv.z * v[j].z / rms_a;
+            t.w = xv.w + gv.w * v[j].w / rms_a;
+            y[c] = t;
+            v[j] = t;
+            sy += t.x * t.x + t.y * t.y + t.z * t.z + t.w * t.w;
+        }
+    }
+    if (!g.yn) return;
+    sy = wave_sum(sy);
+    const float rms_y = sqrtf(sy / static_cast<float>(4 * g.cols4) + g.ey);
+    const f4* gy = reinterpret_cast<const f4*>(g.gy);
+    f4* yn = reinterpret_cast<f4*>(g.yn) + base;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int c = lane + j * kWave;
+        if (c < g.cols4) {
+            const f4 gv = gy[c];
+            f4 t;
+            t.x = gv.x * v[j].x / rms_y;
+            t.y = gv.y * v[j].y / rms_y;
+            t.z = gv.z * v[j].z / rms_y;
+            t.w = gv.w * v[j].w / rms_y;
+            yn[c] = t;
+        }
+    }
+}
+
+// Any width: the same steps reading the rows from memory (cols = 4 * cols4 is not assumed).
+__global__ void __launch_bounds__(kThreads) rms_norm_add_kernel(const NormAddArgs g, int64_t cols) {
+    const int64_t r = row_id();
+    if (r >= g.rows) return;
+    const int lane = lane_id();
+    const float* a = g.a + r * cols;
+    const float* x = g.x + r * cols;
+    float* y = g.y + r * cols;
+    float ss = 0.0f;
+    for (int64_t i = lane; i < cols; i += kWave) ss += a[i] * a[i];
+    ss = wave_sum(ss);
+    const float rms_a = sqrtf(ss / static_cast<float>(cols) + g.ea);
+    float sy = 0.0f;
+    for (int64_t i = lane; i < cols; i += kWave) {
+        const float t = x[i] + g.ga[i] * a[i] / rms_a;
+        y[i] = t;
+        sy += t * t;
+    }
+    if (!g.yn) return;
+    sy = wave_sum(sy);
+    const float rms_y = sqrtf(sy / static_cast<float>(cols) + g.ey);
+    float* yn = g.yn + r * cols;
+    for (int64_t i = lane; i < cols; i += kWave) yn[i] = g.gy[i] * y[i] / rms_y;  // own lane's writes
+}
+
 // ---- softmax_rows (cpu_backend.cpp:292-310) ---------------------------------------------------
 __global__ void __launch_bounds__(kThreads) softmax_kernel(const float* in, float* out, int64_t rows, int64_t cols) {
     const int64_t r = row_id();
@@ -484,6 +583,29 @@ int pxk_rms_norm_forward(const float* in, const float* gamma, float* out, float*
         hipLaunchKernelGGL(rms_norm_kernel, grid, block, 0, S(stream), in, gamma, out, row_rms, rows, cols, eps);
     }
     return launched("pxk_rms_norm_forward");
+}
+
+int pxk_rms_norm_add(const float* x, const float* a, const float* gamma_a, float eps_a, float* y,
+                     const float* gamma_y, float eps_y, float* y_norm, int64_t rows, int64_t cols, void* stream) {
+    int rc;
+    if (!sizes_ok("pxk_rms_norm_add", rows, cols, &rc)) return rc;
+    if (!x || !a || !gamma_a || !y || (y_norm && !gamma_y))
+        return fail(PXK_ERR_INVALID, "pxk_rms_norm_add: a required operand is NULL");
+    const NormAddArgs g{x, a, gamma_a, y, gamma_y, y_norm, rows, static_cast<int>(std::min<int64_t>(cols / 4, 1 << 30)),
+                        eps_a, eps_y};
+    const dim3 grid(rows_grid(rows)), block(kThreads);
+    const int64_t nv = cdiv(cols / 4, kWave);
+    const bool vec = cols % 4 == 0 && nv <= 8 && aligned16(x) && aligned16(a) && aligned16(gamma_a) && aligned16(y) &&
+                     (!y_norm || (aligned16(gamma_y) && aligned16(y_norm)));
+    if (vec && nv <= 2)
+        hipLaunchKernelGGL(rms_norm_add_vec_kernel<2>, grid, block, 0, S(stream), g);
+    else if (vec && nv <= 4)
+        hipLaunchKernelGGL(rms_norm_add_vec_kernel<4>, grid, block, 0, S(stream), g);
+    else if (vec)
+        hipLaunchKernelGGL(rms_norm_add_vec_kernel<8>, grid, block, 0, S(stream), g);
+    else
+        hipLaunchKernelGGL(rms_norm_add_kernel, grid, block, 0, S(stream), g, cols);
+    return launched("pxk_rms_norm_add");
 }
 
 int pxk_softmax_rows(const float* in, float* out, int64_t rows, int64_t cols, void* stream) {

@@ -77,6 +77,7 @@ PXK_SIGNATURES = {
     "pxk_attention_softmax": "ppiifnip",
     "pxk_attention_lrp_scores": "ppppiiffnip",
     "pxk_rms_norm_heads": "pipipiiifp",
+    "pxk_rms_norm_add": "pppfppfpiip",
     "pxk_lrp_rope_rows": "pipipipippppiiiiifnnp",
     "pxk_rope_qk": "ppippipppiiiiinp",
     "pxk_rope_rotate": "ppppiiinnp",
@@ -88,7 +89,7 @@ PXK_SIGNATURES = {
     "pxk_seed_rows": "pipiiippnp",
     "pxk_decode_pick": "piiipippippsp",
     "pxk_decode_attention": "pppippiiiiiifpsp",
-    "pxk_decode_rope_append": "pipipipppiipppiiiinnp",
+    "pxk_decode_rope_append": "pipipipppiipppiiiinnppfp",
 }
 
 

@@ -258,6 +258,34 @@ def test_rms_norm_widths_match_oracle(rows, cols, offset):
 
 
 @gpu
+@pytest.mark.parametrize("rows,cols,offset,with_next", [(4, 640, 0, 1), (37, 576, 0, 1), (5, 2048, 0, 1),
+                                                       (9, 100, 0, 0), (6, 4100, 0, 1), (8, 640, 1, 1)])
+def test_rms_norm_add_matches_oracle_composition(rows, cols, offset, with_next):
+    """A sandwich block's post-norm + residual add + next norm in one kernel, against the oracle's
+    rms_norm_forward, the add and rms_norm_forward again; register-resident widths (2, 3, 8 float4 per
+    lane), the scalar fallback for wide and misaligned rows, and without the next norm."""
+    x, a = G.uniform((rows, cols), 11), G.uniform((rows, cols), 12, -3, 3)
+    ga, gy = G.uniform((cols,), 13, 0.5, 1.5), G.uniform((cols,), 14, 0.5, 1.5)
+    an, rms = np.empty_like(a), np.empty((rows,), np.float32)
+    G.oracle_call("pxo_rms_norm_forward", a, ga, an, rms, rows, cols, 1e-6)
+    y_ref = (x + an).astype(np.float32)
+    yn_ref = np.empty_like(y_ref)
+    G.oracle_call("pxo_rms_norm_forward", y_ref, gy, yn_ref, rms, rows, cols, 1e-5)
+    pad = np.zeros(offset, np.float32)
+    xd, ad = G.dev(np.concatenate([pad, x.ravel()])), G.dev(np.concatenate([pad, a.ravel()]))
+    y, yn = G.empty((rows * cols + offset,)), G.empty((rows * cols + offset,))
+    o = 4 * offset
+    N.call("pxk_rms_norm_add", xd.data_ptr() + o, ad.data_ptr() + o, G.ptr(G.dev(ga)), 1e-6, y.data_ptr() + o,
+           G.ptr(G.dev(gy)) if with_next else None, 1e-5, yn.data_ptr() + o if with_next else None, rows, cols,
+           G.stream())
+    G.assert_close(G.host(y)[offset:].reshape(rows, cols), y_ref, 1e-5, "norm + add")
+    if with_next:
+        G.assert_close(G.host(yn)[offset:].reshape(rows, cols), yn_ref, 1e-5, "next norm")
+    else:
+        assert np.all(np.isnan(G.host(yn)))  # untouched
+
+
+@gpu
 def test_row_kernels_match_oracle():
     rows, cols = 333, 2048
     x, g = G.uniform((rows, cols), 1), G.uniform((cols,), 2)
