@@ -124,7 +124,7 @@ struct DecodeAttnArgs {
     const float* v_cache;
     int64_t seq_stride;
     float* ctx;      // (n, H*D) contiguous
-    float* part;     // per (sequence, head, chunk): running max, sum and D partial context values
+    float* part;     // per (sequence, head, chunk): max, exp-sum, 2 pad, D partial context values
     const int32_t* pos;
     int64_t H, Hkv, D, window, max_keys, chunks;
     float scale;
@@ -132,6 +132,7 @@ struct DecodeAttnArgs {
 };
 
 constexpr int kKeyChunk = 64;  // keys per workgroup of the first pass
+constexpr int kPartHead = 4;   // a chunk's partial: max, exp-sum, two pad floats, then D context values
 static_assert(kKeyChunk == kWave && kThreads == 4 * kKeyChunk, "a lane per key in the softmax, four threads per key");
 typedef float f4 __attribute__((ext_vector_type(4)));
 
@@ -151,10 +152,10 @@ __global__ void __launch_bounds__(kThreads) decode_attention_part_kernel(const D
     const int64_t lo = (a.window > 0 && p + 1 > a.window) ? p + 1 - a.window : 0;
     const int64_t j0 = max(chunk * kKeyChunk, lo), j1 = min(chunk * kKeyChunk + kKeyChunk, p + 1);
     const int nk = j1 > j0 ? static_cast<int>(j1 - j0) : 0;
-    float* out = a.part + (bh * a.chunks + chunk) * (a.D + 2);
+    float* out = a.part + (bh * a.chunks + chunk) * (a.D + kPartHead);
     const int tid = threadIdx.x;
     if (nk == 0) {  // nothing visible here
-        for (int64_t d = tid; d < a.D + 2; d += kThreads) out[d] = d == 0 ? -INFINITY : 0.0f;
+        for (int64_t d = tid; d < a.D + kPartHead; d += kThreads) out[d] = d == 0 ? -INFINITY : 0.0f;
         return;
     }
     for (int64_t d = tid; d < a.D; d += kThreads) qs[d] = a.q[b * a.H * a.D + h * a.D + d];
@@ -191,11 +192,30 @@ __global__ void __launch_bounds__(kThreads) decode_attention_part_kernel(const D
     }
     __syncthreads();
     const float* vb = a.v_cache + b * a.seq_stride + j0 * kvd + hk * a.D;
+    const int64_t nd4 = a.D / 4;
+    if (a.vec && nd4 <= kThreads) {
+        // Key groups of kThreads / nd4 threads: thread (kg, c) sums the float4 column c over keys
+        // kg, kg + G, ...; the groups are added in order.
+        f4* red = reinterpret_cast<f4*>(qs);  // the query is no longer needed; LDS holds D + 64 floats
+        const int G = static_cast<int>(kThreads / nd4), c = static_cast<int>(tid % nd4), kg = static_cast<int>(tid / nd4);
+        f4 acc = {0.f, 0.f, 0.f, 0.f};
+        if (kg < G) {
+#pragma unroll 4
+            for (int j = kg; j < nk; j += G) acc += sc[j] * *reinterpret_cast<const f4*>(vb + j * kvd + 4 * c);
+        }
+        __syncthreads();  // every score read of the query row is done before it is overwritten
+        for (int g = 0; g < G; ++g) {
+            if (kg == g) red[c] = g == 0 ? acc : red[c] + acc;
+            __syncthreads();
+        }
+        if (tid < nd4) *reinterpret_cast<f4*>(out + kPartHead + 4 * tid) = red[tid];
+        return;
+    }
     for (int64_t d = tid; d < a.D; d += kThreads) {
         float acc = 0.0f;
 #pragma unroll 8
         for (int j = 0; j < nk; ++j) acc += sc[j] * vb[j * kvd + d];
-        out[2 + d] = acc;
+        out[kPartHead + d] = acc;
     }
 }
 
@@ -203,19 +223,20 @@ __global__ void __launch_bounds__(kThreads) decode_attention_part_kernel(const D
 // maxima, ctx = sum_c e^(m_c - M) acc_c / sum_c e^(m_c - M) l_c.
 __global__ void __launch_bounds__(kThreads) decode_attention_merge_kernel(const DecodeAttnArgs a) {
     const int64_t bh = blockIdx.x;
-    const float* part = a.part + bh * a.chunks * (a.D + 2);
+    const int64_t ps = a.D + kPartHead;
+    const float* part = a.part + bh * a.chunks * ps;
     float M = -INFINITY;
-    for (int64_t c = 0; c < a.chunks; ++c) M = fmaxf(M, part[c * (a.D + 2)]);
+    for (int64_t c = 0; c < a.chunks; ++c) M = fmaxf(M, part[c * ps]);
     float l = 0.0f;
     for (int64_t c = 0; c < a.chunks; ++c) {
-        const float m = part[c * (a.D + 2)];
-        if (m != -INFINITY) l += expf(m - M) * part[c * (a.D + 2) + 1];
+        const float m = part[c * ps];
+        if (m != -INFINITY) l += expf(m - M) * part[c * ps + 1];
     }
     for (int64_t d = threadIdx.x; d < a.D; d += kThreads) {
         float acc = 0.0f;
         for (int64_t c = 0; c < a.chunks; ++c) {
-            const float m = part[c * (a.D + 2)];
-            if (m != -INFINITY) acc += expf(m - M) * part[c * (a.D + 2) + 2 + d];
+            const float m = part[c * ps];
+            if (m != -INFINITY) acc += expf(m - M) * part[c * ps + kPartHead + d];
         }
         a.ctx[bh * a.D + d] = acc / l;
     }
@@ -375,7 +396,7 @@ extern "C" int pxk_decode_rope_append(const float* q, int64_t ldq, const float* 
 
 extern "C" size_t pxk_decode_attention_workspace(int64_t n, int64_t heads, int64_t head_dim, int64_t max_keys) {
     if (n <= 0 || heads <= 0 || head_dim <= 0 || max_keys <= 0) return 0;
-    return static_cast<size_t>(n * heads * cdiv(max_keys, kKeyChunk) * (head_dim + 2)) * sizeof(float);
+    return static_cast<size_t>(n * heads * cdiv(max_keys, kKeyChunk) * (head_dim + kPartHead)) * sizeof(float);
 }
 
 extern "C" int pxk_decode_attention(const float* q, const float* k_cache, const float* v_cache, int64_t seq_stride,
@@ -394,7 +415,8 @@ extern "C" int pxk_decode_attention(const float* q, const float* k_cache, const 
         return fail(PXK_ERR_WORKSPACE, "pxk_decode_attention: needs %zu workspace bytes", need);
     const int64_t chunks = cdiv(max_keys, kKeyChunk);
     if (n * heads * chunks > (int64_t{1} << 31) - 1) return fail(PXK_ERR_INVALID, "pxk_decode_attention: too large");
-    const int vec = head_dim % 4 == 0 && seq_stride % 4 == 0 && (reinterpret_cast<uintptr_t>(k_cache) & 15u) == 0;
+    const int vec = head_dim % 4 == 0 && seq_stride % 4 == 0 && aligned16(k_cache) && aligned16(v_cache) &&
+                    aligned16(workspace);
     const DecodeAttnArgs a{q,        k_cache, v_cache,  seq_stride, ctx,   workspace, pos, heads,
                            kv_heads, head_dim, window, max_keys, chunks, scale, vec};
     hipLaunchKernelGGL(decode_attention_part_kernel, dim3(static_cast<unsigned>(n * heads * chunks)), dim3(kThreads),
