@@ -51,6 +51,7 @@ BATCH, SEQ, SEED = 1, 512, 1234
 # LXT's AttnLRP (the default, and the headline metric) and Zennit's affine rules at their usual settings.
 RULES = {
     "lxt": dict(rule=0, epsilon=LXT_EPS, bias_in_denominator=True),
+    "eps": dict(rule=0, epsilon=1e-6),
     "gamma": dict(rule=1, epsilon=1e-6, gamma=0.25),
     "zplus": dict(rule=2, epsilon=1e-6, alpha=1.0, beta=0.0),
     "alpha2beta1": dict(rule=2, epsilon=1e-6, alpha=2.0, beta=1.0),
@@ -73,7 +74,7 @@ DECODE_BATCH, DECODE_PROMPT, DECODE_NEW = 4, 64, 256
 # GEMM work of one Linear's relevance relative to its forward GEMM, per rule: epsilon one transposed
 # GEMM; Gamma and AlphaBeta the reference's eight (four denominators, four backward products: here a
 # 2in x 2out stacked GEMM each way); ZBox two backward products (its denominator reuses x W).
-LINEAR_RELEVANCE_GEMMS = {"lxt": 1, "gamma": 8, "zplus": 8, "alpha2beta1": 8, "zbox": 2}
+LINEAR_RELEVANCE_GEMMS = {"lxt": 1, "eps": 1, "gamma": 8, "zplus": 8, "alpha2beta1": 8, "zbox": 2}
 
 
 def gemm_flops_per_sequence(c, L, causal_effective, linear_factor=1):
@@ -529,6 +530,7 @@ def main():
                  N.TILE_32x64_DIRECT: "32x64 direct", N.TILE_32x32_DIRECT: "32x32 direct", N.TILE_SKINNY: "skinny"}[tile]
 
     rule_text = {"lxt": "LxtAttnLrpConfig: eps 1e-9, bias in denominator",
+                 "eps": "LRPRuleConfig{1e-6}: the default pre-bias epsilon rule",
                  "gamma": "Gamma(0.25) on every Linear and the head, eps 1e-6 elsewhere",
                  "zplus": "ZPlus (AlphaBeta 1, 0) on every Linear and the head, eps 1e-6 elsewhere",
                  "alpha2beta1": "AlphaBeta(2, 1) on every Linear and the head, eps 1e-6 elsewhere",

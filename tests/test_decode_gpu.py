@@ -152,6 +152,50 @@ def test_gemma3_270m_widths_generate_and_explain():
     expect_relevance_agrees(G.host(out)[new - 1][:, :l], oracle_prefix_relevance(cfg, params, ids, l, LXT), "last")
 
 
+def test_full_gemma3_270m_decode_job_properties():
+    """The whole decode workload at its full size (Gemma-3-270m shape: 18 layers, 5 sliding : 1 full,
+    vocab 262144; batch 4, 64-token prompts, 256 new tokens), checked by properties that hold at any
+    size: every cached greedy pick is the first maximum of the uncached forward's logits over the
+    same ids (MakeNextTokenLogits), wherever that row's top-2 margin leaves the order decided, with
+    the picked logit within 1e-4; and three generated tokens' grouped explanations equal
+    explain_rows_device over their prefixes alone."""
+    n, p, T = 4, 64, 256
+    cfg = N.model_config(vocab_size=262144, hidden_size=640, num_layers=18, num_heads=4, num_kv_heads=1,
+                         head_dim=256, intermediate_size=2048, rms_norm_eps=1e-6, rope_theta=1e6, hidden_act=1,
+                         qk_norm=1, post_norms=1, norm_weight_offset=1.0,
+                         embed_scale=float(np.float32(np.sqrt(640.0))), query_pre_attn_scalar=256.0,
+                         rope_local_base=10000.0, sliding_window=512,
+                         sliding_layers=sum(1 << i for i in range(18) if i % 6 != 5))
+    lm = models.CausalLM(cfg, seed=1234, std=0.02)
+    prompts = np.random.RandomState(1234).randint(0, cfg.vocab_size, size=(n, p))
+    ids_d, ids, picked = generate(lm, prompts, T)
+    seq = ids.astype(np.int64)
+    logits = lm.forward(seq[:, :p + T - 1])[:, p - 1:]  # rows predicting columns p .. p + T - 1
+    want = logits.argmax(-1)
+    two = np.partition(logits, cfg.vocab_size - 2, axis=-1)[..., -2:]
+    first, second = two.max(-1), two.min(-1)
+    scale = np.maximum(1.0, np.abs(logits).max(-1))
+    decided = (first - second) > 1e-4 * scale
+    got = seq[:, p:]
+    assert decided.mean() > 0.9
+    np.testing.assert_array_equal(got[decided], want[decided])
+    chosen = np.take_along_axis(logits, got[..., None], -1)[..., 0]
+    assert np.all(np.abs(chosen - first) <= 1e-4 * scale)  # an undecided pick is still a maximum
+    assert np.all(np.abs(picked[:, p:] - chosen) <= 1e-4 * scale)
+    W = p + T - 1
+    out = G.empty((T, n, W))
+    lm.explain_generated_device(G.ptr(ids_d), n, p, T, ids.shape[1], LXT, G.ptr(out))
+    rel = G.host(out)
+    for t in (0, 137, T - 1):
+        l = p + t
+        pid = G.dev(np.ascontiguousarray(ids[:, :l]))
+        tg = G.dev(np.ascontiguousarray(ids[:, l]))
+        rows = G.empty((n * l,))
+        lm.explain_rows_device(G.ptr(pid), n, l, G.ptr(tg), 1, LXT, G.ptr(rows))
+        expect_relevance_agrees(rel[t][:, :l], G.host(rows).reshape(n, l), "token %d" % t)
+        assert np.all(rel[t][:, l:] == 0.0)
+
+
 def test_generate_errors_follow_the_reference():
     cfg, params, prompts, _ = dc.case("llama")
     lm = models.CausalLM(to_px(cfg), params)
