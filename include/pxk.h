@@ -188,6 +188,10 @@ int pxk_lrp_bilinear_scale(const float* r, const float* o, float* s, int64_t n, 
 int pxk_swiglu_forward(const float* gu, int64_t ld, float* gate_post, float* hidden, int64_t rows, int64_t f, int act,
                        void* stream);
 /* DeviceBackend::copy_2d (:783), accumulate_rows (:792), gather_rows (:596) */
+/* buf[k * count + i] = buf[i] for k = 1 .. copies - 1 (buf holds copies * count floats): one forward
+ * pass's activations repeated for several relevance seeds of the same sequences. No reference
+ * counterpart; it replaces rerunning the forward per copy. */
+int pxk_repeat_block(float* buf, int64_t count, int64_t copies, void* stream);
 int pxk_copy_2d(float* dst, int64_t dst_stride, const float* src, int64_t src_stride, int64_t rows, int64_t cols,
                 void* stream);
 int pxk_accumulate_rows(const float* in, float* out, int64_t rows, int64_t cols, void* stream);

@@ -98,10 +98,12 @@ private:
     /** @brief Layers, final norm and the head on the last row of each sequence: (n, vocab) logits. */
     const float* forward_last_rows(const float* ids, int64_t n, int64_t l);
     /** @brief explain_rows_device over groups * n sequences of length l (sequence g * n + b),
-     *         seeded at row l - groups + g with the id targets[g + b * target_stride]. */
+     *         seeded at row l - groups + g with the id targets[g + b * target_stride]. ids holds the
+     *         groups * n sequences, or with `replicate` the n sequences every group repeats (the
+     *         forward then runs once and its activations are repeated). */
     void explain_staggered_rows(const float* ids, int64_t n, int64_t groups, int64_t l, const float* targets,
                                 int64_t target_stride, const LRPRuleConfig& config, float* token_relevance,
-                                int64_t* targets_out, bool unit_seed);
+                                int64_t* targets_out, bool unit_seed, bool replicate);
     const float* run_forward_hidden(const float* ids, int64_t n, int64_t l);
 
     int64_t N_ = 0, L_ = 0;

@@ -29,6 +29,9 @@ public:
     [[nodiscard]] const float* data() const noexcept { return t_.data(); }
     /** @brief The size of the last ensure() (the storage may be larger). */
     [[nodiscard]] int64_t size() const noexcept { return n_; }
+    /** @brief Repeats the first `count` floats `copies` times in place (pxk_repeat_block), within
+     *         the storage an earlier, larger ensure() left; throws if that storage is too small. */
+    void repeat(MI355XBackend* be, int64_t count, int64_t copies, const char* who);
     void release() {
         t_ = Tensor();
         n_ = 0;

@@ -35,6 +35,10 @@ public:
      *         (n*l, d) buffer. The ids are validated on the device: an id outside [0, V) gathers
      *         row 0 instead and is reported by device_ids_valid(). */
     const float* run_forward_device(const float* ids, int64_t n, int64_t l);
+    /** @brief After run_forward over n sequences: repeats every activation the relevance pass reads
+     *         `copies` times in place, as if the forward had run over copies * n sequences that
+     *         repeat the n (storage from an earlier pass at least that large). */
+    void replicate_forward(int64_t copies);
     /** @brief Whether every id of the last run_forward_device() was in range (waits for the stream). */
     [[nodiscard]] bool device_ids_valid();
     /** @brief Per-token sums of a (count, d) relevance into out (count). */

@@ -81,6 +81,10 @@ public:
      *         resid + attention output into `resid_out` (the block's first residual add). */
     const float* run_forward(const float* x, int64_t n, int64_t l, const float* resid = nullptr,
                              float* resid_out = nullptr);
+    /** @brief After run_forward over n sequences: repeats every activation the relevance pass reads
+     *         `copies` times in place, as if the forward had run over copies * n sequences that
+     *         repeat the n (storage from an earlier pass at least that large). */
+    void replicate_forward(int64_t copies);
     /** @brief Fused-path relevance; `add` (nullable) is summed into the input relevance. */
     const float* run_relevance(const float* relevance_out, const LRPRuleConfig& config, const float* add = nullptr,
                                const detail::ResidualSplit& split = {});

@@ -38,6 +38,10 @@ public:
 
     /** @brief Fused-path forward into a module-owned buffer. */
     const float* run_forward(const float* x, int64_t rows);
+    /** @brief After run_forward over n sequences: repeats every activation the relevance pass reads
+     *         `copies` times in place, as if the forward had run over copies * n sequences that
+     *         repeat the n (storage from an earlier pass at least that large). */
+    void replicate_forward(int64_t copies);
     [[nodiscard]] const float* output() const noexcept { return out_.data(); }
 
 protected:

@@ -26,6 +26,10 @@ public:
     [[nodiscard]] LinearModule& down_proj() { return down_proj_; }
 
     const float* run_forward(const float* x, int64_t rows, const float* resid = nullptr, float* resid_out = nullptr);
+    /** @brief After run_forward over n sequences: repeats every activation the relevance pass reads
+     *         `copies` times in place, as if the forward had run over copies * n sequences that
+     *         repeat the n (storage from an earlier pass at least that large). */
+    void replicate_forward(int64_t copies);
     const float* run_relevance(const float* relevance_out, const LRPRuleConfig& config, const float* add = nullptr,
                                const detail::ResidualSplit& split = {});
     [[nodiscard]] const float* output() const noexcept;

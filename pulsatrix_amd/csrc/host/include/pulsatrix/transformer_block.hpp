@@ -45,6 +45,10 @@ public:
 
     /** @brief Fused-path forward; x must stay valid until the relevance pass. Returns y2. */
     const float* run_forward(const float* x, int64_t n, int64_t l);
+    /** @brief After run_forward over n sequences: repeats every activation the relevance pass reads
+     *         `copies` times in place, as if the forward had run over copies * n sequences that
+     *         repeat the n (storage from an earlier pass at least that large). */
+    void replicate_forward(int64_t copies);
     const float* run_relevance(const float* relevance_out, const LRPRuleConfig& config);
     /** @brief The epsilon split of this block's output y2 = y1 + mlp, for the GEMM that produces the
      *         block's output relevance to perform into this block's buffers. Valid after run_forward. */

@@ -234,6 +234,21 @@ const float* MultiHeadAttentionModule::run_forward(const float* x, int64_t n, in
     return oy;
 }
 
+void MultiHeadAttentionModule::replicate_forward(int64_t copies) {
+    const int64_t M = N_ * L_, qd = H_ * D_, kvd = Hkv_ * D_, w3 = qd + 2 * kvd, rw = qd + kvd;
+    const char* who = "MultiHeadAttentionModule::replicate_forward";
+    qkv_z_.repeat(be_, M * w3, copies, who);
+    if (config_.qkv_bias) qkv_y_.repeat(be_, M * w3, copies, who);
+    if (config_.use_qk_norm) qk_norm_out_.repeat(be_, M * rw, copies, who);
+    if (config_.use_rope) qk_rot_.repeat(be_, M * rw, copies, who);
+    raw_.repeat(be_, N_ * H_ * L_ * L_, copies, who);
+    p_.repeat(be_, N_ * H_ * L_ * L_, copies, who);
+    ctx_.repeat(be_, M * qd, copies, who);
+    out_z_.repeat(be_, M * d_, copies, who);
+    if (config_.out_bias) out_y_.repeat(be_, M * d_, copies, who);
+    N_ *= copies;
+}
+
 void MultiHeadAttentionModule::export_kv(KVCacheState& cache, int64_t positions) {
     if (x_ == nullptr) throw std::logic_error("MultiHeadAttentionModule::export_kv: called before any forward()");
     if (positions < L_) throw std::invalid_argument("MultiHeadAttentionModule::export_kv: the cache is shorter than the prompt");

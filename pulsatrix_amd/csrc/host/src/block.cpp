@@ -256,6 +256,32 @@ const float* TransformerBlock::run_forward(const float* x, int64_t n, int64_t l)
     return y2;
 }
 
+void SwiGLUModule::replicate_forward(int64_t copies) {
+    const char* who = "SwiGLUModule::replicate_forward";
+    gu_z_.repeat(be_, rows_ * 2 * F_, copies, who);
+    if (use_bias_) gu_y_.repeat(be_, rows_ * 2 * F_, copies, who);
+    gate_post_.repeat(be_, rows_ * F_, copies, who);
+    hidden_.repeat(be_, rows_ * F_, copies, who);
+    down_z_.repeat(be_, rows_ * d_, copies, who);
+    if (use_bias_) down_y_.repeat(be_, rows_ * d_, copies, who);
+    rows_ *= copies;
+}
+
+void TransformerBlock::replicate_forward(int64_t copies) {
+    const int64_t M = N_ * L_;
+    norm1_.replicate_forward(copies);
+    mha_.replicate_forward(copies);
+    norm2_.replicate_forward(copies);
+    swiglu_.replicate_forward(copies);
+    if (post_attn_norm_) {
+        post_attn_norm_->replicate_forward(copies);
+        post_mlp_norm_->replicate_forward(copies);
+    }
+    y1_.repeat(be_, M * d_, copies, "TransformerBlock::replicate_forward");
+    y2_.repeat(be_, M * d_, copies, "TransformerBlock::replicate_forward");
+    N_ *= copies;
+}
+
 const float* TransformerBlock::decode_step(const float* x, const float* x_normed, int64_t n, KVCacheState& cache,
                                           const int32_t* pos, RMSNormModule* next_norm, const float** next_normed) {
     float* y1 = dec_y1_.ensure(be_, n * d_);

@@ -183,16 +183,27 @@ void CausalLM::explain_rows_device(const float* ids, int64_t n, int64_t l, const
                                    const LRPRuleConfig& config, float* token_relevance, int64_t* targets_out,
                                    bool unit_seed) {
     if (n <= 0 || l <= 0) throw std::invalid_argument("CausalLM::explain_rows_device: n and l must be positive");
-    explain_staggered_rows(ids, n, 1, l, targets, target_stride, config, token_relevance, targets_out, unit_seed);
+    explain_staggered_rows(ids, n, 1, l, targets, target_stride, config, token_relevance, targets_out, unit_seed,
+                           false);
 }
 
 void CausalLM::explain_staggered_rows(const float* ids, int64_t n, int64_t groups, int64_t l, const float* targets,
                                       int64_t target_stride, const LRPRuleConfig& config, float* token_relevance,
-                                      int64_t* targets_out, bool unit_seed) {
+                                      int64_t* targets_out, bool unit_seed, bool replicate) {
     const int64_t V = config_.vocab_size, d = config_.hidden_size, S = groups * n, M = S * l;
     void* st = be_->stream();
-    // Layers and final norm over every row; the head on the seeded row of each sequence only.
-    const float* xn = run_forward_hidden(ids, S, l);
+    // Layers and final norm over every row (once over n sequences and repeated when the copies are
+    // identical); the head on the seeded row of each sequence only.
+    const float* xn = nullptr;
+    if (replicate) {
+        xn = run_forward_hidden(ids, n, l);
+        embed_.replicate_forward(groups);
+        for (auto& layer : layers_) layer->replicate_forward(groups);
+        norm_.replicate_forward(groups);
+        N_ = S;
+    } else {
+        xn = run_forward_hidden(ids, S, l);
+    }
     float* xl = last_x_.ensure(be_, S * d);
     for (int64_t g = 0; g < groups; ++g)
         be_->copy_2d(xl + g * n * d, static_cast<size_t>(d), xn + (g * n * l + l - groups + g) * d,
@@ -314,20 +325,25 @@ void CausalLM::explain_generated_device(const float* ids, int64_t n, int64_t pro
     // The model is causal, so a row sees nothing after it and the relevance of a row seeded there
     // reaches no later row: copy g's relevance over its own prefix is that of the pass over the
     // prefix alone (the later rows carry zero). Groups hold up to 16384 rows (fewer for models wider
-    // than 1024, so the pass's activations stay a few GiB); the longest comes first, so its buffers
-    // serve every later group at the same addresses.
+    // than 1024, so the pass's activations stay a few GiB). The longest group comes first and runs
+    // the forward over all its copies, which sizes every buffer; each later group holds no more
+    // rows, runs the forward once over the n prefixes and repeats its activations G times.
     constexpr int64_t kMaxGroup = 32;
-    const int64_t rows = std::clamp<int64_t>(16384 * 1024 / std::max<int64_t>(1, config_.hidden_size), 1024, 16384);
+    int64_t rows = std::clamp<int64_t>(16384 * 1024 / std::max<int64_t>(1, config_.hidden_size), 1024, 16384);
+    bool first = true;
     for (int64_t t1 = new_tokens - 1; t1 >= 0;) {
         const int64_t l = prompt + t1;
         const int64_t G = std::max<int64_t>(1, std::min<int64_t>({t1 + 1, kMaxGroup, rows / (n * l)}));
         const int64_t t0 = t1 - G + 1;
-        float* pid = prompt_ids_.ensure(be_, G * n * l);
-        for (int64_t g = 0; g < G; ++g)
+        const int64_t copies = first ? G : 1;
+        float* pid = prompt_ids_.ensure(be_, copies * n * l);
+        for (int64_t g = 0; g < copies; ++g)
             be_->copy_2d(pid + g * n * l, static_cast<size_t>(l), ids, static_cast<size_t>(ld_ids),
                          static_cast<size_t>(n), static_cast<size_t>(l));
         float* tmp = tok_tmp_.ensure(be_, G * n * l);
-        explain_staggered_rows(pid, n, G, l, ids + (l - G + 1), ld_ids, config, tmp, nullptr, unit_seed);
+        explain_staggered_rows(pid, n, G, l, ids + (l - G + 1), ld_ids, config, tmp, nullptr, unit_seed, !first);
+        if (first) rows = std::max<int64_t>(G * n * l, 1);
+        first = false;
         for (int64_t g = 0; g < G; ++g) {
             const int64_t t = t0 + g, lt = prompt + t;
             float* out = token_relevance + t * n * W;

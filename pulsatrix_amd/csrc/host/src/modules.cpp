@@ -29,6 +29,14 @@ const float* keep_input(MI355XBackend* be, DevBuf& buf, const Tensor& t) {
     return p;
 }
 
+void DevBuf::repeat(MI355XBackend* be, int64_t count, int64_t copies, const char* who) {
+    if (copies <= 1) return;
+    if (t_.numel() < count * copies)
+        throw std::logic_error(std::string(who) + ": no storage for " + std::to_string(copies) + " copies");
+    MI355XBackend::check(pxk_repeat_block(t_.data(), count, copies, be->stream()), who);
+    n_ = count * copies;
+}
+
 }  // namespace detail
 
 // ---- LinearModule (src/linear_module.cpp) ----------------------------------------------------------
@@ -158,6 +166,12 @@ const float* RMSNormModule::run_forward(const float* x, int64_t rows) {
     return out;
 }
 
+void RMSNormModule::replicate_forward(int64_t copies) {
+    out_.repeat(be_, rows_ * d_, copies, "RMSNormModule::replicate_forward");
+    rms_.repeat(be_, rows_, copies, "RMSNormModule::replicate_forward");
+    rows_ *= copies;
+}
+
 Tensor RMSNormModule::forward_impl(const Tensor& input) {
     if (input.rank() != 2 || input.shape().dim(1) != d_)
         throw std::invalid_argument("RMSNormModule::forward: input must be rank-2 (N, num_features)");
@@ -187,6 +201,12 @@ EmbeddingModule::EmbeddingModule(int64_t num_embeddings, int64_t embedding_dim, 
 void EmbeddingModule::set_weight(const std::vector<float>& values) {
     weight_ = Tensor(weight_.shape(), be_, values);
     ++version_;
+}
+
+void EmbeddingModule::replicate_forward(int64_t copies) {
+    const int64_t n = last_shape_.dim(0), l = last_shape_.dim(1);
+    out_.repeat(be_, n * l * d_, copies, "EmbeddingModule::replicate_forward");
+    last_shape_ = Shape({n * copies, l});
 }
 
 const float* EmbeddingModule::run_forward_device(const float* ids, int64_t n, int64_t l) {

@@ -256,6 +256,25 @@ __global__ void __launch_bounds__(kThreads) copy2d_kernel(float* dst, int64_t ds
     }
 }
 
+// buf[k * count + i] = buf[i] for k = 1 .. copies - 1: each thread reads a float4 of the first block
+// once and writes it into every further block.
+__global__ void __launch_bounds__(kThreads) repeat_block_vec_kernel(float* buf, int64_t count4, int64_t copies) {
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    f4* b = reinterpret_cast<f4*>(buf);
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < count4; i += stride) {
+        const f4 v = b[i];
+        for (int64_t k = 1; k < copies; ++k) b[k * count4 + i] = v;
+    }
+}
+__global__ void __launch_bounds__(kThreads) repeat_block_kernel(float* buf, int64_t count, int64_t copies) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < count; i += stride) {
+        const float v = buf[i];
+        for (int64_t k = 1; k < copies; ++k) buf[k * count + i] = v;
+    }
+}
+
 // out[j] += in[i][j] for i in order: one thread per column keeps the reference's order.
 __global__ void __launch_bounds__(kThreads) accumulate_rows_kernel(const float* in, float* out, int64_t rows,
                                                                    int64_t cols) {
@@ -381,6 +400,19 @@ int pxk_copy_2d(float* dst, int64_t ds, const float* src, int64_t ss, int64_t ro
     hipLaunchKernelGGL(copy2d_kernel, dim3(grid_for(rows * cols, kThreads)), dim3(kThreads), 0, S(stream), dst, ds, src,
                        ss, rows, cols);
     return launched("pxk_copy_2d");
+}
+
+int pxk_repeat_block(float* buf, int64_t count, int64_t copies, void* stream) {
+    if (count < 0 || copies < 1) return fail(PXK_ERR_INVALID, "pxk_repeat_block: bad sizes");
+    if (count == 0 || copies == 1) return PXK_OK;
+    if (!buf) return fail(PXK_ERR_INVALID, "pxk_repeat_block: NULL buffer");
+    if (count % 4 == 0 && aligned16(buf))
+        hipLaunchKernelGGL(repeat_block_vec_kernel, dim3(grid_for(count / 4, kThreads)), dim3(kThreads), 0, S(stream),
+                           buf, count / 4, copies);
+    else
+        hipLaunchKernelGGL(repeat_block_kernel, dim3(grid_for(count, kThreads)), dim3(kThreads), 0, S(stream), buf,
+                           count, copies);
+    return launched("pxk_repeat_block");
 }
 
 int pxk_accumulate_rows(const float* in, float* out, int64_t rows, int64_t cols, void* stream) {

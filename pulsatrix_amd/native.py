@@ -61,6 +61,7 @@ PXK_SIGNATURES = {
     "pxk_lrp_bilinear_scale": "pppifp",
     "pxk_swiglu_forward": "pippiinp",
     "pxk_copy_2d": "pipiiip",
+    "pxk_repeat_block": "piip",
     "pxk_accumulate_rows": "ppiip",
     "pxk_gather_rows": "pppiip",
     "pxk_embedding_ids": "piippp",
