@@ -723,15 +723,15 @@ __device__ __forceinline__ int kv_dim(const RelKvArgs& a, int dq, int c) {
     return d < a.D ? d : -1;
 }
 
-template <int U>
+template <int U, int DG>
 struct KvSet {
-    float s[U], p[U], q[U], v[U];
+    float s[U], p[U], q[DG][U], v[DG][U];
     unsigned ok;  // bit u: the lane's row of item u is a real row
 };
 
-template <int NW, int U>
-__device__ __forceinline__ void kv_load(KvSet<U>& r, const RelKvArgs& a, int b, int hk, int grp, int wave, int step,
-                                        int total, int nq, int i_start, int key_c, int dim_c, int g4) {
+template <int NW, int U, int DG>
+__device__ __forceinline__ void kv_load(KvSet<U, DG>& r, const RelKvArgs& a, int b, int hk, int grp, int wave, int step,
+                                        int total, int nq, int i_start, int key_c, const int* dim_c, int g4) {
     r.ok = 0;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -747,33 +747,41 @@ __device__ __forceinline__ void kv_load(KvSet<U>& r, const RelKvArgs& a, int b, 
         const int trow = b * a.l + ic;
         r.s[u] = a.s[srow + key_c];
         r.p[u] = a.p[srow + key_c];
-        r.q[u] = a.q[trow * a.ld_q + h * a.D + dim_c];
-        r.v[u] = a.spv[trow * a.ld_spv + h * a.D + dim_c];
+#pragma unroll
+        for (int g = 0; g < DG; ++g) {
+            r.q[g][u] = a.q[trow * a.ld_q + h * a.D + dim_c[g]];
+            r.v[g][u] = a.spv[trow * a.ld_spv + h * a.D + dim_c[g]];
+        }
     }
 }
 
-template <int U>
-__device__ __forceinline__ void kv_compute(const KvSet<U>& r, f4* acck, f4* accv) {
+template <int U, int DG>
+__device__ __forceinline__ void kv_compute(const KvSet<U, DG>& r, f4 (*acck)[2], f4 (*accv)[2]) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
         const bool ok = (r.ok >> u) & 1u;
         const float as = ok ? r.s[u] : 0.0f, ap = ok ? r.p[u] : 0.0f;
-        acck[u & 1] = __builtin_amdgcn_mfma_f32_16x16x4f32(as, r.q[u], acck[u & 1], 0, 0, 0);
-        accv[u & 1] = __builtin_amdgcn_mfma_f32_16x16x4f32(ap, r.v[u], accv[u & 1], 0, 0, 0);
+#pragma unroll
+        for (int g = 0; g < DG; ++g) {
+            acck[g][u & 1] = __builtin_amdgcn_mfma_f32_16x16x4f32(as, r.q[g][u], acck[g][u & 1], 0, 0, 0);
+            accv[g][u & 1] = __builtin_amdgcn_mfma_f32_16x16x4f32(ap, r.v[g][u], accv[g][u & 1], 0, 0, 0);
+        }
     }
 }
 
-// NW waves per workgroup, U items per register set.
-template <int NW, int U>
+// NW waves per workgroup, U items per register set, DG dim groups of 16 per workgroup: the score
+// rows (s, P) of a key block are read once for DG groups' query and s_pv columns.
+template <int NW, int U, int DG>
 __global__ void __launch_bounds__(NW * kWave) attn_rel_kv_kernel(const RelKvArgs a) {
-    __shared__ float red[2][NW][16][17];  // per-wave k / v partial blocks [key][dim column]
+    __shared__ float red[2][NW][16][17];  // per-wave k / v partial blocks [key][dim column], one group at a time
 
     const int lane = threadIdx.x & 63, g4 = lane >> 4, c = lane & 15;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     int id = blockIdx.x;
     if (a.remap) id = (id % 8) * (gridDim.x / 8) + id / 8;
-    const int dq = id % a.ngroups;
-    const int t = id / a.ngroups;
+    const int ngb = a.ngroups / DG;
+    const int dqb = id % ngb;
+    const int t = id / ngb;
     const int tkb = t % a.nkb, bg = t / a.nkb;
     const int kb = (tkb & 1) ? a.nkb - 1 - (tkb >> 1) : (tkb >> 1);  // long and short causal blocks alternate
     const int hk = bg % a.kv_heads, b = bg / a.kv_heads;
@@ -781,85 +789,98 @@ __global__ void __launch_bounds__(NW * kWave) attn_rel_kv_kernel(const RelKvArgs
     const int m0 = kb * 16;
 
     const int key_c = min(m0 + c, a.l - 1);
-    const int dim = kv_dim(a, dq, c);
-    const int dim_c = dim < 0 ? 0 : dim;
+    int dim_c[DG];
+#pragma unroll
+    for (int g = 0; g < DG; ++g) {
+        const int dim = kv_dim(a, dqb * DG + g, c);
+        dim_c[g] = dim < 0 ? 0 : dim;
+    }
     const int i_start = a.causal ? m0 : 0;
     const int nq = (a.l - i_start + 3) / 4;
     const int total = grp * nq;
     const int mine = total > wave ? (total - wave + NW - 1) / NW : 0;
     const int steps = (mine + U - 1) / U;
 
-    f4 acck[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
-    f4 accv[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
-    KvSet<U> s0, s1;
-    kv_load<NW, U>(s0, a, b, hk, grp, wave, 0, total, nq, i_start, key_c, dim_c, g4);
-    kv_load<NW, U>(s1, a, b, hk, grp, wave, 1, total, nq, i_start, key_c, dim_c, g4);
+    f4 acck[DG][2], accv[DG][2];
+#pragma unroll
+    for (int g = 0; g < DG; ++g)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) acck[g][h] = accv[g][h] = f4{0.f, 0.f, 0.f, 0.f};
+    KvSet<U, DG> s0, s1;
+    kv_load<NW, U, DG>(s0, a, b, hk, grp, wave, 0, total, nq, i_start, key_c, dim_c, g4);
+    kv_load<NW, U, DG>(s1, a, b, hk, grp, wave, 1, total, nq, i_start, key_c, dim_c, g4);
     __builtin_amdgcn_sched_barrier(0);
     for (int st = 0; st < steps; st += 2) {
         kv_compute(s0, acck, accv);
-        kv_load<NW, U>(s0, a, b, hk, grp, wave, st + 2, total, nq, i_start, key_c, dim_c, g4);
+        kv_load<NW, U, DG>(s0, a, b, hk, grp, wave, st + 2, total, nq, i_start, key_c, dim_c, g4);
         __builtin_amdgcn_sched_barrier(0);
         kv_compute(s1, acck, accv);
-        kv_load<NW, U>(s1, a, b, hk, grp, wave, st + 3, total, nq, i_start, key_c, dim_c, g4);
+        kv_load<NW, U, DG>(s1, a, b, hk, grp, wave, st + 3, total, nq, i_start, key_c, dim_c, g4);
         __builtin_amdgcn_sched_barrier(0);
     }
-    const f4 kk = acck[0] + acck[1], vv = accv[0] + accv[1];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        red[0][wave][4 * g4 + r][c] = kk[r];
-        red[1][wave][4 * g4 + r][c] = vv[r];
-    }
-    __syncthreads();
 
-    // Epilogue: thread -> (key row kl, dim column nn) of the 16 x 16 block.
-    if (threadIdx.x >= 256) return;
+    // Epilogue, one dim group at a time: thread -> (key row kl, dim column nn) of its 16 x 16 block.
     const int kl = threadIdx.x >> 4, nn = threadIdx.x & 15;
-    const int m = m0 + kl, d = kv_dim(a, dq, nn);
-    if (m >= a.l || d < 0) return;
-    auto sum4 = [&](int which, int col) {
-        float v = red[which][0][kl][col];
-#pragma unroll
-        for (int w = 1; w < NW; ++w) v += red[which][w][kl][col];
-        return v;
-    };
-    const int row = b * a.l + m, col = hk * a.D + d;
+    const int m = m0 + kl;
+    const int row = b * a.l + m;
     const float eps = a.eps;
-    float rk;
-    if (a.rope) {
-        const int D = a.D, half = D / 2;
-        const int i = a.rope_half ? (d < half ? d : d - half) : d / 2;
-        const int lo = a.rope_half ? i : 2 * i, hi = a.rope_half ? i + half : 2 * i + 1;
-        const int n_lo = a.rope_half ? (nn & 7) : (nn & ~1), n_hi = a.rope_half ? (nn | 8) : (nn | 1);
-        const float acc_lo = sum4(0, n_lo), acc_hi = sum4(0, n_hi);
-        const float* K = a.k + row * a.ld_k + hk * D;
-        const float y_lo = K[lo], y_hi = K[hi];
-        const float r_lo = y_lo * acc_lo, r_hi = y_hi * acc_hi;
-        const float cs = a.cos_t[m * half + i], sn = a.sin_t[m * half + i];
-        const float d0 = stab(y_lo, eps), d1 = stab(y_hi, eps);
-        const float xv = a.k_pre[row * a.ld_k_pre + col];
-        rk = 0.0f;
-        if (d == lo) {
-            rk += (xv * cs / d0) * r_lo;
-            rk += (xv * sn / d1) * r_hi;
-        } else {
-            rk += (xv * -sn / d0) * r_lo;
-            rk += (xv * cs / d1) * r_hi;
+#pragma unroll
+    for (int g = 0; g < DG; ++g) {
+        const f4 kk = acck[g][0] + acck[g][1], vv = accv[g][0] + accv[g][1];
+        if (g > 0) __syncthreads();  // the previous group's epilogue has read red
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            red[0][wave][4 * g4 + r][c] = kk[r];
+            red[1][wave][4 * g4 + r][c] = vv[r];
         }
-    } else {
-        rk = a.k[row * a.ld_k + col] * sum4(0, nn);
+        __syncthreads();
+        const int dq = dqb * DG + g;
+        const int d = kv_dim(a, dq, nn);
+        if (threadIdx.x >= 256 || m >= a.l || d < 0) continue;
+        auto sum4 = [&](int which, int col) {
+            float v = red[which][0][kl][col];
+#pragma unroll
+            for (int w = 1; w < NW; ++w) v += red[which][w][kl][col];
+            return v;
+        };
+        const int col = hk * a.D + d;
+        float rk;
+        if (a.rope) {
+            const int D = a.D, half = D / 2;
+            const int i = a.rope_half ? (d < half ? d : d - half) : d / 2;
+            const int lo = a.rope_half ? i : 2 * i, hi = a.rope_half ? i + half : 2 * i + 1;
+            const int n_lo = a.rope_half ? (nn & 7) : (nn & ~1), n_hi = a.rope_half ? (nn | 8) : (nn | 1);
+            const float acc_lo = sum4(0, n_lo), acc_hi = sum4(0, n_hi);
+            const float* K = a.k + row * a.ld_k + hk * D;
+            const float y_lo = K[lo], y_hi = K[hi];
+            const float r_lo = y_lo * acc_lo, r_hi = y_hi * acc_hi;
+            const float cs = a.cos_t[m * half + i], sn = a.sin_t[m * half + i];
+            const float d0 = stab(y_lo, eps), d1 = stab(y_hi, eps);
+            const float xv = a.k_pre[row * a.ld_k_pre + col];
+            rk = 0.0f;
+            if (d == lo) {
+                rk += (xv * cs / d0) * r_lo;
+                rk += (xv * sn / d1) * r_hi;
+            } else {
+                rk += (xv * -sn / d0) * r_lo;
+                rk += (xv * cs / d1) * r_hi;
+            }
+        } else {
+            rk = a.k[row * a.ld_k + col] * sum4(0, nn);
+        }
+        if (a.key_rel) a.key_rel[row * a.ld_rel + col] = rk;
+        const float rv = a.v[row * a.ld_v + col] * sum4(1, nn);
+        if (a.value_rel) a.value_rel[row * a.ld_rel + col] = rv;
+        if (a.rel_only) {
+            a.g_k[row * a.ld_g + col] = rk;
+            a.g_v[row * a.ld_g + col] = rv;
+            continue;
+        }
+        const float zk = a.bias_k ? a.z_k[row * a.ld_z + col] + a.bias_k[col] : a.z_k[row * a.ld_z + col];
+        a.g_k[row * a.ld_g + col] = rk / stab(zk, eps);
+        const float zv = a.bias_v ? a.z_v[row * a.ld_z + col] + a.bias_v[col] : a.z_v[row * a.ld_z + col];
+        a.g_v[row * a.ld_g + col] = rv / stab(zv, eps);
     }
-    if (a.key_rel) a.key_rel[row * a.ld_rel + col] = rk;
-    const float rv = a.v[row * a.ld_v + col] * sum4(1, nn);
-    if (a.value_rel) a.value_rel[row * a.ld_rel + col] = rv;
-    if (a.rel_only) {
-        a.g_k[row * a.ld_g + col] = rk;
-        a.g_v[row * a.ld_g + col] = rv;
-        return;
-    }
-    const float zk = a.bias_k ? a.z_k[row * a.ld_z + col] + a.bias_k[col] : a.z_k[row * a.ld_z + col];
-    a.g_k[row * a.ld_g + col] = rk / stab(zk, eps);
-    const float zv = a.bias_v ? a.z_v[row * a.ld_z + col] + a.bias_v[col] : a.z_v[row * a.ld_z + col];
-    a.g_v[row * a.ld_g + col] = rv / stab(zv, eps);
 }
 
 }  // namespace
@@ -893,8 +914,17 @@ extern "C" int pxk_attention_relevance_kv(const pxk_attn_rel_kv_desc* d, void* s
                 static_cast<int>(Hkv), static_cast<int>(D), static_cast<int>(ngroups), static_cast<int>(nkb), d->eps,
                 d->causal != 0, d->rope != 0, d->rope_half != 0, blocks % 8 == 0, d->relevance_only != 0};
     // Sixteen waves per workgroup, two items per register set: the widest spread of a long key
-    // block's rows measured fastest at 512 tokens (against 4 or 8 waves and 4 or 8 items).
-    hipLaunchKernelGGL((attn_rel_kv_kernel<16, 2>), dim3(static_cast<unsigned>(blocks)), dim3(16 * kWave), 0,
-                       S(stream), a);
+    // block's rows measured fastest at 512 tokens (against 4 or 8 waves and 4 or 8 items). Four dim
+    // groups per workgroup where they divide evenly and the grid stays above eight workgroups per
+    // CU (many sequences, or head_dim 256), so the score rows are read a quarter as often; a single
+    // 512-token sequence keeps one group per workgroup for the parallelism.
+    if (ngroups % 4 == 0 && blocks / 4 >= 2048) {
+        a.remap = (blocks / 4) % 8 == 0;
+        hipLaunchKernelGGL((attn_rel_kv_kernel<16, 2, 4>), dim3(static_cast<unsigned>(blocks / 4)), dim3(16 * kWave), 0,
+                           S(stream), a);
+    } else {
+        hipLaunchKernelGGL((attn_rel_kv_kernel<16, 2, 1>), dim3(static_cast<unsigned>(blocks)), dim3(16 * kWave), 0,
+                           S(stream), a);
+    }
     return launched("pxk_attention_relevance_kv");
 }
