@@ -82,7 +82,10 @@ enum {
     PXK_EPI_VALUE_REL = 6,   /* r = Y * acc; C = r (may be NULL); C2 = r / stab(Z + bias[n]) */
     PXK_EPI_SWIGLU_REL = 7,  /* SwiGLU relevance: rh = X * acc (X = hidden); c = Y * W (gate_post * up);
                                 rg = (c / (2c + eps sign c)) * rh; C = rg / stab(Z2 + bias[n]) (gate);
-                                C2 = rg / stab(Z3 + bias2[n]) (up). Z stays the prologue's. */
+                                C2 = rg / stab(Z3 + bias2[n]) (up). Z stays the prologue's. Without
+                                biases X, Y and W may all be NULL: gate_post = act(Z2) (gate_act),
+                                up = Z3 and hidden = gate_post * up are recomputed as the forward
+                                computed them, saving three reads per element. */
     PXK_EPI_MUL_X_SPLIT = 8, /* r = X * acc, or Y + X * acc; then the epsilon split of the residual sum
                                 W = Z2 + Z3 whose relevance r is (lrp_residual_split, lrp_math.hpp:33-38):
                                 C = (Z2 / stab(W)) * r, C2 = (Z3 / stab(W)) * r. W must hold Z2 + Z3 as the

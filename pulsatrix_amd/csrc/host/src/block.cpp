@@ -126,11 +126,15 @@ const float* SwiGLUModule::run_relevance(const float* relevance_out, const LRPRu
         d.b = mat(down_proj_.weight_data(), d_);
         d.c = mat(g, f2);
         d.c2 = mat(g + F_, f2);
-        d.x = mat(hidden_.data(), F_);
-        d.y = mat(gate_post_.data(), F_);
-        d.w = mat(gy + F_, f2);
         d.z2 = mat(gz, f2);
         d.z3 = mat(gz + F_, f2);
+        if (use_bias_) {
+            d.x = mat(hidden_.data(), F_);
+            d.y = mat(gate_post_.data(), F_);
+            d.w = mat(gy + F_, f2);
+        } else {  // the epilogue recomputes gate_post, up and hidden from the two z
+            d.gate_act = act_;
+        }
         if (use_bias_ && bid) {
             d.e_bias = mat(gate_proj_.bias_data(), 0);
             d.e_bias2 = mat(up_proj_.bias_data(), 0);

@@ -306,9 +306,20 @@ __device__ void epilogue_rows(const float* Cs, int ldc, int64_t m0, int64_t n0, 
             for (int j = 0; j < 4; ++j) v[j] = r[j] / stab(EB ? zv[j] + bv[j] : zv[j], eps);
             st4(C2 + m * g.c2.ld + n, v, vec, cnt);
         } else if constexpr (EPI == PXK_EPI_SWIGLU_REL) {
-            const f4 rh = ld4(X + m * g.x.ld + n, vec, cnt) * acc;  // hidden * (g_down @ W_down^T)
-            const f4 a = ld4(Y + m * g.y.ld + n, vec, cnt), bb = ld4(W + m * g.w.ld + n, vec, cnt);
             const f4 zg = ld4(Z2 + m * g.z2.ld + n, vec, cnt), zu = ld4(Z3 + m * g.z3.ld + n, vec, cnt);
+            f4 rh, a, bb;
+            if (X) {
+                rh = ld4(X + m * g.x.ld + n, vec, cnt) * acc;  // hidden * (g_down @ W_down^T)
+                a = ld4(Y + m * g.y.ld + n, vec, cnt);
+                bb = ld4(W + m * g.w.ld + n, vec, cnt);
+            } else {  // without biases: gate_post = act(z_gate), up = z_up, hidden = gate_post * up
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    a[j] = gate_activation(zg[j], g.gate_act);
+                    bb[j] = zu[j];
+                    rh[j] = (a[j] * bb[j]) * acc[j];
+                }
+            }
             const f4 bg = EB ? ld4(EB + n, vec, cnt) : f4{0.f, 0.f, 0.f, 0.f};
             const f4 bu = EB2 ? ld4(EB2 + n, vec, cnt) : f4{0.f, 0.f, 0.f, 0.f};
             f4 o1, o2;
@@ -1249,16 +1260,18 @@ int plan(const pxk_gemm_desc* d, Plan* p) {
         return fail(PXK_ERR_INVALID, "pxk_gemm: ADD_RESID needs C3 and X");
     if ((epi == PXK_EPI_ADD_RESID || epi == PXK_EPI_STORE_BIAS) && d->e_bias.ptr && d->c2.ptr == nullptr)
         return fail(PXK_ERR_INVALID, "pxk_gemm: a bias needs output C2");
-    if ((epi == PXK_EPI_MUL_X || epi == PXK_EPI_SPV || epi == PXK_EPI_SWIGLU_REL || epi == PXK_EPI_ROPE_REL) &&
-        d->x.ptr == nullptr)
+    if ((epi == PXK_EPI_MUL_X || epi == PXK_EPI_SPV || epi == PXK_EPI_ROPE_REL) && d->x.ptr == nullptr)
         return fail(PXK_ERR_INVALID, "pxk_gemm: epilogue %d needs X", epi);
+    if (epi == PXK_EPI_SWIGLU_REL && (d->x.ptr == nullptr) != (d->y.ptr == nullptr || d->w.ptr == nullptr))
+        return fail(PXK_ERR_INVALID, "pxk_gemm: SWIGLU_REL takes X, Y and W together, or none (recomputed from Z2, Z3)");
+    if (epi == PXK_EPI_SWIGLU_REL && d->x.ptr == nullptr && (d->e_bias.ptr || d->e_bias2.ptr || d->gate_act < 0 ||
+                                                              d->gate_act > 1))
+        return fail(PXK_ERR_INVALID, "pxk_gemm: SWIGLU_REL recomputes its factors only without biases (gate_act 0 or 1)");
     if ((epi == PXK_EPI_ROPE_REL || epi == PXK_EPI_VALUE_REL) &&
         (d->y.ptr == nullptr || d->z.ptr == nullptr || d->c2.ptr == nullptr))
         return fail(PXK_ERR_INVALID, "pxk_gemm: epilogue %d needs Y, Z and C2", epi);
-    if (epi == PXK_EPI_SWIGLU_REL && (d->y.ptr == nullptr || d->c2.ptr == nullptr))
-        return fail(PXK_ERR_INVALID, "pxk_gemm: SWIGLU_REL needs Y and C2");
-    if (epi == PXK_EPI_SWIGLU_REL && (d->w.ptr == nullptr || d->z2.ptr == nullptr || d->z3.ptr == nullptr))
-        return fail(PXK_ERR_INVALID, "pxk_gemm: SWIGLU_REL needs W, Z2 and Z3");
+    if (epi == PXK_EPI_SWIGLU_REL && (d->c2.ptr == nullptr || d->z2.ptr == nullptr || d->z3.ptr == nullptr))
+        return fail(PXK_ERR_INVALID, "pxk_gemm: SWIGLU_REL needs C2, Z2 and Z3");
     if (epi == PXK_EPI_MUL_X_SPLIT && (d->x.ptr == nullptr || d->c2.ptr == nullptr || d->w.ptr == nullptr ||
                                        d->z2.ptr == nullptr || d->z3.ptr == nullptr))
         return fail(PXK_ERR_INVALID, "pxk_gemm: MUL_X_SPLIT needs X, C2, W, Z2 and Z3");

@@ -250,3 +250,40 @@ def test_rope_rule_rejects_heads_wider_than_the_tile():
     d.cos_t = d.sin_t = 16
     assert N.pxk().pxk_gemm(ctypes.byref(d), None) == 1
     assert b"do not fit" in N.pxk().pxk_last_error()
+
+
+def gate_np(x, act):
+    x = x.astype(np.float64)
+    if act == 1:
+        return 0.5 * x * (1.0 + np.tanh(0.7978845608028654 * (x + 0.044715 * x ** 3)))
+    return x / (1.0 + np.exp(-x))
+
+
+@gpu
+@pytest.mark.parametrize("act", [0, 1])
+@pytest.mark.parametrize("tile,splits", [(0, 0), (N.TILE_128x128, 1), (N.TILE_64x64, 3), (N.TILE_32x32_DIRECT, 1)])
+def test_swiglu_rel_recomputes_its_factors_without_biases(act, tile, splits):
+    """SWIGLU_REL with X, Y and W omitted (no biases): gate_post = act(z_gate), up = z_up and hidden =
+    gate_post * up recomputed in the epilogue, against float64 numpy of the stored-operand form."""
+    m, k, F = 77, 150, 96
+    a, b = G.uniform((m, k), 1), G.uniform((F, k), 2)
+    zd, zg, zu = away((m, k), 6), G.uniform((m, F), 7, -3, 3), G.uniform((m, F), 8, -3, 3)
+    d = N.GemmDesc()
+    d.m, d.n, d.k, d.batch, d.inner, d.kgroups = m, F, k, 1, 1, 1
+    d.trans_b, d.prologue, d.epilogue, d.eps, d.gate_act = 1, N.PRO_DIV_STAB, N.EPI_SWIGLU_REL, EPS, act
+    c, c2 = G.empty((m, F)), G.empty((m, F))
+    d.a = N.operand(G.ptr(G.dev(a)).value, k)
+    d.z = N.operand(G.ptr(G.dev(zd)).value, k)
+    d.b = N.operand(G.ptr(G.dev(b)).value, k)
+    d.c, d.c2 = N.operand(G.ptr(c).value, F), N.operand(G.ptr(c2).value, F)
+    d.z2, d.z3 = N.operand(G.ptr(G.dev(zg)).value, F), N.operand(G.ptr(G.dev(zu)).value, F)
+    d.tile = tile
+    assert run(d, splits) == 0, N.pxk().pxk_last_error()
+    acc = (a.astype(np.float64) / stab(zd)) @ b.astype(np.float64).T
+    gp, up = gate_np(zg, act), zu.astype(np.float64)
+    cc = gp * up
+    rg = (cc / (2 * cc + EPS * np.where(cc >= 0, 1.0, -1.0))) * (gp * up * acc)
+    G.assert_close(G.host(c), rg / stab(zg), 1e-4, "gate share")
+    G.assert_close(G.host(c2), rg / stab(zu), 1e-4, "up share")
+    d.e_bias = N.operand(G.ptr(G.dev(zg[0])).value, 0)
+    assert N.pxk().pxk_gemm(ctypes.byref(d), G.stream()) == 1  # recomputing is only for bias-free layers
