@@ -41,6 +41,9 @@ LXT_EPS = 1e-9
 # 256 MiB copy (FETCH_SIZE x 2.0, WRITE_SIZE x 1.0); median dispatch of five. Valid for the plan
 # it was measured on.
 HEAD_REL_TRAFFIC = {"plan": (2, 32), "bytes": (341338 * 2.0 + 36864 + 19056 * 2.0 + 1152) * 1024}
+# The same for the decode step's tied head (4 x 640 x 262144, skinny NT; `bench.py --decode-probe`,
+# profiles/decode_head_gemm_traffic.md): FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0 of the median dispatch.
+DECODE_HEAD_TRAFFIC = {"plan": (7, 1), "bytes": (327831.8 * 2.0 + 4096) * 1024}
 
 S_CONFIG = dict(vocab_size=49152, hidden_size=576, num_layers=30, num_heads=9, num_kv_heads=3, head_dim=64,
                 intermediate_size=1536, rms_norm_eps=1e-5, rope_theta=100000.0, use_rope=1, rope_rotate_half=1,
@@ -235,6 +238,23 @@ def kernel_probe(torch, N, models):
     del keep
 
 
+def decode_probe(torch, N, models):
+    """Counter-collection workload for the decode line: 5 copies of 256 MiB (the calibration) and 5
+    launches of the decode step's tied head (4 x 640 x 262144, skinny NT), on the backend's stream."""
+    st = models.stream()
+    n = 64 * 1024 * 1024
+    src, dst = torch.rand(n, device="cuda"), torch.empty(n, device="cuda")
+    torch.cuda.synchronize()
+    for _ in range(5):
+        N.call("pxk_copy_2d", dst.data_ptr(), 1 << 20, src.data_ptr(), 1 << 20, 64, 1 << 20, st)
+    desc, _, keep = decode_head_gemm(torch, N, GEMMA_270M, DECODE_BATCH)
+    for _ in range(5):
+        N.gemm(desc, st)
+    models.synchronize()
+    print("decode probe: copy 256 MiB x5, decode-step tied head x5 (plan tile %d, split-K %d)" % N.gemm_plan(desc))
+    del keep
+
+
 # The raw DeviceBackend op sweep: GEMM shapes M x K x N (forward), seeded uniform(-1, 1) data.
 SWEEP_GEMMS = [(512, 576, 1536), (512, 1536, 576), (4096, 2048, 8192), (512, 576, 49152)]
 SWEEP_ELEMENTS = 1 << 26
@@ -414,7 +434,8 @@ def decode_bench(args, torch, N, models):
         "peak": HBM_PEAK_GBS,
         "unit": "GB/s",
         "frac": round(achieved / HBM_PEAK_GBS, 4),
-        "traffic": None,
+        "traffic": DECODE_HEAD_TRAFFIC["bytes"] if N.gemm_plan(desc) == DECODE_HEAD_TRAFFIC["plan"] else None,
+        "traffic_unit": "bytes per launch",
         "avg_launch_us": round(ker_s * 1e6, 2),
         "algorithmic_bytes_per_launch": int(nbytes),
     }
@@ -440,6 +461,8 @@ def main():
     ap.add_argument("--layers", type=int, default=S_CONFIG["num_layers"], help=argparse.SUPPRESS)
     ap.add_argument("--kernel-probe", action="store_true",
                     help="only launch a 256 MiB copy and the LM-head relevance GEMM, 5 times each (for rocprofv3 --pmc)")
+    ap.add_argument("--decode-probe", action="store_true",
+                    help="only launch a 256 MiB copy and the decode step's tied head, 5 times each (for rocprofv3 --pmc)")
     ap.add_argument("--op-sweep", action="store_true",
                     help="time the raw op sweep (GEMM shapes, elementwise over 2^26, RMSNorm 32768 x 2048) instead")
     ap.add_argument("--decode", action="store_true",
@@ -459,6 +482,9 @@ def main():
 
     if args.kernel_probe:
         kernel_probe(torch, N, models)
+        return
+    if args.decode_probe:
+        decode_probe(torch, N, models)
         return
     if args.op_sweep:
         op_sweep(torch, N, models)
