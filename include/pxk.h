@@ -424,10 +424,10 @@ int pxk_lrp_rule_combine(int rule, const float* x, int64_t ldx, const float* c, 
                          const float* split_b, const float* split_sum, float* r_b, float eps, void* stream);
 
 /* A sandwich block's sublayer output a, its post-norm and the residual add, then the norm that reads
- * the sum (Gemma 3, transformer_block.cpp's post_attention / post_feedforward norms followed by the
- * next pre-norm): y = x + gamma_a * a / rms(a), rms(a) = sqrt(mean(a^2) + eps_a), and, when y_norm is
- * given, y_norm = gamma_y * y / rms(y). Row-major rows x cols; replaces rms_norm_forward + add +
- * rms_norm_forward in one pass. */
+ * the sum (Gemma 3; TransformerBlock::forward_cached, transformer_block.cpp:143-151: PostNorm, add,
+ * then norm2 or the next block's norm1): y = x + gamma_a * a / rms(a), rms(a) = sqrt(mean(a^2) +
+ * eps_a), and, when y_norm is given, y_norm = gamma_y * y / rms(y). Row-major rows x cols; replaces
+ * rms_norm_forward + add + rms_norm_forward in one pass. */
 int pxk_rms_norm_add(const float* x, const float* a, const float* gamma_a, float eps_a, float* y,
                      const float* gamma_y, float eps_y, float* y_norm, int64_t rows, int64_t cols, void* stream);
 
