@@ -26,7 +26,7 @@ enum {
     PXK_OK = 0,
     PXK_ERR_INVALID = 1,  /* bad size, layout or mode: nothing was launched */
     PXK_ERR_LAUNCH = 2,   /* the HIP runtime refused the launch */
-    PXK_ERR_WORKSPACE = 3 /* a split-K GEMM was given too small a workspace */
+    PXK_ERR_WORKSPACE = 3 /* a split-K GEMM, decode attention or pick was given too small a workspace */
 };
 
 const char* pxk_last_error(void);

@@ -40,6 +40,29 @@ def test_gemm_rejects_bad_descriptors_without_launching():
     assert N.pxk().pxk_gemm(ctypes.byref(d), None) == 1
 
 
+def test_decode_and_row_entry_points_reject_bad_arguments_without_launching():
+    """CPU-side: the decode, fused-norm and repeat launchers validate on the host (the reference
+    throws on the same misuse; here the C ABI returns PXK_ERR_INVALID with a message)."""
+    lib = N.pxk()
+    p = ctypes.c_void_p(4096)
+    f = ctypes.c_float
+    # QK-Norm needs both scales
+    assert lib.pxk_decode_rope_append(p, 64, p, 64, p, 64, p, p, p, 64, 1, p, p, p, 1, 1, 1, 64, 1, 1, p, None,
+                                      f(1e-6), None) == 1
+    assert b"both" in lib.pxk_last_error()
+    # the cache must hold `positions`
+    assert lib.pxk_decode_rope_append(p, 64, p, 64, p, 64, p, p, p, 63, 1, p, p, p, 1, 1, 1, 64, 1, 1, None, None,
+                                      f(0.0), None) == 1
+    # the next norm needs its scale; NULL operands
+    assert lib.pxk_rms_norm_add(p, p, p, f(1e-6), p, None, f(1e-6), p, 4, 64, None) == 1
+    assert lib.pxk_rms_norm_add(None, p, p, f(1e-6), p, None, f(1e-6), None, 4, 64, None) == 1
+    assert lib.pxk_repeat_block(p, -1, 2, None) == 1 and lib.pxk_repeat_block(p, 8, 0, None) == 1
+    assert lib.pxk_repeat_block(p, 8, 1, None) == 0  # one copy: nothing to write
+    # the pick needs its workspace
+    assert lib.pxk_decode_pick(p, 10, 2, 10, p, 4, p, None, 0, p, None, 0, None) == 3
+    assert lib.pxk_decode_attention(p, p, p, 64, p, p, 1, 1, 1, 64, 0, 1, f(1.0), None, 0, None) == 3
+
+
 def gemm_tol(k):
     return 1e-4 * max(1.0, k / 1024.0)
 
