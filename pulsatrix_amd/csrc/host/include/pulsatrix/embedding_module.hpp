@@ -39,6 +39,8 @@ public:
      *         `copies` times in place, as if the forward had run over copies * n sequences that
      *         repeat the n (storage from an earlier pass at least that large). */
     void replicate_forward(int64_t copies);
+    /** @brief Sizes the buffers replicate_forward() repeats into for `count ids`, without computing. */
+    void reserve_forward(int64_t count);
     /** @brief Whether every id of the last run_forward_device() was in range (waits for the stream). */
     [[nodiscard]] bool device_ids_valid();
     /** @brief Per-token sums of a (count, d) relevance into out (count). */

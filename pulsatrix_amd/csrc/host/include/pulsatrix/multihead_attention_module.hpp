@@ -85,6 +85,8 @@ public:
      *         `copies` times in place, as if the forward had run over copies * n sequences that
      *         repeat the n (storage from an earlier pass at least that large). */
     void replicate_forward(int64_t copies);
+    /** @brief Sizes the buffers replicate_forward() repeats into for `n sequences of length l`, without computing. */
+    void reserve_forward(int64_t n, int64_t l);
     /** @brief Fused-path relevance; `add` (nullable) is summed into the input relevance. */
     const float* run_relevance(const float* relevance_out, const LRPRuleConfig& config, const float* add = nullptr,
                                const detail::ResidualSplit& split = {});

@@ -42,6 +42,8 @@ public:
      *         `copies` times in place, as if the forward had run over copies * n sequences that
      *         repeat the n (storage from an earlier pass at least that large). */
     void replicate_forward(int64_t copies);
+    /** @brief Sizes the buffers replicate_forward() repeats into for `rows`, without computing. */
+    void reserve_forward(int64_t rows);
     [[nodiscard]] const float* output() const noexcept { return out_.data(); }
 
 protected:

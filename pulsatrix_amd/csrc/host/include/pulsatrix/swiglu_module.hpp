@@ -30,6 +30,8 @@ public:
      *         `copies` times in place, as if the forward had run over copies * n sequences that
      *         repeat the n (storage from an earlier pass at least that large). */
     void replicate_forward(int64_t copies);
+    /** @brief Sizes the buffers replicate_forward() repeats into for `rows`, without computing. */
+    void reserve_forward(int64_t rows);
     const float* run_relevance(const float* relevance_out, const LRPRuleConfig& config, const float* add = nullptr,
                                const detail::ResidualSplit& split = {});
     [[nodiscard]] const float* output() const noexcept;

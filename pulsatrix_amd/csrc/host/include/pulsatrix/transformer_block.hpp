@@ -49,6 +49,8 @@ public:
      *         `copies` times in place, as if the forward had run over copies * n sequences that
      *         repeat the n (storage from an earlier pass at least that large). */
     void replicate_forward(int64_t copies);
+    /** @brief Sizes the buffers replicate_forward() repeats into for `n sequences of length l`, without computing. */
+    void reserve_forward(int64_t n, int64_t l);
     const float* run_relevance(const float* relevance_out, const LRPRuleConfig& config);
     /** @brief The epsilon split of this block's output y2 = y1 + mlp, for the GEMM that produces the
      *         block's output relevance to perform into this block's buffers. Valid after run_forward. */

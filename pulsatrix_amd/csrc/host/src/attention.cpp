@@ -234,6 +234,19 @@ const float* MultiHeadAttentionModule::run_forward(const float* x, int64_t n, in
     return oy;
 }
 
+void MultiHeadAttentionModule::reserve_forward(int64_t n, int64_t l) {
+    const int64_t M = n * l, qd = H_ * D_, kvd = Hkv_ * D_, w3 = qd + 2 * kvd, rw = qd + kvd;
+    qkv_z_.ensure(be_, M * w3);
+    if (config_.qkv_bias) qkv_y_.ensure(be_, M * w3);
+    if (config_.use_qk_norm) qk_norm_out_.ensure(be_, M * rw);
+    if (config_.use_rope) qk_rot_.ensure(be_, M * rw);
+    raw_.ensure(be_, n * H_ * l * l);
+    p_.ensure(be_, n * H_ * l * l);
+    ctx_.ensure(be_, M * qd);
+    out_z_.ensure(be_, M * d_);
+    if (config_.out_bias) out_y_.ensure(be_, M * d_);
+}
+
 void MultiHeadAttentionModule::replicate_forward(int64_t copies) {
     const int64_t M = N_ * L_, qd = H_ * D_, kvd = Hkv_ * D_, w3 = qd + 2 * kvd, rw = qd + kvd;
     const char* who = "MultiHeadAttentionModule::replicate_forward";

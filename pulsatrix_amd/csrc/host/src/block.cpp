@@ -260,6 +260,15 @@ const float* TransformerBlock::run_forward(const float* x, int64_t n, int64_t l)
     return y2;
 }
 
+void SwiGLUModule::reserve_forward(int64_t rows) {
+    gu_z_.ensure(be_, rows * 2 * F_);
+    if (use_bias_) gu_y_.ensure(be_, rows * 2 * F_);
+    gate_post_.ensure(be_, rows * F_);
+    hidden_.ensure(be_, rows * F_);
+    down_z_.ensure(be_, rows * d_);
+    if (use_bias_) down_y_.ensure(be_, rows * d_);
+}
+
 void SwiGLUModule::replicate_forward(int64_t copies) {
     const char* who = "SwiGLUModule::replicate_forward";
     gu_z_.repeat(be_, rows_ * 2 * F_, copies, who);
@@ -269,6 +278,20 @@ void SwiGLUModule::replicate_forward(int64_t copies) {
     down_z_.repeat(be_, rows_ * d_, copies, who);
     if (use_bias_) down_y_.repeat(be_, rows_ * d_, copies, who);
     rows_ *= copies;
+}
+
+void TransformerBlock::reserve_forward(int64_t n, int64_t l) {
+    const int64_t M = n * l;
+    norm1_.reserve_forward(M);
+    mha_.reserve_forward(n, l);
+    norm2_.reserve_forward(M);
+    swiglu_.reserve_forward(M);
+    if (post_attn_norm_) {
+        post_attn_norm_->reserve_forward(M);
+        post_mlp_norm_->reserve_forward(M);
+    }
+    y1_.ensure(be_, M * d_);
+    y2_.ensure(be_, M * d_);
 }
 
 void TransformerBlock::replicate_forward(int64_t copies) {

@@ -325,9 +325,9 @@ void CausalLM::explain_generated_device(const float* ids, int64_t n, int64_t pro
     // The model is causal, so a row sees nothing after it and the relevance of a row seeded there
     // reaches no later row: copy g's relevance over its own prefix is that of the pass over the
     // prefix alone (the later rows carry zero). Groups hold up to 16384 rows (fewer for models wider
-    // than 1024, so the pass's activations stay a few GiB). The longest group comes first and runs
-    // the forward over all its copies, which sizes every buffer; each later group holds no more
-    // rows, runs the forward once over the n prefixes and repeats its activations G times.
+    // than 1024, so the pass's activations stay a few GiB). The longest group comes first; its size
+    // sizes every forward buffer once, and each group then runs the forward once over the n
+    // prefixes and repeats its activations G times.
     constexpr int64_t kMaxGroup = 32;
     int64_t rows = std::clamp<int64_t>(16384 * 1024 / std::max<int64_t>(1, config_.hidden_size), 1024, 16384);
     bool first = true;
@@ -335,15 +335,18 @@ void CausalLM::explain_generated_device(const float* ids, int64_t n, int64_t pro
         const int64_t l = prompt + t1;
         const int64_t G = std::max<int64_t>(1, std::min<int64_t>({t1 + 1, kMaxGroup, rows / (n * l)}));
         const int64_t t0 = t1 - G + 1;
-        const int64_t copies = first ? G : 1;
-        float* pid = prompt_ids_.ensure(be_, copies * n * l);
-        for (int64_t g = 0; g < copies; ++g)
-            be_->copy_2d(pid + g * n * l, static_cast<size_t>(l), ids, static_cast<size_t>(ld_ids),
-                         static_cast<size_t>(n), static_cast<size_t>(l));
+        if (first) {  // every later group holds no more rows (and no longer rows) than this one
+            rows = std::max<int64_t>(G * n * l, 1);
+            embed_.reserve_forward(G * n * l);
+            for (auto& layer : layers_) layer->reserve_forward(G * n, l);
+            norm_.reserve_forward(G * n * l);
+            first = false;
+        }
+        float* pid = prompt_ids_.ensure(be_, n * l);
+        be_->copy_2d(pid, static_cast<size_t>(l), ids, static_cast<size_t>(ld_ids), static_cast<size_t>(n),
+                     static_cast<size_t>(l));
         float* tmp = tok_tmp_.ensure(be_, G * n * l);
-        explain_staggered_rows(pid, n, G, l, ids + (l - G + 1), ld_ids, config, tmp, nullptr, unit_seed, !first);
-        if (first) rows = std::max<int64_t>(G * n * l, 1);
-        first = false;
+        explain_staggered_rows(pid, n, G, l, ids + (l - G + 1), ld_ids, config, tmp, nullptr, unit_seed, true);
         for (int64_t g = 0; g < G; ++g) {
             const int64_t t = t0 + g, lt = prompt + t;
             float* out = token_relevance + t * n * W;

@@ -166,6 +166,11 @@ const float* RMSNormModule::run_forward(const float* x, int64_t rows) {
     return out;
 }
 
+void RMSNormModule::reserve_forward(int64_t rows) {
+    out_.ensure(be_, rows * d_);
+    rms_.ensure(be_, rows);
+}
+
 void RMSNormModule::replicate_forward(int64_t copies) {
     out_.repeat(be_, rows_ * d_, copies, "RMSNormModule::replicate_forward");
     rms_.repeat(be_, rows_, copies, "RMSNormModule::replicate_forward");
@@ -202,6 +207,8 @@ void EmbeddingModule::set_weight(const std::vector<float>& values) {
     weight_ = Tensor(weight_.shape(), be_, values);
     ++version_;
 }
+
+void EmbeddingModule::reserve_forward(int64_t count) { out_.ensure(be_, count * d_); }
 
 void EmbeddingModule::replicate_forward(int64_t copies) {
     const int64_t n = last_shape_.dim(0), l = last_shape_.dim(1);
