@@ -34,10 +34,20 @@ def gemma_decode_config():
     return gemma_config(vocab_size=300)
 
 
+def qwen3_decode_config():
+    """Qwen3-style: QK-Norm without sandwich norms, SiLU, GQA 4 / 2, llama3 RoPE scaling (the decode
+    runs past its original context of 8)."""
+    return gemma_config(vocab_size=257, hidden_size=64, num_heads=4, num_kv_heads=2, head_dim=16, hidden_act=0,
+                        qk_norm=1, post_norms=0, norm_weight_offset=0.0, embed_scale=0.0, query_pre_attn_scalar=0.0,
+                        sliding_window=0, sliding_layers=0, rope_local_base=0.0, rope_scaling=2, rope_factor=8.0,
+                        rope_low_freq_factor=1.0, rope_high_freq_factor=4.0, rope_original_max_position=8)
+
+
 CASES = {
     # name: (config factory, param seed, param std, prompt seed, n, prompt, new tokens)
     "llama": (llama_decode_config, 41, 0.2, 1, 3, 7, 12),
     "gemma": (gemma_decode_config, 43, 0.05, 2, 2, 6, 11),
+    "qwen3": (qwen3_decode_config, 47, 0.1, 3, 3, 5, 12),
 }
 
 
