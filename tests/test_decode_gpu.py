@@ -110,6 +110,29 @@ def test_grouped_explanation_matches_single_prefix_passes(name):
         assert np.all(grouped[t][:, l:] == 0.0)
 
 
+@pytest.mark.parametrize("name", ["llama", "gemma"])
+def test_grouped_explanation_under_gamma_matches_single_prefix_passes(name):
+    """The shared-forward groups under Zennit's Gamma (whose rule reads the MLP's hidden and gate
+    activations and the stacked weights) against single-prefix passes, every third token."""
+    cfg, params, prompts, new = dc.case(name)
+    lm = models.CausalLM(to_px(cfg), params)
+    ids_d, ids, _ = generate(lm, prompts, new)
+    n, p = prompts.shape
+    ld, W = ids.shape[1], p + new - 1
+    gamma = oc.lrp_rule(oc.GAMMA, epsilon=0.1, gamma=0.25)
+    out = G.empty((new, n, W))
+    lm.explain_generated_device(G.ptr(ids_d), n, p, new, ld, gamma, G.ptr(out))
+    grouped = G.host(out)
+    for t in range(0, new, 3):
+        l = p + t
+        pid = G.dev(np.ascontiguousarray(ids[:, :l]))
+        tg = G.dev(np.ascontiguousarray(ids[:, l]))
+        rows = G.empty((n * l,))
+        lm.explain_rows_device(G.ptr(pid), n, l, G.ptr(tg), 1, gamma, G.ptr(rows))
+        expect_relevance_agrees(grouped[t][:, :l], G.host(rows).reshape(n, l), "token %d" % t)
+        assert np.all(grouped[t][:, l:] == 0.0)
+
+
 def test_explain_rows_matches_the_dense_explain():
     """Seeding the last rows only (the head on n rows) against the dense explain_device (the head on
     every row) for the same targets, under LXT and Gamma."""
