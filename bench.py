@@ -14,10 +14,12 @@ ids. One step: forward logits, the argmax of the last position's logits seeded w
 to the embeddings, and per-token relevance sums. The ids are resident in HBM before the timed
 region; every step launches the whole path (a HIP graph of it in graph mode).
 
-Prints one JSON line. `roofline` is the dominant GEMM kernel's algorithmic fp32 FLOP rate (timed
-with HIP events on the backend's stream) against MI355X's 157.3 TFLOP/s dense fp32 matrix peak.
+Prints one JSON line. Per-kernel times come from the step's own launches (recorded in one eager step,
+replayed in order with HIP events on the backend's stream): `gemm_pct_peak` is the sum of 2MNK over
+the step's GEMM launches over their summed time against MI355X's 157.3 TFLOP/s dense fp32 matrix
+peak, and `roofline` is the kernel variant with the most time per step.
 `cpu_baseline` times the reference CPUBackend (oracle/_ref where built, else the oracle
-restatement) on the host cores: the same model at 1 and 3 layers, extrapolated linearly to 30.
+restatement) on the host cores: one complete pass of the same 30-layer model.
 """
 import argparse
 import ctypes
@@ -41,6 +43,12 @@ LXT_EPS = 1e-9
 # 256 MiB copy (FETCH_SIZE x 2.0, WRITE_SIZE x 1.0); median dispatch of five. Valid for the plan
 # it was measured on.
 HEAD_REL_TRAFFIC = {"plan": (2, 32), "bytes": (341338 * 2.0 + 36864 + 19056 * 2.0 + 1152) * 1024}
+# HBM bytes per launch of step kernels, by launch-log name, from rocprofv3 --pmc runs of this bench
+# (FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0, the copy calibration above; profiles/*_traffic.md). The
+# roofline line carries the figure of its kernel when that kernel was measured.
+STEP_KERNEL_TRAFFIC = {}
+if HEAD_REL_TRAFFIC["plan"] == (2, 32):
+    STEP_KERNEL_TRAFFIC["gemm 64x64 NN pro1 epi3 split32"] = HEAD_REL_TRAFFIC
 # The same for the decode step's tied head (4 x 640 x 262144, skinny NT; `bench.py --decode-probe`,
 # profiles/decode_head_gemm_traffic.md): FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0 of the median dispatch.
 DECODE_HEAD_TRAFFIC = {"plan": (7, 1), "bytes": (327831.8 * 2.0 + 4096) * 1024}
@@ -100,42 +108,42 @@ def gemm_flops_per_sequence(c, L, causal_effective, linear_factor=1):
 
 
 def time_cpu_baseline(cfg_fields, seq, rule_name="lxt"):
-    """Reference CPUBackend on the host cores, 1 and 3 layers, extrapolated to the full depth."""
+    """Reference CPUBackend (oracle/_ref where built, else the oracle restatement) on the host cores:
+    the full model, one warm-up pass at 1 layer (threads, page faults), then one complete timed
+    forward + argmax seed + relevance pass at the full depth."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import oracle_ctypes as oc
 
     rule = oc.lrp_rule(**RULES[rule_name])
-
     lib, kind = oc.ref(), "reference"
     if lib is None:
         lib, kind = oc.oracle(), "port"
+        lib.lib.pxo_set_split_threads(1)  # CPUBackend runs lrp_linear and the bilinear rule on one thread
     ids = np.random.RandomState(SEED).randint(0, cfg_fields["vocab_size"], size=(1, seq))
-    times = {}
-    for layers in (1, 3):
-        f = dict(cfg_fields, num_layers=layers)
-        cfg = oc.model_config(**f)
-        params = oc.synthetic_params(cfg, SEED)
-        lm = lib.lm(cfg, params)
+
+    def one_pass(fields):
+        cfg = oc.model_config(**fields)
+        lm = lib.lm(cfg, oc.synthetic_params(cfg, SEED))
         t0 = time.perf_counter()
         logits = lm.forward(ids)
         seed = np.zeros_like(logits)
         t = int(np.argmax(logits[0, -1]))
         seed[0, -1, t] = logits[0, -1, t]
         lm.relevance_rule(seed, rule)
-        times[layers] = time.perf_counter() - t0
-        del lm
-    per_layer = (times[3] - times[1]) / 2.0
-    full = times[1] + (cfg_fields["num_layers"] - 1) * per_layer
+        return time.perf_counter() - t0
+
+    warm = one_pass(dict(cfg_fields, num_layers=1))
+    full = one_pass(cfg_fields)
     cores = oc.oracle().lib.pxo_get_threads()
     return {
         "value": round(seq / full, 3),
         "unit": "tokens/s",
         "cores": int(cores),
         "kind": kind,
-        "sample": "1 sequence x %d tokens at the full shape with 1 and 3 of %d layers (%.1f s, %.1f s); "
-                  "time extrapolated per layer to %d layers = %.1f s; GEMMs on %d std::threads "
+        "sample": "1 sequence x %d tokens, the full %d-layer model: one complete timed forward + argmax seed + "
+                  "relevance pass (%.1f s) after a 1-layer warm-up pass (%.1f s); GEMMs on %d std::threads "
                   "(cpu_backend.cpp:38-59), everything else single-threaded"
-                  % (seq, cfg_fields["num_layers"], times[1], times[3], cfg_fields["num_layers"], full, cores),
+                  % (seq, cfg_fields["num_layers"], full, warm, cores),
         "cpu_model": cpu_model(),
         "nproc": os.cpu_count(),
     }
@@ -149,6 +157,34 @@ def cpu_model():
     except OSError:
         pass
     return "unknown"
+
+
+def summarize_launches(launches):
+    """Groups the launch log of one step by kernel variant: calls, seconds, flops and bytes per
+    step, sorted by time; plus totals per family ("gemm", "attention", "rows")."""
+    kernels, families = {}, {}
+    for r in launches:
+        for table, key in ((kernels, r["kernel"]), (families, r["family"])):
+            e = table.setdefault(key, {"kernel": key, "family": r["family"], "calls": 0, "seconds": 0.0, "flops": 0.0,
+                                       "bytes": 0.0})
+            e["calls"] += 1
+            e["seconds"] += r["seconds"]
+            e["flops"] += r["flops"]
+            e["bytes"] += r["bytes"]
+    ordered = sorted(kernels.values(), key=lambda e: -e["seconds"])
+    return {"kernels": ordered, "families": families, "seconds": sum(r["seconds"] for r in launches)}
+
+
+def kernel_row(k):
+    row = {"kernel": k["kernel"], "calls_per_step": k["calls"], "avg_us": round(k["seconds"] / k["calls"] * 1e6, 2),
+           "us_per_step": round(k["seconds"] * 1e6, 1)}
+    if k["flops"] > 0:
+        tf = k["flops"] / k["seconds"] / 1e12
+        row.update(tflops=round(tf, 2), frac=round(tf / FP32_MFMA_PEAK_TFLOPS, 4))
+    elif k["bytes"] > 0:
+        gbs = k["bytes"] / k["seconds"] / 1e9
+        row.update(gbs=round(gbs, 1), frac=round(gbs / HBM_PEAK_GBS, 4))
+    return row
 
 
 def time_kernel(torch, stream, launch, reps):
@@ -204,21 +240,6 @@ def decode_head_gemm(torch, N, c, n):
     desc.b = N.operand(E.data_ptr(), d)
     desc.c = N.operand(out.data_ptr(), V)
     return desc, 4.0 * (V * d + n * d + n * V), (H, E, out)
-
-
-def mlp_gate_up_gemm(torch, N, c, L):
-    """The MLP's [gate | up] forward GEMM as SwiGLUModule::run_forward launches it (L x d x 2F)."""
-    d, F = c["hidden_size"], c["intermediate_size"]
-    g = torch.Generator(device="cuda").manual_seed(2)
-    A = torch.randn(L, d, device="cuda", generator=g)
-    B = torch.randn(d, 2 * F, device="cuda", generator=g) * 0.02
-    C = torch.empty(L, 2 * F, device="cuda")
-    desc = N.GemmDesc()
-    desc.m, desc.n, desc.k, desc.batch, desc.inner, desc.kgroups = L, 2 * F, d, 1, 1, 1
-    desc.a = N.operand(A.data_ptr(), d)
-    desc.b = N.operand(B.data_ptr(), 2 * F)
-    desc.c = N.operand(C.data_ptr(), 2 * F)
-    return desc, 2.0 * L * d * 2 * F, (A, B, C)
 
 
 def kernel_probe(torch, N, models):
@@ -459,6 +480,8 @@ def main():
     ap.add_argument("--mode", choices=("graph", "eager"), default="graph")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--layers", type=int, default=S_CONFIG["num_layers"], help=argparse.SUPPRESS)
+    ap.add_argument("--profile-reps", type=int, default=5,
+                    help="replays of the step's recorded launches for the per-kernel times (default 5)")
     ap.add_argument("--kernel-probe", action="store_true",
                     help="only launch a 256 MiB copy and the LM-head relevance GEMM, 5 times each (for rocprofv3 --pmc)")
     ap.add_argument("--decode-probe", action="store_true",
@@ -501,6 +524,7 @@ def main():
     ids = torch.from_numpy(ids_host).cuda()
     tok = torch.empty(BATCH * SEQ, device="cuda")
     tgt = torch.empty(BATCH, dtype=torch.int64, device="cuda")
+    tok_host = torch.empty(BATCH * SEQ, pin_memory=True)  # each step's relevance D2H lands here
     torch.cuda.synchronize()
     stream = torch.cuda.ExternalStream(models.stream())
 
@@ -509,16 +533,24 @@ def main():
     def eager_step():
         lm.explain_device_rule(ids.data_ptr(), BATCH, SEQ, rule, tok.data_ptr(), tgt.data_ptr())
 
+    run = eager_step
+    if args.mode == "graph":
+        run = lm.replay
+
+    def step():
+        run()
+        with torch.cuda.stream(stream):  # the token relevance to the host, queued behind the pass
+            tok_host.copy_(tok, non_blocking=True)
+
     for _ in range(max(1, args.warmup)):
         eager_step()
     models.synchronize()
-    step = eager_step
     if args.mode == "graph":
         lm.capture_explain_rule(ids.data_ptr(), BATCH, SEQ, rule, tok.data_ptr(), tgt.data_ptr())
-        step = lm.replay
         for _ in range(max(1, args.warmup)):
             step()
         models.synchronize()
+        torch.cuda.synchronize()
     setup_s = time.perf_counter() - t_setup
 
     # ---- timed region: K steps, synchronized on both sides -------------------------------------
@@ -534,8 +566,8 @@ def main():
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     gpu_s = e0.elapsed_time(e1) * 1e-3
-    relevance = tok.cpu().numpy()
-    if not np.all(np.isfinite(relevance)):
+    relevance = tok_host.numpy().copy()
+    if not (np.all(np.isfinite(relevance)) and np.array_equal(relevance, tok.cpu().numpy())):
         print("bench.py: non-finite relevance", file=sys.stderr)
         sys.exit(1)
 
@@ -545,15 +577,20 @@ def main():
     flops_dense = gemm_flops_per_sequence(fields, SEQ, False, lf) * BATCH
     flops_causal = gemm_flops_per_sequence(fields, SEQ, True, lf) * BATCH
 
-    # ---- roofline of the dominant GEMM kernel, HIP events on the backend's stream ---------------
-    desc, flops, keep = head_relevance_gemm(torch, N, fields, SEQ)
-    ker_s = time_kernel(torch, stream, lambda: N.gemm(desc, models.stream()), 20)
-    desc2, flops2, keep2 = mlp_gate_up_gemm(torch, N, fields, SEQ)
-    ker2_s = time_kernel(torch, stream, lambda: N.gemm(desc2, models.stream()), 50)
-    achieved = flops / ker_s / 1e12
-    tile, splits = N.gemm_plan(desc)
-    tile_name = {N.TILE_128x128: "128x128", N.TILE_64x64: "64x64", N.TILE_32x64: "32x64", N.TILE_32x32: "32x32",
-                 N.TILE_32x64_DIRECT: "32x64 direct", N.TILE_32x32_DIRECT: "32x32 direct", N.TILE_SKINNY: "skinny"}[tile]
+    # ---- per-kernel times of the step's own launches, HIP events on the backend's stream ------
+    # One eager step with the launch log open records every launch (kernel variant, arguments,
+    # algorithmic work); the recorded launches are then replayed in their order with an event
+    # before each, so every kernel runs on the step's own buffers, shapes and cache state.
+    launches = models.launch_profile(eager_step, reps=args.profile_reps)
+    prof = summarize_launches(launches)
+    gemm, attn = prof["families"].get("gemm"), prof["families"].get("attention")
+    dom = prof["kernels"][0]  # the most time per step
+    dom_bound = "hbm" if dom["family"] == "rows" else "mfma"
+    if dom_bound == "mfma":
+        achieved, peak, unit = dom["flops"] / dom["seconds"] / 1e12, FP32_MFMA_PEAK_TFLOPS, "TFLOP/s"
+    else:
+        achieved, peak, unit = dom["bytes"] / dom["seconds"] / 1e9, HBM_PEAK_GBS, "GB/s"
+    traffic = STEP_KERNEL_TRAFFIC.get(dom["kernel"])
 
     rule_text = {"lxt": "LxtAttnLrpConfig: eps 1e-9, bias in denominator",
                  "eps": "LRPRuleConfig{1e-6}: the default pre-bias epsilon rule",
@@ -581,32 +618,41 @@ def main():
             "vocab": 49152, "tied": True, "rope_theta": 100000.0, "global_batch": BATCH, "seq_len": SEQ,
             "parallelism": "single GPU", "mode": args.mode,
         },
+        "timing": "value = tokens of K steps / wall time of the K back-to-back steps between synchronisations "
+                  "(a mean, not a per-step median); each step is the whole path plus an asynchronous copy of "
+                  "the token relevance to pinned host memory",
         "gpu_time_ms_per_step": round(gpu_s / args.steps * 1e3, 4),
         "path_gemm_gflop_per_step": {"dense": round(flops_dense / 1e9, 2), "causal": round(flops_causal / 1e9, 2)},
         "path_tflops_dense": round(flops_dense * args.steps / wall / 1e12, 2),
+        "gemm_pct_peak": round(100.0 * gemm["flops"] / gemm["seconds"] / 1e12 / FP32_MFMA_PEAK_TFLOPS, 2),
+        "gemm": {"launches_per_step": gemm["calls"], "gflop_per_step": round(gemm["flops"] / 1e9, 2),
+                 "ms_per_step": round(gemm["seconds"] * 1e3, 4),
+                 "tflops": round(gemm["flops"] / gemm["seconds"] / 1e12, 2),
+                 "how": "sum of 2MNK over the step's own GEMM launches / sum of their in-place event intervals "
+                        "(kernel + dispatch gap), launches replayed in step order on the step's buffers"},
+        "attention": None if attn is None else {
+            "launches_per_step": attn["calls"], "gflop_per_step_dense": round(attn["flops"] / 1e9, 2),
+            "ms_per_step": round(attn["seconds"] * 1e3, 4), "tflops_dense": round(attn["flops"] / attn["seconds"] / 1e12, 2),
+            "pct_peak_dense": round(100.0 * attn["flops"] / attn["seconds"] / 1e12 / FP32_MFMA_PEAK_TFLOPS, 2)},
+        "launches_per_step": len(launches),
+        "launch_ms_per_step": round(prof["seconds"] * 1e3, 4),
         "roofline": {
-            "kernel": "pxk_gemm NN, DIV_STAB prologue, MUL_X epilogue (LM-head relevance 512 x 576 x 49152): "
-                      "gemm_kernel %s tiles with split-K %d%s" % (tile_name, splits,
-                                                                 " + splitk_reduce_kernel" if splits > 1 else ""),
-            "bound": "mfma",
+            "kernel": dom["kernel"],
+            "why": "the kernel variant with the most time per step (%d launches per step)" % dom["calls"],
+            "bound": dom_bound,
             "achieved": round(achieved, 2),
-            "peak": FP32_MFMA_PEAK_TFLOPS,
-            "unit": "TFLOP/s",
-            "frac": round(achieved / FP32_MFMA_PEAK_TFLOPS, 4),
-            "traffic": HEAD_REL_TRAFFIC["bytes"] if (tile, splits) == HEAD_REL_TRAFFIC["plan"] else None,
-            "traffic_unit": "bytes per launch (main kernel + split-K reduce)",
-            "avg_launch_us": round(ker_s * 1e6, 2),
-            "algorithmic_gflop_per_launch": round(flops / 1e9, 3),
-            "algorithmic_bytes_per_launch": 4 * SEQ * S_CONFIG["vocab_size"] * 2 + 4 * S_CONFIG["vocab_size"] * 576 +
-                                            4 * SEQ * 576 * 2,
+            "peak": peak,
+            "unit": unit,
+            "frac": round(achieved / peak, 4),
+            "traffic": None if traffic is None else traffic["bytes"],
+            "traffic_unit": "HBM bytes per launch (FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0, copy-calibrated)",
+            "avg_launch_us": round(dom["seconds"] / dom["calls"] * 1e6, 2),
+            "algorithmic_gflop_per_launch": round(dom["flops"] / dom["calls"] / 1e9, 4),
+            "algorithmic_bytes_per_launch": int(dom["bytes"] / dom["calls"]),
         },
-        "kernels": {
-            "mlp_gate_up_512x576x3072": {"avg_us": round(ker2_s * 1e6, 2),
-                                         "tflops": round(flops2 / ker2_s / 1e12, 2)},
-        },
+        "step_kernels": [kernel_row(k) for k in prof["kernels"][:16]],
         "setup_s": round(setup_s, 1),
     }
-    del keep, keep2
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = time_cpu_baseline(fields, SEQ, args.rule)
         out["gpu_vs_cpu"] = round(value / out["cpu_baseline"]["value"], 1)

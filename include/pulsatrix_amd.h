@@ -94,6 +94,19 @@ int pxa_backend_synchronize(void);
 /* Bytes the backend's caching allocator holds (in use, cached). */
 int pxa_backend_memory(size_t* in_use, size_t* cached);
 
+/* In-process kernel timing (a profiling aid with no reference counterpart; the reference times
+ * whole calls only, docs/gpu-profiling.md). Between start and stop, every kernel launch the fused
+ * path makes on the backend is recorded with its algorithmic work (dense FLOPs for GEMM and
+ * attention kernels, HBM bytes for row kernels). pxa_launch_log_time replays the recorded
+ * launches in their order `reps` times with a HIP event on the backend's stream before each, and
+ * writes each launch's mean interval (kernel time plus the dispatch gap to the next) in seconds.
+ * The replays rewrite the recorded passes' outputs; run them after reading those. */
+int pxa_launch_log_start(void);
+int pxa_launch_log_stop(int64_t* count);
+int pxa_launch_log_entry(int64_t index, char* kernel, size_t kernel_cap, char* family, size_t family_cap,
+                         double* flops, double* bytes);
+int pxa_launch_log_time(int reps, double* seconds);
+
 /* Seeded N(0, stddev) on the host: SplitMix64 bits, Box-Muller in double (src/portable_random.hpp:11-29). */
 void pxa_fill_normal(float* dst, size_t n, uint64_t seed, double stddev);
 int64_t pxa_param_count(const px_model_config* cfg);

@@ -28,6 +28,7 @@ namespace {
 
 thread_local std::string g_error;
 int g_threads = 0;
+int g_split_threads = 1;  // threads for the ops CPUBackend runs single-threaded (split_outer)
 
 using Buf = std::vector<float>;
 
@@ -251,9 +252,27 @@ void gather_rows(const float* table, const float* idx, float* out, size_t count,
 
 // ---- LRP primitives (cpu_backend.cpp:499-566, 681-687; lrp_math.hpp) ----
 
+// Independent outer iterations [0, count) over g_split_threads threads (1 = in order on the calling
+// thread, as CPUBackend runs these ops). Each output element is still produced by one thread in
+// one order, so the results do not depend on the thread count.
+template <typename Body>
+void split_outer(size_t count, const Body& body) {
+    const size_t threads = std::min<size_t>(g_split_threads > 1 ? static_cast<size_t>(g_split_threads) : 1, count);
+    if (threads <= 1) {
+        for (size_t i = 0; i < count; ++i) body(i);
+        return;
+    }
+    std::vector<std::thread> pool;
+    for (size_t t = 0; t < threads; ++t)
+        pool.emplace_back([&body, t, threads, count] {
+            for (size_t i = t; i < count; i += threads) body(i);
+        });
+    for (auto& th : pool) th.join();
+}
+
 void lrp_linear(const float* x, const float* w, const float* z, const float* r, float* r_in, size_t rows, size_t in,
                 size_t out, float eps) {  // cpu_backend.cpp:499-508, lrp_math.hpp:21-30
-    for (size_t n = 0; n < rows; ++n)
+    split_outer(rows, [&](size_t n) {
         for (size_t i = 0; i < in; ++i) {
             float acc = 0.0f;
             const float x_i = x[n * in + i];
@@ -263,6 +282,7 @@ void lrp_linear(const float* x, const float* w, const float* z, const float* r, 
             }
             r_in[n * in + i] = acc;
         }
+    });
 }
 
 void lrp_residual_split(const float* a, const float* b, const float* r, float* ra, float* rb, size_t n,
@@ -293,7 +313,7 @@ float bilinear_scaled_r(const float* o, const float* r_o, size_t idx, float eps)
 void lrp_bilinear_matmul(const float* a, const float* b, const float* o, const float* r_o, float* r_a, float* r_b,
                          size_t slices, size_t m, size_t p, size_t q, float eps,
                          bool bt) {  // cpu_backend.cpp:524-546, lrp_math.hpp:63-86
-    for (size_t s = 0; s < slices; ++s) {
+    split_outer(slices, [&](size_t s) {
         const float* as = a + s * m * p;
         const float* bs = b + s * p * q;
         const float* os = o + s * m * q;
@@ -311,7 +331,7 @@ void lrp_bilinear_matmul(const float* a, const float* b, const float* o, const f
                 for (size_t i = 0; i < m; ++i) acc += as[i * p + j] * b_at(j, k) * bilinear_scaled_r(os, rs, i * q + k, eps);
                 r_b[s * p * q + (bt ? k * p + j : j * q + k)] = acc;
             }
-    }
+    });
 }
 
 void lrp_softmax_rows(const float* x, const float* y, const float* r, float* r_in, size_t rows,
@@ -1082,6 +1102,7 @@ extern "C" {
 
 const char* pxo_last_error(void) { return g_error.c_str(); }
 void pxo_set_threads(int threads) { g_threads = threads > 0 ? threads : 0; }
+void pxo_set_split_threads(int threads) { g_split_threads = threads > 1 ? threads : 1; }
 int pxo_get_threads(void) { return static_cast<int>(worker_threads()); }
 
 void pxo_fill_normal(float* dst, size_t n, uint64_t seed, double stddev) {

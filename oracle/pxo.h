@@ -76,6 +76,10 @@ typedef struct px_lrp_rule {
 const char* pxo_last_error(void);
 void pxo_set_threads(int threads); /* GEMM worker threads; <= 0 restores hardware_concurrency() */
 int pxo_get_threads(void);
+/* Threads over the independent rows / slices of lrp_linear and lrp_bilinear_matmul, which
+ * CPUBackend runs on one thread (default 1, its schedule). Results are identical for any count:
+ * a checker may raise it to finish sooner; the CPU baseline keeps 1. */
+void pxo_set_split_threads(int threads);
 
 /* Seeded N(0, stddev) fill: SplitMix64 bits, Box-Muller in double (src/portable_random.hpp:11-29). */
 void pxo_fill_normal(float* dst, size_t n, uint64_t seed, double stddev);

@@ -5,7 +5,7 @@
  *  causal-LM forward + AttnLRP path. Every path op is a hand-written gfx950 kernel (include/pxk.h);
  *  no hipBLAS. One in-order HIP stream per backend; the host waits only on host copies, dot() and
  *  sum() (hip_backend.hpp:64-71). Device memory comes from a size-class caching allocator with
- *  Pulsatrix's contract (bad_alloc -> release the cache -> retry once; hip_backend.hip:36-54).
+ *  Pulsatrix's contract (pulsatrix/mi355x_allocator.hpp; hip_backend.hip:36-54).
  *  DeviceBackend virtuals outside that path (convolution, pooling, batch/group norm, recurrent
  *  and state-space cells, RL, optimizer steps, dropout, losses, backward passes) throw
  *  std::logic_error naming the op.
@@ -14,43 +14,27 @@
 
 #include <cstddef>
 #include <cstdint>
-#include <mutex>
-#include <unordered_map>
+#include <functional>
+#include <memory>
+#include <string>
 #include <vector>
 
 #include "pulsatrix/device_backend.hpp"
+#include "pulsatrix/mi355x_allocator.hpp"
 #include "pxk.h"
 
 namespace pulsatrix {
 
-/** @brief Size-class cache of device blocks (the role of Pulsatrix's CachingAllocator). */
-class CachingAllocator {
-public:
-    using RawAlloc = void* (*)(size_t bytes, void* ctx);  // returns nullptr on out-of-memory
-    using RawFree = void (*)(void* ptr, void* ctx);
-    CachingAllocator(RawAlloc alloc, RawFree free, void* ctx, size_t budget_bytes);
-    ~CachingAllocator();
-    CachingAllocator(const CachingAllocator&) = delete;
-    CachingAllocator& operator=(const CachingAllocator&) = delete;
+using mi355x::CachingAllocator;
 
-    /** @brief nullptr for 0 bytes; throws std::bad_alloc when the device (or budget) is exhausted. */
-    void* allocate(size_t bytes);
-    void free(void* ptr) noexcept;
-    /** @brief Returns every cached block to the device. */
-    void release_cache() noexcept;
-    size_t bytes_in_use() const;
-    size_t bytes_cached() const;
-    static size_t round_size(size_t bytes);
-
-private:
-    RawAlloc raw_alloc_;
-    RawFree raw_free_;
-    void* ctx_;
-    size_t budget_;
-    mutable std::mutex mu_;
-    std::unordered_map<void*, size_t> live_;
-    std::unordered_map<size_t, std::vector<void*>> cache_;
-    size_t in_use_ = 0, cached_ = 0;
+/** @brief One kernel launch of the fused path, kept while a launch log is open so the launches of
+ *         a pass can be timed in place (MI355XBackend::time_launch_log). */
+struct LaunchRecord {
+    std::string kernel;  ///< kernel and variant, e.g. "gemm 32x64d NN pro0 epi2"
+    std::string family;  ///< "gemm", "attention" or "rows"
+    double flops = 0;    ///< algorithmic FLOPs of the launch (dense, as the reference computes them)
+    double bytes = 0;    ///< algorithmic HBM bytes of the launch (memory-bound kernels)
+    std::function<int(void* stream)> run;  ///< relaunches it with the same arguments
 };
 
 class MI355XBackend : public DeviceBackend {
@@ -198,18 +182,39 @@ public:
     [[nodiscard]] bool has_graph() const noexcept { return graph_exec_ != nullptr; }
     CachingAllocator& allocator() { return *allocator_; }
 
+    /** @brief Runs `f(stream)` (a pxk_* launch returning its status) and, while a launch log is
+     *         open, records it with its algorithmic work. */
+    template <class F>
+    void launch(const char* kernel, const char* family, double flops, double bytes, const char* what, F&& f) {
+        check(f(stream_), what);
+        if (logging_) log_.push_back(LaunchRecord{kernel, family, flops, bytes, std::function<int(void*)>(f)});
+        if (sync_debug_) synchronize();
+    }
+    /** @brief Opens (clearing) / closes the launch log. Every buffer a logged launch touches must
+     *         outlive the log: module buffers do; the GEMM workspace is pinned while it is open. */
+    void start_launch_log();
+    void stop_launch_log();
+    [[nodiscard]] const std::vector<LaunchRecord>& launch_log() const noexcept { return log_; }
+    /** @brief Replays the logged launches in order, `reps` times, with a HIP event on the stream
+     *         before each and after the last; seconds[i] = mean interval of launch i (its kernel
+     *         time plus the dispatch gap before the next). Logged launches rewrite their outputs. */
+    void time_launch_log(int reps, std::vector<double>& seconds);
+
 private:
     float* workspace(size_t bytes);
 
     int device_ = 0;
     void* stream_ = nullptr;
-    CachingAllocator* allocator_ = nullptr;
+    std::unique_ptr<CachingAllocator> allocator_;
     float* ws_ = nullptr;
     size_t ws_bytes_ = 0;
     float* reduce_ = nullptr;  // dot/sum partials + result slot
     void* graph_ = nullptr;
     void* graph_exec_ = nullptr;
     bool sync_debug_ = false;
+    bool logging_ = false;
+    std::vector<LaunchRecord> log_;
+    std::vector<float*> retired_ws_;  // workspaces outgrown while a log was open (logged GEMMs use them)
 };
 
 }  // namespace pulsatrix

@@ -204,9 +204,14 @@ const float* MultiHeadAttentionModule::run_forward(const float* x, int64_t n, in
     float* ctx = ctx_.ensure(be_, M * qd);
     if (fused_attention(l)) {
         // 3-5 fused: scores, mask, softmax and P V in one launch, P and raw kept for relevance.
-        MI355XBackend::check(pxk_attention_forward(q, ldq, k, ldk, v, w3, raw, p, ctx, qd, n, l, H_, Hkv_, D_,
-                                                   score_scale(), causal, st),
-                             "MultiHeadAttentionModule::forward (attention)");
+        const float scale = score_scale();
+        const int64_t H = H_, Hkv = Hkv_, D = D_;
+        // dense algorithmic work: Q K^T and P V over every (query, key) square, as the reference computes it
+        be_->launch("attn_fwd", "attention", 4.0 * n * H * l * l * D, 0.0, "MultiHeadAttentionModule::forward (attention)",
+                    [=](void* s) {
+                        return pxk_attention_forward(q, ldq, k, ldk, v, w3, raw, p, ctx, qd, n, l, H, Hkv, D, scale,
+                                                     causal, s);
+                    });
     } else {
         run_attention_unfused(q, ldq, k, ldk, v, n, l);
     }
@@ -487,7 +492,9 @@ const float* MultiHeadAttentionModule::run_relevance(const float* relevance_out,
         rd.g = g;
         rd.ld_g = w3;
         rd.relevance_only = affine;
-        MI355XBackend::check(pxk_attention_relevance_q(&rd, st), "MultiHeadAttentionModule::propagate_relevance");
+        // r_attn = P * (s_pv V^T) and r_q = Q * (s K): two L x L x D products per head
+        be_->launch("attn_rel_q", "attention", 4.0 * n * H_ * l * l * D_, 0.0,
+                    "MultiHeadAttentionModule::propagate_relevance", [rd](void* s) { return pxk_attention_relevance_q(&rd, s); });
     } else {
         relevance_scores_unfused(spv, eps, bid, affine);
     }
@@ -531,7 +538,10 @@ const float* MultiHeadAttentionModule::run_relevance(const float* relevance_out,
         kd.g_v = g + qd + kvd;
         kd.ld_g = w3;
         kd.relevance_only = affine;
-        MI355XBackend::check(pxk_attention_relevance_kv(&kd, st), "MultiHeadAttentionModule::propagate_relevance (k/v)");
+        // r_k = K * sum_h s_h^T Q_h and r_v = V * sum_h P_h^T s_pv_h: two L x L x D products per query head
+        be_->launch("attn_rel_kv", "attention", 4.0 * n * H_ * l * l * D_, 0.0,
+                    "MultiHeadAttentionModule::propagate_relevance (k/v)",
+                    [kd](void* s) { return pxk_attention_relevance_kv(&kd, s); });
     }
     // 7. the three projections' input relevance in one GEMM: x * ([g_q | g_k | g_v] [Wq | Wk | Wv]^T).
     float* r_in = r_in_.ensure(be_, M * d_);

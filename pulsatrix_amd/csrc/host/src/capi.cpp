@@ -3,7 +3,9 @@
 
 #include <hip/hip_runtime_api.h>
 
+#include <algorithm>
 #include <cmath>
+#include <cstdio>
 #include <functional>
 #include <memory>
 #include <mutex>
@@ -321,8 +323,43 @@ int pxa_backend_synchronize(void) {
 
 int pxa_backend_memory(size_t* in_use, size_t* cached) {
     return guarded([&] {
-        if (in_use) *in_use = backend()->allocator().bytes_in_use();
-        if (cached) *cached = backend()->allocator().bytes_cached();
+        const auto st = backend()->allocator().stats();
+        if (in_use) *in_use = st.in_use_bytes;
+        if (cached) *cached = st.cached_bytes;
+    });
+}
+
+int pxa_launch_log_start(void) {
+    return guarded([&] { backend()->start_launch_log(); });
+}
+
+int pxa_launch_log_stop(int64_t* count) {
+    return guarded([&] {
+        backend()->stop_launch_log();
+        if (count) *count = static_cast<int64_t>(backend()->launch_log().size());
+    });
+}
+
+int pxa_launch_log_entry(int64_t index, char* kernel, size_t kernel_cap, char* family, size_t family_cap,
+                         double* flops, double* bytes) {
+    return guarded([&] {
+        const auto& log = backend()->launch_log();
+        if (index < 0 || static_cast<size_t>(index) >= log.size())
+            throw std::invalid_argument("pxa_launch_log_entry: index outside the log");
+        const LaunchRecord& r = log[static_cast<size_t>(index)];
+        if (kernel && kernel_cap > 0) std::snprintf(kernel, kernel_cap, "%s", r.kernel.c_str());
+        if (family && family_cap > 0) std::snprintf(family, family_cap, "%s", r.family.c_str());
+        if (flops) *flops = r.flops;
+        if (bytes) *bytes = r.bytes;
+    });
+}
+
+int pxa_launch_log_time(int reps, double* seconds) {
+    return guarded([&] {
+        if (reps <= 0) throw std::invalid_argument("pxa_launch_log_time: reps must be positive");
+        std::vector<double> t;
+        backend()->time_launch_log(reps, t);
+        if (seconds) std::copy(t.begin(), t.end(), seconds);
     });
 }
 

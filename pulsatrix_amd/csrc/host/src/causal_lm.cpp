@@ -174,8 +174,11 @@ void CausalLM::explain_device(const float* ids, int64_t n, int64_t l, const LRPR
     const int64_t V = config_.vocab_size, M = n * l;
     const float* logits = run_forward(ids, n, l);
     float* seed = seed_.ensure(be_, M * V);
-    MI355XBackend::check(pxk_lm_seed(logits, n, l, V, targets_in, targets, seed, unit_seed, be_->stream()),
-                         "CausalLM::explain_device (seed)");
+    // the seed's zero fill (N L V floats) plus one scan of each sequence's last logit row
+    const std::vector<int64_t> given = targets_in ? std::vector<int64_t>(targets_in, targets_in + n) : std::vector<int64_t>();
+    be_->launch("lm_seed", "rows", 0.0, 4.0 * (M * V + n * V), "CausalLM::explain_device (seed)", [=](void* st) {
+        return pxk_lm_seed(logits, n, l, V, given.empty() ? nullptr : given.data(), targets, seed, unit_seed, st);
+    });
     embed_.token_relevance(run_relevance(seed, config), M, token_relevance);
 }
 

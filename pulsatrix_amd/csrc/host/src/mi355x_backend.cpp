@@ -4,6 +4,7 @@
 #include <hip/hip_runtime_api.h>
 
 #include <algorithm>
+#include <cstdio>
 #include <cstdlib>
 #include <cstring>
 #include <new>
@@ -25,101 +26,24 @@ void hip_check(hipError_t e, const char* what) {
 
 hipStream_t S(void* s) { return static_cast<hipStream_t>(s); }
 
-void* raw_alloc(size_t bytes, void*) {
+void* raw_alloc(size_t bytes) {
     void* p = nullptr;
-    if (hipMalloc(&p, bytes) != hipSuccess) {
+    const hipError_t e = hipMalloc(&p, bytes);
+    if (e == hipErrorOutOfMemory) {
         (void)hipGetLastError();  // clear the sticky out-of-memory status before a retry
-        return nullptr;
+        throw std::bad_alloc();
     }
+    hip_check(e, "MI355XBackend::allocate (hipMalloc)");
     return p;
 }
 
-void raw_free(void* p, void*) { (void)hipFree(p); }
+void raw_free(void* p) { (void)hipFree(p); }
 
 pxk_operand op(const float* p, int64_t ld) { return pxk_operand{p, ld, 0, 0, 0, 0}; }
 
 constexpr size_t kReduceFloats = 1024 + 64;
 
 }  // namespace
-
-// ---- CachingAllocator --------------------------------------------------------------------------
-
-CachingAllocator::CachingAllocator(RawAlloc alloc, RawFree free, void* ctx, size_t budget_bytes)
-    : raw_alloc_(alloc), raw_free_(free), ctx_(ctx), budget_(budget_bytes) {}
-
-CachingAllocator::~CachingAllocator() {
-    release_cache();
-    std::lock_guard<std::mutex> lock(mu_);
-    for (auto& [p, size] : live_) raw_free_(p, ctx_);
-    live_.clear();
-}
-
-size_t CachingAllocator::round_size(size_t bytes) {
-    // 512 B granules below 1 MiB, then 1 MiB granules: a reused activation of the same shape hits.
-    const size_t small = 512, big = size_t{1} << 20;
-    return bytes < big ? (bytes + small - 1) / small * small : (bytes + big - 1) / big * big;
-}
-
-void* CachingAllocator::allocate(size_t bytes) {
-    if (bytes == 0) return nullptr;
-    const size_t size = round_size(bytes);
-    std::lock_guard<std::mutex> lock(mu_);
-    auto it = cache_.find(size);
-    if (it != cache_.end() && !it->second.empty()) {
-        void* p = it->second.back();
-        it->second.pop_back();
-        cached_ -= size;
-        live_.emplace(p, size);
-        in_use_ += size;
-        return p;
-    }
-    auto attempt = [&]() -> void* {
-        if (budget_ > 0 && in_use_ + cached_ + size > budget_) return nullptr;
-        return raw_alloc_(size, ctx_);
-    };
-    void* p = attempt();
-    if (p == nullptr) {  // out of memory: give the cache back and retry once
-        for (auto& [sz, blocks] : cache_)
-            for (void* b : blocks) raw_free_(b, ctx_);
-        cache_.clear();
-        cached_ = 0;
-        p = attempt();
-    }
-    if (p == nullptr) throw std::bad_alloc();
-    live_.emplace(p, size);
-    in_use_ += size;
-    return p;
-}
-
-void CachingAllocator::free(void* ptr) noexcept {
-    if (ptr == nullptr) return;
-    std::lock_guard<std::mutex> lock(mu_);
-    auto it = live_.find(ptr);
-    if (it == live_.end()) return;
-    const size_t size = it->second;
-    live_.erase(it);
-    in_use_ -= size;
-    cache_[size].push_back(ptr);
-    cached_ += size;
-}
-
-void CachingAllocator::release_cache() noexcept {
-    std::lock_guard<std::mutex> lock(mu_);
-    for (auto& [sz, blocks] : cache_)
-        for (void* b : blocks) raw_free_(b, ctx_);
-    cache_.clear();
-    cached_ = 0;
-}
-
-size_t CachingAllocator::bytes_in_use() const {
-    std::lock_guard<std::mutex> lock(mu_);
-    return in_use_;
-}
-
-size_t CachingAllocator::bytes_cached() const {
-    std::lock_guard<std::mutex> lock(mu_);
-    return cached_;
-}
 
 // ---- MI355XBackend -------------------------------------------------------------------------------
 
@@ -134,8 +58,11 @@ MI355XBackend::MI355XBackend(int device_index) : device_(device_index) {
     stream_ = s;
     size_t budget = 0;
     if (const char* mb = std::getenv("PULSATRIX_HIP_MEMORY_BUDGET_MB")) budget = std::strtoull(mb, nullptr, 10) << 20;
-    sync_debug_ = std::getenv("PULSATRIX_HIP_SYNC_DEBUG") != nullptr;
-    allocator_ = new CachingAllocator(raw_alloc, raw_free, nullptr, budget);
+    const char* debug = std::getenv("PULSATRIX_HIP_SYNC_DEBUG");
+    sync_debug_ = debug != nullptr && std::string(debug) == "1";
+    allocator_ = std::make_unique<CachingAllocator>(
+        raw_alloc, raw_free, [this] { hip_check(hipStreamSynchronize(S(stream_)), "MI355XBackend (allocator)"); },
+        budget);
     reduce_ = static_cast<float*>(allocator_->allocate(kReduceFloats * sizeof(float)));
 }
 
@@ -143,7 +70,7 @@ MI355XBackend::~MI355XBackend() {
     if (stream_) (void)hipStreamSynchronize(S(stream_));
     if (graph_exec_) (void)hipGraphExecDestroy(static_cast<hipGraphExec_t>(graph_exec_));
     if (graph_) (void)hipGraphDestroy(static_cast<hipGraph_t>(graph_));
-    delete allocator_;
+    allocator_.reset();  // synchronizes, then returns every block, before the stream goes away
     if (stream_) (void)hipStreamDestroy(S(stream_));
 }
 
@@ -197,7 +124,10 @@ void MI355XBackend::fill(void* ptr, float value, size_t n) {
 
 float* MI355XBackend::workspace(size_t bytes) {
     if (bytes > ws_bytes_) {
-        if (ws_) allocator_->free(ws_);
+        if (ws_ && logging_)
+            retired_ws_.push_back(ws_);  // a logged GEMM still points at it
+        else if (ws_)
+            allocator_->free(ws_);
         ws_bytes_ = std::max(bytes, ws_bytes_ * 2);
         ws_ = static_cast<float*>(allocator_->allocate(ws_bytes_));
     }
@@ -211,7 +141,55 @@ void MI355XBackend::run_gemm(pxk_gemm_desc& d) {
         d.workspace_bytes = ws_bytes_;
     }
     check(pxk_gemm(&d, stream_), "MI355XBackend gemm");
+    if (logging_) {
+        int32_t tile = 0, splits = 0;
+        check(pxk_gemm_plan(&d, &tile, &splits), "MI355XBackend gemm (plan)");
+        static const char* const kTile[] = {"auto", "128x128", "64x64", "32x64", "32x32", "32x64d", "32x32d", "skinny"};
+        char name[96];
+        std::snprintf(name, sizeof(name), "gemm %s %s%s pro%d epi%d split%d", kTile[tile >= 0 && tile <= 7 ? tile : 0],
+                      d.trans_a ? "T" : "N", d.trans_b ? "T" : "N", d.prologue, d.epilogue, splits);
+        const pxk_gemm_desc copy = d;
+        log_.push_back(LaunchRecord{name, "gemm", 2.0 * d.m * d.n * d.k * d.batch * d.kgroups, 0.0,
+                                    [copy](void* st) { return pxk_gemm(&copy, st); }});
+    }
     if (sync_debug_) synchronize();
+}
+
+void MI355XBackend::start_launch_log() {
+    log_.clear();
+    for (float* w : retired_ws_) allocator_->free(w);
+    retired_ws_.clear();
+    logging_ = true;
+}
+
+void MI355XBackend::stop_launch_log() { logging_ = false; }
+
+void MI355XBackend::time_launch_log(int reps, std::vector<double>& seconds) {
+    const size_t n = log_.size();
+    seconds.assign(n, 0.0);
+    if (n == 0 || reps <= 0) return;
+    std::vector<hipEvent_t> ev(n + 1, nullptr);
+    for (auto& e : ev) hip_check(hipEventCreate(&e), "MI355XBackend::time_launch_log (event)");
+    try {
+        for (const auto& r : log_) check(r.run(stream_), "MI355XBackend::time_launch_log (warm-up)");
+        for (int rep = 0; rep < reps; ++rep) {
+            for (size_t i = 0; i < n; ++i) {
+                hip_check(hipEventRecord(ev[i], S(stream_)), "MI355XBackend::time_launch_log (record)");
+                check(log_[i].run(stream_), "MI355XBackend::time_launch_log");
+            }
+            hip_check(hipEventRecord(ev[n], S(stream_)), "MI355XBackend::time_launch_log (record)");
+            hip_check(hipEventSynchronize(ev[n]), "MI355XBackend::time_launch_log (wait)");
+            for (size_t i = 0; i < n; ++i) {
+                float ms = 0.0f;
+                hip_check(hipEventElapsedTime(&ms, ev[i], ev[i + 1]), "MI355XBackend::time_launch_log (elapsed)");
+                seconds[i] += 1e-3 * ms / reps;
+            }
+        }
+    } catch (...) {
+        for (auto& e : ev) (void)hipEventDestroy(e);
+        throw;
+    }
+    for (auto& e : ev) (void)hipEventDestroy(e);
 }
 
 void MI355XBackend::gemm(const float* a, const float* b, float* out, size_t m, size_t k, size_t n) {

@@ -161,8 +161,12 @@ const float* RMSNormModule::run_forward(const float* x, int64_t rows) {
     rows_ = rows;
     float* out = out_.ensure(be_, rows * d_);
     float* rms = rms_.ensure(be_, rows);
-    MI355XBackend::check(pxk_rms_norm_forward(x, effective_gamma(), out, rms, rows, d_, eps_, be_->stream()),
-                         "RMSNormModule::forward");
+    const float* gamma = effective_gamma();
+    const int64_t d = d_;
+    const float eps = eps_;
+    // x read, out written (8 B per element), one rms per row
+    be_->launch("rms_norm", "rows", 0.0, 8.0 * rows * d + 4.0 * (rows + d), "RMSNormModule::forward",
+                [=](void* st) { return pxk_rms_norm_forward(x, gamma, out, rms, rows, d, eps, st); });
     return out;
 }
 
@@ -224,10 +228,12 @@ const float* EmbeddingModule::run_forward_device(const float* ids, int64_t n, in
     // and reported through ids_status()); the host never waits for them.
     float* checked = ids_checked_.ensure(be_, count);
     auto* status = reinterpret_cast<int32_t*>(ids_status_.ensure(be_, 1));
-    MI355XBackend::check(pxk_embedding_ids(ids, count, num_embeddings(), checked, status, be_->stream()),
-                         "EmbeddingModule::forward");
-    MI355XBackend::check(pxk_gather_rows(weight_.data(), checked, out, count, d_, be_->stream()),
-                         "EmbeddingModule::forward");
+    const int64_t V = num_embeddings(), d = d_;
+    const float* table = weight_.data();
+    be_->launch("embedding_ids", "rows", 0.0, 8.0 * count, "EmbeddingModule::forward",
+                [=](void* st) { return pxk_embedding_ids(ids, count, V, checked, status, st); });
+    be_->launch("gather_rows", "rows", 0.0, 8.0 * count * d + 4.0 * count, "EmbeddingModule::forward",
+                [=](void* st) { return pxk_gather_rows(table, checked, out, count, d, st); });
     return out;
 }
 
@@ -255,8 +261,9 @@ Tensor EmbeddingModule::forward_impl(const Tensor& input) {
 }
 
 void EmbeddingModule::token_relevance(const float* relevance, int64_t count, float* out) {
-    MI355XBackend::check(pxk_row_sums(relevance, out, count, d_, be_->stream()),
-                         "EmbeddingModule::propagate_relevance");
+    const int64_t d = d_;
+    be_->launch("row_sums", "rows", 0.0, 4.0 * count * (d + 1), "EmbeddingModule::propagate_relevance",
+                [=](void* st) { return pxk_row_sums(relevance, out, count, d, st); });
 }
 
 Tensor EmbeddingModule::propagate_relevance(const Tensor& relevance_out, const LRPRuleConfig&) {

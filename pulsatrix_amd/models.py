@@ -196,3 +196,29 @@ def stream():
 
 def synchronize():
     N.host_check(N.host().pxa_backend_synchronize())
+
+
+def launch_profile(run_once, reps=5):
+    """Records every kernel launch of one call of run_once() on the backend (pxa_launch_log_*), then
+    replays those launches in order `reps` times with a HIP event before each. Returns one dict per
+    launch: kernel (name and variant), family ("gemm", "attention", "rows"), algorithmic flops and
+    bytes, and seconds (mean interval: kernel time plus the dispatch gap to the next launch). The
+    replays rewrite the outputs of the recorded pass."""
+    h = N.host()
+    N.host_check(h.pxa_launch_log_start())
+    try:
+        run_once()
+    finally:
+        count = ctypes.c_int64(0)
+        N.host_check(h.pxa_launch_log_stop(ctypes.byref(count)))
+    n = count.value
+    secs = (ctypes.c_double * max(n, 1))()
+    N.host_check(h.pxa_launch_log_time(reps, secs))
+    out = []
+    for i in range(n):
+        kernel, family = ctypes.create_string_buffer(160), ctypes.create_string_buffer(32)
+        flops, nbytes = ctypes.c_double(0), ctypes.c_double(0)
+        N.host_check(h.pxa_launch_log_entry(i, kernel, 160, family, 32, ctypes.byref(flops), ctypes.byref(nbytes)))
+        out.append({"kernel": kernel.value.decode(), "family": family.value.decode(), "flops": flops.value,
+                    "bytes": nbytes.value, "seconds": secs[i]})
+    return out

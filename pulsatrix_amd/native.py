@@ -284,6 +284,12 @@ def host():
             "pxa_backend_stream": (c_vp, []),
             "pxa_backend_synchronize": (ctypes.c_int, []),
             "pxa_backend_memory": (ctypes.c_int, [ctypes.POINTER(ctypes.c_size_t), ctypes.POINTER(ctypes.c_size_t)]),
+            "pxa_launch_log_start": (ctypes.c_int, []),
+            "pxa_launch_log_stop": (ctypes.c_int, [ctypes.POINTER(c_i64)]),
+            "pxa_launch_log_entry": (ctypes.c_int, [c_i64, ctypes.c_char_p, ctypes.c_size_t, ctypes.c_char_p,
+                                                    ctypes.c_size_t, ctypes.POINTER(ctypes.c_double),
+                                                    ctypes.POINTER(ctypes.c_double)]),
+            "pxa_launch_log_time": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(ctypes.c_double)]),
             "pxa_fill_normal": (None, [c_vp, ctypes.c_size_t, ctypes.c_uint64, ctypes.c_double]),
             "pxa_param_count": (c_i64, [cfgp]),
             "pxa_block_param_count": (c_i64, [cfgp]),

@@ -277,6 +277,10 @@ def oracle():
         L.pxo_block_param_count.restype = ctypes.c_int64
         L.pxo_set_threads.argtypes = [ctypes.c_int]
         L.pxo_get_threads.restype = ctypes.c_int
+        L.pxo_set_split_threads.argtypes = [ctypes.c_int]
+        # As a checker the oracle may spread lrp_linear / lrp_bilinear_matmul over threads (the same
+        # numbers for any count); the CPU baseline sets 1 again, CPUBackend's schedule.
+        L.pxo_set_split_threads(min(16, os.cpu_count() or 1))
         L.pxo_rope_tables.argtypes = [ctypes.c_int64, ctypes.c_float, ctypes.c_int64, ctypes.c_int64, _f32p, _f32p]
     return _oracle
 
