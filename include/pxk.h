@@ -152,6 +152,17 @@ typedef struct pxk_gemm_desc {
 size_t pxk_gemm_workspace(const pxk_gemm_desc* d);
 int pxk_gemm(const pxk_gemm_desc* d, void* stream);
 
+/* pxk_gemm without a workspace argument and without any allocation: the split-K partials live in a
+ * static device array of PXK_GEMM_SCRATCH_BYTES per GPU, held until the process ends (its device
+ * address is looked up once per device, on the first call there). d->workspace is ignored. The
+ * plan, kernels and results are pxk_gemm's for the same descriptor; a plan whose partials exceed
+ * the scratch returns PXK_ERR_WORKSPACE before any launch. The array is shared by every call on a
+ * GPU and keeps the last call's partials: calls that overlap on one GPU (other streams, other
+ * threads) race. It has no counterpart in the reference: it is for callers that cannot allocate
+ * (code under HIP graph capture, serving loops, harnesses that forbid hipMalloc). */
+#define PXK_GEMM_SCRATCH_BYTES ((size_t)64 << 20)
+int pxk_gemm_noalloc(const pxk_gemm_desc* d, void* stream);
+
 /* The tile shape (PXK_TILE_*) and split-K count pxk_gemm would launch for this descriptor, after
  * the same validation. Introspection for tuning and tests; no reference counterpart. */
 int pxk_gemm_plan(const pxk_gemm_desc* d, int32_t* tile, int32_t* splits);

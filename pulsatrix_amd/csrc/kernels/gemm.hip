@@ -31,6 +31,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstring>
+#include <mutex>
 #include <type_traits>
 #include <utility>
 
@@ -1497,6 +1498,63 @@ extern "C" int pxk_gemm(const pxk_gemm_desc* d, void* stream) {
         return launched("pxk_gemm split-K reduce");
     }
     return PXK_OK;
+}
+
+// ---- the allocation-free variant ------------------------------------------------------------------
+// Split-K partials in a file-scope device array instead of a caller's workspace. Each GPU the library
+// runs on holds its own copy of the array (PXK_GEMM_SCRATCH_BYTES) until the process ends. Its
+// device address is looked up once per device with hipGetSymbolAddress: in host code the array's
+// name is only a host-side stand-in, never a device address.
+static __device__ __align__(256) float scratch[PXK_GEMM_SCRATCH_BYTES / sizeof(float)];
+
+namespace pxk {
+namespace {
+
+constexpr int kScratchDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch[kScratchDevices] = {};
+
+// The current device's copy of `scratch`, looked up on its first use on that device.
+int scratch_ptr(float** out) {
+    int dev = -1;
+    const hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return fail(PXK_ERR_LAUNCH, "pxk_gemm_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+    if (dev < 0 || dev >= kScratchDevices) return fail(PXK_ERR_INVALID, "pxk_gemm_noalloc: device %d out of range", dev);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch[dev] == nullptr) {
+        void* p = nullptr;
+        const hipError_t r = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (r != hipSuccess || p == nullptr)
+            return fail(PXK_ERR_LAUNCH, "pxk_gemm_noalloc: hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                        hipGetErrorString(r));
+        g_scratch[dev] = static_cast<float*>(p);
+    }
+    *out = g_scratch[dev];
+    return PXK_OK;
+}
+
+}  // namespace
+}  // namespace pxk
+
+extern "C" int pxk_gemm_noalloc(const pxk_gemm_desc* d, void* stream) {
+    if (d == nullptr) return fail(PXK_ERR_INVALID, "pxk_gemm_noalloc: descriptor is NULL");
+    if (d->m == 0 || d->n == 0 || d->batch == 0) return PXK_OK;
+    Plan p;
+    if (const int rc = plan(d, &p)) return rc;
+    const size_t need = workspace_bytes(d, p);
+    if (need > PXK_GEMM_SCRATCH_BYTES)
+        return fail(PXK_ERR_WORKSPACE,
+                    "pxk_gemm_noalloc: split-K %d needs %zu bytes of partials, above the %zu-byte static scratch "
+                    "(request fewer splits, or call pxk_gemm with a workspace)",
+                    p.splits, need, static_cast<size_t>(PXK_GEMM_SCRATCH_BYTES));
+    pxk_gemm_desc e = *d;
+    e.workspace = nullptr;
+    e.workspace_bytes = 0;
+    if (need > 0) {
+        if (const int rc = scratch_ptr(&e.workspace)) return rc;
+        e.workspace_bytes = PXK_GEMM_SCRATCH_BYTES;  // the plan does not depend on the workspace: pxk_gemm
+    }                                                // recomputes the one checked above
+    return pxk_gemm(&e, stream);
 }
 
 extern "C" int pxk_gemm_ex(const float* a, int ta, const float* b, int tb, float* out, int64_t m, int64_t k, int64_t n,

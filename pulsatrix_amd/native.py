@@ -127,6 +127,8 @@ def pxk():
         lib.pxk_version.restype = ctypes.c_char_p
         lib.pxk_gemm.restype = ctypes.c_int
         lib.pxk_gemm.argtypes = [ctypes.POINTER(GemmDesc), c_vp]
+        lib.pxk_gemm_noalloc.restype = ctypes.c_int
+        lib.pxk_gemm_noalloc.argtypes = [ctypes.POINTER(GemmDesc), c_vp]
         lib.pxk_gemm_workspace.restype = ctypes.c_size_t
         lib.pxk_gemm_workspace.argtypes = [ctypes.POINTER(GemmDesc)]
         lib.pxk_gemm_plan.restype = ctypes.c_int
