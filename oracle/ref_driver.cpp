@@ -1,9 +1,16 @@
-// ref_driver.cpp -- C API over the reference's own CPUBackend, TransformerBlock and CausalLM.
+// ref_driver.cpp -- C API over the reference's own TransformerBlock, CausalLM, LinearModule and
+// LRP::explain, on one of two backends.
 //
 // TEST INFRASTRUCTURE ONLY. Compiled by oracle/Makefile together with the reference's path
-// sources, read where they lie under /root/reference (nothing is copied), into
-// oracle/_ref/libpxref.so. The entry points mirror oracle/pxo.h with a pxr_ prefix, so the tests
-// can run the oracle restatement and the real reference on identical inputs.
+// sources, read where they lie under /root/reference (nothing is copied):
+//   * oracle/_ref/libpxref.so         on the reference's own CPUBackend: the entry points mirror
+//                                     oracle/pxo.h with a pxr_ prefix, so the tests run the oracle
+//                                     restatement and the real reference on identical inputs;
+//   * oracle/_ref/libpxref_mi355x.so  (PXR_ON_MI355X) the same reference modules on MI355XBackend,
+//                                     compiled against the reference's own DeviceBackend header:
+//                                     the drop-in, run. It adds pxr_be_*, a shim that calls each
+//                                     DeviceBackend virtual on device pointers, for the primitive
+//                                     tests; its declarations live only here and in the tests.
 
 #include <algorithm>
 #include <cstdint>
@@ -15,10 +22,16 @@
 
 #include "pulsatrix/causal_lm.hpp"
 #include "pulsatrix/cpu_backend.hpp"
+#include "pulsatrix/explainer_context.hpp"
 #include "pulsatrix/hf_model.hpp"
 #include "pulsatrix/linear_module.hpp"
+#include "pulsatrix/lrp.hpp"
 #include "pulsatrix/lrp_rule_config.hpp"
+#include "pulsatrix/relu_module.hpp"
 #include "pulsatrix/transformer_block.hpp"
+#ifdef PXR_ON_MI355X
+#include "pulsatrix/mi355x_backend.hpp"
+#endif
 
 #include "pxo.h"
 
@@ -27,6 +40,18 @@ using namespace pulsatrix;
 namespace {
 
 thread_local std::string g_error;
+
+// The backend every model of this library runs on: the reference's CPUBackend, or one
+// process-wide MI355XBackend on device 0 (created on first use, kept until the process ends).
+DeviceBackend* driver_backend() {
+#ifdef PXR_ON_MI355X
+    static MI355XBackend* be = new MI355XBackend(0);
+    return be;
+#else
+    static CPUBackend be;
+    return &be;
+#endif
+}
 
 template <typename F>
 int guarded(F&& f) {
@@ -155,13 +180,13 @@ void load(Module& m, const std::vector<std::pair<std::string, int64_t>>& layout,
 }
 
 struct RefBlock {
-    CPUBackend be;
+    DeviceBackend* be = driver_backend();
     std::unique_ptr<TransformerBlock> block;
     int64_t n = 0, l = 0, d = 0;
 };
 
 struct RefLM {
-    CPUBackend be;
+    DeviceBackend* be = driver_backend();
     std::unique_ptr<CausalLM> lm;
     px_model_config c{};
     int64_t n = 0, l = 0;
@@ -195,9 +220,9 @@ void* pxr_block_create(const px_model_config* cfg, const float* params) {
     RefBlock* out = nullptr;
     guarded([&] {
         auto b = std::make_unique<RefBlock>();
-        b->block = std::make_unique<TransformerBlock>(attention_config(*cfg), cfg->intermediate_size, &b->be,
+        b->block = std::make_unique<TransformerBlock>(attention_config(*cfg), cfg->intermediate_size, b->be,
                                                       block_options(*cfg));
-        load(*b->block, block_layout(*cfg), params, &b->be);
+        load(*b->block, block_layout(*cfg), params, b->be);
         b->d = cfg->hidden_size;
         out = b.release();
     });
@@ -209,7 +234,7 @@ int pxr_block_forward(void* h, const float* x, int64_t n, int64_t l, float* y) {
         auto* b = static_cast<RefBlock*>(h);
         b->n = n;
         b->l = l;
-        Tensor in(Shape({n, l, b->d}), &b->be, std::vector<float>(x, x + n * l * b->d));
+        Tensor in(Shape({n, l, b->d}), b->be, std::vector<float>(x, x + n * l * b->d));
         const std::vector<float> out = b->block->forward(in).to_host_vector();
         std::copy(out.begin(), out.end(), y);
     });
@@ -218,7 +243,7 @@ int pxr_block_forward(void* h, const float* x, int64_t n, int64_t l, float* y) {
 static int block_relevance(void* h, const float* r_out, const LRPRuleConfig& cfg, float* r_in) {
     return guarded([&] {
         auto* b = static_cast<RefBlock*>(h);
-        Tensor r(Shape({b->n, b->l, b->d}), &b->be, std::vector<float>(r_out, r_out + b->n * b->l * b->d));
+        Tensor r(Shape({b->n, b->l, b->d}), b->be, std::vector<float>(r_out, r_out + b->n * b->l * b->d));
         const std::vector<float> out = b->block->propagate_relevance(r, cfg).to_host_vector();
         std::copy(out.begin(), out.end(), r_in);
     });
@@ -238,13 +263,13 @@ void* pxr_lm_create(const px_model_config* cfg, const float* params) {
     RefLM* out = nullptr;
     guarded([&] {
         auto m = std::make_unique<RefLM>();
-        m->lm = std::make_unique<CausalLM>(hf_config(*cfg), &m->be);
+        m->lm = std::make_unique<CausalLM>(hf_config(*cfg), m->be);
         std::vector<std::pair<std::string, int64_t>> layout{{"embed_tokens.weight", cfg->vocab_size * cfg->hidden_size}};
         for (int64_t i = 0; i < cfg->num_layers; ++i)
             for (const auto& [name, size] : block_layout(*cfg)) layout.push_back({"layers." + std::to_string(i) + "." + name, size});
         layout.push_back({"norm.weight", cfg->hidden_size});
         if (!cfg->tie_word_embeddings) layout.push_back({"lm_head.weight", cfg->hidden_size * cfg->vocab_size});
-        load(*m->lm, layout, params, &m->be);
+        load(*m->lm, layout, params, m->be);
         m->c = *cfg;
         out = m.release();
     });
@@ -258,7 +283,7 @@ int pxr_lm_forward(void* h, const int64_t* ids, int64_t n, int64_t l, float* log
         m->l = l;
         std::vector<float> x(static_cast<size_t>(n * l));
         for (size_t i = 0; i < x.size(); ++i) x[i] = static_cast<float>(ids[i]);
-        const std::vector<float> out = m->lm->forward(Tensor(Shape({n, l}), &m->be, x)).to_host_vector();
+        const std::vector<float> out = m->lm->forward(Tensor(Shape({n, l}), m->be, x)).to_host_vector();
         if (logits) std::copy(out.begin(), out.end(), logits);
     });
 }
@@ -268,7 +293,7 @@ static int lm_relevance(void* h, const float* seed, const LRPRuleConfig& cfg, fl
     return guarded([&] {
         auto* m = static_cast<RefLM*>(h);
         const int64_t V = m->c.vocab_size;
-        Tensor s(Shape({m->n, m->l, V}), &m->be, std::vector<float>(seed, seed + m->n * m->l * V));
+        Tensor s(Shape({m->n, m->l, V}), m->be, std::vector<float>(seed, seed + m->n * m->l * V));
         const std::vector<Tensor> bounds = m->lm->propagate_relevance_by_layer(s, cfg);
         if (r_embed) {
             const std::vector<float> e = bounds.front().to_host_vector();
@@ -308,12 +333,12 @@ void pxr_lm_destroy(void* h) { delete static_cast<RefLM*>(h); }
 int pxr_linear_relevance(const float* x, const float* w, const float* bias, const float* r, int64_t n, int64_t in,
                          int64_t out, float eps, int bias_in_denominator, float* r_in) {
     return guarded([&] {
-        CPUBackend be;
-        LinearModule lin(in, out, &be, bias != nullptr);
+        DeviceBackend* be = driver_backend();
+        LinearModule lin(in, out, be, bias != nullptr);
         lin.set_weight(std::vector<float>(w, w + in * out));
         if (bias) lin.set_bias(std::vector<float>(bias, bias + out));
-        (void)lin.forward(Tensor(Shape({n, in}), &be, std::vector<float>(x, x + n * in)));
-        Tensor rr(Shape({n, out}), &be, std::vector<float>(r, r + n * out));
+        (void)lin.forward(Tensor(Shape({n, in}), be, std::vector<float>(x, x + n * in)));
+        Tensor rr(Shape({n, out}), be, std::vector<float>(r, r + n * out));
         const std::vector<float> res = lin.propagate_relevance(rr, rule(eps, bias_in_denominator)).to_host_vector();
         std::copy(res.begin(), res.end(), r_in);
     });
@@ -322,17 +347,57 @@ int pxr_linear_relevance(const float* x, const float* w, const float* bias, cons
 int pxr_linear_relevance_rule(const float* x, const float* w, const float* bias, const float* r, int64_t n, int64_t in,
                               int64_t out, const px_lrp_rule* rl, float* r_in) {
     return guarded([&] {
-        CPUBackend be;
-        LinearModule lin(in, out, &be, bias != nullptr);
+        DeviceBackend* be = driver_backend();
+        LinearModule lin(in, out, be, bias != nullptr);
         lin.set_weight(std::vector<float>(w, w + in * out));
         if (bias) lin.set_bias(std::vector<float>(bias, bias + out));
-        (void)lin.forward(Tensor(Shape({n, in}), &be, std::vector<float>(x, x + n * in)));
-        Tensor rr(Shape({n, out}), &be, std::vector<float>(r, r + n * out));
+        (void)lin.forward(Tensor(Shape({n, in}), be, std::vector<float>(x, x + n * in)));
+        Tensor rr(Shape({n, out}), be, std::vector<float>(r, r + n * out));
         const std::vector<float> res = lin.propagate_relevance(rr, rule_of(*rl)).to_host_vector();
         std::copy(res.begin(), res.end(), r_in);
     });
 }
 
+// LRP::explain (include/pulsatrix/lrp.hpp:218-241) over the reference's Linear -> ReLU -> ... ->
+// Linear chain in an ExplainerContext, OneHot seeds at targets[n] (one per input row): the path of
+// tests/lrp_reference_test.cpp:285-303. Layer i is (in[i], out[i]) with weights w[i] stored
+// (in, out) and biases b[i]; `relevance` receives the (n, in[0]) attribution, and `in_sum` the
+// Attribution's relevance_in_sum (DeviceBackend::sum). preset 0 applies `r` to every module; 1, 2
+// and 3 are the reference's LRP::epsilon_plus(), epsilon_alpha2_beta1() and
+// epsilon_gamma_box(-3, 3) composites (lrp.hpp:186-197).
+int pxr_mlp_explain(int layers, const int64_t* in, const int64_t* out, const float* const* w, const float* const* b,
+                    const float* x, int64_t n, const int64_t* targets, const px_lrp_rule* r, int preset,
+                    float* relevance, float* in_sum) {
+    return guarded([&] {
+        DeviceBackend* be = driver_backend();
+        std::vector<std::unique_ptr<Module>> owned;
+        std::vector<Module*> chain;
+        for (int i = 0; i < layers; ++i) {
+            auto lin = std::make_unique<LinearModule>(in[i], out[i], be, b[i] != nullptr);
+            lin->set_weight(std::vector<float>(w[i], w[i] + in[i] * out[i]));
+            if (b[i]) lin->set_bias(std::vector<float>(b[i], b[i] + out[i]));
+            chain.push_back(lin.get());
+            owned.push_back(std::move(lin));
+            if (i + 1 < layers) {
+                owned.push_back(std::make_unique<ReluModule>(be));
+                chain.push_back(owned.back().get());
+            }
+        }
+        ExplainerContext ctx(chain);
+        const Tensor input(Shape({n, in[0]}), be, std::vector<float>(x, x + n * in[0]));
+        const LRP lrp = preset == 1   ? LRP::epsilon_plus()
+                        : preset == 2 ? LRP::epsilon_alpha2_beta1()
+                        : preset == 3 ? LRP::epsilon_gamma_box(-3.0f, 3.0f)
+                                      : LRP(rule_of(*r));
+        Attribution a = lrp.explain(ctx, input, LRPTarget{std::vector<int64_t>(targets, targets + n), {}, LRPSeed::OneHot},
+                                    be);
+        const std::vector<float> v = a.values.to_host_vector();
+        std::copy(v.begin(), v.end(), relevance);
+        if (in_sum) *in_sum = std::stof(a.metadata.at("relevance_in_sum"));
+    });
+}
+
+#ifndef PXR_ON_MI355X
 void pxr_lrp_bilinear_matmul(const float* a, const float* b, const float* o, const float* r_o, float* r_a, float* r_b,
                              size_t slices, size_t m, size_t p, size_t q, float eps, int bt) {
     CPUBackend be;
@@ -343,5 +408,91 @@ void pxr_gemm_ex(const float* a, int ta, const float* b, int tb, float* out, siz
     CPUBackend be;
     be.gemm_ex(a, ta != 0, b, tb != 0, out, m, k, n, beta);
 }
+#else
+// ---- pxr_be_*: each DeviceBackend virtual of the process-wide MI355XBackend, device pointers ----
+
+#define PXR_BE(name, params, call) \
+    int pxr_be_##name params { return guarded([&] { driver_backend()->call; }); }
+
+PXR_BE(copy, (void* dst, const void* src, size_t bytes, int dir),
+       copy(dst, src, bytes, static_cast<CopyDirection>(dir)))
+PXR_BE(fill, (float* p, float value, size_t n), fill(p, value, n))
+PXR_BE(gemm, (const float* a, const float* b, float* out, size_t m, size_t k, size_t n), gemm(a, b, out, m, k, n))
+PXR_BE(gemm_ex, (const float* a, int ta, const float* b, int tb, float* out, size_t m, size_t k, size_t n, float beta),
+       gemm_ex(a, ta != 0, b, tb != 0, out, m, k, n, beta))
+PXR_BE(gemm_strided_batched,
+       (const float* a, int ta, size_t sa, const float* b, int tb, size_t sb, float* out, size_t so, size_t m, size_t k,
+        size_t n, size_t batch, float beta),
+       gemm_strided_batched(a, ta != 0, sa, b, tb != 0, sb, out, so, m, k, n, batch, beta))
+PXR_BE(elementwise, (int op, const float* in, float* out, size_t n), elementwise(static_cast<ElementwiseOp>(op), in, out, n))
+PXR_BE(add, (const float* a, const float* b, float* out, size_t n), add(a, b, out, n))
+PXR_BE(mul, (const float* a, const float* b, float* out, size_t n), mul(a, b, out, n))
+PXR_BE(axpby, (float alpha, const float* x, float beta, const float* y, float* out, size_t n),
+       axpby(alpha, x, beta, y, out, n))
+PXR_BE(column_sums, (const float* in, float* out, size_t rows, size_t cols, float beta),
+       column_sums(in, out, rows, cols, beta))
+PXR_BE(add_row_vector, (const float* in, const float* row, float* out, size_t rows, size_t cols),
+       add_row_vector(in, row, out, rows, cols))
+PXR_BE(dot_into, (const float* a, const float* b, size_t n, float* out), dot_into(a, b, n, out))
+PXR_BE(softmax_rows, (const float* in, float* out, size_t rows, size_t cols), softmax_rows(in, out, rows, cols))
+PXR_BE(rms_norm_forward, (const float* in, const float* g, float* out, float* rms, size_t rows, size_t cols, float eps),
+       rms_norm_forward(in, g, out, rms, rows, cols, eps))
+PXR_BE(rope_rotate,
+       (const float* in, const float* c, const float* s, float* out, size_t slices, size_t seq, size_t hd, int inverse,
+        int half),
+       rope_rotate(in, c, s, out, slices, seq, hd, inverse != 0, half != 0))
+PXR_BE(permute_0213, (const float* in, float* out, size_t d0, size_t d1, size_t d2, size_t d3),
+       permute_0213(in, out, d0, d1, d2, d3))
+PXR_BE(attention_mask_fill,
+       (float* scores, const float* keep, size_t batch, size_t heads, size_t q_len, size_t k_len, int causal,
+        size_t q_offset, size_t window, float value),
+       attention_mask_fill(scores, keep, batch, heads, q_len, k_len, causal != 0, q_offset, window, value))
+PXR_BE(gather_rows, (const float* table, const float* idx, float* out, size_t count, size_t dim),
+       gather_rows(table, idx, out, count, dim))
+PXR_BE(lrp_linear,
+       (const float* x, const float* w, const float* z, const float* r, float* r_in, size_t rows, size_t in, size_t out,
+        float eps),
+       lrp_linear(x, w, z, r, r_in, rows, in, out, eps))
+PXR_BE(lrp_residual_split, (const float* a, const float* b, const float* r, float* ra, float* rb, size_t n, float eps),
+       lrp_residual_split(a, b, r, ra, rb, n, eps))
+PXR_BE(lrp_bilinear_elementwise, (const float* a, const float* b, const float* r, float* out, size_t n, float eps),
+       lrp_bilinear_elementwise(a, b, r, out, n, eps))
+PXR_BE(lrp_bilinear_matmul,
+       (const float* a, const float* b, const float* o, const float* r_o, float* r_a, float* r_b, size_t slices,
+        size_t m, size_t p, size_t q, float eps, int bt),
+       lrp_bilinear_matmul(a, b, o, r_o, r_a, r_b, slices, m, p, q, eps, bt != 0))
+PXR_BE(lrp_softmax_rows, (const float* x, const float* y, const float* r, float* r_in, size_t rows, size_t cols),
+       lrp_softmax_rows(x, y, r, r_in, rows, cols))
+PXR_BE(lrp_rope,
+       (const float* x, const float* y, const float* r, const float* c, const float* s, float* r_in, size_t slices,
+        size_t seq, size_t hd, float eps, int half),
+       lrp_rope(x, y, r, c, s, r_in, slices, seq, hd, eps, half != 0))
+PXR_BE(lrp_stabilized_divide,
+       (const float* r, const float* d, const float* gate, float* out, size_t n, float eps, int mode),
+       lrp_stabilized_divide(r, d, gate, out, n, eps, static_cast<LrpGate>(mode)))
+PXR_BE(copy_2d, (float* dst, size_t ds, const float* src, size_t ss, size_t rows, size_t cols),
+       copy_2d(dst, ds, src, ss, rows, cols))
+PXR_BE(accumulate_rows, (const float* in, float* out, size_t rows, size_t cols), accumulate_rows(in, out, rows, cols))
+
+int pxr_be_synchronize(void) {
+    return guarded([&] { static_cast<MI355XBackend*>(driver_backend())->synchronize(); });
+}
+
+int pxr_be_sum(const float* in, size_t n, float* out) {
+    return guarded([&] { *out = driver_backend()->sum(in, n); });
+}
+
+int pxr_be_dot(const float* a, const float* b, size_t n, float* out) {
+    return guarded([&] { *out = driver_backend()->dot(a, b, n); });
+}
+
+int pxr_be_allocate(size_t bytes, void** out) {
+    return guarded([&] { *out = driver_backend()->allocate(bytes); });
+}
+
+void pxr_be_free(void* p) { driver_backend()->free(p); }
+
+int pxr_be_device(void) { return static_cast<int>(driver_backend()->device()); }
+#endif
 
 }  // extern "C"

@@ -107,7 +107,9 @@ void MI355XBackend::copy(void* dst, const void* src, size_t bytes, CopyDirection
         case CopyDirection::DeviceToDevice: kind = hipMemcpyDeviceToDevice; break;
         case CopyDirection::HostToHost: std::memcpy(dst, src, bytes); return;
     }
-    if (kind == hipMemcpyDeviceToDevice && bytes % sizeof(float) == 0) {
+    const bool word_aligned = reinterpret_cast<uintptr_t>(dst) % sizeof(float) == 0 &&
+                              reinterpret_cast<uintptr_t>(src) % sizeof(float) == 0;
+    if (kind == hipMemcpyDeviceToDevice && bytes % sizeof(float) == 0 && word_aligned) {
         // A copy kernel rather than an SDMA copy: it stays inside a captured graph.
         check(pxk_copy_2d(static_cast<float*>(dst), 0, static_cast<const float*>(src), 0, 1,
                           static_cast<int64_t>(bytes / sizeof(float)), stream_),

@@ -5,8 +5,9 @@ Run in a container that has the reference at /root/reference (it never runs on t
     python tests/golden/make_fixtures.py
 
 What it takes, all data (no source text):
-  * hf_tiny/<model>/: the tiny HF checkpoints with their golden logits (transformers) and AttnLRP
-    relevance (LXT 2.1) -- copied byte for byte from tests/fixtures/hf_tiny/.
+  * hf_tiny/<model>/ for llama, qwen2, qwen3 and gemma3: the tiny HF checkpoints with their golden
+    logits (transformers), AttnLRP relevance (LXT 2.1) and the gradient x input negative control
+    (LXT's patches off) -- copied byte for byte from tests/fixtures/hf_tiny/.
   * lxt_values.json: the float vectors pasted into tests/lrp_reference_test.cpp (kMhaLogits,
     kMhaRelevance, kBlockLogits, kBlockRelevance), parsed out of the file's array literals.
   * zennit_values.json: the same file's Zennit 1.0.0 MLP input relevance (kMlpEpsilon1e6,
@@ -21,9 +22,10 @@ import shutil
 REF = os.environ.get("PULSATRIX_REF", "/root/reference")
 HERE = os.path.dirname(os.path.abspath(__file__))
 
-MODELS = ("llama", "qwen2")
-FILES = ("config.json", "golden.safetensors", "attnlrp.safetensors", "model.safetensors",
-         "model.safetensors.index.json", "model-00001-of-00002.safetensors", "model-00002-of-00002.safetensors")
+MODELS = ("llama", "qwen2", "qwen3", "gemma3")
+FILES = ("config.json", "golden.safetensors", "attnlrp.safetensors", "gradient_x_input.safetensors",
+         "model.safetensors", "model.safetensors.index.json", "model-00001-of-00002.safetensors",
+         "model-00002-of-00002.safetensors")
 
 
 def copy_hf_tiny():
@@ -35,6 +37,7 @@ def copy_hf_tiny():
             p = os.path.join(src, f)
             if os.path.exists(p):
                 shutil.copyfile(p, os.path.join(dst, f))
+                os.chmod(os.path.join(dst, f), 0o644)
 
 
 def extract_vectors(names, filename):

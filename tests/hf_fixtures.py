@@ -57,6 +57,12 @@ def hf_tiny(name):
     return cfg, params, golden, attnlrp
 
 
+def gradient_x_input(name):
+    """The negative control of tests/fixtures/hf_tiny/<name>/gradient_x_input.safetensors: LXT with
+    its AttnLRP patches off (plain gradient x input) for the same ids and targets as attnlrp."""
+    return _load_st(os.path.join(GOLDEN, "hf_tiny", name, "gradient_x_input.safetensors"))
+
+
 def config_of(hc):
     """px_model_config of a Hugging Face config.json, as ParseHfConfig + ToAttentionConfig read it
     (src/hf_model.cpp:99-313) for the Llama, Qwen2, Qwen3 and Gemma 3 fields."""

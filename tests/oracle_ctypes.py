@@ -11,6 +11,7 @@ import numpy as np
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 ORACLE_SO = os.path.join(ROOT, "oracle", "liboracle.so")
 REF_SO = os.path.join(ROOT, "oracle", "_ref", "libpxref.so")
+REF_MI355X_SO = os.path.join(ROOT, "oracle", "_ref", "libpxref_mi355x.so")
 
 _f32p = ctypes.POINTER(ctypes.c_float)
 _i64p = ctypes.POINTER(ctypes.c_int64)
@@ -291,6 +292,75 @@ def ref():
     if _ref is None and os.path.exists(REF_SO):
         _ref = _Lib(REF_SO, "pxr_")
     return _ref
+
+
+_ref_mi355x = None
+
+
+def ref_mi355x():
+    """The reference's modules on MI355XBackend (oracle/_ref/libpxref_mi355x.so: the drop-in, run),
+    or None where it was not built. The same pxr_ entry points as ref(), on host arrays, plus
+    pxr_be_* (each DeviceBackend virtual on device pointers) and pxr_mlp_explain."""
+    global _ref_mi355x
+    if _ref_mi355x is None and os.path.exists(REF_MI355X_SO):
+        from pulsatrix_amd import native
+
+        native.pxk()  # the HIP runtime torch loaded, and the kernel library, first
+        lib = _Lib(REF_MI355X_SO, "pxr_")
+        L = lib.lib
+        vp, sz, i, f = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_float
+        sig = {
+            "copy": [vp, vp, sz, i], "fill": [vp, f, sz], "gemm": [vp, vp, vp, sz, sz, sz],
+            "gemm_ex": [vp, i, vp, i, vp, sz, sz, sz, f],
+            "gemm_strided_batched": [vp, i, sz, vp, i, sz, vp, sz, sz, sz, sz, sz, f],
+            "elementwise": [i, vp, vp, sz], "add": [vp, vp, vp, sz], "mul": [vp, vp, vp, sz],
+            "axpby": [f, vp, f, vp, vp, sz], "column_sums": [vp, vp, sz, sz, f], "add_row_vector": [vp, vp, vp, sz, sz],
+            "dot_into": [vp, vp, sz, vp], "softmax_rows": [vp, vp, sz, sz],
+            "rms_norm_forward": [vp, vp, vp, vp, sz, sz, f], "rope_rotate": [vp, vp, vp, vp, sz, sz, sz, i, i],
+            "permute_0213": [vp, vp, sz, sz, sz, sz], "attention_mask_fill": [vp, vp, sz, sz, sz, sz, i, sz, sz, f],
+            "gather_rows": [vp, vp, vp, sz, sz], "lrp_linear": [vp, vp, vp, vp, vp, sz, sz, sz, f],
+            "lrp_residual_split": [vp, vp, vp, vp, vp, sz, f], "lrp_bilinear_elementwise": [vp, vp, vp, vp, sz, f],
+            "lrp_bilinear_matmul": [vp, vp, vp, vp, vp, vp, sz, sz, sz, sz, f, i],
+            "lrp_softmax_rows": [vp, vp, vp, vp, sz, sz], "lrp_rope": [vp, vp, vp, vp, vp, vp, sz, sz, sz, f, i],
+            "lrp_stabilized_divide": [vp, vp, vp, vp, sz, f, i], "copy_2d": [vp, sz, vp, sz, sz, sz],
+            "accumulate_rows": [vp, vp, sz, sz], "synchronize": [], "sum": [vp, sz, vp], "dot": [vp, vp, sz, vp],
+            "allocate": [sz, ctypes.POINTER(vp)],
+        }
+        for name, args in sig.items():
+            fn = getattr(L, "pxr_be_" + name)
+            fn.argtypes, fn.restype = args, ctypes.c_int
+        L.pxr_be_free.argtypes, L.pxr_be_free.restype = [vp], None
+        L.pxr_be_device.restype = ctypes.c_int
+        L.pxr_linear_relevance_rule.argtypes = [_f32p, _f32p, _f32p, _f32p, ctypes.c_int64, ctypes.c_int64,
+                                                ctypes.c_int64, ctypes.POINTER(LrpRule), _f32p]
+        _ref_mi355x = lib
+    return _ref_mi355x
+
+
+def mlp_explain(lib, layers, x, targets, rule, preset=0):
+    """LRP::explain over Linear -> ReLU -> ... -> Linear (pxr_mlp_explain) on `lib`'s backend.
+    layers: [(w (in, out), b (out,) or None)]; preset 0 applies `rule` everywhere, 1-3 are the
+    reference's epsilon_plus, epsilon_alpha2_beta1 and epsilon_gamma_box(-3, 3) composites.
+    Returns (relevance (n, in), relevance_in_sum)."""
+    fn = lib.lib.pxr_mlp_explain
+    fn.argtypes = [ctypes.c_int, _i64p, _i64p, ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_void_p), _f32p,
+                   ctypes.c_int64, _i64p, ctypes.POINTER(LrpRule), ctypes.c_int, _f32p, _f32p]
+    fn.restype = ctypes.c_int
+    ins = np.array([w.shape[0] for w, _ in layers], np.int64)
+    outs = np.array([w.shape[1] for w, _ in layers], np.int64)
+    keep = [np.ascontiguousarray(w, np.float32) for w, _ in layers] + \
+           [None if b is None else np.ascontiguousarray(b, np.float32) for _, b in layers]
+    nl = len(layers)
+    wp = (ctypes.c_void_p * nl)(*[k.ctypes.data for k in keep[:nl]])
+    bp = (ctypes.c_void_p * nl)(*[None if k is None else k.ctypes.data for k in keep[nl:]])
+    x = np.ascontiguousarray(x, np.float32)
+    t = np.ascontiguousarray(targets, np.int64)
+    out = np.empty((x.shape[0], ins[0]), np.float32)
+    total = ctypes.c_float(0)
+    lib.check(lib.lib.pxr_mlp_explain(nl, ins.ctypes.data_as(_i64p), outs.ctypes.data_as(_i64p), wp, bp, fptr(x),
+                                      x.shape[0], t.ctypes.data_as(_i64p), ctypes.byref(rule), preset, fptr(out),
+                                      ctypes.byref(total)))
+    return out, total.value
 
 
 def fill_normal(n, seed, std):

@@ -16,7 +16,7 @@ import pytest
 
 import gpu_util as G
 import oracle_ctypes as oc
-from hf_fixtures import det, hf_tiny, lxt_values, pearson, per_head, sequences
+from hf_fixtures import det, gradient_x_input, hf_tiny, lxt_values, pearson, per_head, sequences
 from pulsatrix_amd import models
 from pulsatrix_amd import native as N
 
@@ -130,7 +130,7 @@ def test_block_with_biases_matches_oracle(rope_half, causal):
         expect_relevance_agrees(gpu.relevance(seed, eps, bid), ref.relevance(seed, eps, bid), "bid=%s" % bid)
 
 
-@pytest.mark.parametrize("name", ["llama", "qwen2"])
+@pytest.mark.parametrize("name", ["llama", "qwen2", "qwen3"])
 def test_causal_lm_matches_transformers_and_lxt_goldens(name):
     """hf_tiny checkpoints: logits vs transformers, AttnLRP vs LXT 2.1, on the MI355X path."""
     cfg, params, golden, ref = hf_tiny(name)
@@ -155,6 +155,27 @@ def test_causal_lm_matches_transformers_and_lxt_goldens(name):
         for i in range(cfg.num_layers):
             assert pearson(per_head(key[i], L, cfg.kv_heads()), ref["key_relevance.%d" % k][i]) > 0.99999
             assert pearson(per_head(value[i], L, cfg.kv_heads()), ref["value_relevance.%d" % k][i]) > 0.99999
+
+
+@pytest.mark.parametrize("name", ["llama", "qwen2", "qwen3", "gemma3"])
+def test_causal_lm_does_not_match_gradient_x_input(name):
+    """The reference's negative control (tests/attnlrp_parity_test.cpp:42-49) on the MI355X path:
+    against LXT's plain gradient x input for the same ids and targets, the AttnLRP relevance fails,
+    with a token correlation below 0.9 on some sequence."""
+    cfg, params, _, _ = hf_tiny(name)
+    neg = gradient_x_input(name)
+    lm = models.CausalLM(to_px(cfg), params)
+    worst = 1.0
+    for k in sequences(neg):
+        ids = neg["ids.%d" % k].reshape(1, -1)
+        L = ids.shape[1]
+        target = int(neg["target.%d" % k][0])
+        logits = lm.forward(ids)
+        seed = np.zeros_like(logits)
+        seed[0, L - 1, target] = logits[0, L - 1, target]
+        _, r_tok = lm.relevance(seed, LXT_EPS, True)
+        worst = min(worst, pearson(r_tok[0], neg["relevance.%d" % k]))
+    assert worst < 0.9, worst
 
 
 def small_lm_config(**kw):

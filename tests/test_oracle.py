@@ -12,7 +12,7 @@ import numpy as np
 import pytest
 
 import oracle_ctypes as oc
-from hf_fixtures import det, hf_tiny, lxt_values, pearson, per_head, sequences
+from hf_fixtures import det, gradient_x_input, hf_tiny, lxt_values, pearson, per_head, sequences
 
 LXT_EPS = 1e-9  # LxtAttnLrpConfig(), src/attnlrp_parity.cpp:67-72
 
@@ -23,7 +23,7 @@ def close(actual, expected, rel=1e-4):
     return np.all(np.abs(np.asarray(actual) - expected) <= tol)
 
 
-@pytest.mark.parametrize("name", ["llama", "qwen2", "gemma3"])
+@pytest.mark.parametrize("name", ["llama", "qwen2", "qwen3", "gemma3"])
 def test_oracle_logits_match_transformers(name):
     cfg, params, golden, _ = hf_tiny(name)
     lm = oc.oracle().lm(cfg, params)
@@ -33,7 +33,7 @@ def test_oracle_logits_match_transformers(name):
         assert close(logits, golden["logits.%d" % k]), (name, k, np.abs(logits - golden["logits.%d" % k]).max())
 
 
-@pytest.mark.parametrize("name", ["llama", "qwen2", "gemma3"])
+@pytest.mark.parametrize("name", ["llama", "qwen2", "qwen3", "gemma3"])
 def test_oracle_attnlrp_matches_lxt(name):
     """The checks of tests/attnlrp_parity_test.cpp:28-51 (via CompareToAttnLrp)."""
     cfg, params, _, ref = hf_tiny(name)
@@ -69,6 +69,27 @@ def test_oracle_attnlrp_negative_control():
     seed[0, L - 1, target] = logits[0, L - 1, target]
     _, r_tok = lm.relevance(seed, LXT_EPS, True)
     assert pearson(r_tok[0], ref["relevance.2"]) < 0.99999
+
+
+@pytest.mark.parametrize("name", ["llama", "qwen2", "qwen3", "gemma3"])
+def test_oracle_attnlrp_does_not_match_gradient_x_input(name):
+    """The reference's negative control (tests/attnlrp_parity_test.cpp:42-49): against LXT's plain
+    gradient x input for the same ids and targets, the AttnLRP relevance fails the gate, with a
+    token correlation below 0.9 on some sequence."""
+    cfg, params, _, ref = hf_tiny(name)
+    neg = gradient_x_input(name)
+    lm = oc.oracle().lm(cfg, params)
+    worst = 1.0
+    for k in sequences(neg):
+        ids = neg["ids.%d" % k].reshape(1, -1)
+        L = ids.shape[1]
+        target = int(neg["target.%d" % k][0])
+        logits = lm.forward(ids)
+        seed = np.zeros_like(logits)
+        seed[0, L - 1, target] = logits[0, L - 1, target]
+        _, r_tok = lm.relevance(seed, LXT_EPS, True)
+        worst = min(worst, pearson(r_tok[0], neg["relevance.%d" % k]))
+    assert worst < 0.9, worst
 
 
 def lxt_block_params():

@@ -169,3 +169,15 @@ def test_oracle_block_rule_bit_identical_to_reference():
     seed = oc.fill_normal(y.size, 8, 1.0).reshape(y.shape)
     for _, c in rc.all_rules():
         assert np.array_equal(o.relevance_rule(seed, c), r.relevance_rule(seed, c))
+
+
+@pytest.mark.skipif(oc.ref() is None, reason="oracle/_ref was not built (no reference sources)")
+@pytest.mark.parametrize("case", __import__("dropin_cases").explain_cases(), ids=lambda c: c[0])
+def test_reference_lrp_explain_reproduces_zennit_mlp(case):
+    """The harness the drop-in tests run on MI355XBackend, on the reference's own CPUBackend:
+    LRP::explain over the Zennit MLP (ExplainerContext, OneHot seeds at targets {2, 1}) matches
+    the Zennit 1.0.0 values; relevance_in_sum is the attribution's sum."""
+    name, rule, preset, key = case
+    rel, total = oc.mlp_explain(oc.ref(), rc.mlp_params(), rc.mlp_input(), rc.MLP_TARGETS, rule, preset)
+    rc.expect_reference_close(rel, rc.zennit_values()[key])
+    assert abs(total - float(rel.astype(np.float64).sum())) <= 1e-5 * max(1.0, abs(total))
