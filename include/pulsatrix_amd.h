@@ -98,9 +98,10 @@ int pxa_backend_memory(size_t* in_use, size_t* cached);
  * whole calls only, docs/gpu-profiling.md). Between start and stop, every kernel launch the fused
  * path makes on the backend is recorded with its algorithmic work (dense FLOPs for GEMM and
  * attention kernels, HBM bytes for row kernels). pxa_launch_log_time replays the recorded
- * launches in their order `reps` times with a HIP event on the backend's stream before each, and
- * writes each launch's mean interval (kernel time plus the dispatch gap to the next) in seconds.
- * The replays rewrite the recorded passes' outputs; run them after reading those. */
+ * launches in their order `reps` times, every kernel recording its own start and end events
+ * (pxk_timing_begin), and writes each launch's mean kernel time (the summed durations of its
+ * kernels) in seconds. The replays rewrite the recorded passes' outputs; run them after reading
+ * those. */
 int pxa_launch_log_start(void);
 int pxa_launch_log_stop(int64_t* count);
 int pxa_launch_log_entry(int64_t index, char* kernel, size_t kernel_cap, char* family, size_t family_cap,

@@ -33,6 +33,15 @@ const char* pxk_last_error(void);
 /* Library and device identification, for the test that the library loads on the GPU box. */
 const char* pxk_version(void);
 
+/* Per-dispatch timing, a profiling aid with no reference counterpart. Between pxk_timing_begin
+ * and pxk_timing_end on one host thread, each kernel that thread launches (up to `capacity`)
+ * records its own start and end events (hipExtLaunchKernelGGL); pxk_timing_count() is the number
+ * of launches recorded so far, and pxk_timing_end waits for them and writes their durations in
+ * milliseconds, in launch order. Launches under HIP graph capture must not run inside a window. */
+int pxk_timing_begin(int capacity);
+int pxk_timing_count(void);
+int pxk_timing_end(float* ms, int capacity);
+
 /* ---- the fused fp32 MFMA GEMM ------------------------------------------------------------------
  * C[b] = op(Aeff[b]) * op(B[b]) over a batch of independent products, fp32 in, fp32 MFMA
  * (v_mfma_f32_16x16x4_f32) with fp32 accumulation, LDS-staged double-buffered tiles of 128x128,
@@ -518,6 +527,33 @@ int pxk_embedding_ids(const float* ids, int64_t count, int64_t vocab, float* ids
  * (unit). seed (N, L, V) is fully written; targets_out (N) as int64. */
 int pxk_lm_seed(const float* logits, int64_t n, int64_t l, int64_t vocab, const int64_t* targets_in,
                 int64_t* targets_out, float* seed, int unit, void* stream);
+
+/* The tied LM head's epsilon-rule relevance (bias in the denominator or not: the tied head's bias
+ * is zero) for the seed pxk_lm_seed forms, without forming it: targets as pxk_lm_seed; for the
+ * last row of each sequence r = x * (R / stab(z_t) * E[t, :]) with R the target's logit z_t
+ * (OutputValue) or 1 (unit); every other row is exactly zero. That is the dense result of
+ * TiedLMHeadModule::propagate_relevance (tied_lm_head_module.cpp:76-111) under
+ * lrp_rules::epsilon_with_bias (lrp_rules.cpp:177-194) for such a seed: the dense product only adds
+ * zeros to the target's term. With a split (r_a != NULL) the relevance of the residual sum
+ * s = a + b is split as lrp_residual_split does (lrp_math.hpp:33-38) into r_a and r_b instead of
+ * being written to r. */
+typedef struct pxk_seed_head_desc {
+    const float* logits;     /* (n * l, vocab) */
+    const float* x;          /* (n * l, d): the head's input */
+    const float* e;          /* (vocab, d): the tied embedding */
+    int64_t n, l, vocab, d;
+    float eps;
+    int32_t unit;
+    const int64_t* targets_in; /* host, n ids, or NULL: the first maximum of each last row */
+    int64_t* targets_out;    /* device, n */
+    float* r;                /* (n * l, d) when there is no split */
+    const float* a;          /* split: (n * l, d) each */
+    const float* b;
+    const float* s;
+    float* r_a;
+    float* r_b;
+} pxk_seed_head_desc;
+int pxk_lm_seed_head_relevance(const pxk_seed_head_desc* d, void* stream);
 
 #ifdef __cplusplus
 }

@@ -195,9 +195,9 @@ public:
     void start_launch_log();
     void stop_launch_log();
     [[nodiscard]] const std::vector<LaunchRecord>& launch_log() const noexcept { return log_; }
-    /** @brief Replays the logged launches in order, `reps` times, with a HIP event on the stream
-     *         before each and after the last; seconds[i] = mean interval of launch i (its kernel
-     *         time plus the dispatch gap before the next). Logged launches rewrite their outputs. */
+    /** @brief Replays the logged launches in order, `reps` times, each dispatch recording its own
+     *         start and end events (pxk_timing_*); seconds[i] = mean summed duration of launch i's
+     *         kernels. Logged launches rewrite their outputs. */
     void time_launch_log(int reps, std::vector<double>& seconds);
 
 private:

@@ -21,6 +21,14 @@ public:
     const float* run_forward(const float* x, int64_t rows);
     const float* run_relevance(const float* relevance_out, const LRPRuleConfig& config,
                                const detail::ResidualSplit& split = {});
+    /** @brief The epsilon rule for the seed pxk_lm_seed would form over n sequences of l rows
+     *         (one-hot at each last row, at targets_in or the argmax), without forming it: only
+     *         the seeded rows are computed, the others are the dense rule's exact zeros
+     *         (pxk_lm_seed_head_relevance). Writes the targets to the device array targets_out.
+     *         Returns the relevance, or nullptr when it went into `split`. */
+    const float* run_seeded_relevance(int64_t n, int64_t l, const int64_t* targets_in, int64_t* targets_out,
+                                      bool unit_seed, const LRPRuleConfig& config,
+                                      const detail::ResidualSplit& split = {});
     [[nodiscard]] const float* logits() const noexcept { return logits_.data(); }
 
 protected:

@@ -173,6 +173,19 @@ void CausalLM::explain_device(const float* ids, int64_t n, int64_t l, const LRPR
                               float* token_relevance, int64_t* targets, const int64_t* targets_in, bool unit_seed) {
     const int64_t V = config_.vocab_size, M = n * l;
     const float* logits = run_forward(ids, n, l);
+    if (tied_head_ && !detail::is_affine_rule(config)) {
+        // The seed is one-hot at each sequence's last row, so the head's epsilon rule has one
+        // nonzero row per sequence: those rows alone, straight into the top block's residual split.
+        detail::validate_rule(config, "CausalLM");
+        const size_t nl = layers_.size();
+        const detail::ResidualSplit top = nl > 0 ? layers_.back()->output_split() : detail::ResidualSplit{};
+        const float* r = tied_head_->run_seeded_relevance(n, l, targets_in, targets, unit_seed, config, top);
+        for (size_t i = nl; i-- > 0;)
+            r = layers_[i]->run_relevance_split(config, i > 0 ? layers_[i - 1]->output_split() : detail::ResidualSplit{});
+        r_embed_ = r;
+        embed_.token_relevance(r, M, token_relevance);
+        return;
+    }
     float* seed = seed_.ensure(be_, M * V);
     // the seed's zero fill (N L V floats) plus one scan of each sequence's last logit row
     const std::vector<int64_t> given = targets_in ? std::vector<int64_t>(targets_in, targets_in + n) : std::vector<int64_t>();

@@ -170,28 +170,29 @@ void MI355XBackend::time_launch_log(int reps, std::vector<double>& seconds) {
     const size_t n = log_.size();
     seconds.assign(n, 0.0);
     if (n == 0 || reps <= 0) return;
-    std::vector<hipEvent_t> ev(n + 1, nullptr);
-    for (auto& e : ev) hip_check(hipEventCreate(&e), "MI355XBackend::time_launch_log (event)");
-    try {
-        for (const auto& r : log_) check(r.run(stream_), "MI355XBackend::time_launch_log (warm-up)");
-        for (int rep = 0; rep < reps; ++rep) {
+    for (const auto& r : log_) check(r.run(stream_), "MI355XBackend::time_launch_log (warm-up)");
+    // Each dispatch records its own start and end (pxk_timing_*), so a launch's time is its kernels'
+    // durations as the GPU ran them, in the order and cache state of the recorded pass.
+    const int capacity = static_cast<int>(8 * n + 64);
+    std::vector<int> first(n + 1);
+    std::vector<float> ms(static_cast<size_t>(capacity));
+    for (int rep = 0; rep < reps; ++rep) {
+        check(pxk_timing_begin(capacity), "MI355XBackend::time_launch_log");
+        try {
             for (size_t i = 0; i < n; ++i) {
-                hip_check(hipEventRecord(ev[i], S(stream_)), "MI355XBackend::time_launch_log (record)");
+                first[i] = pxk_timing_count();
                 check(log_[i].run(stream_), "MI355XBackend::time_launch_log");
             }
-            hip_check(hipEventRecord(ev[n], S(stream_)), "MI355XBackend::time_launch_log (record)");
-            hip_check(hipEventSynchronize(ev[n]), "MI355XBackend::time_launch_log (wait)");
-            for (size_t i = 0; i < n; ++i) {
-                float ms = 0.0f;
-                hip_check(hipEventElapsedTime(&ms, ev[i], ev[i + 1]), "MI355XBackend::time_launch_log (elapsed)");
-                seconds[i] += 1e-3 * ms / reps;
-            }
+        } catch (...) {
+            (void)pxk_timing_end(ms.data(), capacity);
+            throw;
         }
-    } catch (...) {
-        for (auto& e : ev) (void)hipEventDestroy(e);
-        throw;
+        first[n] = pxk_timing_count();
+        check(pxk_timing_end(ms.data(), capacity), "MI355XBackend::time_launch_log");
+        if (first[n] >= capacity) throw std::runtime_error("MI355XBackend::time_launch_log: timing window too small");
+        for (size_t i = 0; i < n; ++i)
+            for (int k = first[i]; k < first[i + 1]; ++k) seconds[i] += 1e-3 * ms[static_cast<size_t>(k)] / reps;
     }
-    for (auto& e : ev) (void)hipEventDestroy(e);
 }
 
 void MI355XBackend::gemm(const float* a, const float* b, float* out, size_t m, size_t k, size_t n) {

@@ -2,6 +2,7 @@
 #include <cmath>
 #include <stdexcept>
 #include <string>
+#include <vector>
 
 #include "pulsatrix/embedding_module.hpp"
 #include "pulsatrix/linear_module.hpp"
@@ -323,6 +324,49 @@ const float* TiedLMHeadModule::run_relevance(const float* relevance_out, const L
     detail::apply_split(d, split, D, config.epsilon);
     be_->run_gemm(d);
     return split.requested() ? nullptr : out;
+}
+
+const float* TiedLMHeadModule::run_seeded_relevance(int64_t n, int64_t l, const int64_t* targets_in,
+                                                    int64_t* targets_out, bool unit_seed, const LRPRuleConfig& config,
+                                                    const detail::ResidualSplit& split) {
+    if (x_ == nullptr) throw std::logic_error("TiedLMHeadModule::propagate_relevance: called before any forward()");
+    detail::validate_rule(config, "TiedLMHeadModule");
+    if (detail::is_affine_rule(config))
+        throw std::invalid_argument("TiedLMHeadModule::run_seeded_relevance: epsilon rules only");
+    if (n * l != rows_) throw std::invalid_argument("TiedLMHeadModule::run_seeded_relevance: n * l must match the forward");
+    const int64_t V = embedding_.num_embeddings(), D = embedding_.embedding_dim();
+    pxk_seed_head_desc d{};
+    d.logits = logits_.data();
+    d.x = x_;
+    d.e = embedding_.weight_data();
+    d.n = n;
+    d.l = l;
+    d.vocab = V;
+    d.d = D;
+    d.eps = config.epsilon;
+    d.unit = unit_seed;
+    d.targets_out = targets_out;
+    float* out = nullptr;
+    if (split.requested()) {
+        d.a = split.a;
+        d.b = split.b;
+        d.s = split.s;
+        d.r_a = split.r_a;
+        d.r_b = split.r_b;
+    } else {
+        out = r_in_.ensure(be_, rows_ * D);
+        d.r = out;
+    }
+    // one scan of each sequence's last logit row, then every row of the relevance written once
+    // (the seeded row also reads its logit and E's target row)
+    const std::vector<int64_t> given = targets_in ? std::vector<int64_t>(targets_in, targets_in + n) : std::vector<int64_t>();
+    const double bytes = 4.0 * (n * V + (split.requested() ? 2 : 1) * rows_ * D + 3 * n * D);
+    be_->launch("head_seeded_relevance", "rows", 0.0, bytes, "TiedLMHeadModule::propagate_relevance", [=](void* st) {
+        pxk_seed_head_desc dd = d;
+        dd.targets_in = given.empty() ? nullptr : given.data();
+        return pxk_lm_seed_head_relevance(&dd, st);
+    });
+    return out;
 }
 
 Tensor TiedLMHeadModule::forward_impl(const Tensor& input) {

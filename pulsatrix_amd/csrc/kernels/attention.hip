@@ -612,7 +612,7 @@ extern "C" int pxk_attention_forward(const float* q, int64_t ldq, const float* k
         hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
                             static_cast<int>(dyn)) != hipSuccess)
         return fail(PXK_ERR_LAUNCH, "pxk_attention_forward: %zu bytes of LDS refused", dyn);
-    hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), dyn, S(stream), a);
+    PXK_LAUNCH(fn, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), dyn, S(stream), a);
     return launched("pxk_attention_forward");
 }
 
@@ -667,7 +667,7 @@ extern "C" int pxk_attention_relevance_q(const pxk_attn_rel_desc* d, void* strea
         hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
                             static_cast<int>(dyn)) != hipSuccess)
         return fail(PXK_ERR_LAUNCH, "pxk_attention_relevance_q: %zu bytes of LDS refused", dyn);
-    hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), dyn, S(stream), a);
+    PXK_LAUNCH(fn, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), dyn, S(stream), a);
     return launched("pxk_attention_relevance_q");
 }
 
@@ -920,10 +920,10 @@ extern "C" int pxk_attention_relevance_kv(const pxk_attn_rel_kv_desc* d, void* s
     // 512-token sequence keeps one group per workgroup for the parallelism.
     if (ngroups % 4 == 0 && blocks / 4 >= 2048) {
         a.remap = (blocks / 4) % 8 == 0;
-        hipLaunchKernelGGL((attn_rel_kv_kernel<16, 2, 4>), dim3(static_cast<unsigned>(blocks / 4)), dim3(16 * kWave), 0,
+        PXK_LAUNCH((attn_rel_kv_kernel<16, 2, 4>), dim3(static_cast<unsigned>(blocks / 4)), dim3(16 * kWave), 0,
                            S(stream), a);
     } else {
-        hipLaunchKernelGGL((attn_rel_kv_kernel<16, 2, 1>), dim3(static_cast<unsigned>(blocks)), dim3(16 * kWave), 0,
+        PXK_LAUNCH((attn_rel_kv_kernel<16, 2, 1>), dim3(static_cast<unsigned>(blocks)), dim3(16 * kWave), 0,
                            S(stream), a);
     }
     return launched("pxk_attention_relevance_kv");

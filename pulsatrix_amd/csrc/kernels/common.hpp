@@ -1,6 +1,7 @@
 // Internal helpers shared by the gfx950 kernel translation units.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -18,6 +19,22 @@ int fail(int code, const char* fmt, ...);
 int launched(const char* what);
 
 inline hipStream_t S(void* s) { return static_cast<hipStream_t>(s); }
+
+// Per-dispatch timing (pxk_timing_begin / pxk_timing_end): while a window is open on the calling
+// thread, each launch takes the next pair of events and records the kernel's own start and end
+// with it (hipExtLaunchKernelGGL), so the host can read every kernel's duration as the GPU ran it.
+// Returns false (a plain launch) when no window is open or its events are used up.
+bool timing_slot(hipEvent_t* start, hipEvent_t* stop);
+
+// Every kernel launch of the library goes through here.
+#define PXK_LAUNCH(kernel, grid, block, shmem, stream, ...)                                                 \
+    do {                                                                                                    \
+        hipEvent_t pxk_ev0_ = nullptr, pxk_ev1_ = nullptr;                                                  \
+        if (::pxk::timing_slot(&pxk_ev0_, &pxk_ev1_))                                                       \
+            hipExtLaunchKernelGGL(kernel, grid, block, shmem, stream, pxk_ev0_, pxk_ev1_, 0u, __VA_ARGS__); \
+        else                                                                                                \
+            hipLaunchKernelGGL(kernel, grid, block, shmem, stream, __VA_ARGS__);                            \
+    } while (0)
 
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 

@@ -82,10 +82,10 @@ extern "C" int pxk_convert_weight(const void* src, int dtype, int64_t rows, int6
     if (transpose) {
         const int64_t tiles = ((rows + kTile - 1) / kTile) * ((cols + kTile - 1) / kTile);
         if (tiles > (int64_t{1} << 31) - 1) return fail(PXK_ERR_INVALID, "pxk_convert_weight: matrix too large");
-        hipLaunchKernelGGL(widen_transpose_kernel, dim3(static_cast<unsigned>(tiles)), dim3(256), 0, S(stream), s, dtype,
+        PXK_LAUNCH(widen_transpose_kernel, dim3(static_cast<unsigned>(tiles)), dim3(256), 0, S(stream), s, dtype,
                            rows, cols, dst);
     } else {
-        hipLaunchKernelGGL(widen_kernel, dim3(grid_for(n, 256)), dim3(256), 0, S(stream), s, dtype, n, dst);
+        PXK_LAUNCH(widen_kernel, dim3(grid_for(n, 256)), dim3(256), 0, S(stream), s, dtype, n, dst);
     }
     return launched("pxk_convert_weight");
 }

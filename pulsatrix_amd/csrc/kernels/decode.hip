@@ -385,12 +385,12 @@ extern "C" int pxk_decode_rope_append(const float* q, int64_t ldq, const float* 
         const size_t lds = static_cast<size_t>(head_dim) * sizeof(float);
         if (lds > 60 * 1024 || n * (heads + kv_heads) > (int64_t{1} << 31) - 1)
             return fail(PXK_ERR_INVALID, "pxk_decode_rope_append: head_dim must fit LDS");
-        hipLaunchKernelGGL(rope_append_norm_kernel, dim3(static_cast<unsigned>(n * (heads + kv_heads))), dim3(kThreads),
+        PXK_LAUNCH(rope_append_norm_kernel, dim3(static_cast<unsigned>(n * (heads + kv_heads))), dim3(kThreads),
                            lds, S(stream), a);
         return launched("pxk_decode_rope_append (QK-Norm)");
     }
     const int64_t work = n * (heads + kv_heads) * (head_dim / 2) + n * kvd;
-    hipLaunchKernelGGL(rope_append_kernel, dim3(grid_for(work, kThreads)), dim3(kThreads), 0, S(stream), a);
+    PXK_LAUNCH(rope_append_kernel, dim3(grid_for(work, kThreads)), dim3(kThreads), 0, S(stream), a);
     return launched("pxk_decode_rope_append");
 }
 
@@ -419,10 +419,10 @@ extern "C" int pxk_decode_attention(const float* q, const float* k_cache, const 
                     aligned16(workspace);
     const DecodeAttnArgs a{q,        k_cache, v_cache,  seq_stride, ctx,   workspace, pos, heads,
                            kv_heads, head_dim, window, max_keys, chunks, scale, vec};
-    hipLaunchKernelGGL(decode_attention_part_kernel, dim3(static_cast<unsigned>(n * heads * chunks)), dim3(kThreads),
+    PXK_LAUNCH(decode_attention_part_kernel, dim3(static_cast<unsigned>(n * heads * chunks)), dim3(kThreads),
                        lds, S(stream), a);
     if (const int rc = launched("pxk_decode_attention")) return rc;
-    hipLaunchKernelGGL(decode_attention_merge_kernel, dim3(static_cast<unsigned>(n * heads)), dim3(kThreads), 0,
+    PXK_LAUNCH(decode_attention_merge_kernel, dim3(static_cast<unsigned>(n * heads)), dim3(kThreads), 0,
                        S(stream), a);
     return launched("pxk_decode_attention (merge)");
 }
@@ -444,16 +444,16 @@ extern "C" int pxk_decode_pick(const float* logits, int64_t ld_logits, int64_t n
     auto* pi = static_cast<int64_t*>(workspace);
     auto* pv = reinterpret_cast<float*>(pi + n * kPickSlices);
     const PickArgs a{logits, ld_logits, vocab, ids, ld_ids, cur, picked_logit, ld_logit, pos, pv, pi};
-    hipLaunchKernelGGL(decode_pick_part_kernel, dim3(kPickSlices, static_cast<unsigned>(n)), dim3(kPickThreads), 0,
+    PXK_LAUNCH(decode_pick_part_kernel, dim3(kPickSlices, static_cast<unsigned>(n)), dim3(kPickThreads), 0,
                        S(stream), a);
     if (const int rc = launched("pxk_decode_pick")) return rc;
-    hipLaunchKernelGGL(decode_pick_merge_kernel, dim3(static_cast<unsigned>(n)), dim3(kWave), 0, S(stream), a);
+    PXK_LAUNCH(decode_pick_merge_kernel, dim3(static_cast<unsigned>(n)), dim3(kWave), 0, S(stream), a);
     return launched("pxk_decode_pick (merge)");
 }
 
 extern "C" int pxk_decode_advance(int32_t* pos, void* stream) {
     if (!pos) return fail(PXK_ERR_INVALID, "pxk_decode_advance: NULL position");
-    hipLaunchKernelGGL(decode_advance_kernel, dim3(1), dim3(kWave), 0, S(stream), pos);
+    PXK_LAUNCH(decode_advance_kernel, dim3(1), dim3(kWave), 0, S(stream), pos);
     return launched("pxk_decode_advance");
 }
 
@@ -464,7 +464,7 @@ extern "C" int pxk_seed_rows(const float* logits, int64_t ld_logits, const float
     if (n == 0) return PXK_OK;
     if (!targets || !seed || (!unit && !logits)) return fail(PXK_ERR_INVALID, "pxk_seed_rows: NULL operand");
     const unsigned gx = static_cast<unsigned>(std::min<int64_t>(cdiv(vocab, kThreads), 1024));
-    hipLaunchKernelGGL(seed_rows_kernel, dim3(gx, static_cast<unsigned>(n)), dim3(kThreads), 0, S(stream), logits,
+    PXK_LAUNCH(seed_rows_kernel, dim3(gx, static_cast<unsigned>(n)), dim3(kThreads), 0, S(stream), logits,
                        ld_logits, targets, stride, vocab, seed, targets_out, unit);
     return launched("pxk_seed_rows");
 }

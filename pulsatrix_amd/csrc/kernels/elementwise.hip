@@ -6,6 +6,8 @@
 #include <cstring>
 #include <string>
 
+#include <vector>
+
 #include "common.hpp"
 
 namespace pxk {
@@ -28,6 +30,25 @@ int launched(const char* what) {
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(PXK_ERR_LAUNCH, "%s: %s", what, hipGetErrorString(e));
     return PXK_OK;
+}
+
+namespace {
+// The calling thread's timing window: 2 events per slot, created on first need and kept.
+struct TimingWindow {
+    std::vector<hipEvent_t> events;
+    int used = 0;
+    bool open = false;
+};
+thread_local TimingWindow g_timing;
+}  // namespace
+
+bool timing_slot(hipEvent_t* start, hipEvent_t* stop) {
+    TimingWindow& w = g_timing;
+    if (!w.open || 2 * (static_cast<size_t>(w.used) + 1) > w.events.size()) return false;
+    *start = w.events[2 * w.used];
+    *stop = w.events[2 * w.used + 1];
+    ++w.used;
+    return true;
 }
 
 namespace {
@@ -156,13 +177,13 @@ int run_map(const char* what, F f, Ptrs<NIN, NOUT> p, int64_t n, void* stream) {
         // operand reaches 16 MiB (beyond what the L2s hold).
         const int64_t g = std::max<int64_t>(1, std::min<int64_t>(cdiv(cdiv(n, 4), kThreads * kUnroll), 32768));
         if (n >= (int64_t{1} << 22))
-            hipLaunchKernelGGL((map_kernel_p<F, NIN, NOUT, true, true>), dim3(static_cast<unsigned>(g)), dim3(kThreads),
+            PXK_LAUNCH((map_kernel_p<F, NIN, NOUT, true, true>), dim3(static_cast<unsigned>(g)), dim3(kThreads),
                                0, S(stream), f, p, n);
         else
-            hipLaunchKernelGGL((map_kernel_p<F, NIN, NOUT, true, false>), dim3(static_cast<unsigned>(g)),
+            PXK_LAUNCH((map_kernel_p<F, NIN, NOUT, true, false>), dim3(static_cast<unsigned>(g)),
                                dim3(kThreads), 0, S(stream), f, p, n);
     } else {
-        hipLaunchKernelGGL((map_kernel_p<F, NIN, NOUT, false, false>), dim3(grid_for(n, kThreads)), dim3(kThreads), 0,
+        PXK_LAUNCH((map_kernel_p<F, NIN, NOUT, false, false>), dim3(grid_for(n, kThreads)), dim3(kThreads), 0,
                            S(stream), f, p, n);
     }
     return launched(what);
@@ -329,6 +350,36 @@ const char* pxk_last_error(void) { return g_error.c_str(); }
 
 const char* pxk_version(void) { return "pxk_gfx950 1.0 (fp32 MFMA 16x16x4, wave64)"; }
 
+int pxk_timing_begin(int capacity) {
+    if (capacity <= 0 || capacity > (1 << 20)) return fail(PXK_ERR_INVALID, "pxk_timing_begin: bad capacity %d", capacity);
+    TimingWindow& w = g_timing;
+    if (w.open) return fail(PXK_ERR_INVALID, "pxk_timing_begin: a window is already open on this thread");
+    while (w.events.size() < 2 * static_cast<size_t>(capacity)) {
+        hipEvent_t e = nullptr;
+        const hipError_t r = hipEventCreate(&e);
+        if (r != hipSuccess) return fail(PXK_ERR_LAUNCH, "pxk_timing_begin: hipEventCreate: %s", hipGetErrorString(r));
+        w.events.push_back(e);
+    }
+    w.used = 0;
+    w.open = true;
+    return PXK_OK;
+}
+
+int pxk_timing_count(void) { return g_timing.used; }
+
+int pxk_timing_end(float* ms, int capacity) {
+    TimingWindow& w = g_timing;
+    if (!w.open) return fail(PXK_ERR_INVALID, "pxk_timing_end: no window is open on this thread");
+    w.open = false;
+    const int n = std::min(w.used, capacity);
+    for (int i = 0; i < n; ++i) {
+        hipError_t r = hipEventSynchronize(w.events[2 * i + 1]);
+        if (r == hipSuccess) r = hipEventElapsedTime(ms + i, w.events[2 * i], w.events[2 * i + 1]);
+        if (r != hipSuccess) return fail(PXK_ERR_LAUNCH, "pxk_timing_end: launch %d: %s", i, hipGetErrorString(r));
+    }
+    return PXK_OK;
+}
+
 int pxk_fill(float* ptr, float value, int64_t n, void* stream) {
     Ptrs<0, 1> p{{nullptr}, {ptr}};
     return run_map<0, 1>("pxk_fill", FillF{value}, p, n, stream);
@@ -356,7 +407,7 @@ int pxk_axpby(float alpha, const float* x, float beta, const float* y, float* ou
 int pxk_add_row_vector(const float* in, const float* row, float* out, int64_t rows, int64_t cols, void* stream) {
     if (rows < 0 || cols < 0) return fail(PXK_ERR_INVALID, "pxk_add_row_vector: negative size");
     if (rows * cols == 0) return PXK_OK;
-    hipLaunchKernelGGL(add_row_kernel, dim3(grid_for(rows * cols, kThreads)), dim3(kThreads), 0, S(stream), in, row,
+    PXK_LAUNCH(add_row_kernel, dim3(grid_for(rows * cols, kThreads)), dim3(kThreads), 0, S(stream), in, row,
                        out, rows, cols);
     return launched("pxk_add_row_vector");
 }
@@ -389,7 +440,7 @@ int pxk_swiglu_forward(const float* gu, int64_t ld, float* gate_post, float* hid
     if (rows < 0 || f < 0 || ld < 2 * f) return fail(PXK_ERR_INVALID, "pxk_swiglu_forward: bad sizes");
     if (act < 0 || act > 1) return fail(PXK_ERR_INVALID, "pxk_swiglu_forward: unknown gate activation %d", act);
     if (rows * f == 0) return PXK_OK;
-    hipLaunchKernelGGL(swiglu_kernel, dim3(grid_for(rows * f, kThreads)), dim3(kThreads), 0, S(stream), gu, ld,
+    PXK_LAUNCH(swiglu_kernel, dim3(grid_for(rows * f, kThreads)), dim3(kThreads), 0, S(stream), gu, ld,
                        gate_post, hidden, rows, f, act);
     return launched("pxk_swiglu_forward");
 }
@@ -397,7 +448,7 @@ int pxk_swiglu_forward(const float* gu, int64_t ld, float* gate_post, float* hid
 int pxk_copy_2d(float* dst, int64_t ds, const float* src, int64_t ss, int64_t rows, int64_t cols, void* stream) {
     if (rows < 0 || cols < 0) return fail(PXK_ERR_INVALID, "pxk_copy_2d: negative size");
     if (rows * cols == 0) return PXK_OK;
-    hipLaunchKernelGGL(copy2d_kernel, dim3(grid_for(rows * cols, kThreads)), dim3(kThreads), 0, S(stream), dst, ds, src,
+    PXK_LAUNCH(copy2d_kernel, dim3(grid_for(rows * cols, kThreads)), dim3(kThreads), 0, S(stream), dst, ds, src,
                        ss, rows, cols);
     return launched("pxk_copy_2d");
 }
@@ -407,10 +458,10 @@ int pxk_repeat_block(float* buf, int64_t count, int64_t copies, void* stream) {
     if (count == 0 || copies == 1) return PXK_OK;
     if (!buf) return fail(PXK_ERR_INVALID, "pxk_repeat_block: NULL buffer");
     if (count % 4 == 0 && aligned16(buf))
-        hipLaunchKernelGGL(repeat_block_vec_kernel, dim3(grid_for(count / 4, kThreads)), dim3(kThreads), 0, S(stream),
+        PXK_LAUNCH(repeat_block_vec_kernel, dim3(grid_for(count / 4, kThreads)), dim3(kThreads), 0, S(stream),
                            buf, count / 4, copies);
     else
-        hipLaunchKernelGGL(repeat_block_kernel, dim3(grid_for(count, kThreads)), dim3(kThreads), 0, S(stream), buf,
+        PXK_LAUNCH(repeat_block_kernel, dim3(grid_for(count, kThreads)), dim3(kThreads), 0, S(stream), buf,
                            count, copies);
     return launched("pxk_repeat_block");
 }
@@ -418,7 +469,7 @@ int pxk_repeat_block(float* buf, int64_t count, int64_t copies, void* stream) {
 int pxk_accumulate_rows(const float* in, float* out, int64_t rows, int64_t cols, void* stream) {
     if (rows < 0 || cols < 0) return fail(PXK_ERR_INVALID, "pxk_accumulate_rows: negative size");
     if (cols == 0) return PXK_OK;
-    hipLaunchKernelGGL(accumulate_rows_kernel, dim3(static_cast<unsigned>(cdiv(cols, kThreads))), dim3(kThreads), 0,
+    PXK_LAUNCH(accumulate_rows_kernel, dim3(static_cast<unsigned>(cdiv(cols, kThreads))), dim3(kThreads), 0,
                        S(stream), in, out, rows, cols);
     return launched("pxk_accumulate_rows");
 }
@@ -426,7 +477,7 @@ int pxk_accumulate_rows(const float* in, float* out, int64_t rows, int64_t cols,
 int pxk_column_sums(const float* in, float* out, int64_t rows, int64_t cols, float beta, void* stream) {
     if (rows < 0 || cols < 0) return fail(PXK_ERR_INVALID, "pxk_column_sums: negative size");
     if (cols == 0) return PXK_OK;
-    hipLaunchKernelGGL(column_sums_kernel, dim3(static_cast<unsigned>(cdiv(cols, kThreads))), dim3(kThreads), 0,
+    PXK_LAUNCH(column_sums_kernel, dim3(static_cast<unsigned>(cdiv(cols, kThreads))), dim3(kThreads), 0,
                        S(stream), in, out, rows, cols, beta);
     return launched("pxk_column_sums");
 }
@@ -435,7 +486,7 @@ int pxk_embedding_ids(const float* ids, int64_t count, int64_t vocab, float* ids
     if (count < 0 || vocab <= 0 || vocab > (int64_t{1} << 24))
         return fail(PXK_ERR_INVALID, "pxk_embedding_ids: count must be >= 0 and vocab in [1, 2^24]");
     if (!status || (count > 0 && (!ids || !ids_out))) return fail(PXK_ERR_INVALID, "pxk_embedding_ids: NULL operand");
-    hipLaunchKernelGGL(embedding_ids_kernel, dim3(1), dim3(kIdThreads), 0, S(stream), ids, count, vocab, ids_out,
+    PXK_LAUNCH(embedding_ids_kernel, dim3(1), dim3(kIdThreads), 0, S(stream), ids, count, vocab, ids_out,
                        status);
     return launched("pxk_embedding_ids");
 }
@@ -443,7 +494,7 @@ int pxk_embedding_ids(const float* ids, int64_t count, int64_t vocab, float* ids
 int pxk_gather_rows(const float* table, const float* indices, float* out, int64_t count, int64_t dim, void* stream) {
     if (count < 0 || dim < 0) return fail(PXK_ERR_INVALID, "pxk_gather_rows: negative size");
     if (count * dim == 0) return PXK_OK;
-    hipLaunchKernelGGL(gather_kernel, dim3(grid_for(count * dim, kThreads)), dim3(kThreads), 0, S(stream), table,
+    PXK_LAUNCH(gather_kernel, dim3(grid_for(count * dim, kThreads)), dim3(kThreads), 0, S(stream), table,
                        indices, out, count, dim);
     return launched("pxk_gather_rows");
 }

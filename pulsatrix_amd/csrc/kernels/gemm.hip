@@ -1471,12 +1471,12 @@ extern "C" int pxk_gemm(const pxk_gemm_desc* d, void* stream) {
         const int wi = p.width == 64 ? 0 : (p.width == 32 ? 1 : 2);
         g.bm = 16;
         const size_t lds = p.skinny->tb ? skinny_nt_lds(d) : 0;
-        hipLaunchKernelGGL(p.skinny->k[mi][p.skinny->tb ? 0 : wi], dim3(static_cast<unsigned>(p.tiles_n * p.splits)),
+        PXK_LAUNCH(p.skinny->k[mi][p.skinny->tb ? 0 : wi], dim3(static_cast<unsigned>(p.tiles_n * p.splits)),
                            dim3(NT), lds, S(stream), g);
         if (const int rc = launched("pxk_gemm (skinny)")) return rc;
         if (p.splits > 1) {
             const dim3 rgrid(static_cast<unsigned>(p.tiles_n), 1, 1);  // at least 16 rows per reduce workgroup
-            hipLaunchKernelGGL(p.skinny->r[wi], rgrid, dim3(NT), 0, S(stream), g);
+            PXK_LAUNCH(p.skinny->r[wi], rgrid, dim3(NT), 0, S(stream), g);
             return launched("pxk_gemm (skinny split-K reduce)");
         }
         return PXK_OK;
@@ -1485,7 +1485,7 @@ extern "C" int pxk_gemm(const pxk_gemm_desc* d, void* stream) {
     const int64_t blocks = p.tiles_m * p.tiles_n * d->batch * p.splits;
     g.remap = blocks % 8 == 0;
     const int has_bias = d->prologue == PXK_PRO_DIV_STAB && d->z_bias.ptr != nullptr;
-    hipLaunchKernelGGL(p.e->k[has_bias][p.tile], dim3(static_cast<unsigned>(blocks)),
+    PXK_LAUNCH(p.e->k[has_bias][p.tile], dim3(static_cast<unsigned>(blocks)),
                        dim3(static_cast<unsigned>(kTileInfo[p.tile].threads)), 0, S(stream), g);
     if (const int rc = launched("pxk_gemm")) return rc;
     if (p.splits > 1) {
@@ -1494,7 +1494,7 @@ extern "C" int pxk_gemm(const pxk_gemm_desc* d, void* stream) {
         const dim3 rgrid(static_cast<unsigned>(p.tiles_n), static_cast<unsigned>(cdiv(d->m, rs)),
                          static_cast<unsigned>(d->batch));
         if (rgrid.y > 65535 || rgrid.z > 65535) return fail(PXK_ERR_INVALID, "pxk_gemm: reduce grid too large");
-        hipLaunchKernelGGL(p.e->r[p.tile], rgrid, dim3(NT), 0, S(stream), g);
+        PXK_LAUNCH(p.e->r[p.tile], rgrid, dim3(NT), 0, S(stream), g);
         return launched("pxk_gemm split-K reduce");
     }
     return PXK_OK;

@@ -530,7 +530,59 @@ __global__ void __launch_bounds__(kSeedThreads) lm_seed_kernel(const float* logi
     if (threadIdx.x == 0) {
         const int64_t t = bi[0];
         targets_out[n] = t;
-        seed[(n * L + (L - 1)) * V + t] = unit ? 1.0f : row[t];
+        if (seed) seed[(n * L + (L - 1)) * V + t] = unit ? 1.0f : row[t];
+    }
+}
+
+// The tied head's epsilon rule for a seed that is one-hot at the last position of each sequence
+// (tied_lm_head_module.cpp:76-111 through lrp_rules::epsilon_with_bias): g = R / stab(z) is zero
+// except at (row, target), so (g E)[row, :] = g_t * E[t, :] and every other row is exactly zero. One
+// workgroup per row; the seeded row reads its target (written by lm_seed_kernel), its logit and
+// E's row t. With a residual split the row's relevance r becomes r_a = a / stab(a + b) * r and
+// r_b = b / stab(a + b) * r (lrp_residual_split, lrp_math.hpp:33-38), with s = a + b as the forward
+// stored it; zero rows split into zeros.
+struct SeedHeadArgs {
+    const float* logits;
+    const float* x;
+    const float* e;
+    const int64_t* targets;
+    float* r;
+    const float* a;
+    const float* b;
+    const float* s;
+    float* r_a;
+    float* r_b;
+    int64_t l, vocab, d;
+    float eps;
+    int unit;
+};
+
+__global__ void __launch_bounds__(kThreads) seed_head_rows_kernel(const SeedHeadArgs g) {
+    const int64_t row = blockIdx.x;
+    const bool seeded = row % g.l == g.l - 1;
+    const int64_t off = row * g.d;
+    float gt = 0.0f;
+    const float* er = nullptr;
+    if (seeded) {
+        const int64_t t = g.targets[row / g.l];
+        const float z = g.logits[row * g.vocab + t];
+        gt = (g.unit ? 1.0f : z) / stab(z, g.eps);
+        er = g.e + t * g.d;
+    }
+    for (int64_t j = threadIdx.x; j < g.d; j += kThreads) {
+        const float r = seeded ? g.x[off + j] * (gt * er[j]) : 0.0f;
+        if (g.r_a) {
+            if (seeded) {
+                const float den = stab(g.s[off + j], g.eps);
+                g.r_a[off + j] = (g.a[off + j] / den) * r;
+                g.r_b[off + j] = (g.b[off + j] / den) * r;
+            } else {
+                g.r_a[off + j] = 0.0f;
+                g.r_b[off + j] = 0.0f;
+            }
+        } else {
+            g.r[off + j] = r;
+        }
     }
 }
 
@@ -538,15 +590,15 @@ template <bool NT>
 void launch_rms_vec(int64_t nv, dim3 grid, dim3 block, hipStream_t st, const float* in, const float* gamma, float* out,
                     float* row_rms, int64_t rows, int cols4, float eps) {
     if (nv <= 2)
-        hipLaunchKernelGGL((rms_norm_vec_kernel<2, NT>), grid, block, 0, st, in, gamma, out, row_rms, rows, cols4, eps);
+        PXK_LAUNCH((rms_norm_vec_kernel<2, NT>), grid, block, 0, st, in, gamma, out, row_rms, rows, cols4, eps);
     else if (nv <= 3)
-        hipLaunchKernelGGL((rms_norm_vec_kernel<3, NT>), grid, block, 0, st, in, gamma, out, row_rms, rows, cols4, eps);
+        PXK_LAUNCH((rms_norm_vec_kernel<3, NT>), grid, block, 0, st, in, gamma, out, row_rms, rows, cols4, eps);
     else if (nv <= 4)
-        hipLaunchKernelGGL((rms_norm_vec_kernel<4, NT>), grid, block, 0, st, in, gamma, out, row_rms, rows, cols4, eps);
+        PXK_LAUNCH((rms_norm_vec_kernel<4, NT>), grid, block, 0, st, in, gamma, out, row_rms, rows, cols4, eps);
     else if (nv <= 8)
-        hipLaunchKernelGGL((rms_norm_vec_kernel<8, NT>), grid, block, 0, st, in, gamma, out, row_rms, rows, cols4, eps);
+        PXK_LAUNCH((rms_norm_vec_kernel<8, NT>), grid, block, 0, st, in, gamma, out, row_rms, rows, cols4, eps);
     else
-        hipLaunchKernelGGL((rms_norm_vec_kernel<16, NT>), grid, block, 0, st, in, gamma, out, row_rms, rows, cols4, eps);
+        PXK_LAUNCH((rms_norm_vec_kernel<16, NT>), grid, block, 0, st, in, gamma, out, row_rms, rows, cols4, eps);
 }
 
 unsigned rows_grid(int64_t rows) { return static_cast<unsigned>(cdiv(rows, kRowsPerBlock)); }
@@ -580,7 +632,7 @@ int pxk_rms_norm_forward(const float* in, const float* gamma, float* out, float*
         else
             launch_rms_vec<false>(nv, grid, block, S(stream), in, gamma, out, row_rms, rows, cols4, eps);
     } else {
-        hipLaunchKernelGGL(rms_norm_kernel, grid, block, 0, S(stream), in, gamma, out, row_rms, rows, cols, eps);
+        PXK_LAUNCH(rms_norm_kernel, grid, block, 0, S(stream), in, gamma, out, row_rms, rows, cols, eps);
     }
     return launched("pxk_rms_norm_forward");
 }
@@ -598,20 +650,20 @@ int pxk_rms_norm_add(const float* x, const float* a, const float* gamma_a, float
     const bool vec = cols % 4 == 0 && nv <= 8 && aligned16(x) && aligned16(a) && aligned16(gamma_a) && aligned16(y) &&
                      (!y_norm || (aligned16(gamma_y) && aligned16(y_norm)));
     if (vec && nv <= 2)
-        hipLaunchKernelGGL(rms_norm_add_vec_kernel<2>, grid, block, 0, S(stream), g);
+        PXK_LAUNCH(rms_norm_add_vec_kernel<2>, grid, block, 0, S(stream), g);
     else if (vec && nv <= 4)
-        hipLaunchKernelGGL(rms_norm_add_vec_kernel<4>, grid, block, 0, S(stream), g);
+        PXK_LAUNCH(rms_norm_add_vec_kernel<4>, grid, block, 0, S(stream), g);
     else if (vec)
-        hipLaunchKernelGGL(rms_norm_add_vec_kernel<8>, grid, block, 0, S(stream), g);
+        PXK_LAUNCH(rms_norm_add_vec_kernel<8>, grid, block, 0, S(stream), g);
     else
-        hipLaunchKernelGGL(rms_norm_add_kernel, grid, block, 0, S(stream), g, cols);
+        PXK_LAUNCH(rms_norm_add_kernel, grid, block, 0, S(stream), g, cols);
     return launched("pxk_rms_norm_add");
 }
 
 int pxk_softmax_rows(const float* in, float* out, int64_t rows, int64_t cols, void* stream) {
     int rc;
     if (!sizes_ok("pxk_softmax_rows", rows, cols, &rc)) return rc;
-    hipLaunchKernelGGL(softmax_kernel, dim3(rows_grid(rows)), dim3(kThreads), 0, S(stream), in, out, rows, cols);
+    PXK_LAUNCH(softmax_kernel, dim3(rows_grid(rows)), dim3(kThreads), 0, S(stream), in, out, rows, cols);
     return launched("pxk_softmax_rows");
 }
 
@@ -619,7 +671,7 @@ int pxk_lrp_softmax_rows(const float* x, const float* y, const float* r, float* 
                          void* stream) {
     int rc;
     if (!sizes_ok("pxk_lrp_softmax_rows", rows, cols, &rc)) return rc;
-    hipLaunchKernelGGL(lrp_softmax_kernel, dim3(rows_grid(rows)), dim3(kThreads), 0, S(stream), x, y, r, r_in, rows,
+    PXK_LAUNCH(lrp_softmax_kernel, dim3(rows_grid(rows)), dim3(kThreads), 0, S(stream), x, y, r, r_in, rows,
                        cols);
     return launched("pxk_lrp_softmax_rows");
 }
@@ -630,7 +682,7 @@ int pxk_row_sums(const float* in, float* out, int64_t rows, int64_t cols, void* 
         if (rc == PXK_OK && rows > 0) return pxk_fill(out, 0.0f, rows, stream);
         return rc;
     }
-    hipLaunchKernelGGL(row_sums_kernel, dim3(rows_grid(rows)), dim3(kThreads), 0, S(stream), in, out, rows, cols);
+    PXK_LAUNCH(row_sums_kernel, dim3(rows_grid(rows)), dim3(kThreads), 0, S(stream), in, out, rows, cols);
     return launched("pxk_row_sums");
 }
 
@@ -641,9 +693,9 @@ static int reduce(const char* what, const float* a, const float* b, int64_t n, f
     if (n < 0) return fail(PXK_ERR_INVALID, "%s: negative size", what);
     if (n == 0) return pxk_fill(out, 0.0f, 1, stream);
     const unsigned blocks = static_cast<unsigned>(std::min<int64_t>(kReduceBlocks, cdiv(n, kThreads)));
-    hipLaunchKernelGGL(reduce_pass1, dim3(blocks), dim3(kThreads), 0, S(stream), a, b, n, partials);
+    PXK_LAUNCH(reduce_pass1, dim3(blocks), dim3(kThreads), 0, S(stream), a, b, n, partials);
     if (const int rc = launched(what)) return rc;
-    hipLaunchKernelGGL(reduce_pass2, dim3(1), dim3(kThreads), 0, S(stream), partials, static_cast<int>(blocks), out);
+    PXK_LAUNCH(reduce_pass2, dim3(1), dim3(kThreads), 0, S(stream), partials, static_cast<int>(blocks), out);
     return launched(what);
 }
 
@@ -660,7 +712,7 @@ int pxk_attention_softmax(const float* raw, float* p, int64_t slices, int64_t l,
     int rc;
     if (!sizes_ok("pxk_attention_softmax", slices, l, &rc)) return rc;
     if (window < 0) return fail(PXK_ERR_INVALID, "pxk_attention_softmax: negative window");
-    hipLaunchKernelGGL(attention_softmax_kernel, dim3(rows_grid(slices * l)), dim3(kThreads), 0, S(stream), raw, p,
+    PXK_LAUNCH(attention_softmax_kernel, dim3(rows_grid(slices * l)), dim3(kThreads), 0, S(stream), raw, p,
                        slices * l, l, scale, causal, window);
     return launched("pxk_attention_softmax");
 }
@@ -670,7 +722,7 @@ int pxk_attention_lrp_scores(const float* r_attn, const float* p, const float* r
     int rc;
     if (!sizes_ok("pxk_attention_lrp_scores", slices, l, &rc)) return rc;
     if (window < 0) return fail(PXK_ERR_INVALID, "pxk_attention_lrp_scores: negative window");
-    hipLaunchKernelGGL(attention_lrp_scores_kernel, dim3(rows_grid(slices * l)), dim3(kThreads), 0, S(stream), r_attn,
+    PXK_LAUNCH(attention_lrp_scores_kernel, dim3(rows_grid(slices * l)), dim3(kThreads), 0, S(stream), r_attn,
                        p, raw, s, slices * l, l, scale, eps, causal, window);
     return launched("pxk_attention_lrp_scores");
 }
@@ -681,7 +733,7 @@ int pxk_rms_norm_heads(const float* in, int64_t ld_in, float* out, int64_t ld_ou
         return fail(PXK_ERR_INVALID, "pxk_rms_norm_heads: bad sizes or row strides");
     if (rows == 0) return PXK_OK;
     if (!in || !out || !gamma) return fail(PXK_ERR_INVALID, "pxk_rms_norm_heads: NULL operand");
-    hipLaunchKernelGGL(rms_norm_heads_kernel, dim3(rows_grid(rows * heads)), dim3(kThreads), 0, S(stream), in, ld_in,
+    PXK_LAUNCH(rms_norm_heads_kernel, dim3(rows_grid(rows * heads)), dim3(kThreads), 0, S(stream), in, ld_in,
                        out, ld_out, gamma, rows, heads, head_dim, eps);
     return launched("pxk_rms_norm_heads");
 }
@@ -699,7 +751,7 @@ int pxk_lrp_rope_rows(const float* acc, int64_t ld_acc, const float* x, int64_t 
         return fail(PXK_ERR_INVALID, "pxk_lrp_rope_rows: a required operand is NULL");
     const RopeRelArgs a{acc, ld_acc, x, ldx, y, ldy, z, ldz, bias, cos_t, sin_t, g, ldg, rows, seq_len, heads,
                         head_dim, eps, rotate_half, rel_only};
-    hipLaunchKernelGGL(rope_rel_rows_kernel, dim3(grid_for(rows * heads * (head_dim / 2), kThreads)), dim3(kThreads), 0,
+    PXK_LAUNCH(rope_rel_rows_kernel, dim3(grid_for(rows * heads * (head_dim / 2), kThreads)), dim3(kThreads), 0,
                        S(stream), a);
     return launched("pxk_lrp_rope_rows");
 }
@@ -713,7 +765,7 @@ int pxk_rope_qk(const float* q_in, const float* k_in, int64_t ld_in, float* q_ou
         return fail(PXK_ERR_INVALID, "pxk_rope_qk: row strides must hold every head");
     if (rows == 0) return PXK_OK;
     const int64_t work = rows * (heads + kv_heads) * (head_dim / 2);
-    hipLaunchKernelGGL(rope_qk_kernel, dim3(grid_for(work, kThreads)), dim3(kThreads), 0, S(stream), q_in, k_in, ld_in,
+    PXK_LAUNCH(rope_qk_kernel, dim3(grid_for(work, kThreads)), dim3(kThreads), 0, S(stream), q_in, k_in, ld_in,
                        q_out, k_out, ld_out, cos_t, sin_t, rows, seq_len, heads, kv_heads, head_dim, rotate_half);
     return launched("pxk_rope_qk");
 }
@@ -724,7 +776,7 @@ int pxk_rope_rotate(const float* in, const float* cos_t, const float* sin_t, flo
         return fail(PXK_ERR_INVALID, "pxk_rope_rotate: bad sizes");
     const int64_t work = slices * seq_len * (head_dim / 2);
     if (work == 0) return PXK_OK;
-    hipLaunchKernelGGL(rope_rotate_kernel, dim3(grid_for(work, kThreads)), dim3(kThreads), 0, S(stream), in, cos_t,
+    PXK_LAUNCH(rope_rotate_kernel, dim3(grid_for(work, kThreads)), dim3(kThreads), 0, S(stream), in, cos_t,
                        sin_t, out, slices, seq_len, head_dim, inverse, rotate_half);
     return launched("pxk_rope_rotate");
 }
@@ -735,7 +787,7 @@ int pxk_lrp_rope(const float* x, const float* y, const float* r, const float* co
         return fail(PXK_ERR_INVALID, "pxk_lrp_rope: bad sizes");
     const int64_t work = slices * seq_len * (head_dim / 2);
     if (work == 0) return PXK_OK;
-    hipLaunchKernelGGL(lrp_rope_kernel, dim3(grid_for(work, kThreads)), dim3(kThreads), 0, S(stream), x, y, r, cos_t,
+    PXK_LAUNCH(lrp_rope_kernel, dim3(grid_for(work, kThreads)), dim3(kThreads), 0, S(stream), x, y, r, cos_t,
                        sin_t, r_in, slices, seq_len, head_dim, eps, rotate_half);
     return launched("pxk_lrp_rope");
 }
@@ -744,7 +796,7 @@ int pxk_permute_0213(const float* in, float* out, int64_t d0, int64_t d1, int64_
     if (d0 < 0 || d1 < 0 || d2 < 0 || d3 < 0) return fail(PXK_ERR_INVALID, "pxk_permute_0213: negative size");
     const int64_t n = d0 * d1 * d2 * d3;
     if (n == 0) return PXK_OK;
-    hipLaunchKernelGGL(permute_kernel, dim3(grid_for(n, kThreads)), dim3(kThreads), 0, S(stream), in, out, d0, d1, d2,
+    PXK_LAUNCH(permute_kernel, dim3(grid_for(n, kThreads)), dim3(kThreads), 0, S(stream), in, out, d0, d1, d2,
                        d3);
     return launched("pxk_permute_0213");
 }
@@ -755,7 +807,7 @@ int pxk_attention_mask_fill(float* scores, const float* key_keep, int64_t batch,
         return fail(PXK_ERR_INVALID, "pxk_attention_mask_fill: negative size");
     const int64_t n = batch * heads * q_len * k_len;
     if (n == 0 || (!causal && key_keep == nullptr)) return PXK_OK;
-    hipLaunchKernelGGL(mask_fill_kernel, dim3(grid_for(n, kThreads)), dim3(kThreads), 0, S(stream), scores, key_keep,
+    PXK_LAUNCH(mask_fill_kernel, dim3(grid_for(n, kThreads)), dim3(kThreads), 0, S(stream), scores, key_keep,
                        batch, heads, q_len, k_len, causal, q_offset, window, value);
     return launched("pxk_attention_mask_fill");
 }
@@ -774,9 +826,38 @@ int pxk_lm_seed(const float* logits, int64_t n, int64_t l, int64_t vocab, const 
         }
     }
     if (const int rc = pxk_fill(seed, 0.0f, n * l * vocab, stream)) return rc;
-    hipLaunchKernelGGL(lm_seed_kernel, dim3(static_cast<unsigned>(n)), dim3(kSeedThreads), 0, S(stream), logits, l, vocab,
+    PXK_LAUNCH(lm_seed_kernel, dim3(static_cast<unsigned>(n)), dim3(kSeedThreads), 0, S(stream), logits, l, vocab,
                        targets_in ? 1 : 0, given, targets_out, seed, unit);
     return launched("pxk_lm_seed");
+}
+
+int pxk_lm_seed_head_relevance(const pxk_seed_head_desc* d, void* stream) {
+    if (d == nullptr) return fail(PXK_ERR_INVALID, "pxk_lm_seed_head_relevance: descriptor is NULL");
+    if (d->n <= 0 || d->l <= 0 || d->vocab <= 0 || d->d <= 0)
+        return fail(PXK_ERR_INVALID, "pxk_lm_seed_head_relevance: sizes must be positive");
+    if (!d->logits || !d->x || !d->e || !d->targets_out)
+        return fail(PXK_ERR_INVALID, "pxk_lm_seed_head_relevance: logits, x, e and targets_out are required");
+    const bool split = d->r_a != nullptr;
+    if (split ? (!d->r_b || !d->a || !d->b || !d->s) : d->r == nullptr)
+        return fail(PXK_ERR_INVALID, "pxk_lm_seed_head_relevance: needs r, or a, b, s, r_a and r_b for the split");
+    if (d->n * d->l > (int64_t{1} << 31) - 1) return fail(PXK_ERR_INVALID, "pxk_lm_seed_head_relevance: too many rows");
+    Targets given{};
+    if (d->targets_in) {
+        if (d->n > 64) return fail(PXK_ERR_INVALID, "pxk_lm_seed_head_relevance: at most 64 sequences with given targets");
+        for (int64_t i = 0; i < d->n; ++i) {
+            if (d->targets_in[i] < 0 || d->targets_in[i] >= d->vocab)
+                return fail(PXK_ERR_INVALID, "pxk_lm_seed_head_relevance: target %lld outside the vocabulary",
+                            static_cast<long long>(d->targets_in[i]));
+            given.t[i] = d->targets_in[i];
+        }
+    }
+    PXK_LAUNCH(lm_seed_kernel, dim3(static_cast<unsigned>(d->n)), dim3(kSeedThreads), 0, S(stream), d->logits, d->l,
+               d->vocab, d->targets_in ? 1 : 0, given, d->targets_out, static_cast<float*>(nullptr), d->unit);
+    if (const int rc = launched("pxk_lm_seed_head_relevance (targets)")) return rc;
+    const SeedHeadArgs a{d->logits, d->x, d->e, d->targets_out, d->r, d->a, d->b, d->s, d->r_a, d->r_b,
+                         d->l, d->vocab, d->d, d->eps, d->unit};
+    PXK_LAUNCH(seed_head_rows_kernel, dim3(static_cast<unsigned>(d->n * d->l)), dim3(kThreads), 0, S(stream), a);
+    return launched("pxk_lm_seed_head_relevance");
 }
 
 }  // extern "C"

@@ -233,11 +233,11 @@ extern "C" int pxk_lrp_rule_weights(const pxk_rule_params* p, const pxk_rule_blo
         const WeightArgs wa{k.w, k.ld, in, k.cols, col0, out, p->rule, p->gamma, p->low, p->high, w2};
         const dim3 grid(static_cast<unsigned>(cdiv(k.cols, 32)), static_cast<unsigned>(cdiv(in, 32)));
         if (k.trans)
-            hipLaunchKernelGGL(rule_weights_kernel<true>, grid, dim3(kThreads), 0, S(stream), wa);
+            PXK_LAUNCH(rule_weights_kernel<true>, grid, dim3(kThreads), 0, S(stream), wa);
         else
-            hipLaunchKernelGGL(rule_weights_kernel<false>, grid, dim3(kThreads), 0, S(stream), wa);
+            PXK_LAUNCH(rule_weights_kernel<false>, grid, dim3(kThreads), 0, S(stream), wa);
         const BiasArgs ba{k.w, k.ld, k.trans, k.bias, in, k.cols, col0, out, p->rule, p->gamma, p->low, p->high, b2};
-        hipLaunchKernelGGL(rule_bias_kernel, dim3(static_cast<unsigned>(cdiv(k.cols, kThreads))), dim3(kThreads), 0,
+        PXK_LAUNCH(rule_bias_kernel, dim3(static_cast<unsigned>(cdiv(k.cols, kThreads))), dim3(kThreads), 0,
                            S(stream), ba);
         if (const int rc = launched("pxk_lrp_rule_weights")) return rc;
         col0 += k.cols;
@@ -249,7 +249,7 @@ extern "C" int pxk_lrp_sign_split(const float* x, int64_t ldx, int64_t rows, int
     if (rows < 0 || in < 0 || ldx < in) return fail(PXK_ERR_INVALID, "pxk_lrp_sign_split: bad sizes");
     if (rows == 0 || in == 0) return PXK_OK;
     if (!x || !out) return fail(PXK_ERR_INVALID, "pxk_lrp_sign_split: NULL operand");
-    hipLaunchKernelGGL(sign_split_kernel, dim3(grid_for(rows * in, kThreads)), dim3(kThreads), 0, S(stream), x, ldx,
+    PXK_LAUNCH(sign_split_kernel, dim3(grid_for(rows * in, kThreads)), dim3(kThreads), 0, S(stream), x, ldx,
                        rows, in, out);
     return launched("pxk_lrp_sign_split");
 }
@@ -268,7 +268,7 @@ extern "C" int pxk_lrp_rule_divide(const pxk_rule_params* p, const float* r, int
         return fail(PXK_ERR_INVALID, "pxk_lrp_rule_divide: a required operand is NULL");
     const DivideArgs a{r, ldr, r_cols, den, ld_den, z, ldz, bias, b2, rows, out, g, ldg, p->rule, p->eps, p->alpha,
                        p->beta};
-    hipLaunchKernelGGL(rule_divide_kernel, dim3(grid_for(rows * out, kThreads)), dim3(kThreads), 0, S(stream), a);
+    PXK_LAUNCH(rule_divide_kernel, dim3(grid_for(rows * out, kThreads)), dim3(kThreads), 0, S(stream), a);
     return launched("pxk_lrp_rule_divide");
 }
 
@@ -283,6 +283,6 @@ extern "C" int pxk_lrp_rule_combine(int rule, const float* x, int64_t ldx, const
     if (!x || !c || !r_in || (split_sum && (!split_a || !split_b || !r_b)))
         return fail(PXK_ERR_INVALID, "pxk_lrp_rule_combine: a required operand is NULL");
     const CombineArgs a{x, ldx, c, ldc, add, rows, in, r_in, ld, split_a, split_b, split_sum, r_b, rule, eps};
-    hipLaunchKernelGGL(rule_combine_kernel, dim3(grid_for(rows * in, kThreads)), dim3(kThreads), 0, S(stream), a);
+    PXK_LAUNCH(rule_combine_kernel, dim3(grid_for(rows * in, kThreads)), dim3(kThreads), 0, S(stream), a);
     return launched("pxk_lrp_rule_combine");
 }

@@ -200,9 +200,9 @@ def synchronize():
 
 def launch_profile(run_once, reps=5):
     """Records every kernel launch of one call of run_once() on the backend (pxa_launch_log_*), then
-    replays those launches in order `reps` times with a HIP event before each. Returns one dict per
-    launch: kernel (name and variant), family ("gemm", "attention", "rows"), algorithmic flops and
-    bytes, and seconds (mean interval: kernel time plus the dispatch gap to the next launch). The
+    replays those launches in order `reps` times, each kernel recording its own start and end
+    events. Returns one dict per launch: kernel (name and variant), family ("gemm", "attention",
+    "rows"), algorithmic flops and bytes, and seconds (the mean summed duration of its kernels). The
     replays rewrite the outputs of the recorded pass."""
     h = N.host()
     N.host_check(h.pxa_launch_log_start())
