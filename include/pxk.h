@@ -555,6 +555,47 @@ typedef struct pxk_seed_head_desc {
 } pxk_seed_head_desc;
 int pxk_lm_seed_head_relevance(const pxk_seed_head_desc* d, void* stream);
 
+/* ---- training and the non-LLM modules' row and element ops (training.hip) ---------------------
+ * Simple kernels for the DeviceBackend virtuals outside the forward + AttnLRP path: one thread per
+ * element, or one wave64 per row with fixed-order wave reductions. Each is the reference's
+ * per-element expression; row sums differ from its sequential loops only by rounding. */
+/* elementwise_backward (device_backend.hpp:428; cpu_backend.cpp:226-270); op as ElementwiseOp. */
+int pxk_elementwise_backward(int op, const float* x, const float* grad_out, float* grad_in, int64_t n, void* stream);
+/* softmax_rows_backward (device_backend.hpp:462; cpu_backend.cpp:312-323): dx = y (dy - sum y dy). */
+int pxk_softmax_rows_backward(const float* y, const float* dy, float* dx, int64_t rows, int64_t cols, void* stream);
+/* rms_norm_backward (device_backend.hpp:557; row_math.hpp:75-86). */
+int pxk_rms_norm_backward(const float* grad_out, const float* gamma, const float* in, const float* row_rms,
+                          float* grad_in, float* gamma_terms, int64_t rows, int64_t cols, void* stream);
+/* layer_norm_forward / layer_norm_backward (device_backend.hpp; row_math.hpp:15-56). */
+int pxk_layer_norm_forward(const float* in, const float* gamma, const float* beta, float* xhat, float* out,
+                           float* row_std, int64_t rows, int64_t cols, float eps, void* stream);
+int pxk_layer_norm_backward(const float* grad_out, const float* gamma, const float* xhat, const float* row_std,
+                            float* grad_in, int64_t rows, int64_t cols, void* stream);
+/* logsumexp_rows (cpu_backend.cpp:325-338). */
+int pxk_logsumexp_rows(const float* in, float* out, int64_t rows, int64_t cols, void* stream);
+/* scatter_add_rows (cpu_backend.cpp:468-475): table[indices[i]] += src[i], i ascending per column. */
+int pxk_scatter_add_rows(const float* src, const float* indices, float* table, int64_t count, int64_t dim,
+                         void* stream);
+/* adam_step (cpu_backend.cpp:340-351). */
+int pxk_adam_step(float* param, const float* grad, float* m, float* v, int64_t n, float lr, float beta1, float beta2,
+                  float eps, float bias_correction1, float bias_correction2, void* stream);
+/* dropout_forward (cpu_backend.cpp:362-369): the counter-based SplitMix64 uniform of (seed, offset + i). */
+int pxk_dropout_forward(const float* in, float* out, float* mask, int64_t n, float p, float scale, uint64_t seed,
+                        uint64_t offset, void* stream);
+/* bce_with_logits (grad 0) and bce_with_logits_grad (grad 1, times scale) (cpu_backend.cpp:371-383). */
+int pxk_bce_with_logits(const float* logits, const float* target, float* out, int64_t n, int grad, float scale,
+                        void* stream);
+/* tanh_gaussian_forward / tanh_gaussian_backward (row_math.hpp:131-160); the row log-probability in double. */
+int pxk_tanh_gaussian_forward(const float* mean, const float* log_std, const float* eps, float* action,
+                              float* std_cache, float* log_prob, int64_t rows, int64_t cols, float stabilizer,
+                              double half_log_two_pi, void* stream);
+int pxk_tanh_gaussian_backward(const float* action, const float* std_cache, const float* eps, const float* grad_action,
+                               const float* grad_log_prob, float* grad_mean, float* grad_log_std, int64_t n,
+                               float stabilizer, void* stream);
+/* top_k_rows (top_k_math.hpp:20-48): NaN ranks highest, ties keep the lower column; indices as floats. */
+int pxk_top_k_rows(const float* in, float* values, float* indices, int64_t rows, int64_t cols, int64_t k, int largest,
+                   void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -142,6 +142,77 @@ void elementwise(int op, const float* in, float* out, size_t n) {  // cpu_backen
     }
 }
 
+// ---- backward of the activation, softmax and RMSNorm rows (training; not on the explain path) ----
+
+float gelu_tanh_slope(float x) {  // pointwise_math.hpp:39-45: 0.5 (1 + t) + 0.5 x (1 - t^2) b (1 + 3 k x^2)
+    const float kBeta = 0.7978845608028654f;
+    const float kKappa = 0.044715f;
+    const float x2 = x * x;
+    const float t = std::tanh(kBeta * (x + kKappa * x2 * x));
+    return 0.5f * (1.0f + t) + 0.5f * x * (1.0f - t * t) * kBeta * (1.0f + 3.0f * kKappa * x2);
+}
+
+float gelu_slope(float x) {  // pointwise_math.hpp:55-60: Phi(x) + x phi(x)
+    const float kInvSqrt2 = 0.7071067811865476f;
+    const float kInvSqrt2Pi = 0.3989422804014327f;
+    return 0.5f * (1.0f + std::erf(x * kInvSqrt2)) + x * kInvSqrt2Pi * std::exp(-0.5f * x * x);
+}
+
+void elementwise_backward(int op, const float* x, const float* gy, float* gx, size_t n) {  // cpu_backend.cpp:226-270
+    for (size_t i = 0; i < n; ++i) {
+        const float v = x[i], g = gy[i];
+        float d = 0.0f;
+        switch (op) {
+            case 0: gx[i] = v > 0.0f ? g : 0.0f; continue;
+            case 1: d = -1.0f; break;
+            case 2: {
+                const float t = std::tanh(v);
+                d = 1.0f - t * t;
+                break;
+            }
+            case 3: {
+                const float sg = sigmoid(v);
+                d = sg * (1.0f - sg);
+                break;
+            }
+            case 4: {
+                const float sg = sigmoid(v);
+                d = sg + v * sg * (1.0f - sg);
+                break;
+            }
+            case 5: d = std::exp(v); break;
+            case 6: d = gelu_tanh_slope(v); break;
+            case 7: d = gelu_slope(v); break;
+            default: throw std::invalid_argument("elementwise_backward: unknown op");
+        }
+        gx[i] = g * d;
+    }
+}
+
+void softmax_rows_backward(const float* y, const float* dy, float* dx, size_t rows, size_t cols) {  // :312-323
+    for (size_t r = 0; r < rows; ++r) {
+        const size_t base = r * cols;
+        float dot = 0.0f;
+        for (size_t j = 0; j < cols; ++j) dot += y[base + j] * dy[base + j];
+        for (size_t j = 0; j < cols; ++j) dx[base + j] = y[base + j] * (dy[base + j] - dot);
+    }
+}
+
+void rms_norm_backward(const float* gy, const float* gamma, const float* x, const float* row_rms, float* gx,
+                       float* gterms, size_t rows, size_t cols) {  // cpu_backend.cpp:410-417, row_math.hpp:75-86
+    const float D = static_cast<float>(cols);
+    for (size_t r = 0; r < rows; ++r) {
+        const size_t o = r * cols;
+        const float rms = row_rms[r];
+        float dot = 0.0f;
+        for (size_t i = 0; i < cols; ++i) dot += gy[o + i] * gamma[i] * x[o + i];
+        for (size_t i = 0; i < cols; ++i) {
+            gterms[o + i] = gy[o + i] * x[o + i] / rms;
+            gx[o + i] = gy[o + i] * gamma[i] / rms - (x[o + i] / (D * rms * rms * rms)) * dot;
+        }
+    }
+}
+
 void add(const float* a, const float* b, float* out, size_t n) {  // :165-169
     for (size_t i = 0; i < n; ++i) out[i] = a[i] + b[i];
 }
@@ -1277,6 +1348,16 @@ void pxo_gemm_ex(const float* a, int ta, const float* b, int tb, float* out, siz
     gemm_ex(a, ta != 0, b, tb != 0, out, m, k, n, beta);
 }
 void pxo_elementwise(int op, const float* in, float* out, size_t n) { elementwise(op, in, out, n); }
+void pxo_elementwise_backward(int op, const float* x, const float* gy, float* gx, size_t n) {
+    elementwise_backward(op, x, gy, gx, n);
+}
+void pxo_softmax_rows_backward(const float* y, const float* dy, float* dx, size_t rows, size_t cols) {
+    softmax_rows_backward(y, dy, dx, rows, cols);
+}
+void pxo_rms_norm_backward(const float* gy, const float* gamma, const float* x, const float* row_rms, float* gx,
+                           float* gterms, size_t rows, size_t cols) {
+    rms_norm_backward(gy, gamma, x, row_rms, gx, gterms, rows, cols);
+}
 void pxo_add(const float* a, const float* b, float* out, size_t n) { add(a, b, out, n); }
 void pxo_mul(const float* a, const float* b, float* out, size_t n) { mul(a, b, out, n); }
 void pxo_axpby(float alpha, const float* x, float beta, const float* y, float* out, size_t n) {

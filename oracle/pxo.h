@@ -126,6 +126,13 @@ void pxo_gemm(const float* a, const float* b, float* out, size_t m, size_t k, si
 void pxo_gemm_ex(const float* a, int transpose_a, const float* b, int transpose_b, float* out, size_t m, size_t k,
                  size_t n, float beta);
 void pxo_elementwise(int op, const float* in, float* out, size_t n);
+/* Backward rows of training (device_backend.hpp:428, 462, 557): ReLU as a select, the other
+ * activations' slopes times the gradient; softmax dx = y (dy - sum y dy); RMSNorm's input
+ * gradient and per-element gamma terms. */
+void pxo_elementwise_backward(int op, const float* x, const float* grad_out, float* grad_in, size_t n);
+void pxo_softmax_rows_backward(const float* y, const float* dy, float* dx, size_t rows, size_t cols);
+void pxo_rms_norm_backward(const float* grad_out, const float* gamma, const float* in, const float* row_rms,
+                           float* grad_in, float* gamma_terms, size_t rows, size_t cols);
 void pxo_add(const float* a, const float* b, float* out, size_t n);
 void pxo_mul(const float* a, const float* b, float* out, size_t n);
 void pxo_axpby(float alpha, const float* x, float beta, const float* y, float* out, size_t n);

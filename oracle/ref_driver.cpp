@@ -398,6 +398,7 @@ int pxr_mlp_explain(int layers, const int64_t* in, const int64_t* out, const flo
 }
 
 #ifndef PXR_ON_MI355X
+// ---- CPU build only: host-pointer helpers of the oracle tests ----
 void pxr_lrp_bilinear_matmul(const float* a, const float* b, const float* o, const float* r_o, float* r_a, float* r_b,
                              size_t slices, size_t m, size_t p, size_t q, float eps, int bt) {
     CPUBackend be;
@@ -408,8 +409,10 @@ void pxr_gemm_ex(const float* a, int ta, const float* b, int tb, float* out, siz
     CPUBackend be;
     be.gemm_ex(a, ta != 0, b, tb != 0, out, m, k, n, beta);
 }
-#else
-// ---- pxr_be_*: each DeviceBackend virtual of the process-wide MI355XBackend, device pointers ----
+#endif
+
+// ---- pxr_be_*: each DeviceBackend virtual of this library's backend: host pointers on the
+// reference's CPUBackend, device pointers on MI355XBackend; the tests run both on the same data ----
 
 #define PXR_BE(name, params, call) \
     int pxr_be_##name params { return guarded([&] { driver_backend()->call; }); }
@@ -474,8 +477,51 @@ PXR_BE(copy_2d, (float* dst, size_t ds, const float* src, size_t ss, size_t rows
        copy_2d(dst, ds, src, ss, rows, cols))
 PXR_BE(accumulate_rows, (const float* in, float* out, size_t rows, size_t cols), accumulate_rows(in, out, rows, cols))
 
+PXR_BE(elementwise_backward, (int op, const float* x, const float* g, float* out, size_t n),
+       elementwise_backward(static_cast<ElementwiseOp>(op), x, g, out, n))
+PXR_BE(softmax_rows_backward, (const float* y, const float* dy, float* dx, size_t rows, size_t cols),
+       softmax_rows_backward(y, dy, dx, rows, cols))
+PXR_BE(rms_norm_backward,
+       (const float* g, const float* gamma, const float* x, const float* rms, float* gx, float* gt, size_t rows,
+        size_t cols),
+       rms_norm_backward(g, gamma, x, rms, gx, gt, rows, cols))
+PXR_BE(layer_norm_forward,
+       (const float* x, const float* gamma, const float* beta, float* xhat, float* out, float* sd, size_t rows,
+        size_t cols, float eps),
+       layer_norm_forward(x, gamma, beta, xhat, out, sd, rows, cols, eps))
+PXR_BE(layer_norm_backward,
+       (const float* g, const float* gamma, const float* xhat, const float* sd, float* gx, size_t rows, size_t cols),
+       layer_norm_backward(g, gamma, xhat, sd, gx, rows, cols))
+PXR_BE(logsumexp_rows, (const float* in, float* out, size_t rows, size_t cols), logsumexp_rows(in, out, rows, cols))
+PXR_BE(scatter_add_rows, (const float* src, const float* idx, float* table, size_t count, size_t dim),
+       scatter_add_rows(src, idx, table, count, dim))
+PXR_BE(adam_step,
+       (float* p, const float* g, float* m, float* v, size_t n, float lr, float b1, float b2, float eps, float c1,
+        float c2),
+       adam_step(p, g, m, v, n, lr, b1, b2, eps, c1, c2))
+PXR_BE(dropout_forward, (const float* in, float* out, float* mask, size_t n, float p, float scale, uint64_t seed,
+                         uint64_t offset),
+       dropout_forward(in, out, mask, n, p, scale, seed, offset))
+PXR_BE(bce_with_logits, (const float* x, const float* y, float* out, size_t n), bce_with_logits(x, y, out, n))
+PXR_BE(bce_with_logits_grad, (const float* x, const float* y, float* out, size_t n, float scale),
+       bce_with_logits_grad(x, y, out, n, scale))
+PXR_BE(tanh_gaussian_forward,
+       (const float* mean, const float* log_std, const float* e, float* action, float* std_cache, float* log_prob,
+        size_t rows, size_t cols, float stabilizer, double half_log_two_pi),
+       tanh_gaussian_forward(mean, log_std, e, action, std_cache, log_prob, rows, cols, stabilizer, half_log_two_pi))
+PXR_BE(tanh_gaussian_backward,
+       (const float* action, const float* std_cache, const float* e, const float* ga, const float* glp, float* gm,
+        float* gls, size_t n, float stabilizer),
+       tanh_gaussian_backward(action, std_cache, e, ga, glp, gm, gls, n, stabilizer))
+PXR_BE(top_k_rows, (const float* in, float* values, float* indices, size_t rows, size_t cols, size_t k, int largest),
+       top_k_rows(in, values, indices, rows, cols, k, largest != 0))
+
 int pxr_be_synchronize(void) {
+#ifdef PXR_ON_MI355X
     return guarded([&] { static_cast<MI355XBackend*>(driver_backend())->synchronize(); });
+#else
+    return 0;
+#endif
 }
 
 int pxr_be_sum(const float* in, size_t n, float* out) {
@@ -493,6 +539,5 @@ int pxr_be_allocate(size_t bytes, void** out) {
 void pxr_be_free(void* p) { driver_backend()->free(p); }
 
 int pxr_be_device(void) { return static_cast<int>(driver_backend()->device()); }
-#endif
 
 }  // extern "C"

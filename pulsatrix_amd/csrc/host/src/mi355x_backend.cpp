@@ -475,44 +475,73 @@ void MI355XBackend::replay() {
 
 // ---- outside the path ---------------------------------------------------------------------------
 
-void MI355XBackend::elementwise_backward(ElementwiseOp, const float*, const float*, float*, size_t) {
-    off_path("elementwise_backward");
+void MI355XBackend::elementwise_backward(ElementwiseOp o, const float* x, const float* grad_out, float* grad_in,
+                                         size_t n) {
+    check(pxk_elementwise_backward(static_cast<int>(o), x, grad_out, grad_in, static_cast<int64_t>(n), stream_),
+          "MI355XBackend::elementwise_backward");
 }
-void MI355XBackend::softmax_rows_backward(const float*, const float*, float*, size_t, size_t) {
-    off_path("softmax_rows_backward");
+void MI355XBackend::softmax_rows_backward(const float* y, const float* dy, float* dx, size_t rows, size_t cols) {
+    check(pxk_softmax_rows_backward(y, dy, dx, static_cast<int64_t>(rows), static_cast<int64_t>(cols), stream_),
+          "MI355XBackend::softmax_rows_backward");
 }
-void MI355XBackend::logsumexp_rows(const float*, float*, size_t, size_t) { off_path("logsumexp_rows"); }
-void MI355XBackend::adam_step(float*, const float*, float*, float*, size_t, float, float, float, float, float, float) {
-    off_path("adam_step");
+void MI355XBackend::logsumexp_rows(const float* in, float* out, size_t rows, size_t cols) {
+    check(pxk_logsumexp_rows(in, out, static_cast<int64_t>(rows), static_cast<int64_t>(cols), stream_),
+          "MI355XBackend::logsumexp_rows");
 }
-void MI355XBackend::dropout_forward(const float*, float*, float*, size_t, float, float, uint64_t, uint64_t) {
-    off_path("dropout_forward");
+void MI355XBackend::adam_step(float* param, const float* grad, float* m, float* v, size_t n, float lr, float beta1,
+                              float beta2, float eps, float bias_correction1, float bias_correction2) {
+    check(pxk_adam_step(param, grad, m, v, static_cast<int64_t>(n), lr, beta1, beta2, eps, bias_correction1,
+                        bias_correction2, stream_),
+          "MI355XBackend::adam_step");
 }
-void MI355XBackend::bce_with_logits(const float*, const float*, float*, size_t) { off_path("bce_with_logits"); }
-void MI355XBackend::bce_with_logits_grad(const float*, const float*, float*, size_t, float) {
-    off_path("bce_with_logits_grad");
+void MI355XBackend::dropout_forward(const float* in, float* out, float* mask, size_t n, float p, float scale,
+                                    uint64_t seed, uint64_t offset) {
+    check(pxk_dropout_forward(in, out, mask, static_cast<int64_t>(n), p, scale, seed, offset, stream_),
+          "MI355XBackend::dropout_forward");
 }
-void MI355XBackend::layer_norm_forward(const float*, const float*, const float*, float*, float*, float*, size_t, size_t,
-                                       float) {
-    off_path("layer_norm_forward");
+void MI355XBackend::bce_with_logits(const float* logits, const float* target, float* out, size_t n) {
+    check(pxk_bce_with_logits(logits, target, out, static_cast<int64_t>(n), 0, 1.0f, stream_),
+          "MI355XBackend::bce_with_logits");
 }
-void MI355XBackend::layer_norm_backward(const float*, const float*, const float*, const float*, float*, size_t, size_t) {
-    off_path("layer_norm_backward");
+void MI355XBackend::bce_with_logits_grad(const float* logits, const float* target, float* grad, size_t n, float scale) {
+    check(pxk_bce_with_logits(logits, target, grad, static_cast<int64_t>(n), 1, scale, stream_),
+          "MI355XBackend::bce_with_logits_grad");
 }
-void MI355XBackend::rms_norm_backward(const float*, const float*, const float*, const float*, float*, float*, size_t,
-                                      size_t) {
-    off_path("rms_norm_backward");
+void MI355XBackend::layer_norm_forward(const float* in, const float* gamma, const float* beta, float* xhat, float* out,
+                                       float* row_std, size_t rows, size_t cols, float eps) {
+    check(pxk_layer_norm_forward(in, gamma, beta, xhat, out, row_std, static_cast<int64_t>(rows),
+                                 static_cast<int64_t>(cols), eps, stream_),
+          "MI355XBackend::layer_norm_forward");
 }
-void MI355XBackend::scatter_add_rows(const float*, const float*, float*, size_t, size_t) {
-    off_path("scatter_add_rows");
+void MI355XBackend::layer_norm_backward(const float* grad_out, const float* gamma, const float* xhat,
+                                        const float* row_std, float* grad_in, size_t rows, size_t cols) {
+    check(pxk_layer_norm_backward(grad_out, gamma, xhat, row_std, grad_in, static_cast<int64_t>(rows),
+                                  static_cast<int64_t>(cols), stream_),
+          "MI355XBackend::layer_norm_backward");
 }
-void MI355XBackend::tanh_gaussian_forward(const float*, const float*, const float*, float*, float*, float*, size_t,
-                                          size_t, float, double) {
-    off_path("tanh_gaussian_forward");
+void MI355XBackend::rms_norm_backward(const float* grad_out, const float* gamma, const float* in, const float* row_rms,
+                                      float* grad_in, float* gamma_terms, size_t rows, size_t cols) {
+    check(pxk_rms_norm_backward(grad_out, gamma, in, row_rms, grad_in, gamma_terms, static_cast<int64_t>(rows),
+                                static_cast<int64_t>(cols), stream_),
+          "MI355XBackend::rms_norm_backward");
 }
-void MI355XBackend::tanh_gaussian_backward(const float*, const float*, const float*, const float*, const float*,
-                                           float*, float*, size_t, float) {
-    off_path("tanh_gaussian_backward");
+void MI355XBackend::scatter_add_rows(const float* src, const float* indices, float* table, size_t count, size_t dim) {
+    check(pxk_scatter_add_rows(src, indices, table, static_cast<int64_t>(count), static_cast<int64_t>(dim), stream_),
+          "MI355XBackend::scatter_add_rows");
+}
+void MI355XBackend::tanh_gaussian_forward(const float* mean, const float* log_std, const float* eps, float* action,
+                                          float* std_cache, float* log_prob, size_t rows, size_t cols,
+                                          float stabilizer, double half_log_two_pi) {
+    check(pxk_tanh_gaussian_forward(mean, log_std, eps, action, std_cache, log_prob, static_cast<int64_t>(rows),
+                                    static_cast<int64_t>(cols), stabilizer, half_log_two_pi, stream_),
+          "MI355XBackend::tanh_gaussian_forward");
+}
+void MI355XBackend::tanh_gaussian_backward(const float* action, const float* std_cache, const float* eps,
+                                           const float* grad_action, const float* grad_log_prob, float* grad_mean,
+                                           float* grad_log_std, size_t n, float stabilizer) {
+    check(pxk_tanh_gaussian_backward(action, std_cache, eps, grad_action, grad_log_prob, grad_mean, grad_log_std,
+                                     static_cast<int64_t>(n), stabilizer, stream_),
+          "MI355XBackend::tanh_gaussian_backward");
 }
 void MI355XBackend::logic_pointwise(LogicOp, int, const float*, const float*, const float*, const float*, float*,
                                     float*, size_t, float) {
@@ -591,6 +620,11 @@ void MI355XBackend::gru_lrp_hprev(const float*, const float*, const float*, cons
 }
 void MI355XBackend::ssm_pass(SsmPassOp, const SsmPassArgs&) { off_path("ssm_pass"); }
 void MI355XBackend::rl_rows(RlRowOp, const RlRowArgs&) { off_path("rl_rows"); }
-void MI355XBackend::top_k_rows(const float*, float*, float*, size_t, size_t, size_t, bool) { off_path("top_k_rows"); }
+void MI355XBackend::top_k_rows(const float* in, float* values, float* indices, size_t rows, size_t cols, size_t k,
+                               bool largest) {
+    check(pxk_top_k_rows(in, values, indices, static_cast<int64_t>(rows), static_cast<int64_t>(cols),
+                         static_cast<int64_t>(k), largest, stream_),
+          "MI355XBackend::top_k_rows");
+}
 
 }  // namespace pulsatrix

@@ -79,6 +79,9 @@ _sig = {
     "pxo_copy_2d": "psps" + "ss",
     "pxo_accumulate_rows": "ppss",
     "pxo_column_sums": "ppssf",
+    "pxo_elementwise_backward": "nppps",
+    "pxo_softmax_rows_backward": "pppss",
+    "pxo_rms_norm_backward": "ppppppss",
 }
 _T = {"p": ctypes.c_void_p, "s": ctypes.c_size_t, "n": ctypes.c_int, "f": ctypes.c_float}
 _bound = False

@@ -291,6 +291,7 @@ def ref():
     global _ref
     if _ref is None and os.path.exists(REF_SO):
         _ref = _Lib(REF_SO, "pxr_")
+        _bind_backend_shim(_ref.lib)
     return _ref
 
 
@@ -307,7 +308,15 @@ def ref_mi355x():
 
         native.pxk()  # the HIP runtime torch loaded, and the kernel library, first
         lib = _Lib(REF_MI355X_SO, "pxr_")
-        L = lib.lib
+        _bind_backend_shim(lib.lib)
+        _ref_mi355x = lib
+    return _ref_mi355x
+
+
+def _bind_backend_shim(L):
+    """Signatures of pxr_be_* (oracle/ref_driver.cpp): each DeviceBackend virtual of the library's
+    backend, host pointers on the reference's CPUBackend, device pointers on MI355XBackend."""
+    if True:
         vp, sz, i, f = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_float
         sig = {
             "copy": [vp, vp, sz, i], "fill": [vp, f, sz], "gemm": [vp, vp, vp, sz, sz, sz],
@@ -325,6 +334,16 @@ def ref_mi355x():
             "lrp_stabilized_divide": [vp, vp, vp, vp, sz, f, i], "copy_2d": [vp, sz, vp, sz, sz, sz],
             "accumulate_rows": [vp, vp, sz, sz], "synchronize": [], "sum": [vp, sz, vp], "dot": [vp, vp, sz, vp],
             "allocate": [sz, ctypes.POINTER(vp)],
+            "elementwise_backward": [i, vp, vp, vp, sz], "softmax_rows_backward": [vp, vp, vp, sz, sz],
+            "rms_norm_backward": [vp, vp, vp, vp, vp, vp, sz, sz],
+            "layer_norm_forward": [vp, vp, vp, vp, vp, vp, sz, sz, f], "layer_norm_backward": [vp, vp, vp, vp, vp, sz, sz],
+            "logsumexp_rows": [vp, vp, sz, sz], "scatter_add_rows": [vp, vp, vp, sz, sz],
+            "adam_step": [vp, vp, vp, vp, sz, f, f, f, f, f, f],
+            "dropout_forward": [vp, vp, vp, sz, f, f, ctypes.c_uint64, ctypes.c_uint64],
+            "bce_with_logits": [vp, vp, vp, sz], "bce_with_logits_grad": [vp, vp, vp, sz, f],
+            "tanh_gaussian_forward": [vp, vp, vp, vp, vp, vp, sz, sz, f, ctypes.c_double],
+            "tanh_gaussian_backward": [vp, vp, vp, vp, vp, vp, vp, sz, f],
+            "top_k_rows": [vp, vp, vp, sz, sz, sz, i],
         }
         for name, args in sig.items():
             fn = getattr(L, "pxr_be_" + name)
@@ -333,8 +352,6 @@ def ref_mi355x():
         L.pxr_be_device.restype = ctypes.c_int
         L.pxr_linear_relevance_rule.argtypes = [_f32p, _f32p, _f32p, _f32p, ctypes.c_int64, ctypes.c_int64,
                                                 ctypes.c_int64, ctypes.POINTER(LrpRule), _f32p]
-        _ref_mi355x = lib
-    return _ref_mi355x
 
 
 def mlp_explain(lib, layers, x, targets, rule, preset=0):

@@ -395,3 +395,102 @@ def test_virtual_allocation_contract(lib):
     assert p.value
     lib.lib.pxr_be_free(p)
     lib.lib.pxr_be_free(None)
+
+
+# ---- training and non-LLM row / element virtuals: MI355XBackend against the reference CPUBackend ----
+
+def cpu_vs_gpu(lib, name, arrays, outs, args, rel=1e-5, exact=()):
+    """Runs pxr_be_<name> on the reference CPUBackend (oracle/_ref/libpxref.so, host arrays) and on
+    MI355XBackend (device copies of the same arrays); `args` names arrays by key and passes scalars
+    through. Compares each array in `outs` (exactly for the keys in `exact`)."""
+    cpu = oc.ref()
+    if cpu is None:
+        pytest.skip("oracle/_ref/libpxref.so was not built")
+    host = {k: np.ascontiguousarray(v).copy() for k, v in arrays.items()}
+    dev = {k: G.dev(v) for k, v in arrays.items()}
+    cpu.check(getattr(cpu.lib, "pxr_be_" + name)(*[host[a].ctypes.data if isinstance(a, str) else a for a in args]))
+    be(lib, name, *[dev[a] if isinstance(a, str) else a for a in args])
+    for k in outs:
+        got, exp = G.host(dev[k]), host[k]
+        if k in exact:
+            assert np.array_equal(got, exp, equal_nan=True), (name, k)
+        else:
+            G.assert_close(got, exp, rel, "%s %s" % (name, k))
+
+
+def test_virtual_backward_rows_against_reference_and_oracle(lib):
+    """elementwise_backward (every op), softmax_rows_backward and rms_norm_backward
+    (device_backend.hpp:428, 462, 557): against the compiled reference, and the trio's oracle
+    restatement (pinned bit for bit to it on the CPU) at the same tolerance."""
+    n, rows, cols = 100003, 70, 300
+    x, g = G.uniform((n,), 1) * 3, G.uniform((n,), 2)
+    for op in range(8):
+        cpu_vs_gpu(lib, "elementwise_backward", {"x": x, "g": g, "o": np.zeros_like(x)}, ["o"], [op, "x", "g", "o", n],
+                   exact=("o",) if op in (0, 1) else ())
+        ref = np.empty_like(x)
+        G.oracle_call("pxo_elementwise_backward", op, x, g, ref, n)
+        out = G.empty((n,))
+        be(lib, "elementwise_backward", op, G.dev(x), G.dev(g), out, n)
+        G.assert_close(G.host(out), ref, 1e-5, "elementwise_backward %d vs oracle" % op)
+    y = np.exp(G.uniform((rows, cols), 3))
+    y /= y.sum(axis=1, keepdims=True)
+    dy = G.uniform((rows, cols), 4)
+    cpu_vs_gpu(lib, "softmax_rows_backward", {"y": y, "dy": dy, "dx": np.zeros_like(y)}, ["dx"],
+               ["y", "dy", "dx", rows, cols])
+    xin, gamma = G.uniform((rows, cols), 5), G.uniform((cols,), 6)
+    rms = np.sqrt((xin.astype(np.float64) ** 2).mean(axis=1) + 1e-5).astype(np.float32)
+    cpu_vs_gpu(lib, "rms_norm_backward", {"g": dy, "gamma": gamma, "x": xin, "rms": rms, "gx": np.zeros_like(xin),
+                                          "gt": np.zeros_like(xin)}, ["gx", "gt"],
+               ["g", "gamma", "x", "rms", "gx", "gt", rows, cols])
+
+
+def test_virtual_layer_norm_logsumexp_scatter(lib):
+    rows, cols = 45, 257
+    x, gamma, beta, gy = G.uniform((rows, cols), 1) * 2, G.uniform((cols,), 2), G.uniform((cols,), 3), \
+        G.uniform((rows, cols), 4)
+    z = np.zeros_like(x)
+    cpu_vs_gpu(lib, "layer_norm_forward", {"x": x, "gamma": gamma, "beta": beta, "xhat": z, "out": z,
+                                           "sd": np.zeros(rows, np.float32)}, ["xhat", "out", "sd"],
+               ["x", "gamma", "beta", "xhat", "out", "sd", rows, cols, 1e-5])
+    xhat = (x - x.mean(axis=1, keepdims=True)) / np.sqrt(x.var(axis=1, keepdims=True) + 1e-5)
+    sd = np.sqrt(x.astype(np.float64).var(axis=1) + 1e-5).astype(np.float32)
+    cpu_vs_gpu(lib, "layer_norm_backward", {"g": gy, "gamma": gamma, "xhat": xhat.astype(np.float32), "sd": sd,
+                                            "gx": z}, ["gx"], ["g", "gamma", "xhat", "sd", "gx", rows, cols])
+    cpu_vs_gpu(lib, "logsumexp_rows", {"x": x * 5, "o": np.zeros(rows, np.float32)}, ["o"], ["x", "o", rows, cols])
+    # repeated indices accumulate in source order; the reference sums the same way per column
+    idx = np.array([3, 0, 3, 7, 3, 1, 0], np.float32)
+    src, table = G.uniform((7, 33), 5), G.uniform((8, 33), 6)
+    cpu_vs_gpu(lib, "scatter_add_rows", {"src": src, "idx": idx, "t": table}, ["t"], ["src", "idx", "t", 7, 33],
+               exact=("t",))
+
+
+def test_virtual_optimizer_dropout_losses_policy_topk(lib):
+    n = 10007
+    p, g, m, v = G.uniform((n,), 1), G.uniform((n,), 2), G.uniform((n,), 3) * 0.1, np.abs(G.uniform((n,), 4)) * 0.1
+    cpu_vs_gpu(lib, "adam_step", {"p": p, "g": g, "m": m, "v": v}, ["p", "m", "v"],
+               ["p", "g", "m", "v", n, 1e-3, 0.9, 0.999, 1e-8, 0.1, 0.001], rel=1e-6)
+    x = G.uniform((n,), 5)
+    z = np.zeros_like(x)
+    cpu_vs_gpu(lib, "dropout_forward", {"x": x, "o": z, "mask": z}, ["o", "mask"],
+               ["x", "o", "mask", n, 0.3, 1.0 / 0.7, 1234, 99], exact=("o", "mask"))
+    y = (G.uniform((n,), 6) > 0).astype(np.float32)
+    xl = x * 30  # both tails of the stable forms
+    cpu_vs_gpu(lib, "bce_with_logits", {"x": xl, "y": y, "o": z}, ["o"], ["x", "y", "o", n], rel=1e-6)
+    cpu_vs_gpu(lib, "bce_with_logits_grad", {"x": xl, "y": y, "o": z}, ["o"], ["x", "y", "o", n, 0.5], rel=1e-6)
+    rows, cols = 33, 6
+    mean, ls, e = G.uniform((rows, cols), 7), G.uniform((rows, cols), 8) * 0.5, G.uniform((rows, cols), 9)
+    zz = np.zeros((rows, cols), np.float32)
+    cpu_vs_gpu(lib, "tanh_gaussian_forward", {"mean": mean, "ls": ls, "e": e, "a": zz, "sd": zz,
+                                              "lp": np.zeros(rows, np.float32)}, ["a", "sd", "lp"],
+               ["mean", "ls", "e", "a", "sd", "lp", rows, cols, 1e-6, 0.9189385332046727], rel=1e-5)
+    a, sd = np.tanh(mean + np.exp(ls) * e).astype(np.float32), np.exp(ls).astype(np.float32)
+    ga, glp = G.uniform((rows, cols), 10), G.uniform((rows, cols), 11)
+    cpu_vs_gpu(lib, "tanh_gaussian_backward", {"a": a, "sd": sd, "e": e, "ga": ga, "glp": glp, "gm": zz, "gls": zz},
+               ["gm", "gls"], ["a", "sd", "e", "ga", "glp", "gm", "gls", rows * cols, 1e-6], rel=1e-5)
+    vals = G.uniform((19, 50), 12)
+    vals[3, 7] = np.nan
+    vals[5, :10] = 0.25  # ties keep the lower column
+    k = 6
+    for largest in (1, 0):
+        cpu_vs_gpu(lib, "top_k_rows", {"x": vals, "v": np.zeros((19, k), np.float32), "i": np.zeros((19, k), np.float32)},
+                   ["v", "i"], ["x", "v", "i", 19, 50, k, largest], exact=("v", "i"))

@@ -283,3 +283,52 @@ def test_oracle_gemma_block_bit_identical_to_reference():
     assert np.array_equal(yo, r.forward(x))
     seed = oc.fill_normal(yo.size, 8, 1.0).reshape(yo.shape)
     assert np.array_equal(o.relevance(seed, 0.1, True), r.relevance(seed, 0.1, True))
+
+
+@pytest.mark.skipif(oc.ref() is None, reason="oracle/_ref was not built (no reference sources)")
+def test_oracle_backward_rows_bit_identical_to_reference():
+    """The oracle's elementwise_backward (every op), softmax_rows_backward and rms_norm_backward
+    against the compiled reference CPUBackend on the same data: bit for bit."""
+    import gpu_util as G
+    R = oc.ref().lib
+    n, rows, cols = 4099, 37, 129
+    x, g = G.uniform((n,), 1) * 3, G.uniform((n,), 2)
+    for op in range(8):
+        a, b = np.empty_like(x), np.empty_like(x)
+        G.oracle_call("pxo_elementwise_backward", op, x, g, a, n)
+        R.pxr_be_elementwise_backward(op, x.ctypes.data, g.ctypes.data, b.ctypes.data, n)
+        assert np.array_equal(a, b, equal_nan=True), op
+    # ReLU is a select: a non-finite gradient where x <= 0 still gives 0
+    gi = g.copy()
+    gi[x <= 0] = np.inf
+    a = np.empty_like(x)
+    G.oracle_call("pxo_elementwise_backward", 0, x, gi, a, n)
+    assert np.all(a[x <= 0] == 0)
+    y = np.exp(G.uniform((rows, cols), 3))
+    y /= y.sum(axis=1, keepdims=True)
+    dy = G.uniform((rows, cols), 4)
+    a, b = np.empty_like(y), np.empty_like(y)
+    G.oracle_call("pxo_softmax_rows_backward", y, dy, a, rows, cols)
+    R.pxr_be_softmax_rows_backward(y.ctypes.data, dy.ctypes.data, b.ctypes.data, rows, cols)
+    assert np.array_equal(a, b)
+    # closed form: each row of dx sums to sum(y dy) (1 - sum y) = 0 for a softmax row
+    assert np.abs(a.astype(np.float64).sum(axis=1)).max() < 1e-5
+    xin, gamma = G.uniform((rows, cols), 5), G.uniform((cols,), 6)
+    rms = np.sqrt((xin.astype(np.float64) ** 2).mean(axis=1) + 1e-5).astype(np.float32)
+    ga, gb, ta, tb = (np.empty_like(xin) for _ in range(4))
+    G.oracle_call("pxo_rms_norm_backward", dy, gamma, xin, rms, ga, ta, rows, cols)
+    R.pxr_be_rms_norm_backward(dy.ctypes.data, gamma.ctypes.data, xin.ctypes.data, rms.ctypes.data, gb.ctypes.data,
+                               tb.ctypes.data, rows, cols)
+    assert np.array_equal(ga, gb) and np.array_equal(ta, tb)
+    # against the derivative itself, by central differences of RMSNorm in float64
+    x64, g64, gam = xin.astype(np.float64), dy.astype(np.float64), gamma.astype(np.float64)
+
+    def f(x):
+        return ((gam * x / np.sqrt((x ** 2).mean(axis=1, keepdims=True) + 1e-5)) * g64).sum()
+
+    h = 1e-6
+    for (r, c) in ((0, 0), (5, 17), (36, 128)):
+        e = np.zeros_like(x64)
+        e[r, c] = h
+        num = (f(x64 + e) - f(x64 - e)) / (2 * h)
+        assert abs(num - ga[r, c]) <= 1e-4 * max(1.0, abs(num)), (r, c, num, ga[r, c])
