@@ -190,6 +190,7 @@ struct RefLM {
     std::unique_ptr<CausalLM> lm;
     px_model_config c{};
     int64_t n = 0, l = 0;
+    std::vector<std::pair<std::string, int64_t>> layout;  // the parameter blob's order
 };
 
 LRPRuleConfig rule(float eps, int bias_in_denominator) {
@@ -271,6 +272,7 @@ void* pxr_lm_create(const px_model_config* cfg, const float* params) {
         if (!cfg->tie_word_embeddings) layout.push_back({"lm_head.weight", cfg->hidden_size * cfg->vocab_size});
         load(*m->lm, layout, params, m->be);
         m->c = *cfg;
+        m->layout = layout;
         out = m.release();
     });
     return out;
@@ -329,6 +331,26 @@ int pxr_lm_relevance_rule(void* h, const float* seed, const px_lrp_rule* r, floa
 }
 
 void pxr_lm_destroy(void* h) { delete static_cast<RefLM*>(h); }
+
+// CausalLM::backward (causal_lm.cpp:82-92) of grad_logits (N, L, V) after the last forward; every
+// parameter's gradient goes to grads in the parameter blob's layout.
+int pxr_lm_backward(void* h, const float* grad_logits, float* grads) {
+    return guarded([&] {
+        auto* m = static_cast<RefLM*>(h);
+        const int64_t V = m->c.vocab_size;
+        Tensor g(Shape({m->n, m->l, V}), m->be, std::vector<float>(grad_logits, grad_logits + m->n * m->l * V));
+        (void)m->lm->backward(g);
+        std::map<std::string, Tensor*> by_name;
+        for (NamedParamRef& p : m->lm->named_parameters()) by_name.emplace(p.name, p.ref.grad);
+        float* out = grads;
+        for (const auto& [name, size] : m->layout) {
+            const std::vector<float> v = by_name.at(name)->to_host_vector();
+            if (static_cast<int64_t>(v.size()) != size) throw std::runtime_error("pxr_lm_backward: size of " + name);
+            std::copy(v.begin(), v.end(), out);
+            out += size;
+        }
+    });
+}
 
 int pxr_linear_relevance(const float* x, const float* w, const float* bias, const float* r, int64_t n, int64_t in,
                          int64_t out, float eps, int bias_in_denominator, float* r_in) {
