@@ -177,6 +177,15 @@ int pxa_lm_generate_device(void* lm, float* ids, int64_t n, int64_t prompt, int6
  * cached generation): token_rel (new_tokens, n, prompt + new_tokens - 1) in HBM, zero past each prefix. */
 int pxa_lm_explain_generated_device(void* lm, const float* ids, int64_t n, int64_t prompt, int64_t new_tokens,
                                     int64_t ld_ids, const px_lrp_rule* rule, float* token_rel, int unit_seed);
+/* CausalLM::next_token_logits(max_length) (include/pulsatrix/causal_lm.hpp:116): a cached next-token
+ * function for the reference's Generate (generation.hpp:95-135), over the MI355X decode kernels.
+ * _create returns NULL on error (pxa_last_error). pxa_lm_next_token_logits(f, tokens, n, logits,
+ * vocab) writes the next token's logits after tokens[0 .. n) (host int64 ids) into logits (host,
+ * vocab floats; vocab must be the model's); its signature is the callback a Generate() binding
+ * takes, with f as the context. The function holds the model, which must outlive it. */
+void* pxa_lm_next_token_logits_create(void* lm, int64_t max_length);
+int pxa_lm_next_token_logits(void* f, const int64_t* tokens, int64_t n, float* logits, int64_t vocab);
+void pxa_lm_next_token_logits_destroy(void* f);
 /* After a device-side pass (explain or replay): 0 when every id was in [0, vocab), else -1 with
  * the reference's message ("EmbeddingModule::forward: index out of range [0, num_embeddings)") in
  * pxa_last_error(); an out-of-range id is gathered as id 0 so the pass itself completes. Waits for

@@ -23,6 +23,7 @@
 #include "pulsatrix/causal_lm.hpp"
 #include "pulsatrix/cpu_backend.hpp"
 #include "pulsatrix/explainer_context.hpp"
+#include "pulsatrix/generation.hpp"
 #include "pulsatrix/hf_model.hpp"
 #include "pulsatrix/linear_module.hpp"
 #include "pulsatrix/lrp.hpp"
@@ -351,6 +352,60 @@ int pxr_lm_backward(void* h, const float* grad_logits, float* grads) {
         }
     });
 }
+
+// A next-token function behind a C callback (the product's pxa_lm_next_token_logits, or the
+// reference CausalLM's own below): the logits after tokens[0 .. n) into logits (vocab floats).
+typedef int (*pxr_next_token_cb)(void* ctx, const int64_t* tokens, int64_t n, float* logits, int64_t vocab);
+
+// Generate (generation.hpp:95-135, generation.cpp) over such a callback with a GenerationConfig
+// built from the arguments (seed < 0: unset). new_tokens and log_probs hold up to cap entries.
+int pxr_generate(pxr_next_token_cb cb, void* ctx, int64_t vocab, const int64_t* prompt, int64_t n_prompt,
+                 int64_t max_new_tokens, int64_t min_new_tokens, const int64_t* eos, int64_t n_eos, int do_sample,
+                 float temperature, int64_t top_k, float top_p, float min_p, float repetition_penalty, int64_t seed,
+                 int64_t* new_tokens, float* log_probs, int64_t cap, int64_t* n_new, int* finish_reason) {
+    return guarded([&] {
+        NextTokenLogitsFn model = [cb, ctx, vocab](const std::vector<int64_t>& tokens) {
+            std::vector<float> out(static_cast<size_t>(vocab));
+            if (cb(ctx, tokens.data(), static_cast<int64_t>(tokens.size()), out.data(), vocab) != 0)
+                throw std::runtime_error("pxr_generate: the next-token callback failed");
+            return out;
+        };
+        GenerationConfig gc;
+        gc.max_new_tokens = max_new_tokens;
+        gc.min_new_tokens = min_new_tokens;
+        gc.eos_token_ids.assign(eos, eos + n_eos);
+        gc.do_sample = do_sample != 0;
+        gc.temperature = temperature;
+        gc.top_k = top_k;
+        gc.top_p = top_p;
+        gc.min_p = min_p;
+        gc.repetition_penalty = repetition_penalty;
+        if (seed >= 0) gc.seed = static_cast<uint64_t>(seed);
+        const GenerationResult r = Generate(model, std::vector<int64_t>(prompt, prompt + n_prompt), gc);
+        if (static_cast<int64_t>(r.new_tokens.size()) > cap) throw std::runtime_error("pxr_generate: output too small");
+        std::copy(r.new_tokens.begin(), r.new_tokens.end(), new_tokens);
+        std::copy(r.log_probs.begin(), r.log_probs.end(), log_probs);
+        *n_new = static_cast<int64_t>(r.new_tokens.size());
+        *finish_reason = r.finish_reason == FinishReason::Eos ? 0 : 1;
+    });
+}
+
+// CausalLM::next_token_logits (causal_lm.hpp:116) of the reference model, behind the callback.
+void* pxr_lm_next_token_logits_create(void* h, int64_t max_length) {
+    NextTokenLogitsFn* out = nullptr;
+    guarded([&] { out = new NextTokenLogitsFn(static_cast<RefLM*>(h)->lm->next_token_logits(max_length)); });
+    return out;
+}
+
+int pxr_lm_next_token_logits(void* f, const int64_t* tokens, int64_t n, float* logits, int64_t vocab) {
+    return guarded([&] {
+        const std::vector<float> v = (*static_cast<NextTokenLogitsFn*>(f))(std::vector<int64_t>(tokens, tokens + n));
+        if (static_cast<int64_t>(v.size()) != vocab) throw std::runtime_error("pxr_lm_next_token_logits: vocab");
+        std::copy(v.begin(), v.end(), logits);
+    });
+}
+
+void pxr_lm_next_token_logits_destroy(void* f) { delete static_cast<NextTokenLogitsFn*>(f); }
 
 int pxr_linear_relevance(const float* x, const float* w, const float* bias, const float* r, int64_t n, int64_t in,
                          int64_t out, float eps, int bias_in_denominator, float* r_in) {

@@ -14,6 +14,7 @@
 #include <vector>
 
 #include "pulsatrix/embedding_module.hpp"
+#include "pulsatrix/generation.hpp"
 #include "pulsatrix/hf_model.hpp"
 #include "pulsatrix/linear_module.hpp"
 #include "pulsatrix/rms_norm_module.hpp"
@@ -71,6 +72,17 @@ public:
      *         zero past each prefix. */
     void explain_generated_device(const float* ids, int64_t n, int64_t prompt, int64_t new_tokens, int64_t ld_ids,
                                   const LRPRuleConfig& config, float* token_relevance, bool unit_seed = false);
+    /** @brief A cached next-token function for the reference's Generate (causal_lm.hpp:116, built
+     *         there as MakeCachedNextTokenLogits, generation.cpp:189-258): the first call (and any call
+     *         that is not a short extension of the history) runs one forward over the sequence and
+     *         fills KV caches of max_length positions; each call that extends the history by a few
+     *         tokens runs one decode step per token, replaying a HIP graph of the step (recaptured
+     *         whenever the backend has allocated since). The same sequence again returns the last
+     *         logits; a prefix of the history reruns its last token. Holds this model, which must
+     *         outlive it; one function per sequence being generated.
+     *  @throws std::logic_error for a bidirectional model; (when called) std::invalid_argument for an
+     *          empty sequence, one longer than max_length, or an id outside [0, vocab). */
+    [[nodiscard]] NextTokenLogitsFn next_token_logits(int64_t max_length);
     /** @brief Whether every id of the last device-side pass was in [0, vocab) (waits for the
      *         stream). An out-of-range id is gathered as id 0, so its pass completes; the reference
      *         would have thrown "EmbeddingModule::forward: index out of range [0, num_embeddings)". */
@@ -105,6 +117,11 @@ private:
                                 int64_t target_stride, const LRPRuleConfig& config, float* token_relevance,
                                 int64_t* targets_out, bool unit_seed, bool replicate);
     const float* run_forward_hidden(const float* ids, int64_t n, int64_t l);
+    /** @brief One decode step of n sequences: token ids `cur` (n floats in HBM) at the device
+     *         position *pos, through every layer's cache; returns the (n, vocab) logits. */
+    const float* decode_logits(const float* cur, int64_t n, std::vector<KVCacheState>& caches, const int32_t* pos);
+    struct NextTokenState;
+    std::vector<float> next_token_call(NextTokenState& s, const std::vector<int64_t>& tokens);
 
     int64_t N_ = 0, L_ = 0;
     const float* r_embed_ = nullptr;

@@ -181,6 +181,10 @@ public:
     void replay();
     [[nodiscard]] bool has_graph() const noexcept { return graph_exec_ != nullptr; }
     CachingAllocator& allocator() { return *allocator_; }
+    /** @brief Counts the backend's allocations (allocate() and workspace growth). A graph captured
+     *         at one count still addresses live buffers while the count is unchanged: a buffer that
+     *         moved was reallocated. */
+    [[nodiscard]] uint64_t allocation_epoch() const noexcept { return allocations_; }
 
     /** @brief Runs `f(stream)` (a pxk_* launch returning its status) and, while a launch log is
      *         open, records it with its algorithmic work. */
@@ -208,6 +212,7 @@ private:
     std::unique_ptr<CachingAllocator> allocator_;
     float* ws_ = nullptr;
     size_t ws_bytes_ = 0;
+    uint64_t allocations_ = 0;
     float* reduce_ = nullptr;  // dot/sum partials + result slot
     void* graph_ = nullptr;
     void* graph_exec_ = nullptr;

@@ -599,6 +599,36 @@ int pxa_lm_explain_generated_device(void* handle, const float* ids, int64_t n, i
     });
 }
 
+namespace {
+struct NextTokenHandle {
+    NextTokenLogitsFn fn;
+    int64_t vocab;
+};
+}  // namespace
+
+void* pxa_lm_next_token_logits_create(void* handle, int64_t max_length) {
+    NextTokenHandle* out = nullptr;
+    guarded([&] {
+        auto* h = static_cast<LmHandle*>(handle);
+        out = new NextTokenHandle{h->lm->next_token_logits(max_length), h->lm->config().vocab_size};
+    });
+    return out;
+}
+
+int pxa_lm_next_token_logits(void* f, const int64_t* tokens, int64_t n, float* logits, int64_t vocab) {
+    return guarded([&] {
+        auto* h = static_cast<NextTokenHandle*>(f);
+        if (vocab != h->vocab)
+            throw std::invalid_argument("pxa_lm_next_token_logits: the logits buffer holds " + std::to_string(vocab) +
+                                        " entries, the vocabulary " + std::to_string(h->vocab));
+        if (n < 0) throw std::invalid_argument("pxa_lm_next_token_logits: negative length");
+        const std::vector<float> out = h->fn(std::vector<int64_t>(tokens, tokens + n));
+        std::copy(out.begin(), out.end(), logits);
+    });
+}
+
+void pxa_lm_next_token_logits_destroy(void* f) { delete static_cast<NextTokenHandle*>(f); }
+
 int pxa_lm_replay(void*) {
     return guarded([&] { backend()->replay(); });
 }

@@ -259,7 +259,7 @@ void CausalLM::generate_greedy_device(float* ids, int64_t n, int64_t prompt, int
         throw std::invalid_argument("CausalLM::generate: n, the prompt length and new_tokens must be positive");
     if (ld_ids < prompt + new_tokens)
         throw std::invalid_argument("CausalLM::generate: the id rows must hold the prompt and every new token");
-    const int64_t V = config_.vocab_size, d = config_.hidden_size;
+    const int64_t V = config_.vocab_size;
     const int64_t positions = prompt + new_tokens - 1;  // the last generated token is never fed back
     void* st = be_->stream();
     // 1. the prompts: one forward fills every layer's cache; its last rows pick the first token.
@@ -283,20 +283,7 @@ void CausalLM::generate_greedy_device(float* ids, int64_t n, int64_t prompt, int
     };
     pick(logits);
     // 2. decode steps: the step's own token in, the next one out, at the device position.
-    auto step = [&] {
-        float* x = dec_x_.ensure(be_, n * d);
-        MI355XBackend::check(pxk_gather_rows(embed_.weight_data(), cur, x, n, d, st), "CausalLM::generate");
-        if (config_.embed_scale != 1.0f)
-            MI355XBackend::check(pxk_axpby(config_.embed_scale, x, 0.0f, nullptr, x, n * d, st), "CausalLM::generate");
-        const float* h = x;
-        const float* hn = nullptr;  // norm1(h) of the next layer (or the final norm) when a block wrote it
-        for (size_t i = 0; i < layers_.size(); ++i) {
-            RMSNormModule* next = i + 1 < layers_.size() ? &layers_[i + 1]->norm1() : &norm_;
-            h = layers_[i]->decode_step(h, hn, n, caches_[i], pos, next, &hn);
-        }
-        if (!hn) hn = norm_.run_forward(h, n);
-        pick(tied_head_ ? tied_head_->run_forward(hn, n) : lm_head_->run_forward(hn, n));
-    };
+    auto step = [&] { pick(decode_logits(cur, n, caches_, pos)); };
     if (new_tokens < 2) return;
     step();  // eagerly once: every buffer and workspace the step uses exists before the capture
     if (new_tokens < 3) return;
@@ -328,6 +315,130 @@ void CausalLM::generate_greedy_device(float* ids, int64_t n, int64_t prompt, int
     (void)hipGraphDestroy(graph);
     hip(rc, "replay");
     hip(done, "synchronize");
+}
+
+const float* CausalLM::decode_logits(const float* cur, int64_t n, std::vector<KVCacheState>& caches,
+                                     const int32_t* pos) {
+    const int64_t d = config_.hidden_size;
+    void* st = be_->stream();
+    float* x = dec_x_.ensure(be_, n * d);
+    MI355XBackend::check(pxk_gather_rows(embed_.weight_data(), cur, x, n, d, st), "CausalLM::decode");
+    if (config_.embed_scale != 1.0f)
+        MI355XBackend::check(pxk_axpby(config_.embed_scale, x, 0.0f, nullptr, x, n * d, st), "CausalLM::decode");
+    const float* h = x;
+    const float* hn = nullptr;  // norm1(h) of the next layer (or the final norm) when a block wrote it
+    for (size_t i = 0; i < layers_.size(); ++i) {
+        RMSNormModule* next = i + 1 < layers_.size() ? &layers_[i + 1]->norm1() : &norm_;
+        h = layers_[i]->decode_step(h, hn, n, caches[i], pos, next, &hn);
+    }
+    if (!hn) hn = norm_.run_forward(h, n);
+    return tied_head_ ? tied_head_->run_forward(hn, n) : lm_head_->run_forward(hn, n);
+}
+
+// The state a next_token_logits() function owns: its KV caches, the history and its logits, the
+// step's device inputs (token id and position) and the captured graph of the step.
+struct CausalLM::NextTokenState {
+    explicit NextTokenState(int64_t max) : max_length(max) {}
+    ~NextTokenState() { release_graph(); }
+    NextTokenState(const NextTokenState&) = delete;
+    NextTokenState& operator=(const NextTokenState&) = delete;
+    void release_graph() {
+        if (exec) (void)hipGraphExecDestroy(exec);
+        if (graph) (void)hipGraphDestroy(graph);
+        exec = nullptr;
+        graph = nullptr;
+    }
+    int64_t max_length;
+    std::vector<KVCacheState> caches;
+    std::vector<int64_t> processed;
+    std::vector<float> last_logits;
+    detail::DevBuf cur, pos;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    uint64_t epoch = 0;                   // the backend's allocation count the graph was captured at
+    const float* graph_logits = nullptr;  // where the captured step writes its logits
+};
+
+NextTokenLogitsFn CausalLM::next_token_logits(int64_t max_length) {
+    if (!config_.causal)
+        throw std::logic_error("CausalLM::next_token_logits: the model attends bidirectionally (a diffusion LM), so it "
+                               "has no next-token cache");
+    if (max_length <= 0) throw std::invalid_argument("CausalLM::next_token_logits: max_length must be positive");
+    auto state = std::make_shared<NextTokenState>(max_length);
+    return [this, state](const std::vector<int64_t>& tokens) { return next_token_call(*state, tokens); };
+}
+
+std::vector<float> CausalLM::next_token_call(NextTokenState& s, const std::vector<int64_t>& tokens) {
+    // Validation and history handling as MakeCachedNextTokenLogits (generation.cpp:214-236).
+    if (tokens.empty()) throw std::invalid_argument("MakeCachedNextTokenLogits: the sequence is empty");
+    const auto L = static_cast<int64_t>(tokens.size());
+    if (L > s.max_length)
+        throw std::invalid_argument("MakeCachedNextTokenLogits: " + std::to_string(L) + " tokens don't fit in caches of " +
+                                    std::to_string(s.max_length));
+    const int64_t V = config_.vocab_size;
+    for (const int64_t t : tokens)
+        if (t < 0 || t >= V) throw std::invalid_argument("EmbeddingModule::forward: index out of range [0, num_embeddings)");
+    size_t shared = 0;
+    while (shared < tokens.size() && shared < s.processed.size() && tokens[shared] == s.processed[shared]) ++shared;
+    if (shared == tokens.size() && shared == s.processed.size()) return s.last_logits;  // the same sequence again
+    if (shared == tokens.size()) --shared;  // a prefix of the history: rerun its last token for its logits
+    // A short extension runs one decode step per new token over the caches (positions before
+    // `shared` hold this sequence's keys and values already); anything else is one forward over
+    // the whole sequence, whose keys and values then fill the caches.
+    constexpr size_t kMaxSteps = 8;
+    const float* logits = nullptr;
+    void* st = be_->stream();
+    if (shared == 0 || tokens.size() - shared > kMaxSteps) {
+        std::vector<float> ids(tokens.begin(), tokens.end());
+        float* pid = prompt_ids_.ensure(be_, L);
+        be_->copy(pid, ids.data(), ids.size() * sizeof(float), CopyDirection::HostToDevice);
+        logits = forward_last_rows(pid, 1, L);
+        s.caches.resize(layers_.size());
+        for (size_t i = 0; i < layers_.size(); ++i) layers_[i]->mha().export_kv(s.caches[i], s.max_length);
+    } else {
+        float* cur = s.cur.ensure(be_, 1);
+        auto* pos = reinterpret_cast<int32_t*>(s.pos.ensure(be_, 1));
+        for (size_t t = shared; t < tokens.size(); ++t) {
+            const float id = static_cast<float>(tokens[t]);
+            const int32_t p = static_cast<int32_t>(t);
+            be_->copy(cur, &id, sizeof(id), CopyDirection::HostToDevice);
+            be_->copy(pos, &p, sizeof(p), CopyDirection::HostToDevice);
+            if (s.exec && s.epoch == be_->allocation_epoch()) {
+                const hipError_t rc = hipGraphLaunch(s.exec, static_cast<hipStream_t>(st));
+                if (rc != hipSuccess)
+                    throw std::runtime_error(std::string("CausalLM::next_token_logits: replay: ") + hipGetErrorString(rc));
+                logits = s.graph_logits;
+                continue;
+            }
+            // Eager (its buffers now exist), then capture the same step for the calls that follow.
+            s.release_graph();
+            logits = decode_logits(cur, 1, s.caches, pos);
+            hipGraph_t g = nullptr;
+            if (hipStreamBeginCapture(static_cast<hipStream_t>(st), hipStreamCaptureModeThreadLocal) != hipSuccess)
+                throw std::runtime_error("CausalLM::next_token_logits: begin capture");
+            const float* captured = nullptr;
+            try {
+                captured = decode_logits(cur, 1, s.caches, pos);
+            } catch (...) {
+                (void)hipStreamEndCapture(static_cast<hipStream_t>(st), &g);
+                if (g) (void)hipGraphDestroy(g);
+                throw;
+            }
+            if (hipStreamEndCapture(static_cast<hipStream_t>(st), &g) != hipSuccess)
+                throw std::runtime_error("CausalLM::next_token_logits: end capture");
+            s.graph = g;
+            if (hipGraphInstantiate(&s.exec, g, nullptr, nullptr, 0) != hipSuccess) {
+                s.release_graph();
+                throw std::runtime_error("CausalLM::next_token_logits: instantiate");
+            }
+            s.graph_logits = captured;
+            s.epoch = be_->allocation_epoch();
+        }
+    }
+    s.last_logits.resize(static_cast<size_t>(V));
+    be_->copy(s.last_logits.data(), logits, static_cast<size_t>(V) * sizeof(float), CopyDirection::DeviceToHost);
+    s.processed = tokens;
+    return s.last_logits;
 }
 
 void CausalLM::explain_generated_device(const float* ids, int64_t n, int64_t prompt, int64_t new_tokens, int64_t ld_ids,

@@ -85,6 +85,7 @@ void MI355XBackend::synchronize() { hip_check(hipStreamSynchronize(S(stream_)), 
 
 void* MI355XBackend::allocate(size_t bytes) {
     if (bytes == 0) return nullptr;
+    ++allocations_;
     try {
         return allocator_->allocate(bytes);
     } catch (const std::bad_alloc&) {
@@ -132,6 +133,7 @@ float* MI355XBackend::workspace(size_t bytes) {
             allocator_->free(ws_);
         ws_bytes_ = std::max(bytes, ws_bytes_ * 2);
         ws_ = static_cast<float*>(allocator_->allocate(ws_bytes_));
+        ++allocations_;
     }
     return ws_;
 }

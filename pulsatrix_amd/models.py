@@ -173,6 +173,10 @@ class CausalLM:
                                                               ctypes.byref(N.as_rule(rule)), token_rel_ptr,
                                                               int(unit_seed)))
 
+    def next_token_logits(self, max_length):
+        """CausalLM::next_token_logits: a cached next-token function over the decode kernels."""
+        return NextTokenLogits(self, max_length)
+
     def replay(self):
         N.host_check(N.host().pxa_lm_replay(self.h))
 
@@ -187,6 +191,36 @@ class CausalLM:
     def __del__(self):
         if getattr(self, "h", None):
             N.host().pxa_lm_destroy(self.h)
+            self.h = None
+
+
+class NextTokenLogits:
+    """The function CausalLM::next_token_logits(max_length) returns: call it with the token ids so
+    far to get the next token's logits (numpy, vocab floats). `callback` is the C function and
+    context a Generate() binding takes."""
+
+    def __init__(self, lm, max_length):
+        self.lm = lm  # the function holds the model
+        self.vocab = int(lm.cfg.vocab_size)
+        self.h = N.host().pxa_lm_next_token_logits_create(lm.h, max_length)
+        if not self.h:
+            raise N.PxkError(N.host().pxa_last_error().decode())
+
+    def __call__(self, tokens):
+        t = np.ascontiguousarray(tokens, dtype=np.int64)
+        out = np.empty(self.vocab, np.float32)
+        N.host_check(N.host().pxa_lm_next_token_logits(self.h, t.ctypes.data_as(ctypes.POINTER(ctypes.c_int64)),
+                                                       t.size, _p(out), self.vocab))
+        return out
+
+    @property
+    def callback(self):
+        """(function pointer, context) of pxa_lm_next_token_logits for this function."""
+        return ctypes.cast(N.host().pxa_lm_next_token_logits, ctypes.c_void_p).value, self.h
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            N.host().pxa_lm_next_token_logits_destroy(self.h)
             self.h = None
 
 

@@ -322,6 +322,9 @@ def host():
             "pxa_lm_generate_device": (ctypes.c_int, [c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_vp]),
             "pxa_lm_explain_generated_device": (ctypes.c_int, [c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, rulep, c_vp,
                                                                ctypes.c_int]),
+            "pxa_lm_next_token_logits_create": (c_vp, [c_vp, c_i64]),
+            "pxa_lm_next_token_logits": (ctypes.c_int, [c_vp, i64p, c_i64, c_vp, c_i64]),
+            "pxa_lm_next_token_logits_destroy": (None, [c_vp]),
             "pxa_lm_check_device_ids": (ctypes.c_int, [c_vp]),
             "pxa_lm_last_logits": (c_vp, [c_vp]),
             "pxa_lm_last_embedding_relevance": (c_vp, [c_vp]),

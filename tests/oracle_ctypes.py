@@ -292,7 +292,72 @@ def ref():
     if _ref is None and os.path.exists(REF_SO):
         _ref = _Lib(REF_SO, "pxr_")
         _bind_backend_shim(_ref.lib)
+        _bind_generate(_ref.lib)
     return _ref
+
+
+def _bind_generate(L):
+    """pxr_generate (the reference's Generate over a C next-token callback) and the reference
+    CausalLM's own next_token_logits behind that callback (oracle/ref_driver.cpp)."""
+    vp, i64 = ctypes.c_void_p, ctypes.c_int64
+    L.pxr_generate.restype = ctypes.c_int
+    L.pxr_generate.argtypes = [vp, vp, i64, _i64p, i64, i64, i64, _i64p, i64, ctypes.c_int, ctypes.c_float, i64,
+                               ctypes.c_float, ctypes.c_float, ctypes.c_float, i64, _i64p, _f32p, i64, _i64p,
+                               ctypes.POINTER(ctypes.c_int)]
+    L.pxr_lm_next_token_logits_create.restype = vp
+    L.pxr_lm_next_token_logits_create.argtypes = [vp, i64]
+    L.pxr_lm_next_token_logits.restype = ctypes.c_int
+    L.pxr_lm_next_token_logits.argtypes = [vp, _i64p, i64, _f32p, i64]
+    L.pxr_lm_next_token_logits_destroy.restype = None
+    L.pxr_lm_next_token_logits_destroy.argtypes = [vp]
+
+
+def ref_generate(model, vocab, prompt, max_new_tokens, min_new_tokens=0, eos=(), do_sample=False, temperature=1.0,
+                 top_k=0, top_p=1.0, min_p=0.0, repetition_penalty=1.0, seed=-1):
+    """The reference's Generate (generation.hpp:95-135) over `model`, a next-token function object
+    whose `callback` is its (C function pointer, context); the object stays referenced for the call.
+    Returns (new tokens, their log-probabilities, finish reason 'eos' or 'length')."""
+    lib = ref()
+    fn, ctx = model.callback
+    p = np.ascontiguousarray(prompt, dtype=np.int64)
+    e = np.ascontiguousarray(list(eos) or [0], dtype=np.int64)
+    cap = max(1, int(max_new_tokens))
+    toks = np.zeros(cap, np.int64)
+    logp = np.zeros(cap, np.float32)
+    n_new, fin = ctypes.c_int64(), ctypes.c_int()
+    lib.check(lib.lib.pxr_generate(fn, ctx, vocab, p.ctypes.data_as(_i64p), p.size, max_new_tokens, min_new_tokens,
+                                   e.ctypes.data_as(_i64p), len(eos), int(do_sample), temperature, top_k, top_p, min_p,
+                                   repetition_penalty, seed, toks.ctypes.data_as(_i64p), fptr(logp), cap,
+                                   ctypes.byref(n_new), ctypes.byref(fin)))
+    k = n_new.value
+    return toks[:k], logp[:k], ("eos" if fin.value == 0 else "length")
+
+
+class RefNextToken:
+    """The compiled reference CausalLM's next_token_logits(max_length) (causal_lm.hpp:116)."""
+
+    def __init__(self, lm, max_length):
+        self.lm = lm
+        L = lm.lib.lib
+        self.h = L.pxr_lm_next_token_logits_create(lm.h, max_length)
+        if not self.h:
+            raise RuntimeError(lm.lib.fn("last_error")().decode())
+
+    def __call__(self, tokens):
+        t = np.ascontiguousarray(tokens, dtype=np.int64)
+        out = np.empty(self.lm.cfg.vocab_size, np.float32)
+        self.lm.lib.check(self.lm.lib.lib.pxr_lm_next_token_logits(self.h, t.ctypes.data_as(_i64p), t.size, fptr(out),
+                                                                   out.size))
+        return out
+
+    @property
+    def callback(self):
+        return ctypes.cast(self.lm.lib.lib.pxr_lm_next_token_logits, ctypes.c_void_p).value, self.h
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            self.lm.lib.lib.pxr_lm_next_token_logits_destroy(self.h)
+            self.h = None
 
 
 _ref_mi355x = None
