@@ -37,18 +37,21 @@ FP32_MFMA_PEAK_TFLOPS = 157.3
 HBM_PEAK_GBS = 8000.0
 LXT_EPS = 1e-9
 
-# HBM bytes of one launch of the LM-head relevance GEMM (main kernel + split-K reduce), from two
-# rocprofv3 --pmc runs of `bench.py --kernel-probe` (FETCH_SIZE, then WRITE_SIZE; see
-# profiles/head_relevance_gemm_traffic.md), each scaled by what the counter reads for the probe's
-# 256 MiB copy (FETCH_SIZE x 2.0, WRITE_SIZE x 1.0); median dispatch of five. Valid for the plan
-# it was measured on.
-HEAD_REL_TRAFFIC = {"plan": (2, 32), "bytes": (341338 * 2.0 + 36864 + 19056 * 2.0 + 1152) * 1024}
-# HBM bytes per launch of step kernels, by launch-log name, from rocprofv3 --pmc runs of this bench
-# (FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0, the copy calibration above; profiles/*_traffic.md). The
-# roofline line carries the figure of its kernel when that kernel was measured.
-STEP_KERNEL_TRAFFIC = {}
-if HEAD_REL_TRAFFIC["plan"] == (2, 32):
-    STEP_KERNEL_TRAFFIC["gemm 64x64 NN pro1 epi3 split32"] = HEAD_REL_TRAFFIC
+# HBM bytes per launch of the step's kernels, by launch-log name: FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0
+# KiB (the factors a 256 MiB copy reads for the two counters) of the median dispatch, from rocprofv3
+# --pmc runs of this bench (profiles/explain_s512_step_counters.md). A launch's kernels add up (the
+# split-K GEMM and its reduce); the o and down projections share one name and are averaged. The
+# roofline line carries the figure of its kernel when that kernel was measured under this plan.
+STEP_KERNEL_TRAFFIC = {name: kib * 1024 for name, kib in {
+    "gemm 32x32 NT pro0 epi8 split8": 39929,  # gate|up relevance 22502 + its split-K reduce 17427
+    "gemm 32x64d NN pro0 epi2 split1": 24798,  # o projection 15198, down projection 34398
+    "gemm 32x64 NN pro0 epi10 split1": 28726,  # gate|up projection (SwiGLU epilogue)
+    "gemm 32x32 NT pro1 epi7 split1": 34595,  # down relevance
+    "gemm 32x64d NT pro0 epi8 split1": 27521,  # q|k|v relevance (residual split)
+    "gemm 32x64d NT pro1 epi4 split1": 23263,  # o relevance
+    "gemm 32x64d NN pro0 epi9 split1": 17076,  # q|k|v projection (RoPE epilogue)
+    "attn_fwd": 22100, "attn_rel_q": 30580, "attn_rel_kv": 19310, "rms_norm": 2375,
+}.items()}
 # The same for the decode step's tied head (4 x 640 x 262144, skinny NT; `bench.py --decode-probe`,
 # profiles/decode_head_gemm_traffic.md): FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0 of the median dispatch.
 DECODE_HEAD_TRAFFIC = {"plan": (7, 1), "bytes": (327831.8 * 2.0 + 4096) * 1024}
@@ -184,6 +187,10 @@ def kernel_row(k):
     elif k["bytes"] > 0:
         gbs = k["bytes"] / k["seconds"] / 1e9
         row.update(gbs=round(gbs, 1), frac=round(gbs / HBM_PEAK_GBS, 4))
+    if k["bytes"] > 0:
+        row["algorithmic_mb"] = round(k["bytes"] / k["calls"] / 1e6, 2)
+    if k["kernel"] in STEP_KERNEL_TRAFFIC:
+        row["hbm_mb"] = round(STEP_KERNEL_TRAFFIC[k["kernel"]] / 1e6, 2)
     return row
 
 

@@ -152,8 +152,18 @@ void MI355XBackend::run_gemm(pxk_gemm_desc& d) {
         char name[96];
         std::snprintf(name, sizeof(name), "gemm %s %s%s pro%d epi%d split%d", kTile[tile >= 0 && tile <= 7 ? tile : 0],
                       d.trans_a ? "T" : "N", d.trans_b ? "T" : "N", d.prologue, d.epilogue, splits);
+        // Algorithmic bytes: every operand once (A, B, the prologue's denominators, the
+        // epilogue's inputs and outputs), none of the split-K partials or re-reads.
+        const double bt = static_cast<double>(d.batch), g = static_cast<double>(d.kgroups);
+        const double mn = static_cast<double>(d.m) * d.n * bt, mk = static_cast<double>(d.m) * d.k * g * bt;
+        const double kn = static_cast<double>(d.k) * d.n * g * (d.b.batch_stride || d.b.inner_stride ? bt : 1.0);
+        double floats = mk + kn + (d.z.ptr && d.prologue != PXK_PRO_NONE ? mk : 0.0);
+        for (const pxk_operand* o : {&d.c, &d.c2, &d.c3, &d.x, &d.y, &d.w, &d.z2, &d.z3})
+            if (o->ptr) floats += mn;
+        if (d.z.ptr && d.prologue == PXK_PRO_NONE) floats += mn;  // the RoPE / value rules read Z like C
+        if (d.epilogue == PXK_EPI_STORE && d.beta != 0.0f) floats += mn;  // C read back
         const pxk_gemm_desc copy = d;
-        log_.push_back(LaunchRecord{name, "gemm", 2.0 * d.m * d.n * d.k * d.batch * d.kgroups, 0.0,
+        log_.push_back(LaunchRecord{name, "gemm", 2.0 * d.m * d.n * d.k * d.batch * d.kgroups, 4.0 * floats,
                                     [copy](void* st) { return pxk_gemm(&copy, st); }});
     }
     if (sync_debug_) synchronize();
