@@ -596,6 +596,111 @@ int pxk_tanh_gaussian_backward(const float* action, const float* std_cache, cons
 int pxk_top_k_rows(const float* in, float* values, float* indices, int64_t rows, int64_t cols, int64_t k, int largest,
                    void* stream);
 
+/* ---- the non-LLM modules' ops (module_ops.hip): simple, correct kernels, one thread per output,
+ * lane or row, adding in the reference's loop order; no atomics. Op codes are the reference enums'
+ * declaration order. -------------------------------------------------------------------------- */
+
+/* logic_pointwise (device_backend.hpp:663, lrp_math.hpp:125-270): op 0-2 Conjunction forward /
+ * backward / LRP, 3-5 Disjunction; norm 0 product, 1 Lukasiewicz, 2 Godel. g_or_r is read by the
+ * backward and LRP passes, y by LRP only; out_b is written by the backward and LRP passes. */
+int pxk_logic_pointwise(int op, int norm, const float* a, const float* b, const float* g_or_r, const float* y,
+                        float* out_a, float* out_b, int64_t n, float eps, void* stream);
+/* aggregator_forward / _backward / _lrp (device_backend.hpp:667-676, lrp_math.hpp:272-306): the power
+ * mean over the leading axis of (n, cols), one thread per column. */
+int pxk_aggregator_forward(const float* x, float* mean_pow, float* out, int64_t n, int64_t cols, float p,
+                           void* stream);
+int pxk_aggregator_backward(const float* x, const float* mean_pow, const float* grad_out, float* grad_in, int64_t n,
+                            int64_t cols, float p, void* stream);
+int pxk_aggregator_lrp(const float* x, const float* mean_pow, const float* r_out, float* r_in, int64_t n, int64_t cols,
+                       float p, float eps, void* stream);
+
+/* ConvGeometry (device_backend.hpp:173-180). */
+typedef struct pxk_conv_geometry {
+    int64_t kh, kw, stride_h, stride_w, pad_h, pad_w;
+} pxk_conv_geometry;
+/* im2col (device_backend.hpp:683): (n, c, h, w) -> (n, c kh kw, out_h out_w) patches, padding reads 0. */
+int pxk_im2col(const float* in, float* col, int64_t n, int64_t c, int64_t h, int64_t w, const pxk_conv_geometry* g,
+               void* stream);
+/* col2im_add (device_backend.hpp:691): patches added back into out (n, c, h, w), one thread per pixel
+ * gathering its taps in the CPU scatter's order. */
+int pxk_col2im_add(const float* col, float* out, int64_t n, int64_t c, int64_t h, int64_t w,
+                   const pxk_conv_geometry* g, void* stream);
+/* add_channel_vector (device_backend.hpp:695): out[i][ch][k] = in[i][ch][k] + vec[ch]; out may alias in. */
+int pxk_add_channel_vector(const float* in, const float* vec, float* out, int64_t n, int64_t c, int64_t inner,
+                           void* stream);
+/* lrp_conv (device_backend.hpp:702, cnn_math.hpp:84-93): the Conv2D epsilon rule in patch space. */
+int pxk_lrp_conv(const float* col, const float* kernel, const float* pre_bias, const float* r, float* r_col, int64_t n,
+                 int64_t out_channels, int64_t p, int64_t q, float eps, void* stream);
+/* max_pool_forward / max_unpool (device_backend.hpp:720-729, cnn_math.hpp:106-160). */
+int pxk_max_pool_forward(const float* in, float* out, float* argmax, int64_t planes, int64_t h, int64_t w, int64_t kh,
+                         int64_t kw, int64_t sh, int64_t sw, int64_t ph, int64_t pw, void* stream);
+int pxk_max_unpool(const float* src, const float* argmax, float* dst, int64_t planes, int64_t h, int64_t w, int64_t kh,
+                   int64_t kw, int64_t sh, int64_t sw, int64_t ph, int64_t pw, void* stream);
+/* avg_pool_forward / avg_pool_backward / lrp_avg_pool (device_backend.hpp:731-741, cnn_math.hpp:162-184):
+ * non-overlapping windows; grad_in and r_in cover the windows only (the caller zeroes the rest). */
+int pxk_avg_pool_forward(const float* in, float* out, int64_t planes, int64_t h, int64_t w, int64_t kh, int64_t kw,
+                         void* stream);
+int pxk_avg_pool_backward(const float* grad_out, float* grad_in, int64_t planes, int64_t h, int64_t w, int64_t kh,
+                          int64_t kw, void* stream);
+int pxk_lrp_avg_pool(const float* x, const float* r, float* r_in, int64_t planes, int64_t h, int64_t w, int64_t kh,
+                     int64_t kw, float eps, void* stream);
+/* batch_norm_forward / _backward / _update_running / _eval_forward / _eval_backward
+ * (device_backend.hpp:743-766, cnn_math.hpp:186-330): one thread per channel of (n, c, spatial). */
+int pxk_batch_norm_forward(const float* in, const float* gamma, const float* beta, float* xhat, float* out,
+                           float* channel_std, int64_t n, int64_t c, int64_t spatial, float eps, void* stream);
+int pxk_batch_norm_backward(const float* grad_out, const float* gamma, const float* xhat, const float* channel_std,
+                            float* grad_in, float* gamma_grad, float* beta_grad, int64_t n, int64_t c, int64_t spatial,
+                            void* stream);
+int pxk_batch_norm_update_running(const float* in, float* running_mean, float* running_var, int64_t n, int64_t c,
+                                  int64_t spatial, float momentum, void* stream);
+int pxk_batch_norm_eval_forward(const float* in, const float* gamma, const float* beta, const float* running_mean,
+                                const float* running_var, float* xhat, float* out, float* channel_std, int64_t n,
+                                int64_t c, int64_t spatial, float eps, void* stream);
+int pxk_batch_norm_eval_backward(const float* grad_out, const float* gamma, const float* xhat,
+                                 const float* channel_std, float* grad_in, float* gamma_grad, float* beta_grad,
+                                 int64_t n, int64_t c, int64_t spatial, void* stream);
+/* group_norm_forward / _backward (device_backend.hpp:768-776, cnn_math.hpp:332-413): one thread per
+ * (example, group); the parameter gradients one thread per channel. */
+int pxk_group_norm_forward(const float* in, const float* gamma, const float* beta, float* xhat, float* out,
+                           float* group_std, int64_t n, int64_t c, int64_t spatial, int64_t groups, float eps,
+                           void* stream);
+int pxk_group_norm_backward(const float* grad_out, const float* gamma, const float* xhat, const float* group_std,
+                            float* grad_in, float* gamma_grad, float* beta_grad, int64_t n, int64_t c, int64_t spatial,
+                            int64_t groups, void* stream);
+
+/* RecurrentCellArgs (device_backend.hpp:91-95); recurrent_cell (:795, recurrent_math.hpp:18-106), op 0
+ * RnnBackward, 1 LstmForward, 2 LstmBackward, 3 LstmLrp, 4 GruBackward, 5 GruLrp, slots as
+ * device_backend.hpp:75-87 documents; n elements. */
+typedef struct pxk_recurrent_args {
+    const float* in[10];
+    float* out[6];
+    float eps;
+} pxk_recurrent_args;
+int pxk_recurrent_cell(int op, const pxk_recurrent_args* args, int64_t n, void* stream);
+/* gru_lrp_hprev (device_backend.hpp:801, recurrent_math.hpp:108-124). */
+int pxk_gru_lrp_hprev(const float* h_prev, const float* w_hn, const float* hn, const float* r_term_b,
+                      const float* direct, float* r_hprev, int64_t rows, int64_t hidden, float eps, void* stream);
+/* SsmPassArgs (device_backend.hpp:158-167); ssm_pass (:813, ssm_math.hpp), op = SsmPassOp's order
+ * (0 MambaForward .. 18 ReverseTimeSum), slots and lanes as device_backend.hpp:97-134 documents.
+ * Carry and state buffers the reference's callers zero are zeroed by them here too. */
+typedef struct pxk_ssm_args {
+    const float* in[12];
+    float* out[10];
+    int64_t n, l, d, s;
+    float eps, gamma;
+} pxk_ssm_args;
+int pxk_ssm_pass(int op, const pxk_ssm_args* args, void* stream);
+/* RlRowArgs (device_backend.hpp:208-219); rl_rows (:824, rl_math.hpp), op = RlRowOp's order (0 DqnLoss
+ * .. 8 TokenCeLoss); one thread per row (per element for PolyakBlend). */
+typedef struct pxk_rl_args {
+    const float* in[5];
+    float* out[4];
+    int64_t rows, cols;
+    float scale, lower, upper, gamma, tau;
+    int64_t ignore_index;
+} pxk_rl_args;
+int pxk_rl_rows(int op, const pxk_rl_args* args, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -593,6 +593,124 @@ PXR_BE(tanh_gaussian_backward,
 PXR_BE(top_k_rows, (const float* in, float* values, float* indices, size_t rows, size_t cols, size_t k, int largest),
        top_k_rows(in, values, indices, rows, cols, k, largest != 0))
 
+// The non-LLM modules' virtuals. ConvGeometry goes as six sizes; the slot structs of recurrent_cell,
+// ssm_pass and rl_rows as arrays of pointers (10 / 6, 12 / 10 and 5 / 4 entries) and their scalars.
+PXR_BE(logic_pointwise,
+       (int op, int norm, const float* a, const float* b, const float* g, const float* y, float* oa, float* ob, size_t n,
+        float eps),
+       logic_pointwise(static_cast<LogicOp>(op), norm, a, b, g, y, oa, ob, n, eps))
+PXR_BE(aggregator_forward, (const float* x, float* mp, float* out, size_t n, size_t cols, float p),
+       aggregator_forward(x, mp, out, n, cols, p))
+PXR_BE(aggregator_backward, (const float* x, const float* mp, const float* go, float* gi, size_t n, size_t cols, float p),
+       aggregator_backward(x, mp, go, gi, n, cols, p))
+PXR_BE(aggregator_lrp,
+       (const float* x, const float* mp, const float* ro, float* ri, size_t n, size_t cols, float p, float eps),
+       aggregator_lrp(x, mp, ro, ri, n, cols, p, eps))
+PXR_BE(im2col,
+       (const float* in, float* col, size_t n, size_t c, size_t h, size_t w, size_t kh, size_t kw, size_t sh, size_t sw,
+        size_t ph, size_t pw),
+       im2col(in, col, n, c, h, w, ConvGeometry{kh, kw, sh, sw, ph, pw}))
+PXR_BE(col2im_add,
+       (const float* col, float* out, size_t n, size_t c, size_t h, size_t w, size_t kh, size_t kw, size_t sh, size_t sw,
+        size_t ph, size_t pw),
+       col2im_add(col, out, n, c, h, w, ConvGeometry{kh, kw, sh, sw, ph, pw}))
+PXR_BE(add_channel_vector, (const float* in, const float* vec, float* out, size_t n, size_t c, size_t inner),
+       add_channel_vector(in, vec, out, n, c, inner))
+PXR_BE(lrp_conv,
+       (const float* col, const float* kernel, const float* z, const float* r, float* rc, size_t n, size_t oc, size_t p,
+        size_t q, float eps),
+       lrp_conv(col, kernel, z, r, rc, n, oc, p, q, eps))
+PXR_BE(max_pool_forward,
+       (const float* in, float* out, float* am, size_t planes, size_t h, size_t w, size_t kh, size_t kw, size_t sh,
+        size_t sw, size_t ph, size_t pw),
+       max_pool_forward(in, out, am, planes, h, w, kh, kw, sh, sw, ph, pw))
+PXR_BE(max_unpool,
+       (const float* src, const float* am, float* dst, size_t planes, size_t h, size_t w, size_t kh, size_t kw, size_t sh,
+        size_t sw, size_t ph, size_t pw),
+       max_unpool(src, am, dst, planes, h, w, kh, kw, sh, sw, ph, pw))
+PXR_BE(avg_pool_forward, (const float* in, float* out, size_t planes, size_t h, size_t w, size_t kh, size_t kw),
+       avg_pool_forward(in, out, planes, h, w, kh, kw))
+PXR_BE(avg_pool_backward, (const float* go, float* gi, size_t planes, size_t h, size_t w, size_t kh, size_t kw),
+       avg_pool_backward(go, gi, planes, h, w, kh, kw))
+PXR_BE(lrp_avg_pool,
+       (const float* x, const float* r, float* ri, size_t planes, size_t h, size_t w, size_t kh, size_t kw, float eps),
+       lrp_avg_pool(x, r, ri, planes, h, w, kh, kw, eps))
+PXR_BE(batch_norm_forward,
+       (const float* in, const float* gm, const float* bt, float* xh, float* out, float* sd, size_t n, size_t c,
+        size_t sp, float eps),
+       batch_norm_forward(in, gm, bt, xh, out, sd, n, c, sp, eps))
+PXR_BE(batch_norm_backward,
+       (const float* go, const float* gm, const float* xh, const float* sd, float* gi, float* gg, float* bg, size_t n,
+        size_t c, size_t sp),
+       batch_norm_backward(go, gm, xh, sd, gi, gg, bg, n, c, sp))
+PXR_BE(batch_norm_update_running,
+       (const float* in, float* rm, float* rv, size_t n, size_t c, size_t sp, float momentum),
+       batch_norm_update_running(in, rm, rv, n, c, sp, momentum))
+PXR_BE(batch_norm_eval_forward,
+       (const float* in, const float* gm, const float* bt, const float* rm, const float* rv, float* xh, float* out,
+        float* sd, size_t n, size_t c, size_t sp, float eps),
+       batch_norm_eval_forward(in, gm, bt, rm, rv, xh, out, sd, n, c, sp, eps))
+PXR_BE(batch_norm_eval_backward,
+       (const float* go, const float* gm, const float* xh, const float* sd, float* gi, float* gg, float* bg, size_t n,
+        size_t c, size_t sp),
+       batch_norm_eval_backward(go, gm, xh, sd, gi, gg, bg, n, c, sp))
+PXR_BE(group_norm_forward,
+       (const float* in, const float* gm, const float* bt, float* xh, float* out, float* sd, size_t n, size_t c,
+        size_t sp, size_t groups, float eps),
+       group_norm_forward(in, gm, bt, xh, out, sd, n, c, sp, groups, eps))
+PXR_BE(group_norm_backward,
+       (const float* go, const float* gm, const float* xh, const float* sd, float* gi, float* gg, float* bg, size_t n,
+        size_t c, size_t sp, size_t groups),
+       group_norm_backward(go, gm, xh, sd, gi, gg, bg, n, c, sp, groups))
+PXR_BE(gru_lrp_hprev,
+       (const float* hp, const float* w, const float* hn, const float* rb, const float* direct, float* out, size_t rows,
+        size_t hidden, float eps),
+       gru_lrp_hprev(hp, w, hn, rb, direct, out, rows, hidden, eps))
+
+int pxr_be_recurrent_cell(int op, const float* const* in, float* const* out, float eps, size_t n) {
+    return guarded([&] {
+        RecurrentCellArgs a;
+        std::copy(in, in + 10, a.in);
+        std::copy(out, out + 6, a.out);
+        a.eps = eps;
+        driver_backend()->recurrent_cell(static_cast<RecurrentCellOp>(op), a, n);
+    });
+}
+
+int pxr_be_ssm_pass(int op, const float* const* in, float* const* out, int64_t n, int64_t l, int64_t d, int64_t s,
+                    float eps, float gamma) {
+    return guarded([&] {
+        SsmPassArgs a;
+        std::copy(in, in + 12, a.in);
+        std::copy(out, out + 10, a.out);
+        a.n = n;
+        a.l = l;
+        a.d = d;
+        a.s = s;
+        a.eps = eps;
+        a.gamma = gamma;
+        driver_backend()->ssm_pass(static_cast<SsmPassOp>(op), a);
+    });
+}
+
+int pxr_be_rl_rows(int op, const float* const* in, float* const* out, int64_t rows, int64_t cols, float scale,
+                   float lower, float upper, float gamma, float tau, int64_t ignore_index) {
+    return guarded([&] {
+        RlRowArgs a;
+        std::copy(in, in + 5, a.in);
+        std::copy(out, out + 4, a.out);
+        a.rows = rows;
+        a.cols = cols;
+        a.scale = scale;
+        a.lower = lower;
+        a.upper = upper;
+        a.gamma = gamma;
+        a.tau = tau;
+        a.ignore_index = ignore_index;
+        driver_backend()->rl_rows(static_cast<RlRowOp>(op), a);
+    });
+}
+
 int pxr_be_synchronize(void) {
 #ifdef PXR_ON_MI355X
     return guarded([&] { static_cast<MI355XBackend*>(driver_backend())->synchronize(); });

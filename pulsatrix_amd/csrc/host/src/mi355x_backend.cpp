@@ -7,6 +7,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <iterator>
 #include <new>
 #include <stdexcept>
 #include <string>
@@ -17,11 +18,6 @@ namespace {
 
 void hip_check(hipError_t e, const char* what) {
     if (e != hipSuccess) throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
-}
-
-[[noreturn]] void off_path(const char* op) {
-    throw std::logic_error(std::string("MI355XBackend::") + op +
-                           ": outside the causal-LM forward + AttnLRP path this backend implements");
 }
 
 hipStream_t S(void* s) { return static_cast<hipStream_t>(s); }
@@ -555,83 +551,167 @@ void MI355XBackend::tanh_gaussian_backward(const float* action, const float* std
                                      static_cast<int64_t>(n), stabilizer, stream_),
           "MI355XBackend::tanh_gaussian_backward");
 }
-void MI355XBackend::logic_pointwise(LogicOp, int, const float*, const float*, const float*, const float*, float*,
-                                    float*, size_t, float) {
-    off_path("logic_pointwise");
+void MI355XBackend::logic_pointwise(LogicOp op, int norm, const float* a, const float* b, const float* g_or_r,
+                                    const float* y, float* out_a, float* out_b, size_t n, float eps) {
+    check(pxk_logic_pointwise(static_cast<int>(op), norm, a, b, g_or_r, y, out_a, out_b, static_cast<int64_t>(n), eps,
+                              stream_),
+          "MI355XBackend::logic_pointwise");
 }
-void MI355XBackend::aggregator_forward(const float*, float*, float*, size_t, size_t, float) {
-    off_path("aggregator_forward");
+void MI355XBackend::aggregator_forward(const float* x, float* mean_pow, float* out, size_t n, size_t cols, float p) {
+    check(pxk_aggregator_forward(x, mean_pow, out, static_cast<int64_t>(n), static_cast<int64_t>(cols), p, stream_),
+          "MI355XBackend::aggregator_forward");
 }
-void MI355XBackend::aggregator_backward(const float*, const float*, const float*, float*, size_t, size_t, float) {
-    off_path("aggregator_backward");
+void MI355XBackend::aggregator_backward(const float* x, const float* mean_pow, const float* grad_out, float* grad_in,
+                                        size_t n, size_t cols, float p) {
+    check(pxk_aggregator_backward(x, mean_pow, grad_out, grad_in, static_cast<int64_t>(n), static_cast<int64_t>(cols), p,
+                                  stream_),
+          "MI355XBackend::aggregator_backward");
 }
-void MI355XBackend::aggregator_lrp(const float*, const float*, const float*, float*, size_t, size_t, float, float) {
-    off_path("aggregator_lrp");
+void MI355XBackend::aggregator_lrp(const float* x, const float* mean_pow, const float* r_out, float* r_in, size_t n,
+                                   size_t cols, float p, float eps) {
+    check(pxk_aggregator_lrp(x, mean_pow, r_out, r_in, static_cast<int64_t>(n), static_cast<int64_t>(cols), p, eps,
+                             stream_),
+          "MI355XBackend::aggregator_lrp");
 }
-void MI355XBackend::im2col(const float*, float*, size_t, size_t, size_t, size_t, const ConvGeometry&) {
-    off_path("im2col");
+
+namespace {
+pxk_conv_geometry geometry(const ConvGeometry& g) {
+    return pxk_conv_geometry{static_cast<int64_t>(g.kh),       static_cast<int64_t>(g.kw),
+                             static_cast<int64_t>(g.stride_h), static_cast<int64_t>(g.stride_w),
+                             static_cast<int64_t>(g.pad_h),    static_cast<int64_t>(g.pad_w)};
 }
-void MI355XBackend::col2im_add(const float*, float*, size_t, size_t, size_t, size_t, const ConvGeometry&) {
-    off_path("col2im_add");
+int64_t i64(size_t v) { return static_cast<int64_t>(v); }
+}  // namespace
+
+void MI355XBackend::im2col(const float* in, float* col, size_t n, size_t c, size_t h, size_t w,
+                           const ConvGeometry& geometry_) {
+    const pxk_conv_geometry g = geometry(geometry_);
+    check(pxk_im2col(in, col, i64(n), i64(c), i64(h), i64(w), &g, stream_), "MI355XBackend::im2col");
 }
-void MI355XBackend::add_channel_vector(const float*, const float*, float*, size_t, size_t, size_t) {
-    off_path("add_channel_vector");
+void MI355XBackend::col2im_add(const float* col, float* out, size_t n, size_t c, size_t h, size_t w,
+                               const ConvGeometry& geometry_) {
+    const pxk_conv_geometry g = geometry(geometry_);
+    check(pxk_col2im_add(col, out, i64(n), i64(c), i64(h), i64(w), &g, stream_), "MI355XBackend::col2im_add");
 }
-void MI355XBackend::lrp_conv(const float*, const float*, const float*, const float*, float*, size_t, size_t, size_t,
-                             size_t, float) {
-    off_path("lrp_conv");
+void MI355XBackend::add_channel_vector(const float* in, const float* vec, float* out, size_t n, size_t c, size_t inner) {
+    check(pxk_add_channel_vector(in, vec, out, i64(n), i64(c), i64(inner), stream_), "MI355XBackend::add_channel_vector");
 }
-void MI355XBackend::max_pool_forward(const float*, float*, float*, size_t, size_t, size_t, size_t, size_t, size_t,
-                                     size_t, size_t, size_t) {
-    off_path("max_pool_forward");
+void MI355XBackend::lrp_conv(const float* col, const float* kernel, const float* pre_bias, const float* r, float* r_col,
+                             size_t n, size_t out_channels, size_t p, size_t q, float eps) {
+    check(pxk_lrp_conv(col, kernel, pre_bias, r, r_col, i64(n), i64(out_channels), i64(p), i64(q), eps, stream_),
+          "MI355XBackend::lrp_conv");
 }
-void MI355XBackend::max_unpool(const float*, const float*, float*, size_t, size_t, size_t, size_t, size_t, size_t,
-                               size_t, size_t, size_t) {
-    off_path("max_unpool");
+void MI355XBackend::max_pool_forward(const float* in, float* out, float* argmax, size_t planes, size_t h, size_t w,
+                                     size_t kh, size_t kw, size_t sh, size_t sw, size_t ph, size_t pw) {
+    check(pxk_max_pool_forward(in, out, argmax, i64(planes), i64(h), i64(w), i64(kh), i64(kw), i64(sh), i64(sw), i64(ph),
+                               i64(pw), stream_),
+          "MI355XBackend::max_pool_forward");
 }
-void MI355XBackend::avg_pool_forward(const float*, float*, size_t, size_t, size_t, size_t, size_t) {
-    off_path("avg_pool_forward");
+void MI355XBackend::max_unpool(const float* src, const float* argmax, float* dst, size_t planes, size_t h, size_t w,
+                               size_t kh, size_t kw, size_t sh, size_t sw, size_t ph, size_t pw) {
+    check(pxk_max_unpool(src, argmax, dst, i64(planes), i64(h), i64(w), i64(kh), i64(kw), i64(sh), i64(sw), i64(ph),
+                         i64(pw), stream_),
+          "MI355XBackend::max_unpool");
 }
-void MI355XBackend::avg_pool_backward(const float*, float*, size_t, size_t, size_t, size_t, size_t) {
-    off_path("avg_pool_backward");
+void MI355XBackend::avg_pool_forward(const float* in, float* out, size_t planes, size_t h, size_t w, size_t kh,
+                                     size_t kw) {
+    check(pxk_avg_pool_forward(in, out, i64(planes), i64(h), i64(w), i64(kh), i64(kw), stream_),
+          "MI355XBackend::avg_pool_forward");
 }
-void MI355XBackend::lrp_avg_pool(const float*, const float*, float*, size_t, size_t, size_t, size_t, size_t, float) {
-    off_path("lrp_avg_pool");
+void MI355XBackend::avg_pool_backward(const float* grad_out, float* grad_in, size_t planes, size_t h, size_t w,
+                                      size_t kh, size_t kw) {
+    check(pxk_avg_pool_backward(grad_out, grad_in, i64(planes), i64(h), i64(w), i64(kh), i64(kw), stream_),
+          "MI355XBackend::avg_pool_backward");
 }
-void MI355XBackend::batch_norm_forward(const float*, const float*, const float*, float*, float*, float*, size_t, size_t,
-                                       size_t, float) {
-    off_path("batch_norm_forward");
+void MI355XBackend::lrp_avg_pool(const float* x, const float* r, float* r_in, size_t planes, size_t h, size_t w,
+                                 size_t kh, size_t kw, float eps) {
+    check(pxk_lrp_avg_pool(x, r, r_in, i64(planes), i64(h), i64(w), i64(kh), i64(kw), eps, stream_),
+          "MI355XBackend::lrp_avg_pool");
 }
-void MI355XBackend::batch_norm_backward(const float*, const float*, const float*, const float*, float*, float*, float*,
-                                        size_t, size_t, size_t) {
-    off_path("batch_norm_backward");
+void MI355XBackend::batch_norm_forward(const float* in, const float* gamma, const float* beta, float* xhat, float* out,
+                                       float* channel_std, size_t n, size_t c, size_t spatial, float eps) {
+    check(pxk_batch_norm_forward(in, gamma, beta, xhat, out, channel_std, i64(n), i64(c), i64(spatial), eps, stream_),
+          "MI355XBackend::batch_norm_forward");
 }
-void MI355XBackend::batch_norm_update_running(const float*, float*, float*, size_t, size_t, size_t, float) {
-    off_path("batch_norm_update_running");
+void MI355XBackend::batch_norm_backward(const float* grad_out, const float* gamma, const float* xhat,
+                                        const float* channel_std, float* grad_in, float* gamma_grad, float* beta_grad,
+                                        size_t n, size_t c, size_t spatial) {
+    check(pxk_batch_norm_backward(grad_out, gamma, xhat, channel_std, grad_in, gamma_grad, beta_grad, i64(n), i64(c),
+                                  i64(spatial), stream_),
+          "MI355XBackend::batch_norm_backward");
 }
-void MI355XBackend::batch_norm_eval_forward(const float*, const float*, const float*, const float*, const float*,
-                                            float*, float*, float*, size_t, size_t, size_t, float) {
-    off_path("batch_norm_eval_forward");
+void MI355XBackend::batch_norm_update_running(const float* in, float* running_mean, float* running_var, size_t n,
+                                              size_t c, size_t spatial, float momentum) {
+    check(pxk_batch_norm_update_running(in, running_mean, running_var, i64(n), i64(c), i64(spatial), momentum, stream_),
+          "MI355XBackend::batch_norm_update_running");
 }
-void MI355XBackend::batch_norm_eval_backward(const float*, const float*, const float*, const float*, float*, float*,
-                                             float*, size_t, size_t, size_t) {
-    off_path("batch_norm_eval_backward");
+void MI355XBackend::batch_norm_eval_forward(const float* in, const float* gamma, const float* beta,
+                                            const float* running_mean, const float* running_var, float* xhat,
+                                            float* out, float* channel_std, size_t n, size_t c, size_t spatial,
+                                            float eps) {
+    check(pxk_batch_norm_eval_forward(in, gamma, beta, running_mean, running_var, xhat, out, channel_std, i64(n), i64(c),
+                                      i64(spatial), eps, stream_),
+          "MI355XBackend::batch_norm_eval_forward");
 }
-void MI355XBackend::group_norm_forward(const float*, const float*, const float*, float*, float*, float*, size_t, size_t,
-                                       size_t, size_t, float) {
-    off_path("group_norm_forward");
+void MI355XBackend::batch_norm_eval_backward(const float* grad_out, const float* gamma, const float* xhat,
+                                             const float* channel_std, float* grad_in, float* gamma_grad,
+                                             float* beta_grad, size_t n, size_t c, size_t spatial) {
+    check(pxk_batch_norm_eval_backward(grad_out, gamma, xhat, channel_std, grad_in, gamma_grad, beta_grad, i64(n), i64(c),
+                                       i64(spatial), stream_),
+          "MI355XBackend::batch_norm_eval_backward");
 }
-void MI355XBackend::group_norm_backward(const float*, const float*, const float*, const float*, float*, float*, float*,
-                                        size_t, size_t, size_t, size_t) {
-    off_path("group_norm_backward");
+void MI355XBackend::group_norm_forward(const float* in, const float* gamma, const float* beta, float* xhat, float* out,
+                                       float* group_std, size_t n, size_t c, size_t spatial, size_t num_groups,
+                                       float eps) {
+    check(pxk_group_norm_forward(in, gamma, beta, xhat, out, group_std, i64(n), i64(c), i64(spatial), i64(num_groups),
+                                 eps, stream_),
+          "MI355XBackend::group_norm_forward");
 }
-void MI355XBackend::recurrent_cell(RecurrentCellOp, const RecurrentCellArgs&, size_t) { off_path("recurrent_cell"); }
-void MI355XBackend::gru_lrp_hprev(const float*, const float*, const float*, const float*, const float*, float*, size_t,
-                                  size_t, float) {
-    off_path("gru_lrp_hprev");
+void MI355XBackend::group_norm_backward(const float* grad_out, const float* gamma, const float* xhat,
+                                        const float* group_std, float* grad_in, float* gamma_grad, float* beta_grad,
+                                        size_t n, size_t c, size_t spatial, size_t num_groups) {
+    check(pxk_group_norm_backward(grad_out, gamma, xhat, group_std, grad_in, gamma_grad, beta_grad, i64(n), i64(c),
+                                  i64(spatial), i64(num_groups), stream_),
+          "MI355XBackend::group_norm_backward");
 }
-void MI355XBackend::ssm_pass(SsmPassOp, const SsmPassArgs&) { off_path("ssm_pass"); }
-void MI355XBackend::rl_rows(RlRowOp, const RlRowArgs&) { off_path("rl_rows"); }
+void MI355XBackend::recurrent_cell(RecurrentCellOp op, const RecurrentCellArgs& args, size_t n) {
+    pxk_recurrent_args a{};
+    std::copy(std::begin(args.in), std::end(args.in), a.in);
+    std::copy(std::begin(args.out), std::end(args.out), a.out);
+    a.eps = args.eps;
+    check(pxk_recurrent_cell(static_cast<int>(op), &a, i64(n), stream_), "MI355XBackend::recurrent_cell");
+}
+void MI355XBackend::gru_lrp_hprev(const float* h_prev, const float* w_hn, const float* hn, const float* r_term_b,
+                                  const float* direct, float* r_hprev, size_t rows, size_t hidden, float eps) {
+    check(pxk_gru_lrp_hprev(h_prev, w_hn, hn, r_term_b, direct, r_hprev, i64(rows), i64(hidden), eps, stream_),
+          "MI355XBackend::gru_lrp_hprev");
+}
+void MI355XBackend::ssm_pass(SsmPassOp op, const SsmPassArgs& args) {
+    pxk_ssm_args a{};
+    std::copy(std::begin(args.in), std::end(args.in), a.in);
+    std::copy(std::begin(args.out), std::end(args.out), a.out);
+    a.n = args.n;
+    a.l = args.l;
+    a.d = args.d;
+    a.s = args.s;
+    a.eps = args.eps;
+    a.gamma = args.gamma;
+    check(pxk_ssm_pass(static_cast<int>(op), &a, stream_), "MI355XBackend::ssm_pass");
+}
+void MI355XBackend::rl_rows(RlRowOp op, const RlRowArgs& args) {
+    pxk_rl_args a{};
+    std::copy(std::begin(args.in), std::end(args.in), a.in);
+    std::copy(std::begin(args.out), std::end(args.out), a.out);
+    a.rows = args.rows;
+    a.cols = args.cols;
+    a.scale = args.scale;
+    a.lower = args.lower;
+    a.upper = args.upper;
+    a.gamma = args.gamma;
+    a.tau = args.tau;
+    a.ignore_index = args.ignore_index;
+    check(pxk_rl_rows(static_cast<int>(op), &a, stream_), "MI355XBackend::rl_rows");
+}
 void MI355XBackend::top_k_rows(const float* in, float* values, float* indices, size_t rows, size_t cols, size_t k,
                                bool largest) {
     check(pxk_top_k_rows(in, values, indices, static_cast<int64_t>(rows), static_cast<int64_t>(cols),

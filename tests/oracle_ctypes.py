@@ -409,6 +409,26 @@ def _bind_backend_shim(L):
             "tanh_gaussian_forward": [vp, vp, vp, vp, vp, vp, sz, sz, f, ctypes.c_double],
             "tanh_gaussian_backward": [vp, vp, vp, vp, vp, vp, vp, sz, f],
             "top_k_rows": [vp, vp, vp, sz, sz, sz, i],
+            "logic_pointwise": [i, i, vp, vp, vp, vp, vp, vp, sz, f],
+            "aggregator_forward": [vp, vp, vp, sz, sz, f], "aggregator_backward": [vp, vp, vp, vp, sz, sz, f],
+            "aggregator_lrp": [vp, vp, vp, vp, sz, sz, f, f],
+            "im2col": [vp, vp] + [sz] * 10, "col2im_add": [vp, vp] + [sz] * 10,
+            "add_channel_vector": [vp, vp, vp, sz, sz, sz], "lrp_conv": [vp, vp, vp, vp, vp, sz, sz, sz, sz, f],
+            "max_pool_forward": [vp, vp, vp] + [sz] * 9, "max_unpool": [vp, vp, vp] + [sz] * 9,
+            "avg_pool_forward": [vp, vp, sz, sz, sz, sz, sz], "avg_pool_backward": [vp, vp, sz, sz, sz, sz, sz],
+            "lrp_avg_pool": [vp, vp, vp, sz, sz, sz, sz, sz, f],
+            "batch_norm_forward": [vp, vp, vp, vp, vp, vp, sz, sz, sz, f],
+            "batch_norm_backward": [vp, vp, vp, vp, vp, vp, vp, sz, sz, sz],
+            "batch_norm_update_running": [vp, vp, vp, sz, sz, sz, f],
+            "batch_norm_eval_forward": [vp, vp, vp, vp, vp, vp, vp, vp, sz, sz, sz, f],
+            "batch_norm_eval_backward": [vp, vp, vp, vp, vp, vp, vp, sz, sz, sz],
+            "group_norm_forward": [vp, vp, vp, vp, vp, vp, sz, sz, sz, sz, f],
+            "group_norm_backward": [vp, vp, vp, vp, vp, vp, vp, sz, sz, sz, sz],
+            "gru_lrp_hprev": [vp, vp, vp, vp, vp, vp, sz, sz, f],
+            "recurrent_cell": [i, ctypes.POINTER(vp), ctypes.POINTER(vp), f, sz],
+            "ssm_pass": [i, ctypes.POINTER(vp), ctypes.POINTER(vp)] + [ctypes.c_int64] * 4 + [f, f],
+            "rl_rows": [i, ctypes.POINTER(vp), ctypes.POINTER(vp), ctypes.c_int64, ctypes.c_int64, f, f, f, f, f,
+                        ctypes.c_int64],
         }
         for name, args in sig.items():
             fn = getattr(L, "pxr_be_" + name)
