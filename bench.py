@@ -653,7 +653,7 @@ def main():
             "peak": peak,
             "unit": unit,
             "frac": round(achieved / peak, 4),
-            "traffic": None if traffic is None else traffic["bytes"],
+            "traffic": None if traffic is None else int(traffic),
             "traffic_unit": "HBM bytes per launch (FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0, copy-calibrated)",
             "avg_launch_us": round(dom["seconds"] / dom["calls"] * 1e6, 2),
             "algorithmic_gflop_per_launch": round(dom["flops"] / dom["calls"] / 1e9, 4),
