@@ -474,6 +474,11 @@ int pxk_decode_rope_append(const float* q, int64_t ldq, const float* k, int64_t 
  * workspace (pxk_decode_attention_workspace() bytes), then one workgroup per (sequence, head)
  * merges the partials. */
 size_t pxk_decode_attention_workspace(int64_t n, int64_t heads, int64_t head_dim, int64_t max_keys);
+/* The keys [j0, j1) that 64-key chunk `chunk` of pxk_decode_attention reads for a query at cache
+ * position pos (clamped to [0, max_keys)) under a sliding window (0: none); j1 <= j0 when the chunk
+ * holds none. The kernel's own definition, on the host: introspection for tests, no reference
+ * counterpart. */
+int pxk_decode_chunk_keys(int64_t pos, int64_t max_keys, int64_t window, int64_t chunk, int64_t* j0, int64_t* j1);
 int pxk_decode_attention(const float* q, const float* k_cache, const float* v_cache, int64_t seq_stride, float* ctx,
                          const int32_t* pos, int64_t n, int64_t heads, int64_t kv_heads, int64_t head_dim,
                          int64_t window, int64_t max_keys, float scale, float* workspace, size_t workspace_bytes,

@@ -136,6 +136,19 @@ constexpr int kPartHead = 4;   // a chunk's partial: max, exp-sum, two pad float
 static_assert(kKeyChunk == kWave && kThreads == 4 * kKeyChunk, "a lane per key in the softmax, four threads per key");
 typedef float f4 __attribute__((ext_vector_type(4)));
 
+// The keys [j0, j1) of 64-key `chunk` that a query at cache position *pos sees: the position is
+// clamped to the cache, a sliding layer's window starts at p + 1 - window (attention_masked,
+// row_math.hpp:117-126), and a chunk wholly outside [lo, p] gets j1 <= j0. One definition for the
+// kernel and for pxk_decode_chunk_keys, which checks it on the host.
+__host__ __device__ inline void chunk_keys(int64_t pos, int64_t max_keys, int64_t window, int64_t chunk, int64_t* j0,
+                                           int64_t* j1) {
+    const int64_t p = pos < 0 ? 0 : (pos > max_keys - 1 ? max_keys - 1 : pos);
+    const int64_t lo = (window > 0 && p + 1 > window) ? p + 1 - window : 0;
+    const int64_t c0 = chunk * kKeyChunk, c1 = c0 + kKeyChunk;
+    *j0 = c0 > lo ? c0 : lo;
+    *j1 = c1 < p + 1 ? c1 : p + 1;
+}
+
 // First pass, one workgroup per (sequence, query head, 64-key chunk): the chunk's visible keys
 // (within [lo, pos], a sliding layer's window per attention_masked, row_math.hpp:117-126) scored
 // against the query by four threads per key (each on every fourth float4 of head_dim, summed with
@@ -148,9 +161,8 @@ __global__ void __launch_bounds__(kThreads) decode_attention_part_kernel(const D
     const int64_t bh = blockIdx.x / a.chunks, chunk = blockIdx.x - bh * a.chunks;
     const int64_t b = bh / a.H, h = bh - b * a.H, hk = h / (a.H / a.Hkv);
     const int64_t kvd = a.Hkv * a.D;
-    const int64_t p = min(max(static_cast<int64_t>(*a.pos), int64_t{0}), a.max_keys - 1);
-    const int64_t lo = (a.window > 0 && p + 1 > a.window) ? p + 1 - a.window : 0;
-    const int64_t j0 = max(chunk * kKeyChunk, lo), j1 = min(chunk * kKeyChunk + kKeyChunk, p + 1);
+    int64_t j0, j1;
+    chunk_keys(static_cast<int64_t>(*a.pos), a.max_keys, a.window, chunk, &j0, &j1);
     const int nk = j1 > j0 ? static_cast<int>(j1 - j0) : 0;
     float* out = a.part + (bh * a.chunks + chunk) * (a.D + kPartHead);
     const int tid = threadIdx.x;
@@ -425,6 +437,14 @@ extern "C" int pxk_decode_attention(const float* q, const float* k_cache, const 
     PXK_LAUNCH(decode_attention_merge_kernel, dim3(static_cast<unsigned>(n * heads)), dim3(kThreads), 0,
                        S(stream), a);
     return launched("pxk_decode_attention (merge)");
+}
+
+extern "C" int pxk_decode_chunk_keys(int64_t pos, int64_t max_keys, int64_t window, int64_t chunk, int64_t* j0,
+                                     int64_t* j1) {
+    if (max_keys <= 0 || window < 0 || chunk < 0 || !j0 || !j1)
+        return fail(PXK_ERR_INVALID, "pxk_decode_chunk_keys: bad arguments");
+    chunk_keys(pos, max_keys, window, chunk, j0, j1);
+    return PXK_OK;
 }
 
 extern "C" size_t pxk_decode_pick_workspace(int64_t n) {

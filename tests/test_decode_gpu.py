@@ -16,6 +16,7 @@ import oracle_ctypes as oc
 from pulsatrix_amd import models
 from pulsatrix_amd import native as N
 from test_model_gpu import LXT_EPS, expect_relevance_agrees, to_px
+from test_oracle import gemma_config
 
 pytestmark = pytest.mark.gpu
 LXT = oc.lrp_rule(oc.EPSILON, epsilon=LXT_EPS, bias_in_denominator=True)
@@ -43,6 +44,26 @@ def test_generate_matches_oracle_greedy(name):
     p = prompts.shape[1]
     np.testing.assert_array_equal(ids[:, :p + new].astype(np.int64), want)
     assert np.all(ids[:, p + new:] == -1.0), "nothing is written past the new tokens"
+    got = picked[:, p:p + new]
+    assert np.all(np.abs(got - want_logit) <= 1e-4 * np.maximum(1.0, np.abs(want_logit)))
+
+
+def test_sliding_window_spanning_several_key_chunks():
+    """A window of 100 keys over up to 239 positions (150-token prompts, 90 new tokens) on a Gemma 3
+    variant whose layers 0 and 2 slide: at the last steps the query sees keys 140-239, so the
+    64-key chunks 0 and 1 hold nothing visible (empty partials the merge skips), chunk 2 is cut by
+    the window and chunk 3 by the position. Greedy ids against the oracle's uncached decode, the
+    picked logits within 1e-4."""
+    cfg = gemma_config(vocab_size=300, sliding_window=100)
+    params = oc.synthetic_params(cfg, 64, std=0.05)
+    prompts = np.random.RandomState(9).randint(0, 300, size=(2, 150))
+    new = 90
+    want, want_logit, margin = dc.oracle_greedy(cfg, params, prompts, new)
+    assert margin > 1e-3, "the case needs a clear greedy path"
+    lm = models.CausalLM(to_px(cfg), params)
+    _, ids, picked = generate(lm, prompts, new)
+    p = prompts.shape[1]
+    np.testing.assert_array_equal(ids[:, :p + new].astype(np.int64), want)
     got = picked[:, p:p + new]
     assert np.all(np.abs(got - want_logit) <= 1e-4 * np.maximum(1.0, np.abs(want_logit)))
 
