@@ -836,6 +836,45 @@ __global__ void __launch_bounds__(NT) splitk_reduce_kernel(const Args g) {
     if (g.causal == PXK_CAUSAL_TRI && n0 > (m0 / g.bm) * g.bm + g.bm - 1) return;  // tile never computed
     const int row = threadIdx.x / (BN / 4), col = 4 * (threadIdx.x % (BN / 4));
     const int64_t m = m0 + row, n = n0 + col;
+    if constexpr (EPI == PXK_EPI_MUL_X_SPLIT) {
+        // Elementwise epilogue: the thread's epilogue operands are loaded with its partials, so
+        // both wait on memory once, and the result goes straight out (no LDS pass). The same
+        // expressions, in the same order, as epilogue_rows.
+        if (m >= g.M || n >= g.N) return;
+        const int cnt = g.N - n < 4 ? static_cast<int>(g.N - n) : 4;
+        const bool vp = (g.N % 4) == 0 && cnt == 4, ve = g.vec_e && cnt == 4;
+        const int64_t inner = g.inner;
+        const float* Y = g.y.p ? obase(g.y, b, inner, 0) + m * g.y.ld + n : nullptr;
+        const f4 x = ld4(obase(g.x, b, inner, 0) + m * g.x.ld + n, ve, cnt);
+        const f4 sa = ld4(obase(g.z2, b, inner, 0) + m * g.z2.ld + n, ve, cnt);
+        const f4 sb = ld4(obase(g.z3, b, inner, 0) + m * g.z3.ld + n, ve, cnt);
+        const f4 sum = ld4(obase(g.w, b, inner, 0) + m * g.w.ld + n, ve, cnt);
+        const f4 y = Y ? ld4(Y, ve, cnt) : f4{0.f, 0.f, 0.f, 0.f};
+        const int64_t plane = g.batch * g.M * g.N;
+        const float* P = g.ws + (b * g.M + m) * g.N + n;
+        f4 acc = {0.f, 0.f, 0.f, 0.f};
+        int k = 0;
+        for (; k + 8 <= g.splits; k += 8) {
+            f4 t[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) t[u] = ld4(P + (k + u) * plane, vp, cnt);
+#pragma unroll
+            for (int u = 0; u < 8; ++u) acc += t[u];
+        }
+        for (; k < g.splits; ++k) acc += ld4(P + k * plane, vp, cnt);
+        f4 v = x * acc;
+        if (Y) v = y + v;
+        f4 ra, rb;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float denom = stab(sum[j], g.eps);
+            ra[j] = (sa[j] / denom) * v[j];
+            rb[j] = (sb[j] / denom) * v[j];
+        }
+        st4(obase_w(g.c, b, inner) + m * g.c.ld + n, ra, ve, cnt);
+        st4(obase_w(g.c2, b, inner) + m * g.c2.ld + n, rb, ve, cnt);
+        return;
+    }
     f4 v = {0.f, 0.f, 0.f, 0.f};
     if (m < g.M && n < g.N) {
         const int cnt = g.N - n < 4 ? static_cast<int>(g.N - n) : 4;
@@ -1049,7 +1088,8 @@ constexpr int kTiles = 6;  // PXK_TILE_128x128 .. PXK_TILE_32x32_DIRECT
 
 struct TileInfo {
     int bm, bn, bk, threads, smem_bytes;
-    double floor_us;  // a K stage of a workgroup alone on its CU (load latency bound), measured
+    double floor_us;     // a K stage of a workgroup alone on its CU (load latency bound), measured
+    double floor_nt_us;  // the same for an NT product with the DIV_STAB prologue (A, Z, B all K-contiguous)
     double util;      // MFMA utilisation when several waves share a SIMD, measured
 };
 
@@ -1106,12 +1146,15 @@ constexpr int smem_of() {
 }
 
 const TileInfo kTileInfo[kTiles] = {
-    {128, 128, 32, C128::NT, smem_of<C128>(), 1.0, 0.75},
-    {64, 64, 32, C64::NT, smem_of<C64>(), 0.8, 0.65},
-    {32, 64, 64, C32x64::NT, smem_of<C32x64>(), 0.8, 0.55},
-    {32, 32, 64, C32::NT, smem_of<C32>(), 0.8, 0.5},
-    {32, 64, 64, C32x64::NT, 4 * C32x64::KS * 32 * C32x64::LDC, 0.65, 0.55},  // direct loads
-    {32, 32, 64, C32::NT, 4 * C32::KS * 32 * C32::LDC, 0.65, 0.5},
+    {128, 128, 32, C128::NT, smem_of<C128>(), 1.0, 1.0, 0.75},
+    {64, 64, 32, C64::NT, smem_of<C64>(), 0.8, 0.8, 0.65},
+    {32, 64, 64, C32x64::NT, smem_of<C32x64>(), 0.8, 0.8, 0.55},
+    {32, 32, 64, C32::NT, smem_of<C32>(), 0.8, 0.8, 0.5},
+    // Direct loads: an NT relevance GEMM with the stabilised-divide prologue streams A, Z and B as
+    // K-contiguous rows, each 16-lane group reading 16 rows x 64 B per instruction; at 512 rows
+    // it runs 10-15% slower than from LDS panels (without the prologue the direct tile still wins).
+    {32, 64, 64, C32x64::NT, 4 * C32x64::KS * 32 * C32x64::LDC, 0.65, 1.0, 0.55},
+    {32, 32, 64, C32::NT, 4 * C32::KS * 32 * C32::LDC, 0.65, 1.0, 0.5},
 };
 
 // The skinny kernels built: B layout, epilogue, kernels for up to 4, 8 and 16 rows (NN: with 64-,
@@ -1234,7 +1277,8 @@ double estimate(const pxk_gemm_desc* d, const TileInfo& t, double tiles, double 
     const double per = std::ceil(stages / splits);
     const double waves_per_simd = std::ceil(tiles * splits / 256.0);
     const double mfma_us = static_cast<double>(t.bm) * t.bn * t.bk / 128.0 / 2400.0;
-    const double stage_us = std::max(t.floor_us, waves_per_simd * mfma_us / t.util);
+    const double floor = d->trans_b && d->prologue != PXK_PRO_NONE ? t.floor_nt_us : t.floor_us;
+    const double stage_us = std::max(floor, waves_per_simd * mfma_us / t.util);
     double us = 4.0 + per * stage_us;
     if (splits > 1) us += 6.0 + 2.0 * splits * d->batch * d->m * d->n * 4.0 / 5.0e6;
     return us;
