@@ -44,7 +44,7 @@ LXT_EPS = 1e-9
 # roofline line carries the figure of its kernel when that kernel was measured under this plan.
 STEP_KERNEL_TRAFFIC = {name: kib * 1024 for name, kib in {
     "gemm 32x32 NT pro0 epi8 split8": 39929,  # gate|up relevance 22502 + its split-K reduce 17427
-    "gemm 32x64d NN pro0 epi2 split1": 24798,  # o projection 15198, down projection 34398
+    "gemm 32x64d NN pro0 epi2 split1": 24798,  # o projection 15198, down projection 34398 (before the 32x48 tile)
     "gemm 32x64 NN pro0 epi10 split1": 28726,  # gate|up projection (SwiGLU epilogue)
     "gemm 32x32 NT pro1 epi7 split1": 34595,  # down relevance
     "gemm 32x64d NT pro0 epi8 split1": 27521,  # q|k|v relevance (residual split)
@@ -334,7 +334,7 @@ def op_sweep(torch, N, models):
     stream = torch.cuda.ExternalStream(raw_st)
     rows = []
     tile_name = {N.TILE_128x128: "128x128", N.TILE_64x64: "64x64", N.TILE_32x64: "32x64", N.TILE_32x32: "32x32",
-                 N.TILE_32x64_DIRECT: "32x64d", N.TILE_32x32_DIRECT: "32x32d"}
+                 N.TILE_32x64_DIRECT: "32x64d", N.TILE_32x32_DIRECT: "32x32d", N.TILE_32x48_DIRECT: "32x48d"}
     for (M, K, Nn) in SWEEP_GEMMS:
         for orient in ("NN", "NT", "TN"):
             desc, keep = sweep_gemm(torch, N, M, K, Nn, orient)

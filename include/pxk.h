@@ -118,10 +118,11 @@ enum {
     PXK_TILE_32x32 = 4,   /* as 32x64 */
     PXK_TILE_32x64_DIRECT = 5, /* as 32x64, each wave streaming its operands from L2 into registers */
     PXK_TILE_32x32_DIRECT = 6,
-    PXK_TILE_SKINNY = 7   /* m <= 16, unbatched, A untransposed, no prologue or causal range: B streamed
+    PXK_TILE_SKINNY = 7,  /* m <= 16, unbatched, A untransposed, no prologue or causal range: B streamed
                              with 128-bit vector loads, A in LDS, 64-column tiles; NN split over K
                              (STORE, STORE_BIAS, ADD_RESID, SWIGLU_FWD), NT in one pass (STORE, K up
                              to about 4000 rows at m <= 4). PXK_TILE_AUTO picks it whenever it applies */
+    PXK_TILE_32x48_DIRECT = 8 /* as 32x64 direct, 48 columns: 192 workgroups over a 512 x 576 output */
 };
 
 typedef struct pxk_gemm_desc {

@@ -97,6 +97,7 @@ using C128 = Cfg<128, 128, 2, 2, 1, 1>;
 using C64 = Cfg<64, 64, 2, 2, 1, 3>;
 using C32x64 = Cfg<32, 64, 1, 1, 4, 2>;
 using C32 = Cfg<32, 32, 1, 1, 4, 3>;
+using C32x48 = Cfg<32, 48, 1, 1, 4, 2>;  // direct loads only: 192 workgroups over 512 x 576
 
 template <class F, int... Is>
 __device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, Is...>) {
@@ -826,7 +827,8 @@ __global__ void __launch_bounds__(C::NT) gemm_direct_kernel(const Args g) {
 }
 
 // Sums the split partials of a slab of rows in split order and runs the tile epilogue. One
-// workgroup per RS x BN slab, one float4 column per thread.
+// workgroup per RS x BN slab, one float4 column per thread (threads past RS rows idle when BN / 4
+// does not divide the workgroup).
 template <int BN, int EPI>
 __global__ void __launch_bounds__(NT) splitk_reduce_kernel(const Args g) {
     constexpr int RS = 4 * NT / BN, LDC = BN + 4;
@@ -836,11 +838,12 @@ __global__ void __launch_bounds__(NT) splitk_reduce_kernel(const Args g) {
     if (g.causal == PXK_CAUSAL_TRI && n0 > (m0 / g.bm) * g.bm + g.bm - 1) return;  // tile never computed
     const int row = threadIdx.x / (BN / 4), col = 4 * (threadIdx.x % (BN / 4));
     const int64_t m = m0 + row, n = n0 + col;
+    const bool mine = row < RS;
     if constexpr (EPI == PXK_EPI_MUL_X_SPLIT) {
         // Elementwise epilogue: the thread's epilogue operands are loaded with its partials, so
         // both wait on memory once, and the result goes straight out (no LDS pass). The same
         // expressions, in the same order, as epilogue_rows.
-        if (m >= g.M || n >= g.N) return;
+        if (!mine || m >= g.M || n >= g.N) return;
         const int cnt = g.N - n < 4 ? static_cast<int>(g.N - n) : 4;
         const bool vp = (g.N % 4) == 0 && cnt == 4, ve = g.vec_e && cnt == 4;
         const int64_t inner = g.inner;
@@ -876,7 +879,7 @@ __global__ void __launch_bounds__(NT) splitk_reduce_kernel(const Args g) {
         return;
     }
     f4 v = {0.f, 0.f, 0.f, 0.f};
-    if (m < g.M && n < g.N) {
+    if (mine && m < g.M && n < g.N) {
         const int cnt = g.N - n < 4 ? static_cast<int>(g.N - n) : 4;
         const bool vec = (g.N % 4) == 0 && cnt == 4;
         const int64_t plane = g.batch * g.M * g.N;
@@ -891,7 +894,7 @@ __global__ void __launch_bounds__(NT) splitk_reduce_kernel(const Args g) {
         }
         for (; k < g.splits; ++k) v += ld4(P + k * plane, vec, cnt);
     }
-    *reinterpret_cast<f4*>(Cs + row * LDC + col) = v;
+    if (mine) *reinterpret_cast<f4*>(Cs + row * LDC + col) = v;
     __syncthreads();
     epilogue_rows<RS, BN, EPI, NT>(Cs, LDC, m0, n0, b, g);
 }
@@ -1084,13 +1087,22 @@ __global__ void __launch_bounds__(NT) skinny_nt_kernel(const Args g) {
 
 using KernelFn = void (*)(const Args);
 
-constexpr int kTiles = 6;  // PXK_TILE_128x128 .. PXK_TILE_32x32_DIRECT
+constexpr int kTiles = 7;  // PXK_TILE_128x128 .. PXK_TILE_32x32_DIRECT, then PXK_TILE_32x48_DIRECT
+
+// Plan index <-> PXK_TILE_*: the MFMA tiles in table order, the skinny kernels after them.
+constexpr int kSkinnyTile = kTiles;
+int public_tile(int t) { return t < 6 ? t + 1 : (t == 6 ? PXK_TILE_32x48_DIRECT : PXK_TILE_SKINNY); }
+int plan_tile(int id) {  // -1: none
+    if (id >= PXK_TILE_128x128 && id <= PXK_TILE_32x32_DIRECT) return id - 1;
+    if (id == PXK_TILE_32x48_DIRECT) return 6;
+    return id == PXK_TILE_SKINNY ? kSkinnyTile : -1;
+}
 
 struct TileInfo {
     int bm, bn, bk, threads, smem_bytes;
-    double floor_us;     // a K stage of a workgroup alone on its CU (load latency bound), measured
-    double floor_nt_us;  // the same for an NT product with the DIV_STAB prologue (A, Z, B all K-contiguous)
+    double floor_us;  // a K stage of a workgroup alone on its CU (load latency bound), measured
     double util;      // MFMA utilisation when several waves share a SIMD, measured
+    bool direct;      // waves stream their operands from L2 into registers (no LDS panels)
 };
 
 struct Entry {
@@ -1102,12 +1114,13 @@ struct Entry {
 #define PXK_KSET(TA, TB, P, EPI)                                                                    \
     {gemm_kernel<C128, TA, TB, P, EPI>, gemm_kernel<C64, TA, TB, P, EPI>, gemm_kernel<C32x64, TA, TB, P, EPI>, \
      gemm_kernel<C32, TA, TB, P, EPI>, gemm_direct_kernel<C32x64, TA, TB, P, EPI>,                         \
-     gemm_direct_kernel<C32, TA, TB, P, EPI>}
+     gemm_direct_kernel<C32, TA, TB, P, EPI>, gemm_direct_kernel<C32x48, TA, TB, P, EPI>}
 #define PXK_GEMM_ENTRY(TA, TB, PRO, EPI)                                                                   \
     Entry {                                                                                                \
         TA, TB, PRO, EPI, {PXK_KSET(TA, TB, PRO, EPI), PXK_KSET(TA, TB, (PRO ? kProStabBias : PRO), EPI)}, \
             {splitk_reduce_kernel<128, EPI>, splitk_reduce_kernel<64, EPI>, splitk_reduce_kernel<64, EPI>, \
-             splitk_reduce_kernel<32, EPI>, splitk_reduce_kernel<64, EPI>, splitk_reduce_kernel<32, EPI>},  \
+             splitk_reduce_kernel<32, EPI>, splitk_reduce_kernel<64, EPI>, splitk_reduce_kernel<32, EPI>,   \
+             splitk_reduce_kernel<48, EPI>},                                                                \
     }
 
 const Entry kTable[] = {
@@ -1146,15 +1159,13 @@ constexpr int smem_of() {
 }
 
 const TileInfo kTileInfo[kTiles] = {
-    {128, 128, 32, C128::NT, smem_of<C128>(), 1.0, 1.0, 0.75},
-    {64, 64, 32, C64::NT, smem_of<C64>(), 0.8, 0.8, 0.65},
-    {32, 64, 64, C32x64::NT, smem_of<C32x64>(), 0.8, 0.8, 0.55},
-    {32, 32, 64, C32::NT, smem_of<C32>(), 0.8, 0.8, 0.5},
-    // Direct loads: an NT relevance GEMM with the stabilised-divide prologue streams A, Z and B as
-    // K-contiguous rows, each 16-lane group reading 16 rows x 64 B per instruction; at 512 rows
-    // it runs 10-15% slower than from LDS panels (without the prologue the direct tile still wins).
-    {32, 64, 64, C32x64::NT, 4 * C32x64::KS * 32 * C32x64::LDC, 0.65, 1.0, 0.55},
-    {32, 32, 64, C32::NT, 4 * C32::KS * 32 * C32::LDC, 0.65, 1.0, 0.5},
+    {128, 128, 32, C128::NT, smem_of<C128>(), 1.0, 0.75, false},
+    {64, 64, 32, C64::NT, smem_of<C64>(), 0.8, 0.65, false},
+    {32, 64, 64, C32x64::NT, smem_of<C32x64>(), 0.8, 0.55, false},
+    {32, 32, 64, C32::NT, smem_of<C32>(), 0.8, 0.5, false},
+    {32, 64, 64, C32x64::NT, 4 * C32x64::KS * 32 * C32x64::LDC, 0.65, 0.55, true},
+    {32, 32, 64, C32::NT, 4 * C32::KS * 32 * C32::LDC, 0.65, 0.5, true},
+    {32, 48, 64, C32x48::NT, 4 * C32x48::KS * 32 * C32x48::LDC, 0.65, 0.55, true},
 };
 
 // The skinny kernels built: B layout, epilogue, kernels for up to 4, 8 and 16 rows (NN: with 64-,
@@ -1186,7 +1197,6 @@ const SkinnyEntry kSkinny[] = {
                 {nullptr, nullptr, nullptr}},
 };
 
-constexpr int kSkinnyTile = kTiles;  // plan index of PXK_TILE_SKINNY
 constexpr int kSkinnyMaxLds = 64 * 1024;
 
 int skinny_mb(int64_t m) { return m <= 4 ? 4 : (m <= 8 ? 8 : 16); }
@@ -1277,8 +1287,15 @@ double estimate(const pxk_gemm_desc* d, const TileInfo& t, double tiles, double 
     const double per = std::ceil(stages / splits);
     const double waves_per_simd = std::ceil(tiles * splits / 256.0);
     const double mfma_us = static_cast<double>(t.bm) * t.bn * t.bk / 128.0 / 2400.0;
-    const double floor = d->trans_b && d->prologue != PXK_PRO_NONE ? t.floor_nt_us : t.floor_us;
-    const double stage_us = std::max(floor, waves_per_simd * mfma_us / t.util);
+    double floor = t.floor_us, util = t.util;
+    if (t.direct && d->trans_b && d->prologue != PXK_PRO_NONE) {
+        // An NT relevance GEMM with the stabilised-divide prologue streams A, Z and B as K-contiguous
+        // rows, each 16-lane group reading 16 rows x 64 B per instruction: at 512 rows the direct
+        // tiles run 10-25% slower than from LDS panels (measured; without the prologue they win).
+        floor = 1.0;
+        util *= 0.65;
+    }
+    const double stage_us = std::max(floor, waves_per_simd * mfma_us / util);
     double us = 4.0 + per * stage_us;
     if (splits > 1) us += 6.0 + 2.0 * splits * d->batch * d->m * d->n * 4.0 / 5.0e6;
     return us;
@@ -1289,8 +1306,9 @@ int plan(const pxk_gemm_desc* d, Plan* p) {
     if (d->k < 0 || d->inner <= 0 || d->kgroups <= 0 || d->batch % d->inner != 0)
         return fail(PXK_ERR_INVALID, "pxk_gemm: bad k, inner or kgroups (batch must be a multiple of inner)");
     if (d->causal < 0 || d->causal > 3) return fail(PXK_ERR_INVALID, "pxk_gemm: unknown causal mode %d", d->causal);
-    if (d->tile < 0 || d->tile > kTiles + 1) return fail(PXK_ERR_INVALID, "pxk_gemm: unknown tile %d", d->tile);
-    const TileInfo* forced = d->tile > 0 && d->tile <= kTiles ? &kTileInfo[d->tile - 1] : nullptr;
+    const int want = d->tile == 0 ? -1 : plan_tile(d->tile);  // the forced plan tile, if any
+    if (d->tile != 0 && want < 0) return fail(PXK_ERR_INVALID, "pxk_gemm: unknown tile %d", d->tile);
+    const TileInfo* forced = want >= 0 && want < kTiles ? &kTileInfo[want] : nullptr;
     if (d->splits < 0 || d->splits > 4096) return fail(PXK_ERR_INVALID, "pxk_gemm: bad split count %d", d->splits);
     p->e = find_entry(d->trans_a != 0, d->trans_b != 0, d->prologue, d->epilogue);
     if (!p->e)
@@ -1359,7 +1377,7 @@ int plan(const pxk_gemm_desc* d, Plan* p) {
     // (64 columns for the SwiGLU gate, whose gate and up blocks interleave in 64s), and no split over
     // K unless a workgroup would stream more than 1 MiB of B.
     p->skinny = nullptr;
-    if (d->tile == 0 || d->tile == kSkinnyTile + 1) {
+    if (d->tile == 0 || want == kSkinnyTile) {
         if (const SkinnyEntry* se = skinny_entry(d)) {
             p->skinny = se;
             p->tile = kSkinnyTile;
@@ -1380,7 +1398,7 @@ int plan(const pxk_gemm_desc* d, Plan* p) {
             if (p->tiles_n * p->splits > (int64_t{1} << 31) - 1) return fail(PXK_ERR_INVALID, "pxk_gemm: grid too large");
             return PXK_OK;
         }
-        if (d->tile == kSkinnyTile + 1)
+        if (want == kSkinnyTile)
             return fail(PXK_ERR_INVALID,
                         "pxk_gemm: the skinny tile needs m <= 16, batch 1, no prologue or causal range, A untransposed "
                         "and a built epilogue (STORE, STORE_BIAS, ADD_RESID, SWIGLU_FWD; NT: STORE, K up to the LDS)");
@@ -1391,7 +1409,7 @@ int plan(const pxk_gemm_desc* d, Plan* p) {
     int best_t = -1, best_s = 1;
     double best = 0.0;
     for (int t = 0; t < kTiles; ++t) {
-        if (d->tile > 0 && t != d->tile - 1) continue;
+        if (d->tile > 0 && t != want) continue;
         const TileInfo& ti = kTileInfo[t];
         if ((epi == PXK_EPI_ROPE_REL || epi == PXK_EPI_ROPE_FWD) && !rope_fits(d, ti.bn)) continue;
         if (epi == PXK_EPI_SWIGLU_FWD && ti.bn % 64 != 0) continue;
@@ -1439,7 +1457,7 @@ extern "C" int pxk_gemm_supported(int ta, int tb, int pro, int epi) { return fin
 extern "C" int pxk_gemm_plan(const pxk_gemm_desc* d, int32_t* tile, int32_t* splits) {
     Plan p;
     if (const int rc = plan(d, &p)) return rc;
-    if (tile) *tile = p.tile + 1;
+    if (tile) *tile = public_tile(p.tile);
     if (splits) *splits = p.splits;
     return PXK_OK;
 }

@@ -27,9 +27,10 @@ COMBOS = [
     (0, 1, N.PRO_NONE, N.EPI_MUL_X_SPLIT), (0, 0, N.PRO_DIV_STAB, N.EPI_MUL_X_SPLIT),
     (0, 1, N.PRO_DIV_STAB, N.EPI_MUL_X_SPLIT), (0, 0, N.PRO_NONE, N.EPI_ROPE_FWD),
 ]
-TILES = [N.TILE_128x128, N.TILE_64x64, N.TILE_32x64, N.TILE_32x32, N.TILE_32x64_DIRECT, N.TILE_32x32_DIRECT]
+TILES = [N.TILE_128x128, N.TILE_64x64, N.TILE_32x64, N.TILE_32x32, N.TILE_32x64_DIRECT, N.TILE_32x32_DIRECT,
+         N.TILE_32x48_DIRECT]
 TILE_BN = {N.TILE_128x128: 128, N.TILE_64x64: 64, N.TILE_32x64: 64, N.TILE_32x32: 32, N.TILE_32x64_DIRECT: 64,
-           N.TILE_32x32_DIRECT: 32}
+           N.TILE_32x32_DIRECT: 32, N.TILE_32x48_DIRECT: 48}
 EPS = 1e-6
 
 
