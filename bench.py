@@ -43,14 +43,14 @@ LXT_EPS = 1e-9
 # split-K GEMM and its reduce); the o and down projections share one name and are averaged. The
 # roofline line carries the figure of its kernel when that kernel was measured under this plan.
 STEP_KERNEL_TRAFFIC = {name: kib * 1024 for name, kib in {
-    "gemm 32x32 NT pro0 epi8 split8": 39929,  # gate|up relevance 22502 + its split-K reduce 17427
-    "gemm 32x64d NN pro0 epi2 split1": 24798,  # o projection 15198, down projection 34398 (before the 32x48 tile)
-    "gemm 32x64 NN pro0 epi10 split1": 28726,  # gate|up projection (SwiGLU epilogue)
-    "gemm 32x32 NT pro1 epi7 split1": 34595,  # down relevance
-    "gemm 32x64d NT pro0 epi8 split1": 27521,  # q|k|v relevance (residual split)
-    "gemm 32x64d NT pro1 epi4 split1": 23263,  # o relevance
+    "gemm 32x48d NT pro0 epi8 split4": 40358,  # gate|up relevance 24106 + its split-K reduce 16252
+    "gemm 32x48d NN pro0 epi2 split1": 24524,  # o and down projections (median of both)
+    "gemm 32x64 NN pro0 epi10 split1": 28732,  # gate|up projection (SwiGLU epilogue)
+    "gemm 32x32 NT pro1 epi7 split1": 34588,  # down relevance
+    "gemm 32x48d NT pro0 epi8 split1": 27844,  # q|k|v relevance (residual split)
+    "gemm 32x64 NT pro1 epi4 split1": 23280,  # o relevance
     "gemm 32x64d NN pro0 epi9 split1": 17076,  # q|k|v projection (RoPE epilogue)
-    "attn_fwd": 22100, "attn_rel_q": 30580, "attn_rel_kv": 19310, "rms_norm": 2375,
+    "attn_fwd": 22100, "attn_rel_q": 30582, "attn_rel_kv": 19310, "rms_norm": 2376,
 }.items()}
 # The same for the decode step's tied head (4 x 640 x 262144, skinny NT; `bench.py --decode-probe`,
 # profiles/decode_head_gemm_traffic.md): FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0 of the median dispatch.
