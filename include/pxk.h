@@ -98,7 +98,10 @@ enum {
     PXK_EPI_MUL_X_SPLIT = 8, /* r = X * acc, or Y + X * acc; then the epsilon split of the residual sum
                                 W = Z2 + Z3 whose relevance r is (lrp_residual_split, lrp_math.hpp:33-38):
                                 C = (Z2 / stab(W)) * r, C2 = (Z3 / stab(W)) * r. W must hold Z2 + Z3 as the
-                                forward computed it. Z stays the prologue's. */
+                                forward computed it. Z stays the prologue's. With c2_den given, C2 is
+                                that share divided by its consumer's stabilised denominator,
+                                C2 = ((Z3 / stab(W)) * r) / stab(c2_den + c2_den_bias[n]): the next
+                                relevance GEMM then reads it without the DIV_STAB prologue. */
     PXK_EPI_ROPE_FWD = 9,    /* C = acc; C2 = y = acc + bias[n] when a bias is given (else y = acc); and
                                 for columns n < rope_cols, C3 = y rotated pairwise at position m
                                 (rope_rotate, row_math.hpp:93-110; pairs inside each head_dim block) */
@@ -156,6 +159,8 @@ typedef struct pxk_gemm_desc {
     int64_t rope_cols;    /* ROPE_FWD: the leading columns (whole heads) that are rotated into C3 */
     int32_t gate_act;     /* SWIGLU_FWD's gate: 0 SiLU, 1 GeLU tanh (pointwise_math.hpp:32-36) */
     int32_t reserved;
+    pxk_operand c2_den;      /* MUL_X_SPLIT, ptr nullable: C2 is divided by stab(c2_den + c2_den_bias[n]) */
+    pxk_operand c2_den_bias; /* bias over n of that denominator (ld 0), ptr nullable */
 } pxk_gemm_desc;
 
 /* Bytes of workspace pxk_gemm needs for this descriptor (0 when it runs without split-K). */
@@ -558,6 +563,8 @@ typedef struct pxk_seed_head_desc {
     const float* s;
     float* r_a;
     float* r_b;
+    const float* b_den;      /* split, nullable: r_b is divided by stab(b_den + b_den_bias[j]), the */
+    const float* b_den_bias; /* denominator of the relevance GEMM that reads it (as PXK_EPI_MUL_X_SPLIT's c2_den) */
 } pxk_seed_head_desc;
 int pxk_lm_seed_head_relevance(const pxk_seed_head_desc* d, void* stream);
 

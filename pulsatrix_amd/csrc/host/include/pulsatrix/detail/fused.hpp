@@ -84,6 +84,11 @@ struct ResidualSplit {
     const float* s = nullptr;
     float* r_a = nullptr;
     float* r_b = nullptr;
+    /** Nullable: r_b is written divided by stab(b_den + b_den_bias[n]), the stabilised denominator
+     *  of the epsilon-rule GEMM that reads r_b next, which then runs without its DIV_STAB prologue.
+     *  Laid out like r_b; only epsilon-rule producers (GEMM epilogues, the seeded head) honour it. */
+    const float* b_den = nullptr;
+    const float* b_den_bias = nullptr;
     [[nodiscard]] bool requested() const noexcept { return r_a != nullptr; }
 };
 
@@ -97,6 +102,10 @@ inline void apply_split(pxk_gemm_desc& d, const ResidualSplit& sp, int64_t ld, f
     d.z2 = mat(sp.a, ld);
     d.z3 = mat(sp.b, ld);
     d.w = mat(sp.s, ld);
+    if (sp.b_den) {
+        d.c2_den = mat(sp.b_den, ld);
+        if (sp.b_den_bias) d.c2_den_bias = mat(sp.b_den_bias, 0);
+    }
 }
 
 }  // namespace pulsatrix::detail

@@ -87,9 +87,14 @@ public:
     void replicate_forward(int64_t copies);
     /** @brief Sizes the buffers replicate_forward() repeats into for `n sequences of length l`, without computing. */
     void reserve_forward(int64_t n, int64_t l);
-    /** @brief Fused-path relevance; `add` (nullable) is summed into the input relevance. */
+    /** @brief Fused-path relevance; `add` (nullable) is summed into the input relevance. `divided`:
+     *         relevance_out already holds R / stab(z) of the output projection (a producer honoured
+     *         relevance_denominator()), so no prologue divides it. */
     const float* run_relevance(const float* relevance_out, const LRPRuleConfig& config, const float* add = nullptr,
-                               const detail::ResidualSplit& split = {});
+                               const detail::ResidualSplit& split = {}, bool divided = false);
+    /** @brief The epsilon rule's denominator of the output projection for `config`: its pre-bias
+     *         output z and, under the bias-in-denominator rule, its bias (else nullptr). */
+    void relevance_denominator(const LRPRuleConfig& config, const float** den, const float** bias) const;
     /** @brief The attention output (after the output projection's bias) of the last forward. */
     [[nodiscard]] const float* output() const noexcept;
 

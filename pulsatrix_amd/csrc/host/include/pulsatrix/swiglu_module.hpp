@@ -32,8 +32,13 @@ public:
     void replicate_forward(int64_t copies);
     /** @brief Sizes the buffers replicate_forward() repeats into for `rows`, without computing. */
     void reserve_forward(int64_t rows);
+    /** @brief Fused-path relevance. `divided`: relevance_out already holds R / stab(z) of the down
+     *         projection (a producer honoured relevance_denominator()), so no prologue divides it. */
     const float* run_relevance(const float* relevance_out, const LRPRuleConfig& config, const float* add = nullptr,
-                               const detail::ResidualSplit& split = {});
+                               const detail::ResidualSplit& split = {}, bool divided = false);
+    /** @brief The epsilon rule's denominator of the down projection for `config`: its pre-bias
+     *         output z and, under the bias-in-denominator rule, its bias (else nullptr). */
+    void relevance_denominator(const LRPRuleConfig& config, const float** den, const float** bias) const;
     [[nodiscard]] const float* output() const noexcept;
 
 protected:

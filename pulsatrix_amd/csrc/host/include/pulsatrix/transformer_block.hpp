@@ -53,8 +53,10 @@ public:
     void reserve_forward(int64_t n, int64_t l);
     const float* run_relevance(const float* relevance_out, const LRPRuleConfig& config);
     /** @brief The epsilon split of this block's output y2 = y1 + mlp, for the GEMM that produces the
-     *         block's output relevance to perform into this block's buffers. Valid after run_forward. */
-    detail::ResidualSplit output_split();
+     *         block's output relevance to perform into this block's buffers. Valid after run_forward.
+     *         With `divide_for` (an epsilon rule), the MLP's share is requested divided by the down
+     *         projection's denominator: the producer must honour ResidualSplit::b_den. */
+    detail::ResidualSplit output_split(const LRPRuleConfig* divide_for = nullptr);
     /** @brief Relevance pass once the producer applied output_split(); `below` is the split the block
      *         underneath asks for (its output is this block's input), or none. Returns the input
      *         relevance when `below` is empty, else nullptr. */
@@ -85,6 +87,7 @@ private:
     const float* x_ = nullptr;
     Shape last_shape_;
     detail::DevBuf x_copy_, y1_, y2_, r_y1d_, r_ffn_, r_y1_, r_xd_, r_attn_, dec_y1_, dec_y2_, dec_n2_, dec_next_;
+    bool r_ffn_divided_ = false;  // the last output_split() asked for the MLP's share pre-divided
 };
 
 }  // namespace pulsatrix

@@ -400,14 +400,23 @@ void MultiHeadAttentionModule::run_attention_unfused(const float* q, int64_t ldq
     }
 }
 
+void MultiHeadAttentionModule::relevance_denominator(const LRPRuleConfig& config, const float** den,
+                                                     const float** bias) const {
+    *den = out_z_.data();
+    *bias = detail::rule_bias(out_proj_.bias_data(), config_.out_bias, config.epsilon_bias_in_denominator);
+}
+
 const float* MultiHeadAttentionModule::run_relevance(const float* relevance_out, const LRPRuleConfig& config,
-                                                     const float* add, const detail::ResidualSplit& split) {
+                                                     const float* add, const detail::ResidualSplit& split,
+                                                     bool divided) {
     if (x_ == nullptr)
         throw std::logic_error("MultiHeadAttentionModule::propagate_relevance: called before any forward()");
     detail::validate_rule(config, "LinearModule");  // the projections validate it (linear_module.cpp:342)
     // Gamma / AlphaBeta / ZBox reach the four projections; the bilinear, softmax and RoPE rules
     // read only epsilon (multihead_attention_module.cpp:404-485).
     const bool affine = detail::is_affine_rule(config);
+    if (affine && divided)
+        throw std::logic_error("MultiHeadAttentionModule::propagate_relevance: a divided relevance under a rule");
     const int64_t n = N_, l = L_, M = n * l, qd = H_ * D_, kvd = Hkv_ * D_, w3 = qd + 2 * kvd, grp = H_ / Hkv_;
     const int64_t LL = l * l;
     const bool causal = config_.causal, bid = config.epsilon_bias_in_denominator;
@@ -438,12 +447,14 @@ const float* MultiHeadAttentionModule::run_relevance(const float* relevance_out,
     } else {
         pxk_gemm_desc d = gemm_desc(M, qd, d_);
         d.trans_b = 1;
-        d.prologue = PXK_PRO_DIV_STAB;
         d.epilogue = PXK_EPI_SPV;
         d.eps = eps;
         d.a = mat(relevance_out, d_);
-        d.z = mat(out_z_.data(), d_);
-        if (const float* bo = detail::rule_bias(out_proj_.bias_data(), config_.out_bias, bid)) d.z_bias = mat(bo, 0);
+        if (!divided) {  // else the producer of relevance_out already divided it by stab(z + bias)
+            d.prologue = PXK_PRO_DIV_STAB;
+            d.z = mat(out_z_.data(), d_);
+            if (const float* bo = detail::rule_bias(out_proj_.bias_data(), config_.out_bias, bid)) d.z_bias = mat(bo, 0);
+        }
         d.b = mat(out_proj_.weight_data(), d_);
         d.c = mat(spv, qd);
         d.x = mat(ctx_.data(), qd);

@@ -104,25 +104,35 @@ const float* SwiGLUModule::run_forward(const float* x, int64_t rows, const float
     return dy;
 }
 
+void SwiGLUModule::relevance_denominator(const LRPRuleConfig& config, const float** den, const float** bias) const {
+    *den = down_z_.data();
+    *bias = detail::rule_bias(down_proj_.bias_data(), use_bias_, config.epsilon_bias_in_denominator);
+}
+
 const float* SwiGLUModule::run_relevance(const float* relevance_out, const LRPRuleConfig& config, const float* add,
-                                         const detail::ResidualSplit& split) {
+                                         const detail::ResidualSplit& split, bool divided) {
     if (x_ == nullptr) throw std::logic_error("SwiGLUModule::propagate_relevance: called before any forward()");
     detail::validate_rule(config, "LinearModule");  // the projections validate it (linear_module.cpp:342)
     const bool bid = config.epsilon_bias_in_denominator;
     const int64_t rows = rows_, f2 = 2 * F_;
     const float* gz = gu_z_.data();
     const float* gy = use_bias_ ? gu_y_.data() : gz;
-    if (detail::is_affine_rule(config)) return run_relevance_rule(relevance_out, config, add, split);
+    if (detail::is_affine_rule(config)) {
+        if (divided) throw std::logic_error("SwiGLUModule::propagate_relevance: a divided relevance under a rule");
+        return run_relevance_rule(relevance_out, config, add, split);
+    }
     float* g = g_.ensure(be_, rows * f2);
     {  // down projection's rule, Eq. 15's gate * up split and both projections' denominators
         pxk_gemm_desc d = gemm_desc(rows, F_, d_);
         d.trans_b = 1;
-        d.prologue = PXK_PRO_DIV_STAB;
         d.epilogue = PXK_EPI_SWIGLU_REL;
         d.eps = config.epsilon;
         d.a = mat(relevance_out, d_);
-        d.z = mat(down_z_.data(), d_);
-        if (const float* bd = detail::rule_bias(down_proj_.bias_data(), use_bias_, bid)) d.z_bias = mat(bd, 0);
+        if (!divided) {  // else the producer of relevance_out already divided it by stab(z + bias)
+            d.prologue = PXK_PRO_DIV_STAB;
+            d.z = mat(down_z_.data(), d_);
+            if (const float* bd = detail::rule_bias(down_proj_.bias_data(), use_bias_, bid)) d.z_bias = mat(bd, 0);
+        }
         d.b = mat(down_proj_.weight_data(), d_);
         d.c = mat(g, f2);
         d.c2 = mat(g + F_, f2);
@@ -339,9 +349,12 @@ const float* TransformerBlock::decode_step(const float* x, const float* x_normed
     return y2;
 }
 
-detail::ResidualSplit TransformerBlock::output_split() {
+detail::ResidualSplit TransformerBlock::output_split(const LRPRuleConfig* divide_for) {
     const int64_t n = N_ * L_ * d_;
-    return {y1_.data(), ffn_out_, y2_.data(), r_y1d_.ensure(be_, n), r_ffn_.ensure(be_, n)};
+    detail::ResidualSplit sp{y1_.data(), ffn_out_, y2_.data(), r_y1d_.ensure(be_, n), r_ffn_.ensure(be_, n)};
+    r_ffn_divided_ = divide_for != nullptr && !detail::is_affine_rule(*divide_for);
+    if (r_ffn_divided_) swiglu_.relevance_denominator(*divide_for, &sp.b_den, &sp.b_den_bias);
+    return sp;
 }
 
 const float* TransformerBlock::run_relevance_split(const LRPRuleConfig& config, const detail::ResidualSplit& below) {
@@ -352,8 +365,13 @@ const float* TransformerBlock::run_relevance_split(const LRPRuleConfig& config, 
     float* rxd = r_xd_.ensure(be_, n);
     float* rattn = r_attn_.ensure(be_, n);
     // The sandwich norms pass relevance unchanged (PostNormRelevance, transformer_block.cpp:92-95).
-    swiglu_.run_relevance(r_ffn_.data(), config, r_y1d_.data(), {x_, attn_out_, y1_.data(), rxd, rattn});
-    return mha_.run_relevance(rattn, config, rxd, below);
+    // Under an epsilon rule the MLP's last GEMM writes the attention's share already divided by
+    // the output projection's denominator, so that projection's relevance GEMM has no prologue.
+    detail::ResidualSplit up{x_, attn_out_, y1_.data(), rxd, rattn};
+    const bool divide = !detail::is_affine_rule(config);
+    if (divide) mha_.relevance_denominator(config, &up.b_den, &up.b_den_bias);
+    swiglu_.run_relevance(r_ffn_.data(), config, r_y1d_.data(), up, r_ffn_divided_);
+    return mha_.run_relevance(rattn, config, rxd, below, divide);
 }
 
 const float* TransformerBlock::run_relevance(const float* relevance_out, const LRPRuleConfig& config) {

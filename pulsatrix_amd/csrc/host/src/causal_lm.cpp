@@ -160,11 +160,11 @@ const float* CausalLM::run_relevance(const float* seed, const LRPRuleConfig& con
     // sum's relevance: the head's for the top block's output, each block's q/k/v GEMM for the
     // output of the block below.
     const size_t nl = layers_.size();
-    const detail::ResidualSplit top = nl > 0 ? layers_.back()->output_split() : detail::ResidualSplit{};
+    const detail::ResidualSplit top = nl > 0 ? layers_.back()->output_split(&config) : detail::ResidualSplit{};
     const float* r = tied_head_ ? tied_head_->run_relevance(seed, config, top)
                                 : lm_head_->run_relevance(seed, config, nullptr, top);
     for (size_t i = nl; i-- > 0;)
-        r = layers_[i]->run_relevance_split(config, i > 0 ? layers_[i - 1]->output_split() : detail::ResidualSplit{});
+        r = layers_[i]->run_relevance_split(config, i > 0 ? layers_[i - 1]->output_split(&config) : detail::ResidualSplit{});
     r_embed_ = r;
     return r;
 }
@@ -178,10 +178,10 @@ void CausalLM::explain_device(const float* ids, int64_t n, int64_t l, const LRPR
         // nonzero row per sequence: those rows alone, straight into the top block's residual split.
         detail::validate_rule(config, "CausalLM");
         const size_t nl = layers_.size();
-        const detail::ResidualSplit top = nl > 0 ? layers_.back()->output_split() : detail::ResidualSplit{};
+        const detail::ResidualSplit top = nl > 0 ? layers_.back()->output_split(&config) : detail::ResidualSplit{};
         const float* r = tied_head_->run_seeded_relevance(n, l, targets_in, targets, unit_seed, config, top);
         for (size_t i = nl; i-- > 0;)
-            r = layers_[i]->run_relevance_split(config, i > 0 ? layers_[i - 1]->output_split() : detail::ResidualSplit{});
+            r = layers_[i]->run_relevance_split(config, i > 0 ? layers_[i - 1]->output_split(&config) : detail::ResidualSplit{});
         r_embed_ = r;
         embed_.token_relevance(r, M, token_relevance);
         return;
@@ -244,7 +244,7 @@ void CausalLM::explain_staggered_rows(const float* ids, int64_t n, int64_t group
         MI355XBackend::check(pxk_lrp_residual_split(top.a, top.b, rtop, top.r_a, top.r_b, M * d, config.epsilon, st),
                              "CausalLM::explain_rows_device");
         for (size_t i = layers_.size(); i-- > 0;)
-            r = layers_[i]->run_relevance_split(config, i > 0 ? layers_[i - 1]->output_split() : detail::ResidualSplit{});
+            r = layers_[i]->run_relevance_split(config, i > 0 ? layers_[i - 1]->output_split(&config) : detail::ResidualSplit{});
     }
     r_embed_ = r;
     embed_.token_relevance(r, M, token_relevance);

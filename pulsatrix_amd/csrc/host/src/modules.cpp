@@ -353,6 +353,8 @@ const float* TiedLMHeadModule::run_seeded_relevance(int64_t n, int64_t l, const 
         d.s = split.s;
         d.r_a = split.r_a;
         d.r_b = split.r_b;
+        d.b_den = split.b_den;
+        d.b_den_bias = split.b_den_bias;
     } else {
         out = r_in_.ensure(be_, rows_ * D);
         d.r = out;

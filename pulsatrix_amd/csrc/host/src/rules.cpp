@@ -101,6 +101,8 @@ void AffineRule::run(MI355XBackend* be, const LRPRuleConfig& config, uint64_t ve
         d.c = mat(c, 2 * in);
         be->run_gemm(d);
     }
+    if (split.b_den)
+        throw std::logic_error("AffineRule: a rule's residual split cannot divide by the next layer's denominator");
     if (split.requested()) {
         MI355XBackend::check(pxk_lrp_rule_combine(rp.rule, p.x, p.ldx, c, 2 * in, p.add, rows, in, split.r_a, in,
                                                   split.a, split.b, split.s, split.r_b, config.epsilon, st),

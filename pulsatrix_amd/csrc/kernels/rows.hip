@@ -552,6 +552,8 @@ struct SeedHeadArgs {
     const float* s;
     float* r_a;
     float* r_b;
+    const float* b_den;
+    const float* b_den_bias;
     int64_t l, vocab, d;
     float eps;
     int unit;
@@ -575,7 +577,9 @@ __global__ void __launch_bounds__(kThreads) seed_head_rows_kernel(const SeedHead
             if (seeded) {
                 const float den = stab(g.s[off + j], g.eps);
                 g.r_a[off + j] = (g.a[off + j] / den) * r;
-                g.r_b[off + j] = (g.b[off + j] / den) * r;
+                float rb = (g.b[off + j] / den) * r;
+                if (g.b_den) rb = rb / stab(g.b_den_bias ? g.b_den[off + j] + g.b_den_bias[j] : g.b_den[off + j], g.eps);
+                g.r_b[off + j] = rb;
             } else {
                 g.r_a[off + j] = 0.0f;
                 g.r_b[off + j] = 0.0f;
@@ -854,8 +858,10 @@ int pxk_lm_seed_head_relevance(const pxk_seed_head_desc* d, void* stream) {
     PXK_LAUNCH(lm_seed_kernel, dim3(static_cast<unsigned>(d->n)), dim3(kSeedThreads), 0, S(stream), d->logits, d->l,
                d->vocab, d->targets_in ? 1 : 0, given, d->targets_out, static_cast<float*>(nullptr), d->unit);
     if (const int rc = launched("pxk_lm_seed_head_relevance (targets)")) return rc;
+    if ((d->b_den || d->b_den_bias) && (!split || !d->b_den))
+        return fail(PXK_ERR_INVALID, "pxk_lm_seed_head_relevance: b_den belongs to the split, its bias only with b_den");
     const SeedHeadArgs a{d->logits, d->x, d->e, d->targets_out, d->r, d->a, d->b, d->s, d->r_a, d->r_b,
-                         d->l, d->vocab, d->d, d->eps, d->unit};
+                         d->b_den, d->b_den_bias, d->l, d->vocab, d->d, d->eps, d->unit};
     PXK_LAUNCH(seed_head_rows_kernel, dim3(static_cast<unsigned>(d->n * d->l)), dim3(kThreads), 0, S(stream), a);
     return launched("pxk_lm_seed_head_relevance");
 }

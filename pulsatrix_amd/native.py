@@ -35,7 +35,8 @@ class GemmDesc(ctypes.Structure):
                 ("e_bias", Operand), ("e_bias2", Operand),
                 ("cos_t", c_vp), ("sin_t", c_vp), ("head_dim", c_i64), ("rope_half", ctypes.c_int32),
                 ("tile", ctypes.c_int32), ("workspace", c_vp), ("workspace_bytes", ctypes.c_size_t),
-                ("rope_cols", c_i64), ("gate_act", ctypes.c_int32), ("reserved", ctypes.c_int32)]
+                ("rope_cols", c_i64), ("gate_act", ctypes.c_int32), ("reserved", ctypes.c_int32),
+                ("c2_den", Operand), ("c2_den_bias", Operand)]
 
 
 CAUSAL_NONE, CAUSAL_TRI, CAUSAL_K_LE_M, CAUSAL_K_GE_M = 0, 1, 2, 3

@@ -26,6 +26,7 @@ COMBOS = [
     (1, 0, N.PRO_NONE, N.EPI_VALUE_REL), (0, 1, N.PRO_DIV_STAB, N.EPI_SWIGLU_REL),
     (0, 1, N.PRO_NONE, N.EPI_MUL_X_SPLIT), (0, 0, N.PRO_DIV_STAB, N.EPI_MUL_X_SPLIT),
     (0, 1, N.PRO_DIV_STAB, N.EPI_MUL_X_SPLIT), (0, 0, N.PRO_NONE, N.EPI_ROPE_FWD),
+    (0, 1, N.PRO_NONE, N.EPI_SPV), (0, 1, N.PRO_NONE, N.EPI_SWIGLU_REL),
 ]
 TILES = [N.TILE_128x128, N.TILE_64x64, N.TILE_32x64, N.TILE_32x32, N.TILE_32x64_DIRECT, N.TILE_32x32_DIRECT,
          N.TILE_32x48_DIRECT]
@@ -189,6 +190,69 @@ def test_fused_gemm_on_every_tile(combo, tile, splits):
 
 @gpu
 @pytest.mark.parametrize("splits", [1, 3])
+@pytest.mark.parametrize("tile", TILES)
+@pytest.mark.parametrize("tb,pro,bias", [(1, N.PRO_NONE, True), (0, N.PRO_DIV_STAB, False), (1, N.PRO_DIV_STAB, True)])
+def test_split_share_divided_by_the_next_denominator(tb, pro, bias, tile, splits):
+    """MUL_X_SPLIT with c2_den: C2 = ((Z3 / stab(W)) r) / stab(c2_den + c2_den_bias[n]), the share the next
+    relevance GEMM then reads without its DIV_STAB prologue; C is the plain first share."""
+    m, n, k = 77, 128, 150
+    a, b = G.uniform((m, k), 1), G.uniform((n, k) if tb else (k, n), 2)
+    x, y, w = G.uniform((m, n), 3), G.uniform((m, n), 4), away((m, n), 5)
+    z2, z3, den, db = G.uniform((m, n), 7), G.uniform((m, n), 8), away((m, n), 9), G.uniform((n,), 10, -0.2, 0.2)
+    zp, zb = away((m, k), 12), G.uniform((k,), 13)
+    a64 = a.astype(np.float64)
+    if pro == N.PRO_DIV_STAB:
+        a64 = a64 / stab(zp.astype(np.float64) + zb)
+    acc = a64 @ (b.T if tb else b).astype(np.float64)
+    r = y + x * acc
+    want_c = (z2 / stab(w)) * r
+    want_c2 = (z3 / stab(w)) * r / stab(den + (db if bias else 0.0))
+    c, c2 = G.empty((m, n)), G.empty((m, n))
+    d = N.GemmDesc()
+    d.m, d.n, d.k, d.batch, d.inner, d.kgroups = m, n, k, 1, 1, 1
+    d.trans_b, d.prologue, d.epilogue, d.eps, d.tile = tb, pro, N.EPI_MUL_X_SPLIT, EPS, tile
+    d.a = N.operand(G.ptr(G.dev(a)).value, k)
+    d.b = N.operand(G.ptr(G.dev(b)).value, k if tb else n)
+    d.c, d.c2 = N.operand(G.ptr(c).value, n), N.operand(G.ptr(c2).value, n)
+    for key, v in (("x", x), ("y", y), ("w", w), ("z2", z2), ("z3", z3), ("c2_den", den)):
+        setattr(d, key, N.operand(G.ptr(G.dev(v)).value, n))
+    if bias:
+        d.c2_den_bias = N.operand(G.ptr(G.dev(db)).value, 0)
+    if pro == N.PRO_DIV_STAB:
+        d.z = N.operand(G.ptr(G.dev(zp)).value, k)
+        d.z_bias = N.operand(G.ptr(G.dev(zb)).value, 0)
+    rc = run(d, splits)
+    assert rc == 0, N.pxk().pxk_last_error()
+    G.assert_close(G.host(c), want_c, 2e-5, "tile %d splits %d first share" % (tile, splits))
+    G.assert_close(G.host(c2), want_c2, 2e-5, "tile %d splits %d divided second share" % (tile, splits))
+
+
+def skip_if_device_present():
+    """Placeholder-pointer rejection tests rely on host validation refusing the descriptor; where a
+    GPU is visible they are skipped, so a regression there can never launch on a placeholder."""
+    if N.host().pxa_device_count() > 0:
+        pytest.skip("a GPU is present: placeholder-pointer rejection tests run only without one")
+
+
+def test_split_denominator_only_with_the_split_epilogue():
+    """CPU-side: c2_den is refused on any other epilogue, and its bias without it; nothing is launched."""
+    skip_if_device_present()
+    d = N.GemmDesc()
+    d.m, d.n, d.k, d.batch, d.inner, d.kgroups = 8, 8, 8, 1, 1, 1
+    for key in ("a", "b", "c", "c2", "x", "w", "z2", "z3"):
+        setattr(d, key, N.operand(16, 8))  # never dereferenced: validation fails first
+    d.epilogue = N.EPI_MUL_X
+    d.c2_den = N.operand(16, 8)
+    assert N.pxk().pxk_gemm(ctypes.byref(d), None) == 1
+    assert b"c2_den" in N.pxk().pxk_last_error()
+    d.epilogue = N.EPI_MUL_X_SPLIT
+    d.c2_den = N.operand(None, 0)
+    d.c2_den_bias = N.operand(16, 0)
+    assert N.pxk().pxk_gemm(ctypes.byref(d), None) == 1
+
+
+@gpu
+@pytest.mark.parametrize("splits", [1, 3])
 @pytest.mark.parametrize("tile", [t for t in TILES if TILE_BN[t] % 64 == 0])
 def test_swiglu_gate_epilogue(tile, splits):
     """SWIGLU_FWD: B's columns alternate 32-wide gate and up blocks; C gets z as [gate | up] halves,
@@ -243,6 +307,7 @@ def test_rope_rule_epilogue_interleaved_and_half_pairs(half, tile):
 
 def test_rope_rule_rejects_heads_wider_than_the_tile():
     """CPU-side: a 64-wide head cannot be split across 32-wide tiles; nothing is launched."""
+    skip_if_device_present()
     d = N.GemmDesc()
     d.m, d.n, d.k, d.batch, d.inner, d.kgroups = 8, 128, 8, 1, 1, 1
     d.epilogue, d.tile, d.head_dim = N.EPI_ROPE_REL, N.TILE_32x32, 64
@@ -262,25 +327,32 @@ def gate_np(x, act):
 
 @gpu
 @pytest.mark.parametrize("act", [0, 1])
-@pytest.mark.parametrize("tile,splits", [(0, 0), (N.TILE_128x128, 1), (N.TILE_64x64, 3), (N.TILE_32x32_DIRECT, 1)])
-def test_swiglu_rel_recomputes_its_factors_without_biases(act, tile, splits):
+@pytest.mark.parametrize("pro", [N.PRO_DIV_STAB, N.PRO_NONE])
+@pytest.mark.parametrize("tile,splits", [(0, 0), (N.TILE_128x128, 1), (N.TILE_64x64, 3), (N.TILE_32x32_DIRECT, 1),
+                                         (N.TILE_32x48_DIRECT, 1), (N.TILE_32x32, 1)])
+def test_swiglu_rel_recomputes_its_factors_without_biases(act, pro, tile, splits):
     """SWIGLU_REL with X, Y and W omitted (no biases): gate_post = act(z_gate), up = z_up and hidden =
-    gate_post * up recomputed in the epilogue, against float64 numpy of the stored-operand form."""
+    gate_post * up recomputed in the epilogue, against float64 numpy of the stored-operand form; with
+    the DIV_STAB prologue, or on an A already divided (the fused path's pre-divided relevance)."""
     m, k, F = 77, 150, 96
     a, b = G.uniform((m, k), 1), G.uniform((F, k), 2)
     zd, zg, zu = away((m, k), 6), G.uniform((m, F), 7, -3, 3), G.uniform((m, F), 8, -3, 3)
     d = N.GemmDesc()
     d.m, d.n, d.k, d.batch, d.inner, d.kgroups = m, F, k, 1, 1, 1
-    d.trans_b, d.prologue, d.epilogue, d.eps, d.gate_act = 1, N.PRO_DIV_STAB, N.EPI_SWIGLU_REL, EPS, act
+    d.trans_b, d.prologue, d.epilogue, d.eps, d.gate_act = 1, pro, N.EPI_SWIGLU_REL, EPS, act
     c, c2 = G.empty((m, F)), G.empty((m, F))
+    if pro == N.PRO_NONE:
+        a = (a.astype(np.float64) / stab(zd)).astype(np.float32)
+        zd = np.ones_like(zd)
     d.a = N.operand(G.ptr(G.dev(a)).value, k)
-    d.z = N.operand(G.ptr(G.dev(zd)).value, k)
+    if pro == N.PRO_DIV_STAB:
+        d.z = N.operand(G.ptr(G.dev(zd)).value, k)
     d.b = N.operand(G.ptr(G.dev(b)).value, k)
     d.c, d.c2 = N.operand(G.ptr(c).value, F), N.operand(G.ptr(c2).value, F)
     d.z2, d.z3 = N.operand(G.ptr(G.dev(zg)).value, F), N.operand(G.ptr(G.dev(zu)).value, F)
     d.tile = tile
     assert run(d, splits) == 0, N.pxk().pxk_last_error()
-    acc = (a.astype(np.float64) / stab(zd)) @ b.astype(np.float64).T
+    acc = (a.astype(np.float64) / (stab(zd) if pro == N.PRO_DIV_STAB else 1.0)) @ b.astype(np.float64).T
     gp, up = gate_np(zg, act), zu.astype(np.float64)
     cc = gp * up
     rg = (cc / (2 * cc + EPS * np.where(cc >= 0, 1.0, -1.0))) * (gp * up * acc)
