@@ -1173,16 +1173,5 @@ constexpr int skinny_rows(int mb) { return mb == 4 ? 16 : (mb == 8 ? 16 : 8); }
             {splitk_reduce_kernel<64, EPI>, splitk_reduce_kernel<32, EPI>, splitk_reduce_kernel<16, EPI>}         \
     }
 
-const SkinnyEntry kSkinny[] = {
-    PXK_SKINNY_NN(PXK_EPI_STORE),
-    PXK_SKINNY_NN(PXK_EPI_STORE_BIAS),
-    PXK_SKINNY_NN(PXK_EPI_ADD_RESID),
-    PXK_SKINNY_NN(PXK_EPI_SWIGLU_FWD),
-    SkinnyEntry{1,
-                PXK_EPI_STORE,
-                {{skinny_nt_kernel<4, PXK_EPI_STORE>}, {skinny_nt_kernel<8, PXK_EPI_STORE>}, {skinny_nt_kernel<16, PXK_EPI_STORE>}},
-                {nullptr, nullptr, nullptr}},
-};
-
 }  // namespace
 }  // namespace pxk
