@@ -77,7 +77,15 @@ enum {
 
 enum {
     PXK_PRO_NONE = 0,
-    PXK_PRO_DIV_STAB = 1 /* A / (Z + bias[k] + eps * sign(Z + bias[k])), sign(0) = +1 (lrp_math.hpp:17) */
+    PXK_PRO_DIV_STAB = 1, /* A / (Z + bias[k] + eps * sign(Z + bias[k])), sign(0) = +1 (lrp_math.hpp:17) */
+    PXK_PRO_RMS = 2       /* A is the input x of an RMSNorm over its K columns (rms_norm_module.cpp:51-68;
+                             RMSNormForward, row_math.hpp) whose gamma the caller has folded into B
+                             (B[k][n] = gamma[k] W[k][n], pxk_scale_rows): the product is taken over the
+                             norm's output y[m][k] = gamma[k] x[m][k] / rms[m] with
+                             rms[m] = sqrt(mean_k x[m][k]^2 + norm_eps), computed as
+                             (sum_k x[m][k] B[k][n]) / rms[m]. A untransposed, no k-groups, causal range,
+                             split-K, z or z_bias; row_rms (nullable) receives rms, batch b at b * m + row.
+                             Replaces the norm's separate row kernel. */
 };
 
 enum {
@@ -161,6 +169,13 @@ typedef struct pxk_gemm_desc {
     int32_t reserved;
     pxk_operand c2_den;      /* MUL_X_SPLIT, ptr nullable: C2 is divided by stab(c2_den + c2_den_bias[n]) */
     pxk_operand c2_den_bias; /* bias over n of that denominator (ld 0), ptr nullable */
+    const float* x_rms;      /* MUL_X, MUL_X_SPLIT, nullable (with x_gamma): X holds an RMSNorm's input x and
+                                the epilogue reads y = x_gamma[n] * X[m][n] / x_rms[m] (the norm's output,
+                                as its row kernel computes it) in its place. Unbatched. */
+    const float* x_gamma;
+    float* row_rms;          /* PXK_PRO_RMS: receives rms[m] (nullable) */
+    float norm_eps;          /* PXK_PRO_RMS */
+    int32_t reserved2;
 } pxk_gemm_desc;
 
 /* Bytes of workspace pxk_gemm needs for this descriptor (0 when it runs without split-K). */
@@ -202,6 +217,10 @@ int pxk_mul(const float* a, const float* b, float* out, int64_t n, void* stream)
 int pxk_axpby(float alpha, const float* x, float beta, const float* y, float* out, int64_t n, void* stream);
 /* DeviceBackend::add_row_vector (:405) */
 int pxk_add_row_vector(const float* in, const float* row, float* out, int64_t rows, int64_t cols, void* stream);
+/* out[i][j] = in[i][j] * scale[i]: an RMSNorm's gamma folded into the (in x out) weight of the
+ * projection that reads the norm's output (PXK_PRO_RMS). No reference counterpart: the reference
+ * applies gamma in the norm (rms_norm_module.cpp:51-68). */
+int pxk_scale_rows(const float* in, const float* scale, float* out, int64_t rows, int64_t cols, void* stream);
 /* DeviceBackend::lrp_residual_split (:631), lrp_bilinear_elementwise (:635), lrp_stabilized_divide (:712) */
 int pxk_lrp_residual_split(const float* a, const float* b, const float* r, float* r_a, float* r_b, int64_t n,
                            float eps, void* stream);

@@ -78,9 +78,11 @@ public:
     [[nodiscard]] float score_scale() const;
 
     /** @brief Fused-path forward. With `resid`, the output projection's epilogue also writes
-     *         resid + attention output into `resid_out` (the block's first residual add). */
+     *         resid + attention output into `resid_out` (the block's first residual add). With
+     *         `norm`, x is that RMSNorm's input and the q/k/v GEMM applies the norm itself
+     *         (RMSNormModule::fold); the relevance pass then reads the norm's output the same way. */
     const float* run_forward(const float* x, int64_t n, int64_t l, const float* resid = nullptr,
-                             float* resid_out = nullptr);
+                             float* resid_out = nullptr, RMSNormModule* norm = nullptr);
     /** @brief After run_forward over n sequences: repeats every activation the relevance pass reads
      *         `copies` times in place, as if the forward had run over copies * n sequences that
      *         repeat the n (storage from an earlier pass at least that large). */
@@ -135,6 +137,11 @@ private:
     int64_t N_ = 0, L_ = 0;
     const float* x_ = nullptr;
     detail::DevBuf x_copy_, qkv_z_, qkv_y_, qk_norm_out_, qk_rot_, raw_, p_, ctx_, out_z_, out_y_;
+    RMSNormModule* norm_in_ = nullptr;  // the RMSNorm folded into the q/k/v GEMM by the last forward, if any
+    detail::DevBuf wqkv_g_;             // [Wq | Wk | Wv] with the folded norm's gamma on its rows
+    const RMSNormModule* wg_norm_ = nullptr;
+    uint64_t wg_version_ = ~uint64_t{0}, wg_packed_ = ~uint64_t{0};
+    const float* folded_weights(RMSNormModule* norm);
     detail::DevBuf spv_, ra_, g_, r_in_, rctx_;
     detail::DevBuf dec_z_, dec_y_, dec_qkn_, dec_q_, dec_ctx_, dec_oz_, dec_oy_, dec_ws_;
     detail::AffineRule out_rule_, qkv_rule_;

@@ -34,10 +34,21 @@ public:
     /** @brief The scale the forward applies: gamma, or offset + gamma computed on the device. */
     const float* effective_gamma();
     [[nodiscard]] float eps() const noexcept { return eps_; }
+    /** @brief Changes whenever the effective scale may have changed. */
+    [[nodiscard]] uint64_t version() const noexcept { return version_; }
     [[nodiscard]] int64_t num_features() const noexcept { return d_; }
 
     /** @brief Fused-path forward into a module-owned buffer. */
     const float* run_forward(const float* x, int64_t rows);
+    /** @brief Fused path with the norm folded into the GEMM that reads its output (PXK_PRO_RMS):
+     *         that GEMM normalises `rows` rows of its input itself and writes each row's rms into the
+     *         buffer returned here; the norm's output is not stored. */
+    float* fold(int64_t rows);
+    /** @brief After fold(): the norm's output of the input x the GEMM read, computed and stored now
+     *         (for the consumers that read it stored: the Gamma / AlphaBeta / ZBox rules). */
+    const float* materialize(const float* x);
+    /** @brief Each row's rms from the last forward or fold(). */
+    [[nodiscard]] const float* rms() const noexcept { return rms_.data(); }
     /** @brief After run_forward over n sequences: repeats every activation the relevance pass reads
      *         `copies` times in place, as if the forward had run over copies * n sequences that
      *         repeat the n (storage from an earlier pass at least that large). */
@@ -57,6 +68,7 @@ private:
     float offset_ = 0.0f;
     uint64_t version_ = 0, eff_version_ = ~uint64_t{0};
     int64_t rows_ = 0;
+    bool folded_ = false;  // the last forward was folded into a GEMM: out_ holds nothing of it
     detail::DevBuf out_, rms_, eff_;
 };
 

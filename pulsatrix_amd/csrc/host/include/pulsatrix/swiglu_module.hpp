@@ -12,6 +12,8 @@
 
 namespace pulsatrix {
 
+class RMSNormModule;
+
 enum class GatedActivation { Silu, GeluTanh };
 
 class SwiGLUModule : public Module {
@@ -25,7 +27,11 @@ public:
     [[nodiscard]] LinearModule& up_proj() { return up_proj_; }
     [[nodiscard]] LinearModule& down_proj() { return down_proj_; }
 
-    const float* run_forward(const float* x, int64_t rows, const float* resid = nullptr, float* resid_out = nullptr);
+    /** @brief Fused-path forward. With `norm`, x is that RMSNorm's input and the gate/up GEMM
+     *         applies the norm itself (RMSNormModule::fold); the relevance pass then reads the norm's
+     *         output the same way. */
+    const float* run_forward(const float* x, int64_t rows, const float* resid = nullptr, float* resid_out = nullptr,
+                             RMSNormModule* norm = nullptr);
     /** @brief After run_forward over n sequences: repeats every activation the relevance pass reads
      *         `copies` times in place, as if the forward had run over copies * n sequences that
      *         repeat the n (storage from an earlier pass at least that large). */
@@ -62,6 +68,11 @@ private:
     const float* x_ = nullptr;
     Shape last_shape_;
     detail::DevBuf x_copy_, gu_z_, gu_y_, gate_post_, hidden_, down_z_, down_y_, g_, r_in_;
+    RMSNormModule* norm_in_ = nullptr;  // the RMSNorm folded into the gate/up GEMM by the last forward, if any
+    detail::DevBuf wgu_g_;              // the gate/up GEMM's weight with the folded norm's gamma on its rows
+    const RMSNormModule* wg_norm_ = nullptr;
+    uint64_t wg_version_ = ~uint64_t{0}, wg_packed_ = ~uint64_t{0};
+    const float* folded_weights(RMSNormModule* norm);
     detail::AffineRule down_rule_, gate_up_rule_;
 };
 

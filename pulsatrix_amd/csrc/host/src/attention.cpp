@@ -2,6 +2,7 @@
 #include <cmath>
 #include <stdexcept>
 
+#include "pulsatrix/rms_norm_module.hpp"
 #include "pulsatrix/multihead_attention_module.hpp"
 
 namespace pulsatrix {
@@ -106,6 +107,22 @@ void MultiHeadAttentionModule::pack_weights() {
     packed_version_ = v;
 }
 
+// [Wq | Wk | Wv] with row k scaled by the norm's gamma[k]: x (Wq' | Wk' | Wv') / rms is the
+// projection of the norm's output gamma x / rms (PXK_PRO_RMS). Rebuilt when the projections or the
+// norm's scale change.
+const float* MultiHeadAttentionModule::folded_weights(RMSNormModule* norm) {
+    if (wg_norm_ != norm || wg_version_ != norm->version() || wg_packed_ != packed_version_ || wqkv_g_.size() == 0) {
+        const int64_t w3 = H_ * D_ + 2 * Hkv_ * D_;
+        float* w = wqkv_g_.ensure(be_, d_ * w3);
+        MI355XBackend::check(pxk_scale_rows(wqkv_.data(), norm->effective_gamma(), w, d_, w3, be_->stream()),
+                             "MultiHeadAttentionModule::forward");
+        wg_norm_ = norm;
+        wg_version_ = norm->version();
+        wg_packed_ = packed_version_;
+    }
+    return wqkv_g_.data();
+}
+
 void MultiHeadAttentionModule::ensure_tables(int64_t l) {
     // Position-major tables: the first l rows of a longer table are this length's table, so the
     // tables only grow (no host work when the length shrinks, as it does along a decode).
@@ -135,12 +152,13 @@ const float* MultiHeadAttentionModule::output() const noexcept {
 }
 
 const float* MultiHeadAttentionModule::run_forward(const float* x, int64_t n, int64_t l, const float* resid,
-                                                   float* resid_out) {
+                                                   float* resid_out, RMSNormModule* norm) {
     pack_weights();
     ensure_tables(l);
     N_ = n;
     L_ = l;
     x_ = x;
+    norm_in_ = norm;
     const int64_t M = n * l, qd = H_ * D_, kvd = Hkv_ * D_, w3 = qd + 2 * kvd, LL = l * l;
     const bool causal = config_.causal;
     void* st = be_->stream();
@@ -162,6 +180,12 @@ const float* MultiHeadAttentionModule::run_forward(const float* x, int64_t n, in
         d.a = mat(x, d_, l * d_);
         d.b = mat(wqkv_.data(), w3);
         d.c = mat(z, w3, l * w3);
+        if (norm) {  // the block's pre-norm applied by this GEMM: gamma in the weights, x / rms per row
+            d.prologue = PXK_PRO_RMS;
+            d.b = mat(folded_weights(norm), w3);
+            d.norm_eps = norm->eps();
+            d.row_rms = norm->fold(M);
+        }
         if (config_.qkv_bias) {
             d.epilogue = PXK_EPI_STORE_BIAS;
             d.c2 = mat(y, w3, l * w3);
@@ -562,7 +586,9 @@ const float* MultiHeadAttentionModule::run_relevance(const float* relevance_out,
                       {{q_proj_.weight_data(), qd, qd, false, qb ? q_proj_.bias_data() : nullptr},
                        {k_proj_.weight_data(), kvd, kvd, false, qb ? k_proj_.bias_data() : nullptr},
                        {v_proj_.weight_data(), kvd, kvd, false, qb ? v_proj_.bias_data() : nullptr}},
-                      {x_, d_, M, d_, z, w3, qb ? bqkv_.data() : nullptr, g, w3, w3, r_in, add}, split);
+                      {norm_in_ ? norm_in_->materialize(x_) : x_, d_, M, d_, z, w3, qb ? bqkv_.data() : nullptr, g,
+                       w3, w3, r_in, add},
+                      split);
     } else {
         pxk_gemm_desc d = gemm_desc(M, d_, w3);
         d.trans_b = 1;
@@ -571,6 +597,10 @@ const float* MultiHeadAttentionModule::run_relevance(const float* relevance_out,
         d.b = mat(wqkv_.data(), w3);
         d.c = mat(r_in, d_);
         d.x = mat(x_, d_);
+        if (norm_in_) {  // x_ is the folded norm's input: the epilogue forms its output from the rms
+            d.x_rms = norm_in_->rms();
+            d.x_gamma = norm_in_->effective_gamma();
+        }
         if (add) d.y = mat(add, d_);
         detail::apply_split(d, split, d_, eps);
         be_->run_gemm(d);

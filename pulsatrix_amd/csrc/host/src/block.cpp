@@ -1,6 +1,7 @@
 // SwiGLUModule and TransformerBlock on MI355XBackend.
 #include <stdexcept>
 
+#include "pulsatrix/rms_norm_module.hpp"
 #include "pulsatrix/swiglu_module.hpp"
 #include "pulsatrix/transformer_block.hpp"
 
@@ -46,12 +47,38 @@ void SwiGLUModule::pack_weights() {
     packed_version_ = v;
 }
 
+// The gate/up GEMM's weight (interleaved for the fused gate, else [Wgate | Wup]) with row k scaled
+// by the norm's gamma[k] (PXK_PRO_RMS). Rebuilt when the projections or the norm's scale change.
+const float* SwiGLUModule::folded_weights(RMSNormModule* norm) {
+    if (wg_norm_ != norm || wg_version_ != norm->version() || wg_packed_ != packed_version_ || wgu_g_.size() == 0) {
+        const int64_t f2 = 2 * F_;
+        float* w = wgu_g_.ensure(be_, d_ * f2);
+        MI355XBackend::check(pxk_scale_rows(fused_gate() ? wgu_il_.data() : wgu_.data(), norm->effective_gamma(), w,
+                                            d_, f2, be_->stream()),
+                             "SwiGLUModule::forward");
+        wg_norm_ = norm;
+        wg_version_ = norm->version();
+        wg_packed_ = packed_version_;
+    }
+    return wgu_g_.data();
+}
+
 const float* SwiGLUModule::output() const noexcept { return use_bias_ ? down_y_.data() : down_z_.data(); }
 
-const float* SwiGLUModule::run_forward(const float* x, int64_t rows, const float* resid, float* resid_out) {
+const float* SwiGLUModule::run_forward(const float* x, int64_t rows, const float* resid, float* resid_out,
+                                       RMSNormModule* norm) {
     pack_weights();
     x_ = x;
+    norm_in_ = norm;
     rows_ = rows;
+    // the block's pre-norm applied by the gate/up GEMM: gamma in the weights, x / rms per row
+    auto fold = [&](pxk_gemm_desc& d) {
+        if (!norm) return;
+        d.prologue = PXK_PRO_RMS;
+        d.b = mat(folded_weights(norm), 2 * F_);
+        d.norm_eps = norm->eps();
+        d.row_rms = norm->fold(rows);
+    };
     const int64_t f2 = 2 * F_;
     float* gz = gu_z_.ensure(be_, rows * f2);
     float* gy = gz;
@@ -66,6 +93,7 @@ const float* SwiGLUModule::run_forward(const float* x, int64_t rows, const float
         d.c3 = mat(gp, F_);
         d.epilogue = PXK_EPI_SWIGLU_FWD;
         d.gate_act = act_;
+        fold(d);
         be_->run_gemm(d);
     } else {  // gate and up projections in one GEMM, then the gate
         pxk_gemm_desc d = gemm_desc(rows, f2, d_);
@@ -78,6 +106,7 @@ const float* SwiGLUModule::run_forward(const float* x, int64_t rows, const float
             d.c2 = mat(gy, f2);
             d.e_bias = mat(bgu_.data(), 0);
         }
+        fold(d);
         be_->run_gemm(d);
         MI355XBackend::check(pxk_swiglu_forward(gy, f2, gp, h, rows, F_, act_, be_->stream()), "SwiGLUModule::forward");
     }
@@ -160,6 +189,10 @@ const float* SwiGLUModule::run_relevance(const float* relevance_out, const LRPRu
         d.b = mat(wgu_.data(), f2);
         d.c = mat(r_in, d_);
         d.x = mat(x_, d_);
+        if (norm_in_) {  // x_ is the folded norm's input: the epilogue forms its output from the rms
+            d.x_rms = norm_in_->rms();
+            d.x_gamma = norm_in_->effective_gamma();
+        }
         if (add) d.y = mat(add, d_);
         detail::apply_split(d, split, d_, config.epsilon);
         be_->run_gemm(d);
@@ -189,7 +222,9 @@ const float* SwiGLUModule::run_relevance_rule(const float* relevance_out, const 
     const float* bu = use_bias_ ? up_proj_.bias_data() : nullptr;
     gate_up_rule_.run(be_, config, gate_proj_.version() + up_proj_.version(),
                       {{gate_proj_.weight_data(), F_, F_, false, bg}, {up_proj_.weight_data(), F_, F_, false, bu}},
-                      {x_, d_, rows, d_, gz, f2, use_bias_ ? bgu_.data() : nullptr, rh, F_, F_, r_in, add}, split);
+                      {norm_in_ ? norm_in_->materialize(x_) : x_, d_, rows, d_, gz, f2, use_bias_ ? bgu_.data() : nullptr,
+                       rh, F_, F_, r_in, add},
+                      split);
     return split.requested() ? nullptr : r_in;
 }
 
@@ -254,18 +289,29 @@ const float* TransformerBlock::run_forward(const float* x, int64_t n, int64_t l)
     const int64_t M = n * l;
     float* y1 = y1_.ensure(be_, M * d_);
     float* y2 = y2_.ensure(be_, M * d_);
+    // Each pre-norm is applied by the projection GEMM that reads it (RMSNormModule::fold), except
+    // for a handful of rows, where the skinny kernels of the unfused path are faster.
+    const bool fold = M > 16;
     if (!post_attn_norm_) {
-        mha_.run_forward(norm1_.run_forward(x, M), n, l, x, y1);     // y1 = x + attn(norm1(x))
-        swiglu_.run_forward(norm2_.run_forward(y1, M), M, y1, y2);    // y2 = y1 + mlp(norm2(y1))
+        if (fold) {
+            mha_.run_forward(x, n, l, x, y1, &norm1_);          // y1 = x + attn(norm1(x))
+            swiglu_.run_forward(y1, M, y1, y2, &norm2_);        // y2 = y1 + mlp(norm2(y1))
+        } else {
+            mha_.run_forward(norm1_.run_forward(x, M), n, l, x, y1);
+            swiglu_.run_forward(norm2_.run_forward(y1, M), M, y1, y2);
+        }
         attn_out_ = mha_.output();
         ffn_out_ = swiglu_.output();
         return y2;
     }
     // Sandwich norms: y1 = x + post_attn_norm(attn(norm1(x))), y2 = y1 + post_mlp_norm(mlp(norm2(y1))).
     void* st = be_->stream();
-    attn_out_ = post_attn_norm_->run_forward(mha_.run_forward(norm1_.run_forward(x, M), n, l), M);
+    attn_out_ = post_attn_norm_->run_forward(
+        fold ? mha_.run_forward(x, n, l, nullptr, nullptr, &norm1_) : mha_.run_forward(norm1_.run_forward(x, M), n, l), M);
     MI355XBackend::check(pxk_add(x, attn_out_, y1, M * d_, st), "TransformerBlock::forward");
-    ffn_out_ = post_mlp_norm_->run_forward(swiglu_.run_forward(norm2_.run_forward(y1, M), M), M);
+    ffn_out_ = post_mlp_norm_->run_forward(
+        fold ? swiglu_.run_forward(y1, M, nullptr, nullptr, &norm2_) : swiglu_.run_forward(norm2_.run_forward(y1, M), M),
+        M);
     MI355XBackend::check(pxk_add(y1, ffn_out_, y2, M * d_, st), "TransformerBlock::forward");
     return y2;
 }

@@ -160,6 +160,7 @@ const float* RMSNormModule::effective_gamma() {
 
 const float* RMSNormModule::run_forward(const float* x, int64_t rows) {
     rows_ = rows;
+    folded_ = false;
     float* out = out_.ensure(be_, rows * d_);
     float* rms = rms_.ensure(be_, rows);
     const float* gamma = effective_gamma();
@@ -171,13 +172,33 @@ const float* RMSNormModule::run_forward(const float* x, int64_t rows) {
     return out;
 }
 
+float* RMSNormModule::fold(int64_t rows) {
+    rows_ = rows;
+    folded_ = true;
+    return rms_.ensure(be_, rows);
+}
+
+const float* RMSNormModule::materialize(const float* x) {
+    if (!folded_) return out_.data();
+    float* out = out_.ensure(be_, rows_ * d_);
+    const float* gamma = effective_gamma();
+    const int64_t rows = rows_, d = d_;
+    const float eps = eps_;
+    // The rms the folding GEMM wrote stays; the row kernel recomputes its own for the output.
+    be_->launch("rms_norm", "rows", 0.0, 8.0 * rows * d + 4.0 * d, "RMSNormModule::forward", [=](void* st) {
+        return pxk_rms_norm_forward(x, gamma, out, nullptr, rows, d, eps, st);
+    });
+    folded_ = false;
+    return out;
+}
+
 void RMSNormModule::reserve_forward(int64_t rows) {
     out_.ensure(be_, rows * d_);
     rms_.ensure(be_, rows);
 }
 
 void RMSNormModule::replicate_forward(int64_t copies) {
-    out_.repeat(be_, rows_ * d_, copies, "RMSNormModule::replicate_forward");
+    if (!folded_) out_.repeat(be_, rows_ * d_, copies, "RMSNormModule::replicate_forward");
     rms_.repeat(be_, rows_, copies, "RMSNormModule::replicate_forward");
     rows_ *= copies;
 }

@@ -255,6 +255,13 @@ __global__ void __launch_bounds__(kThreads) add_row_kernel(const float* in, cons
     for (int64_t i = blockIdx.x * kThreads + threadIdx.x; i < n; i += stride) out[i] = in[i] + row[i % cols];
 }
 
+// scale_rows: out[i][j] = in[i][j] * scale[i].
+__global__ void __launch_bounds__(kThreads) scale_rows_kernel(const float* in, const float* scale, float* out,
+                                                              int64_t rows, int64_t cols) {
+    const int64_t n = rows * cols, stride = static_cast<int64_t>(gridDim.x) * kThreads;
+    for (int64_t i = blockIdx.x * kThreads + threadIdx.x; i < n; i += stride) out[i] = in[i] * scale[i / cols];
+}
+
 // SwiGLU gate over a [gate | up] row block (swiglu_module.cpp:80-88).
 __global__ void __launch_bounds__(kThreads) swiglu_kernel(const float* gu, int64_t ld, float* gate_post, float* hidden,
                                                           int64_t rows, int64_t f, int act) {
@@ -410,6 +417,15 @@ int pxk_add_row_vector(const float* in, const float* row, float* out, int64_t ro
     PXK_LAUNCH(add_row_kernel, dim3(grid_for(rows * cols, kThreads)), dim3(kThreads), 0, S(stream), in, row,
                        out, rows, cols);
     return launched("pxk_add_row_vector");
+}
+
+int pxk_scale_rows(const float* in, const float* scale, float* out, int64_t rows, int64_t cols, void* stream) {
+    if (rows < 0 || cols < 0) return fail(PXK_ERR_INVALID, "pxk_scale_rows: negative size");
+    if (rows * cols == 0) return PXK_OK;
+    if (in == nullptr || scale == nullptr || out == nullptr) return fail(PXK_ERR_INVALID, "pxk_scale_rows: NULL operand");
+    PXK_LAUNCH(scale_rows_kernel, dim3(grid_for(rows * cols, kThreads)), dim3(kThreads), 0, S(stream), in, scale, out,
+               rows, cols);
+    return launched("pxk_scale_rows");
 }
 
 int pxk_lrp_residual_split(const float* a, const float* b, const float* r, float* r_a, float* r_b, int64_t n,

@@ -147,10 +147,16 @@ double estimate(const pxk_gemm_desc* d, const TileInfo& t, double tiles, double 
         // tiles run 10-25% slower than from LDS panels (measured; without the prologue they win).
         floor = 1.0;
         util *= 0.65;
+    } else if (t.direct && d->trans_b && waves_per_simd > 1.0) {
+        // The same fragment-shaped loads with two or more workgroups per CU: they saturate the
+        // vector memory path (a 512 x 1536 x 576 NT product runs 1.2-1.9 us faster on LDS panels).
+        util *= 0.75;
     }
     const double stage_us = std::max(floor, waves_per_simd * mfma_us / util);
     double us = 4.0 + per * stage_us;
-    if (splits > 1) us += 6.0 + 2.0 * splits * d->batch * d->m * d->n * 4.0 / 5.0e6;
+    // The reduction launch (its own latency floor) and the partials' round trip through HBM. At
+    // 512 x 576 x 3072 the unsplit direct tile beats split-K 4 with its reduce by about 1 us.
+    if (splits > 1) us += 7.5 + 2.0 * splits * d->batch * d->m * d->n * 4.0 / 5.0e6;
     return us;
 }
 
@@ -194,6 +200,15 @@ int plan(const pxk_gemm_desc* d, Plan* p) {
     if ((d->c2_den.ptr != nullptr || d->c2_den_bias.ptr != nullptr) &&
         (epi != PXK_EPI_MUL_X_SPLIT || d->c2_den.ptr == nullptr))
         return fail(PXK_ERR_INVALID, "pxk_gemm: c2_den (and its bias) belong to MUL_X_SPLIT, the bias only with c2_den");
+    if (d->prologue == PXK_PRO_RMS &&
+        (d->trans_a != 0 || d->kgroups != 1 || d->causal != PXK_CAUSAL_NONE || d->splits > 1 ||
+         d->z.ptr != nullptr || d->z_bias.ptr != nullptr || d->k <= 0 || !(d->norm_eps >= 0.0f)))
+        return fail(PXK_ERR_INVALID,
+                    "pxk_gemm: the RMS prologue takes an untransposed A without k-groups, causal range or split-K, "
+                    "gamma folded into B (no z or z_bias), k > 0 and norm_eps >= 0");
+    if ((d->x_rms != nullptr) != (d->x_gamma != nullptr) ||
+        (d->x_rms && ((epi != PXK_EPI_MUL_X && epi != PXK_EPI_MUL_X_SPLIT) || d->batch != 1)))
+        return fail(PXK_ERR_INVALID, "pxk_gemm: x_rms and x_gamma go together, on an unbatched MUL_X or MUL_X_SPLIT");
     if (d->prologue == PXK_PRO_DIV_STAB && d->z.ptr == nullptr)
         return fail(PXK_ERR_INVALID, "pxk_gemm: the DIV_STAB prologue needs Z");
     if (d->prologue == PXK_PRO_DIV_STAB && (epi == PXK_EPI_ROPE_REL || epi == PXK_EPI_VALUE_REL))
@@ -278,6 +293,7 @@ int plan(const pxk_gemm_desc* d, Plan* p) {
         if (big_only && tiles < 256.0) continue;
         for (int s = 1; s <= 64; s *= 2) {
             if (d->splits > 0 && s != 1) break;
+            if (d->prologue == PXK_PRO_RMS && s != 1) break;  // the rows' sums of squares need the whole K
             const int splits = d->splits > 0 ? d->splits : s;
             if (d->splits == 0 && s > 1 && (big_only || stages / s < 2.0)) break;
             const double us = estimate(d, ti, tiles, stages, splits);
@@ -367,6 +383,10 @@ extern "C" int pxk_gemm(const pxk_gemm_desc* d, void* stream) {
     g.eb2 = to_op(d->e_bias2);
     g.c2d = to_op(d->c2_den);
     g.c2db = to_op(d->c2_den_bias);
+    g.xr = d->x_rms;
+    g.xg = d->x_gamma;
+    g.row_rms = d->prologue == PXK_PRO_RMS ? d->row_rms : nullptr;
+    g.norm_eps = d->norm_eps;
     g.cos_t = d->cos_t;
     g.sin_t = d->sin_t;
     g.head_dim = d->head_dim;
@@ -383,6 +403,7 @@ extern "C" int pxk_gemm(const pxk_gemm_desc* d, void* stream) {
               vec_ok(d->x, d->n) && vec_ok(d->y, d->n) && vec_ok(d->w, d->n) && vec_ok(d->z2, d->n) &&
               vec_ok(d->z3, d->n) && vec_ok(d->e_bias, d->n) && vec_ok(d->e_bias2, d->n) &&
               vec_ok(d->c2_den, d->n) && vec_ok(d->c2_den_bias, d->n) &&
+              (d->x_gamma == nullptr || aligned16(d->x_gamma)) &&
               (d->epilogue == PXK_EPI_ROPE_REL || d->epilogue == PXK_EPI_VALUE_REL ? vec_ok(d->z, d->n) : true);
     g.tiles_m = static_cast<int>(p.tiles_m);
     g.tiles_n = static_cast<int>(p.tiles_n);

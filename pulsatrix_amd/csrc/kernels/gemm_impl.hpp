@@ -59,6 +59,10 @@ struct Args {
     float beta, eps;
     Op a, b, c, z, zb, c2, c3, x, y, w, z2, z3, eb, eb2;
     Op c2d, c2db;  // MUL_X_SPLIT: C2's denominator and its bias over n (nullable)
+    const float* xr;  // MUL_X, MUL_X_SPLIT: X is an RMSNorm's input, normalised by rms xr[m] and gamma xg[n]
+    const float* xg;
+    float* row_rms;  // PXK_PRO_RMS: each row's rms (nullable)
+    float norm_eps;
     const float* cos_t;
     const float* sin_t;
     int64_t head_dim, rope_cols;
@@ -128,8 +132,28 @@ __device__ __forceinline__ float* obase_w(const Op& o, int64_t b, int64_t inner)
 }
 
 constexpr int NT = 256;
-// Kernel-side prologue variants: PXK_PRO_NONE, PXK_PRO_DIV_STAB without a bias over k, and with one.
-constexpr int kProStabBias = 2;
+// Kernel-side prologue variants: PXK_PRO_NONE, PXK_PRO_DIV_STAB without a bias over k, with one
+// (kProStabBias), and PXK_PRO_RMS (the rows' sums of squares of A kept; gamma is in B).
+constexpr int kProStabBias = 3;
+static_assert(kProStabBias != PXK_PRO_NONE && kProStabBias != PXK_PRO_DIV_STAB && kProStabBias != PXK_PRO_RMS,
+              "internal prologue id collides with a public one");
+
+// The rms of an RMSNorm row from its sum of squares over K, as the row kernel computes it
+// (rms_norm_vec_kernel: sqrtf(ss / cols + eps)); the K-slice partials are added in slice order.
+__device__ __forceinline__ float rms_of(const float* rss, int parts, int stride, int row, int64_t K, float eps) {
+    float t = 0.0f;
+    for (int q = 0; q < parts; ++q) t += rss[q * stride + row];
+    return sqrtf(t / static_cast<float>(K) + eps);
+}
+
+// y of an RMSNorm rebuilt from its input x, gamma over the row and the row's rms, with the row
+// kernel's expression (gamma * x / rms): relevance epilogues read the norm's input this way.
+__device__ __forceinline__ f4 norm_x(f4 x, f4 gamma, float rms) {
+    f4 y;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) y[j] = gamma[j] * x[j] / rms;
+    return y;
+}
 
 // NS_: register sets of prefetched stages. Stage t + 1 .. t + NS are in flight while stage t is
 // on the MFMA pipe, so the short stages of the small tiles still cover a global load's latency.
@@ -258,7 +282,9 @@ __device__ void epilogue_rows(const float* Cs, int ldc, int64_t m0, int64_t n0, 
             }
             st4(C3 + m * g.c3.ld + n, ld4(X + m * g.x.ld + n, vec, cnt) + y, vec, cnt);
         } else if constexpr (EPI == PXK_EPI_MUL_X) {
-            f4 v = ld4(X + m * g.x.ld + n, vec, cnt) * acc;
+            f4 xv = ld4(X + m * g.x.ld + n, vec, cnt);
+            if (g.xr) xv = norm_x(xv, ld4(g.xg + n, vec, cnt), g.xr[m]);
+            f4 v = xv * acc;
             if (Y) v = ld4(Y + m * g.y.ld + n, vec, cnt) + v;
             st4(C + m * g.c.ld + n, v, vec, cnt);
         } else if constexpr (EPI == PXK_EPI_SWIGLU_FWD) {
@@ -303,7 +329,9 @@ __device__ void epilogue_rows(const float* Cs, int ldc, int64_t m0, int64_t n0, 
                 st4(C3 + m * g.c3.ld + n, out, vec, cnt);
             }
         } else if constexpr (EPI == PXK_EPI_MUL_X_SPLIT) {
-            f4 v = ld4(X + m * g.x.ld + n, vec, cnt) * acc;
+            f4 xv = ld4(X + m * g.x.ld + n, vec, cnt);
+            if (g.xr) xv = norm_x(xv, ld4(g.xg + n, vec, cnt), g.xr[m]);
+            f4 v = xv * acc;
             if (Y) v = ld4(Y + m * g.y.ld + n, vec, cnt) + v;
             const f4 sa = ld4(Z2 + m * g.z2.ld + n, vec, cnt), sb = ld4(Z3 + m * g.z3.ld + n, vec, cnt);
             const f4 sum = ld4(W + m * g.w.ld + n, vec, cnt);
@@ -412,11 +440,13 @@ __device__ void epilogue_rows(const float* Cs, int ldc, int64_t m0, int64_t n0, 
 template <int R, int BK, bool KC, int PRO, int T>
 struct PanelLoader {
     using P = Panel<R, BK, KC, T>;
-    static constexpr bool DS = PRO != PXK_PRO_NONE;
+    static constexpr bool RMS = PRO == PXK_PRO_RMS;  // A only, K-contiguous
+    static constexpr bool DS = PRO == PXK_PRO_DIV_STAB || PRO == kProStabBias;
     static constexpr bool HB = PRO == kProStabBias;
     f4 v[P::NV];
     f4 z[DS ? P::NV : 1];   // prologue denominators
     f4 zb[HB ? P::NV : 1];  // prologue bias over k
+    float ss[RMS ? P::NV : 1] = {};  // RMS: the sums of squares of this thread's share of its rows
 
     __device__ __forceinline__ static void coords(int idx, int64_t r0, int64_t k0, int64_t& r, int64_t& c) {
         if constexpr (KC) {
@@ -484,7 +514,9 @@ struct PanelLoader {
             // A element a is divided once per N tile that reads it, so the prologue multiplies by
             // v_rcp_f32 (within 1 ulp of 1/x) instead of the IEEE division sequence; |stab(z)| >= eps
             // keeps the operand normal.
-            if constexpr (HB) {
+            if constexpr (RMS) {
+                ss[i] += a[0] * a[0] + a[1] * a[1] + a[2] * a[2] + a[3] * a[3];
+            } else if constexpr (HB) {
 #pragma unroll
                 for (int j = 0; j < 4; ++j) a[j] = a[j] * __builtin_amdgcn_rcpf(stab(z[i][j] + zb[i][j], eps));
             } else if constexpr (DS) {
@@ -535,9 +567,13 @@ __device__ __forceinline__ void tile_of(const Args& g, int& tm, int& tn, int& tz
 // Each wave's accumulators (one partial tile per K slice) -> LDS, summed in slice order; then the
 // split-K partial store or the tile epilogue. smem holds KS * BM * (BN + 4) floats and no wave
 // still reads it.
+// With `rss` (PXK_PRO_RMS: `parts` partial sums of squares per tile row, `parts` x BM floats in LDS,
+// written before the call), every accumulator row is divided by its rms and the tile in the first
+// N column writes the rows' rms to g.row_rms.
 template <class C, int EPI>
 __device__ __forceinline__ void finish_tile(f4 (&acc)[C::TM][C::TN], float* smem, int ks, int wm, int wn, int lane,
-                                            int tid, int64_t m0, int64_t n0, int64_t split, int64_t b, const Args& g) {
+                                            int tid, int64_t m0, int64_t n0, int64_t split, int64_t b, const Args& g,
+                                            const float* rss = nullptr, int parts = 0) {
     constexpr int BM = C::BM, BN = C::BN, TM = C::TM, TN = C::TN, LDC = C::LDC, PART = BM * LDC;
     float* Cp = smem + ks * PART;
 #pragma unroll
@@ -548,14 +584,21 @@ __device__ __forceinline__ void finish_tile(f4 (&acc)[C::TM][C::TN], float* smem
             for (int r = 0; r < 4; ++r)
                 Cp[(wm + 16 * i + 4 * (lane >> 4) + r) * LDC + wn + 16 * j + (lane & 15)] = acc[i][j][r];
     __syncthreads();
-    if constexpr (C::KS > 1) {  // sum the K-slice partials in slice order
+    if (C::KS > 1 || rss) {  // sum the K-slice partials in slice order; under PXK_PRO_RMS divide by the rms
         for (int it = tid; it < BM * (BN / 4); it += C::NT) {
-            const int off = (it / (BN / 4)) * LDC + 4 * (it % (BN / 4));
+            const int row = it / (BN / 4), off = row * LDC + 4 * (it % (BN / 4));
             f4 v = *reinterpret_cast<const f4*>(smem + off);
 #pragma unroll
             for (int q = 1; q < C::KS; ++q) v += *reinterpret_cast<const f4*>(smem + q * PART + off);
+            if (rss) {
+                const float r = rms_of(rss, parts, BM, row, g.K, g.norm_eps);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) v[j] = v[j] / r;
+            }
             *reinterpret_cast<f4*>(smem + off) = v;
         }
+        if (rss && n0 == 0 && g.row_rms && tid < BM && m0 + tid < g.M)
+            g.row_rms[b * g.M + m0 + tid] = rms_of(rss, parts, BM, tid, g.K, g.norm_eps);
         __syncthreads();
     }
     if (g.splits > 1) {  // raw partial tile -> workspace [split][batch][M][N]
@@ -580,6 +623,7 @@ __global__ void __launch_bounds__(C::NT) gemm_kernel(const Args g) {
     using PA = typename L::PA;
     using PB = typename L::PB;
     __shared__ __attribute__((aligned(16))) float smem[L::SIZE];
+    __shared__ float s_rss[PRO == PXK_PRO_RMS ? BM : 1];  // PXK_PRO_RMS: each tile row's sum of squares
 
     int tm, tn, tz;
     tile_of(g, tm, tn, tz);
@@ -613,8 +657,9 @@ __global__ void __launch_bounds__(C::NT) gemm_kernel(const Args g) {
     int64_t lt = 0, grp = nkb > 0 ? t0 / nkb : 0, kb = nkb > 0 ? t0 % nkb : 0;  // 32-bit division
     const float* A = obase(g.a, b, g.inner, grp);
     const float* B = obase(g.b, b, g.inner, grp);
-    const float* Z = PRO != PXK_PRO_NONE ? obase(g.z, b, g.inner, grp) : nullptr;
-    const float* ZB = PRO == kProStabBias ? obase(g.zb, b, g.inner, grp) : nullptr;
+    constexpr bool kZ = PRO == PXK_PRO_DIV_STAB || PRO == kProStabBias, kZB = PRO == kProStabBias;
+    const float* Z = kZ ? obase(g.z, b, g.inner, grp) : nullptr;
+    const float* ZB = kZB ? obase(g.zb, b, g.inner, grp) : nullptr;
     auto advance = [&]() {
         ++lt;
         if (++kb == nkb) {  // next k-group: rebase the operands
@@ -622,8 +667,8 @@ __global__ void __launch_bounds__(C::NT) gemm_kernel(const Args g) {
             ++grp;
             A = obase(g.a, b, g.inner, grp);
             B = obase(g.b, b, g.inner, grp);
-            if constexpr (PRO != PXK_PRO_NONE) Z = obase(g.z, b, g.inner, grp);
-            if constexpr (PRO == kProStabBias) ZB = obase(g.zb, b, g.inner, grp);
+            if constexpr (kZ) Z = obase(g.z, b, g.inner, grp);
+            if constexpr (kZB) ZB = obase(g.zb, b, g.inner, grp);
         }
     };
     auto commit = [&](auto S, int64_t t) {  // register set S holds stage t -> LDS buffer t % 2
@@ -712,8 +757,20 @@ __global__ void __launch_bounds__(C::NT) gemm_kernel(const Args g) {
         }
     }
 
+    if constexpr (PRO == PXK_PRO_RMS) {
+        // Each A element was committed once, by the thread that loaded it; the BK / 4 consecutive
+        // threads that share a row add their sums (lanes of one wave), one of them writes it.
+        static_for<PA::NV>([&](auto I) {
+            float v = 0.0f;
+            static_for<NS>([&](auto S) { v += la[S.value].ss[I.value]; });
+#pragma unroll
+            for (int o = 1; o < BK / 4; o <<= 1) v += __shfl_xor(v, o, 64);
+            const int idx = tid + I.value * C::NT;
+            if (idx % (BK / 4) == 0) s_rss[idx / (BK / 4)] = v;
+        });
+    }
     // The loop ended on a barrier: LDS is free for the partial tiles.
-    finish_tile<C, EPI>(acc, smem, ks, wm, wn, lane, tid, m0, n0, split, b, g);
+    finish_tile<C, EPI>(acc, smem, ks, wm, wn, lane, tid, m0, n0, split, b, g, PRO == PXK_PRO_RMS ? s_rss : nullptr, 1);
 }
 
 // ---- direct-load variant of the K-sliced tiles ---------------------------------------------------
@@ -725,7 +782,8 @@ __global__ void __launch_bounds__(C::NT) gemm_kernel(const Args g) {
 // reloaded (unused), so no branch surrounds a load. LDS is used once, to merge the four slices.
 template <class C, bool TA, bool TB, int PRO>
 struct DirectChunk {
-    static constexpr bool DS = PRO != PXK_PRO_NONE, HB = PRO == kProStabBias;
+    static constexpr bool RMS = PRO == PXK_PRO_RMS;
+    static constexpr bool DS = PRO == PXK_PRO_DIV_STAB || PRO == kProStabBias, HB = PRO == kProStabBias;
     f4 a[C::TM], b[C::TN];
     f4 z[DS ? C::TM : 1];
     f4 zb;  // bias over k, the same for every A row
@@ -792,8 +850,13 @@ struct DirectChunk {
         }
     }
 
-    __device__ __forceinline__ void mma(f4 (&acc)[C::TM][C::TN], float eps) {
-        if constexpr (DS) {
+    __device__ __forceinline__ void mma(f4 (&acc)[C::TM][C::TN], float eps, float (&ss)[C::TM]) {
+        if constexpr (RMS) {
+#pragma unroll
+            for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+                for (int s = 0; s < 4; ++s) ss[i] += a[i][s] * a[i][s];
+        } else if constexpr (DS) {
 #pragma unroll
             for (int i = 0; i < C::TM; ++i)
 #pragma unroll
@@ -817,6 +880,7 @@ __global__ void __launch_bounds__(C::NT) gemm_direct_kernel(const Args g) {
     static_assert(C::WM == 1 && C::WN == 1, "direct loads: every wave owns the whole tile");
     constexpr int BM = C::BM, BN = C::BN, TM = C::TM, TN = C::TN, KS = C::KS, PF = 3;
     __shared__ __attribute__((aligned(16))) float smem[KS * BM * C::LDC];
+    __shared__ float s_rss[PRO == PXK_PRO_RMS ? KS * BM : 1];  // PXK_PRO_RMS: per K slice, each row's sum of squares
 
     int tm, tn, tz;
     tile_of(g, tm, tn, tz);
@@ -840,13 +904,15 @@ __global__ void __launch_bounds__(C::NT) gemm_direct_kernel(const Args g) {
     for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
+    float ss[TM] = {};  // PXK_PRO_RMS: this lane's sums of squares of rows 16 i + lane % 16
 
     // Cursor over this wave's chunks: (grp, kk) of flattened chunk `first + KS * u`.
     int grp = nch > 0 ? first / nch : 0, kk = nch > 0 ? first % nch : 0, lu = 0;
     const float* A = obase(g.a, b, g.inner, grp);
     const float* B = obase(g.b, b, g.inner, grp);
-    const float* Z = PRO != PXK_PRO_NONE ? obase(g.z, b, g.inner, grp) : nullptr;
-    const float* ZB = PRO == kProStabBias ? obase(g.zb, b, g.inner, grp) : nullptr;
+    constexpr bool kZ = PRO == PXK_PRO_DIV_STAB || PRO == kProStabBias, kZB = PRO == kProStabBias;
+    const float* Z = kZ ? obase(g.z, b, g.inner, grp) : nullptr;
+    const float* ZB = kZB ? obase(g.zb, b, g.inner, grp) : nullptr;
     auto advance = [&]() {  // to this wave's next chunk
         ++lu;
         kk += KS;
@@ -859,8 +925,8 @@ __global__ void __launch_bounds__(C::NT) gemm_direct_kernel(const Args g) {
         if (moved) {
             A = obase(g.a, b, g.inner, grp);
             B = obase(g.b, b, g.inner, grp);
-            if constexpr (PRO != PXK_PRO_NONE) Z = obase(g.z, b, g.inner, grp);
-            if constexpr (PRO == kProStabBias) ZB = obase(g.zb, b, g.inner, grp);
+            if constexpr (kZ) Z = obase(g.z, b, g.inner, grp);
+            if constexpr (kZB) ZB = obase(g.zb, b, g.inner, grp);
         }
     };
     const bool interior = m0 + BM <= g.M && n0 + BN <= g.N && k_lo + 16 * static_cast<int64_t>(nch) <= g.K &&
@@ -875,7 +941,7 @@ __global__ void __launch_bounds__(C::NT) gemm_direct_kernel(const Args g) {
             static_for<PF>([&](auto U) { load(U); });
             for (int u0 = 0; u0 < nw; u0 += PF) {
                 static_for<PF>([&](auto U) {
-                    if (u0 + U.value < nw) ch[U.value].mma(acc, g.eps);
+                    if (u0 + U.value < nw) ch[U.value].mma(acc, g.eps, ss);
                     load(U);  // chunk u0 + U + PF (or the last one again)
                 });
             }
@@ -883,12 +949,23 @@ __global__ void __launch_bounds__(C::NT) gemm_direct_kernel(const Args g) {
             DirectChunk<C, TA, TB, PRO> ch;
             for (int u = 0; u < nw; ++u) {
                 ch.load_guarded(g, A, Z, ZB, B, m0, n0, k_lo + 16 * kk, lane);
-                ch.mma(acc, g.eps);
+                ch.mma(acc, g.eps, ss);
                 if (u + 1 < nw) advance();
             }
         }
     }
-    finish_tile<C, EPI>(acc, smem, ks, 0, 0, lane, tid, m0, n0, split, b, g);
+    if constexpr (PRO == PXK_PRO_RMS) {
+        // Lane (c, g) summed rows 16 i + c over its K values; the four lane groups, then (in
+        // finish_tile) the K slices in slice order.
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+            float v = ss[i];
+            v += __shfl_xor(v, 16, 64);
+            v += __shfl_xor(v, 32, 64);
+            if (lane < 16) s_rss[ks * BM + 16 * i + lane] = v;
+        }
+    }
+    finish_tile<C, EPI>(acc, smem, ks, 0, 0, lane, tid, m0, n0, split, b, g, PRO == PXK_PRO_RMS ? s_rss : nullptr, KS);
 }
 
 // Sums the split partials of a slab of rows in split order and runs the tile epilogue. One
@@ -913,7 +990,8 @@ __global__ void __launch_bounds__(NT) splitk_reduce_kernel(const Args g) {
         const bool vp = (g.N % 4) == 0 && cnt == 4, ve = g.vec_e && cnt == 4;
         const int64_t inner = g.inner;
         const float* Y = g.y.p ? obase(g.y, b, inner, 0) + m * g.y.ld + n : nullptr;
-        const f4 x = ld4(obase(g.x, b, inner, 0) + m * g.x.ld + n, ve, cnt);
+        f4 x = ld4(obase(g.x, b, inner, 0) + m * g.x.ld + n, ve, cnt);
+        if (g.xr) x = norm_x(x, ld4(g.xg + n, ve, cnt), g.xr[m]);
         const f4 sa = ld4(obase(g.z2, b, inner, 0) + m * g.z2.ld + n, ve, cnt);
         const f4 sb = ld4(obase(g.z3, b, inner, 0) + m * g.z3.ld + n, ve, cnt);
         const f4 sum = ld4(obase(g.w, b, inner, 0) + m * g.w.ld + n, ve, cnt);
@@ -1157,7 +1235,7 @@ __global__ void __launch_bounds__(NT) skinny_nt_kernel(const Args g) {
      gemm_direct_kernel<C32, TA, TB, P, EPI>, gemm_direct_kernel<C32x48, TA, TB, P, EPI>}
 #define PXK_GEMM_ENTRY(TA, TB, PRO, EPI)                                                                   \
     Entry {                                                                                                \
-        TA, TB, PRO, EPI, {PXK_KSET(TA, TB, PRO, EPI), PXK_KSET(TA, TB, (PRO ? kProStabBias : PRO), EPI)}, \
+        TA, TB, PRO, EPI, {PXK_KSET(TA, TB, PRO, EPI), PXK_KSET(TA, TB, (PRO == PXK_PRO_DIV_STAB ? kProStabBias : PRO), EPI)}, \
             {splitk_reduce_kernel<128, EPI>, splitk_reduce_kernel<64, EPI>, splitk_reduce_kernel<64, EPI>, \
              splitk_reduce_kernel<32, EPI>, splitk_reduce_kernel<64, EPI>, splitk_reduce_kernel<32, EPI>,   \
              splitk_reduce_kernel<48, EPI>},                                                                \

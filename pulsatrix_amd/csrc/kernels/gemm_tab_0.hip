@@ -10,6 +10,7 @@ const Entry kTable0[] = {
     PXK_GEMM_ENTRY(0, 0, PXK_PRO_NONE, PXK_EPI_MUL_X),
     PXK_GEMM_ENTRY(0, 0, PXK_PRO_NONE, PXK_EPI_ROPE_REL),
     PXK_GEMM_ENTRY(0, 0, PXK_PRO_NONE, PXK_EPI_ROPE_FWD),
+    PXK_GEMM_ENTRY(0, 0, PXK_PRO_RMS, PXK_EPI_STORE),
 };
 const int kTable0Size = static_cast<int>(sizeof(kTable0) / sizeof(kTable0[0]));
 

@@ -10,6 +10,7 @@ const Entry kTable2[] = {
     PXK_GEMM_ENTRY(1, 0, PXK_PRO_NONE, PXK_EPI_MUL_X),
     PXK_GEMM_ENTRY(0, 0, PXK_PRO_NONE, PXK_EPI_VALUE_REL),
     PXK_GEMM_ENTRY(0, 0, PXK_PRO_DIV_STAB, PXK_EPI_MUL_X_SPLIT),
+    PXK_GEMM_ENTRY(0, 0, PXK_PRO_RMS, PXK_EPI_ROPE_FWD),
 };
 const int kTable2Size = static_cast<int>(sizeof(kTable2) / sizeof(kTable2[0]));
 

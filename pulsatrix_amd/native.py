@@ -36,11 +36,12 @@ class GemmDesc(ctypes.Structure):
                 ("cos_t", c_vp), ("sin_t", c_vp), ("head_dim", c_i64), ("rope_half", ctypes.c_int32),
                 ("tile", ctypes.c_int32), ("workspace", c_vp), ("workspace_bytes", ctypes.c_size_t),
                 ("rope_cols", c_i64), ("gate_act", ctypes.c_int32), ("reserved", ctypes.c_int32),
-                ("c2_den", Operand), ("c2_den_bias", Operand)]
+                ("c2_den", Operand), ("c2_den_bias", Operand), ("x_rms", c_vp), ("x_gamma", c_vp), ("row_rms", c_vp),
+                ("norm_eps", ctypes.c_float), ("reserved2", ctypes.c_int32)]
 
 
 CAUSAL_NONE, CAUSAL_TRI, CAUSAL_K_LE_M, CAUSAL_K_GE_M = 0, 1, 2, 3
-PRO_NONE, PRO_DIV_STAB = 0, 1
+PRO_NONE, PRO_DIV_STAB, PRO_RMS = 0, 1, 2
 (EPI_STORE, EPI_STORE_BIAS, EPI_ADD_RESID, EPI_MUL_X, EPI_SPV, EPI_ROPE_REL, EPI_VALUE_REL,
  EPI_SWIGLU_REL, EPI_MUL_X_SPLIT, EPI_ROPE_FWD, EPI_SWIGLU_FWD) = range(11)
 TILE_AUTO, TILE_128x128, TILE_64x64, TILE_32x64, TILE_32x32, TILE_32x64_DIRECT, TILE_32x32_DIRECT, TILE_SKINNY = range(8)
@@ -57,6 +58,7 @@ PXK_SIGNATURES = {
     "pxk_mul": "pppip",
     "pxk_axpby": "fpfppip",
     "pxk_add_row_vector": "pppiip",
+    "pxk_scale_rows": "pppiip",
     "pxk_lrp_residual_split": "pppppifp",
     "pxk_lrp_bilinear_elementwise": "ppppifp",
     "pxk_lrp_stabilized_divide": "ppppifnp",

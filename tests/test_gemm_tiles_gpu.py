@@ -360,3 +360,137 @@ def test_swiglu_rel_recomputes_its_factors_without_biases(act, pro, tile, splits
     G.assert_close(G.host(c2), rg / stab(zu), 1e-4, "up share")
     d.e_bias = N.operand(G.ptr(G.dev(zg[0])).value, 0)
     assert N.pxk().pxk_gemm(ctypes.byref(d), G.stream()) == 1  # recomputing is only for bias-free layers
+
+
+def rms_norm_np(x, gamma, eps):
+    """RMSNormForward (row_math.hpp; rms_norm_module.cpp:51-68) in float64: gamma * x / rms."""
+    x = x.astype(np.float64)
+    rms = np.sqrt((x * x).mean(axis=1) + eps)
+    return gamma.astype(np.float64)[None, :] * x / rms[:, None], rms
+
+
+@gpu
+@pytest.mark.parametrize("tile", TILES)
+@pytest.mark.parametrize("epi", [N.EPI_STORE, N.EPI_STORE_BIAS, N.EPI_ROPE_FWD, N.EPI_SWIGLU_FWD])
+def test_rms_prologue_on_every_tile(tile, epi):
+    """PXK_PRO_RMS: A is an RMSNorm's input x and B the weight scaled by gamma; the product runs over
+    y = gamma x / rms (the norm's row kernel folded into the GEMM) and row_rms receives rms, against
+    float64 numpy of the unfolded y W."""
+    if epi == N.EPI_SWIGLU_FWD and TILE_BN[tile] % 64:
+        pytest.skip("SWIGLU_FWD needs 64-wide tile multiples")
+    D = 64 if TILE_BN[tile] >= 64 else 16
+    if epi == N.EPI_ROPE_FWD and TILE_BN[tile] < D:
+        pytest.skip("heads wider than the tile")
+    m, k, n, eps = 77, 148, 128, 1e-5
+    x, gamma = G.uniform((m, k), 41), G.uniform((k,), 42, 0.5, 1.5)
+    w = G.uniform((k, n), 43)
+    b = (gamma[:, None] * w).astype(np.float32)  # gamma folded into the weight, as pxk_scale_rows does
+    y, rms = rms_norm_np(x, gamma, eps)
+    acc = y @ w.astype(np.float64)
+    eb = G.uniform((n,), 44)
+    c, c2, c3 = G.empty((m, n)), G.empty((m, n)), G.empty((m, n))
+    rms_out = G.empty((m,))
+    d = N.GemmDesc()
+    d.m, d.n, d.k, d.batch, d.inner, d.kgroups = m, n, k, 1, 1, 1
+    d.prologue, d.epilogue, d.tile, d.norm_eps = N.PRO_RMS, epi, tile, eps
+    d.a, d.b = N.operand(G.ptr(G.dev(x)).value, k), N.operand(G.ptr(G.dev(b)).value, n)
+    d.row_rms = G.ptr(rms_out).value
+    d.c, d.c2, d.c3 = (N.operand(G.ptr(t).value, n) for t in (c, c2, c3))
+    want = {"c": acc}
+    if epi == N.EPI_STORE_BIAS:
+        d.e_bias = N.operand(G.ptr(G.dev(eb)).value, 0)
+        want["c2"] = acc + eb
+    if epi == N.EPI_ROPE_FWD:
+        cos, sin = rope_tables(m, D)
+        d.cos_t, d.sin_t = G.ptr(G.dev(cos)).value, G.ptr(G.dev(sin)).value
+        d.head_dim, d.rope_half, d.rope_cols = D, 1, n - D
+        want["c3"] = rotate(acc, cos, sin, D, True)
+    if epi == N.EPI_SWIGLU_FWD:
+        F = n // 2
+        hid, gp = G.empty((m, F)), G.empty((m, F))
+        d.c2, d.c3 = N.operand(G.ptr(hid).value, F), N.operand(G.ptr(gp).value, F)
+        blocks = np.arange(n).reshape(-1, 64)
+        zg, zu = acc[:, blocks[:, :32].ravel()], acc[:, blocks[:, 32:].ravel()]
+        want = {"c": np.concatenate([zg, zu], axis=1)}
+        gate = zg / (1.0 + np.exp(-zg))
+    assert N.pxk().pxk_gemm(ctypes.byref(d), G.stream()) == 0, N.pxk().pxk_last_error()
+    got = {"c": c, "c2": c2, "c3": c3}
+    for key, ref in want.items():
+        out = G.host(got[key])
+        if epi == N.EPI_ROPE_FWD and key == "c3":
+            out, ref = out[:, :n - D], ref[:, :n - D]
+        G.assert_close(out, ref, 2e-5, "tile %d output %s" % (tile, key))
+    if epi == N.EPI_SWIGLU_FWD:
+        G.assert_close(G.host(gp), gate, 2e-5, "gate_post")
+        G.assert_close(G.host(hid), gate * zu, 2e-5, "hidden")
+    G.assert_close(G.host(rms_out), rms, 1e-6, "rms")
+
+
+@gpu
+@pytest.mark.parametrize("splits", [1, 3])
+@pytest.mark.parametrize("tile", [0, N.TILE_32x48_DIRECT, N.TILE_32x32, N.TILE_64x64])
+@pytest.mark.parametrize("epi", [N.EPI_MUL_X, N.EPI_MUL_X_SPLIT])
+def test_relevance_epilogue_reads_a_norm_input(epi, tile, splits):
+    """MUL_X / MUL_X_SPLIT with x_rms and x_gamma: X holds the norm's input x, and the epilogue uses
+    y = gamma x / rms in its place (the value the norm's row kernel would have stored)."""
+    m, k, n, eps = 77, 150, 128, 1e-5
+    a, b = G.uniform((m, k), 51), G.uniform((n, k), 52)
+    x, gamma = G.uniform((m, n), 53), G.uniform((n,), 54, 0.5, 1.5)
+    y, rms = rms_norm_np(x, gamma, eps)
+    acc = a.astype(np.float64) @ b.astype(np.float64).T
+    r = y * acc
+    out, out2 = G.empty((m, n)), G.empty((m, n))
+    d = N.GemmDesc()
+    d.m, d.n, d.k, d.batch, d.inner, d.kgroups = m, n, k, 1, 1, 1
+    d.trans_b, d.epilogue, d.eps, d.tile = 1, epi, EPS, tile
+    d.a, d.b = N.operand(G.ptr(G.dev(a)).value, k), N.operand(G.ptr(G.dev(b)).value, k)
+    d.c, d.c2 = N.operand(G.ptr(out).value, n), N.operand(G.ptr(out2).value, n)
+    d.x = N.operand(G.ptr(G.dev(x)).value, n)
+    d.x_rms = G.ptr(G.dev(rms.astype(np.float32))).value
+    d.x_gamma = G.ptr(G.dev(gamma)).value
+    want = {"c": r}
+    if epi == N.EPI_MUL_X_SPLIT:
+        z2, z3, w = G.uniform((m, n), 55), G.uniform((m, n), 56), away((m, n), 57)
+        for key, v in (("z2", z2), ("z3", z3), ("w", w)):
+            setattr(d, key, N.operand(G.ptr(G.dev(v)).value, n))
+        want = {"c": (z2 / stab(w)) * r, "c2": (z3 / stab(w)) * r}
+    assert run(d, splits) == 0, N.pxk().pxk_last_error()
+    got = {"c": out, "c2": out2}
+    for key, ref in want.items():
+        G.assert_close(G.host(got[key]), ref, 2e-5, "tile %d splits %d %s" % (tile, splits, key))
+
+
+def test_rms_prologue_and_normed_input_reject_misuse():
+    """CPU-side: the RMS prologue takes gamma in B, an untransposed A, no k-groups and no split-K; x_rms and
+    x_gamma go together on MUL_X / MUL_X_SPLIT. Nothing is launched."""
+    skip_if_device_present()
+    lib = N.pxk()
+
+    def base():
+        d = N.GemmDesc()
+        d.m, d.n, d.k, d.batch, d.inner, d.kgroups = 8, 8, 8, 1, 1, 1
+        for key in ("a", "b", "c", "c2", "x", "w", "z2", "z3"):
+            setattr(d, key, N.operand(16, 8))  # never dereferenced: validation fails first
+        d.prologue, d.norm_eps = N.PRO_RMS, 1e-5
+        return d
+
+    d = base()
+    d.z_bias = N.operand(16, 0)  # gamma belongs in B
+    assert lib.pxk_gemm(ctypes.byref(d), None) == 1 and b"RMS prologue" in lib.pxk_last_error()
+    d = base()
+    d.norm_eps = -1.0
+    assert lib.pxk_gemm(ctypes.byref(d), None) == 1
+    d = base()
+    d.trans_a = 1
+    assert lib.pxk_gemm(ctypes.byref(d), None) == 1
+    d = base()
+    d.kgroups = 2
+    assert lib.pxk_gemm(ctypes.byref(d), None) == 1
+    d = base()
+    d.splits = 2
+    assert lib.pxk_gemm(ctypes.byref(d), None) == 1
+    d = base()
+    d.prologue, d.epilogue, d.x_rms = N.PRO_NONE, N.EPI_MUL_X, 16
+    assert lib.pxk_gemm(ctypes.byref(d), None) == 1 and b"x_gamma" in lib.pxk_last_error()
+    d.x_gamma, d.epilogue = 16, N.EPI_SPV
+    assert lib.pxk_gemm(ctypes.byref(d), None) == 1
