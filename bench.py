@@ -334,7 +334,8 @@ def op_sweep(torch, N, models):
     stream = torch.cuda.ExternalStream(raw_st)
     rows = []
     tile_name = {N.TILE_128x128: "128x128", N.TILE_64x64: "64x64", N.TILE_32x64: "32x64", N.TILE_32x32: "32x32",
-                 N.TILE_32x64_DIRECT: "32x64d", N.TILE_32x32_DIRECT: "32x32d", N.TILE_32x48_DIRECT: "32x48d"}
+                 N.TILE_32x64_DIRECT: "32x64d", N.TILE_32x32_DIRECT: "32x32d", N.TILE_32x48_DIRECT: "32x48d",
+                 N.TILE_32x48: "32x48"}
     for (M, K, Nn) in SWEEP_GEMMS:
         for orient in ("NN", "NT", "TN"):
             desc, keep = sweep_gemm(torch, N, M, K, Nn, orient)

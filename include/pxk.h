@@ -133,7 +133,8 @@ enum {
                              with 128-bit vector loads, A in LDS, 64-column tiles; NN split over K
                              (STORE, STORE_BIAS, ADD_RESID, SWIGLU_FWD), NT in one pass (STORE, K up
                              to about 4000 rows at m <= 4). PXK_TILE_AUTO picks it whenever it applies */
-    PXK_TILE_32x48_DIRECT = 8 /* as 32x64 direct, 48 columns: 192 workgroups over a 512 x 576 output */
+    PXK_TILE_32x48_DIRECT = 8, /* as 32x64 direct, 48 columns: 192 workgroups over a 512 x 576 output */
+    PXK_TILE_32x48 = 9        /* as 32x64, 48 columns */
 };
 
 typedef struct pxk_gemm_desc {

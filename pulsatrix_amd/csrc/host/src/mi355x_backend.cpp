@@ -144,10 +144,10 @@ void MI355XBackend::run_gemm(pxk_gemm_desc& d) {
     if (logging_) {
         int32_t tile = 0, splits = 0;
         check(pxk_gemm_plan(&d, &tile, &splits), "MI355XBackend gemm (plan)");
-        static const char* const kTile[] = {"auto",   "128x128", "64x64",  "32x64", "32x32",
-                                            "32x64d", "32x32d",  "skinny", "32x48d"};
+        static const char* const kTile[] = {"auto",   "128x128", "64x64",  "32x64",  "32x32",
+                                            "32x64d", "32x32d",  "skinny", "32x48d", "32x48"};
         char name[96];
-        std::snprintf(name, sizeof(name), "gemm %s %s%s pro%d epi%d split%d", kTile[tile >= 0 && tile <= 8 ? tile : 0],
+        std::snprintf(name, sizeof(name), "gemm %s %s%s pro%d epi%d split%d", kTile[tile >= 0 && tile <= 9 ? tile : 0],
                       d.trans_a ? "T" : "N", d.trans_b ? "T" : "N", d.prologue, d.epilogue, splits);
         // Algorithmic bytes: every operand once (A, B, the prologue's denominators, the
         // epilogue's inputs and outputs), none of the split-K partials or re-reads.

@@ -11,10 +11,15 @@ const Table kTables[] = {{kTable0, kTable0Size}, {kTable1, kTable1Size}, {kTable
 
 // Plan index <-> PXK_TILE_*: the MFMA tiles in table order, the skinny kernels after them.
 constexpr int kSkinnyTile = kTiles;
-int public_tile(int t) { return t < 6 ? t + 1 : (t == 6 ? PXK_TILE_32x48_DIRECT : PXK_TILE_SKINNY); }
+int public_tile(int t) {
+    if (t < 6) return t + 1;
+    if (t == 6) return PXK_TILE_32x48_DIRECT;
+    return t == 7 ? PXK_TILE_32x48 : PXK_TILE_SKINNY;
+}
 int plan_tile(int id) {  // -1: none
     if (id >= PXK_TILE_128x128 && id <= PXK_TILE_32x32_DIRECT) return id - 1;
     if (id == PXK_TILE_32x48_DIRECT) return 6;
+    if (id == PXK_TILE_32x48) return 7;
     return id == PXK_TILE_SKINNY ? kSkinnyTile : -1;
 }
 
@@ -43,6 +48,7 @@ const TileInfo kTileInfo[kTiles] = {
     {32, 64, 64, C32x64::NT, 4 * C32x64::KS * 32 * C32x64::LDC, 0.65, 0.55, true},
     {32, 32, 64, C32::NT, 4 * C32::KS * 32 * C32::LDC, 0.65, 0.5, true},
     {32, 48, 64, C32x48::NT, 4 * C32x48::KS * 32 * C32x48::LDC, 0.65, 0.55, true},
+    {32, 48, 64, C32x48::NT, smem_of<C32x48>(), 0.8, 0.55, false},
 };
 
 constexpr int kSkinnyMaxLds = 64 * 1024;

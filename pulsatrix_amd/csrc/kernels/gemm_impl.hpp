@@ -76,7 +76,7 @@ struct Args {
 
 using KernelFn = void (*)(const Args);
 
-constexpr int kTiles = 7;  // PXK_TILE_128x128 .. PXK_TILE_32x32_DIRECT, then PXK_TILE_32x48_DIRECT
+constexpr int kTiles = 8;  // PXK_TILE_128x128 .. PXK_TILE_32x32_DIRECT, PXK_TILE_32x48_DIRECT, PXK_TILE_32x48
 
 // One (transpose, prologue, epilogue) combination: its kernel on every tile shape, without and
 // with a prologue bias over k, and the split-K reduce for each tile width.
@@ -172,7 +172,7 @@ using C128 = Cfg<128, 128, 2, 2, 1, 1>;
 using C64 = Cfg<64, 64, 2, 2, 1, 3>;
 using C32x64 = Cfg<32, 64, 1, 1, 4, 2>;
 using C32 = Cfg<32, 32, 1, 1, 4, 3>;
-using C32x48 = Cfg<32, 48, 1, 1, 4, 2>;  // direct loads only: 192 workgroups over 512 x 576
+using C32x48 = Cfg<32, 48, 1, 1, 4, 2>;  // 192 workgroups over 512 x 576
 
 template <class F, int... Is>
 __device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, Is...>) {
@@ -1232,13 +1232,14 @@ __global__ void __launch_bounds__(NT) skinny_nt_kernel(const Args g) {
 #define PXK_KSET(TA, TB, P, EPI)                                                                    \
     {gemm_kernel<C128, TA, TB, P, EPI>, gemm_kernel<C64, TA, TB, P, EPI>, gemm_kernel<C32x64, TA, TB, P, EPI>, \
      gemm_kernel<C32, TA, TB, P, EPI>, gemm_direct_kernel<C32x64, TA, TB, P, EPI>,                         \
-     gemm_direct_kernel<C32, TA, TB, P, EPI>, gemm_direct_kernel<C32x48, TA, TB, P, EPI>}
+     gemm_direct_kernel<C32, TA, TB, P, EPI>, gemm_direct_kernel<C32x48, TA, TB, P, EPI>,                  \
+     gemm_kernel<C32x48, TA, TB, P, EPI>}
 #define PXK_GEMM_ENTRY(TA, TB, PRO, EPI)                                                                   \
     Entry {                                                                                                \
         TA, TB, PRO, EPI, {PXK_KSET(TA, TB, PRO, EPI), PXK_KSET(TA, TB, (PRO == PXK_PRO_DIV_STAB ? kProStabBias : PRO), EPI)}, \
             {splitk_reduce_kernel<128, EPI>, splitk_reduce_kernel<64, EPI>, splitk_reduce_kernel<64, EPI>, \
              splitk_reduce_kernel<32, EPI>, splitk_reduce_kernel<64, EPI>, splitk_reduce_kernel<32, EPI>,   \
-             splitk_reduce_kernel<48, EPI>},                                                                \
+             splitk_reduce_kernel<48, EPI>, splitk_reduce_kernel<48, EPI>},                                 \
     }
 
 constexpr int skinny_rows(int mb) { return mb == 4 ? 16 : (mb == 8 ? 16 : 8); }

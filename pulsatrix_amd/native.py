@@ -46,6 +46,7 @@ PRO_NONE, PRO_DIV_STAB, PRO_RMS = 0, 1, 2
  EPI_SWIGLU_REL, EPI_MUL_X_SPLIT, EPI_ROPE_FWD, EPI_SWIGLU_FWD) = range(11)
 TILE_AUTO, TILE_128x128, TILE_64x64, TILE_32x64, TILE_32x32, TILE_32x64_DIRECT, TILE_32x32_DIRECT, TILE_SKINNY = range(8)
 TILE_32x48_DIRECT = 8
+TILE_32x48 = 9
 
 # (name, restype, argtypes) of every pxk entry point; `p` = device pointer (void*), `i` = int64,
 # `f` = float, `n` = int, `s` = size_t.

@@ -29,9 +29,9 @@ COMBOS = [
     (0, 1, N.PRO_NONE, N.EPI_SPV), (0, 1, N.PRO_NONE, N.EPI_SWIGLU_REL),
 ]
 TILES = [N.TILE_128x128, N.TILE_64x64, N.TILE_32x64, N.TILE_32x32, N.TILE_32x64_DIRECT, N.TILE_32x32_DIRECT,
-         N.TILE_32x48_DIRECT]
+         N.TILE_32x48_DIRECT, N.TILE_32x48]
 TILE_BN = {N.TILE_128x128: 128, N.TILE_64x64: 64, N.TILE_32x64: 64, N.TILE_32x32: 32, N.TILE_32x64_DIRECT: 64,
-           N.TILE_32x32_DIRECT: 32, N.TILE_32x48_DIRECT: 48}
+           N.TILE_32x32_DIRECT: 32, N.TILE_32x48_DIRECT: 48, N.TILE_32x48: 48}
 EPS = 1e-6
 
 
