@@ -38,19 +38,25 @@ HBM_PEAK_GBS = 8000.0
 LXT_EPS = 1e-9
 
 # HBM bytes per launch of the step's kernels, by launch-log name: FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0
-# KiB (the factors a 256 MiB copy reads for the two counters) of the median dispatch, from rocprofv3
-# --pmc runs of this bench (profiles/explain_s512_step_counters.md). A launch's kernels add up (the
-# split-K GEMM and its reduce); the o and down projections share one name and are averaged. The
-# roofline line carries the figure of its kernel when that kernel was measured under this plan.
+# KiB (the factors a 256 MiB copy reads for the two counters), the median over a launch name's
+# launches, from rocprofv3 --pmc runs of this bench summarised by `bench.py --pmc-table`
+# (profiles/explain_s512_step_counters.md). A launch's kernels add up (the split-K GEMM and its
+# reduce); the o and down projections share one name. The roofline line carries the figure of its
+# kernel when that kernel was measured under this plan.
 STEP_KERNEL_TRAFFIC = {name: kib * 1024 for name, kib in {
-    "gemm 32x48d NT pro0 epi8 split4": 40358,  # gate|up relevance 24106 + its split-K reduce 16252
-    "gemm 32x48d NN pro0 epi2 split1": 24524,  # o and down projections (median of both)
-    "gemm 32x64 NN pro0 epi10 split1": 28732,  # gate|up projection (SwiGLU epilogue)
-    "gemm 32x32 NT pro1 epi7 split1": 34588,  # down relevance
-    "gemm 32x48d NT pro0 epi8 split1": 27844,  # q|k|v relevance (residual split)
-    "gemm 32x64 NT pro1 epi4 split1": 23280,  # o relevance
-    "gemm 32x64d NN pro0 epi9 split1": 17076,  # q|k|v projection (RoPE epilogue)
-    "attn_fwd": 22100, "attn_rel_q": 30582, "attn_rel_kv": 19310, "rms_norm": 2376,
+    "gemm 32x64d NN pro2 epi9 split1": 17082,  # q|k|v projection (norm folded, RoPE epilogue)
+    "attn_fwd": 22100,
+    "gemm 32x48d NN pro0 epi2 split1": 24536,  # o and down projections (median of both)
+    "gemm 32x64 NN pro2 epi10 split1": 28750,  # gate|up projection (norm folded, SwiGLU epilogue)
+    "gemm 128x128 NT pro0 epi0 split1": 241456,  # LM head forward
+    "head_seeded_relevance": 2554,
+    "gemm 32x48 NT pro0 epi7 split1": 25360,  # down relevance (SwiGLU rule epilogue)
+    "gemm 32x48 NT pro0 epi8 split4": 38780,  # gate|up relevance + its split-K reduce and residual split
+    "gemm 32x48d NT pro0 epi4 split1": 13688,  # o relevance (s_pv epilogue)
+    "attn_rel_q": 30580,
+    "attn_rel_kv": 19310,
+    "gemm 32x48d NT pro0 epi8 split1": 26540,  # q|k|v relevance (residual split)
+    "gemm 32x48d NT pro0 epi3 split1": 22428,  # q|k|v relevance of block 0
 }.items()}
 # The same for the decode step's tied head (4 x 640 x 262144, skinny NT; `bench.py --decode-probe`,
 # profiles/decode_head_gemm_traffic.md): FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0 of the median dispatch.
@@ -480,6 +486,68 @@ def decode_bench(args, torch, N, models):
     print(json.dumps(out), flush=True)
 
 
+def pmc_table(names_path, dbs):
+    """Per-launch counters of the step from rocprofv3 --pmc databases of `bench.py --steps 1
+    --warmup 1 --mode eager --profile-reps 1 --launch-names NAMES` (one counter group per run). That
+    run ends with one timed replay of the recorded step, so the last dispatches of each database are
+    that replay's, launch by launch as NAMES lists them (a launch dispatching two kernels, a split-K
+    GEMM and its reduce, adds both). Per launch name and counter: the median over its launches of the
+    counter summed over their dispatches. Derived columns where their counters are present: HBM MB =
+    (FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0) KiB (the factors a 256 MiB copy reads: bench.py
+    --kernel-probe); MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / 1024 SIMDs / (duration x 2.4 GHz); waves
+    per CU = SQ_WAVE_CYCLES x 4 / (duration x 2.4 GHz) / 256, with the launch's duration as that run
+    measured it (counter collection slows kernels by 10-15%)."""
+    import sqlite3
+    names = []
+    with open(names_path) as f:
+        for line in f:
+            name, disp = line.rstrip("\n").rsplit("\t", 1)
+            names.append((name, int(disp)))
+    need = sum(d for _, d in names)
+    per = {}  # counter -> {launch name: [value per launch]}; "duration ns" per database
+
+    def assign(counter, vals):
+        if len(vals) < need:
+            raise SystemExit("%d dispatches with %s, the step's replay needs %d" % (len(vals), counter, need))
+        tail, at = vals[len(vals) - need:], 0
+        table = per.setdefault(counter, {})
+        for name, d in names:
+            table.setdefault(name, []).append(sum(tail[at:at + d]))
+            at += d
+
+    for db in dbs:
+        c = sqlite3.connect(db)
+        rows = c.execute("select dispatch_id, counter_name, sum(counter_value), max(duration) from pmc_events "
+                         "group by dispatch_id, counter_name order by dispatch_id").fetchall()
+        counters = sorted({r[1] for r in rows})
+        for counter in counters:
+            assign(counter, [v for _, cn, v, _ in rows if cn == counter])
+        if "SQ_WAVE_CYCLES" in counters or "SQ_VALU_MFMA_BUSY_CYCLES" in counters:
+            assign("duration ns", [dur for _, cn, _, dur in rows if cn == counters[0]])
+    med = lambda name, counter: float(np.median(per[counter][name])) if name in per.get(counter, {}) else None
+    order = []
+    for n, _ in names:
+        if n not in order:
+            order.append(n)
+    counters = [k for k in sorted(per) if k != "duration ns"]
+    derived = []
+    if "FETCH_SIZE" in per and "WRITE_SIZE" in per:
+        derived.append(("HBM MB (F x 2 + W)", lambda n: (2.0 * med(n, "FETCH_SIZE") + med(n, "WRITE_SIZE")) * 1024 / 1e6))
+    if "duration ns" in per:
+        ghz = lambda n: med(n, "duration ns") * 2.4
+        if "SQ_VALU_MFMA_BUSY_CYCLES" in per:
+            derived.append(("MFMA busy %", lambda n: 100.0 * med(n, "SQ_VALU_MFMA_BUSY_CYCLES") / 1024 / ghz(n)))
+        if "SQ_WAVE_CYCLES" in per:
+            derived.append(("waves / CU", lambda n: med(n, "SQ_WAVE_CYCLES") * 4 / ghz(n) / 256))
+        counters = ["duration ns"] + counters
+    print("| launch | per step | " + " | ".join(counters + [d for d, _ in derived]) + " |")
+    print("|---|---:|" + "---:|" * (len(counters) + len(derived)))
+    for n in order:
+        vals = ["%.0f" % med(n, k) if med(n, k) is not None else "-" for k in counters]
+        vals += ["%.2f" % fn(n) for _, fn in derived]
+        print("| %s | %d | %s |" % (n, sum(1 for x, _ in names if x == n), " | ".join(vals)))
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -500,7 +568,15 @@ def main():
                     help="the Gemma-3-270m decode workload (batch 4, 64 -> 256 tokens, AttnLRP per generated token)")
     ap.add_argument("--rule", choices=sorted(RULES), default="lxt",
                     help="the LRP rule of the relevance pass (default: LXT's AttnLRP epsilon rule, the headline)")
+    ap.add_argument("--launch-names", metavar="FILE",
+                    help="write the step's launches (name and kernels dispatched, in order) to FILE")
+    ap.add_argument("--pmc-table", nargs="+", metavar=("NAMES", "DB"),
+                    help="offline: the per-launch HBM traffic of the step from rocprofv3 --pmc FETCH_SIZE / "
+                         "WRITE_SIZE databases of a --profile-reps 1 run and its --launch-names file")
     args = ap.parse_args()
+    if args.pmc_table:
+        pmc_table(args.pmc_table[0], args.pmc_table[1:])
+        return
     if args.gpus != 1:
         print("bench.py: this build measures one MI355X (the path runs on one GPU; --gpus %d is not supported)"
               % args.gpus, file=sys.stderr)
@@ -591,6 +667,10 @@ def main():
     # recording its own start and end events, so each kernel runs on the step's own buffers,
     # shapes and cache state and is timed without the gaps between launches.
     launches = models.launch_profile(eager_step, reps=args.profile_reps)
+    if args.launch_names:
+        with open(args.launch_names, "w") as f:
+            for r in launches:
+                f.write("%s\t%d\n" % (r["kernel"], r["dispatches"]))
     prof = summarize_launches(launches)
     gemm, attn = prof["families"].get("gemm"), prof["families"].get("attention")
     dom = prof["kernels"][0]  # the most time per step

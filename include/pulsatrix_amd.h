@@ -107,6 +107,9 @@ int pxa_launch_log_stop(int64_t* count);
 int pxa_launch_log_entry(int64_t index, char* kernel, size_t kernel_cap, char* family, size_t family_cap,
                          double* flops, double* bytes);
 int pxa_launch_log_time(int reps, double* seconds);
+/* The number of kernels launch `index` dispatched in the last pxa_launch_log_time replay (a split-K
+ * GEMM dispatches two): how a profiler's per-dispatch records map back onto the launches. */
+int pxa_launch_log_dispatches(int64_t index, int32_t* count);
 
 /* Seeded N(0, stddev) on the host: SplitMix64 bits, Box-Muller in double (src/portable_random.hpp:11-29). */
 void pxa_fill_normal(float* dst, size_t n, uint64_t seed, double stddev);

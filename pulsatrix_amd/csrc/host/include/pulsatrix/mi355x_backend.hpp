@@ -35,6 +35,7 @@ struct LaunchRecord {
     double flops = 0;    ///< algorithmic FLOPs of the launch (dense, as the reference computes them)
     double bytes = 0;    ///< algorithmic HBM bytes of the launch (memory-bound kernels)
     std::function<int(void* stream)> run;  ///< relaunches it with the same arguments
+    int dispatches = 0;  ///< kernels it dispatched in the last time_launch_log replay
 };
 
 class MI355XBackend : public DeviceBackend {

@@ -354,6 +354,15 @@ int pxa_launch_log_entry(int64_t index, char* kernel, size_t kernel_cap, char* f
     });
 }
 
+int pxa_launch_log_dispatches(int64_t index, int32_t* count) {
+    return guarded([&] {
+        const auto& log = backend()->launch_log();
+        if (index < 0 || static_cast<size_t>(index) >= log.size() || count == nullptr)
+            throw std::invalid_argument("pxa_launch_log_dispatches: index outside the log, or count NULL");
+        *count = log[static_cast<size_t>(index)].dispatches;
+    });
+}
+
 int pxa_launch_log_time(int reps, double* seconds) {
     return guarded([&] {
         if (reps <= 0) throw std::invalid_argument("pxa_launch_log_time: reps must be positive");

@@ -155,10 +155,13 @@ void MI355XBackend::run_gemm(pxk_gemm_desc& d) {
         const double mn = static_cast<double>(d.m) * d.n * bt, mk = static_cast<double>(d.m) * d.k * g * bt;
         const double kn = static_cast<double>(d.k) * d.n * g * (d.b.batch_stride || d.b.inner_stride ? bt : 1.0);
         double floats = mk + kn + (d.z.ptr && d.prologue != PXK_PRO_NONE ? mk : 0.0);
-        for (const pxk_operand* o : {&d.c, &d.c2, &d.c3, &d.x, &d.y, &d.w, &d.z2, &d.z3})
+        for (const pxk_operand* o : {&d.c, &d.c2, &d.c3, &d.x, &d.y, &d.w, &d.z2, &d.z3, &d.c2_den})
             if (o->ptr) floats += mn;
         if (d.z.ptr && d.prologue == PXK_PRO_NONE) floats += mn;  // the RoPE / value rules read Z like C
         if (d.epilogue == PXK_EPI_STORE && d.beta != 0.0f) floats += mn;  // C read back
+        if (d.x_rms) floats += static_cast<double>(d.m) * bt;                // the rows' rms
+        if (d.x_gamma) floats += static_cast<double>(d.n);                  // the norm's gains
+        if (d.row_rms) floats += static_cast<double>(d.m) * bt;              // rms written out
         const pxk_gemm_desc copy = d;
         log_.push_back(LaunchRecord{name, "gemm", 2.0 * d.m * d.n * d.k * d.batch * d.kgroups, 4.0 * floats,
                                     [copy](void* st) { return pxk_gemm(&copy, st); }});
@@ -199,8 +202,10 @@ void MI355XBackend::time_launch_log(int reps, std::vector<double>& seconds) {
         first[n] = pxk_timing_count();
         check(pxk_timing_end(ms.data(), capacity), "MI355XBackend::time_launch_log");
         if (first[n] >= capacity) throw std::runtime_error("MI355XBackend::time_launch_log: timing window too small");
-        for (size_t i = 0; i < n; ++i)
+        for (size_t i = 0; i < n; ++i) {
             for (int k = first[i]; k < first[i + 1]; ++k) seconds[i] += 1e-3 * ms[static_cast<size_t>(k)] / reps;
+            log_[i].dispatches = first[i + 1] - first[i];
+        }
     }
 }
 

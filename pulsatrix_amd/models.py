@@ -236,8 +236,8 @@ def launch_profile(run_once, reps=5):
     """Records every kernel launch of one call of run_once() on the backend (pxa_launch_log_*), then
     replays those launches in order `reps` times, each kernel recording its own start and end
     events. Returns one dict per launch: kernel (name and variant), family ("gemm", "attention",
-    "rows"), algorithmic flops and bytes, and seconds (the mean summed duration of its kernels). The
-    replays rewrite the outputs of the recorded pass."""
+    "rows"), algorithmic flops and bytes, seconds (the mean summed duration of its kernels) and the
+    number of kernels it dispatched. The replays rewrite the outputs of the recorded pass."""
     h = N.host()
     N.host_check(h.pxa_launch_log_start())
     try:
@@ -253,6 +253,8 @@ def launch_profile(run_once, reps=5):
         kernel, family = ctypes.create_string_buffer(160), ctypes.create_string_buffer(32)
         flops, nbytes = ctypes.c_double(0), ctypes.c_double(0)
         N.host_check(h.pxa_launch_log_entry(i, kernel, 160, family, 32, ctypes.byref(flops), ctypes.byref(nbytes)))
+        disp = ctypes.c_int32(0)
+        N.host_check(h.pxa_launch_log_dispatches(i, ctypes.byref(disp)))
         out.append({"kernel": kernel.value.decode(), "family": family.value.decode(), "flops": flops.value,
-                    "bytes": nbytes.value, "seconds": secs[i]})
+                    "bytes": nbytes.value, "seconds": secs[i], "dispatches": disp.value})
     return out

@@ -297,6 +297,7 @@ def host():
                                                     ctypes.c_size_t, ctypes.POINTER(ctypes.c_double),
                                                     ctypes.POINTER(ctypes.c_double)]),
             "pxa_launch_log_time": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(ctypes.c_double)]),
+            "pxa_launch_log_dispatches": (ctypes.c_int, [c_i64, ctypes.POINTER(ctypes.c_int32)]),
             "pxa_fill_normal": (None, [c_vp, ctypes.c_size_t, ctypes.c_uint64, ctypes.c_double]),
             "pxa_param_count": (c_i64, [cfgp]),
             "pxa_block_param_count": (c_i64, [cfgp]),
