@@ -278,6 +278,17 @@ int pxk_attention_supported(int64_t head_dim, int64_t seq_len, int64_t ldq, int6
 int pxk_attention_forward(const float* q, int64_t ldq, const float* k, int64_t ldk, const float* v, int64_t ldv,
                           float* raw, float* p, float* ctx, int64_t ldctx, int64_t n, int64_t l, int64_t heads,
                           int64_t kv_heads, int64_t head_dim, float scale, int causal, void* stream);
+/* The same forward with the softmax's row statistics: per query head and row, the max
+ * m = max over the visible keys of scale * raw and 1 / sum of exp(scale * raw - m) into stats
+ * (n, heads, l, 2), from which P = exp(scale * raw - m) * (1 / sum) is recomputed where the
+ * relevance pass needs it (pxk_attention_relevance_q / _kv with their stats operand). raw and p
+ * are optional here (NULL: not written); with neither there are no score rows in LDS and no
+ * sequence-length limit beyond 65536. ctx as above; head_dim a multiple of 4 up to 128, q/k row
+ * strides a multiple of 4. */
+int pxk_attention_forward_stats(const float* q, int64_t ldq, const float* k, int64_t ldk, const float* v,
+                                int64_t ldv, float* raw, float* p, float* stats, float* ctx, int64_t ldctx,
+                                int64_t n, int64_t l, int64_t heads, int64_t kv_heads, int64_t head_dim, float scale,
+                                int causal, void* stream);
 
 /* The AttnLRP pass of one attention layer through the steps that need whole score rows, fused per
  * query head and 16-row block (MultiHeadAttentionModule::propagate_relevance,
@@ -315,6 +326,20 @@ typedef struct pxk_attn_rel_desc {
     const float* sin_t;
     float* g;
     int64_t ld_g;
+    /* The recomputing form, selected by a non-NULL stats: p and raw are not read (may be NULL).
+     * Per 16-key tile the kernel recomputes raw = Q K^T (the forward's product, from q and k as
+     * given here) and P = exp(scale raw - m) / sum from the forward's row statistics
+     * (pxk_attention_forward_stats), and takes the softmax rule's row sum of r_attn as
+     * s_pv . ctx, which equals the sum of P * (s_pv V^T) over the keys. s and p_out (both
+     * nullable) receive s and P over each 16-row block's 16-key tiles up to its diagonal, zeros
+     * at the masked keys within them (all that pxk_attention_relevance_kv reads under `causal`);
+     * entries past those tiles are left as they were. No sequence-length limit beyond 65536; q, k
+     * and ctx 16-byte aligned with row strides a multiple of 4. */
+    const float* ctx;   /* the attention output P V, head-packed as the forward writes it */
+    int64_t ld_ctx;
+    const float* stats; /* (n, heads, l, 2): max of scale * raw and 1 / sum per row */
+    float* row_sum;     /* nullable: receives s_pv . ctx per (n, heads, l) row */
+    float* p_out;       /* nullable: receives P (n, heads, l, l) on the visible keys */
 } pxk_attn_rel_desc;
 int pxk_attention_relevance_q(const pxk_attn_rel_desc* d, void* stream);
 

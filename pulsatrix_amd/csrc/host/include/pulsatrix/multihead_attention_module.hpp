@@ -137,6 +137,7 @@ private:
     int64_t N_ = 0, L_ = 0;
     const float* x_ = nullptr;
     detail::DevBuf x_copy_, qkv_z_, qkv_y_, qk_norm_out_, qk_rot_, raw_, p_, ctx_, out_z_, out_y_;
+    detail::DevBuf stats_;  // fused path: the softmax's max and 1 / sum per (sequence, head, row)
     RMSNormModule* norm_in_ = nullptr;  // the RMSNorm folded into the q/k/v GEMM by the last forward, if any
     detail::DevBuf wqkv_g_;             // [Wq | Wk | Wv] with the folded norm's gamma on its rows
     const RMSNormModule* wg_norm_ = nullptr;

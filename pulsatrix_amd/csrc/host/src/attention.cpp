@@ -223,20 +223,23 @@ const float* MultiHeadAttentionModule::run_forward(const float* x, int64_t n, in
     const float* k = config_.use_rope ? rot + qd : pre + qd;
     const float* v = y + qd + kvd;
     const int64_t ldq = config_.use_rope ? rw : ld_pre, ldk = ldq;
-    float* raw = raw_.ensure(be_, n * H_ * LL);
-    float* p = p_.ensure(be_, n * H_ * LL);
+    const bool fused = fused_attention(l);
     float* ctx = ctx_.ensure(be_, M * qd);
-    if (fused_attention(l)) {
-        // 3-5 fused: scores, mask, softmax and P V in one launch, P and raw kept for relevance.
+    if (fused) {
+        // 3-5 fused: scores, mask, softmax and P V in one launch. The relevance pass recomputes the
+        // scores and P from q, k and the rows' softmax statistics, which are all that is kept.
+        float* stats = stats_.ensure(be_, n * H_ * l * 2);
         const float scale = score_scale();
         const int64_t H = H_, Hkv = Hkv_, D = D_;
         // dense algorithmic work: Q K^T and P V over every (query, key) square, as the reference computes it
         be_->launch("attn_fwd", "attention", 4.0 * n * H * l * l * D, 0.0, "MultiHeadAttentionModule::forward (attention)",
                     [=](void* s) {
-                        return pxk_attention_forward(q, ldq, k, ldk, v, w3, raw, p, ctx, qd, n, l, H, Hkv, D, scale,
-                                                     causal, s);
+                        return pxk_attention_forward_stats(q, ldq, k, ldk, v, w3, nullptr, nullptr, stats, ctx, qd,
+                                                           n, l, H, Hkv, D, scale, causal, s);
                     });
     } else {
+        raw_.ensure(be_, n * H_ * LL);
+        p_.ensure(be_, n * H_ * LL);
         run_attention_unfused(q, ldq, k, ldk, v, n, l);
     }
     // 6. output projection, with the block's residual add fused into the epilogue when asked.
@@ -269,8 +272,12 @@ void MultiHeadAttentionModule::reserve_forward(int64_t n, int64_t l) {
     if (config_.qkv_bias) qkv_y_.ensure(be_, M * w3);
     if (config_.use_qk_norm) qk_norm_out_.ensure(be_, M * rw);
     if (config_.use_rope) qk_rot_.ensure(be_, M * rw);
-    raw_.ensure(be_, n * H_ * l * l);
-    p_.ensure(be_, n * H_ * l * l);
+    if (fused_attention(l)) {
+        stats_.ensure(be_, n * H_ * l * 2);
+    } else {
+        raw_.ensure(be_, n * H_ * l * l);
+        p_.ensure(be_, n * H_ * l * l);
+    }
     ctx_.ensure(be_, M * qd);
     out_z_.ensure(be_, M * d_);
     if (config_.out_bias) out_y_.ensure(be_, M * d_);
@@ -283,8 +290,12 @@ void MultiHeadAttentionModule::replicate_forward(int64_t copies) {
     if (config_.qkv_bias) qkv_y_.repeat(be_, M * w3, copies, who);
     if (config_.use_qk_norm) qk_norm_out_.repeat(be_, M * rw, copies, who);
     if (config_.use_rope) qk_rot_.repeat(be_, M * rw, copies, who);
-    raw_.repeat(be_, N_ * H_ * L_ * L_, copies, who);
-    p_.repeat(be_, N_ * H_ * L_ * L_, copies, who);
+    if (fused_attention(L_)) {
+        stats_.repeat(be_, N_ * H_ * L_ * 2, copies, who);
+    } else {
+        raw_.repeat(be_, N_ * H_ * L_ * L_, copies, who);
+        p_.repeat(be_, N_ * H_ * L_ * L_, copies, who);
+    }
     ctx_.repeat(be_, M * qd, copies, who);
     out_z_.repeat(be_, M * d_, copies, who);
     if (config_.out_bias) out_y_.repeat(be_, M * d_, copies, who);
@@ -485,7 +496,9 @@ const float* MultiHeadAttentionModule::run_relevance(const float* relevance_out,
         be_->run_gemm(d);
     }
     float* ra = ra_.ensure(be_, n * H_ * LL);  // r_attn, then the Q K^T factor s
-    const float* p = p_.data();
+    // P: the forward's on the unfused path; on the fused path the q-side kernel recomputes it and
+    // writes it here for the key side.
+    float* p = p_.ensure(be_, n * H_ * LL);
     // [g_q | g_k | g_v]: relevance / stab(z) per projection, or the relevances themselves under a rule
     float* g = g_.ensure(be_, M * w3);
     if (!key_rel_.data() || key_rel_.numel() != M * kvd) {
@@ -512,8 +525,6 @@ const float* MultiHeadAttentionModule::run_relevance(const float* relevance_out,
         rd.ld_v = w3;
         rd.k = k;
         rd.ld_k = ldk;
-        rd.p = p;
-        rd.raw = raw_.data();
         rd.s = ra;
         rd.q = q;
         rd.ld_q = ldq;
@@ -527,6 +538,12 @@ const float* MultiHeadAttentionModule::run_relevance(const float* relevance_out,
         rd.g = g;
         rd.ld_g = w3;
         rd.relevance_only = affine;
+        // The recomputing form: raw and P from q, k and the forward's statistics, the softmax
+        // rule's row sums of r_attn as s_pv . ctx.
+        rd.ctx = ctx_.data();
+        rd.ld_ctx = qd;
+        rd.stats = stats_.data();
+        rd.p_out = p;
         // r_attn = P * (s_pv V^T) and r_q = Q * (s K): two L x L x D products per head
         be_->launch("attn_rel_q", "attention", 4.0 * n * H_ * l * l * D_, 0.0,
                     "MultiHeadAttentionModule::propagate_relevance", [rd](void* s) { return pxk_attention_relevance_q(&rd, s); });

@@ -48,7 +48,9 @@ struct FwdArgs {
     int n, l, heads, kv_heads, D;
     float scale;
     int causal;
-    int lds_ld;  // row stride of the LDS score block
+    int lds_ld;    // row stride of the LDS score block
+    float* stats;  // nullable: (n, heads, l, 2) the rows' softmax max of scale * raw and 1 / sum
+    int keep;      // raw or P is written: the raw scores wait in LDS for the last pass
 };
 
 __device__ __forceinline__ float row_max4(float v) {
@@ -157,8 +159,8 @@ __global__ void __launch_bounds__(kThreads) attn_fwd_kernel(const FwdArgs a) {
         // s[r] = raw score of (row, key0 + 4 g + r), kept in LDS for the last pass.
         const int kk0 = key0 + 4 * g;
         // A tile past the last one (the second of a pair) lands on column block ntile, inside the
-        // LDS row and past every visible key of this block: written, never read. No branch.
-        *reinterpret_cast<f4*>(sc + c * ld + 16 * min(kt, ntile) + 4 * g) = s;
+        // LDS row and past every visible key of this block: written, never read.
+        if (a.keep) *reinterpret_cast<f4*>(sc + c * ld + 16 * min(kt, ntile) + 4 * g) = s;
         float x[4];
         bool valid[4];
         float mt = -INFINITY;
@@ -240,6 +242,11 @@ __global__ void __launch_bounds__(kThreads) attn_fwd_kernel(const FwdArgs a) {
         if (cc == 0) {
             f_m[rr] = mx;
             f_s[rr] = tot;
+            if (a.stats && orow < l) {
+                float* st = a.stats + 2 * (((static_cast<int64_t>(b) * a.heads + h) * l) + orow);
+                st[0] = mx;
+                st[1] = 1.0f / tot;
+            }
         }
         if (orow < l) {
             float* cp = a.ctx + (static_cast<int64_t>(b) * l + orow) * a.ldctx + h * D;
@@ -251,6 +258,7 @@ __global__ void __launch_bounds__(kThreads) attn_fwd_kernel(const FwdArgs a) {
             }
         }
     }
+    if (!a.keep) return;  // uniform: the statistics form writes no score rows
     __syncthreads();
 
     // raw (visible keys) and P (every key, zeros past the visible ones) as contiguous row segments.
@@ -258,15 +266,16 @@ __global__ void __launch_bounds__(kThreads) attn_fwd_kernel(const FwdArgs a) {
         const float mx = f_m[rr], inv = 1.0f / f_s[rr];
         const int vis = a.causal ? orow + 1 : l;
         const int64_t off = ((static_cast<int64_t>(b) * a.heads + h) * l + orow) * l;
-        float* prow = a.p + off;
-        float* rrow = a.raw + off;
+        float* prow = a.p ? a.p + off : nullptr;
+        float* rrow = a.raw ? a.raw + off : nullptr;
         const float* srow = sc + rr * ld;
         if constexpr (VEC) {
             for (int k0 = 4 * cc; k0 < l; k0 += 64) {
                 f4 out = {0.f, 0.f, 0.f, 0.f};
                 if (k0 < vis) {
                     const f4 x = *reinterpret_cast<const f4*>(srow + k0);
-                    if (k0 + 3 < vis) {
+                    if (!a.raw) {
+                    } else if (k0 + 3 < vis) {
                         *reinterpret_cast<f4*>(rrow + k0) = x;
                     } else {
 #pragma unroll
@@ -276,17 +285,17 @@ __global__ void __launch_bounds__(kThreads) attn_fwd_kernel(const FwdArgs a) {
 #pragma unroll
                     for (int r = 0; r < 4; ++r) out[r] = k0 + r < vis ? __expf(a.scale * x[r] - mx) * inv : 0.0f;
                 }
-                *reinterpret_cast<f4*>(prow + k0) = out;
+                if (a.p) *reinterpret_cast<f4*>(prow + k0) = out;
             }
         } else {
             for (int k = cc; k < l; k += 16) {
                 float out = 0.0f;
                 if (k < vis) {
                     const float x = srow[k];
-                    rrow[k] = x;
+                    if (a.raw) rrow[k] = x;
                     out = __expf(a.scale * x - mx) * inv;
                 }
-                prow[k] = out;
+                if (a.p) prow[k] = out;
             }
         }
     }
@@ -312,6 +321,11 @@ struct RelArgs {
     int causal, rope, rope_half;
     int lds_ld;
     int rel_only;  // g receives the relevance itself (no projection denominator)
+    const float* ctx;    // the attention output, head-packed (recomputing form)
+    int ld_ctx;
+    const float* stats;  // the forward's row statistics (recomputing form), or null
+    float* row_sum;      // nullable (recomputing form): receives s_pv . ctx per row
+    float* p_out;        // nullable (recomputing form): receives P on the visible keys
 };
 
 template <int DT, bool VEC>
@@ -351,11 +365,41 @@ __global__ void __launch_bounds__(kThreads) attn_rel_q_kernel(const RelArgs a) {
     const int vis_end = a.causal ? min(i0 + 16, l) : l;
     const int ntile = (vis_end + 15) / 16;
 
+    // The query share's operands, loaded before the key loop so the last pass waits on no memory:
+    // thread (rr, cc) takes dims d = cc + 16 j of row i0 + rr (rows and dims clamped; the clamped
+    // ones are never stored). y_lo / y_hi: the rotated q at the dim's RoPE pair (y at d without
+    // RoPE); cs / sn: the pair's angle; xq: q before the rotation; zq, bq: z and the bias.
+    const int rr = threadIdx.x >> 4, cc = threadIdx.x & 15;
+    const int orow = i0 + rr;
+    const int half = D / 2;
+    float y_lo[DT], y_hi[DT], cs[DT], sn[DT], xq[DT], zq[DT], bq[DT];
+    {
+        const int64_t tok = static_cast<int64_t>(b) * l + min(orow, l - 1);
+        const float* qr = a.q + tok * a.ld_q + h * D;
+#pragma unroll
+        for (int j = 0; j < DT; ++j) {
+            const int d = min(cc + 16 * j, D - 1);
+            if (a.rope) {
+                const int i = a.rope_half ? (d < half ? d : d - half) : d / 2;
+                const int lo = a.rope_half ? i : 2 * i, hi = a.rope_half ? i + half : 2 * i + 1;
+                y_lo[j] = qr[lo];
+                y_hi[j] = qr[hi];
+                cs[j] = a.cos_t[static_cast<int64_t>(min(orow, l - 1)) * half + i];
+                sn[j] = a.sin_t[static_cast<int64_t>(min(orow, l - 1)) * half + i];
+                xq[j] = a.q_pre[tok * a.ld_q_pre + h * D + d];
+            } else {
+                y_lo[j] = qr[d];
+                y_hi[j] = cs[j] = sn[j] = xq[j] = 0.0f;
+            }
+            zq[j] = a.rel_only ? 1.0f : a.z[tok * a.ld_z + h * D + d];
+            bq[j] = a.bias ? a.bias[h * D + d] : 0.0f;
+        }
+    }
+
     // Both passes walk this wave's tiles two at a time with two register sets: a set is reloaded
     // with the tile after next right after its last read, the second tile of a pair runs even
     // past the last tile (all its keys masked: it adds nothing and stores nothing to LDS), and
     // loads clamp their addresses, so no branch surrounds a load.
-    const int ldv = a.ld_v, ldk = a.ld_k;
     auto p4 = [&](const float* rowp, int kt) -> f4 {  // 4 entries of a score row at tile kt, clamped
         const int kk0 = 16 * min(kt, ntile - 1) + 4 * g;
         if constexpr (VEC) return *reinterpret_cast<const f4*>(rowp + min(kk0, l - 4));
@@ -372,103 +416,106 @@ __global__ void __launch_bounds__(kThreads) attn_rel_q_kernel(const RelArgs a) {
         }
     };
 
-    // Pass 1: r_attn = P * (s_pv V^T), row sums. A operand: va[t][s] = V[key0 + c][16 t + 4 g + s].
-    f4 va[2][DT], pa[2];
-    auto load1 = [&](int set, int kt) {
-        const float* vp = vbase + min(16 * min(kt, ntile - 1) + c, l - 1) * ldv;
-#pragma unroll
-        for (int t = 0; t < DT; ++t) va[set][t] = *reinterpret_cast<const f4*>(vp + min(16 * t + 4 * g, D - 4));
-        pa[set] = p4(prow, kt);
-    };
-    float rs = 0.0f;
-    auto tile1 = [&](int set, int kt) {
-        const int kk0 = 16 * kt + 4 * g;
-        f4 u = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int t = 0; t < DT; ++t)
-#pragma unroll
-            for (int st = 0; st < 4; ++st) u = __builtin_amdgcn_mfma_f32_16x16x4f32(va[set][t][st], bf[t][st], u, 0, 0, 0);
-        bool valid[4];
-        valid_mask(kk0, valid);
-        f4 r4;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            r4[r] = valid[r] ? pa[set][r] * u[r] : 0.0f;
-            rs += r4[r];
-        }
-        *reinterpret_cast<f4*>(ra + c * ld + 16 * min(kt, ntile) + 4 * g) = r4;  // past the end: never read
-        // The set is reloaded only after its last read: a copy of a register whose reload is in
-        // flight would make the wave wait for that reload.
-        __builtin_amdgcn_sched_barrier(0);
-        load1(set, kt + 2 * kWaves);
-        __builtin_amdgcn_sched_barrier(0);
-    };
-    load1(0, wave);
-    load1(1, wave + kWaves);
-    __builtin_amdgcn_s_waitcnt(0);  // enter the loop with nothing in flight (as in attn_fwd_kernel)
-    for (int kt = wave; kt < ntile; kt += 2 * kWaves) {
-        tile1(0, kt);
-        tile1(1, kt + kWaves);
-    }
-    rs = row_sum4(rs);
-    if (g == 0) s_sum[wave][c] = rs;
-    __syncthreads();
-    if (threadIdx.x < 16) {
-        float t = 0.0f;
-#pragma unroll
-        for (int w = 0; w < kWaves; ++w) t += s_sum[w][threadIdx.x];
-        f_sum[threadIdx.x] = t;
-    }
-    __syncthreads();
-
-    // Pass 2: s = (scale raw)(r_attn - P sum) / (2 raw + eps sign raw); (s K)^T += K^T s^T with
-    // A operand kb[t][s] = K[key0 + 4 g + s][16 t + c] and B = this lane's s values.
-    const float sum = f_sum[c];
+    const int ldv = a.ld_v, ldk = a.ld_k;
     f4 acc[DT];
 #pragma unroll
     for (int t = 0; t < DT; ++t) acc[t] = f4{0.f, 0.f, 0.f, 0.f};
-    f4 kb[2][DT], pb[2], rb2[2];
-    auto load2 = [&](int set, int kt) {
-        const int key0 = 16 * min(kt, ntile - 1);
+    {
+        // Pass 1: r_attn = P * (s_pv V^T), row sums. A operand: va[t][s] = V[key0 + c][16 t + 4 g + s].
+        f4 va[2][DT], pa[2];
+        auto load1 = [&](int set, int kt) {
+            const float* vp = vbase + min(16 * min(kt, ntile - 1) + c, l - 1) * ldv;
 #pragma unroll
-        for (int st = 0; st < 4; ++st) {
-            const float* kp = kbase + min(key0 + 4 * g + st, l - 1) * ldk;
+            for (int t = 0; t < DT; ++t) va[set][t] = *reinterpret_cast<const f4*>(vp + min(16 * t + 4 * g, D - 4));
+            pa[set] = p4(prow, kt);
+        };
+        float rs = 0.0f;
+        auto tile1 = [&](int set, int kt) {
+            const int kk0 = 16 * kt + 4 * g;
+            f4 u = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int t = 0; t < DT; ++t) kb[set][t][st] = kp[min(16 * t + c, D - 1)];
+            for (int t = 0; t < DT; ++t)
+#pragma unroll
+                for (int st = 0; st < 4; ++st) u = __builtin_amdgcn_mfma_f32_16x16x4f32(va[set][t][st], bf[t][st], u, 0, 0, 0);
+            bool valid[4];
+            valid_mask(kk0, valid);
+            f4 r4;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                r4[r] = valid[r] ? pa[set][r] * u[r] : 0.0f;
+                rs += r4[r];
+            }
+            *reinterpret_cast<f4*>(ra + c * ld + 16 * min(kt, ntile) + 4 * g) = r4;  // past the end: never read
+            // The set is reloaded only after its last read: a copy of a register whose reload is in
+            // flight would make the wave wait for that reload.
+            __builtin_amdgcn_sched_barrier(0);
+            load1(set, kt + 2 * kWaves);
+            __builtin_amdgcn_sched_barrier(0);
+        };
+        load1(0, wave);
+        load1(1, wave + kWaves);
+        __builtin_amdgcn_s_waitcnt(0);  // enter the loop with nothing in flight (as in attn_fwd_kernel)
+        for (int kt = wave; kt < ntile; kt += 2 * kWaves) {
+            tile1(0, kt);
+            tile1(1, kt + kWaves);
         }
-        pb[set] = p4(prow, kt);
-        rb2[set] = p4(rrow, kt);
-    };
-    auto tile2 = [&](int set, int kt) {
-        const int kk0 = 16 * kt + 4 * g;
-        const f4 pv = pb[set], rw = rb2[set];
-        const int lcol = 16 * min(kt, ntile) + 4 * g;  // past the end: a masked, never-stored column
-        const f4 r4 = *reinterpret_cast<const f4*>(ra + c * ld + lcol);
-        bool valid[4];
-        valid_mask(kk0, valid);
-        f4 s4;
+        rs = row_sum4(rs);
+        if (g == 0) s_sum[wave][c] = rs;
+        __syncthreads();
+        if (threadIdx.x < 16) {
+            float t = 0.0f;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const float o = rw[r];
-            const float rsc = (a.scale * o) * (r4[r] - pv[r] * sum);
-            s4[r] = valid[r] ? rsc / (2.0f * o + a.eps * ((o >= 0.0f) ? 1.0f : -1.0f)) : 0.0f;
+            for (int w = 0; w < kWaves; ++w) t += s_sum[w][threadIdx.x];
+            f_sum[threadIdx.x] = t;
         }
-        *reinterpret_cast<f4*>(ra + c * ld + lcol) = s4;
+        __syncthreads();
+
+        // Pass 2: s = (scale raw)(r_attn - P sum) / (2 raw + eps sign raw); (s K)^T += K^T s^T with
+        // A operand kb[t][s] = K[key0 + 4 g + s][16 t + c] and B = this lane's s values.
+        const float sum = f_sum[c];
+        f4 kb[2][DT], pb[2], rb2[2];
+        auto load2 = [&](int set, int kt) {
+            const int key0 = 16 * min(kt, ntile - 1);
 #pragma unroll
-        for (int t = 0; t < DT; ++t)
+            for (int st = 0; st < 4; ++st) {
+                const float* kp = kbase + min(key0 + 4 * g + st, l - 1) * ldk;
 #pragma unroll
-            for (int st = 0; st < 4; ++st)
-                acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(kb[set][t][st], s4[st], acc[t], 0, 0, 0);
-        __builtin_amdgcn_sched_barrier(0);
-        load2(set, kt + 2 * kWaves);
-        __builtin_amdgcn_sched_barrier(0);
-    };
-    load2(0, wave);
-    load2(1, wave + kWaves);
-    __builtin_amdgcn_s_waitcnt(0);
-    for (int kt = wave; kt < ntile; kt += 2 * kWaves) {
-        tile2(0, kt);
-        tile2(1, kt + kWaves);
+                for (int t = 0; t < DT; ++t) kb[set][t][st] = kp[min(16 * t + c, D - 1)];
+            }
+            pb[set] = p4(prow, kt);
+            rb2[set] = p4(rrow, kt);
+        };
+        auto tile2 = [&](int set, int kt) {
+            const int kk0 = 16 * kt + 4 * g;
+            const f4 pv = pb[set], rw = rb2[set];
+            const int lcol = 16 * min(kt, ntile) + 4 * g;  // past the end: a masked, never-stored column
+            const f4 r4 = *reinterpret_cast<const f4*>(ra + c * ld + lcol);
+            bool valid[4];
+            valid_mask(kk0, valid);
+            f4 s4;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float o = rw[r];
+                const float rsc = (a.scale * o) * (r4[r] - pv[r] * sum);
+                s4[r] = valid[r] ? rsc / (2.0f * o + a.eps * ((o >= 0.0f) ? 1.0f : -1.0f)) : 0.0f;
+            }
+            *reinterpret_cast<f4*>(ra + c * ld + lcol) = s4;
+#pragma unroll
+            for (int t = 0; t < DT; ++t)
+#pragma unroll
+                for (int st = 0; st < 4; ++st)
+                    acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(kb[set][t][st], s4[st], acc[t], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            load2(set, kt + 2 * kWaves);
+            __builtin_amdgcn_sched_barrier(0);
+        };
+        load2(0, wave);
+        load2(1, wave + kWaves);
+        __builtin_amdgcn_s_waitcnt(0);
+        for (int kt = wave; kt < ntile; kt += 2 * kWaves) {
+            tile2(0, kt);
+            tile2(1, kt + kWaves);
+        }
     }
     // Merge: acc[t][r] = (s K)^T[16 t + 4 g + r][row c] of this wave.
 #pragma unroll
@@ -476,7 +523,6 @@ __global__ void __launch_bounds__(kThreads) attn_rel_q_kernel(const RelArgs a) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) s_acc[wave][c][16 * t + 4 * g + r] = acc[t][r];
     __syncthreads();
-    const int rr = threadIdx.x >> 4, cc = threadIdx.x & 15;
     for (int d = cc; d < D; d += 16) {
         float v = 0.0f;
 #pragma unroll
@@ -485,7 +531,6 @@ __global__ void __launch_bounds__(kThreads) attn_rel_q_kernel(const RelArgs a) {
     }
     __syncthreads();
 
-    const int orow = i0 + rr;
     if (orow < l) {
         // s over the whole row (zeros past the visible keys), contiguous.
         const int vis = a.causal ? orow + 1 : l;
@@ -506,41 +551,320 @@ __global__ void __launch_bounds__(kThreads) attn_rel_q_kernel(const RelArgs a) {
         }
         // Query share: r = Q_rot * (s K), the RoPE epsilon rule (lrp_math.hpp:104-123), then q_proj's
         // denominator: g = r_in / stab(z + bias).
-        const int64_t tok = static_cast<int64_t>(b) * l + orow;
-        const float* qr = a.q + tok * a.ld_q + h * D;
-        const float* qx = a.q_pre + tok * a.ld_q_pre + h * D;
-        const float* zr = a.rel_only ? nullptr : a.z + tok * a.ld_z + h * D;
-        const float* br = a.bias ? a.bias + h * D : nullptr;
-        float* gr = a.g + tok * a.ld_g + h * D;
-        const int half = D / 2;
-        for (int d = cc; d < D; d += 16) {
+        float* gr = a.g + (static_cast<int64_t>(b) * l + orow) * a.ld_g + h * D;
+#pragma unroll
+        for (int j = 0; j < DT; ++j) {
+            const int d = cc + 16 * j;
+            if (d >= D) continue;
             float r_in;
             if (a.rope) {
                 const int i = a.rope_half ? (d < half ? d : d - half) : d / 2;
                 const int lo = a.rope_half ? i : 2 * i, hi = a.rope_half ? i + half : 2 * i + 1;
-                const float y_lo = qr[lo], y_hi = qr[hi];
-                const float r_lo = y_lo * m_acc[rr][lo], r_hi = y_hi * m_acc[rr][hi];
-                const float cs = a.cos_t[static_cast<int64_t>(orow) * half + i];
-                const float sn = a.sin_t[static_cast<int64_t>(orow) * half + i];
-                const float d0 = stab(y_lo, a.eps), d1 = stab(y_hi, a.eps);
-                const float xv = qx[d];
+                const float r_lo = y_lo[j] * m_acc[rr][lo], r_hi = y_hi[j] * m_acc[rr][hi];
+                const float d0 = stab(y_lo[j], a.eps), d1 = stab(y_hi[j], a.eps);
+                const float xv = xq[j];
                 r_in = 0.0f;
                 if (d == lo) {
-                    r_in += (xv * cs / d0) * r_lo;
-                    r_in += (xv * sn / d1) * r_hi;
+                    r_in += (xv * cs[j] / d0) * r_lo;
+                    r_in += (xv * sn[j] / d1) * r_hi;
                 } else {
-                    r_in += (xv * -sn / d0) * r_lo;
-                    r_in += (xv * cs / d1) * r_hi;
+                    r_in += (xv * -sn[j] / d0) * r_lo;
+                    r_in += (xv * cs[j] / d1) * r_hi;
                 }
             } else {
-                r_in = qr[d] * m_acc[rr][d];
+                r_in = y_lo[j] * m_acc[rr][d];
             }
-            if (a.rel_only) {
-                gr[d] = r_in;
+            gr[d] = a.rel_only ? r_in : r_in / stab(a.bias ? zq[j] + bq[j] : zq[j], a.eps);
+        }
+    }
+}
+
+// Recomputing form (pxk_attention_relevance_q with stats and ctx): no score rows are read. Per
+// 16-key tile the kernel forms raw^T = K Q^T again (the forward's MFMA sequence, so the same
+// values), P = exp(scale raw - m) / sum from the row statistics the forward kept, and
+// u = s_pv V^T; the softmax rule's row sum of r_attn = P u is s_pv[row] . ctx[row] (the sum over
+// the keys of P[row][k] (s_pv[row] . V[k])), a D-long dot product before the loop. Then
+// s = (scale raw)(r_attn - P sum) / (2 raw + eps sign raw) and (s K)^T += K^T s^T.
+//
+// Memory. Everything the block reads outside the key loop (its 16 rows of Q, s_pv, ctx, and of
+// q_pre, z, the RoPE angles for the query share, the bias and the row statistics) comes in one
+// burst of whole-row 16-byte loads spread over the workgroup, into LDS; the waves take their
+// fragments from there. The key loop reads only K and V tiles of the block's KV head (shared by
+// all its blocks in L2), as 16 whole rows per tile; the transposed K fragments of (s K)^T come
+// from those rows through a per-wave LDS tile rather than a second, gathering load. s and P, when
+// asked for, are stored straight from the tile registers over the block's tiles.
+template <int DT, bool VEC, int NW>
+__global__ void __launch_bounds__(NW * kWave) attn_rel_q2_kernel(const RelArgs a) {
+    constexpr int NT = NW * kWave;
+    constexpr int RT = NT / 16;                 // threads per row in the last pass
+    constexpr int DJ = (16 * DT + RT - 1) / RT;  // head dims per thread in the last pass
+    constexpr int RS = 16 * DT + 4;             // LDS row stride of a 16-row operand block
+    constexpr int HS = 8 * DT + 4;              // LDS row stride of the RoPE angle blocks
+    // A wave's slot holds its K tile during the key loop, then its (s K)^T partial for the merge.
+    __shared__ __attribute__((aligned(16))) float wave_lds[NW][16][RS];
+    __shared__ __attribute__((aligned(16))) float op_lds[5][16][RS];  // Q, s_pv, ctx, q_pre, z rows
+    __shared__ __attribute__((aligned(16))) float ang_lds[2][16][HS];  // cos, sin rows
+    __shared__ __attribute__((aligned(16))) float bias_lds[16 * DT];
+    __shared__ float stat_lds[16][2];
+    __shared__ float m_acc[16][RS];
+
+    const int lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: the tile loop is scalar
+    const int l = a.l, D = a.D;
+    const int nrb = (l + 15) / 16;
+    // Long causal rows first, heads fastest: the heaviest blocks start first and spread over the CUs.
+    const int nbh = a.n * a.heads;
+    const int rb = nrb - 1 - static_cast<int>(blockIdx.x) / nbh, bh = static_cast<int>(blockIdx.x) % nbh;
+    const int h = bh % a.heads, b = bh / a.heads;
+    const int hk = h / (a.heads / a.kv_heads);
+    const int i0 = rb * 16, row = i0 + c;
+    const int vis_end = a.causal ? min(i0 + 16, l) : l;
+    const int ntile = (vis_end + 15) / 16;
+    const int vis_row = a.causal ? min(row + 1, l) : l;  // keys visible to the lane's row
+    const int half = D / 2;
+
+    // K and V tiles, two sets: kf[t][s] = K[key0 + c][16 t + 4 g + s] (A of raw^T), va[t][s] =
+    // V[key0 + c][16 t + 4 g + s] (A of u). A set is reloaded with the tile after next right after
+    // its last read, addresses clamped, so no branch surrounds a load.
+    const float* vbase = a.v + static_cast<int64_t>(b) * l * a.ld_v + hk * D;
+    const float* kbase = a.k + static_cast<int64_t>(b) * l * a.ld_k + hk * D;
+    const int ldv = a.ld_v, ldk = a.ld_k;
+    f4 kf[2][DT], va[2][DT];
+    auto load = [&](int set, int kt) {
+        const int kr = min(16 * min(kt, ntile - 1) + c, l - 1);
+        const float* kp = kbase + kr * ldk;
+        const float* vp = vbase + kr * ldv;
+#pragma unroll
+        for (int t = 0; t < DT; ++t) {
+            kf[set][t] = *reinterpret_cast<const f4*>(kp + min(16 * t + 4 * g, D - 4));
+            va[set][t] = *reinterpret_cast<const f4*>(vp + min(16 * t + 4 * g, D - 4));
+        }
+    };
+    // ---- the burst: the block's row operands into LDS, and the first two K / V tiles ----
+    // Every load is issued before any LDS store (fixed per-thread counts, unrolled), so the burst
+    // costs one memory round trip.
+    {
+        constexpr int F4N = (16 * 4 * DT + NT - 1) / NT;  // 16-byte pieces per thread per operand
+        constexpr int SCN = (16 * 16 * DT + NT - 1) / NT;  // scalars per thread per operand
+        constexpr int ANN = (16 * 8 * DT + NT - 1) / NT;   // angles per thread per table
+        const int q4n = D / 4;
+        const int64_t tok0 = static_cast<int64_t>(b) * l;
+        f4 lq[F4N], ls[F4N], lc[F4N];
+#pragma unroll
+        for (int j = 0; j < F4N; ++j) {
+            const int i = min(static_cast<int>(threadIdx.x) + NT * j, 16 * q4n - 1);
+            const int r = i / q4n, c4 = 4 * (i - r * q4n);
+            const int64_t tok = tok0 + min(i0 + r, l - 1);
+            const int col = h * D + c4;
+            lq[j] = *reinterpret_cast<const f4*>(a.q + tok * a.ld_q + col);
+            ls[j] = *reinterpret_cast<const f4*>(a.spv + tok * a.ld_spv + col);
+            lc[j] = *reinterpret_cast<const f4*>(a.ctx + tok * a.ld_ctx + col);
+        }
+        // The query share's operands, read as scalars (their strides need not be multiples of 4).
+        float lx[SCN], lz[SCN];
+#pragma unroll
+        for (int j = 0; j < SCN; ++j) {
+            const int i = min(static_cast<int>(threadIdx.x) + NT * j, 16 * D - 1);
+            const int r = i / D, d = i - r * D;
+            const int64_t tok = tok0 + min(i0 + r, l - 1);
+            lx[j] = a.rope ? a.q_pre[tok * a.ld_q_pre + h * D + d] : 0.0f;
+            lz[j] = a.rel_only ? 0.0f : a.z[tok * a.ld_z + h * D + d];
+        }
+        float lcs[ANN], lsn[ANN];
+#pragma unroll
+        for (int j = 0; j < ANN; ++j) {
+            const int i = min(static_cast<int>(threadIdx.x) + NT * j, 16 * max(half, 1) - 1);
+            const int r = i / max(half, 1), jj = i - r * max(half, 1);
+            const int64_t pos = min(i0 + r, l - 1);
+            lcs[j] = a.rope ? a.cos_t[pos * half + jj] : 0.0f;
+            lsn[j] = a.rope ? a.sin_t[pos * half + jj] : 0.0f;
+        }
+        const float lb = (a.bias && static_cast<int>(threadIdx.x) < D) ? a.bias[h * D + threadIdx.x] : 0.0f;
+        const int sr_ = min(static_cast<int>(threadIdx.x) >> 1, 15);
+        const float lst =
+            a.stats[2 * ((static_cast<int64_t>(b) * a.heads + h) * l + min(i0 + sr_, l - 1)) + (threadIdx.x & 1)];
+        load(0, wave);
+        load(1, wave + NW);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int j = 0; j < F4N; ++j) {
+            const int i = static_cast<int>(threadIdx.x) + NT * j;
+            if (i < 16 * q4n) {
+                const int r = i / q4n, c4 = 4 * (i - r * q4n);
+                *reinterpret_cast<f4*>(&op_lds[0][r][c4]) = lq[j];
+                *reinterpret_cast<f4*>(&op_lds[1][r][c4]) = ls[j];
+                *reinterpret_cast<f4*>(&op_lds[2][r][c4]) = lc[j];
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < SCN; ++j) {
+            const int i = static_cast<int>(threadIdx.x) + NT * j;
+            if (i < 16 * D) {
+                const int r = i / D, d = i - r * D;
+                op_lds[3][r][d] = lx[j];
+                op_lds[4][r][d] = lz[j];
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < ANN; ++j) {
+            const int i = static_cast<int>(threadIdx.x) + NT * j;
+            if (i < 16 * half) {
+                const int r = i / half, jj = i - r * half;
+                ang_lds[0][r][jj] = lcs[j];
+                ang_lds[1][r][jj] = lsn[j];
+            }
+        }
+        if (static_cast<int>(threadIdx.x) < D) bias_lds[threadIdx.x] = lb;
+        if (threadIdx.x < 32) stat_lds[sr_][threadIdx.x & 1] = lst;
+        // Q and s_pv columns past head_dim read as zeros in the fragments below.
+        for (int i = threadIdx.x; i < 16 * (16 * DT - D); i += NT) {
+            const int r = i / (16 * DT - D), d = D + i - r * (16 * DT - D);
+            op_lds[0][r][d] = 0.0f;
+            op_lds[1][r][d] = 0.0f;
+        }
+    }
+    __syncthreads();
+
+    // Lane (c, g) takes dims 16 t + 4 g .. of row c: Q (B operand of raw^T) and s_pv (B operand of
+    // u) are read from LDS per tile (zeros past head_dim); sum = s_pv . ctx of the row (its four
+    // lanes l, l ^ 16, l ^ 32, l ^ 48).
+    float sum = 0.0f;
+#pragma unroll
+    for (int t = 0; t < DT; ++t) {
+        const int d0 = min(16 * t + 4 * g, D - 4);
+        const f4 bv = *reinterpret_cast<const f4*>(&op_lds[1][c][16 * t + 4 * g]);
+        const f4 cv = *reinterpret_cast<const f4*>(&op_lds[2][c][d0]);
+        sum += bv[0] * cv[0] + bv[1] * cv[1] + bv[2] * cv[2] + bv[3] * cv[3];
+    }
+    sum = row_sum4(sum);
+    const float m_row = stat_lds[c][0], inv_row = stat_lds[c][1];
+    if (a.row_sum && g == 0 && row < l) a.row_sum[(static_cast<int64_t>(b) * a.heads + h) * l + row] = sum;
+
+    float* s_row = a.s ? a.s + (static_cast<int64_t>(b) * a.heads + h) * l * l + static_cast<int64_t>(row) * l : nullptr;
+    float* p_row = a.p_out ? a.p_out + (static_cast<int64_t>(b) * a.heads + h) * l * l + static_cast<int64_t>(row) * l
+                           : nullptr;
+    float(*kt_w)[RS] = wave_lds[wave];
+    f4 acc[DT];
+#pragma unroll
+    for (int t = 0; t < DT; ++t) acc[t] = f4{0.f, 0.f, 0.f, 0.f};
+    auto tile = [&](int set, int kt) {
+        const int kk0 = 16 * kt + 4 * g;
+        // The K tile's rows into the wave's LDS tile, for the transposed fragments below.
+#pragma unroll
+        for (int t = 0; t < DT; ++t) *reinterpret_cast<f4*>(&kt_w[c][16 * t + 4 * g]) = kf[set][t];
+        __builtin_amdgcn_wave_barrier();
+        // raw^T tile, the forward's sequence: lane (c, g) gets raw[row c][key kk0 + r].
+        f4 sr = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int t = 0; t < DT; ++t) {
+            const f4 qf = *reinterpret_cast<const f4*>(&op_lds[0][c][16 * t + 4 * g]);
+#pragma unroll
+            for (int st = 0; st < 4; ++st) sr = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[set][t][st], qf[st], sr, 0, 0, 0);
+        }
+        f4 u = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int t = 0; t < DT; ++t) {
+            const f4 bf = *reinterpret_cast<const f4*>(&op_lds[1][c][16 * t + 4 * g]);
+#pragma unroll
+            for (int st = 0; st < 4; ++st) u = __builtin_amdgcn_mfma_f32_16x16x4f32(va[set][t][st], bf[st], u, 0, 0, 0);
+        }
+        // kb[t][s] = K[key0 + 4 g + s][16 t + c] (A of (s K)^T)
+        f4 kb[DT];
+#pragma unroll
+        for (int t = 0; t < DT; ++t)
+#pragma unroll
+            for (int st = 0; st < 4; ++st) kb[t][st] = kt_w[4 * g + st][16 * t + c];
+        f4 s4, p4v;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const bool valid = kk0 + r < vis_row;
+            const float o = sr[r];
+            const float pv = valid ? __expf(a.scale * o - m_row) * inv_row : 0.0f;
+            const float rsc = (a.scale * o) * (pv * u[r] - pv * sum);
+            // The hardware reciprocal (1 ulp) in place of a full-precision divide.
+            s4[r] = valid ? rsc * __builtin_amdgcn_rcpf(2.0f * o + a.eps * ((o >= 0.0f) ? 1.0f : -1.0f)) : 0.0f;
+            p4v[r] = pv;
+        }
+        // s and P over the block's tiles up to its diagonal, zeros at the masked keys within them:
+        // the key side reads each row's keys up to the end of its diagonal tile.
+        if (row < l && kt < ntile && kk0 < l) {
+            if constexpr (VEC) {
+                if (s_row) *reinterpret_cast<f4*>(s_row + kk0) = s4;
+                if (p_row) *reinterpret_cast<f4*>(p_row + kk0) = p4v;
             } else {
-                const float zz = br ? zr[d] + br[d] : zr[d];
-                gr[d] = r_in / stab(zz, a.eps);
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    if (kk0 + r < l) {
+                        if (s_row) s_row[kk0 + r] = s4[r];
+                        if (p_row) p_row[kk0 + r] = p4v[r];
+                    }
             }
+        }
+#pragma unroll
+        for (int t = 0; t < DT; ++t)
+#pragma unroll
+            for (int st = 0; st < 4; ++st)
+                acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(kb[t][st], s4[st], acc[t], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        load(set, kt + 2 * NW);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    // Tiles in pairs, the second unconditionally: past the last tile every key is masked.
+    for (int kt = wave; kt < ntile; kt += 2 * NW) {
+        tile(0, kt);
+        tile(1, kt + NW);
+    }
+
+    // Merge: acc[t][r] = (s K)^T[16 t + 4 g + r][row c] of this wave, summed in wave order.
+    __builtin_amdgcn_wave_barrier();  // the wave's last K-tile reads are issued before its slot is rewritten
+#pragma unroll
+    for (int t = 0; t < DT; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) wave_lds[wave][c][16 * t + 4 * g + r] = acc[t][r];
+    __syncthreads();
+    const int rr = threadIdx.x / RT, cc = threadIdx.x % RT;
+    const int orow = i0 + rr;
+    for (int d = cc; d < D; d += RT) {
+        float v = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) v += wave_lds[w][rr][d];
+        m_acc[rr][d] = v;
+    }
+    __syncthreads();
+    if (orow >= l) return;
+
+    // Query share: r = Q_rot * (s K), the RoPE epsilon rule (lrp_math.hpp:104-123), then q_proj's
+    // denominator: g = r_in / stab(z + bias). Thread (rr, cc) takes dims d = cc + RT j of row i0 + rr.
+    float* gr = a.g + (static_cast<int64_t>(b) * l + orow) * a.ld_g + h * D;
+#pragma unroll
+    for (int j = 0; j < DJ; ++j) {
+        const int d = cc + RT * j;
+        if (d >= D) continue;
+        float r_in;
+        if (a.rope) {
+            const int i = a.rope_half ? (d < half ? d : d - half) : d / 2;
+            const int lo = a.rope_half ? i : 2 * i, hi = a.rope_half ? i + half : 2 * i + 1;
+            const float y_lo = op_lds[0][rr][lo], y_hi = op_lds[0][rr][hi];
+            const float r_lo = y_lo * m_acc[rr][lo], r_hi = y_hi * m_acc[rr][hi];
+            const float cs = ang_lds[0][rr][i], sn = ang_lds[1][rr][i];
+            const float d0 = stab(y_lo, a.eps), d1 = stab(y_hi, a.eps);
+            const float xv = op_lds[3][rr][d];
+            r_in = 0.0f;
+            if (d == lo) {
+                r_in += (xv * cs / d0) * r_lo;
+                r_in += (xv * sn / d1) * r_hi;
+            } else {
+                r_in += (xv * -sn / d0) * r_lo;
+                r_in += (xv * cs / d1) * r_hi;
+            }
+        } else {
+            r_in = op_lds[0][rr][d] * m_acc[rr][d];
+        }
+        if (a.rel_only) {
+            gr[d] = r_in;
+        } else {
+            const float zz = op_lds[4][rr][d];
+            gr[d] = r_in / stab(a.bias ? zz + bias_lds[d] : zz, a.eps);
         }
     }
 }
@@ -554,10 +878,12 @@ namespace {
 
 constexpr int kMaxLds = 160 * 1024;  // gfx950 LDS per workgroup
 
-// Row stride of the LDS score block: a multiple of 64 floats plus 16, so a wave's 16-byte
-// accesses to 4 consecutive rows (the score-tile writes, the last pass's row reads) fall in
-// distinct banks.
-int score_lds_ld(int64_t l) { return static_cast<int>((l + 63) / 64 * 64 + 16); }
+// Row stride of the LDS score block: a multiple of 64 floats plus 20. The 16 columns past the
+// rounded length take the branch-free tile past the last one (written, never read). The score-tile
+// accesses put 16 rows' 16-byte pieces in one instruction (lane c at row c): 20 c modulo 64 gives
+// 16 distinct groups of 4 banks (4 floats apart modulo 64 would too, but leaves no room past the
+// end). The last pass reads whole row segments, 16 lanes per row.
+int score_lds_ld(int64_t l) { return static_cast<int>((l + 63) / 64 * 64 + 20); }
 
 template <int DT>
 int static_lds() {
@@ -578,42 +904,67 @@ extern "C" int pxk_attention_supported(int64_t head_dim, int64_t seq_len, int64_
            seq_len >= 0 && seq_len <= 8192 && lds_bytes_needed(head_dim, seq_len) <= kMaxLds;
 }
 
-extern "C" int pxk_attention_forward(const float* q, int64_t ldq, const float* k, int64_t ldk, const float* v,
-                                     int64_t ldv, float* raw, float* p, float* ctx, int64_t ldctx, int64_t n,
-                                     int64_t l, int64_t heads, int64_t kv_heads, int64_t head_dim, float scale,
-                                     int causal, void* stream) {
+namespace {
+
+int attention_forward(const float* q, int64_t ldq, const float* k, int64_t ldk, const float* v, int64_t ldv,
+                      float* raw, float* p, float* stats, float* ctx, int64_t ldctx, int64_t n, int64_t l,
+                      int64_t heads, int64_t kv_heads, int64_t head_dim, float scale, int causal, void* stream,
+                      const char* who) {
+    const bool keep = raw || p;
     if (n < 0 || l < 0 || heads <= 0 || kv_heads <= 0 || heads % kv_heads != 0)
-        return fail(PXK_ERR_INVALID, "pxk_attention_forward: bad sizes (heads must be a multiple of kv_heads)");
-    if (!pxk_attention_supported(head_dim, l, ldq, ldk, ldv) || ldq < heads * head_dim ||
-        ldk < kv_heads * head_dim || ldv < kv_heads * head_dim || ldctx < heads * head_dim)
-        return fail(PXK_ERR_INVALID, "pxk_attention_forward: head_dim must be a multiple of 4 up to 128, the "
-                                     "sequence's score rows must fit LDS (about 2000 tokens), and the row strides "
-                                     "must hold every head (q and k strides a multiple of 4)");
-    if (!aligned16(q) || !aligned16(k))
-        return fail(PXK_ERR_INVALID, "pxk_attention_forward: q and k must be 16-byte aligned");
+        return fail(PXK_ERR_INVALID, "%s: bad sizes (heads must be a multiple of kv_heads)", who);
+    const bool shape_ok = keep ? pxk_attention_supported(head_dim, l, ldq, ldk, ldv) != 0
+                               : head_dim > 0 && head_dim <= 128 && head_dim % 4 == 0 && ldq % 4 == 0 &&
+                                     ldk % 4 == 0 && ldv >= head_dim && l <= 65536;
+    if (!shape_ok || ldq < heads * head_dim || ldk < kv_heads * head_dim || ldv < kv_heads * head_dim ||
+        ldctx < heads * head_dim)
+        return fail(PXK_ERR_INVALID, "%s: head_dim must be a multiple of 4 up to 128, the sequence's score rows "
+                                     "must fit LDS when raw or P is written (about 2000 tokens), and the row "
+                                     "strides must hold every head (q and k strides a multiple of 4)", who);
+    if (!aligned16(q) || !aligned16(k)) return fail(PXK_ERR_INVALID, "%s: q and k must be 16-byte aligned", who);
     if (n == 0 || l == 0) return PXK_OK;
     const int64_t blocks = n * heads * ((l + 15) / 16);
     if (blocks > (int64_t{1} << 31) - 1 || n * heads * l * l > (int64_t{1} << 40) || l * ldk >= (int64_t{1} << 31) ||
         l * ldv >= (int64_t{1} << 31))
-        return fail(PXK_ERR_INVALID, "pxk_attention_forward: problem too large");
+        return fail(PXK_ERR_INVALID, "%s: problem too large", who);
     const int lds_ld = score_lds_ld(l);
     FwdArgs a{q, k, v, raw, p, ctx, ldq, ldk, ldv, ldctx, static_cast<int>(n), static_cast<int>(l),
               static_cast<int>(heads), static_cast<int>(kv_heads), static_cast<int>(head_dim), scale, causal != 0,
-              lds_ld};
-    const bool vec = l % 4 == 0 && aligned16(raw) && aligned16(p);
+              lds_ld, stats, keep};
+    const bool vec = l % 4 == 0 && (!raw || aligned16(raw)) && (!p || aligned16(p));
     using K = void (*)(const FwdArgs);
     static const K table[2][4] = {
         {attn_fwd_kernel<1, false>, attn_fwd_kernel<2, false>, attn_fwd_kernel<4, false>, attn_fwd_kernel<8, false>},
         {attn_fwd_kernel<1, true>, attn_fwd_kernel<2, true>, attn_fwd_kernel<4, true>, attn_fwd_kernel<8, true>}};
     const int dt = dt_of(head_dim);
     const K fn = table[vec ? 1 : 0][dt == 1 ? 0 : dt == 2 ? 1 : dt == 4 ? 2 : 3];
-    const size_t dyn = static_cast<size_t>(16) * lds_ld * sizeof(float);
+    const size_t dyn = keep ? static_cast<size_t>(16) * lds_ld * sizeof(float) : 0;
     if (dyn > 64 * 1024 &&
         hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
                             static_cast<int>(dyn)) != hipSuccess)
-        return fail(PXK_ERR_LAUNCH, "pxk_attention_forward: %zu bytes of LDS refused", dyn);
+        return fail(PXK_ERR_LAUNCH, "%s: %zu bytes of LDS refused", who, dyn);
     PXK_LAUNCH(fn, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), dyn, S(stream), a);
-    return launched("pxk_attention_forward");
+    return launched(who);
+}
+
+}  // namespace
+
+extern "C" int pxk_attention_forward(const float* q, int64_t ldq, const float* k, int64_t ldk, const float* v,
+                                     int64_t ldv, float* raw, float* p, float* ctx, int64_t ldctx, int64_t n,
+                                     int64_t l, int64_t heads, int64_t kv_heads, int64_t head_dim, float scale,
+                                     int causal, void* stream) {
+    if (!raw || !p) return fail(PXK_ERR_INVALID, "pxk_attention_forward: raw and p are required");
+    return attention_forward(q, ldq, k, ldk, v, ldv, raw, p, nullptr, ctx, ldctx, n, l, heads, kv_heads, head_dim,
+                             scale, causal, stream, "pxk_attention_forward");
+}
+
+extern "C" int pxk_attention_forward_stats(const float* q, int64_t ldq, const float* k, int64_t ldk, const float* v,
+                                           int64_t ldv, float* raw, float* p, float* stats, float* ctx, int64_t ldctx,
+                                           int64_t n, int64_t l, int64_t heads, int64_t kv_heads, int64_t head_dim,
+                                           float scale, int causal, void* stream) {
+    if (!stats) return fail(PXK_ERR_INVALID, "pxk_attention_forward_stats: stats is required");
+    return attention_forward(q, ldq, k, ldk, v, ldv, raw, p, stats, ctx, ldctx, n, l, heads, kv_heads, head_dim,
+                             scale, causal, stream, "pxk_attention_forward_stats");
 }
 
 namespace {
@@ -623,17 +974,35 @@ int rel_static_lds() {
     return static_cast<int>(sizeof(float) * (kWaves * 16 + 16 + (kWaves + 1) * 16 * (16 * DT + 4)));
 }
 
+// Waves per block of the recomputing q relevance: eight (two per SIMD, so one wave's exponentials
+// and divides overlap the other's MFMA chains), four at head_dim 128.
+template <int DT>
+constexpr int rel_q2_waves() {
+    return DT == 8 ? 4 : 8;
+}
+
+template <int DT>
+int rel2_static_lds() {
+    return static_cast<int>(sizeof(float) * ((rel_q2_waves<DT>() + 6) * 16 * (16 * DT + 4) + 2 * 16 * (8 * DT + 4) +
+                                             16 * DT + 32));
+}
+
 }  // namespace
 
 extern "C" int pxk_attention_relevance_q(const pxk_attn_rel_desc* d, void* stream) {
     const int64_t n = d->n, l = d->l, H = d->heads, Hkv = d->kv_heads, D = d->head_dim;
+    const bool rc = d->stats != nullptr;  // the recomputing form
     if (n < 0 || l < 0 || H <= 0 || Hkv <= 0 || H % Hkv != 0)
         return fail(PXK_ERR_INVALID, "pxk_attention_relevance_q: bad sizes (heads must be a multiple of kv_heads)");
     if (D <= 0 || D > 128 || D % 4 != 0 || (d->rope && D % 2 != 0))
         return fail(PXK_ERR_INVALID, "pxk_attention_relevance_q: head_dim must be a multiple of 4 up to 128");
-    if (!d->spv || !d->v || !d->k || !d->p || !d->raw || !d->s || !d->q || (!d->z && !d->relevance_only) || !d->g ||
-        (d->rope && (!d->q_pre || !d->cos_t || !d->sin_t)))
+    if (!d->spv || !d->v || !d->k || !d->q || (!d->z && !d->relevance_only) || !d->g ||
+        (rc ? !d->ctx : (!d->p || !d->raw || !d->s)) || (d->rope && (!d->q_pre || !d->cos_t || !d->sin_t)))
         return fail(PXK_ERR_INVALID, "pxk_attention_relevance_q: a required operand is NULL");
+    if (rc && (d->ld_ctx % 4 || !aligned16(d->ctx) || d->ld_ctx < H * D || d->ld_q % 4 || !aligned16(d->q) ||
+               d->ld_k % 4 || !aligned16(d->k)))
+        return fail(PXK_ERR_INVALID, "pxk_attention_relevance_q: ctx, q and k must be 16-byte aligned with row "
+                                     "strides that are a multiple of 4 (ctx's holding every head)");
     if (d->ld_spv % 4 || d->ld_v % 4 || !aligned16(d->spv) || !aligned16(d->v) || d->ld_spv < H * D ||
         d->ld_v < Hkv * D || d->ld_k < Hkv * D || d->ld_q < H * D || d->ld_z < H * D || d->ld_g < H * D ||
         (d->rope && d->ld_q_pre < H * D))
@@ -641,33 +1010,46 @@ extern "C" int pxk_attention_relevance_q(const pxk_attn_rel_desc* d, void* strea
                                      "16-byte aligned with strides a multiple of 4)");
     const int lds_ld = score_lds_ld(l);
     const int dt = dt_of(D);
-    const int stat = dt == 8 ? rel_static_lds<8>() : rel_static_lds<4>();
-    const size_t dyn = static_cast<size_t>(16) * lds_ld * sizeof(float);
-    if (l > 8192 || stat + static_cast<int64_t>(dyn) > kMaxLds)
+    const int stat = rc ? (dt == 8 ? rel2_static_lds<8>() : rel2_static_lds<4>())
+                        : (dt == 8 ? rel_static_lds<8>() : rel_static_lds<4>());
+    // Score rows wait in LDS for s in the two-pass form; the recomputing form keeps none.
+    const size_t dyn = rc ? 0 : static_cast<size_t>(16) * lds_ld * sizeof(float);
+    if (l > (rc ? 65536 : 8192) || stat + static_cast<int64_t>(dyn) > kMaxLds)
         return fail(PXK_ERR_INVALID, "pxk_attention_relevance_q: the sequence's score rows must fit LDS");
     if (n == 0 || l == 0) return PXK_OK;
     const int64_t blocks = n * H * ((l + 15) / 16);
-    const int64_t lds_max = std::max({d->ld_spv, d->ld_v, d->ld_k, d->ld_q, d->ld_q_pre, d->ld_z, d->ld_g});
-    if (blocks > (int64_t{1} << 31) - 1 || n * l * lds_max >= (int64_t{1} << 31))
+    const int64_t lds_max = std::max({d->ld_spv, d->ld_v, d->ld_k, d->ld_q, d->ld_q_pre, d->ld_z, d->ld_g,
+                                      rc ? d->ld_ctx : int64_t{0}});
+    if (blocks > (int64_t{1} << 31) - 1 || n * l * lds_max >= (int64_t{1} << 31) ||
+        ((d->s || d->p_out) && n * H * l * l >= (int64_t{1} << 40)))
         return fail(PXK_ERR_INVALID, "pxk_attention_relevance_q: problem too large");
     RelArgs a{d->spv, d->v, d->k, d->p, d->raw, d->s, d->q, d->q_pre, d->z, d->bias, d->cos_t, d->sin_t, d->g,
               static_cast<int>(d->ld_spv), static_cast<int>(d->ld_v), static_cast<int>(d->ld_k),
               static_cast<int>(d->ld_q), static_cast<int>(d->ld_q_pre), static_cast<int>(d->ld_z),
               static_cast<int>(d->ld_g), static_cast<int>(n), static_cast<int>(l), static_cast<int>(H),
               static_cast<int>(Hkv), static_cast<int>(D), d->scale, d->eps, d->causal != 0, d->rope != 0,
-              d->rope_half != 0, lds_ld, d->relevance_only != 0};
-    const bool vec = l % 4 == 0 && aligned16(d->p) && aligned16(d->raw) && aligned16(d->s);
+              d->rope_half != 0, lds_ld, d->relevance_only != 0, d->ctx, static_cast<int>(d->ld_ctx), d->stats,
+              d->row_sum, rc ? d->p_out : nullptr};
+    const bool vec = l % 4 == 0 && (!d->p || aligned16(d->p)) && (!d->raw || aligned16(d->raw)) &&
+                     (!d->s || aligned16(d->s)) && (!rc || !d->p_out || aligned16(d->p_out));
     using K = void (*)(const RelArgs);
-    static const K table[2][4] = {
+    static const K two_pass[2][4] = {
         {attn_rel_q_kernel<1, false>, attn_rel_q_kernel<2, false>, attn_rel_q_kernel<4, false>,
          attn_rel_q_kernel<8, false>},
         {attn_rel_q_kernel<1, true>, attn_rel_q_kernel<2, true>, attn_rel_q_kernel<4, true>, attn_rel_q_kernel<8, true>}};
-    const K fn = table[vec ? 1 : 0][dt == 1 ? 0 : dt == 2 ? 1 : dt == 4 ? 2 : 3];
+    static const K recompute[2][4] = {
+        {attn_rel_q2_kernel<1, false, rel_q2_waves<1>()>, attn_rel_q2_kernel<2, false, rel_q2_waves<2>()>,
+         attn_rel_q2_kernel<4, false, rel_q2_waves<4>()>, attn_rel_q2_kernel<8, false, rel_q2_waves<8>()>},
+        {attn_rel_q2_kernel<1, true, rel_q2_waves<1>()>, attn_rel_q2_kernel<2, true, rel_q2_waves<2>()>,
+         attn_rel_q2_kernel<4, true, rel_q2_waves<4>()>, attn_rel_q2_kernel<8, true, rel_q2_waves<8>()>}};
+    const int di = dt == 1 ? 0 : dt == 2 ? 1 : dt == 4 ? 2 : 3;
+    const K fn = rc ? recompute[vec ? 1 : 0][di] : two_pass[vec ? 1 : 0][di];
+    const int threads = rc ? (dt == 8 ? rel_q2_waves<8>() : rel_q2_waves<4>()) * kWave : kThreads;
     if (dyn > 64 * 1024 &&
         hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
                             static_cast<int>(dyn)) != hipSuccess)
         return fail(PXK_ERR_LAUNCH, "pxk_attention_relevance_q: %zu bytes of LDS refused", dyn);
-    PXK_LAUNCH(fn, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), dyn, S(stream), a);
+    PXK_LAUNCH(fn, dim3(static_cast<unsigned>(blocks)), dim3(threads), dyn, S(stream), a);
     return launched("pxk_attention_relevance_q");
 }
 

@@ -80,6 +80,7 @@ PXK_SIGNATURES = {
     "pxk_dot": "ppippp",
     "pxk_attention_supported": "iiiii",
     "pxk_attention_forward": "pipipipppiiiiiifnp",
+    "pxk_attention_forward_stats": "pipipippppiiiiiifnp",
     "pxk_attention_softmax": "ppiifnip",
     "pxk_attention_lrp_scores": "ppppiiffnip",
     "pxk_rms_norm_heads": "pipipiiifp",
@@ -184,7 +185,8 @@ class AttnRelDesc(ctypes.Structure):
                 ("spv", c_vp), ("ld_spv", c_i64), ("v", c_vp), ("ld_v", c_i64), ("k", c_vp), ("ld_k", c_i64),
                 ("p", c_vp), ("raw", c_vp), ("s", c_vp), ("q", c_vp), ("ld_q", c_i64), ("q_pre", c_vp),
                 ("ld_q_pre", c_i64), ("z", c_vp), ("ld_z", c_i64), ("bias", c_vp), ("cos_t", c_vp), ("sin_t", c_vp),
-                ("g", c_vp), ("ld_g", c_i64)]
+                ("g", c_vp), ("ld_g", c_i64), ("ctx", c_vp), ("ld_ctx", c_i64),
+                ("stats", c_vp), ("row_sum", c_vp), ("p_out", c_vp)]
 
 
 class AttnRelKvDesc(ctypes.Structure):

@@ -67,6 +67,50 @@ def test_fused_attention_forward_matches_numpy(n, L, H, Hkv, D, causal):
 
 
 @gpu
+@pytest.mark.parametrize("with_p", [0, 1])
+@pytest.mark.parametrize("n,L,H,Hkv,D", [(1, 37, 4, 2, 16), (2, 64, 3, 1, 12), (1, 512, 9, 3, 64), (1, 50, 2, 2, 128),
+                                         (1, 2600, 2, 1, 64)])
+def test_fused_attention_forward_stats_matches_numpy(n, L, H, Hkv, D, with_p):
+    """The statistics form: ctx and, per row, the softmax max of scale * raw and 1 / sum. Without P
+    or raw it needs no LDS for score rows, so 2600 tokens (past the score-row form's limit) run."""
+    print("forward stats n=%d L=%d H=%d Hkv=%d D=%d with_p=%d" % (n, L, H, Hkv, D, with_p), flush=True)
+    if with_p and L > 2000:
+        pytest.skip("P is kept only within the score-row form's LDS limit")
+    qd, kvd = H * D, Hkv * D
+    w3 = qd + 2 * kvd
+    qkv = G.uniform((n * L, w3), 21 + L + D)
+    scale = 1.0 / np.sqrt(D)
+    qkv_d = G.dev(qkv)
+    stats, ctx = G.empty((n, H, L, 2)), G.empty((n * L, qd))
+    p = G.empty((n, H, L, L)) if with_p else None
+    base = qkv_d.data_ptr()
+    N.call("pxk_attention_forward_stats", base, w3, base + 4 * qd, w3, base + 4 * (qd + kvd), w3, None,
+           G.ptr(p) if with_p else None, G.ptr(stats), G.ptr(ctx), qd, n, L, H, Hkv, D, scale, 1, G.stream())
+    q, k, v = qkv[:, :qd], qkv[:, qd:qd + kvd], qkv[:, qd + kvd:]
+    grp = H // Hkv
+    qh = q.reshape(n, L, H, D).transpose(0, 2, 1, 3).astype(np.float64)
+    kh = np.repeat(k.reshape(n, L, Hkv, D).transpose(0, 2, 1, 3), grp, axis=1).astype(np.float64)
+    vh = np.repeat(v.reshape(n, L, Hkv, D).transpose(0, 2, 1, 3), grp, axis=1).astype(np.float64)
+    want_st = np.empty((n, H, L, 2))
+    want_ctx = np.empty((n, H, L, D))
+    for b in range(n):  # per head, so the 2600-token case stays small
+        for h in range(H):
+            x = scale * (qh[b, h] @ kh[b, h].T)
+            x = np.where(np.tril(np.ones((L, L), bool)), x, -np.inf)
+            m = x.max(-1)
+            e = np.exp(x - m[:, None])
+            ssum = e.sum(-1)
+            want_st[b, h, :, 0], want_st[b, h, :, 1] = m, 1.0 / ssum
+            want_ctx[b, h] = (e / ssum[:, None]) @ vh[b, h]
+            if with_p:
+                G.assert_close(G.host(p)[b, h], e / ssum[:, None], 1e-4, "P")
+    got = G.host(stats)
+    G.assert_close(got[..., 0], want_st[..., 0], 1e-4, "row max")
+    G.assert_close(got[..., 1], want_st[..., 1], 1e-4, "1 / row sum")
+    G.assert_close(G.host(ctx), want_ctx.transpose(0, 2, 1, 3).reshape(n * L, qd), 1e-4, "ctx")
+
+
+@gpu
 def test_fused_attention_is_deterministic():
     n, L, H, Hkv, D = 1, 200, 4, 2, 64
     q, k, v = G.uniform((n * L, H * D), 1), G.uniform((n * L, Hkv * D), 2), G.uniform((n * L, Hkv * D), 3)
@@ -131,22 +175,40 @@ def relevance_q_reference(spv, q, q_pre, k, v, z, bias, p, raw, cos, sin, n, L, 
 
 
 @gpu
+@pytest.mark.parametrize("recompute", [0, 1])
 @pytest.mark.parametrize("rope,half,bias", [(1, 1, 0), (1, 0, 1), (0, 0, 1)])
 @pytest.mark.parametrize("causal", [1, 0])
-@pytest.mark.parametrize("n,L,H,Hkv,D", [(1, 37, 4, 2, 16), (2, 64, 3, 1, 12), (1, 128, 9, 3, 64), (1, 40, 2, 2, 128)])
-def test_fused_attention_relevance_matches_numpy(n, L, H, Hkv, D, causal, rope, half, bias):
+@pytest.mark.parametrize("n,L,H,Hkv,D", [(1, 37, 4, 2, 16), (2, 64, 3, 1, 12), (1, 128, 9, 3, 64), (1, 40, 2, 2, 128),
+                                         (1, 512, 9, 3, 64)])
+def test_fused_attention_relevance_matches_numpy(n, L, H, Hkv, D, causal, rope, half, bias, recompute):
+    """recompute: the kernel gets no raw scores or P, only the forward's row statistics and the
+    attention output ctx = P V; it recomputes raw = Q K^T and P and takes the softmax rule's row
+    sums as s_pv . ctx, while the reference sums r_attn over the keys. Its q and k hold multiples
+    of 0.5 up to 1 in magnitude, so raw = Q K^T is exact in float32 and float64 alike."""
+    print("q relevance n=%d L=%d H=%d Hkv=%d D=%d causal=%d rope=%d half=%d recompute=%d"
+          % (n, L, H, Hkv, D, causal, rope, half, recompute), flush=True)
     qd, kvd = H * D, Hkv * D
+    grp = H // Hkv
     scale, eps = 1.0 / np.sqrt(D), 1e-6
     rs = np.random.RandomState(L + D)
     away = lambda *shape: (rs.uniform(0.5, 1.5, shape) * rs.choice([-1.0, 1.0], shape)).astype(np.float32)
+    halves = lambda *shape: rs.choice([-1.0, -0.5, 0.5, 1.0], shape).astype(np.float32)
     spv, q, q_pre, z = G.uniform((n * L, qd), 1), away(n * L, qd), G.uniform((n * L, qd), 3), away(n * L, qd)
     k, v = G.uniform((n * L, kvd), 4), G.uniform((n * L, kvd), 5)
     b = (G.uniform((qd,), 6) * 0.1) if bias else None
-    raw = away(n, H, L, L)  # denominators 2 raw + eps sign raw stay clear of 0
+    if recompute:
+        q, k = halves(n * L, qd), halves(n * L, kvd)
+        qh = q.reshape(n, L, H, D).transpose(0, 2, 1, 3).astype(np.float64)
+        kh = np.repeat(k.reshape(n, L, Hkv, D).transpose(0, 2, 1, 3), grp, axis=1).astype(np.float64)
+        raw = (qh @ kh.transpose(0, 1, 3, 2)).astype(np.float32)
+    else:
+        raw = away(n, H, L, L)  # denominators 2 raw + eps sign raw stay clear of 0
     vis = np.tril(np.ones((L, L), bool)) if causal else np.ones((L, L), bool)
     x = np.where(vis, scale * raw.astype(np.float64), -np.inf)
-    e = np.exp(x - x.max(-1, keepdims=True))
+    mx = x.max(-1, keepdims=True)
+    e = np.exp(x - mx)
     p = (e / e.sum(-1, keepdims=True)).astype(np.float32)
+    stats = np.stack([mx[..., 0], 1.0 / e.sum(-1)], axis=-1).astype(np.float32)
     ang = np.arange(L)[:, None] * (10000.0 ** (-np.arange(D // 2) * 2.0 / D))[None, :]
     cos, sin = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
     want_s, want_g = relevance_q_reference(spv, q, q_pre, k, v, z, b, p.astype(np.float64), raw.astype(np.float64),
@@ -166,10 +228,30 @@ def test_fused_attention_relevance_matches_numpy(n, L, H, Hkv, D, causal, rope, 
     d.bias = G.ptr(G.dev(b)).value if bias else None
     d.cos_t, d.sin_t = G.ptr(dv["cos"]).value, G.ptr(dv["sin"]).value
     d.g, d.ld_g = G.ptr(g_out).value, qd
+    if recompute:
+        v_h = np.repeat(v.reshape(n, L, Hkv, D).transpose(0, 2, 1, 3), grp, axis=1).astype(np.float64)
+        ctx = (p.astype(np.float64) @ v_h).transpose(0, 2, 1, 3).reshape(n * L, qd).astype(np.float32)
+        ctx_d, stats_d, rsum, p_out = G.dev(ctx), G.dev(stats), G.empty((n, H, L)), G.empty((n, H, L, L))
+        d.ctx, d.ld_ctx, d.stats, d.row_sum = G.ptr(ctx_d).value, qd, G.ptr(stats_d).value, G.ptr(rsum).value
+        d.p_out = G.ptr(p_out).value
+        d.p = d.raw = None  # not read
     assert N.pxk().pxk_attention_relevance_q(ctypes.byref(d), G.stream()) == 0, N.pxk().pxk_last_error()
+    if recompute:  # s_pv . ctx per row
+        spv_h = spv.reshape(n, L, H, D).transpose(0, 2, 1, 3).astype(np.float64)
+        ctx_h = ctx.reshape(n, L, H, D).transpose(0, 2, 1, 3).astype(np.float64)
+        G.assert_close(G.host(rsum), (spv_h * ctx_h).sum(-1), 1e-4, "row_sum")
     got_s = G.host(s_out)
-    G.assert_close(got_s, want_s, 1e-4, "s")
-    assert np.all(got_s[..., ~vis] == 0.0)
+    if recompute:  # s and P on the visible keys, zeros at the masked keys of the diagonal tiles
+        got_p = G.host(p_out)
+        G.assert_close(got_s[..., vis], want_s[..., vis], 1e-4, "s")
+        G.assert_close(got_p[..., vis], p.astype(np.float64)[..., vis], 1e-4, "P")
+        if causal:
+            i, j = np.meshgrid(np.arange(L), np.arange(L), indexing="ij")
+            diag = (j > i) & (j < np.minimum(16 * (i // 16 + 1), L))
+            assert np.all(got_s[..., diag] == 0.0) and np.all(got_p[..., diag] == 0.0)
+    else:
+        G.assert_close(got_s, want_s, 1e-4, "s")
+        assert np.all(got_s[..., ~vis] == 0.0)
     G.assert_close(G.host(g_out), want_g, 1e-4, "g_q")
 
 
@@ -248,6 +330,72 @@ def test_fused_attention_kv_relevance_matches_numpy(n, L, H, Hkv, D, causal, rop
     assert N.pxk().pxk_attention_relevance_kv(ctypes.byref(d), G.stream()) == 0, N.pxk().pxk_last_error()
     for got, ref, name in zip(outs, want, ("key_rel", "value_rel", "g_k", "g_v")):
         G.assert_close(G.host(got), ref, 1e-4, name)
+
+
+@gpu
+@pytest.mark.parametrize("n,L,H,Hkv,D", [(1, 200, 4, 2, 64), (2, 37, 3, 1, 16), (1, 512, 9, 3, 64)])
+def test_recomputing_chain_matches_score_row_chain(n, L, H, Hkv, D):
+    """The step's attention relevance chain in its recomputing form (forward with row statistics,
+    q side recomputing raw and P and writing s and P into NaN-filled buffers, key side reading
+    them) against the score-row form (forward keeping raw and P, two-pass q side): the same
+    [g_q | g_k | g_v]. q and k hold multiples of 0.5, so raw = Q K^T is exact."""
+    print("recomputing chain n=%d L=%d H=%d Hkv=%d D=%d" % (n, L, H, Hkv, D), flush=True)
+    qd, kvd = H * D, Hkv * D
+    w3 = qd + 2 * kvd
+    scale, eps = 1.0 / np.sqrt(D), 1e-9
+    rs = np.random.RandomState(7 * L + D)
+    qkv = rs.choice([-1.0, -0.5, 0.5, 1.0], (n * L, w3)).astype(np.float32)
+    qkv[:, qd + kvd:] = G.uniform((n * L, kvd), 1)  # v
+    spv = G.uniform((n * L, qd), 2)
+    pre = G.uniform((n * L, qd + kvd), 3)  # q | k before the rotation
+    z = (rs.uniform(0.5, 1.5, (n * L, w3)) * rs.choice([-1.0, 1.0], (n * L, w3))).astype(np.float32)
+    ang = np.arange(L)[:, None] * (10000.0 ** (-np.arange(D // 2) * 2.0 / D))[None, :]
+    cos, sin = G.dev(np.cos(ang).astype(np.float32)), G.dev(np.sin(ang).astype(np.float32))
+    qkv_d, spv_d, pre_d, z_d = G.dev(qkv), G.dev(spv), G.dev(pre), G.dev(z)
+    base = qkv_d.data_ptr()
+
+    def chain(recompute):
+        ctx, g = G.empty((n * L, qd)), G.empty((n * L, w3))
+        s_buf, p_buf = G.empty((n, H, L, L)), G.empty((n, H, L, L))  # NaN: unwritten entries show
+        stats = G.empty((n, H, L, 2))
+        if recompute:
+            N.call("pxk_attention_forward_stats", base, w3, base + 4 * qd, w3, base + 4 * (qd + kvd), w3, None, None,
+                   G.ptr(stats), G.ptr(ctx), qd, n, L, H, Hkv, D, scale, 1, G.stream())
+        else:
+            raw = G.empty((n, H, L, L))
+            N.call("pxk_attention_forward", base, w3, base + 4 * qd, w3, base + 4 * (qd + kvd), w3, G.ptr(raw),
+                   G.ptr(p_buf), G.ptr(ctx), qd, n, L, H, Hkv, D, scale, 1, G.stream())
+        d = N.AttnRelDesc()
+        d.n, d.l, d.heads, d.kv_heads, d.head_dim = n, L, H, Hkv, D
+        d.scale, d.eps, d.causal, d.rope, d.rope_half = scale, eps, 1, 1, 1
+        d.spv, d.ld_spv = spv_d.data_ptr(), qd
+        d.v, d.ld_v, d.k, d.ld_k = base + 4 * (qd + kvd), w3, base + 4 * qd, w3
+        d.s = G.ptr(s_buf).value
+        d.q, d.ld_q, d.q_pre, d.ld_q_pre = base, w3, pre_d.data_ptr(), qd + kvd
+        d.z, d.ld_z = z_d.data_ptr(), w3
+        d.cos_t, d.sin_t = cos.data_ptr(), sin.data_ptr()
+        d.g, d.ld_g = G.ptr(g).value, w3
+        if recompute:
+            d.ctx, d.ld_ctx, d.stats, d.p_out = G.ptr(ctx).value, qd, G.ptr(stats).value, G.ptr(p_buf).value
+        else:
+            d.p, d.raw = G.ptr(p_buf).value, G.ptr(raw).value
+        assert N.pxk().pxk_attention_relevance_q(ctypes.byref(d), G.stream()) == 0, N.pxk().pxk_last_error()
+        kd = N.AttnRelKvDesc()
+        kd.n, kd.l, kd.heads, kd.kv_heads, kd.head_dim = n, L, H, Hkv, D
+        kd.eps, kd.causal, kd.rope, kd.rope_half = eps, 1, 1, 1
+        kd.s, kd.p, kd.q, kd.ld_q = G.ptr(s_buf).value, G.ptr(p_buf).value, base, w3
+        kd.spv, kd.ld_spv = spv_d.data_ptr(), qd
+        kd.k, kd.ld_k, kd.k_pre, kd.ld_k_pre = base + 4 * qd, w3, pre_d.data_ptr() + 4 * qd, qd + kvd
+        kd.v, kd.ld_v = base + 4 * (qd + kvd), w3
+        kd.z_k, kd.z_v, kd.ld_z = z_d.data_ptr() + 4 * qd, z_d.data_ptr() + 4 * (qd + kvd), w3
+        kd.cos_t, kd.sin_t = cos.data_ptr(), sin.data_ptr()
+        kd.g_k, kd.g_v, kd.ld_g = G.ptr(g).value + 4 * qd, G.ptr(g).value + 4 * (qd + kvd), w3
+        assert N.pxk().pxk_attention_relevance_kv(ctypes.byref(kd), G.stream()) == 0, N.pxk().pxk_last_error()
+        return G.host(g)
+
+    want, got = chain(False), chain(True)
+    assert np.all(np.isfinite(got))
+    G.assert_close(got, want, 1e-4, "[g_q | g_k | g_v]")
 
 
 def test_fused_attention_kv_relevance_rejects_bad_descs():
