@@ -640,7 +640,7 @@ __global__ void __launch_bounds__(NW * kWave) attn_rel_q2_kernel(const RelArgs a
             va[set][t] = *reinterpret_cast<const f4*>(vp + min(16 * t + 4 * g, D - 4));
         }
     };
-    // ---- the burst: the block's row operands into LDS, and the first two K / V tiles ----
+    // ---- the burst: the block's row operands into LDS, and the first K / V tile ----
     // Every load is issued before any LDS store (fixed per-thread counts, unrolled), so the burst
     // costs one memory round trip.
     {
@@ -684,7 +684,6 @@ __global__ void __launch_bounds__(NW * kWave) attn_rel_q2_kernel(const RelArgs a
         const float lst =
             a.stats[2 * ((static_cast<int64_t>(b) * a.heads + h) * l + min(i0 + sr_, l - 1)) + (threadIdx.x & 1)];
         load(0, wave);
-        load(1, wave + NW);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int j = 0; j < F4N; ++j) {
@@ -724,6 +723,9 @@ __global__ void __launch_bounds__(NW * kWave) attn_rel_q2_kernel(const RelArgs a
         }
     }
     __syncthreads();
+
+    // The second tile set is requested once the burst has landed: it overlaps the first tile.
+    load(1, wave + NW);
 
     // Lane (c, g) takes dims 16 t + 4 g .. of row c: Q (B operand of raw^T) and s_pv (B operand of
     // u) are read from LDS per tile (zeros past head_dim); sum = s_pv . ctx of the row (its four
