@@ -205,11 +205,11 @@ __global__ void __launch_bounds__(kThreads) attn_fwd_kernel(const FwdArgs a) {
     // context unchanged. No branch splits the load stream.
     load_k(0, wave);
     load_v(0, wave);
+    // The first set and Q have landed before the second set is requested: it overlaps the first
+    // tile, and the loop head's wait covers only the loop's own reloads (two tiles ahead).
+    __builtin_amdgcn_s_waitcnt(0);
     load_k(1, wave + kWaves);
     load_v(1, wave + kWaves);
-    // Enter the loop with nothing in flight: the loop head's wait then covers only the loop's own
-    // reloads (two tiles ahead) instead of draining every load at each iteration.
-    __builtin_amdgcn_s_waitcnt(0);
     for (int kt = wave; kt < ntile; kt += 2 * kWaves) {
         tile(0, kt);
         tile(1, kt + kWaves);
