@@ -968,6 +968,22 @@ __global__ void __launch_bounds__(C::NT) gemm_direct_kernel(const Args g) {
     finish_tile<C, EPI>(acc, smem, ks, 0, 0, lane, tid, m0, n0, split, b, g, PRO == PXK_PRO_RMS ? s_rss : nullptr, KS);
 }
 
+// The split partials of one 4-column group, added in split order. Eight loads are in flight at a
+// time, all issued before any is added (the split indices past the count read the last partial
+// again and are not added), so fewer than eight splits cost one memory round trip, not one each.
+__device__ __forceinline__ f4 sum_partials(const float* P, int64_t plane, int splits, bool vec, int cnt) {
+    f4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int k = 0; k < splits; k += 8) {
+        f4 t[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) t[u] = ld4(P + min(k + u, splits - 1) * plane, vec, cnt);
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            if (k + u < splits) acc += t[u];
+    }
+    return acc;
+}
+
 // Sums the split partials of a slab of rows in split order and runs the tile epilogue. One
 // workgroup per RS x BN slab, one float4 column per thread (threads past RS rows idle when BN / 4
 // does not divide the workgroup).
@@ -998,16 +1014,7 @@ __global__ void __launch_bounds__(NT) splitk_reduce_kernel(const Args g) {
         const f4 y = Y ? ld4(Y, ve, cnt) : f4{0.f, 0.f, 0.f, 0.f};
         const int64_t plane = g.batch * g.M * g.N;
         const float* P = g.ws + (b * g.M + m) * g.N + n;
-        f4 acc = {0.f, 0.f, 0.f, 0.f};
-        int k = 0;
-        for (; k + 8 <= g.splits; k += 8) {
-            f4 t[8];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) t[u] = ld4(P + (k + u) * plane, vp, cnt);
-#pragma unroll
-            for (int u = 0; u < 8; ++u) acc += t[u];
-        }
-        for (; k < g.splits; ++k) acc += ld4(P + k * plane, vp, cnt);
+        f4 acc = sum_partials(P, plane, g.splits, vp, cnt);
         f4 v = x * acc;
         if (Y) v = y + v;
         f4 ra, rb;
@@ -1030,15 +1037,7 @@ __global__ void __launch_bounds__(NT) splitk_reduce_kernel(const Args g) {
         const bool vec = (g.N % 4) == 0 && cnt == 4;
         const int64_t plane = g.batch * g.M * g.N;
         const float* P = g.ws + (b * g.M + m) * g.N + n;
-        int k = 0;
-        for (; k + 8 <= g.splits; k += 8) {
-            f4 t[8];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) t[u] = ld4(P + (k + u) * plane, vec, cnt);
-#pragma unroll
-            for (int u = 0; u < 8; ++u) v += t[u];
-        }
-        for (; k < g.splits; ++k) v += ld4(P + k * plane, vec, cnt);
+        v = sum_partials(P, plane, g.splits, vec, cnt);
     }
     if (mine) *reinterpret_cast<f4*>(Cs + row * LDC + col) = v;
     __syncthreads();
