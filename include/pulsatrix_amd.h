@@ -155,7 +155,10 @@ int pxa_lm_relevance_rule(void* lm, const float* seed, const px_lrp_rule* rule, 
  * sums into token_rel (n*l, HBM) and targets (n int64, HBM). Asynchronous on pxa_backend_stream(). */
 int pxa_lm_explain_device(void* lm, const float* ids, int64_t n, int64_t l, float eps, int bias_in_denominator,
                           float* token_rel, int64_t* targets, const int64_t* targets_in, int unit_seed);
-/* Captures one pxa_lm_explain_device call into a HIP graph (no launch); pxa_lm_replay runs it. */
+/* Runs one pxa_lm_explain_device call eagerly (so that every buffer it needs exists at its size),
+ * then captures the same call into a HIP graph owned by this model, replacing the model's earlier
+ * graph; pxa_lm_replay(lm) runs it. A capture whose work would still free device memory is refused.
+ * The graph keeps the caller's ids / token_rel / targets pointers, which must stay valid. */
 int pxa_lm_capture_explain(void* lm, const float* ids, int64_t n, int64_t l, float eps, int bias_in_denominator,
                            float* token_rel, int64_t* targets);
 /* The same two under any rule. */
@@ -163,6 +166,10 @@ int pxa_lm_explain_device_rule(void* lm, const float* ids, int64_t n, int64_t l,
                                float* token_rel, int64_t* targets, const int64_t* targets_in, int unit_seed);
 int pxa_lm_capture_explain_rule(void* lm, const float* ids, int64_t n, int64_t l, const px_lrp_rule* rule,
                                 float* token_rel, int64_t* targets);
+/* Replays this model's captured graph on pxa_backend_stream(). Refused before any launch (-1,
+ * pxa_last_error) when nothing was captured for it, when the handle is unknown or destroyed, or when
+ * a device block the graph addresses has been freed or reallocated since the capture (a later pass
+ * at a longer length, the shared split-K pool grown): capture again. */
 int pxa_lm_replay(void* lm);
 /* Forward over ids (n*l floats, HBM) and the LRP pass seeded at each sequence's last row only: the
  * target id targets[b * target_stride] (floats in HBM) with its logit (or 1 with unit_seed). The head
@@ -185,7 +192,7 @@ int pxa_lm_explain_generated_device(void* lm, const float* ids, int64_t n, int64
  * _create returns NULL on error (pxa_last_error). pxa_lm_next_token_logits(f, tokens, n, logits,
  * vocab) writes the next token's logits after tokens[0 .. n) (host int64 ids) into logits (host,
  * vocab floats; vocab must be the model's); its signature is the callback a Generate() binding
- * takes, with f as the context. The function holds the model, which must outlive it. */
+ * takes, with f as the context. Calls after the model was destroyed are refused (-1). */
 void* pxa_lm_next_token_logits_create(void* lm, int64_t max_length);
 int pxa_lm_next_token_logits(void* f, const int64_t* tokens, int64_t n, float* logits, int64_t vocab);
 void pxa_lm_next_token_logits_destroy(void* f);
@@ -197,6 +204,9 @@ int pxa_lm_check_device_ids(void* lm);
 /* Device pointers of the last pass: logits (n*l*vocab), embedding-level relevance (n*l*d). */
 const float* pxa_lm_last_logits(void* lm);
 const float* pxa_lm_last_embedding_relevance(void* lm);
+/* Destroys the model and its captured graph (after the backend's stream drains). A destroyed handle
+ * is refused by every entry point that returns a status (-1, "unknown or destroyed model handle");
+ * destroying it again is a no-op. */
 void pxa_lm_destroy(void* lm);
 
 #ifdef __cplusplus

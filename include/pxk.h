@@ -185,7 +185,9 @@ int pxk_gemm(const pxk_gemm_desc* d, void* stream);
 
 /* pxk_gemm without a workspace argument and without any allocation: the split-K partials live in a
  * static device array of PXK_GEMM_SCRATCH_BYTES per GPU, held until the process ends (its device
- * address is looked up once per device, on the first call there). d->workspace is ignored. The
+ * address is looked up once per device, on the first split-K call there, which must be made outside
+ * any stream capture: under capture that first call returns PXK_ERR_INVALID and launches nothing;
+ * after it, captured calls are valid). d->workspace is ignored. The
  * plan, kernels and results are pxk_gemm's for the same descriptor; a plan whose partials exceed
  * the scratch returns PXK_ERR_WORKSPACE before any launch. The array is shared by every call on a
  * GPU and keeps the last call's partials: calls that overlap on one GPU (other streams, other
@@ -265,6 +267,12 @@ int pxk_dot(const float* a, const float* b, int64_t n, float* out, float* partia
 size_t pxk_reduce_partials(int64_t n);
 
 /* ---- attention ------------------------------------------------------------------------------- */
+/* Byte range of the attention forward's K or V tile buffer resource, counted from the tile's first
+ * row key0 of one head's column segment in a row-major operand with row stride ld: it ends with the
+ * head's head_dim values of the sequence's last row (l - 1), so rows past the sequence and columns
+ * past head_dim on that row read 0. The kernel's own definition, on the host: introspection for
+ * tests, no reference counterpart. -1 on bad arguments. */
+int64_t pxk_attention_kv_tile_records(int64_t l, int64_t key0, int64_t ld, int64_t head_dim);
 /* Fused causal (or full) GQA attention forward over (n, l) tokens: raw = Q K^T per query head,
  * P = softmax(scale * raw) over the visible keys, ctx = P V, in one launch. q, k, v are token-major
  * head-packed rows (row b*l + i, head h at column h*head_dim; query head h reads KV head

@@ -12,7 +12,11 @@
  *    * a failed device allocation (the raw allocator throws std::bad_alloc or returns nullptr)
  *      releases the cache and retries once, then throws std::bad_alloc;
  *    * memory goes back to the device only after the synchronize callback has run (empty_cache(),
- *      the destructor, the release before a retry), since queued kernels may still read a block.
+ *      the destructor, the release before a retry, a free whose block cannot be cached), since
+ *      queued kernels may still read a block;
+ *    * when host memory for the bookkeeping runs out, allocate() throws std::bad_alloc with the block
+ *      returned (to the cache, or to the device if it was fresh) and free() hands the block to the
+ *      device after the synchronize.
  *  Device-independent: the raw operations are injected, so the logic runs in CPU-only tests.
  *  Safe on one in-order stream: a block freed by the host was last used by work already queued on
  *  that stream, and its next user's work is queued after it.
@@ -63,6 +67,7 @@ public:
 private:
     void drop_cache_locked(bool sync);  // (synchronize,) raw_free every cached block; mutex held
     void* raw_try(size_t size);  // nullptr when the device refuses
+    bool mark_live_locked(void* p, size_t size) noexcept;  // false when the bookkeeping cannot grow
 
     RawAlloc raw_alloc_;
     RawFree raw_free_;

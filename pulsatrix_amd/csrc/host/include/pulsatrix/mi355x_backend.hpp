@@ -7,8 +7,8 @@
  *  sum() (hip_backend.hpp:64-71). Device memory comes from a size-class caching allocator with
  *  Pulsatrix's contract (pulsatrix/mi355x_allocator.hpp; hip_backend.hip:36-54).
  *  DeviceBackend virtuals outside that path (convolution, pooling, batch/group norm, recurrent
- *  and state-space cells, RL, optimizer steps, dropout, losses, backward passes) throw
- *  std::logic_error naming the op.
+ *  and state-space cells, RL, optimizer steps, dropout, losses, backward passes) run simple
+ *  gfx950 kernels (training.hip, module_ops.hip) that add in the reference CPUBackend's order.
  */
 #pragma once
 
@@ -17,6 +17,7 @@
 #include <functional>
 #include <memory>
 #include <string>
+#include <unordered_map>
 #include <vector>
 
 #include "pulsatrix/device_backend.hpp"
@@ -36,6 +37,35 @@ struct LaunchRecord {
     double bytes = 0;    ///< algorithmic HBM bytes of the launch (memory-bound kernels)
     std::function<int(void* stream)> run;  ///< relaunches it with the same arguments
     int dispatches = 0;  ///< kernels it dispatched in the last time_launch_log replay
+};
+
+class MI355XBackend;
+
+/** @brief A HIP graph of work captured on an MI355XBackend's stream for one owner (a model).
+ *
+ *  The graph addresses the device blocks its launches used at capture time. replay() refuses,
+ *  before launching anything, once any block that existed when the owner last captured and that
+ *  was allocated for this owner (or the backend's shared split-K pool) has been freed: a longer
+ *  pass regrew a buffer, the pool grew, or the owner released its buffers. Destroying the graph
+ *  waits for the backend's stream first. */
+class CapturedGraph {
+public:
+    ~CapturedGraph();
+    CapturedGraph(const CapturedGraph&) = delete;
+    CapturedGraph& operator=(const CapturedGraph&) = delete;
+    /** @brief Launches the graph on the backend's stream; throws std::logic_error if it is stale. */
+    void replay();
+    /** @brief Whether every block the graph may address is still the one it captured. */
+    [[nodiscard]] bool valid() const noexcept;
+
+private:
+    friend class MI355XBackend;
+    CapturedGraph() = default;
+    MI355XBackend* be_ = nullptr;
+    void* exec_ = nullptr;
+    uint64_t owner_ = 0;
+    uint64_t owner_retired_ = 0;   // the owner's freed pre-capture blocks at capture time
+    uint64_t shared_retired_ = 0;  // the shared pool's, likewise
 };
 
 class MI355XBackend : public DeviceBackend {
@@ -175,12 +205,23 @@ public:
     void run_gemm(pxk_gemm_desc& d);
     /** @brief Throws (std::invalid_argument / std::runtime_error) unless rc == PXK_OK. */
     static void check(int rc, const char* what);
-    /** @brief Capture everything queued between begin_capture() and end_capture() into a HIP
-     *         graph; replay() relaunches it with one call. Buffers used inside must not move. */
-    void begin_capture();
-    void end_capture();
-    void replay();
-    [[nodiscard]] bool has_graph() const noexcept { return graph_exec_ != nullptr; }
+    /** @brief Captures what `work` queues on the stream into a HIP graph owned by the caller, on
+     *         behalf of `owner` (work runs with that owner current). Nothing runs on the device. The
+     *         capture is refused (std::logic_error, no graph) if the work frees device memory while it
+     *         is captured: a captured launch may address the freed block. Run the work once eagerly
+     *         at the same shapes first, so that every buffer it uses already exists. */
+    std::unique_ptr<CapturedGraph> capture(uint64_t owner, const std::function<void()>& work);
+    /** @brief A fresh owner tag (never 0). Blocks allocated while an owner is current carry its tag;
+     *         graphs and launch logs are validated against the frees of their owner's blocks. */
+    uint64_t new_owner() noexcept { return ++owner_count_; }
+    /** @brief Sets the current owner (0: none) and returns the previous one. */
+    uint64_t set_owner(uint64_t owner) noexcept {
+        const uint64_t prev = owner_;
+        owner_ = owner;
+        return prev;
+    }
+    /** @brief Drops an owner's bookkeeping (its model is gone; its graphs must be gone first). */
+    void forget_owner(uint64_t owner);
     CachingAllocator& allocator() { return *allocator_; }
     /** @brief Counts the backend's allocations (allocate() and workspace growth). A graph captured
      *         at one count still addresses live buffers while the count is unchanged: a buffer that
@@ -192,11 +233,16 @@ public:
     template <class F>
     void launch(const char* kernel, const char* family, double flops, double bytes, const char* what, F&& f) {
         check(f(stream_), what);
-        if (logging_) log_.push_back(LaunchRecord{kernel, family, flops, bytes, std::function<int(void*)>(f)});
+        if (logging_) {
+            log_.push_back(LaunchRecord{kernel, family, flops, bytes, std::function<int(void*)>(f)});
+            if (owner_ != 0) log_owner_ = owner_;  // the model whose buffers the log addresses
+        }
         if (sync_debug_) synchronize();
     }
     /** @brief Opens (clearing) / closes the launch log. Every buffer a logged launch touches must
-     *         outlive the log: module buffers do; the GEMM workspace is pinned while it is open. */
+     *         outlive the log: module buffers do; the GEMM workspace is pinned while it is open.
+     *         Closing it snapshots the current owner's blocks as a capture does, and
+     *         time_launch_log refuses once one of them has been freed. */
     void start_launch_log();
     void stop_launch_log();
     [[nodiscard]] const std::vector<LaunchRecord>& launch_log() const noexcept { return log_; }
@@ -206,7 +252,21 @@ public:
     void time_launch_log(int reps, std::vector<double>& seconds);
 
 private:
+    friend class CapturedGraph;
+    struct Block {
+        uint64_t serial;  // allocation order
+        uint64_t owner;   // the owner current at allocation; kSharedOwner for the split-K pool
+    };
+    struct OwnerState {
+        uint64_t captured_serial = 0;  // blocks up to this serial existed at the owner's last capture
+        uint64_t retired = 0;          // how many of those have been freed since
+    };
+    static constexpr uint64_t kSharedOwner = ~uint64_t{0};
     float* workspace(size_t bytes);
+    void* track(void* p, uint64_t owner);
+    void untrack(void* p) noexcept;
+    void snapshot(uint64_t owner, uint64_t& owner_retired, uint64_t& shared_retired);
+    [[nodiscard]] bool unchanged(uint64_t owner, uint64_t owner_retired, uint64_t shared_retired) const noexcept;
 
     int device_ = 0;
     void* stream_ = nullptr;
@@ -215,9 +275,14 @@ private:
     size_t ws_bytes_ = 0;
     uint64_t allocations_ = 0;
     float* reduce_ = nullptr;  // dot/sum partials + result slot
-    void* graph_ = nullptr;
-    void* graph_exec_ = nullptr;
     bool sync_debug_ = false;
+    uint64_t owner_ = 0, owner_count_ = 0;
+    std::unordered_map<void*, Block> blocks_;             // live allocations
+    std::unordered_map<uint64_t, OwnerState> owners_;     // owners that captured a graph or a log
+    uint64_t shared_captured_serial_ = 0, shared_retired_ = 0;
+    bool capturing_ = false;
+    uint64_t frees_in_capture_ = 0;
+    uint64_t log_owner_ = 0, log_owner_retired_ = 0, log_shared_retired_ = 0;
     bool logging_ = false;
     std::vector<LaunchRecord> log_;
     std::vector<float*> retired_ws_;  // workspaces outgrown while a log was open (logged GEMMs use them)

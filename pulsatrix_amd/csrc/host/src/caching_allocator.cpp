@@ -71,9 +71,12 @@ void* CachingAllocator::allocate(size_t bytes) {
     if (hit != cached_.end() && !hit->second.empty()) {
         void* p = hit->second.back();
         hit->second.pop_back();
+        if (!mark_live_locked(p, size)) {
+            hit->second.push_back(p);  // back where it was (the vector still has the capacity)
+            throw std::bad_alloc();
+        }
         stats_.cached_bytes -= size;
         ++stats_.cache_hits;
-        live_.emplace(p, size);
         stats_.in_use_bytes += size;
         if (stats_.in_use_bytes > stats_.peak_in_use_bytes) stats_.peak_in_use_bytes = stats_.in_use_bytes;
         return p;
@@ -88,7 +91,11 @@ void* CachingAllocator::allocate(size_t bytes) {
         p = raw_try(size);
         if (p == nullptr) throw std::bad_alloc();
     }
-    live_.emplace(p, size);
+    if (!mark_live_locked(p, size)) {  // no host memory to record it: the fresh block goes straight back
+        raw_free_(p);
+        ++stats_.raw_frees;
+        throw std::bad_alloc();
+    }
     stats_.in_use_bytes += size;
     if (stats_.in_use_bytes > stats_.peak_in_use_bytes) stats_.peak_in_use_bytes = stats_.in_use_bytes;
     return p;
@@ -105,9 +112,24 @@ void CachingAllocator::free(void* ptr) noexcept {
     try {
         cached_[size].push_back(ptr);
         stats_.cached_bytes += size;
-    } catch (...) {  // no memory for the bookkeeping: hand the block straight back
-        raw_free_(ptr);
-        ++stats_.raw_frees;
+    } catch (...) {
+        // No host memory to cache it: the block goes back to the device, after the synchronize
+        // (queued work may still read it). If even that fails, it is leaked rather than freed early.
+        try {
+            if (synchronize_) synchronize_();
+            raw_free_(ptr);
+            ++stats_.raw_frees;
+        } catch (...) {
+        }
+    }
+}
+
+bool CachingAllocator::mark_live_locked(void* p, size_t size) noexcept {
+    try {
+        live_.emplace(p, size);
+        return true;
+    } catch (...) {
+        return false;
     }
 }
 

@@ -11,6 +11,7 @@
 #include <mutex>
 #include <stdexcept>
 #include <string>
+#include <unordered_set>
 #include <utility>
 #include <vector>
 
@@ -25,23 +26,27 @@ namespace {
 
 thread_local std::string g_error;
 
-template <typename F>
-int guarded(F&& f) {
-    try {
-        f();
-        return 0;
-    } catch (const std::exception& e) {
-        g_error = e.what();
-        return -1;
-    }
-}
-
 std::once_flag g_once;
 std::unique_ptr<MI355XBackend> g_backend;
 
 MI355XBackend* backend() {
     std::call_once(g_once, [] { g_backend = std::make_unique<MI355XBackend>(0); });
     return g_backend.get();
+}
+
+// Every entry point runs through guarded(): exceptions become -1 plus pxa_last_error(), and the
+// model a call named (lm_handle) stops being the backend's current owner when the call returns.
+template <typename F>
+int guarded(F&& f) {
+    int rc = 0;
+    try {
+        f();
+    } catch (const std::exception& e) {
+        g_error = e.what();
+        rc = -1;
+    }
+    if (g_backend) g_backend->set_owner(0);
+    return rc;
 }
 
 int64_t kv_heads(const px_model_config& c) { return c.num_kv_heads > 0 ? c.num_kv_heads : c.num_heads; }
@@ -205,18 +210,52 @@ struct BlockHandle {
     int64_t d = 0, n = 0, l = 0;
 };
 
+// A model handle. Its device blocks are allocated under its own owner tag, and its captured explain
+// graph (declared after the model, so destroyed first) is validated against their frees.
 struct LmHandle {
+    uint64_t owner = 0;
     std::unique_ptr<CausalLM> lm;
+    std::unique_ptr<CapturedGraph> graph;
     px_model_config cfg{};
     int64_t n = 0, l = 0;
 };
+
+// Live model handles: a destroyed or foreign handle is refused instead of dereferenced.
+std::mutex g_lm_mutex;
+std::unordered_set<const void*> g_lms;
+
+LmHandle* new_lm_handle() {
+    auto h = std::make_unique<LmHandle>();
+    h->owner = backend()->new_owner();
+    backend()->set_owner(h->owner);  // the model's buffers carry its tag
+    return h.release();
+}
+
+LmHandle* register_lm(std::unique_ptr<LmHandle> h) {
+    std::lock_guard<std::mutex> lock(g_lm_mutex);
+    g_lms.insert(h.get());
+    return h.release();
+}
+
+LmHandle* find_lm(const void* handle) {
+    std::lock_guard<std::mutex> lock(g_lm_mutex);
+    return g_lms.count(handle) ? static_cast<LmHandle*>(const_cast<void*>(handle)) : nullptr;
+}
+
+// The live model behind a handle, made the backend's current owner for the rest of the call.
+LmHandle* lm_handle(const void* handle) {
+    LmHandle* h = find_lm(handle);
+    if (h == nullptr) throw std::invalid_argument("unknown or destroyed model handle");
+    backend()->set_owner(h->owner);
+    return h;
+}
 
 LmHandle* make_lm(const px_model_config& c, const float* params) {
     if (c.vocab_size <= 0 || c.num_layers <= 0) throw std::invalid_argument("model config: vocab_size and num_layers must be positive");
     const HfModelConfig hc = hf_config(c);
     if (!c.use_rope || !c.rope_rotate_half)
         throw std::invalid_argument("model config: the causal LM uses rotate-half RoPE (ToAttentionConfig)");
-    auto h = std::make_unique<LmHandle>();
+    std::unique_ptr<LmHandle> h(new_lm_handle());
     h->cfg = c;
     h->lm = std::make_unique<CausalLM>(hc, backend());
     const float* p = params;
@@ -224,7 +263,7 @@ LmHandle* make_lm(const px_model_config& c, const float* params) {
     for (int64_t i = 0; i < c.num_layers; ++i) load_block(h->lm->layer(i), p);
     h->lm->norm().set_gamma(take(p, c.hidden_size));
     if (!c.tie_word_embeddings) h->lm->lm_head()->set_weight(take(p, c.hidden_size * c.vocab_size));
-    return h.release();
+    return register_lm(std::move(h));
 }
 
 LRPRuleConfig rule(float eps, int bias_in_denominator) {
@@ -247,19 +286,12 @@ LRPRuleConfig rule(const px_lrp_rule* p) {
     return r;
 }
 
-void capture(const std::function<void()>& work) {
-    MI355XBackend* be = backend();
-    be->begin_capture();
-    try {
-        work();
-    } catch (...) {
-        try {
-            be->end_capture();
-        } catch (...) {
-        }
-        throw;
-    }
-    be->end_capture();
+// Runs `work` once eagerly, so that every buffer it uses exists at its final size, then captures
+// it into the model's own graph (replacing any earlier one).
+void capture(LmHandle* h, const std::function<void()>& work) {
+    h->graph.reset();
+    work();
+    h->graph = backend()->capture(h->owner, work);
 }
 
 void block_relevance(void* handle, const float* r_out, const LRPRuleConfig& cfg, float* r_in) {
@@ -273,7 +305,7 @@ void block_relevance(void* handle, const float* r_out, const LRPRuleConfig& cfg,
 
 void lm_relevance(void* handle, const float* seed, const LRPRuleConfig& cfg, float* r_embed, float* r_tokens,
                   float* key_rel, float* value_rel) {
-    auto* h = static_cast<LmHandle*>(handle);
+    LmHandle* h = lm_handle(handle);
     if (h->n == 0) throw std::logic_error("CausalLM::propagate_relevance_by_layer: called before any forward()");
     CausalLM& lm = *h->lm;
     const px_model_config& c = h->cfg;
@@ -481,7 +513,7 @@ void* pxa_lm_load(const char* directory, px_model_config* cfg_out) {
     LmHandle* out = nullptr;
     guarded([&] {
         if (directory == nullptr) throw std::invalid_argument("pxa_lm_load: directory is NULL");
-        auto h = std::make_unique<LmHandle>();
+        std::unique_ptr<LmHandle> h(new_lm_handle());
         h->lm = LoadCausalLM(directory, backend());
         const HfModelConfig& hc = h->lm->config();
         px_model_config& c = h->cfg;
@@ -519,14 +551,14 @@ void* pxa_lm_load(const char* directory, px_model_config* cfg_out) {
         for (size_t i = 0; i < hc.layer_types.size() && i < 64; ++i)
             if (hc.layer_types[i] == "sliding_attention") c.sliding_layers |= uint64_t{1} << i;
         if (cfg_out) *cfg_out = c;
-        out = h.release();
+        out = register_lm(std::move(h));
     });
     return out;
 }
 
 int pxa_lm_forward(void* handle, const int64_t* ids, int64_t n, int64_t l, float* logits) {
     return guarded([&] {
-        auto* h = static_cast<LmHandle*>(handle);
+        LmHandle* h = lm_handle(handle);
         std::vector<float> f(static_cast<size_t>(n * l));
         for (size_t i = 0; i < f.size(); ++i) f[i] = static_cast<float>(ids[i]);
         Tensor out = h->lm->forward(Tensor(Shape({n, l}), backend(), f));
@@ -553,7 +585,7 @@ int pxa_lm_relevance_rule(void* handle, const float* seed, const px_lrp_rule* p,
 int pxa_lm_explain_device(void* handle, const float* ids, int64_t n, int64_t l, float eps, int bias_in_denominator,
                           float* token_rel, int64_t* targets, const int64_t* targets_in, int unit_seed) {
     return guarded([&] {
-        auto* h = static_cast<LmHandle*>(handle);
+        LmHandle* h = lm_handle(handle);
         h->lm->explain_device(ids, n, l, rule(eps, bias_in_denominator), token_rel, targets, targets_in, unit_seed != 0);
     });
 }
@@ -561,16 +593,16 @@ int pxa_lm_explain_device(void* handle, const float* ids, int64_t n, int64_t l, 
 int pxa_lm_capture_explain(void* handle, const float* ids, int64_t n, int64_t l, float eps, int bias_in_denominator,
                            float* token_rel, int64_t* targets) {
     return guarded([&] {
-        auto* h = static_cast<LmHandle*>(handle);
+        LmHandle* h = lm_handle(handle);
         const LRPRuleConfig cfg = rule(eps, bias_in_denominator);
-        capture([&] { h->lm->explain_device(ids, n, l, cfg, token_rel, targets, nullptr, false); });
+        capture(h, [&] { h->lm->explain_device(ids, n, l, cfg, token_rel, targets, nullptr, false); });
     });
 }
 
 int pxa_lm_explain_device_rule(void* handle, const float* ids, int64_t n, int64_t l, const px_lrp_rule* p,
                                float* token_rel, int64_t* targets, const int64_t* targets_in, int unit_seed) {
     return guarded([&] {
-        auto* h = static_cast<LmHandle*>(handle);
+        LmHandle* h = lm_handle(handle);
         h->lm->explain_device(ids, n, l, rule(p), token_rel, targets, targets_in, unit_seed != 0);
     });
 }
@@ -578,9 +610,9 @@ int pxa_lm_explain_device_rule(void* handle, const float* ids, int64_t n, int64_
 int pxa_lm_capture_explain_rule(void* handle, const float* ids, int64_t n, int64_t l, const px_lrp_rule* p,
                                 float* token_rel, int64_t* targets) {
     return guarded([&] {
-        auto* h = static_cast<LmHandle*>(handle);
+        LmHandle* h = lm_handle(handle);
         const LRPRuleConfig cfg = rule(p);
-        capture([&] { h->lm->explain_device(ids, n, l, cfg, token_rel, targets, nullptr, false); });
+        capture(h, [&] { h->lm->explain_device(ids, n, l, cfg, token_rel, targets, nullptr, false); });
     });
 }
 
@@ -588,7 +620,7 @@ int pxa_lm_explain_rows_device(void* handle, const float* ids, int64_t n, int64_
                                int64_t target_stride, const px_lrp_rule* p, float* token_rel, int64_t* targets_out,
                                int unit_seed) {
     return guarded([&] {
-        static_cast<LmHandle*>(handle)->lm->explain_rows_device(ids, n, l, targets, target_stride, rule(p), token_rel,
+        lm_handle(handle)->lm->explain_rows_device(ids, n, l, targets, target_stride, rule(p), token_rel,
                                                                 targets_out, unit_seed != 0);
     });
 }
@@ -596,14 +628,14 @@ int pxa_lm_explain_rows_device(void* handle, const float* ids, int64_t n, int64_
 int pxa_lm_generate_device(void* handle, float* ids, int64_t n, int64_t prompt, int64_t new_tokens, int64_t ld_ids,
                            float* picked_logit) {
     return guarded([&] {
-        static_cast<LmHandle*>(handle)->lm->generate_greedy_device(ids, n, prompt, new_tokens, ld_ids, picked_logit);
+        lm_handle(handle)->lm->generate_greedy_device(ids, n, prompt, new_tokens, ld_ids, picked_logit);
     });
 }
 
 int pxa_lm_explain_generated_device(void* handle, const float* ids, int64_t n, int64_t prompt, int64_t new_tokens,
                                     int64_t ld_ids, const px_lrp_rule* p, float* token_rel, int unit_seed) {
     return guarded([&] {
-        static_cast<LmHandle*>(handle)->lm->explain_generated_device(ids, n, prompt, new_tokens, ld_ids, rule(p),
+        lm_handle(handle)->lm->explain_generated_device(ids, n, prompt, new_tokens, ld_ids, rule(p),
                                                                      token_rel, unit_seed != 0);
     });
 }
@@ -612,14 +644,15 @@ namespace {
 struct NextTokenHandle {
     NextTokenLogitsFn fn;
     int64_t vocab;
+    const void* model;  // the LmHandle whose caches and buffers fn uses
 };
 }  // namespace
 
 void* pxa_lm_next_token_logits_create(void* handle, int64_t max_length) {
     NextTokenHandle* out = nullptr;
     guarded([&] {
-        auto* h = static_cast<LmHandle*>(handle);
-        out = new NextTokenHandle{h->lm->next_token_logits(max_length), h->lm->config().vocab_size};
+        LmHandle* h = lm_handle(handle);
+        out = new NextTokenHandle{h->lm->next_token_logits(max_length), h->lm->config().vocab_size, h};
     });
     return out;
 }
@@ -627,6 +660,8 @@ void* pxa_lm_next_token_logits_create(void* handle, int64_t max_length) {
 int pxa_lm_next_token_logits(void* f, const int64_t* tokens, int64_t n, float* logits, int64_t vocab) {
     return guarded([&] {
         auto* h = static_cast<NextTokenHandle*>(f);
+        if (h == nullptr) throw std::invalid_argument("pxa_lm_next_token_logits: NULL function handle");
+        (void)lm_handle(h->model);  // refuses a function whose model was destroyed
         if (vocab != h->vocab)
             throw std::invalid_argument("pxa_lm_next_token_logits: the logits buffer holds " + std::to_string(vocab) +
                                         " entries, the vocabulary " + std::to_string(h->vocab));
@@ -638,22 +673,40 @@ int pxa_lm_next_token_logits(void* f, const int64_t* tokens, int64_t n, float* l
 
 void pxa_lm_next_token_logits_destroy(void* f) { delete static_cast<NextTokenHandle*>(f); }
 
-int pxa_lm_replay(void*) {
-    return guarded([&] { backend()->replay(); });
+int pxa_lm_replay(void* handle) {
+    return guarded([&] {
+        LmHandle* h = lm_handle(handle);
+        if (!h->graph) throw std::logic_error("pxa_lm_replay: nothing was captured for this model");
+        h->graph->replay();
+    });
 }
 
 int pxa_lm_check_device_ids(void* handle) {
     return guarded([&] {
-        if (!static_cast<LmHandle*>(handle)->lm->device_ids_valid())
+        if (!lm_handle(handle)->lm->device_ids_valid())
             throw std::invalid_argument("EmbeddingModule::forward: index out of range [0, num_embeddings)");
     });
 }
 
-const float* pxa_lm_last_logits(void* handle) { return static_cast<LmHandle*>(handle)->lm->last_logits(); }
+const float* pxa_lm_last_logits(void* handle) {
+    LmHandle* h = find_lm(handle);
+    return h ? h->lm->last_logits() : nullptr;
+}
 const float* pxa_lm_last_embedding_relevance(void* handle) {
-    return static_cast<LmHandle*>(handle)->lm->last_embedding_relevance();
+    LmHandle* h = find_lm(handle);
+    return h ? h->lm->last_embedding_relevance() : nullptr;
 }
 
-void pxa_lm_destroy(void* handle) { delete static_cast<LmHandle*>(handle); }
+void pxa_lm_destroy(void* handle) {
+    LmHandle* h = nullptr;
+    {
+        std::lock_guard<std::mutex> lock(g_lm_mutex);
+        if (g_lms.erase(handle) == 0) return;  // NULL, unknown or already destroyed
+        h = static_cast<LmHandle*>(handle);
+    }
+    const uint64_t owner = h->owner;
+    delete h;  // its graph first (after the stream drains), then the model's buffers
+    if (g_backend) g_backend->forget_owner(owner);
+}
 
 }  // extern "C"

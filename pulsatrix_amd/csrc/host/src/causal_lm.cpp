@@ -17,35 +17,39 @@ bool HfModelConfig::is_sliding_layer(int64_t i) const {
            layer_types[static_cast<size_t>(i)] == "sliding_attention";
 }
 
+// Rotary inverse frequencies theta^(-2p / head_dim) for the pairs p < head_dim / 2, in double, then
+// the two rope_scaling kinds the loader accepts. "linear" divides every frequency by the factor.
+// "llama3" is Hugging Face's published llama3 rule (_compute_llama3_parameters): with the original
+// context C, a frequency whose wavelength 2 pi / f exceeds C / low_freq_factor is divided by the
+// factor, one whose wavelength is below C / high_freq_factor is kept, and the band between (both
+// edges included) blends the two with t = (C / wavelength - low) / (high - low) as
+// (1 - t) f / factor + t f, the operations in the order Hugging Face evaluates them.
 std::vector<double> RopeInverseFrequencies(const HfModelConfig& config) {
-    const int64_t half = config.head_dim / 2;
-    std::vector<double> inv(static_cast<size_t>(half));
-    for (int64_t i = 0; i < half; ++i)
-        inv[static_cast<size_t>(i)] = 1.0 / std::pow(static_cast<double>(config.rope_theta),
-                                                     2.0 * static_cast<double>(i) / static_cast<double>(config.head_dim));
-    if (!config.rope_scaling) return inv;
-    const HfRopeScaling& s = *config.rope_scaling;
-    if (s.type == "linear") {
-        for (double& f : inv) f /= s.factor;
-        return inv;
+    const double dim = static_cast<double>(config.head_dim);
+    std::vector<double> freq;
+    freq.reserve(static_cast<size_t>(config.head_dim / 2));
+    for (int64_t pair = 0; pair < config.head_dim / 2; ++pair)
+        freq.push_back(1.0 / std::pow(static_cast<double>(config.rope_theta), 2.0 * static_cast<double>(pair) / dim));
+    if (!config.rope_scaling) return freq;
+    const HfRopeScaling& rs = *config.rope_scaling;
+    if (rs.type == "linear") {
+        std::transform(freq.begin(), freq.end(), freq.begin(), [&](double f) { return f / rs.factor; });
+        return freq;
     }
-    if (s.type != "llama3")
-        throw std::invalid_argument("RopeInverseFrequencies: rope_scaling \"" + s.type + "\" is not supported");
-    // Hugging Face's _compute_llama3_parameters: stretch low frequencies, keep high ones,
-    // interpolate in between (wavelen == high_wavelen counts as in between).
-    const double old_len = static_cast<double>(s.original_max_position_embeddings);
-    const double low_wavelen = old_len / s.low_freq_factor, high_wavelen = old_len / s.high_freq_factor;
-    constexpr double kPi = 3.14159265358979323846;
-    for (double& f : inv) {
-        const double wavelen = 2.0 * kPi / f;
-        if (wavelen > low_wavelen) {
-            f /= s.factor;
-        } else if (wavelen >= high_wavelen) {
-            const double smooth = (old_len / wavelen - s.low_freq_factor) / (s.high_freq_factor - s.low_freq_factor);
-            f = (1.0 - smooth) * f / s.factor + smooth * f;
-        }
-    }
-    return inv;
+    if (rs.type != "llama3")
+        throw std::invalid_argument("RopeInverseFrequencies: rope_scaling \"" + rs.type + "\" is not supported");
+    const double context = static_cast<double>(rs.original_max_position_embeddings);
+    const double stretch_above = context / rs.low_freq_factor;  // longer wavelengths: divided by the factor
+    const double keep_below = context / rs.high_freq_factor;    // shorter wavelengths: unchanged
+    const double full_turn = 2.0 * 3.14159265358979323846;
+    std::transform(freq.begin(), freq.end(), freq.begin(), [&](double f) {
+        const double wavelength = full_turn / f;
+        if (wavelength > stretch_above) return f / rs.factor;
+        if (wavelength < keep_below) return f;
+        const double t = (context / wavelength - rs.low_freq_factor) / (rs.high_freq_factor - rs.low_freq_factor);
+        return (1.0 - t) * f / rs.factor + t * f;
+    });
+    return freq;
 }
 
 AttentionConfig ToAttentionConfig(const HfModelConfig& config) {

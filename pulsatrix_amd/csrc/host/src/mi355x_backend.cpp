@@ -64,8 +64,6 @@ MI355XBackend::MI355XBackend(int device_index) : device_(device_index) {
 
 MI355XBackend::~MI355XBackend() {
     if (stream_) (void)hipStreamSynchronize(S(stream_));
-    if (graph_exec_) (void)hipGraphExecDestroy(static_cast<hipGraphExec_t>(graph_exec_));
-    if (graph_) (void)hipGraphDestroy(static_cast<hipGraph_t>(graph_));
     allocator_.reset();  // synchronizes, then returns every block, before the stream goes away
     if (stream_) (void)hipStreamDestroy(S(stream_));
 }
@@ -81,18 +79,63 @@ void MI355XBackend::synchronize() { hip_check(hipStreamSynchronize(S(stream_)), 
 
 void* MI355XBackend::allocate(size_t bytes) {
     if (bytes == 0) return nullptr;
-    ++allocations_;
+    void* p = nullptr;
     try {
-        return allocator_->allocate(bytes);
+        p = allocator_->allocate(bytes);
     } catch (const std::bad_alloc&) {
         throw std::runtime_error("MI355XBackend::allocate: failed to allocate " + std::to_string(bytes) + " bytes");
     }
+    return track(p, owner_);
 }
 
 void MI355XBackend::free(void* ptr) noexcept {
+    if (ptr == nullptr) return;
+    untrack(ptr);
     // Kernels queued on the stream may still read the block; the allocator only recycles it to
     // later work on the same in-order stream, so no wait is needed.
     allocator_->free(ptr);
+}
+
+void* MI355XBackend::track(void* p, uint64_t owner) {
+    try {
+        blocks_.emplace(p, Block{++allocations_, owner});
+    } catch (...) {
+        allocator_->free(p);
+        throw;
+    }
+    return p;
+}
+
+void MI355XBackend::untrack(void* p) noexcept {
+    const auto it = blocks_.find(p);
+    if (it == blocks_.end()) return;
+    const Block b = it->second;
+    blocks_.erase(it);
+    if (capturing_) ++frees_in_capture_;
+    if (b.owner == kSharedOwner) {
+        if (b.serial <= shared_captured_serial_) ++shared_retired_;
+        return;
+    }
+    const auto o = owners_.find(b.owner);
+    if (o != owners_.end() && b.serial <= o->second.captured_serial) ++o->second.retired;
+}
+
+void MI355XBackend::snapshot(uint64_t owner, uint64_t& owner_retired, uint64_t& shared_retired) {
+    OwnerState& st = owners_[owner];
+    st.captured_serial = allocations_;
+    shared_captured_serial_ = allocations_;
+    owner_retired = st.retired;
+    shared_retired = shared_retired_;
+}
+
+bool MI355XBackend::unchanged(uint64_t owner, uint64_t owner_retired, uint64_t shared_retired) const noexcept {
+    const auto o = owners_.find(owner);
+    return o != owners_.end() && o->second.retired == owner_retired && shared_retired_ == shared_retired;
+}
+
+void MI355XBackend::forget_owner(uint64_t owner) {
+    owners_.erase(owner);
+    if (owner_ == owner) owner_ = 0;
 }
 
 void MI355XBackend::copy(void* dst, const void* src, size_t bytes, CopyDirection dir) {
@@ -123,13 +166,15 @@ void MI355XBackend::fill(void* ptr, float value, size_t n) {
 
 float* MI355XBackend::workspace(size_t bytes) {
     if (bytes > ws_bytes_) {
-        if (ws_ && logging_)
+        if (ws_ && logging_) {
             retired_ws_.push_back(ws_);  // a logged GEMM still points at it
-        else if (ws_)
+        } else if (ws_) {
+            untrack(ws_);
             allocator_->free(ws_);
+        }
+        ws_ = nullptr;
         ws_bytes_ = std::max(bytes, ws_bytes_ * 2);
-        ws_ = static_cast<float*>(allocator_->allocate(ws_bytes_));
-        ++allocations_;
+        ws_ = static_cast<float*>(track(allocator_->allocate(ws_bytes_), kSharedOwner));
     }
     return ws_;
 }
@@ -163,6 +208,7 @@ void MI355XBackend::run_gemm(pxk_gemm_desc& d) {
         if (d.x_gamma) floats += static_cast<double>(d.n);                  // the norm's gains
         if (d.row_rms) floats += static_cast<double>(d.m) * bt;              // rms written out
         const pxk_gemm_desc copy = d;
+        if (owner_ != 0) log_owner_ = owner_;
         log_.push_back(LaunchRecord{name, "gemm", 2.0 * d.m * d.n * d.k * d.batch * d.kgroups, 4.0 * floats,
                                     [copy](void* st) { return pxk_gemm(&copy, st); }});
     }
@@ -171,17 +217,29 @@ void MI355XBackend::run_gemm(pxk_gemm_desc& d) {
 
 void MI355XBackend::start_launch_log() {
     log_.clear();
-    for (float* w : retired_ws_) allocator_->free(w);
+    for (float* w : retired_ws_) {
+        untrack(w);
+        allocator_->free(w);
+    }
     retired_ws_.clear();
     logging_ = true;
+    log_owner_ = owner_;
 }
 
-void MI355XBackend::stop_launch_log() { logging_ = false; }
+void MI355XBackend::stop_launch_log() {
+    if (!logging_) return;
+    logging_ = false;
+    snapshot(log_owner_, log_owner_retired_, log_shared_retired_);
+}
 
 void MI355XBackend::time_launch_log(int reps, std::vector<double>& seconds) {
     const size_t n = log_.size();
     seconds.assign(n, 0.0);
     if (n == 0 || reps <= 0) return;
+    if (logging_) throw std::logic_error("MI355XBackend::time_launch_log: the launch log is still open");
+    if (!unchanged(log_owner_, log_owner_retired_, log_shared_retired_))
+        throw std::logic_error("MI355XBackend::time_launch_log: device memory the logged launches address was "
+                               "freed since the log closed; record the pass again");
     for (const auto& r : log_) check(r.run(stream_), "MI355XBackend::time_launch_log (warm-up)");
     // Each dispatch records its own start and end (pxk_timing_*), so a launch's time is its kernels'
     // durations as the GPU ran them, in the order and cache state of the recorded pass.
@@ -461,30 +519,61 @@ void MI355XBackend::accumulate_rows(const float* in, float* out, size_t rows, si
 
 // ---- graphs ------------------------------------------------------------------------------------
 
-void MI355XBackend::begin_capture() {
-    if (graph_exec_) {
-        (void)hipGraphExecDestroy(static_cast<hipGraphExec_t>(graph_exec_));
-        graph_exec_ = nullptr;
-    }
-    if (graph_) {
-        (void)hipGraphDestroy(static_cast<hipGraph_t>(graph_));
-        graph_ = nullptr;
-    }
-    hip_check(hipStreamBeginCapture(S(stream_), hipStreamCaptureModeThreadLocal), "MI355XBackend::begin_capture");
-}
-
-void MI355XBackend::end_capture() {
+std::unique_ptr<CapturedGraph> MI355XBackend::capture(uint64_t owner, const std::function<void()>& work) {
+    if (owner == 0) throw std::invalid_argument("MI355XBackend::capture: no owner");
+    if (capturing_) throw std::logic_error("MI355XBackend::capture: a capture is already in progress");
+    const uint64_t prev_owner = set_owner(owner);
+    hip_check(hipStreamBeginCapture(S(stream_), hipStreamCaptureModeThreadLocal), "MI355XBackend::capture");
+    capturing_ = true;
+    frees_in_capture_ = 0;
     hipGraph_t g = nullptr;
-    hip_check(hipStreamEndCapture(S(stream_), &g), "MI355XBackend::end_capture");
-    graph_ = g;
+    try {
+        work();
+    } catch (...) {
+        capturing_ = false;
+        (void)hipStreamEndCapture(S(stream_), &g);
+        if (g) (void)hipGraphDestroy(g);
+        // A runtime call the capture refused leaves its status behind as the thread's last error;
+        // clear it, or the next launch would report it.
+        (void)hipGetLastError();
+        set_owner(prev_owner);
+        throw;
+    }
+    capturing_ = false;
+    set_owner(prev_owner);
+    hip_check(hipStreamEndCapture(S(stream_), &g), "MI355XBackend::capture (end)");
+    if (frees_in_capture_ != 0) {
+        (void)hipGraphDestroy(g);
+        throw std::logic_error("MI355XBackend::capture: the captured work freed " + std::to_string(frees_in_capture_) +
+                               " device block(s) that its launches may address; run it once eagerly at the same "
+                               "shapes before capturing");
+    }
     hipGraphExec_t e = nullptr;
-    hip_check(hipGraphInstantiate(&e, g, nullptr, nullptr, 0), "MI355XBackend::end_capture (instantiate)");
-    graph_exec_ = e;
+    const hipError_t rc = hipGraphInstantiate(&e, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    hip_check(rc, "MI355XBackend::capture (instantiate)");
+    std::unique_ptr<CapturedGraph> out(new CapturedGraph());
+    out->be_ = this;
+    out->exec_ = e;
+    out->owner_ = owner;
+    snapshot(owner, out->owner_retired_, out->shared_retired_);
+    return out;
 }
 
-void MI355XBackend::replay() {
-    if (!graph_exec_) throw std::logic_error("MI355XBackend::replay: nothing was captured");
-    hip_check(hipGraphLaunch(static_cast<hipGraphExec_t>(graph_exec_), S(stream_)), "MI355XBackend::replay");
+CapturedGraph::~CapturedGraph() {
+    if (exec_) {
+        (void)hipStreamSynchronize(S(be_->stream()));  // a replay may still be running
+        (void)hipGraphExecDestroy(static_cast<hipGraphExec_t>(exec_));
+    }
+}
+
+bool CapturedGraph::valid() const noexcept { return be_->unchanged(owner_, owner_retired_, shared_retired_); }
+
+void CapturedGraph::replay() {
+    if (!valid())
+        throw std::logic_error("replay: device memory the captured graph addresses was freed or reallocated since "
+                               "the capture (a longer pass regrew a buffer, or the split-K pool grew); capture again");
+    hip_check(hipGraphLaunch(static_cast<hipGraphExec_t>(exec_), S(be_->stream())), "replay");
 }
 
 // ---- outside the path ---------------------------------------------------------------------------

@@ -62,6 +62,14 @@ __device__ __forceinline__ float row_sum4(float v) {
     return v + __shfl_xor(v, 32, kWave);
 }
 
+// Byte range of the forward's K or V tile resource, counted from the tile's first row (key0) of one
+// head's column segment in a row-major (rows, ldr) operand: it ends with the head's D values of the
+// sequence's last row (l - 1). One definition for the kernel and for pxk_attention_kv_tile_records,
+// which checks it on the host.
+__host__ __device__ inline int kv_tile_records(int l, int key0, int ldr, int D) {
+    return ((l - 1 - key0) * ldr + D) * 4;
+}
+
 // DT: head_dim in 16-wide tiles (D <= 16 DT, D % 4 == 0). VEC: l % 4 == 0 (128-bit row stores).
 template <int DT, bool VEC>
 __global__ void __launch_bounds__(kThreads) attn_fwd_kernel(const FwdArgs a) {
@@ -114,17 +122,17 @@ __global__ void __launch_bounds__(kThreads) attn_fwd_kernel(const FwdArgs a) {
     // The loads are buffer loads: a tile's rows start at a scalar base (the buffer resource, built
     // per tile with scalar instructions) and each lane's offsets are fixed for the whole loop, with
     // the head-dimension step in the instruction's immediate offset, so a tile costs no vector
-    // address arithmetic. Rows past the sequence fall outside the resource's range and read 0 (a
-    // V row there meets a zero probability anyway); columns past head_dim read finite neighbouring
-    // data (a K column there meets a zero Q fragment, a ctx row there is never stored). The range
-    // ends with the head's last row, so no load leaves the caller's rows.
+    // address arithmetic. The resource's range (kv_tile_records) ends with the head's D values of
+    // the sequence's last row: rows past the sequence, and columns past head_dim on that last row,
+    // fall outside it and read 0 (a V row there meets a zero probability anyway), so no load ever
+    // leaves the operand. Columns past head_dim on earlier rows read finite neighbouring data of the
+    // same matrix (a K column there meets a zero Q fragment, a ctx row there is never stored).
     f4 kf[2][DT], vf[2][DT];
     const int ldk = static_cast<int>(a.ldk), ldv = static_cast<int>(a.ldv);
-    const int kvcol = hk * D;
     const int koff = (c * ldk + 4 * g) * 4, voff = ((4 * g) * ldv + c) * 4;
     auto rsrc = [&](const float* base, int key0, int ldr) {
         return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base + key0 * ldr), 0,
-                                                 ((l - key0) * ldr - kvcol) * 4, 0x00020000);
+                                                 kv_tile_records(l, key0, ldr, D), 0x00020000);
     };
     auto load_k = [&](int set, int kt) {
         const int key0 = 16 * min(kt, ntile - 1);  // past the last tile: the last one again, unused
@@ -901,6 +909,15 @@ int lds_bytes_needed(int64_t head_dim, int64_t l) {
 
 }  // namespace
 
+extern "C" int64_t pxk_attention_kv_tile_records(int64_t l, int64_t key0, int64_t ld, int64_t head_dim) {
+    if (l <= 0 || key0 < 0 || key0 >= l || ld < head_dim || head_dim <= 0 ||
+        (l * ld + head_dim) * 4 >= (int64_t{1} << 31)) {
+        (void)fail(PXK_ERR_INVALID, "pxk_attention_kv_tile_records: bad arguments");
+        return -1;
+    }
+    return kv_tile_records(static_cast<int>(l), static_cast<int>(key0), static_cast<int>(ld), static_cast<int>(head_dim));
+}
+
 extern "C" int pxk_attention_supported(int64_t head_dim, int64_t seq_len, int64_t ldq, int64_t ldk, int64_t ldv) {
     return head_dim > 0 && head_dim <= 128 && head_dim % 4 == 0 && ldq % 4 == 0 && ldk % 4 == 0 && ldv >= head_dim &&
            seq_len >= 0 && seq_len <= 8192 && lds_bytes_needed(head_dim, seq_len) <= kMaxLds;
@@ -926,8 +943,9 @@ int attention_forward(const float* q, int64_t ldq, const float* k, int64_t ldk, 
     if (!aligned16(q) || !aligned16(k)) return fail(PXK_ERR_INVALID, "%s: q and k must be 16-byte aligned", who);
     if (n == 0 || l == 0) return PXK_OK;
     const int64_t blocks = n * heads * ((l + 15) / 16);
-    if (blocks > (int64_t{1} << 31) - 1 || n * heads * l * l > (int64_t{1} << 40) || l * ldk >= (int64_t{1} << 31) ||
-        l * ldv >= (int64_t{1} << 31))
+    // The K / V tile resources count bytes in 32 bits (kv_tile_records).
+    if (blocks > (int64_t{1} << 31) - 1 || n * heads * l * l > (int64_t{1} << 40) ||
+        (l * ldk + head_dim) * 4 >= (int64_t{1} << 31) || (l * ldv + head_dim) * 4 >= (int64_t{1} << 31))
         return fail(PXK_ERR_INVALID, "%s: problem too large", who);
     const int lds_ld = score_lds_ld(l);
     FwdArgs a{q, k, v, raw, p, ctx, ldq, ldk, ldv, ldctx, static_cast<int>(n), static_cast<int>(l),

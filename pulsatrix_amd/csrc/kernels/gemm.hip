@@ -462,14 +462,23 @@ constexpr int kScratchDevices = 64;
 std::mutex g_scratch_mu;
 float* g_scratch[kScratchDevices] = {};
 
-// The current device's copy of `scratch`, looked up on its first use on that device.
-int scratch_ptr(float** out) {
+// The current device's copy of `scratch`, looked up on its first use on that device. That first use
+// must not be inside a stream capture: the lookup is a runtime call, not stream work, so it is
+// refused there (one eager call on the device first makes every later captured call valid).
+int scratch_ptr(float** out, void* stream) {
     int dev = -1;
     const hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return fail(PXK_ERR_LAUNCH, "pxk_gemm_noalloc: hipGetDevice: %s", hipGetErrorString(e));
     if (dev < 0 || dev >= kScratchDevices) return fail(PXK_ERR_INVALID, "pxk_gemm_noalloc: device %d out of range", dev);
     std::lock_guard<std::mutex> lock(g_scratch_mu);
     if (g_scratch[dev] == nullptr) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        const hipError_t q = hipStreamIsCapturing(S(stream), &cs);
+        if (q != hipSuccess || cs != hipStreamCaptureStatusNone)
+            return fail(PXK_ERR_INVALID,
+                        "pxk_gemm_noalloc: the first split-K call on device %d is inside a stream capture; call it "
+                        "once outside any capture first (the scratch address is looked up then)",
+                        dev);
         void* p = nullptr;
         const hipError_t r = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
         if (r != hipSuccess || p == nullptr)
@@ -499,7 +508,7 @@ extern "C" int pxk_gemm_noalloc(const pxk_gemm_desc* d, void* stream) {
     e.workspace = nullptr;
     e.workspace_bytes = 0;
     if (need > 0) {
-        if (const int rc = scratch_ptr(&e.workspace)) return rc;
+        if (const int rc = scratch_ptr(&e.workspace, stream)) return rc;
         e.workspace_bytes = PXK_GEMM_SCRATCH_BYTES;  // the plan does not depend on the workspace: pxk_gemm
     }                                                // recomputes the one checked above
     return pxk_gemm(&e, stream);

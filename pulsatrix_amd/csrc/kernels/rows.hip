@@ -845,6 +845,8 @@ int pxk_lm_seed_head_relevance(const pxk_seed_head_desc* d, void* stream) {
     if (split ? (!d->r_b || !d->a || !d->b || !d->s) : d->r == nullptr)
         return fail(PXK_ERR_INVALID, "pxk_lm_seed_head_relevance: needs r, or a, b, s, r_a and r_b for the split");
     if (d->n * d->l > (int64_t{1} << 31) - 1) return fail(PXK_ERR_INVALID, "pxk_lm_seed_head_relevance: too many rows");
+    if ((d->b_den || d->b_den_bias) && (!split || !d->b_den))
+        return fail(PXK_ERR_INVALID, "pxk_lm_seed_head_relevance: b_den belongs to the split, its bias only with b_den");
     Targets given{};
     if (d->targets_in) {
         if (d->n > 64) return fail(PXK_ERR_INVALID, "pxk_lm_seed_head_relevance: at most 64 sequences with given targets");
@@ -858,8 +860,6 @@ int pxk_lm_seed_head_relevance(const pxk_seed_head_desc* d, void* stream) {
     PXK_LAUNCH(lm_seed_kernel, dim3(static_cast<unsigned>(d->n)), dim3(kSeedThreads), 0, S(stream), d->logits, d->l,
                d->vocab, d->targets_in ? 1 : 0, given, d->targets_out, static_cast<float*>(nullptr), d->unit);
     if (const int rc = launched("pxk_lm_seed_head_relevance (targets)")) return rc;
-    if ((d->b_den || d->b_den_bias) && (!split || !d->b_den))
-        return fail(PXK_ERR_INVALID, "pxk_lm_seed_head_relevance: b_den belongs to the split, its bias only with b_den");
     const SeedHeadArgs a{d->logits, d->x, d->e, d->targets_out, d->r, d->a, d->b, d->s, d->r_a, d->r_b,
                          d->b_den, d->b_den_bias, d->l, d->vocab, d->d, d->eps, d->unit};
     PXK_LAUNCH(seed_head_rows_kernel, dim3(static_cast<unsigned>(d->n * d->l)), dim3(kThreads), 0, S(stream), a);

@@ -4,13 +4,29 @@
 // Built and run by tests/test_allocator_cpu.py; prints one line per failed check and exits 1.
 #include <cstdio>
 #include <cstdlib>
-#include <map>
 #include <new>
-#include <set>
 
 #include "pulsatrix/mi355x_allocator.hpp"
 
 using pulsatrix::mi355x::CachingAllocator;
+
+// The next operator new throws std::bad_alloc while g_fail_next_new is set (and clears it): host
+// memory for the allocator's own bookkeeping running out at that point.
+bool g_fail_next_new = false;
+
+void* operator new(size_t n) {
+    if (g_fail_next_new) {
+        g_fail_next_new = false;
+        throw std::bad_alloc();
+    }
+    if (void* p = std::malloc(n == 0 ? 1 : n)) return p;
+    throw std::bad_alloc();
+}
+void* operator new[](size_t n) { return operator new(n); }
+void operator delete(void* p) noexcept { std::free(p); }
+void operator delete[](void* p) noexcept { std::free(p); }
+void operator delete(void* p, size_t) noexcept { std::free(p); }
+void operator delete[](void* p, size_t) noexcept { std::free(p); }
 
 namespace {
 
@@ -33,36 +49,58 @@ bool throws_bad_alloc(F f) {
     return false;
 }
 
-// Host memory standing in for HBM: counts raw allocations, frees and synchronizations, and
-// refuses requests beyond `capacity` (0 = unlimited), as hipMalloc does when HBM is full.
-struct FakeDevice {
-    size_t capacity = 0, held = 0;
+// A pretend HBM for the allocator's injected callbacks: up to 64 blocks of host memory in fixed
+// slots (so the callbacks themselves never call operator new), a byte limit (0 = none) past which
+// it refuses the way hipMalloc does when HBM is full (by throwing, or by returning nullptr when
+// `null_on_full`), and counters of raw allocations, frees and synchronizations.
+struct HostHbm {
+    struct Slot {
+        void* p = nullptr;
+        size_t bytes = 0;
+    };
+    Slot slot[64];
+    size_t limit = 0, held = 0;
     int mallocs = 0, frees = 0, syncs = 0;
-    bool return_null = false;  // fail by returning nullptr instead of throwing
-    std::map<void*, size_t> sizes;
-    std::set<void*> live;
+    bool null_on_full = false;
 
+    [[nodiscard]] bool holds(const void* p) const {
+        for (const Slot& s : slot)
+            if (s.p == p && p != nullptr) return true;
+        return false;
+    }
+    [[nodiscard]] int blocks() const {
+        int k = 0;
+        for (const Slot& s : slot) k += s.p != nullptr;
+        return k;
+    }
+    void* take(size_t bytes) {
+        if (limit != 0 && held + bytes > limit) {
+            if (null_on_full) return nullptr;
+            throw std::bad_alloc();
+        }
+        for (Slot& s : slot) {
+            if (s.p != nullptr) continue;
+            s.p = std::malloc(bytes);
+            s.bytes = bytes;
+            held += bytes;
+            ++mallocs;
+            return s.p;
+        }
+        throw std::bad_alloc();  // out of slots
+    }
+    void give(void* p) {
+        for (Slot& s : slot) {
+            if (s.p != p) continue;
+            std::free(s.p);
+            held -= s.bytes;
+            s = Slot{};
+            ++frees;
+            return;
+        }
+    }
     CachingAllocator make(size_t budget = 0) {
-        return CachingAllocator(
-            [this](size_t bytes) -> void* {
-                if (capacity != 0 && held + bytes > capacity) {
-                    if (return_null) return nullptr;
-                    throw std::bad_alloc();
-                }
-                void* p = std::malloc(bytes);
-                ++mallocs;
-                held += bytes;
-                sizes[p] = bytes;
-                live.insert(p);
-                return p;
-            },
-            [this](void* p) {
-                ++frees;
-                held -= sizes[p];
-                live.erase(p);
-                std::free(p);
-            },
-            [this] { ++syncs; }, budget);
+        return CachingAllocator([this](size_t b) { return take(b); }, [this](void* p) { give(p); },
+                                [this] { ++syncs; }, budget);
     }
 };
 
@@ -83,7 +121,7 @@ void size_classes() {
 }
 
 void freed_block_is_reused_for_its_class() {
-    FakeDevice dev;
+    HostHbm dev;
     CachingAllocator a = dev.make();
     void* p = a.allocate(100);
     a.free(p);
@@ -96,7 +134,7 @@ void freed_block_is_reused_for_its_class() {
 }
 
 void tracks_in_use_cached_and_peak() {
-    FakeDevice dev;
+    HostHbm dev;
     CachingAllocator a = dev.make();
     void* p = a.allocate(1000);
     void* q = a.allocate(2000);
@@ -111,7 +149,7 @@ void tracks_in_use_cached_and_peak() {
 }
 
 void empty_cache_synchronizes_then_releases_only_cached() {
-    FakeDevice dev;
+    HostHbm dev;
     CachingAllocator a = dev.make();
     void* kept = a.allocate(512);
     a.free(a.allocate(1024));
@@ -120,11 +158,11 @@ void empty_cache_synchronizes_then_releases_only_cached() {
     CHECK(dev.syncs > syncs);  // never hand back memory a queued kernel may still read
     CHECK(dev.frees == 1);
     CHECK(a.stats().cached_bytes == 0u);
-    CHECK(dev.live.count(kept) == 1u);
+    CHECK(dev.holds(kept));
 }
 
 void over_budget_releases_the_cache_first() {
-    FakeDevice dev;
+    HostHbm dev;
     CachingAllocator a = dev.make(4096);
     a.free(a.allocate(2048));
     const int syncs = dev.syncs;
@@ -137,7 +175,7 @@ void over_budget_releases_the_cache_first() {
 }
 
 void request_beyond_budget_throws_and_changes_nothing() {
-    FakeDevice dev;
+    HostHbm dev;
     CachingAllocator a = dev.make(4096);
     void* p = a.allocate(3000);
     CHECK(throws_bad_alloc([&] { (void)a.allocate(2000); }));
@@ -152,15 +190,15 @@ void request_beyond_budget_throws_and_changes_nothing() {
 
 void device_failure_releases_the_cache_and_retries() {
     for (int null_mode = 0; null_mode < 2; ++null_mode) {
-        FakeDevice dev;
-        dev.capacity = 4096;
-        dev.return_null = null_mode == 1;
+        HostHbm dev;
+        dev.limit = 4096;
+        dev.null_on_full = null_mode == 1;
         CachingAllocator a = dev.make();  // no budget: only the device refuses
         a.free(a.allocate(2048));
         void* p = a.allocate(3000);  // fails once (2048 held + 3072 > 4096), succeeds after the release
         CHECK(p != nullptr);
         CHECK(dev.frees == 1);
-        dev.capacity = 1;
+        dev.limit = 1;
         CHECK(throws_bad_alloc([&] { (void)a.allocate(8000); }));  // nothing left to release
         CHECK(a.stats().in_use_bytes == 3072u);
         a.free(p);
@@ -168,7 +206,7 @@ void device_failure_releases_the_cache_and_retries() {
 }
 
 void zero_bytes_and_null() {
-    FakeDevice dev;
+    HostHbm dev;
     CachingAllocator a = dev.make();
     CHECK(a.allocate(0) == nullptr);
     a.free(nullptr);
@@ -179,13 +217,13 @@ void zero_bytes_and_null() {
 }
 
 void destruction_releases_everything() {
-    FakeDevice dev;
+    HostHbm dev;
     {
         CachingAllocator a = dev.make();
         (void)a.allocate(100);  // still in use: released too, the device goes away
         a.free(a.allocate(5000));
     }
-    CHECK(dev.live.empty());
+    CHECK(dev.blocks() == 0);
     CHECK(dev.mallocs == dev.frees);
     CHECK(dev.syncs >= 1);
 }
@@ -195,12 +233,45 @@ void budget_from_environment() {
     const char* mb = std::getenv("PULSATRIX_HIP_MEMORY_BUDGET_MB");
     if (mb == nullptr) return;
     const size_t budget = static_cast<size_t>(std::strtoull(mb, nullptr, 10)) << 20;
-    FakeDevice dev;
+    HostHbm dev;
     CachingAllocator a = dev.make(budget);
     void* p = a.allocate(budget - (size_t{1} << 20));
     CHECK(p != nullptr);
     CHECK(throws_bad_alloc([&] { (void)a.allocate(size_t{2} << 20); }));
     a.free(p);
+}
+
+void bookkeeping_failure_returns_the_block() {
+    HostHbm dev;
+    CachingAllocator a = dev.make();
+    // a fresh block whose entry cannot be recorded goes straight back to the device
+    g_fail_next_new = true;
+    CHECK(throws_bad_alloc([&] { (void)a.allocate(700); }));
+    g_fail_next_new = false;
+    CHECK(dev.blocks() == 0 && dev.mallocs == 1 && dev.frees == 1);
+    CHECK(a.stats().in_use_bytes == 0u);
+    // a cached block whose entry cannot be recorded stays cached
+    void* p = a.allocate(700);
+    a.free(p);
+    const size_t cached = a.stats().cached_bytes;
+    g_fail_next_new = true;
+    CHECK(throws_bad_alloc([&] { (void)a.allocate(700); }));
+    g_fail_next_new = false;
+    CHECK(a.stats().cached_bytes == cached && a.stats().in_use_bytes == 0u);
+    CHECK(a.allocate(700) == p);  // and is handed out by the next request of its class
+}
+
+void free_without_cache_room_synchronizes_before_releasing() {
+    HostHbm dev;
+    CachingAllocator a = dev.make();
+    void* p = a.allocate(3000);  // a size class with no cache entry yet: caching it needs a new node
+    const int syncs = dev.syncs;
+    g_fail_next_new = true;
+    a.free(p);
+    g_fail_next_new = false;
+    CHECK(!dev.holds(p) && dev.frees == 1);
+    CHECK(dev.syncs > syncs);  // queued work may still read it
+    CHECK(a.stats().in_use_bytes == 0u && a.stats().cached_bytes == 0u);
 }
 
 }  // namespace
@@ -216,6 +287,8 @@ int main() {
     zero_bytes_and_null();
     destruction_releases_everything();
     budget_from_environment();
+    bookkeeping_failure_returns_the_block();
+    free_without_cache_room_synchronizes_before_releasing();
     std::printf("%s\n", g_failed == 0 ? "all allocator checks passed" : "allocator checks failed");
     return g_failed == 0 ? 0 : 1;
 }

@@ -23,7 +23,8 @@ pytestmark = pytest.mark.gpu
 
 def need_ref():
     if oc.ref() is None:
-        pytest.skip("oracle/_ref is not built")
+        pytest.fail("oracle/_ref is not built: the boundary evidence needs it "
+                    "(__graft_entry__.build() builds it where the reference sources are)")
 
 
 def oracle_last_logits(cfg, params, tokens):

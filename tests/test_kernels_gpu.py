@@ -73,6 +73,31 @@ def test_decode_and_row_entry_points_reject_bad_arguments_without_launching():
     assert lib.pxk_decode_attention(p, p, p, 64, p, p, 1, 1, 1, 64, 0, 1, f(1.0), None, 0, None) == 3
 
 
+class SeedHeadDesc(ctypes.Structure):
+    """pxk_seed_head_desc (include/pxk.h)."""
+    _fields_ = [("logits", ctypes.c_void_p), ("x", ctypes.c_void_p), ("e", ctypes.c_void_p),
+                ("n", ctypes.c_int64), ("l", ctypes.c_int64), ("vocab", ctypes.c_int64), ("d", ctypes.c_int64),
+                ("eps", ctypes.c_float), ("unit", ctypes.c_int32), ("targets_in", ctypes.c_void_p),
+                ("targets_out", ctypes.c_void_p), ("r", ctypes.c_void_p), ("a", ctypes.c_void_p),
+                ("b", ctypes.c_void_p), ("s", ctypes.c_void_p), ("r_a", ctypes.c_void_p), ("r_b", ctypes.c_void_p),
+                ("b_den", ctypes.c_void_p), ("b_den_bias", ctypes.c_void_p)]
+
+
+def test_seed_head_relevance_rejects_bad_descriptors_without_launching():
+    """CPU-side: a b_den without the split (or a bias without b_den) is refused before the targets
+    kernel launches, so nothing is written (a launch here would fail with PXK_ERR_LAUNCH instead)."""
+    skip_if_device_present()
+    lib = N.pxk()
+    p = 4096
+    d = SeedHeadDesc(logits=p, x=p, e=p, n=1, l=4, vocab=16, d=8, eps=1e-9, unit=0, targets_out=p, r=p, b_den=p)
+    assert lib.pxk_lm_seed_head_relevance(ctypes.byref(d), None) == 1
+    assert b"b_den belongs to the split" in lib.pxk_last_error()
+    d = SeedHeadDesc(logits=p, x=p, e=p, n=1, l=4, vocab=16, d=8, eps=1e-9, unit=0, targets_out=p, a=p, b=p, s=p,
+                     r_a=p, r_b=p, b_den_bias=p)
+    assert lib.pxk_lm_seed_head_relevance(ctypes.byref(d), None) == 1
+    assert b"b_den belongs to the split" in lib.pxk_last_error()
+
+
 def gemm_tol(k):
     return 1e-4 * max(1.0, k / 1024.0)
 

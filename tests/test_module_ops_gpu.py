@@ -36,7 +36,8 @@ def slots_vs_cpu(lib, name, op, ins, outs, tail, nin, nout, rel=1e-5, exact=()):
     (None for unused slots; outs hold the initial contents, e.g. zeroed carries and states)."""
     cpu = oc.ref()
     if cpu is None:
-        pytest.skip("oracle/_ref/libpxref.so was not built")
+        pytest.fail("oracle/_ref/libpxref.so was not built: the boundary evidence needs it "
+                    "(__graft_entry__.build() builds it where the reference sources are)")
     vp = ctypes.c_void_p
     h_in = [None if a is None else np.ascontiguousarray(a, np.float32).copy() for a in ins]
     h_out = [None if a is None else np.ascontiguousarray(a, np.float32).copy() for a in outs]

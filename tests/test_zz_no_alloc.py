@@ -81,3 +81,56 @@ def test_gemm_noalloc_refuses_plans_beyond_the_scratch_before_launching():
     assert N.pxk().pxk_gemm_noalloc(ctypes.byref(desc), None) == 3
     assert b"static scratch" in N.pxk().pxk_last_error()
     assert N.pxk().pxk_gemm_noalloc(None, None) == 1
+
+
+_CAPTURE_CHILD = r'''
+import ctypes, sys
+import numpy as np
+sys.path[:0] = [sys.argv[1], sys.argv[1] + "/tests"]
+import torch
+import gpu_util as G
+from pulsatrix_amd import native as N
+import test_zz_no_alloc as T
+
+desc, outs = T.head_relevance_desc(torch, 96, 200, 3000, 4)
+desc.splits = 6
+side = torch.cuda.Stream()
+torch.cuda.synchronize()
+g = torch.cuda.CUDAGraph()
+desc.c = N.operand(outs[1].data_ptr(), desc.n)
+with torch.cuda.graph(g, stream=side):
+    rc_first = N.pxk().pxk_gemm_noalloc(ctypes.byref(desc), ctypes.c_void_p(side.cuda_stream))
+msg = N.pxk().pxk_last_error().decode()
+print("first-call-under-capture rc", rc_first, flush=True)
+assert rc_first == 1 and "inside a stream capture" in msg, (rc_first, msg)
+ref, got, _ = T.run_pair(torch, desc, outs)  # one eager call on the device: the scratch address is known
+assert np.array_equal(got, ref)
+out = G.keep(torch.full((96, 200), float("nan"), device="cuda"))
+desc.c = N.operand(out.data_ptr(), desc.n)
+g2 = torch.cuda.CUDAGraph()
+with torch.cuda.graph(g2, stream=side):
+    rc = N.pxk().pxk_gemm_noalloc(ctypes.byref(desc), ctypes.c_void_p(side.cuda_stream))
+assert rc == 0, N.pxk().pxk_last_error()
+for i in range(3):  # replays, with eager work between them
+    out.fill_(float("nan"))
+    torch.cuda.synchronize()
+    g2.replay()
+    torch.cuda.synchronize()
+    assert np.array_equal(G.host(out), ref), "replay %d" % i
+    T.run_pair(torch, desc, outs)
+print("captured replays match pxk_gemm", flush=True)
+'''
+
+
+@pytest.mark.gpu
+def test_gemm_noalloc_first_call_under_capture_refused_then_captured_calls_replay():
+    """In a fresh process, so that the first split-K call on the device is the captured one: it is
+    refused without launching; after one eager call, a captured call replays to pxk_gemm's bits."""
+    import os
+    import subprocess
+    import sys
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, "-c", _CAPTURE_CHILD, root], capture_output=True, text=True, timeout=300)
+    print(r.stdout)
+    assert r.returncode == 0, r.stdout + r.stderr
