@@ -5,6 +5,8 @@
     python bench.py --kernel-probe    # 256 MiB copy + LM-head relevance GEMM, for rocprofv3 --pmc runs
     python bench.py --rule gamma      # the same step under Zennit's Gamma(0.25) (or zplus, alpha2beta1, zbox)
     python bench.py --decode          # Gemma-3-270m shape: batched KV-cached greedy decode + AttnLRP per token
+    python bench.py --l1b             # Llama-3.2-1B shape, batch 8 x 1024: the explain step at large shapes
+    python bench.py --block           # config B: one TransformerBlock, GPU and reference CPUBackend
 
 Workload: the SmolLM2-135M-shaped causal LM (30 layers, hidden 576, 9 query / 3 KV heads of 64,
 SwiGLU FFN 1536, vocab 49152, tied embeddings, RMSNorm eps 1e-5, RoPE theta 100000), fp32,
@@ -19,7 +21,8 @@ replayed in order with HIP events on the backend's stream): `gemm_pct_peak` is t
 the step's GEMM launches over their summed time against MI355X's 157.3 TFLOP/s dense fp32 matrix
 peak, and `roofline` is the kernel variant with the most time per step.
 `cpu_baseline` times the reference CPUBackend (oracle/_ref where built, else the oracle
-restatement) on the host cores: one complete pass of the same 30-layer model.
+restatement) on the host cores: the median of three complete passes of the same 30-layer model
+after a full-depth warm-up.
 """
 import argparse
 import ctypes
@@ -66,6 +69,17 @@ S_CONFIG = dict(vocab_size=49152, hidden_size=576, num_layers=30, num_heads=9, n
                 intermediate_size=1536, rms_norm_eps=1e-5, rope_theta=100000.0, use_rope=1, rope_rotate_half=1,
                 causal=1, qkv_bias=0, out_bias=0, mlp_bias=0, tie_word_embeddings=1, reserved=0)
 BATCH, SEQ, SEED = 1, 512, 1234
+
+# Llama-3.2-1B's shape (random init), batch 8 x 1024: the large-shape GEMM and attention regime. The
+# CPU baseline runs a bounded sample of it, one sequence of L1B_CPU_SEQ tokens at the full depth.
+L1B_CONFIG = dict(S_CONFIG, vocab_size=128256, hidden_size=2048, num_layers=16, num_heads=32, num_kv_heads=8,
+                  head_dim=64, intermediate_size=8192, rope_theta=500000.0)
+L1B_BATCH, L1B_SEQ, L1B_CPU_SEQ = 8, 1024, 128
+
+# Config B: one block at the SmolLM2 widths, theta 10000, seq 128.
+B_CONFIG = dict(hidden_size=576, num_heads=9, num_kv_heads=3, head_dim=64, intermediate_size=1536, rms_norm_eps=1e-5,
+                rope_theta=10000.0)
+B_SEQ = 128
 
 # The rules --rule selects (LRPRuleConfig fields; LRPRule order 0 Epsilon, 1 Gamma, 2 AlphaBeta, 3 ZBox):
 # LXT's AttnLRP (the default, and the headline metric) and Zennit's affine rules at their usual settings.
@@ -116,10 +130,21 @@ def gemm_flops_per_sequence(c, L, causal_effective, linear_factor=1):
     return fwd + rel
 
 
-def time_cpu_baseline(cfg_fields, seq, rule_name="lxt"):
+def attention_executed_flops(c, L, n):
+    """MFMA work the fused attention kernels of one explain step execute: every L x L x D product over
+    the visible 16 x 16 tiles of the causal triangle (nrb (nrb + 1) / 2 tiles per head): the forward's
+    two (Q K^T, P V), the q side's three (Q K^T again, s_pv V^T, s K) and the key side's two (s^T Q,
+    P^T s_pv), per query head and sequence."""
+    H, D, layers = c["num_heads"], c["head_dim"], c["num_layers"]
+    nrb = (L + 15) // 16
+    per_product = nrb * (nrb + 1) // 2 * 2.0 * 16 * 16 * D
+    return layers * n * H * 7 * per_product
+
+
+def time_cpu_baseline(cfg_fields, seq, rule_name="lxt", batch=1, timed=3):
     """Reference CPUBackend (oracle/_ref where built, else the oracle restatement) on the host cores:
-    the full model, one warm-up pass at 1 layer (threads, page faults), then one complete timed
-    forward + argmax seed + relevance pass at the full depth."""
+    the model built once, one full-depth warm-up pass (threads, page faults), then `timed` complete
+    forward + argmax seed + relevance passes at the full depth; the median is reported."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import oracle_ctypes as oc
 
@@ -128,31 +153,33 @@ def time_cpu_baseline(cfg_fields, seq, rule_name="lxt"):
     if lib is None:
         lib, kind = oc.oracle(), "port"
         lib.lib.pxo_set_split_threads(1)  # CPUBackend runs lrp_linear and the bilinear rule on one thread
-    ids = np.random.RandomState(SEED).randint(0, cfg_fields["vocab_size"], size=(1, seq))
+    ids = np.random.RandomState(SEED).randint(0, cfg_fields["vocab_size"], size=(batch, seq))
+    cfg = oc.model_config(**cfg_fields)
+    lm = lib.lm(cfg, oc.synthetic_params(cfg, SEED))
 
-    def one_pass(fields):
-        cfg = oc.model_config(**fields)
-        lm = lib.lm(cfg, oc.synthetic_params(cfg, SEED))
+    def one_pass():
         t0 = time.perf_counter()
         logits = lm.forward(ids)
         seed = np.zeros_like(logits)
-        t = int(np.argmax(logits[0, -1]))
-        seed[0, -1, t] = logits[0, -1, t]
+        for b in range(batch):
+            t = int(np.argmax(logits[b, -1]))
+            seed[b, -1, t] = logits[b, -1, t]
         lm.relevance_rule(seed, rule)
         return time.perf_counter() - t0
 
-    warm = one_pass(dict(cfg_fields, num_layers=1))
-    full = one_pass(cfg_fields)
+    warm = one_pass()
+    runs = [one_pass() for _ in range(timed)]
+    med = float(np.median(runs))
     cores = oc.oracle().lib.pxo_get_threads()
     return {
-        "value": round(seq / full, 3),
+        "value": round(batch * seq / med, 3),
         "unit": "tokens/s",
         "cores": int(cores),
         "kind": kind,
-        "sample": "1 sequence x %d tokens, the full %d-layer model: one complete timed forward + argmax seed + "
-                  "relevance pass (%.1f s) after a 1-layer warm-up pass (%.1f s); GEMMs on %d std::threads "
+        "sample": "%d sequence(s) x %d tokens, the full %d-layer model: median of %d timed forward + argmax seed + "
+                  "relevance passes (%s s) after one full-depth warm-up pass (%.1f s); GEMMs on %d std::threads "
                   "(cpu_backend.cpp:38-59), everything else single-threaded"
-                  % (seq, cfg_fields["num_layers"], full, warm, cores),
+                  % (batch, seq, cfg_fields["num_layers"], timed, ", ".join("%.1f" % r for r in runs), warm, cores),
         "cpu_model": cpu_model(),
         "nproc": os.cpu_count(),
     }
@@ -184,7 +211,7 @@ def summarize_launches(launches):
     return {"kernels": ordered, "families": families, "seconds": sum(r["seconds"] for r in launches)}
 
 
-def kernel_row(k):
+def kernel_row(k, traffic=STEP_KERNEL_TRAFFIC):
     row = {"kernel": k["kernel"], "calls_per_step": k["calls"], "avg_us": round(k["seconds"] / k["calls"] * 1e6, 2),
            "us_per_step": round(k["seconds"] * 1e6, 1)}
     if k["flops"] > 0:
@@ -195,8 +222,8 @@ def kernel_row(k):
         row.update(gbs=round(gbs, 1), frac=round(gbs / HBM_PEAK_GBS, 4))
     if k["bytes"] > 0:
         row["algorithmic_mb"] = round(k["bytes"] / k["calls"] / 1e6, 2)
-    if k["kernel"] in STEP_KERNEL_TRAFFIC:
-        row["hbm_mb"] = round(STEP_KERNEL_TRAFFIC[k["kernel"]] / 1e6, 2)
+    if k["kernel"] in traffic:
+        row["hbm_mb"] = round(traffic[k["kernel"]] / 1e6, 2)
     return row
 
 
@@ -555,7 +582,13 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--mode", choices=("graph", "eager"), default="graph")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--layers", type=int, default=S_CONFIG["num_layers"], help=argparse.SUPPRESS)
+    ap.add_argument("--layers", type=int, default=0, help=argparse.SUPPRESS)
+    ap.add_argument("--l1b", action="store_true",
+                    help="the Llama-3.2-1B-shaped explain step (16 layers, hidden 2048, 32/8 heads, FFN 8192, vocab "
+                         "128256, theta 500000) over batch 8 x 1024 instead of the headline S workload")
+    ap.add_argument("--block", action="store_true",
+                    help="config B: one TransformerBlock forward + epsilon-LRP relevance at seq 128, GPU and "
+                         "reference CPUBackend (2 warm-ups, median of 10)")
     ap.add_argument("--profile-reps", type=int, default=5,
                     help="replays of the step's recorded launches for the per-kernel times (default 5)")
     ap.add_argument("--kernel-probe", action="store_true",
@@ -600,22 +633,44 @@ def main():
         decode_bench(args, torch, N, models)
         return
 
-    fields = dict(S_CONFIG, num_layers=args.layers)
+    if args.block:
+        block_bench(args, N, models)
+        return
+    if args.l1b:
+        explain_bench(args, torch, N, models, dict(L1B_CONFIG, num_layers=args.layers or L1B_CONFIG["num_layers"]),
+                      L1B_BATCH, L1B_SEQ, "l1b")
+        return
+    explain_bench(args, torch, N, models, dict(S_CONFIG, num_layers=args.layers or S_CONFIG["num_layers"]), BATCH,
+                  SEQ, "s512")
+
+
+RULE_TEXT = {"lxt": "LxtAttnLrpConfig: eps 1e-9, bias in denominator",
+             "eps": "LRPRuleConfig{1e-6}: the default pre-bias epsilon rule",
+             "gamma": "Gamma(0.25) on every Linear and the head, eps 1e-6 elsewhere",
+             "zplus": "ZPlus (AlphaBeta 1, 0) on every Linear and the head, eps 1e-6 elsewhere",
+             "alpha2beta1": "AlphaBeta(2, 1) on every Linear and the head, eps 1e-6 elsewhere",
+             "zbox": "ZBox(-3, 3) on every Linear and the head, eps 1e-6 elsewhere"}
+
+
+def explain_bench(args, torch, N, models, fields, batch, seq, which):
+    """The explain step (forward logits, on-device argmax seed at each sequence's last position, the
+    relevance pass, per-token sums, the token relevance to pinned host memory) timed over K steps;
+    the per-kernel table from the step's own launches; the CPU baseline on a bounded sample."""
     cfg = N.model_config(**fields)
     t_setup = time.perf_counter()
     lm = models.CausalLM(cfg, seed=SEED, std=0.02)
-    ids_host = np.random.RandomState(SEED).randint(0, cfg.vocab_size, size=(BATCH, SEQ)).astype(np.float32)
+    ids_host = np.random.RandomState(SEED).randint(0, cfg.vocab_size, size=(batch, seq)).astype(np.float32)
     ids = torch.from_numpy(ids_host).cuda()
-    tok = torch.empty(BATCH * SEQ, device="cuda")
-    tgt = torch.empty(BATCH, dtype=torch.int64, device="cuda")
-    tok_host = torch.empty(BATCH * SEQ, pin_memory=True)  # each step's relevance D2H lands here
+    tok = torch.empty(batch * seq, device="cuda")
+    tgt = torch.empty(batch, dtype=torch.int64, device="cuda")
+    tok_host = torch.empty(batch * seq, pin_memory=True)  # each step's relevance D2H lands here
     torch.cuda.synchronize()
     stream = torch.cuda.ExternalStream(models.stream())
 
     rule = N.lrp_rule(**RULES[args.rule])
 
     def eager_step():
-        lm.explain_device_rule(ids.data_ptr(), BATCH, SEQ, rule, tok.data_ptr(), tgt.data_ptr())
+        lm.explain_device_rule(ids.data_ptr(), batch, seq, rule, tok.data_ptr(), tgt.data_ptr())
 
     run = eager_step
     if args.mode == "graph":
@@ -630,7 +685,7 @@ def main():
         eager_step()
     models.synchronize()
     if args.mode == "graph":
-        lm.capture_explain_rule(ids.data_ptr(), BATCH, SEQ, rule, tok.data_ptr(), tgt.data_ptr())
+        lm.capture_explain_rule(ids.data_ptr(), batch, seq, rule, tok.data_ptr(), tgt.data_ptr())
         for _ in range(max(1, args.warmup)):
             step()
         models.synchronize()
@@ -655,11 +710,11 @@ def main():
         print("bench.py: non-finite relevance", file=sys.stderr)
         sys.exit(1)
 
-    tokens = BATCH * SEQ * args.steps
+    tokens = batch * seq * args.steps
     value = tokens / wall
     lf = LINEAR_RELEVANCE_GEMMS[args.rule]
-    flops_dense = gemm_flops_per_sequence(fields, SEQ, False, lf) * BATCH
-    flops_causal = gemm_flops_per_sequence(fields, SEQ, True, lf) * BATCH
+    flops_dense = gemm_flops_per_sequence(fields, seq, False, lf) * batch
+    flops_causal = gemm_flops_per_sequence(fields, seq, True, lf) * batch
 
     # ---- per-kernel times of the step's own launches, HIP events on the backend's stream ------
     # One eager step with the launch log open records every launch (kernel variant, arguments,
@@ -679,16 +734,17 @@ def main():
         achieved, peak, unit = dom["flops"] / dom["seconds"] / 1e12, FP32_MFMA_PEAK_TFLOPS, "TFLOP/s"
     else:
         achieved, peak, unit = dom["bytes"] / dom["seconds"] / 1e9, HBM_PEAK_GBS, "GB/s"
-    traffic = STEP_KERNEL_TRAFFIC.get(dom["kernel"])
+    traffic_table = STEP_KERNEL_TRAFFIC if which == "s512" else {}  # measured for the S step's plans only
+    traffic = traffic_table.get(dom["kernel"])
+    # Work the step executes: its GEMM launches' 2 M N K plus the attention kernels' MFMA products
+    # over the causal tiles (no dense head relevance: the seeded rows alone run).
+    attn_exec = attention_executed_flops(fields, seq, batch) if attn is not None else 0.0
+    flops_exec = (gemm["flops"] if gemm else 0.0) + attn_exec
 
-    rule_text = {"lxt": "LxtAttnLrpConfig: eps 1e-9, bias in denominator",
-                 "eps": "LRPRuleConfig{1e-6}: the default pre-bias epsilon rule",
-                 "gamma": "Gamma(0.25) on every Linear and the head, eps 1e-6 elsewhere",
-                 "zplus": "ZPlus (AlphaBeta 1, 0) on every Linear and the head, eps 1e-6 elsewhere",
-                 "alpha2beta1": "AlphaBeta(2, 1) on every Linear and the head, eps 1e-6 elsewhere",
-                 "zbox": "ZBox(-3, 3) on every Linear and the head, eps 1e-6 elsewhere"}[args.rule]
+    shape = {"s512": "SmolLM2-135M-shaped causal LM", "l1b": "Llama-3.2-1B-shaped causal LM"}[which]
     out = {
-        "metric": "forward+AttnLRP tokens/s, 135M-shape LM seq 512; GEMM % fp32 MFMA peak",
+        "metric": {"s512": "forward+AttnLRP tokens/s, 135M-shape LM seq 512; GEMM % fp32 MFMA peak",
+                   "l1b": "forward+AttnLRP tokens/s, Llama-3.2-1B-shape LM 8 x 1024; GEMM % fp32 MFMA peak"}[which],
         "value": round(value, 2),
         "unit": "tokens/s",
         "n_gpus": 1,
@@ -701,18 +757,25 @@ def main():
         "dtype": "fp32",
         "data": "synthetic: random-init N(0,0.02) weights from seed %d, uniform-random token ids" % SEED,
         "config": {
-            "workload": "SmolLM2-135M-shaped causal LM forward + AttnLRP (%s), argmax seed at the last "
-                        "position, batch 1 x seq 512" % rule_text,
-            "layers": fields["num_layers"], "hidden": 576, "heads": "9/3", "head_dim": 64, "ffn": 1536,
-            "vocab": 49152, "tied": True, "rope_theta": 100000.0, "global_batch": BATCH, "seq_len": SEQ,
+            "workload": "%s forward + AttnLRP (%s), argmax seed at the last position of each sequence, batch %d x "
+                        "seq %d" % (shape, RULE_TEXT[args.rule], batch, seq),
+            "layers": fields["num_layers"], "hidden": fields["hidden_size"],
+            "heads": "%d/%d" % (fields["num_heads"], fields["num_kv_heads"]), "head_dim": fields["head_dim"],
+            "ffn": fields["intermediate_size"], "vocab": fields["vocab_size"], "tied": True,
+            "rope_theta": fields["rope_theta"], "global_batch": batch, "seq_len": seq,
             "parallelism": "single GPU", "mode": args.mode,
         },
         "timing": "value = tokens of K steps / wall time of the K back-to-back steps between synchronisations "
                   "(a mean, not a per-step median); each step is the whole path plus an asynchronous copy of "
                   "the token relevance to pinned host memory",
         "gpu_time_ms_per_step": round(gpu_s / args.steps * 1e3, 4),
-        "path_gemm_gflop_per_step": {"dense": round(flops_dense / 1e9, 2), "causal": round(flops_causal / 1e9, 2)},
+        "path_gemm_gflop_per_step": {"dense": round(flops_dense / 1e9, 2), "causal": round(flops_causal / 1e9, 2),
+                                     "executed": round(flops_exec / 1e9, 2)},
         "path_tflops_dense": round(flops_dense * args.steps / wall / 1e12, 2),
+        "path_tflops_executed": round(flops_exec * args.steps / wall / 1e12, 2),
+        "path_flops_note": "dense: the reference's count (every L^2 attention square, the dense head relevance); "
+                           "executed: the step's GEMM launches (the head relevance runs on the seeded rows alone) "
+                           "plus the attention kernels' MFMA products over the causal tiles",
         "gemm_pct_peak": round(100.0 * gemm["flops"] / gemm["seconds"] / 1e12 / FP32_MFMA_PEAK_TFLOPS, 2),
         "gemm": {"launches_per_step": gemm["calls"], "gflop_per_step": round(gemm["flops"] / 1e9, 2),
                  "ms_per_step": round(gemm["seconds"] * 1e3, 4),
@@ -722,7 +785,9 @@ def main():
                         "recorded launches are replayed in step order on the step's buffers"},
         "attention": None if attn is None else {
             "launches_per_step": attn["calls"], "gflop_per_step_dense": round(attn["flops"] / 1e9, 2),
+            "gflop_per_step_executed": round(attn_exec / 1e9, 2),
             "ms_per_step": round(attn["seconds"] * 1e3, 4), "tflops_dense": round(attn["flops"] / attn["seconds"] / 1e12, 2),
+            "tflops_executed": round(attn_exec / attn["seconds"] / 1e12, 2),
             "pct_peak_dense": round(100.0 * attn["flops"] / attn["seconds"] / 1e12 / FP32_MFMA_PEAK_TFLOPS, 2)},
         "launches_per_step": len(launches),
         "kernel_ms_per_step": round(prof["seconds"] * 1e3, 4),
@@ -740,12 +805,87 @@ def main():
             "algorithmic_gflop_per_launch": round(dom["flops"] / dom["calls"] / 1e9, 4),
             "algorithmic_bytes_per_launch": int(dom["bytes"] / dom["calls"]),
         },
-        "step_kernels": [kernel_row(k) for k in prof["kernels"][:16]],
+        "step_kernels": [kernel_row(k, traffic_table) for k in prof["kernels"][:16]],
         "setup_s": round(setup_s, 1),
     }
     if not args.no_cpu_baseline:
-        out["cpu_baseline"] = time_cpu_baseline(fields, SEQ, args.rule)
+        if which == "s512":
+            out["cpu_baseline"] = time_cpu_baseline(fields, seq, args.rule)
+        else:
+            # A bounded sample: one sequence of L1B_CPU_SEQ tokens at the full depth (the whole
+            # 8 x 1024 batch would take the host cores hours).
+            cb = time_cpu_baseline(fields, L1B_CPU_SEQ, args.rule, timed=1)
+            cb["sample"] = "bounded sample, not the GPU's batch: " + cb["sample"]
+            out["cpu_baseline"] = cb
         out["gpu_vs_cpu"] = round(value / out["cpu_baseline"]["value"], 1)
+    del lm
+    print(json.dumps(out), flush=True)
+
+
+def block_bench(args, N, models):
+    """Config B: one TransformerBlock (hidden 576, 9 / 3 heads of 64, SwiGLU FFN 1536, RMSNorm eps
+    1e-5, RoPE theta 10000), weights N(0, 0.02) from a seed with RMSNorm gamma 1, x ~ N(0, 1) of shape
+    (1, 128, 576); forward, then epsilon-LRP (LRPRuleConfig{1e-6}) relevance from R_out = y at
+    channel 0 (LRPSeed::OutputValue) back to the block input. Host arrays in and out on both sides
+    (the block's public forward() / propagate_relevance()). 2 warm-ups, then the median of 10 timed
+    runs, on the MI355X path and on the reference CPUBackend."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle_ctypes as oc
+
+    cfg = oc.model_config(**B_CONFIG)
+    params = oc.synthetic_params(cfg, SEED, block=True)
+    x = oc.fill_normal(B_SEQ * B_CONFIG["hidden_size"], SEED + 1, 1.0).reshape(1, B_SEQ, B_CONFIG["hidden_size"])
+    gpu = models.Block(N.ModelConfig(**{f: getattr(cfg, f) for f, _ in cfg._fields_}), params)
+    lib, kind = oc.ref(), "reference"
+    if lib is None:
+        lib, kind = oc.oracle(), "port"
+    cpu = lib.block(cfg, params)
+
+    def run(block):
+        t0 = time.perf_counter()
+        y = block.forward(x)
+        seed = np.zeros_like(y)
+        seed[..., 0] = y[..., 0]
+        r = block.relevance(seed, 1e-6, False)
+        return time.perf_counter() - t0, y, r
+
+    def timed(block):
+        for _ in range(2):
+            run(block)
+        runs = [run(block) for _ in range(10)]
+        return float(np.median([t for t, _, _ in runs])), runs[-1][1], runs[-1][2]
+
+    g_s, g_y, g_r = timed(gpu)
+    c_s, c_y, c_r = timed(cpu)
+    y_err = float(np.abs(g_y - c_y).max() / max(1.0, np.abs(c_y).max()))
+    r_err = float(np.abs(g_r - c_r).max() / np.abs(c_r).max())
+    if not (y_err <= 1e-4 and r_err <= 1e-3):
+        print("bench.py: config B results differ from the CPU reference (%.2e, %.2e)" % (y_err, r_err), file=sys.stderr)
+        sys.exit(1)
+    out = {
+        "metric": "TransformerBlock forward + epsilon-LRP relevance, config B (seq 128): ms per call, host to host",
+        "value": round(g_s * 1e3, 4),
+        "unit": "ms",
+        "n_gpus": 1,
+        "steps": 10,
+        "warmup": 2,
+        "higher_is_better": False,
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic: N(0,0.02) weights from seed %d (RMSNorm gamma 1), x ~ N(0,1)" % SEED,
+        "config": {"workload": "one Llama-style TransformerBlock, hidden 576, 9/3 heads of 64, SwiGLU 1536, "
+                               "theta 10000, batch 1 x seq 128; forward, then LRPRuleConfig{1e-6} relevance from "
+                               "R_out = y at channel 0 (OutputValue seed)", "parallelism": "single GPU"},
+        "timing": "median of 10 calls of forward() + propagate_relevance() after 2 warm-ups; each call copies x "
+                  "and R_out from the host and the outputs back, as the block's public API does",
+        "tokens_per_s": round(B_SEQ / g_s, 1),
+        "parity": {"forward_max_rel": y_err, "relevance_max_rel_to_max": r_err},
+        "cpu_baseline": {"value": round(c_s * 1e3, 3), "unit": "ms", "kind": kind,
+                         "cores": int(oc.oracle().lib.pxo_get_threads()),
+                         "sample": "the same block and inputs: median of 10 calls after 2 warm-ups",
+                         "cpu_model": cpu_model(), "nproc": os.cpu_count()},
+        "gpu_vs_cpu": round(c_s / g_s, 1),
+    }
     print(json.dumps(out), flush=True)
 
 
