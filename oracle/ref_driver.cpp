@@ -28,6 +28,7 @@
 #include "pulsatrix/linear_module.hpp"
 #include "pulsatrix/lrp.hpp"
 #include "pulsatrix/lrp_rule_config.hpp"
+#include "pulsatrix/multihead_attention_module.hpp"
 #include "pulsatrix/relu_module.hpp"
 #include "pulsatrix/transformer_block.hpp"
 #ifdef PXR_ON_MI355X
@@ -260,6 +261,97 @@ int pxr_block_relevance_rule(void* h, const float* r_out, const px_lrp_rule* r, 
 }
 
 void pxr_block_destroy(void* h) { delete static_cast<RefBlock*>(h); }
+
+// One case of the reference's Hugging Face attention tests (tests/attention_reference_test.cpp:
+// 105-200), run through the reference's own MultiHeadAttentionModule on this library's backend:
+// the AttentionConfig (rotate-half RoPE), the weights and biases ((in, out) layout), the QK-Norm
+// gains, the key padding mask (n * l keep flags) and the position offset as given; forward of x
+// (n, l, d_model) into out, then the backward of sum(out * g) into grad_in.
+struct pxr_mha_spec {
+    int64_t d_model, heads, kv_heads, head_dim;
+    float rope_base;
+    int32_t qkv_bias, qk_norm, causal;
+    int64_t position_offset, n, l;
+    const float *wq, *bq, *wk, *bk, *wv, *bv, *wo, *q_gamma, *k_gamma, *keep;
+};
+
+int pxr_mha_case(const pxr_mha_spec* s, const float* x, const float* g, float* out, float* grad_in) {
+    return guarded([&] {
+        DeviceBackend* be = driver_backend();
+        AttentionConfig c;
+        c.d_model = s->d_model;
+        c.num_heads = s->heads;
+        c.num_kv_heads = s->kv_heads;
+        c.head_dim = s->head_dim;
+        c.rope_layout = RoPELayout::RotateHalf;
+        c.rope_base = s->rope_base;
+        c.use_qk_norm = s->qk_norm != 0;
+        c.qkv_bias = s->qkv_bias != 0;
+        c.out_bias = false;
+        c.causal = s->causal != 0;
+        MultiHeadAttentionModule attn(c, be);
+        const int64_t qd = s->heads * s->head_dim, kvd = s->kv_heads * s->head_dim, d = s->d_model;
+        auto vec = [](const float* p, int64_t count) { return std::vector<float>(p, p + count); };
+        attn.q_proj().set_weight(vec(s->wq, d * qd));
+        attn.k_proj().set_weight(vec(s->wk, d * kvd));
+        attn.v_proj().set_weight(vec(s->wv, d * kvd));
+        attn.out_proj().set_weight(vec(s->wo, qd * d));
+        if (s->qkv_bias) {
+            attn.q_proj().set_bias(vec(s->bq, qd));
+            attn.k_proj().set_bias(vec(s->bk, kvd));
+            attn.v_proj().set_bias(vec(s->bv, kvd));
+        }
+        if (s->qk_norm) {
+            attn.q_norm()->set_gamma(vec(s->q_gamma, s->head_dim));
+            attn.k_norm()->set_gamma(vec(s->k_gamma, s->head_dim));
+        }
+        if (s->position_offset) attn.set_position_offset(s->position_offset);
+        const int64_t count = s->n * s->l * d;
+        if (s->keep) attn.set_key_padding_mask(Tensor(Shape({s->n, s->l}), be, vec(s->keep, s->n * s->l)));
+        const std::vector<float> y = attn.forward(Tensor(Shape({s->n, s->l, d}), be, vec(x, count))).to_host_vector();
+        std::copy(y.begin(), y.end(), out);
+        const std::vector<float> gi = attn.backward(Tensor(Shape({s->n, s->l, d}), be, vec(g, count))).to_host_vector();
+        std::copy(gi.begin(), gi.end(), grad_in);
+    });
+}
+
+// The reference's independent-AttnLRP block test (tests/transformer_block_test.cpp:262-318): the
+// legacy TransformerBlock(d_model, heads, d_ff, backend, use_rope = false, use_qk_norm = false)
+// with the given gains and (in, out) weights (norm1, q, k, v, out, norm2, gate, up, down, packed in
+// that order), forward of x (1, l, d_model) into y, then propagate_relevance(r_out, LRPRuleConfig{})
+// into r_in.
+int pxr_legacy_block_case(int64_t d_model, int64_t heads, int64_t d_ff, int64_t l, const float* params, const float* x,
+                          const float* r_out, float* y, float* r_in) {
+    return guarded([&] {
+        DeviceBackend* be = driver_backend();
+        TransformerBlock block(d_model, heads, d_ff, be, false, false);
+        const float* p = params;
+        auto take = [&p](int64_t count) {
+            std::vector<float> v(p, p + count);
+            p += count;
+            return v;
+        };
+        const int64_t d = d_model;
+        block.norm1().set_gamma(take(d));
+        block.mha().q_proj().set_weight(take(d * d));
+        block.mha().k_proj().set_weight(take(d * d));
+        block.mha().v_proj().set_weight(take(d * d));
+        block.mha().out_proj().set_weight(take(d * d));
+        block.norm2().set_gamma(take(d));
+        block.swiglu().gate_proj().set_weight(take(d * d_ff));
+        block.swiglu().up_proj().set_weight(take(d * d_ff));
+        block.swiglu().down_proj().set_weight(take(d_ff * d));
+        const int64_t count = l * d;
+        const std::vector<float> out =
+            block.forward(Tensor(Shape({1, l, d}), be, std::vector<float>(x, x + count))).to_host_vector();
+        std::copy(out.begin(), out.end(), y);
+        const std::vector<float> r =
+            block.propagate_relevance(Tensor(Shape({1, l, d}), be, std::vector<float>(r_out, r_out + count)),
+                                      LRPRuleConfig{})
+                .to_host_vector();
+        std::copy(r.begin(), r.end(), r_in);
+    });
+}
 
 void* pxr_lm_create(const px_model_config* cfg, const float* params) {
     RefLM* out = nullptr;

@@ -12,6 +12,9 @@ them to the reference's own fixtures and to the oracle:
   * the Zennit 1.0.0 MLP through LRP::explain, every uniform rule and the three composites, at the
     reference's tolerance (tests/lrp_reference_test.cpp:85-91, 285-303);
   * a TransformerBlock at config B and a small CausalLM against the oracle, both epsilon rules;
+  * the reference's Hugging Face attention cases (Llama / Qwen2 with padding and a position offset /
+    Qwen3 with QK-Norm: forward and input gradient, tests/attention_reference_test.cpp) and its
+    independent NumPy AttnLRP block (tests/transformer_block_test.cpp:262-318) at their tolerances;
   * every path virtual against the oracle's restatement of CPUBackend on seeded uniform(-1, 1)
     inputs with non-square shapes, |gpu - cpu| <= 1e-4 (tests/backend_primitive_equivalence_cases.hpp:
     22-75), GEMMs with the K-scaled tolerance of tests/test_kernels_gpu.py.
@@ -24,6 +27,7 @@ import numpy as np
 import pytest
 
 import dropin_cases as dc
+import hf_attention_cases as hc
 import gpu_util as G
 import oracle_ctypes as oc
 import rules_cases as rc
@@ -54,6 +58,26 @@ def be(lib, name, *args):
 
 
 # ---- the reference's models on MI355XBackend ---------------------------------------------------
+
+@pytest.mark.parametrize("name", sorted(hc.CASES))
+def test_reference_attention_on_mi355x_matches_hf_attention_values(lib, name):
+    """tests/attention_reference_test.cpp through MI355XBackend: Llama (GQA, right padding), Qwen2
+    (MQA, biases, left padding, position offset 3) and Qwen3 (QK-Norm) attention, forward and the
+    input gradient, against the values transformers 5.18.0 produced, at 1e-4 * max(1, |x|)."""
+    out, grad = hc.run_mha_case(lib, name)
+    want_out, want_grad = hc.expected(name)
+    hc.assert_matches_reference(out, want_out, name + " forward")
+    hc.assert_matches_reference(grad, want_grad, name + " input gradient")
+
+
+def test_reference_block_on_mi355x_matches_numpy_attnlrp_values(lib):
+    """tests/transformer_block_test.cpp:262-318 through MI355XBackend: the independent NumPy AttnLRP
+    transcription's forward and LRPRuleConfig{} input relevance, within 1e-4."""
+    y, r = hc.run_legacy_block_case(lib)
+    v = hc.legacy_block_values()
+    assert np.abs(y - np.array(v["expected_y"], np.float32)).max() <= 1e-4
+    assert np.abs(r - np.array(v["expected_r_x"], np.float32)).max() <= 1e-4
+
 
 @pytest.mark.parametrize("name", ["llama", "qwen2", "qwen3", "gemma3"])
 def test_reference_causal_lm_on_mi355x_matches_goldens(lib, name):
