@@ -406,3 +406,98 @@ def test_fused_attention_kv_relevance_rejects_bad_descs():
     d.heads = 4
     assert N.pxk().pxk_attention_relevance_kv(ctypes.byref(d), None) == 1  # NULL operands
     assert b"NULL" in N.pxk().pxk_last_error()
+
+
+@gpu
+def test_recomputed_scores_match_the_forwards_raw_with_random_inputs():
+    """Uniform-random q and k (products not exact in float32) at the SmolLM2 shapes, causal GQA with
+    RoPE. The q side recomputes raw = Q K^T and P from the forward's row statistics; s = r_sc /
+    (2 raw + eps sign raw) is most sensitive where raw is near 0. The reference is float64
+    arithmetic on the score-row forward's own float32 raw scores. Some query rows and key rows are
+    planted so that their scores are a single product (the key's head zero apart from its first
+    coordinate kappa, the query's first half zero apart from delta): raw = delta * kappa exactly, whatever the
+    summation order, at 0, +-1e-7 .. 5e-6 (both sides of eps = 1e-6, both signs), so the sign rule
+    and the small-denominator range are checked at known scores. The key side then reads the s and P
+    the q side wrote: g_k and g_v against the float64 key-side sequence on the same s and P."""
+    n, L, H, Hkv, D = 1, 512, 9, 3, 64
+    print("recomputed scores vs forward raw, random inputs", flush=True)
+    qd, kvd = H * D, Hkv * D
+    w3 = qd + 2 * kvd
+    scale, eps = 1.0 / np.sqrt(D), 1e-6
+    qkv = G.uniform((n * L, w3), 11)
+    q_rows, deltas = [64, 200, 333, 400, 511], [0.0, 1e-7, -2.5e-7, 1e-6, -5e-6]
+    k_rows, kappas = [0, 17, 63, 64, 150, 333], [1.0, 0.5, -3.0, 0.25, -1.0, 2.0]
+    for i, delta in zip(q_rows, deltas):
+        for h in range(H):
+            qkv[i, h * D:h * D + D // 2] = 0.0
+            qkv[i, h * D] = delta
+    for j, kappa in zip(k_rows, kappas):
+        for hk in range(Hkv):
+            col = qd + hk * D
+            qkv[j, col:col + D] = 0.0
+            qkv[j, col] = kappa
+    spv, q_pre = G.uniform((n * L, qd), 12), G.uniform((n * L, qd + kvd), 13)
+    rs = np.random.RandomState(14)
+    z = (rs.uniform(0.5, 1.5, (n * L, w3)) * rs.choice([-1.0, 1.0], (n * L, w3))).astype(np.float32)
+    ang = np.arange(L)[:, None] * (10000.0 ** (-np.arange(D // 2) * 2.0 / D))[None, :]
+    cos, sin = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+    qkv_d, spv_d, pre_d, z_d, cos_d, sin_d = (G.dev(a) for a in (qkv, spv, q_pre, z, cos, sin))
+    base = qkv_d.data_ptr()
+    raw, p_fwd, ctx = G.empty((n, H, L, L)), G.empty((n, H, L, L)), G.empty((n * L, qd))
+    N.call("pxk_attention_forward", base, w3, base + 4 * qd, w3, base + 4 * (qd + kvd), w3, G.ptr(raw), G.ptr(p_fwd),
+           G.ptr(ctx), qd, n, L, H, Hkv, D, scale, 1, G.stream())
+    stats, ctx2 = G.empty((n, H, L, 2)), G.empty((n * L, qd))
+    N.call("pxk_attention_forward_stats", base, w3, base + 4 * qd, w3, base + 4 * (qd + kvd), w3, None, None,
+           G.ptr(stats), G.ptr(ctx2), qd, n, L, H, Hkv, D, scale, 1, G.stream())
+    raw_h = G.host(raw).astype(np.float64)
+    vis = np.tril(np.ones((L, L), bool))
+    planted = np.zeros((L, L), bool)
+    for i, delta in zip(q_rows, deltas):
+        for j, kappa in zip(k_rows, kappas):
+            if j <= i:
+                planted[i, j] = True
+                assert np.all(raw_h[0, :, i, j] == np.float64(np.float32(delta) * np.float32(kappa)))
+    q_h, k_h, v_h = qkv[:, :qd], qkv[:, qd:qd + kvd], qkv[:, qd + kvd:]
+    x = np.where(vis, scale * raw_h, -np.inf)
+    mx = x.max(-1, keepdims=True)
+    e = np.exp(x - mx)
+    p = e / e.sum(-1, keepdims=True)
+    want_s, want_g = relevance_q_reference(spv, q_h, q_pre[:, :qd], k_h, v_h, z[:, :qd], None, p, raw_h,
+                                           cos.astype(np.float64), sin.astype(np.float64), n, L, H, Hkv, D, scale,
+                                           eps, 1, 1, 1)
+    s_buf, p_buf, g = G.empty((n, H, L, L)), G.empty((n, H, L, L)), G.empty((n * L, qd))
+    d = N.AttnRelDesc()
+    d.n, d.l, d.heads, d.kv_heads, d.head_dim = n, L, H, Hkv, D
+    d.scale, d.eps, d.causal, d.rope, d.rope_half = scale, eps, 1, 1, 1
+    d.spv, d.ld_spv = spv_d.data_ptr(), qd
+    d.v, d.ld_v, d.k, d.ld_k = base + 4 * (qd + kvd), w3, base + 4 * qd, w3
+    d.s, d.p_out = G.ptr(s_buf).value, G.ptr(p_buf).value
+    d.q, d.ld_q, d.q_pre, d.ld_q_pre = base, w3, pre_d.data_ptr(), qd + kvd
+    d.z, d.ld_z = z_d.data_ptr(), w3
+    d.cos_t, d.sin_t = cos_d.data_ptr(), sin_d.data_ptr()
+    d.g, d.ld_g = G.ptr(g).value, qd
+    d.ctx, d.ld_ctx, d.stats = G.ptr(ctx2).value, qd, G.ptr(stats).value
+    assert N.pxk().pxk_attention_relevance_q(ctypes.byref(d), G.stream()) == 0, N.pxk().pxk_last_error()
+    got_s, got_p = G.host(s_buf), G.host(p_buf)
+    G.assert_close(got_p[..., vis], p[..., vis], 1e-5, "P")
+    G.assert_close(got_s[..., vis], want_s[..., vis], 1e-4, "s")
+    G.assert_close(got_s[..., planted], want_s[..., planted], 1e-4, "s at the planted scores near 0")
+    G.assert_close(G.host(g), want_g, 1e-4, "g_q")
+    # The key side over the s and P the q side wrote.
+    k_pre, z_k, z_v = q_pre[:, qd:], z[:, qd:qd + kvd], z[:, qd + kvd:]
+    want_kv = relevance_kv_reference(want_s, p, q_h, spv, k_h, k_pre, v_h, z_k, z_v, None, None,
+                                     cos.astype(np.float64), sin.astype(np.float64), n, L, H, Hkv, D, eps, 1, 1, 1)
+    gk, gv = G.empty((n * L, kvd)), G.empty((n * L, kvd))
+    kd = N.AttnRelKvDesc()
+    kd.n, kd.l, kd.heads, kd.kv_heads, kd.head_dim = n, L, H, Hkv, D
+    kd.eps, kd.causal, kd.rope, kd.rope_half = eps, 1, 1, 1
+    kd.q, kd.ld_q, kd.spv, kd.ld_spv = base, w3, spv_d.data_ptr(), qd
+    kd.k, kd.ld_k, kd.k_pre, kd.ld_k_pre = base + 4 * qd, w3, pre_d.data_ptr() + 4 * qd, qd + kvd
+    kd.v, kd.ld_v = base + 4 * (qd + kvd), w3
+    kd.z_k, kd.z_v, kd.ld_z = z_d.data_ptr() + 4 * qd, z_d.data_ptr() + 4 * (qd + kvd), w3
+    kd.cos_t, kd.sin_t = cos_d.data_ptr(), sin_d.data_ptr()
+    kd.g_k, kd.g_v, kd.ld_g = G.ptr(gk).value, G.ptr(gv).value, kvd
+    kd.s, kd.p = G.ptr(s_buf).value, G.ptr(p_buf).value
+    assert N.pxk().pxk_attention_relevance_kv(ctypes.byref(kd), G.stream()) == 0, N.pxk().pxk_last_error()
+    G.assert_close(G.host(gk), want_kv[2], 1e-4, "g_k")
+    G.assert_close(G.host(gv), want_kv[3], 1e-4, "g_v")
