@@ -1317,16 +1317,17 @@ extern "C" int pxk_attention_relevance_kv(const pxk_attn_rel_kv_desc* d, void* s
                 static_cast<int>(d->ld_g), static_cast<int>(n), static_cast<int>(l), static_cast<int>(H),
                 static_cast<int>(Hkv), static_cast<int>(D), static_cast<int>(ngroups), static_cast<int>(nkb), d->eps,
                 d->causal != 0, d->rope != 0, d->rope_half != 0, blocks % 8 == 0, d->relevance_only != 0};
-    // Sixteen waves per workgroup: the widest spread of a long key block's rows measured fastest at
-    // 512 tokens (against 4 or 8 waves). Four dim groups per workgroup where they divide evenly and
-    // the grid stays above eight workgroups per CU (many sequences, or head_dim 256), so the score
-    // rows are read a quarter as often, two items per register set. Otherwise two dim groups where
-    // they divide (the score rows read half as often, 192 workgroups for one 512-token sequence of
-    // three KV heads) with one item per set: 20.2 us against 23.2 for one group and two items, 34
-    // for four groups (96 workgroups) at 1 x 512, 9 heads, head_dim 64.
+    // One item per register set throughout. Four dim groups per workgroup where they divide evenly
+    // and the grid stays above eight workgroups per CU (many sequences, or head_dim 256), so the
+    // score rows are read a quarter as often, on eight waves: 1089 us against 1165 for sixteen
+    // waves with two items per set, 1209 for two groups, at 8 x 1024, 32 / 8 heads of 64.
+    // Otherwise sixteen waves, the widest spread of a long key block's rows, and two dim groups
+    // where they divide (the score rows read half as often, 192 workgroups for one 512-token
+    // sequence of three KV heads): 20.2 us against 23.2 for one group and two items per set, 34 for
+    // four groups (96 workgroups) at 1 x 512, 9 / 3 heads of 64.
     if (ngroups % 4 == 0 && blocks / 4 >= 2048) {
         a.remap = (blocks / 4) % 8 == 0;
-        PXK_LAUNCH((attn_rel_kv_kernel<16, 2, 4>), dim3(static_cast<unsigned>(blocks / 4)), dim3(16 * kWave), 0,
+        PXK_LAUNCH((attn_rel_kv_kernel<8, 1, 4>), dim3(static_cast<unsigned>(blocks / 4)), dim3(8 * kWave), 0,
                            S(stream), a);
     } else if (ngroups % 2 == 0) {
         a.remap = (blocks / 2) % 8 == 0;

@@ -333,6 +333,14 @@ def test_fused_attention_kv_relevance_matches_numpy(n, L, H, Hkv, D, causal, rop
 
 
 @gpu
+@pytest.mark.parametrize("causal,rope,half,bias", [(1, 1, 1, 0), (0, 0, 0, 1)])
+def test_fused_attention_kv_relevance_large_grid(causal, rope, half, bias):
+    """The launch with four head-dim groups per workgroup, taken once the grid holds 2048 such
+    workgroups: 4 sequences x 32 KV heads x 16 key blocks x 4 groups / 4 here."""
+    test_fused_attention_kv_relevance_matches_numpy(4, 256, 32, 32, 64, causal, rope, half, bias)
+
+
+@gpu
 @pytest.mark.parametrize("n,L,H,Hkv,D", [(1, 200, 4, 2, 64), (2, 37, 3, 1, 16), (1, 512, 9, 3, 64)])
 def test_recomputing_chain_matches_score_row_chain(n, L, H, Hkv, D):
     """The step's attention relevance chain in its recomputing form (forward with row statistics,
