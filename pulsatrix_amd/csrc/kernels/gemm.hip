@@ -321,6 +321,26 @@ int plan(const pxk_gemm_desc* d, Plan* p) {
     return PXK_OK;
 }
 
+// M-tiles per group of the tile order (tile_of) when each XCD takes a run of `run` consecutive
+// tiles: the divisor of tiles_m whose group_m x ceil(run / group_m) block of tiles reads the fewest
+// panel bytes per XCD (group_m A panels of bm rows, the N-tiles' B panels of bn columns; K is
+// common). With runs as long as a whole slice the order stays M-fastest (group_m = tiles_m). At 512
+// x 576 on 32x48 tiles (16 x 12 tiles, runs of 24) that is 8 x 3 blocks, each A panel fetched by 4
+// XCDs and each B panel by 2, against every XCD fetching every A panel in the M-fastest order.
+int group_m(int64_t tiles_m, int64_t tiles_n, int64_t run, int bm, int bn) {
+    if (run >= tiles_m * tiles_n) return static_cast<int>(tiles_m);
+    int64_t best = tiles_m, best_cost = -1;
+    for (int64_t gm = 1; gm <= tiles_m; ++gm) {
+        if (tiles_m % gm != 0) continue;
+        const int64_t cost = gm * bm + cdiv(run, gm) * bn;
+        if (best_cost < 0 || cost < best_cost) {
+            best_cost = cost;
+            best = gm;
+        }
+    }
+    return static_cast<int>(best);
+}
+
 size_t workspace_bytes(const pxk_gemm_desc* d, const Plan& p) {
     return p.splits > 1 ? static_cast<size_t>(p.splits) * d->batch * d->m * d->n * sizeof(float) : 0;
 }
@@ -432,6 +452,8 @@ extern "C" int pxk_gemm(const pxk_gemm_desc* d, void* stream) {
     g.bm = kTileInfo[p.tile].bm;
     const int64_t blocks = p.tiles_m * p.tiles_n * d->batch * p.splits;
     g.remap = blocks % 8 == 0;
+    g.group_m = g.remap ? group_m(p.tiles_m, p.tiles_n, blocks / 8, kTileInfo[p.tile].bm, kTileInfo[p.tile].bn)
+                        : g.tiles_m;
     const int has_bias = d->prologue == PXK_PRO_DIV_STAB && d->z_bias.ptr != nullptr;
     PXK_LAUNCH(p.e->k[has_bias][p.tile], dim3(static_cast<unsigned>(blocks)),
                        dim3(static_cast<unsigned>(kTileInfo[p.tile].threads)), 0, S(stream), g);

@@ -69,7 +69,8 @@ struct Args {
     int rope_half, gate_act;
     int vec_a, vec_b, vec_e;  // 128-bit global access allowed: A (and Z), B, epilogue operands
     int tiles_m, tiles_n, bm;
-    int remap;  // XCD-grouped block order
+    int remap;    // XCD-grouped block order
+    int group_m;  // M-tiles per group of the tile order (divides tiles_m; tiles_m: M fastest)
     float* ws;
     int64_t kc;  // skinny path: K rows per split
 };
@@ -552,16 +553,23 @@ __device__ __forceinline__ int64_t k_end(const Args& g, int64_t m0, int64_t bm) 
 }
 
 // Block index -> (M tile, N tile, batch * splits + split).
+// Tile order within one (batch, split) slice: groups of group_m M-tiles, M fastest within a group,
+// then the N-tiles, then the next group. With the XCD regrouping each XCD's contiguous run of tiles
+// is then a group_m x (run / group_m) block, so fewer XCDs fetch each A and B panel into their L2.
 __device__ __forceinline__ void tile_of(const Args& g, int& tm, int& tn, int& tz) {
     int id = static_cast<int>(blockIdx.x);
     if (g.remap) {
         const int per = static_cast<int>(gridDim.x) / 8;
         id = (id % 8) * per + id / 8;
     }
-    tm = id % g.tiles_m;
-    id /= g.tiles_m;
-    tn = id % g.tiles_n;
-    tz = id / g.tiles_n;
+    const int slice = g.tiles_m * g.tiles_n;
+    tz = id / slice;
+    int r = id - tz * slice;
+    const int span = g.group_m * g.tiles_n;
+    const int sr = r / span;
+    r -= sr * span;
+    tm = sr * g.group_m + r % g.group_m;
+    tn = r / g.group_m;
 }
 
 // Each wave's accumulators (one partial tile per K slice) -> LDS, summed in slice order; then the
