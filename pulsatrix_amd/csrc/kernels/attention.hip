@@ -1077,18 +1077,19 @@ extern "C" int pxk_attention_relevance_q(const pxk_attn_rel_desc* d, void* strea
 
 // ---- key and value shares (pxk_attention_relevance_kv) ------------------------------------------------
 //
-// One workgroup owns 16 keys of one KV head and one group of 16 head dimensions, closed under the
-// RoPE pairing: dims 8j..8j+7 with their partners 8j+half.. under rotate-half, 16j..16j+15 for
-// adjacent pairs or no RoPE. Its products are D[key][dim] = sum over (query head of the group,
-// query row) of s[row][key] * Q[row][dim] and P[row][key] * s_pv[row][dim]: v_mfma_f32_16x16x4_f32
-// with A = one 16-key segment of 4 score rows and B = the matching 4 query rows' dims, so every
-// operand is a single coalesced float per lane. The (head, 4-row) items go round-robin over the
-// four waves, each with two accumulator pairs; the waves merge in LDS in wave order
-// (deterministic). Loads run two item groups ahead in two register sets, with addresses clamped
-// in range and rows past the end masked to 0 in the A operand, so the loop has no branch around a
-// load. Causal: rows before the block's first key hold only masked (zero) entries and are skipped.
-// Workgroups are ordered so each group of eight pairs a long causal key block with a short one,
-// and (with a multiple of 8 workgroups) a group shares one XCD and its L2.
+// One workgroup owns 16 keys of one KV head and DG groups of 16 head dimensions, each group closed
+// under the RoPE pairing: dims 8j..8j+7 with their partners 8j+half.. under rotate-half,
+// 16j..16j+15 for adjacent pairs or no RoPE. Its products are D[key][dim] = sum over (query head of
+// the group, query row) of s[row][key] * Q[row][dim] and P[row][key] * s_pv[row][dim]:
+// v_mfma_f32_16x16x4_f32 with A = one 16-key segment of 4 score rows and B = the matching 4 query
+// rows' dims, so every operand is a single coalesced float per lane, and each score segment serves
+// the DG groups. The (head, 4-row) items go round-robin over the NW waves, each with two accumulator
+// pairs per group; the waves merge in LDS in wave order (deterministic). Loads run two register
+// sets of U items ahead, with addresses clamped in range and rows past the end masked to 0 in the A
+// operand, so the loop has no branch around a load. Causal: rows before the block's first key hold
+// only masked (zero) entries and are skipped. Workgroups are ordered so each group of eight pairs a
+// long causal key block with a short one, and (with a multiple of 8 workgroups) a group shares one
+// XCD and its L2.
 namespace {
 
 
