@@ -53,13 +53,32 @@ struct FwdArgs {
     int keep;      // raw or P is written: the raw scores wait in LDS for the last pass
 };
 
+// Lane l's value and lane (l ^ 16)'s, or (l ^ 32)'s, one in each half of the pair: v_permlane16_swap
+// (odd 16-lane rows of the first operand with even rows of the second) and v_permlane32_swap (upper
+// half with lower half) on two copies of v. They are VALU operations, where a shuffle is an LDS
+// permute and a wait on it. Every lane of the wave must be active.
+__device__ __forceinline__ void pair16(float v, float& x, float& y) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    x = __uint_as_float(r[0]);
+    y = __uint_as_float(r[1]);
+}
+__device__ __forceinline__ void pair32(float v, float& x, float& y) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    x = __uint_as_float(r[0]);
+    y = __uint_as_float(r[1]);
+}
+// Over the four lanes c, c + 16, c + 32, c + 48 (one score row), pairs at distance 16 first.
 __device__ __forceinline__ float row_max4(float v) {
-    v = fmaxf(v, __shfl_xor(v, 16, kWave));
-    return fmaxf(v, __shfl_xor(v, 32, kWave));
+    float x, y;
+    pair16(v, x, y);
+    pair32(fmaxf(x, y), x, y);
+    return fmaxf(x, y);
 }
 __device__ __forceinline__ float row_sum4(float v) {
-    v += __shfl_xor(v, 16, kWave);
-    return v + __shfl_xor(v, 32, kWave);
+    float x, y;
+    pair16(v, x, y);
+    pair32(x + y, x, y);
+    return x + y;
 }
 
 // Byte range of the forward's K or V tile resource, counted from the tile's first row (key0) of one
