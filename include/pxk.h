@@ -297,6 +297,14 @@ int pxk_attention_forward_stats(const float* q, int64_t ldq, const float* k, int
                                 int64_t ldv, float* raw, float* p, float* stats, float* ctx, int64_t ldctx,
                                 int64_t n, int64_t l, int64_t heads, int64_t kv_heads, int64_t head_dim, float scale,
                                 int causal, void* stream);
+/* Whether pxk_attention_forward_stats, with neither raw nor p, runs a shape GQA-shared: one
+ * workgroup per (sequence, KV head, 16-row block) whose waves are the KV head's query heads, each
+ * K / V tile read into LDS once for the group (v 16-byte aligned with a row stride a multiple of 4
+ * besides). 1 where each 16-row block has at least 16 (sequence, KV head) workgroups, 512 in all,
+ * and 2, 3, 4 or 8 query heads per KV head; else 0 (the per-head kernel, whose waves split a
+ * block's key tiles). No counterpart in the reference, whose forward is per head
+ * (multihead_attention_module.cpp:268-291): it names the plan, as pxk_gemm_plan does. */
+int pxk_attention_forward_gqa(int64_t n, int64_t l, int64_t heads, int64_t kv_heads);
 
 /* The AttnLRP pass of one attention layer through the steps that need whole score rows, fused per
  * query head and 16-row block (MultiHeadAttentionModule::propagate_relevance,

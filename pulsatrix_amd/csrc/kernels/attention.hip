@@ -328,6 +328,154 @@ __global__ void __launch_bounds__(kThreads) attn_fwd_kernel(const FwdArgs a) {
     }
 }
 
+// GQA-shared forward (statistics form), for grids many times the chip's size: one workgroup per
+// (sequence, KV head, 16-row block) and one wave per query head of the KV head's group, each wave
+// over all of the block's key tiles with its own online softmax, so no merge. Every K / V tile
+// comes from memory once per workgroup into LDS (two buffers: the next tile's loads are in flight
+// while the current one is on the MFMAs) and feeds the G waves, where attn_fwd_kernel reads it once
+// per query head through the vector memory path. Per wave the arithmetic is attn_fwd_kernel's, tile
+// after tile.
+template <int DT, int G>
+__global__ void __launch_bounds__(G * kWave) attn_fwd_gqa_kernel(const FwdArgs a) {
+    constexpr int NT = G * kWave, LD = 16 * DT + 4;
+    constexpr int PER = (16 * 4 * DT + NT - 1) / NT;                      // float4 per thread per tile operand
+    __shared__ __attribute__((aligned(16))) float kv_lds[2][2][16][LD];  // [buffer][K, V][key][dim]
+
+    const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, c = lane & 15;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: the query head
+    const int l = a.l, D = a.D;
+    const int nrb = (l + 15) / 16;
+    // Long causal rows first, KV heads fastest.
+    const int nbk = a.n * a.kv_heads;
+    const int rb = nrb - 1 - static_cast<int>(blockIdx.x) / nbk, bk = static_cast<int>(blockIdx.x) % nbk;
+    const int hk = bk % a.kv_heads, b = bk / a.kv_heads;
+    const int h = hk * G + wave;
+    const int i0 = rb * 16, row = i0 + c;
+    const bool row_ok = row < l;
+
+    // Q^T fragments: qf[t][s] = Q[row][16 t + 4 g + s], zero past head_dim.
+    f4 qf[DT];
+    {
+        const float* qp = a.q + (static_cast<int64_t>(b) * l + (row_ok ? row : l - 1)) * a.ldq + h * D;
+#pragma unroll
+        for (int t = 0; t < DT; ++t) {
+            const int d0 = 16 * t + 4 * g;
+            qf[t] = *reinterpret_cast<const f4*>(qp + min(d0, D - 4)) * (d0 < D ? 1.0f : 0.0f);
+        }
+    }
+    const float* kbase = a.k + static_cast<int64_t>(b) * l * a.ldk + hk * D;
+    const float* vbase = a.v + static_cast<int64_t>(b) * l * a.ldv + hk * D;
+    const int vis_end = a.causal ? min(i0 + 16, l) : l;
+    const int ntile = (vis_end + 15) / 16;
+    const int q4 = D / 4;
+
+    // Columns past head_dim stay zero in both buffers: K's meet zero Q fragments, V's feed context
+    // dims that are never stored.
+    for (int i = tid; i < 2 * 2 * 16 * (16 * DT - D); i += NT) {
+        const int w = 16 * DT - D, r = i / w, col = D + i - r * w;
+        (&kv_lds[0][0][0][0])[r * LD + col] = 0.0f;
+    }
+    // A tile's 16 K rows and 16 V rows as float4 pieces over the workgroup; rows past the sequence
+    // read its last row (finite: their keys are masked and meet zero probabilities).
+    f4 sk[PER], sv[PER];
+    auto fetch = [&](int kt) {
+#pragma unroll
+        for (int j = 0; j < PER; ++j) {
+            const int i = min(tid + NT * j, 16 * q4 - 1);
+            const int r = i / q4, c4 = 4 * (i - r * q4);
+            const int64_t key = min(16 * kt + r, l - 1);
+            sk[j] = *reinterpret_cast<const f4*>(kbase + key * a.ldk + c4);
+            sv[j] = *reinterpret_cast<const f4*>(vbase + key * a.ldv + c4);
+        }
+    };
+    auto stash = [&](int buf) {
+#pragma unroll
+        for (int j = 0; j < PER; ++j) {
+            const int i = tid + NT * j;
+            if (i < 16 * q4) {
+                const int r = i / q4, c4 = 4 * (i - r * q4);
+                *reinterpret_cast<f4*>(&kv_lds[buf][0][r][c4]) = sk[j];
+                *reinterpret_cast<f4*>(&kv_lds[buf][1][r][c4]) = sv[j];
+            }
+        }
+    };
+
+    float m = -INFINITY, ssum = 0.0f;
+    f4 acc[DT];
+#pragma unroll
+    for (int t = 0; t < DT; ++t) acc[t] = f4{0.f, 0.f, 0.f, 0.f};
+    fetch(0);
+    stash(0);
+    __syncthreads();
+    for (int kt = 0; kt < ntile; ++kt) {
+        const int buf = kt & 1;
+        if (kt + 1 < ntile) fetch(kt + 1);  // uniform
+        // S^T tile = K[16 kt .. 16 kt + 15] Q^T over the head dimension.
+        f4 s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int t = 0; t < DT; ++t) {
+            const f4 kf = *reinterpret_cast<const f4*>(&kv_lds[buf][0][c][16 * t + 4 * g]);
+#pragma unroll
+            for (int st = 0; st < 4; ++st) s = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[st], qf[t][st], s, 0, 0, 0);
+        }
+        // s[r] = raw score of (row, 16 kt + 4 g + r); the online softmax step of attn_fwd_kernel.
+        const int kk0 = 16 * kt + 4 * g;
+        float x[4];
+        bool valid[4];
+        float mt = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int kk = kk0 + r;
+            valid[r] = (kk < l) & ((!a.causal) | (kk <= row));
+            x[r] = a.scale * s[r];
+            mt = fmaxf(mt, valid[r] ? x[r] : -INFINITY);
+        }
+        mt = row_max4(mt);
+        const float m_new = fmaxf(m, mt);
+        const float alpha = m_new == -INFINITY ? 1.0f : __expf(m - m_new);
+        float e[4];
+        float part = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            e[r] = valid[r] ? __expf(x[r] - m_new) : 0.0f;
+            part += e[r];
+        }
+        ssum = ssum * alpha + part;
+        m = m_new;
+        if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {
+#pragma unroll
+            for (int t = 0; t < DT; ++t) acc[t] *= alpha;
+        }
+        // ctx^T (D x rows) += V^T (D x keys) P^T (keys x rows): vf = V[16 kt + 4 g + st][16 t + c].
+#pragma unroll
+        for (int t = 0; t < DT; ++t) {
+#pragma unroll
+            for (int st = 0; st < 4; ++st)
+                acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv_lds[buf][1][4 * g + st][16 * t + c], e[st], acc[t], 0, 0, 0);
+        }
+        // The other buffer was last read in the previous iteration, before its barrier.
+        if (kt + 1 < ntile) stash(buf ^ 1);
+        __syncthreads();
+    }
+    // acc[t][r] = ctx^T[16 t + 4 g + r][row c] of head h; the row's sum over its four lanes.
+    ssum = row_sum4(ssum);
+    if (row_ok) {
+        float* cp = a.ctx + (static_cast<int64_t>(b) * l + row) * a.ldctx + h * D;
+#pragma unroll
+        for (int t = 0; t < DT; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int d = 16 * t + 4 * g + r;
+                if (d < D) cp[d] = acc[t][r] / ssum;
+            }
+        if (g == 0) {
+            float* st = a.stats + 2 * (((static_cast<int64_t>(b) * a.heads + h) * l) + row);
+            st[0] = m;
+            st[1] = 1.0f / ssum;
+        }
+    }
+}
+
 struct RelArgs {
     const float* spv;
     const float* v;
@@ -914,6 +1062,21 @@ constexpr int kMaxLds = 160 * 1024;  // gfx950 LDS per workgroup
 // end). The last pass reads whole row segments, 16 lanes per row.
 int score_lds_ld(int64_t l) { return static_cast<int>((l + 63) / 64 * 64 + 20); }
 
+// When the statistics-form forward runs GQA-shared: at least 16 (sequence, KV head) workgroups per
+// 16-row block and 512 workgroups in all, with 2, 3, 4 or 8 query heads per KV head. Per launch at
+// head_dim 64: 8 x 1024 tokens with 32 / 8 heads 642 -> 396 us, 4 x 1024 265 -> 198, 2 x 1024
+// 133 -> 123; kept on the per-head kernel, where the heaviest blocks' tile chains (all of a block's
+// key tiles in one wave) bound the launch: 1 x 1024 (70 against 87 us), 1 x 2048 (222 against 228),
+// 1 x 4096 with 16 / 8 heads (393 against 537), 1 x 512 with 9 / 3 (14.5 against 37).
+constexpr int64_t kGqaMinGroups = 16, kGqaMinBlocks = 512;
+
+bool gqa_forward(int64_t n, int64_t l, int64_t heads, int64_t kv_heads) {
+    if (n <= 0 || l <= 0 || heads <= 0 || kv_heads <= 0 || heads % kv_heads != 0) return false;
+    const int64_t grp = heads / kv_heads;
+    return (grp == 2 || grp == 3 || grp == 4 || grp == 8) && n * kv_heads >= kGqaMinGroups &&
+           n * kv_heads * ((l + 15) / 16) >= kGqaMinBlocks;
+}
+
 template <int DT>
 int static_lds() {
     return static_cast<int>(sizeof(float) * (2 * kWaves * 16 + kWaves * 16 * (16 * DT + 4) + 2 * 16));
@@ -970,13 +1133,30 @@ int attention_forward(const float* q, int64_t ldq, const float* k, int64_t ldk, 
     FwdArgs a{q, k, v, raw, p, ctx, ldq, ldk, ldv, ldctx, static_cast<int>(n), static_cast<int>(l),
               static_cast<int>(heads), static_cast<int>(kv_heads), static_cast<int>(head_dim), scale, causal != 0,
               lds_ld, stats, keep};
+    const int dt = dt_of(head_dim);
+    const int di = dt == 1 ? 0 : dt == 2 ? 1 : dt == 4 ? 2 : 3;
+    // Many workgroups per CU: the GQA-shared kernel (one workgroup per KV head and row block, each
+    // K / V tile read once for the group's query heads); fewer: the per-head kernel, whose four
+    // waves split each block's key tiles and so shorten the heaviest blocks' chains.
+    const int64_t grp = heads / kv_heads, gblocks = n * kv_heads * ((l + 15) / 16);
+    const int gi = grp == 2 ? 0 : grp == 3 ? 1 : grp == 4 ? 2 : grp == 8 ? 3 : -1;
+    if (!keep && stats && gqa_forward(n, l, heads, kv_heads) && ldv % 4 == 0 && aligned16(v)) {
+        using KG = void (*)(const FwdArgs);
+        static const KG gqa[4][4] = {
+            {attn_fwd_gqa_kernel<1, 2>, attn_fwd_gqa_kernel<2, 2>, attn_fwd_gqa_kernel<4, 2>, attn_fwd_gqa_kernel<8, 2>},
+            {attn_fwd_gqa_kernel<1, 3>, attn_fwd_gqa_kernel<2, 3>, attn_fwd_gqa_kernel<4, 3>, attn_fwd_gqa_kernel<8, 3>},
+            {attn_fwd_gqa_kernel<1, 4>, attn_fwd_gqa_kernel<2, 4>, attn_fwd_gqa_kernel<4, 4>, attn_fwd_gqa_kernel<8, 4>},
+            {attn_fwd_gqa_kernel<1, 8>, attn_fwd_gqa_kernel<2, 8>, attn_fwd_gqa_kernel<4, 8>, attn_fwd_gqa_kernel<8, 8>}};
+        PXK_LAUNCH(gqa[gi][di], dim3(static_cast<unsigned>(gblocks)), dim3(static_cast<unsigned>(grp * kWave)), 0,
+                   S(stream), a);
+        return launched(who);
+    }
     const bool vec = l % 4 == 0 && (!raw || aligned16(raw)) && (!p || aligned16(p));
     using K = void (*)(const FwdArgs);
     static const K table[2][4] = {
         {attn_fwd_kernel<1, false>, attn_fwd_kernel<2, false>, attn_fwd_kernel<4, false>, attn_fwd_kernel<8, false>},
         {attn_fwd_kernel<1, true>, attn_fwd_kernel<2, true>, attn_fwd_kernel<4, true>, attn_fwd_kernel<8, true>}};
-    const int dt = dt_of(head_dim);
-    const K fn = table[vec ? 1 : 0][dt == 1 ? 0 : dt == 2 ? 1 : dt == 4 ? 2 : 3];
+    const K fn = table[vec ? 1 : 0][di];
     const size_t dyn = keep ? static_cast<size_t>(16) * lds_ld * sizeof(float) : 0;
     if (dyn > 64 * 1024 &&
         hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -995,6 +1175,10 @@ extern "C" int pxk_attention_forward(const float* q, int64_t ldq, const float* k
     if (!raw || !p) return fail(PXK_ERR_INVALID, "pxk_attention_forward: raw and p are required");
     return attention_forward(q, ldq, k, ldk, v, ldv, raw, p, nullptr, ctx, ldctx, n, l, heads, kv_heads, head_dim,
                              scale, causal, stream, "pxk_attention_forward");
+}
+
+extern "C" int pxk_attention_forward_gqa(int64_t n, int64_t l, int64_t heads, int64_t kv_heads) {
+    return gqa_forward(n, l, heads, kv_heads) ? 1 : 0;
 }
 
 extern "C" int pxk_attention_forward_stats(const float* q, int64_t ldq, const float* k, int64_t ldk, const float* v,

@@ -509,3 +509,57 @@ def test_recomputed_scores_match_the_forwards_raw_with_random_inputs():
     assert N.pxk().pxk_attention_relevance_kv(ctypes.byref(kd), G.stream()) == 0, N.pxk().pxk_last_error()
     G.assert_close(G.host(gk), want_kv[2], 1e-4, "g_k")
     G.assert_close(G.host(gv), want_kv[3], 1e-4, "g_v")
+
+
+def gqa_plan():
+    fn = N.pxk().pxk_attention_forward_gqa
+    fn.argtypes = [ctypes.c_int64] * 4
+    fn.restype = ctypes.c_int
+    return fn
+
+
+def test_gqa_shared_forward_plan():
+    """CPU-side: which statistics-form shapes run GQA-shared (the shapes the rule was measured on)."""
+    plan = gqa_plan()
+    assert plan(8, 1024, 32, 8) == 1 and plan(4, 1024, 32, 8) == 1 and plan(2, 1024, 32, 8) == 1
+    assert plan(1, 1024, 32, 8) == 0 and plan(1, 2048, 32, 8) == 0 and plan(1, 4096, 16, 8) == 0
+    assert plan(1, 512, 9, 3) == 0 and plan(4, 512, 9, 3) == 0  # the 135M shape: the per-head kernel
+    assert plan(2, 1024, 16, 2) == 0  # four (sequence, KV head) workgroups per row block
+    assert plan(16, 512, 40, 8) == 0  # five query heads per KV head: no GQA-shared build
+    assert plan(16, 16, 32, 8) == 0  # 128 workgroups in all
+    assert plan(0, 512, 32, 8) == 0 and plan(8, 1024, 30, 8) == 0 and plan(8, 0, 32, 8) == 0
+
+
+@gpu
+@pytest.mark.parametrize("causal", [1, 0])
+@pytest.mark.parametrize("n,L,H,Hkv,D", [(4, 512, 8, 4, 64), (2, 500, 24, 8, 40), (4, 520, 16, 4, 32),
+                                         (16, 512, 8, 1, 12), (4, 512, 8, 4, 128)])
+def test_gqa_shared_forward_matches_numpy(n, L, H, Hkv, D, causal):
+    """The statistics form on shapes that run GQA-shared (one workgroup per KV head and 16-row block,
+    a wave per query head over all of the block's key tiles, K / V tiles through LDS): ctx and the
+    rows' max and 1 / sum against float64 numpy, ragged lengths and head_dims below a 16 multiple
+    included; and two launches bitwise equal."""
+    print("gqa forward n=%d L=%d H=%d Hkv=%d D=%d causal=%d" % (n, L, H, Hkv, D, causal), flush=True)
+    assert gqa_plan()(n, L, H, Hkv) == 1
+    qd, kvd = H * D, Hkv * D
+    w3 = qd + 2 * kvd
+    qkv = G.uniform((n * L, w3), 31 + L + D)
+    scale = 1.0 / np.sqrt(D)
+    qkv_d = G.dev(qkv)
+    base = qkv_d.data_ptr()
+    outs = []
+    for _ in range(2):
+        stats, ctx = G.empty((n, H, L, 2)), G.empty((n * L, qd))
+        N.call("pxk_attention_forward_stats", base, w3, base + 4 * qd, w3, base + 4 * (qd + kvd), w3, None, None,
+               G.ptr(stats), G.ptr(ctx), qd, n, L, H, Hkv, D, scale, causal, G.stream())
+        outs.append((G.host(stats), G.host(ctx)))
+    assert np.array_equal(outs[0][0], outs[1][0]) and np.array_equal(outs[0][1], outs[1][1])
+    raw, p, want_ctx, vis = attention_reference(qkv[:, :qd], qkv[:, qd:qd + kvd], qkv[:, qd + kvd:], n, L, H, Hkv, D,
+                                                scale, causal)
+    x = np.where(vis, scale * raw, -np.inf)
+    m = x.max(-1)
+    ssum = np.exp(x - m[..., None]).sum(-1)
+    got_st, got_ctx = outs[0]
+    G.assert_close(got_st[..., 0], m, 1e-4, "row max")
+    G.assert_close(got_st[..., 1], 1.0 / ssum, 1e-4, "1 / row sum")
+    G.assert_close(got_ctx, want_ctx, 1e-4, "ctx")
