@@ -1046,6 +1046,195 @@ __global__ void __launch_bounds__(NW * kWave) attn_rel_q2_kernel(const RelArgs a
     }
 }
 
+// GQA-shared recomputing q side, for grids many times the chip's size: one workgroup per
+// (sequence, KV head, 16-row block) and one wave per query head of the KV head's group, each wave
+// over all of the block's key tiles, so no merge. Every K / V tile comes from memory into LDS once
+// for the group (two buffers, the next tile's loads in flight during the current one) and supplies
+// the waves' K, V and transposed K fragments; each wave keeps its head's Q and s_pv fragments in
+// registers. Per tile the arithmetic is attn_rel_q2_kernel's, and so is the query share at the end
+// (its operands read from memory, once per workgroup).
+template <int DT, int G, bool VEC>
+__global__ void __launch_bounds__(G * kWave) attn_rel_q2_gqa_kernel(const RelArgs a) {
+    constexpr int NT = G * kWave, LD = 16 * DT + 4;
+    constexpr int PER = (16 * 4 * DT + NT - 1) / NT;  // float4 per thread per tile operand
+    __shared__ __attribute__((aligned(16))) float kv_lds[2][2][16][LD];  // [buffer][K, V][key][dim]
+    __shared__ __attribute__((aligned(16))) float m_acc[G][16][LD];      // each head's (s K) rows
+
+    const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, c = lane & 15;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: the query head
+    const int l = a.l, D = a.D;
+    const int nrb = (l + 15) / 16;
+    // Long causal rows first, KV heads fastest.
+    const int nbk = a.n * a.kv_heads;
+    const int rb = nrb - 1 - static_cast<int>(blockIdx.x) / nbk, bk = static_cast<int>(blockIdx.x) % nbk;
+    const int hk = bk % a.kv_heads, b = bk / a.kv_heads;
+    const int h = hk * G + wave;
+    const int i0 = rb * 16, row = i0 + c;
+    const int vis_end = a.causal ? min(i0 + 16, l) : l;
+    const int ntile = (vis_end + 15) / 16;
+    const int vis_row = a.causal ? min(row + 1, l) : l;  // keys visible to the lane's row
+    const int64_t tok0 = static_cast<int64_t>(b) * l, tok = tok0 + min(row, l - 1);
+    const int q4 = D / 4;
+
+    // Lane (c, g) holds dims 16 t + 4 g .. of row c: Q (B operand of raw^T) and s_pv (B operand of
+    // u), zeros past head_dim; sum = s_pv . ctx of the row over its four lanes.
+    f4 qf[DT], sf[DT];
+    float sum = 0.0f;
+#pragma unroll
+    for (int t = 0; t < DT; ++t) {
+        const int d0 = 16 * t + 4 * g, dc = min(d0, D - 4);
+        const float keep = d0 < D ? 1.0f : 0.0f;
+        qf[t] = *reinterpret_cast<const f4*>(a.q + tok * a.ld_q + h * D + dc) * keep;
+        sf[t] = *reinterpret_cast<const f4*>(a.spv + tok * a.ld_spv + h * D + dc) * keep;
+        const f4 cv = *reinterpret_cast<const f4*>(a.ctx + tok * a.ld_ctx + h * D + dc);
+        sum += sf[t][0] * cv[0] + sf[t][1] * cv[1] + sf[t][2] * cv[2] + sf[t][3] * cv[3];
+    }
+    sum = row_sum4(sum);
+    const float* strow = a.stats + 2 * ((static_cast<int64_t>(b) * a.heads + h) * l + min(row, l - 1));
+    const float m_row = strow[0], inv_row = strow[1];
+    if (a.row_sum && g == 0 && row < l) a.row_sum[(static_cast<int64_t>(b) * a.heads + h) * l + row] = sum;
+    float* s_row = a.s ? a.s + (static_cast<int64_t>(b) * a.heads + h) * l * l + static_cast<int64_t>(row) * l : nullptr;
+    float* p_row = a.p_out ? a.p_out + (static_cast<int64_t>(b) * a.heads + h) * l * l + static_cast<int64_t>(row) * l
+                           : nullptr;
+
+    const float* kbase = a.k + tok0 * a.ld_k + hk * D;
+    const float* vbase = a.v + tok0 * a.ld_v + hk * D;
+    // Columns past head_dim stay zero in both buffers: K's meet zero Q fragments and feed (s K)
+    // dims that are never stored, V's meet zero s_pv fragments.
+    for (int i = tid; i < 2 * 2 * 16 * (16 * DT - D); i += NT) {
+        const int w = 16 * DT - D, r = i / w, col = D + i - r * w;
+        (&kv_lds[0][0][0][0])[r * LD + col] = 0.0f;
+    }
+    // A tile's 16 K rows and 16 V rows as float4 pieces over the workgroup; rows past the sequence
+    // read its last row (finite: their keys are masked).
+    f4 sk[PER], sv[PER];
+    auto fetch = [&](int kt) {
+#pragma unroll
+        for (int j = 0; j < PER; ++j) {
+            const int i = min(tid + NT * j, 16 * q4 - 1);
+            const int r = i / q4, c4 = 4 * (i - r * q4);
+            const int64_t key = min(16 * kt + r, l - 1);
+            sk[j] = *reinterpret_cast<const f4*>(kbase + key * a.ld_k + c4);
+            sv[j] = *reinterpret_cast<const f4*>(vbase + key * a.ld_v + c4);
+        }
+    };
+    auto stash = [&](int buf) {
+#pragma unroll
+        for (int j = 0; j < PER; ++j) {
+            const int i = tid + NT * j;
+            if (i < 16 * q4) {
+                const int r = i / q4, c4 = 4 * (i - r * q4);
+                *reinterpret_cast<f4*>(&kv_lds[buf][0][r][c4]) = sk[j];
+                *reinterpret_cast<f4*>(&kv_lds[buf][1][r][c4]) = sv[j];
+            }
+        }
+    };
+
+    f4 acc[DT];
+#pragma unroll
+    for (int t = 0; t < DT; ++t) acc[t] = f4{0.f, 0.f, 0.f, 0.f};
+    fetch(0);
+    stash(0);
+    __syncthreads();
+    for (int kt = 0; kt < ntile; ++kt) {
+        const int buf = kt & 1;
+        if (kt + 1 < ntile) fetch(kt + 1);  // uniform
+        const int kk0 = 16 * kt + 4 * g;
+        // raw^T tile, the forward's sequence: lane (c, g) gets raw[row c][key kk0 + r]; u[r] =
+        // s_pv[row c] . V[key kk0 + r].
+        f4 sr = {0.f, 0.f, 0.f, 0.f}, u = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int t = 0; t < DT; ++t) {
+            const f4 kf = *reinterpret_cast<const f4*>(&kv_lds[buf][0][c][16 * t + 4 * g]);
+#pragma unroll
+            for (int st = 0; st < 4; ++st) sr = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[st], qf[t][st], sr, 0, 0, 0);
+        }
+#pragma unroll
+        for (int t = 0; t < DT; ++t) {
+            const f4 vf = *reinterpret_cast<const f4*>(&kv_lds[buf][1][c][16 * t + 4 * g]);
+#pragma unroll
+            for (int st = 0; st < 4; ++st) u = __builtin_amdgcn_mfma_f32_16x16x4f32(vf[st], sf[t][st], u, 0, 0, 0);
+        }
+        f4 s4, p4v;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const bool valid = kk0 + r < vis_row;
+            const float o = sr[r];
+            const float pv = valid ? __expf(a.scale * o - m_row) * inv_row : 0.0f;
+            const float rsc = (a.scale * o) * (pv * u[r] - pv * sum);
+            // The hardware reciprocal (1 ulp) in place of a full-precision divide.
+            s4[r] = valid ? rsc * __builtin_amdgcn_rcpf(2.0f * o + a.eps * ((o >= 0.0f) ? 1.0f : -1.0f)) : 0.0f;
+            p4v[r] = pv;
+        }
+        // s and P over the block's tiles up to its diagonal, zeros at the masked keys within them.
+        if (row < l && kk0 < l) {
+            if constexpr (VEC) {
+                if (s_row) *reinterpret_cast<f4*>(s_row + kk0) = s4;
+                if (p_row) *reinterpret_cast<f4*>(p_row + kk0) = p4v;
+            } else {
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    if (kk0 + r < l) {
+                        if (s_row) s_row[kk0 + r] = s4[r];
+                        if (p_row) p_row[kk0 + r] = p4v[r];
+                    }
+            }
+        }
+        // (s K)^T += K^T s^T: A = K[16 kt + 4 g + st][16 t + c].
+#pragma unroll
+        for (int t = 0; t < DT; ++t)
+#pragma unroll
+            for (int st = 0; st < 4; ++st)
+                acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv_lds[buf][0][4 * g + st][16 * t + c], s4[st], acc[t], 0, 0, 0);
+        // The other buffer was last read in the previous iteration, before its barrier.
+        if (kt + 1 < ntile) stash(buf ^ 1);
+        __syncthreads();
+    }
+
+    // acc[t][r] = (s K)^T[16 t + 4 g + r][row c] of head h, into the wave's rows.
+#pragma unroll
+    for (int t = 0; t < DT; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) m_acc[wave][c][16 * t + 4 * g + r] = acc[t][r];
+    __builtin_amdgcn_wave_barrier();
+    // Query share: r = Q_rot * (s K), the RoPE epsilon rule (lrp_math.hpp:104-123), then q_proj's
+    // denominator: g = r_in / stab(z + bias). Lane (rr, cc) takes dims cc + 4 j of row i0 + rr.
+    const int rr = lane >> 2, cc = lane & 3, orow = i0 + rr;
+    if (orow >= l) return;
+    const int half = D / 2;
+    const int64_t otok = tok0 + orow;
+    const float* yq = a.q + otok * a.ld_q + h * D;
+    float* gr = a.g + otok * a.ld_g + h * D;
+    for (int d = cc; d < D; d += 4) {
+        float r_in;
+        if (a.rope) {
+            const int i = a.rope_half ? (d < half ? d : d - half) : d / 2;
+            const int lo = a.rope_half ? i : 2 * i, hi = a.rope_half ? i + half : 2 * i + 1;
+            const float y_lo = yq[lo], y_hi = yq[hi];
+            const float r_lo = y_lo * m_acc[wave][rr][lo], r_hi = y_hi * m_acc[wave][rr][hi];
+            const float cs = a.cos_t[static_cast<int64_t>(orow) * half + i], sn = a.sin_t[static_cast<int64_t>(orow) * half + i];
+            const float d0 = stab(y_lo, a.eps), d1 = stab(y_hi, a.eps);
+            const float xv = a.q_pre[otok * a.ld_q_pre + h * D + d];
+            r_in = 0.0f;
+            if (d == lo) {
+                r_in += (xv * cs / d0) * r_lo;
+                r_in += (xv * sn / d1) * r_hi;
+            } else {
+                r_in += (xv * -sn / d0) * r_lo;
+                r_in += (xv * cs / d1) * r_hi;
+            }
+        } else {
+            r_in = yq[d] * m_acc[wave][rr][d];
+        }
+        if (a.rel_only) {
+            gr[d] = r_in;
+        } else {
+            const float zz = a.z[otok * a.ld_z + h * D + d];
+            gr[d] = r_in / stab(a.bias ? zz + a.bias[h * D + d] : zz, a.eps);
+        }
+    }
+}
+
 }  // namespace
 }  // namespace pxk
 
@@ -1268,6 +1457,21 @@ extern "C" int pxk_attention_relevance_q(const pxk_attn_rel_desc* d, void* strea
         {attn_rel_q2_kernel<1, true, rel_q2_waves<1>()>, attn_rel_q2_kernel<2, true, rel_q2_waves<2>()>,
          attn_rel_q2_kernel<4, true, rel_q2_waves<4>()>, attn_rel_q2_kernel<8, true, rel_q2_waves<8>()>}};
     const int di = dt == 1 ? 0 : dt == 2 ? 1 : dt == 4 ? 2 : 3;
+    if (rc && gqa_forward(n, l, H, Hkv)) {
+        // Wide grids: the GQA-shared form, under the forward's rule (the shapes where the
+        // statistics-form forward runs GQA-shared).
+#define PXK_Q2G(G) {attn_rel_q2_gqa_kernel<1, G, false>, attn_rel_q2_gqa_kernel<2, G, false>, \
+                    attn_rel_q2_gqa_kernel<4, G, false>, attn_rel_q2_gqa_kernel<8, G, false>}, \
+                   {attn_rel_q2_gqa_kernel<1, G, true>, attn_rel_q2_gqa_kernel<2, G, true>, \
+                    attn_rel_q2_gqa_kernel<4, G, true>, attn_rel_q2_gqa_kernel<8, G, true>}
+        static const K gqa[4][2][4] = {{PXK_Q2G(2)}, {PXK_Q2G(3)}, {PXK_Q2G(4)}, {PXK_Q2G(8)}};
+#undef PXK_Q2G
+        const int64_t grp = H / Hkv;
+        const int gi = grp == 2 ? 0 : grp == 3 ? 1 : grp == 4 ? 2 : 3;
+        PXK_LAUNCH(gqa[gi][vec ? 1 : 0][di], dim3(static_cast<unsigned>(n * Hkv * ((l + 15) / 16))),
+                   dim3(static_cast<unsigned>(grp * kWave)), 0, S(stream), a);
+        return launched("pxk_attention_relevance_q");
+    }
     const K fn = rc ? recompute[vec ? 1 : 0][di] : two_pass[vec ? 1 : 0][di];
     const int threads = rc ? (dt == 8 ? rel_q2_waves<8>() : rel_q2_waves<4>()) * kWave : kThreads;
     if (dyn > 64 * 1024 &&

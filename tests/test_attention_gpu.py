@@ -341,12 +341,13 @@ def test_fused_attention_kv_relevance_large_grid(causal, rope, half, bias):
 
 
 @gpu
-@pytest.mark.parametrize("n,L,H,Hkv,D", [(1, 200, 4, 2, 64), (2, 37, 3, 1, 16), (1, 512, 9, 3, 64)])
+@pytest.mark.parametrize("n,L,H,Hkv,D", [(1, 200, 4, 2, 64), (2, 37, 3, 1, 16), (1, 512, 9, 3, 64), (4, 512, 8, 4, 64)])
 def test_recomputing_chain_matches_score_row_chain(n, L, H, Hkv, D):
     """The step's attention relevance chain in its recomputing form (forward with row statistics,
     q side recomputing raw and P and writing s and P into NaN-filled buffers, key side reading
     them) against the score-row form (forward keeping raw and P, two-pass q side): the same
-    [g_q | g_k | g_v]. q and k hold multiples of 0.5, so raw = Q K^T is exact."""
+    [g_q | g_k | g_v]. q and k hold multiples of 0.5, so raw = Q K^T is exact. At 4 x 512 with
+    8 / 4 heads the recomputing forward and q side run GQA-shared."""
     print("recomputing chain n=%d L=%d H=%d Hkv=%d D=%d" % (n, L, H, Hkv, D), flush=True)
     qd, kvd = H * D, Hkv * D
     w3 = qd + 2 * kvd
@@ -563,3 +564,16 @@ def test_gqa_shared_forward_matches_numpy(n, L, H, Hkv, D, causal):
     G.assert_close(got_st[..., 0], m, 1e-4, "row max")
     G.assert_close(got_st[..., 1], 1.0 / ssum, 1e-4, "1 / row sum")
     G.assert_close(got_ctx, want_ctx, 1e-4, "ctx")
+
+
+@gpu
+@pytest.mark.parametrize("causal", [1, 0])
+@pytest.mark.parametrize("n,L,H,Hkv,D,rope,half,bias", [(4, 512, 8, 4, 64, 1, 1, 0), (2, 500, 24, 8, 40, 1, 0, 1),
+                                                       (16, 512, 8, 1, 12, 0, 0, 1), (4, 520, 16, 4, 32, 1, 1, 1)])
+def test_gqa_shared_q_relevance_matches_numpy(n, L, H, Hkv, D, rope, half, bias, causal):
+    """The recomputing q side on shapes that run GQA-shared (one workgroup per KV head and 16-row
+    block, a wave per query head over all of the block's key tiles, K / V tiles through LDS), with
+    the checks of test_fused_attention_relevance_matches_numpy: s and P on the visible keys, zeros
+    at the masked keys of the diagonal tiles, the row sums s_pv . ctx and g_q, against float64."""
+    assert gqa_plan()(n, L, H, Hkv) == 1
+    test_fused_attention_relevance_matches_numpy(n, L, H, Hkv, D, causal, rope, half, bias, 1)
