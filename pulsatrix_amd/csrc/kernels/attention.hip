@@ -1535,15 +1535,16 @@ __device__ __forceinline__ int kv_dim(const RelKvArgs& a, int dq, int c) {
     return d < a.D ? d : -1;
 }
 
-template <int U, int DG>
+template <int U, int DG, int KB>
 struct KvSet {
-    float s[U], p[U], q[DG][U], v[DG][U];
-    unsigned ok;  // bit u: the lane's row of item u is a real row
+    float s[KB][U], p[KB][U], q[DG][U], v[DG][U];
+    unsigned ok;  // bit KB u + j: the lane's row of item u is a real row that sees key block j
 };
 
-template <int NW, int U, int DG>
-__device__ __forceinline__ void kv_load(KvSet<U, DG>& r, const RelKvArgs& a, int b, int hk, int grp, int wave, int step,
-                                        int total, int nq, int i_start, int key_c, const int* dim_c, int g4) {
+template <int NW, int U, int DG, int KB>
+__device__ __forceinline__ void kv_load(KvSet<U, DG, KB>& r, const RelKvArgs& a, int b, int hk, int grp, int wave,
+                                        int step, int total, int nq, int i_start, const int* key_c,
+                                        const int* row_from, const int* dim_c, int g4) {
     r.ok = 0;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -1554,11 +1555,16 @@ __device__ __forceinline__ void kv_load(KvSet<U, DG>& r, const RelKvArgs& a, int
         const int h = hk * grp + j;
         const int i = i_start + 4 * qi + g4;
         const int ic = i < a.l ? i : a.l - 1;
-        if (it_ok && i < a.l) r.ok |= 1u << u;
         const int srow = ((b * a.heads + h) * a.l + ic) * a.l;
         const int trow = b * a.l + ic;
-        r.s[u] = a.s[srow + key_c];
-        r.p[u] = a.p[srow + key_c];
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) {
+            // Key block kb is read only from rows at or past its first row (the q side writes each
+            // row's keys up to the end of its diagonal tile); other rows take zeros.
+            if (it_ok && i < a.l && i >= row_from[kb]) r.ok |= 1u << (KB * u + kb);
+            r.s[kb][u] = a.s[srow + key_c[kb]];
+            r.p[kb][u] = a.p[srow + key_c[kb]];
+        }
 #pragma unroll
         for (int g = 0; g < DG; ++g) {
             r.q[g][u] = a.q[trow * a.ld_q + h * a.D + dim_c[g]];
@@ -1567,23 +1573,26 @@ __device__ __forceinline__ void kv_load(KvSet<U, DG>& r, const RelKvArgs& a, int
     }
 }
 
-template <int U, int DG>
-__device__ __forceinline__ void kv_compute(const KvSet<U, DG>& r, f4 (*acck)[2], f4 (*accv)[2]) {
+template <int U, int DG, int KB>
+__device__ __forceinline__ void kv_compute(const KvSet<U, DG, KB>& r, f4 (*acck)[DG][2], f4 (*accv)[DG][2]) {
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-        const bool ok = (r.ok >> u) & 1u;
-        const float as = ok ? r.s[u] : 0.0f, ap = ok ? r.p[u] : 0.0f;
+    for (int u = 0; u < U; ++u)
 #pragma unroll
-        for (int g = 0; g < DG; ++g) {
-            acck[g][u & 1] = __builtin_amdgcn_mfma_f32_16x16x4f32(as, r.q[g][u], acck[g][u & 1], 0, 0, 0);
-            accv[g][u & 1] = __builtin_amdgcn_mfma_f32_16x16x4f32(ap, r.v[g][u], accv[g][u & 1], 0, 0, 0);
+        for (int kb = 0; kb < KB; ++kb) {
+            const bool ok = (r.ok >> (KB * u + kb)) & 1u;
+            const float as = ok ? r.s[kb][u] : 0.0f, ap = ok ? r.p[kb][u] : 0.0f;
+#pragma unroll
+            for (int g = 0; g < DG; ++g) {
+                acck[kb][g][u & 1] = __builtin_amdgcn_mfma_f32_16x16x4f32(as, r.q[g][u], acck[kb][g][u & 1], 0, 0, 0);
+                accv[kb][g][u & 1] = __builtin_amdgcn_mfma_f32_16x16x4f32(ap, r.v[g][u], accv[kb][g][u & 1], 0, 0, 0);
+            }
         }
-    }
 }
 
-// NW waves per workgroup, U items per register set, DG dim groups of 16 per workgroup: the score
-// rows (s, P) of a key block are read once for DG groups' query and s_pv columns.
-template <int NW, int U, int DG>
+// NW waves per workgroup, U items per register set, DG dim groups of 16 and KB consecutive 16-key
+// blocks per workgroup: the score rows (s, P) of a key block are read once for DG groups' query
+// and s_pv columns, and each query and s_pv row once for KB key blocks.
+template <int NW, int U, int DG, int KB>
 __global__ void __launch_bounds__(NW * kWave) attn_rel_kv_kernel(const RelKvArgs a) {
     __shared__ float red[2][NW][16][17];  // per-wave k / v partial blocks [key][dim column], one group at a time
 
@@ -1594,13 +1603,20 @@ __global__ void __launch_bounds__(NW * kWave) attn_rel_kv_kernel(const RelKvArgs
     const int ngb = a.ngroups / DG;
     const int dqb = id % ngb;
     const int t = id / ngb;
-    const int tkb = t % a.nkb, bg = t / a.nkb;
-    const int kb = (tkb & 1) ? a.nkb - 1 - (tkb >> 1) : (tkb >> 1);  // long and short causal blocks alternate
+    const int nkg = (a.nkb + KB - 1) / KB;  // groups of KB key blocks
+    const int tkb = t % nkg, bg = t / nkg;
+    const int kg = (tkb & 1) ? nkg - 1 - (tkb >> 1) : (tkb >> 1);  // long and short causal blocks alternate
     const int hk = bg % a.kv_heads, b = bg / a.kv_heads;
     const int grp = a.heads / a.kv_heads;
-    const int m0 = kb * 16;
+    const int m0 = kg * KB * 16;
 
-    const int key_c = min(m0 + c, a.l - 1);
+    int key_c[KB], row_from[KB];  // the lane's key column and the first row reading it, per key block
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) {
+        key_c[kb] = min(m0 + 16 * kb + c, a.l - 1);
+        // A key block past the sequence (the last group's second block) is read by no row.
+        row_from[kb] = m0 + 16 * kb >= a.l ? a.l : (a.causal ? m0 + 16 * kb : 0);
+    }
     int dim_c[DG];
 #pragma unroll
     for (int g = 0; g < DG; ++g) {
@@ -1613,33 +1629,37 @@ __global__ void __launch_bounds__(NW * kWave) attn_rel_kv_kernel(const RelKvArgs
     const int mine = total > wave ? (total - wave + NW - 1) / NW : 0;
     const int steps = (mine + U - 1) / U;
 
-    f4 acck[DG][2], accv[DG][2];
+    f4 acck[KB][DG][2], accv[KB][DG][2];
 #pragma unroll
-    for (int g = 0; g < DG; ++g)
+    for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
-        for (int h = 0; h < 2; ++h) acck[g][h] = accv[g][h] = f4{0.f, 0.f, 0.f, 0.f};
-    KvSet<U, DG> s0, s1;
-    kv_load<NW, U, DG>(s0, a, b, hk, grp, wave, 0, total, nq, i_start, key_c, dim_c, g4);
-    kv_load<NW, U, DG>(s1, a, b, hk, grp, wave, 1, total, nq, i_start, key_c, dim_c, g4);
+        for (int g = 0; g < DG; ++g)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) acck[kb][g][h] = accv[kb][g][h] = f4{0.f, 0.f, 0.f, 0.f};
+    KvSet<U, DG, KB> s0, s1;
+    kv_load<NW, U, DG, KB>(s0, a, b, hk, grp, wave, 0, total, nq, i_start, key_c, row_from, dim_c, g4);
+    kv_load<NW, U, DG, KB>(s1, a, b, hk, grp, wave, 1, total, nq, i_start, key_c, row_from, dim_c, g4);
     __builtin_amdgcn_sched_barrier(0);
     for (int st = 0; st < steps; st += 2) {
         kv_compute(s0, acck, accv);
-        kv_load<NW, U, DG>(s0, a, b, hk, grp, wave, st + 2, total, nq, i_start, key_c, dim_c, g4);
+        kv_load<NW, U, DG, KB>(s0, a, b, hk, grp, wave, st + 2, total, nq, i_start, key_c, row_from, dim_c, g4);
         __builtin_amdgcn_sched_barrier(0);
         kv_compute(s1, acck, accv);
-        kv_load<NW, U, DG>(s1, a, b, hk, grp, wave, st + 3, total, nq, i_start, key_c, dim_c, g4);
+        kv_load<NW, U, DG, KB>(s1, a, b, hk, grp, wave, st + 3, total, nq, i_start, key_c, row_from, dim_c, g4);
         __builtin_amdgcn_sched_barrier(0);
     }
 
-    // Epilogue, one dim group at a time: thread -> (key row kl, dim column nn) of its 16 x 16 block.
+    // Epilogue, one key block and dim group at a time: thread -> (key row kl, dim column nn) of its
+    // 16 x 16 block.
     const int kl = threadIdx.x >> 4, nn = threadIdx.x & 15;
-    const int m = m0 + kl;
-    const int row = b * a.l + m;
     const float eps = a.eps;
 #pragma unroll
-    for (int g = 0; g < DG; ++g) {
-        const f4 kk = acck[g][0] + acck[g][1], vv = accv[g][0] + accv[g][1];
-        if (g > 0) __syncthreads();  // the previous group's epilogue has read red
+    for (int e = 0; e < KB * DG; ++e) {
+        const int kb = e / DG, g = e % DG;
+        const int m = m0 + 16 * kb + kl;
+        const int row = b * a.l + m;
+        const f4 kk = acck[kb][g][0] + acck[kb][g][1], vv = accv[kb][g][0] + accv[kb][g][1];
+        if (e > 0) __syncthreads();  // the previous block's epilogue has read red
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             red[0][wave][4 * g4 + r][c] = kk[r];
@@ -1697,6 +1717,9 @@ __global__ void __launch_bounds__(NW * kWave) attn_rel_kv_kernel(const RelKvArgs
 
 }  // namespace
 
+// 16-key blocks per workgroup of the wide-grid key side (four dim groups per workgroup).
+constexpr int kKvBlocks = 2;
+
 extern "C" int pxk_attention_relevance_kv(const pxk_attn_rel_kv_desc* d, void* stream) {
     const int64_t n = d->n, l = d->l, H = d->heads, Hkv = d->kv_heads, D = d->head_dim;
     if (n < 0 || l < 0 || H <= 0 || Hkv <= 0 || H % Hkv != 0 || D <= 0 || D > 1024 || (d->rope && D % 2 != 0))
@@ -1725,24 +1748,29 @@ extern "C" int pxk_attention_relevance_kv(const pxk_attn_rel_kv_desc* d, void* s
                 static_cast<int>(d->ld_g), static_cast<int>(n), static_cast<int>(l), static_cast<int>(H),
                 static_cast<int>(Hkv), static_cast<int>(D), static_cast<int>(ngroups), static_cast<int>(nkb), d->eps,
                 d->causal != 0, d->rope != 0, d->rope_half != 0, blocks % 8 == 0, d->relevance_only != 0};
-    // One item per register set throughout. Four dim groups per workgroup where they divide evenly
-    // and the grid stays above eight workgroups per CU (many sequences, or head_dim 256), so the
-    // score rows are read a quarter as often, on eight waves: 1089 us against 1165 for sixteen
-    // waves with two items per set, 1209 for two groups, at 8 x 1024, 32 / 8 heads of 64.
-    // Otherwise sixteen waves, the widest spread of a long key block's rows, and two dim groups
-    // where they divide (the score rows read half as often, 192 workgroups for one 512-token
+    // One item per register set throughout. Four dim groups and two 16-key blocks per workgroup
+    // where the dim groups divide evenly and there are at least 512 (KV head, key block, 4 groups)
+    // units (wide grids: many sequences, long ones, or head_dim 256), so each score row is read a
+    // quarter as often and each query and s_pv row half as often, on eight waves: at 32 / 8 heads
+    // of 64, 8 x 1024 tokens 706 us against 1101 with one key block per workgroup (1165 for sixteen
+    // waves with two items per set, 1209 for two groups), 2 x 1024 233 against 340 for two groups,
+    // 1 x 2048 377 against 625, 1 x 1024 121 against 138; four key blocks per workgroup 739 at
+    // 8 x 1024. Otherwise sixteen waves, the widest spread of a long key block's rows, and two dim
+    // groups where they divide (the score rows read half as often, 192 workgroups for one 512-token
     // sequence of three KV heads): 20.2 us against 23.2 for one group and two items per set, 34 for
-    // four groups (96 workgroups) at 1 x 512, 9 / 3 heads of 64.
-    if (ngroups % 4 == 0 && blocks / 4 >= 2048) {
-        a.remap = (blocks / 4) % 8 == 0;
-        PXK_LAUNCH((attn_rel_kv_kernel<8, 1, 4>), dim3(static_cast<unsigned>(blocks / 4)), dim3(8 * kWave), 0,
+    // four groups (96 workgroups) at 1 x 512, 9 / 3 heads of 64; at 4 x 512 (384 units) 46 against
+    // 53 for the wide form.
+    if (ngroups % 4 == 0 && blocks / 4 >= 512) {
+        const int64_t wg = n * Hkv * ((nkb + kKvBlocks - 1) / kKvBlocks) * (ngroups / 4);
+        a.remap = wg % 8 == 0;
+        PXK_LAUNCH((attn_rel_kv_kernel<8, 1, 4, kKvBlocks>), dim3(static_cast<unsigned>(wg)), dim3(8 * kWave), 0,
                            S(stream), a);
     } else if (ngroups % 2 == 0) {
         a.remap = (blocks / 2) % 8 == 0;
-        PXK_LAUNCH((attn_rel_kv_kernel<16, 1, 2>), dim3(static_cast<unsigned>(blocks / 2)), dim3(16 * kWave), 0,
+        PXK_LAUNCH((attn_rel_kv_kernel<16, 1, 2, 1>), dim3(static_cast<unsigned>(blocks / 2)), dim3(16 * kWave), 0,
                            S(stream), a);
     } else {
-        PXK_LAUNCH((attn_rel_kv_kernel<16, 1, 1>), dim3(static_cast<unsigned>(blocks)), dim3(16 * kWave), 0,
+        PXK_LAUNCH((attn_rel_kv_kernel<16, 1, 1, 1>), dim3(static_cast<unsigned>(blocks)), dim3(16 * kWave), 0,
                            S(stream), a);
     }
     return launched("pxk_attention_relevance_kv");

@@ -333,11 +333,14 @@ def test_fused_attention_kv_relevance_matches_numpy(n, L, H, Hkv, D, causal, rop
 
 
 @gpu
-@pytest.mark.parametrize("causal,rope,half,bias", [(1, 1, 1, 0), (0, 0, 0, 1)])
-def test_fused_attention_kv_relevance_large_grid(causal, rope, half, bias):
-    """The launch with four head-dim groups per workgroup, taken once the grid holds 2048 such
-    workgroups: 4 sequences x 32 KV heads x 16 key blocks x 4 groups / 4 here."""
-    test_fused_attention_kv_relevance_matches_numpy(4, 256, 32, 32, 64, causal, rope, half, bias)
+@pytest.mark.parametrize("n,L,H,Hkv,D", [(4, 256, 32, 32, 64), (4, 232, 32, 32, 64), (4, 200, 16, 8, 128)])
+@pytest.mark.parametrize("causal,rope,half,bias", [(1, 1, 1, 0), (0, 0, 0, 1), (1, 1, 0, 1)])
+def test_fused_attention_kv_relevance_large_grid(n, L, H, Hkv, D, causal, rope, half, bias):
+    """The wide-grid launch, four head-dim groups and two 16-key blocks per workgroup, taken from 512
+    (KV head, key block, four groups) units: 4 x 32 x 16 (x 4 / 4) = 2048 at 4 x 256 tokens; an odd
+    count of key blocks at 232 tokens (15: the last workgroup's second block lies past the
+    sequence); head_dim 128 (8 groups) with 13 key blocks."""
+    test_fused_attention_kv_relevance_matches_numpy(n, L, H, Hkv, D, causal, rope, half, bias)
 
 
 @gpu
