@@ -9,6 +9,7 @@
   second run), the on-device targets are the argmax of the on-device logits, and a sequence's
   relevance does not depend on the batch it runs in (sequence 3 of the batch against the same
   sequence run alone, at the relevance gate)."""
+import ctypes
 import time
 
 import numpy as np
@@ -17,6 +18,7 @@ import pytest
 import gpu_util as G
 import oracle_ctypes as oc
 from pulsatrix_amd import models
+from pulsatrix_amd import native as N
 from test_model_gpu import argmax_seed, expect_logits_agree, expect_relevance_agrees, to_px
 
 pytestmark = pytest.mark.gpu
@@ -47,6 +49,31 @@ def test_l1b_widths_match_oracle():
     print("L1B widths, 2 layers, batch 2 x 64", flush=True)
     params = oc.synthetic_params(cfg, 41)
     ids = np.random.RandomState(42).randint(0, cfg.vocab_size, size=(2, 64))
+    gpu = models.CausalLM(to_px(cfg), params)
+    lg = gpu.forward(ids)
+    ref = oc.oracle().lm(cfg, params)
+    lr = ref.forward(ids)
+    expect_logits_agree(lg, lr, "logits")
+    seed = argmax_seed(lr)
+    a = gpu.relevance(seed, LXT_EPS, True, want_kv=True)
+    b = ref.relevance(seed, LXT_EPS, True, want_kv=True)
+    for what, x, y in zip(("embedding", "tokens", "keys", "values"), a, b):
+        expect_relevance_agrees(x, y, what)
+
+
+def test_wide_grid_attention_matches_oracle():
+    """A batch wide enough for the attention kernels' wide-grid forms (8 sequences x 4 KV heads: the
+    GQA-shared forward and q side, the key side with two key blocks per workgroup), at reduced
+    widths so the oracle runs it: 2 layers, hidden 256, 16 / 4 heads of 64, batch 8 x 256."""
+    cfg = oc.model_config(vocab_size=1000, hidden_size=256, num_layers=2, num_heads=16, num_kv_heads=4, head_dim=64,
+                          intermediate_size=512, rms_norm_eps=1e-5, rope_theta=10000.0)
+    print("wide-grid attention, 2 layers, batch 8 x 256", flush=True)
+    fn = N.pxk().pxk_attention_forward_gqa
+    fn.argtypes = [ctypes.c_int64] * 4
+    fn.restype = ctypes.c_int
+    assert fn(8, 256, 16, 4) == 1
+    params = oc.synthetic_params(cfg, 43)
+    ids = np.random.RandomState(44).randint(0, cfg.vocab_size, size=(8, 256))
     gpu = models.CausalLM(to_px(cfg), params)
     lg = gpu.forward(ids)
     ref = oc.oracle().lm(cfg, params)
