@@ -225,6 +225,16 @@ __device__ __forceinline__ void st4(float* p, f4 v, bool vec, int cnt) {
     for (int j = 0; j < 4; ++j)
         if (j < cnt) p[j] = v[j];
 }
+// Split-K partials, which the reduce launch reads next, are stored as ordinary lines.
+__device__ __forceinline__ void st4_keep(float* p, f4 v, bool vec, int cnt) {
+    if (vec) {
+        *reinterpret_cast<f4*>(p) = v;
+        return;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        if (j < cnt) p[j] = v[j];
+}
 
 // MUL_X_SPLIT's second share divided by the stabilised denominator of the relevance GEMM that reads
 // it next (that GEMM then needs no DIV_STAB prologue): r / stab(den + bias[n]).
@@ -620,7 +630,7 @@ __device__ __forceinline__ void finish_tile(f4 (&acc)[C::TM][C::TN], float* smem
             const int64_t m = m0 + row, n = n0 + col;
             if (m >= g.M || n >= g.N) continue;
             const int cnt = g.N - n < 4 ? static_cast<int>(g.N - n) : 4;
-            st4(P + m * g.N + n, *reinterpret_cast<const f4*>(smem + row * LDC + col), vec && cnt == 4, cnt);
+            st4_keep(P + m * g.N + n, *reinterpret_cast<const f4*>(smem + row * LDC + col), vec && cnt == 4, cnt);
         }
         return;
     }
