@@ -291,7 +291,7 @@ def relevance_kv_reference(s, p, q, spv, k, k_pre, v, z_k, z_v, bk, bv, cos, sin
 @pytest.mark.parametrize("rope,half,bias", [(1, 1, 0), (1, 0, 1), (0, 0, 1)])
 @pytest.mark.parametrize("causal", [1, 0])
 @pytest.mark.parametrize("n,L,H,Hkv,D", [(1, 37, 4, 2, 16), (2, 64, 3, 1, 12), (1, 128, 9, 3, 64), (1, 40, 2, 2, 128),
-                                         (1, 512, 9, 3, 64), (2, 70, 4, 4, 20)])
+                                         (1, 512, 9, 3, 64), (2, 70, 4, 4, 20), (1, 23, 6, 2, 8)])
 def test_fused_attention_kv_relevance_matches_numpy(n, L, H, Hkv, D, causal, rope, half, bias):
     print("kv relevance n=%d L=%d H=%d Hkv=%d D=%d causal=%d rope=%d half=%d" % (n, L, H, Hkv, D, causal, rope, half),
           flush=True)
@@ -333,13 +333,15 @@ def test_fused_attention_kv_relevance_matches_numpy(n, L, H, Hkv, D, causal, rop
 
 
 @gpu
-@pytest.mark.parametrize("n,L,H,Hkv,D", [(4, 256, 32, 32, 64), (4, 232, 32, 32, 64), (4, 200, 16, 8, 128)])
+@pytest.mark.parametrize("n,L,H,Hkv,D", [(4, 256, 32, 32, 64), (4, 232, 32, 32, 64), (4, 200, 16, 8, 128),
+                                         (4, 230, 32, 32, 64)])
 @pytest.mark.parametrize("causal,rope,half,bias", [(1, 1, 1, 0), (0, 0, 0, 1), (1, 1, 0, 1)])
 def test_fused_attention_kv_relevance_large_grid(n, L, H, Hkv, D, causal, rope, half, bias):
     """The wide-grid launch, four head-dim groups and two 16-key blocks per workgroup, taken from 512
     (KV head, key block, four groups) units: 4 x 32 x 16 (x 4 / 4) = 2048 at 4 x 256 tokens; an odd
     count of key blocks at 232 tokens (15: the last workgroup's second block lies past the
-    sequence); head_dim 128 (8 groups) with 13 key blocks."""
+    sequence); head_dim 128 (8 groups) with 13 key blocks; 230 tokens, whose last 4-row chunk holds
+    two rows."""
     test_fused_attention_kv_relevance_matches_numpy(n, L, H, Hkv, D, causal, rope, half, bias)
 
 
