@@ -1838,10 +1838,21 @@ extern "C" int pxk_attention_relevance_kv(const pxk_attn_rel_kv_desc* d, void* s
     // sequence of three KV heads): 20.2 us against 23.2 for one group and two items per set, 34 for
     // four groups (96 workgroups) at 1 x 512, 9 / 3 heads of 64; at 4 x 512 (384 units) 46 against
     // 53 for the wide form.
+    // Between the two: four dim groups per workgroup, one 16-key block, sixteen waves, from 128
+    // (KV head, key block) pairs (one workgroup each at head_dim 64), where the score rows read once
+    // instead of twice beat the wider spread (with the scalar-base loader, at 9 / 3 heads of 64:
+    // 2 x 512 26.1 against 30.4 us, 1 x 1024 41.5 against 53.0, 1 x 2048 133.8 against 166.8; 16 / 4
+    // heads at 1 x 1024 53.1 against 69.5; 4 x 512 45.3 against 47.0). Below 128 pairs (1 x 512
+    // with 3 KV heads: 96) two groups stay ahead, 17.9 against 25.4 us.
+    const int64_t pairs = n * Hkv * nkb;
     if (ngroups % 4 == 0 && blocks / 4 >= 512) {
         const int64_t wg = n * Hkv * ((nkb + kKvBlocks - 1) / kKvBlocks) * (ngroups / 4);
         a.remap = wg % 8 == 0;
         PXK_LAUNCH((attn_rel_kv_kernel<8, 1, 4, kKvBlocks>), dim3(static_cast<unsigned>(wg)), dim3(8 * kWave), 0,
+                           S(stream), a);
+    } else if (ngroups % 4 == 0 && pairs >= 128) {
+        a.remap = (blocks / 4) % 8 == 0;
+        PXK_LAUNCH((attn_rel_kv_kernel<16, 1, 4, 1>), dim3(static_cast<unsigned>(blocks / 4)), dim3(16 * kWave), 0,
                            S(stream), a);
     } else if (ngroups % 2 == 0) {
         a.remap = (blocks / 2) % 8 == 0;

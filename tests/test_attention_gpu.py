@@ -334,14 +334,15 @@ def test_fused_attention_kv_relevance_matches_numpy(n, L, H, Hkv, D, causal, rop
 
 @gpu
 @pytest.mark.parametrize("n,L,H,Hkv,D", [(4, 256, 32, 32, 64), (4, 232, 32, 32, 64), (4, 200, 16, 8, 128),
-                                         (4, 230, 32, 32, 64)])
+                                         (4, 230, 32, 32, 64), (2, 500, 8, 4, 64), (1, 1030, 6, 3, 64)])
 @pytest.mark.parametrize("causal,rope,half,bias", [(1, 1, 1, 0), (0, 0, 0, 1), (1, 1, 0, 1)])
 def test_fused_attention_kv_relevance_large_grid(n, L, H, Hkv, D, causal, rope, half, bias):
     """The wide-grid launch, four head-dim groups and two 16-key blocks per workgroup, taken from 512
     (KV head, key block, four groups) units: 4 x 32 x 16 (x 4 / 4) = 2048 at 4 x 256 tokens; an odd
     count of key blocks at 232 tokens (15: the last workgroup's second block lies past the
     sequence); head_dim 128 (8 groups) with 13 key blocks; 230 tokens, whose last 4-row chunk holds
-    two rows."""
+    two rows. Then the four-group, one-block launch for 128 to 511 (KV head, key block) pairs: 256
+    at 2 x 500 tokens with 4 KV heads, 195 at 1030 tokens with 3 (its last chunk two rows long)."""
     test_fused_attention_kv_relevance_matches_numpy(n, L, H, Hkv, D, causal, rope, half, bias)
 
 
