@@ -48,18 +48,18 @@ LXT_EPS = 1e-9
 # kernel when that kernel was measured under this plan.
 STEP_KERNEL_TRAFFIC = {name: kib * 1024 for name, kib in {
     "gemm 32x64d NN pro2 epi9 split1": 14094,  # q|k|v projection (norm folded, RoPE epilogue)
-    "attn_fwd": 8234,  # fused attention forward, statistics form (ctx and per-row softmax statistics)
-    "gemm 32x48d NN pro0 epi2 split1": 17657,  # o and down projections (median of both)
+    "attn_fwd": 8240,  # fused attention forward, statistics form (ctx and per-row softmax statistics)
+    "gemm 32x48d NN pro0 epi2 split1": 17649,  # o and down projections (median of both)
     "gemm 32x64 NN pro2 epi10 split1": 28750,  # gate|up projection (norm folded, SwiGLU epilogue)
-    "gemm 128x128 NT pro0 epi0 split1": 228936,  # LM head forward
+    "gemm 128x128 NT pro0 epi0 split1": 228592,  # LM head forward
     "head_seeded_relevance": 2554,
-    "gemm 32x48 NT pro0 epi7 split1": 24947,  # down relevance (SwiGLU rule epilogue)
-    "gemm 32x48 NT pro0 epi8 split4": 39472,  # gate|up relevance + its split-K reduce and residual split
-    "gemm 32x48d NT pro0 epi4 split1": 9850,  # o relevance (s_pv epilogue)
-    "attn_rel_q": 22326,  # q side, recomputing raw and P; writes s and P for the key side
-    "attn_rel_kv": 19342,  # key / value side
-    "gemm 32x48d NT pro0 epi8 split1": 19931,  # q|k|v relevance (residual split)
-    "gemm 32x48d NT pro0 epi3 split1": 16012,  # q|k|v relevance of block 0
+    "gemm 32x48 NT pro0 epi7 split1": 24936,  # down relevance (SwiGLU rule epilogue)
+    "gemm 32x48 NT pro0 epi8 split4": 38806,  # gate|up relevance + its split-K reduce and residual split
+    "gemm 32x48d NT pro0 epi4 split1": 9856,  # o relevance (s_pv epilogue)
+    "attn_rel_q": 22324,  # q side, recomputing raw and P; writes s and P for the key side
+    "attn_rel_kv": 19364,  # key / value side
+    "gemm 32x48d NT pro0 epi8 split1": 19934,  # q|k|v relevance (residual split)
+    "gemm 32x48d NT pro0 epi3 split1": 16014,  # q|k|v relevance of block 0
 }.items()}
 # The same for the decode step's tied head (4 x 640 x 262144, skinny NT; `bench.py --decode-probe`,
 # profiles/decode_head_gemm_traffic.md): FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0 of the median dispatch.
