@@ -800,19 +800,27 @@ __global__ void __launch_bounds__(NW * kWave) attn_rel_q2_kernel(const RelArgs a
 
     // K and V tiles, two sets: kf[t][s] = K[key0 + c][16 t + 4 g + s] (A of raw^T), va[t][s] =
     // V[key0 + c][16 t + 4 g + s] (A of u). A set is reloaded with the tile after next right after
-    // its last read, addresses clamped, so no branch surrounds a load.
+    // its last read; past the last tile the last one again, so no branch surrounds a load. As in
+    // attn_fwd_kernel the loads are buffer loads from a per-tile resource built with scalar
+    // instructions, each lane's byte offset fixed for the loop, the range (kv_tile_records) ending
+    // with the head's D values of the sequence's last row: rows past the sequence read 0 (their keys
+    // are masked), columns past head_dim read finite neighbouring data that meets zero Q and s_pv
+    // fragments, and their (s K) dims are never stored.
     const float* vbase = a.v + static_cast<int64_t>(b) * l * a.ld_v + hk * D;
     const float* kbase = a.k + static_cast<int64_t>(b) * l * a.ld_k + hk * D;
     const int ldv = a.ld_v, ldk = a.ld_k;
+    const int koff = (c * ldk + 4 * g) * 4, voff = (c * ldv + 4 * g) * 4;
     f4 kf[2][DT], va[2][DT];
     auto load = [&](int set, int kt) {
-        const int kr = min(16 * min(kt, ntile - 1) + c, l - 1);
-        const float* kp = kbase + kr * ldk;
-        const float* vp = vbase + kr * ldv;
+        const int key0 = 16 * min(kt, ntile - 1);
+        const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float*>(kbase + key0 * ldk), 0, kv_tile_records(l, key0, ldk, D), 0x00020000);
+        const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float*>(vbase + key0 * ldv), 0, kv_tile_records(l, key0, ldv, D), 0x00020000);
 #pragma unroll
         for (int t = 0; t < DT; ++t) {
-            kf[set][t] = *reinterpret_cast<const f4*>(kp + min(16 * t + 4 * g, D - 4));
-            va[set][t] = *reinterpret_cast<const f4*>(vp + min(16 * t + 4 * g, D - 4));
+            kf[set][t] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rk, koff + 64 * t, 0, 0));
+            va[set][t] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rv, voff + 64 * t, 0, 0));
         }
     };
     // ---- the burst: the block's row operands into LDS, and the first K / V tile ----
@@ -1434,8 +1442,11 @@ extern "C" int pxk_attention_relevance_q(const pxk_attn_rel_desc* d, void* strea
     const int64_t blocks = n * H * ((l + 15) / 16);
     const int64_t lds_max = std::max({d->ld_spv, d->ld_v, d->ld_k, d->ld_q, d->ld_q_pre, d->ld_z, d->ld_g,
                                       rc ? d->ld_ctx : int64_t{0}});
+    // The recomputing form's K / V tile resources count bytes in 32 bits (kv_tile_records), as the
+    // forward's do.
     if (blocks > (int64_t{1} << 31) - 1 || n * l * lds_max >= (int64_t{1} << 31) ||
-        ((d->s || d->p_out) && n * H * l * l >= (int64_t{1} << 40)))
+        ((d->s || d->p_out) && n * H * l * l >= (int64_t{1} << 40)) ||
+        (rc && ((l * d->ld_k + D) * 4 >= (int64_t{1} << 31) || (l * d->ld_v + D) * 4 >= (int64_t{1} << 31))))
         return fail(PXK_ERR_INVALID, "pxk_attention_relevance_q: problem too large");
     RelArgs a{d->spv, d->v, d->k, d->p, d->raw, d->s, d->q, d->q_pre, d->z, d->bias, d->cos_t, d->sin_t, d->g,
               static_cast<int>(d->ld_spv), static_cast<int>(d->ld_v), static_cast<int>(d->ld_k),

@@ -1,4 +1,5 @@
-"""Every address the attention forward's K / V tile loads can touch, checked on the host.
+"""Every address the attention forward's K / V tile loads (and the recomputing q side's, which read
+V with K's lane layout) can touch, checked on the host.
 
 attn_fwd_kernel reads each 16-key tile of a KV head through a buffer resource whose range is
 pxk_attention_kv_tile_records(l, key0, ld, head_dim) bytes from the tile's first row of the head's
@@ -45,16 +46,17 @@ def layouts(n, l, heads, kv_heads, d):
     yield "tight", 0, kvd, rows * kvd, 0, kvd, rows * kvd
 
 
-def max_reach(records_fn, n, l, kv_heads, d, col, ld, size):
+def max_reach(records_fn, n, l, kv_heads, d, col, ld, size, patterns=(0, 1)):
     """The largest element index inside the range, over every sequence, KV head and tile, relative to
-    the operand allocation (must be < size), and the smallest (must be >= 0)."""
+    the operand allocation (must be < size), and the smallest (must be >= 0). patterns: the lane
+    layouts read (0: 16-byte rows, 1: 4-byte columns)."""
     dt = dt_of(d)
     k_off, v_off = lane_dwords(ld, dt)
     hi, lo = -1, 1 << 62
     for key0 in range(0, l, 16):
         for hk in range(kv_heads):
             records = records_fn(l, key0, ld, d, hk)
-            for offs in (k_off, v_off):
+            for offs in [(k_off, v_off)[i] for i in patterns]:
                 inside = offs[offs * 4 < records]
                 if inside.size == 0:
                     continue
@@ -87,6 +89,16 @@ def test_forward_kv_tile_loads_stay_inside_their_operands():
             for what, col, ld, size in (("K", kc, kld, ksize), ("V", vc, vld, vsize)):
                 hi, lo = max_reach(rec, n, l, hkv, d, col, ld, size)
                 assert 0 <= lo and hi < size, (name, what, n, l, h, hkv, d, hi, size)
+
+
+def test_q_side_v_tile_loads_stay_inside_their_operand():
+    """attn_rel_q2_kernel reads its V tiles with K's lane layout (16-byte rows, c * ld + 4 g + 16 t)
+    through the same range: every dword inside it must lie inside the V operand too."""
+    rec = library_records()
+    for n, l, h, hkv, d in SHAPES:
+        for name, _, _, _, vc, vld, vsize in layouts(n, l, h, hkv, d):
+            hi, lo = max_reach(rec, n, l, hkv, d, vc, vld, vsize, patterns=(0,))
+            assert 0 <= lo and hi < vsize, (name, n, l, h, hkv, d, hi, vsize)
 
 
 def test_range_ends_with_the_heads_values_of_the_last_row():
