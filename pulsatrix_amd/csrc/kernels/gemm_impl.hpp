@@ -492,6 +492,30 @@ struct PanelLoader {
         }
     }
 
+    // Byte offsets of this thread's 16-byte pieces from the panel's first element, the same for
+    // every stage: the loop then loads from a wave-uniform panel base in scalar registers plus a
+    // fixed lane offset (global_load ... saddr), with no per-stage vector address arithmetic.
+    // Requires R * ld < 2^29 (checked by the caller).
+    __device__ __forceinline__ static void lane_offsets(int64_t ld, unsigned (&off)[P::NV]) {
+        const int tid = threadIdx.x;
+#pragma unroll
+        for (int i = 0; i < P::NV; ++i) {
+            int64_t r, c;
+            coords(tid + i * T, 0, 0, r, c);
+            off[i] = 4u * static_cast<unsigned>(r * ld + c);
+        }
+    }
+
+    // issue_fast without a prologue operand: the panel at `base` (its first element), as a buffer
+    // resource built with scalar instructions and the lanes' fixed offsets (every piece lies inside
+    // the matrix on this path; the range only has to cover the panel).
+    __device__ __forceinline__ void issue_base(const float* base, const unsigned (&off)[P::NV]) {
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), 0, 0x7FFFFFFF, 0x00020000);
+#pragma unroll
+        for (int i = 0; i < P::NV; ++i)
+            v[i] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rs, static_cast<int>(off[i]), 0, 0));
+    }
+
     // Any panel: element-wise bounds checks, zeros outside the matrix.
     __device__ __forceinline__ void issue(const Args& g, const float* A, int64_t lda, const float* Z, int64_t ldz,
                                           const float* ZB, int64_t mn, int64_t r0, int64_t k0) {
@@ -725,11 +749,24 @@ __global__ void __launch_bounds__(C::NT) gemm_kernel(const Args g) {
     // commits), so the loop body has no branches around vector loads.
     const bool k_inside = k_lo + nkb * BK <= g.K;
     const bool fast = nt >= NS + 1 && k_inside && g.vec_a && g.vec_b && m0 + BM <= g.M && n0 + BN <= g.N;
-    if (fast) {
+    // Panels addressed as a uniform base plus fixed 32-bit lane offsets (no prologue operand, and
+    // every panel's extent under 2^29 bytes: 128 rows of strides below 2^20 floats).
+    const bool based = g.a.ld < (int64_t{1} << 20) && g.b.ld < (int64_t{1} << 20);
+    unsigned offa[PA::NV], offb[PB::NV];
+    PanelLoader<BM, BK, !TA, PRO, C::NT>::lane_offsets(g.a.ld, offa);
+    PanelLoader<BN, BK, TB, PXK_PRO_NONE, C::NT>::lane_offsets(g.b.ld, offb);
+    // The fast loop, with its loads from uniform panel bases (BASED) or from full addresses; one
+    // or the other is compiled per launch shape, with no branch around the loads inside.
+    auto run_fast = [&](auto BASED) {
         auto issue = [&](auto S) {
             const int64_t k0 = k_lo + kb * BK;
-            la[S.value].issue_fast(A, g.a.ld, Z, g.z.ld, ZB, m0, k0);
-            lb[S.value].issue_fast(B, g.b.ld, nullptr, 0, nullptr, n0, k0);
+            if constexpr (BASED.value) {
+                la[S.value].issue_base(!TA ? A + m0 * g.a.ld + k0 : A + k0 * g.a.ld + m0, offa);
+                lb[S.value].issue_base(TB ? B + n0 * g.b.ld + k0 : B + k0 * g.b.ld + n0, offb);
+            } else {
+                la[S.value].issue_fast(A, g.a.ld, Z, g.z.ld, ZB, m0, k0);
+                lb[S.value].issue_fast(B, g.b.ld, nullptr, 0, nullptr, n0, k0);
+            }
             if (lt + 1 < nt) advance();
         };
         issue(std::integral_constant<int, 0>{});
@@ -758,6 +795,11 @@ __global__ void __launch_bounds__(C::NT) gemm_kernel(const Args g) {
                 __syncthreads();
             }
         });
+    };
+    if (fast && based && !kZ) {
+        run_fast(std::true_type{});
+    } else if (fast) {
+        run_fast(std::false_type{});
     } else if (nt > 0) {
         // Edge tiles and short K ranges: bounds-checked loads, one stage ahead.
         auto issue = [&]() {
