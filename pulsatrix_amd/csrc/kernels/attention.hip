@@ -375,17 +375,28 @@ __global__ void __launch_bounds__(G * kWave) attn_fwd_gqa_kernel(const FwdArgs a
         const int w = 16 * DT - D, r = i / w, col = D + i - r * w;
         (&kv_lds[0][0][0][0])[r * LD + col] = 0.0f;
     }
-    // A tile's 16 K rows and 16 V rows as float4 pieces over the workgroup; rows past the sequence
-    // read its last row (finite: their keys are masked and meet zero probabilities).
+    // A tile's 16 K rows and 16 V rows as float4 pieces over the workgroup, through per-tile buffer
+    // resources (kv_tile_records, as in attn_fwd_kernel) and each thread's byte offsets, fixed for
+    // the loop: rows past the sequence read 0 (their keys are masked and meet zero probabilities).
     f4 sk[PER], sv[PER];
+    int koff[PER], voff[PER];
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+        const int i = min(tid + NT * j, 16 * q4 - 1);
+        const int r = i / q4, c4 = 4 * (i - r * q4);
+        koff[j] = (r * static_cast<int>(a.ldk) + c4) * 4;
+        voff[j] = (r * static_cast<int>(a.ldv) + c4) * 4;
+    }
     auto fetch = [&](int kt) {
+        const int key0 = 16 * kt;
+        const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float*>(kbase + key0 * a.ldk), 0, kv_tile_records(l, key0, static_cast<int>(a.ldk), D), 0x00020000);
+        const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float*>(vbase + key0 * a.ldv), 0, kv_tile_records(l, key0, static_cast<int>(a.ldv), D), 0x00020000);
 #pragma unroll
         for (int j = 0; j < PER; ++j) {
-            const int i = min(tid + NT * j, 16 * q4 - 1);
-            const int r = i / q4, c4 = 4 * (i - r * q4);
-            const int64_t key = min(16 * kt + r, l - 1);
-            sk[j] = *reinterpret_cast<const f4*>(kbase + key * a.ldk + c4);
-            sv[j] = *reinterpret_cast<const f4*>(vbase + key * a.ldv + c4);
+            sk[j] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rk, koff[j], 0, 0));
+            sv[j] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rv, voff[j], 0, 0));
         }
     };
     auto stash = [&](int buf) {
@@ -1113,17 +1124,28 @@ __global__ void __launch_bounds__(G * kWave) attn_rel_q2_gqa_kernel(const RelArg
         const int w = 16 * DT - D, r = i / w, col = D + i - r * w;
         (&kv_lds[0][0][0][0])[r * LD + col] = 0.0f;
     }
-    // A tile's 16 K rows and 16 V rows as float4 pieces over the workgroup; rows past the sequence
-    // read its last row (finite: their keys are masked).
+    // A tile's 16 K rows and 16 V rows as float4 pieces over the workgroup, through per-tile buffer
+    // resources (kv_tile_records) and each thread's byte offsets, fixed for the loop: rows past the
+    // sequence read 0 (their keys are masked).
     f4 sk[PER], sv[PER];
+    int koff[PER], voff[PER];
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+        const int i = min(tid + NT * j, 16 * q4 - 1);
+        const int r = i / q4, c4 = 4 * (i - r * q4);
+        koff[j] = (r * a.ld_k + c4) * 4;
+        voff[j] = (r * a.ld_v + c4) * 4;
+    }
     auto fetch = [&](int kt) {
+        const int key0 = 16 * kt;
+        const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float*>(kbase + key0 * a.ld_k), 0, kv_tile_records(l, key0, a.ld_k, D), 0x00020000);
+        const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float*>(vbase + key0 * a.ld_v), 0, kv_tile_records(l, key0, a.ld_v, D), 0x00020000);
 #pragma unroll
         for (int j = 0; j < PER; ++j) {
-            const int i = min(tid + NT * j, 16 * q4 - 1);
-            const int r = i / q4, c4 = 4 * (i - r * q4);
-            const int64_t key = min(16 * kt + r, l - 1);
-            sk[j] = *reinterpret_cast<const f4*>(kbase + key * a.ld_k + c4);
-            sv[j] = *reinterpret_cast<const f4*>(vbase + key * a.ld_v + c4);
+            sk[j] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rk, koff[j], 0, 0));
+            sv[j] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rv, voff[j], 0, 0));
         }
     };
     auto stash = [&](int buf) {

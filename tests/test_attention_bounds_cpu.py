@@ -1,5 +1,6 @@
 """Every address the attention forward's K / V tile loads (and the recomputing q side's, which read
-V with K's lane layout) can touch, checked on the host.
+V with K's lane layout, and the GQA-shared kernels' 16-byte row pieces, a subset of K's layout)
+can touch, checked on the host.
 
 attn_fwd_kernel reads each 16-key tile of a KV head through a buffer resource whose range is
 pxk_attention_kv_tile_records(l, key0, ld, head_dim) bytes from the tile's first row of the head's
