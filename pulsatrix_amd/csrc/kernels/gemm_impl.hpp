@@ -322,14 +322,21 @@ __device__ void epilogue_rows(const float* Cs, int ldc, int64_t m0, int64_t n0, 
             st4(C + m * g.c.ld + n, acc, vec, cnt);
             if (EB) st4(C2 + m * g.c2.ld + n, acc + ld4(EB + n, vec, cnt), vec, cnt);
             if (n < g.rope_cols) {
-                const int64_t D = g.head_dim, half = D / 2;
+                // head_dim is even and n a multiple of 4: one modulo places the four columns.
+                const int D = static_cast<int>(g.head_dim), half = D / 2;
+                const int dn = static_cast<int>(n % D);
                 f4 out = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     if (j >= cnt) continue;
                     const int64_t nj = n + j;
-                    const int64_t d = nj % D, hb = nj - d;
-                    const int64_t i = g.rope_half ? (d < half ? d : d - half) : d / 2;
+                    int d = dn + j;
+                    int64_t hb = n - dn;
+                    if (d >= D) {  // head_dim not a multiple of 4: the next head
+                        d -= D;
+                        hb += D;
+                    }
+                    const int i = g.rope_half ? (d < half ? d : d - half) : d / 2;
                     const int64_t lo = hb + (g.rope_half ? i : 2 * i), hi = hb + (g.rope_half ? i + half : 2 * i + 1);
                     float x0 = Cs[row * ldc + static_cast<int>(lo - n0)];
                     float x1 = Cs[row * ldc + static_cast<int>(hi - n0)];

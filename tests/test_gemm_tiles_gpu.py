@@ -189,6 +189,39 @@ def test_fused_gemm_on_every_tile(combo, tile, splits):
 
 
 @gpu
+@pytest.mark.parametrize("tile", [N.TILE_32x48_DIRECT, N.TILE_32x48])
+@pytest.mark.parametrize("D", [2, 6])
+def test_rope_forward_with_head_dim_not_a_multiple_of_4(D, tile):
+    """ROPE_FWD where a thread's four columns cross a head boundary (head_dim 2 and 6 on 48-wide
+    tiles, 96 columns, whole heads per tile), against float64 numpy."""
+    m, n, k = 70, 96, 40
+    a, b = G.uniform((m, k), 1), G.uniform((k, n), 2)
+    eb = G.uniform((n,), 10)
+    cos, sin = rope_tables(m, D)
+    acc = a.astype(np.float64) @ b.astype(np.float64)
+    t64 = {"eb": eb.astype(np.float64), "cos": cos.astype(np.float64), "sin": sin.astype(np.float64)}
+    want = expected(N.EPI_ROPE_FWD, acc, t64, D, True)
+    outs = {key: G.empty((m, n)) for key in ("c", "c2", "c3")}
+    d = N.GemmDesc()
+    d.m, d.n, d.k, d.batch, d.inner, d.kgroups = m, n, k, 1, 1, 1
+    d.epilogue, d.eps, d.tile = N.EPI_ROPE_FWD, EPS, tile
+    d.a, d.b = N.operand(G.ptr(G.dev(a)).value, k), N.operand(G.ptr(G.dev(b)).value, n)
+    for key in ("c", "c2", "c3"):
+        setattr(d, key, N.operand(G.ptr(outs[key]).value, n))
+    d.e_bias = N.operand(G.ptr(G.dev(eb)).value, 0)
+    dc, ds = G.dev(cos), G.dev(sin)
+    d.cos_t, d.sin_t = G.ptr(dc).value, G.ptr(ds).value
+    d.head_dim, d.rope_half = D, 1
+    d.rope_cols = n - 2 * D
+    assert run(d, 1) == 0, N.pxk().pxk_last_error()
+    for key, ref in want.items():
+        got = G.host(outs[key])
+        if key == "c3":
+            got, ref = got[:, :n - 2 * D], ref[:, :n - 2 * D]
+        G.assert_close(got, ref, 2e-5, "head_dim %d tile %d output %s" % (D, tile, key))
+
+
+@gpu
 @pytest.mark.parametrize("splits", [1, 3])
 @pytest.mark.parametrize("tile", TILES)
 @pytest.mark.parametrize("tb,pro,bias", [(1, N.PRO_NONE, True), (0, N.PRO_DIV_STAB, False), (1, N.PRO_DIV_STAB, True)])
