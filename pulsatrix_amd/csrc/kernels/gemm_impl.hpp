@@ -500,9 +500,9 @@ struct PanelLoader {
     }
 
     // Byte offsets of this thread's 16-byte pieces from the panel's first element, the same for
-    // every stage: the loop then loads from a wave-uniform panel base in scalar registers plus a
-    // fixed lane offset (global_load ... saddr), with no per-stage vector address arithmetic.
-    // Requires R * ld < 2^29 (checked by the caller).
+    // every stage: the loop then loads through a buffer resource at the panel's first element
+    // (scalar registers) plus these fixed lane offsets, with no per-stage vector address
+    // arithmetic. Requires R * ld < 2^29 (checked by the caller).
     __device__ __forceinline__ static void lane_offsets(int64_t ld, unsigned (&off)[P::NV]) {
         const int tid = threadIdx.x;
 #pragma unroll
@@ -762,8 +762,8 @@ __global__ void __launch_bounds__(C::NT) gemm_kernel(const Args g) {
     unsigned offa[PA::NV], offb[PB::NV];
     PanelLoader<BM, BK, !TA, PRO, C::NT>::lane_offsets(g.a.ld, offa);
     PanelLoader<BN, BK, TB, PXK_PRO_NONE, C::NT>::lane_offsets(g.b.ld, offb);
-    // The fast loop, with its loads from uniform panel bases (BASED) or from full addresses; one
-    // or the other is compiled per launch shape, with no branch around the loads inside.
+    // The fast loop, with its loads through per-stage panel resources (BASED) or from full
+    // addresses: both are compiled, each launch runs one, and neither has a branch around its loads.
     auto run_fast = [&](auto BASED) {
         auto issue = [&](auto S) {
             const int64_t k0 = k_lo + kb * BK;
