@@ -125,6 +125,7 @@ __global__ void __launch_bounds__(kThreads) attn_fwd_kernel(const FwdArgs a) {
     const float* vbase = a.v + static_cast<int64_t>(b) * l * a.ldv + hk * D;
     const int vis_end = a.causal ? min(i0 + 16, l) : l;
     const int ntile = (vis_end + 15) / 16;
+    const int last_key = a.causal ? min(row, l - 1) : l - 1;  // the lane's row sees keys 0 .. last_key
 
     float m = -INFINITY, ssum = 0.0f;
     f4 acc[DT];
@@ -193,8 +194,7 @@ __global__ void __launch_bounds__(kThreads) attn_fwd_kernel(const FwdArgs a) {
         float mt = -INFINITY;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const int kk = kk0 + r;
-            valid[r] = (kk < l) & ((!a.causal) | (kk <= row));
+            valid[r] = kk0 + r <= last_key;
             x[r] = a.scale * s[r];
             mt = fmaxf(mt, valid[r] ? x[r] : -INFINITY);
         }
