@@ -351,6 +351,7 @@ __global__ void __launch_bounds__(G * kWave) attn_fwd_gqa_kernel(const FwdArgs a
     const int hk = bk % a.kv_heads, b = bk / a.kv_heads;
     const int h = hk * G + wave;
     const int i0 = rb * 16, row = i0 + c;
+    const int last_key = a.causal ? min(row, l - 1) : l - 1;  // the lane's row sees keys 0 .. last_key
     const bool row_ok = row < l;
 
     // Q^T fragments: qf[t][s] = Q[row][16 t + 4 g + s], zero past head_dim.
@@ -436,8 +437,7 @@ __global__ void __launch_bounds__(G * kWave) attn_fwd_gqa_kernel(const FwdArgs a
         float mt = -INFINITY;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const int kk = kk0 + r;
-            valid[r] = (kk < l) & ((!a.causal) | (kk <= row));
+            valid[r] = kk0 + r <= last_key;
             x[r] = a.scale * s[r];
             mt = fmaxf(mt, valid[r] ? x[r] : -INFINITY);
         }
@@ -594,12 +594,10 @@ __global__ void __launch_bounds__(kThreads) attn_rel_q_kernel(const RelArgs a) {
         for (int j = 0; j < 4; ++j) v[j] = rowp[min(kk0 + j, l - 1)];
         return v;
     };
+    const int last_key = a.causal ? min(row, l - 1) : l - 1;  // the lane's row sees keys 0 .. last_key
     auto valid_mask = [&](int kk0, bool (&valid)[4]) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int kk = kk0 + r;
-            valid[r] = (kk < l) & ((!a.causal) | (kk <= row));
-        }
+        for (int r = 0; r < 4; ++r) valid[r] = kk0 + r <= last_key;
     };
 
     const int ldv = a.ld_v, ldk = a.ld_k;
