@@ -694,7 +694,7 @@ __global__ void __launch_bounds__(C::NT) gemm_kernel(const Args g) {
     const int per = (total + g.splits - 1) / g.splits;
     const int t0 = static_cast<int>(split) * per < total ? static_cast<int>(split) * per : total;
     const int t1 = t0 + per < total ? t0 + per : total;
-    const int64_t nt = t1 - t0;
+    const int nt = t1 - t0;  // stage counters in 32 bits: compared and advanced on the scalar unit
 
     f4 acc[TM][TN];
 #pragma unroll
@@ -706,7 +706,7 @@ __global__ void __launch_bounds__(C::NT) gemm_kernel(const Args g) {
     PanelLoader<BM, BK, !TA, PRO, C::NT> la[NS];
     PanelLoader<BN, BK, TB, PXK_PRO_NONE, C::NT> lb[NS];
     // Load cursor: stage `lt` of the flattened (k-group, K stage) range, at (grp, kb).
-    int64_t lt = 0, grp = nkb > 0 ? t0 / nkb : 0, kb = nkb > 0 ? t0 % nkb : 0;  // 32-bit division
+    int lt = 0, grp = nkb > 0 ? t0 / nkb : 0, kb = nkb > 0 ? t0 % nkb : 0;  // 32-bit division
     const float* A = obase(g.a, b, g.inner, grp);
     const float* B = obase(g.b, b, g.inner, grp);
     constexpr bool kZ = PRO == PXK_PRO_DIV_STAB || PRO == kProStabBias, kZB = PRO == kProStabBias;
@@ -723,12 +723,12 @@ __global__ void __launch_bounds__(C::NT) gemm_kernel(const Args g) {
             if constexpr (kZB) ZB = obase(g.zb, b, g.inner, grp);
         }
     };
-    auto commit = [&](auto S, int64_t t) {  // register set S holds stage t -> LDS buffer t % 2
+    auto commit = [&](auto S, int t) {  // register set S holds stage t -> LDS buffer t % 2
         float* dst = smem + (t & 1) * L::STAGE;
         la[S.value].commit(dst, g.eps);
         lb[S.value].commit(dst + PA::SIZE, g.eps);
     };
-    auto compute = [&](int64_t t) {
+    auto compute = [&](int t) {
         const float* As = smem + (t & 1) * L::STAGE;
         const float* Bs = As + PA::SIZE;
 #pragma unroll
@@ -780,11 +780,11 @@ __global__ void __launch_bounds__(C::NT) gemm_kernel(const Args g) {
         commit(std::integral_constant<int, 0>{}, 0);
         static_for<NS>([&](auto U) { issue(std::integral_constant<int, (U.value + 1) % NS>{}); });
         __syncthreads();
-        const int64_t main_iters = (nt - 2) / NS * NS;  // a multiple of NS, >= nt - NS - 1
-        for (int64_t tb = 0; tb < main_iters; tb += NS) {
+        const int main_iters = (nt - 2) / NS * NS;  // a multiple of NS, >= nt - NS - 1
+        for (int tb = 0; tb < main_iters; tb += NS) {
             static_for<NS>([&](auto U) {
                 constexpr int nxt = (U.value + 1) % NS;
-                const int64_t t = tb + U.value;
+                const int t = tb + U.value;
                 // Buffer (t + 1) % 2 was last read by stage t - 1, before the previous barrier, so
                 // stage t + 1 goes to LDS first and its writes overlap this stage's MFMAs.
                 commit(std::integral_constant<int, nxt>{}, t + 1);
@@ -795,7 +795,7 @@ __global__ void __launch_bounds__(C::NT) gemm_kernel(const Args g) {
         }
         static_for<NS + 1>([&](auto U) {  // the last 2 .. NS + 1 stages: already in flight
             constexpr int nxt = (U.value + 1) % NS;
-            const int64_t t = main_iters + U.value;
+            const int t = main_iters + U.value;
             if (t < nt) {
                 if (t + 1 < nt) commit(std::integral_constant<int, nxt>{}, t + 1);
                 compute(t);
@@ -818,7 +818,7 @@ __global__ void __launch_bounds__(C::NT) gemm_kernel(const Args g) {
         issue();
         commit(std::integral_constant<int, 0>{}, 0);
         __syncthreads();
-        for (int64_t t = 0; t < nt; ++t) {
+        for (int t = 0; t < nt; ++t) {
             const bool more = t + 1 < nt;
             if (more) issue();
             compute(t);
